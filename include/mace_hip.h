@@ -1,0 +1,114 @@
+/*
+ * mace_hip.h -- C ABI of the MI355X MACE energy / forces / stress engine.
+ *
+ * The library replaces the reference's per-step compiled function
+ *   step(pos, node_attrs, edge_index, shifts, cell, batch) -> ((E, node_energy), dE/dpos)
+ * of `mace_mlx/calculators.py:424-476` and its stress variant
+ * `calculators.py:482-563`, plus the matscipy neighbour list with skin caching of
+ * `calculators.py:44-55,266-310`.  The Python host (`mace_mlx_amd.calculators`)
+ * keeps the reference's ASE-facing API (`mace_mp`, `mace_off`, `MACECalculator`)
+ * and drives these entry points through ctypes.
+ *
+ * Conventions
+ *   - Every entry point returns MACE_OK (0) or a negative MACE_ERR_* code; the
+ *     message of the last failure is available from mace_last_error().  No C++
+ *     exception crosses the boundary.
+ *   - The caller owns every host array; the context owns all device memory and
+ *     one HIP stream.  A context is not re-entrant (one thread at a time);
+ *     several contexts may share a device.
+ *   - Edges follow the reference: edge_index = [sender i; receiver j], shift S,
+ *     edge vector D = x_j - x_i + S @ cell (`utils.py:47-84`).
+ */
+#ifndef MACE_HIP_H
+#define MACE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MACE_OK 0
+#define MACE_ERR_INVALID (-1)     /* bad argument / inconsistent sizes   -> ValueError */
+#define MACE_ERR_HIP (-2)         /* HIP runtime failure                 -> RuntimeError */
+#define MACE_ERR_UNSUPPORTED (-3) /* model topology not implemented      -> NotImplementedError */
+#define MACE_ERR_STATE (-4)       /* call order (model / system missing) -> RuntimeError */
+#define MACE_ERR_SPECIES (-5)     /* species index outside the model     -> ValueError */
+
+/* mace_step flags */
+#define MACE_STEP_FORCES 1u        /* compute forces (always on in practice)               */
+#define MACE_STEP_STRESS 2u        /* also compute the virial dE/d(eps) (calculators.py:526) */
+#define MACE_STEP_FORCE_NL 4u      /* rebuild the neighbour list regardless of the skin     */
+
+typedef struct mace_ctx mace_ctx;
+
+/* Model dimensions; every array passed to mace_model_set_tensor is checked
+ * against the sizes these imply. */
+typedef struct mace_model_dims {
+  int32_t num_elements;      /* one-hot width (len(z_table))                    */
+  int32_t num_channels;      /* multiplicity of every irrep block (128)         */
+  int32_t max_ell;           /* spherical-harmonic degree (3)                   */
+  int32_t num_bessel;        /* radial basis size (8)                           */
+  int32_t num_poly_cutoff;   /* polynomial envelope order p (5)                 */
+  int32_t num_layers;        /* interaction layers (2)                          */
+  int32_t radial_hidden;     /* width of the radial MLP hidden layers (64)      */
+  int32_t radial_depth;      /* number of hidden layers of the radial MLP (3)   */
+  int32_t layer_in_blocks[4];  /* input irreps of layer l: blocks 0e,1o,2e[:n]  */
+  int32_t layer_hid_blocks[4]; /* hidden (output) irreps of layer l             */
+  int32_t correlation[4];
+  int32_t has_zbl;
+  int32_t zbl_p;
+  double r_max;
+  double zbl_a_exp;
+  double zbl_a_prefactor;
+  double zbl_scale;          /* ScaleShiftMACE scale applied to the pair term  */
+} mace_model_dims;
+
+/* Context lifetime.  device = HIP device ordinal. */
+int mace_create(int32_t device, mace_ctx** out);
+void mace_destroy(mace_ctx* ctx);
+const char* mace_last_error(const mace_ctx* ctx);
+
+/* Model upload.  Tensor names and layouts are produced by
+ * mace_mlx_amd.device_model from the reference's config.json + weights.npz
+ * (`model.py:664-720`); see that module for the list. */
+int mace_model_begin(mace_ctx* ctx, const mace_model_dims* dims);
+int mace_model_set_tensor(mace_ctx* ctx, const char* name, const float* data, int64_t count);
+int mace_model_end(mace_ctx* ctx);
+
+/* System topology: atom count, species index per atom (0..num_elements-1),
+ * cell (row-major 3x3, rows = lattice vectors) and pbc flags.  Changing the
+ * cell or pbc beyond 1e-10 invalidates the neighbour list
+ * (`calculators.py:266-283`).  skin <= 0 rebuilds every step. */
+int mace_set_system(mace_ctx* ctx, int32_t n_atoms, const int32_t* species,
+                    const double* cell9, const uint8_t* pbc3, double skin);
+
+/* One energy + forces (+ virial) evaluation at `positions` (n_atoms x 3, Angstrom).
+ *   energy       : total energy (eV)
+ *   node_energy  : n_atoms per-atom energies, may be NULL
+ *   forces       : n_atoms x 3, -dE/dpos, may be NULL
+ *   virial9      : dE/d(eps_sym) (3x3, row-major; stress = virial / |det cell|),
+ *                  only with MACE_STEP_STRESS, may be NULL
+ * Synchronous.  Rebuilds the neighbour list on the device when the skin
+ * criterion of `calculators.py:266-283` fails. */
+int mace_step(mace_ctx* ctx, const double* positions, uint32_t flags, double* energy,
+              double* node_energy, double* forces, double* virial9);
+
+/* Test hooks.  mace_set_edges installs an explicit edge list (bypassing the
+ * neighbour list until the next mace_set_system); mace_get_edges copies the
+ * current list (receiver-sorted) out.  *n_edges returns the count; arrays may be
+ * NULL to query the count only. */
+int mace_set_edges(mace_ctx* ctx, int64_t n_edges, const int32_t* sender,
+                   const int32_t* receiver, const int32_t* shifts3);
+int mace_get_edges(mace_ctx* ctx, int64_t capacity, int32_t* sender, int32_t* receiver,
+                   int32_t* shifts3, int64_t* n_edges);
+
+/* Timing of the last mace_step (device milliseconds, HIP events on the
+ * context's stream): [0] whole step, [1] neighbour list (0 if cached),
+ * [2] forward, [3] backward.  Returns the number of values written. */
+int mace_get_timings(const mace_ctx* ctx, double* out, int32_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MACE_HIP_H */

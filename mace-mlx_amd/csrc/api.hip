@@ -1,0 +1,926 @@
+// C ABI of the engine (include/mace_hip.h): context, model upload, topology,
+// device neighbour list with skin cache, and the energy / forces / virial step.
+#include <hip/hip_runtime.h>
+#include <hipcub/hipcub.hpp>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/mace_hip.h"
+#include "common.h"
+
+using namespace mace;
+
+namespace {
+
+struct Err {
+  int code;
+};
+
+#define HIPCHK(expr)                                                                          \
+  do {                                                                                        \
+    hipError_t _e = (expr);                                                                   \
+    if (_e != hipSuccess) fail(MACE_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(_e)); \
+  } while (0)
+
+template <class T>
+struct DBuf {
+  T* p = nullptr;
+  size_t n = 0;
+  void ensure(size_t count);
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+};
+
+std::string g_fail_msg;
+[[noreturn]] void fail(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_fail_msg = buf;
+  throw Err{code};
+}
+
+template <class T>
+void DBuf<T>::ensure(size_t count) {
+  if (count <= n && p) return;
+  release();
+  size_t c = std::max<size_t>(count, 1);
+  HIPCHK(hipMalloc((void**)&p, c * sizeof(T)));
+  n = c;
+}
+
+int n_tp_slots(int lin) { return lin == 1 ? TP1_NSLOT : lin == 2 ? TP2_NSLOT : TP3_NSLOT; }
+int n_tp_acc(int lin) { return lin == 1 ? TP1_NACC : lin == 2 ? TP2_NACC : TP3_NACC; }
+const int* tp_l3(int lin) { return lin == 1 ? TP1_L3 : lin == 2 ? TP2_L3 : TP3_L3; }
+const int* tp_accoff(int lin) { return lin == 1 ? TP1_ACC : lin == 2 ? TP2_ACC : TP3_ACC; }
+int sc_kt(int lout, int corr) {
+  static const int kt[3][3] = {{SC_L0_C1_KT, SC_L0_C2_KT, SC_L0_C3_KT},
+                               {SC_L1_C1_KT, SC_L1_C2_KT, SC_L1_C3_KT},
+                               {SC_L2_C1_KT, SC_L2_C2_KT, SC_L2_C3_KT}};
+  return kt[lout][corr - 1];
+}
+
+struct Layer {
+  int lin = 1, lhid = 1, corr = 3;
+  int din = 0, dhid = 0, dmid = 0, dint = 0, wn = 0;
+  DBuf<float> up[3], upT[3], skip[3], skipT[3], mlp[4], lin_[4], linT[4], sc[3], plin[3], plinT[3];
+  DBuf<float> ro, ro1, ro2;
+  int nskip = 0;
+  // per-step activations
+  DBuf<float> h_up, A, w, ro_e;
+};
+
+}  // namespace
+
+struct mace_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string err;
+  // model
+  bool model_ready = false;
+  mace_model_dims dims{};
+  std::map<std::string, std::vector<float>> host_tensors;
+  std::vector<Layer> layers;
+  DBuf<float> e0, bessel_w, zbl_z, zbl_cov, embed;
+  // system
+  int N = 0;
+  std::vector<int> species_h;
+  double cell[9] = {0};
+  uint8_t pbc[3] = {0, 0, 0};
+  double skin = 0.5;
+  bool system_ready = false;
+  DBuf<int> species;
+  DBuf<double> pos;
+  double* pos_pinned = nullptr;
+  size_t pos_pinned_n = 0;
+  // neighbour list state
+  bool nl_valid = false, edges_manual = false;
+  std::vector<double> nl_pos;  // positions at the last rebuild
+  int64_t E = 0;
+  DBuf<int> sender, receiver, shifts, rowptr, rowptr_s, perm_s;
+  DBuf<int> nl_img, nl_bin, nl_bin_sorted, nl_atoms, nl_iota, nl_counts, nl_bin_count, nl_bin_start;
+  DBuf<double> nl_wpos;
+  DBuf<int> e_tmp_i, e_tmp_j, e_tmp_s, e_perm, e_keys;
+  DBuf<unsigned char> cub_tmp;
+  // per-step edge buffers
+  DBuf<EdgeGeom> geom;
+  DBuf<float> Y, ef, zbl_e, gY, gef, gv, gw;
+  DBuf<double> vir_part;
+  // node buffers
+  std::vector<DBuf<float>> h;  // h[0..L]
+  DBuf<float> M, B, gB, gA, gM, gh0, gh1, gup, ypre, node_e;
+  DBuf<double> out;  // [energy, vir9, forces 3N]
+  double* out_pinned = nullptr;
+  float* ne_pinned = nullptr;
+  size_t out_pinned_n = 0;
+  hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+  double timings[4] = {0, 0, 0, 0};
+  bool last_nl = false;
+};
+
+namespace {
+
+int guard(mace_ctx* ctx, const std::function<void()>& fn) {
+  try {
+    fn();
+    return MACE_OK;
+  } catch (const Err& e) {
+    if (ctx) ctx->err = g_fail_msg;
+    return e.code;
+  } catch (const std::exception& e) {
+    if (ctx) ctx->err = e.what();
+    return MACE_ERR_INVALID;
+  }
+}
+
+void set_device(mace_ctx* c) { HIPCHK(hipSetDevice(c->device)); }
+
+const std::vector<float>& tensor(mace_ctx* c, const std::string& name, size_t count) {
+  auto it = c->host_tensors.find(name);
+  if (it == c->host_tensors.end()) fail(MACE_ERR_INVALID, "model tensor '%s' missing", name.c_str());
+  if (it->second.size() != count)
+    fail(MACE_ERR_INVALID, "model tensor '%s' has %zu values, expected %zu", name.c_str(), it->second.size(), count);
+  return it->second;
+}
+
+void upload(mace_ctx* c, DBuf<float>& dst, const std::vector<float>& v) {
+  dst.ensure(v.size());
+  HIPCHK(hipMemcpy(dst.p, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
+}
+
+std::vector<float> transpose(const std::vector<float>& a, int rows, int cols, int batch = 1) {
+  std::vector<float> t(a.size());
+  for (int b = 0; b < batch; ++b)
+    for (int i = 0; i < rows; ++i)
+      for (int j = 0; j < cols; ++j)
+        t[(size_t)b * rows * cols + (size_t)j * rows + i] = a[(size_t)b * rows * cols + (size_t)i * cols + j];
+  return t;
+}
+
+void build_model(mace_ctx* c) {
+  const auto& d = c->dims;
+  const int C = NC;
+  if (d.num_channels != NC) fail(MACE_ERR_UNSUPPORTED, "num_channels=%d (compiled for %d)", d.num_channels, NC);
+  if (d.max_ell != 3) fail(MACE_ERR_UNSUPPORTED, "max_ell=%d (compiled for 3)", d.max_ell);
+  if (d.radial_hidden != RADIAL_H || d.radial_depth != 3)
+    fail(MACE_ERR_UNSUPPORTED, "radial MLP %dx%d (compiled for 3 hidden layers of %d)", d.radial_depth,
+         d.radial_hidden, RADIAL_H);
+  if (d.num_bessel < 1 || d.num_bessel > NBESSEL_MAX) fail(MACE_ERR_UNSUPPORTED, "num_bessel=%d", d.num_bessel);
+  if (d.num_layers < 1 || d.num_layers > 4) fail(MACE_ERR_UNSUPPORTED, "num_layers=%d", d.num_layers);
+  if (d.num_elements < 1) fail(MACE_ERR_INVALID, "num_elements=%d", d.num_elements);
+  const int nel = d.num_elements, nb = d.num_bessel;
+  upload(c, c->e0, tensor(c, "e0", nel));
+  upload(c, c->bessel_w, tensor(c, "bessel_w", nb));
+  upload(c, c->embed, tensor(c, "embed", (size_t)nel * C));
+  if (d.has_zbl) {
+    upload(c, c->zbl_z, tensor(c, "zbl_z", nel));
+    upload(c, c->zbl_cov, tensor(c, "zbl_cov", nel));
+  }
+  c->layers.clear();
+  c->layers.resize(d.num_layers);
+  for (int l = 0; l < d.num_layers; ++l) {
+    Layer& L = c->layers[l];
+    L.lin = d.layer_in_blocks[l];
+    L.lhid = d.layer_hid_blocks[l];
+    L.corr = d.correlation[l];
+    if (L.lin < 1 || L.lin > 3 || L.lhid < 1 || L.lhid > 3)
+      fail(MACE_ERR_UNSUPPORTED, "layer %d irreps blocks in=%d hid=%d", l, L.lin, L.lhid);
+    if (L.corr < 1 || L.corr > 3) fail(MACE_ERR_UNSUPPORTED, "correlation %d", L.corr);
+    if (l == 0 && L.lin != 1) fail(MACE_ERR_UNSUPPORTED, "first layer input must be scalar");
+    if (l > 0 && L.lin != d.layer_hid_blocks[l - 1]) fail(MACE_ERR_INVALID, "layer %d input mismatch", l);
+    L.din = C * L.lin * L.lin;
+    L.dhid = C * L.lhid * L.lhid;
+    L.dint = C * 16;
+    L.dmid = C * n_tp_acc(L.lin);
+    L.wn = C * n_tp_slots(L.lin);
+    const std::string p = "L" + std::to_string(l) + ".";
+    for (int b = 0; b < L.lin; ++b) {
+      const auto& w = tensor(c, p + "up." + std::to_string(b), (size_t)C * C);
+      upload(c, L.up[b], w);
+      upload(c, L.upT[b], transpose(w, C, C));
+    }
+    L.nskip = std::min(L.lin, L.lhid);
+    for (int b = 0; b < L.nskip; ++b) {
+      const auto& w = tensor(c, p + "skip." + std::to_string(b), (size_t)nel * C * C);
+      upload(c, L.skip[b], w);
+      upload(c, L.skipT[b], transpose(w, C, C, nel));
+    }
+    upload(c, L.mlp[0], tensor(c, p + "mlp.0", (size_t)nb * RADIAL_H));
+    upload(c, L.mlp[1], tensor(c, p + "mlp.1", (size_t)RADIAL_H * RADIAL_H));
+    upload(c, L.mlp[2], tensor(c, p + "mlp.2", (size_t)RADIAL_H * RADIAL_H));
+    upload(c, L.mlp[3], tensor(c, p + "mlp.3", (size_t)RADIAL_H * L.wn));
+    const int* l3 = tp_l3(L.lin);
+    for (int lo = 0; lo < 4; ++lo) {
+      int ns = 0;
+      for (int s = 0; s < n_tp_slots(L.lin); ++s) ns += (l3[s] == lo);
+      const auto& w = tensor(c, p + "lin." + std::to_string(lo), (size_t)ns * C * C);
+      upload(c, L.lin_[lo], w);
+      upload(c, L.linT[lo], transpose(w, ns * C, C));
+    }
+    for (int b = 0; b < L.lhid; ++b) {
+      upload(c, L.sc[b], tensor(c, p + "sc." + std::to_string(b), (size_t)nel * sc_kt(b, L.corr) * C));
+      const auto& w = tensor(c, p + "plin." + std::to_string(b), (size_t)C * C);
+      upload(c, L.plin[b], w);
+      upload(c, L.plinT[b], transpose(w, C, C));
+    }
+    if (l < d.num_layers - 1) {
+      upload(c, L.ro, tensor(c, p + "ro", C));
+    } else {
+      if (L.lhid != 1) fail(MACE_ERR_UNSUPPORTED, "last layer must be scalar");
+      upload(c, L.ro1, tensor(c, p + "ro1", (size_t)C * 16));
+      upload(c, L.ro2, tensor(c, p + "ro2", 16));
+    }
+  }
+  c->host_tensors.clear();
+  c->model_ready = true;
+}
+
+// ---------------------------------------------------------------------------
+// buffers
+// ---------------------------------------------------------------------------
+void ensure_node_buffers(mace_ctx* c) {
+  const int N = std::max(c->N, 1);
+  const int L = (int)c->layers.size();
+  c->h.resize(L + 1);
+  int maxd = NC * 16;
+  for (int l = 0; l < L; ++l) {
+    Layer& ly = c->layers[l];
+    c->h[l].ensure((size_t)N * ly.din);
+    ly.h_up.ensure((size_t)N * ly.din);
+    ly.A.ensure((size_t)N * ly.dint);
+    ly.ro_e.ensure(N);
+    maxd = std::max({maxd, ly.dmid, ly.din, ly.dhid});
+  }
+  c->h[L].ensure((size_t)N * c->layers[L - 1].dhid);
+  c->M.ensure((size_t)N * maxd);
+  c->B.ensure((size_t)N * maxd);
+  c->gB.ensure((size_t)N * maxd);
+  c->gA.ensure((size_t)N * maxd);
+  c->gM.ensure((size_t)N * maxd);
+  c->gh0.ensure((size_t)N * maxd);
+  c->gh1.ensure((size_t)N * maxd);
+  c->gup.ensure((size_t)N * maxd);
+  c->ypre.ensure((size_t)N * 16);
+  c->node_e.ensure(N);
+  c->out.ensure(10 + 3 * (size_t)N);
+  c->pos.ensure(3 * (size_t)N);
+  if (c->out_pinned_n < (size_t)N) {
+    if (c->out_pinned) (void)hipHostFree(c->out_pinned);
+    if (c->ne_pinned) (void)hipHostFree(c->ne_pinned);
+    if (c->pos_pinned) (void)hipHostFree(c->pos_pinned);
+    HIPCHK(hipHostMalloc((void**)&c->out_pinned, (10 + 3 * (size_t)N) * sizeof(double), hipHostMallocDefault));
+    HIPCHK(hipHostMalloc((void**)&c->ne_pinned, (size_t)N * sizeof(float), hipHostMallocDefault));
+    HIPCHK(hipHostMalloc((void**)&c->pos_pinned, 3 * (size_t)N * sizeof(double), hipHostMallocDefault));
+    c->out_pinned_n = N;
+  }
+}
+
+void ensure_edge_buffers(mace_ctx* c, int64_t E) {
+  const size_t e = (size_t)std::max<int64_t>(E, 1);
+  int maxw = 0;
+  for (auto& ly : c->layers) {
+    ly.w.ensure(e * ly.wn);
+    maxw = std::max(maxw, ly.wn);
+  }
+  c->geom.ensure(e);
+  c->Y.ensure(e * 16);
+  c->ef.ensure(e * c->dims.num_bessel);
+  c->zbl_e.ensure(e);
+  c->gY.ensure(e * 16);
+  c->gef.ensure(e * c->dims.num_bessel);
+  c->gv.ensure(e * 3);
+  c->gw.ensure(e * maxw);
+  c->vir_part.ensure(9 * ((e + 255) / 256));
+}
+
+void ensure_edge_index(mace_ctx* c, int64_t E) {
+  const size_t e = (size_t)std::max<int64_t>(E, 1);
+  c->sender.ensure(e);
+  c->receiver.ensure(e);
+  c->shifts.ensure(3 * e);
+  c->perm_s.ensure(e);
+  c->e_keys.ensure(e);
+  c->e_perm.ensure(e);
+  c->nl_iota.ensure(std::max<size_t>(e, (size_t)c->N + 1));
+  c->e_tmp_i.ensure(e);
+  c->e_tmp_j.ensure(e);
+  c->e_tmp_s.ensure(3 * e);
+}
+
+int bits_for(int64_t maxval) {
+  int b = 1;
+  while (b < 31 && ((int64_t)1 << b) <= maxval) ++b;
+  return b;
+}
+
+void cub_sort_pairs(mace_ctx* c, const int* kin, int* kout, const int* vin, int* vout, int64_t n, int64_t maxkey) {
+  if (n <= 0) return;
+  size_t bytes = 0;
+  HIPCHK(hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, kin, kout, vin, vout, (int)n, 0, bits_for(maxkey),
+                                            c->stream));
+  c->cub_tmp.ensure(bytes);
+  HIPCHK(hipcub::DeviceRadixSort::SortPairs(c->cub_tmp.p, bytes, kin, kout, vin, vout, (int)n, 0, bits_for(maxkey),
+                                            c->stream));
+}
+
+void cub_exclusive_sum(mace_ctx* c, const int* in, int* out, int64_t n) {
+  size_t bytes = 0;
+  HIPCHK(hipcub::DeviceScan::ExclusiveSum(nullptr, bytes, in, out, (int)n, c->stream));
+  c->cub_tmp.ensure(bytes);
+  HIPCHK(hipcub::DeviceScan::ExclusiveSum(c->cub_tmp.p, bytes, in, out, (int)n, c->stream));
+}
+
+// CSR rowptr from (unsorted) keys: counts + exclusive scan over n+1 entries
+void build_rowptr(mace_ctx* c, const int* keys, int64_t E, int n, int* rowptr) {
+  c->nl_counts.ensure((size_t)n + 1);
+  HIPCHK(hipMemsetAsync(c->nl_counts.p, 0, ((size_t)n + 1) * sizeof(int), c->stream));
+  launch_count_keys(c->stream, E, keys, c->nl_counts.p);
+  cub_exclusive_sum(c, c->nl_counts.p, rowptr, (int64_t)n + 1);
+}
+
+// sender-side CSR: perm_s = edge ids stably sorted by sender
+void build_sender_csr(mace_ctx* c) {
+  const int64_t E = c->E;
+  c->rowptr_s.ensure((size_t)c->N + 1);
+  if (E > 0) {
+    launch_fill_iota(c->stream, (int)E, c->nl_iota.p);
+    cub_sort_pairs(c, c->sender.p, c->e_keys.p, c->nl_iota.p, c->perm_s.p, E, c->N);
+  }
+  build_rowptr(c, c->sender.p, E, c->N, c->rowptr_s.p);
+}
+
+double plane_spacing(const double* cell, int k) {
+  const double* a = cell + 3 * ((k + 1) % 3);
+  const double* b = cell + 3 * ((k + 2) % 3);
+  const double cx = a[1] * b[2] - a[2] * b[1], cy = a[2] * b[0] - a[0] * b[2], cz = a[0] * b[1] - a[1] * b[0];
+  const double vol = std::fabs(cell[0] * (cell[4] * cell[8] - cell[5] * cell[7]) -
+                               cell[1] * (cell[3] * cell[8] - cell[5] * cell[6]) +
+                               cell[2] * (cell[3] * cell[7] - cell[4] * cell[6]));
+  return vol / std::sqrt(cx * cx + cy * cy + cz * cz);
+}
+
+bool invert3(const double* m, double* inv) {
+  const double det = m[0] * (m[4] * m[8] - m[5] * m[7]) - m[1] * (m[3] * m[8] - m[5] * m[6]) +
+                     m[2] * (m[3] * m[7] - m[4] * m[6]);
+  if (std::fabs(det) < 1e-300) return false;
+  inv[0] = (m[4] * m[8] - m[5] * m[7]) / det;
+  inv[1] = (m[2] * m[7] - m[1] * m[8]) / det;
+  inv[2] = (m[1] * m[5] - m[2] * m[4]) / det;
+  inv[3] = (m[5] * m[6] - m[3] * m[8]) / det;
+  inv[4] = (m[0] * m[8] - m[2] * m[6]) / det;
+  inv[5] = (m[2] * m[3] - m[0] * m[5]) / det;
+  inv[6] = (m[3] * m[7] - m[4] * m[6]) / det;
+  inv[7] = (m[1] * m[6] - m[0] * m[7]) / det;
+  inv[8] = (m[0] * m[4] - m[1] * m[3]) / det;
+  return true;
+}
+
+// Effective cell for the binning: periodic rows are the cell rows; each
+// non-periodic row is replaced by a vector orthogonal to the periodic rows that
+// spans the atoms' extent plus a margin (positions along it are never wrapped).
+NLParams nl_params(mace_ctx* c, const double* pos, double cutoff) {
+  NLParams p{};
+  double cell[9];
+  std::memcpy(cell, c->cell, sizeof cell);
+  const int N = c->N;
+  int nper = 0;
+  for (int k = 0; k < 3; ++k) nper += c->pbc[k] ? 1 : 0;
+  double origin[3] = {0, 0, 0};
+  if (nper < 3) {
+    // orthonormal directions for the non-periodic axes
+    double dirs[3][3];
+    std::vector<int> per, non;
+    for (int k = 0; k < 3; ++k) (c->pbc[k] ? per : non).push_back(k);
+    if (per.size() == 2) {
+      const double* a = cell + 3 * per[0];
+      const double* b = cell + 3 * per[1];
+      double n[3] = {a[1] * b[2] - a[2] * b[1], a[2] * b[0] - a[0] * b[2], a[0] * b[1] - a[1] * b[0]};
+      const double nn = std::sqrt(n[0] * n[0] + n[1] * n[1] + n[2] * n[2]);
+      if (nn < 1e-12) fail(MACE_ERR_INVALID, "degenerate periodic cell vectors");
+      for (int q = 0; q < 3; ++q) dirs[non[0]][q] = n[q] / nn;
+    } else if (per.size() == 1) {
+      const double* a = cell + 3 * per[0];
+      const double na = std::sqrt(a[0] * a[0] + a[1] * a[1] + a[2] * a[2]);
+      if (na < 1e-12) fail(MACE_ERR_INVALID, "degenerate periodic cell vector");
+      double e1[3] = {a[0] / na, a[1] / na, a[2] / na};
+      double t[3] = {1, 0, 0};
+      if (std::fabs(e1[0]) > 0.9) t[0] = 0, t[1] = 1;
+      double u[3] = {e1[1] * t[2] - e1[2] * t[1], e1[2] * t[0] - e1[0] * t[2], e1[0] * t[1] - e1[1] * t[0]};
+      const double nu = std::sqrt(u[0] * u[0] + u[1] * u[1] + u[2] * u[2]);
+      for (int q = 0; q < 3; ++q) u[q] /= nu;
+      double v[3] = {e1[1] * u[2] - e1[2] * u[1], e1[2] * u[0] - e1[0] * u[2], e1[0] * u[1] - e1[1] * u[0]};
+      for (int q = 0; q < 3; ++q) dirs[non[0]][q] = u[q], dirs[non[1]][q] = v[q];
+    } else {
+      for (int k = 0; k < 3; ++k)
+        for (int q = 0; q < 3; ++q) dirs[k][q] = (k == q) ? 1.0 : 0.0;
+    }
+    for (int k : non) {
+      double lo = 1e300, hi = -1e300;
+      for (int i = 0; i < N; ++i) {
+        const double s = pos[3 * i] * dirs[k][0] + pos[3 * i + 1] * dirs[k][1] + pos[3 * i + 2] * dirs[k][2];
+        lo = std::min(lo, s);
+        hi = std::max(hi, s);
+      }
+      if (N == 0) lo = hi = 0;
+      const double len = (hi - lo) + 2.0 * cutoff + 1.0;
+      for (int q = 0; q < 3; ++q) {
+        cell[3 * k + q] = dirs[k][q] * len;
+        origin[q] += dirs[k][q] * (lo - cutoff - 0.5);
+      }
+    }
+  }
+  std::memcpy(p.cell, cell, sizeof cell);
+  if (!invert3(cell, p.inv)) fail(MACE_ERR_INVALID, "cell is singular for a periodic direction");
+  for (int k = 0; k < 3; ++k) {
+    p.origin[k] = origin[k];
+    p.periodic[k] = c->pbc[k] ? 1 : 0;
+    const double d = plane_spacing(cell, k);
+    int nbin = (int)std::floor(d / cutoff);
+    nbin = std::max(1, std::min(nbin, 256));
+    p.nbin[k] = nbin;
+    p.range[k] = (int)std::ceil(cutoff * nbin / d + 1e-9);
+    if (!p.periodic[k]) p.range[k] = std::min(p.range[k], nbin);
+  }
+  p.cutoff2 = cutoff * cutoff;
+  return p;
+}
+
+void build_nl(mace_ctx* c, const double* pos_host) {
+  const int N = c->N;
+  const double cutoff = c->dims.r_max + std::max(c->skin, 0.0);
+  NLParams p = nl_params(c, pos_host, cutoff);
+  const int nbins = p.nbin[0] * p.nbin[1] * p.nbin[2];
+  c->nl_wpos.ensure(3 * (size_t)N);
+  c->nl_img.ensure(3 * (size_t)N);
+  c->nl_bin.ensure(N);
+  c->nl_bin_sorted.ensure(N);
+  c->nl_atoms.ensure(N);
+  c->nl_iota.ensure((size_t)N + 1);
+  c->nl_bin_start.ensure((size_t)nbins + 1);
+  c->rowptr.ensure((size_t)N + 1);
+  launch_nl_bin(c->stream, N, c->pos.p, p, c->nl_wpos.p, c->nl_img.p, c->nl_bin.p);
+  launch_fill_iota(c->stream, N, c->nl_iota.p);
+  cub_sort_pairs(c, c->nl_bin.p, c->nl_bin_sorted.p, c->nl_iota.p, c->nl_atoms.p, N, nbins);
+  build_rowptr(c, c->nl_bin.p, N, nbins, c->nl_bin_start.p);
+  c->nl_counts.ensure((size_t)N + 1);
+  HIPCHK(hipMemsetAsync(c->nl_counts.p, 0, ((size_t)N + 1) * sizeof(int), c->stream));
+  launch_nl_count(c->stream, N, p, c->nl_wpos.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, c->nl_counts.p);
+  // reuse nl_iota as scan output scratch? rowptr directly:
+  cub_exclusive_sum(c, c->nl_counts.p, c->rowptr.p, (int64_t)N + 1);
+  int Eh = 0;
+  HIPCHK(hipMemcpyAsync(&Eh, c->rowptr.p + N, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(hipStreamSynchronize(c->stream));
+  c->E = Eh;
+  ensure_edge_index(c, c->E);
+  launch_nl_fill(c->stream, N, p, c->nl_wpos.p, c->nl_img.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p,
+                 c->rowptr.p, c->sender.p, c->receiver.p, c->shifts.p);
+  build_sender_csr(c);
+  ensure_edge_buffers(c, c->E);
+  c->nl_pos.assign(pos_host, pos_host + 3 * (size_t)N);
+  c->nl_valid = true;
+}
+
+__global__ void k_gather_edges(int64_t E, const int* perm, const int* si, const int* ri, const int* ss, int* so,
+                               int* ro, int* sso) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const int q = perm[e];
+  so[e] = si[q];
+  ro[e] = ri[q];
+  sso[3 * e] = ss[3 * q];
+  sso[3 * e + 1] = ss[3 * q + 1];
+  sso[3 * e + 2] = ss[3 * q + 2];
+}
+
+// ---------------------------------------------------------------------------
+// the step
+// ---------------------------------------------------------------------------
+LinearDesc lin_desc(int d, int K, int Cout, int ldx, int in_base, int in_stride, int ldy, int out_base,
+                    int out_stride, int acc) {
+  LinearDesc D;
+  D.d = d;
+  D.K = K;
+  D.Cout = Cout;
+  D.ldx = ldx;
+  D.in_base = in_base;
+  D.in_stride = in_stride;
+  D.ldy = ldy;
+  D.out_base = out_base;
+  D.out_stride = out_stride;
+  D.accumulate = acc;
+  return D;
+}
+
+FrontParams front_params(mace_ctx* c) {
+  FrontParams p{};
+  std::memcpy(p.cell, c->cell, sizeof p.cell);
+  p.r_max = (float)c->dims.r_max;
+  p.bessel_pref = (float)std::sqrt(2.0 / c->dims.r_max);
+  p.nbessel = c->dims.num_bessel;
+  p.pcut = c->dims.num_poly_cutoff;
+  p.has_zbl = c->dims.has_zbl;
+  p.zbl_p = c->dims.zbl_p;
+  p.zbl_a_exp = (float)c->dims.zbl_a_exp;
+  p.zbl_a_pref = (float)c->dims.zbl_a_prefactor;
+  p.zbl_scale = (float)c->dims.zbl_scale;
+  return p;
+}
+
+// skip connection for hidden block b (rows 2b+1, input block b of h)
+void run_skip(mace_ctx* c, Layer& L, int b, const float* h, float* out, int ldo, int acc) {
+  const int d = 2 * b + 1;
+  LinearDesc D = lin_desc(d, NC, NC, L.din, NC * b * b, 0, ldo, NC * b * b, 0, acc);
+  if (c->dims.num_elements == 1)
+    launch_linear(c->stream, c->N, D, h, L.skip[b].p, out);
+  else
+    launch_linear_species(c->stream, c->N, D, h, L.skip[b].p, c->species.p, out);
+}
+
+void run_skip_T(mace_ctx* c, Layer& L, int b, const float* gout, int ldg, float* gh) {
+  const int d = 2 * b + 1;
+  LinearDesc D = lin_desc(d, NC, NC, ldg, NC * b * b, 0, L.din, NC * b * b, 0, 1);
+  if (c->dims.num_elements == 1)
+    launch_linear(c->stream, c->N, D, gout, L.skipT[b].p, gh);
+  else
+    launch_linear_species(c->stream, c->N, D, gout, L.skipT[b].p, c->species.p, gh);
+}
+
+void forward(mace_ctx* c) {
+  hipStream_t st = c->stream;
+  const int N = c->N;
+  const int64_t E = c->E;
+  const int nb = c->dims.num_bessel;
+  FrontParams fp = front_params(c);
+  launch_edge_fwd(st, E, c->pos.p, c->sender.p, c->receiver.p, c->shifts.p, c->species.p, c->bessel_w.p, c->zbl_z.p,
+                  c->zbl_cov.p, fp, c->geom.p, c->Y.p, c->ef.p, c->zbl_e.p);
+  launch_embed(st, N, c->species.p, c->embed.p, c->layers[0].din, c->h[0].p);
+  for (size_t l = 0; l < c->layers.size(); ++l) {
+    Layer& L = c->layers[l];
+    const float* h = c->h[l].p;
+    float* hn = c->h[l + 1].p;
+    launch_mlp_fwd(st, E, nb, L.wn, c->ef.p, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, L.mlp[3].p, L.w.p);
+    for (int b = 0; b < L.lin; ++b) {
+      LinearDesc D = lin_desc(2 * b + 1, NC, NC, L.din, NC * b * b, 0, L.din, NC * b * b, 0, 0);
+      launch_linear(st, N, D, h, L.up[b].p, L.h_up.p);
+    }
+    launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, L.w.p, L.h_up.p, c->M.p);
+    const int* l3 = tp_l3(L.lin);
+    const int* ao = tp_accoff(L.lin);
+    const int ns = n_tp_slots(L.lin);
+    for (int lo = 0; lo < 4; ++lo) {
+      int first = -1, cnt = 0;
+      for (int s = 0; s < ns; ++s)
+        if (l3[s] == lo) {
+          if (first < 0) first = s;
+          ++cnt;
+        }
+      const int d = 2 * lo + 1;
+      LinearDesc D = lin_desc(d, cnt * NC, NC, L.dmid, NC * ao[first], NC * d, L.dint, NC * lo * lo, 0, 0);
+      launch_linear(st, N, D, c->M.p, L.lin_[lo].p, L.A.p);
+    }
+    const float* scw[3] = {L.sc[0].p, L.sc[1].p, L.sc[2].p};
+    launch_sc_fwd(st, N, L.lhid, L.corr, L.A.p, L.dint, c->species.p, scw, c->B.p, L.dhid);
+    for (int b = 0; b < L.lhid; ++b) {
+      LinearDesc D = lin_desc(2 * b + 1, NC, NC, L.dhid, NC * b * b, 0, L.dhid, NC * b * b, 0, 0);
+      launch_linear(st, N, D, c->B.p, L.plin[b].p, hn);
+    }
+    for (int b = 0; b < L.nskip; ++b) run_skip(c, L, b, h, hn, L.dhid, 1);
+    if (l + 1 < c->layers.size())
+      launch_readout_linear(st, N, hn, L.dhid, L.ro.p, L.ro_e.p);
+    else
+      launch_readout_mlp(st, N, hn, L.dhid, L.ro1.p, L.ro2.p, L.ro_e.p, c->ypre.p);
+  }
+  const float* ro[4];
+  for (size_t l = 0; l < c->layers.size(); ++l) ro[l] = c->layers[l].ro_e.p;
+  launch_node_energy(st, N, c->species.p, c->e0.p, c->rowptr.p, c->dims.has_zbl ? c->zbl_e.p : nullptr, ro,
+                     (int)c->layers.size(), c->node_e.p, c->out.p);
+}
+
+void backward(mace_ctx* c, bool stress) {
+  hipStream_t st = c->stream;
+  const int N = c->N;
+  const int64_t E = c->E;
+  const int nb = c->dims.num_bessel;
+  const int L = (int)c->layers.size();
+  // dE/dh_L from the nonlinear readout
+  float* gh = c->gh0.p;
+  float* gh_next = c->gh1.p;
+  launch_readout_mlp_bwd(st, N, c->ypre.p, c->layers[L - 1].ro1.p, c->layers[L - 1].ro2.p, gh,
+                         c->layers[L - 1].dhid);
+  for (int l = L - 1; l >= 0; --l) {
+    Layer& Ly = c->layers[l];
+    // gB = PLin^T gh
+    for (int b = 0; b < Ly.lhid; ++b) {
+      LinearDesc D = lin_desc(2 * b + 1, NC, NC, Ly.dhid, NC * b * b, 0, Ly.dhid, NC * b * b, 0, 0);
+      launch_linear(st, N, D, gh, Ly.plinT[b].p, c->gB.p);
+    }
+    const float* scw[3] = {Ly.sc[0].p, Ly.sc[1].p, Ly.sc[2].p};
+    launch_sc_bwd(st, N, Ly.lhid, Ly.corr, Ly.A.p, Ly.dint, c->species.p, scw, c->gB.p, Ly.dhid, c->gA.p);
+    const int* l3 = tp_l3(Ly.lin);
+    const int* ao = tp_accoff(Ly.lin);
+    const int ns = n_tp_slots(Ly.lin);
+    for (int lo = 0; lo < 4; ++lo) {
+      int first = -1, cnt = 0;
+      for (int s = 0; s < ns; ++s)
+        if (l3[s] == lo) {
+          if (first < 0) first = s;
+          ++cnt;
+        }
+      const int d = 2 * lo + 1;
+      LinearDesc D = lin_desc(d, NC, cnt * NC, Ly.dint, NC * lo * lo, 0, Ly.dmid, NC * ao[first], NC * d, 0);
+      launch_linear(st, N, D, c->gA.p, Ly.linT[lo].p, c->gM.p);
+    }
+    const int first_edge_grad = (l == L - 1) ? 0 : 1;  // gY / gef: write on the first layer visited
+    if (l > 0) {
+      launch_tp_bwd_send(st, Ly.lin, N, c->rowptr_s.p, c->perm_s.p, c->receiver.p, c->Y.p, Ly.w.p, Ly.h_up.p,
+                         c->gM.p, c->gw.p, c->gY.p, c->gup.p, first_edge_grad);
+    } else {
+      launch_tp_bwd_recv(st, Ly.lin, N, c->rowptr.p, c->sender.p, c->Y.p, Ly.w.p, Ly.h_up.p, c->gM.p, c->gw.p,
+                         c->gY.p, first_edge_grad);
+    }
+    launch_mlp_bwd(st, E, nb, Ly.wn, c->ef.p, Ly.mlp[0].p, Ly.mlp[1].p, Ly.mlp[2].p, Ly.mlp[3].p, c->gw.p, c->gef.p,
+                   first_edge_grad);
+    if (l > 0) {
+      // dE/dh_l = Up^T gup + Skip^T gh + readout_{l-1}'
+      for (int b = 0; b < Ly.lin; ++b) {
+        LinearDesc D = lin_desc(2 * b + 1, NC, NC, Ly.din, NC * b * b, 0, Ly.din, NC * b * b, 0, 0);
+        launch_linear(st, N, D, c->gup.p, Ly.upT[b].p, gh_next);
+      }
+      for (int b = 0; b < Ly.nskip; ++b) run_skip_T(c, Ly, b, gh, Ly.dhid, gh_next);
+      launch_readout_linear_bwd(st, N, c->layers[l - 1].ro.p, gh_next, Ly.din, 1);
+      std::swap(gh, gh_next);
+    }
+  }
+  FrontParams fp = front_params(c);
+  const int nblk = (int)((E + 255) / 256);
+  launch_edge_bwd(st, E, c->sender.p, c->receiver.p, c->species.p, c->bessel_w.p, c->zbl_z.p, c->zbl_cov.p, fp,
+                  c->geom.p, c->gY.p, c->gef.p, c->gv.p, stress ? c->vir_part.p : nullptr, nblk);
+  launch_forces(st, N, c->rowptr.p, c->rowptr_s.p, c->perm_s.p, c->gv.p, c->out.p + 10);
+  if (stress) {
+    if (E > 0)
+      launch_virial_reduce(st, c->vir_part.p, nblk, c->out.p + 1);
+    else
+      HIPCHK(hipMemsetAsync(c->out.p + 1, 0, 9 * sizeof(double), st));
+  }
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+int mace_create(int32_t device, mace_ctx** out) {
+  if (!out) return MACE_ERR_INVALID;
+  *out = nullptr;
+  mace_ctx* c = new mace_ctx();
+  c->device = device;
+  int rc = guard(c, [&] {
+    int n = 0;
+    HIPCHK(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) fail(MACE_ERR_INVALID, "device %d out of range (%d devices)", device, n);
+    set_device(c);
+    HIPCHK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    for (auto& e : c->ev) HIPCHK(hipEventCreate(&e));
+  });
+  if (rc != MACE_OK) {
+    g_fail_msg = c->err;
+    delete c;
+    return rc;
+  }
+  *out = c;
+  return MACE_OK;
+}
+
+static void free_all(mace_ctx* c) {
+  for (auto& L : c->layers) {
+    for (auto* arr : {L.up, L.upT, L.skip, L.skipT, L.sc, L.plin, L.plinT})
+      for (int i = 0; i < 3; ++i) arr[i].release();
+    for (int i = 0; i < 4; ++i) L.mlp[i].release(), L.lin_[i].release(), L.linT[i].release();
+    L.ro.release(), L.ro1.release(), L.ro2.release(), L.h_up.release(), L.A.release(), L.w.release(),
+        L.ro_e.release();
+  }
+  for (auto& b : c->h) b.release();
+  for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->embed, &c->Y, &c->ef, &c->zbl_e, &c->gY, &c->gef,
+                  &c->gv, &c->gw, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup, &c->ypre,
+                  &c->node_e})
+    b->release();
+  for (auto* b : {&c->species, &c->sender, &c->receiver, &c->shifts, &c->rowptr, &c->rowptr_s, &c->perm_s,
+                  &c->nl_img, &c->nl_bin, &c->nl_bin_sorted, &c->nl_atoms, &c->nl_iota, &c->nl_counts,
+                  &c->nl_bin_count, &c->nl_bin_start, &c->e_tmp_i, &c->e_tmp_j, &c->e_tmp_s, &c->e_perm,
+                  &c->e_keys})
+    b->release();
+  c->pos.release();
+  c->nl_wpos.release();
+  c->vir_part.release();
+  c->out.release();
+  c->geom.release();
+  c->cub_tmp.release();
+  if (c->out_pinned) (void)hipHostFree(c->out_pinned);
+  if (c->ne_pinned) (void)hipHostFree(c->ne_pinned);
+  if (c->pos_pinned) (void)hipHostFree(c->pos_pinned);
+  c->out_pinned = nullptr;
+  c->ne_pinned = nullptr;
+  c->pos_pinned = nullptr;
+}
+
+void mace_destroy(mace_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  free_all(c);
+  for (auto& e : c->ev)
+    if (e) (void)hipEventDestroy(e);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+const char* mace_last_error(const mace_ctx* c) { return c ? c->err.c_str() : g_fail_msg.c_str(); }
+
+int mace_model_begin(mace_ctx* c, const mace_model_dims* dims) {
+  if (!c || !dims) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    c->dims = *dims;
+    c->host_tensors.clear();
+    c->model_ready = false;
+  });
+}
+
+int mace_model_set_tensor(mace_ctx* c, const char* name, const float* data, int64_t count) {
+  if (!c || !name || (count > 0 && !data) || count < 0) return MACE_ERR_INVALID;
+  return guard(c, [&] { c->host_tensors[name] = std::vector<float>(data, data + count); });
+}
+
+int mace_model_end(mace_ctx* c) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    set_device(c);
+    build_model(c);
+    if (c->system_ready) ensure_node_buffers(c);
+  });
+}
+
+int mace_set_system(mace_ctx* c, int32_t n, const int32_t* species, const double* cell9, const uint8_t* pbc3,
+                    double skin) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    if (!c->model_ready) fail(MACE_ERR_STATE, "model not loaded");
+    if (n < 0 || (n > 0 && !species) || !cell9 || !pbc3) fail(MACE_ERR_INVALID, "bad system arguments");
+    set_device(c);
+    for (int i = 0; i < n; ++i)
+      if (species[i] < 0 || species[i] >= c->dims.num_elements)
+        fail(MACE_ERR_SPECIES, "atom %d: species index %d outside [0, %d)", i, species[i], c->dims.num_elements);
+    bool topo_changed = (n != c->N) || !c->system_ready;
+    for (int k = 0; k < 3; ++k) topo_changed |= ((pbc3[k] != 0) != (c->pbc[k] != 0));
+    for (int k = 0; k < 9; ++k) topo_changed |= std::fabs(cell9[k] - c->cell[k]) > 1e-10;
+    topo_changed |= (skin != c->skin);
+    c->N = n;
+    c->skin = skin;
+    std::memcpy(c->cell, cell9, sizeof c->cell);
+    for (int k = 0; k < 3; ++k) c->pbc[k] = pbc3[k] ? 1 : 0;
+    ensure_node_buffers(c);
+    c->species.ensure(std::max(n, 1));
+    if (n > 0) HIPCHK(hipMemcpy(c->species.p, species, (size_t)n * sizeof(int), hipMemcpyHostToDevice));
+    c->species_h.assign(species, species + n);
+    if (topo_changed) {
+      c->nl_valid = false;
+      c->edges_manual = false;
+    }
+    c->system_ready = true;
+  });
+}
+
+int mace_set_edges(mace_ctx* c, int64_t E, const int32_t* sender, const int32_t* receiver, const int32_t* shifts3) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    if (!c->system_ready) fail(MACE_ERR_STATE, "system not set");
+    if (E < 0 || (E > 0 && (!sender || !receiver || !shifts3))) fail(MACE_ERR_INVALID, "bad edge arrays");
+    if (E > INT32_MAX / 4) fail(MACE_ERR_INVALID, "too many edges");
+    for (int64_t e = 0; e < E; ++e)
+      if (sender[e] < 0 || sender[e] >= c->N || receiver[e] < 0 || receiver[e] >= c->N)
+        fail(MACE_ERR_INVALID, "edge %lld references atom outside [0, %d)", (long long)e, c->N);
+    set_device(c);
+    c->E = E;
+    ensure_edge_index(c, E);
+    if (E > 0) {
+      HIPCHK(hipMemcpy(c->e_tmp_i.p, sender, E * sizeof(int), hipMemcpyHostToDevice));
+      HIPCHK(hipMemcpy(c->e_tmp_j.p, receiver, E * sizeof(int), hipMemcpyHostToDevice));
+      HIPCHK(hipMemcpy(c->e_tmp_s.p, shifts3, 3 * E * sizeof(int), hipMemcpyHostToDevice));
+      launch_fill_iota(c->stream, (int)E, c->nl_iota.p);
+      cub_sort_pairs(c, c->e_tmp_j.p, c->e_keys.p, c->nl_iota.p, c->e_perm.p, E, c->N);
+      hipLaunchKernelGGL(k_gather_edges, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, c->stream, E, c->e_perm.p,
+                         c->e_tmp_i.p, c->e_tmp_j.p, c->e_tmp_s.p, c->sender.p, c->receiver.p, c->shifts.p);
+    }
+    c->rowptr.ensure((size_t)c->N + 1);
+    build_rowptr(c, c->receiver.p, E, c->N, c->rowptr.p);
+    build_sender_csr(c);
+    ensure_edge_buffers(c, E);
+    HIPCHK(hipStreamSynchronize(c->stream));
+    c->nl_valid = true;
+    c->edges_manual = true;
+  });
+}
+
+int mace_get_edges(mace_ctx* c, int64_t cap, int32_t* sender, int32_t* receiver, int32_t* shifts3, int64_t* n_edges) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    if (!c->nl_valid) fail(MACE_ERR_STATE, "no edge list (call mace_step first)");
+    if (n_edges) *n_edges = c->E;
+    if (!sender && !receiver && !shifts3) return;
+    if (cap < c->E) fail(MACE_ERR_INVALID, "capacity %lld < %lld edges", (long long)cap, (long long)c->E);
+    set_device(c);
+    HIPCHK(hipStreamSynchronize(c->stream));
+    if (c->E > 0) {
+      if (sender) HIPCHK(hipMemcpy(sender, c->sender.p, c->E * sizeof(int), hipMemcpyDeviceToHost));
+      if (receiver) HIPCHK(hipMemcpy(receiver, c->receiver.p, c->E * sizeof(int), hipMemcpyDeviceToHost));
+      if (shifts3) HIPCHK(hipMemcpy(shifts3, c->shifts.p, 3 * c->E * sizeof(int), hipMemcpyDeviceToHost));
+    }
+  });
+}
+
+int mace_step(mace_ctx* c, const double* positions, uint32_t flags, double* energy, double* node_energy,
+              double* forces, double* virial9) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    if (!c->system_ready) fail(MACE_ERR_STATE, "system not set");
+    if (c->N > 0 && !positions) fail(MACE_ERR_INVALID, "positions is NULL");
+    if (!energy) fail(MACE_ERR_INVALID, "energy is NULL");
+    set_device(c);
+    const int N = c->N;
+    const bool stress = (flags & MACE_STEP_STRESS) != 0;
+    hipStream_t st = c->stream;
+    HIPCHK(hipEventRecord(c->ev[0], st));
+    std::memcpy(c->pos_pinned, positions, 3 * (size_t)N * sizeof(double));
+    if (N > 0) HIPCHK(hipMemcpyAsync(c->pos.p, c->pos_pinned, 3 * (size_t)N * sizeof(double), hipMemcpyHostToDevice, st));
+    // neighbour-list cache check (calculators.py:266-283)
+    bool rebuild = !c->nl_valid || (flags & MACE_STEP_FORCE_NL);
+    if (!rebuild && !c->edges_manual) {
+      if (c->skin <= 0) {
+        rebuild = true;
+      } else {
+        double maxd2 = 0;
+        for (int i = 0; i < N; ++i) {
+          double d2 = 0;
+          for (int k = 0; k < 3; ++k) {
+            const double d = positions[3 * i + k] - c->nl_pos[3 * i + k];
+            d2 += d * d;
+          }
+          maxd2 = std::max(maxd2, d2);
+        }
+        rebuild = std::sqrt(maxd2) > c->skin / 2;
+      }
+    }
+    if (c->edges_manual && (flags & MACE_STEP_FORCE_NL)) c->edges_manual = false;
+    c->last_nl = rebuild && !c->edges_manual;
+    if (c->last_nl) build_nl(c, positions);
+    HIPCHK(hipEventRecord(c->ev[1], st));
+    forward(c);
+    HIPCHK(hipEventRecord(c->ev[2], st));
+    backward(c, stress);
+    HIPCHK(hipEventRecord(c->ev[3], st));
+    HIPCHK(hipMemcpyAsync(c->out_pinned, c->out.p, (10 + 3 * (size_t)N) * sizeof(double), hipMemcpyDeviceToHost, st));
+    if (node_energy && N > 0)
+      HIPCHK(hipMemcpyAsync(c->ne_pinned, c->node_e.p, (size_t)N * sizeof(float), hipMemcpyDeviceToHost, st));
+    HIPCHK(hipEventRecord(c->ev[4], st));
+    HIPCHK(hipStreamSynchronize(st));
+    HIPCHK(hipGetLastError());
+    *energy = c->out_pinned[0];
+    if (virial9 && stress)
+      for (int a = 0; a < 3; ++a)
+        for (int b = 0; b < 3; ++b)
+          virial9[3 * a + b] = 0.5 * (c->out_pinned[1 + 3 * a + b] + c->out_pinned[1 + 3 * b + a]);
+    if (forces) std::memcpy(forces, c->out_pinned + 10, 3 * (size_t)N * sizeof(double));
+    if (node_energy)
+      for (int i = 0; i < N; ++i) node_energy[i] = (double)c->ne_pinned[i];
+    float ms[4];
+    HIPCHK(hipEventElapsedTime(&ms[0], c->ev[0], c->ev[4]));
+    HIPCHK(hipEventElapsedTime(&ms[1], c->ev[0], c->ev[1]));
+    HIPCHK(hipEventElapsedTime(&ms[2], c->ev[1], c->ev[2]));
+    HIPCHK(hipEventElapsedTime(&ms[3], c->ev[2], c->ev[3]));
+    for (int k = 0; k < 4; ++k) c->timings[k] = ms[k];
+    if (!c->last_nl) c->timings[1] = 0.0;
+  });
+}
+
+int mace_get_timings(const mace_ctx* c, double* out, int32_t n) {
+  if (!c || !out) return MACE_ERR_INVALID;
+  const int m = std::min<int32_t>(n, 4);
+  for (int k = 0; k < m; ++k) out[k] = c->timings[k];
+  return m;
+}
+
+}  // extern "C"

@@ -1,0 +1,134 @@
+// Internal declarations shared by the kernel translation units and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gen/tables.h"
+
+namespace mace {
+
+// Channel multiplicity of every irrep block.  The launchers check it at model
+// load time; all kernels are compiled for this width.
+constexpr int NC = 128;
+constexpr int NBESSEL_MAX = 16;
+constexpr int RADIAL_H = 64;   // radial-MLP hidden width compiled in
+
+// Node feature layout (all internal node tensors): blocks in irreps order,
+// inside a block the element (channel u, component m) sits at m * NC + u.
+__host__ __device__ constexpr int block_off(int l) { return NC * l * l; }  // blocks 0..l-1 dense
+
+struct EdgeGeom {        // per-edge record written by the front end
+  float x, y, z, r;
+};
+
+// ----------------------------------------------------------------------------
+// launchers (kernels_*.hip)
+// ----------------------------------------------------------------------------
+
+// edge front end: vectors, SH, radial features, ZBL edge energies
+struct FrontParams {
+  double cell[9];
+  float r_max;
+  float bessel_pref;     // sqrt(2 / r_max)
+  int nbessel;
+  int pcut;
+  int has_zbl;
+  int zbl_p;
+  float zbl_a_exp;
+  float zbl_a_pref;
+  float zbl_scale;
+};
+void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* sender,
+                     const int* receiver, const int* shifts, const int* species,
+                     const float* bessel_w, const float* zbl_z, const float* zbl_cov,
+                     const FrontParams& p, EdgeGeom* geom, float* Y, float* ef, float* zbl_e);
+void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver,
+                     const int* species, const float* bessel_w, const float* zbl_z,
+                     const float* zbl_cov, const FrontParams& p, const EdgeGeom* geom,
+                     const float* gY, const float* gef, float* gv, double* vir_part,
+                     int nblk_vir);
+
+// radial MLP: ef (E x nb) -> w (E x W); weights [in][out] row-major
+void launch_mlp_fwd(hipStream_t st, int64_t E, int nb, int W, const float* ef,
+                    const float* W0, const float* W1, const float* W2, const float* W3,
+                    float* w);
+void launch_mlp_bwd(hipStream_t st, int64_t E, int nb, int W, const float* ef,
+                    const float* W0, const float* W1, const float* W2, const float* W3,
+                    const float* gw, float* gef, int accumulate);
+
+// conv TP fused with the receiver-CSR scatter
+void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
+                   const float* Y, const float* w, const float* up, float* M);
+// TP VJP, receiver-centric (no input gradient; layer 0)
+void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
+                        const float* Y, const float* w, const float* up, const float* gM,
+                        float* gw, float* gY, int accumulate_gY);
+// TP VJP, sender-centric (input gradient gup; layers >= 1)
+void launch_tp_bwd_send(hipStream_t st, int lin, int N, const int* rowptr_s, const int* perm_s,
+                        const int* receiver, const float* Y, const float* w, const float* up,
+                        const float* gM, float* gw, float* gY, float* gup, int accumulate_gY);
+
+// node linear: Y[n, out_base + (c/NC)*out_stride + m*NC + c%NC] (+)=
+//   sum_k X[n, in_base + (k/NC)*in_stride + m*NC + k%NC] * W[k][c]
+struct LinearDesc {
+  int d;            // rows per node (2l+1)
+  int K, Cout;      // multiples of NC
+  int ldx, in_base, in_stride;
+  int ldy, out_base, out_stride;
+  int accumulate;   // 0: overwrite, 1: add into Y
+};
+void launch_linear(hipStream_t st, int N, const LinearDesc& d, const float* X, const float* W,
+                   float* Y);
+// per-species weights W[z][K][Cout] (skip connection with one-hot attributes)
+void launch_linear_species(hipStream_t st, int N, const LinearDesc& d, const float* X,
+                           const float* W, const int* species, float* Y);
+
+void launch_embed(hipStream_t st, int N, const int* species, const float* emb, int ld, float* h);
+
+// symmetric contraction (all output blocks of one product layer)
+void launch_sc_fwd(hipStream_t st, int N, int nout, int corr, const float* A, int ldA,
+                   const int* species, const float* const* Wsc, float* B, int ldB);
+void launch_sc_bwd(hipStream_t st, int N, int nout, int corr, const float* A, int ldA,
+                   const int* species, const float* const* Wsc, const float* gB, int ldB,
+                   float* gA);
+
+// readouts.  linear: e[n] = h[n, 0:NC] . w ; nonlinear: 16-wide SiLU MLP
+void launch_readout_linear(hipStream_t st, int N, const float* h, int ldh, const float* w,
+                           float* e);
+void launch_readout_mlp(hipStream_t st, int N, const float* h, int ldh, const float* W1,
+                        const float* W2, float* e, float* ypre);
+void launch_readout_mlp_bwd(hipStream_t st, int N, const float* ypre, const float* W1,
+                            const float* W2, float* gh, int ldh);
+void launch_readout_linear_bwd(hipStream_t st, int N, const float* w, float* gh, int ldh,
+                               int accumulate);
+
+void launch_node_energy(hipStream_t st, int N, const int* species, const float* e0,
+                        const int* rowptr, const float* zbl_e, const float* const* ro,
+                        int nro, float* node_e, double* energy);
+void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s,
+                   const int* perm_s, const float* gv, double* forces);
+void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir);
+
+// neighbour list
+struct NLParams {
+  double cell[9];       // effective cell (rows)
+  double inv[9];        // inverse of the effective cell
+  double origin[3];
+  int periodic[3];
+  int nbin[3];
+  int range[3];
+  double cutoff2;
+};
+void launch_nl_bin(hipStream_t st, int N, const double* pos, const NLParams& p, double* wpos,
+                   int* img, int* bin);
+void launch_nl_count(hipStream_t st, int N, const NLParams& p, const double* wpos,
+                     const int* bin, const int* bin_start, const int* bin_atoms, int* counts);
+void launch_nl_fill(hipStream_t st, int N, const NLParams& p, const double* wpos,
+                    const int* img, const int* bin, const int* bin_start, const int* bin_atoms,
+                    const int* rowptr, int* sender, int* receiver, int* shifts);
+void launch_fill_iota(hipStream_t st, int n, int* out);
+void launch_count_keys(hipStream_t st, int64_t E, const int* keys, int* counts);
+void launch_bin_start(hipStream_t st, int N, int nbins, const int* sorted_bins, int* bin_start);
+
+}  // namespace mace

@@ -1,0 +1,536 @@
+// Edge-parallel kernels: front end (geometry, spherical harmonics, radial basis,
+// ZBL), its VJP, the radial MLP forward/backward, and the device neighbour list.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace mace {
+
+namespace {
+
+constexpr float SQRT3 = 1.7320508075688772f;
+
+__device__ __forceinline__ float poly_env(float u, int p, float* denv) {
+  // envelope(u) = 1 - c1 u^p + c2 u^(p+1) - c3 u^(p+2) for u < 1, else 0
+  // (radial.py:18-34); also returns d envelope / du.
+  if (!(u < 1.0f)) {
+    *denv = 0.f;
+    return 0.f;
+  }
+  const float pf = (float)p;
+  const float c1 = (pf + 1.f) * (pf + 2.f) * 0.5f, c2 = pf * (pf + 2.f), c3 = pf * (pf + 1.f) * 0.5f;
+  float up1 = 1.f;  // u^(p-1)
+  for (int i = 0; i < p - 1; ++i) up1 *= u;
+  const float up = up1 * u;
+  *denv = -c1 * pf * up1 + c2 * (pf + 1.f) * up - c3 * (pf + 2.f) * up * u;
+  return 1.f - c1 * up + c2 * up * u - c3 * up * u * u;
+}
+
+__device__ __forceinline__ void sh16(float ux, float uy, float uz, float* Y) {
+  Y[0] = 1.f;
+  Y[1] = SQRT3 * ux;
+  Y[2] = SQRT3 * uy;
+  Y[3] = SQRT3 * uz;
+#pragma unroll
+  for (int k = 4; k < 16; ++k) Y[k] = 0.f;
+#pragma unroll
+  for (int t = 0; t < SH2_NT; ++t) Y[4 + SH2_K[t]] += SH2_V[t] * Y[1 + SH2_I[t]] * Y[1 + SH2_J[t]];
+#pragma unroll
+  for (int t = 0; t < SH3_NT; ++t) Y[9 + SH3_K[t]] += SH3_V[t] * Y[4 + SH3_I[t]] * Y[1 + SH3_J[t]];
+}
+
+__device__ __forceinline__ void edge_vec(const double* __restrict__ pos, const int* __restrict__ sh,
+                                         const double* cell, int s, int r, int64_t e, float& x,
+                                         float& y, float& z) {
+  const double S0 = sh[3 * e], S1 = sh[3 * e + 1], S2 = sh[3 * e + 2];
+  x = (float)(pos[3 * r] - pos[3 * s] + S0 * cell[0] + S1 * cell[3] + S2 * cell[6]);
+  y = (float)(pos[3 * r + 1] - pos[3 * s + 1] + S0 * cell[1] + S1 * cell[4] + S2 * cell[7]);
+  z = (float)(pos[3 * r + 2] - pos[3 * s + 2] + S0 * cell[2] + S1 * cell[5] + S2 * cell[8]);
+}
+
+__device__ __forceinline__ float zbl_phi(float x, float* dphi) {
+  const float e0 = expf(-3.2f * x), e1 = expf(-0.9423f * x), e2 = expf(-0.4028f * x),
+              e3 = expf(-0.2016f * x);
+  *dphi = -3.2f * 0.1818f * e0 - 0.9423f * 0.5099f * e1 - 0.4028f * 0.2802f * e2 -
+          0.2016f * 0.02817f * e3;
+  return 0.1818f * e0 + 0.5099f * e1 + 0.2802f * e2 + 0.02817f * e3;
+}
+
+__global__ void __launch_bounds__(256) k_edge_fwd(
+    int64_t E, const double* __restrict__ pos, const int* __restrict__ sender,
+    const int* __restrict__ receiver, const int* __restrict__ shifts, const int* __restrict__ species,
+    const float* __restrict__ bessel_w, const float* __restrict__ zbl_z,
+    const float* __restrict__ zbl_cov, FrontParams p, EdgeGeom* __restrict__ geom,
+    float* __restrict__ Y, float* __restrict__ ef, float* __restrict__ zbl_e) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const int s = sender[e], r = receiver[e];
+  float x, y, z;
+  edge_vec(pos, shifts, p.cell, s, r, e, x, y, z);
+  const float rr = sqrtf(fmaxf(x * x + y * y + z * z, 1e-24f));
+  geom[e] = EdgeGeom{x, y, z, rr};
+  const float inv = 1.f / rr;
+  float Yl[16];
+  sh16(x * inv, y * inv, z * inv, Yl);
+  float4* Y4 = reinterpret_cast<float4*>(Y + 16 * e);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) Y4[q] = make_float4(Yl[4 * q], Yl[4 * q + 1], Yl[4 * q + 2], Yl[4 * q + 3]);
+  float denv;
+  const float env = poly_env(rr / p.r_max, p.pcut, &denv);
+  for (int n = 0; n < p.nbessel; ++n) {
+    const float w = bessel_w[n];
+    const float b = (rr == 0.f) ? p.bessel_pref * w : p.bessel_pref * sinf(w * rr) / rr;
+    ef[(int64_t)p.nbessel * e + n] = b * env;
+  }
+  if (p.has_zbl) {
+    const int zs = species[s], zr = species[r];
+    const float Zu = zbl_z[zs], Zv = zbl_z[zr];
+    const float a = p.zbl_a_pref * 0.529f / (powf(Zu, p.zbl_a_exp) + powf(Zv, p.zbl_a_exp));
+    float dphi;
+    const float phi = zbl_phi(rr / a, &dphi);
+    const float rmax = zbl_cov[zs] + zbl_cov[zr];
+    float dz;
+    const float envz = poly_env(rr / rmax, p.zbl_p, &dz);
+    zbl_e[e] = p.zbl_scale * 0.5f * (14.3996f * Zu * Zv) / rr * phi * envz;
+  }
+}
+
+__global__ void __launch_bounds__(256) k_edge_bwd(
+    int64_t E, const int* __restrict__ sender, const int* __restrict__ receiver,
+    const int* __restrict__ species, const float* __restrict__ bessel_w,
+    const float* __restrict__ zbl_z, const float* __restrict__ zbl_cov, FrontParams p,
+    const EdgeGeom* __restrict__ geom, const float* __restrict__ gY, const float* __restrict__ gef,
+    float* __restrict__ gv, double* __restrict__ vir_part) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  double vir[9];
+#pragma unroll
+  for (int k = 0; k < 9; ++k) vir[k] = 0.0;
+  if (e < E) {
+    const EdgeGeom g = geom[e];
+    const float rr = g.r;
+    const float inv = 1.f / rr;
+    const float ux = g.x * inv, uy = g.y * inv, uz = g.z * inv;
+    float Yl[16];
+    sh16(ux, uy, uz, Yl);
+    float G[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) G[k] = gY[16 * e + k];
+    // reverse through the recursion (l = 3, then l = 2)
+#pragma unroll
+    for (int t = 0; t < SH3_NT; ++t) {
+      const float gk = G[9 + SH3_K[t]] * SH3_V[t];
+      G[4 + SH3_I[t]] += gk * Yl[1 + SH3_J[t]];
+      G[1 + SH3_J[t]] += gk * Yl[4 + SH3_I[t]];
+    }
+#pragma unroll
+    for (int t = 0; t < SH2_NT; ++t) {
+      const float gk = G[4 + SH2_K[t]] * SH2_V[t];
+      G[1 + SH2_I[t]] += gk * Yl[1 + SH2_J[t]];
+      G[1 + SH2_J[t]] += gk * Yl[1 + SH2_I[t]];
+    }
+    const float gux = SQRT3 * G[1], guy = SQRT3 * G[2], guz = SQRT3 * G[3];
+    const float dot = gux * ux + guy * uy + guz * uz;
+    float gx = (gux - dot * ux) * inv, gy = (guy - dot * uy) * inv, gz = (guz - dot * uz) * inv;
+    // radial part
+    float denv;
+    const float env = poly_env(rr / p.r_max, p.pcut, &denv);
+    float gr = 0.f;
+    for (int n = 0; n < p.nbessel; ++n) {
+      const float w = bessel_w[n];
+      float b, db;
+      if (rr == 0.f) {
+        b = p.bessel_pref * w;
+        db = 0.f;
+      } else {
+        float sn, cs;
+        sincosf(w * rr, &sn, &cs);
+        b = p.bessel_pref * sn / rr;
+        db = p.bessel_pref * (w * cs * rr - sn) / (rr * rr);
+      }
+      gr += gef[(int64_t)p.nbessel * e + n] * (db * env + b * denv / p.r_max);
+    }
+    if (p.has_zbl) {
+      const int zs = species[sender[e]], zr = species[receiver[e]];
+      const float Zu = zbl_z[zs], Zv = zbl_z[zr];
+      const float a = p.zbl_a_pref * 0.529f / (powf(Zu, p.zbl_a_exp) + powf(Zv, p.zbl_a_exp));
+      float dphi;
+      const float phi = zbl_phi(rr / a, &dphi);
+      const float rmax = zbl_cov[zs] + zbl_cov[zr];
+      float dz;
+      const float envz = poly_env(rr / rmax, p.zbl_p, &dz);
+      const float K = p.zbl_scale * 0.5f * 14.3996f * Zu * Zv;
+      gr += K * ((dphi / a) / rr * envz - phi / (rr * rr) * envz + phi / rr * dz / rmax);
+    }
+    gx += gr * ux;
+    gy += gr * uy;
+    gz += gr * uz;
+    gv[3 * e] = gx;
+    gv[3 * e + 1] = gy;
+    gv[3 * e + 2] = gz;
+    const float v[3] = {g.x, g.y, g.z}, gg[3] = {gx, gy, gz};
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int b = 0; b < 3; ++b) vir[3 * a + b] = (double)v[a] * (double)gg[b];
+  }
+  if (vir_part == nullptr) return;
+  __shared__ double red[9][256];
+#pragma unroll
+  for (int k = 0; k < 9; ++k) red[k][threadIdx.x] = vir[k];
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if ((int)threadIdx.x < off)
+#pragma unroll
+      for (int k = 0; k < 9; ++k) red[k][threadIdx.x] += red[k][threadIdx.x + off];
+    __syncthreads();
+  }
+  if (threadIdx.x < 9) vir_part[9 * blockIdx.x + threadIdx.x] = red[threadIdx.x][0];
+}
+
+// ---------------------------------------------------------------------------
+// radial MLP: edge tiles, hidden activations in LDS
+// ---------------------------------------------------------------------------
+constexpr int TE = 64;    // forward tile
+constexpr int TEB = 32;   // backward tile (more live LDS arrays)
+constexpr int HP = RADIAL_H + 4;  // padded row (keeps float4 alignment)
+
+__device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
+__device__ __forceinline__ float dsilu(float x) {
+  const float s = 1.f / (1.f + expf(-x));
+  return s * (1.f + x * (1.f - s));
+}
+
+// out[e][j] = sum_k in[e][k] W[k][j] over a T x 64 tile (W row-major [K][64]);
+// thread: column j = t & 63, rows (T/4)*(t >> 6) .. +T/4.  Writes the
+// pre-activation into pre (if not null) and silu(.) into out.
+template <int T>
+__device__ __forceinline__ void dense64(const float (*in)[HP], int K, const float* __restrict__ W,
+                                        float (*pre)[HP], float (*out)[HP]) {
+  constexpr int R = T / 4;
+  const int j = threadIdx.x & 63, r0 = (threadIdx.x >> 6) * R;
+  float acc[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) acc[i] = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const float w = W[k * RADIAL_H + j];
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = fmaf(in[r0 + i][k], w, acc[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    if (pre) pre[r0 + i][j] = acc[i];
+    out[r0 + i][j] = silu(acc[i]);
+  }
+}
+
+__global__ void __launch_bounds__(256) k_mlp_fwd(int64_t E, int nb, int W, const float* __restrict__ ef,
+                                                 const float* __restrict__ W0, const float* __restrict__ W1,
+                                                 const float* __restrict__ W2, const float* __restrict__ W3,
+                                                 float* __restrict__ w) {
+  __shared__ __align__(16) float sA[TE][HP];
+  __shared__ __align__(16) float sB[TE][HP];
+  const int64_t e0 = (int64_t)blockIdx.x * TE;
+  const int t = threadIdx.x;
+  for (int i = t; i < TE * nb; i += 256) {
+    const int e = i / nb, k = i % nb;
+    sA[e][k] = (e0 + e < E) ? ef[(e0 + e) * nb + k] : 0.f;
+  }
+  __syncthreads();
+  dense64<TE>(sA, nb, W0, nullptr, sB);
+  __syncthreads();
+  dense64<TE>(sB, RADIAL_H, W1, nullptr, sA);
+  __syncthreads();
+  dense64<TE>(sA, RADIAL_H, W2, nullptr, sB);
+  __syncthreads();
+  // last layer: each thread one output column at a time, all TE rows
+  for (int j = t; j < W; j += 256) {
+    float acc[TE];
+#pragma unroll
+    for (int i = 0; i < TE; ++i) acc[i] = 0.f;
+    for (int k = 0; k < RADIAL_H; k += 4) {
+      const float w0 = W3[(k + 0) * W + j], w1 = W3[(k + 1) * W + j], w2 = W3[(k + 2) * W + j],
+                  w3 = W3[(k + 3) * W + j];
+#pragma unroll
+      for (int i = 0; i < TE; ++i) {
+        const float4 h = *reinterpret_cast<const float4*>(&sB[i][k]);
+        acc[i] = fmaf(h.w, w3, fmaf(h.z, w2, fmaf(h.y, w1, fmaf(h.x, w0, acc[i]))));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < TE; ++i)
+      if (e0 + i < E) w[(e0 + i) * W + j] = acc[i];
+  }
+}
+
+__global__ void __launch_bounds__(256) k_mlp_bwd(int64_t E, int nb, int W, const float* __restrict__ ef,
+                                                 const float* __restrict__ W0, const float* __restrict__ W1,
+                                                 const float* __restrict__ W2, const float* __restrict__ W3,
+                                                 const float* __restrict__ gw, float* __restrict__ gef,
+                                                 int accumulate) {
+  constexpr int R = TEB / 4;
+  __shared__ __align__(16) float sIn[TEB][HP];
+  __shared__ __align__(16) float sP1[TEB][HP], sP2[TEB][HP], sP3[TEB][HP];
+  __shared__ __align__(16) float sH[64][HP];   // activations, later W3 tiles (64 rows)
+  __shared__ __align__(16) float sG[TEB][HP];
+  const int64_t e0 = (int64_t)blockIdx.x * TEB;
+  const int t = threadIdx.x;
+  for (int i = t; i < TEB * nb; i += 256) {
+    const int e = i / nb, k = i % nb;
+    sIn[e][k] = (e0 + e < E) ? ef[(e0 + e) * nb + k] : 0.f;
+  }
+  __syncthreads();
+  // recompute the forward pre-activations a1, a2, a3
+  dense64<TEB>(sIn, nb, W0, sP1, sH);
+  __syncthreads();
+  dense64<TEB>(sH, RADIAL_H, W1, sP2, sG);
+  __syncthreads();
+  dense64<TEB>(sG, RADIAL_H, W2, sP3, sH);
+  __syncthreads();
+  const int k = t & 63, r0 = (t >> 6) * R;
+  // g_h3[e][k] = sum_j gw[e][j] W3[k][j]
+  {
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = 0.f;
+    for (int j0 = 0; j0 < W; j0 += 64) {
+      __syncthreads();
+      for (int i = t; i < TEB * 64; i += 256) {
+        const int e = i >> 6, c = i & 63;
+        sG[e][c] = (e0 + e < E && j0 + c < W) ? gw[(e0 + e) * W + j0 + c] : 0.f;
+      }
+      for (int i = t; i < 64 * 64; i += 256) {
+        const int kk = i >> 6, c = i & 63;
+        sH[kk][c] = (j0 + c < W) ? W3[kk * W + j0 + c] : 0.f;
+      }
+      __syncthreads();
+      for (int c = 0; c < 64; c += 4) {
+        const float4 wk = *reinterpret_cast<const float4*>(&sH[k][c]);
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+          const float4 g = *reinterpret_cast<const float4*>(&sG[r0 + i][c]);
+          acc[i] = fmaf(g.w, wk.w, fmaf(g.z, wk.z, fmaf(g.y, wk.y, fmaf(g.x, wk.x, acc[i]))));
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < R; ++i) sG[r0 + i][k] = acc[i] * dsilu(sP3[r0 + i][k]);  // g_a3
+  }
+  __syncthreads();
+  // g_a2 = (g_a3 @ W2^T) * silu'(a2); g_a1 = (g_a2 @ W1^T) * silu'(a1)
+  for (int layer = 0; layer < 2; ++layer) {
+    const float* Wl = layer == 0 ? W2 : W1;
+    float(*P)[HP] = layer == 0 ? sP2 : sP1;
+    float acc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) acc[i] = 0.f;
+    for (int j = 0; j < RADIAL_H; ++j) {
+      const float w = Wl[k * RADIAL_H + j];
+#pragma unroll
+      for (int i = 0; i < R; ++i) acc[i] = fmaf(sG[r0 + i][j], w, acc[i]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < R; ++i) sG[r0 + i][k] = acc[i] * dsilu(P[r0 + i][k]);
+    __syncthreads();
+  }
+  // g_ef[e][k] = sum_j g_a1[e][j] W0[k][j]
+  for (int i = t; i < TEB * nb; i += 256) {
+    const int e = i / nb, kk = i % nb;
+    if (e0 + e >= E) continue;
+    float acc = 0.f;
+    for (int j = 0; j < RADIAL_H; ++j) acc = fmaf(sG[e][j], W0[kk * RADIAL_H + j], acc);
+    float* dst = gef + (e0 + e) * nb + kk;
+    *dst = accumulate ? *dst + acc : acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// neighbour list
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int floordiv(int a, int b) {
+  int q = a / b;
+  if ((a % b != 0) && ((a < 0) != (b < 0))) --q;
+  return q;
+}
+
+__global__ void k_nl_bin(int N, const double* __restrict__ pos, NLParams p, double* __restrict__ wpos,
+                         int* __restrict__ img, int* __restrict__ bin) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  const double d0 = pos[3 * i] - p.origin[0], d1 = pos[3 * i + 1] - p.origin[1],
+               d2 = pos[3 * i + 2] - p.origin[2];
+  double f[3], w[3];
+  int b[3];
+  for (int k = 0; k < 3; ++k) {
+    f[k] = d0 * p.inv[0 * 3 + k] + d1 * p.inv[1 * 3 + k] + d2 * p.inv[2 * 3 + k];
+    int n = 0;
+    if (p.periodic[k]) {
+      n = (int)floor(f[k]);
+      w[k] = f[k] - (double)n;
+      if (w[k] >= 1.0) {  // rounding guard
+        w[k] -= 1.0;
+        n += 1;
+      }
+    } else {
+      w[k] = f[k];
+    }
+    img[3 * i + k] = n;
+    int bk = (int)floor(w[k] * p.nbin[k]);
+    bk = bk < 0 ? 0 : (bk >= p.nbin[k] ? p.nbin[k] - 1 : bk);
+    b[k] = bk;
+  }
+  for (int k = 0; k < 3; ++k)
+    wpos[3 * i + k] = w[0] * p.cell[0 * 3 + k] + w[1] * p.cell[1 * 3 + k] + w[2] * p.cell[2 * 3 + k];
+  bin[i] = (b[0] * p.nbin[1] + b[1]) * p.nbin[2] + b[2];
+}
+
+template <bool FILL>
+__device__ __forceinline__ int nl_visit(int j, const NLParams& p, const double* __restrict__ wpos,
+                                        const int* __restrict__ img, const int* __restrict__ bin,
+                                        const int* __restrict__ bin_start,
+                                        const int* __restrict__ bin_atoms, int out0,
+                                        int* __restrict__ sender, int* __restrict__ receiver,
+                                        int* __restrict__ shifts) {
+  const int bj = bin[j];
+  const int b2 = bj % p.nbin[2], b1 = (bj / p.nbin[2]) % p.nbin[1], b0 = bj / (p.nbin[2] * p.nbin[1]);
+  const double xj = wpos[3 * j], yj = wpos[3 * j + 1], zj = wpos[3 * j + 2];
+  int cnt = 0;
+  for (int o0 = -p.range[0]; o0 <= p.range[0]; ++o0) {
+    int c0 = b0 + o0, T0 = 0;
+    if (p.periodic[0]) { T0 = floordiv(c0, p.nbin[0]); c0 -= T0 * p.nbin[0]; }
+    else if (c0 < 0 || c0 >= p.nbin[0]) continue;
+    for (int o1 = -p.range[1]; o1 <= p.range[1]; ++o1) {
+      int c1 = b1 + o1, T1 = 0;
+      if (p.periodic[1]) { T1 = floordiv(c1, p.nbin[1]); c1 -= T1 * p.nbin[1]; }
+      else if (c1 < 0 || c1 >= p.nbin[1]) continue;
+      for (int o2 = -p.range[2]; o2 <= p.range[2]; ++o2) {
+        int c2 = b2 + o2, T2 = 0;
+        if (p.periodic[2]) { T2 = floordiv(c2, p.nbin[2]); c2 -= T2 * p.nbin[2]; }
+        else if (c2 < 0 || c2 >= p.nbin[2]) continue;
+        const double tx = T0 * p.cell[0] + T1 * p.cell[3] + T2 * p.cell[6];
+        const double ty = T0 * p.cell[1] + T1 * p.cell[4] + T2 * p.cell[7];
+        const double tz = T0 * p.cell[2] + T1 * p.cell[5] + T2 * p.cell[8];
+        const int cb = (c0 * p.nbin[1] + c1) * p.nbin[2] + c2;
+        for (int q = bin_start[cb]; q < bin_start[cb + 1]; ++q) {
+          const int i = bin_atoms[q];
+          if (i == j && T0 == 0 && T1 == 0 && T2 == 0) continue;
+          // image of atom i at wpos_i + T.cell; D = x_j - x_i(image)
+          const double dx = xj - (wpos[3 * i] + tx), dy = yj - (wpos[3 * i + 1] + ty),
+                       dz = zj - (wpos[3 * i + 2] + tz);
+          if (dx * dx + dy * dy + dz * dz < p.cutoff2) {
+            if (FILL) {
+              const int o = out0 + cnt;
+              sender[o] = i;
+              receiver[o] = j;
+              // D = x_j - x_i + S.cell with x = wpos + img.cell  =>  S = -T - img_j + img_i
+              shifts[3 * o + 0] = -T0 - img[3 * j + 0] + img[3 * i + 0];
+              shifts[3 * o + 1] = -T1 - img[3 * j + 1] + img[3 * i + 1];
+              shifts[3 * o + 2] = -T2 - img[3 * j + 2] + img[3 * i + 2];
+            }
+            ++cnt;
+          }
+        }
+      }
+    }
+  }
+  return cnt;
+}
+
+__global__ void k_nl_count(int N, NLParams p, const double* __restrict__ wpos, const int* __restrict__ bin,
+                           const int* __restrict__ bin_start, const int* __restrict__ bin_atoms,
+                           int* __restrict__ counts) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= N) return;
+  counts[j] = nl_visit<false>(j, p, wpos, nullptr, bin, bin_start, bin_atoms, 0, nullptr, nullptr, nullptr);
+}
+
+__global__ void k_nl_fill(int N, NLParams p, const double* __restrict__ wpos, const int* __restrict__ img,
+                          const int* __restrict__ bin, const int* __restrict__ bin_start,
+                          const int* __restrict__ bin_atoms, const int* __restrict__ rowptr,
+                          int* __restrict__ sender, int* __restrict__ receiver, int* __restrict__ shifts) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= N) return;
+  nl_visit<true>(j, p, wpos, img, bin, bin_start, bin_atoms, rowptr[j], sender, receiver, shifts);
+}
+
+__global__ void k_iota(int n, int* out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = i;
+}
+
+__global__ void k_count_keys(int64_t E, const int* __restrict__ keys, int* __restrict__ counts) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < E) atomicAdd(&counts[keys[e]], 1);  // integer counts: order-independent
+}
+
+}  // namespace
+
+static inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
+
+void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* sender, const int* receiver,
+                     const int* shifts, const int* species, const float* bessel_w, const float* zbl_z,
+                     const float* zbl_cov, const FrontParams& p, EdgeGeom* geom, float* Y, float* ef,
+                     float* zbl_e) {
+  if (E <= 0) return;
+  hipLaunchKernelGGL(k_edge_fwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, pos, sender, receiver, shifts,
+                     species, bessel_w, zbl_z, zbl_cov, p, geom, Y, ef, zbl_e);
+}
+
+void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,
+                     const float* bessel_w, const float* zbl_z, const float* zbl_cov, const FrontParams& p,
+                     const EdgeGeom* geom, const float* gY, const float* gef, float* gv, double* vir_part,
+                     int nblk_vir) {
+  if (E <= 0) return;
+  (void)nblk_vir;
+  hipLaunchKernelGGL(k_edge_bwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, sender, receiver, species,
+                     bessel_w, zbl_z, zbl_cov, p, geom, gY, gef, gv, vir_part);
+}
+
+void launch_mlp_fwd(hipStream_t st, int64_t E, int nb, int W, const float* ef, const float* W0,
+                    const float* W1, const float* W2, const float* W3, float* w) {
+  if (E <= 0) return;
+  hipLaunchKernelGGL(k_mlp_fwd, dim3(nblk(E, TE)), dim3(256), 0, st, E, nb, W, ef, W0, W1, W2, W3, w);
+}
+
+void launch_mlp_bwd(hipStream_t st, int64_t E, int nb, int W, const float* ef, const float* W0,
+                    const float* W1, const float* W2, const float* W3, const float* gw, float* gef,
+                    int accumulate) {
+  if (E <= 0) return;
+  hipLaunchKernelGGL(k_mlp_bwd, dim3(nblk(E, TEB)), dim3(256), 0, st, E, nb, W, ef, W0, W1, W2, W3, gw, gef,
+                     accumulate);
+}
+
+void launch_nl_bin(hipStream_t st, int N, const double* pos, const NLParams& p, double* wpos, int* img,
+                   int* bin) {
+  if (N <= 0) return;
+  hipLaunchKernelGGL(k_nl_bin, dim3(nblk(N, 256)), dim3(256), 0, st, N, pos, p, wpos, img, bin);
+}
+
+void launch_nl_count(hipStream_t st, int N, const NLParams& p, const double* wpos, const int* bin,
+                     const int* bin_start, const int* bin_atoms, int* counts) {
+  if (N <= 0) return;
+  hipLaunchKernelGGL(k_nl_count, dim3(nblk(N, 128)), dim3(128), 0, st, N, p, wpos, bin, bin_start, bin_atoms,
+                     counts);
+}
+
+void launch_nl_fill(hipStream_t st, int N, const NLParams& p, const double* wpos, const int* img,
+                    const int* bin, const int* bin_start, const int* bin_atoms, const int* rowptr,
+                    int* sender, int* receiver, int* shifts) {
+  if (N <= 0) return;
+  hipLaunchKernelGGL(k_nl_fill, dim3(nblk(N, 128)), dim3(128), 0, st, N, p, wpos, img, bin, bin_start,
+                     bin_atoms, rowptr, sender, receiver, shifts);
+}
+
+void launch_fill_iota(hipStream_t st, int n, int* out) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_iota, dim3(nblk(n, 256)), dim3(256), 0, st, n, out);
+}
+
+void launch_count_keys(hipStream_t st, int64_t E, const int* keys, int* counts) {
+  if (E <= 0) return;
+  hipLaunchKernelGGL(k_count_keys, dim3(nblk(E, 256)), dim3(256), 0, st, E, keys, counts);
+}
+
+}  // namespace mace

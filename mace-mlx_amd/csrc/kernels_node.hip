@@ -1,0 +1,410 @@
+// Node-parallel kernels: irrep-wise linears, the species-gathered skip
+// connection, node embedding, symmetric contraction (+VJP), readouts, energy
+// assembly and the deterministic force / virial reductions.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace mace {
+namespace {
+
+// ---------------------------------------------------------------------------
+// linear: rows (n, m), 64 x 64 output tiles, K staged 32 at a time through LDS
+// ---------------------------------------------------------------------------
+constexpr int LT = 64, LK = 32;
+
+__device__ __forceinline__ int64_t lin_in_addr(const LinearDesc& D, int row, int k) {
+  const int n = row / D.d, m = row - n * D.d;
+  return (int64_t)n * D.ldx + D.in_base + (k / NC) * D.in_stride + m * NC + (k % NC);
+}
+__device__ __forceinline__ int64_t lin_out_addr(const LinearDesc& D, int row, int c) {
+  const int n = row / D.d, m = row - n * D.d;
+  return (int64_t)n * D.ldy + D.out_base + (c / NC) * D.out_stride + m * NC + (c % NC);
+}
+
+__global__ void __launch_bounds__(256) k_linear(int rows, LinearDesc D, const float* __restrict__ X,
+                                                const float* __restrict__ W, float* __restrict__ Yo) {
+  __shared__ __align__(16) float sA[LK][LT + 4];
+  __shared__ __align__(16) float sB[LK][LT + 4];
+  const int t = threadIdx.x;
+  const int row0 = blockIdx.x * LT, col0 = blockIdx.y * LT;
+  const int tr = t >> 4, tc = t & 15;
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+  for (int k0 = 0; k0 < D.K; k0 += LK) {
+    __syncthreads();
+    // A tile: 64 rows x 32 k (coalesced along k)
+#pragma unroll
+    for (int q = 0; q < (LT * LK) / 256; ++q) {
+      const int idx = t + 256 * q;
+      const int k = idx & (LK - 1), r = idx / LK;
+      const int row = row0 + r;
+      sA[k][r] = (row < rows) ? X[lin_in_addr(D, row, k0 + k)] : 0.f;
+    }
+    // B tile: 32 k x 64 cols
+#pragma unroll
+    for (int q = 0; q < (LT * LK) / 256; ++q) {
+      const int idx = t + 256 * q;
+      const int c = idx & (LT - 1), k = idx / LT;
+      sB[k][c] = W[(int64_t)(k0 + k) * D.Cout + col0 + c];
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int k = 0; k < LK; ++k) {
+      const float4 a = *reinterpret_cast<const float4*>(&sA[k][tr * 4]);
+      const float4 b = *reinterpret_cast<const float4*>(&sB[k][tc * 4]);
+      const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + tr * 4 + i;
+    if (row >= rows) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t o = lin_out_addr(D, row, col0 + tc * 4 + j);
+      Yo[o] = D.accumulate ? Yo[o] + acc[i][j] : acc[i][j];
+    }
+  }
+}
+
+// per-species weights: one thread per (row, output column)
+__global__ void __launch_bounds__(NC) k_linear_species(int rows, LinearDesc D, const float* __restrict__ X,
+                                                       const float* __restrict__ W, const int* __restrict__ species,
+                                                       float* __restrict__ Yo) {
+  const int row = blockIdx.x;
+  const int c = blockIdx.y * NC + threadIdx.x;
+  const int n = row / D.d;
+  const float* Wz = W + (int64_t)species[n] * D.K * D.Cout;
+  float acc = 0.f;
+  for (int k = 0; k < D.K; ++k) acc = fmaf(X[lin_in_addr(D, row, k)], Wz[(int64_t)k * D.Cout + c], acc);
+  const int64_t o = lin_out_addr(D, row, c);
+  Yo[o] = D.accumulate ? Yo[o] + acc : acc;
+}
+
+__global__ void k_embed(int N, const int* __restrict__ species, const float* __restrict__ emb, int ld,
+                        float* __restrict__ h) {
+  const int n = blockIdx.x, u = threadIdx.x;
+  h[(int64_t)n * ld + u] = emb[species[n] * NC + u];
+}
+
+// ---------------------------------------------------------------------------
+// symmetric contraction: thread = (node, channel); generated polynomials
+// ---------------------------------------------------------------------------
+struct ScW {
+  const float* w[3];
+};
+
+template <int LOUT, int CORR>
+struct ScPoly;
+#define MACE_SC(L, C)                                                                              \
+  template <>                                                                                      \
+  struct ScPoly<L, C> {                                                                            \
+    static constexpr int KT = SC_L##L##_C##C##_KT;                                                 \
+    __device__ static void fwd(const float* f, const float* w, float* o) { sc_l##L##_c##C##_fwd(f, w, o); } \
+    __device__ static void vjp(const float* f, const float* w, const float* go, float* g) {       \
+      sc_l##L##_c##C##_vjp(f, w, go, g);                                                           \
+    }                                                                                              \
+  };
+MACE_SC(0, 1) MACE_SC(0, 2) MACE_SC(0, 3)
+MACE_SC(1, 1) MACE_SC(1, 2) MACE_SC(1, 3)
+MACE_SC(2, 1) MACE_SC(2, 2) MACE_SC(2, 3)
+#undef MACE_SC
+
+template <int LOUT, int CORR>
+__device__ __forceinline__ void sc_block_fwd(const float* f, const float* __restrict__ Wl, int z, int c,
+                                             float* __restrict__ Bn) {
+  using P = ScPoly<LOUT, CORR>;
+  float w[P::KT];
+  const float* wz = Wl + (int64_t)z * P::KT * NC + c;
+#pragma unroll
+  for (int k = 0; k < P::KT; ++k) w[k] = wz[k * NC];
+  float o[2 * LOUT + 1];
+  P::fwd(f, w, o);
+#pragma unroll
+  for (int m = 0; m < 2 * LOUT + 1; ++m) Bn[NC * (LOUT * LOUT + m) + c] = o[m];
+}
+
+template <int LOUT, int CORR>
+__device__ __forceinline__ void sc_block_vjp(const float* f, const float* __restrict__ Wl, int z, int c,
+                                             const float* __restrict__ gBn, float* g) {
+  using P = ScPoly<LOUT, CORR>;
+  float w[P::KT];
+  const float* wz = Wl + (int64_t)z * P::KT * NC + c;
+#pragma unroll
+  for (int k = 0; k < P::KT; ++k) w[k] = wz[k * NC];
+  float go[2 * LOUT + 1];
+#pragma unroll
+  for (int m = 0; m < 2 * LOUT + 1; ++m) go[m] = gBn[NC * (LOUT * LOUT + m) + c];
+  float gl[16];
+  P::vjp(f, w, go, gl);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) g[i] += gl[i];
+}
+
+template <int CORR>
+__global__ void __launch_bounds__(NC) k_sc_fwd(int N, int nout, const float* __restrict__ A, int ldA,
+                                               const int* __restrict__ species, ScW W, float* __restrict__ B,
+                                               int ldB) {
+  const int n = blockIdx.x, c = threadIdx.x;
+  float f[16];
+  const float* An = A + (int64_t)n * ldA + c;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) f[i] = An[i * NC];
+  const int z = species[n];
+  float* Bn = B + (int64_t)n * ldB;
+  sc_block_fwd<0, CORR>(f, W.w[0], z, c, Bn);
+  if (nout > 1) sc_block_fwd<1, CORR>(f, W.w[1], z, c, Bn);
+  if (nout > 2) sc_block_fwd<2, CORR>(f, W.w[2], z, c, Bn);
+}
+
+template <int CORR>
+__global__ void __launch_bounds__(NC) k_sc_bwd(int N, int nout, const float* __restrict__ A, int ldA,
+                                               const int* __restrict__ species, ScW W, const float* __restrict__ gB,
+                                               int ldB, float* __restrict__ gA) {
+  const int n = blockIdx.x, c = threadIdx.x;
+  float f[16], g[16];
+  const float* An = A + (int64_t)n * ldA + c;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    f[i] = An[i * NC];
+    g[i] = 0.f;
+  }
+  const int z = species[n];
+  const float* gBn = gB + (int64_t)n * ldB;
+  sc_block_vjp<0, CORR>(f, W.w[0], z, c, gBn, g);
+  if (nout > 1) sc_block_vjp<1, CORR>(f, W.w[1], z, c, gBn, g);
+  if (nout > 2) sc_block_vjp<2, CORR>(f, W.w[2], z, c, gBn, g);
+  float* gAn = gA + (int64_t)n * ldA + c;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) gAn[i * NC] = g[i];
+}
+
+// ---------------------------------------------------------------------------
+// readouts (one 64-lane wavefront per node)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__global__ void __launch_bounds__(64) k_readout_linear(int N, const float* __restrict__ h, int ldh,
+                                                       const float* __restrict__ w, float* __restrict__ e) {
+  const int n = blockIdx.x, l = threadIdx.x;
+  const float* hn = h + (int64_t)n * ldh;
+  float a = 0.f;
+  for (int u = l; u < NC; u += 64) a = fmaf(hn[u], w[u], a);
+  a = wave_sum(a);
+  if (l == 0) e[n] = a;
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+
+__global__ void __launch_bounds__(64) k_readout_mlp(int N, const float* __restrict__ h, int ldh,
+                                                    const float* __restrict__ W1, const float* __restrict__ W2,
+                                                    float* __restrict__ e, float* __restrict__ ypre) {
+  const int n = blockIdx.x, l = threadIdx.x;
+  const float* hn = h + (int64_t)n * ldh;
+  float y[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) y[j] = 0.f;
+  for (int u = l; u < NC; u += 64) {
+    const float x = hn[u];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) y[j] = fmaf(x, W1[u * 16 + j], y[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) y[j] = wave_sum(y[j]);
+  if (l == 0) {
+    float a = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      ypre[(int64_t)n * 16 + j] = y[j];
+      a = fmaf(silu_f(y[j]), W2[j], a);
+    }
+    e[n] = a;
+  }
+}
+
+__global__ void __launch_bounds__(NC) k_readout_mlp_bwd(int N, const float* __restrict__ ypre,
+                                                        const float* __restrict__ W1, const float* __restrict__ W2,
+                                                        float* __restrict__ gh, int ldh) {
+  const int n = blockIdx.x, u = threadIdx.x;
+  float a = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float y = ypre[(int64_t)n * 16 + j];
+    const float s = 1.f / (1.f + expf(-y));
+    a = fmaf(W1[u * 16 + j], W2[j] * s * (1.f + y * (1.f - s)), a);
+  }
+  gh[(int64_t)n * ldh + u] = a;
+}
+
+__global__ void __launch_bounds__(NC) k_readout_linear_bwd(int N, const float* __restrict__ w,
+                                                           float* __restrict__ gh, int ldh, int accumulate) {
+  const int n = blockIdx.x, u = threadIdx.x;
+  float* p = gh + (int64_t)n * ldh + u;
+  *p = accumulate ? *p + w[u] : w[u];
+}
+
+// ---------------------------------------------------------------------------
+// energy assembly and reductions (fixed order: deterministic)
+// ---------------------------------------------------------------------------
+struct RoPtrs {
+  const float* p[4];
+};
+
+__global__ void __launch_bounds__(1024) k_node_energy(int N, const int* __restrict__ species,
+                                                      const float* __restrict__ e0, const int* __restrict__ rowptr,
+                                                      const float* __restrict__ zbl_e, RoPtrs ro, int nro,
+                                                      float* __restrict__ node_e, double* __restrict__ energy) {
+  __shared__ double red[1024];
+  double acc = 0.0;
+  for (int n = threadIdx.x; n < N; n += 1024) {
+    float v = e0[species[n]];
+    if (zbl_e) {
+      float z = 0.f;
+      for (int e = rowptr[n]; e < rowptr[n + 1]; ++e) z += zbl_e[e];
+      v += z;
+    }
+    for (int l = 0; l < nro; ++l) v += ro.p[l][n];
+    node_e[n] = v;
+    acc += (double)v;
+  }
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int off = 512; off > 0; off >>= 1) {
+    if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *energy = red[0];
+}
+
+__global__ void k_forces(int N, const int* __restrict__ rowptr, const int* __restrict__ rowptr_s,
+                         const int* __restrict__ perm_s, const float* __restrict__ gv, double* __restrict__ F) {
+  const int a = blockIdx.x * blockDim.x + threadIdx.x;
+  if (a >= N) return;
+  double fx = 0.0, fy = 0.0, fz = 0.0;
+  for (int e = rowptr[a]; e < rowptr[a + 1]; ++e) {  // a is the receiver: dE/dpos_a += g
+    fx -= gv[3 * e];
+    fy -= gv[3 * e + 1];
+    fz -= gv[3 * e + 2];
+  }
+  for (int k = rowptr_s[a]; k < rowptr_s[a + 1]; ++k) {  // a is the sender: dE/dpos_a -= g
+    const int e = perm_s[k];
+    fx += gv[3 * e];
+    fy += gv[3 * e + 1];
+    fz += gv[3 * e + 2];
+  }
+  F[3 * a] = fx;
+  F[3 * a + 1] = fy;
+  F[3 * a + 2] = fz;
+}
+
+__global__ void k_virial_reduce(const double* __restrict__ part, int nblk, double* __restrict__ vir) {
+  const int k = threadIdx.x;
+  if (k >= 9) return;
+  double a = 0.0;
+  for (int b = 0; b < nblk; ++b) a += part[9 * b + k];
+  vir[k] = a;
+}
+
+}  // namespace
+
+static inline unsigned cdiv(int64_t a, int b) { return (unsigned)((a + b - 1) / b); }
+
+void launch_linear(hipStream_t st, int N, const LinearDesc& d, const float* X, const float* W, float* Y) {
+  const int rows = N * d.d;
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(k_linear, dim3(cdiv(rows, LT), d.Cout / LT), dim3(256), 0, st, rows, d, X, W, Y);
+}
+
+void launch_linear_species(hipStream_t st, int N, const LinearDesc& d, const float* X, const float* W,
+                           const int* species, float* Y) {
+  const int rows = N * d.d;
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(k_linear_species, dim3(rows, d.Cout / NC), dim3(NC), 0, st, rows, d, X, W, species, Y);
+}
+
+void launch_embed(hipStream_t st, int N, const int* species, const float* emb, int ld, float* h) {
+  if (N <= 0) return;
+  hipLaunchKernelGGL(k_embed, dim3(N), dim3(NC), 0, st, N, species, emb, ld, h);
+}
+
+void launch_sc_fwd(hipStream_t st, int N, int nout, int corr, const float* A, int ldA, const int* species,
+                   const float* const* Wsc, float* B, int ldB) {
+  if (N <= 0) return;
+  ScW w{{Wsc[0], nout > 1 ? Wsc[1] : nullptr, nout > 2 ? Wsc[2] : nullptr}};
+  switch (corr) {
+    case 1: hipLaunchKernelGGL(k_sc_fwd<1>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB); break;
+    case 2: hipLaunchKernelGGL(k_sc_fwd<2>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB); break;
+    case 3: hipLaunchKernelGGL(k_sc_fwd<3>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB); break;
+  }
+}
+
+void launch_sc_bwd(hipStream_t st, int N, int nout, int corr, const float* A, int ldA, const int* species,
+                   const float* const* Wsc, const float* gB, int ldB, float* gA) {
+  if (N <= 0) return;
+  ScW w{{Wsc[0], nout > 1 ? Wsc[1] : nullptr, nout > 2 ? Wsc[2] : nullptr}};
+  switch (corr) {
+    case 1:
+      hipLaunchKernelGGL(k_sc_bwd<1>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, gB, ldB, gA);
+      break;
+    case 2:
+      hipLaunchKernelGGL(k_sc_bwd<2>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, gB, ldB, gA);
+      break;
+    case 3:
+      hipLaunchKernelGGL(k_sc_bwd<3>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, gB, ldB, gA);
+      break;
+  }
+}
+
+void launch_readout_linear(hipStream_t st, int N, const float* h, int ldh, const float* w, float* e) {
+  if (N <= 0) return;
+  hipLaunchKernelGGL(k_readout_linear, dim3(N), dim3(64), 0, st, N, h, ldh, w, e);
+}
+
+void launch_readout_mlp(hipStream_t st, int N, const float* h, int ldh, const float* W1, const float* W2,
+                        float* e, float* ypre) {
+  if (N <= 0) return;
+  hipLaunchKernelGGL(k_readout_mlp, dim3(N), dim3(64), 0, st, N, h, ldh, W1, W2, e, ypre);
+}
+
+void launch_readout_mlp_bwd(hipStream_t st, int N, const float* ypre, const float* W1, const float* W2,
+                            float* gh, int ldh) {
+  if (N <= 0) return;
+  hipLaunchKernelGGL(k_readout_mlp_bwd, dim3(N), dim3(NC), 0, st, N, ypre, W1, W2, gh, ldh);
+}
+
+void launch_readout_linear_bwd(hipStream_t st, int N, const float* w, float* gh, int ldh, int accumulate) {
+  if (N <= 0) return;
+  hipLaunchKernelGGL(k_readout_linear_bwd, dim3(N), dim3(NC), 0, st, N, w, gh, ldh, accumulate);
+}
+
+void launch_node_energy(hipStream_t st, int N, const int* species, const float* e0, const int* rowptr,
+                        const float* zbl_e, const float* const* ro, int nro, float* node_e, double* energy) {
+  RoPtrs r{{nullptr, nullptr, nullptr, nullptr}};
+  for (int l = 0; l < nro && l < 4; ++l) r.p[l] = ro[l];
+  hipLaunchKernelGGL(k_node_energy, dim3(1), dim3(1024), 0, st, N, species, e0, rowptr, zbl_e, r, nro, node_e,
+                     energy);
+}
+
+void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s, const int* perm_s,
+                   const float* gv, double* forces) {
+  if (N <= 0) return;
+  hipLaunchKernelGGL(k_forces, dim3(cdiv(N, 256)), dim3(256), 0, st, N, rowptr, rowptr_s, perm_s, gv, forces);
+}
+
+void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir) {
+  hipLaunchKernelGGL(k_virial_reduce, dim3(1), dim3(64), 0, st, part, nblk, vir);
+}
+
+}  // namespace mace

@@ -1,0 +1,193 @@
+"""ctypes binding of the HIP engine's C ABI (include/mace_hip.h).
+
+The library is loaded from ``mace_mlx_amd/_lib/libmace_hip.so``.  There is no
+fallback: if the library is missing or no HIP device is present, construction
+raises.  Status codes map to the exception types the reference raises for the
+same conditions (`calculators.py:100-136,345-354`).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from typing import Optional, Tuple
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmace_hip.so"
+
+MACE_OK = 0
+MACE_ERR_INVALID = -1
+MACE_ERR_HIP = -2
+MACE_ERR_UNSUPPORTED = -3
+MACE_ERR_STATE = -4
+MACE_ERR_SPECIES = -5
+
+STEP_FORCES = 1
+STEP_STRESS = 2
+STEP_FORCE_NL = 4
+
+EXPORTED_SYMBOLS = (
+    "mace_create", "mace_destroy", "mace_last_error", "mace_model_begin", "mace_model_set_tensor",
+    "mace_model_end", "mace_set_system", "mace_step", "mace_set_edges", "mace_get_edges",
+    "mace_get_timings",
+)
+
+
+class HipError(RuntimeError):
+    pass
+
+
+class ModelDims(ctypes.Structure):
+    _fields_ = [
+        ("num_elements", ctypes.c_int32), ("num_channels", ctypes.c_int32),
+        ("max_ell", ctypes.c_int32), ("num_bessel", ctypes.c_int32),
+        ("num_poly_cutoff", ctypes.c_int32), ("num_layers", ctypes.c_int32),
+        ("radial_hidden", ctypes.c_int32), ("radial_depth", ctypes.c_int32),
+        ("layer_in_blocks", ctypes.c_int32 * 4), ("layer_hid_blocks", ctypes.c_int32 * 4),
+        ("correlation", ctypes.c_int32 * 4), ("has_zbl", ctypes.c_int32), ("zbl_p", ctypes.c_int32),
+        ("r_max", ctypes.c_double), ("zbl_a_exp", ctypes.c_double),
+        ("zbl_a_prefactor", ctypes.c_double), ("zbl_scale", ctypes.c_double),
+    ]
+
+
+_lib = None
+
+
+def load_library(path: Optional[str] = None) -> ctypes.CDLL:
+    """Load (once) and type the engine library; raises if it is not built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else Path(os.environ.get("MACE_HIP_LIB", LIB_PATH))
+    if not p.exists():
+        raise ImportError(f"HIP engine library not found at {p}; build it with "
+                          "`python -c 'import __graft_entry__ as g; g.build()'` (hipcc, gfx950)")
+    lib = ctypes.CDLL(str(p))
+    P, I32, I64, D, U32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_double, ctypes.c_uint32
+    sig = {
+        "mace_create": (ctypes.c_int, [I32, ctypes.POINTER(P)]),
+        "mace_destroy": (None, [P]),
+        "mace_last_error": (ctypes.c_char_p, [P]),
+        "mace_model_begin": (ctypes.c_int, [P, ctypes.POINTER(ModelDims)]),
+        "mace_model_set_tensor": (ctypes.c_int, [P, ctypes.c_char_p, P, I64]),
+        "mace_model_end": (ctypes.c_int, [P]),
+        "mace_set_system": (ctypes.c_int, [P, I32, P, P, P, D]),
+        "mace_step": (ctypes.c_int, [P, P, U32, ctypes.POINTER(D), P, P, P]),
+        "mace_set_edges": (ctypes.c_int, [P, I64, P, P, P]),
+        "mace_get_edges": (ctypes.c_int, [P, I64, P, P, P, ctypes.POINTER(I64)]),
+        "mace_get_timings": (ctypes.c_int, [P, P, I32]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _ptr(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+class Engine:
+    """One engine context on one HIP device (not thread-safe, like the reference's
+    calculator which is driven from one Python thread)."""
+
+    def __init__(self, device: int = 0):
+        self._lib = load_library()
+        h = ctypes.c_void_p()
+        rc = self._lib.mace_create(int(device), ctypes.byref(h))
+        if rc != MACE_OK:
+            msg = self._lib.mace_last_error(None)
+            self._raise(rc, msg.decode() if msg else "mace_create failed")
+        self._h = h
+        self.n_atoms = 0
+
+    def _raise(self, rc: int, msg: str):
+        if rc in (MACE_ERR_INVALID, MACE_ERR_SPECIES):
+            raise ValueError(msg)
+        if rc == MACE_ERR_UNSUPPORTED:
+            raise NotImplementedError(msg)
+        if rc == MACE_ERR_HIP:
+            raise HipError(msg)
+        raise RuntimeError(msg)
+
+    def _check(self, rc: int):
+        if rc != MACE_OK:
+            msg = self._lib.mace_last_error(self._h)
+            self._raise(rc, msg.decode() if msg else f"error {rc}")
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._lib.mace_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- model --------------------------------------------------------------
+    def load_model(self, dm) -> None:
+        d = ModelDims()
+        for k, v in dm.dims.items():
+            if isinstance(v, list):
+                arr = getattr(d, k)
+                for i, x in enumerate(v):
+                    arr[i] = int(x)
+            else:
+                setattr(d, k, v)
+        self._check(self._lib.mace_model_begin(self._h, ctypes.byref(d)))
+        for name, t in dm.tensors.items():
+            t = np.ascontiguousarray(t, dtype=np.float32)
+            self._check(self._lib.mace_model_set_tensor(self._h, name.encode(), _ptr(t), t.size))
+        self._check(self._lib.mace_model_end(self._h))
+
+    # -- system -------------------------------------------------------------
+    def set_system(self, species: np.ndarray, cell: np.ndarray, pbc, skin: float) -> None:
+        sp = np.ascontiguousarray(species, dtype=np.int32)
+        cl = np.ascontiguousarray(np.asarray(cell, dtype=np.float64).reshape(9))
+        pb = np.ascontiguousarray(np.asarray(pbc, dtype=bool).reshape(3).astype(np.uint8))
+        self._check(self._lib.mace_set_system(self._h, len(sp), _ptr(sp), _ptr(cl), _ptr(pb), float(skin)))
+        self.n_atoms = len(sp)
+
+    def step(self, positions: np.ndarray, stress: bool = False, force_nl: bool = False,
+             node_energy: bool = True) -> Tuple[float, Optional[np.ndarray], np.ndarray, Optional[np.ndarray]]:
+        pos = np.ascontiguousarray(positions, dtype=np.float64).reshape(-1, 3)
+        if len(pos) != self.n_atoms:
+            raise ValueError(f"positions has {len(pos)} atoms, system has {self.n_atoms}")
+        e = ctypes.c_double()
+        ne = np.empty(self.n_atoms, dtype=np.float64) if node_energy else None
+        f = np.empty((self.n_atoms, 3), dtype=np.float64)
+        v = np.empty((3, 3), dtype=np.float64) if stress else None
+        flags = STEP_FORCES | (STEP_STRESS if stress else 0) | (STEP_FORCE_NL if force_nl else 0)
+        self._check(self._lib.mace_step(self._h, _ptr(pos), flags, ctypes.byref(e), _ptr(ne), _ptr(f), _ptr(v)))
+        return e.value, ne, f, v
+
+    # -- test hooks -----------------------------------------------------------
+    def set_edges(self, sender, receiver, shifts) -> None:
+        s = np.ascontiguousarray(sender, dtype=np.int32)
+        r = np.ascontiguousarray(receiver, dtype=np.int32)
+        S = np.ascontiguousarray(np.asarray(shifts).reshape(-1, 3), dtype=np.int32)
+        if not (len(s) == len(r) == len(S)):
+            raise ValueError("sender / receiver / shifts lengths differ")
+        self._check(self._lib.mace_set_edges(self._h, len(s), _ptr(s), _ptr(r), _ptr(S)))
+
+    def get_edges(self):
+        n = ctypes.c_int64()
+        self._check(self._lib.mace_get_edges(self._h, 0, None, None, None, ctypes.byref(n)))
+        E = n.value
+        s = np.empty(E, np.int32)
+        r = np.empty(E, np.int32)
+        S = np.empty((E, 3), np.int32)
+        self._check(self._lib.mace_get_edges(self._h, E, _ptr(s), _ptr(r), _ptr(S), ctypes.byref(n)))
+        return s, r, S
+
+    def timings(self) -> np.ndarray:
+        out = np.zeros(4, dtype=np.float64)
+        self._lib.mace_get_timings(self._h, _ptr(out), 4)
+        return out

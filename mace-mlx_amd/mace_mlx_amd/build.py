@@ -1,0 +1,30 @@
+"""Build the HIP engine in-tree: generate the constant tables, then hipcc (gfx950).
+
+``python -m mace_mlx_amd.build`` or ``__graft_entry__.build()``.
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+CSRC = Path(__file__).resolve().parents[1] / "csrc"
+
+
+def build(jobs: int = 4, verbose: bool = False) -> Path:
+    env = dict(os.environ)
+    env.setdefault("PYTHON", sys.executable)
+    subprocess.run([sys.executable, str(CSRC / "gen_tables.py"), str(CSRC / "gen")], check=True,
+                   stdout=None if verbose else subprocess.DEVNULL)
+    proc = subprocess.run(["make", "-C", str(CSRC), f"-j{jobs}"], env=env, capture_output=not verbose, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write((proc.stdout or "") + (proc.stderr or ""))
+        raise RuntimeError("HIP engine build failed")
+    from ._ffi import LIB_PATH
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,158 @@
+"""Reference-layout model -> named tensors for the HIP engine.
+
+Reads a model in the reference's format (`model.py:664-720`: config.json +
+weights.npz, key names of `converter.py`) and produces the dims struct and the
+tensors `mace_model_set_tensor` expects.  All normalisation constants of the
+reference (path weights, CG factors, 1/avg_num_neighbors, ScaleShift scale and
+shift) are folded in here, once, in float64, and the per-block matrices are laid
+out for the kernels' component-major node layout (element (u, m) of a block at
+``m * C + u``).
+
+Tensor names (C = channels, n_el = elements, per layer prefix ``L{l}.``):
+
+  e0 [n_el]                       atomic energies (+ shift for ScaleShiftMACE)
+  bessel_w [nb]                   Bessel frequencies
+  zbl_z, zbl_cov [n_el]           atomic number and covalent radius per element
+  embed [n_el][C]                 node embedding (one-hot linear, pw folded)
+  L.up.b [C][C]                   linear_up, block l=b
+  L.skip.b [n_el][C][C]           skip FCTP for hidden block b (CG * pw folded)
+  L.mlp.k                         radial MLP layer k, [in][out]
+  L.lin.l [nslots(l)*C][C]        message linear for output l (pw / avg folded)
+  L.sc.b [n_el][K3+K2+K1][C]      symmetric-contraction weights, output block b
+  L.plin.b [C][C]                 product linear
+  L.ro [C] | L.ro1 [C][16], L.ro2 [16]   readouts (scale folded)
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Dict, List
+
+import numpy as np
+
+from .cg import u_matrix, wigner_3j
+from .irreps import Irrep, Irreps
+from .model_io import COVALENT_RADII, ModelConfig, conv_tp_instructions, linear_instructions
+
+
+class UnsupportedModel(NotImplementedError):
+    pass
+
+
+def _blocks(irreps: Irreps, C: int) -> int:
+    """Number of leading blocks 0e, 1o, 2e, ... (all multiplicity C)."""
+    for b, blk in enumerate(irreps):
+        if blk.mul != C or blk.ir != Irrep(b, (-1) ** b):
+            raise UnsupportedModel(f"irreps {irreps}: blocks must be {C}x0e+{C}x1o+{C}x2e...")
+    if len(irreps) > 3:
+        raise UnsupportedModel(f"irreps {irreps}: at most l=2 hidden features are compiled in")
+    return len(irreps)
+
+
+@dataclass
+class DeviceModel:
+    dims: dict
+    tensors: Dict[str, np.ndarray]
+    z_table: List[int]
+    r_max: float
+
+
+def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray]) -> DeviceModel:
+    cfg.check_supported()
+    if cfg.model_type not in ("MACE", "ScaleShiftMACE"):
+        raise UnsupportedModel(f"model_type={cfg.model_type}")
+    C = cfg.num_features
+    nel = cfg.num_elements
+    if cfg.max_ell != 3:
+        raise UnsupportedModel("max_ell must be 3")
+    if list(cfg.radial_MLP) != [64, 64, 64]:
+        raise UnsupportedModel(f"radial_MLP={cfg.radial_MLP}")
+    scale = float(cfg.scale) if cfg.model_type == "ScaleShiftMACE" else 1.0
+    shift = float(cfg.shift) if cfg.model_type == "ScaleShiftMACE" else 0.0
+    for v, nm in ((scale, "scale"), (shift, "shift")):
+        if isinstance(v, (list, tuple)):
+            raise UnsupportedModel(f"per-head {nm}")
+    z_table = list(cfg.z_table) if cfg.z_table else list(range(nel))
+    T: Dict[str, np.ndarray] = {}
+    f64 = lambda k: np.asarray(w[k], dtype=np.float64)
+
+    T["e0"] = f64("atomic_energies_fn.atomic_energies").reshape(-1) + shift
+    T["bessel_w"] = f64("radial_embedding.bessel_fn.bessel_weights").reshape(-1)
+    T["zbl_z"] = np.asarray(z_table, dtype=np.float64)
+    T["zbl_cov"] = COVALENT_RADII[np.asarray(z_table)]
+    attrs = Irreps(f"{nel}x0e")
+    scal = Irreps([b for b in cfg.hidden if b.ir.l == 0])
+    (inst,) = linear_instructions(attrs, scal)
+    T["embed"] = f64("node_embedding.linear.weights.0") * inst[4]
+
+    ins, hids = cfg.layer_inputs(), cfg.hidden_per_layer()
+    n_layers = cfg.num_interactions
+    dims = dict(num_elements=nel, num_channels=C, max_ell=cfg.max_ell, num_bessel=cfg.num_bessel,
+                num_poly_cutoff=cfg.num_polynomial_cutoff, num_layers=n_layers, radial_hidden=64,
+                radial_depth=3, layer_in_blocks=[0] * 4, layer_hid_blocks=[0] * 4, correlation=[0] * 4,
+                has_zbl=int(bool(cfg.pair_repulsion)), zbl_p=6, r_max=float(cfg.r_max),
+                zbl_a_exp=0.3, zbl_a_prefactor=0.4543, zbl_scale=scale)
+    if cfg.pair_repulsion:
+        dims["zbl_p"] = int(cfg.pair_repulsion.get("p", 6))
+        dims["zbl_a_exp"] = float(cfg.pair_repulsion.get("a_exp", 0.3))
+        dims["zbl_a_prefactor"] = float(cfg.pair_repulsion.get("a_prefactor", 0.4543))
+    inter = cfg.interaction_irreps
+    coupling = Irreps([(1, b.ir) for b in inter])
+    for l in range(n_layers):
+        p = f"L{l}."
+        q = f"interactions.{l}"
+        irr_in, hid = ins[l], hids[l]
+        lin, lhid = _blocks(irr_in, C), _blocks(hid, C)
+        dims["layer_in_blocks"][l] = lin
+        dims["layer_hid_blocks"][l] = lhid
+        dims["correlation"][l] = int(cfg.correlation[l])
+        # linear_up
+        for n, (ji, jo, mi, mo, pw) in enumerate(linear_instructions(irr_in, irr_in)):
+            assert ji == jo
+            T[f"{p}up.{ji}"] = f64(f"{q}.linear_up.weights.{n}") * pw
+        # skip FCTP with one-hot attributes: out[w,k] = pw * sum_u W[u,z,w] x[u,i] cg[i,0,k]
+        from .model_io import fctp_instructions
+        for n, (i1, i2, io, pw) in enumerate(fctp_instructions(irr_in, attrs, hid)):
+            l1, lo = irr_in[i1].ir.l, hid[io].ir.l
+            cg = wigner_3j(l1, 0, lo)[:, 0, :]
+            c = cg[0, 0]
+            if l1 != lo or not np.allclose(cg, c * np.eye(2 * l1 + 1), atol=1e-12):
+                raise UnsupportedModel("skip connection with non-diagonal coupling")
+            W = f64(f"{q}.skip_tp.tp.weights.{n}")          # (C, n_el, C)
+            T[f"{p}skip.{io}"] = np.transpose(W, (1, 0, 2)) * (pw * c)
+        # radial MLP, nn.Linear (out, in) -> [in][out]
+        for k in range(4):
+            T[f"{p}mlp.{k}"] = f64(f"{q}.conv_tp_weights.layers.{2 * k}.weight").T
+        # message linear (irreps_mid -> interaction irreps) / avg_num_neighbors
+        mid, _ = conv_tp_instructions(irr_in, cfg.sh_irreps, inter)
+        per_out = {}
+        for n, (ji, jo, mi, mo, pw) in enumerate(linear_instructions(mid, inter)):
+            per_out.setdefault(jo, []).append(f64(f"{q}.linear.weights.{n}") * pw / cfg.avg_num_neighbors)
+        for jo in range(len(inter)):
+            T[f"{p}lin.{jo}"] = np.concatenate(per_out[jo], axis=0)
+        # symmetric contraction
+        r = f"products.{l}.symmetric_contractions.contractions"
+        corr = int(cfg.correlation[l])
+        for b, blk in enumerate(hid):
+            parts = []
+            keys = [f"{r}.{b}.weights_max"] + [f"{r}.{b}.weights.{i}" for i in range(corr - 1)]
+            for key, nu in zip(keys, range(corr, 0, -1)):
+                Wn = f64(key)
+                if not np.any(np.abs(u_matrix(coupling, blk.ir, nu)) > 1e-15):
+                    Wn = np.zeros_like(Wn)   # symmetric_contraction.py:255-262
+                parts.append(Wn)
+            T[f"{p}sc.{b}"] = np.concatenate(parts, axis=1)   # (n_el, KT, C)
+        for n, (ji, jo, mi, mo, pw) in enumerate(linear_instructions(hid, hid)):
+            T[f"{p}plin.{jo}"] = f64(f"products.{l}.linear.weights.{n}") * pw
+        ro = f"readouts.{l}"
+        if l < n_layers - 1:
+            (ji, jo, mi, mo, pw), = linear_instructions(hid, Irreps("0e"))
+            T[f"{p}ro"] = f64(f"{ro}.linear.weights.0").reshape(-1) * pw * scale
+        else:
+            (i1,) = linear_instructions(hid, Irreps("16x0e"))
+            (i2,) = linear_instructions(Irreps("16x0e"), Irreps("0e"))
+            T[f"{p}ro1"] = f64(f"{ro}.linear_1.weights.0") * i1[4]
+            T[f"{p}ro2"] = f64(f"{ro}.linear_2.weights.0").reshape(-1) * i2[4] * scale
+    return DeviceModel(dims=dims, tensors={k: np.ascontiguousarray(v, dtype=np.float32) for k, v in T.items()},
+                       z_table=z_table, r_max=float(cfg.r_max))

@@ -1,0 +1,310 @@
+"""Model files in the reference layout: ``config.json`` + ``weights.npz``.
+
+The on-disk format is the one the reference loads in `model.py:664-720`: a JSON
+dict of `MACE.__init__` keyword arguments (`model.py:59-82`) plus ``model_type``,
+``scale``, ``shift`` and ``z_table``, and an ``.npz`` of float arrays keyed by the
+MLX module path (key names as written by `converter.py:315-366,636`, e.g.
+``interactions.1.conv_tp_weights.layers.4.weight``).
+
+This module also builds *random-init* models of the BASELINE architectures with
+the reference's own initialisation distributions (the reference draws them from
+MLX's RNG, which cannot be reproduced here, so models are exchanged as files):
+
+* EquivariantLinear weights ~ N(0, 1)                       (`linear.py:70`)
+* FullyConnectedTensorProduct weights ~ N(0, 1)             (`tensor_product.py:286`)
+* SymmetricContraction weights ~ N(0, 1) / n_params         (`symmetric_contraction.py:240-252`)
+* radial-MLP ``nn.Linear`` weights, stored (out, in): the distribution a
+  converted e3nn ``FullyConnectedNet`` has after `converter.py:578-646` folds its
+  normalisation into the weights -- N(0, 1) / sqrt(fan_in), times the SiLU
+  second-moment factor 1.6791768 (`utils.py:17`) for every layer that follows a
+  SiLU.  (MLX's own default, U(+-1/sqrt(fan_in)), shrinks the signal ~3x per
+  layer and leaves random models with forces ~1e-4 eV/A, too small to test.)
+* Bessel frequencies n*pi/r_max                             (`radial.py:49-51`)
+"""
+
+from __future__ import annotations
+
+import json
+import math
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Dict, List, Optional
+
+import numpy as np
+
+from .irreps import Irrep, Irreps
+
+# 1 / sqrt(E[silu(x)^2]) for x ~ N(0, 1) (`utils.py:17`)
+SILU_NORM_FACTOR = 1.6791768074035645
+
+# Published covalent radii (Cordero et al., Dalton Trans. 2008, 2832), in
+# Angstrom, indexed by atomic number (index 0 is a placeholder).  The reference
+# reads the same table from ase.data.covalent_radii (`radial.py:145-154`).
+COVALENT_RADII = np.array([
+    0.20, 0.31, 0.28, 1.28, 0.96, 0.84, 0.76, 0.71, 0.66, 0.57, 0.58,  # 0-10
+    1.66, 1.41, 1.21, 1.11, 1.07, 1.05, 1.02, 1.06, 2.03, 1.76,        # 11-20
+    1.70, 1.60, 1.53, 1.39, 1.39, 1.32, 1.26, 1.24, 1.32, 1.22,        # 21-30
+    1.22, 1.20, 1.19, 1.20, 1.20, 1.16, 2.20, 1.95, 1.90, 1.75,        # 31-40
+    1.64, 1.54, 1.47, 1.46, 1.42, 1.39, 1.45, 1.44, 1.42, 1.39,        # 41-50
+    1.39, 1.38, 1.39, 1.40, 2.44, 2.15, 2.07, 2.04, 2.03, 2.01,        # 51-60
+    1.99, 1.98, 1.98, 1.96, 1.94, 1.92, 1.92, 1.89, 1.90, 1.87,        # 61-70
+    1.87, 1.75, 1.70, 1.62, 1.51, 1.44, 1.41, 1.36, 1.36, 1.32,        # 71-80
+    1.45, 1.46, 1.48, 1.40, 1.50, 1.50, 2.60, 2.21, 2.15, 2.06,        # 81-90
+    2.00, 1.96, 1.90, 1.87, 1.80, 1.69,                                # 91-96
+], dtype=np.float64)
+
+
+@dataclass
+class ModelConfig:
+    """Subset of `MACE.__init__` arguments (`model.py:59-82`) this engine runs."""
+
+    r_max: float
+    num_bessel: int = 10
+    num_polynomial_cutoff: int = 5
+    max_ell: int = 3
+    num_interactions: int = 2
+    hidden_irreps: str = "128x0e"
+    correlation: List[int] = field(default_factory=lambda: [3, 3])
+    num_elements: int = 89
+    atomic_energies: Optional[List[float]] = None
+    avg_num_neighbors: float = 1.0
+    radial_MLP: List[int] = field(default_factory=lambda: [64, 64, 64])
+    gate: str = "silu"
+    model_type: str = "MACE"
+    scale: float = 1.0
+    shift: float = 0.0
+    z_table: Optional[List[int]] = None
+    pair_repulsion: Optional[dict] = None
+    heads: Optional[List[str]] = None
+    first_interaction_nonresidual: bool = False
+    use_density_normalization: bool = False
+    distance_transform: Optional[dict] = None
+    interaction_cls: str = "RealAgnosticResidualInteractionBlock"
+    apply_cutoff: bool = True
+    use_agnostic_product: bool = False
+    edge_irreps: Optional[str] = None
+
+    @staticmethod
+    def from_dict(d: dict) -> "ModelConfig":
+        d = dict(d)
+        # load_model's default when the key is missing (model.py:680)
+        d.setdefault("model_type", "ScaleShiftMACE")
+        corr = d.get("correlation", 3)
+        n_int = int(d.get("num_interactions", 2))
+        if isinstance(corr, int):
+            corr = [corr] * n_int
+        d["correlation"] = [int(c) for c in corr]
+        known = set(ModelConfig.__dataclass_fields__)
+        unknown = sorted(set(d) - known)
+        if unknown:
+            raise ValueError(f"unsupported config keys: {unknown}")
+        return ModelConfig(**d)
+
+    def to_dict(self) -> dict:
+        out = {k: getattr(self, k) for k in self.__dataclass_fields__}
+        return {k: v for k, v in out.items() if v is not None}
+
+    # --- derived architecture (model.py:96-145) -----------------------------
+    @property
+    def hidden(self) -> Irreps:
+        return Irreps(self.hidden_irreps)
+
+    @property
+    def num_features(self) -> int:
+        return self.hidden[0].mul
+
+    @property
+    def sh_irreps(self) -> Irreps:
+        return Irreps.spherical_harmonics(self.max_ell)
+
+    @property
+    def interaction_irreps(self) -> Irreps:
+        return Irreps([(self.num_features, b.ir) for b in self.sh_irreps])
+
+    def hidden_per_layer(self) -> List[Irreps]:
+        scal = Irreps([b for b in self.hidden if b.ir.l == 0])
+        return [self.hidden if i < self.num_interactions - 1 else scal
+                for i in range(self.num_interactions)]
+
+    def layer_inputs(self) -> List[Irreps]:
+        scal = Irreps([b for b in self.hidden if b.ir.l == 0])
+        hid = self.hidden_per_layer()
+        return [scal] + hid[:-1]
+
+    def check_supported(self) -> None:
+        """Raise NotImplementedError for topology options outside this engine."""
+        if self.interaction_cls != "RealAgnosticResidualInteractionBlock":
+            raise NotImplementedError(f"interaction_cls={self.interaction_cls}")
+        for flag in ("first_interaction_nonresidual", "use_density_normalization",
+                     "use_agnostic_product"):
+            if getattr(self, flag):
+                raise NotImplementedError(flag)
+        if self.distance_transform is not None:
+            raise NotImplementedError("distance_transform (Agnesi)")
+        if not self.apply_cutoff:
+            raise NotImplementedError("apply_cutoff=False")
+        if self.heads is not None and len(self.heads) > 1:
+            raise NotImplementedError("multi-head models")
+        if self.gate != "silu":
+            raise NotImplementedError(f"gate={self.gate}")
+        if any(b.ir.l == 0 and b.ir.p != 1 for b in self.hidden):
+            raise NotImplementedError("pseudoscalar hidden irreps")
+
+
+def load_config(model_dir: str | Path) -> ModelConfig:
+    with open(Path(model_dir) / "config.json") as f:
+        return ModelConfig.from_dict(json.load(f))
+
+
+def load_weights(model_dir: str | Path) -> Dict[str, np.ndarray]:
+    with np.load(Path(model_dir) / "weights.npz", allow_pickle=False) as z:
+        return {k: np.asarray(z[k]) for k in z.files}
+
+
+def save_model(model_dir: str | Path, cfg: ModelConfig, weights: Dict[str, np.ndarray]) -> Path:
+    p = Path(model_dir)
+    p.mkdir(parents=True, exist_ok=True)
+    with open(p / "config.json", "w") as f:
+        json.dump(cfg.to_dict(), f, indent=1)
+    np.savez(p / "weights.npz", **{k: np.asarray(v, dtype=np.float32) for k, v in weights.items()})
+    return p
+
+
+# ---------------------------------------------------------------------------
+# Weight-key inventory (shapes) for a config, in the reference's module layout
+# ---------------------------------------------------------------------------
+
+
+def linear_instructions(irreps_in: Irreps, irreps_out: Irreps):
+    """EquivariantLinear instruction list (`linear.py:46-74`): outer loop over
+    input blocks, inner over output blocks; path weight 1/sqrt(sum of input
+    multiplicities feeding the output block)."""
+    tot = {}
+    for jo, bo in enumerate(irreps_out):
+        tot[jo] = sum(bi.mul for bi in irreps_in if bi.ir == bo.ir)
+    out = []
+    for ji, bi in enumerate(irreps_in):
+        for jo, bo in enumerate(irreps_out):
+            if bi.ir != bo.ir:
+                continue
+            pw = 1.0 / math.sqrt(tot[jo]) if tot[jo] > 0 else 1.0
+            out.append((ji, jo, bi.mul, bo.mul, pw))
+    return out
+
+
+def conv_tp_instructions(irreps1: Irreps, irreps2: Irreps, target: Irreps):
+    """`tp_out_irreps_with_instructions` (`utils.py:87-156`): returns the sorted
+    mid irreps and [(i1, i2, i_out, path_weight)] sorted by i_out."""
+    outs, inst = [], []
+    for i, b1 in enumerate(irreps1):
+        for j, b2 in enumerate(irreps2):
+            for ir in b1.ir.couple(b2.ir):
+                if ir in target:
+                    inst.append((i, j, len(outs), b2.mul))
+                    outs.append((b1.mul, ir))
+    alpha = {}
+    for (_, _, k, m2) in inst:
+        alpha[k] = alpha.get(k, 0.0) + m2
+    mid = Irreps(outs)
+    mid_sorted, _, inv = mid.sorted_with_perm()
+    res = []
+    for (i, j, k, _) in inst:
+        pw = math.sqrt(outs[k][1].dim / alpha[k]) if alpha[k] > 0 else 1.0
+        res.append((i, j, inv[k], pw))
+    res.sort(key=lambda t: t[2])
+    return mid_sorted, res
+
+
+def fctp_instructions(irreps1: Irreps, irreps2: Irreps, irreps_out: Irreps):
+    """FullyConnectedTensorProduct instructions (`tensor_product.py:1068-1098`):
+    [(i1, i2, i_out, path_weight)] in (i1, i2, i_out) loop order."""
+    inst = []
+    for i, b1 in enumerate(irreps1):
+        for j, b2 in enumerate(irreps2):
+            for k, bo in enumerate(irreps_out):
+                if b1.ir.p * b2.ir.p != bo.ir.p:
+                    continue
+                if not (abs(b1.ir.l - b2.ir.l) <= bo.ir.l <= b1.ir.l + b2.ir.l):
+                    continue
+                inst.append((i, j, k))
+    alpha = {}
+    for (i, j, k) in inst:
+        alpha[k] = alpha.get(k, 0.0) + irreps1[i].mul * irreps2[j].mul
+    return [(i, j, k, math.sqrt(irreps_out[k].ir.dim / alpha[k])) for (i, j, k) in inst]
+
+
+def weight_shapes(cfg: ModelConfig) -> Dict[str, tuple]:
+    """Key -> shape for every array the reference's MACE module tree holds."""
+    from .cg import u_matrix  # local import: scipy-free callers stay light
+
+    cfg.check_supported()
+    shapes: Dict[str, tuple] = {}
+    nel = cfg.num_elements
+    C = cfg.num_features
+    attrs = Irreps(f"{nel}x0e")
+    shapes["atomic_energies_fn.atomic_energies"] = (nel,)
+    scal = Irreps([b for b in cfg.hidden if b.ir.l == 0])
+    for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(attrs, scal)):
+        shapes[f"node_embedding.linear.weights.{n}"] = (mi, mo)
+    shapes["radial_embedding.bessel_fn.bessel_weights"] = (cfg.num_bessel,)
+    inter = cfg.interaction_irreps
+    for li, (irr_in, hid) in enumerate(zip(cfg.layer_inputs(), cfg.hidden_per_layer())):
+        p = f"interactions.{li}"
+        for n, (i, j, k, _) in enumerate(fctp_instructions(irr_in, attrs, hid)):
+            shapes[f"{p}.skip_tp.tp.weights.{n}"] = (irr_in[i].mul, attrs[j].mul, hid[k].mul)
+        for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(irr_in, irr_in)):
+            shapes[f"{p}.linear_up.weights.{n}"] = (mi, mo)
+        mid, tpi = conv_tp_instructions(irr_in, cfg.sh_irreps, inter)
+        wnum = sum(irr_in[i].mul * cfg.sh_irreps[j].mul for (i, j, _, _) in tpi)
+        dims = [cfg.num_bessel] + list(cfg.radial_MLP) + [wnum]
+        for n in range(len(dims) - 1):
+            shapes[f"{p}.conv_tp_weights.layers.{2 * n}.weight"] = (dims[n + 1], dims[n])
+        for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(mid, inter)):
+            shapes[f"{p}.linear.weights.{n}"] = (mi, mo)
+        q = f"products.{li}"
+        coupling = Irreps([(1, b.ir) for b in inter])
+        for ci, b in enumerate(hid):
+            cp = f"{q}.symmetric_contractions.contractions.{ci}"
+            corr = cfg.correlation[li]
+            shapes[f"{cp}.weights_max"] = (nel, u_matrix(coupling, b.ir, corr).shape[-1], C)
+            for wi, nu in enumerate(range(corr - 1, 0, -1)):
+                shapes[f"{cp}.weights.{wi}"] = (nel, u_matrix(coupling, b.ir, nu).shape[-1], C)
+        for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(hid, hid)):
+            shapes[f"{q}.linear.weights.{n}"] = (mi, mo)
+        r = f"readouts.{li}"
+        if li < cfg.num_interactions - 1:
+            for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(hid, Irreps("0e"))):
+                shapes[f"{r}.linear.weights.{n}"] = (mi, mo)
+        else:
+            mlp = Irreps("16x0e")
+            for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(hid, mlp)):
+                shapes[f"{r}.linear_1.weights.{n}"] = (mi, mo)
+            for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(mlp, Irreps("0e"))):
+                shapes[f"{r}.linear_2.weights.{n}"] = (mi, mo)
+    return shapes
+
+
+def random_init(cfg: ModelConfig, seed: int = 0) -> Dict[str, np.ndarray]:
+    """Random-init weights with the reference's initialisation distributions.
+
+    Keys are drawn in sorted order from one ``np.random.default_rng(seed)``
+    stream, so the result depends only on (cfg, seed)."""
+    rng = np.random.default_rng(seed)
+    shapes = weight_shapes(cfg)
+    w: Dict[str, np.ndarray] = {}
+    for key in sorted(shapes):
+        shp = shapes[key]
+        if key == "atomic_energies_fn.atomic_energies":
+            ae = cfg.atomic_energies
+            w[key] = np.zeros(shp) if ae is None else np.asarray(ae, dtype=np.float64).reshape(shp)
+        elif key == "radial_embedding.bessel_fn.bessel_weights":
+            w[key] = np.arange(1, shp[0] + 1, dtype=np.float64) * math.pi / cfg.r_max
+        elif ".conv_tp_weights." in key:
+            layer = int(key.split(".layers.")[1].split(".")[0])
+            scale = 1.0 / math.sqrt(shp[1]) * (SILU_NORM_FACTOR if layer > 0 else 1.0)
+            w[key] = rng.standard_normal(shp) * scale
+        elif ".symmetric_contractions." in key:
+            w[key] = rng.standard_normal(shp) / shp[1]
+        else:
+            w[key] = rng.standard_normal(shp)
+    return {k: v.astype(np.float32) for k, v in w.items()}

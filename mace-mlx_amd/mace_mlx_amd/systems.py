@@ -1,0 +1,146 @@
+"""Synthetic structures and models for the five benchmark configurations.
+
+ASE is not required.  Lattices are built in the order ASE uses
+(``bulk(..., cubic=True)`` followed by ``atoms.repeat((n1, n2, n3))``: copies of
+the conventional cell ordered with the first repeat index outermost), and rattled
+the way the reference's benchmarks do it
+(``pos += np.random.default_rng(seed).normal(scale=sigma, size=(N, 3))``,
+`docs/prototypes/xbench.py:85-86`).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from pathlib import Path
+from typing import List, Optional
+
+import numpy as np
+
+from .model_io import ModelConfig, random_init, save_model
+
+# conventional cells in fractional coordinates
+_DIAMOND = np.array([
+    (0, 0, 0), (0.25, 0.25, 0.25), (0, 0.5, 0.5), (0.25, 0.75, 0.75),
+    (0.5, 0, 0.5), (0.75, 0.25, 0.75), (0.5, 0.5, 0), (0.75, 0.75, 0.25)])
+_FCC = np.array([(0, 0, 0), (0, 0.5, 0.5), (0.5, 0, 0.5), (0.5, 0.5, 0)])
+
+HEA_SPECIES = [26, 28, 27, 24, 25]  # Fe, Ni, Co, Cr, Mn
+
+
+@dataclass
+class System:
+    """Plain structure record (positions in Angstrom, Cartesian)."""
+
+    positions: np.ndarray      # (N, 3) float64
+    numbers: np.ndarray        # (N,) int64 atomic numbers
+    cell: np.ndarray           # (3, 3) float64, rows are lattice vectors
+    pbc: np.ndarray            # (3,) bool
+    name: str = ""
+
+    def __len__(self) -> int:
+        return len(self.numbers)
+
+    # duck-typed subset of ase.Atoms used by the calculator
+    def get_positions(self):
+        return self.positions.copy()
+
+    def get_atomic_numbers(self):
+        return self.numbers.copy()
+
+    def get_cell(self):
+        return self.cell.copy()
+
+    def copy(self) -> "System":
+        return System(self.positions.copy(), self.numbers.copy(), self.cell.copy(),
+                      self.pbc.copy(), self.name)
+
+
+def lattice(basis: np.ndarray, a: float, reps, z) -> System:
+    reps = tuple(int(r) for r in reps)
+    cell0 = np.eye(3) * a
+    frac = []
+    for m0 in range(reps[0]):
+        for m1 in range(reps[1]):
+            for m2 in range(reps[2]):
+                frac.append(basis + np.array([m0, m1, m2], dtype=np.float64))
+    frac = np.concatenate(frac, axis=0)
+    pos = frac @ cell0
+    cell = cell0 * np.array(reps, dtype=np.float64)[:, None]
+    n = len(pos)
+    numbers = np.full(n, z, dtype=np.int64) if np.isscalar(z) else np.asarray(z, np.int64)
+    return System(pos, numbers, cell, np.array([True, True, True]))
+
+
+def diamond_si(reps, a: float = 5.43) -> System:
+    return lattice(_DIAMOND, a, reps, 14)
+
+
+def rattle(s: System, sigma: float, seed: int, rng: Optional[np.random.Generator] = None) -> System:
+    rng = np.random.default_rng(seed) if rng is None else rng
+    out = s.copy()
+    out.positions = out.positions + rng.normal(scale=sigma, size=out.positions.shape)
+    return out
+
+
+def arch_config(arch: str, num_elements: int = 1, z_table=None, zbl: bool = False,
+                atomic_energies=None, avg_num_neighbors: float = 1.0) -> ModelConfig:
+    hidden = {"small": "128x0e", "medium": "128x0e+128x1o",
+              "large": "128x0e+128x1o+128x2e"}[arch]
+    return ModelConfig(
+        r_max=6.0, num_bessel=8, num_polynomial_cutoff=5, max_ell=3,
+        num_interactions=2, hidden_irreps=hidden, correlation=[3, 3],
+        num_elements=num_elements, atomic_energies=atomic_energies,
+        avg_num_neighbors=avg_num_neighbors, radial_MLP=[64, 64, 64],
+        model_type="MACE", z_table=list(z_table) if z_table is not None else [14],
+        pair_repulsion={"p": 6, "a_exp": 0.3, "a_prefactor": 0.4543} if zbl else None,
+    )
+
+
+@dataclass
+class BenchConfig:
+    index: int
+    name: str
+    system: System
+    model: ModelConfig
+    properties: List[str]
+    dtype: str = "float32"
+
+
+def make_config(index: int) -> BenchConfig:
+    """Configurations 1..5 of the benchmark definition (0-based index 0..4)."""
+    if index == 0:
+        s = rattle(diamond_si((2, 2, 2)), 0.01, 0)
+        m = arch_config("small")
+        return BenchConfig(0, "Si64-small", s, m, ["energy", "forces"])
+    if index == 1:
+        s = rattle(diamond_si((5, 5, 5)), 0.03, 1)
+        m = arch_config("medium", zbl=True)
+        return BenchConfig(1, "Si1000-medium", s, m, ["energy", "forces"])
+    if index == 2:
+        s = diamond_si((5, 5, 10))
+        s.positions *= 1.02
+        s.cell *= 1.02
+        s = rattle(s, 0.03, 2)
+        m = arch_config("medium")
+        return BenchConfig(2, "Si2000-medium-strained", s, m, ["energy", "forces", "stress"])
+    if index == 3:
+        s = rattle(diamond_si((8, 8, 8)), 0.05, 3)
+        m = arch_config("large")
+        return BenchConfig(3, "Si4096-large", s, m, ["energy", "forces", "stress"])
+    if index == 4:
+        rng = np.random.default_rng(4)
+        base = lattice(_FCC, 3.6, (20, 20, 20), 26)
+        kinds = rng.integers(0, 5, len(base))
+        base.numbers = np.array(HEA_SPECIES, dtype=np.int64)[kinds]
+        s = rattle(base, 0.05, 4, rng=rng)
+        e0rng = np.random.default_rng(1004)
+        e0 = (-5.0 + e0rng.normal(scale=2.0, size=89)).tolist()
+        m = arch_config("medium", num_elements=89, z_table=range(1, 90),
+                        atomic_energies=e0)
+        return BenchConfig(4, "HEA32000-medium-fp16", s, m, ["energy", "forces"],
+                           dtype="float16")
+    raise ValueError(index)
+
+
+def write_model_dir(cfg: ModelConfig, path, seed: int = 0) -> Path:
+    return save_model(path, cfg, random_init(cfg, seed))

@@ -1,0 +1,34 @@
+"""CPU parity oracle -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this package, and only as the checker / CPU baseline.
+The product path (``mace_mlx_amd``) never imports it and has no CPU fallback:
+without the HIP library it raises.
+
+Contents
+--------
+``model``      PyTorch-CPU (float64 / float32) restatement of the reference MACE
+               energy model; forces and stress come from torch autograd, i.e.
+               independently of the hand-written GPU VJPs.
+``neighbors``  float64 brute-force periodic neighbour enumeration (i, j, S).
+
+Pinning (what checks each part against something other than itself):
+
+* coupling constants (3j, D, U) -- golden vectors written from the reference's
+  own `clebsch_gordan.py` (tests/golden/cg_fixtures.npz) plus 3j invariants;
+* spherical harmonics -- closed forms for l <= 2, component norm 2l+1,
+  equivariance under the reference's Wigner-D;
+* Bessel / cutoff / ZBL -- closed-form values and boundary behaviour;
+* neighbour list -- edge counts recorded by the reference (2944 for Si64,
+  46000 for Si1000, `docs/prototypes/profile_results.json`), shell counts, and
+  the (i, j, S) <-> (j, i, -S) pairing;
+* whole model -- finite-difference forces and stress, translation / rotation /
+  permutation invariance, sum of forces = 0, stress symmetry, the stress-path
+  forces equal the energy-path forces, single-atom and far-pair cases;
+* symmetric contraction -- the row-compressed main step equals the dense einsum
+  definition (`symmetric_contraction.py:95-121`) on random tensors.
+
+Parity unpinned: the MLX-executed values of the reference itself (MLX is not
+installable here), MLX's RNG / initialisers (weights are exchanged as files),
+and ASE's covalent-radius table (a published table is vendored instead).
+"""
