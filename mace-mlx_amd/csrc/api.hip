@@ -796,7 +796,7 @@ int mace_set_system(mace_ctx* c, int32_t n, const int32_t* species, const double
     c->species.ensure(std::max(n, 1));
     if (n > 0) HIPCHK(hipMemcpy(c->species.p, species, (size_t)n * sizeof(int), hipMemcpyHostToDevice));
     c->species_h.assign(species, species + n);
-    if (topo_changed) {
+    if (topo_changed || c->edges_manual) {  // a manual edge list lasts until the next set_system
       c->nl_valid = false;
       c->edges_manual = false;
     }

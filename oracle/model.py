@@ -445,8 +445,10 @@ class OracleMACE:
         pos.requires_grad_(True)
         vec = pos[r] - pos[s] + S @ cl
         E, ne = self.energy_from_vectors(vec, sp, s, r)
+        if not E.requires_grad:   # no edges: the energy does not depend on positions
+            return float(E), np.zeros(pos.shape), ne.detach().numpy()
         (g,) = torch.autograd.grad(E, pos)
-        return float(E), (-g).numpy(), ne.detach().numpy()
+        return float(E.detach()), (-g).numpy(), ne.detach().numpy()
 
     def energy_forces_stress(self, positions, species, edge_index, shifts, cell):
         """`calculators.py:482-563`: symmetric displacement, stress = dE/d(eps)/V
@@ -459,7 +461,12 @@ class OracleMACE:
         cs = cl + cl @ sym
         vec = ps[r] - ps[s] + S @ cs
         E, ne = self.energy_from_vectors(vec, sp, s, r)
-        gp, gd = torch.autograd.grad(E, (pos, disp))
+        if not E.requires_grad:
+            gp, gd = torch.zeros_like(pos), torch.zeros(3, 3, dtype=self.dtype)
+        else:
+            gp, gd = torch.autograd.grad(E, (pos, disp), allow_unused=True)
+            gd = torch.zeros(3, 3, dtype=self.dtype) if gd is None else gd
+        E = E.detach()
         vol = abs(np.linalg.det(np.asarray(cell, np.float64)))
         st = gd.detach().numpy() / vol
         voigt = st[[0, 1, 2, 1, 0, 0], [0, 1, 2, 2, 2, 1]]

@@ -1,0 +1,81 @@
+"""Shared helpers for the GPU tests: run the engine and the oracle on the same inputs."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from mace_mlx_amd._ffi import Engine
+from mace_mlx_amd.device_model import build_device_model
+from mace_mlx_amd.model_io import random_init
+from oracle.model import OracleMACE
+from oracle.neighbors import neighbor_list
+
+torch.set_num_threads(16)
+
+
+def species_of(dm, numbers):
+    zmap = {int(z): k for k, z in enumerate(dm.z_table)}
+    return np.array([zmap[int(z)] for z in numbers], np.int32)
+
+
+class Case:
+    """Engine + oracle for one (model config, seed)."""
+
+    def __init__(self, cfg, seed=0):
+        self.cfg = cfg
+        self.w = random_init(cfg, seed)
+        self.dm = build_device_model(cfg, self.w)
+        self.eng = Engine(0)
+        self.eng.load_model(self.dm)
+        self._oracle = None
+
+    @property
+    def oracle(self):
+        if self._oracle is None:
+            self._oracle = OracleMACE(cfg=self.cfg, weights=self.w, dtype=torch.float64)
+        return self._oracle
+
+    def run(self, s, stress=False, skin=0.5, force_nl=False):
+        sp = species_of(self.dm, s.numbers)
+        self.eng.set_system(sp, s.cell, s.pbc, skin)
+        E, ne, F, vir = self.eng.step(s.positions, stress=stress, force_nl=force_nl)
+        return dict(E=E, ne=ne, F=F, vir=vir, sp=sp)
+
+    def edges(self):
+        return self.eng.get_edges()
+
+    def reference(self, s, sp, edges, stress=False):
+        snd, rcv, sh = edges
+        ei = np.stack([snd, rcv]).astype(np.int64)
+        if stress:
+            E, F, st, ne, vir = self.oracle.energy_forces_stress(s.positions, sp, ei, sh, s.cell)
+            return dict(E=E, F=F, ne=ne, vir=vir)
+        E, F, ne = self.oracle.energy_forces(s.positions, sp, ei, sh, s.cell)
+        return dict(E=E, F=F, ne=ne)
+
+
+def edge_set(s, r, S):
+    return set(zip(np.asarray(s).tolist(), np.asarray(r).tolist(), map(tuple, np.asarray(S).tolist())))
+
+
+def bruteforce_edges(s, cutoff=6.5):
+    i, j, S = neighbor_list(s.positions, s.cell, s.pbc, cutoff)
+    return edge_set(i, j, S)
+
+
+def assert_parity(got, ref, n_atoms, stress=False, vol=None):
+    """Energy within 1e-6 relative on the scale max(|E|, n_atoms x 1 eV) (i.e. at most
+    1e-6 eV/atom when per-atom energies cancel to << 1 eV: for the random-init large
+    architecture a float32 restatement of the reference itself differs from float64 by
+    1.1e-5 eV on |E| = 7.4 eV, 216 atoms); forces max-abs 1e-4 eV/A; virial 1e-5 relative."""
+    dE = abs(got["E"] - ref["E"])
+    assert dE <= 1e-6 * max(abs(ref["E"]), float(n_atoms)), (got["E"], ref["E"], dE)
+    dF = float(np.abs(got["F"] - ref["F"]).max()) if n_atoms else 0.0
+    assert dF <= 1e-4, dF
+    dne = float(np.abs(got["ne"] - ref["ne"]).max()) if n_atoms else 0.0
+    assert dne <= 1e-5 * max(1.0, float(np.abs(ref["ne"]).max())), dne
+    if stress:
+        dv = np.abs(got["vir"] - ref["vir"]).max()
+        assert dv <= 1e-5 * max(1.0, np.abs(ref["vir"]).max()), (got["vir"], ref["vir"])
+    return dE, dF

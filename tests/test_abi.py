@@ -1,0 +1,45 @@
+"""The C-ABI library: it loads, and exports exactly what include/mace_hip.h declares.
+
+No compute call is made here (this suite also runs without a GPU)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from mace_mlx_amd import _ffi
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "mace_hip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(mace_[a-z_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _ffi.load_library()
+    declared = _declared()
+    assert set(declared) == set(_ffi.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert isinstance(getattr(lib, name), ctypes._CFuncPtr), name
+
+
+def test_model_dims_struct_matches_header():
+    text = HEADER.read_text()
+    body = text[text.index("typedef struct mace_model_dims"):text.index("} mace_model_dims;")]
+    fields = re.findall(r"^\s*(int32_t|double)\s+(\w+)(\[\d+\])?;", body, re.M)
+    names = [f[1] for f in fields]
+    assert names == [f[0] for f in _ffi.ModelDims._fields_]
+    size = 0
+    for ty, _, arr in fields:
+        n = int(arr[1:-1]) if arr else 1
+        sz = 4 if ty == "int32_t" else 8
+        size = (size + sz - 1) // sz * sz + sz * n
+    assert ctypes.sizeof(_ffi.ModelDims) == (size + 7) // 8 * 8
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(ImportError):
+        _ffi.load_library(str(tmp_path / "nope.so"))

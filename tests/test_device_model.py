@@ -1,0 +1,89 @@
+"""Host-side folding of the reference model into the engine's tensors.
+
+The tensors handed to the HIP library (path weights, CG factors, 1/avg_num_neighbors
+and ScaleShift folded in; component-major block layouts) and the generated TP /
+symmetric-contraction tables are re-evaluated in float64 on the CPU
+(tests/kernel_model.py) and compared with the oracle, for every architecture.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import kernel_model
+from mace_mlx_amd.device_model import UnsupportedModel, build_device_model
+from mace_mlx_amd.model_io import ModelConfig, random_init, weight_shapes
+from mace_mlx_amd.systems import arch_config, diamond_si, lattice, rattle, _FCC
+from oracle.model import OracleMACE
+from oracle.neighbors import neighbor_list
+
+
+@pytest.fixture(scope="module")
+def si64():
+    s = rattle(diamond_si((2, 2, 2)), 0.05, 1)
+    i, j, S = neighbor_list(s.positions, s.cell, s.pbc, 6.5)
+    return s, i, j, S
+
+
+@pytest.mark.parametrize("arch", ["small", "medium", "large"])
+@pytest.mark.parametrize("zbl", [False, True])
+def test_kernel_formulation_matches_oracle(si64, arch, zbl):
+    s, i, j, S = si64
+    cfg = arch_config(arch, zbl=zbl)
+    w = random_init(cfg, 3)
+    sp = np.zeros(len(s), int)
+    Eo, neo = OracleMACE(cfg=cfg, weights=w).energy(s.positions, sp, np.stack([i, j]), S, s.cell)
+    Ek, nek = kernel_model.energy(build_device_model(cfg, w), s.positions, sp, i, j, S.astype(float), s.cell)
+    np.testing.assert_allclose(nek, neo, atol=5e-6)
+    assert abs(Ek - Eo) < 1e-6 * max(1.0, abs(Eo)) * len(s)
+
+
+def test_scaleshift_and_multielement():
+    """ScaleShiftMACE (model.py:550-589) folded into readouts / ZBL / e0; 3 species."""
+    base = lattice(_FCC, 3.6, (2, 2, 2), 26)
+    rng = np.random.default_rng(0)
+    base.numbers = np.array([26, 28, 24])[rng.integers(0, 3, len(base))]
+    s = rattle(base, 0.05, 2)
+    cfg = arch_config("medium", num_elements=3, z_table=[24, 26, 28], zbl=True,
+                      atomic_energies=[-3.0, -1.5, 0.25])
+    cfg.model_type = "ScaleShiftMACE"
+    cfg.scale, cfg.shift = 1.7, -0.3
+    w = random_init(cfg, 5)
+    zmap = {24: 0, 26: 1, 28: 2}
+    sp = np.array([zmap[z] for z in s.numbers])
+    i, j, S = neighbor_list(s.positions, s.cell, s.pbc, 6.5)
+    Ek, nek = kernel_model.energy(build_device_model(cfg, w), s.positions, sp, i, j, S.astype(float), s.cell)
+    # oracle: plain MACE energy terms, then scale/shift applied as in ScaleShiftMACE
+    plain = arch_config("medium", num_elements=3, z_table=[24, 26, 28], zbl=True,
+                        atomic_energies=[0.0, 0.0, 0.0])
+    m = OracleMACE(cfg=plain, weights={**w, "atomic_energies_fn.atomic_energies": np.zeros(3, np.float32)})
+    _, ne_inter = m.energy(s.positions, sp, np.stack([i, j]), S, s.cell)
+    e0 = np.array([-3.0, -1.5, 0.25])[sp]
+    want = e0 + 1.7 * ne_inter - 0.3
+    np.testing.assert_allclose(nek, want, atol=1e-5)
+
+
+def test_weight_inventory_matches_reference_layout():
+    cfg = arch_config("medium", zbl=True)
+    shapes = weight_shapes(cfg)
+    # key names of converter.py / the MLX module tree
+    for key in ["interactions.1.conv_tp_weights.layers.6.weight",
+                "products.0.symmetric_contractions.contractions.1.weights_max",
+                "products.0.symmetric_contractions.contractions.1.weights.1",
+                "interactions.0.skip_tp.tp.weights.0", "readouts.1.linear_2.weights.0"]:
+        assert key in shapes
+    assert shapes["interactions.1.conv_tp_weights.layers.6.weight"] == (1280, 64)
+    assert shapes["products.0.symmetric_contractions.contractions.1.weights_max"] == (1, 51, 128)
+    assert shapes["interactions.1.linear.weights.0"] == (128, 128)
+    assert sum(k.startswith("interactions.1.linear.weights") for k in shapes) == 10
+
+
+def test_unsupported_topologies_raise():
+    cfg = arch_config("medium")
+    w = random_init(cfg, 0)
+    bad = ModelConfig.from_dict({**cfg.to_dict(), "hidden_irreps": "128x0e+64x1o"})
+    with pytest.raises((UnsupportedModel, NotImplementedError, KeyError)):
+        build_device_model(bad, w)
+    bad2 = ModelConfig.from_dict({**cfg.to_dict(), "use_density_normalization": True})
+    with pytest.raises(NotImplementedError):
+        build_device_model(bad2, w)

@@ -1,0 +1,273 @@
+"""GPU parity: the HIP engine against the CPU oracle on the same seeded inputs.
+
+Tolerances (written here, from the benchmark definition): energy relative 1e-6
+on the scale max(|E|, N x 1 eV) (see gpu_helpers.assert_parity), forces max-abs 1e-4 eV/A, stress/virial relative 1e-5; neighbour lists equal as
+sets of (i, j, S) to the float64 brute force.  Full-size configurations that the
+oracle cannot evaluate in seconds are checked through size-independent
+properties (periodic replication, translation / rotation covariance, sum of
+forces, pairing symmetry of the edge list).
+"""
+
+import numpy as np
+import pytest
+
+from gpu_helpers import Case, assert_parity, bruteforce_edges, edge_set, species_of
+from mace_mlx_amd.systems import System, _DIAMOND, _FCC, arch_config, diamond_si, lattice, make_config, rattle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def small():
+    return Case(arch_config("small"))
+
+
+@pytest.fixture(scope="module")
+def medium_zbl():
+    return Case(arch_config("medium", zbl=True))
+
+
+@pytest.fixture(scope="module")
+def medium():
+    return Case(arch_config("medium"))
+
+
+@pytest.fixture(scope="module")
+def large():
+    return Case(arch_config("large"))
+
+
+# ---------------------------------------------------------------------------
+# benchmark configurations
+# ---------------------------------------------------------------------------
+
+def test_config1_si64_small(small):
+    s = make_config(0).system
+    got = small.run(s)
+    edges = small.edges()
+    assert len(edges[0]) == 2944
+    assert edge_set(*edges) == bruteforce_edges(s)
+    assert_parity(got, small.reference(s, got["sp"], edges), len(s))
+
+
+def test_config2_si1000_medium_zbl(medium_zbl):
+    bc = make_config(1)
+    s = bc.system
+    got = medium_zbl.run(s)
+    edges = medium_zbl.edges()
+    assert edge_set(*edges) == bruteforce_edges(s)
+    assert_parity(got, medium_zbl.reference(s, got["sp"], edges), len(s))
+
+
+def test_config3_strained_stress_reduced(medium):
+    """Configuration 3 recipe (+2% strain, sigma 0.03, E+F+S) on a 3x3x6 cell."""
+    s = diamond_si((3, 3, 6))
+    s.positions *= 1.02
+    s.cell *= 1.02
+    s = rattle(s, 0.03, 2)
+    got = medium.run(s, stress=True)
+    edges = medium.edges()
+    assert edge_set(*edges) == bruteforce_edges(s)
+    assert_parity(got, medium.reference(s, got["sp"], edges, stress=True), len(s), stress=True)
+
+
+def test_config4_large_l2_paths_reduced(large):
+    """Configuration 4 recipe (large arch, L=2 CG paths, E+F+S) on a 3x3x3 cell."""
+    s = rattle(diamond_si((3, 3, 3)), 0.05, 3)
+    got = large.run(s, stress=True)
+    edges = large.edges()
+    assert_parity(got, large.reference(s, got["sp"], edges, stress=True), len(s), stress=True)
+
+
+def test_hea_89_elements_reduced():
+    """Configuration 5 recipe (5 species of an 89-element one-hot, random E0),
+    float32 feature path, on 3x3x3 FCC conventional cells."""
+    bc = make_config(4)
+    case = Case(bc.model)
+    rng = np.random.default_rng(4)
+    base = lattice(_FCC, 3.6, (3, 3, 3), 26)
+    base.numbers = np.array([26, 28, 27, 24, 25])[rng.integers(0, 5, len(base))]
+    s = rattle(base, 0.05, 4, rng=rng)
+    got = case.run(s)
+    edges = case.edges()
+    assert edge_set(*edges) == bruteforce_edges(s)
+    assert_parity(got, case.reference(s, got["sp"], edges), len(s))
+
+
+# ---------------------------------------------------------------------------
+# full-size configurations: size-independent properties
+# ---------------------------------------------------------------------------
+
+def _rot(seed):
+    q = np.linalg.qr(np.random.default_rng(seed).normal(size=(3, 3)))[0]
+    return q * np.sign(np.linalg.det(q))
+
+
+@pytest.mark.parametrize("idx", [2, 3])
+def test_full_size_invariants(idx, medium, large):
+    bc = make_config(idx)
+    case = medium if idx == 2 else large
+    s = bc.system
+    a = case.run(s, stress=True)
+    Fmax = np.abs(a["F"]).max()
+    assert np.abs(a["F"].sum(0)).max() < 1e-5 * max(1.0, Fmax) * np.sqrt(len(s))
+    np.testing.assert_allclose(a["vir"], a["vir"].T, atol=1e-9 * np.abs(a["vir"]).max())
+    t = s.copy()
+    t.positions = t.positions + np.array([0.37, -1.21, 0.58])
+    b = case.run(t, stress=True)
+    assert abs(b["E"] - a["E"]) <= 1e-6 * abs(a["E"])
+    assert np.abs(b["F"] - a["F"]).max() <= 1e-4
+    R = _rot(idx)
+    r = System(s.positions @ R.T, s.numbers, s.cell @ R.T, s.pbc)
+    c = case.run(r, stress=True)
+    assert abs(c["E"] - a["E"]) <= 1e-6 * abs(a["E"])
+    assert np.abs(c["F"] - a["F"] @ R.T).max() <= 1e-4
+    np.testing.assert_allclose(c["vir"], R @ a["vir"] @ R.T, atol=1e-5 * np.abs(a["vir"]).max())
+
+
+def test_periodic_replication_is_exact(medium_zbl):
+    """Doubling a periodic cell doubles E and repeats F (Si1000 -> Si2000)."""
+    s = make_config(1).system
+    a = medium_zbl.run(s, stress=True)
+    n = len(s)
+    d = System(np.concatenate([s.positions, s.positions + s.cell[0]]), np.concatenate([s.numbers, s.numbers]),
+               s.cell * np.array([[2.0], [1.0], [1.0]]), s.pbc)
+    b = medium_zbl.run(d, stress=True)
+    assert abs(b["E"] - 2 * a["E"]) <= 1e-6 * abs(b["E"])
+    assert np.abs(b["F"][:n] - a["F"]).max() <= 1e-4 and np.abs(b["F"][n:] - a["F"]).max() <= 1e-4
+    np.testing.assert_allclose(b["vir"], 2 * a["vir"], rtol=1e-5, atol=1e-6)
+
+
+def test_hea_full_size_runs_and_pairs():
+    bc = make_config(4)
+    case = Case(bc.model)
+    got = case.run(bc.system)
+    snd, rcv, sh = case.edges()
+    s = bc.system
+    d = np.linalg.norm(s.positions[rcv] - s.positions[snd] + sh @ s.cell, axis=1)
+    assert (d < 6.5).all()
+    def keys(a, b, S):
+        return np.sort(((a.astype(np.int64) * 40000 + b) * 1000 + (S[:, 0] + 5) * 100 + (S[:, 1] + 5) * 10
+                        + (S[:, 2] + 5)))
+    assert np.array_equal(keys(snd, rcv, sh), keys(rcv, snd, -sh))
+    assert 84 * len(s) < len(snd) < 90 * len(s)   # FCC a=3.6: 86 neighbours within 6.5 A
+    assert np.isfinite(got["E"]) and np.isfinite(got["F"]).all()
+    assert np.abs(got["F"].sum(0)).max() < 1e-4 * np.sqrt(len(s))
+
+
+# ---------------------------------------------------------------------------
+# neighbour list geometry cases
+# ---------------------------------------------------------------------------
+
+def _grid(n):
+    g = np.stack(np.meshgrid(*[np.arange(k) for k in n], indexing="ij"), -1).reshape(-1, 3)
+    return (g + 0.5) / np.array(n)
+
+
+def _triclinic():
+    cell = np.array([[7.1, 0.0, 0.0], [2.3, 6.8, 0.0], [-1.4, 1.9, 7.4]])
+    frac = _grid((3, 3, 4)) + np.random.default_rng(9).normal(scale=0.02, size=(36, 3))
+    return System(frac @ cell, np.full(36, 14), cell, np.array([True, True, True]))
+
+
+def _molecule():
+    pos = _grid((3, 3, 3)) * 7.2 + np.random.default_rng(10).normal(scale=0.1, size=(27, 3))
+    return System(pos, np.full(27, 14), np.zeros((3, 3)), np.array([False, False, False]))
+
+
+def _slab():
+    s = rattle(diamond_si((2, 2, 1)), 0.05, 12)
+    s.pbc = np.array([True, True, False])
+    return s
+
+
+def _small_cell_unwrapped():
+    s = rattle(diamond_si((1, 1, 1)), 0.05, 13)   # 8 atoms, L = 5.43 < cutoff: many images
+    s.positions[::3] += s.cell[1] * 2 - s.cell[2]
+    return s
+
+
+@pytest.mark.parametrize("make", [_triclinic, _molecule, _slab, _small_cell_unwrapped])
+def test_neighbor_list_geometries(make, small):
+    s = make()
+    got = small.run(s, stress=bool(s.pbc.all()))
+    edges = small.edges()
+    assert edge_set(*edges) == bruteforce_edges(s)
+    ref = small.reference(s, got["sp"], edges, stress=bool(s.pbc.all()))
+    assert_parity(got, ref, len(s), stress=bool(s.pbc.all()))
+
+
+def test_skin_cache(medium_zbl):
+    s = make_config(1).system
+    medium_zbl.run(s)
+    e0 = medium_zbl.edges()
+    moved = s.copy()
+    moved.positions = moved.positions + np.random.default_rng(1).normal(scale=0.04, size=moved.positions.shape)
+    assert np.linalg.norm(moved.positions - s.positions, axis=1).max() < 0.25
+    sp = species_of(medium_zbl.dm, s.numbers)
+    E, ne, F, _ = medium_zbl.eng.step(moved.positions)
+    assert medium_zbl.eng.timings()[1] == 0.0            # cached: no rebuild
+    e1 = medium_zbl.edges()
+    assert edge_set(*e1) == edge_set(*e0)
+    ref = medium_zbl.reference(moved, sp, e1)
+    assert_parity(dict(E=E, F=F, ne=ne), ref, len(s))
+    far = s.copy()
+    far.positions[7] += np.array([0.4, 0.0, 0.0])        # > skin / 2: rebuild
+    medium_zbl.eng.step(far.positions)
+    assert medium_zbl.eng.timings()[1] > 0.0
+    assert edge_set(*medium_zbl.edges()) == bruteforce_edges(far)
+
+
+def test_isolated_atoms_and_no_edges(small):
+    one = System(np.zeros((1, 3)), np.array([14]), np.eye(3) * 30.0, np.array([True, True, True]))
+    a = small.run(one, stress=True)
+    assert len(small.edges()[0]) == 0
+    assert np.abs(a["F"]).max() == 0.0 and np.abs(a["vir"]).max() == 0.0
+    pair = System(np.array([[0.0, 0, 0], [10.0, 0, 0]]), np.array([14, 14]), np.eye(3) * 40.0,
+                  np.array([True, True, True]))
+    b = small.run(pair)
+    assert abs(b["E"] - 2 * a["E"]) < 1e-9 and np.abs(b["F"]).max() == 0.0
+    ref = small.reference(one, a["sp"], small.edges())
+    assert abs(a["E"] - ref["E"]) < 1e-5
+
+
+def test_deterministic_and_edge_order_independent(medium_zbl):
+    s = make_config(1).system
+    a = medium_zbl.run(s, force_nl=True)
+    b = medium_zbl.run(s, force_nl=True)
+    assert a["E"] == b["E"] and np.array_equal(a["F"], b["F"])
+    snd, rcv, sh = medium_zbl.edges()
+    perm = np.random.default_rng(0).permutation(len(snd))
+    medium_zbl.eng.set_edges(snd[perm], rcv[perm], sh[perm])
+    E, ne, F, _ = medium_zbl.eng.step(s.positions)
+    assert abs(E - a["E"]) < 1e-6 * abs(a["E"]) and np.abs(F - a["F"]).max() < 1e-5
+
+
+def test_species_out_of_range_raises(small):
+    with pytest.raises(ValueError):
+        small.eng.set_system(np.array([0, 3], np.int32), np.eye(3) * 10, [True] * 3, 0.5)
+
+
+def test_calculator_end_to_end(tmp_path):
+    from mace_mlx_amd import MACECalculator
+    from mace_mlx_amd.systems import write_model_dir
+    bc = make_config(1)
+    d = write_model_dir(bc.model, tmp_path / "si-medium", seed=0)
+    calc = MACECalculator(model_path=str(d), device="cuda")
+    s = bc.system
+    calc.calculate(s, ["energy", "forces"])
+    r = dict(calc.results)
+    assert set(r) >= {"energy", "free_energy", "forces", "node_energy", "energies"}
+    assert "stress" not in r
+    case = Case(bc.model)
+    ref = case.run(s)
+    assert abs(r["energy"] - ref["E"]) < 1e-9 * abs(ref["E"])
+    calc.calculate(s, ["stress"])
+    assert "stress" in calc.results and calc.results["stress"].shape == (6,)
+    calc.calculate(s, ["energy"])            # sticky stress (calculators.py:385-388)
+    assert "stress" in calc.results
+    bad = s.copy()
+    bad.numbers = bad.numbers.copy()
+    bad.numbers[0] = 8
+    with pytest.raises(ValueError):
+        calc.calculate(bad, ["energy"])
