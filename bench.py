@@ -1,0 +1,258 @@
+"""Benchmark: ms per energy+forces step and atom-steps/s on one MI355X.
+
+Workload: diamond Si 5x5x5 (1000 atoms, rattled
+sigma 0.03 from seed 1), MACE 'medium' architecture (128x0e+128x1o, lmax 3,
+correlation 3, 2 layers, 8 Bessel, r_cut 6, ZBL on), random-init fp32 weights
+from seed 0, energy + forces per step; neighbour list cached (skin 0.5, the
+reference's benchmark protocol, docs/prototypes/xbench.py:89-101).
+
+Timed region: W warm-up steps, then K steps of ``mace_step_device`` (positions
+and results resident in HBM; no host copies), bracketed by device
+synchronisation.  A second pass of K steps with per-launch HIP events gives each
+kernel's average duration; the dominant kernel's algorithmic bytes (or flops)
+per launch divided by that duration is the roofline ``achieved`` figure.  The CPU
+baseline is the float32 CPU oracle (a restatement of the reference algorithm;
+MLX cannot run here) on the host cores, on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--config 1]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "mace-mlx_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+FP32_MFMA_PEAK_TFS = 157.3     # MI355X dense fp32 matrix
+
+
+def algorithmic_work(site: str, ctx: dict):
+    """(bound, amount per launch, unit) for a kernel site of the step.
+
+    Bytes count compulsory unique traffic (node arrays once, fp32, int32
+    indices); flops count multiply-adds as 2."""
+    N, E, C, nb, H = ctx["N"], ctx["E"], 128, ctx["nb"], 64
+    name, _, lyr = site.partition(".L")
+    lay = ctx["layers"][int(lyr)] if lyr else None
+    if name == "tp_fwd":
+        b = 4 * (N * lay["din"] + E * 16 + E * lay["wn"] + N * lay["dmid"]) + 4 * (E + N + 1)
+        return "hbm", b, "GB/s"
+    if name == "tp_bwd":
+        gup = lay["din"] if int(lyr) > 0 else 0
+        b = 4 * (N * lay["dmid"] + N * lay["din"] + N * gup + 2 * E * 16 + 2 * E * lay["wn"]) + 8 * (E + N + 1)
+        return "hbm", b, "GB/s"
+    if name == "mlp_fwd":
+        return "mfma", 2 * E * (nb * H + 2 * H * H + H * lay["wn"]), "TFLOP/s"
+    if name == "mlp_bwd":
+        return "mfma", 2 * E * (2 * (nb * H + 2 * H * H) + H * lay["wn"]), "TFLOP/s"
+    if name.startswith("linear") or name.startswith("skip"):
+        return "mfma", ctx["linear_flops"].get(site, 0), "TFLOP/s"
+    if name in ("sc_fwd", "sc_bwd"):
+        return "hbm", 4 * N * (16 * C + lay["dhid"]) * (2 if name == "sc_bwd" else 1), "GB/s"
+    if name == "edge_fwd":
+        return "hbm", E * (8 + 12 + 16 + 16 * 4 + nb * 4 + 4) + N * 24, "GB/s"
+    if name == "edge_bwd":
+        return "hbm", E * (16 + 16 * 4 + nb * 4 + 12 + 8), "GB/s"
+    if name == "forces":
+        return "hbm", E * (12 * 2 + 8) + N * 24 + 8 * (N + 1), "GB/s"
+    return "hbm", 0, "GB/s"
+
+
+def linear_flops(cfg_layers, N):
+    """2 * rows * K * Cout summed per linear site (all blocks of a layer)."""
+    out = {}
+    C = 128
+    for l, lay in enumerate(cfg_layers):
+        lin, lhid, nslot_by_l = lay["lin"], lay["lhid"], lay["nslot_by_l"]
+        up = sum(2 * N * (2 * b + 1) * C * C for b in range(lin))
+        msg = sum(2 * N * (2 * lo + 1) * nslot_by_l[lo] * C * C for lo in range(4))
+        prod = sum(2 * N * (2 * b + 1) * C * C for b in range(lhid))
+        skip = sum(2 * N * (2 * b + 1) * C * C for b in range(min(lin, lhid)))
+        out.update({f"linear_up.L{l}": up, f"linear_msg.L{l}": msg, f"linear_prod.L{l}": prod,
+                    f"skip.L{l}": skip, f"linear_up_bwd.L{l}": up, f"linear_msg_bwd.L{l}": msg,
+                    f"linear_prod_bwd.L{l}": prod, f"skip_bwd.L{l}": skip})
+    return out
+
+
+def load_traffic(site: str):
+    """HBM bytes per launch of `site` measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    (profiles/traffic.json, written from the committed pmc summaries), or None."""
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        d = json.loads(p.read_text())
+        rec = d.get(site)
+        return None if rec is None else float(rec["bytes_per_launch"])
+    except Exception:
+        return None
+
+
+def cpu_baseline(bc, weights, edges, species, budget_s=25.0):
+    """float32 oracle on the host cores (bounded sample: 1 warm-up + up to 3 steps)."""
+    import torch
+    sys.path.insert(0, str(ROOT))
+    from oracle.model import OracleMACE
+    threads = torch.get_num_threads()
+    m = OracleMACE(cfg=bc.model, weights=weights, dtype=torch.float32)
+    s = bc.system
+    ei = np.stack([edges[0], edges[1]]).astype(np.int64)
+    t0 = time.perf_counter()
+    m.energy_forces(s.positions, species, ei, edges[2], s.cell)
+    warm = time.perf_counter() - t0
+    times = []
+    while len(times) < 3 and sum(times) + warm < budget_s:
+        t = time.perf_counter()
+        m.energy_forces(s.positions, species, ei, edges[2], s.cell)
+        times.append(time.perf_counter() - t)
+    med = float(np.median(times)) if times else warm
+    return {"value": len(s) / med, "unit": "atom-steps/s", "cores": threads, "kind": "port",
+            "sample": f"{bc.name} E+F, float32 CPU oracle (torch, {threads} threads), median of "
+                      f"{max(len(times), 1)} step(s) after 1 warm-up; {med * 1e3:.0f} ms/step"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=1, help="benchmark configuration index 0..4")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-table", action="store_true", help="print per-kernel times to stderr")
+    ap.add_argument("--copy-calib-mb", type=float, default=0.0,
+                    help="run a plain device copy of this size first (rocprof counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "multi-GPU sharding is design-only", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from mace_mlx_amd._ffi import Engine
+    from mace_mlx_amd.device_model import build_device_model
+    from mace_mlx_amd.model_io import random_init
+    from mace_mlx_amd.systems import make_config
+    sys.path.insert(0, str(ROOT / "mace-mlx_amd" / "csrc"))
+    import gen_tables
+
+    if args.copy_calib_mb > 0:
+        n = int(args.copy_calib_mb * (1 << 20) // 4)
+        a = torch.ones(n, device="cuda", dtype=torch.float32)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+
+    bc = make_config(args.config)
+    if bc.dtype != "float32":
+        print(f"configuration {bc.name}: {bc.dtype} feature path not built; running float32", file=sys.stderr)
+    weights = random_init(bc.model, 0)
+    dm = build_device_model(bc.model, weights)
+    eng = Engine(0)
+    eng.load_model(dm)
+    s = bc.system
+    zmap = {int(z): k for k, z in enumerate(dm.z_table)}
+    species = np.array([zmap[int(z)] for z in s.numbers], np.int32)
+    eng.set_system(species, s.cell, s.pbc, 0.5)
+    stress = "stress" in bc.properties
+    E_host, _, F_host, _ = eng.step(s.positions, stress=stress)          # builds the neighbour list
+    edges = eng.get_edges()
+    N, E = len(s), len(edges[0])
+
+    pos_d = torch.from_numpy(np.ascontiguousarray(s.positions, dtype=np.float64)).cuda()
+    out_d = torch.zeros(10 + 3 * N, dtype=torch.float64, device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress)
+    eng.sync()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress)
+    eng.sync()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) / args.steps * 1e3
+    out = out_d.cpu().numpy()
+    assert abs(out[0] - E_host) <= 1e-9 * abs(E_host) and np.abs(out[10:].reshape(N, 3) - F_host).max() < 1e-9
+
+    # host-array path (PCIe-inclusive, as the ASE calculator uses it)
+    th = time.perf_counter()
+    for _ in range(args.steps):
+        eng.step(s.positions, stress=stress)
+    ms_host = (time.perf_counter() - th) / args.steps * 1e3
+
+    # per-kernel pass
+    eng.set_profiling(True)
+    for _ in range(args.steps):
+        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress)
+    kt = eng.kernel_times()
+    eng.set_profiling(False)
+    layers = []
+    for l in range(dm.dims["num_layers"]):
+        lin, lhid = dm.dims["layer_in_blocks"][l], dm.dims["layer_hid_blocks"][l]
+        slots = gen_tables.tp_layout(lin)
+        layers.append(dict(lin=lin, lhid=lhid, din=128 * lin * lin, dhid=128 * lhid * lhid,
+                           dmid=128 * sum(2 * x[2] + 1 for x in slots), wn=128 * len(slots),
+                           nslot_by_l=[sum(1 for x in slots if x[2] == lo) for lo in range(4)]))
+    ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_flops=linear_flops(layers, N))
+    per_step = {k: (v[0] / args.steps, v[1] // args.steps) for k, v in kt.items()}
+    dom = max(per_step, key=lambda k: per_step[k][0])
+    bound, amount, unit = algorithmic_work(dom, ctx)
+    launches = max(per_step[dom][1], 1)
+    avg_ms = per_step[dom][0] / launches
+    if bound == "hbm":
+        achieved = amount / launches / (avg_ms * 1e-3) / 1e9 if launches > 1 else amount / (avg_ms * 1e-3) / 1e9
+        peak = HBM_PEAK_GBS
+    else:
+        achieved = amount / launches / (avg_ms * 1e-3) / 1e12
+        peak = FP32_MFMA_PEAK_TFS
+    roofline = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+                "frac": round(achieved / peak, 4), "traffic": load_traffic(dom), "kernel": dom,
+                "avg_launch_ms": round(avg_ms, 5)}
+    if args.kernel_table:
+        tot = sum(v[0] for v in per_step.values())
+        print(f"{'site':24s} {'ms/step':>9s} {'share':>6s} {'launch':>6s}  roofline", file=sys.stderr)
+        for k, (t, n) in sorted(per_step.items(), key=lambda kv: -kv[1][0]):
+            b, a, u = algorithmic_work(k, ctx)
+            per = t / max(n, 1) * 1e-3
+            ach = (a / max(n, 1)) / per / (1e9 if b == "hbm" else 1e12) if a else 0.0
+            pk = HBM_PEAK_GBS if b == "hbm" else FP32_MFMA_PEAK_TFS
+            print(f"{k:24s} {t:9.4f} {t / tot * 100:5.1f}% {n:6d}  {ach:9.2f} {u} ({ach / pk * 100:.1f}% of {b})",
+                  file=sys.stderr)
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(bc, weights, edges, species)
+    line = {
+        "metric": "ms per energy+forces step (Si1000, medium arch, fp32); atom-steps/sec",
+        "value": round(N * args.steps / (t1 - t0), 1),
+        "unit": "atom-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "ms_per_step_host_arrays": round(ms_host, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded lattice + rattle, random-init weights)",
+        "config": {"workload": bc.name, "n_atoms": N, "n_edges": E,
+                   "properties": "energy+forces+stress" if stress else "energy+forces",
+                   "neighbour_list": "cached (skin 0.5)"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

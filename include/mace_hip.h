@@ -103,6 +103,28 @@ int mace_set_edges(mace_ctx* ctx, int64_t n_edges, const int32_t* sender,
 int mace_get_edges(mace_ctx* ctx, int64_t capacity, int32_t* sender, int32_t* receiver,
                    int32_t* shifts3, int64_t* n_edges);
 
+/* Device-resident variant of mace_step for callers that keep positions and
+ * results in HBM (MD integrators on the GPU, benchmarks).  d_positions: device
+ * array n_atoms x 3 (double); d_out: device array of 10 + 3 n_atoms doubles that
+ * receives [energy, virial (3x3, symmetrised, zero without MACE_STEP_STRESS),
+ * forces (n_atoms x 3)].  Work is queued on the context's stream and the call
+ * returns without synchronising (mace_sync waits).  The neighbour list is used
+ * as cached: the caller guarantees no atom moved more than skin/2 since the last
+ * rebuild, or passes MACE_STEP_FORCE_NL (which rebuilds, synchronously).
+ * No host-side counterpart in the reference (its step always round-trips
+ * through host arrays, calculators.py:455-476). */
+int mace_step_device(mace_ctx* ctx, const double* d_positions, uint32_t flags, double* d_out);
+int mace_sync(mace_ctx* ctx);
+
+/* Per-launch-site device timing (HIP events around every kernel launch of the
+ * step, on the context's stream).  Enabling adds two event records per launch.
+ * mace_get_kernel_times synchronises, then reports for each site its name
+ * ('\n'-separated in names), accumulated milliseconds and launch count, and
+ * resets the accumulators.  *n_sites receives the number of sites. */
+int mace_set_profiling(mace_ctx* ctx, int32_t enable);
+int mace_get_kernel_times(mace_ctx* ctx, char* names, int64_t names_len, double* total_ms,
+                          int64_t* counts, int32_t capacity, int32_t* n_sites);
+
 /* Timing of the last mace_step (device milliseconds, HIP events on the
  * context's stream): [0] whole step, [1] neighbour list (0 if cached),
  * [2] forward, [3] backward.  Returns the number of values written. */

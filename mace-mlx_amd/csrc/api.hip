@@ -129,6 +129,16 @@ struct mace_ctx {
   hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
   double timings[4] = {0, 0, 0, 0};
   bool last_nl = false;
+  // per-launch-site profiling
+  bool profiling = false;
+  std::vector<hipEvent_t> ev_pool;
+  size_t ev_used = 0;
+  struct Pending {
+    std::string name;
+    size_t e0, e1;
+  };
+  std::vector<Pending> pending;
+  std::map<std::string, std::pair<double, int64_t>> prof_acc;
 };
 
 namespace {
@@ -147,6 +157,53 @@ int guard(mace_ctx* ctx, const std::function<void()>& fn) {
 }
 
 void set_device(mace_ctx* c) { HIPCHK(hipSetDevice(c->device)); }
+
+size_t prof_event(mace_ctx* c) {
+  if (c->ev_used == c->ev_pool.size()) {
+    hipEvent_t e;
+    HIPCHK(hipEventCreate(&e));
+    c->ev_pool.push_back(e);
+  }
+  return c->ev_used++;
+}
+
+// Brackets one kernel launch with HIP events on the context stream when
+// profiling is enabled (no-op otherwise).
+struct Site {
+  mace_ctx* c;
+  std::string name;
+  size_t e0 = 0;
+  Site(mace_ctx* ctx, std::string nm) : c(ctx), name(std::move(nm)) {
+    if (!c->profiling) return;
+    e0 = prof_event(c);
+    HIPCHK(hipEventRecord(c->ev_pool[e0], c->stream));
+  }
+  ~Site() noexcept(false) {
+    if (!c->profiling) return;
+    const size_t e1 = prof_event(c);
+    HIPCHK(hipEventRecord(c->ev_pool[e1], c->stream));
+    c->pending.push_back({name, e0, e1});
+  }
+};
+
+void prof_harvest(mace_ctx* c) {
+  if (c->pending.empty()) {
+    c->ev_used = 0;
+    return;
+  }
+  HIPCHK(hipStreamSynchronize(c->stream));
+  for (auto& p : c->pending) {
+    float ms = 0.f;
+    HIPCHK(hipEventElapsedTime(&ms, c->ev_pool[p.e0], c->ev_pool[p.e1]));
+    auto& a = c->prof_acc[p.name];
+    a.first += ms;
+    a.second += 1;
+  }
+  c->pending.clear();
+  c->ev_used = 0;
+}
+
+std::string lname(const char* base, size_t l) { return std::string(base) + ".L" + std::to_string(l); }
 
 const std::vector<float>& tensor(mace_ctx* c, const std::string& name, size_t count) {
   auto it = c->host_tensors.find(name);
@@ -558,46 +615,68 @@ void run_skip_T(mace_ctx* c, Layer& L, int b, const float* gout, int ldg, float*
     launch_linear_species(c->stream, c->N, D, gout, L.skipT[b].p, c->species.p, gh);
 }
 
-void forward(mace_ctx* c) {
+void forward(mace_ctx* c, const double* pos, double* out) {
   hipStream_t st = c->stream;
   const int N = c->N;
   const int64_t E = c->E;
   const int nb = c->dims.num_bessel;
   FrontParams fp = front_params(c);
-  launch_edge_fwd(st, E, c->pos.p, c->sender.p, c->receiver.p, c->shifts.p, c->species.p, c->bessel_w.p, c->zbl_z.p,
-                  c->zbl_cov.p, fp, c->geom.p, c->Y.p, c->ef.p, c->zbl_e.p);
-  launch_embed(st, N, c->species.p, c->embed.p, c->layers[0].din, c->h[0].p);
+  {
+    Site s(c, "edge_fwd");
+    launch_edge_fwd(st, E, pos, c->sender.p, c->receiver.p, c->shifts.p, c->species.p, c->bessel_w.p, c->zbl_z.p,
+                    c->zbl_cov.p, fp, c->geom.p, c->Y.p, c->ef.p, c->zbl_e.p);
+  }
+  {
+    Site s(c, "embed");
+    launch_embed(st, N, c->species.p, c->embed.p, c->layers[0].din, c->h[0].p);
+  }
   for (size_t l = 0; l < c->layers.size(); ++l) {
     Layer& L = c->layers[l];
     const float* h = c->h[l].p;
     float* hn = c->h[l + 1].p;
-    launch_mlp_fwd(st, E, nb, L.wn, c->ef.p, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, L.mlp[3].p, L.w.p);
+    {
+      Site s(c, lname("mlp_fwd", l));
+      launch_mlp_fwd(st, E, nb, L.wn, c->ef.p, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, L.mlp[3].p, L.w.p);
+    }
     for (int b = 0; b < L.lin; ++b) {
+      Site s(c, lname("linear_up", l));
       LinearDesc D = lin_desc(2 * b + 1, NC, NC, L.din, NC * b * b, 0, L.din, NC * b * b, 0, 0);
       launch_linear(st, N, D, h, L.up[b].p, L.h_up.p);
     }
-    launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, L.w.p, L.h_up.p, c->M.p);
+    {
+      Site s(c, lname("tp_fwd", l));
+      launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, L.w.p, L.h_up.p, c->M.p);
+    }
     const int* l3 = tp_l3(L.lin);
     const int* ao = tp_accoff(L.lin);
     const int ns = n_tp_slots(L.lin);
     for (int lo = 0; lo < 4; ++lo) {
       int first = -1, cnt = 0;
-      for (int s = 0; s < ns; ++s)
-        if (l3[s] == lo) {
-          if (first < 0) first = s;
+      for (int q = 0; q < ns; ++q)
+        if (l3[q] == lo) {
+          if (first < 0) first = q;
           ++cnt;
         }
       const int d = 2 * lo + 1;
+      Site s(c, lname("linear_msg", l));
       LinearDesc D = lin_desc(d, cnt * NC, NC, L.dmid, NC * ao[first], NC * d, L.dint, NC * lo * lo, 0, 0);
       launch_linear(st, N, D, c->M.p, L.lin_[lo].p, L.A.p);
     }
     const float* scw[3] = {L.sc[0].p, L.sc[1].p, L.sc[2].p};
-    launch_sc_fwd(st, N, L.lhid, L.corr, L.A.p, L.dint, c->species.p, scw, c->B.p, L.dhid);
+    {
+      Site s(c, lname("sc_fwd", l));
+      launch_sc_fwd(st, N, L.lhid, L.corr, L.A.p, L.dint, c->species.p, scw, c->B.p, L.dhid);
+    }
     for (int b = 0; b < L.lhid; ++b) {
+      Site s(c, lname("linear_prod", l));
       LinearDesc D = lin_desc(2 * b + 1, NC, NC, L.dhid, NC * b * b, 0, L.dhid, NC * b * b, 0, 0);
       launch_linear(st, N, D, c->B.p, L.plin[b].p, hn);
     }
-    for (int b = 0; b < L.nskip; ++b) run_skip(c, L, b, h, hn, L.dhid, 1);
+    for (int b = 0; b < L.nskip; ++b) {
+      Site s(c, lname("skip", l));
+      run_skip(c, L, b, h, hn, L.dhid, 1);
+    }
+    Site s(c, lname("readout", l));
     if (l + 1 < c->layers.size())
       launch_readout_linear(st, N, hn, L.dhid, L.ro.p, L.ro_e.p);
     else
@@ -605,11 +684,12 @@ void forward(mace_ctx* c) {
   }
   const float* ro[4];
   for (size_t l = 0; l < c->layers.size(); ++l) ro[l] = c->layers[l].ro_e.p;
+  Site s(c, "node_energy");
   launch_node_energy(st, N, c->species.p, c->e0.p, c->rowptr.p, c->dims.has_zbl ? c->zbl_e.p : nullptr, ro,
-                     (int)c->layers.size(), c->node_e.p, c->out.p);
+                     (int)c->layers.size(), c->node_e.p, out);
 }
 
-void backward(mace_ctx* c, bool stress) {
+void backward(mace_ctx* c, bool stress, double* out) {
   hipStream_t st = c->stream;
   const int N = c->N;
   const int64_t E = c->E;
@@ -618,63 +698,84 @@ void backward(mace_ctx* c, bool stress) {
   // dE/dh_L from the nonlinear readout
   float* gh = c->gh0.p;
   float* gh_next = c->gh1.p;
-  launch_readout_mlp_bwd(st, N, c->ypre.p, c->layers[L - 1].ro1.p, c->layers[L - 1].ro2.p, gh,
-                         c->layers[L - 1].dhid);
+  {
+    Site s(c, "readout_bwd");
+    launch_readout_mlp_bwd(st, N, c->ypre.p, c->layers[L - 1].ro1.p, c->layers[L - 1].ro2.p, gh,
+                           c->layers[L - 1].dhid);
+  }
   for (int l = L - 1; l >= 0; --l) {
     Layer& Ly = c->layers[l];
-    // gB = PLin^T gh
-    for (int b = 0; b < Ly.lhid; ++b) {
+    for (int b = 0; b < Ly.lhid; ++b) {  // gB = PLin^T gh
+      Site s(c, lname("linear_prod_bwd", l));
       LinearDesc D = lin_desc(2 * b + 1, NC, NC, Ly.dhid, NC * b * b, 0, Ly.dhid, NC * b * b, 0, 0);
       launch_linear(st, N, D, gh, Ly.plinT[b].p, c->gB.p);
     }
     const float* scw[3] = {Ly.sc[0].p, Ly.sc[1].p, Ly.sc[2].p};
-    launch_sc_bwd(st, N, Ly.lhid, Ly.corr, Ly.A.p, Ly.dint, c->species.p, scw, c->gB.p, Ly.dhid, c->gA.p);
+    {
+      Site s(c, lname("sc_bwd", l));
+      launch_sc_bwd(st, N, Ly.lhid, Ly.corr, Ly.A.p, Ly.dint, c->species.p, scw, c->gB.p, Ly.dhid, c->gA.p);
+    }
     const int* l3 = tp_l3(Ly.lin);
     const int* ao = tp_accoff(Ly.lin);
     const int ns = n_tp_slots(Ly.lin);
     for (int lo = 0; lo < 4; ++lo) {
       int first = -1, cnt = 0;
-      for (int s = 0; s < ns; ++s)
-        if (l3[s] == lo) {
-          if (first < 0) first = s;
+      for (int q = 0; q < ns; ++q)
+        if (l3[q] == lo) {
+          if (first < 0) first = q;
           ++cnt;
         }
       const int d = 2 * lo + 1;
+      Site s(c, lname("linear_msg_bwd", l));
       LinearDesc D = lin_desc(d, NC, cnt * NC, Ly.dint, NC * lo * lo, 0, Ly.dmid, NC * ao[first], NC * d, 0);
       launch_linear(st, N, D, c->gA.p, Ly.linT[lo].p, c->gM.p);
     }
     const int first_edge_grad = (l == L - 1) ? 0 : 1;  // gY / gef: write on the first layer visited
     if (l > 0) {
+      Site s(c, lname("tp_bwd", l));
       launch_tp_bwd_send(st, Ly.lin, N, c->rowptr_s.p, c->perm_s.p, c->receiver.p, c->Y.p, Ly.w.p, Ly.h_up.p,
                          c->gM.p, c->gw.p, c->gY.p, c->gup.p, first_edge_grad);
     } else {
+      Site s(c, lname("tp_bwd", l));
       launch_tp_bwd_recv(st, Ly.lin, N, c->rowptr.p, c->sender.p, c->Y.p, Ly.w.p, Ly.h_up.p, c->gM.p, c->gw.p,
                          c->gY.p, first_edge_grad);
     }
-    launch_mlp_bwd(st, E, nb, Ly.wn, c->ef.p, Ly.mlp[0].p, Ly.mlp[1].p, Ly.mlp[2].p, Ly.mlp[3].p, c->gw.p, c->gef.p,
-                   first_edge_grad);
+    {
+      Site s(c, lname("mlp_bwd", l));
+      launch_mlp_bwd(st, E, nb, Ly.wn, c->ef.p, Ly.mlp[0].p, Ly.mlp[1].p, Ly.mlp[2].p, Ly.mlp[3].p, c->gw.p,
+                     c->gef.p, first_edge_grad);
+    }
     if (l > 0) {
       // dE/dh_l = Up^T gup + Skip^T gh + readout_{l-1}'
       for (int b = 0; b < Ly.lin; ++b) {
+        Site s(c, lname("linear_up_bwd", l));
         LinearDesc D = lin_desc(2 * b + 1, NC, NC, Ly.din, NC * b * b, 0, Ly.din, NC * b * b, 0, 0);
         launch_linear(st, N, D, c->gup.p, Ly.upT[b].p, gh_next);
       }
-      for (int b = 0; b < Ly.nskip; ++b) run_skip_T(c, Ly, b, gh, Ly.dhid, gh_next);
-      launch_readout_linear_bwd(st, N, c->layers[l - 1].ro.p, gh_next, Ly.din, 1);
+      for (int b = 0; b < Ly.nskip; ++b) {
+        Site s(c, lname("skip_bwd", l));
+        run_skip_T(c, Ly, b, gh, Ly.dhid, gh_next);
+      }
+      {
+        Site s(c, lname("readout_bwd", l - 1));
+        launch_readout_linear_bwd(st, N, c->layers[l - 1].ro.p, gh_next, Ly.din, 1);
+      }
       std::swap(gh, gh_next);
     }
   }
   FrontParams fp = front_params(c);
   const int nblk = (int)((E + 255) / 256);
-  launch_edge_bwd(st, E, c->sender.p, c->receiver.p, c->species.p, c->bessel_w.p, c->zbl_z.p, c->zbl_cov.p, fp,
-                  c->geom.p, c->gY.p, c->gef.p, c->gv.p, stress ? c->vir_part.p : nullptr, nblk);
-  launch_forces(st, N, c->rowptr.p, c->rowptr_s.p, c->perm_s.p, c->gv.p, c->out.p + 10);
-  if (stress) {
-    if (E > 0)
-      launch_virial_reduce(st, c->vir_part.p, nblk, c->out.p + 1);
-    else
-      HIPCHK(hipMemsetAsync(c->out.p + 1, 0, 9 * sizeof(double), st));
+  {
+    Site s(c, "edge_bwd");
+    launch_edge_bwd(st, E, c->sender.p, c->receiver.p, c->species.p, c->bessel_w.p, c->zbl_z.p, c->zbl_cov.p, fp,
+                    c->geom.p, c->gY.p, c->gef.p, c->gv.p, stress ? c->vir_part.p : nullptr, nblk);
   }
+  {
+    Site s(c, "forces");
+    launch_forces(st, N, c->rowptr.p, c->rowptr_s.p, c->perm_s.p, c->gv.p, out + 10);
+  }
+  Site s(c, "virial");
+  launch_virial_reduce(st, c->vir_part.p, (stress && E > 0) ? nblk : 0, out + 1);
 }
 
 }  // namespace
@@ -745,6 +846,7 @@ void mace_destroy(mace_ctx* c) {
   free_all(c);
   for (auto& e : c->ev)
     if (e) (void)hipEventDestroy(e);
+  for (auto& e : c->ev_pool) (void)hipEventDestroy(e);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -888,9 +990,9 @@ int mace_step(mace_ctx* c, const double* positions, uint32_t flags, double* ener
     c->last_nl = rebuild && !c->edges_manual;
     if (c->last_nl) build_nl(c, positions);
     HIPCHK(hipEventRecord(c->ev[1], st));
-    forward(c);
+    forward(c, c->pos.p, c->out.p);
     HIPCHK(hipEventRecord(c->ev[2], st));
-    backward(c, stress);
+    backward(c, stress, c->out.p);
     HIPCHK(hipEventRecord(c->ev[3], st));
     HIPCHK(hipMemcpyAsync(c->out_pinned, c->out.p, (10 + 3 * (size_t)N) * sizeof(double), hipMemcpyDeviceToHost, st));
     if (node_energy && N > 0)
@@ -899,10 +1001,7 @@ int mace_step(mace_ctx* c, const double* positions, uint32_t flags, double* ener
     HIPCHK(hipStreamSynchronize(st));
     HIPCHK(hipGetLastError());
     *energy = c->out_pinned[0];
-    if (virial9 && stress)
-      for (int a = 0; a < 3; ++a)
-        for (int b = 0; b < 3; ++b)
-          virial9[3 * a + b] = 0.5 * (c->out_pinned[1 + 3 * a + b] + c->out_pinned[1 + 3 * b + a]);
+    if (virial9 && stress) std::memcpy(virial9, c->out_pinned + 1, 9 * sizeof(double));
     if (forces) std::memcpy(forces, c->out_pinned + 10, 3 * (size_t)N * sizeof(double));
     if (node_energy)
       for (int i = 0; i < N; ++i) node_energy[i] = (double)c->ne_pinned[i];
@@ -913,6 +1012,72 @@ int mace_step(mace_ctx* c, const double* positions, uint32_t flags, double* ener
     HIPCHK(hipEventElapsedTime(&ms[3], c->ev[2], c->ev[3]));
     for (int k = 0; k < 4; ++k) c->timings[k] = ms[k];
     if (!c->last_nl) c->timings[1] = 0.0;
+    prof_harvest(c);
+  });
+}
+
+int mace_step_device(mace_ctx* c, const double* d_positions, uint32_t flags, double* d_out) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    if (!c->system_ready) fail(MACE_ERR_STATE, "system not set");
+    if ((c->N > 0 && !d_positions) || !d_out) fail(MACE_ERR_INVALID, "NULL device pointer");
+    set_device(c);
+    const int N = c->N;
+    hipStream_t st = c->stream;
+    if ((flags & MACE_STEP_FORCE_NL) || !c->nl_valid) {
+      // rebuild needs host positions for the non-periodic extents: synchronous
+      if (N > 0)
+        HIPCHK(hipMemcpyAsync(c->pos.p, d_positions, 3 * (size_t)N * sizeof(double), hipMemcpyDeviceToDevice, st));
+      std::vector<double> host(3 * (size_t)N);
+      if (N > 0) HIPCHK(hipMemcpyAsync(host.data(), d_positions, host.size() * sizeof(double), hipMemcpyDeviceToHost, st));
+      HIPCHK(hipStreamSynchronize(st));
+      c->edges_manual = false;
+      build_nl(c, host.data());
+    }
+    forward(c, d_positions, d_out);
+    backward(c, (flags & MACE_STEP_STRESS) != 0, d_out);
+  });
+}
+
+int mace_sync(mace_ctx* c) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    set_device(c);
+    HIPCHK(hipStreamSynchronize(c->stream));
+    HIPCHK(hipGetLastError());
+    prof_harvest(c);
+  });
+}
+
+int mace_set_profiling(mace_ctx* c, int32_t enable) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    prof_harvest(c);
+    c->profiling = enable != 0;
+    c->prof_acc.clear();
+  });
+}
+
+int mace_get_kernel_times(mace_ctx* c, char* names, int64_t names_len, double* total_ms, int64_t* counts,
+                          int32_t capacity, int32_t* n_sites) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    set_device(c);
+    prof_harvest(c);
+    if (n_sites) *n_sites = (int32_t)c->prof_acc.size();
+    if (!names) return;
+    std::string all;
+    int32_t i = 0;
+    for (auto& kv : c->prof_acc) {
+      if (i >= capacity) break;
+      all += kv.first + "\n";
+      if (total_ms) total_ms[i] = kv.second.first;
+      if (counts) counts[i] = kv.second.second;
+      ++i;
+    }
+    if ((int64_t)all.size() + 1 > names_len) fail(MACE_ERR_INVALID, "names buffer too small (%zu)", all.size() + 1);
+    std::memcpy(names, all.c_str(), all.size() + 1);
+    c->prof_acc.clear();
   });
 }
 

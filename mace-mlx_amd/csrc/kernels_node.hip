@@ -309,12 +309,22 @@ __global__ void k_forces(int N, const int* __restrict__ rowptr, const int* __res
   F[3 * a + 2] = fz;
 }
 
+// G[a][b] = sum_e v_e[a] g_e[b] summed over blocks in order; writes the
+// symmetrised virial dE/d(eps_sym) = (G + G^T) / 2 (calculators.py:536-561).
+// nblk == 0 writes zeros.
 __global__ void k_virial_reduce(const double* __restrict__ part, int nblk, double* __restrict__ vir) {
+  __shared__ double G[9];
   const int k = threadIdx.x;
-  if (k >= 9) return;
-  double a = 0.0;
-  for (int b = 0; b < nblk; ++b) a += part[9 * b + k];
-  vir[k] = a;
+  if (k < 9) {
+    double a = 0.0;
+    for (int b = 0; b < nblk; ++b) a += part[9 * b + k];
+    G[k] = a;
+  }
+  __syncthreads();
+  if (k < 9) {
+    const int r = k / 3, c = k % 3;
+    vir[k] = 0.5 * (G[3 * r + c] + G[3 * c + r]);
+  }
 }
 
 }  // namespace

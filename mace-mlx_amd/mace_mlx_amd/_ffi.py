@@ -31,7 +31,7 @@ STEP_FORCE_NL = 4
 EXPORTED_SYMBOLS = (
     "mace_create", "mace_destroy", "mace_last_error", "mace_model_begin", "mace_model_set_tensor",
     "mace_model_end", "mace_set_system", "mace_step", "mace_set_edges", "mace_get_edges",
-    "mace_get_timings",
+    "mace_get_timings", "mace_step_device", "mace_sync", "mace_set_profiling", "mace_get_kernel_times",
 )
 
 
@@ -78,6 +78,10 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
         "mace_set_edges": (ctypes.c_int, [P, I64, P, P, P]),
         "mace_get_edges": (ctypes.c_int, [P, I64, P, P, P, ctypes.POINTER(I64)]),
         "mace_get_timings": (ctypes.c_int, [P, P, I32]),
+        "mace_step_device": (ctypes.c_int, [P, P, U32, P]),
+        "mace_sync": (ctypes.c_int, [P]),
+        "mace_set_profiling": (ctypes.c_int, [P, I32]),
+        "mace_get_kernel_times": (ctypes.c_int, [P, ctypes.c_char_p, I64, P, P, I32, ctypes.POINTER(I32)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -186,6 +190,31 @@ class Engine:
         S = np.empty((E, 3), np.int32)
         self._check(self._lib.mace_get_edges(self._h, E, _ptr(s), _ptr(r), _ptr(S), ctypes.byref(n)))
         return s, r, S
+
+    def step_device(self, d_positions: int, d_out: int, stress: bool = False, force_nl: bool = False) -> None:
+        """Queue one step on device buffers (raw device addresses); see mace_step_device."""
+        flags = STEP_FORCES | (STEP_STRESS if stress else 0) | (STEP_FORCE_NL if force_nl else 0)
+        self._check(self._lib.mace_step_device(self._h, ctypes.c_void_p(d_positions), flags,
+                                               ctypes.c_void_p(d_out)))
+
+    def sync(self) -> None:
+        self._check(self._lib.mace_sync(self._h))
+
+    def set_profiling(self, enable: bool) -> None:
+        self._check(self._lib.mace_set_profiling(self._h, int(bool(enable))))
+
+    def kernel_times(self) -> dict:
+        """{site: (total_ms, launches)} accumulated since the last call."""
+        n = ctypes.c_int32()
+        self._check(self._lib.mace_get_kernel_times(self._h, None, 0, None, None, 0, ctypes.byref(n)))
+        cap = n.value
+        buf = ctypes.create_string_buffer(64 * max(cap, 1) + 1)
+        tot = np.zeros(max(cap, 1), np.float64)
+        cnt = np.zeros(max(cap, 1), np.int64)
+        self._check(self._lib.mace_get_kernel_times(self._h, buf, len(buf), _ptr(tot), _ptr(cnt), cap,
+                                                    ctypes.byref(n)))
+        names = buf.value.decode().split("\n")[:cap]
+        return {nm: (float(tot[i]), int(cnt[i])) for i, nm in enumerate(names)}
 
     def timings(self) -> np.ndarray:
         out = np.zeros(4, dtype=np.float64)
