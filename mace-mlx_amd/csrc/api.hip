@@ -76,7 +76,7 @@ int sc_kt(int lout, int corr) {
 struct Layer {
   int lin = 1, lhid = 1, corr = 3;
   int din = 0, dhid = 0, dmid = 0, dint = 0, wn = 0;
-  DBuf<float> up[3], upT[3], skip[3], skipT[3], mlp[4], lin_[4], linT[4], sc[3], plin[3], plinT[3];
+  DBuf<float> up[3], upT[3], skip[3], skipT[3], mlp[4], mlpT[4], lin_[4], linT[4], sc[3], plin[3], plinT[3];
   DBuf<float> ro, ro1, ro2;
   int nskip = 0;
   // per-step activations
@@ -123,6 +123,7 @@ struct mace_ctx {
   std::vector<DBuf<float>> h;  // h[0..L]
   DBuf<float> M, B, gB, gA, gM, gh0, gh1, gup, ypre, node_e;
   DBuf<double> out;  // [energy, vir9, forces 3N]
+  DBuf<double> e_part;  // per-block energy partials
   double* out_pinned = nullptr;
   float* ne_pinned = nullptr;
   size_t out_pinned_n = 0;
@@ -275,10 +276,15 @@ void build_model(mace_ctx* c) {
       upload(c, L.skip[b], w);
       upload(c, L.skipT[b], transpose(w, C, C, nel));
     }
-    upload(c, L.mlp[0], tensor(c, p + "mlp.0", (size_t)nb * RADIAL_H));
-    upload(c, L.mlp[1], tensor(c, p + "mlp.1", (size_t)RADIAL_H * RADIAL_H));
-    upload(c, L.mlp[2], tensor(c, p + "mlp.2", (size_t)RADIAL_H * RADIAL_H));
-    upload(c, L.mlp[3], tensor(c, p + "mlp.3", (size_t)RADIAL_H * L.wn));
+    {
+      const int rows[4] = {nb, RADIAL_H, RADIAL_H, RADIAL_H};
+      const int cols[4] = {RADIAL_H, RADIAL_H, RADIAL_H, L.wn};
+      for (int k = 0; k < 4; ++k) {
+        const auto& w = tensor(c, p + "mlp." + std::to_string(k), (size_t)rows[k] * cols[k]);
+        upload(c, L.mlp[k], w);
+        upload(c, L.mlpT[k], transpose(w, rows[k], cols[k]));
+      }
+    }
     const int* l3 = tp_l3(L.lin);
     for (int lo = 0; lo < 4; ++lo) {
       int ns = 0;
@@ -332,6 +338,7 @@ void ensure_node_buffers(mace_ctx* c) {
   c->gup.ensure((size_t)N * maxd);
   c->ypre.ensure((size_t)N * 16);
   c->node_e.ensure(N);
+  c->e_part.ensure((N + 255) / 256 + 1);
   c->out.ensure(10 + 3 * (size_t)N);
   c->pos.ensure(3 * (size_t)N);
   if (c->out_pinned_n < (size_t)N) {
@@ -581,6 +588,37 @@ LinearDesc lin_desc(int d, int K, int Cout, int ldx, int in_base, int in_stride,
   return D;
 }
 
+GemmProb gprob(int N, int d, int K1, int Cout, const float* X1, int ldx1, int base1, int stride1, const float* W1,
+                float* Y, int ldy, int obase, int ostride) {
+  GemmProb P{};
+  P.d = d;
+  P.rows = N * d;
+  P.K1 = K1;
+  P.K2 = 0;
+  P.Cout = Cout;
+  P.X1 = X1;
+  P.ldx1 = ldx1;
+  P.in_base1 = base1;
+  P.in_stride1 = stride1;
+  P.W1 = W1;
+  P.Y = Y;
+  P.ldy = ldy;
+  P.out_base = obase;
+  P.out_stride = ostride;
+  return P;
+}
+
+void slot_range(const Layer& L, int lo, int* first, int* cnt) {
+  const int* l3 = tp_l3(L.lin);
+  *first = -1;
+  *cnt = 0;
+  for (int q = 0; q < n_tp_slots(L.lin); ++q)
+    if (l3[q] == lo) {
+      if (*first < 0) *first = q;
+      ++*cnt;
+    }
+}
+
 FrontParams front_params(mace_ctx* c) {
   FrontParams p{};
   std::memcpy(p.cell, c->cell, sizeof p.cell);
@@ -638,44 +676,59 @@ void forward(mace_ctx* c, const double* pos, double* out) {
       Site s(c, lname("mlp_fwd", l));
       launch_mlp_fwd(st, E, nb, L.wn, c->ef.p, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, L.mlp[3].p, L.w.p);
     }
-    for (int b = 0; b < L.lin; ++b) {
+    {
       Site s(c, lname("linear_up", l));
-      LinearDesc D = lin_desc(2 * b + 1, NC, NC, L.din, NC * b * b, 0, L.din, NC * b * b, 0, 0);
-      launch_linear(st, N, D, h, L.up[b].p, L.h_up.p);
+      GemmGroup g{};
+      for (int b = 0; b < L.lin; ++b)
+        g.p[g.n++] = gprob(N, 2 * b + 1, NC, NC, h, L.din, NC * b * b, 0, L.up[b].p, L.h_up.p, L.din, NC * b * b, 0);
+      launch_gemm_group(st, g);
     }
     {
       Site s(c, lname("tp_fwd", l));
       launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, L.w.p, L.h_up.p, c->M.p);
     }
-    const int* l3 = tp_l3(L.lin);
     const int* ao = tp_accoff(L.lin);
-    const int ns = n_tp_slots(L.lin);
-    for (int lo = 0; lo < 4; ++lo) {
-      int first = -1, cnt = 0;
-      for (int q = 0; q < ns; ++q)
-        if (l3[q] == lo) {
-          if (first < 0) first = q;
-          ++cnt;
-        }
-      const int d = 2 * lo + 1;
+    {
       Site s(c, lname("linear_msg", l));
-      LinearDesc D = lin_desc(d, cnt * NC, NC, L.dmid, NC * ao[first], NC * d, L.dint, NC * lo * lo, 0, 0);
-      launch_linear(st, N, D, c->M.p, L.lin_[lo].p, L.A.p);
+      GemmGroup g{};
+      for (int lo = 0; lo < 4; ++lo) {
+        int first, cnt;
+        slot_range(L, lo, &first, &cnt);
+        const int d = 2 * lo + 1;
+        g.p[g.n++] = gprob(N, d, cnt * NC, NC, c->M.p, L.dmid, NC * ao[first], NC * d, L.lin_[lo].p, L.A.p, L.dint,
+                           NC * lo * lo, 0);
+      }
+      launch_gemm_group(st, g);
     }
     const float* scw[3] = {L.sc[0].p, L.sc[1].p, L.sc[2].p};
     {
       Site s(c, lname("sc_fwd", l));
       launch_sc_fwd(st, N, L.lhid, L.corr, L.A.p, L.dint, c->species.p, scw, c->B.p, L.dhid);
     }
-    for (int b = 0; b < L.lhid; ++b) {
+    const bool one_el = c->dims.num_elements == 1;
+    {
+      // h' = PLin(B) + Skip(h): one two-operand GEMM per hidden block (one element)
       Site s(c, lname("linear_prod", l));
-      LinearDesc D = lin_desc(2 * b + 1, NC, NC, L.dhid, NC * b * b, 0, L.dhid, NC * b * b, 0, 0);
-      launch_linear(st, N, D, c->B.p, L.plin[b].p, hn);
+      GemmGroup g{};
+      for (int b = 0; b < L.lhid; ++b) {
+        GemmProb P = gprob(N, 2 * b + 1, NC, NC, c->B.p, L.dhid, NC * b * b, 0, L.plin[b].p, hn, L.dhid, NC * b * b, 0);
+        if (one_el && b < L.nskip) {
+          P.K2 = NC;
+          P.X2 = h;
+          P.ldx2 = L.din;
+          P.in_base2 = NC * b * b;
+          P.in_stride2 = 0;
+          P.W2 = L.skip[b].p;
+        }
+        g.p[g.n++] = P;
+      }
+      launch_gemm_group(st, g);
     }
-    for (int b = 0; b < L.nskip; ++b) {
-      Site s(c, lname("skip", l));
-      run_skip(c, L, b, h, hn, L.dhid, 1);
-    }
+    if (!one_el)
+      for (int b = 0; b < L.nskip; ++b) {
+        Site s(c, lname("skip", l));
+        run_skip(c, L, b, h, hn, L.dhid, 1);
+      }
     Site s(c, lname("readout", l));
     if (l + 1 < c->layers.size())
       launch_readout_linear(st, N, hn, L.dhid, L.ro.p, L.ro_e.p);
@@ -686,7 +739,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
   for (size_t l = 0; l < c->layers.size(); ++l) ro[l] = c->layers[l].ro_e.p;
   Site s(c, "node_energy");
   launch_node_energy(st, N, c->species.p, c->e0.p, c->rowptr.p, c->dims.has_zbl ? c->zbl_e.p : nullptr, ro,
-                     (int)c->layers.size(), c->node_e.p, out);
+                     (int)c->layers.size(), c->node_e.p, c->e_part.p, out);
 }
 
 void backward(mace_ctx* c, bool stress, double* out) {
@@ -705,30 +758,32 @@ void backward(mace_ctx* c, bool stress, double* out) {
   }
   for (int l = L - 1; l >= 0; --l) {
     Layer& Ly = c->layers[l];
-    for (int b = 0; b < Ly.lhid; ++b) {  // gB = PLin^T gh
+    const bool one_el = c->dims.num_elements == 1;
+    {  // gB = PLin^T gh
       Site s(c, lname("linear_prod_bwd", l));
-      LinearDesc D = lin_desc(2 * b + 1, NC, NC, Ly.dhid, NC * b * b, 0, Ly.dhid, NC * b * b, 0, 0);
-      launch_linear(st, N, D, gh, Ly.plinT[b].p, c->gB.p);
+      GemmGroup g{};
+      for (int b = 0; b < Ly.lhid; ++b)
+        g.p[g.n++] =
+            gprob(N, 2 * b + 1, NC, NC, gh, Ly.dhid, NC * b * b, 0, Ly.plinT[b].p, c->gB.p, Ly.dhid, NC * b * b, 0);
+      launch_gemm_group(st, g);
     }
     const float* scw[3] = {Ly.sc[0].p, Ly.sc[1].p, Ly.sc[2].p};
     {
       Site s(c, lname("sc_bwd", l));
       launch_sc_bwd(st, N, Ly.lhid, Ly.corr, Ly.A.p, Ly.dint, c->species.p, scw, c->gB.p, Ly.dhid, c->gA.p);
     }
-    const int* l3 = tp_l3(Ly.lin);
     const int* ao = tp_accoff(Ly.lin);
-    const int ns = n_tp_slots(Ly.lin);
-    for (int lo = 0; lo < 4; ++lo) {
-      int first = -1, cnt = 0;
-      for (int q = 0; q < ns; ++q)
-        if (l3[q] == lo) {
-          if (first < 0) first = q;
-          ++cnt;
-        }
-      const int d = 2 * lo + 1;
+    {
       Site s(c, lname("linear_msg_bwd", l));
-      LinearDesc D = lin_desc(d, NC, cnt * NC, Ly.dint, NC * lo * lo, 0, Ly.dmid, NC * ao[first], NC * d, 0);
-      launch_linear(st, N, D, c->gA.p, Ly.linT[lo].p, c->gM.p);
+      GemmGroup g{};
+      for (int lo = 0; lo < 4; ++lo) {
+        int first, cnt;
+        slot_range(Ly, lo, &first, &cnt);
+        const int d = 2 * lo + 1;
+        g.p[g.n++] = gprob(N, d, NC, cnt * NC, c->gA.p, Ly.dint, NC * lo * lo, 0, Ly.linT[lo].p, c->gM.p, Ly.dmid,
+                           NC * ao[first], NC * d);
+      }
+      launch_gemm_group(st, g);
     }
     const int first_edge_grad = (l == L - 1) ? 0 : 1;  // gY / gef: write on the first layer visited
     if (l > 0) {
@@ -742,24 +797,36 @@ void backward(mace_ctx* c, bool stress, double* out) {
     }
     {
       Site s(c, lname("mlp_bwd", l));
-      launch_mlp_bwd(st, E, nb, Ly.wn, c->ef.p, Ly.mlp[0].p, Ly.mlp[1].p, Ly.mlp[2].p, Ly.mlp[3].p, c->gw.p,
-                     c->gef.p, first_edge_grad);
+      launch_mlp_bwd(st, E, nb, Ly.wn, c->ef.p, Ly.mlp[0].p, Ly.mlp[1].p, Ly.mlp[2].p, Ly.mlpT[0].p, Ly.mlpT[1].p,
+                     Ly.mlpT[2].p, Ly.mlpT[3].p, c->gw.p, c->gef.p, first_edge_grad);
     }
     if (l > 0) {
       // dE/dh_l = Up^T gup + Skip^T gh + readout_{l-1}'
-      for (int b = 0; b < Ly.lin; ++b) {
-        Site s(c, lname("linear_up_bwd", l));
-        LinearDesc D = lin_desc(2 * b + 1, NC, NC, Ly.din, NC * b * b, 0, Ly.din, NC * b * b, 0, 0);
-        launch_linear(st, N, D, c->gup.p, Ly.upT[b].p, gh_next);
-      }
-      for (int b = 0; b < Ly.nskip; ++b) {
-        Site s(c, lname("skip_bwd", l));
-        run_skip_T(c, Ly, b, gh, Ly.dhid, gh_next);
-      }
       {
-        Site s(c, lname("readout_bwd", l - 1));
-        launch_readout_linear_bwd(st, N, c->layers[l - 1].ro.p, gh_next, Ly.din, 1);
+        // dE/dh_l = Up^T gup + Skip^T gh (one element) + readout_{l-1}' (bias on the 0e block)
+        Site s(c, lname("linear_up_bwd", l));
+        GemmGroup g{};
+        for (int b = 0; b < Ly.lin; ++b) {
+          GemmProb P =
+              gprob(N, 2 * b + 1, NC, NC, c->gup.p, Ly.din, NC * b * b, 0, Ly.upT[b].p, gh_next, Ly.din, NC * b * b, 0);
+          if (one_el && b < Ly.nskip) {
+            P.K2 = NC;
+            P.X2 = gh;
+            P.ldx2 = Ly.dhid;
+            P.in_base2 = NC * b * b;
+            P.in_stride2 = 0;
+            P.W2 = Ly.skipT[b].p;
+          }
+          if (b == 0) P.bias = c->layers[l - 1].ro.p;
+          g.p[g.n++] = P;
+        }
+        launch_gemm_group(st, g);
       }
+      if (!one_el)
+        for (int b = 0; b < Ly.nskip; ++b) {
+          Site s(c, lname("skip_bwd", l));
+          run_skip_T(c, Ly, b, gh, Ly.dhid, gh_next);
+        }
       std::swap(gh, gh_next);
     }
   }
@@ -811,7 +878,7 @@ static void free_all(mace_ctx* c) {
   for (auto& L : c->layers) {
     for (auto* arr : {L.up, L.upT, L.skip, L.skipT, L.sc, L.plin, L.plinT})
       for (int i = 0; i < 3; ++i) arr[i].release();
-    for (int i = 0; i < 4; ++i) L.mlp[i].release(), L.lin_[i].release(), L.linT[i].release();
+    for (int i = 0; i < 4; ++i) L.mlp[i].release(), L.mlpT[i].release(), L.lin_[i].release(), L.linT[i].release();
     L.ro.release(), L.ro1.release(), L.ro2.release(), L.h_up.release(), L.A.release(), L.w.release(),
         L.ro_e.release();
   }
@@ -829,6 +896,7 @@ static void free_all(mace_ctx* c) {
   c->nl_wpos.release();
   c->vir_part.release();
   c->out.release();
+  c->e_part.release();
   c->geom.release();
   c->cub_tmp.release();
   if (c->out_pinned) (void)hipHostFree(c->out_pinned);

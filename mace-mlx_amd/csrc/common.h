@@ -53,9 +53,12 @@ void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* re
 void launch_mlp_fwd(hipStream_t st, int64_t E, int nb, int W, const float* ef,
                     const float* W0, const float* W1, const float* W2, const float* W3,
                     float* w);
+// backward takes the forward weights (recompute) and their transposes
+// (W0T [64][nb], W1T/W2T [64][64], W3T [W][64])
 void launch_mlp_bwd(hipStream_t st, int64_t E, int nb, int W, const float* ef,
-                    const float* W0, const float* W1, const float* W2, const float* W3,
-                    const float* gw, float* gef, int accumulate);
+                    const float* W0, const float* W1, const float* W2, const float* W0T,
+                    const float* W1T, const float* W2T, const float* W3T, const float* gw,
+                    float* gef, int accumulate);
 
 // conv TP fused with the receiver-CSR scatter
 void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
@@ -84,6 +87,31 @@ void launch_linear(hipStream_t st, int N, const LinearDesc& d, const float* X, c
 void launch_linear_species(hipStream_t st, int N, const LinearDesc& d, const float* X,
                            const float* W, const int* species, float* Y);
 
+// Grouped fp32-MFMA GEMM over node rows: up to GEMM_MAX problems in one launch.
+// Each problem: Y[row, c] (+)= sum_k X1[row, k] W1[k][c] + sum_k X2[row, k] W2[k][c] + bias[c]
+// with rows (node n, component m), row-addressing as in LinearDesc.
+constexpr int GEMM_MAX = 8;
+struct GemmProb {
+  int d, rows, K1, K2, Cout;
+  const float* X1;
+  int ldx1, in_base1, in_stride1;
+  const float* W1;
+  const float* X2;
+  int ldx2, in_base2, in_stride2;
+  const float* W2;
+  float* Y;
+  int ldy, out_base, out_stride;
+  const float* bias;
+  int accumulate;
+  int tiles_n, tile_begin;
+};
+struct GemmGroup {
+  GemmProb p[GEMM_MAX];
+  int n;
+  int total_tiles;
+};
+void launch_gemm_group(hipStream_t st, GemmGroup& g);
+
 void launch_embed(hipStream_t st, int N, const int* species, const float* emb, int ld, float* h);
 
 // symmetric contraction (all output blocks of one product layer)
@@ -105,7 +133,7 @@ void launch_readout_linear_bwd(hipStream_t st, int N, const float* w, float* gh,
 
 void launch_node_energy(hipStream_t st, int N, const int* species, const float* e0,
                         const int* rowptr, const float* zbl_e, const float* const* ro,
-                        int nro, float* node_e, double* energy);
+                        int nro, float* node_e, double* part, double* energy);
 void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s,
                    const int* perm_s, const float* gv, double* forces);
 void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir);
@@ -129,6 +157,5 @@ void launch_nl_fill(hipStream_t st, int N, const NLParams& p, const double* wpos
                     const int* rowptr, int* sender, int* receiver, int* shifts);
 void launch_fill_iota(hipStream_t st, int n, int* out);
 void launch_count_keys(hipStream_t st, int64_t E, const int* keys, int* counts);
-void launch_bin_start(hipStream_t st, int N, int nbins, const int* sorted_bins, int* bin_start);
 
 }  // namespace mace

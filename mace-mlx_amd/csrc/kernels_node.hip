@@ -89,6 +89,65 @@ __global__ void __launch_bounds__(NC) k_linear_species(int rows, LinearDesc D, c
   Yo[o] = D.accumulate ? Yo[o] + acc : acc;
 }
 
+// ---------------------------------------------------------------------------
+// grouped GEMM on fp32 matrix cores: one wave per 16-row x 64-column tile
+// (v_mfma_f32_16x16x4f32; lane l holds A[l%16][k], B[k][l%16], D[4(l/16)+i][l%16];
+// within a 16-wide k chunk lane group g = l/16 takes k = 16c + 4g + s at step s,
+// so its A values arrive as one float4)
+// ---------------------------------------------------------------------------
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void gemm_operand(const float* __restrict__ X, int ldx, int base, int stride,
+                                             const float* __restrict__ W, int K, int Cout, int col0, int n,
+                                             int m, bool live, int r, int g, f4v* acc) {
+  const float* xrow = X + (int64_t)n * ldx + base + m * NC;
+  for (int c = 0; c < K; c += 16) {
+    const int kb = c / NC, kk = c % NC;
+    const float4 a4 = live ? *reinterpret_cast<const float4*>(xrow + kb * stride + kk + 4 * g)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const float* wr = W + (int64_t)(c + 4 * g + s) * Cout + col0 + r;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], wr[16 * t], acc[t], 0, 0, 0);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(64) k_gemm_group(GemmGroup G) {
+  int q = 0;
+  while (q + 1 < G.n && (int)blockIdx.x >= G.p[q + 1].tile_begin) ++q;
+  const GemmProb& P = G.p[q];
+  const int t = blockIdx.x - P.tile_begin;
+  const int tm = t / P.tiles_n, tn = t % P.tiles_n;
+  const int l = threadIdx.x, r = l & 15, g = l >> 4;
+  const int col0 = tn * 64;
+  const int row = tm * 16 + r;
+  const bool live = row < P.rows;
+  const int n = live ? row / P.d : 0, m = live ? row - n * P.d : 0;
+  f4v acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = f4v{0.f, 0.f, 0.f, 0.f};
+  gemm_operand(P.X1, P.ldx1, P.in_base1, P.in_stride1, P.W1, P.K1, P.Cout, col0, n, m, live, r, g, acc);
+  if (P.K2 > 0)
+    gemm_operand(P.X2, P.ldx2, P.in_base2, P.in_stride2, P.W2, P.K2, P.Cout, col0, n, m, live, r, g, acc);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ro = tm * 16 + 4 * g + i;
+    if (ro >= P.rows) continue;
+    const int no = ro / P.d, mo = ro - no * P.d;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const int col = col0 + 16 * tt + r;
+      float v = acc[tt][i];
+      if (P.bias) v += P.bias[col];
+      float* y = P.Y + (int64_t)no * P.ldy + P.out_base + (col / NC) * P.out_stride + mo * NC + (col % NC);
+      *y = P.accumulate ? *y + v : v;
+    }
+  }
+}
+
 __global__ void k_embed(int N, const int* __restrict__ species, const float* __restrict__ emb, int ld,
                         float* __restrict__ h) {
   const int n = blockIdx.x, u = threadIdx.x;
@@ -262,13 +321,14 @@ struct RoPtrs {
   const float* p[4];
 };
 
-__global__ void __launch_bounds__(1024) k_node_energy(int N, const int* __restrict__ species,
-                                                      const float* __restrict__ e0, const int* __restrict__ rowptr,
-                                                      const float* __restrict__ zbl_e, RoPtrs ro, int nro,
-                                                      float* __restrict__ node_e, double* __restrict__ energy) {
-  __shared__ double red[1024];
+__global__ void __launch_bounds__(256) k_node_energy(int N, const int* __restrict__ species,
+                                                     const float* __restrict__ e0, const int* __restrict__ rowptr,
+                                                     const float* __restrict__ zbl_e, RoPtrs ro, int nro,
+                                                     float* __restrict__ node_e, double* __restrict__ part) {
+  __shared__ double red[256];
+  const int n = blockIdx.x * 256 + threadIdx.x;
   double acc = 0.0;
-  for (int n = threadIdx.x; n < N; n += 1024) {
+  if (n < N) {
     float v = e0[species[n]];
     if (zbl_e) {
       float z = 0.f;
@@ -277,36 +337,64 @@ __global__ void __launch_bounds__(1024) k_node_energy(int N, const int* __restri
     }
     for (int l = 0; l < nro; ++l) v += ro.p[l][n];
     node_e[n] = v;
-    acc += (double)v;
+    acc = (double)v;
   }
   red[threadIdx.x] = acc;
   __syncthreads();
-  for (int off = 512; off > 0; off >>= 1) {
+  for (int off = 128; off > 0; off >>= 1) {
     if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
     __syncthreads();
   }
-  if (threadIdx.x == 0) *energy = red[0];
+  if (threadIdx.x == 0) part[blockIdx.x] = red[0];
 }
 
-__global__ void k_forces(int N, const int* __restrict__ rowptr, const int* __restrict__ rowptr_s,
-                         const int* __restrict__ perm_s, const float* __restrict__ gv, double* __restrict__ F) {
-  const int a = blockIdx.x * blockDim.x + threadIdx.x;
-  if (a >= N) return;
+// fixed-order sum of block partials (deterministic)
+__global__ void __launch_bounds__(256) k_sum_partials(const double* __restrict__ part, int nblk,
+                                                      double* __restrict__ out) {
+  __shared__ double red[256];
+  double a = 0.0;
+  for (int b = threadIdx.x; b < nblk; b += 256) a += part[b];
+  red[threadIdx.x] = a;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *out = red[0];
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// one wavefront per atom: F_a = -(sum over edges received by a - sum over edges sent by a) of dE/dv
+__global__ void __launch_bounds__(256) k_forces(int N, const int* __restrict__ rowptr, const int* __restrict__ rowptr_s,
+                                                const int* __restrict__ perm_s, const float* __restrict__ gv,
+                                                double* __restrict__ F) {
+  const int a = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+  if (a >= N) return;  // whole wavefront exits together
   double fx = 0.0, fy = 0.0, fz = 0.0;
-  for (int e = rowptr[a]; e < rowptr[a + 1]; ++e) {  // a is the receiver: dE/dpos_a += g
+  for (int e = rowptr[a] + l; e < rowptr[a + 1]; e += 64) {
     fx -= gv[3 * e];
     fy -= gv[3 * e + 1];
     fz -= gv[3 * e + 2];
   }
-  for (int k = rowptr_s[a]; k < rowptr_s[a + 1]; ++k) {  // a is the sender: dE/dpos_a -= g
+  for (int k = rowptr_s[a] + l; k < rowptr_s[a + 1]; k += 64) {
     const int e = perm_s[k];
     fx += gv[3 * e];
     fy += gv[3 * e + 1];
     fz += gv[3 * e + 2];
   }
-  F[3 * a] = fx;
-  F[3 * a + 1] = fy;
-  F[3 * a + 2] = fz;
+  fx = wave_sum_d(fx);
+  fy = wave_sum_d(fy);
+  fz = wave_sum_d(fz);
+  if (l == 0) {
+    F[3 * a] = fx;
+    F[3 * a + 1] = fy;
+    F[3 * a + 2] = fz;
+  }
 }
 
 // G[a][b] = sum_e v_e[a] g_e[b] summed over blocks in order; writes the
@@ -400,17 +488,34 @@ void launch_readout_linear_bwd(hipStream_t st, int N, const float* w, float* gh,
 }
 
 void launch_node_energy(hipStream_t st, int N, const int* species, const float* e0, const int* rowptr,
-                        const float* zbl_e, const float* const* ro, int nro, float* node_e, double* energy) {
+                        const float* zbl_e, const float* const* ro, int nro, float* node_e, double* part,
+                        double* energy) {
   RoPtrs r{{nullptr, nullptr, nullptr, nullptr}};
   for (int l = 0; l < nro && l < 4; ++l) r.p[l] = ro[l];
-  hipLaunchKernelGGL(k_node_energy, dim3(1), dim3(1024), 0, st, N, species, e0, rowptr, zbl_e, r, nro, node_e,
-                     energy);
+  const int nblk = (int)cdiv(N, 256);
+  if (nblk > 0)
+    hipLaunchKernelGGL(k_node_energy, dim3(nblk), dim3(256), 0, st, N, species, e0, rowptr, zbl_e, r, nro, node_e,
+                       part);
+  hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(256), 0, st, part, nblk, energy);
 }
 
 void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s, const int* perm_s,
                    const float* gv, double* forces) {
   if (N <= 0) return;
-  hipLaunchKernelGGL(k_forces, dim3(cdiv(N, 256)), dim3(256), 0, st, N, rowptr, rowptr_s, perm_s, gv, forces);
+  hipLaunchKernelGGL(k_forces, dim3(cdiv(N, 4)), dim3(256), 0, st, N, rowptr, rowptr_s, perm_s, gv, forces);
+}
+
+void launch_gemm_group(hipStream_t st, GemmGroup& g) {
+  int tiles = 0;
+  for (int q = 0; q < g.n; ++q) {
+    GemmProb& P = g.p[q];
+    P.tiles_n = P.Cout / 64;
+    P.tile_begin = tiles;
+    tiles += (int)cdiv(P.rows, 16) * P.tiles_n;
+  }
+  g.total_tiles = tiles;
+  if (tiles <= 0) return;
+  hipLaunchKernelGGL(k_gemm_group, dim3(tiles), dim3(64), 0, st, g);
 }
 
 void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir) {
