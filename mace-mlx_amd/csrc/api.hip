@@ -94,6 +94,8 @@ struct mace_ctx {
   mace_model_dims dims{};
   std::map<std::string, std::vector<float>> host_tensors;
   std::vector<Layer> layers;
+  int max_lin = 1;
+  int mts = 0;  // row stride of the per-edge TP tables Mt (0: no layer has l1 >= 1 inputs)
   DBuf<float> e0, bessel_w, zbl_z, zbl_cov, embed;
   // system
   int N = 0;
@@ -117,7 +119,7 @@ struct mace_ctx {
   DBuf<unsigned char> cub_tmp;
   // per-step edge buffers
   DBuf<EdgeGeom> geom;
-  DBuf<float> Y, ef, zbl_e, gY, gef, gv, gw;
+  DBuf<float> Y, Mt, ef, zbl_e, gY, gef, gv, gw;
   DBuf<double> vir_part;
   // node buffers
   std::vector<DBuf<float>> h;  // h[0..L]
@@ -307,6 +309,9 @@ void build_model(mace_ctx* c) {
       upload(c, L.ro2, tensor(c, p + "ro2", 16));
     }
   }
+  c->max_lin = 1;
+  for (const Layer& L : c->layers) c->max_lin = std::max(c->max_lin, L.lin);
+  c->mts = (tp_table_entries(c->max_lin) + 15) / 16 * 16;
   c->host_tensors.clear();
   c->model_ready = true;
 }
@@ -363,7 +368,8 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   c->Y.ensure(e * 16);
   c->ef.ensure(e * c->dims.num_bessel);
   c->zbl_e.ensure(e);
-  c->gY.ensure(e * 16);
+  c->gY.ensure(e * 32);
+  if (c->mts > 0) c->Mt.ensure(e * c->mts);
   c->gef.ensure(e * c->dims.num_bessel);
   c->gv.ensure(e * 3);
   c->gw.ensure(e * maxw);
@@ -664,6 +670,10 @@ void forward(mace_ctx* c, const double* pos, double* out) {
     launch_edge_fwd(st, E, pos, c->sender.p, c->receiver.p, c->shifts.p, c->species.p, c->bessel_w.p, c->zbl_z.p,
                     c->zbl_cov.p, fp, c->geom.p, c->Y.p, c->ef.p, c->zbl_e.p);
   }
+  if (c->mts > 0) {
+    Site s(c, "tp_tables");
+    launch_tp_tables(st, E, c->max_lin, c->Y.p, c->Mt.p, c->mts);
+  }
   {
     Site s(c, "embed");
     launch_embed(st, N, c->species.p, c->embed.p, c->layers[0].din, c->h[0].p);
@@ -685,7 +695,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
     }
     {
       Site s(c, lname("tp_fwd", l));
-      launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, L.w.p, L.h_up.p, c->M.p);
+      launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.w.p, L.h_up.p, c->M.p);
     }
     const int* ao = tp_accoff(L.lin);
     {
@@ -788,12 +798,12 @@ void backward(mace_ctx* c, bool stress, double* out) {
     const int first_edge_grad = (l == L - 1) ? 0 : 1;  // gY / gef: write on the first layer visited
     if (l > 0) {
       Site s(c, lname("tp_bwd", l));
-      launch_tp_bwd_send(st, Ly.lin, N, c->rowptr_s.p, c->perm_s.p, c->receiver.p, c->Y.p, Ly.w.p, Ly.h_up.p,
-                         c->gM.p, c->gw.p, c->gY.p, c->gup.p, first_edge_grad);
+      launch_tp_bwd_send(st, Ly.lin, N, c->rowptr_s.p, c->perm_s.p, c->receiver.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p,
+                         Ly.h_up.p, c->gM.p, c->gw.p, c->gY.p, c->gup.p, first_edge_grad);
     } else {
       Site s(c, lname("tp_bwd", l));
-      launch_tp_bwd_recv(st, Ly.lin, N, c->rowptr.p, c->sender.p, c->Y.p, Ly.w.p, Ly.h_up.p, c->gM.p, c->gw.p,
-                         c->gY.p, first_edge_grad);
+      launch_tp_bwd_recv(st, Ly.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p, Ly.h_up.p,
+                         c->gM.p, c->gw.p, c->gY.p, first_edge_grad);
     }
     {
       Site s(c, lname("mlp_bwd", l));
@@ -883,7 +893,7 @@ static void free_all(mace_ctx* c) {
         L.ro_e.release();
   }
   for (auto& b : c->h) b.release();
-  for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->embed, &c->Y, &c->ef, &c->zbl_e, &c->gY, &c->gef,
+  for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->embed, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
                   &c->gv, &c->gw, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup, &c->ypre,
                   &c->node_e})
     b->release();
@@ -940,7 +950,10 @@ int mace_model_end(mace_ctx* c) {
   return guard(c, [&] {
     set_device(c);
     build_model(c);
-    if (c->system_ready) ensure_node_buffers(c);
+    if (c->system_ready) {
+      ensure_node_buffers(c);
+      ensure_edge_buffers(c, c->E);  // per-layer edge buffers of the new model
+    }
   });
 }
 

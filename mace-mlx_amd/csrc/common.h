@@ -60,17 +60,21 @@ void launch_mlp_bwd(hipStream_t st, int64_t E, int nb, int W, const float* ef,
                     const float* W1T, const float* W2T, const float* W3T, const float* gw,
                     float* gef, int accumulate);
 
+// per-edge x2-first tables Mt[e] (row stride mts) for the l1 >= 1 TP paths
+int tp_table_entries(int max_lin);
+void launch_tp_tables(hipStream_t st, int64_t E, int max_lin, const float* Y, float* Mt, int mts);
 // conv TP fused with the receiver-CSR scatter
 void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
-                   const float* Y, const float* w, const float* up, float* M);
-// TP VJP, receiver-centric (no input gradient; layer 0)
+                   const float* Y, const float* Mt, int mts, const float* w, const float* up, float* M);
+// TP VJP, receiver-centric (no input gradient; layer 0); gY is [E][2][16] (per channel half)
 void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
-                        const float* Y, const float* w, const float* up, const float* gM,
-                        float* gw, float* gY, int accumulate_gY);
+                        const float* Y, const float* Mt, int mts, const float* w, const float* up,
+                        const float* gM, float* gw, float* gY, int accumulate_gY);
 // TP VJP, sender-centric (input gradient gup; layers >= 1)
 void launch_tp_bwd_send(hipStream_t st, int lin, int N, const int* rowptr_s, const int* perm_s,
-                        const int* receiver, const float* Y, const float* w, const float* up,
-                        const float* gM, float* gw, float* gY, float* gup, int accumulate_gY);
+                        const int* receiver, const float* Y, const float* Mt, int mts, const float* w,
+                        const float* up, const float* gM, float* gw, float* gY, float* gup,
+                        int accumulate_gY);
 
 // node linear: Y[n, out_base + (c/NC)*out_stride + m*NC + c%NC] (+)=
 //   sum_k X[n, in_base + (k/NC)*in_stride + m*NC + k%NC] * W[k][c]

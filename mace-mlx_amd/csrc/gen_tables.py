@@ -66,6 +66,7 @@ def emit_sh(out):
 
 
 def emit_tp(out, lin: int):
+    """Emit the layout and M tables of one TP variant; returns {l1: (K, starts, js, vs)}."""
     slots = tp_layout(lin)
     ns = len(slots)
     d = [2 * s[2] + 1 for s in slots]
@@ -87,6 +88,7 @@ def emit_tp(out, lin: int):
         col[sidx] = kcount.get(l1, 0)
         kcount[l1] = kcount.get(l1, 0) + 2 * l3 + 1
     out.append(f"constexpr int {P}_COL[] = {{{', '.join(str(col.get(s, -1)) for s in range(ns))}}};")
+    tables = {}
     for l1 in range(1, 3):
         K = kcount.get(l1, 0)
         out.append(f"constexpr int {P}_K{l1} = {K};")
@@ -113,6 +115,8 @@ def emit_tp(out, lin: int):
         out.append(f"constexpr int {P}_M{l1}_START[] = {{{', '.join(map(str, starts))}}};")
         out.append(f"constexpr int {P}_M{l1}_J[] = {{{', '.join(map(str, js))}}};")
         out.append(f"constexpr float {P}_M{l1}_V[] = {{{', '.join(f32(v) for v in vs)}}};")
+        tables[l1] = (K, starts, js, vs)
+    return tables
 
 
 def sc_poly(lout: int, corr: int):
@@ -200,8 +204,11 @@ def main(out_dir: str) -> None:
     out = ["// Generated by gen_tables.py -- do not edit.", "#pragma once", ""]
     out.append(f"constexpr int SH_DIM = {SH_DIM};")
     emit_sh(out)
-    for lin in (1, 2, 3):
-        emit_tp(out, lin)
+    tabs = {lin: emit_tp(out, lin) for lin in (1, 2, 3)}
+    # The per-edge M tables are built once (TP3 layout) and shared by every layer,
+    # so the l1 = 1 columns must coincide for 2 and 3 input blocks.
+    if tabs[2][1] != tabs[3][1]:
+        raise RuntimeError("M1 tables differ between 2 and 3 input blocks")
     for lout in (0, 1, 2):
         for corr in (1, 2, 3):
             emit_sc(out, lout, corr)

@@ -114,7 +114,7 @@ __global__ void __launch_bounds__(256) k_edge_bwd(
     sh16(ux, uy, uz, Yl);
     float G[16];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) G[k] = gY[16 * e + k];
+    for (int k = 0; k < 16; ++k) G[k] = gY[32 * e + k] + gY[32 * e + 16 + k];  // two channel halves
     // reverse through the recursion (l = 3, then l = 2)
 #pragma unroll
     for (int t = 0; t < SH3_NT; ++t) {

@@ -9,12 +9,22 @@
 // Layouts (internal): x = up[n][NC*(l1^2 + i) + u]; M[n][NC*acc(slot, k) + u];
 // w[e][slot*NC + u]; Y[e][16].
 //
-// One workgroup of NC threads (thread = channel u) owns one node.  Edges are
-// processed in batches of EB: their SH rows are staged in LDS and turned into
-// the x2-first tables M_l1[i][col] = sum_j Y_j C[i, j, k] pw (shared by all
-// channels), then every thread accumulates its channel's outputs in registers.
-// The segmented sum is the register accumulation itself: no atomics, results
-// are deterministic.
+// Per-edge x2-first tables Mt[e] = [M1(3 x K1) | M2(5 x K2)] with
+// M_l1[i][col] = sum_j Y_j C[i, j, k] pw are built once per step by
+// k_tp_tables (they depend only on Y) and shared by every layer.
+//
+// TP kernels: one workgroup per node, NG groups of NC threads (thread = channel
+// u, so a node's 128 channels are two wave64s per group).  Group g takes a
+// contiguous share of the node's edges.  Edge indices, senders and the Y / Mt
+// rows are wave-uniform, so they are read through scalar loads; the next
+// edge's weights and inputs are loaded while the current one is computed.
+// There is no barrier inside the edge loop; the NG partial results are
+// combined once at the end in a fixed order (deterministic, no atomics).
+//
+// dL/dY of an edge is a sum over the 128 channels: each wave reduces its 64
+// lanes' 16 partials with a recursive-halving shuffle (17 exchanges) and
+// stores them in gY[e][half][16] (half = which 64 channels); the edge backward
+// adds the two halves.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -30,178 +40,246 @@ struct TPT;
   struct TPT<N> {                                                                  \
     static constexpr int NSLOT = TP##N##_NSLOT, NACC = TP##N##_NACC;               \
     static constexpr int K1 = TP##N##_K1, K2 = TP##N##_K2;                         \
-    static constexpr int M1_NE = TP##N##_M1_NE, M2_NE = TP##N##_M2_NE;             \
     __host__ __device__ static constexpr int l1(int s) { return TP##N##_L1[s]; }   \
     __host__ __device__ static constexpr int l2(int s) { return TP##N##_L2[s]; }   \
     __host__ __device__ static constexpr int l3(int s) { return TP##N##_L3[s]; }   \
     __host__ __device__ static constexpr int acc(int s) { return TP##N##_ACC[s]; } \
     __host__ __device__ static constexpr int col(int s) { return TP##N##_COL[s]; } \
-    __device__ static constexpr int m1s(int q) { return TP##N##_M1_START[q]; }    \
-    __device__ static constexpr int m1j(int x) { return TP##N##_M1_J[x]; }        \
-    __device__ static constexpr float m1v(int x) { return TP##N##_M1_V[x]; }      \
-    __device__ static constexpr int m2s(int q) { return TP##N##_M2_START[q]; }    \
-    __device__ static constexpr int m2j(int x) { return TP##N##_M2_J[x]; }        \
-    __device__ static constexpr float m2v(int x) { return TP##N##_M2_V[x]; }      \
   };
 MACE_TP_TRAITS(1)
 MACE_TP_TRAITS(2)
 MACE_TP_TRAITS(3)
 #undef MACE_TP_TRAITS
 
-constexpr int EB_F = 8;  // edges per LDS batch, forward
-constexpr int EB_B = 4;  // edges per LDS batch, backward (gY transpose buffer)
+// M-table entry q (row-major i*K + c) terms, in the shared (3-block) layout
+__device__ constexpr int m1s(int q) { return TP3_M1_START[q]; }
+__device__ constexpr int m1j(int x) { return TP3_M1_J[x]; }
+__device__ constexpr float m1v(int x) { return TP3_M1_V[x]; }
+__device__ constexpr int m2s(int q) { return TP3_M2_START[q]; }
+__device__ constexpr int m2j(int x) { return TP3_M2_J[x]; }
+__device__ constexpr float m2v(int x) { return TP3_M2_V[x]; }
+constexpr int MT_M2 = TP3_M1_NE;  // offset of the l1 = 2 table inside an Mt row
 
+static_assert(TP2_K1 == TP3_K1, "shared M1 layout");
+
+// Inputs of one edge for one channel, loaded ahead of use.
 template <int LIN>
-struct Smem {
-  using T = TPT<LIN>;
-  static constexpr int M1W = T::M1_NE > 0 ? T::M1_NE : 1;
-  static constexpr int M2W = T::M2_NE > 0 ? T::M2_NE : 1;
+struct EdgeIn {
+  float w[TPT<LIN>::NSLOT];
+  float x0, x1[3], x2[5];
 };
 
-// Stage Y rows of a batch and build the x2-first tables.
-template <int LIN, int EB>
-__device__ __forceinline__ void stage_batch(int nb, const int* eid, const float* __restrict__ Y,
-                                            float (*sY)[16], float (*sM1)[Smem<LIN>::M1W],
-                                            float (*sM2)[Smem<LIN>::M2W]) {
-  using T = TPT<LIN>;
-  const int u = threadIdx.x;
-  for (int t = u; t < nb * 16; t += NC) sY[t >> 4][t & 15] = Y[(int64_t)eid[t >> 4] * 16 + (t & 15)];
-  __syncthreads();
-  if constexpr (T::M1_NE > 0) {
-    for (int t = u; t < nb * T::M1_NE; t += NC) {
-      const int b = t / T::M1_NE, q = t % T::M1_NE;
-      float a = 0.f;
-      for (int x = T::m1s(q); x < T::m1s(q + 1); ++x) a = fmaf(sY[b][T::m1j(x)], T::m1v(x), a);
-      sM1[b][q] = a;
-    }
-  }
-  if constexpr (T::M2_NE > 0) {
-    for (int t = u; t < nb * T::M2_NE; t += NC) {
-      const int b = t / T::M2_NE, q = t % T::M2_NE;
-      float a = 0.f;
-      for (int x = T::m2s(q); x < T::m2s(q + 1); ++x) a = fmaf(sY[b][T::m2j(x)], T::m2v(x), a);
-      sM2[b][q] = a;
-    }
-  }
-  __syncthreads();
-}
-
 template <int LIN>
-__device__ __forceinline__ void load_x(const float* __restrict__ xs, int u, float& x0, float* x1, float* x2) {
-  x0 = xs[u];
+__device__ __forceinline__ void load_x(const float* __restrict__ xs, float& x0, float* x1, float* x2) {
+  x0 = xs[0];
   if constexpr (LIN >= 2) {
 #pragma unroll
-    for (int i = 0; i < 3; ++i) x1[i] = xs[NC * (1 + i) + u];
+    for (int i = 0; i < 3; ++i) x1[i] = xs[NC * (1 + i)];
   }
   if constexpr (LIN >= 3) {
 #pragma unroll
-    for (int i = 0; i < 5; ++i) x2[i] = xs[NC * (4 + i) + u];
+    for (int i = 0; i < 5; ++i) x2[i] = xs[NC * (4 + i)];
   }
 }
 
 template <int LIN>
-__global__ void __launch_bounds__(NC) k_tp_fwd(int N, const int* __restrict__ rowptr,
-                                               const int* __restrict__ sender, const float* __restrict__ Y,
-                                               const float* __restrict__ w, const float* __restrict__ up,
-                                               float* __restrict__ M) {
-  using T = TPT<LIN>;
-  constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, WN = NC * T::NSLOT;
-  __shared__ float sY[EB_F][16];
-  __shared__ float sM1[EB_F][Smem<LIN>::M1W];
-  __shared__ float sM2[EB_F][Smem<LIN>::M2W];
-  __shared__ int sE[EB_F], sS[EB_F];
-  const int n = blockIdx.x, u = threadIdx.x;
-  float acc[T::NACC];
+__device__ __forceinline__ void load_w(const float* __restrict__ we, float* wv) {
 #pragma unroll
-  for (int a = 0; a < T::NACC; ++a) acc[a] = 0.f;
-  const int beg = rowptr[n], end = rowptr[n + 1];
-  for (int e0 = beg; e0 < end; e0 += EB_F) {
-    const int nb = min(EB_F, end - e0);
-    __syncthreads();
-    if (u < nb) {
-      sE[u] = e0 + u;
-      sS[u] = sender[e0 + u];
-    }
-    __syncthreads();
-    stage_batch<LIN, EB_F>(nb, sE, Y, sY, sM1, sM2);
-    for (int b = 0; b < nb; ++b) {
-      const int64_t e = sE[b];
-      float x0, x1[3], x2[5];
-      load_x<LIN>(up + (int64_t)sS[b] * DIN, u, x0, x1, x2);
-      const float* we = w + e * WN + u;
-#pragma unroll
-      for (int s = 0; s < T::NSLOT; ++s) {
-        const float ww = we[s * NC];
-        constexpr int dummy = 0;
-        (void)dummy;
-        const int a0 = T::acc(s), d = 2 * T::l3(s) + 1;
-        if (T::l1(s) == 0) {
-          const float xw = x0 * ww;
-#pragma unroll
-          for (int m = 0; m < d; ++m) acc[a0 + m] = fmaf(xw, sY[b][T::l2(s) * T::l2(s) + m], acc[a0 + m]);
-        } else if (T::l1(s) == 1) {
-          const int c0 = T::col(s);
-#pragma unroll
-          for (int k = 0; k < d; ++k) {
-            float t = 0.f;
-#pragma unroll
-            for (int i = 0; i < 3; ++i) t = fmaf(x1[i], sM1[b][i * T::K1 + c0 + k], t);
-            acc[a0 + k] = fmaf(ww, t, acc[a0 + k]);
-          }
-        } else {
-          const int c0 = T::col(s);
-#pragma unroll
-          for (int k = 0; k < d; ++k) {
-            float t = 0.f;
-#pragma unroll
-            for (int i = 0; i < 5; ++i) t = fmaf(x2[i], sM2[b][i * T::K2 + c0 + k], t);
-            acc[a0 + k] = fmaf(ww, t, acc[a0 + k]);
-          }
-        }
-      }
-    }
-  }
-  float* Mn = M + (int64_t)n * DMID + u;
-#pragma unroll
-  for (int a = 0; a < T::NACC; ++a) Mn[a * NC] = acc[a];
+  for (int s = 0; s < TPT<LIN>::NSLOT; ++s) wv[s] = we[s * NC];
 }
 
-// Per-edge VJP of one thread's channel: given g = dL/dM[recv] (this channel),
-// accumulates the input gradient (if GX), writes dL/dw and adds this channel's
-// share of dL/dY into gYu.
-template <int LIN, bool GX>
-__device__ __forceinline__ void tp_edge_vjp(const float* g, const float* __restrict__ we, float* __restrict__ gwe,
-                                            float x0, const float* x1, const float* x2, const float* sYb,
-                                            const float* sM1b, const float* sM2b, float& gx0, float* gx1,
-                                            float* gx2, float* gYu) {
+// Forward contribution of one edge to this channel's accumulators.
+template <int LIN>
+__device__ __forceinline__ void tp_edge_fwd(float* acc, const EdgeIn<LIN>& in, const float* __restrict__ Ye,
+                                            const float* __restrict__ Me) {
   using T = TPT<LIN>;
 #pragma unroll
   for (int s = 0; s < T::NSLOT; ++s) {
-    const float ww = we[s * NC];
+    const float ww = in.w[s];
+    const int a0 = T::acc(s), d = 2 * T::l3(s) + 1;
+    if (T::l1(s) == 0) {
+      const float xw = in.x0 * ww;
+#pragma unroll
+      for (int m = 0; m < d; ++m) acc[a0 + m] = fmaf(xw, Ye[T::l2(s) * T::l2(s) + m], acc[a0 + m]);
+    } else if (T::l1(s) == 1) {
+      const int c0 = T::col(s);
+#pragma unroll
+      for (int k = 0; k < d; ++k) {
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) t = fmaf(in.x1[i], Me[i * T::K1 + c0 + k], t);
+        acc[a0 + k] = fmaf(ww, t, acc[a0 + k]);
+      }
+    } else {
+      const int c0 = T::col(s);
+#pragma unroll
+      for (int k = 0; k < d; ++k) {
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) t = fmaf(in.x2[i], Me[MT_M2 + i * T::K2 + c0 + k], t);
+        acc[a0 + k] = fmaf(ww, t, acc[a0 + k]);
+      }
+    }
+  }
+}
+
+// Group of NC threads this thread belongs to.  NC is a multiple of the wave
+// size, so the value is wave-uniform; readfirstlane tells the compiler, which
+// then keeps edge indices in scalar registers and reads the per-edge Y / Mt
+// rows with scalar loads.
+__device__ __forceinline__ int group_id() {
+  static_assert(NC % 64 == 0, "a group spans whole waves");
+  return __builtin_amdgcn_readfirstlane(threadIdx.x / NC);
+}
+
+// share [gb, ge) of a node's edge range [beg, end) taken by group g of NG
+template <int NG>
+__device__ __forceinline__ void group_range(int beg, int end, int g, int& gb, int& ge) {
+  const int per = (end - beg + NG - 1) / NG;
+  gb = min(end, beg + g * per);
+  ge = min(end, gb + per);
+}
+
+// Fixed-order combine of per-group register vectors v[NV] into group 0.
+template <int NV, int NG>
+__device__ __forceinline__ void combine_groups(float* v, int g, int u, float (*sRed)[NC]) {
+#pragma unroll 1
+  for (int q = NG - 1; q >= 1; --q) {
+    __syncthreads();
+    if (g == q)
+#pragma unroll
+      for (int a = 0; a < NV; ++a) sRed[a][u] = v[a];
+    __syncthreads();
+    if (g == q - 1)
+#pragma unroll
+      for (int a = 0; a < NV; ++a) v[a] += sRed[a][u];
+  }
+}
+
+template <int LIN, int NG>
+__global__ void __launch_bounds__(NC* NG) k_tp_fwd(int N, const int* __restrict__ rowptr,
+                                                   const int* __restrict__ sender, const float* __restrict__ Y,
+                                                   const float* __restrict__ Mt, int mts,
+                                                   const float* __restrict__ w, const float* __restrict__ up,
+                                                   float* __restrict__ M) {
+  using T = TPT<LIN>;
+  constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, WN = NC * T::NSLOT;
+  const int n = blockIdx.x, g = group_id(), u = threadIdx.x % NC;
+  float acc[T::NACC];
+#pragma unroll
+  for (int a = 0; a < T::NACC; ++a) acc[a] = 0.f;
+  int gb, ge;
+  group_range<NG>(rowptr[n], rowptr[n + 1], g, gb, ge);
+  if (gb < ge) {
+    EdgeIn<LIN> cur, nxt;
+    load_w<LIN>(w + (int64_t)gb * WN + u, cur.w);
+    load_x<LIN>(up + (int64_t)sender[gb] * DIN + u, cur.x0, cur.x1, cur.x2);
+#pragma unroll 1
+    for (int e = gb; e < ge; ++e) {
+      if (e + 1 < ge) {
+        load_w<LIN>(w + (int64_t)(e + 1) * WN + u, nxt.w);
+        load_x<LIN>(up + (int64_t)sender[e + 1] * DIN + u, nxt.x0, nxt.x1, nxt.x2);
+      }
+      tp_edge_fwd<LIN>(acc, cur, Y + (int64_t)e * 16, Mt + (int64_t)e * mts);
+      cur = nxt;
+    }
+  }
+  if constexpr (NG > 1) {
+    __shared__ float sRed[T::NACC][NC];
+    combine_groups<T::NACC, NG>(acc, g, u, sRed);
+  }
+  if (g == 0) {
+    float* Mn = M + (int64_t)n * DMID + u;
+#pragma unroll
+    for (int a = 0; a < T::NACC; ++a) Mn[a * NC] = acc[a];
+  }
+}
+
+// Sum over the 64 lanes of a wave of v[16]: lane l returns the total of
+// component (l >> 2) & 15.  Recursive halving: each exchange step halves the
+// components a lane keeps, then two plain butterflies finish the sum.
+__device__ __forceinline__ float wave_sum16(const float* v) {
+  const int lane = __lane_id();
+  float a[8], b[4], c[2];
+  {
+    const bool hi = lane & 32;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float send = hi ? v[k] : v[k + 8], keep = hi ? v[k + 8] : v[k];
+      a[k] = keep + __shfl_xor(send, 32);
+    }
+  }
+  {
+    const bool hi = lane & 16;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float send = hi ? a[k] : a[k + 4], keep = hi ? a[k + 4] : a[k];
+      b[k] = keep + __shfl_xor(send, 16);
+    }
+  }
+  {
+    const bool hi = lane & 8;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const float send = hi ? b[k] : b[k + 2], keep = hi ? b[k + 2] : b[k];
+      c[k] = keep + __shfl_xor(send, 8);
+    }
+  }
+  const bool hi = lane & 4;
+  const float send = hi ? c[0] : c[1], keep = hi ? c[1] : c[0];
+  float d = keep + __shfl_xor(send, 4);
+  d += __shfl_xor(d, 2);
+  d += __shfl_xor(d, 1);
+  return d;
+}
+
+// Store this wave's reduced dL/dY of edge e into gY[e][half][16].
+__device__ __forceinline__ void store_gY(const float* gYu, int64_t e, int u, float* __restrict__ gY, int accumulate) {
+  const float s = wave_sum16(gYu);
+  const int lane = __lane_id();
+  if ((lane & 3) == 0) {
+    float* dst = gY + e * 32 + (u >> 6) * 16 + (lane >> 2);
+    *dst = accumulate ? *dst + s : s;
+  }
+}
+
+// Per-edge VJP of one channel: given g = dL/dM[recv] (this channel), writes
+// dL/dw, accumulates the input gradient (if GX) and this channel's dL/dY.
+template <int LIN, bool GX>
+__device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& in, float* __restrict__ gwe,
+                                            const float* __restrict__ Ye, const float* __restrict__ Me, float& gx0,
+                                            float* gx1, float* gx2, float* gYu) {
+  using T = TPT<LIN>;
+#pragma unroll
+  for (int s = 0; s < T::NSLOT; ++s) {
+    const float ww = in.w[s];
     const int a0 = T::acc(s), d = 2 * T::l3(s) + 1, l2 = T::l2(s);
     float gws = 0.f;
     if (T::l1(s) == 0) {
       float t = 0.f;
+      const float xw = in.x0 * ww;
 #pragma unroll
       for (int m = 0; m < d; ++m) {
-        t = fmaf(g[a0 + m], sYb[l2 * l2 + m], t);
-        gYu[l2 * l2 + m] = fmaf(x0 * ww, g[a0 + m], gYu[l2 * l2 + m]);
+        t = fmaf(g[a0 + m], Ye[l2 * l2 + m], t);
+        gYu[l2 * l2 + m] = fmaf(xw, g[a0 + m], gYu[l2 * l2 + m]);
       }
-      gws = x0 * t;
+      gws = in.x0 * t;
       if (GX) gx0 = fmaf(ww, t, gx0);
     } else if (T::l1(s) == 1) {
       const int c0 = T::col(s);
 #pragma unroll
       for (int k = 0; k < d; ++k) {
+        const float wg = ww * g[a0 + k];
         float mk = 0.f;
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
           const int q = i * T::K1 + c0 + k;
-          mk = fmaf(x1[i], sM1b[q], mk);
-          if (GX) gx1[i] = fmaf(ww * g[a0 + k], sM1b[q], gx1[i]);
-          const float c = ww * x1[i] * g[a0 + k];
+          const float mq = Me[q];
+          mk = fmaf(in.x1[i], mq, mk);
+          if (GX) gx1[i] = fmaf(wg, mq, gx1[i]);
+          const float cq = wg * in.x1[i];
 #pragma unroll
-          for (int x = T::m1s(q); x < T::m1s(q + 1); ++x) gYu[T::m1j(x)] = fmaf(c, T::m1v(x), gYu[T::m1j(x)]);
+          for (int x = m1s(q); x < m1s(q + 1); ++x) gYu[m1j(x)] = fmaf(cq, m1v(x), gYu[m1j(x)]);
         }
         gws = fmaf(g[a0 + k], mk, gws);
       }
@@ -209,15 +287,17 @@ __device__ __forceinline__ void tp_edge_vjp(const float* g, const float* __restr
       const int c0 = T::col(s);
 #pragma unroll
       for (int k = 0; k < d; ++k) {
+        const float wg = ww * g[a0 + k];
         float mk = 0.f;
 #pragma unroll
         for (int i = 0; i < 5; ++i) {
           const int q = i * T::K2 + c0 + k;
-          mk = fmaf(x2[i], sM2b[q], mk);
-          if (GX) gx2[i] = fmaf(ww * g[a0 + k], sM2b[q], gx2[i]);
-          const float c = ww * x2[i] * g[a0 + k];
+          const float mq = Me[MT_M2 + q];
+          mk = fmaf(in.x2[i], mq, mk);
+          if (GX) gx2[i] = fmaf(wg, mq, gx2[i]);
+          const float cq = wg * in.x2[i];
 #pragma unroll
-          for (int x = T::m2s(q); x < T::m2s(q + 1); ++x) gYu[T::m2j(x)] = fmaf(c, T::m2v(x), gYu[T::m2j(x)]);
+          for (int x = m2s(q); x < m2s(q + 1); ++x) gYu[m2j(x)] = fmaf(cq, m2v(x), gYu[m2j(x)]);
         }
         gws = fmaf(g[a0 + k], mk, gws);
       }
@@ -226,181 +306,180 @@ __device__ __forceinline__ void tp_edge_vjp(const float* g, const float* __restr
   }
 }
 
-// Block reduction of the per-channel dL/dY partials of a batch: sR[b*16 + j][u].
-__device__ __forceinline__ void reduce_gY(int nb, const int* eid, float (*sR)[NC + 1], float* __restrict__ gY,
-                                          int accumulate) {
-  const int u = threadIdx.x;
-  const int q = u >> 1, h = u & 1;  // row q = b*16 + j (EB_B*16 = 64 rows), half h
-  float a = 0.f;
-#pragma unroll 8
-  for (int c = 0; c < NC / 2; ++c) a += sR[q][h * (NC / 2) + c];
-  a += __shfl_xor(a, 1);
-  const int b = q >> 4, j = q & 15;
-  if (h == 0 && b < nb) {
-    float* dst = gY + (int64_t)eid[b] * 16 + j;
-    *dst = accumulate ? *dst + a : a;
-  }
-}
-
-template <int LIN>
-__global__ void __launch_bounds__(NC) k_tp_bwd_recv(int N, const int* __restrict__ rowptr,
-                                                    const int* __restrict__ sender, const float* __restrict__ Y,
-                                                    const float* __restrict__ w, const float* __restrict__ up,
-                                                    const float* __restrict__ gM, float* __restrict__ gw,
-                                                    float* __restrict__ gY, int accumulate_gY) {
+// Receiver-centric VJP (no input gradient): used for the first interaction,
+// whose input features are the constant species embedding.
+template <int LIN, int NG>
+__global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __restrict__ rowptr,
+                                                        const int* __restrict__ sender, const float* __restrict__ Y,
+                                                        const float* __restrict__ Mt, int mts,
+                                                        const float* __restrict__ w, const float* __restrict__ up,
+                                                        const float* __restrict__ gM, float* __restrict__ gw,
+                                                        float* __restrict__ gY, int accumulate_gY) {
   using T = TPT<LIN>;
   constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, WN = NC * T::NSLOT;
-  static_assert(EB_B * 16 == NC / 2, "gY reduction maps 2 threads per row");
-  __shared__ float sY[EB_B][16];
-  __shared__ float sM1[EB_B][Smem<LIN>::M1W];
-  __shared__ float sM2[EB_B][Smem<LIN>::M2W];
-  __shared__ float sR[EB_B * 16][NC + 1];
-  __shared__ int sE[EB_B], sS[EB_B];
-  const int n = blockIdx.x, u = threadIdx.x;
-  float g[T::NACC];
+  const int n = blockIdx.x, g = group_id(), u = threadIdx.x % NC;
+  int gb, ge;
+  group_range<NG>(rowptr[n], rowptr[n + 1], g, gb, ge);
+  if (gb >= ge) return;
+  float gm[T::NACC];
   const float* gMn = gM + (int64_t)n * DMID + u;
 #pragma unroll
-  for (int a = 0; a < T::NACC; ++a) g[a] = gMn[a * NC];
-  const int beg = rowptr[n], end = rowptr[n + 1];
-  for (int e0 = beg; e0 < end; e0 += EB_B) {
-    const int nb = min(EB_B, end - e0);
-    __syncthreads();
-    if (u < nb) {
-      sE[u] = e0 + u;
-      sS[u] = sender[e0 + u];
+  for (int a = 0; a < T::NACC; ++a) gm[a] = gMn[a * NC];
+  EdgeIn<LIN> cur, nxt;
+  load_w<LIN>(w + (int64_t)gb * WN + u, cur.w);
+  load_x<LIN>(up + (int64_t)sender[gb] * DIN + u, cur.x0, cur.x1, cur.x2);
+#pragma unroll 1
+  for (int e = gb; e < ge; ++e) {
+    if (e + 1 < ge) {
+      load_w<LIN>(w + (int64_t)(e + 1) * WN + u, nxt.w);
+      load_x<LIN>(up + (int64_t)sender[e + 1] * DIN + u, nxt.x0, nxt.x1, nxt.x2);
     }
-    __syncthreads();
-    stage_batch<LIN, EB_B>(nb, sE, Y, sY, sM1, sM2);
-    for (int b = 0; b < EB_B; ++b) {
-      float gYu[16];
+    float gYu[16];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) gYu[j] = 0.f;
-      if (b < nb) {
-        const int64_t e = sE[b];
-        float x0, x1[3], x2[5], gx0 = 0.f, gx1[3], gx2[5];
-        load_x<LIN>(up + (int64_t)sS[b] * DIN, u, x0, x1, x2);
-        tp_edge_vjp<LIN, false>(g, w + e * WN + u, gw + e * WN + u, x0, x1, x2, sY[b], sM1[b], sM2[b], gx0,
-                                gx1, gx2, gYu);
-      }
-#pragma unroll
-      for (int j = 0; j < 16; ++j) sR[b * 16 + j][u] = gYu[j];
-    }
-    __syncthreads();
-    reduce_gY(nb, sE, sR, gY, accumulate_gY);
+    for (int j = 0; j < 16; ++j) gYu[j] = 0.f;
+    float gx0 = 0.f, gx1[3], gx2[5];
+    tp_edge_vjp<LIN, false>(gm, cur, gw + (int64_t)e * WN + u, Y + (int64_t)e * 16, Mt + (int64_t)e * mts, gx0,
+                            gx1, gx2, gYu);
+    store_gY(gYu, e, u, gY, accumulate_gY);
+    cur = nxt;
   }
 }
 
-template <int LIN>
-__global__ void __launch_bounds__(NC) k_tp_bwd_send(int N, const int* __restrict__ rowptr_s,
-                                                    const int* __restrict__ perm_s,
-                                                    const int* __restrict__ receiver, const float* __restrict__ Y,
-                                                    const float* __restrict__ w, const float* __restrict__ up,
-                                                    const float* __restrict__ gM, float* __restrict__ gw,
-                                                    float* __restrict__ gY, float* __restrict__ gup,
-                                                    int accumulate_gY) {
+// Sender-centric VJP: the block of node a walks the edges it sends (through
+// the sender permutation) and accumulates dL/dx[a] in registers.
+template <int LIN, int NG>
+__global__ void __launch_bounds__(NC* NG) k_tp_bwd_send(int N, const int* __restrict__ rowptr_s,
+                                                        const int* __restrict__ perm_s,
+                                                        const int* __restrict__ receiver,
+                                                        const float* __restrict__ Y, const float* __restrict__ Mt,
+                                                        int mts, const float* __restrict__ w,
+                                                        const float* __restrict__ up, const float* __restrict__ gM,
+                                                        float* __restrict__ gw, float* __restrict__ gY,
+                                                        float* __restrict__ gup, int accumulate_gY) {
   using T = TPT<LIN>;
   constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, WN = NC * T::NSLOT;
-  __shared__ float sY[EB_B][16];
-  __shared__ float sM1[EB_B][Smem<LIN>::M1W];
-  __shared__ float sM2[EB_B][Smem<LIN>::M2W];
-  __shared__ float sR[EB_B * 16][NC + 1];
-  __shared__ int sE[EB_B], sRv[EB_B];
-  const int a = blockIdx.x, u = threadIdx.x;
-  float x0, x1[3], x2[5];
-  load_x<LIN>(up + (int64_t)a * DIN, u, x0, x1, x2);
-  float gx0 = 0.f, gx1[3] = {0.f, 0.f, 0.f}, gx2[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
-  const int beg = rowptr_s[a], end = rowptr_s[a + 1];
-  for (int k0 = beg; k0 < end; k0 += EB_B) {
-    const int nb = min(EB_B, end - k0);
-    __syncthreads();
-    if (u < nb) {
-      const int e = perm_s[k0 + u];
-      sE[u] = e;
-      sRv[u] = receiver[e];
+  constexpr int NX = LIN * LIN;
+  const int a = blockIdx.x, g = group_id(), u = threadIdx.x % NC;
+  EdgeIn<LIN> cur;  // x is the sender node's own input, w changes per edge
+  load_x<LIN>(up + (int64_t)a * DIN + u, cur.x0, cur.x1, cur.x2);
+  float gx[NX];
+#pragma unroll
+  for (int i = 0; i < NX; ++i) gx[i] = 0.f;
+  int gb, ge;
+  group_range<NG>(rowptr_s[a], rowptr_s[a + 1], g, gb, ge);
+  if (gb < ge) {
+    float gmc[T::NACC], gmn[T::NACC], wn[T::NSLOT];
+    int ec = perm_s[gb];
+    load_w<LIN>(w + (int64_t)ec * WN + u, cur.w);
+    {
+      const float* p = gM + (int64_t)receiver[ec] * DMID + u;
+#pragma unroll
+      for (int q = 0; q < T::NACC; ++q) gmc[q] = p[q * NC];
     }
-    __syncthreads();
-    stage_batch<LIN, EB_B>(nb, sE, Y, sY, sM1, sM2);
-    for (int b = 0; b < EB_B; ++b) {
+#pragma unroll 1
+    for (int k = gb; k < ge; ++k) {
+      int en = ec;
+      if (k + 1 < ge) {
+        en = perm_s[k + 1];
+        load_w<LIN>(w + (int64_t)en * WN + u, wn);
+        const float* p = gM + (int64_t)receiver[en] * DMID + u;
+#pragma unroll
+        for (int q = 0; q < T::NACC; ++q) gmn[q] = p[q * NC];
+      }
       float gYu[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) gYu[j] = 0.f;
-      if (b < nb) {
-        const int64_t e = sE[b];
-        float g[T::NACC];
-        const float* gMr = gM + (int64_t)sRv[b] * DMID + u;
+      float gx1[3] = {0.f, 0.f, 0.f}, gx2[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+      float gx0 = 0.f;
+      tp_edge_vjp<LIN, true>(gmc, cur, gw + (int64_t)ec * WN + u, Y + (int64_t)ec * 16, Mt + (int64_t)ec * mts,
+                             gx0, gx1, gx2, gYu);
+      gx[0] += gx0;
+      if constexpr (LIN >= 2) {
 #pragma unroll
-        for (int q = 0; q < T::NACC; ++q) g[q] = gMr[q * NC];
-        tp_edge_vjp<LIN, true>(g, w + e * WN + u, gw + e * WN + u, x0, x1, x2, sY[b], sM1[b], sM2[b], gx0, gx1,
-                               gx2, gYu);
+        for (int i = 0; i < 3; ++i) gx[1 + i] += gx1[i];
       }
+      if constexpr (LIN >= 3) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) sR[b * 16 + j][u] = gYu[j];
+        for (int i = 0; i < 5; ++i) gx[4 + i] += gx2[i];
+      }
+      store_gY(gYu, ec, u, gY, accumulate_gY);
+#pragma unroll
+      for (int s = 0; s < T::NSLOT; ++s) cur.w[s] = wn[s];
+#pragma unroll
+      for (int q = 0; q < T::NACC; ++q) gmc[q] = gmn[q];
+      ec = en;
     }
-    __syncthreads();
-    reduce_gY(nb, sE, sR, gY, accumulate_gY);
   }
-  float* go = gup + (int64_t)a * DIN + u;
-  go[0] = gx0;
-  if constexpr (LIN >= 2) {
-#pragma unroll
-    for (int i = 0; i < 3; ++i) go[NC * (1 + i)] = gx1[i];
+  if constexpr (NG > 1) {
+    __shared__ float sRed[NX][NC];
+    combine_groups<NX, NG>(gx, g, u, sRed);
   }
-  if constexpr (LIN >= 3) {
+  if (g == 0) {
+    float* go = gup + (int64_t)a * DIN + u;
 #pragma unroll
-    for (int i = 0; i < 5; ++i) go[NC * (4 + i)] = gx2[i];
+    for (int i = 0; i < NX; ++i) go[NC * i] = gx[i];
   }
 }
+
+// Mt[e] = [M1 (3 x K1) | M2 (5 x K2)] from Y[e]; one thread per table entry.
+__global__ void __launch_bounds__(256) k_tp_tables(int64_t E, int nent, const float* __restrict__ Y,
+                                                   float* __restrict__ Mt, int mts) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= E * nent) return;
+  const int64_t e = t / nent;
+  const int q = (int)(t - e * nent);
+  const float* y = Y + e * 16;
+  float a = 0.f;
+  if (q < TP3_M1_NE) {
+    for (int x = m1s(q); x < m1s(q + 1); ++x) a = fmaf(y[m1j(x)], m1v(x), a);
+  } else {
+    const int r = q - TP3_M1_NE;
+    for (int x = m2s(r); x < m2s(r + 1); ++x) a = fmaf(y[m2j(x)], m2v(x), a);
+  }
+  Mt[e * mts + q] = a;
+}
+
+// groups per node for each number of input blocks
+constexpr int ng_for(int lin) { return lin == 1 ? 2 : 2; }
 
 }  // namespace
 
-void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int* sender, const float* Y,
-                   const float* w, const float* up, float* M) {
-  if (N <= 0) return;
-  switch (lin) {
-    case 1: hipLaunchKernelGGL(k_tp_fwd<1>, dim3(N), dim3(NC), 0, st, N, rowptr, sender, Y, w, up, M); break;
-    case 2: hipLaunchKernelGGL(k_tp_fwd<2>, dim3(N), dim3(NC), 0, st, N, rowptr, sender, Y, w, up, M); break;
-    case 3: hipLaunchKernelGGL(k_tp_fwd<3>, dim3(N), dim3(NC), 0, st, N, rowptr, sender, Y, w, up, M); break;
+int tp_table_entries(int max_lin) { return max_lin >= 3 ? TP3_M1_NE + TP3_M2_NE : max_lin == 2 ? TP3_M1_NE : 0; }
+
+void launch_tp_tables(hipStream_t st, int64_t E, int max_lin, const float* Y, float* Mt, int mts) {
+  const int nent = tp_table_entries(max_lin);
+  if (E <= 0 || nent == 0) return;
+  const int64_t total = E * nent;
+  hipLaunchKernelGGL(k_tp_tables, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, E, nent, Y, Mt, mts);
+}
+
+#define MACE_TP_DISPATCH(KERNEL, ...)                                                                   \
+  switch (lin) {                                                                                        \
+    case 1: hipLaunchKernelGGL((KERNEL<1, ng_for(1)>), dim3(N), dim3(NC * ng_for(1)), 0, st, __VA_ARGS__); break; \
+    case 2: hipLaunchKernelGGL((KERNEL<2, ng_for(2)>), dim3(N), dim3(NC * ng_for(2)), 0, st, __VA_ARGS__); break; \
+    case 3: hipLaunchKernelGGL((KERNEL<3, ng_for(3)>), dim3(N), dim3(NC * ng_for(3)), 0, st, __VA_ARGS__); break; \
   }
+
+void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int* sender, const float* Y,
+                   const float* Mt, int mts, const float* w, const float* up, float* M) {
+  if (N <= 0) return;
+  MACE_TP_DISPATCH(k_tp_fwd, N, rowptr, sender, Y, Mt, mts, w, up, M)
 }
 
 void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const int* sender, const float* Y,
-                        const float* w, const float* up, const float* gM, float* gw, float* gY,
-                        int accumulate_gY) {
+                        const float* Mt, int mts, const float* w, const float* up, const float* gM, float* gw,
+                        float* gY, int accumulate_gY) {
   if (N <= 0) return;
-  switch (lin) {
-    case 1:
-      hipLaunchKernelGGL(k_tp_bwd_recv<1>, dim3(N), dim3(NC), 0, st, N, rowptr, sender, Y, w, up, gM, gw, gY,
-                         accumulate_gY);
-      break;
-    case 2:
-      hipLaunchKernelGGL(k_tp_bwd_recv<2>, dim3(N), dim3(NC), 0, st, N, rowptr, sender, Y, w, up, gM, gw, gY,
-                         accumulate_gY);
-      break;
-    case 3:
-      hipLaunchKernelGGL(k_tp_bwd_recv<3>, dim3(N), dim3(NC), 0, st, N, rowptr, sender, Y, w, up, gM, gw, gY,
-                         accumulate_gY);
-      break;
-  }
+  MACE_TP_DISPATCH(k_tp_bwd_recv, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gY, accumulate_gY)
 }
 
 void launch_tp_bwd_send(hipStream_t st, int lin, int N, const int* rowptr_s, const int* perm_s,
-                        const int* receiver, const float* Y, const float* w, const float* up, const float* gM,
-                        float* gw, float* gY, float* gup, int accumulate_gY) {
+                        const int* receiver, const float* Y, const float* Mt, int mts, const float* w,
+                        const float* up, const float* gM, float* gw, float* gY, float* gup, int accumulate_gY) {
   if (N <= 0) return;
-  switch (lin) {
-    case 1:
-      hipLaunchKernelGGL(k_tp_bwd_send<1>, dim3(N), dim3(NC), 0, st, N, rowptr_s, perm_s, receiver, Y, w, up, gM,
-                         gw, gY, gup, accumulate_gY);
-      break;
-    case 2:
-      hipLaunchKernelGGL(k_tp_bwd_send<2>, dim3(N), dim3(NC), 0, st, N, rowptr_s, perm_s, receiver, Y, w, up, gM,
-                         gw, gY, gup, accumulate_gY);
-      break;
-    case 3:
-      hipLaunchKernelGGL(k_tp_bwd_send<3>, dim3(N), dim3(NC), 0, st, N, rowptr_s, perm_s, receiver, Y, w, up, gM,
-                         gw, gY, gup, accumulate_gY);
-      break;
-  }
+  MACE_TP_DISPATCH(k_tp_bwd_send, N, rowptr_s, perm_s, receiver, Y, Mt, mts, w, up, gM, gw, gY, gup,
+                   accumulate_gY)
 }
+#undef MACE_TP_DISPATCH
 
 }  // namespace mace
