@@ -47,9 +47,10 @@ def algorithmic_work(site: str, ctx: dict):
         b = 4 * (N * lay["din"] + E * 16 + E * lay["wn"] + N * lay["dmid"]) + 4 * (E + N + 1)
         return "hbm", b, "GB/s"
     if name == "tp_bwd":
-        gup = lay["din"] if int(lyr) > 0 else 0
-        b = 4 * (N * lay["dmid"] + N * lay["din"] + N * gup + 2 * E * 16 + 2 * E * lay["wn"]) + 8 * (E + N + 1)
+        b = 4 * (N * lay["dmid"] + N * lay["din"] + 2 * E * 16 + 2 * E * lay["wn"]) + 8 * (E + N + 1)
         return "hbm", b, "GB/s"
+    if name == "tp_gather":  # segmented sum of the per-edge input-gradient rows
+        return "hbm", 4 * (E * lay["din"] + N * lay["din"]) + 4 * (N + 1), "GB/s"
     if name == "mlp_fwd":
         return "mfma", 2 * E * (nb * H + 2 * H * H + H * lay["wn"]), "TFLOP/s"
     if name == "mlp_bwd":

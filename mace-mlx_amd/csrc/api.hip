@@ -112,14 +112,14 @@ struct mace_ctx {
   bool nl_valid = false, edges_manual = false;
   std::vector<double> nl_pos;  // positions at the last rebuild
   int64_t E = 0;
-  DBuf<int> sender, receiver, shifts, rowptr, rowptr_s, perm_s;
+  DBuf<int> sender, receiver, shifts, rowptr, rowptr_s, perm_s, pos_s;
   DBuf<int> nl_img, nl_bin, nl_bin_sorted, nl_atoms, nl_iota, nl_counts, nl_bin_count, nl_bin_start;
   DBuf<double> nl_wpos;
   DBuf<int> e_tmp_i, e_tmp_j, e_tmp_s, e_perm, e_keys;
   DBuf<unsigned char> cub_tmp;
   // per-step edge buffers
   DBuf<EdgeGeom> geom;
-  DBuf<float> Y, Mt, ef, zbl_e, gY, gef, gv, gw;
+  DBuf<float> Y, Mt, ef, zbl_e, gY, gef, gv, gw, gxe;
   DBuf<double> vir_part;
   // node buffers
   std::vector<DBuf<float>> h;  // h[0..L]
@@ -364,6 +364,9 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
     ly.w.ensure(e * ly.wn);
     maxw = std::max(maxw, ly.wn);
   }
+  size_t maxdin = 0;  // per-edge input gradients of the layers after the first
+  for (size_t l = 1; l < c->layers.size(); ++l) maxdin = std::max(maxdin, (size_t)c->layers[l].din);
+  if (maxdin > 0) c->gxe.ensure(e * maxdin);
   c->geom.ensure(e);
   c->Y.ensure(e * 16);
   c->ef.ensure(e * c->dims.num_bessel);
@@ -382,6 +385,7 @@ void ensure_edge_index(mace_ctx* c, int64_t E) {
   c->receiver.ensure(e);
   c->shifts.ensure(3 * e);
   c->perm_s.ensure(e);
+  c->pos_s.ensure(e);
   c->e_keys.ensure(e);
   c->e_perm.ensure(e);
   c->nl_iota.ensure(std::max<size_t>(e, (size_t)c->N + 1));
@@ -421,13 +425,20 @@ void build_rowptr(mace_ctx* c, const int* keys, int64_t E, int n, int* rowptr) {
   cub_exclusive_sum(c, c->nl_counts.p, rowptr, (int64_t)n + 1);
 }
 
-// sender-side CSR: perm_s = edge ids stably sorted by sender
+__global__ void k_invert_perm(int64_t E, const int* __restrict__ perm, int* __restrict__ pos) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k < E) pos[perm[k]] = (int)k;
+}
+
+// sender-side CSR: perm_s = edge ids stably sorted by sender, pos_s its inverse
 void build_sender_csr(mace_ctx* c) {
   const int64_t E = c->E;
   c->rowptr_s.ensure((size_t)c->N + 1);
   if (E > 0) {
     launch_fill_iota(c->stream, (int)E, c->nl_iota.p);
     cub_sort_pairs(c, c->sender.p, c->e_keys.p, c->nl_iota.p, c->perm_s.p, E, c->N);
+    hipLaunchKernelGGL(k_invert_perm, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, c->stream, E, c->perm_s.p,
+                       c->pos_s.p);
   }
   build_rowptr(c, c->sender.p, E, c->N, c->rowptr_s.p);
 }
@@ -796,14 +807,15 @@ void backward(mace_ctx* c, bool stress, double* out) {
       launch_gemm_group(st, g);
     }
     const int first_edge_grad = (l == L - 1) ? 0 : 1;  // gY / gef: write on the first layer visited
-    if (l > 0) {
-      Site s(c, lname("tp_bwd", l));
-      launch_tp_bwd_send(st, Ly.lin, N, c->rowptr_s.p, c->perm_s.p, c->receiver.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p,
-                         Ly.h_up.p, c->gM.p, c->gw.p, c->gY.p, c->gup.p, first_edge_grad);
-    } else {
+    {
+      // layers after the first also need dL/dx: per-edge rows in sender order, then a segmented sum
       Site s(c, lname("tp_bwd", l));
       launch_tp_bwd_recv(st, Ly.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p, Ly.h_up.p,
-                         c->gM.p, c->gw.p, c->gY.p, first_edge_grad);
+                         c->gM.p, c->gw.p, c->gY.p, first_edge_grad, c->pos_s.p, l > 0 ? c->gxe.p : nullptr);
+    }
+    if (l > 0) {
+      Site s(c, lname("tp_gather", l));
+      launch_tp_gather_gx(st, Ly.lin, N, c->rowptr_s.p, c->gxe.p, c->gup.p);
     }
     {
       Site s(c, lname("mlp_bwd", l));
@@ -894,10 +906,10 @@ static void free_all(mace_ctx* c) {
   }
   for (auto& b : c->h) b.release();
   for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->embed, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
-                  &c->gv, &c->gw, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup, &c->ypre,
+                  &c->gv, &c->gw, &c->gxe, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup, &c->ypre,
                   &c->node_e})
     b->release();
-  for (auto* b : {&c->species, &c->sender, &c->receiver, &c->shifts, &c->rowptr, &c->rowptr_s, &c->perm_s,
+  for (auto* b : {&c->species, &c->sender, &c->receiver, &c->shifts, &c->rowptr, &c->rowptr_s, &c->perm_s, &c->pos_s,
                   &c->nl_img, &c->nl_bin, &c->nl_bin_sorted, &c->nl_atoms, &c->nl_iota, &c->nl_counts,
                   &c->nl_bin_count, &c->nl_bin_start, &c->e_tmp_i, &c->e_tmp_j, &c->e_tmp_s, &c->e_perm,
                   &c->e_keys})

@@ -66,15 +66,15 @@ void launch_tp_tables(hipStream_t st, int64_t E, int max_lin, const float* Y, fl
 // conv TP fused with the receiver-CSR scatter
 void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
                    const float* Y, const float* Mt, int mts, const float* w, const float* up, float* M);
-// TP VJP, receiver-centric (no input gradient; layer 0); gY is [E][2][16] (per channel half)
+// TP VJP, receiver-centric; gY is [E][2][16] (per channel half).  With gxe != null the
+// per-edge input gradient is also stored, row pos_s[e] of gxe ([E][LIN^2 * NC], sender order)
 void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
                         const float* Y, const float* Mt, int mts, const float* w, const float* up,
-                        const float* gM, float* gw, float* gY, int accumulate_gY);
-// TP VJP, sender-centric (input gradient gup; layers >= 1)
-void launch_tp_bwd_send(hipStream_t st, int lin, int N, const int* rowptr_s, const int* perm_s,
-                        const int* receiver, const float* Y, const float* Mt, int mts, const float* w,
-                        const float* up, const float* gM, float* gw, float* gY, float* gup,
-                        int accumulate_gY);
+                        const float* gM, float* gw, float* gY, int accumulate_gY, const int* pos_s,
+                        float* gxe);
+// gup[a] = sum of the sender-ordered gxe rows of node a
+void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe,
+                         float* gup);
 
 // node linear: Y[n, out_base + (c/NC)*out_stride + m*NC + c%NC] (+)=
 //   sum_k X[n, in_base + (k/NC)*in_stride + m*NC + k%NC] * W[k][c]

@@ -285,19 +285,24 @@ __global__ void __launch_bounds__(256) k_mlp_fwd(int64_t E, int nb, int W, const
       a[rt][c / 4 + 2] = v.z;
       a[rt][c / 4 + 3] = v.w;
     }
-  const int per = W / 4;  // columns per wave (multiple of 32)
-  for (int c0 = wv * per; c0 < (wv + 1) * per; c0 += 16) {
+  // columns per wave (W = 128 * slots, so a multiple of 32); the B values of
+  // the next 16-column tile are loaded while the current one is multiplied
+  const int per = W / 4, cbeg = wv * per, cend = cbeg + per;
+  float bq[16], bn[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) bq[q] = W3[(int64_t)(16 * (q >> 2) + 4 * g + (q & 3)) * W + cbeg + r];
+  for (int c0 = cbeg; c0 < cend; c0 += 16) {
+    if (c0 + 16 < cend) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) bn[q] = W3[(int64_t)(16 * (q >> 2) + 4 * g + (q & 3)) * W + c0 + 16 + r];
+    }
     f4v o[4];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) o[rt] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < RADIAL_H; c += 16)
+    for (int q = 0; q < 16; ++q)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float b = W3[(int64_t)(c + 4 * g + s) * W + c0 + r];
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) o[rt] = mfma16(a[rt][c / 4 + s], b, o[rt]);
-      }
+      for (int rt = 0; rt < 4; ++rt) o[rt] = mfma16(a[rt][q], bq[q], o[rt]);
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
@@ -305,6 +310,8 @@ __global__ void __launch_bounds__(256) k_mlp_fwd(int64_t E, int nb, int W, const
         const int64_t e = e0 + 16 * rt + 4 * g + i;
         if (e < E) w[e * W + c0 + r] = o[rt][i];
       }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) bq[q] = bn[q];
   }
 }
 
@@ -344,15 +351,27 @@ __global__ void __launch_bounds__(256) k_mlp_bwd(int64_t E, int nb, int W, const
   const int64_t er = e0 + r;
   const bool live = er < E;
   const float* gwr = gw + (live ? er : 0) * (int64_t)W;
+  // software pipeline: the gw float4 and the 16 B values of chunk c + 16 are
+  // loaded while chunk c is multiplied
+  float4 ac = live ? *reinterpret_cast<const float4*>(gwr + 4 * g) : make_float4(0.f, 0.f, 0.f, 0.f), an = ac;
+  float bq[16], bn[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) bq[q] = W3T[(int64_t)(4 * g + (q >> 2)) * RADIAL_H + 16 * (q & 3) + r];
   for (int c = 0; c < W; c += 16) {
-    float4 a4 = live ? *reinterpret_cast<const float4*>(gwr + c + 4 * g) : make_float4(0.f, 0.f, 0.f, 0.f);
-    const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+    if (c + 16 < W) {
+      if (live) an = *reinterpret_cast<const float4*>(gwr + c + 16 + 4 * g);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const float* br = W3T + (int64_t)(c + 4 * g + s) * RADIAL_H + r;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) t[q] = mfma16(av[s], br[16 * q], t[q]);
+      for (int q = 0; q < 16; ++q)
+        bn[q] = W3T[(int64_t)(c + 16 + 4 * g + (q >> 2)) * RADIAL_H + 16 * (q & 3) + r];
     }
+    const float av[4] = {ac.x, ac.y, ac.z, ac.w};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) t[q] = mfma16(av[s], bq[4 * s + q], t[q]);
+    ac = an;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) bq[q] = bn[q];
   }
   // back through the hidden layers: g_a3 -> g_h2 -> g_a2 -> g_h1
 #pragma unroll

@@ -306,15 +306,20 @@ __device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& i
   }
 }
 
-// Receiver-centric VJP (no input gradient): used for the first interaction,
-// whose input features are the constant species embedding.
-template <int LIN, int NG>
+// Receiver-centric VJP.  Node n's block walks its incoming edges with dL/dM[n]
+// held in registers.  With GX the per-edge input gradient
+//   gxe[pos_s[e]][l1^2 + i][u] = dL/dx[send(e), l1, i, u] restricted to edge e
+// is stored in sender order (pos_s = inverse of the sender permutation), so
+// k_tp_gather_gx sums each node's rows as one contiguous segment.  Without GX
+// (first interaction: constant embedding input) only dL/dw and dL/dY are made.
+template <int LIN, int NG, bool GX>
 __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __restrict__ rowptr,
                                                         const int* __restrict__ sender, const float* __restrict__ Y,
                                                         const float* __restrict__ Mt, int mts,
                                                         const float* __restrict__ w, const float* __restrict__ up,
                                                         const float* __restrict__ gM, float* __restrict__ gw,
-                                                        float* __restrict__ gY, int accumulate_gY) {
+                                                        float* __restrict__ gY, int accumulate_gY,
+                                                        const int* __restrict__ pos_s, float* __restrict__ gxe) {
   using T = TPT<LIN>;
   constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, WN = NC * T::NSLOT;
   const int n = blockIdx.x, g = group_id(), u = threadIdx.x % NC;
@@ -337,88 +342,43 @@ __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __rest
     float gYu[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) gYu[j] = 0.f;
-    float gx0 = 0.f, gx1[3], gx2[5];
-    tp_edge_vjp<LIN, false>(gm, cur, gw + (int64_t)e * WN + u, Y + (int64_t)e * 16, Mt + (int64_t)e * mts, gx0,
-                            gx1, gx2, gYu);
+    float gx0 = 0.f, gx1[3] = {0.f, 0.f, 0.f}, gx2[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+    tp_edge_vjp<LIN, GX>(gm, cur, gw + (int64_t)e * WN + u, Y + (int64_t)e * 16, Mt + (int64_t)e * mts, gx0,
+                         gx1, gx2, gYu);
+    if constexpr (GX) {
+      float* dst = gxe + (int64_t)pos_s[e] * DIN + u;
+      dst[0] = gx0;
+      if constexpr (LIN >= 2) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i) dst[NC * (1 + i)] = gx1[i];
+      }
+      if constexpr (LIN >= 3) {
+#pragma unroll
+        for (int i = 0; i < 5; ++i) dst[NC * (4 + i)] = gx2[i];
+      }
+    }
     store_gY(gYu, e, u, gY, accumulate_gY);
     cur = nxt;
   }
 }
 
-// Sender-centric VJP: the block of node a walks the edges it sends (through
-// the sender permutation) and accumulates dL/dx[a] in registers.
-template <int LIN, int NG>
-__global__ void __launch_bounds__(NC* NG) k_tp_bwd_send(int N, const int* __restrict__ rowptr_s,
-                                                        const int* __restrict__ perm_s,
-                                                        const int* __restrict__ receiver,
-                                                        const float* __restrict__ Y, const float* __restrict__ Mt,
-                                                        int mts, const float* __restrict__ w,
-                                                        const float* __restrict__ up, const float* __restrict__ gM,
-                                                        float* __restrict__ gw, float* __restrict__ gY,
-                                                        float* __restrict__ gup, int accumulate_gY) {
-  using T = TPT<LIN>;
-  constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, WN = NC * T::NSLOT;
-  constexpr int NX = LIN * LIN;
-  const int a = blockIdx.x, g = group_id(), u = threadIdx.x % NC;
-  EdgeIn<LIN> cur;  // x is the sender node's own input, w changes per edge
-  load_x<LIN>(up + (int64_t)a * DIN + u, cur.x0, cur.x1, cur.x2);
-  float gx[NX];
-#pragma unroll
-  for (int i = 0; i < NX; ++i) gx[i] = 0.f;
-  int gb, ge;
-  group_range<NG>(rowptr_s[a], rowptr_s[a + 1], g, gb, ge);
-  if (gb < ge) {
-    float gmc[T::NACC], gmn[T::NACC], wn[T::NSLOT];
-    int ec = perm_s[gb];
-    load_w<LIN>(w + (int64_t)ec * WN + u, cur.w);
-    {
-      const float* p = gM + (int64_t)receiver[ec] * DMID + u;
-#pragma unroll
-      for (int q = 0; q < T::NACC; ++q) gmc[q] = p[q * NC];
-    }
-#pragma unroll 1
-    for (int k = gb; k < ge; ++k) {
-      int en = ec;
-      if (k + 1 < ge) {
-        en = perm_s[k + 1];
-        load_w<LIN>(w + (int64_t)en * WN + u, wn);
-        const float* p = gM + (int64_t)receiver[en] * DMID + u;
-#pragma unroll
-        for (int q = 0; q < T::NACC; ++q) gmn[q] = p[q * NC];
-      }
-      float gYu[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) gYu[j] = 0.f;
-      float gx1[3] = {0.f, 0.f, 0.f}, gx2[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
-      float gx0 = 0.f;
-      tp_edge_vjp<LIN, true>(gmc, cur, gw + (int64_t)ec * WN + u, Y + (int64_t)ec * 16, Mt + (int64_t)ec * mts,
-                             gx0, gx1, gx2, gYu);
-      gx[0] += gx0;
-      if constexpr (LIN >= 2) {
-#pragma unroll
-        for (int i = 0; i < 3; ++i) gx[1 + i] += gx1[i];
-      }
-      if constexpr (LIN >= 3) {
-#pragma unroll
-        for (int i = 0; i < 5; ++i) gx[4 + i] += gx2[i];
-      }
-      store_gY(gYu, ec, u, gY, accumulate_gY);
-#pragma unroll
-      for (int s = 0; s < T::NSLOT; ++s) cur.w[s] = wn[s];
-#pragma unroll
-      for (int q = 0; q < T::NACC; ++q) gmc[q] = gmn[q];
-      ec = en;
-    }
+// gup[a][row][u] = sum over the edges sent by a (a contiguous segment of the
+// sender-ordered gxe rows, summed in order); grid (N, LIN^2), NC threads.
+__global__ void __launch_bounds__(NC) k_tp_gather_gx(int N, int din, const int* __restrict__ rowptr_s,
+                                                     const float* __restrict__ gxe, float* __restrict__ gup) {
+  const int a = blockIdx.x, row = blockIdx.y, u = threadIdx.x;
+  const int beg = rowptr_s[a], end = rowptr_s[a + 1];
+  const float* src = gxe + (int64_t)row * NC + u;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int k = beg;
+  for (; k + 3 < end; k += 4) {
+    s0 += src[(int64_t)k * din];
+    s1 += src[(int64_t)(k + 1) * din];
+    s2 += src[(int64_t)(k + 2) * din];
+    s3 += src[(int64_t)(k + 3) * din];
   }
-  if constexpr (NG > 1) {
-    __shared__ float sRed[NX][NC];
-    combine_groups<NX, NG>(gx, g, u, sRed);
-  }
-  if (g == 0) {
-    float* go = gup + (int64_t)a * DIN + u;
-#pragma unroll
-    for (int i = 0; i < NX; ++i) go[NC * i] = gx[i];
-  }
+  for (; k < end; ++k) s0 += src[(int64_t)k * din];
+  gup[(int64_t)a * din + row * NC + u] = (s0 + s1) + (s2 + s3);
 }
 
 // Mt[e] = [M1 (3 x K1) | M2 (5 x K2)] from Y[e]; one thread per table entry.
@@ -442,6 +402,22 @@ __global__ void __launch_bounds__(256) k_tp_tables(int64_t E, int nent, const fl
 // groups per node for each number of input blocks
 constexpr int ng_for(int lin) { return lin == 1 ? 2 : 2; }
 
+template <int LIN>
+void launch_fwd(hipStream_t st, int N, const int* rowptr, const int* sender, const float* Y, const float* Mt, int mts,
+                const float* w, const float* up, float* M) {
+  constexpr int NG = ng_for(LIN);
+  hipLaunchKernelGGL((k_tp_fwd<LIN, NG>), dim3(N), dim3(NC * NG), 0, st, N, rowptr, sender, Y, Mt, mts, w, up, M);
+}
+
+template <int LIN, bool GX>
+void launch_recv(hipStream_t st, int N, const int* rowptr, const int* sender, const float* Y, const float* Mt,
+                 int mts, const float* w, const float* up, const float* gM, float* gw, float* gY, int accumulate_gY,
+                 const int* pos_s, float* gxe) {
+  constexpr int NG = ng_for(LIN);
+  hipLaunchKernelGGL((k_tp_bwd_recv<LIN, NG, GX>), dim3(N), dim3(NC * NG), 0, st, N, rowptr, sender, Y, Mt, mts, w,
+                     up, gM, gw, gY, accumulate_gY, pos_s, gxe);
+}
+
 }  // namespace
 
 int tp_table_entries(int max_lin) { return max_lin >= 3 ? TP3_M1_NE + TP3_M2_NE : max_lin == 2 ? TP3_M1_NE : 0; }
@@ -453,33 +429,33 @@ void launch_tp_tables(hipStream_t st, int64_t E, int max_lin, const float* Y, fl
   hipLaunchKernelGGL(k_tp_tables, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, E, nent, Y, Mt, mts);
 }
 
-#define MACE_TP_DISPATCH(KERNEL, ...)                                                                   \
-  switch (lin) {                                                                                        \
-    case 1: hipLaunchKernelGGL((KERNEL<1, ng_for(1)>), dim3(N), dim3(NC * ng_for(1)), 0, st, __VA_ARGS__); break; \
-    case 2: hipLaunchKernelGGL((KERNEL<2, ng_for(2)>), dim3(N), dim3(NC * ng_for(2)), 0, st, __VA_ARGS__); break; \
-    case 3: hipLaunchKernelGGL((KERNEL<3, ng_for(3)>), dim3(N), dim3(NC * ng_for(3)), 0, st, __VA_ARGS__); break; \
-  }
-
 void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int* sender, const float* Y,
                    const float* Mt, int mts, const float* w, const float* up, float* M) {
   if (N <= 0) return;
-  MACE_TP_DISPATCH(k_tp_fwd, N, rowptr, sender, Y, Mt, mts, w, up, M)
+  switch (lin) {
+    case 1: launch_fwd<1>(st, N, rowptr, sender, Y, Mt, mts, w, up, M); break;
+    case 2: launch_fwd<2>(st, N, rowptr, sender, Y, Mt, mts, w, up, M); break;
+    case 3: launch_fwd<3>(st, N, rowptr, sender, Y, Mt, mts, w, up, M); break;
+  }
 }
 
 void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const int* sender, const float* Y,
                         const float* Mt, int mts, const float* w, const float* up, const float* gM, float* gw,
-                        float* gY, int accumulate_gY) {
+                        float* gY, int accumulate_gY, const int* pos_s, float* gxe) {
   if (N <= 0) return;
-  MACE_TP_DISPATCH(k_tp_bwd_recv, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gY, accumulate_gY)
+#define MACE_RECV(L, G) launch_recv<L, G>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gY, accumulate_gY, pos_s, gxe)
+  const bool gx = gxe != nullptr;
+  switch (lin) {
+    case 1: gx ? MACE_RECV(1, true) : MACE_RECV(1, false); break;
+    case 2: gx ? MACE_RECV(2, true) : MACE_RECV(2, false); break;
+    case 3: gx ? MACE_RECV(3, true) : MACE_RECV(3, false); break;
+  }
+#undef MACE_RECV
 }
 
-void launch_tp_bwd_send(hipStream_t st, int lin, int N, const int* rowptr_s, const int* perm_s,
-                        const int* receiver, const float* Y, const float* Mt, int mts, const float* w,
-                        const float* up, const float* gM, float* gw, float* gY, float* gup, int accumulate_gY) {
+void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe, float* gup) {
   if (N <= 0) return;
-  MACE_TP_DISPATCH(k_tp_bwd_send, N, rowptr_s, perm_s, receiver, Y, Mt, mts, w, up, gM, gw, gY, gup,
-                   accumulate_gY)
+  hipLaunchKernelGGL(k_tp_gather_gx, dim3(N, lin * lin), dim3(NC), 0, st, N, NC * lin * lin, rowptr_s, gxe, gup);
 }
-#undef MACE_TP_DISPATCH
 
 }  // namespace mace
