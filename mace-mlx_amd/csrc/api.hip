@@ -119,7 +119,7 @@ struct mace_ctx {
   DBuf<unsigned char> cub_tmp;
   // per-step edge buffers
   DBuf<EdgeGeom> geom;
-  DBuf<float> Y, Mt, ef, zbl_e, gY, gef, gv, gw, gxe;
+  DBuf<float> Y, Mt, ef, zbl_e, gY, gef, gv, gw, gxe, h3;
   DBuf<double> vir_part;
   // node buffers
   std::vector<DBuf<float>> h;  // h[0..L]
@@ -374,6 +374,7 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   c->gY.ensure(e * 32);
   if (c->mts > 0) c->Mt.ensure(e * c->mts);
   c->gef.ensure(e * c->dims.num_bessel);
+  c->h3.ensure(e * RADIAL_H);
   c->gv.ensure(e * 3);
   c->gw.ensure(e * maxw);
   c->vir_part.ensure(9 * ((e + 255) / 256));
@@ -695,7 +696,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
     float* hn = c->h[l + 1].p;
     {
       Site s(c, lname("mlp_fwd", l));
-      launch_mlp_fwd(st, E, nb, L.wn, c->ef.p, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, L.mlp[3].p, L.w.p);
+      launch_mlp_fwd(st, E, nb, L.wn, c->ef.p, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, L.mlpT[3].p, c->h3.p, L.w.p);
     }
     {
       Site s(c, lname("linear_up", l));
@@ -819,8 +820,8 @@ void backward(mace_ctx* c, bool stress, double* out) {
     }
     {
       Site s(c, lname("mlp_bwd", l));
-      launch_mlp_bwd(st, E, nb, Ly.wn, c->ef.p, Ly.mlp[0].p, Ly.mlp[1].p, Ly.mlp[2].p, Ly.mlpT[0].p, Ly.mlpT[1].p,
-                     Ly.mlpT[2].p, Ly.mlpT[3].p, c->gw.p, c->gef.p, first_edge_grad);
+      launch_mlp_bwd(st, E, nb, Ly.wn, c->ef.p, Ly.mlp[0].p, Ly.mlp[1].p, Ly.mlp[2].p, Ly.mlp[3].p, c->gw.p,
+                     c->h3.p, c->gef.p, first_edge_grad);
     }
     if (l > 0) {
       // dE/dh_l = Up^T gup + Skip^T gh + readout_{l-1}'
@@ -906,7 +907,7 @@ static void free_all(mace_ctx* c) {
   }
   for (auto& b : c->h) b.release();
   for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->embed, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
-                  &c->gv, &c->gw, &c->gxe, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup, &c->ypre,
+                  &c->gv, &c->gw, &c->gxe, &c->h3, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup, &c->ypre,
                   &c->node_e})
     b->release();
   for (auto* b : {&c->species, &c->sender, &c->receiver, &c->shifts, &c->rowptr, &c->rowptr_s, &c->perm_s, &c->pos_s,

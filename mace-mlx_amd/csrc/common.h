@@ -49,15 +49,13 @@ void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* re
                      const float* gY, const float* gef, float* gv, double* vir_part,
                      int nblk_vir);
 
-// radial MLP: ef (E x nb) -> w (E x W); weights [in][out] row-major
-void launch_mlp_fwd(hipStream_t st, int64_t E, int nb, int W, const float* ef,
-                    const float* W0, const float* W1, const float* W2, const float* W3,
-                    float* w);
-// backward takes the forward weights (recompute) and their transposes
-// (W0T [64][nb], W1T/W2T [64][64], W3T [W][64])
-void launch_mlp_bwd(hipStream_t st, int64_t E, int nb, int W, const float* ef,
-                    const float* W0, const float* W1, const float* W2, const float* W0T,
-                    const float* W1T, const float* W2T, const float* W3T, const float* gw,
+// radial MLP: ef (E x nb) -> w (E x W); weights [in][out] row-major, W3T = W3 transposed [W][64];
+// h3 is an [E][64] scratch buffer
+void launch_mlp_fwd(hipStream_t st, int64_t E, int nb, int W, const float* ef, const float* W0,
+                    const float* W1, const float* W2, const float* W3T, float* h3, float* w);
+// radial MLP VJP: gef (+)= dL/def from gw; gh3 is an [E][64] scratch buffer
+void launch_mlp_bwd(hipStream_t st, int64_t E, int nb, int W, const float* ef, const float* W0,
+                    const float* W1, const float* W2, const float* W3, const float* gw, float* gh3,
                     float* gef, int accumulate);
 
 // per-edge x2-first tables Mt[e] (row stride mts) for the l1 >= 1 TP paths

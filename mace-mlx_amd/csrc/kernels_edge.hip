@@ -188,239 +188,6 @@ __global__ void __launch_bounds__(256) k_edge_bwd(
 }
 
 // ---------------------------------------------------------------------------
-// radial MLP on fp32 matrix cores (v_mfma_f32_16x16x4f32)
-//
-// Fragment layout of the 16x16x4 instruction (verified on gfx950): lane l holds
-// A[l%16][k] and B[k][l%16] with k = l/16; the accumulator element i of lane l
-// is D[4*(l/16) + i][l%16].  The contraction index may be permuted freely as
-// long as A and B agree, so for a 16-wide k chunk c lane group g = l/16 takes
-// k = 16c + 4g + s at step s: each lane then reads its A values as one float4.
-// ---------------------------------------------------------------------------
-typedef float f4v __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ f4v mfma16(float a, float b, f4v c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
-__device__ __forceinline__ float dsilu(float x) {
-  const float s = 1.f / (1.f + expf(-x));
-  return s * (1.f + x * (1.f - s));
-}
-
-constexpr int RT = 16;            // edges per wave (one MFMA row tile)
-constexpr int XP = RADIAL_H + 4;  // padded LDS row
-
-// One wave: out(16 x 64) = A(16 x K) @ W(K x 64), A from a wave-private LDS tile
-// (row-major, stride XP), W row-major [K][64] in global memory.  Returns the four accumulator tiles (column tiles 0..3).
-__device__ __forceinline__ void wave_gemm_64(const float (*A)[XP], int K, const float* __restrict__ W, f4v* acc) {
-  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
-  if (K % 16 != 0) {  // radial-basis input (K = num_bessel): plain k-steps k = k0 + g, zero padded
-    for (int k0 = 0; k0 < K; k0 += 4) {
-      const int k = k0 + g;
-      const float a = (k < K) ? A[r][k] : 0.f;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t] = mfma16(a, (k < K) ? W[k * RADIAL_H + 16 * t + r] : 0.f, acc[t]);
-    }
-    return;
-  }
-  for (int c = 0; c < K; c += 16) {
-    const float4 a4 = *reinterpret_cast<const float4*>(&A[r][c + 4 * g]);
-    const float av[4] = {a4.x, a4.y, a4.z, a4.w};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const float* wr = W + (c + 4 * g + s) * RADIAL_H + r;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t] = mfma16(av[s], wr[16 * t], acc[t]);
-    }
-  }
-}
-
-// Store accumulator tiles (optionally through silu) into a wave-private LDS tile.
-__device__ __forceinline__ void store_tile(float (*X)[XP], const f4v* acc, bool act) {
-  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) X[4 * g + i][16 * t + r] = act ? silu(acc[t][i]) : acc[t][i];
-}
-
-// forward: block = 4 waves, 64 edges.  Hidden layers: wave w owns rows 16w..16w+15.
-// Last layer: all 64 rows, output columns split across the 4 waves.
-__global__ void __launch_bounds__(256) k_mlp_fwd(int64_t E, int nb, int W, const float* __restrict__ ef,
-                                                 const float* __restrict__ W0, const float* __restrict__ W1,
-                                                 const float* __restrict__ W2, const float* __restrict__ W3,
-                                                 float* __restrict__ w) {
-  __shared__ __align__(16) float sX[4][RT][XP];
-  __shared__ __align__(16) float sY[4][RT][XP];
-  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
-  const int64_t e0 = (int64_t)blockIdx.x * 64;
-  for (int i = l; i < RT * nb; i += 64) {
-    const int e = i / nb, k = i % nb;
-    const int64_t ee = e0 + 16 * wv + e;
-    sX[wv][e][k] = (ee < E) ? ef[ee * nb + k] : 0.f;
-  }
-  __syncthreads();
-  f4v acc[4];
-  wave_gemm_64(sX[wv], nb, W0, acc);
-  store_tile(sY[wv], acc, true);
-  __syncthreads();
-  wave_gemm_64(sY[wv], RADIAL_H, W1, acc);
-  store_tile(sX[wv], acc, true);
-  __syncthreads();
-  wave_gemm_64(sX[wv], RADIAL_H, W2, acc);
-  store_tile(sY[wv], acc, true);
-  __syncthreads();
-  // last layer: A fragments of all four row tiles (h3 in sY[0..3]) into registers
-  float a[4][RADIAL_H / 4];
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-    for (int c = 0; c < RADIAL_H; c += 16) {
-      const float4 v = *reinterpret_cast<const float4*>(&sY[rt][r][c + 4 * g]);
-      a[rt][c / 4 + 0] = v.x;
-      a[rt][c / 4 + 1] = v.y;
-      a[rt][c / 4 + 2] = v.z;
-      a[rt][c / 4 + 3] = v.w;
-    }
-  // columns per wave (W = 128 * slots, so a multiple of 32); the B values of
-  // the next 16-column tile are loaded while the current one is multiplied
-  const int per = W / 4, cbeg = wv * per, cend = cbeg + per;
-  float bq[16], bn[16];
-#pragma unroll
-  for (int q = 0; q < 16; ++q) bq[q] = W3[(int64_t)(16 * (q >> 2) + 4 * g + (q & 3)) * W + cbeg + r];
-  for (int c0 = cbeg; c0 < cend; c0 += 16) {
-    if (c0 + 16 < cend) {
-#pragma unroll
-      for (int q = 0; q < 16; ++q) bn[q] = W3[(int64_t)(16 * (q >> 2) + 4 * g + (q & 3)) * W + c0 + 16 + r];
-    }
-    f4v o[4];
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) o[rt] = f4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int q = 0; q < 16; ++q)
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt) o[rt] = mfma16(a[rt][q], bq[q], o[rt]);
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t e = e0 + 16 * rt + 4 * g + i;
-        if (e < E) w[e * W + c0 + r] = o[rt][i];
-      }
-#pragma unroll
-    for (int q = 0; q < 16; ++q) bq[q] = bn[q];
-  }
-}
-
-// backward: every wave independently handles 16 edges.  Recomputes the hidden
-// pre-activations (kept as accumulator fragments), then
-//   g_h3 = gw @ W3^T, g_a3 = g_h3 * silu'(a3), g_a2 = (g_a3 @ W2^T) * silu'(a2),
-//   g_a1 = (g_a2 @ W1^T) * silu'(a1), g_ef = g_a1 @ W0^T.
-// WkT are the transposed weights: W3T [W][64], W2T/W1T [64][64], W0T [64][nb].
-__global__ void __launch_bounds__(256) k_mlp_bwd(int64_t E, int nb, int W, const float* __restrict__ ef,
-                                                 const float* __restrict__ W0, const float* __restrict__ W1,
-                                                 const float* __restrict__ W2, const float* __restrict__ W0T,
-                                                 const float* __restrict__ W1T, const float* __restrict__ W2T,
-                                                 const float* __restrict__ W3T, const float* __restrict__ gw,
-                                                 float* __restrict__ gef, int accumulate) {
-  __shared__ __align__(16) float sX[4][RT][XP];
-  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
-  const int64_t e0 = (int64_t)blockIdx.x * 64 + 16 * wv;
-  float(*X)[XP] = sX[wv];
-  for (int i = l; i < RT * nb; i += 64) {
-    const int e = i / nb, k = i % nb;
-    X[e][k] = (e0 + e < E) ? ef[(e0 + e) * nb + k] : 0.f;
-  }
-  __syncthreads();
-  f4v a1[4], a2[4], a3[4], t[4];
-  wave_gemm_64(X, nb, W0, a1);
-  __syncthreads();
-  store_tile(X, a1, true);
-  __syncthreads();
-  wave_gemm_64(X, RADIAL_H, W1, a2);
-  __syncthreads();
-  store_tile(X, a2, true);
-  __syncthreads();
-  wave_gemm_64(X, RADIAL_H, W2, a3);
-  // g_h3 = gw (16 x W) @ W3T (W x 64)
-#pragma unroll
-  for (int q = 0; q < 4; ++q) t[q] = f4v{0.f, 0.f, 0.f, 0.f};
-  const int64_t er = e0 + r;
-  const bool live = er < E;
-  const float* gwr = gw + (live ? er : 0) * (int64_t)W;
-  // software pipeline: the gw float4 and the 16 B values of chunk c + 16 are
-  // loaded while chunk c is multiplied
-  float4 ac = live ? *reinterpret_cast<const float4*>(gwr + 4 * g) : make_float4(0.f, 0.f, 0.f, 0.f), an = ac;
-  float bq[16], bn[16];
-#pragma unroll
-  for (int q = 0; q < 16; ++q) bq[q] = W3T[(int64_t)(4 * g + (q >> 2)) * RADIAL_H + 16 * (q & 3) + r];
-  for (int c = 0; c < W; c += 16) {
-    if (c + 16 < W) {
-      if (live) an = *reinterpret_cast<const float4*>(gwr + c + 16 + 4 * g);
-#pragma unroll
-      for (int q = 0; q < 16; ++q)
-        bn[q] = W3T[(int64_t)(c + 16 + 4 * g + (q >> 2)) * RADIAL_H + 16 * (q & 3) + r];
-    }
-    const float av[4] = {ac.x, ac.y, ac.z, ac.w};
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) t[q] = mfma16(av[s], bq[4 * s + q], t[q]);
-    ac = an;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) bq[q] = bn[q];
-  }
-  // back through the hidden layers: g_a3 -> g_h2 -> g_a2 -> g_h1
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) t[q][i] *= dsilu(a3[q][i]);
-  __syncthreads();
-  store_tile(X, t, false);
-  __syncthreads();
-  wave_gemm_64(X, RADIAL_H, W2T, t);
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) t[q][i] *= dsilu(a2[q][i]);
-  __syncthreads();
-  store_tile(X, t, false);
-  __syncthreads();
-  wave_gemm_64(X, RADIAL_H, W1T, t);
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) t[q][i] *= dsilu(a1[q][i]);
-  __syncthreads();
-  store_tile(X, t, false);
-  __syncthreads();
-  // g_ef (16 x nb) = g_a1 (16 x 64) @ W0T (64 x nb): one column tile, columns >= nb padded
-  f4v o = f4v{0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < RADIAL_H; c += 16) {
-    const float4 a4 = *reinterpret_cast<const float4*>(&X[r][c + 4 * g]);
-    const float av[4] = {a4.x, a4.y, a4.z, a4.w};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const float b = (r < nb) ? W0T[(c + 4 * g + s) * nb + r] : 0.f;
-      o = mfma16(av[s], b, o);
-    }
-  }
-  if (r < nb) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t e = e0 + 4 * g + i;
-      if (e < E) {
-        float* dst = gef + e * nb + r;
-        *dst = accumulate ? *dst + o[i] : o[i];
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
 // neighbour list
 // ---------------------------------------------------------------------------
 
@@ -561,20 +328,6 @@ void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* re
   (void)nblk_vir;
   hipLaunchKernelGGL(k_edge_bwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, sender, receiver, species,
                      bessel_w, zbl_z, zbl_cov, p, geom, gY, gef, gv, vir_part);
-}
-
-void launch_mlp_fwd(hipStream_t st, int64_t E, int nb, int W, const float* ef, const float* W0,
-                    const float* W1, const float* W2, const float* W3, float* w) {
-  if (E <= 0) return;
-  hipLaunchKernelGGL(k_mlp_fwd, dim3(nblk(E, 64)), dim3(256), 0, st, E, nb, W, ef, W0, W1, W2, W3, w);
-}
-
-void launch_mlp_bwd(hipStream_t st, int64_t E, int nb, int W, const float* ef, const float* W0,
-                    const float* W1, const float* W2, const float* W0T, const float* W1T, const float* W2T,
-                    const float* W3T, const float* gw, float* gef, int accumulate) {
-  if (E <= 0) return;
-  hipLaunchKernelGGL(k_mlp_bwd, dim3(nblk(E, 64)), dim3(256), 0, st, E, nb, W, ef, W0, W1, W2, W0T, W1T, W2T,
-                     W3T, gw, gef, accumulate);
 }
 
 void launch_nl_bin(hipStream_t st, int N, const double* pos, const NLParams& p, double* wpos, int* img,
