@@ -606,7 +606,7 @@ LinearDesc lin_desc(int d, int K, int Cout, int ldx, int in_base, int in_stride,
   return D;
 }
 
-GemmProb gprob(int N, int d, int K1, int Cout, const float* X1, int ldx1, int base1, int stride1, const float* W1,
+GemmProb gprob(int N, int d, int K1, int Cout, const float* X1, int ldx1, int base1, int stride1, const float* WT1,
                 float* Y, int ldy, int obase, int ostride) {
   GemmProb P{};
   P.d = d;
@@ -618,7 +618,7 @@ GemmProb gprob(int N, int d, int K1, int Cout, const float* X1, int ldx1, int ba
   P.ldx1 = ldx1;
   P.in_base1 = base1;
   P.in_stride1 = stride1;
-  P.W1 = W1;
+  P.WT1 = WT1;
   P.Y = Y;
   P.ldy = ldy;
   P.out_base = obase;
@@ -702,7 +702,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
       Site s(c, lname("linear_up", l));
       GemmGroup g{};
       for (int b = 0; b < L.lin; ++b)
-        g.p[g.n++] = gprob(N, 2 * b + 1, NC, NC, h, L.din, NC * b * b, 0, L.up[b].p, L.h_up.p, L.din, NC * b * b, 0);
+        g.p[g.n++] = gprob(N, 2 * b + 1, NC, NC, h, L.din, NC * b * b, 0, L.upT[b].p, L.h_up.p, L.din, NC * b * b, 0);
       launch_gemm_group(st, g);
     }
     {
@@ -717,7 +717,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
         int first, cnt;
         slot_range(L, lo, &first, &cnt);
         const int d = 2 * lo + 1;
-        g.p[g.n++] = gprob(N, d, cnt * NC, NC, c->M.p, L.dmid, NC * ao[first], NC * d, L.lin_[lo].p, L.A.p, L.dint,
+        g.p[g.n++] = gprob(N, d, cnt * NC, NC, c->M.p, L.dmid, NC * ao[first], NC * d, L.linT[lo].p, L.A.p, L.dint,
                            NC * lo * lo, 0);
       }
       launch_gemm_group(st, g);
@@ -733,14 +733,14 @@ void forward(mace_ctx* c, const double* pos, double* out) {
       Site s(c, lname("linear_prod", l));
       GemmGroup g{};
       for (int b = 0; b < L.lhid; ++b) {
-        GemmProb P = gprob(N, 2 * b + 1, NC, NC, c->B.p, L.dhid, NC * b * b, 0, L.plin[b].p, hn, L.dhid, NC * b * b, 0);
+        GemmProb P = gprob(N, 2 * b + 1, NC, NC, c->B.p, L.dhid, NC * b * b, 0, L.plinT[b].p, hn, L.dhid, NC * b * b, 0);
         if (one_el && b < L.nskip) {
           P.K2 = NC;
           P.X2 = h;
           P.ldx2 = L.din;
           P.in_base2 = NC * b * b;
           P.in_stride2 = 0;
-          P.W2 = L.skip[b].p;
+          P.WT2 = L.skipT[b].p;
         }
         g.p[g.n++] = P;
       }
@@ -786,7 +786,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
       GemmGroup g{};
       for (int b = 0; b < Ly.lhid; ++b)
         g.p[g.n++] =
-            gprob(N, 2 * b + 1, NC, NC, gh, Ly.dhid, NC * b * b, 0, Ly.plinT[b].p, c->gB.p, Ly.dhid, NC * b * b, 0);
+            gprob(N, 2 * b + 1, NC, NC, gh, Ly.dhid, NC * b * b, 0, Ly.plin[b].p, c->gB.p, Ly.dhid, NC * b * b, 0);
       launch_gemm_group(st, g);
     }
     const float* scw[3] = {Ly.sc[0].p, Ly.sc[1].p, Ly.sc[2].p};
@@ -802,7 +802,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
         int first, cnt;
         slot_range(Ly, lo, &first, &cnt);
         const int d = 2 * lo + 1;
-        g.p[g.n++] = gprob(N, d, NC, cnt * NC, c->gA.p, Ly.dint, NC * lo * lo, 0, Ly.linT[lo].p, c->gM.p, Ly.dmid,
+        g.p[g.n++] = gprob(N, d, NC, cnt * NC, c->gA.p, Ly.dint, NC * lo * lo, 0, Ly.lin_[lo].p, c->gM.p, Ly.dmid,
                            NC * ao[first], NC * d);
       }
       launch_gemm_group(st, g);
@@ -831,14 +831,14 @@ void backward(mace_ctx* c, bool stress, double* out) {
         GemmGroup g{};
         for (int b = 0; b < Ly.lin; ++b) {
           GemmProb P =
-              gprob(N, 2 * b + 1, NC, NC, c->gup.p, Ly.din, NC * b * b, 0, Ly.upT[b].p, gh_next, Ly.din, NC * b * b, 0);
+              gprob(N, 2 * b + 1, NC, NC, c->gup.p, Ly.din, NC * b * b, 0, Ly.up[b].p, gh_next, Ly.din, NC * b * b, 0);
           if (one_el && b < Ly.nskip) {
             P.K2 = NC;
             P.X2 = gh;
             P.ldx2 = Ly.dhid;
             P.in_base2 = NC * b * b;
             P.in_stride2 = 0;
-            P.W2 = Ly.skipT[b].p;
+            P.WT2 = Ly.skip[b].p;
           }
           if (b == 0) P.bias = c->layers[l - 1].ro.p;
           g.p[g.n++] = P;

@@ -90,17 +90,17 @@ void launch_linear_species(hipStream_t st, int N, const LinearDesc& d, const flo
                            const float* W, const int* species, float* Y);
 
 // Grouped fp32-MFMA GEMM over node rows: up to GEMM_MAX problems in one launch.
-// Each problem: Y[row, c] (+)= sum_k X1[row, k] W1[k][c] + sum_k X2[row, k] W2[k][c] + bias[c]
+// Each problem: Y[row, c] (+)= sum_k X1[row, k] WT1[c][k] + sum_k X2[row, k] WT2[c][k] + bias[c]
 // with rows (node n, component m), row-addressing as in LinearDesc.
 constexpr int GEMM_MAX = 8;
 struct GemmProb {
   int d, rows, K1, K2, Cout;
   const float* X1;
   int ldx1, in_base1, in_stride1;
-  const float* W1;
+  const float* WT1;  // B^T of operand 1: [Cout][K1]
   const float* X2;
   int ldx2, in_base2, in_stride2;
-  const float* W2;
+  const float* WT2;  // B^T of operand 2: [Cout][K2]
   float* Y;
   int ldy, out_base, out_stride;
   const float* bias;

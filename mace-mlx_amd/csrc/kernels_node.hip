@@ -90,59 +90,117 @@ __global__ void __launch_bounds__(NC) k_linear_species(int rows, LinearDesc D, c
 }
 
 // ---------------------------------------------------------------------------
-// grouped GEMM on fp32 matrix cores: one wave per 16-row x 64-column tile
-// (v_mfma_f32_16x16x4f32; lane l holds A[l%16][k], B[k][l%16], D[4(l/16)+i][l%16];
-// within a 16-wide k chunk lane group g = l/16 takes k = 16c + 4g + s at step s,
-// so its A values arrive as one float4)
+// grouped GEMM on fp32 matrix cores (v_mfma_f32_16x16x4f32; lane l holds
+// A[l%16][k], B[k][l%16], D[4(l/16)+i][l%16]; within a 16-wide k chunk lane
+// group g = l/16 takes k = 16c + 4g + s at step s, so A and B^T rows give one
+// float4 per lane and chunk).
+//
+// A block is 4 waves; each wave computes a 16 x (16 CT) output tile (CT = 1:
+// block = 16 rows x 64 columns; CT = 4: block = 32 rows x 128 columns).  The K dimension (operand 1, then operand 2) is consumed in batches
+// of KB 16-wide chunks whose loads are all in flight together; with DB the
+// next batch is loaded while the current one is multiplied.  Small groups
+// (few row tiles) use CT = 1 for parallelism, large ones CT = 4 so that each
+// A fragment feeds four column tiles.
 // ---------------------------------------------------------------------------
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ void gemm_operand(const float* __restrict__ X, int ldx, int base, int stride,
-                                             const float* __restrict__ W, int K, int Cout, int col0, int n,
-                                             int m, bool live, int r, int g, f4v* acc) {
-  const float* xrow = X + (int64_t)n * ldx + base + m * NC;
-  for (int c = 0; c < K; c += 16) {
-    const int kb = c / NC, kk = c % NC;
-    const float4 a4 = live ? *reinterpret_cast<const float4*>(xrow + kb * stride + kk + 4 * g)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
-    const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+struct GemmChunkSrc {
+  const float* xrow1;  // row n, block m of operand 1
+  const float* xrow2;
+  const float* wt1;    // B^T row of the first output column of operand 1
+  const float* wt2;
+  int K1, K2, stride1, stride2;
+};
+
+template <int CT>
+__device__ __forceinline__ void gemm_load_chunk(const GemmChunkSrc& S, int ci, int g, float4& a, float4* b) {
+  int k = ci * 16;
+  const bool first = k < S.K1;
+  if (!first) k -= S.K1;
+  const float* xr = first ? S.xrow1 : S.xrow2;
+  const int st = first ? S.stride1 : S.stride2, K = first ? S.K1 : S.K2;
+  const float* wr = first ? S.wt1 : S.wt2;
+  a = *reinterpret_cast<const float4*>(xr + (k / NC) * st + (k % NC) + 4 * g);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const float* wr = W + (int64_t)(c + 4 * g + s) * Cout + col0 + r;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], wr[16 * t], acc[t], 0, 0, 0);
-    }
-  }
+  for (int t = 0; t < CT; ++t) b[t] = *reinterpret_cast<const float4*>(wr + (int64_t)16 * t * K + k + 4 * g);
 }
 
-__global__ void __launch_bounds__(64) k_gemm_group(GemmGroup G) {
+template <int CT, int KB, bool DB>
+__global__ void __launch_bounds__(256) k_gemm_group(GemmGroup G) {
   int q = 0;
   while (q + 1 < G.n && (int)blockIdx.x >= G.p[q + 1].tile_begin) ++q;
   const GemmProb& P = G.p[q];
   const int t = blockIdx.x - P.tile_begin;
+  constexpr int WROWS = CT == 4 ? 2 : 1, WCOLS = 4 / WROWS;  // waves per block along rows / columns
   const int tm = t / P.tiles_n, tn = t % P.tiles_n;
-  const int l = threadIdx.x, r = l & 15, g = l >> 4;
-  const int col0 = tn * 64;
-  const int row = tm * 16 + r;
+  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const int rt = tm * WROWS + wv / WCOLS;  // this wave's 16-row tile
+  const int col0 = tn * (WCOLS * 16 * CT) + (wv % WCOLS) * 16 * CT;
+  const int row = rt * 16 + r;
   const bool live = row < P.rows;
-  const int n = live ? row / P.d : 0, m = live ? row - n * P.d : 0;
-  f4v acc[4];
+  const int n = live ? row / P.d : 0, m = live ? row - n * P.d : 0;  // dead rows read row 0, store nothing
+  GemmChunkSrc S;
+  S.xrow1 = P.X1 + (int64_t)n * P.ldx1 + P.in_base1 + m * NC;
+  S.xrow2 = P.K2 > 0 ? P.X2 + (int64_t)n * P.ldx2 + P.in_base2 + m * NC : S.xrow1;
+  S.wt1 = P.WT1 + (int64_t)(col0 + r) * P.K1;
+  S.wt2 = P.K2 > 0 ? P.WT2 + (int64_t)(col0 + r) * P.K2 : S.wt1;
+  S.K1 = P.K1;
+  S.K2 = P.K2;
+  S.stride1 = P.in_stride1;
+  S.stride2 = P.in_stride2;
+  const int nch = (P.K1 + P.K2) / 16;
+  f4v acc[CT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) acc[i] = f4v{0.f, 0.f, 0.f, 0.f};
-  gemm_operand(P.X1, P.ldx1, P.in_base1, P.in_stride1, P.W1, P.K1, P.Cout, col0, n, m, live, r, g, acc);
-  if (P.K2 > 0)
-    gemm_operand(P.X2, P.ldx2, P.in_base2, P.in_stride2, P.W2, P.K2, P.Cout, col0, n, m, live, r, g, acc);
+  for (int u = 0; u < CT; ++u) acc[u] = f4v{0.f, 0.f, 0.f, 0.f};
+  float4 a[KB], b[KB][CT], an[DB ? KB : 1], bn[DB ? KB : 1][CT];
+  if (DB) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ro = tm * 16 + 4 * g + i;
-    if (ro >= P.rows) continue;
-    const int no = ro / P.d, mo = ro - no * P.d;
+    for (int j = 0; j < KB; ++j)
+      if (j < nch) gemm_load_chunk<CT>(S, j, g, a[j], b[j]);
+  }
+  for (int c0 = 0; c0 < nch; c0 += KB) {
+    if (DB) {
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const int col = col0 + 16 * tt + r;
-      float v = acc[tt][i];
-      if (P.bias) v += P.bias[col];
+      for (int j = 0; j < KB; ++j)
+        if (c0 + KB + j < nch) gemm_load_chunk<CT>(S, c0 + KB + j, g, an[DB ? j : 0], bn[DB ? j : 0]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < KB; ++j)
+        if (c0 + j < nch) gemm_load_chunk<CT>(S, c0 + j, g, a[j], b[j]);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // all loads of the batch issued before the multiplies
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      if (c0 + j < nch) {
+        const float av[4] = {a[j].x, a[j].y, a[j].z, a[j].w};
+#pragma unroll
+        for (int u = 0; u < CT; ++u) {
+          const float bv[4] = {b[j][u].x, b[j][u].y, b[j][u].z, b[j][u].w};
+#pragma unroll
+          for (int s2 = 0; s2 < 4; ++s2) acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s2], bv[s2], acc[u], 0, 0, 0);
+        }
+      }
+    }
+    if (DB) {
+#pragma unroll
+      for (int j = 0; j < KB; ++j) {
+        a[j] = an[DB ? j : 0];
+#pragma unroll
+        for (int u = 0; u < CT; ++u) b[j][u] = bn[DB ? j : 0][u];
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < CT; ++u) {
+    const int col = col0 + 16 * u + r;
+    const float bias = P.bias ? P.bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ro = rt * 16 + 4 * g + i;
+      if (ro >= P.rows) continue;
+      const int no = ro / P.d, mo = ro - no * P.d;
       float* y = P.Y + (int64_t)no * P.ldy + P.out_base + (col / NC) * P.out_stride + mo * NC + (col % NC);
+      const float v = acc[u][i] + bias;
       *y = P.accumulate ? *y + v : v;
     }
   }
@@ -506,16 +564,23 @@ void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s
 }
 
 void launch_gemm_group(hipStream_t st, GemmGroup& g) {
+  int row_tiles = 0;
+  for (int q = 0; q < g.n; ++q) row_tiles += (int)cdiv(g.p[q].rows, 16) * (g.p[q].Cout / 64);
+  const bool wide = row_tiles >= 1024;  // enough blocks even with four column tiles per wave
+  const int rows_per_block = wide ? 32 : 16, cols_per_block = wide ? 128 : 64;  // Cout is a multiple of 128
   int tiles = 0;
   for (int q = 0; q < g.n; ++q) {
     GemmProb& P = g.p[q];
-    P.tiles_n = P.Cout / 64;
+    P.tiles_n = P.Cout / cols_per_block;
     P.tile_begin = tiles;
-    tiles += (int)cdiv(P.rows, 16) * P.tiles_n;
+    tiles += (int)cdiv(P.rows, rows_per_block) * P.tiles_n;
   }
   g.total_tiles = tiles;
   if (tiles <= 0) return;
-  hipLaunchKernelGGL(k_gemm_group, dim3(tiles), dim3(64), 0, st, g);
+  if (wide)
+    hipLaunchKernelGGL((k_gemm_group<4, 2, false>), dim3(tiles), dim3(256), 0, st, g);
+  else
+    hipLaunchKernelGGL((k_gemm_group<1, 8, true>), dim3(tiles), dim3(256), 0, st, g);
 }
 
 void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir) {
