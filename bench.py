@@ -51,10 +51,14 @@ def algorithmic_work(site: str, ctx: dict):
         return "hbm", b, "GB/s"
     if name == "tp_gather":  # segmented sum of the per-edge input-gradient rows
         return "hbm", 4 * (E * lay["din"] + N * lay["din"]) + 4 * (N + 1), "GB/s"
-    if name == "mlp_fwd":
-        return "mfma", 2 * E * (nb * H + 2 * H * H + H * lay["wn"]), "TFLOP/s"
-    if name == "mlp_bwd":
-        return "mfma", 2 * E * (2 * (nb * H + 2 * H * H) + H * lay["wn"]), "TFLOP/s"
+    if name == "mlp_hidden":  # three small layers
+        return "mfma", 2 * E * (nb * H + 2 * H * H), "TFLOP/s"
+    if name == "mlp_out":  # w = h3 @ W3
+        return "mfma", 2 * E * H * lay["wn"], "TFLOP/s"
+    if name == "mlp_gh3":  # dL/dh3 = gw @ W3^T
+        return "mfma", 2 * E * H * lay["wn"], "TFLOP/s"
+    if name == "mlp_hidden_bwd":  # recomputed forward + backward of the small layers
+        return "mfma", 2 * E * 2 * (nb * H + 2 * H * H), "TFLOP/s"
     if name.startswith("linear") or name.startswith("skip"):
         return "mfma", ctx["linear_flops"].get(site, 0), "TFLOP/s"
     if name in ("sc_fwd", "sc_bwd"):
@@ -146,10 +150,13 @@ def main():
     import gen_tables
 
     if args.copy_calib_mb > 0:
+        # counter calibration: one elementwise kernel that reads and writes exactly
+        # copy_calib_mb MiB each (b = 2 a); its FETCH_SIZE / WRITE_SIZE give the scale
         n = int(args.copy_calib_mb * (1 << 20) // 4)
         a = torch.ones(n, device="cuda", dtype=torch.float32)
         b = torch.empty_like(a)
-        b.copy_(a)
+        torch.cuda.synchronize()
+        torch.mul(a, 2.0, out=b)
         torch.cuda.synchronize()
         del a, b
 

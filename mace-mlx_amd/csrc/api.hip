@@ -695,8 +695,12 @@ void forward(mace_ctx* c, const double* pos, double* out) {
     const float* h = c->h[l].p;
     float* hn = c->h[l + 1].p;
     {
-      Site s(c, lname("mlp_fwd", l));
-      launch_mlp_fwd(st, E, nb, L.wn, c->ef.p, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, L.mlpT[3].p, c->h3.p, L.w.p);
+      Site s(c, lname("mlp_hidden", l));
+      launch_mlp_hidden(st, E, nb, c->ef.p, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, c->h3.p);
+    }
+    {
+      Site s(c, lname("mlp_out", l));
+      launch_mlp_out(st, E, L.wn, c->h3.p, L.mlpT[3].p, L.w.p);
     }
     {
       Site s(c, lname("linear_up", l));
@@ -819,9 +823,13 @@ void backward(mace_ctx* c, bool stress, double* out) {
       launch_tp_gather_gx(st, Ly.lin, N, c->rowptr_s.p, c->gxe.p, c->gup.p);
     }
     {
-      Site s(c, lname("mlp_bwd", l));
-      launch_mlp_bwd(st, E, nb, Ly.wn, c->ef.p, Ly.mlp[0].p, Ly.mlp[1].p, Ly.mlp[2].p, Ly.mlp[3].p, c->gw.p,
-                     c->h3.p, c->gef.p, first_edge_grad);
+      Site s(c, lname("mlp_gh3", l));
+      launch_mlp_gh3(st, E, Ly.wn, c->gw.p, Ly.mlp[3].p, c->h3.p);
+    }
+    {
+      Site s(c, lname("mlp_hidden_bwd", l));
+      launch_mlp_hidden_bwd(st, E, nb, c->ef.p, Ly.mlp[0].p, Ly.mlp[1].p, Ly.mlp[2].p, c->h3.p, c->gef.p,
+                            first_edge_grad);
     }
     if (l > 0) {
       // dE/dh_l = Up^T gup + Skip^T gh + readout_{l-1}'

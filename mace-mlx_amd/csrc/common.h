@@ -49,14 +49,16 @@ void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* re
                      const float* gY, const float* gef, float* gv, double* vir_part,
                      int nblk_vir);
 
-// radial MLP: ef (E x nb) -> w (E x W); weights [in][out] row-major, W3T = W3 transposed [W][64];
-// h3 is an [E][64] scratch buffer
-void launch_mlp_fwd(hipStream_t st, int64_t E, int nb, int W, const float* ef, const float* W0,
-                    const float* W1, const float* W2, const float* W3T, float* h3, float* w);
-// radial MLP VJP: gef (+)= dL/def from gw; gh3 is an [E][64] scratch buffer
-void launch_mlp_bwd(hipStream_t st, int64_t E, int nb, int W, const float* ef, const float* W0,
-                    const float* W1, const float* W2, const float* W3, const float* gw, float* gh3,
-                    float* gef, int accumulate);
+// radial MLP, ef (E x nb) -> w (E x W); weights [in][out] row-major, W3T = W3 transposed [W][64].
+// h3 [E][64] = silu(silu(silu(ef W0) W1) W2); w = h3 W3
+void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0,
+                       const float* W1, const float* W2, float* h3);
+void launch_mlp_out(hipStream_t st, int64_t E, int W, const float* h3, const float* W3T, float* w);
+// VJP: gh3 = gw W3^T, then gef (+)= dL/def through the recomputed hidden layers
+void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3);
+void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0,
+                           const float* W1, const float* W2, const float* gh3, float* gef,
+                           int accumulate);
 
 // per-edge x2-first tables Mt[e] (row stride mts) for the l1 >= 1 TP paths
 int tp_table_entries(int max_lin);

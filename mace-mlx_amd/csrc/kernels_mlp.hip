@@ -375,17 +375,25 @@ inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
 // staging the weights once and walking several 64-edge groups
 inline unsigned hidden_grid(int64_t E) { return (unsigned)std::min<int64_t>((E + 63) / 64, 512); }
 
-void launch_mlp_fwd(hipStream_t st, int64_t E, int nb, int W, const float* ef, const float* W0, const float* W1,
-                    const float* W2, const float* W3T, float* h3, float* w) {
+void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0, const float* W1,
+                       const float* W2, float* h3) {
   if (E <= 0) return;
   hipLaunchKernelGGL(k_mlp_hidden, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, W0, W1, W2, h3);
+}
+
+void launch_mlp_out(hipStream_t st, int64_t E, int W, const float* h3, const float* W3T, float* w) {
+  if (E <= 0) return;
   hipLaunchKernelGGL(k_mlp_out, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, h3, W3T, w);
 }
 
-void launch_mlp_bwd(hipStream_t st, int64_t E, int nb, int W, const float* ef, const float* W0, const float* W1,
-                    const float* W2, const float* W3, const float* gw, float* gh3, float* gef, int accumulate) {
+void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3) {
   if (E <= 0) return;
   hipLaunchKernelGGL(k_mlp_gh3, dim3(nblk(E, 32)), dim3(256), 0, st, E, W, gw, W3, gh3);
+}
+
+void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0, const float* W1,
+                           const float* W2, const float* gh3, float* gef, int accumulate) {
+  if (E <= 0) return;
   hipLaunchKernelGGL(k_mlp_hidden_bwd, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, W0, W1, W2, gh3, gef,
                      accumulate);
 }

@@ -82,10 +82,15 @@ __device__ __forceinline__ void load_x(const float* __restrict__ xs, float& x0, 
   }
 }
 
-template <int LIN>
+// Per-edge weights.  In the VJP they are a read-once stream written long
+// before (NT: nontemporal loads, which keep them from evicting the gathered
+// node rows and the edge tables from L2); the forward pass reads them right
+// after the radial MLP wrote them and uses plain loads, which can hit in the
+// last-level cache.
+template <int LIN, bool NT>
 __device__ __forceinline__ void load_w(const float* __restrict__ we, float* wv) {
 #pragma unroll
-  for (int s = 0; s < TPT<LIN>::NSLOT; ++s) wv[s] = we[s * NC];
+  for (int s = 0; s < TPT<LIN>::NSLOT; ++s) wv[s] = NT ? __builtin_nontemporal_load(we + s * NC) : we[s * NC];
 }
 
 // Forward contribution of one edge to this channel's accumulators.
@@ -172,12 +177,12 @@ __global__ void __launch_bounds__(NC* NG) k_tp_fwd(int N, const int* __restrict_
   group_range<NG>(rowptr[n], rowptr[n + 1], g, gb, ge);
   if (gb < ge) {
     EdgeIn<LIN> cur, nxt;
-    load_w<LIN>(w + (int64_t)gb * WN + u, cur.w);
+    load_w<LIN, false>(w + (int64_t)gb * WN + u, cur.w);
     load_x<LIN>(up + (int64_t)sender[gb] * DIN + u, cur.x0, cur.x1, cur.x2);
 #pragma unroll 1
     for (int e = gb; e < ge; ++e) {
       if (e + 1 < ge) {
-        load_w<LIN>(w + (int64_t)(e + 1) * WN + u, nxt.w);
+        load_w<LIN, false>(w + (int64_t)(e + 1) * WN + u, nxt.w);
         load_x<LIN>(up + (int64_t)sender[e + 1] * DIN + u, nxt.x0, nxt.x1, nxt.x2);
       }
       tp_edge_fwd<LIN>(acc, cur, Y + (int64_t)e * 16, Mt + (int64_t)e * mts);
@@ -331,12 +336,12 @@ __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __rest
 #pragma unroll
   for (int a = 0; a < T::NACC; ++a) gm[a] = gMn[a * NC];
   EdgeIn<LIN> cur, nxt;
-  load_w<LIN>(w + (int64_t)gb * WN + u, cur.w);
+  load_w<LIN, true>(w + (int64_t)gb * WN + u, cur.w);
   load_x<LIN>(up + (int64_t)sender[gb] * DIN + u, cur.x0, cur.x1, cur.x2);
 #pragma unroll 1
   for (int e = gb; e < ge; ++e) {
     if (e + 1 < ge) {
-      load_w<LIN>(w + (int64_t)(e + 1) * WN + u, nxt.w);
+      load_w<LIN, true>(w + (int64_t)(e + 1) * WN + u, nxt.w);
       load_x<LIN>(up + (int64_t)sender[e + 1] * DIN + u, nxt.x0, nxt.x1, nxt.x2);
     }
     float gYu[16];
