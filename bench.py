@@ -125,6 +125,86 @@ def cpu_baseline(bc, weights, edges, species, budget_s=25.0):
                       f"{max(len(times), 1)} step(s) after 1 warm-up; {med * 1e3:.0f} ms/step"}
 
 
+def layer_shapes(dm):
+    """Per-layer widths (din, dhid, dmid, wn, slots per output degree) of a device model."""
+    sys.path.insert(0, str(ROOT / "mace-mlx_amd" / "csrc"))
+    import gen_tables
+    layers = []
+    for l in range(dm.dims["num_layers"]):
+        lin, lhid = dm.dims["layer_in_blocks"][l], dm.dims["layer_hid_blocks"][l]
+        slots = gen_tables.tp_layout(lin)
+        layers.append(dict(lin=lin, lhid=lhid, din=128 * lin * lin, dhid=128 * lhid * lhid,
+                           dmid=128 * sum(2 * x[2] + 1 for x in slots), wn=128 * len(slots),
+                           nslot_by_l=[sum(1 for x in slots if x[2] == lo) for lo in range(4)]))
+    return layers
+
+
+def tp_scatter_frac(per_step, ctx):
+    """Edge TP + scatter kernels (forward, VJP, gather) against the compulsory bytes of both
+    passes of every layer: achieved GB/s / HBM peak."""
+    sites = [k for k in per_step if k.split(".")[0] in ("tp_fwd", "tp_bwd", "tp_gather")]
+    t = sum(per_step[k][0] for k in sites)
+    b = sum(algorithmic_work(k, ctx)[1] for k in sites if not k.startswith("tp_gather"))
+    return (b / (t * 1e-3) / 1e9) / HBM_PEAK_GBS if t > 0 else 0.0
+
+
+def measure_config(idx, steps, warmup):
+    """Steady-state and rebuild step times plus per-site roofline for configuration idx."""
+    import torch
+    from mace_mlx_amd._ffi import Engine
+    from mace_mlx_amd.device_model import build_device_model
+    from mace_mlx_amd.model_io import random_init
+    from mace_mlx_amd.systems import make_config
+    bc = make_config(idx)
+    weights = random_init(bc.model, 0)
+    dm = build_device_model(bc.model, weights)
+    eng = Engine(0)
+    eng.load_model(dm)
+    s = bc.system
+    zmap = {int(z): k for k, z in enumerate(dm.z_table)}
+    species = np.array([zmap[int(z)] for z in s.numbers], np.int32)
+    eng.set_system(species, s.cell, s.pbc, 0.5)
+    stress = "stress" in bc.properties
+    eng.step(s.positions, stress=stress)
+    N, E = len(s), len(eng.get_edges()[0])
+    pos_d = torch.from_numpy(np.ascontiguousarray(s.positions, dtype=np.float64)).cuda()
+    out_d = torch.zeros(10 + 3 * N, dtype=torch.float64, device="cuda")
+    for _ in range(warmup):
+        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress)
+    eng.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress)
+    eng.sync()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    t0 = time.perf_counter()
+    for _ in range(3):
+        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress, force_nl=True)
+    eng.sync()
+    ms_nl = (time.perf_counter() - t0) / 3 * 1e3
+    eng.set_profiling(True)
+    for _ in range(steps):
+        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress)
+    eng.sync()
+    kt = eng.kernel_times()
+    eng.set_profiling(False)
+    layers = layer_shapes(dm)
+    ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_flops=linear_flops(layers, N))
+    per_step = {k: (v[0] / steps, v[1] // steps) for k, v in kt.items()}
+    dom = max(per_step, key=lambda k: per_step[k][0])
+    b, a, u = algorithmic_work(dom, ctx)
+    t, n = per_step[dom]
+    ach = (a / max(n, 1)) / (t / max(n, 1) * 1e-3) / (1e9 if b == "hbm" else 1e12)
+    frac = ach / (HBM_PEAK_GBS if b == "hbm" else FP32_MFMA_PEAK_TFS)
+    res = {"workload": bc.name, "n_atoms": N, "n_edges": E, "properties": "+".join(bc.properties),
+           "feature_dtype": "fp32", "ms_per_step": round(ms, 4), "ms_per_step_nl_rebuild": round(ms_nl, 4),
+           "atom_steps_per_s": round(N / ms * 1e3, 1), "dominant": dom, "dominant_frac": round(frac, 4),
+           "tp_scatter_hbm_frac": round(tp_scatter_frac(per_step, ctx), 4)}
+    del eng, pos_d, out_d
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -133,6 +213,8 @@ def main():
     ap.add_argument("--config", type=int, default=1, help="benchmark configuration index 0..4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-table", action="store_true", help="print per-kernel times to stderr")
+    ap.add_argument("--sweep", action="store_true",
+                    help="also measure every benchmark configuration (table on stderr, 'sweep' in the JSON)")
     ap.add_argument("--copy-calib-mb", type=float, default=0.0,
                     help="run a plain device copy of this size first (rocprof counter calibration)")
     args = ap.parse_args()
@@ -146,9 +228,6 @@ def main():
     from mace_mlx_amd.device_model import build_device_model
     from mace_mlx_amd.model_io import random_init
     from mace_mlx_amd.systems import make_config
-    sys.path.insert(0, str(ROOT / "mace-mlx_amd" / "csrc"))
-    import gen_tables
-
     if args.copy_calib_mb > 0:
         # counter calibration: one elementwise kernel that reads and writes exactly
         # copy_calib_mb MiB each (b = 2 a); its FETCH_SIZE / WRITE_SIZE give the scale
@@ -205,13 +284,7 @@ def main():
         eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress)
     kt = eng.kernel_times()
     eng.set_profiling(False)
-    layers = []
-    for l in range(dm.dims["num_layers"]):
-        lin, lhid = dm.dims["layer_in_blocks"][l], dm.dims["layer_hid_blocks"][l]
-        slots = gen_tables.tp_layout(lin)
-        layers.append(dict(lin=lin, lhid=lhid, din=128 * lin * lin, dhid=128 * lhid * lhid,
-                           dmid=128 * sum(2 * x[2] + 1 for x in slots), wn=128 * len(slots),
-                           nslot_by_l=[sum(1 for x in slots if x[2] == lo) for lo in range(4)]))
+    layers = layer_shapes(dm)
     ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_flops=linear_flops(layers, N))
     per_step = {k: (v[0] / args.steps, v[1] // args.steps) for k, v in kt.items()}
     dom = max(per_step, key=lambda k: per_step[k][0])
@@ -226,7 +299,7 @@ def main():
         peak = FP32_MFMA_PEAK_TFS
     roofline = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
                 "frac": round(achieved / peak, 4), "traffic": load_traffic(dom), "kernel": dom,
-                "avg_launch_ms": round(avg_ms, 5)}
+                "avg_launch_ms": round(avg_ms, 5), "tp_scatter_hbm_frac": round(tp_scatter_frac(per_step, ctx), 4)}
     if args.kernel_table:
         tot = sum(v[0] for v in per_step.values())
         print(f"{'site':24s} {'ms/step':>9s} {'share':>6s} {'launch':>6s}  roofline", file=sys.stderr)
@@ -238,6 +311,27 @@ def main():
             print(f"{k:24s} {t:9.4f} {t / tot * 100:5.1f}% {n:6d}  {ach:9.2f} {u} ({ach / pk * 100:.1f}% of {b})",
                   file=sys.stderr)
 
+    # neighbour-list rebuild included (the reference's benchmark.py:168-style number)
+    eng.sync()
+    tr = time.perf_counter()
+    nrb = max(3, args.steps // 4)
+    for _ in range(nrb):
+        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress, force_nl=True)
+    eng.sync()
+    ms_rebuild = (time.perf_counter() - tr) / nrb * 1e3
+    del pos_d, out_d
+
+    sweep = None
+    if args.sweep:
+        del eng
+        sweep = [measure_config(i, max(5, args.steps // 2), args.warmup) for i in range(5)]
+        print(f"{'config':16s} {'N':>6s} {'E':>9s} {'ms/step':>9s} {'+NL ms':>8s} {'atom-steps/s':>13s}  "
+              f"dominant site (frac of its roofline)   TP+scatter HBM frac", file=sys.stderr)
+        for r in sweep:
+            print(f"{r['workload']:16s} {r['n_atoms']:6d} {r['n_edges']:9d} {r['ms_per_step']:9.3f} "
+                  f"{r['ms_per_step_nl_rebuild']:8.3f} {r['atom_steps_per_s']:13.0f}  "
+                  f"{r['dominant']:18s} ({r['dominant_frac']:.3f})   {r['tp_scatter_hbm_frac']:.3f}", file=sys.stderr)
+
     cpu = None if args.no_cpu_baseline else cpu_baseline(bc, weights, edges, species)
     line = {
         "metric": "ms per energy+forces step (Si1000, medium arch, fp32); atom-steps/sec",
@@ -248,6 +342,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
         "ms_per_step_host_arrays": round(ms_host, 4),
+        "ms_per_step_nl_rebuild": round(ms_rebuild, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -259,6 +354,8 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
+    if sweep is not None:
+        line["sweep"] = sweep
     print(json.dumps(line))
 
 
