@@ -88,17 +88,20 @@ def linear_flops(cfg_layers, N):
     return out
 
 
-def load_traffic(site: str):
+def load_traffic(site: str, workload: str):
     """HBM bytes per launch of `site` measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
-    (profiles/traffic.json, written from the committed pmc summaries), or None."""
+    (profiles/traffic.json, written from the committed pmc summaries) for this workload,
+    or None."""
     p = ROOT / "profiles" / "traffic.json"
     if not p.exists():
         return None
     try:
         d = json.loads(p.read_text())
+        if d.get("_calibration", {}).get("workload") != workload:
+            return None
         rec = d.get(site)
         return None if rec is None else float(rec["bytes_per_launch"])
-    except Exception:
+    except (ValueError, KeyError, TypeError):
         return None
 
 
@@ -298,7 +301,7 @@ def main():
         achieved = amount / launches / (avg_ms * 1e-3) / 1e12
         peak = FP32_MFMA_PEAK_TFS
     roofline = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-                "frac": round(achieved / peak, 4), "traffic": load_traffic(dom), "kernel": dom,
+                "frac": round(achieved / peak, 4), "traffic": load_traffic(dom, bc.name), "kernel": dom,
                 "avg_launch_ms": round(avg_ms, 5), "tp_scatter_hbm_frac": round(tp_scatter_frac(per_step, ctx), 4)}
     if args.kernel_table:
         tot = sum(v[0] for v in per_step.values())

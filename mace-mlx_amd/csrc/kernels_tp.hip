@@ -96,7 +96,7 @@ __device__ __forceinline__ void load_w(const float* __restrict__ we, float* wv) 
 // Forward contribution of one edge to this channel's accumulators.
 template <int LIN>
 __device__ __forceinline__ void tp_edge_fwd(float* acc, const EdgeIn<LIN>& in, const float* __restrict__ Ye,
-                                            const float* __restrict__ Me) {
+                                            const float* __restrict__ Me, const float* M2) {
   using T = TPT<LIN>;
 #pragma unroll
   for (int s = 0; s < T::NSLOT; ++s) {
@@ -121,10 +121,13 @@ __device__ __forceinline__ void tp_edge_fwd(float* acc, const EdgeIn<LIN>& in, c
       for (int k = 0; k < d; ++k) {
         float t = 0.f;
 #pragma unroll
-        for (int i = 0; i < 5; ++i) t = fmaf(in.x2[i], Me[MT_M2 + i * T::K2 + c0 + k], t);
+        for (int i = 0; i < 5; ++i) t = fmaf(in.x2[i], M2[i * T::K2 + c0 + k], t);
         acc[a0 + k] = fmaf(ww, t, acc[a0 + k]);
       }
     }
+    // three input blocks: keep each slot's LDS table reads next to their use
+    // (hoisting all 155 of them would cost as many registers)
+    if constexpr (LIN == 3) __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -136,6 +139,31 @@ __device__ __forceinline__ int group_id() {
   static_assert(NC % 64 == 0, "a group spans whole waves");
   return __builtin_amdgcn_readfirstlane(threadIdx.x / NC);
 }
+
+// With three input blocks an edge's tables hold 72 + 155 values, more than the
+// scalar registers take; the l1 = 2 part is then staged per wave in LDS
+// (double-buffered, the next edge's part loaded into registers while the
+// current edge is computed) and read back as broadcast LDS loads.
+constexpr int M2N = TP3_M2_NE, M2PAD = 160;
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+struct M2Stage {
+  float r[3];
+  __device__ __forceinline__ void load(const float* __restrict__ row, int lane) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) r[j] = (lane + 64 * j < M2N) ? row[lane + 64 * j] : 0.f;
+  }
+  __device__ __forceinline__ void store(float* buf, int lane) const {
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      if (lane + 64 * j < M2N) buf[lane + 64 * j] = r[j];
+  }
+};
 
 // share [gb, ge) of a node's edge range [beg, end) taken by group g of NG
 template <int NG>
@@ -173,19 +201,40 @@ __global__ void __launch_bounds__(NC* NG) k_tp_fwd(int N, const int* __restrict_
   float acc[T::NACC];
 #pragma unroll
   for (int a = 0; a < T::NACC; ++a) acc[a] = 0.f;
+  constexpr bool STAGE = LIN == 3;
+  __shared__ float sM2[STAGE ? 2 * NG * 2 * M2PAD : 1];  // [wave][buffer][M2PAD]
+  const int lane = threadIdx.x & 63;
+  float* m2buf = sM2 + (STAGE ? (threadIdx.x >> 6) * 2 * M2PAD : 0);
   int gb, ge;
   group_range<NG>(rowptr[n], rowptr[n + 1], g, gb, ge);
   if (gb < ge) {
     EdgeIn<LIN> cur, nxt;
+    M2Stage stg;
     load_w<LIN, false>(w + (int64_t)gb * WN + u, cur.w);
     load_x<LIN>(up + (int64_t)sender[gb] * DIN + u, cur.x0, cur.x1, cur.x2);
+    if constexpr (STAGE) {
+      stg.load(Mt + (int64_t)gb * mts + MT_M2, lane);
+      stg.store(m2buf, lane);
+      wave_sync();
+    }
+    int buf = 0;
 #pragma unroll 1
     for (int e = gb; e < ge; ++e) {
       if (e + 1 < ge) {
         load_w<LIN, false>(w + (int64_t)(e + 1) * WN + u, nxt.w);
         load_x<LIN>(up + (int64_t)sender[e + 1] * DIN + u, nxt.x0, nxt.x1, nxt.x2);
+        if constexpr (STAGE) stg.load(Mt + (int64_t)(e + 1) * mts + MT_M2, lane);
       }
-      tp_edge_fwd<LIN>(acc, cur, Y + (int64_t)e * 16, Mt + (int64_t)e * mts);
+      const float* Me = Mt + (int64_t)e * mts;
+      tp_edge_fwd<LIN>(acc, cur, Y + (int64_t)e * 16, Me, STAGE ? m2buf + buf * M2PAD : Me + MT_M2);
+      if constexpr (STAGE) {
+        if (e + 1 < ge) {
+          wave_sync();
+          stg.store(m2buf + (buf ^ 1) * M2PAD, lane);
+          wave_sync();
+          buf ^= 1;
+        }
+      }
       cur = nxt;
     }
   }
@@ -252,8 +301,8 @@ __device__ __forceinline__ void store_gY(const float* gYu, int64_t e, int u, flo
 // dL/dw, accumulates the input gradient (if GX) and this channel's dL/dY.
 template <int LIN, bool GX>
 __device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& in, float* __restrict__ gwe,
-                                            const float* __restrict__ Ye, const float* __restrict__ Me, float& gx0,
-                                            float* gx1, float* gx2, float* gYu) {
+                                            const float* __restrict__ Ye, const float* __restrict__ Me,
+                                            const float* M2, float& gx0, float* gx1, float* gx2, float* gYu) {
   using T = TPT<LIN>;
 #pragma unroll
   for (int s = 0; s < T::NSLOT; ++s) {
@@ -297,7 +346,7 @@ __device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& i
 #pragma unroll
         for (int i = 0; i < 5; ++i) {
           const int q = i * T::K2 + c0 + k;
-          const float mq = Me[MT_M2 + q];
+          const float mq = M2[q];
           mk = fmaf(in.x2[i], mq, mk);
           if (GX) gx2[i] = fmaf(wg, mq, gx2[i]);
           const float cq = wg * in.x2[i];
@@ -308,6 +357,7 @@ __device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& i
       }
     }
     gwe[s * NC] = gws;
+    if constexpr (LIN == 3) __builtin_amdgcn_sched_barrier(0);  // as in tp_edge_fwd
   }
 }
 
@@ -335,21 +385,34 @@ __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __rest
   const float* gMn = gM + (int64_t)n * DMID + u;
 #pragma unroll
   for (int a = 0; a < T::NACC; ++a) gm[a] = gMn[a * NC];
+  constexpr bool STAGE = LIN == 3;
+  __shared__ float sM2[STAGE ? 2 * NG * 2 * M2PAD : 1];  // [wave][buffer][M2PAD]
+  const int lane = threadIdx.x & 63;
+  float* m2buf = sM2 + (STAGE ? (threadIdx.x >> 6) * 2 * M2PAD : 0);
   EdgeIn<LIN> cur, nxt;
+  M2Stage stg;
   load_w<LIN, true>(w + (int64_t)gb * WN + u, cur.w);
   load_x<LIN>(up + (int64_t)sender[gb] * DIN + u, cur.x0, cur.x1, cur.x2);
+  if constexpr (STAGE) {
+    stg.load(Mt + (int64_t)gb * mts + MT_M2, lane);
+    stg.store(m2buf, lane);
+    wave_sync();
+  }
+  int buf = 0;
 #pragma unroll 1
   for (int e = gb; e < ge; ++e) {
     if (e + 1 < ge) {
       load_w<LIN, true>(w + (int64_t)(e + 1) * WN + u, nxt.w);
       load_x<LIN>(up + (int64_t)sender[e + 1] * DIN + u, nxt.x0, nxt.x1, nxt.x2);
+      if constexpr (STAGE) stg.load(Mt + (int64_t)(e + 1) * mts + MT_M2, lane);
     }
     float gYu[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) gYu[j] = 0.f;
     float gx0 = 0.f, gx1[3] = {0.f, 0.f, 0.f}, gx2[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
-    tp_edge_vjp<LIN, GX>(gm, cur, gw + (int64_t)e * WN + u, Y + (int64_t)e * 16, Mt + (int64_t)e * mts, gx0,
-                         gx1, gx2, gYu);
+    const float* Me = Mt + (int64_t)e * mts;
+    tp_edge_vjp<LIN, GX>(gm, cur, gw + (int64_t)e * WN + u, Y + (int64_t)e * 16, Me,
+                         STAGE ? m2buf + buf * M2PAD : Me + MT_M2, gx0, gx1, gx2, gYu);
     if constexpr (GX) {
       float* dst = gxe + (int64_t)pos_s[e] * DIN + u;
       dst[0] = gx0;
@@ -363,6 +426,14 @@ __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __rest
       }
     }
     store_gY(gYu, e, u, gY, accumulate_gY);
+    if constexpr (STAGE) {
+      if (e + 1 < ge) {
+        wave_sync();
+        stg.store(m2buf + (buf ^ 1) * M2PAD, lane);
+        wave_sync();
+        buf ^= 1;
+      }
+    }
     cur = nxt;
   }
 }
