@@ -110,7 +110,14 @@ def cpu_baseline(bc, weights, edges, species, budget_s=25.0):
     import torch
     sys.path.insert(0, str(ROOT))
     from oracle.model import OracleMACE
-    threads = torch.get_num_threads()
+    threads = len(os.sched_getaffinity(0))  # all host cores this process may use
+    torch.set_num_threads(threads)
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
     m = OracleMACE(cfg=bc.model, weights=weights, dtype=torch.float32)
     s = bc.system
     ei = np.stack([edges[0], edges[1]]).astype(np.int64)
@@ -124,7 +131,7 @@ def cpu_baseline(bc, weights, edges, species, budget_s=25.0):
         times.append(time.perf_counter() - t)
     med = float(np.median(times)) if times else warm
     return {"value": len(s) / med, "unit": "atom-steps/s", "cores": threads, "kind": "port",
-            "sample": f"{bc.name} E+F, float32 CPU oracle (torch, {threads} threads), median of "
+            "sample": f"{bc.name} E+F, float32 CPU oracle (torch, {threads} threads on {model}), median of "
                       f"{max(len(times), 1)} step(s) after 1 warm-up; {med * 1e3:.0f} ms/step"}
 
 
@@ -160,7 +167,7 @@ def measure_config(idx, steps, warmup):
     from mace_mlx_amd.systems import make_config
     bc = make_config(idx)
     weights = random_init(bc.model, 0)
-    dm = build_device_model(bc.model, weights)
+    dm = build_device_model(bc.model, weights, dtype=bc.dtype)
     eng = Engine(0)
     eng.load_model(dm)
     s = bc.system
@@ -200,7 +207,7 @@ def measure_config(idx, steps, warmup):
     ach = (a / max(n, 1)) / (t / max(n, 1) * 1e-3) / (1e9 if b == "hbm" else 1e12)
     frac = ach / (HBM_PEAK_GBS if b == "hbm" else FP32_MFMA_PEAK_TFS)
     res = {"workload": bc.name, "n_atoms": N, "n_edges": E, "properties": "+".join(bc.properties),
-           "feature_dtype": "fp32", "ms_per_step": round(ms, 4), "ms_per_step_nl_rebuild": round(ms_nl, 4),
+           "feature_dtype": bc.dtype, "ms_per_step": round(ms, 4), "ms_per_step_nl_rebuild": round(ms_nl, 4),
            "atom_steps_per_s": round(N / ms * 1e3, 1), "dominant": dom, "dominant_frac": round(frac, 4),
            "tp_scatter_hbm_frac": round(tp_scatter_frac(per_step, ctx), 4)}
     del eng, pos_d, out_d
@@ -243,10 +250,8 @@ def main():
         del a, b
 
     bc = make_config(args.config)
-    if bc.dtype != "float32":
-        print(f"configuration {bc.name}: {bc.dtype} feature path not built; running float32", file=sys.stderr)
     weights = random_init(bc.model, 0)
-    dm = build_device_model(bc.model, weights)
+    dm = build_device_model(bc.model, weights, dtype=bc.dtype)
     eng = Engine(0)
     eng.load_model(dm)
     s = bc.system
@@ -349,7 +354,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "fp32" if bc.dtype == "float32" else "fp16 features / fp32 accumulation",
         "data": "synthetic (seeded lattice + rattle, random-init weights)",
         "config": {"workload": bc.name, "n_atoms": N, "n_edges": E,
                    "properties": "energy+forces+stress" if stress else "energy+forces",

@@ -62,6 +62,11 @@ typedef struct mace_model_dims {
   double zbl_a_exp;
   double zbl_a_prefactor;
   double zbl_scale;          /* ScaleShiftMACE scale applied to the pair term  */
+  int32_t feature_half;      /* 1: float16 feature policy (model.py:1-15, 592-661): weights
+                                rounded to fp16 on the host except E0 / Bessel frequencies,
+                                SH and radial features and every stored activation of the
+                                feature path rounded to fp16, TP weights held in fp16,
+                                accumulation in fp32; 0: float32 throughout               */
 } mace_model_dims;
 
 /* Context lifetime.  device = HIP device ordinal. */

@@ -78,9 +78,12 @@ struct Layer {
   int din = 0, dhid = 0, dmid = 0, dint = 0, wn = 0;
   DBuf<float> up[3], upT[3], skip[3], skipT[3], mlp[4], mlpT[4], lin_[4], linT[4], sc[3], plin[3], plinT[3];
   DBuf<float> ro, ro1, ro2;
+  DBuf<_Float16> mlpT3h;  // fp16 copy of W3^T (float16 feature policy)
   int nskip = 0;
-  // per-step activations
+  // per-step activations (TP weights: w, or wh under the float16 feature policy)
   DBuf<float> h_up, A, w, ro_e;
+  DBuf<_Float16> wh;
+  const void* wptr(bool half) const { return half ? static_cast<const void*>(wh.p) : static_cast<const void*>(w.p); }
 };
 
 }  // namespace
@@ -120,6 +123,7 @@ struct mace_ctx {
   // per-step edge buffers
   DBuf<EdgeGeom> geom;
   DBuf<float> Y, Mt, ef, zbl_e, gY, gef, gv, gw, gxe, h3;
+  DBuf<_Float16> h3h;  // radial-MLP hidden output under the float16 feature policy
   DBuf<double> vir_part;
   // node buffers
   std::vector<DBuf<float>> h;  // h[0..L]
@@ -221,6 +225,13 @@ void upload(mace_ctx* c, DBuf<float>& dst, const std::vector<float>& v) {
   HIPCHK(hipMemcpy(dst.p, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
 }
 
+void upload_half(mace_ctx* c, DBuf<_Float16>& dst, const std::vector<float>& v) {
+  std::vector<_Float16> h(v.size());
+  for (size_t i = 0; i < v.size(); ++i) h[i] = (_Float16)v[i];
+  dst.ensure(h.size());
+  HIPCHK(hipMemcpy(dst.p, h.data(), h.size() * sizeof(_Float16), hipMemcpyHostToDevice));
+}
+
 std::vector<float> transpose(const std::vector<float>& a, int rows, int cols, int batch = 1) {
   std::vector<float> t(a.size());
   for (int b = 0; b < batch; ++b)
@@ -228,6 +239,17 @@ std::vector<float> transpose(const std::vector<float>& a, int rows, int cols, in
       for (int j = 0; j < cols; ++j)
         t[(size_t)b * rows * cols + (size_t)j * rows + i] = a[(size_t)b * rows * cols + (size_t)i * cols + j];
   return t;
+}
+
+void free_layers(mace_ctx* c) {
+  for (auto& L : c->layers) {
+    for (auto* arr : {L.up, L.upT, L.skip, L.skipT, L.sc, L.plin, L.plinT})
+      for (int i = 0; i < 3; ++i) arr[i].release();
+    for (int i = 0; i < 4; ++i) L.mlp[i].release(), L.mlpT[i].release(), L.lin_[i].release(), L.linT[i].release();
+    L.ro.release(), L.ro1.release(), L.ro2.release(), L.h_up.release(), L.A.release(), L.w.release(),
+        L.ro_e.release(), L.wh.release(), L.mlpT3h.release();
+  }
+  c->layers.clear();
 }
 
 void build_model(mace_ctx* c) {
@@ -249,7 +271,7 @@ void build_model(mace_ctx* c) {
     upload(c, c->zbl_z, tensor(c, "zbl_z", nel));
     upload(c, c->zbl_cov, tensor(c, "zbl_cov", nel));
   }
-  c->layers.clear();
+  free_layers(c);
   c->layers.resize(d.num_layers);
   for (int l = 0; l < d.num_layers; ++l) {
     Layer& L = c->layers[l];
@@ -285,6 +307,7 @@ void build_model(mace_ctx* c) {
         const auto& w = tensor(c, p + "mlp." + std::to_string(k), (size_t)rows[k] * cols[k]);
         upload(c, L.mlp[k], w);
         upload(c, L.mlpT[k], transpose(w, rows[k], cols[k]));
+        if (k == 3 && d.feature_half) upload_half(c, L.mlpT3h, transpose(w, rows[k], cols[k]));
       }
     }
     const int* l3 = tp_l3(L.lin);
@@ -360,10 +383,15 @@ void ensure_node_buffers(mace_ctx* c) {
 void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   const size_t e = (size_t)std::max<int64_t>(E, 1);
   int maxw = 0;
+  const bool half = c->dims.feature_half != 0;
   for (auto& ly : c->layers) {
-    ly.w.ensure(e * ly.wn);
+    if (half)
+      ly.wh.ensure(e * ly.wn);
+    else
+      ly.w.ensure(e * ly.wn);
     maxw = std::max(maxw, ly.wn);
   }
+  if (half) c->h3h.ensure(e * RADIAL_H);
   size_t maxdin = 0;  // per-edge input gradients of the layers after the first
   for (size_t l = 1; l < c->layers.size(); ++l) maxdin = std::max(maxdin, (size_t)c->layers[l].din);
   if (maxdin > 0) c->gxe.ensure(e * maxdin);
@@ -603,6 +631,7 @@ LinearDesc lin_desc(int d, int K, int Cout, int ldx, int in_base, int in_stride,
   D.out_base = out_base;
   D.out_stride = out_stride;
   D.accumulate = acc;
+  D.round_half = 0;
   return D;
 }
 
@@ -649,13 +678,15 @@ FrontParams front_params(mace_ctx* c) {
   p.zbl_a_exp = (float)c->dims.zbl_a_exp;
   p.zbl_a_pref = (float)c->dims.zbl_a_prefactor;
   p.zbl_scale = (float)c->dims.zbl_scale;
+  p.feature_half = c->dims.feature_half != 0;
   return p;
 }
 
 // skip connection for hidden block b (rows 2b+1, input block b of h)
-void run_skip(mace_ctx* c, Layer& L, int b, const float* h, float* out, int ldo, int acc) {
+void run_skip(mace_ctx* c, Layer& L, int b, const float* h, float* out, int ldo, int acc, int half) {
   const int d = 2 * b + 1;
   LinearDesc D = lin_desc(d, NC, NC, L.din, NC * b * b, 0, ldo, NC * b * b, 0, acc);
+  D.round_half = half;
   if (c->dims.num_elements == 1)
     launch_linear(c->stream, c->N, D, h, L.skip[b].p, out);
   else
@@ -676,6 +707,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
   const int N = c->N;
   const int64_t E = c->E;
   const int nb = c->dims.num_bessel;
+  const int half = c->dims.feature_half != 0;
   FrontParams fp = front_params(c);
   {
     Site s(c, "edge_fwd");
@@ -688,7 +720,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
   }
   {
     Site s(c, "embed");
-    launch_embed(st, N, c->species.p, c->embed.p, c->layers[0].din, c->h[0].p);
+    launch_embed(st, N, c->species.p, c->embed.p, c->layers[0].din, c->h[0].p, half);
   }
   for (size_t l = 0; l < c->layers.size(); ++l) {
     Layer& L = c->layers[l];
@@ -696,27 +728,34 @@ void forward(mace_ctx* c, const double* pos, double* out) {
     float* hn = c->h[l + 1].p;
     {
       Site s(c, lname("mlp_hidden", l));
-      launch_mlp_hidden(st, E, nb, c->ef.p, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, c->h3.p);
+      launch_mlp_hidden(st, E, nb, c->ef.p, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p,
+                        half ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), half);
     }
     {
       Site s(c, lname("mlp_out", l));
-      launch_mlp_out(st, E, L.wn, c->h3.p, L.mlpT[3].p, L.w.p);
+      if (half)
+        launch_mlp_out(st, E, L.wn, c->h3h.p, L.mlpT3h.p, L.wh.p, 1);
+      else
+        launch_mlp_out(st, E, L.wn, c->h3.p, L.mlpT[3].p, L.w.p, 0);
     }
     {
       Site s(c, lname("linear_up", l));
       GemmGroup g{};
+      g.round_half = half;
       for (int b = 0; b < L.lin; ++b)
         g.p[g.n++] = gprob(N, 2 * b + 1, NC, NC, h, L.din, NC * b * b, 0, L.upT[b].p, L.h_up.p, L.din, NC * b * b, 0);
       launch_gemm_group(st, g);
     }
     {
       Site s(c, lname("tp_fwd", l));
-      launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.w.p, L.h_up.p, c->M.p);
+      launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.wptr(half), L.h_up.p, c->M.p,
+                    half);
     }
     const int* ao = tp_accoff(L.lin);
     {
       Site s(c, lname("linear_msg", l));
       GemmGroup g{};
+      g.round_half = half;
       for (int lo = 0; lo < 4; ++lo) {
         int first, cnt;
         slot_range(L, lo, &first, &cnt);
@@ -729,13 +768,14 @@ void forward(mace_ctx* c, const double* pos, double* out) {
     const float* scw[3] = {L.sc[0].p, L.sc[1].p, L.sc[2].p};
     {
       Site s(c, lname("sc_fwd", l));
-      launch_sc_fwd(st, N, L.lhid, L.corr, L.A.p, L.dint, c->species.p, scw, c->B.p, L.dhid);
+      launch_sc_fwd(st, N, L.lhid, L.corr, L.A.p, L.dint, c->species.p, scw, c->B.p, L.dhid, half);
     }
     const bool one_el = c->dims.num_elements == 1;
     {
       // h' = PLin(B) + Skip(h): one two-operand GEMM per hidden block (one element)
       Site s(c, lname("linear_prod", l));
       GemmGroup g{};
+      g.round_half = half;
       for (int b = 0; b < L.lhid; ++b) {
         GemmProb P = gprob(N, 2 * b + 1, NC, NC, c->B.p, L.dhid, NC * b * b, 0, L.plinT[b].p, hn, L.dhid, NC * b * b, 0);
         if (one_el && b < L.nskip) {
@@ -753,13 +793,13 @@ void forward(mace_ctx* c, const double* pos, double* out) {
     if (!one_el)
       for (int b = 0; b < L.nskip; ++b) {
         Site s(c, lname("skip", l));
-        run_skip(c, L, b, h, hn, L.dhid, 1);
+        run_skip(c, L, b, h, hn, L.dhid, 1, half);
       }
     Site s(c, lname("readout", l));
     if (l + 1 < c->layers.size())
-      launch_readout_linear(st, N, hn, L.dhid, L.ro.p, L.ro_e.p);
+      launch_readout_linear(st, N, hn, L.dhid, L.ro.p, L.ro_e.p, half);
     else
-      launch_readout_mlp(st, N, hn, L.dhid, L.ro1.p, L.ro2.p, L.ro_e.p, c->ypre.p);
+      launch_readout_mlp(st, N, hn, L.dhid, L.ro1.p, L.ro2.p, L.ro_e.p, c->ypre.p, half);
   }
   const float* ro[4];
   for (size_t l = 0; l < c->layers.size(); ++l) ro[l] = c->layers[l].ro_e.p;
@@ -774,6 +814,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
   const int64_t E = c->E;
   const int nb = c->dims.num_bessel;
   const int L = (int)c->layers.size();
+  const int half = c->dims.feature_half != 0;
   // dE/dh_L from the nonlinear readout
   float* gh = c->gh0.p;
   float* gh_next = c->gh1.p;
@@ -815,8 +856,9 @@ void backward(mace_ctx* c, bool stress, double* out) {
     {
       // layers after the first also need dL/dx: per-edge rows in sender order, then a segmented sum
       Site s(c, lname("tp_bwd", l));
-      launch_tp_bwd_recv(st, Ly.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p, Ly.h_up.p,
-                         c->gM.p, c->gw.p, c->gY.p, first_edge_grad, c->pos_s.p, l > 0 ? c->gxe.p : nullptr);
+      launch_tp_bwd_recv(st, Ly.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.wptr(half),
+                         Ly.h_up.p, c->gM.p, c->gw.p, c->gY.p, first_edge_grad, c->pos_s.p,
+                         l > 0 ? c->gxe.p : nullptr, half);
     }
     if (l > 0) {
       Site s(c, lname("tp_gather", l));
@@ -829,7 +871,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
     {
       Site s(c, lname("mlp_hidden_bwd", l));
       launch_mlp_hidden_bwd(st, E, nb, c->ef.p, Ly.mlp[0].p, Ly.mlp[1].p, Ly.mlp[2].p, c->h3.p, c->gef.p,
-                            first_edge_grad);
+                            first_edge_grad, half);
     }
     if (l > 0) {
       // dE/dh_l = Up^T gup + Skip^T gh + readout_{l-1}'
@@ -906,14 +948,9 @@ int mace_create(int32_t device, mace_ctx** out) {
 }
 
 static void free_all(mace_ctx* c) {
-  for (auto& L : c->layers) {
-    for (auto* arr : {L.up, L.upT, L.skip, L.skipT, L.sc, L.plin, L.plinT})
-      for (int i = 0; i < 3; ++i) arr[i].release();
-    for (int i = 0; i < 4; ++i) L.mlp[i].release(), L.mlpT[i].release(), L.lin_[i].release(), L.linT[i].release();
-    L.ro.release(), L.ro1.release(), L.ro2.release(), L.h_up.release(), L.A.release(), L.w.release(),
-        L.ro_e.release();
-  }
+  free_layers(c);
   for (auto& b : c->h) b.release();
+  c->h3h.release();
   for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->embed, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
                   &c->gv, &c->gw, &c->gxe, &c->h3, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup, &c->ypre,
                   &c->node_e})

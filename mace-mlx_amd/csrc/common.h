@@ -38,7 +38,12 @@ struct FrontParams {
   float zbl_a_exp;
   float zbl_a_pref;
   float zbl_scale;
+  int feature_half;      // float16 feature policy: SH and radial features rounded to fp16
 };
+
+// x rounded to the nearest fp16 value when `half` (the stored activations of a
+// model run under the float16 feature policy), else x
+__device__ __forceinline__ float qh(float x, bool half) { return half ? (float)(_Float16)x : x; }
 void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* sender,
                      const int* receiver, const int* shifts, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov,
@@ -50,28 +55,32 @@ void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* re
                      int nblk_vir);
 
 // radial MLP, ef (E x nb) -> w (E x W); weights [in][out] row-major, W3T = W3 transposed [W][64].
-// h3 [E][64] = silu(silu(silu(ef W0) W1) W2); w = h3 W3
+// h3 [E][64] = silu(silu(silu(ef W0) W1) W2); w = h3 W3.  half (float16 feature policy): hidden
+// activations rounded to fp16, h3, W3T and w are fp16 arrays (fp32 accumulation); else fp32.
 void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0,
-                       const float* W1, const float* W2, float* h3);
-void launch_mlp_out(hipStream_t st, int64_t E, int W, const float* h3, const float* W3T, float* w);
+                       const float* W1, const float* W2, void* h3, int half);
+void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w,
+                    int half);
 // VJP: gh3 = gw W3^T, then gef (+)= dL/def through the recomputed hidden layers
 void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3);
 void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0,
                            const float* W1, const float* W2, const float* gh3, float* gef,
-                           int accumulate);
+                           int accumulate, int half);
 
 // per-edge x2-first tables Mt[e] (row stride mts) for the l1 >= 1 TP paths
 int tp_table_entries(int max_lin);
 void launch_tp_tables(hipStream_t st, int64_t E, int max_lin, const float* Y, float* Mt, int mts);
-// conv TP fused with the receiver-CSR scatter
+// conv TP fused with the receiver-CSR scatter; w is float, or _Float16 when half (float16
+// feature policy: M rounded to fp16 values)
 void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
-                   const float* Y, const float* Mt, int mts, const float* w, const float* up, float* M);
+                   const float* Y, const float* Mt, int mts, const void* w, const float* up, float* M,
+                   int half);
 // TP VJP, receiver-centric; gY is [E][2][16] (per channel half).  With gxe != null the
 // per-edge input gradient is also stored, row pos_s[e] of gxe ([E][LIN^2 * NC], sender order)
 void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
-                        const float* Y, const float* Mt, int mts, const float* w, const float* up,
+                        const float* Y, const float* Mt, int mts, const void* w, const float* up,
                         const float* gM, float* gw, float* gY, int accumulate_gY, const int* pos_s,
-                        float* gxe);
+                        float* gxe, int half);
 // gup[a] = sum of the sender-ordered gxe rows of node a
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe,
                          float* gup);
@@ -84,6 +93,7 @@ struct LinearDesc {
   int ldx, in_base, in_stride;
   int ldy, out_base, out_stride;
   int accumulate;   // 0: overwrite, 1: add into Y
+  int round_half;   // stored value rounded to fp16 (float16 feature policy)
 };
 void launch_linear(hipStream_t st, int N, const LinearDesc& d, const float* X, const float* W,
                    float* Y);
@@ -113,23 +123,24 @@ struct GemmGroup {
   GemmProb p[GEMM_MAX];
   int n;
   int total_tiles;
+  int round_half;  // outputs rounded to fp16 values (float16 feature policy)
 };
 void launch_gemm_group(hipStream_t st, GemmGroup& g);
 
-void launch_embed(hipStream_t st, int N, const int* species, const float* emb, int ld, float* h);
+void launch_embed(hipStream_t st, int N, const int* species, const float* emb, int ld, float* h, int half);
 
 // symmetric contraction (all output blocks of one product layer)
 void launch_sc_fwd(hipStream_t st, int N, int nout, int corr, const float* A, int ldA,
-                   const int* species, const float* const* Wsc, float* B, int ldB);
+                   const int* species, const float* const* Wsc, float* B, int ldB, int half);
 void launch_sc_bwd(hipStream_t st, int N, int nout, int corr, const float* A, int ldA,
                    const int* species, const float* const* Wsc, const float* gB, int ldB,
                    float* gA);
 
 // readouts.  linear: e[n] = h[n, 0:NC] . w ; nonlinear: 16-wide SiLU MLP
 void launch_readout_linear(hipStream_t st, int N, const float* h, int ldh, const float* w,
-                           float* e);
+                           float* e, int half);
 void launch_readout_mlp(hipStream_t st, int N, const float* h, int ldh, const float* W1,
-                        const float* W2, float* e, float* ypre);
+                        const float* W2, float* e, float* ypre, int half);
 void launch_readout_mlp_bwd(hipStream_t st, int N, const float* ypre, const float* W1,
                             const float* W2, float* gh, int ldh);
 void launch_readout_linear_bwd(hipStream_t st, int N, const float* w, float* gh, int ldh,

@@ -74,13 +74,15 @@ __global__ void __launch_bounds__(256) k_edge_fwd(
   sh16(x * inv, y * inv, z * inv, Yl);
   float4* Y4 = reinterpret_cast<float4*>(Y + 16 * e);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) Y4[q] = make_float4(Yl[4 * q], Yl[4 * q + 1], Yl[4 * q + 2], Yl[4 * q + 3]);
+  for (int q = 0; q < 4; ++q)
+    Y4[q] = make_float4(qh(Yl[4 * q], p.feature_half), qh(Yl[4 * q + 1], p.feature_half),
+                        qh(Yl[4 * q + 2], p.feature_half), qh(Yl[4 * q + 3], p.feature_half));
   float denv;
   const float env = poly_env(rr / p.r_max, p.pcut, &denv);
   for (int n = 0; n < p.nbessel; ++n) {
     const float w = bessel_w[n];
     const float b = (rr == 0.f) ? p.bessel_pref * w : p.bessel_pref * sinf(w * rr) / rr;
-    ef[(int64_t)p.nbessel * e + n] = b * env;
+    ef[(int64_t)p.nbessel * e + n] = qh(b * env, p.feature_half);
   }
   if (p.has_zbl) {
     const int zs = species[s], zr = species[r];

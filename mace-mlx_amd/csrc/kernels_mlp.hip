@@ -109,18 +109,19 @@ __device__ __forceinline__ void wave_gemm_lds(const float (*A)[XP], int K, const
 }
 
 // accumulator tiles (optionally through silu) -> wave-private LDS tile
-__device__ __forceinline__ void store_tile(float (*X)[XP], const f4v* acc, bool act) {
+// (activations rounded to fp16 values under the float16 feature policy)
+__device__ __forceinline__ void store_tile(float (*X)[XP], const f4v* acc, bool act, bool half = false) {
   const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) X[4 * g + i][16 * t + r] = act ? silu(acc[t][i]) : acc[t][i];
+    for (int i = 0; i < 4; ++i) X[4 * g + i][16 * t + r] = act ? qh(silu(acc[t][i]), half) : acc[t][i];
 }
 
 // Rows e0..e0+15 of ef into the wave's tile, then the three hidden layers;
 // leaves the pre-activations a1..a3 in accumulator layout.
 __device__ __forceinline__ void hidden_fwd(float (*X)[XP], const MlpW& sw, int64_t E, int64_t e0, int nb,
-                                           const float* __restrict__ ef, f4v* a1, f4v* a2, f4v* a3) {
+                                           const float* __restrict__ ef, f4v* a1, f4v* a2, f4v* a3, bool half) {
   const int l = threadIdx.x & 63;
   for (int i = l; i < RT * nb; i += 64) {
     const int e = i / nb, k = i % nb;
@@ -129,20 +130,23 @@ __device__ __forceinline__ void hidden_fwd(float (*X)[XP], const MlpW& sw, int64
   wave_sync();
   wave_gemm_lds<false>(X, nb, sw.w0, a1);
   wave_sync();
-  store_tile(X, a1, true);
+  store_tile(X, a1, true, half);
   wave_sync();
   wave_gemm_lds<false>(X, H, sw.w1, a2);
   wave_sync();
-  store_tile(X, a2, true);
+  store_tile(X, a2, true, half);
   wave_sync();
   wave_gemm_lds<false>(X, H, sw.w2, a3);
   wave_sync();
 }
 
 // Waves walk 16-edge groups (grid-stride) after the block has staged W0..W2.
+// HT = float, or _Float16 under the float16 feature policy.
+template <typename HT>
 __global__ void __launch_bounds__(256) k_mlp_hidden(int64_t E, int nb, const float* __restrict__ ef,
                                                     const float* __restrict__ W0, const float* __restrict__ W1,
-                                                    const float* __restrict__ W2, float* __restrict__ h3) {
+                                                    const float* __restrict__ W2, HT* __restrict__ h3) {
+  constexpr bool HALF = sizeof(HT) == 2;
   __shared__ MlpW sw;
   __shared__ __align__(16) float sX[4][RT][XP];
   stage_weights(sw, nb, W0, W1, W2);
@@ -151,13 +155,13 @@ __global__ void __launch_bounds__(256) k_mlp_hidden(int64_t E, int nb, const flo
   for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
     const int64_t e0 = gi * RT;
     f4v a1[4], a2[4], a3[4];
-    hidden_fwd(sX[wv], sw, E, e0, nb, ef, a1, a2, a3);
+    hidden_fwd(sX[wv], sw, E, e0, nb, ef, a1, a2, a3, HALF);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t e = e0 + 4 * g + i;
       if (e < E)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) h3[e * H + 16 * t + r] = silu(a3[t][i]);
+        for (int t = 0; t < 4; ++t) h3[e * H + 16 * t + r] = (HT)silu(a3[t][i]);
     }
   }
 }
@@ -231,6 +235,82 @@ __global__ void __launch_bounds__(256) k_mlp_out(int64_t E, int W, const float* 
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int c = 0; c < 4; ++c) b[u][c] = bn[u][c];
+  }
+}
+
+// Float16 feature policy: w[E][W] (fp16) = h3[E][64] (fp16) @ W3 (fp16, given
+// transposed W3T [W][64]) on v_mfma_f32_16x16x32_f16 with fp32 accumulation;
+// lane l holds A[l%16][8(l/16) .. +7] and B[8(l/16) .. +7][l%16] of a 32-wide
+// k chunk (checked on gfx950), D as in the fp32 instruction.  Tiling as in
+// k_mlp_out; each 64 x 32 result is staged in LDS as fp16 and written as 64-byte
+// row segments.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f4v mfma16h(h8 a, h8 b, f4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__global__ void __launch_bounds__(256) k_mlp_out_h(int64_t E, int W, const _Float16* __restrict__ h3,
+                                                   const _Float16* __restrict__ W3T, _Float16* __restrict__ w) {
+  __shared__ __align__(16) _Float16 sO[4][64][40];
+  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * 64;
+  const int per = W / 8;
+  const int cb = blockIdx.y * (W / 2) + wv * per, ce = cb + per;
+  h8 a[4][2];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int64_t row = min(row0 + 16 * t + r, E - 1);  // rows past the end are computed, not stored
+#pragma unroll
+    for (int c = 0; c < 2; ++c) a[t][c] = *reinterpret_cast<const h8*>(h3 + row * H + 32 * c + 8 * g);
+  }
+  h8 b[2][2], bn[2][2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      b[u][c] = *reinterpret_cast<const h8*>(W3T + (int64_t)min(cb + 16 * u + r, W - 1) * H + 32 * c + 8 * g);
+  _Float16(*O)[40] = sO[wv];
+  for (int c0 = cb; c0 < ce; c0 += 32) {
+    if (c0 + 32 < ce) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          bn[u][c] = *reinterpret_cast<const h8*>(W3T + (int64_t)min(c0 + 32 + 16 * u + r, W - 1) * H + 32 * c +
+                                                  8 * g);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    f4v o[4][2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) o[t][u] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) o[t][u] = mfma16h(a[t][c], b[u][c], o[t][u]);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) O[16 * t + 4 * g + i][16 * u + r] = (_Float16)o[t][u][i];
+    wave_sync();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {  // lane l: row l/4 + 16q, columns 8 (l%4) .. + 7
+      const int rr = (l >> 2) + 16 * q;
+      const int64_t row = row0 + rr;
+      if (row < E && c0 + 8 * (l & 3) < ce)
+        *reinterpret_cast<h8*>(&w[row * W + c0 + 8 * (l & 3)]) = *reinterpret_cast<const h8*>(&O[rr][8 * (l & 3)]);
+    }
+    wave_sync();
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) b[u][c] = bn[u][c];
   }
 }
 
@@ -311,7 +391,7 @@ __global__ void __launch_bounds__(256) k_mlp_gh3(int64_t E, int W, const float* 
 __global__ void __launch_bounds__(256) k_mlp_hidden_bwd(int64_t E, int nb, const float* __restrict__ ef,
                                                         const float* __restrict__ W0, const float* __restrict__ W1,
                                                         const float* __restrict__ W2, const float* __restrict__ gh3,
-                                                        float* __restrict__ gef, int accumulate) {
+                                                        float* __restrict__ gef, int accumulate, int half) {
   __shared__ MlpW sw;
   __shared__ __align__(16) float sX[4][RT][XP];
   stage_weights(sw, nb, W0, W1, W2);
@@ -321,7 +401,7 @@ __global__ void __launch_bounds__(256) k_mlp_hidden_bwd(int64_t E, int nb, const
   for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
     const int64_t e0 = gi * RT;
     f4v a1[4], a2[4], a3[4], t[4];
-    hidden_fwd(X, sw, E, e0, nb, ef, a1, a2, a3);
+    hidden_fwd(X, sw, E, e0, nb, ef, a1, a2, a3, half);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t e = e0 + 4 * g + i;
@@ -376,14 +456,24 @@ inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
 inline unsigned hidden_grid(int64_t E) { return (unsigned)std::min<int64_t>((E + 63) / 64, 512); }
 
 void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0, const float* W1,
-                       const float* W2, float* h3) {
+                       const float* W2, void* h3, int half) {
   if (E <= 0) return;
-  hipLaunchKernelGGL(k_mlp_hidden, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, W0, W1, W2, h3);
+  if (half)
+    hipLaunchKernelGGL(k_mlp_hidden<_Float16>, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, W0, W1, W2,
+                       static_cast<_Float16*>(h3));
+  else
+    hipLaunchKernelGGL(k_mlp_hidden<float>, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, W0, W1, W2,
+                       static_cast<float*>(h3));
 }
 
-void launch_mlp_out(hipStream_t st, int64_t E, int W, const float* h3, const float* W3T, float* w) {
+void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w, int half) {
   if (E <= 0) return;
-  hipLaunchKernelGGL(k_mlp_out, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, h3, W3T, w);
+  if (half)
+    hipLaunchKernelGGL(k_mlp_out_h, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const _Float16*>(h3),
+                       static_cast<const _Float16*>(W3T), static_cast<_Float16*>(w));
+  else
+    hipLaunchKernelGGL(k_mlp_out, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const float*>(h3),
+                       static_cast<const float*>(W3T), static_cast<float*>(w));
 }
 
 void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3) {
@@ -392,10 +482,10 @@ void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const flo
 }
 
 void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0, const float* W1,
-                           const float* W2, const float* gh3, float* gef, int accumulate) {
+                           const float* W2, const float* gh3, float* gef, int accumulate, int half) {
   if (E <= 0) return;
   hipLaunchKernelGGL(k_mlp_hidden_bwd, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, W0, W1, W2, gh3, gef,
-                     accumulate);
+                     accumulate, half);
 }
 
 }  // namespace mace

@@ -70,7 +70,7 @@ __global__ void __launch_bounds__(256) k_linear(int rows, LinearDesc D, const fl
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t o = lin_out_addr(D, row, col0 + tc * 4 + j);
-      Yo[o] = D.accumulate ? Yo[o] + acc[i][j] : acc[i][j];
+      Yo[o] = qh(D.accumulate ? Yo[o] + acc[i][j] : acc[i][j], D.round_half);
     }
   }
 }
@@ -86,7 +86,7 @@ __global__ void __launch_bounds__(NC) k_linear_species(int rows, LinearDesc D, c
   float acc = 0.f;
   for (int k = 0; k < D.K; ++k) acc = fmaf(X[lin_in_addr(D, row, k)], Wz[(int64_t)k * D.Cout + c], acc);
   const int64_t o = lin_out_addr(D, row, c);
-  Yo[o] = D.accumulate ? Yo[o] + acc : acc;
+  Yo[o] = qh(D.accumulate ? Yo[o] + acc : acc, D.round_half);
 }
 
 // ---------------------------------------------------------------------------
@@ -201,15 +201,15 @@ __global__ void __launch_bounds__(256) k_gemm_group(GemmGroup G) {
       const int no = ro / P.d, mo = ro - no * P.d;
       float* y = P.Y + (int64_t)no * P.ldy + P.out_base + (col / NC) * P.out_stride + mo * NC + (col % NC);
       const float v = acc[u][i] + bias;
-      *y = P.accumulate ? *y + v : v;
+      *y = qh(P.accumulate ? *y + v : v, G.round_half);
     }
   }
 }
 
 __global__ void k_embed(int N, const int* __restrict__ species, const float* __restrict__ emb, int ld,
-                        float* __restrict__ h) {
+                        float* __restrict__ h, int half) {
   const int n = blockIdx.x, u = threadIdx.x;
-  h[(int64_t)n * ld + u] = emb[species[n] * NC + u];
+  h[(int64_t)n * ld + u] = qh(emb[species[n] * NC + u], half);
 }
 
 // ---------------------------------------------------------------------------
@@ -237,7 +237,7 @@ MACE_SC(2, 1) MACE_SC(2, 2) MACE_SC(2, 3)
 
 template <int LOUT, int CORR>
 __device__ __forceinline__ void sc_block_fwd(const float* f, const float* __restrict__ Wl, int z, int c,
-                                             float* __restrict__ Bn) {
+                                             float* __restrict__ Bn, bool half) {
   using P = ScPoly<LOUT, CORR>;
   float w[P::KT];
   const float* wz = Wl + (int64_t)z * P::KT * NC + c;
@@ -246,7 +246,7 @@ __device__ __forceinline__ void sc_block_fwd(const float* f, const float* __rest
   float o[2 * LOUT + 1];
   P::fwd(f, w, o);
 #pragma unroll
-  for (int m = 0; m < 2 * LOUT + 1; ++m) Bn[NC * (LOUT * LOUT + m) + c] = o[m];
+  for (int m = 0; m < 2 * LOUT + 1; ++m) Bn[NC * (LOUT * LOUT + m) + c] = qh(o[m], half);
 }
 
 template <int LOUT, int CORR>
@@ -269,7 +269,7 @@ __device__ __forceinline__ void sc_block_vjp(const float* f, const float* __rest
 template <int CORR>
 __global__ void __launch_bounds__(NC) k_sc_fwd(int N, int nout, const float* __restrict__ A, int ldA,
                                                const int* __restrict__ species, ScW W, float* __restrict__ B,
-                                               int ldB) {
+                                               int ldB, int half) {
   const int n = blockIdx.x, c = threadIdx.x;
   float f[16];
   const float* An = A + (int64_t)n * ldA + c;
@@ -277,9 +277,9 @@ __global__ void __launch_bounds__(NC) k_sc_fwd(int N, int nout, const float* __r
   for (int i = 0; i < 16; ++i) f[i] = An[i * NC];
   const int z = species[n];
   float* Bn = B + (int64_t)n * ldB;
-  sc_block_fwd<0, CORR>(f, W.w[0], z, c, Bn);
-  if (nout > 1) sc_block_fwd<1, CORR>(f, W.w[1], z, c, Bn);
-  if (nout > 2) sc_block_fwd<2, CORR>(f, W.w[2], z, c, Bn);
+  sc_block_fwd<0, CORR>(f, W.w[0], z, c, Bn, half);
+  if (nout > 1) sc_block_fwd<1, CORR>(f, W.w[1], z, c, Bn, half);
+  if (nout > 2) sc_block_fwd<2, CORR>(f, W.w[2], z, c, Bn, half);
 }
 
 template <int CORR>
@@ -314,20 +314,20 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 __global__ void __launch_bounds__(64) k_readout_linear(int N, const float* __restrict__ h, int ldh,
-                                                       const float* __restrict__ w, float* __restrict__ e) {
+                                                       const float* __restrict__ w, float* __restrict__ e, int half) {
   const int n = blockIdx.x, l = threadIdx.x;
   const float* hn = h + (int64_t)n * ldh;
   float a = 0.f;
   for (int u = l; u < NC; u += 64) a = fmaf(hn[u], w[u], a);
   a = wave_sum(a);
-  if (l == 0) e[n] = a;
+  if (l == 0) e[n] = qh(a, half);
 }
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
 
 __global__ void __launch_bounds__(64) k_readout_mlp(int N, const float* __restrict__ h, int ldh,
                                                     const float* __restrict__ W1, const float* __restrict__ W2,
-                                                    float* __restrict__ e, float* __restrict__ ypre) {
+                                                    float* __restrict__ e, float* __restrict__ ypre, int half) {
   const int n = blockIdx.x, l = threadIdx.x;
   const float* hn = h + (int64_t)n * ldh;
   float y[16];
@@ -344,10 +344,11 @@ __global__ void __launch_bounds__(64) k_readout_mlp(int N, const float* __restri
     float a = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      ypre[(int64_t)n * 16 + j] = y[j];
-      a = fmaf(silu_f(y[j]), W2[j], a);
+      const float yj = qh(y[j], half);
+      ypre[(int64_t)n * 16 + j] = yj;
+      a = fmaf(qh(silu_f(yj), half), W2[j], a);
     }
-    e[n] = a;
+    e[n] = qh(a, half);
   }
 }
 
@@ -490,19 +491,19 @@ void launch_linear_species(hipStream_t st, int N, const LinearDesc& d, const flo
   hipLaunchKernelGGL(k_linear_species, dim3(rows, d.Cout / NC), dim3(NC), 0, st, rows, d, X, W, species, Y);
 }
 
-void launch_embed(hipStream_t st, int N, const int* species, const float* emb, int ld, float* h) {
+void launch_embed(hipStream_t st, int N, const int* species, const float* emb, int ld, float* h, int half) {
   if (N <= 0) return;
-  hipLaunchKernelGGL(k_embed, dim3(N), dim3(NC), 0, st, N, species, emb, ld, h);
+  hipLaunchKernelGGL(k_embed, dim3(N), dim3(NC), 0, st, N, species, emb, ld, h, half);
 }
 
 void launch_sc_fwd(hipStream_t st, int N, int nout, int corr, const float* A, int ldA, const int* species,
-                   const float* const* Wsc, float* B, int ldB) {
+                   const float* const* Wsc, float* B, int ldB, int half) {
   if (N <= 0) return;
   ScW w{{Wsc[0], nout > 1 ? Wsc[1] : nullptr, nout > 2 ? Wsc[2] : nullptr}};
   switch (corr) {
-    case 1: hipLaunchKernelGGL(k_sc_fwd<1>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB); break;
-    case 2: hipLaunchKernelGGL(k_sc_fwd<2>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB); break;
-    case 3: hipLaunchKernelGGL(k_sc_fwd<3>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB); break;
+    case 1: hipLaunchKernelGGL(k_sc_fwd<1>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB, half); break;
+    case 2: hipLaunchKernelGGL(k_sc_fwd<2>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB, half); break;
+    case 3: hipLaunchKernelGGL(k_sc_fwd<3>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB, half); break;
   }
 }
 
@@ -523,15 +524,15 @@ void launch_sc_bwd(hipStream_t st, int N, int nout, int corr, const float* A, in
   }
 }
 
-void launch_readout_linear(hipStream_t st, int N, const float* h, int ldh, const float* w, float* e) {
+void launch_readout_linear(hipStream_t st, int N, const float* h, int ldh, const float* w, float* e, int half) {
   if (N <= 0) return;
-  hipLaunchKernelGGL(k_readout_linear, dim3(N), dim3(64), 0, st, N, h, ldh, w, e);
+  hipLaunchKernelGGL(k_readout_linear, dim3(N), dim3(64), 0, st, N, h, ldh, w, e, half);
 }
 
 void launch_readout_mlp(hipStream_t st, int N, const float* h, int ldh, const float* W1, const float* W2,
-                        float* e, float* ypre) {
+                        float* e, float* ypre, int half) {
   if (N <= 0) return;
-  hipLaunchKernelGGL(k_readout_mlp, dim3(N), dim3(64), 0, st, N, h, ldh, W1, W2, e, ypre);
+  hipLaunchKernelGGL(k_readout_mlp, dim3(N), dim3(64), 0, st, N, h, ldh, W1, W2, e, ypre, half);
 }
 
 void launch_readout_mlp_bwd(hipStream_t st, int N, const float* ypre, const float* W1, const float* W2,

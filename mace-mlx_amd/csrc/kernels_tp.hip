@@ -87,10 +87,12 @@ __device__ __forceinline__ void load_x(const float* __restrict__ xs, float& x0, 
 // node rows and the edge tables from L2); the forward pass reads them right
 // after the radial MLP wrote them and uses plain loads, which can hit in the
 // last-level cache.
-template <int LIN, bool NT>
-__device__ __forceinline__ void load_w(const float* __restrict__ we, float* wv) {
+// WT = float, or _Float16 under the float16 feature policy.
+template <int LIN, bool NT, typename WT>
+__device__ __forceinline__ void load_w(const WT* __restrict__ we, float* wv) {
 #pragma unroll
-  for (int s = 0; s < TPT<LIN>::NSLOT; ++s) wv[s] = NT ? __builtin_nontemporal_load(we + s * NC) : we[s * NC];
+  for (int s = 0; s < TPT<LIN>::NSLOT; ++s)
+    wv[s] = (float)(NT ? __builtin_nontemporal_load(we + s * NC) : we[s * NC]);
 }
 
 // Forward contribution of one edge to this channel's accumulators.
@@ -189,12 +191,12 @@ __device__ __forceinline__ void combine_groups(float* v, int g, int u, float (*s
   }
 }
 
-template <int LIN, int NG>
+template <int LIN, int NG, typename WT>
 __global__ void __launch_bounds__(NC* NG) k_tp_fwd(int N, const int* __restrict__ rowptr,
                                                    const int* __restrict__ sender, const float* __restrict__ Y,
                                                    const float* __restrict__ Mt, int mts,
-                                                   const float* __restrict__ w, const float* __restrict__ up,
-                                                   float* __restrict__ M) {
+                                                   const WT* __restrict__ w, const float* __restrict__ up,
+                                                   float* __restrict__ M, int half) {
   using T = TPT<LIN>;
   constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, WN = NC * T::NSLOT;
   const int n = blockIdx.x, g = group_id(), u = threadIdx.x % NC;
@@ -210,7 +212,7 @@ __global__ void __launch_bounds__(NC* NG) k_tp_fwd(int N, const int* __restrict_
   if (gb < ge) {
     EdgeIn<LIN> cur, nxt;
     M2Stage stg;
-    load_w<LIN, false>(w + (int64_t)gb * WN + u, cur.w);
+    load_w<LIN, false, WT>(w + (int64_t)gb * WN + u, cur.w);
     load_x<LIN>(up + (int64_t)sender[gb] * DIN + u, cur.x0, cur.x1, cur.x2);
     if constexpr (STAGE) {
       stg.load(Mt + (int64_t)gb * mts + MT_M2, lane);
@@ -221,7 +223,7 @@ __global__ void __launch_bounds__(NC* NG) k_tp_fwd(int N, const int* __restrict_
 #pragma unroll 1
     for (int e = gb; e < ge; ++e) {
       if (e + 1 < ge) {
-        load_w<LIN, false>(w + (int64_t)(e + 1) * WN + u, nxt.w);
+        load_w<LIN, false, WT>(w + (int64_t)(e + 1) * WN + u, nxt.w);
         load_x<LIN>(up + (int64_t)sender[e + 1] * DIN + u, nxt.x0, nxt.x1, nxt.x2);
         if constexpr (STAGE) stg.load(Mt + (int64_t)(e + 1) * mts + MT_M2, lane);
       }
@@ -245,7 +247,7 @@ __global__ void __launch_bounds__(NC* NG) k_tp_fwd(int N, const int* __restrict_
   if (g == 0) {
     float* Mn = M + (int64_t)n * DMID + u;
 #pragma unroll
-    for (int a = 0; a < T::NACC; ++a) Mn[a * NC] = acc[a];
+    for (int a = 0; a < T::NACC; ++a) Mn[a * NC] = qh(acc[a], half);
   }
 }
 
@@ -367,11 +369,11 @@ __device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& i
 // is stored in sender order (pos_s = inverse of the sender permutation), so
 // k_tp_gather_gx sums each node's rows as one contiguous segment.  Without GX
 // (first interaction: constant embedding input) only dL/dw and dL/dY are made.
-template <int LIN, int NG, bool GX>
+template <int LIN, int NG, bool GX, typename WT>
 __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __restrict__ rowptr,
                                                         const int* __restrict__ sender, const float* __restrict__ Y,
                                                         const float* __restrict__ Mt, int mts,
-                                                        const float* __restrict__ w, const float* __restrict__ up,
+                                                        const WT* __restrict__ w, const float* __restrict__ up,
                                                         const float* __restrict__ gM, float* __restrict__ gw,
                                                         float* __restrict__ gY, int accumulate_gY,
                                                         const int* __restrict__ pos_s, float* __restrict__ gxe) {
@@ -391,7 +393,7 @@ __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __rest
   float* m2buf = sM2 + (STAGE ? (threadIdx.x >> 6) * 2 * M2PAD : 0);
   EdgeIn<LIN> cur, nxt;
   M2Stage stg;
-  load_w<LIN, true>(w + (int64_t)gb * WN + u, cur.w);
+  load_w<LIN, true, WT>(w + (int64_t)gb * WN + u, cur.w);
   load_x<LIN>(up + (int64_t)sender[gb] * DIN + u, cur.x0, cur.x1, cur.x2);
   if constexpr (STAGE) {
     stg.load(Mt + (int64_t)gb * mts + MT_M2, lane);
@@ -402,7 +404,7 @@ __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __rest
 #pragma unroll 1
   for (int e = gb; e < ge; ++e) {
     if (e + 1 < ge) {
-      load_w<LIN, true>(w + (int64_t)(e + 1) * WN + u, nxt.w);
+      load_w<LIN, true, WT>(w + (int64_t)(e + 1) * WN + u, nxt.w);
       load_x<LIN>(up + (int64_t)sender[e + 1] * DIN + u, nxt.x0, nxt.x1, nxt.x2);
       if constexpr (STAGE) stg.load(Mt + (int64_t)(e + 1) * mts + MT_M2, lane);
     }
@@ -478,20 +480,21 @@ __global__ void __launch_bounds__(256) k_tp_tables(int64_t E, int nent, const fl
 // groups per node for each number of input blocks
 constexpr int ng_for(int lin) { return lin == 1 ? 2 : 2; }
 
-template <int LIN>
+template <int LIN, typename WT>
 void launch_fwd(hipStream_t st, int N, const int* rowptr, const int* sender, const float* Y, const float* Mt, int mts,
-                const float* w, const float* up, float* M) {
+                const void* w, const float* up, float* M, int half) {
   constexpr int NG = ng_for(LIN);
-  hipLaunchKernelGGL((k_tp_fwd<LIN, NG>), dim3(N), dim3(NC * NG), 0, st, N, rowptr, sender, Y, Mt, mts, w, up, M);
+  hipLaunchKernelGGL((k_tp_fwd<LIN, NG, WT>), dim3(N), dim3(NC * NG), 0, st, N, rowptr, sender, Y, Mt, mts,
+                     static_cast<const WT*>(w), up, M, half);
 }
 
-template <int LIN, bool GX>
+template <int LIN, bool GX, typename WT>
 void launch_recv(hipStream_t st, int N, const int* rowptr, const int* sender, const float* Y, const float* Mt,
-                 int mts, const float* w, const float* up, const float* gM, float* gw, float* gY, int accumulate_gY,
+                 int mts, const void* w, const float* up, const float* gM, float* gw, float* gY, int accumulate_gY,
                  const int* pos_s, float* gxe) {
   constexpr int NG = ng_for(LIN);
-  hipLaunchKernelGGL((k_tp_bwd_recv<LIN, NG, GX>), dim3(N), dim3(NC * NG), 0, st, N, rowptr, sender, Y, Mt, mts, w,
-                     up, gM, gw, gY, accumulate_gY, pos_s, gxe);
+  hipLaunchKernelGGL((k_tp_bwd_recv<LIN, NG, GX, WT>), dim3(N), dim3(NC * NG), 0, st, N, rowptr, sender, Y, Mt,
+                     mts, static_cast<const WT*>(w), up, gM, gw, gY, accumulate_gY, pos_s, gxe);
 }
 
 }  // namespace
@@ -506,20 +509,27 @@ void launch_tp_tables(hipStream_t st, int64_t E, int max_lin, const float* Y, fl
 }
 
 void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int* sender, const float* Y,
-                   const float* Mt, int mts, const float* w, const float* up, float* M) {
+                   const float* Mt, int mts, const void* w, const float* up, float* M, int half) {
   if (N <= 0) return;
+#define MACE_FWD(L)                                                        \
+  half ? launch_fwd<L, _Float16>(st, N, rowptr, sender, Y, Mt, mts, w, up, M, half) \
+       : launch_fwd<L, float>(st, N, rowptr, sender, Y, Mt, mts, w, up, M, half)
   switch (lin) {
-    case 1: launch_fwd<1>(st, N, rowptr, sender, Y, Mt, mts, w, up, M); break;
-    case 2: launch_fwd<2>(st, N, rowptr, sender, Y, Mt, mts, w, up, M); break;
-    case 3: launch_fwd<3>(st, N, rowptr, sender, Y, Mt, mts, w, up, M); break;
+    case 1: MACE_FWD(1); break;
+    case 2: MACE_FWD(2); break;
+    case 3: MACE_FWD(3); break;
   }
+#undef MACE_FWD
 }
 
 void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const int* sender, const float* Y,
-                        const float* Mt, int mts, const float* w, const float* up, const float* gM, float* gw,
-                        float* gY, int accumulate_gY, const int* pos_s, float* gxe) {
+                        const float* Mt, int mts, const void* w, const float* up, const float* gM, float* gw,
+                        float* gY, int accumulate_gY, const int* pos_s, float* gxe, int half) {
   if (N <= 0) return;
-#define MACE_RECV(L, G) launch_recv<L, G>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gY, accumulate_gY, pos_s, gxe)
+#define MACE_RECV(L, G)                                                                                          \
+  half ? launch_recv<L, G, _Float16>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gY, accumulate_gY, pos_s, \
+                                     gxe)                                                                        \
+       : launch_recv<L, G, float>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gY, accumulate_gY, pos_s, gxe)
   const bool gx = gxe != nullptr;
   switch (lin) {
     case 1: gx ? MACE_RECV(1, true) : MACE_RECV(1, false); break;

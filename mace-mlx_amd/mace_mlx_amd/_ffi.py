@@ -49,6 +49,7 @@ class ModelDims(ctypes.Structure):
         ("correlation", ctypes.c_int32 * 4), ("has_zbl", ctypes.c_int32), ("zbl_p", ctypes.c_int32),
         ("r_max", ctypes.c_double), ("zbl_a_exp", ctypes.c_double),
         ("zbl_a_prefactor", ctypes.c_double), ("zbl_scale", ctypes.c_double),
+        ("feature_half", ctypes.c_int32),
     ]
 
 

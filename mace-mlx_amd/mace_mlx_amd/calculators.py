@@ -125,8 +125,8 @@ class MACEHIPCalculator(_AseCalculator):
             warnings.warn("the HIP engine computes in float32; falling back from float64 "
                           "(results differ from float64 at the float32 precision level)")
             default_dtype = "float32"
-        if default_dtype != "float32":
-            raise NotImplementedError(f"default_dtype={default_dtype!r} (float32 is implemented)")
+        if default_dtype not in ("float32", "float16"):
+            raise NotImplementedError(f"default_dtype={default_dtype!r} (float32 and float16 are implemented)")
         dev = _DEVICE_MAP.get(str(device).split(":")[0], device)
         if dev != "gpu":
             raise NotImplementedError(f"device={device!r}: this engine runs on AMD GPUs only")
@@ -140,7 +140,8 @@ class MACEHIPCalculator(_AseCalculator):
             raise ValueError(f"Head '{head}' not found in model heads: {self.config.heads}")
         self._head = head
         weights = load_weights(model_dir)
-        self._dm = build_device_model(self.config, weights)
+        self._dm = build_device_model(self.config, weights, dtype=default_dtype)
+        self.default_dtype = default_dtype
         self.r_max = float(self.config.r_max)
         self.z_table = list(self._dm.z_table)
         self._z_to_idx = {int(z): i for i, z in enumerate(self.z_table)}

@@ -58,7 +58,27 @@ class DeviceModel:
     r_max: float
 
 
-def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray]) -> DeviceModel:
+# Arrays the reference keeps in float32 when the model runs in float16
+# (`model.py:627-647` _pin_float32): baseline energies and Bessel frequencies
+# (covalent radii are tables, never model weights).
+FP32_PINNED = ("atomic_energies_fn.atomic_energies", "radial_embedding.bessel_fn.bessel_weights")
+
+
+def round_weights_fp16(w: Dict[str, np.ndarray]) -> Dict[str, np.ndarray]:
+    """The weights of a float16 model (`model.py:705-711`: set_dtype, then re-pin): every
+    floating array rounded to fp16 except FP32_PINNED."""
+    return {k: (np.asarray(v) if k in FP32_PINNED else
+                np.asarray(v, dtype=np.float32).astype(np.float16).astype(np.float64))
+            for k, v in w.items()}
+
+
+def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = "float32") -> DeviceModel:
+    """Fold a model (config + reference-layout weights) into the engine's tensors.  dtype
+    "float16" selects the reference's half-precision feature policy."""
+    if dtype not in ("float32", "float16"):
+        raise UnsupportedModel(f"dtype={dtype!r} (float32 and float16 are implemented)")
+    if dtype == "float16":
+        w = round_weights_fp16(w)
     cfg.check_supported()
     if cfg.model_type not in ("MACE", "ScaleShiftMACE"):
         raise UnsupportedModel(f"model_type={cfg.model_type}")
@@ -92,7 +112,8 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray]) -> DeviceMode
                 num_poly_cutoff=cfg.num_polynomial_cutoff, num_layers=n_layers, radial_hidden=64,
                 radial_depth=3, layer_in_blocks=[0] * 4, layer_hid_blocks=[0] * 4, correlation=[0] * 4,
                 has_zbl=int(bool(cfg.pair_repulsion)), zbl_p=6, r_max=float(cfg.r_max),
-                zbl_a_exp=0.3, zbl_a_prefactor=0.4543, zbl_scale=scale)
+                zbl_a_exp=0.3, zbl_a_prefactor=0.4543, zbl_scale=scale,
+                feature_half=int(dtype == "float16"))
     if cfg.pair_repulsion:
         dims["zbl_p"] = int(cfg.pair_repulsion.get("p", 6))
         dims["zbl_a_exp"] = float(cfg.pair_repulsion.get("a_exp", 0.3))

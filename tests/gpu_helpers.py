@@ -6,7 +6,7 @@ import numpy as np
 import torch
 
 from mace_mlx_amd._ffi import Engine
-from mace_mlx_amd.device_model import build_device_model
+from mace_mlx_amd.device_model import build_device_model, round_weights_fp16
 from mace_mlx_amd.model_io import random_init
 from oracle.model import OracleMACE
 from oracle.neighbors import neighbor_list
@@ -20,12 +20,15 @@ def species_of(dm, numbers):
 
 
 class Case:
-    """Engine + oracle for one (model config, seed)."""
+    """Engine + oracle for one (model config, seed, feature dtype).  For "float16" the
+    oracle evaluates the same half-precision model (weights rounded to fp16 except the
+    pinned ones) in float64, i.e. without the feature-path roundings."""
 
-    def __init__(self, cfg, seed=0):
+    def __init__(self, cfg, seed=0, dtype="float32"):
         self.cfg = cfg
         self.w = random_init(cfg, seed)
-        self.dm = build_device_model(cfg, self.w)
+        self.w_model = round_weights_fp16(self.w) if dtype == "float16" else self.w
+        self.dm = build_device_model(cfg, self.w, dtype=dtype)
         self.eng = Engine(0)
         self.eng.load_model(self.dm)
         self._oracle = None
@@ -33,7 +36,7 @@ class Case:
     @property
     def oracle(self):
         if self._oracle is None:
-            self._oracle = OracleMACE(cfg=self.cfg, weights=self.w, dtype=torch.float64)
+            self._oracle = OracleMACE(cfg=self.cfg, weights=self.w_model, dtype=torch.float64)
         return self._oracle
 
     def run(self, s, stress=False, skin=0.5, force_nl=False):

@@ -87,3 +87,28 @@ def test_unsupported_topologies_raise():
     bad2 = ModelConfig.from_dict({**cfg.to_dict(), "use_density_normalization": True})
     with pytest.raises(NotImplementedError):
         build_device_model(bad2, w)
+
+
+def test_float16_policy_rounds_all_but_pinned_weights():
+    """float16 models (`model.py:705-711`): every weight array becomes fp16 except the
+    atomic energies and the Bessel frequencies (`_pin_float32`, `model.py:627-647`)."""
+    from mace_mlx_amd.device_model import FP32_PINNED, round_weights_fp16
+    cfg = arch_config("medium")
+    w = random_init(cfg, 0)
+    w16 = round_weights_fp16(w)
+    assert set(w16) == set(w)
+    for k, v in w16.items():
+        v = np.asarray(v, dtype=np.float64)
+        if k in FP32_PINNED:
+            np.testing.assert_array_equal(v, np.asarray(w[k], dtype=np.float64))
+        else:
+            np.testing.assert_array_equal(v, v.astype(np.float16).astype(np.float64))
+    bessel = "radial_embedding.bessel_fn.bessel_weights"
+    assert not np.array_equal(np.asarray(w[bessel]).astype(np.float16).astype(np.float64), np.asarray(w[bessel]))
+    dm16 = build_device_model(cfg, w, dtype="float16")
+    dm_r = build_device_model(cfg, w16, dtype="float32")
+    assert dm16.dims["feature_half"] == 1 and dm_r.dims["feature_half"] == 0
+    for k in dm16.tensors:   # the half model is the float32 fold of the rounded weights
+        np.testing.assert_array_equal(dm16.tensors[k], dm_r.tensors[k])
+    with pytest.raises(UnsupportedModel):
+        build_device_model(cfg, w, dtype="bfloat16")
