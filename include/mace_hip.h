@@ -130,6 +130,15 @@ int mace_set_profiling(mace_ctx* ctx, int32_t enable);
 int mace_get_kernel_times(mace_ctx* ctx, char* names, int64_t names_len, double* total_ms,
                           int64_t* counts, int32_t capacity, int32_t* n_sites);
 
+/* Step replay through HIP graphs (default on).  The forward and the backward
+ * launches of a step are captured once per (positions, output, stress) binding
+ * and neighbour-list / buffer state, then replayed with one hipGraphLaunch
+ * each; any rebuild or reallocation discards them.  Profiling mode always runs
+ * eagerly.  Results are identical either way (the kernels are deterministic).
+ * No counterpart in the reference (its analogue is mx.compile,
+ * calculators.py:424-453). */
+int mace_set_graphs(mace_ctx* ctx, int32_t enable);
+
 /* Timing of the last mace_step (device milliseconds, HIP events on the
  * context's stream): [0] whole step, [1] neighbour list (0 if cached),
  * [2] forward, [3] backward.  Returns the number of values written. */

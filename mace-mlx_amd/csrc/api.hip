@@ -136,6 +136,15 @@ struct mace_ctx {
   hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
   double timings[4] = {0, 0, 0, 0};
   bool last_nl = false;
+  // captured step graphs (forward, backward) and what they were captured for
+  struct StepGraph {
+    hipGraphExec_t exec = nullptr;
+    const void* a = nullptr;
+    const void* b = nullptr;
+    int flag = 0;
+  };
+  bool use_graphs = true;
+  StepGraph g_fwd, g_bwd;
   // per-launch-site profiling
   bool profiling = false;
   std::vector<hipEvent_t> ev_pool;
@@ -241,6 +250,8 @@ std::vector<float> transpose(const std::vector<float>& a, int rows, int cols, in
   return t;
 }
 
+void invalidate_graphs(mace_ctx* c);
+
 void free_layers(mace_ctx* c) {
   for (auto& L : c->layers) {
     for (auto* arr : {L.up, L.upT, L.skip, L.skipT, L.sc, L.plin, L.plinT})
@@ -253,6 +264,7 @@ void free_layers(mace_ctx* c) {
 }
 
 void build_model(mace_ctx* c) {
+  invalidate_graphs(c);
   const auto& d = c->dims;
   const int C = NC;
   if (d.num_channels != NC) fail(MACE_ERR_UNSUPPORTED, "num_channels=%d (compiled for %d)", d.num_channels, NC);
@@ -343,6 +355,7 @@ void build_model(mace_ctx* c) {
 // buffers
 // ---------------------------------------------------------------------------
 void ensure_node_buffers(mace_ctx* c) {
+  invalidate_graphs(c);
   const int N = std::max(c->N, 1);
   const int L = (int)c->layers.size();
   c->h.resize(L + 1);
@@ -381,6 +394,7 @@ void ensure_node_buffers(mace_ctx* c) {
 }
 
 void ensure_edge_buffers(mace_ctx* c, int64_t E) {
+  invalidate_graphs(c);
   const size_t e = (size_t)std::max<int64_t>(E, 1);
   int maxw = 0;
   const bool half = c->dims.feature_half != 0;
@@ -569,6 +583,7 @@ NLParams nl_params(mace_ctx* c, const double* pos, double cutoff) {
 }
 
 void build_nl(mace_ctx* c, const double* pos_host) {
+  invalidate_graphs(c);
   const int N = c->N;
   const double cutoff = c->dims.r_max + std::max(c->skin, 0.0);
   NLParams p = nl_params(c, pos_host, cutoff);
@@ -700,6 +715,49 @@ void run_skip_T(mace_ctx* c, Layer& L, int b, const float* gout, int ldg, float*
     launch_linear(c->stream, c->N, D, gout, L.skipT[b].p, gh);
   else
     launch_linear_species(c->stream, c->N, D, gout, L.skipT[b].p, c->species.p, gh);
+}
+
+// Discard captured step graphs (launch arguments or buffers changed).
+void invalidate_graphs(mace_ctx* c) {
+  for (auto* g : {&c->g_fwd, &c->g_bwd}) {
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    *g = mace_ctx::StepGraph{};
+  }
+}
+
+// Run body() (a sequence of launches on c->stream) through a graph captured
+// for the binding (a, b, flag), capturing it first if needed; eager when
+// graphs are off or per-launch profiling is on.
+template <class F>
+void run_captured(mace_ctx* c, mace_ctx::StepGraph& g, const void* a, const void* b, int flag, F&& body) {
+  if (!c->use_graphs || c->profiling) {
+    body();
+    return;
+  }
+  if (!g.exec || g.a != a || g.b != b || g.flag != flag) {
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    g = mace_ctx::StepGraph{};
+    hipGraph_t graph = nullptr;
+    HIPCHK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    try {
+      body();
+    } catch (...) {
+      (void)hipStreamEndCapture(c->stream, &graph);
+      if (graph) (void)hipGraphDestroy(graph);
+      throw;
+    }
+    HIPCHK(hipStreamEndCapture(c->stream, &graph));
+    const hipError_t e = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) {
+      g.exec = nullptr;
+      fail(MACE_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    }
+    g.a = a;
+    g.b = b;
+    g.flag = flag;
+  }
+  HIPCHK(hipGraphLaunch(g.exec, c->stream));
 }
 
 void forward(mace_ctx* c, const double* pos, double* out) {
@@ -948,6 +1006,7 @@ int mace_create(int32_t device, mace_ctx** out) {
 }
 
 static void free_all(mace_ctx* c) {
+  invalidate_graphs(c);
   free_layers(c);
   for (auto& b : c->h) b.release();
   c->h3h.release();
@@ -1129,9 +1188,9 @@ int mace_step(mace_ctx* c, const double* positions, uint32_t flags, double* ener
     c->last_nl = rebuild && !c->edges_manual;
     if (c->last_nl) build_nl(c, positions);
     HIPCHK(hipEventRecord(c->ev[1], st));
-    forward(c, c->pos.p, c->out.p);
+    run_captured(c, c->g_fwd, c->pos.p, c->out.p, 0, [&] { forward(c, c->pos.p, c->out.p); });
     HIPCHK(hipEventRecord(c->ev[2], st));
-    backward(c, stress, c->out.p);
+    run_captured(c, c->g_bwd, c->out.p, nullptr, stress, [&] { backward(c, stress, c->out.p); });
     HIPCHK(hipEventRecord(c->ev[3], st));
     HIPCHK(hipMemcpyAsync(c->out_pinned, c->out.p, (10 + 3 * (size_t)N) * sizeof(double), hipMemcpyDeviceToHost, st));
     if (node_energy && N > 0)
@@ -1173,8 +1232,18 @@ int mace_step_device(mace_ctx* c, const double* d_positions, uint32_t flags, dou
       c->edges_manual = false;
       build_nl(c, host.data());
     }
-    forward(c, d_positions, d_out);
-    backward(c, (flags & MACE_STEP_STRESS) != 0, d_out);
+    const bool stress = (flags & MACE_STEP_STRESS) != 0;
+    run_captured(c, c->g_fwd, d_positions, d_out, 0, [&] { forward(c, d_positions, d_out); });
+    run_captured(c, c->g_bwd, d_out, nullptr, stress, [&] { backward(c, stress, d_out); });
+  });
+}
+
+int mace_set_graphs(mace_ctx* c, int32_t enable) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    set_device(c);
+    c->use_graphs = enable != 0;
+    if (!c->use_graphs) invalidate_graphs(c);
   });
 }
 

@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "mace_create", "mace_destroy", "mace_last_error", "mace_model_begin", "mace_model_set_tensor",
     "mace_model_end", "mace_set_system", "mace_step", "mace_set_edges", "mace_get_edges",
     "mace_get_timings", "mace_step_device", "mace_sync", "mace_set_profiling", "mace_get_kernel_times",
+    "mace_set_graphs",
 )
 
 
@@ -82,6 +83,7 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
         "mace_step_device": (ctypes.c_int, [P, P, U32, P]),
         "mace_sync": (ctypes.c_int, [P]),
         "mace_set_profiling": (ctypes.c_int, [P, I32]),
+        "mace_set_graphs": (ctypes.c_int, [P, I32]),
         "mace_get_kernel_times": (ctypes.c_int, [P, ctypes.c_char_p, I64, P, P, I32, ctypes.POINTER(I32)]),
     }
     for name, (res, args) in sig.items():
@@ -203,6 +205,10 @@ class Engine:
 
     def set_profiling(self, enable: bool) -> None:
         self._check(self._lib.mace_set_profiling(self._h, int(bool(enable))))
+
+    def set_graphs(self, enable: bool) -> None:
+        """Replay steps through captured HIP graphs (default) or launch them eagerly."""
+        self._check(self._lib.mace_set_graphs(self._h, int(bool(enable))))
 
     def kernel_times(self) -> dict:
         """{site: (total_ms, launches)} accumulated since the last call."""
