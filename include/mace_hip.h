@@ -67,6 +67,15 @@ typedef struct mace_model_dims {
                                 SH and radial features and every stored activation of the
                                 feature path rounded to fp16, TP weights held in fp16,
                                 accumulation in fp32; 0: float32 throughout               */
+  int32_t density_norm;      /* 1: density-normalised interactions (blocks.py:282-490):
+                                tensor L<l>.dens, message linear / (1 + sum tanh((ef.w)^2)) */
+  int32_t first_nonresidual; /* 1: first interaction without residual skip; its skip FCTP
+                                acts on the message (blocks.py:68-176): tensors L0.mskip.<l> */
+  int32_t agnesi;            /* 1: Agnesi distance transform before the Bessel basis
+                                (radial.py:207-262): tensor agnesi_cov (radius per element) */
+  double agnesi_q;
+  double agnesi_p;
+  double agnesi_a;
 } mace_model_dims;
 
 /* Context lifetime.  device = HIP device ordinal. */

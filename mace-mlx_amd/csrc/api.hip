@@ -79,9 +79,12 @@ struct Layer {
   DBuf<float> up[3], upT[3], skip[3], skipT[3], mlp[4], mlpT[4], lin_[4], linT[4], sc[3], plin[3], plinT[3];
   DBuf<float> ro, ro1, ro2;
   DBuf<_Float16> mlpT3h;  // fp16 copy of W3^T (float16 feature policy)
+  bool resid = true;       // residual block (skip from the input); else the skip acts on the message
+  DBuf<float> mskip[4], mskipT[4], dens;
   int nskip = 0;
   // per-step activations (TP weights: w, or wh under the float16 feature policy)
   DBuf<float> h_up, A, w, ro_e;
+  DBuf<float> A2, rinv;  // message after its skip FCTP (non-residual block); 1 / (1 + density)
   DBuf<_Float16> wh;
   const void* wptr(bool half) const { return half ? static_cast<const void*>(wh.p) : static_cast<const void*>(w.p); }
 };
@@ -99,7 +102,8 @@ struct mace_ctx {
   std::vector<Layer> layers;
   int max_lin = 1;
   int mts = 0;  // row stride of the per-edge TP tables Mt (0: no layer has l1 >= 1 inputs)
-  DBuf<float> e0, bessel_w, zbl_z, zbl_cov, embed;
+  DBuf<float> e0, bessel_w, zbl_z, zbl_cov, ag_cov, embed;
+  DBuf<float> gA2, grho;  // backward scratch of the message skip / density normalisation
   // system
   int N = 0;
   std::vector<int> species_h;
@@ -258,7 +262,8 @@ void free_layers(mace_ctx* c) {
       for (int i = 0; i < 3; ++i) arr[i].release();
     for (int i = 0; i < 4; ++i) L.mlp[i].release(), L.mlpT[i].release(), L.lin_[i].release(), L.linT[i].release();
     L.ro.release(), L.ro1.release(), L.ro2.release(), L.h_up.release(), L.A.release(), L.w.release(),
-        L.ro_e.release(), L.wh.release(), L.mlpT3h.release();
+        L.ro_e.release(), L.wh.release(), L.mlpT3h.release(), L.A2.release(), L.rinv.release(), L.dens.release();
+    for (int i = 0; i < 4; ++i) L.mskip[i].release(), L.mskipT[i].release();
   }
   c->layers.clear();
 }
@@ -283,6 +288,7 @@ void build_model(mace_ctx* c) {
     upload(c, c->zbl_z, tensor(c, "zbl_z", nel));
     upload(c, c->zbl_cov, tensor(c, "zbl_cov", nel));
   }
+  if (d.agnesi) upload(c, c->ag_cov, tensor(c, "agnesi_cov", nel));
   free_layers(c);
   c->layers.resize(d.num_layers);
   for (int l = 0; l < d.num_layers; ++l) {
@@ -306,12 +312,20 @@ void build_model(mace_ctx* c) {
       upload(c, L.up[b], w);
       upload(c, L.upT[b], transpose(w, C, C));
     }
-    L.nskip = std::min(L.lin, L.lhid);
+    L.resid = !(l == 0 && d.first_nonresidual);
+    L.nskip = L.resid ? std::min(L.lin, L.lhid) : 0;
     for (int b = 0; b < L.nskip; ++b) {
       const auto& w = tensor(c, p + "skip." + std::to_string(b), (size_t)nel * C * C);
       upload(c, L.skip[b], w);
       upload(c, L.skipT[b], transpose(w, C, C, nel));
     }
+    if (!L.resid)
+      for (int lo = 0; lo < 4; ++lo) {
+        const auto& w = tensor(c, p + "mskip." + std::to_string(lo), (size_t)nel * C * C);
+        upload(c, L.mskip[lo], w);
+        upload(c, L.mskipT[lo], transpose(w, C, C, nel));
+      }
+    if (d.density_norm) upload(c, L.dens, tensor(c, p + "dens", nb));
     {
       const int rows[4] = {nb, RADIAL_H, RADIAL_H, RADIAL_H};
       const int cols[4] = {RADIAL_H, RADIAL_H, RADIAL_H, L.wn};
@@ -366,6 +380,8 @@ void ensure_node_buffers(mace_ctx* c) {
     ly.h_up.ensure((size_t)N * ly.din);
     ly.A.ensure((size_t)N * ly.dint);
     ly.ro_e.ensure(N);
+    if (!ly.resid) ly.A2.ensure((size_t)N * ly.dint);
+    if (c->dims.density_norm) ly.rinv.ensure(N);
     maxd = std::max({maxd, ly.dmid, ly.din, ly.dhid});
   }
   c->h[L].ensure((size_t)N * c->layers[L - 1].dhid);
@@ -377,6 +393,8 @@ void ensure_node_buffers(mace_ctx* c) {
   c->gh0.ensure((size_t)N * maxd);
   c->gh1.ensure((size_t)N * maxd);
   c->gup.ensure((size_t)N * maxd);
+  c->gA2.ensure((size_t)N * maxd);
+  c->grho.ensure(N);
   c->ypre.ensure((size_t)N * 16);
   c->node_e.ensure(N);
   c->e_part.ensure((N + 255) / 256 + 1);
@@ -694,6 +712,10 @@ FrontParams front_params(mace_ctx* c) {
   p.zbl_a_pref = (float)c->dims.zbl_a_prefactor;
   p.zbl_scale = (float)c->dims.zbl_scale;
   p.feature_half = c->dims.feature_half != 0;
+  p.agnesi = c->dims.agnesi != 0;
+  p.ag_q = (float)c->dims.agnesi_q;
+  p.ag_p = (float)c->dims.agnesi_p;
+  p.ag_a = (float)c->dims.agnesi_a;
   return p;
 }
 
@@ -706,6 +728,19 @@ void run_skip(mace_ctx* c, Layer& L, int b, const float* h, float* out, int ldo,
     launch_linear(c->stream, c->N, D, h, L.skip[b].p, out);
   else
     launch_linear_species(c->stream, c->N, D, h, L.skip[b].p, c->species.p, out);
+}
+
+// Message skip FCTP of a non-residual block (blocks.py:171-176): per interaction block lo,
+// out[n][lo] = in[n][lo] W_lo[species(n)] (W given per element, pw and CG folded).
+void run_msg_skip(mace_ctx* c, Layer& L, const float* in, float* out, const DBuf<float>* W, int half) {
+  for (int lo = 0; lo < 4; ++lo) {
+    LinearDesc D = lin_desc(2 * lo + 1, NC, NC, L.dint, NC * lo * lo, 0, L.dint, NC * lo * lo, 0, 0);
+    D.round_half = half;
+    if (c->dims.num_elements == 1)
+      launch_linear(c->stream, c->N, D, in, W[lo].p, out);
+    else
+      launch_linear_species(c->stream, c->N, D, in, W[lo].p, c->species.p, out);
+  }
 }
 
 void run_skip_T(mace_ctx* c, Layer& L, int b, const float* gout, int ldg, float* gh) {
@@ -770,7 +805,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
   {
     Site s(c, "edge_fwd");
     launch_edge_fwd(st, E, pos, c->sender.p, c->receiver.p, c->shifts.p, c->species.p, c->bessel_w.p, c->zbl_z.p,
-                    c->zbl_cov.p, fp, c->geom.p, c->Y.p, c->ef.p, c->zbl_e.p);
+                    c->zbl_cov.p, c->ag_cov.p, fp, c->geom.p, c->Y.p, c->ef.p, c->zbl_e.p);
   }
   if (c->mts > 0) {
     Site s(c, "tp_tables");
@@ -810,6 +845,10 @@ void forward(mace_ctx* c, const double* pos, double* out) {
                     half);
     }
     const int* ao = tp_accoff(L.lin);
+    if (c->dims.density_norm) {
+      Site s(c, lname("density", l));
+      launch_density_fwd(st, N, c->rowptr.p, c->ef.p, nb, L.dens.p, L.rinv.p);
+    }
     {
       Site s(c, lname("linear_msg", l));
       GemmGroup g{};
@@ -820,13 +859,19 @@ void forward(mace_ctx* c, const double* pos, double* out) {
         const int d = 2 * lo + 1;
         g.p[g.n++] = gprob(N, d, cnt * NC, NC, c->M.p, L.dmid, NC * ao[first], NC * d, L.linT[lo].p, L.A.p, L.dint,
                            NC * lo * lo, 0);
+        if (c->dims.density_norm) g.p[g.n - 1].rowscale = L.rinv.p;
       }
       launch_gemm_group(st, g);
     }
+    if (!L.resid) {  // non-residual block: species-dependent skip FCTP on the message
+      Site s(c, lname("message_skip", l));
+      run_msg_skip(c, L, L.A.p, L.A2.p, L.mskip, half);
+    }
+    const float* sc_in = L.resid ? L.A.p : L.A2.p;
     const float* scw[3] = {L.sc[0].p, L.sc[1].p, L.sc[2].p};
     {
       Site s(c, lname("sc_fwd", l));
-      launch_sc_fwd(st, N, L.lhid, L.corr, L.A.p, L.dint, c->species.p, scw, c->B.p, L.dhid, half);
+      launch_sc_fwd(st, N, L.lhid, L.corr, sc_in, L.dint, c->species.p, scw, c->B.p, L.dhid, half);
     }
     const bool one_el = c->dims.num_elements == 1;
     {
@@ -895,7 +940,19 @@ void backward(mace_ctx* c, bool stress, double* out) {
     const float* scw[3] = {Ly.sc[0].p, Ly.sc[1].p, Ly.sc[2].p};
     {
       Site s(c, lname("sc_bwd", l));
-      launch_sc_bwd(st, N, Ly.lhid, Ly.corr, Ly.A.p, Ly.dint, c->species.p, scw, c->gB.p, Ly.dhid, c->gA.p);
+      launch_sc_bwd(st, N, Ly.lhid, Ly.corr, Ly.resid ? Ly.A.p : Ly.A2.p, Ly.dint, c->species.p, scw, c->gB.p,
+                    Ly.dhid, c->gA.p);
+    }
+    // gradient of the (normalised) message linear's output
+    const float* gmsg = c->gA.p;
+    if (!Ly.resid) {
+      Site s(c, lname("message_skip_bwd", l));
+      run_msg_skip(c, Ly, c->gA.p, c->gA2.p, Ly.mskipT, 0);
+      gmsg = c->gA2.p;
+    }
+    if (c->dims.density_norm) {
+      Site s(c, lname("density_bwd", l));
+      launch_density_node_bwd(st, N, Ly.dint, gmsg, Ly.A.p, Ly.rinv.p, c->grho.p);
     }
     const int* ao = tp_accoff(Ly.lin);
     {
@@ -905,8 +962,9 @@ void backward(mace_ctx* c, bool stress, double* out) {
         int first, cnt;
         slot_range(Ly, lo, &first, &cnt);
         const int d = 2 * lo + 1;
-        g.p[g.n++] = gprob(N, d, NC, cnt * NC, c->gA.p, Ly.dint, NC * lo * lo, 0, Ly.lin_[lo].p, c->gM.p, Ly.dmid,
+        g.p[g.n++] = gprob(N, d, NC, cnt * NC, gmsg, Ly.dint, NC * lo * lo, 0, Ly.lin_[lo].p, c->gM.p, Ly.dmid,
                            NC * ao[first], NC * d);
+        if (c->dims.density_norm) g.p[g.n - 1].rowscale = Ly.rinv.p;
       }
       launch_gemm_group(st, g);
     }
@@ -930,6 +988,10 @@ void backward(mace_ctx* c, bool stress, double* out) {
       Site s(c, lname("mlp_hidden_bwd", l));
       launch_mlp_hidden_bwd(st, E, nb, c->ef.p, Ly.mlp[0].p, Ly.mlp[1].p, Ly.mlp[2].p, c->h3.p, c->gef.p,
                             first_edge_grad, half);
+    }
+    if (c->dims.density_norm) {  // edge densities' share of dL/def (after gef has been written)
+      Site s(c, lname("density_edge_bwd", l));
+      launch_density_edge_bwd(st, E, c->receiver.p, c->ef.p, nb, Ly.dens.p, c->grho.p, c->gef.p);
     }
     if (l > 0) {
       // dE/dh_l = Up^T gup + Skip^T gh + readout_{l-1}'
@@ -965,7 +1027,8 @@ void backward(mace_ctx* c, bool stress, double* out) {
   const int nblk = (int)((E + 255) / 256);
   {
     Site s(c, "edge_bwd");
-    launch_edge_bwd(st, E, c->sender.p, c->receiver.p, c->species.p, c->bessel_w.p, c->zbl_z.p, c->zbl_cov.p, fp,
+    launch_edge_bwd(st, E, c->sender.p, c->receiver.p, c->species.p, c->bessel_w.p, c->zbl_z.p, c->zbl_cov.p,
+                    c->ag_cov.p, fp,
                     c->geom.p, c->gY.p, c->gef.p, c->gv.p, stress ? c->vir_part.p : nullptr, nblk);
   }
   {
@@ -1010,7 +1073,7 @@ static void free_all(mace_ctx* c) {
   free_layers(c);
   for (auto& b : c->h) b.release();
   c->h3h.release();
-  for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->embed, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
+  for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->ag_cov, &c->gA2, &c->grho, &c->embed, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
                   &c->gv, &c->gw, &c->gxe, &c->h3, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup, &c->ypre,
                   &c->node_e})
     b->release();

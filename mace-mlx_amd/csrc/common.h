@@ -39,20 +39,33 @@ struct FrontParams {
   float zbl_a_pref;
   float zbl_scale;
   int feature_half;      // float16 feature policy: SH and radial features rounded to fp16
+  int agnesi;            // Agnesi distance transform of r before the Bessel basis
+  float ag_q, ag_p, ag_a;
 };
 
 // x rounded to the nearest fp16 value when `half` (the stored activations of a
 // model run under the float16 feature policy), else x
 __device__ __forceinline__ float qh(float x, bool half) { return half ? (float)(_Float16)x : x; }
+// ag_cov: covalent radius per species for the Agnesi transform (unused without it)
 void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* sender,
                      const int* receiver, const int* shifts, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov,
-                     const FrontParams& p, EdgeGeom* geom, float* Y, float* ef, float* zbl_e);
+                     const float* ag_cov, const FrontParams& p, EdgeGeom* geom, float* Y, float* ef,
+                     float* zbl_e);
 void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver,
                      const int* species, const float* bessel_w, const float* zbl_z,
-                     const float* zbl_cov, const FrontParams& p, const EdgeGeom* geom,
-                     const float* gY, const float* gef, float* gv, double* vir_part,
-                     int nblk_vir);
+                     const float* zbl_cov, const float* ag_cov, const FrontParams& p,
+                     const EdgeGeom* geom, const float* gY, const float* gef, float* gv,
+                     double* vir_part, int nblk_vir);
+// density normalisation (blocks.py:372-380): rinv[n] = 1 / (1 + sum_{e -> n} tanh((ef_e . wd)^2))
+void launch_density_fwd(hipStream_t st, int N, const int* rowptr, const float* ef, int nb,
+                        const float* wd, float* rinv);
+// grho[n] = -rinv[n] * sum_j gA[n][j] A[n][j]  (A: the normalised message, dint values per node)
+void launch_density_node_bwd(hipStream_t st, int N, int dint, const float* gA, const float* A,
+                             const float* rinv, float* grho);
+// gef[e] += grho[recv(e)] * d tanh((ef_e . wd)^2) / d ef_e
+void launch_density_edge_bwd(hipStream_t st, int64_t E, const int* receiver, const float* ef, int nb,
+                             const float* wd, const float* grho, float* gef);
 
 // radial MLP, ef (E x nb) -> w (E x W); weights [in][out] row-major, W3T = W3 transposed [W][64].
 // h3 [E][64] = silu(silu(silu(ef W0) W1) W2); w = h3 W3.  half (float16 feature policy): hidden
@@ -116,6 +129,7 @@ struct GemmProb {
   float* Y;
   int ldy, out_base, out_stride;
   const float* bias;
+  const float* rowscale;  // optional per-node factor on the product (before bias / accumulate)
   int accumulate;
   int tiles_n, tile_begin;
 };

@@ -56,11 +56,23 @@ __device__ __forceinline__ float zbl_phi(float x, float* dphi) {
   return 0.1818f * e0 + 0.5099f * e1 + 0.2802f * e2 + 0.02817f * e3;
 }
 
+// Agnesi transform (radial.py:231-262): t = 1 / (1 + a x^q / (1 + x^(q-p))),
+// x = r / r0; returns t and dt/dr.
+__device__ __forceinline__ float agnesi_t(float r, float r0, const FrontParams& p, float* dtdr) {
+  const float x = fmaxf(r / r0, 1e-12f);
+  const float xq = powf(x, p.ag_q), xqp = powf(x, p.ag_q - p.ag_p);
+  const float den = 1.f + xqp;
+  const float t = 1.f / (1.f + p.ag_a * xq / den);
+  const float dfdx = p.ag_a * (p.ag_q * xq * den - (p.ag_q - p.ag_p) * xq * xqp) / (x * den * den);
+  *dtdr = -t * t * dfdx / r0;
+  return t;
+}
+
 __global__ void __launch_bounds__(256) k_edge_fwd(
     int64_t E, const double* __restrict__ pos, const int* __restrict__ sender,
     const int* __restrict__ receiver, const int* __restrict__ shifts, const int* __restrict__ species,
     const float* __restrict__ bessel_w, const float* __restrict__ zbl_z,
-    const float* __restrict__ zbl_cov, FrontParams p, EdgeGeom* __restrict__ geom,
+    const float* __restrict__ zbl_cov, const float* __restrict__ ag_cov, FrontParams p, EdgeGeom* __restrict__ geom,
     float* __restrict__ Y, float* __restrict__ ef, float* __restrict__ zbl_e) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= E) return;
@@ -79,9 +91,14 @@ __global__ void __launch_bounds__(256) k_edge_fwd(
                         qh(Yl[4 * q + 2], p.feature_half), qh(Yl[4 * q + 3], p.feature_half));
   float denv;
   const float env = poly_env(rr / p.r_max, p.pcut, &denv);
+  float rb = rr;  // argument of the Bessel basis
+  if (p.agnesi) {
+    float dtdr;
+    rb = agnesi_t(rr, 0.5f * (ag_cov[species[s]] + ag_cov[species[r]]), p, &dtdr);
+  }
   for (int n = 0; n < p.nbessel; ++n) {
     const float w = bessel_w[n];
-    const float b = (rr == 0.f) ? p.bessel_pref * w : p.bessel_pref * sinf(w * rr) / rr;
+    const float b = (rb == 0.f) ? p.bessel_pref * w : p.bessel_pref * sinf(w * rb) / rb;
     ef[(int64_t)p.nbessel * e + n] = qh(b * env, p.feature_half);
   }
   if (p.has_zbl) {
@@ -100,8 +117,8 @@ __global__ void __launch_bounds__(256) k_edge_fwd(
 __global__ void __launch_bounds__(256) k_edge_bwd(
     int64_t E, const int* __restrict__ sender, const int* __restrict__ receiver,
     const int* __restrict__ species, const float* __restrict__ bessel_w,
-    const float* __restrict__ zbl_z, const float* __restrict__ zbl_cov, FrontParams p,
-    const EdgeGeom* __restrict__ geom, const float* __restrict__ gY, const float* __restrict__ gef,
+    const float* __restrict__ zbl_z, const float* __restrict__ zbl_cov, const float* __restrict__ ag_cov,
+    FrontParams p, const EdgeGeom* __restrict__ geom, const float* __restrict__ gY, const float* __restrict__ gef,
     float* __restrict__ gv, double* __restrict__ vir_part) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   double vir[9];
@@ -136,20 +153,22 @@ __global__ void __launch_bounds__(256) k_edge_bwd(
     // radial part
     float denv;
     const float env = poly_env(rr / p.r_max, p.pcut, &denv);
+    float rb = rr, drb = 1.f;  // Bessel argument and its derivative in r
+    if (p.agnesi) rb = agnesi_t(rr, 0.5f * (ag_cov[species[sender[e]]] + ag_cov[species[receiver[e]]]), p, &drb);
     float gr = 0.f;
     for (int n = 0; n < p.nbessel; ++n) {
       const float w = bessel_w[n];
       float b, db;
-      if (rr == 0.f) {
+      if (rb == 0.f) {
         b = p.bessel_pref * w;
         db = 0.f;
       } else {
         float sn, cs;
-        sincosf(w * rr, &sn, &cs);
-        b = p.bessel_pref * sn / rr;
-        db = p.bessel_pref * (w * cs * rr - sn) / (rr * rr);
+        sincosf(w * rb, &sn, &cs);
+        b = p.bessel_pref * sn / rb;
+        db = p.bessel_pref * (w * cs * rb - sn) / (rb * rb);
       }
-      gr += gef[(int64_t)p.nbessel * e + n] * (db * env + b * denv / p.r_max);
+      gr += gef[(int64_t)p.nbessel * e + n] * (db * drb * env + b * denv / p.r_max);
     }
     if (p.has_zbl) {
       const int zs = species[sender[e]], zr = species[receiver[e]];
@@ -187,6 +206,61 @@ __global__ void __launch_bounds__(256) k_edge_bwd(
     __syncthreads();
   }
   if (threadIdx.x < 9) vir_part[9 * blockIdx.x + threadIdx.x] = red[threadIdx.x][0];
+}
+
+// ---------------------------------------------------------------------------
+// density normalisation (blocks.py:282-490): one wave per node, fixed-order sums
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float edge_density_arg(const float* __restrict__ ef, int nb, const float* __restrict__ wd,
+                                                  int64_t e) {
+  float s = 0.f;
+  for (int k = 0; k < nb; ++k) s = fmaf(ef[e * nb + k], wd[k], s);
+  return s;
+}
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__global__ void __launch_bounds__(256) k_density_fwd(int N, const int* __restrict__ rowptr,
+                                                     const float* __restrict__ ef, int nb,
+                                                     const float* __restrict__ wd, float* __restrict__ rinv) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+  if (n >= N) return;
+  float acc = 0.f;
+  for (int e = rowptr[n] + l; e < rowptr[n + 1]; e += 64) {
+    const float s = edge_density_arg(ef, nb, wd, e);
+    acc += tanhf(s * s);
+  }
+  acc = wave_sum_f(acc);
+  if (l == 0) rinv[n] = 1.f / (1.f + acc);
+}
+
+__global__ void __launch_bounds__(256) k_density_node_bwd(int N, int dint, const float* __restrict__ gA,
+                                                          const float* __restrict__ A, const float* __restrict__ rinv,
+                                                          float* __restrict__ grho) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+  if (n >= N) return;
+  const float* g = gA + (int64_t)n * dint;
+  const float* a = A + (int64_t)n * dint;
+  float acc = 0.f;
+  for (int j = l; j < dint; j += 64) acc = fmaf(g[j], a[j], acc);
+  acc = wave_sum_f(acc);
+  if (l == 0) grho[n] = -rinv[n] * acc;
+}
+
+__global__ void __launch_bounds__(256) k_density_edge_bwd(int64_t E, const int* __restrict__ receiver,
+                                                          const float* __restrict__ ef, int nb,
+                                                          const float* __restrict__ wd, const float* __restrict__ grho,
+                                                          float* __restrict__ gef) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const float s = edge_density_arg(ef, nb, wd, e);
+  const float d = tanhf(s * s);
+  const float c = grho[receiver[e]] * (1.f - d * d) * 2.f * s;
+  for (int k = 0; k < nb; ++k) gef[e * nb + k] += c * wd[k];
 }
 
 // ---------------------------------------------------------------------------
@@ -315,21 +389,39 @@ static inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / 
 
 void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* sender, const int* receiver,
                      const int* shifts, const int* species, const float* bessel_w, const float* zbl_z,
-                     const float* zbl_cov, const FrontParams& p, EdgeGeom* geom, float* Y, float* ef,
-                     float* zbl_e) {
+                     const float* zbl_cov, const float* ag_cov, const FrontParams& p, EdgeGeom* geom, float* Y,
+                     float* ef, float* zbl_e) {
   if (E <= 0) return;
   hipLaunchKernelGGL(k_edge_fwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, pos, sender, receiver, shifts,
-                     species, bessel_w, zbl_z, zbl_cov, p, geom, Y, ef, zbl_e);
+                     species, bessel_w, zbl_z, zbl_cov, ag_cov, p, geom, Y, ef, zbl_e);
 }
 
 void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,
-                     const float* bessel_w, const float* zbl_z, const float* zbl_cov, const FrontParams& p,
-                     const EdgeGeom* geom, const float* gY, const float* gef, float* gv, double* vir_part,
-                     int nblk_vir) {
+                     const float* bessel_w, const float* zbl_z, const float* zbl_cov, const float* ag_cov,
+                     const FrontParams& p, const EdgeGeom* geom, const float* gY, const float* gef, float* gv,
+                     double* vir_part, int nblk_vir) {
   if (E <= 0) return;
   (void)nblk_vir;
   hipLaunchKernelGGL(k_edge_bwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, sender, receiver, species,
-                     bessel_w, zbl_z, zbl_cov, p, geom, gY, gef, gv, vir_part);
+                     bessel_w, zbl_z, zbl_cov, ag_cov, p, geom, gY, gef, gv, vir_part);
+}
+
+void launch_density_fwd(hipStream_t st, int N, const int* rowptr, const float* ef, int nb, const float* wd,
+                        float* rinv) {
+  if (N <= 0) return;
+  hipLaunchKernelGGL(k_density_fwd, dim3(nblk(N, 4)), dim3(256), 0, st, N, rowptr, ef, nb, wd, rinv);
+}
+
+void launch_density_node_bwd(hipStream_t st, int N, int dint, const float* gA, const float* A, const float* rinv,
+                             float* grho) {
+  if (N <= 0) return;
+  hipLaunchKernelGGL(k_density_node_bwd, dim3(nblk(N, 4)), dim3(256), 0, st, N, dint, gA, A, rinv, grho);
+}
+
+void launch_density_edge_bwd(hipStream_t st, int64_t E, const int* receiver, const float* ef, int nb,
+                             const float* wd, const float* grho, float* gef) {
+  if (E <= 0) return;
+  hipLaunchKernelGGL(k_density_edge_bwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, receiver, ef, nb, wd, grho, gef);
 }
 
 void launch_nl_bin(hipStream_t st, int N, const double* pos, const NLParams& p, double* wpos, int* img,

@@ -200,7 +200,7 @@ __global__ void __launch_bounds__(256) k_gemm_group(GemmGroup G) {
       if (ro >= P.rows) continue;
       const int no = ro / P.d, mo = ro - no * P.d;
       float* y = P.Y + (int64_t)no * P.ldy + P.out_base + (col / NC) * P.out_stride + mo * NC + (col % NC);
-      const float v = acc[u][i] + bias;
+      const float v = acc[u][i] * (P.rowscale ? P.rowscale[no] : 1.f) + bias;
       *y = qh(P.accumulate ? *y + v : v, G.round_half);
     }
   }

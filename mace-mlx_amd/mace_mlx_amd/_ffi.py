@@ -50,7 +50,9 @@ class ModelDims(ctypes.Structure):
         ("correlation", ctypes.c_int32 * 4), ("has_zbl", ctypes.c_int32), ("zbl_p", ctypes.c_int32),
         ("r_max", ctypes.c_double), ("zbl_a_exp", ctypes.c_double),
         ("zbl_a_prefactor", ctypes.c_double), ("zbl_scale", ctypes.c_double),
-        ("feature_half", ctypes.c_int32),
+        ("feature_half", ctypes.c_int32), ("density_norm", ctypes.c_int32),
+        ("first_nonresidual", ctypes.c_int32), ("agnesi", ctypes.c_int32),
+        ("agnesi_q", ctypes.c_double), ("agnesi_p", ctypes.c_double), ("agnesi_a", ctypes.c_double),
     ]
 
 

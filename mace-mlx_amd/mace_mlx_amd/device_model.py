@@ -15,9 +15,12 @@ Tensor names (C = channels, n_el = elements, per layer prefix ``L{l}.``):
   zbl_z, zbl_cov [n_el]           atomic number and covalent radius per element
   embed [n_el][C]                 node embedding (one-hot linear, pw folded)
   L.up.b [C][C]                   linear_up, block l=b
-  L.skip.b [n_el][C][C]           skip FCTP for hidden block b (CG * pw folded)
+  agnesi_cov [n_el]               covalent radius per element (Agnesi transform only)
+  L.skip.b [n_el][C][C]           skip FCTP for hidden block b (CG * pw folded; residual blocks)
+  L.mskip.l [n_el][C][C]          message skip FCTP, interaction block l (non-residual first block)
+  L.dens [nb]                     density_fn weights (density-normalised blocks)
   L.mlp.k                         radial MLP layer k, [in][out]
-  L.lin.l [nslots(l)*C][C]        message linear for output l (pw / avg folded)
+  L.lin.l [nslots(l)*C][C]        message linear for output l (pw folded; / avg unless density)
   L.sc.b [n_el][K3+K2+K1][C]      symmetric-contraction weights, output block b
   L.plin.b [C][C]                 product linear
   L.ro [C] | L.ro1 [C][16], L.ro2 [16]   readouts (scale folded)
@@ -113,7 +116,14 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = 
                 radial_depth=3, layer_in_blocks=[0] * 4, layer_hid_blocks=[0] * 4, correlation=[0] * 4,
                 has_zbl=int(bool(cfg.pair_repulsion)), zbl_p=6, r_max=float(cfg.r_max),
                 zbl_a_exp=0.3, zbl_a_prefactor=0.4543, zbl_scale=scale,
-                feature_half=int(dtype == "float16"))
+                feature_half=int(dtype == "float16"),
+                density_norm=int(bool(cfg.use_density_normalization)),
+                first_nonresidual=int(bool(cfg.first_interaction_nonresidual)),
+                agnesi=int(cfg.agnesi() is not None), agnesi_q=0.0, agnesi_p=0.0, agnesi_a=0.0)
+    ag = cfg.agnesi()
+    if ag is not None:
+        dims.update(agnesi_q=ag["q"], agnesi_p=ag["p"], agnesi_a=ag["a"])
+        T["agnesi_cov"] = cfg.agnesi_radii()[np.asarray(z_table)]
     if cfg.pair_repulsion:
         dims["zbl_p"] = int(cfg.pair_repulsion.get("p", 6))
         dims["zbl_a_exp"] = float(cfg.pair_repulsion.get("a_exp", 0.3))
@@ -132,24 +142,31 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = 
         for n, (ji, jo, mi, mo, pw) in enumerate(linear_instructions(irr_in, irr_in)):
             assert ji == jo
             T[f"{p}up.{ji}"] = f64(f"{q}.linear_up.weights.{n}") * pw
-        # skip FCTP with one-hot attributes: out[w,k] = pw * sum_u W[u,z,w] x[u,i] cg[i,0,k]
+        # skip FCTP with one-hot attributes: out[w,k] = pw * sum_u W[u,z,w] x[u,i] cg[i,0,k];
+        # residual blocks: input -> hidden ("skip"); non-residual first block: message ->
+        # message ("mskip", blocks.py:68-176)
         from .model_io import fctp_instructions
-        for n, (i1, i2, io, pw) in enumerate(fctp_instructions(irr_in, attrs, hid)):
-            l1, lo = irr_in[i1].ir.l, hid[io].ir.l
+        resid = cfg.residual(l)
+        s_in, s_out, s_name = (irr_in, hid, "skip") if resid else (inter, inter, "mskip")
+        for n, (i1, i2, io, pw) in enumerate(fctp_instructions(s_in, attrs, s_out)):
+            l1, lo = s_in[i1].ir.l, s_out[io].ir.l
             cg = wigner_3j(l1, 0, lo)[:, 0, :]
             c = cg[0, 0]
             if l1 != lo or not np.allclose(cg, c * np.eye(2 * l1 + 1), atol=1e-12):
                 raise UnsupportedModel("skip connection with non-diagonal coupling")
             W = f64(f"{q}.skip_tp.tp.weights.{n}")          # (C, n_el, C)
-            T[f"{p}skip.{io}"] = np.transpose(W, (1, 0, 2)) * (pw * c)
+            T[f"{p}{s_name}.{io}"] = np.transpose(W, (1, 0, 2)) * (pw * c)
+        if cfg.use_density_normalization:
+            T[f"{p}dens"] = f64(f"{q}.density_fn.weight").reshape(-1)
         # radial MLP, nn.Linear (out, in) -> [in][out]
         for k in range(4):
             T[f"{p}mlp.{k}"] = f64(f"{q}.conv_tp_weights.layers.{2 * k}.weight").T
         # message linear (irreps_mid -> interaction irreps) / avg_num_neighbors
         mid, _ = conv_tp_instructions(irr_in, cfg.sh_irreps, inter)
         per_out = {}
+        norm = 1.0 if cfg.use_density_normalization else 1.0 / cfg.avg_num_neighbors
         for n, (ji, jo, mi, mo, pw) in enumerate(linear_instructions(mid, inter)):
-            per_out.setdefault(jo, []).append(f64(f"{q}.linear.weights.{n}") * pw / cfg.avg_num_neighbors)
+            per_out.setdefault(jo, []).append(f64(f"{q}.linear.weights.{n}") * pw * norm)
         for jo in range(len(inter)):
             T[f"{p}lin.{jo}"] = np.concatenate(per_out[jo], axis=0)
         # symmetric contraction

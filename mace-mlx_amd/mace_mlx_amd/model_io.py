@@ -104,6 +104,23 @@ class ModelConfig:
         out = {k: getattr(self, k) for k in self.__dataclass_fields__}
         return {k: v for k, v in out.items() if v is not None}
 
+    def agnesi(self) -> Optional[dict]:
+        """AgnesiTransform parameters (`radial.py:207-229` defaults), or None."""
+        if self.distance_transform is None:
+            return None
+        d = {"q": 0.9183, "p": 4.5791, "a": 1.0805}
+        d.update({k: float(self.distance_transform[k]) for k in ("q", "p", "a") if k in self.distance_transform})
+        return d
+
+    def agnesi_radii(self) -> np.ndarray:
+        """Covalent radii (Å) by atomic number used by the distance transform."""
+        cov = (self.distance_transform or {}).get("covalent_radii")
+        return np.asarray(cov if cov is not None else COVALENT_RADII, dtype=np.float64)
+
+    def residual(self, layer: int) -> bool:
+        """Interaction `layer` adds the skip FCTP of its input (`model.py:213-247`)."""
+        return not (layer == 0 and self.first_interaction_nonresidual)
+
     # --- derived architecture (model.py:96-145) -----------------------------
     @property
     def hidden(self) -> Irreps:
@@ -135,12 +152,12 @@ class ModelConfig:
         """Raise NotImplementedError for topology options outside this engine."""
         if self.interaction_cls != "RealAgnosticResidualInteractionBlock":
             raise NotImplementedError(f"interaction_cls={self.interaction_cls}")
-        for flag in ("first_interaction_nonresidual", "use_density_normalization",
-                     "use_agnostic_product"):
-            if getattr(self, flag):
-                raise NotImplementedError(flag)
+        if self.use_agnostic_product:
+            raise NotImplementedError("use_agnostic_product")
         if self.distance_transform is not None:
-            raise NotImplementedError("distance_transform (Agnesi)")
+            unknown = set(self.distance_transform) - {"q", "p", "a", "covalent_radii"}
+            if unknown:
+                raise NotImplementedError(f"distance_transform keys {sorted(unknown)}")
         if not self.apply_cutoff:
             raise NotImplementedError("apply_cutoff=False")
         if self.heads is not None and len(self.heads) > 1:
@@ -250,8 +267,13 @@ def weight_shapes(cfg: ModelConfig) -> Dict[str, tuple]:
     inter = cfg.interaction_irreps
     for li, (irr_in, hid) in enumerate(zip(cfg.layer_inputs(), cfg.hidden_per_layer())):
         p = f"interactions.{li}"
-        for n, (i, j, k, _) in enumerate(fctp_instructions(irr_in, attrs, hid)):
-            shapes[f"{p}.skip_tp.tp.weights.{n}"] = (irr_in[i].mul, attrs[j].mul, hid[k].mul)
+        # residual blocks skip from the layer input to the hidden irreps; the non-residual
+        # first block (blocks.py:68-176) applies its skip FCTP to the message
+        s_in, s_out = (irr_in, hid) if cfg.residual(li) else (inter, inter)
+        for n, (i, j, k, _) in enumerate(fctp_instructions(s_in, attrs, s_out)):
+            shapes[f"{p}.skip_tp.tp.weights.{n}"] = (s_in[i].mul, attrs[j].mul, s_out[k].mul)
+        if cfg.use_density_normalization:  # nn.Linear(num_radial, 1, bias=False), blocks.py:331-332
+            shapes[f"{p}.density_fn.weight"] = (1, cfg.num_bessel)
         for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(irr_in, irr_in)):
             shapes[f"{p}.linear_up.weights.{n}"] = (mi, mo)
         mid, tpi = conv_tp_instructions(irr_in, cfg.sh_irreps, inter)
@@ -303,6 +325,8 @@ def random_init(cfg: ModelConfig, seed: int = 0) -> Dict[str, np.ndarray]:
             layer = int(key.split(".layers.")[1].split(".")[0])
             scale = 1.0 / math.sqrt(shp[1]) * (SILU_NORM_FACTOR if layer > 0 else 1.0)
             w[key] = rng.standard_normal(shp) * scale
+        elif key.endswith(".density_fn.weight"):
+            w[key] = rng.standard_normal(shp) / math.sqrt(shp[1])
         elif ".symmetric_contractions." in key:
             w[key] = rng.standard_normal(shp) / shp[1]
         else:

@@ -83,16 +83,24 @@ def rattle(s: System, sigma: float, seed: int, rng: Optional[np.random.Generator
 
 
 def arch_config(arch: str, num_elements: int = 1, z_table=None, zbl: bool = False,
-                atomic_energies=None, avg_num_neighbors: float = 1.0) -> ModelConfig:
+                atomic_energies=None, avg_num_neighbors: float = 1.0,
+                trained_topology: bool = False) -> ModelConfig:
+    """Benchmark architectures.  trained_topology selects the layout of the reference's
+    default foundation models (medium-mpa-0 family, `model.py:153-247`): Agnesi distance
+    transform, density-normalised interactions, non-residual first interaction, 10 Bessel
+    functions."""
     hidden = {"small": "128x0e", "medium": "128x0e+128x1o",
               "large": "128x0e+128x1o+128x2e"}[arch]
     return ModelConfig(
-        r_max=6.0, num_bessel=8, num_polynomial_cutoff=5, max_ell=3,
+        r_max=6.0, num_bessel=10 if trained_topology else 8, num_polynomial_cutoff=5, max_ell=3,
         num_interactions=2, hidden_irreps=hidden, correlation=[3, 3],
         num_elements=num_elements, atomic_energies=atomic_energies,
         avg_num_neighbors=avg_num_neighbors, radial_MLP=[64, 64, 64],
         model_type="MACE", z_table=list(z_table) if z_table is not None else [14],
         pair_repulsion={"p": 6, "a_exp": 0.3, "a_prefactor": 0.4543} if zbl else None,
+        distance_transform={"q": 0.9183, "p": 4.5791, "a": 1.0805} if trained_topology else None,
+        use_density_normalization=trained_topology,
+        first_interaction_nonresidual=trained_topology,
     )
 
 

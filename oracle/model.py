@@ -13,7 +13,10 @@ Semantics follow the reference's generic code paths:
 * symmetric contraction        `symmetric_contraction.py:505-595` (row-compressed main
                                step over U's nonzero (i, k) pairs + dense lower chain,
                                i.e. the reference's CPU path)
-* interaction / product / readout blocks `blocks.py:179-279,493-608`
+* interaction / product / readout blocks `blocks.py:179-279,493-608`; the trained-model
+                               variants: Agnesi distance transform `radial.py:207-262`,
+                               density normalisation `blocks.py:282-490`, non-residual
+                               first interaction `blocks.py:68-176`, `model.py:213-247`
 * energy assembly              `model.py:403-438`
 * forces / stress              `calculators.py:440-563` (autograd; symmetric displacement)
 
@@ -86,6 +89,15 @@ def bessel(r: torch.Tensor, w: torch.Tensor, r_max: float) -> torch.Tensor:
     safe = torch.where(x == 0.0, torch.ones_like(x), x)
     out = math.sqrt(2.0 / r_max) * num / safe
     return torch.where(x == 0.0, math.sqrt(2.0 / r_max) * w[None, :].expand_as(out), out)
+
+
+def agnesi(r, zs, zr, params, radii):
+    """AgnesiTransform, `radial.py:231-262`: r / r0 with r0 the mean covalent radius of
+    the pair, mapped to 1 / (1 + a x^q / (1 + x^(q - p)))."""
+    r0 = 0.5 * (radii[zs] + radii[zr])
+    x = torch.clamp(r / r0, min=1e-12)
+    q, p, a = params["q"], params["p"], params["a"]
+    return 1.0 / (1.0 + a * x ** q / (1.0 + x ** (q - p)))
 
 
 def zbl_node_energy(r, zs, zr, receiver, n_nodes, params):
@@ -345,8 +357,13 @@ class OracleMACE:
         for li in range(cfg.num_interactions):
             p = f"interactions.{li}"
             hid = hid_layers[li]
-            L = {}
-            L["skip"] = SkipFCTP(irr_in, nel, hid, wl(f"{p}.skip_tp.tp.weights"))
+            L = {"resid": cfg.residual(li)}
+            if L["resid"]:
+                L["skip"] = SkipFCTP(irr_in, nel, hid, wl(f"{p}.skip_tp.tp.weights"))
+            else:
+                L["skip"] = SkipFCTP(inter, nel, inter, wl(f"{p}.skip_tp.tp.weights"))
+            if cfg.use_density_normalization:
+                L["dens"] = W[f"{p}.density_fn.weight"]
             L["up"] = Linear(irr_in, irr_in, wl(f"{p}.linear_up.weights"))
             L["tp"] = ConvTP(irr_in, sh, inter)
             mats, n = [], 0
@@ -375,6 +392,8 @@ class OracleMACE:
         self.sh_lmax = cfg.max_ell
         self.e0 = W["atomic_energies_fn.atomic_energies"].reshape(-1)
         self.bw = W["radial_embedding.bessel_fn.bessel_weights"]
+        self.agnesi = cfg.agnesi()
+        self.radii = _t(cfg.agnesi_radii(), dtype)
 
     # -- forward from edge vectors ------------------------------------------
     def energy_from_vectors(self, vec, species, sender, receiver):
@@ -385,18 +404,33 @@ class OracleMACE:
         onehot = torch.nn.functional.one_hot(species, self.nel).to(dtype)
         node_e0 = self.e0[species]
         Y = spherical_harmonics(vec, self.sh_lmax)
-        ef = bessel(r, self.bw, cfg.r_max) * poly_envelope(r / cfg.r_max, cfg.num_polynomial_cutoff)[:, None]
+        if self.agnesi is not None:
+            z = self.z_table[species]
+            rb = agnesi(r, z[sender], z[receiver], self.agnesi, self.radii)
+        else:
+            rb = r
+        ef = bessel(rb, self.bw, cfg.r_max) * poly_envelope(r / cfg.r_max, cfg.num_polynomial_cutoff)[:, None]
         terms = [node_e0]
         if cfg.pair_repulsion:
             z = self.z_table[species]
             terms.append(zbl_node_energy(r, z[sender], z[receiver], receiver, N, cfg.pair_repulsion))
         h = self.embed(onehot).detach()
         for L in self.layers:
-            sc = L["skip"](h, onehot)
+            sc = L["skip"](h, onehot) if L["resid"] else None
             up = L["up"](h)
             msg = self._message(L, up, Y, ef, sender, receiver, N)
-            msg = L["lin"](msg) / cfg.avg_num_neighbors
-            h = L["plin"](L["sc"](msg, species)) + sc
+            msg = L["lin"](msg)
+            if "dens" in L:   # density normalisation, blocks.py:372-380
+                d = torch.tanh((ef @ L["dens"].T) ** 2)[:, 0]
+                rho = torch.zeros(N, dtype=dtype).index_add(0, receiver, d)
+                msg = msg / (rho + 1.0)[:, None]
+            else:
+                msg = msg / cfg.avg_num_neighbors
+            if not L["resid"]:
+                msg = L["skip"](msg, onehot)
+            h = L["plin"](L["sc"](msg, species))
+            if sc is not None:
+                h = h + sc
             ro = L["ro"]
             if ro[0] == "linear":
                 terms.append(ro[1](h)[:, 0])

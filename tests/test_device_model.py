@@ -84,9 +84,11 @@ def test_unsupported_topologies_raise():
     bad = ModelConfig.from_dict({**cfg.to_dict(), "hidden_irreps": "128x0e+64x1o"})
     with pytest.raises((UnsupportedModel, NotImplementedError, KeyError)):
         build_device_model(bad, w)
-    bad2 = ModelConfig.from_dict({**cfg.to_dict(), "use_density_normalization": True})
-    with pytest.raises(NotImplementedError):
-        build_device_model(bad2, w)
+    for key, val in (("use_agnostic_product", True), ("apply_cutoff", False),
+                     ("interaction_cls", "RealAgnosticResidualNonLinearInteractionBlock")):
+        bad2 = ModelConfig.from_dict({**cfg.to_dict(), key: val})
+        with pytest.raises(NotImplementedError):
+            build_device_model(bad2, w)
 
 
 def test_float16_policy_rounds_all_but_pinned_weights():

@@ -94,6 +94,22 @@ def test_hea_89_elements_reduced():
     assert_parity(got, case.reference(s, got["sp"], edges), len(s))
 
 
+@pytest.mark.parametrize("arch", ["medium", "large"])
+def test_trained_topology_parity(arch):
+    """The layout of the reference's default foundation models (medium-mpa-0 family,
+    `model.py:153-247`): Agnesi distance transform, density-normalised interactions,
+    non-residual first interaction with a two-element message skip, 10 Bessel functions;
+    E, F and stress against the float64 oracle."""
+    cfg = arch_config(arch, num_elements=2, z_table=[8, 14], zbl=True, trained_topology=True)
+    case = Case(cfg, seed=3)
+    s = rattle(diamond_si((3, 3, 3)), 0.05, 12)
+    s.numbers = np.where(np.arange(len(s)) % 3 == 0, 8, 14)
+    got = case.run(s, stress=True)
+    edges = case.edges()
+    assert edge_set(*edges) == bruteforce_edges(s)
+    assert_parity(got, case.reference(s, got["sp"], edges, stress=True), len(s), stress=True)
+
+
 def _fp16_errors(got, ref, n):
     dF = got["F"] - ref["F"]
     rms = float(np.sqrt((ref["F"] ** 2).mean()))

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from mace_mlx_amd.model_io import random_init
+from mace_mlx_amd.model_io import COVALENT_RADII, random_init, weight_shapes
 from mace_mlx_amd.systems import arch_config, diamond_si, make_config, rattle
 from oracle import model as om
 from oracle.neighbors import neighbor_list
@@ -223,3 +223,95 @@ def test_symmetric_contraction_equals_dense_definition():
         out = np.einsum(f"bc{pre}i,bci->bc{pre}", c1, f.numpy())
         want = out.reshape(b, -1)
         np.testing.assert_allclose(got, want, atol=1e-10)
+
+
+# ---------------------------------------------------------------------------
+# trained-model topology (Agnesi transform, density normalisation, non-residual
+# first interaction)
+# ---------------------------------------------------------------------------
+
+def test_agnesi_transform_closed_form():
+    """radial.py:231-262: t(x) = 1 / (1 + a x^q / (1 + x^(q-p))), x = r / r0."""
+    prm = {"q": 0.9183, "p": 4.5791, "a": 1.0805}
+    radii = torch.tensor(COVALENT_RADII, dtype=torch.float64)
+    r0 = 0.5 * (COVALENT_RADII[14] + COVALENT_RADII[8])
+    r = torch.tensor([r0, 0.5 * r0, 2.0 * r0, 1e-9, 50.0], dtype=torch.float64)
+    z1, z2 = torch.full((5,), 14), torch.full((5,), 8)
+    t = om.agnesi(r, z1, z2, prm, radii).numpy()
+    assert abs(t[0] - 1.0 / (1.0 + prm["a"] / 2.0)) < 1e-14          # x = 1
+    x = 0.5
+    assert abs(t[1] - 1.0 / (1.0 + prm["a"] * x ** prm["q"] / (1.0 + x ** (prm["q"] - prm["p"])))) < 1e-14
+    assert t[3] > 1.0 - 1e-6                                          # r -> 0: t -> 1
+    xl = 50.0 / r0                                                    # r -> inf: t ~ 1 / (1 + a x^q)
+    assert abs(t[4] * (1.0 + prm["a"] * xl ** prm["q"]) - 1.0) < 1e-4
+    assert np.all(np.diff(t[[3, 1, 0, 2, 4]]) < 0)                    # decreasing in r
+
+
+@pytest.fixture(scope="module")
+def mpa():
+    cfg = arch_config("medium", num_elements=2, z_table=[8, 14], trained_topology=True)
+    w = random_init(cfg, 3)
+    m = om.OracleMACE(cfg=cfg, weights=w)
+    s = rattle(diamond_si((2, 2, 2)), 0.05, 12)
+    s.numbers = np.where(np.arange(len(s)) % 3 == 0, 8, 14)
+    i, j, S = neighbor_list(s.positions, s.cell, s.pbc, 6.5)
+    sp = (s.numbers == 14).astype(int)
+    return cfg, w, m, s, np.stack([i, j]), S, sp
+
+
+def test_trained_topology_forces_stress_and_invariance(mpa):
+    cfg, w, m, s, ei, S, sp = mpa
+    E, F, st, ne, vir = m.energy_forces_stress(s.positions, sp, ei, S, s.cell)
+    h = 1e-4
+    for a, k in [(0, 0), (7, 1), (33, 2)]:
+        p1, p2 = s.positions.copy(), s.positions.copy()
+        p1[a, k] += h
+        p2[a, k] -= h
+        fd = -(m.energy(p1, sp, ei, S, s.cell)[0] - m.energy(p2, sp, ei, S, s.cell)[0]) / (2 * h)
+        assert abs(fd - F[a, k]) < 1e-6 * max(1.0, abs(F[a, k]))
+    np.testing.assert_allclose(F.sum(0), 0.0, atol=1e-10)
+    q = np.linalg.qr(np.random.default_rng(7).normal(size=(3, 3)))[0]
+    R = q * np.sign(np.linalg.det(q))
+    Er, Fr, _ = m.energy_forces(s.positions @ R.T, sp, ei, S, s.cell @ R.T)
+    assert abs(Er - E) < 1e-9 * abs(E)
+    np.testing.assert_allclose(Fr, F @ R.T, atol=1e-9)
+
+
+def test_density_normalisation_reduces_to_unit_average(mpa):
+    """With density_fn = 0 every edge density is tanh(0) = 0, so dividing by (density + 1)
+    is the plain block with avg_num_neighbors = 1 (blocks.py:372-380 vs 262-264)."""
+    cfg, w, m, s, ei, S, sp = mpa
+    w0 = {k: (np.zeros_like(v) if k.endswith("density_fn.weight") else v) for k, v in w.items()}
+    cfg_plain = arch_config("medium", num_elements=2, z_table=[8, 14], trained_topology=True)
+    cfg_plain.use_density_normalization = False
+    w_plain = {k: v for k, v in w.items() if not k.endswith("density_fn.weight")}
+    E0 = om.OracleMACE(cfg=cfg, weights=w0).energy(s.positions, sp, ei, S, s.cell)[0]
+    E1 = om.OracleMACE(cfg=cfg_plain, weights=w_plain).energy(s.positions, sp, ei, S, s.cell)[0]
+    assert abs(E0 - E1) < 1e-10 * abs(E1)
+
+
+def test_nonresidual_first_block_with_identity_skip():
+    """blocks.py:68-176: the non-residual block applies its skip FCTP to the message.
+    With W[u, z, w] = delta_uw sqrt(C n_el) (path weight 1/sqrt(C n_el), 3j = I/sqrt(2l+1))
+    that FCTP is the identity, so the model equals the residual layout with a zero
+    first-layer skip."""
+    cfg = arch_config("medium", num_elements=2, z_table=[8, 14])
+    cfg.first_interaction_nonresidual = True
+    w = random_init(cfg, 4)
+    C, nel = 128, 2
+    eye = np.zeros((C, nel, C))
+    for z in range(nel):
+        eye[:, z, :] = np.eye(C) * math.sqrt(C * nel)
+    w_id = {k: (eye if k.startswith("interactions.0.skip_tp.") else v) for k, v in w.items()}
+    cfg_res = arch_config("medium", num_elements=2, z_table=[8, 14])
+    w_res = {k: v for k, v in w.items() if not k.startswith("interactions.0.skip_tp.")}
+    for k, shp in weight_shapes(cfg_res).items():
+        if k.startswith("interactions.0.skip_tp."):
+            w_res[k] = np.zeros(shp)
+    s = rattle(diamond_si((2, 2, 2)), 0.05, 13)
+    sp = (np.arange(len(s)) % 2).astype(int)
+    i, j, S = neighbor_list(s.positions, s.cell, s.pbc, 6.5)
+    ei = np.stack([i, j])
+    Ea = om.OracleMACE(cfg=cfg, weights=w_id).energy(s.positions, sp, ei, S, s.cell)[0]
+    Eb = om.OracleMACE(cfg=cfg_res, weights=w_res).energy(s.positions, sp, ei, S, s.cell)[0]
+    assert abs(Ea - Eb) < 1e-9 * max(1.0, abs(Eb))
