@@ -304,6 +304,11 @@ __global__ void k_nl_bin(int N, const double* __restrict__ pos, NLParams p, doub
   bin[i] = (b[0] * p.nbin[1] + b[1]) * p.nbin[2] + b[2];
 }
 
+// One wave per receiver atom j: the wave walks j's neighbour cells in a fixed
+// order and its lanes test the cell's atoms 64 at a time; hits are counted
+// with a ballot, and in the fill pass each hit lane writes at the running
+// count plus its rank among the hit lanes, so the edge order (cell order, then
+// position in the cell) is deterministic and identical in both passes.
 template <bool FILL>
 __device__ __forceinline__ int nl_visit(int j, const NLParams& p, const double* __restrict__ wpos,
                                         const int* __restrict__ img, const int* __restrict__ bin,
@@ -311,6 +316,7 @@ __device__ __forceinline__ int nl_visit(int j, const NLParams& p, const double* 
                                         const int* __restrict__ bin_atoms, int out0,
                                         int* __restrict__ sender, int* __restrict__ receiver,
                                         int* __restrict__ shifts) {
+  const int lane = __lane_id();
   const int bj = bin[j];
   const int b2 = bj % p.nbin[2], b1 = (bj / p.nbin[2]) % p.nbin[1], b0 = bj / (p.nbin[2] * p.nbin[1]);
   const double xj = wpos[3 * j], yj = wpos[3 * j + 1], zj = wpos[3 * j + 2];
@@ -331,24 +337,31 @@ __device__ __forceinline__ int nl_visit(int j, const NLParams& p, const double* 
         const double ty = T0 * p.cell[1] + T1 * p.cell[4] + T2 * p.cell[7];
         const double tz = T0 * p.cell[2] + T1 * p.cell[5] + T2 * p.cell[8];
         const int cb = (c0 * p.nbin[1] + c1) * p.nbin[2] + c2;
-        for (int q = bin_start[cb]; q < bin_start[cb + 1]; ++q) {
-          const int i = bin_atoms[q];
-          if (i == j && T0 == 0 && T1 == 0 && T2 == 0) continue;
-          // image of atom i at wpos_i + T.cell; D = x_j - x_i(image)
-          const double dx = xj - (wpos[3 * i] + tx), dy = yj - (wpos[3 * i + 1] + ty),
-                       dz = zj - (wpos[3 * i + 2] + tz);
-          if (dx * dx + dy * dy + dz * dz < p.cutoff2) {
-            if (FILL) {
-              const int o = out0 + cnt;
-              sender[o] = i;
-              receiver[o] = j;
-              // D = x_j - x_i + S.cell with x = wpos + img.cell  =>  S = -T - img_j + img_i
-              shifts[3 * o + 0] = -T0 - img[3 * j + 0] + img[3 * i + 0];
-              shifts[3 * o + 1] = -T1 - img[3 * j + 1] + img[3 * i + 1];
-              shifts[3 * o + 2] = -T2 - img[3 * j + 2] + img[3 * i + 2];
+        const int qe = bin_start[cb + 1];
+        for (int q0 = bin_start[cb]; q0 < qe; q0 += 64) {
+          const int q = q0 + lane;
+          bool hit = false;
+          int i = 0;
+          if (q < qe) {
+            i = bin_atoms[q];
+            if (!(i == j && T0 == 0 && T1 == 0 && T2 == 0)) {
+              // image of atom i at wpos_i + T.cell; D = x_j - x_i(image)
+              const double dx = xj - (wpos[3 * i] + tx), dy = yj - (wpos[3 * i + 1] + ty),
+                           dz = zj - (wpos[3 * i + 2] + tz);
+              hit = dx * dx + dy * dy + dz * dz < p.cutoff2;
             }
-            ++cnt;
           }
+          const unsigned long long m = __ballot(hit);
+          if (FILL && hit) {
+            const int o = out0 + cnt + __popcll(m & ((1ull << lane) - 1ull));
+            sender[o] = i;
+            receiver[o] = j;
+            // D = x_j - x_i + S.cell with x = wpos + img.cell  =>  S = -T - img_j + img_i
+            shifts[3 * o + 0] = -T0 - img[3 * j + 0] + img[3 * i + 0];
+            shifts[3 * o + 1] = -T1 - img[3 * j + 1] + img[3 * i + 1];
+            shifts[3 * o + 2] = -T2 - img[3 * j + 2] + img[3 * i + 2];
+          }
+          cnt += __popcll(m);
         }
       }
     }
@@ -356,19 +369,23 @@ __device__ __forceinline__ int nl_visit(int j, const NLParams& p, const double* 
   return cnt;
 }
 
-__global__ void k_nl_count(int N, NLParams p, const double* __restrict__ wpos, const int* __restrict__ bin,
-                           const int* __restrict__ bin_start, const int* __restrict__ bin_atoms,
-                           int* __restrict__ counts) {
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+// four receiver atoms per 256-thread block, one wave each
+__global__ void __launch_bounds__(256) k_nl_count(int N, NLParams p, const double* __restrict__ wpos,
+                                                  const int* __restrict__ bin, const int* __restrict__ bin_start,
+                                                  const int* __restrict__ bin_atoms, int* __restrict__ counts) {
+  const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (j >= N) return;
-  counts[j] = nl_visit<false>(j, p, wpos, nullptr, bin, bin_start, bin_atoms, 0, nullptr, nullptr, nullptr);
+  const int c = nl_visit<false>(j, p, wpos, nullptr, bin, bin_start, bin_atoms, 0, nullptr, nullptr, nullptr);
+  if (__lane_id() == 0) counts[j] = c;
 }
 
-__global__ void k_nl_fill(int N, NLParams p, const double* __restrict__ wpos, const int* __restrict__ img,
-                          const int* __restrict__ bin, const int* __restrict__ bin_start,
-                          const int* __restrict__ bin_atoms, const int* __restrict__ rowptr,
-                          int* __restrict__ sender, int* __restrict__ receiver, int* __restrict__ shifts) {
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ void __launch_bounds__(256) k_nl_fill(int N, NLParams p, const double* __restrict__ wpos,
+                                                 const int* __restrict__ img, const int* __restrict__ bin,
+                                                 const int* __restrict__ bin_start,
+                                                 const int* __restrict__ bin_atoms, const int* __restrict__ rowptr,
+                                                 int* __restrict__ sender, int* __restrict__ receiver,
+                                                 int* __restrict__ shifts) {
+  const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (j >= N) return;
   nl_visit<true>(j, p, wpos, img, bin, bin_start, bin_atoms, rowptr[j], sender, receiver, shifts);
 }
@@ -433,7 +450,7 @@ void launch_nl_bin(hipStream_t st, int N, const double* pos, const NLParams& p, 
 void launch_nl_count(hipStream_t st, int N, const NLParams& p, const double* wpos, const int* bin,
                      const int* bin_start, const int* bin_atoms, int* counts) {
   if (N <= 0) return;
-  hipLaunchKernelGGL(k_nl_count, dim3(nblk(N, 128)), dim3(128), 0, st, N, p, wpos, bin, bin_start, bin_atoms,
+  hipLaunchKernelGGL(k_nl_count, dim3(nblk(N, 4)), dim3(256), 0, st, N, p, wpos, bin, bin_start, bin_atoms,
                      counts);
 }
 
@@ -441,7 +458,7 @@ void launch_nl_fill(hipStream_t st, int N, const NLParams& p, const double* wpos
                     const int* bin, const int* bin_start, const int* bin_atoms, const int* rowptr,
                     int* sender, int* receiver, int* shifts) {
   if (N <= 0) return;
-  hipLaunchKernelGGL(k_nl_fill, dim3(nblk(N, 128)), dim3(128), 0, st, N, p, wpos, img, bin, bin_start,
+  hipLaunchKernelGGL(k_nl_fill, dim3(nblk(N, 4)), dim3(256), 0, st, N, p, wpos, img, bin, bin_start,
                      bin_atoms, rowptr, sender, receiver, shifts);
 }
 
