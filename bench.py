@@ -33,6 +33,17 @@ sys.path.insert(0, str(ROOT / "mace-mlx_amd"))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_MFMA_PEAK_TFS = 157.3     # MI355X dense fp32 matrix
+FP16_MFMA_PEAK_TFS = 2500.0    # MI355X dense fp16 matrix (the radial MLP's output and gradient
+                               # products run on it under the float16 feature policy)
+
+
+def peak_of(site: str, bound: str, ctx: dict) -> float:
+    """Roofline peak for a site: HBM bandwidth, or the matrix-core rate of its data type."""
+    if bound == "hbm":
+        return HBM_PEAK_GBS
+    if ctx.get("half") and site.split(".")[0] in ("mlp_out", "mlp_gh3"):
+        return FP16_MFMA_PEAK_TFS
+    return FP32_MFMA_PEAK_TFS
 
 
 def algorithmic_work(site: str, ctx: dict):
@@ -199,13 +210,14 @@ def measure_config(idx, steps, warmup):
     kt = eng.kernel_times()
     eng.set_profiling(False)
     layers = layer_shapes(dm)
-    ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_flops=linear_flops(layers, N))
+    ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_flops=linear_flops(layers, N),
+               half=bc.dtype == "float16")
     per_step = {k: (v[0] / steps, v[1] // steps) for k, v in kt.items()}
     dom = max(per_step, key=lambda k: per_step[k][0])
     b, a, u = algorithmic_work(dom, ctx)
     t, n = per_step[dom]
     ach = (a / max(n, 1)) / (t / max(n, 1) * 1e-3) / (1e9 if b == "hbm" else 1e12)
-    frac = ach / (HBM_PEAK_GBS if b == "hbm" else FP32_MFMA_PEAK_TFS)
+    frac = ach / peak_of(dom, b, ctx)
     res = {"workload": bc.name, "n_atoms": N, "n_edges": E, "properties": "+".join(bc.properties),
            "feature_dtype": bc.dtype, "ms_per_step": round(ms, 4), "ms_per_step_nl_rebuild": round(ms_nl, 4),
            "atom_steps_per_s": round(N / ms * 1e3, 1), "dominant": dom, "dominant_frac": round(frac, 4),
@@ -293,7 +305,8 @@ def main():
     kt = eng.kernel_times()
     eng.set_profiling(False)
     layers = layer_shapes(dm)
-    ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_flops=linear_flops(layers, N))
+    ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_flops=linear_flops(layers, N),
+               half=bc.dtype == "float16")
     per_step = {k: (v[0] / args.steps, v[1] // args.steps) for k, v in kt.items()}
     dom = max(per_step, key=lambda k: per_step[k][0])
     bound, amount, unit = algorithmic_work(dom, ctx)
@@ -301,10 +314,9 @@ def main():
     avg_ms = per_step[dom][0] / launches
     if bound == "hbm":
         achieved = amount / launches / (avg_ms * 1e-3) / 1e9 if launches > 1 else amount / (avg_ms * 1e-3) / 1e9
-        peak = HBM_PEAK_GBS
     else:
         achieved = amount / launches / (avg_ms * 1e-3) / 1e12
-        peak = FP32_MFMA_PEAK_TFS
+    peak = peak_of(dom, bound, ctx)
     roofline = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
                 "frac": round(achieved / peak, 4), "traffic": load_traffic(dom, bc.name), "kernel": dom,
                 "avg_launch_ms": round(avg_ms, 5), "tp_scatter_hbm_frac": round(tp_scatter_frac(per_step, ctx), 4)}
@@ -315,7 +327,7 @@ def main():
             b, a, u = algorithmic_work(k, ctx)
             per = t / max(n, 1) * 1e-3
             ach = (a / max(n, 1)) / per / (1e9 if b == "hbm" else 1e12) if a else 0.0
-            pk = HBM_PEAK_GBS if b == "hbm" else FP32_MFMA_PEAK_TFS
+            pk = peak_of(k, b, ctx)
             print(f"{k:24s} {t:9.4f} {t / tot * 100:5.1f}% {n:6d}  {ach:9.2f} {u} ({ach / pk * 100:.1f}% of {b})",
                   file=sys.stderr)
 

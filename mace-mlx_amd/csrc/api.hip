@@ -78,7 +78,7 @@ struct Layer {
   int din = 0, dhid = 0, dmid = 0, dint = 0, wn = 0;
   DBuf<float> up[3], upT[3], skip[3], skipT[3], mlp[4], mlpT[4], lin_[4], linT[4], sc[3], plin[3], plinT[3];
   DBuf<float> ro, ro1, ro2;
-  DBuf<_Float16> mlpT3h;  // fp16 copy of W3^T (float16 feature policy)
+  DBuf<_Float16> mlpT3h, mlp3h;  // fp16 copies of W3^T and W3 (float16 feature policy)
   bool resid = true;       // residual block (skip from the input); else the skip acts on the message
   DBuf<float> mskip[4], mskipT[4], dens;
   int nskip = 0;
@@ -127,7 +127,8 @@ struct mace_ctx {
   // per-step edge buffers
   DBuf<EdgeGeom> geom;
   DBuf<float> Y, Mt, ef, zbl_e, gY, gef, gv, gw, gxe, h3;
-  DBuf<_Float16> h3h;  // radial-MLP hidden output under the float16 feature policy
+  DBuf<_Float16> h3h, gwh;  // radial-MLP hidden output, dL/dw under the float16 feature policy
+  DBuf<float> gscale;       // per-(edge, channel half) scale of gwh
   DBuf<double> vir_part;
   // node buffers
   std::vector<DBuf<float>> h;  // h[0..L]
@@ -262,7 +263,7 @@ void free_layers(mace_ctx* c) {
       for (int i = 0; i < 3; ++i) arr[i].release();
     for (int i = 0; i < 4; ++i) L.mlp[i].release(), L.mlpT[i].release(), L.lin_[i].release(), L.linT[i].release();
     L.ro.release(), L.ro1.release(), L.ro2.release(), L.h_up.release(), L.A.release(), L.w.release(),
-        L.ro_e.release(), L.wh.release(), L.mlpT3h.release(), L.A2.release(), L.rinv.release(), L.dens.release();
+        L.ro_e.release(), L.wh.release(), L.mlpT3h.release(), L.mlp3h.release(), L.A2.release(), L.rinv.release(), L.dens.release();
     for (int i = 0; i < 4; ++i) L.mskip[i].release(), L.mskipT[i].release();
   }
   c->layers.clear();
@@ -333,7 +334,10 @@ void build_model(mace_ctx* c) {
         const auto& w = tensor(c, p + "mlp." + std::to_string(k), (size_t)rows[k] * cols[k]);
         upload(c, L.mlp[k], w);
         upload(c, L.mlpT[k], transpose(w, rows[k], cols[k]));
-        if (k == 3 && d.feature_half) upload_half(c, L.mlpT3h, transpose(w, rows[k], cols[k]));
+        if (k == 3 && d.feature_half) {
+          upload_half(c, L.mlpT3h, transpose(w, rows[k], cols[k]));
+          upload_half(c, L.mlp3h, w);
+        }
       }
     }
     const int* l3 = tp_l3(L.lin);
@@ -436,7 +440,12 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   c->gef.ensure(e * c->dims.num_bessel);
   c->h3.ensure(e * RADIAL_H);
   c->gv.ensure(e * 3);
-  c->gw.ensure(e * maxw);
+  if (half) {
+    c->gwh.ensure(e * maxw);
+    c->gscale.ensure(e * 2);
+  } else {
+    c->gw.ensure(e * maxw);
+  }
   c->vir_part.ensure(9 * ((e + 255) / 256));
 }
 
@@ -973,8 +982,8 @@ void backward(mace_ctx* c, bool stress, double* out) {
       // layers after the first also need dL/dx: per-edge rows in sender order, then a segmented sum
       Site s(c, lname("tp_bwd", l));
       launch_tp_bwd_recv(st, Ly.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.wptr(half),
-                         Ly.h_up.p, c->gM.p, c->gw.p, c->gY.p, first_edge_grad, c->pos_s.p,
-                         l > 0 ? c->gxe.p : nullptr, half);
+                         Ly.h_up.p, c->gM.p, half ? static_cast<void*>(c->gwh.p) : static_cast<void*>(c->gw.p),
+                         c->gscale.p, c->gY.p, first_edge_grad, c->pos_s.p, l > 0 ? c->gxe.p : nullptr, half);
     }
     if (l > 0) {
       Site s(c, lname("tp_gather", l));
@@ -982,7 +991,10 @@ void backward(mace_ctx* c, bool stress, double* out) {
     }
     {
       Site s(c, lname("mlp_gh3", l));
-      launch_mlp_gh3(st, E, Ly.wn, c->gw.p, Ly.mlp[3].p, c->h3.p);
+      if (half)
+        launch_mlp_gh3_h(st, E, Ly.wn, c->gwh.p, c->gscale.p, Ly.mlp3h.p, c->h3.p);
+      else
+        launch_mlp_gh3(st, E, Ly.wn, c->gw.p, Ly.mlp[3].p, c->h3.p);
     }
     {
       Site s(c, lname("mlp_hidden_bwd", l));
@@ -1073,6 +1085,8 @@ static void free_all(mace_ctx* c) {
   free_layers(c);
   for (auto& b : c->h) b.release();
   c->h3h.release();
+  c->gwh.release();
+  c->gscale.release();
   for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->ag_cov, &c->gA2, &c->grho, &c->embed, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
                   &c->gv, &c->gw, &c->gxe, &c->h3, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup, &c->ypre,
                   &c->node_e})

@@ -76,6 +76,9 @@ void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void
                     int half);
 // VJP: gh3 = gw W3^T, then gef (+)= dL/def through the recomputed hidden layers
 void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3);
+// float16 feature policy: gw fp16 with per-(edge, channel half) scales, W3 fp16 [64][W]
+void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const float* gscale, const void* W3h,
+                      float* gh3);
 void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0,
                            const float* W1, const float* W2, const float* gh3, float* gef,
                            int accumulate, int half);
@@ -89,11 +92,12 @@ void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int*
                    const float* Y, const float* Mt, int mts, const void* w, const float* up, float* M,
                    int half);
 // TP VJP, receiver-centric; gY is [E][2][16] (per channel half).  With gxe != null the
-// per-edge input gradient is also stored, row pos_s[e] of gxe ([E][LIN^2 * NC], sender order)
+// per-edge input gradient is also stored, row pos_s[e] of gxe ([E][LIN^2 * NC], sender order).
+// half: w and gw are fp16, gw scaled per (edge, channel half) by 1 / gscale[e][half]
 void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
                         const float* Y, const float* Mt, int mts, const void* w, const float* up,
-                        const float* gM, float* gw, float* gY, int accumulate_gY, const int* pos_s,
-                        float* gxe, int half);
+                        const float* gM, void* gw, float* gscale, float* gY, int accumulate_gY,
+                        const int* pos_s, float* gxe, int half);
 // gup[a] = sum of the sender-ordered gxe rows of node a
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe,
                          float* gup);

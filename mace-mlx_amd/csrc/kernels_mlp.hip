@@ -384,6 +384,94 @@ __global__ void __launch_bounds__(256) k_mlp_gh3(int64_t E, int W, const float* 
   }
 }
 
+// Float16 feature policy: gh3 = gw @ W3^T with gw fp16 [E][W] scaled per (edge,
+// channel half) -- gw[e][slot*128 + u] * gscale[e][u / 64] is the gradient -- and
+// W3 fp16 [64][W]; v_mfma_f32_16x16x32_f16 with fp32 accumulation.  A 32-wide k
+// chunk lies in one channel half, so the products of the two halves accumulate
+// separately and are combined with their row scales before the fixed-order
+// cross-wave sum.  Block = 32 edges, K split over the 4 waves, gw chunks loaded
+// GH_PF ahead.
+__global__ void __launch_bounds__(256) k_mlp_gh3_h(int64_t E, int W, const _Float16* __restrict__ gw,
+                                                   const float* __restrict__ gscale,
+                                                   const _Float16* __restrict__ W3h, float* __restrict__ gh3) {
+  __shared__ f4v sP[4][8][64];
+  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * 32;
+  const int kq = W / 4, kb = wv * kq, nch = kq / 32;
+  const _Float16* ar[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t row = min(row0 + 16 * t + r, E - 1);  // rows past the end are computed, not stored
+    ar[t] = gw + row * (int64_t)W + kb + 8 * g;
+  }
+  const _Float16* br = W3h + (int64_t)r * W + kb + 8 * g;
+  h8 ring[GH_PF][2], b[4], bn[4];
+#pragma unroll
+  for (int p = 0; p < GH_PF; ++p)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) ring[p][t] = *reinterpret_cast<const h8*>(ar[t] + 32 * min(p, nch - 1));
+#pragma unroll
+  for (int u = 0; u < 4; ++u) b[u] = *reinterpret_cast<const h8*>(br + (int64_t)16 * u * W);
+  f4v acc[2][2][4];  // [channel half][row tile][column tile]
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[hh][t][u] = f4v{0.f, 0.f, 0.f, 0.f};
+  for (int ch = 0; ch < nch; ch += GH_PF) {
+#pragma unroll
+    for (int p = 0; p < GH_PF; ++p) {
+      const int cc = ch + p;
+      if (cc < nch) {
+        const int nbk = min(cc + 1, nch - 1), na = min(cc + GH_PF, nch - 1);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) bn[u] = *reinterpret_cast<const h8*>(br + (int64_t)16 * u * W + 32 * nbk);
+        const h8 cur[2] = {ring[p][0], ring[p][1]};
+#pragma unroll
+        for (int t = 0; t < 2; ++t) ring[p][t] = *reinterpret_cast<const h8*>(ar[t] + 32 * na);
+        __builtin_amdgcn_sched_barrier(0);
+        if ((kb + 32 * cc) & 64) {  // second channel half of a slot
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[1][t][u] = mfma16h(cur[t], b[u], acc[1][t][u]);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[0][t][u] = mfma16h(cur[t], b[u], acc[0][t][u]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) b[u] = bn[u];
+      }
+    }
+  }
+  // combine the halves with their row scales (rows 4g + i of each row tile)
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t row = min(row0 + 16 * t + 4 * g + i, E - 1);
+      const float s0 = gscale[2 * row], s1 = gscale[2 * row + 1];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[0][t][u][i] = acc[0][t][u][i] * s0 + acc[1][t][u][i] * s1;
+    }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) sP[wv][t][l] = acc[0][t >> 2][t & 3];
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int t = 2 * wv + h, rt = t >> 2, ct = t & 3;
+    const f4v sm = ((sP[0][t][l] + sP[1][t][l]) + sP[2][t][l]) + sP[3][t][l];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t row = row0 + 16 * rt + 4 * g + i;
+      if (row < E) gh3[row * H + 16 * ct + r] = sm[i];
+    }
+  }
+}
+
 // dL/def from dL/dh3: recompute a1..a3, then
 //   g_a3 = g_h3 * silu'(a3), g_a2 = (g_a3 W2^T) * silu'(a2),
 //   g_a1 = (g_a2 W1^T) * silu'(a1), g_ef = g_a1 W0^T
@@ -479,6 +567,13 @@ void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void
 void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3) {
   if (E <= 0) return;
   hipLaunchKernelGGL(k_mlp_gh3, dim3(nblk(E, 32)), dim3(256), 0, st, E, W, gw, W3, gh3);
+}
+
+void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const float* gscale, const void* W3h,
+                      float* gh3) {
+  if (E <= 0) return;
+  hipLaunchKernelGGL(k_mlp_gh3_h, dim3(nblk(E, 32)), dim3(256), 0, st, E, W, static_cast<const _Float16*>(gw),
+                     gscale, static_cast<const _Float16*>(W3h), gh3);
 }
 
 void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0, const float* W1,

@@ -289,6 +289,31 @@ __device__ __forceinline__ float wave_sum16(const float* v) {
   return d;
 }
 
+// dL/dw of one edge and channel (all slots) into row gwe (stride NC).  GWT =
+// float, or _Float16 under the float16 feature policy: each wave then scales
+// its 64 channels x slots by a power of two that maps their largest magnitude
+// into [2^14, 2^15) (so small gradients keep fp16 precision) and stores the
+// inverse in gscale[e][half].
+template <int NSLOT, typename GWT>
+__device__ __forceinline__ void store_gw(const float* gws, GWT* __restrict__ gwe, float* __restrict__ gscale,
+                                         int64_t e, int u) {
+  if constexpr (sizeof(GWT) == 4) {
+#pragma unroll
+    for (int s = 0; s < NSLOT; ++s) gwe[s * NC] = gws[s];
+  } else {
+    float m = 0.f;
+#pragma unroll
+    for (int s = 0; s < NSLOT; ++s) m = fmaxf(m, fabsf(gws[s]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const int ex = m > 0.f ? ilogbf(m) : 0;
+    const float sc = ldexpf(1.f, 14 - ex);
+#pragma unroll
+    for (int s = 0; s < NSLOT; ++s) gwe[s * NC] = (GWT)(gws[s] * sc);
+    if ((u & 63) == 0) gscale[e * 2 + (u >> 6)] = ldexpf(1.f, ex - 14);
+  }
+}
+
 // Store this wave's reduced dL/dY of edge e into gY[e][half][16].
 __device__ __forceinline__ void store_gY(const float* gYu, int64_t e, int u, float* __restrict__ gY, int accumulate) {
   const float s = wave_sum16(gYu);
@@ -302,7 +327,7 @@ __device__ __forceinline__ void store_gY(const float* gYu, int64_t e, int u, flo
 // Per-edge VJP of one channel: given g = dL/dM[recv] (this channel), writes
 // dL/dw, accumulates the input gradient (if GX) and this channel's dL/dY.
 template <int LIN, bool GX>
-__device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& in, float* __restrict__ gwe,
+__device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& in, float* gw_out,
                                             const float* __restrict__ Ye, const float* __restrict__ Me,
                                             const float* M2, float& gx0, float* gx1, float* gx2, float* gYu) {
   using T = TPT<LIN>;
@@ -358,7 +383,7 @@ __device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& i
         gws = fmaf(g[a0 + k], mk, gws);
       }
     }
-    gwe[s * NC] = gws;
+    gw_out[s] = gws;
     if constexpr (LIN == 3) __builtin_amdgcn_sched_barrier(0);  // as in tp_edge_fwd
   }
 }
@@ -374,7 +399,8 @@ __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __rest
                                                         const int* __restrict__ sender, const float* __restrict__ Y,
                                                         const float* __restrict__ Mt, int mts,
                                                         const WT* __restrict__ w, const float* __restrict__ up,
-                                                        const float* __restrict__ gM, float* __restrict__ gw,
+                                                        const float* __restrict__ gM, WT* __restrict__ gw,
+                                                        float* __restrict__ gscale,
                                                         float* __restrict__ gY, int accumulate_gY,
                                                         const int* __restrict__ pos_s, float* __restrict__ gxe) {
   using T = TPT<LIN>;
@@ -413,8 +439,10 @@ __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __rest
     for (int j = 0; j < 16; ++j) gYu[j] = 0.f;
     float gx0 = 0.f, gx1[3] = {0.f, 0.f, 0.f}, gx2[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
     const float* Me = Mt + (int64_t)e * mts;
-    tp_edge_vjp<LIN, GX>(gm, cur, gw + (int64_t)e * WN + u, Y + (int64_t)e * 16, Me,
-                         STAGE ? m2buf + buf * M2PAD : Me + MT_M2, gx0, gx1, gx2, gYu);
+    float gws[T::NSLOT];
+    tp_edge_vjp<LIN, GX>(gm, cur, gws, Y + (int64_t)e * 16, Me, STAGE ? m2buf + buf * M2PAD : Me + MT_M2, gx0,
+                         gx1, gx2, gYu);
+    store_gw<T::NSLOT>(gws, gw + (int64_t)e * WN + u, gscale, e, u);
     if constexpr (GX) {
       float* dst = gxe + (int64_t)pos_s[e] * DIN + u;
       dst[0] = gx0;
@@ -490,11 +518,12 @@ void launch_fwd(hipStream_t st, int N, const int* rowptr, const int* sender, con
 
 template <int LIN, bool GX, typename WT>
 void launch_recv(hipStream_t st, int N, const int* rowptr, const int* sender, const float* Y, const float* Mt,
-                 int mts, const void* w, const float* up, const float* gM, float* gw, float* gY, int accumulate_gY,
-                 const int* pos_s, float* gxe) {
+                 int mts, const void* w, const float* up, const float* gM, void* gw, float* gscale, float* gY,
+                 int accumulate_gY, const int* pos_s, float* gxe) {
   constexpr int NG = ng_for(LIN);
   hipLaunchKernelGGL((k_tp_bwd_recv<LIN, NG, GX, WT>), dim3(N), dim3(NC * NG), 0, st, N, rowptr, sender, Y, Mt,
-                     mts, static_cast<const WT*>(w), up, gM, gw, gY, accumulate_gY, pos_s, gxe);
+                     mts, static_cast<const WT*>(w), up, gM, static_cast<WT*>(gw), gscale, gY, accumulate_gY,
+                     pos_s, gxe);
 }
 
 }  // namespace
@@ -523,13 +552,14 @@ void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int*
 }
 
 void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const int* sender, const float* Y,
-                        const float* Mt, int mts, const void* w, const float* up, const float* gM, float* gw,
-                        float* gY, int accumulate_gY, const int* pos_s, float* gxe, int half) {
+                        const float* Mt, int mts, const void* w, const float* up, const float* gM, void* gw,
+                        float* gscale, float* gY, int accumulate_gY, const int* pos_s, float* gxe, int half) {
   if (N <= 0) return;
 #define MACE_RECV(L, G)                                                                                          \
-  half ? launch_recv<L, G, _Float16>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gY, accumulate_gY, pos_s, \
-                                     gxe)                                                                        \
-       : launch_recv<L, G, float>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gY, accumulate_gY, pos_s, gxe)
+  half ? launch_recv<L, G, _Float16>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gscale, gY, accumulate_gY, \
+                                     pos_s, gxe)                                                                 \
+       : launch_recv<L, G, float>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gscale, gY, accumulate_gY,   \
+                                  pos_s, gxe)
   const bool gx = gxe != nullptr;
   switch (lin) {
     case 1: gx ? MACE_RECV(1, true) : MACE_RECV(1, false); break;
