@@ -459,18 +459,31 @@ __global__ void __launch_bounds__(256) k_forces(int N, const int* __restrict__ r
 // G[a][b] = sum_e v_e[a] g_e[b] summed over blocks in order; writes the
 // symmetrised virial dE/d(eps_sym) = (G + G^T) / 2 (calculators.py:536-561).
 // nblk == 0 writes zeros.
-__global__ void k_virial_reduce(const double* __restrict__ part, int nblk, double* __restrict__ vir) {
-  __shared__ double G[9];
-  const int k = threadIdx.x;
-  if (k < 9) {
-    double a = 0.0;
-    for (int b = 0; b < nblk; ++b) a += part[9 * b + k];
-    G[k] = a;
-  }
+// Sum of the per-block virial partials (one 256-thread block): thread t adds
+// partials t, t + 256, ... in order, then a fixed-order tree over the threads
+// (deterministic); the result is symmetrised.
+__global__ void __launch_bounds__(256) k_virial_reduce(const double* __restrict__ part, int nblk,
+                                                       double* __restrict__ vir) {
+  __shared__ double red[9][256];
+  const int t = threadIdx.x;
+  double a[9];
+#pragma unroll
+  for (int k = 0; k < 9; ++k) a[k] = 0.0;
+  for (int b = t; b < nblk; b += 256)
+#pragma unroll
+    for (int k = 0; k < 9; ++k) a[k] += part[9 * b + k];
+#pragma unroll
+  for (int k = 0; k < 9; ++k) red[k][t] = a[k];
   __syncthreads();
-  if (k < 9) {
-    const int r = k / 3, c = k % 3;
-    vir[k] = 0.5 * (G[3 * r + c] + G[3 * c + r]);
+  for (int off = 128; off > 0; off >>= 1) {
+    if (t < off)
+#pragma unroll
+      for (int k = 0; k < 9; ++k) red[k][t] += red[k][t + off];
+    __syncthreads();
+  }
+  if (t < 9) {
+    const int r = t / 3, c = t % 3;
+    vir[t] = 0.5 * (red[3 * r + c][0] + red[3 * c + r][0]);
   }
 }
 
@@ -585,7 +598,7 @@ void launch_gemm_group(hipStream_t st, GemmGroup& g) {
 }
 
 void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir) {
-  hipLaunchKernelGGL(k_virial_reduce, dim3(1), dim3(64), 0, st, part, nblk, vir);
+  hipLaunchKernelGGL(k_virial_reduce, dim3(1), dim3(256), 0, st, part, nblk, vir);
 }
 
 }  // namespace mace

@@ -487,22 +487,43 @@ __global__ void __launch_bounds__(NC) k_tp_gather_gx(int N, int din, const int* 
   gup[(int64_t)a * din + row * NC + u] = (s0 + s1) + (s2 + s3);
 }
 
-// Mt[e] = [M1 (3 x K1) | M2 (5 x K2)] from Y[e]; one thread per table entry.
-__global__ void __launch_bounds__(256) k_tp_tables(int64_t E, int nent, const float* __restrict__ Y,
-                                                   float* __restrict__ Mt, int mts) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= E * nent) return;
-  const int64_t e = t / nent;
-  const int q = (int)(t - e * nent);
-  const float* y = Y + e * 16;
-  float a = 0.f;
-  if (q < TP3_M1_NE) {
+// Mt[e] = [M1 (3 x K1) | M2 (5 x K2)] from Y[e].  Block of 64 edges: thread e
+// evaluates its edge's entries with compile-time CG terms into an LDS row, then
+// the block writes the 64 rows out coalesced.  NENT = 72 (M1) or 227 (M1 + M2).
+template <int NENT>
+__global__ void __launch_bounds__(64) k_tp_tables(int64_t E, const float* __restrict__ Y, float* __restrict__ Mt,
+                                                  int mts) {
+  constexpr int RS = NENT + 1;  // odd LDS row stride: conflict-free column writes
+  __shared__ float sT[64 * RS];
+  const int t = threadIdx.x;
+  const int64_t e0 = (int64_t)blockIdx.x * 64, e = e0 + t;
+  float y[16];
+  const float* ye = Y + min(e, E - 1) * 16;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) y[j] = ye[j];
+  float* row = sT + t * RS;
+#pragma unroll
+  for (int q = 0; q < TP3_M1_NE; ++q) {
+    float a = 0.f;
+#pragma unroll
     for (int x = m1s(q); x < m1s(q + 1); ++x) a = fmaf(y[m1j(x)], m1v(x), a);
-  } else {
-    const int r = q - TP3_M1_NE;
-    for (int x = m2s(r); x < m2s(r + 1); ++x) a = fmaf(y[m2j(x)], m2v(x), a);
+    row[q] = a;
   }
-  Mt[e * mts + q] = a;
+  if constexpr (NENT > TP3_M1_NE) {
+#pragma unroll
+    for (int q = 0; q < TP3_M2_NE; ++q) {
+      float a = 0.f;
+#pragma unroll
+      for (int x = m2s(q); x < m2s(q + 1); ++x) a = fmaf(y[m2j(x)], m2v(x), a);
+      row[TP3_M1_NE + q] = a;
+    }
+  }
+  __syncthreads();
+  const int nrow = (int)min<int64_t>(64, E - e0);
+  for (int i = t; i < nrow * NENT; i += 64) {
+    const int rr = i / NENT, q = i - rr * NENT;
+    Mt[(e0 + rr) * mts + q] = sT[rr * RS + q];
+  }
 }
 
 // groups per node for each number of input blocks
@@ -533,8 +554,11 @@ int tp_table_entries(int max_lin) { return max_lin >= 3 ? TP3_M1_NE + TP3_M2_NE 
 void launch_tp_tables(hipStream_t st, int64_t E, int max_lin, const float* Y, float* Mt, int mts) {
   const int nent = tp_table_entries(max_lin);
   if (E <= 0 || nent == 0) return;
-  const int64_t total = E * nent;
-  hipLaunchKernelGGL(k_tp_tables, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, E, nent, Y, Mt, mts);
+  const unsigned nb = (unsigned)((E + 63) / 64);
+  if (nent == TP3_M1_NE)
+    hipLaunchKernelGGL(k_tp_tables<TP3_M1_NE>, dim3(nb), dim3(64), 0, st, E, Y, Mt, mts);
+  else
+    hipLaunchKernelGGL(k_tp_tables<TP3_M1_NE + TP3_M2_NE>, dim3(nb), dim3(64), 0, st, E, Y, Mt, mts);
 }
 
 void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int* sender, const float* Y,
