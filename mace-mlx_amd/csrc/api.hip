@@ -79,6 +79,8 @@ struct Layer {
   DBuf<float> up[3], upT[3], skip[3], skipT[3], mlp[4], mlpT[4], lin_[4], linT[4], sc[3], plin[3], plinT[3];
   DBuf<float> ro, ro1, ro2;
   DBuf<_Float16> mlpT3h, mlp3h;  // fp16 copies of W3^T and W3 (float16 feature policy)
+  DBuf<_Float16> mlpT3x, mlp3x;  // [hi | lo] fp16 planes of W3^T and W3 scaled by 1 / w3inv (float32 policy)
+  float w3inv = 1.f;
   bool resid = true;       // residual block (skip from the input); else the skip acts on the message
   DBuf<float> mskip[4], mskipT[4], dens;
   int nskip = 0;
@@ -128,7 +130,8 @@ struct mace_ctx {
   DBuf<EdgeGeom> geom;
   DBuf<float> Y, Mt, ef, zbl_e, gY, gef, gv, gw, gxe, h3;
   DBuf<_Float16> h3h, gwh;  // radial-MLP hidden output, dL/dw under the float16 feature policy
-  DBuf<float> gscale;       // per-(edge, channel half) scale of gwh
+  DBuf<float> gscale;       // per-(edge, channel half) scale of gwh, or of gw as split fp16 planes
+  DBuf<float> h3inv;        // per-edge inverse scale of h3 as split fp16 pairs
   DBuf<double> vir_part;
   // node buffers
   std::vector<DBuf<float>> h;  // h[0..L]
@@ -149,6 +152,7 @@ struct mace_ctx {
     int flag = 0;
   };
   bool use_graphs = true;
+  bool split_mlp = true;  // float32 policy: radial-MLP output products on fp16 matrix cores (split operands)
   StepGraph g_fwd, g_bwd;
   // per-launch-site profiling
   bool profiling = false;
@@ -246,6 +250,19 @@ void upload_half(mace_ctx* c, DBuf<_Float16>& dst, const std::vector<float>& v) 
   HIPCHK(hipMemcpy(dst.p, h.data(), h.size() * sizeof(_Float16), hipMemcpyHostToDevice));
 }
 
+// v * scale as consecutive fp16 planes [hi | lo], hi = fp16(x), lo = fp16(x - hi)
+void upload_split(mace_ctx* c, DBuf<_Float16>& dst, const std::vector<float>& v, float scale) {
+  std::vector<_Float16> h(2 * v.size());
+  for (size_t i = 0; i < v.size(); ++i) {
+    const float x = v[i] * scale;
+    const _Float16 hi = (_Float16)x;
+    h[i] = hi;
+    h[v.size() + i] = (_Float16)(x - (float)hi);
+  }
+  dst.ensure(h.size());
+  HIPCHK(hipMemcpy(dst.p, h.data(), h.size() * sizeof(_Float16), hipMemcpyHostToDevice));
+}
+
 std::vector<float> transpose(const std::vector<float>& a, int rows, int cols, int batch = 1) {
   std::vector<float> t(a.size());
   for (int b = 0; b < batch; ++b)
@@ -263,7 +280,8 @@ void free_layers(mace_ctx* c) {
       for (int i = 0; i < 3; ++i) arr[i].release();
     for (int i = 0; i < 4; ++i) L.mlp[i].release(), L.mlpT[i].release(), L.lin_[i].release(), L.linT[i].release();
     L.ro.release(), L.ro1.release(), L.ro2.release(), L.h_up.release(), L.A.release(), L.w.release(),
-        L.ro_e.release(), L.wh.release(), L.mlpT3h.release(), L.mlp3h.release(), L.A2.release(), L.rinv.release(), L.dens.release();
+        L.ro_e.release(), L.wh.release(), L.mlpT3h.release(), L.mlp3h.release(), L.A2.release(), L.rinv.release(),
+        L.dens.release(), L.mlpT3x.release(), L.mlp3x.release();
     for (int i = 0; i < 4; ++i) L.mskip[i].release(), L.mskipT[i].release();
   }
   c->layers.clear();
@@ -338,6 +356,14 @@ void build_model(mace_ctx* c) {
           upload_half(c, L.mlpT3h, transpose(w, rows[k], cols[k]));
           upload_half(c, L.mlp3h, w);
         }
+        if (k == 3 && !d.feature_half) {  // split operands: largest magnitude scaled into [2^14, 2^15)
+          float m = 0.f;
+          for (float x : w) m = std::max(m, std::fabs(x));
+          const int ex = m > 0.f ? std::ilogb(m) : 0;
+          L.w3inv = std::ldexp(1.f, ex - 14);
+          upload_split(c, L.mlpT3x, transpose(w, rows[k], cols[k]), std::ldexp(1.f, 14 - ex));
+          upload_split(c, L.mlp3x, w, std::ldexp(1.f, 14 - ex));
+        }
       }
     }
     const int* l3 = tp_l3(L.lin);
@@ -401,7 +427,7 @@ void ensure_node_buffers(mace_ctx* c) {
   c->grho.ensure(N);
   c->ypre.ensure((size_t)N * 16);
   c->node_e.ensure(N);
-  c->e_part.ensure((N + 255) / 256 + 1);
+  c->e_part.ensure((N + 3) / 4 + 1);
   c->out.ensure(10 + 3 * (size_t)N);
   c->pos.ensure(3 * (size_t)N);
   if (c->out_pinned_n < (size_t)N) {
@@ -440,12 +466,12 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   c->gef.ensure(e * c->dims.num_bessel);
   c->h3.ensure(e * RADIAL_H);
   c->gv.ensure(e * 3);
-  if (half) {
+  if (half)
     c->gwh.ensure(e * maxw);
-    c->gscale.ensure(e * 2);
-  } else {
-    c->gw.ensure(e * maxw);
-  }
+  else
+    c->gw.ensure(e * maxw);  // split: hi and lo fp16 planes of E x wn each
+  c->gscale.ensure(e * 2);
+  c->h3inv.ensure(e);
   c->vir_part.ensure(9 * ((e + 255) / 256));
 }
 
@@ -810,6 +836,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
   const int64_t E = c->E;
   const int nb = c->dims.num_bessel;
   const int half = c->dims.feature_half != 0;
+  const bool split = !half && c->split_mlp;
   FrontParams fp = front_params(c);
   {
     Site s(c, "edge_fwd");
@@ -830,13 +857,17 @@ void forward(mace_ctx* c, const double* pos, double* out) {
     float* hn = c->h[l + 1].p;
     {
       Site s(c, lname("mlp_hidden", l));
+      // split: h3 holds E x 2 x 64 fp16 (the same bytes as E x 64 floats)
       launch_mlp_hidden(st, E, nb, c->ef.p, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p,
-                        half ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), half);
+                        half ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), c->h3inv.p,
+                        half ? 1 : split ? 2 : 0);
     }
     {
       Site s(c, lname("mlp_out", l));
       if (half)
         launch_mlp_out(st, E, L.wn, c->h3h.p, L.mlpT3h.p, L.wh.p, 1);
+      else if (split)
+        launch_mlp_out_x(st, E, L.wn, c->h3.p, c->h3inv.p, L.mlpT3x.p, L.w3inv, L.w.p);
       else
         launch_mlp_out(st, E, L.wn, c->h3.p, L.mlpT[3].p, L.w.p, 0);
     }
@@ -927,6 +958,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
   const int nb = c->dims.num_bessel;
   const int L = (int)c->layers.size();
   const int half = c->dims.feature_half != 0;
+  const bool split = !half && c->split_mlp;
   // dE/dh_L from the nonlinear readout
   float* gh = c->gh0.p;
   float* gh_next = c->gh1.p;
@@ -983,7 +1015,8 @@ void backward(mace_ctx* c, bool stress, double* out) {
       Site s(c, lname("tp_bwd", l));
       launch_tp_bwd_recv(st, Ly.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.wptr(half),
                          Ly.h_up.p, c->gM.p, half ? static_cast<void*>(c->gwh.p) : static_cast<void*>(c->gw.p),
-                         c->gscale.p, c->gY.p, first_edge_grad, c->pos_s.p, l > 0 ? c->gxe.p : nullptr, half);
+                         c->gscale.p, E * (int64_t)Ly.wn, c->gY.p, first_edge_grad, c->pos_s.p,
+                         l > 0 ? c->gxe.p : nullptr, half, split);
     }
     if (l > 0) {
       Site s(c, lname("tp_gather", l));
@@ -993,6 +1026,8 @@ void backward(mace_ctx* c, bool stress, double* out) {
       Site s(c, lname("mlp_gh3", l));
       if (half)
         launch_mlp_gh3_h(st, E, Ly.wn, c->gwh.p, c->gscale.p, Ly.mlp3h.p, c->h3.p);
+      else if (split)
+        launch_mlp_gh3_x(st, E, Ly.wn, c->gw.p, c->gscale.p, Ly.mlp3x.p, Ly.w3inv, c->h3.p);
       else
         launch_mlp_gh3(st, E, Ly.wn, c->gw.p, Ly.mlp[3].p, c->h3.p);
     }
@@ -1321,6 +1356,15 @@ int mace_set_graphs(mace_ctx* c, int32_t enable) {
     set_device(c);
     c->use_graphs = enable != 0;
     if (!c->use_graphs) invalidate_graphs(c);
+  });
+}
+
+int mace_set_mlp_split(mace_ctx* c, int32_t enable) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    set_device(c);
+    c->split_mlp = enable != 0;
+    invalidate_graphs(c);
   });
 }
 

@@ -68,17 +68,27 @@ void launch_density_edge_bwd(hipStream_t st, int64_t E, const int* receiver, con
                              const float* wd, const float* grho, float* gef);
 
 // radial MLP, ef (E x nb) -> w (E x W); weights [in][out] row-major, W3T = W3 transposed [W][64].
-// h3 [E][64] = silu(silu(silu(ef W0) W1) W2); w = h3 W3.  half (float16 feature policy): hidden
-// activations rounded to fp16, h3, W3T and w are fp16 arrays (fp32 accumulation); else fp32.
+// h3 [E][64] = silu(silu(silu(ef W0) W1) W2); w = h3 W3.  mode 0: fp32 h3; 1 (float16 feature
+// policy): hidden activations rounded to fp16, h3 fp16; 2: h3 as scaled fp16 hi/lo pairs
+// [E][2][64] with inverse row scales h3inv[E] (operand of launch_mlp_out_x).
 void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0,
-                       const float* W1, const float* W2, void* h3, int half);
+                       const float* W1, const float* W2, void* h3, float* h3inv, int mode);
+// half: h3, W3T and w fp16 arrays (fp32 accumulation); else fp32
 void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w,
                     int half);
+// float32 policy on fp16 matrix cores: w (fp32) from the split h3 of mode 2 and W3Tx = [hi | lo]
+// fp16 planes of W3^T [W][64] scaled by 1 / cscale
+void launch_mlp_out_x(hipStream_t st, int64_t E, int W, const void* h3x, const float* h3inv,
+                      const void* W3Tx, float cscale, float* w);
 // VJP: gh3 = gw W3^T, then gef (+)= dL/def through the recomputed hidden layers
 void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3);
 // float16 feature policy: gw fp16 with per-(edge, channel half) scales, W3 fp16 [64][W]
 void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const float* gscale, const void* W3h,
                       float* gh3);
+// float32 policy on fp16 matrix cores: gw as split planes (launch_tp_bwd_recv with split),
+// W3x = [hi | lo] fp16 planes of W3 [64][W] scaled by 1 / cscale
+void launch_mlp_gh3_x(hipStream_t st, int64_t E, int W, const void* gwx, const float* gscale, const void* W3x,
+                      float cscale, float* gh3);
 void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0,
                            const float* W1, const float* W2, const float* gh3, float* gef,
                            int accumulate, int half);
@@ -94,10 +104,12 @@ void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int*
 // TP VJP, receiver-centric; gY is [E][2][16] (per channel half).  With gxe != null the
 // per-edge input gradient is also stored, row pos_s[e] of gxe ([E][LIN^2 * NC], sender order).
 // half: w and gw are fp16, gw scaled per (edge, channel half) by 1 / gscale[e][half]
+// gw: float [E][W]; under the float16 policy (half) fp16 [E][W] scaled per (edge, channel
+// half) by gscale; with split, two fp16 planes hi / lo (lo at gw_lo elements) scaled likewise
 void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
                         const float* Y, const float* Mt, int mts, const void* w, const float* up,
-                        const float* gM, void* gw, float* gscale, float* gY, int accumulate_gY,
-                        const int* pos_s, float* gxe, int half);
+                        const float* gM, void* gw, float* gscale, int64_t gw_lo, float* gY, int accumulate_gY,
+                        const int* pos_s, float* gxe, int half, int split);
 // gup[a] = sum of the sender-ordered gxe rows of node a
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe,
                          float* gup);

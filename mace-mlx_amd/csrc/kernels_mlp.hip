@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -141,12 +142,18 @@ __device__ __forceinline__ void hidden_fwd(float (*X)[XP], const MlpW& sw, int64
 }
 
 // Waves walk 16-edge groups (grid-stride) after the block has staged W0..W2.
-// HT = float, or _Float16 under the float16 feature policy.
-template <typename HT>
+// Output h3 by MODE: H3_F32 float [E][64]; H3_F16 (float16 feature policy)
+// _Float16 [E][64]; H3_SPLIT (operand of the split-fp16 product) _Float16
+// [E][2][64]: row e scaled by a power of two that maps its largest magnitude into
+// [2^14, 2^15), then hi = fp16(v) in [e][0] and lo = fp16(v - hi) in [e][1];
+// h3inv[e] = the inverse scale.
+constexpr int H3_F32 = 0, H3_F16 = 1, H3_SPLIT = 2;
+
+template <int MODE>
 __global__ void __launch_bounds__(256) k_mlp_hidden(int64_t E, int nb, const float* __restrict__ ef,
                                                     const float* __restrict__ W0, const float* __restrict__ W1,
-                                                    const float* __restrict__ W2, HT* __restrict__ h3) {
-  constexpr bool HALF = sizeof(HT) == 2;
+                                                    const float* __restrict__ W2, void* __restrict__ h3v,
+                                                    float* __restrict__ h3inv) {
   __shared__ MlpW sw;
   __shared__ __align__(16) float sX[4][RT][XP];
   stage_weights(sw, nb, W0, W1, W2);
@@ -155,13 +162,38 @@ __global__ void __launch_bounds__(256) k_mlp_hidden(int64_t E, int nb, const flo
   for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
     const int64_t e0 = gi * RT;
     f4v a1[4], a2[4], a3[4];
-    hidden_fwd(sX[wv], sw, E, e0, nb, ef, a1, a2, a3, HALF);
+    hidden_fwd(sX[wv], sw, E, e0, nb, ef, a1, a2, a3, MODE == H3_F16);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t e = e0 + 4 * g + i;
-      if (e < E)
+      const int64_t e = e0 + 4 * g + i;  // row 4g + i lies in lanes 16g .. 16g + 15, columns 16t + r
+      if constexpr (MODE == H3_SPLIT) {
+        float v[4], m = 0.f;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) h3[e * H + 16 * t + r] = (HT)silu(a3[t][i]);
+        for (int t = 0; t < 4; ++t) {
+          v[t] = silu(a3[t][i]);
+          m = fmaxf(m, fabsf(v[t]));
+        }
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+        const int ex = m > 0.f ? ilogbf(m) : 0;
+        const float sc = ldexpf(1.f, 14 - ex);
+        if (e < E) {
+          _Float16* dst = static_cast<_Float16*>(h3v) + e * 2 * H;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float x = v[t] * sc;
+            const _Float16 hi = (_Float16)x;
+            dst[16 * t + r] = hi;
+            dst[H + 16 * t + r] = (_Float16)(x - (float)hi);
+          }
+          if (r == 0) h3inv[e] = ldexpf(1.f, ex - 14);
+        }
+      } else {
+        using HT = typename std::conditional<MODE == H3_F16, _Float16, float>::type;
+        if (e < E)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) static_cast<HT*>(h3v)[e * H + 16 * t + r] = (HT)silu(a3[t][i]);
+      }
     }
   }
 }
@@ -311,6 +343,99 @@ __global__ void __launch_bounds__(256) k_mlp_out_h(int64_t E, int W, const _Floa
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int c = 0; c < 2; ++c) b[u][c] = bn[u][c];
+  }
+}
+
+// Float32 policy on fp16 matrix cores: w[E][W] (fp32) = h3 @ W3 with both
+// operands split into fp16 pairs, a = a_hi + a_lo (h3 per-row scaled, see
+// k_mlp_hidden; W3 scaled by one power of two, cscale = its inverse), and
+//   a b ~ a_hi b_hi + a_hi b_lo + a_lo b_hi
+// on v_mfma_f32_16x16x32_f16 with fp32 accumulation (the dropped a_lo b_lo and
+// the split residuals are about 2^-22 of |a b|).  W3Tx = [hi | lo] planes of W3^T
+// [W][64].  Tiling, prefetch and the LDS-staged 128-byte row stores as in
+// k_mlp_out; the row scales are applied when the tile is staged.
+__global__ void __launch_bounds__(256) k_mlp_out_x(int64_t E, int W, const _Float16* __restrict__ h3x,
+                                                   const float* __restrict__ h3inv,
+                                                   const _Float16* __restrict__ W3Tx, float cscale,
+                                                   float* __restrict__ w) {
+  __shared__ __align__(16) float sO[4][64][36];
+  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * 64;
+  const int per = W / 8;
+  const int cb = blockIdx.y * (W / 2) + wv * per, ce = cb + per;
+  h8 ah[4][2], al[4][2];
+  float rs[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int64_t row = min(row0 + 16 * t + r, E - 1);  // rows past the end are computed, not stored
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      ah[t][c] = *reinterpret_cast<const h8*>(h3x + row * 2 * H + 32 * c + 8 * g);
+      al[t][c] = *reinterpret_cast<const h8*>(h3x + row * 2 * H + H + 32 * c + 8 * g);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rs[t][i] = h3inv[min(row0 + 16 * t + 4 * g + i, E - 1)] * cscale;
+  }
+  const _Float16* W3lo = W3Tx + (int64_t)W * H;
+  h8 bh[2][2], bl[2][2], bnh[2][2], bnl[2][2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int64_t o = (int64_t)min(cb + 16 * u + r, W - 1) * H + 32 * c + 8 * g;
+      bh[u][c] = *reinterpret_cast<const h8*>(W3Tx + o);
+      bl[u][c] = *reinterpret_cast<const h8*>(W3lo + o);
+    }
+  float(*O)[36] = sO[wv];
+  for (int c0 = cb; c0 < ce; c0 += 32) {
+    if (c0 + 32 < ce) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int64_t o = (int64_t)min(c0 + 32 + 16 * u + r, W - 1) * H + 32 * c + 8 * g;
+          bnh[u][c] = *reinterpret_cast<const h8*>(W3Tx + o);
+          bnl[u][c] = *reinterpret_cast<const h8*>(W3lo + o);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the multiplies
+    f4v o[4][2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) o[t][u] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          o[t][u] = mfma16h(ah[t][c], bl[u][c], o[t][u]);
+          o[t][u] = mfma16h(al[t][c], bh[u][c], o[t][u]);
+          o[t][u] = mfma16h(ah[t][c], bh[u][c], o[t][u]);
+        }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) O[16 * t + 4 * g + i][16 * u + r] = o[t][u][i] * rs[t][i];
+    wave_sync();
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {  // lane l: row l/8 + 8q, columns 4 (l%8) .. + 3
+      const int rr = (l >> 3) + 8 * q;
+      const int64_t row = row0 + rr;
+      if (row < E && c0 + 4 * (l & 7) < ce)
+        *reinterpret_cast<float4*>(&w[row * W + c0 + 4 * (l & 7)]) = ld4(&O[rr][4 * (l & 7)]);
+    }
+    wave_sync();
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        bh[u][c] = bnh[u][c];
+        bl[u][c] = bnl[u][c];
+      }
   }
 }
 
@@ -472,6 +597,118 @@ __global__ void __launch_bounds__(256) k_mlp_gh3_h(int64_t E, int W, const _Floa
   }
 }
 
+// Float32 policy on fp16 matrix cores: gh3 = gw @ W3^T with gw given as the
+// scaled split pair of k_tp_bwd_recv (hi plane gwx, lo plane gwx + E W; row
+// scales gscale[e][channel half]) and W3x = [hi | lo] planes of W3 [64][W]
+// scaled by 1 / cscale; three fp16 products per pair as in k_mlp_out_x.  Block
+// = 32 edges, K split over the 4 waves, gw chunks loaded GX_PF ahead; the two
+// channel halves accumulate separately and are combined with their row scales
+// before the fixed-order cross-wave sum.
+constexpr int GX_PF = 2;
+
+__global__ void __launch_bounds__(256) k_mlp_gh3_x(int64_t E, int W, const _Float16* __restrict__ gwx,
+                                                   const float* __restrict__ gscale,
+                                                   const _Float16* __restrict__ W3x, float cscale,
+                                                   float* __restrict__ gh3) {
+  __shared__ f4v sP[4][8][64];
+  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * 32, lo_a = E * (int64_t)W, lo_b = (int64_t)H * W;
+  const int kq = W / 4, kb = wv * kq, nch = kq / 32;
+  const _Float16* ar[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t row = min(row0 + 16 * t + r, E - 1);  // rows past the end are computed, not stored
+    ar[t] = gwx + row * (int64_t)W + kb + 8 * g;
+  }
+  const _Float16* br = W3x + (int64_t)r * W + kb + 8 * g;
+  h8 ring[GX_PF][2][2], b[4][2], bn[4][2];  // [.][row tile][hi, lo]
+#pragma unroll
+  for (int p = 0; p < GX_PF; ++p)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int64_t o = 32 * min(p, nch - 1);
+      ring[p][t][0] = *reinterpret_cast<const h8*>(ar[t] + o);
+      ring[p][t][1] = *reinterpret_cast<const h8*>(ar[t] + lo_a + o);
+    }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    b[u][0] = *reinterpret_cast<const h8*>(br + (int64_t)16 * u * W);
+    b[u][1] = *reinterpret_cast<const h8*>(br + lo_b + (int64_t)16 * u * W);
+  }
+  f4v acc[2][2][4];  // [channel half][row tile][column tile]
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[hh][t][u] = f4v{0.f, 0.f, 0.f, 0.f};
+  for (int ch = 0; ch < nch; ch += GX_PF) {
+#pragma unroll
+    for (int p = 0; p < GX_PF; ++p) {
+      const int cc = ch + p;
+      if (cc < nch) {
+        const int nbk = min(cc + 1, nch - 1), na = min(cc + GX_PF, nch - 1);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int64_t o = (int64_t)16 * u * W + 32 * nbk;
+          bn[u][0] = *reinterpret_cast<const h8*>(br + o);
+          bn[u][1] = *reinterpret_cast<const h8*>(br + lo_b + o);
+        }
+        h8 cur[2][2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          cur[t][0] = ring[p][t][0];
+          cur[t][1] = ring[p][t][1];
+          ring[p][t][0] = *reinterpret_cast<const h8*>(ar[t] + 32 * na);
+          ring[p][t][1] = *reinterpret_cast<const h8*>(ar[t] + lo_a + 32 * na);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the multiplies
+        const int hh = ((kb + 32 * cc) & 64) ? 1 : 0;  // channel half of this chunk (uniform)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            f4v a = hh ? acc[1][t][u] : acc[0][t][u];
+            a = mfma16h(cur[t][0], b[u][1], a);
+            a = mfma16h(cur[t][1], b[u][0], a);
+            a = mfma16h(cur[t][0], b[u][0], a);
+            if (hh)
+              acc[1][t][u] = a;
+            else
+              acc[0][t][u] = a;
+          }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          b[u][0] = bn[u][0];
+          b[u][1] = bn[u][1];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t row = min(row0 + 16 * t + 4 * g + i, E - 1);
+      const float s0 = gscale[2 * row] * cscale, s1 = gscale[2 * row + 1] * cscale;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[0][t][u][i] = acc[0][t][u][i] * s0 + acc[1][t][u][i] * s1;
+    }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) sP[wv][t][l] = acc[0][t >> 2][t & 3];
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int t = 2 * wv + h, rt = t >> 2, ct = t & 3;
+    const f4v sm = ((sP[0][t][l] + sP[1][t][l]) + sP[2][t][l]) + sP[3][t][l];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t row = row0 + 16 * rt + 4 * g + i;
+      if (row < E) gh3[row * H + 16 * ct + r] = sm[i];
+    }
+  }
+}
+
 // dL/def from dL/dh3: recompute a1..a3, then
 //   g_a3 = g_h3 * silu'(a3), g_a2 = (g_a3 W2^T) * silu'(a2),
 //   g_a1 = (g_a2 W1^T) * silu'(a1), g_ef = g_a1 W0^T
@@ -544,14 +781,15 @@ inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
 inline unsigned hidden_grid(int64_t E) { return (unsigned)std::min<int64_t>((E + 63) / 64, 512); }
 
 void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0, const float* W1,
-                       const float* W2, void* h3, int half) {
+                       const float* W2, void* h3, float* h3inv, int mode) {
   if (E <= 0) return;
-  if (half)
-    hipLaunchKernelGGL(k_mlp_hidden<_Float16>, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, W0, W1, W2,
-                       static_cast<_Float16*>(h3));
+  const dim3 grid(hidden_grid(E)), blk(256);
+  if (mode == H3_SPLIT)
+    hipLaunchKernelGGL(k_mlp_hidden<H3_SPLIT>, grid, blk, 0, st, E, nb, ef, W0, W1, W2, h3, h3inv);
+  else if (mode == H3_F16)
+    hipLaunchKernelGGL(k_mlp_hidden<H3_F16>, grid, blk, 0, st, E, nb, ef, W0, W1, W2, h3, h3inv);
   else
-    hipLaunchKernelGGL(k_mlp_hidden<float>, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, W0, W1, W2,
-                       static_cast<float*>(h3));
+    hipLaunchKernelGGL(k_mlp_hidden<H3_F32>, grid, blk, 0, st, E, nb, ef, W0, W1, W2, h3, h3inv);
 }
 
 void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w, int half) {
@@ -564,9 +802,23 @@ void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void
                        static_cast<const float*>(W3T), static_cast<float*>(w));
 }
 
+void launch_mlp_out_x(hipStream_t st, int64_t E, int W, const void* h3x, const float* h3inv, const void* W3Tx,
+                      float cscale, float* w) {
+  if (E <= 0) return;
+  hipLaunchKernelGGL(k_mlp_out_x, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const _Float16*>(h3x),
+                     h3inv, static_cast<const _Float16*>(W3Tx), cscale, w);
+}
+
 void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3) {
   if (E <= 0) return;
   hipLaunchKernelGGL(k_mlp_gh3, dim3(nblk(E, 32)), dim3(256), 0, st, E, W, gw, W3, gh3);
+}
+
+void launch_mlp_gh3_x(hipStream_t st, int64_t E, int W, const void* gwx, const float* gscale, const void* W3x,
+                      float cscale, float* gh3) {
+  if (E <= 0) return;
+  hipLaunchKernelGGL(k_mlp_gh3_x, dim3(nblk(E, 32)), dim3(256), 0, st, E, W, static_cast<const _Float16*>(gwx),
+                     gscale, static_cast<const _Float16*>(W3x), cscale, gh3);
 }
 
 void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const float* gscale, const void* W3h,

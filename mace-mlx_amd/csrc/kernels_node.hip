@@ -380,31 +380,29 @@ struct RoPtrs {
   const float* p[4];
 };
 
+// one wavefront per atom: the pair-repulsion energies of the atom's received edges are read
+// coalesced and summed by a fixed shuffle tree; block partial = sum of its four atoms
 __global__ void __launch_bounds__(256) k_node_energy(int N, const int* __restrict__ species,
                                                      const float* __restrict__ e0, const int* __restrict__ rowptr,
                                                      const float* __restrict__ zbl_e, RoPtrs ro, int nro,
                                                      float* __restrict__ node_e, double* __restrict__ part) {
-  __shared__ double red[256];
-  const int n = blockIdx.x * 256 + threadIdx.x;
+  __shared__ double red[4];
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + w;
   double acc = 0.0;
-  if (n < N) {
-    float v = e0[species[n]];
-    if (zbl_e) {
-      float z = 0.f;
-      for (int e = rowptr[n]; e < rowptr[n + 1]; ++e) z += zbl_e[e];
-      v += z;
-    }
-    for (int l = 0; l < nro; ++l) v += ro.p[l][n];
-    node_e[n] = v;
+  if (n < N) {  // wave-uniform
+    float z = 0.f;
+    if (zbl_e)
+      for (int e = rowptr[n] + l; e < rowptr[n + 1]; e += 64) z += zbl_e[e];
+    z = wave_sum(z);
+    float v = e0[species[n]] + z;
+    for (int k = 0; k < nro; ++k) v += ro.p[k][n];
+    if (l == 0) node_e[n] = v;
     acc = (double)v;
   }
-  red[threadIdx.x] = acc;
+  if (l == 0) red[w] = acc;
   __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) part[blockIdx.x] = red[0];
+  if (threadIdx.x == 0) part[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 // fixed-order sum of block partials (deterministic)
@@ -564,7 +562,7 @@ void launch_node_energy(hipStream_t st, int N, const int* species, const float* 
                         double* energy) {
   RoPtrs r{{nullptr, nullptr, nullptr, nullptr}};
   for (int l = 0; l < nro && l < 4; ++l) r.p[l] = ro[l];
-  const int nblk = (int)cdiv(N, 256);
+  const int nblk = (int)cdiv(N, 4);
   if (nblk > 0)
     hipLaunchKernelGGL(k_node_energy, dim3(nblk), dim3(256), 0, st, N, species, e0, rowptr, zbl_e, r, nro, node_e,
                        part);

@@ -23,6 +23,13 @@ def build(jobs: int = 4, verbose: bool = False) -> Path:
         sys.stderr.write((proc.stdout or "") + (proc.stderr or ""))
         raise RuntimeError("HIP engine build failed")
     from ._ffi import LIB_PATH
+    # every kernel the host registers must exist in the gfx950 code object (the HIP runtime
+    # aborts at the first launch of one that does not)
+    chk = subprocess.run([sys.executable, str(CSRC / "check_kernel_symbols.py"), str(LIB_PATH)],
+                         capture_output=True, text=True)
+    if chk.returncode != 0:
+        sys.stderr.write(chk.stdout + chk.stderr)
+        raise RuntimeError("HIP engine build: host / device kernel names differ")
     return LIB_PATH
 
 

@@ -43,3 +43,31 @@ def test_model_dims_struct_matches_header():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(ImportError):
         _ffi.load_library(str(tmp_path / "nope.so"))
+
+
+def _symcheck():
+    import importlib.util
+    p = Path(__file__).resolve().parents[1] / "mace-mlx_amd" / "csrc" / "check_kernel_symbols.py"
+    spec = importlib.util.spec_from_file_location("check_kernel_symbols", p)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_every_registered_kernel_is_in_the_gfx950_code_object():
+    """The HIP runtime aborts at the first launch of a kernel whose host-registered
+    (mangled) name is absent from the device code object; host and device mangle
+    differently when a kernel parameter type depends on an unnamed enum."""
+    chk = _symcheck()
+    assert chk.check(_ffi.LIB_PATH) == []
+
+
+def test_symbol_check_detects_a_missing_kernel():
+    """Plant a mismatch: drop one kernel from the device-name set the check compares with."""
+    chk = _symcheck()
+    data = Path(_ffi.LIB_PATH).read_bytes()
+    host, dev = chk.host_kernels(data), chk.device_kernels(data)
+    assert host and host <= dev
+    victim = sorted(host)[0]
+    assert sorted(host - (dev - {victim})) == [victim]
+    assert any("k_tp_bwd_recv" in h for h in host) and any("k_mlp_out" in h for h in host)
