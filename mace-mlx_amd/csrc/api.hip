@@ -130,7 +130,7 @@ struct mace_ctx {
   DBuf<EdgeGeom> geom;
   DBuf<float> Y, Mt, ef, zbl_e, gY, gef, gv, gw, gxe, h3;
   DBuf<_Float16> h3h, gwh;  // radial-MLP hidden output, dL/dw under the float16 feature policy
-  DBuf<float> gscale;       // per-(edge, channel half) scale of gwh, or of gw as split fp16 planes
+  DBuf<float> gscale;       // per-(edge, channel half) scale of gwh
   DBuf<float> h3inv;        // per-edge inverse scale of h3 as split fp16 pairs
   DBuf<double> vir_part;
   // node buffers
@@ -469,7 +469,7 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   if (half)
     c->gwh.ensure(e * maxw);
   else
-    c->gw.ensure(e * maxw);  // split: hi and lo fp16 planes of E x wn each
+    c->gw.ensure(e * maxw);
   c->gscale.ensure(e * 2);
   c->h3inv.ensure(e);
   c->vir_part.ensure(9 * ((e + 255) / 256));
@@ -1015,8 +1015,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
       Site s(c, lname("tp_bwd", l));
       launch_tp_bwd_recv(st, Ly.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.wptr(half),
                          Ly.h_up.p, c->gM.p, half ? static_cast<void*>(c->gwh.p) : static_cast<void*>(c->gw.p),
-                         c->gscale.p, E * (int64_t)Ly.wn, c->gY.p, first_edge_grad, c->pos_s.p,
-                         l > 0 ? c->gxe.p : nullptr, half, split);
+                         c->gscale.p, c->gY.p, first_edge_grad, c->pos_s.p, l > 0 ? c->gxe.p : nullptr, half);
     }
     if (l > 0) {
       Site s(c, lname("tp_gather", l));
@@ -1027,7 +1026,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
       if (half)
         launch_mlp_gh3_h(st, E, Ly.wn, c->gwh.p, c->gscale.p, Ly.mlp3h.p, c->h3.p);
       else if (split)
-        launch_mlp_gh3_x(st, E, Ly.wn, c->gw.p, c->gscale.p, Ly.mlp3x.p, Ly.w3inv, c->h3.p);
+        launch_mlp_gh3_x(st, E, Ly.wn, c->gw.p, Ly.mlp3x.p, Ly.w3inv, c->h3.p);
       else
         launch_mlp_gh3(st, E, Ly.wn, c->gw.p, Ly.mlp[3].p, c->h3.p);
     }

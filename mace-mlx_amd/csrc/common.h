@@ -85,10 +85,10 @@ void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const flo
 // float16 feature policy: gw fp16 with per-(edge, channel half) scales, W3 fp16 [64][W]
 void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const float* gscale, const void* W3h,
                       float* gh3);
-// float32 policy on fp16 matrix cores: gw as split planes (launch_tp_bwd_recv with split),
-// W3x = [hi | lo] fp16 planes of W3 [64][W] scaled by 1 / cscale
-void launch_mlp_gh3_x(hipStream_t st, int64_t E, int W, const void* gwx, const float* gscale, const void* W3x,
-                      float cscale, float* gh3);
+// float32 policy on fp16 matrix cores: gw fp32 [E][W] (split per edge and 32-wide k chunk in the
+// kernel), W3x = [hi | lo] fp16 planes of W3 [64][W] scaled by 1 / cscale
+void launch_mlp_gh3_x(hipStream_t st, int64_t E, int W, const float* gw, const void* W3x, float cscale,
+                      float* gh3);
 void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0,
                            const float* W1, const float* W2, const float* gh3, float* gef,
                            int accumulate, int half);
@@ -104,12 +104,12 @@ void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int*
 // TP VJP, receiver-centric; gY is [E][2][16] (per channel half).  With gxe != null the
 // per-edge input gradient is also stored, row pos_s[e] of gxe ([E][LIN^2 * NC], sender order).
 // half: w and gw are fp16, gw scaled per (edge, channel half) by 1 / gscale[e][half]
-// gw: float [E][W]; under the float16 policy (half) fp16 [E][W] scaled per (edge, channel
-// half) by gscale; with split, two fp16 planes hi / lo (lo at gw_lo elements) scaled likewise
+// gw: float [E][W], or under the float16 policy (half) fp16 [E][W] scaled per (edge, channel
+// half) by gscale
 void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
                         const float* Y, const float* Mt, int mts, const void* w, const float* up,
-                        const float* gM, void* gw, float* gscale, int64_t gw_lo, float* gY, int accumulate_gY,
-                        const int* pos_s, float* gxe, int half, int split);
+                        const float* gM, void* gw, float* gscale, float* gY, int accumulate_gY,
+                        const int* pos_s, float* gxe, int half);
 // gup[a] = sum of the sender-ordered gxe rows of node a
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe,
                          float* gup);

@@ -597,116 +597,102 @@ __global__ void __launch_bounds__(256) k_mlp_gh3_h(int64_t E, int W, const _Floa
   }
 }
 
-// Float32 policy on fp16 matrix cores: gh3 = gw @ W3^T with gw given as the
-// scaled split pair of k_tp_bwd_recv (hi plane gwx, lo plane gwx + E W; row
-// scales gscale[e][channel half]) and W3x = [hi | lo] planes of W3 [64][W]
-// scaled by 1 / cscale; three fp16 products per pair as in k_mlp_out_x.  Block
-// = 32 edges, K split over the 4 waves, gw chunks loaded GX_PF ahead; the two
-// channel halves accumulate separately and are combined with their row scales
-// before the fixed-order cross-wave sum.
+// Float32 policy on fp16 matrix cores: gh3 = gw @ W3^T from the fp32 gradient gw
+// [E][W].  Each wave runs the whole K loop for 16 edges in 32-wide chunks; the
+// block stages each chunk of W3x = [hi | lo] planes of W3 [64][W] (scaled by
+// 1 / cscale) in LDS, double-buffered.  Operand roles are swapped (A = W3 rows
+// j, B = gw^T with the edges as columns), so lane (g, r) owns edge r's eight k
+// values of the chunk and the output column of that edge: it scales them by the
+// power of two that maps the chunk's largest |gw| of the edge (reduced over the
+// four lanes of the edge) into [2^14, 2^15), splits them into fp16 hi + lo and
+// folds the inverse scale into its accumulators after the chunk's three products
+//   W3_hi x gw_lo + W3_lo x gw_hi + W3_hi x gw_hi
+// (about 2^-22 relative per product).  gw loaded GX_PF chunks ahead.
 constexpr int GX_PF = 2;
 
-__global__ void __launch_bounds__(256) k_mlp_gh3_x(int64_t E, int W, const _Float16* __restrict__ gwx,
-                                                   const float* __restrict__ gscale,
+__global__ void __launch_bounds__(256) k_mlp_gh3_x(int64_t E, int W, const float* __restrict__ gw,
                                                    const _Float16* __restrict__ W3x, float cscale,
                                                    float* __restrict__ gh3) {
-  __shared__ f4v sP[4][8][64];
+  __shared__ __align__(16) _Float16 sB[2][2][H][32];  // [buffer][hi, lo][j][k of the chunk]
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
-  const int64_t row0 = (int64_t)blockIdx.x * 32, lo_a = E * (int64_t)W, lo_b = (int64_t)H * W;
-  const int kq = W / 4, kb = wv * kq, nch = kq / 32;
-  const _Float16* ar[2];
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wv) * 16, lo_b = (int64_t)H * W;
+  const int nch = W / 32;
+  const float* ar = gw + min(row0 + r, E - 1) * (int64_t)W + 8 * g;  // rows past the end: computed, not stored
+  const int bj = threadIdx.x >> 2, bk = 8 * (threadIdx.x & 3);      // staging: one 8-wide k piece of row bj
+  const _Float16* bsrc = W3x + (int64_t)bj * W + bk;
+  float4 ring[GX_PF][2];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int64_t row = min(row0 + 16 * t + r, E - 1);  // rows past the end are computed, not stored
-    ar[t] = gwx + row * (int64_t)W + kb + 8 * g;
+  for (int p = 0; p < GX_PF; ++p) {
+    const float* q = ar + 32 * min(p, nch - 1);
+    ring[p][0] = ld4(q);
+    ring[p][1] = ld4(q + 4);
   }
-  const _Float16* br = W3x + (int64_t)r * W + kb + 8 * g;
-  h8 ring[GX_PF][2][2], b[4][2], bn[4][2];  // [.][row tile][hi, lo]
+  h8 st0 = *reinterpret_cast<const h8*>(bsrc), st1 = *reinterpret_cast<const h8*>(bsrc + lo_b);
+  *reinterpret_cast<h8*>(&sB[0][0][bj][bk]) = st0;
+  *reinterpret_cast<h8*>(&sB[0][1][bj][bk]) = st1;
+  __syncthreads();
+  f4v acc[4];
 #pragma unroll
-  for (int p = 0; p < GX_PF; ++p)
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int64_t o = 32 * min(p, nch - 1);
-      ring[p][t][0] = *reinterpret_cast<const h8*>(ar[t] + o);
-      ring[p][t][1] = *reinterpret_cast<const h8*>(ar[t] + lo_a + o);
-    }
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    b[u][0] = *reinterpret_cast<const h8*>(br + (int64_t)16 * u * W);
-    b[u][1] = *reinterpret_cast<const h8*>(br + lo_b + (int64_t)16 * u * W);
-  }
-  f4v acc[2][2][4];  // [channel half][row tile][column tile]
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int u = 0; u < 4; ++u) acc[hh][t][u] = f4v{0.f, 0.f, 0.f, 0.f};
+  for (int u = 0; u < 4; ++u) acc[u] = f4v{0.f, 0.f, 0.f, 0.f};
   for (int ch = 0; ch < nch; ch += GX_PF) {
 #pragma unroll
     for (int p = 0; p < GX_PF; ++p) {
       const int cc = ch + p;
-      if (cc < nch) {
-        const int nbk = min(cc + 1, nch - 1), na = min(cc + GX_PF, nch - 1);
+      if (cc < nch) {  // uniform over the block
+        const int buf = cc & 1;
+        if (cc + 1 < nch) {
+          st0 = *reinterpret_cast<const h8*>(bsrc + 32 * (cc + 1));
+          st1 = *reinterpret_cast<const h8*>(bsrc + lo_b + 32 * (cc + 1));
+        }
+        const float4 c0 = ring[p][0], c1 = ring[p][1];
+        {
+          const float* q = ar + 32 * min(cc + GX_PF, nch - 1);
+          ring[p][0] = ld4(q);
+          ring[p][1] = ld4(q + 4);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the arithmetic
+        const float v[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        float m = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(v[q]));
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        // floor(log2 m) from the exponent field; zero / subnormal chunks take -100 (finite scales)
+        const int ex = max((int)((__float_as_uint(m) >> 23) & 0xff) - 127, -100);
+        const float sc = __uint_as_float((unsigned)(127 + 14 - ex) << 23);
+        const float inv = __uint_as_float((unsigned)(127 - 14 + ex) << 23);
+        h8 xh, xl;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const float x = v[q] * sc;
+          const _Float16 hi = (_Float16)x;
+          xh[q] = hi;
+          xl[q] = (_Float16)(x - (float)hi);
+        }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          const int64_t o = (int64_t)16 * u * W + 32 * nbk;
-          bn[u][0] = *reinterpret_cast<const h8*>(br + o);
-          bn[u][1] = *reinterpret_cast<const h8*>(br + lo_b + o);
+          const h8 wh = *reinterpret_cast<const h8*>(&sB[buf][0][16 * u + r][8 * g]);
+          const h8 wl = *reinterpret_cast<const h8*>(&sB[buf][1][16 * u + r][8 * g]);
+          f4v d = mfma16h(wl, xh, f4v{0.f, 0.f, 0.f, 0.f});
+          d = mfma16h(wh, xl, d);
+          d = mfma16h(wh, xh, d);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[u][i] = fmaf(d[i], inv, acc[u][i]);
         }
-        h8 cur[2][2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          cur[t][0] = ring[p][t][0];
-          cur[t][1] = ring[p][t][1];
-          ring[p][t][0] = *reinterpret_cast<const h8*>(ar[t] + 32 * na);
-          ring[p][t][1] = *reinterpret_cast<const h8*>(ar[t] + lo_a + 32 * na);
+        if (cc + 1 < nch) {
+          *reinterpret_cast<h8*>(&sB[buf ^ 1][0][bj][bk]) = st0;
+          *reinterpret_cast<h8*>(&sB[buf ^ 1][1][bj][bk]) = st1;
         }
-        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the multiplies
-        const int hh = ((kb + 32 * cc) & 64) ? 1 : 0;  // channel half of this chunk (uniform)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            f4v a = hh ? acc[1][t][u] : acc[0][t][u];
-            a = mfma16h(cur[t][0], b[u][1], a);
-            a = mfma16h(cur[t][1], b[u][0], a);
-            a = mfma16h(cur[t][0], b[u][0], a);
-            if (hh)
-              acc[1][t][u] = a;
-            else
-              acc[0][t][u] = a;
-          }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          b[u][0] = bn[u][0];
-          b[u][1] = bn[u][1];
-        }
+        __syncthreads();
       }
     }
   }
+  const int64_t row = row0 + r;  // lane (g, r) holds gh3[row][16u + 4g + i]
+  if (row < E)
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t row = min(row0 + 16 * t + 4 * g + i, E - 1);
-      const float s0 = gscale[2 * row] * cscale, s1 = gscale[2 * row + 1] * cscale;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) acc[0][t][u][i] = acc[0][t][u][i] * s0 + acc[1][t][u][i] * s1;
-    }
-#pragma unroll
-  for (int t = 0; t < 8; ++t) sP[wv][t][l] = acc[0][t >> 2][t & 3];
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int t = 2 * wv + h, rt = t >> 2, ct = t & 3;
-    const f4v sm = ((sP[0][t][l] + sP[1][t][l]) + sP[2][t][l]) + sP[3][t][l];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t row = row0 + 16 * rt + 4 * g + i;
-      if (row < E) gh3[row * H + 16 * ct + r] = sm[i];
-    }
-  }
+    for (int u = 0; u < 4; ++u)
+      *reinterpret_cast<float4*>(gh3 + row * H + 16 * u + 4 * g) =
+          float4{acc[u][0] * cscale, acc[u][1] * cscale, acc[u][2] * cscale, acc[u][3] * cscale};
 }
 
 // dL/def from dL/dh3: recompute a1..a3, then
@@ -814,11 +800,11 @@ void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const flo
   hipLaunchKernelGGL(k_mlp_gh3, dim3(nblk(E, 32)), dim3(256), 0, st, E, W, gw, W3, gh3);
 }
 
-void launch_mlp_gh3_x(hipStream_t st, int64_t E, int W, const void* gwx, const float* gscale, const void* W3x,
-                      float cscale, float* gh3) {
+void launch_mlp_gh3_x(hipStream_t st, int64_t E, int W, const float* gw, const void* W3x, float cscale,
+                      float* gh3) {
   if (E <= 0) return;
-  hipLaunchKernelGGL(k_mlp_gh3_x, dim3(nblk(E, 32)), dim3(256), 0, st, E, W, static_cast<const _Float16*>(gwx),
-                     gscale, static_cast<const _Float16*>(W3x), cscale, gh3);
+  hipLaunchKernelGGL(k_mlp_gh3_x, dim3(nblk(E, 64)), dim3(256), 0, st, E, W, gw,
+                     static_cast<const _Float16*>(W3x), cscale, gh3);
 }
 
 void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const float* gscale, const void* W3h,

@@ -27,8 +27,6 @@
 // adds the two halves.
 #include <hip/hip_runtime.h>
 
-#include <type_traits>
-
 #include "common.h"
 
 namespace mace {
@@ -291,23 +289,15 @@ __device__ __forceinline__ float wave_sum16(const float* v) {
   return d;
 }
 
-// Storage of dL/dw.  GW_F32: float.  GW_F16 (float16 feature policy) and
-// GW_SPLIT (float32 policy, for the split-fp16 gradient product): each wave
-// scales its 64 channels x slots by a power of two that maps their largest
-// magnitude into [2^14, 2^15) (so small gradients keep fp16 precision) and
-// stores the inverse in gscale[e][half]; GW_F16 keeps the fp16 value, GW_SPLIT
-// the pair hi = fp16(v), lo = fp16(v - hi) (hi in one plane, lo in a second
-// plane gw_lo elements further), which represents v to about 2^-22 relative.
-constexpr int GW_F32 = 0, GW_F16 = 1, GW_SPLIT = 2;
-
-template <int GWM>
-using gw_t = typename std::conditional<GWM == GW_F32, float, _Float16>::type;
-
-// dL/dw of one edge and channel (all slots) into row gwe (stride NC).
-template <int NSLOT, int GWM>
-__device__ __forceinline__ void store_gw(const float* gws, gw_t<GWM>* __restrict__ gwe, float* __restrict__ gscale,
-                                         int64_t e, int u, int64_t gw_lo) {
-  if constexpr (GWM == GW_F32) {
+// dL/dw of one edge and channel (all slots) into row gwe (stride NC).  GWT =
+// float, or _Float16 under the float16 feature policy: each wave then scales
+// its 64 channels x slots by a power of two that maps their largest magnitude
+// into [2^14, 2^15) (so small gradients keep fp16 precision) and stores the
+// inverse in gscale[e][half].
+template <int NSLOT, typename GWT>
+__device__ __forceinline__ void store_gw(const float* gws, GWT* __restrict__ gwe, float* __restrict__ gscale,
+                                         int64_t e, int u) {
+  if constexpr (sizeof(GWT) == 4) {
 #pragma unroll
     for (int s = 0; s < NSLOT; ++s) gwe[s * NC] = gws[s];
   } else {
@@ -319,12 +309,7 @@ __device__ __forceinline__ void store_gw(const float* gws, gw_t<GWM>* __restrict
     const int ex = m > 0.f ? ilogbf(m) : 0;
     const float sc = ldexpf(1.f, 14 - ex);
 #pragma unroll
-    for (int s = 0; s < NSLOT; ++s) {
-      const float v = gws[s] * sc;
-      const _Float16 hi = (_Float16)v;
-      gwe[s * NC] = hi;
-      if constexpr (GWM == GW_SPLIT) gwe[gw_lo + s * NC] = (_Float16)(v - (float)hi);
-    }
+    for (int s = 0; s < NSLOT; ++s) gwe[s * NC] = (GWT)(gws[s] * sc);
     if ((u & 63) == 0) gscale[e * 2 + (u >> 6)] = ldexpf(1.f, ex - 14);
   }
 }
@@ -409,20 +394,17 @@ __device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& i
 // is stored in sender order (pos_s = inverse of the sender permutation), so
 // k_tp_gather_gx sums each node's rows as one contiguous segment.  Without GX
 // (first interaction: constant embedding input) only dL/dw and dL/dY are made.
-template <int LIN, int NG, bool GX, typename WT, int GWM>
+template <int LIN, int NG, bool GX, typename WT>
 __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __restrict__ rowptr,
                                                         const int* __restrict__ sender, const float* __restrict__ Y,
                                                         const float* __restrict__ Mt, int mts,
                                                         const WT* __restrict__ w, const float* __restrict__ up,
-                                                        const float* __restrict__ gM, void* __restrict__ gwv,
-                                                        float* __restrict__ gscale, int64_t gw_lo,
+                                                        const float* __restrict__ gM, WT* __restrict__ gw,
+                                                        float* __restrict__ gscale,
                                                         float* __restrict__ gY, int accumulate_gY,
                                                         const int* __restrict__ pos_s, float* __restrict__ gxe) {
   using T = TPT<LIN>;
   constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, WN = NC * T::NSLOT;
-  // (void* in the signature: kernel parameter types must not depend on the
-  // template arguments, or host and device may mangle the name differently)
-  gw_t<GWM>* __restrict__ gw = static_cast<gw_t<GWM>*>(gwv);
   const int n = blockIdx.x, g = group_id(), u = threadIdx.x % NC;
   int gb, ge;
   group_range<NG>(rowptr[n], rowptr[n + 1], g, gb, ge);
@@ -460,7 +442,7 @@ __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __rest
     float gws[T::NSLOT];
     tp_edge_vjp<LIN, GX>(gm, cur, gws, Y + (int64_t)e * 16, Me, STAGE ? m2buf + buf * M2PAD : Me + MT_M2, gx0,
                          gx1, gx2, gYu);
-    store_gw<T::NSLOT, GWM>(gws, gw + (int64_t)e * WN + u, gscale, e, u, gw_lo);
+    store_gw<T::NSLOT>(gws, gw + (int64_t)e * WN + u, gscale, e, u);
     if constexpr (GX) {
       float* dst = gxe + (int64_t)pos_s[e] * DIN + u;
       dst[0] = gx0;
@@ -555,14 +537,14 @@ void launch_fwd(hipStream_t st, int N, const int* rowptr, const int* sender, con
                      static_cast<const WT*>(w), up, M, half);
 }
 
-template <int LIN, bool GX, typename WT, int GWM>
+template <int LIN, bool GX, typename WT>
 void launch_recv(hipStream_t st, int N, const int* rowptr, const int* sender, const float* Y, const float* Mt,
-                 int mts, const void* w, const float* up, const float* gM, void* gw, float* gscale, int64_t gw_lo,
-                 float* gY, int accumulate_gY, const int* pos_s, float* gxe) {
+                 int mts, const void* w, const float* up, const float* gM, void* gw, float* gscale, float* gY,
+                 int accumulate_gY, const int* pos_s, float* gxe) {
   constexpr int NG = ng_for(LIN);
-  hipLaunchKernelGGL((k_tp_bwd_recv<LIN, NG, GX, WT, GWM>), dim3(N), dim3(NC * NG), 0, st, N, rowptr, sender, Y,
-                     Mt, mts, static_cast<const WT*>(w), up, gM, gw, gscale, gw_lo, gY,
-                     accumulate_gY, pos_s, gxe);
+  hipLaunchKernelGGL((k_tp_bwd_recv<LIN, NG, GX, WT>), dim3(N), dim3(NC * NG), 0, st, N, rowptr, sender, Y, Mt,
+                     mts, static_cast<const WT*>(w), up, gM, static_cast<WT*>(gw), gscale, gY, accumulate_gY,
+                     pos_s, gxe);
 }
 
 }  // namespace
@@ -595,16 +577,13 @@ void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int*
 
 void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const int* sender, const float* Y,
                         const float* Mt, int mts, const void* w, const float* up, const float* gM, void* gw,
-                        float* gscale, int64_t gw_lo, float* gY, int accumulate_gY, const int* pos_s, float* gxe,
-                        int half, int split) {
+                        float* gscale, float* gY, int accumulate_gY, const int* pos_s, float* gxe, int half) {
   if (N <= 0) return;
-#define MACE_RECV(L, G)                                                                                           \
-  half    ? launch_recv<L, G, _Float16, GW_F16>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gscale, gw_lo, \
-                                                gY, accumulate_gY, pos_s, gxe)                                    \
-  : split ? launch_recv<L, G, float, GW_SPLIT>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gscale, gw_lo,   \
-                                               gY, accumulate_gY, pos_s, gxe)                                     \
-          : launch_recv<L, G, float, GW_F32>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gscale, gw_lo, gY, \
-                                             accumulate_gY, pos_s, gxe)
+#define MACE_RECV(L, G)                                                                                          \
+  half ? launch_recv<L, G, _Float16>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gscale, gY, accumulate_gY, \
+                                     pos_s, gxe)                                                                 \
+       : launch_recv<L, G, float>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gscale, gY, accumulate_gY,   \
+                                  pos_s, gxe)
   const bool gx = gxe != nullptr;
   switch (lin) {
     case 1: gx ? MACE_RECV(1, true) : MACE_RECV(1, false); break;
