@@ -80,6 +80,7 @@ struct Layer {
   DBuf<float> ro, ro1, ro2;
   DBuf<_Float16> mlpT3h, mlp3h;  // fp16 copies of W3^T and W3 (float16 feature policy)
   DBuf<_Float16> mlpT3x, mlp3x;  // [hi | lo] fp16 planes of W3^T and W3 scaled by 1 / w3inv (float32 policy)
+  DBuf<unsigned char> mlp_tiles;  // permuted W0..W2 tile images of the hidden-layer kernels
   float w3inv = 1.f;
   bool resid = true;       // residual block (skip from the input); else the skip acts on the message
   DBuf<float> mskip[4], mskipT[4], dens;
@@ -87,6 +88,7 @@ struct Layer {
   // per-step activations (TP weights: w, or wh under the float16 feature policy)
   DBuf<float> h_up, A, w, ro_e;
   DBuf<float> A2, rinv;  // message after its skip FCTP (non-residual block); 1 / (1 + density)
+  DBuf<float> ds;        // silu' of the radial MLP's pre-activations, [E][3][64]
   DBuf<_Float16> wh;
   const void* wptr(bool half) const { return half ? static_cast<const void*>(wh.p) : static_cast<const void*>(w.p); }
 };
@@ -281,7 +283,7 @@ void free_layers(mace_ctx* c) {
     for (int i = 0; i < 4; ++i) L.mlp[i].release(), L.mlpT[i].release(), L.lin_[i].release(), L.linT[i].release();
     L.ro.release(), L.ro1.release(), L.ro2.release(), L.h_up.release(), L.A.release(), L.w.release(),
         L.ro_e.release(), L.wh.release(), L.mlpT3h.release(), L.mlp3h.release(), L.A2.release(), L.rinv.release(),
-        L.dens.release(), L.mlpT3x.release(), L.mlp3x.release();
+        L.dens.release(), L.mlpT3x.release(), L.mlp3x.release(), L.mlp_tiles.release(), L.ds.release();
     for (int i = 0; i < 4; ++i) L.mskip[i].release(), L.mskipT[i].release();
   }
   c->layers.clear();
@@ -365,6 +367,10 @@ void build_model(mace_ctx* c) {
           upload_split(c, L.mlp3x, w, std::ldexp(1.f, 14 - ex));
         }
       }
+      L.mlp_tiles.ensure(mlp_tile_bytes());
+      launch_mlp_permute(c->stream, nb, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, L.mlp_tiles.p);
+      HIPCHK(hipGetLastError());
+      HIPCHK(hipStreamSynchronize(c->stream));
     }
     const int* l3 = tp_l3(L.lin);
     for (int lo = 0; lo < 4; ++lo) {
@@ -452,6 +458,7 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
     else
       ly.w.ensure(e * ly.wn);
     maxw = std::max(maxw, ly.wn);
+    ly.ds.ensure(e * 3 * RADIAL_H);
   }
   if (half) c->h3h.ensure(e * RADIAL_H);
   size_t maxdin = 0;  // per-edge input gradients of the layers after the first
@@ -858,8 +865,8 @@ void forward(mace_ctx* c, const double* pos, double* out) {
     {
       Site s(c, lname("mlp_hidden", l));
       // split: h3 holds E x 2 x 64 fp16 (the same bytes as E x 64 floats)
-      launch_mlp_hidden(st, E, nb, c->ef.p, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p,
-                        half ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), c->h3inv.p,
+      launch_mlp_hidden(st, E, nb, c->ef.p, L.mlp_tiles.p,
+                        half ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), c->h3inv.p, L.ds.p,
                         half ? 1 : split ? 2 : 0);
     }
     {
@@ -1032,8 +1039,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
     }
     {
       Site s(c, lname("mlp_hidden_bwd", l));
-      launch_mlp_hidden_bwd(st, E, nb, c->ef.p, Ly.mlp[0].p, Ly.mlp[1].p, Ly.mlp[2].p, c->h3.p, c->gef.p,
-                            first_edge_grad, half);
+      launch_mlp_hidden_bwd(st, E, nb, Ly.mlp_tiles.p, Ly.ds.p, c->h3.p, c->gef.p, first_edge_grad);
     }
     if (c->dims.density_norm) {  // edge densities' share of dL/def (after gef has been written)
       Site s(c, lname("density_edge_bwd", l));

@@ -68,11 +68,15 @@ void launch_density_edge_bwd(hipStream_t st, int64_t E, const int* receiver, con
                              const float* wd, const float* grho, float* gef);
 
 // radial MLP, ef (E x nb) -> w (E x W); weights [in][out] row-major, W3T = W3 transposed [W][64].
-// h3 [E][64] = silu(silu(silu(ef W0) W1) W2); w = h3 W3.  mode 0: fp32 h3; 1 (float16 feature
-// policy): hidden activations rounded to fp16, h3 fp16; 2: h3 as scaled fp16 hi/lo pairs
-// [E][2][64] with inverse row scales h3inv[E] (operand of launch_mlp_out_x).
-void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0,
-                       const float* W1, const float* W2, void* h3, float* h3inv, int mode);
+// h3 [E][64] = silu(silu(silu(ef W0) W1) W2); w = h3 W3.  W0..W2 enter as tile images built once
+// per model by launch_mlp_permute (mlp_tile_bytes() bytes).  mode 0: fp32 h3; 1 (float16 feature
+// policy): hidden activations rounded to fp16, h3 fp16; 2: h3 as scaled fp16 hi/lo pairs [E][2][64]
+// with inverse row scales h3inv[E] (operand of launch_mlp_out_x).  ds (may be null): silu' of the
+// three pre-activations, ds[E][3][64], for launch_mlp_hidden_bwd.
+size_t mlp_tile_bytes();
+void launch_mlp_permute(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2, void* tiles);
+void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const void* tiles, void* h3,
+                       float* h3inv, float* ds, int mode);
 // half: h3, W3T and w fp16 arrays (fp32 accumulation); else fp32
 void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w,
                     int half);
@@ -80,7 +84,7 @@ void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void
 // fp16 planes of W3^T [W][64] scaled by 1 / cscale
 void launch_mlp_out_x(hipStream_t st, int64_t E, int W, const void* h3x, const float* h3inv,
                       const void* W3Tx, float cscale, float* w);
-// VJP: gh3 = gw W3^T, then gef (+)= dL/def through the recomputed hidden layers
+// VJP: gh3 = gw W3^T, then gef (+)= dL/def through the hidden layers (saved silu' values)
 void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3);
 // float16 feature policy: gw fp16 with per-(edge, channel half) scales, W3 fp16 [64][W]
 void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const float* gscale, const void* W3h,
@@ -89,9 +93,8 @@ void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const fl
 // kernel), W3x = [hi | lo] fp16 planes of W3 [64][W] scaled by 1 / cscale
 void launch_mlp_gh3_x(hipStream_t st, int64_t E, int W, const float* gw, const void* W3x, float cscale,
                       float* gh3);
-void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0,
-                           const float* W1, const float* W2, const float* gh3, float* gef,
-                           int accumulate, int half);
+void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const void* tiles, const float* ds,
+                           const float* gh3, float* gef, int accumulate);
 
 // per-edge x2-first tables Mt[e] (row stride mts) for the l1 >= 1 TP paths
 int tp_table_entries(int max_lin);

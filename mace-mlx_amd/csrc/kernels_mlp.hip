@@ -6,10 +6,11 @@
 // Shapes: ef [E][nb], W0 [nb][64], W1, W2 [64][64], W3 [64][W] (W = 128 * slots).
 //
 // The work is split so every launch has thousands of waves:
-//   k_mlp_hidden     W0..W2 staged in LDS, 16-edge groups per wave: h3 [E][64]
-//   k_mlp_out        w = h3 @ W3, block tile 64 edges x W/2 columns
-//   k_mlp_gh3        dL/dh3 = gw @ W3^T, 32 edges per block, K split over 4 waves, deep prefetch
-//   k_mlp_hidden_bwd same grouping: recompute the pre-activations, back to dL/def
+//   k_mlp_hidden     16 edges per wave, activations in registers, permuted W0..W2 tiles in LDS: h3
+//   k_mlp_out        w = h3 @ W3, block tile 64 edges x W/2 columns (k_mlp_out_h: fp16 policy;
+//                    k_mlp_out_x: float32 policy on fp16 matrix cores with split operands)
+//   k_mlp_gh3        dL/dh3 = gw @ W3^T (k_mlp_gh3_h: fp16 policy; k_mlp_gh3_x: split operands)
+//   k_mlp_hidden_bwd as k_mlp_hidden, from the saved silu' values back to dL/def
 //
 // Fragment layout of the 16x16x4 instruction (checked on gfx950): lane l holds
 // A[l%16][k] and B[k][l%16] with k = l/16; accumulator element i of lane l is
@@ -56,92 +57,141 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 constexpr int H = RADIAL_H;  // hidden width (64)
-constexpr int XP = H + 4;    // padded LDS row
-constexpr int RT = 16;       // edges per wave in the hidden-layer kernels
 
-constexpr int WP = H + 1;  // LDS row stride of the staged weights (conflict-free both ways)
+// ---------------------------------------------------------------------------
+// Hidden layers, activations held in registers.
+//
+// Each wave takes 16 edges.  Products run with swapped roles, Y^T = W^T X^T:
+// A = weight rows (output feature n = 16 t' + r), B = X^T with the 16 edges as
+// columns, so lane (g, r) supplies edge r's inputs and receives, for output
+// tile t', D[4g + i][r] = Y[edge r][n = 16 t' + 4g + i].  After a layer each lane
+// therefore holds 16 of its edge's 64 features, n in {16 t + 4 g + i}, kept as
+// v[4 t + i].  The next layer contracts over those registers directly: at k
+// step s = 4 t + i lane group g supplies k = pi(s, g) = 16 t + 4 g + i (the
+// steps cover every k once), and the weight tiles are staged in LDS permuted to
+// the same order, one float4 (the four output tiles t') per lane and step.  The
+// first layer contracts over the Bessel features with pi(s, g) = 4 s + g.
+// ---------------------------------------------------------------------------
+constexpr int NB4 = NBESSEL_MAX / 4;
 
-// The three small weight matrices of one radial MLP, staged once per block.
-struct MlpW {
-  float w0[NBESSEL_MAX][WP];
-  float w1[H][WP];
-  float w2[H][WP];
+__device__ __forceinline__ int kperm(int s, int g) { return 16 * (s >> 2) + 4 * g + (s & 3); }
+
+// forward weight tiles: w0[s][g][r] = W0[4s + g][16 t' + r] (zero past nb),
+// w1/w2[s][g][r] = W[kperm(s, g)][16 t' + r], t' = float4 component
+struct MlpFwdW {
+  float4 w0[NB4][4][16];
+  float4 w1[16][4][16];
+  float4 w2[16][4][16];
+};
+// transposed tiles of the backward pass: wTq[s][g][r] = W[16 t' + r][kperm(s, g)];
+// w0T[t][g][r] = W0[r][16 t + 4 g + i] (component i; zero for r >= nb)
+struct MlpBwdW {
+  float4 w1T[16][4][16];
+  float4 w2T[16][4][16];
+  float4 w0T[4][4][16];
 };
 
-__device__ __forceinline__ void stage_weights(MlpW& sw, int nb, const float* __restrict__ W0,
-                                              const float* __restrict__ W1, const float* __restrict__ W2) {
-  for (int i = threadIdx.x; i < nb * H; i += blockDim.x) sw.w0[i / H][i % H] = W0[i];
-  for (int i = threadIdx.x; i < H * H; i += blockDim.x) {
-    sw.w1[i / H][i % H] = W1[i];
-    sw.w2[i / H][i % H] = W2[i];
+__device__ void stage_fwd(MlpFwdW& sw, int nb, const float* __restrict__ W0, const float* __restrict__ W1,
+                          const float* __restrict__ W2) {
+  float* w0 = &sw.w0[0][0][0].x;
+  for (int i = threadIdx.x; i < NB4 * 4 * 16 * 4; i += blockDim.x) {
+    const int tp = i & 3, r = (i >> 2) & 15, g = (i >> 6) & 3, st = i >> 8, k = 4 * st + g;
+    w0[i] = k < nb ? W0[k * H + 16 * tp + r] : 0.f;
   }
-  __syncthreads();
+  float* w1 = &sw.w1[0][0][0].x;
+  float* w2 = &sw.w2[0][0][0].x;
+  for (int i = threadIdx.x; i < 16 * 4 * 16 * 4; i += blockDim.x) {
+    const int tp = i & 3, r = (i >> 2) & 15, g = (i >> 6) & 3, st = i >> 8, k = kperm(st, g);
+    w1[i] = W1[k * H + 16 * tp + r];
+    w2[i] = W2[k * H + 16 * tp + r];
+  }
 }
 
-// One wave: out(16 x 64) = A(16 x K) @ B(K x 64), A in a wave-private LDS tile
-// (row stride XP); B[k][n] = Wl[k][n], or Wl[n][k] when TR (the transposed
-// product of the backward pass), Wl staged in LDS with row stride WP.
-template <bool TR>
-__device__ __forceinline__ void wave_gemm_lds(const float (*A)[XP], int K, const float (*Wl)[WP], f4v* acc) {
+__device__ void stage_bwd(MlpBwdW& sw, int nb, const float* __restrict__ W0, const float* __restrict__ W1,
+                          const float* __restrict__ W2) {
+  float* w1 = &sw.w1T[0][0][0].x;
+  float* w2 = &sw.w2T[0][0][0].x;
+  for (int i = threadIdx.x; i < 16 * 4 * 16 * 4; i += blockDim.x) {
+    const int tp = i & 3, r = (i >> 2) & 15, g = (i >> 6) & 3, st = i >> 8, n = kperm(st, g);
+    w1[i] = W1[(16 * tp + r) * H + n];
+    w2[i] = W2[(16 * tp + r) * H + n];
+  }
+  float* w0 = &sw.w0T[0][0][0].x;
+  for (int i = threadIdx.x; i < 4 * 4 * 16 * 4; i += blockDim.x) {
+    const int ii = i & 3, r = (i >> 2) & 15, g = (i >> 6) & 3, t = i >> 8;
+    w0[i] = r < nb ? W0[r * H + 16 * t + 4 * g + ii] : 0.f;
+  }
+}
+
+// builds the tile images once per model (one block); the kernels then stage them
+// with coalesced float4 copies
+__global__ void __launch_bounds__(256) k_mlp_permute(int nb, const float* __restrict__ W0,
+                                                     const float* __restrict__ W1, const float* __restrict__ W2,
+                                                     MlpFwdW* __restrict__ fw, MlpBwdW* __restrict__ bw) {
+  stage_fwd(*fw, nb, W0, W1, W2);
+  stage_bwd(*bw, nb, W0, W1, W2);
+}
+
+template <typename T>
+__device__ __forceinline__ void stage_copy(T& dst, const T* __restrict__ src) {
+  constexpr int N4 = sizeof(T) / 16;
+  float4* d = reinterpret_cast<float4*>(&dst);
+  const float4* q = reinterpret_cast<const float4*>(src);
+  for (int i = threadIdx.x; i < N4; i += blockDim.x) d[i] = q[i];
+}
+
+// one 64-wide layer: acc[t'] = sum over the 16 k steps of W-tile (t') x v[s]
+__device__ __forceinline__ void layer64(const float4 (*w)[4][16], const float* v, f4v* acc) {
   const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
-  if (K % 16 != 0) {  // radial-basis input (K = num_bessel): plain k-steps, zero padded
-    for (int k0 = 0; k0 < K; k0 += 4) {
-      const int k = k0 + g;
-      const float a = (k < K) ? A[r][k] : 0.f;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float b = (k < K) ? (TR ? Wl[16 * t + r][k] : Wl[k][16 * t + r]) : 0.f;
-        acc[t] = mfma16(a, b, acc[t]);
-      }
-    }
-    return;
-  }
-  for (int c = 0; c < K; c += 16) {
-    const float4 a4 = ld4(&A[r][c + 4 * g]);
+  for (int st = 0; st < 16; ++st) {
+    const float4 wv = w[st][g][r];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int k = c + 4 * g + s;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t] = mfma16(comp(a4, s), TR ? Wl[16 * t + r][k] : Wl[k][16 * t + r], acc[t]);
-    }
+    for (int t = 0; t < 4; ++t) acc[t] = mfma16(comp(wv, t), v[st], acc[t]);
   }
 }
 
-// accumulator tiles (optionally through silu) -> wave-private LDS tile
-// (activations rounded to fp16 values under the float16 feature policy)
-__device__ __forceinline__ void store_tile(float (*X)[XP], const f4v* acc, bool act, bool half = false) {
-  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+// silu' of one layer's pre-activations (lane layout) into a saved row: d[16t + i] (d = row + 4g)
+__device__ __forceinline__ void store_ds(float* d, const f4v* a) {
 #pragma unroll
   for (int t = 0; t < 4; ++t)
+    *reinterpret_cast<float4*>(d + 16 * t) = float4{dsilu(a[t][0]), dsilu(a[t][1]), dsilu(a[t][2]), dsilu(a[t][3])};
+}
+
+// The three hidden layers for edges e0 .. e0+15 (lane's edge e0 + r): leaves the
+// pre-activations a3 (a[t][i] = feature 16t + 4g + i); activations between
+// layers rounded to fp16 values under the float16 feature policy.  dsp (null or
+// the lane's position in row ds[e][0][.]) receives silu' of a1..a3.
+__device__ __forceinline__ void hidden_fwd(const MlpFwdW& sw, int64_t E, int64_t e0, int nb,
+                                           const float* __restrict__ ef, f4v* a3, bool half, float* dsp) {
+  f4v a1[4], a2[4];
+  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const int64_t e = e0 + r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) X[4 * g + i][16 * t + r] = act ? qh(silu(acc[t][i]), half) : acc[t][i];
-}
-
-// Rows e0..e0+15 of ef into the wave's tile, then the three hidden layers;
-// leaves the pre-activations a1..a3 in accumulator layout.
-__device__ __forceinline__ void hidden_fwd(float (*X)[XP], const MlpW& sw, int64_t E, int64_t e0, int nb,
-                                           const float* __restrict__ ef, f4v* a1, f4v* a2, f4v* a3, bool half) {
-  const int l = threadIdx.x & 63;
-  for (int i = l; i < RT * nb; i += 64) {
-    const int e = i / nb, k = i % nb;
-    X[e][k] = (e0 + e < E) ? ef[(e0 + e) * nb + k] : 0.f;
+  for (int t = 0; t < 4; ++t) a1[t] = f4v{0.f, 0.f, 0.f, 0.f};
+  const int nst = (nb + 3) >> 2;
+  for (int st = 0; st < nst; ++st) {
+    const int k = 4 * st + g;
+    const float x = (e < E && k < nb) ? ef[e * nb + k] : 0.f;
+    const float4 wv = sw.w0[st][g][r];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) a1[t] = mfma16(comp(wv, t), x, a1[t]);
   }
-  wave_sync();
-  wave_gemm_lds<false>(X, nb, sw.w0, a1);
-  wave_sync();
-  store_tile(X, a1, true, half);
-  wave_sync();
-  wave_gemm_lds<false>(X, H, sw.w1, a2);
-  wave_sync();
-  store_tile(X, a2, true, half);
-  wave_sync();
-  wave_gemm_lds<false>(X, H, sw.w2, a3);
-  wave_sync();
+  float v[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) v[q] = qh(silu(a1[q >> 2][q & 3]), half);
+  if (dsp) store_ds(dsp, a1);
+  layer64(sw.w1, v, a2);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) v[q] = qh(silu(a2[q >> 2][q & 3]), half);
+  if (dsp) store_ds(dsp + H, a2);
+  layer64(sw.w2, v, a3);
+  if (dsp) store_ds(dsp + 2 * H, a3);
 }
 
-// Waves walk 16-edge groups (grid-stride) after the block has staged W0..W2.
+// 16-edge groups per wave (grid-stride) after the block has staged the weights.
 // Output h3 by MODE: H3_F32 float [E][64]; H3_F16 (float16 feature policy)
 // _Float16 [E][64]; H3_SPLIT (operand of the split-fp16 product) _Float16
 // [E][2][64]: row e scaled by a power of two that maps its largest magnitude into
@@ -149,51 +199,62 @@ __device__ __forceinline__ void hidden_fwd(float (*X)[XP], const MlpW& sw, int64
 // h3inv[e] = the inverse scale.
 constexpr int H3_F32 = 0, H3_F16 = 1, H3_SPLIT = 2;
 
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+// ds (optional): silu'(a1), silu'(a2), silu'(a3) as ds[e][layer][64] for the backward pass.
 template <int MODE>
 __global__ void __launch_bounds__(256) k_mlp_hidden(int64_t E, int nb, const float* __restrict__ ef,
-                                                    const float* __restrict__ W0, const float* __restrict__ W1,
-                                                    const float* __restrict__ W2, void* __restrict__ h3v,
-                                                    float* __restrict__ h3inv) {
-  __shared__ MlpW sw;
-  __shared__ __align__(16) float sX[4][RT][XP];
-  stage_weights(sw, nb, W0, W1, W2);
+                                                    const MlpFwdW* __restrict__ tiles, void* __restrict__ h3v,
+                                                    float* __restrict__ h3inv, float* __restrict__ ds) {
+  __shared__ MlpFwdW sw;
+  stage_copy(sw, tiles);
+  __syncthreads();
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
-  const int64_t ngroups = (E + RT - 1) / RT;
+  const int64_t ngroups = (E + 15) / 16;
   for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
-    const int64_t e0 = gi * RT;
-    f4v a1[4], a2[4], a3[4];
-    hidden_fwd(sX[wv], sw, E, e0, nb, ef, a1, a2, a3, MODE == H3_F16);
+    const int64_t e0 = gi * 16, e = e0 + r;
+    f4v a3[4];
+    hidden_fwd(sw, E, e0, nb, ef, a3, MODE == H3_F16, (ds && e < E) ? ds + e * 3 * H + 4 * g : nullptr);
+    float v[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t e = e0 + 4 * g + i;  // row 4g + i lies in lanes 16g .. 16g + 15, columns 16t + r
-      if constexpr (MODE == H3_SPLIT) {
-        float v[4], m = 0.f;
+    for (int q = 0; q < 16; ++q) v[q] = silu(a3[q >> 2][q & 3]);
+    if constexpr (MODE == H3_SPLIT) {
+      float m = 0.f;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) m = fmaxf(m, fabsf(v[q]));
+      m = fmaxf(m, __shfl_xor(m, 16));  // the four lanes of edge r
+      m = fmaxf(m, __shfl_xor(m, 32));
+      // floor(log2 m) from the exponent field; zero / subnormal rows take -100 (finite scales)
+      const int ex = max((int)((__float_as_uint(m) >> 23) & 0xff) - 127, -100);
+      const float sc = __uint_as_float((unsigned)(127 + 14 - ex) << 23);
+      if (e < E) {
+        _Float16* dst = static_cast<_Float16*>(h3v) + e * 2 * H;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          v[t] = silu(a3[t][i]);
-          m = fmaxf(m, fabsf(v[t]));
-        }
+          h4 hi, lo;
 #pragma unroll
-        for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-        const int ex = m > 0.f ? ilogbf(m) : 0;
-        const float sc = ldexpf(1.f, 14 - ex);
-        if (e < E) {
-          _Float16* dst = static_cast<_Float16*>(h3v) + e * 2 * H;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float x = v[t] * sc;
-            const _Float16 hi = (_Float16)x;
-            dst[16 * t + r] = hi;
-            dst[H + 16 * t + r] = (_Float16)(x - (float)hi);
+          for (int i = 0; i < 4; ++i) {
+            const float x = v[4 * t + i] * sc;
+            hi[i] = (_Float16)x;
+            lo[i] = (_Float16)(x - (float)hi[i]);
           }
-          if (r == 0) h3inv[e] = ldexpf(1.f, ex - 14);
+          *reinterpret_cast<h4*>(dst + 16 * t + 4 * g) = hi;
+          *reinterpret_cast<h4*>(dst + H + 16 * t + 4 * g) = lo;
         }
-      } else {
-        using HT = typename std::conditional<MODE == H3_F16, _Float16, float>::type;
-        if (e < E)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) static_cast<HT*>(h3v)[e * H + 16 * t + r] = (HT)silu(a3[t][i]);
+        if (g == 0) h3inv[e] = __uint_as_float((unsigned)(127 - 14 + ex) << 23);
       }
+    } else if constexpr (MODE == H3_F16) {
+      if (e < E)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          *reinterpret_cast<h4*>(static_cast<_Float16*>(h3v) + e * H + 16 * t + 4 * g) =
+              h4{(_Float16)v[4 * t], (_Float16)v[4 * t + 1], (_Float16)v[4 * t + 2], (_Float16)v[4 * t + 3]};
+    } else {
+      if (e < E)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          *reinterpret_cast<float4*>(static_cast<float*>(h3v) + e * H + 16 * t + 4 * g) =
+              float4{v[4 * t], v[4 * t + 1], v[4 * t + 2], v[4 * t + 3]};
     }
   }
 }
@@ -695,66 +756,62 @@ __global__ void __launch_bounds__(256) k_mlp_gh3_x(int64_t E, int W, const float
           float4{acc[u][0] * cscale, acc[u][1] * cscale, acc[u][2] * cscale, acc[u][3] * cscale};
 }
 
-// dL/def from dL/dh3: recompute a1..a3, then
+// dL/def from dL/dh3 for 16 edges per wave, with silu'(a1..a3) saved by the
+// forward kernel (ds[e][layer][64]):
 //   g_a3 = g_h3 * silu'(a3), g_a2 = (g_a3 W2^T) * silu'(a2),
 //   g_a1 = (g_a2 W1^T) * silu'(a1), g_ef = g_a1 W0^T
-// (the transposed products read the staged W0..W2 transposed).
-__global__ void __launch_bounds__(256) k_mlp_hidden_bwd(int64_t E, int nb, const float* __restrict__ ef,
-                                                        const float* __restrict__ W0, const float* __restrict__ W1,
-                                                        const float* __restrict__ W2, const float* __restrict__ gh3,
-                                                        float* __restrict__ gef, int accumulate, int half) {
-  __shared__ MlpW sw;
-  __shared__ __align__(16) float sX[4][RT][XP];
-  stage_weights(sw, nb, W0, W1, W2);
+// in the register layout of the forward pass (the transposed products read the
+// staged transposed tiles; g_ef comes out as D[k = 4g + i][edge r], k < nb).
+__device__ __forceinline__ void ld_row16(const float* p, int g, float* v) {  // features 16t + 4g + i
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const float4 x = ld4(p + 16 * t + 4 * g);
+    v[4 * t] = x.x, v[4 * t + 1] = x.y, v[4 * t + 2] = x.z, v[4 * t + 3] = x.w;
+  }
+}
+
+__global__ void __launch_bounds__(256) k_mlp_hidden_bwd(int64_t E, int nb, const MlpBwdW* __restrict__ tiles,
+                                                        const float* __restrict__ ds, const float* __restrict__ gh3,
+                                                        float* __restrict__ gef, int accumulate) {
+  __shared__ MlpBwdW sw;
+  stage_copy(sw, tiles);
+  __syncthreads();
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
-  float(*X)[XP] = sX[wv];
-  const int64_t ngroups = (E + RT - 1) / RT;
+  const int64_t ngroups = (E + 15) / 16;
   for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
-    const int64_t e0 = gi * RT;
-    f4v a1[4], a2[4], a3[4], t[4];
-    hidden_fwd(X, sw, E, e0, nb, ef, a1, a2, a3, half);
+    const int64_t e0 = gi * 16, e = e0 + r, ec = e < E ? e : E - 1;  // rows past the end: computed, not stored
+    const float* d = ds + ec * 3 * H;
+    float v[16], dv[16];
+    f4v acc[4];
+    ld_row16(gh3 + ec * H, g, v);
+    ld_row16(d + 2 * H, g, dv);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t e = e0 + 4 * g + i;
+    for (int q = 0; q < 16; ++q) v[q] *= dv[q];
+    ld_row16(d + H, g, dv);
+    layer64(sw.w2T, v, acc);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) t[q][i] = (e < E) ? gh3[e * H + 16 * q + r] * dsilu(a3[q][i]) : 0.f;
-    }
-    store_tile(X, t, false);
-    wave_sync();
-    wave_gemm_lds<true>(X, H, sw.w2, t);
+    for (int q = 0; q < 16; ++q) v[q] = acc[q >> 2][q & 3] * dv[q];
+    ld_row16(d, g, dv);
+    layer64(sw.w1T, v, acc);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) t[q][i] *= dsilu(a2[q][i]);
-    wave_sync();
-    store_tile(X, t, false);
-    wave_sync();
-    wave_gemm_lds<true>(X, H, sw.w1, t);
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) t[q][i] *= dsilu(a1[q][i]);
-    wave_sync();
-    store_tile(X, t, false);
-    wave_sync();
-    // g_ef (16 x nb) = g_a1 (16 x 64) @ W0^T: one column tile, columns >= nb padded
+    for (int q = 0; q < 16; ++q) v[q] = acc[q >> 2][q & 3] * dv[q];
     f4v o = f4v{0.f, 0.f, 0.f, 0.f};
-    for (int c = 0; c < H; c += 16) {
-      const float4 a4 = ld4(&X[r][c + 4 * g]);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) o = mfma16(comp(a4, s), (r < nb) ? sw.w0[r][c + 4 * g + s] : 0.f, o);
+    for (int t = 0; t < 4; ++t) {
+      const float4 wq = sw.w0T[t][g][r];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o = mfma16(comp(wq, i), v[4 * t + i], o);
     }
-    if (r < nb) {
+    if (e < E) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t e = e0 + 4 * g + i;
-        if (e < E) {
-          float* dst = gef + e * nb + r;
+        const int k = 4 * g + i;
+        if (k < nb) {
+          float* dst = gef + e * nb + k;
           *dst = accumulate ? *dst + o[i] : o[i];
         }
       }
     }
-    wave_sync();
   }
 }
 
@@ -766,16 +823,25 @@ inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
 // staging the weights once and walking several 64-edge groups
 inline unsigned hidden_grid(int64_t E) { return (unsigned)std::min<int64_t>((E + 63) / 64, 512); }
 
-void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0, const float* W1,
-                       const float* W2, void* h3, float* h3inv, int mode) {
+size_t mlp_tile_bytes() { return sizeof(MlpFwdW) + sizeof(MlpBwdW); }
+
+void launch_mlp_permute(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2, void* tiles) {
+  MlpFwdW* fw = static_cast<MlpFwdW*>(tiles);
+  MlpBwdW* bw = reinterpret_cast<MlpBwdW*>(static_cast<char*>(tiles) + sizeof(MlpFwdW));
+  hipLaunchKernelGGL(k_mlp_permute, dim3(1), dim3(256), 0, st, nb, W0, W1, W2, fw, bw);
+}
+
+void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const void* tiles, void* h3,
+                       float* h3inv, float* ds, int mode) {
   if (E <= 0) return;
   const dim3 grid(hidden_grid(E)), blk(256);
+  const MlpFwdW* fw = static_cast<const MlpFwdW*>(tiles);
   if (mode == H3_SPLIT)
-    hipLaunchKernelGGL(k_mlp_hidden<H3_SPLIT>, grid, blk, 0, st, E, nb, ef, W0, W1, W2, h3, h3inv);
+    hipLaunchKernelGGL(k_mlp_hidden<H3_SPLIT>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
   else if (mode == H3_F16)
-    hipLaunchKernelGGL(k_mlp_hidden<H3_F16>, grid, blk, 0, st, E, nb, ef, W0, W1, W2, h3, h3inv);
+    hipLaunchKernelGGL(k_mlp_hidden<H3_F16>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
   else
-    hipLaunchKernelGGL(k_mlp_hidden<H3_F32>, grid, blk, 0, st, E, nb, ef, W0, W1, W2, h3, h3inv);
+    hipLaunchKernelGGL(k_mlp_hidden<H3_F32>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
 }
 
 void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w, int half) {
@@ -814,11 +880,11 @@ void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const fl
                      gscale, static_cast<const _Float16*>(W3h), gh3);
 }
 
-void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* W0, const float* W1,
-                           const float* W2, const float* gh3, float* gef, int accumulate, int half) {
+void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const void* tiles, const float* ds, const float* gh3,
+                           float* gef, int accumulate) {
   if (E <= 0) return;
-  hipLaunchKernelGGL(k_mlp_hidden_bwd, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, W0, W1, W2, gh3, gef,
-                     accumulate, half);
+  const MlpBwdW* bw = reinterpret_cast<const MlpBwdW*>(static_cast<const char*>(tiles) + sizeof(MlpFwdW));
+  hipLaunchKernelGGL(k_mlp_hidden_bwd, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, bw, ds, gh3, gef, accumulate);
 }
 
 }  // namespace mace
