@@ -33,17 +33,11 @@ sys.path.insert(0, str(ROOT / "mace-mlx_amd"))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_MFMA_PEAK_TFS = 157.3     # MI355X dense fp32 matrix
-FP16_MFMA_PEAK_TFS = 2500.0    # MI355X dense fp16 matrix (the radial MLP's output and gradient
-                               # products run on it under the float16 feature policy)
 
 
 def peak_of(site: str, bound: str, ctx: dict) -> float:
     """Roofline peak for a site: HBM bandwidth, or the matrix-core rate of its data type."""
-    if bound == "hbm":
-        return HBM_PEAK_GBS
-    if ctx.get("half") and site.split(".")[0] in ("mlp_out", "mlp_gh3"):
-        return FP16_MFMA_PEAK_TFS
-    return FP32_MFMA_PEAK_TFS
+    return HBM_PEAK_GBS if bound == "hbm" else FP32_MFMA_PEAK_TFS
 
 
 def algorithmic_work(site: str, ctx: dict):
@@ -64,12 +58,17 @@ def algorithmic_work(site: str, ctx: dict):
         return "hbm", 4 * (E * lay["din"] + N * lay["din"]) + 4 * (N + 1), "GB/s"
     if name == "mlp_hidden":  # three small layers
         return "mfma", 2 * E * (nb * H + 2 * H * H), "TFLOP/s"
-    if name == "mlp_out":  # w = h3 @ W3
+    if name in ("mlp_out", "mlp_gh3"):
+        # w = h3 @ W3 and dL/dh3 = gw @ W3^T.  On fp16 matrix cores (split fp32 operands, or the
+        # float16 policy) the product needs at most a quarter of the time of the E x W stream it
+        # writes / reads, so the bound is HBM: that stream plus the E x 64 side
+        if ctx.get("half"):
+            return "hbm", 2 * E * lay["wn"] + 2 * E * H + (8 * E if name == "mlp_gh3" else 0), "GB/s"
+        if ctx.get("split"):
+            return "hbm", 4 * E * lay["wn"] + 4 * E * H + 4 * E, "GB/s"
         return "mfma", 2 * E * H * lay["wn"], "TFLOP/s"
-    if name == "mlp_gh3":  # dL/dh3 = gw @ W3^T
-        return "mfma", 2 * E * H * lay["wn"], "TFLOP/s"
-    if name == "mlp_hidden_bwd":  # recomputed forward + backward of the small layers
-        return "mfma", 2 * E * 2 * (nb * H + 2 * H * H), "TFLOP/s"
+    if name == "mlp_hidden_bwd":  # the three transposed products (silu' saved by the forward)
+        return "mfma", 2 * E * (nb * H + 2 * H * H), "TFLOP/s"
     if name.startswith("linear") or name.startswith("skip"):
         return "mfma", ctx["linear_flops"].get(site, 0), "TFLOP/s"
     if name in ("sc_fwd", "sc_bwd"):
@@ -211,7 +210,7 @@ def measure_config(idx, steps, warmup):
     eng.set_profiling(False)
     layers = layer_shapes(dm)
     ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_flops=linear_flops(layers, N),
-               half=bc.dtype == "float16")
+               half=bc.dtype == "float16", split=bc.dtype != "float16")
     per_step = {k: (v[0] / steps, v[1] // steps) for k, v in kt.items()}
     dom = max(per_step, key=lambda k: per_step[k][0])
     b, a, u = algorithmic_work(dom, ctx)
@@ -306,7 +305,7 @@ def main():
     eng.set_profiling(False)
     layers = layer_shapes(dm)
     ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_flops=linear_flops(layers, N),
-               half=bc.dtype == "float16")
+               half=bc.dtype == "float16", split=bc.dtype != "float16")
     per_step = {k: (v[0] / args.steps, v[1] // args.steps) for k, v in kt.items()}
     dom = max(per_step, key=lambda k: per_step[k][0])
     bound, amount, unit = algorithmic_work(dom, ctx)

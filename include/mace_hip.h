@@ -148,14 +148,16 @@ int mace_get_kernel_times(mace_ctx* ctx, char* names, int64_t names_len, double*
  * calculators.py:424-453). */
 int mace_set_graphs(mace_ctx* ctx, int32_t enable);
 
-/* Float32 policy: products of the radial MLP's output layer (w = h3 W3 and its
- * transpose in the backward pass) on fp16 matrix cores with operands split into
- * fp16 pairs, a = a_hi + a_lo (per-row power-of-two scales), three products per
- * pair and fp32 accumulation: about 2^-21 relative error per product, i.e. the
- * float32 tolerances hold (default on).  0 selects fp32 matrix-core products.
- * Ignored under the float16 feature policy.  No counterpart in the reference
- * (its matmuls run in the model dtype, model.py:592-661). */
-int mace_set_mlp_split(mace_ctx* ctx, int32_t enable);
+/* Float32 policy: matrix products on fp16 matrix cores with both operands split
+ * into fp16 pairs, a = a_hi + a_lo (power-of-two scales per row and 32-wide k
+ * chunk, or per weight matrix), three products per pair and fp32 accumulation:
+ * about 2^-21 relative error per product, within the float32 tolerances (default
+ * on).  Covers the radial MLP's output layer (w = h3 W3 and its transpose in the
+ * backward pass) and the node linears (up / message / product / skip, both
+ * passes).  0 selects fp32 matrix cores throughout.  Ignored under the float16
+ * feature policy.  No counterpart in the reference (its matmuls run in the model
+ * dtype, model.py:592-661). */
+int mace_set_split_products(mace_ctx* ctx, int32_t enable);
 
 /* Timing of the last mace_step (device milliseconds, HIP events on the
  * context's stream): [0] whole step, [1] neighbour list (0 if cached),

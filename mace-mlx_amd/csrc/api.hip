@@ -154,7 +154,12 @@ struct mace_ctx {
     int flag = 0;
   };
   bool use_graphs = true;
-  bool split_mlp = true;  // float32 policy: radial-MLP output products on fp16 matrix cores (split operands)
+  bool split_products = true;  // float32 policy: matrix products on fp16 matrix cores (split operands)
+  struct SplitW {
+    DBuf<_Float16> x;  // [hi | lo] planes of the weights scaled by 1 / winv
+    float winv = 1.f;
+  };
+  std::map<const float*, SplitW> wsplit;  // split copies of the grouped-GEMM weights, by device pointer
   StepGraph g_fwd, g_bwd;
   // per-launch-site profiling
   bool profiling = false;
@@ -265,6 +270,19 @@ void upload_split(mace_ctx* c, DBuf<_Float16>& dst, const std::vector<float>& v,
   HIPCHK(hipMemcpy(dst.p, h.data(), h.size() * sizeof(_Float16), hipMemcpyHostToDevice));
 }
 
+// split copy of `count` device floats at p (largest magnitude scaled into [2^14, 2^15))
+void make_split(mace_ctx* c, const float* p, size_t count) {
+  if (!p || count == 0 || c->wsplit.count(p)) return;
+  std::vector<float> h(count);
+  HIPCHK(hipMemcpy(h.data(), p, count * sizeof(float), hipMemcpyDeviceToHost));
+  float m = 0.f;
+  for (float x : h) m = std::max(m, std::fabs(x));
+  const int ex = m > 0.f ? std::ilogb(m) : 0;
+  auto& sw = c->wsplit[p];
+  sw.winv = std::ldexp(1.f, ex - 14);
+  upload_split(c, sw.x, h, std::ldexp(1.f, 14 - ex));
+}
+
 std::vector<float> transpose(const std::vector<float>& a, int rows, int cols, int batch = 1) {
   std::vector<float> t(a.size());
   for (int b = 0; b < batch; ++b)
@@ -287,6 +305,8 @@ void free_layers(mace_ctx* c) {
     for (int i = 0; i < 4; ++i) L.mskip[i].release(), L.mskipT[i].release();
   }
   c->layers.clear();
+  for (auto& kv : c->wsplit) kv.second.x.release();
+  c->wsplit.clear();
 }
 
 void build_model(mace_ctx* c) {
@@ -392,6 +412,20 @@ void build_model(mace_ctx* c) {
       if (L.lhid != 1) fail(MACE_ERR_UNSUPPORTED, "last layer must be scalar");
       upload(c, L.ro1, tensor(c, p + "ro1", (size_t)C * 16));
       upload(c, L.ro2, tensor(c, p + "ro2", 16));
+    }
+  }
+  if (!d.feature_half) {  // split copies of every weight matrix the grouped products use
+    const size_t CC = (size_t)C * C;
+    for (Layer& L : c->layers) {
+      for (int b = 0; b < L.lin; ++b) make_split(c, L.up[b].p, CC), make_split(c, L.upT[b].p, CC);
+      for (int b = 0; b < L.lhid; ++b) make_split(c, L.plin[b].p, CC), make_split(c, L.plinT[b].p, CC);
+      for (int b = 0; b < L.nskip; ++b) make_split(c, L.skip[b].p, CC), make_split(c, L.skipT[b].p, CC);
+      const int* l3 = tp_l3(L.lin);
+      for (int lo = 0; lo < 4; ++lo) {
+        size_t ns = 0;
+        for (int q = 0; q < n_tp_slots(L.lin); ++q) ns += (l3[q] == lo);
+        make_split(c, L.lin_[lo].p, ns * CC), make_split(c, L.linT[lo].p, ns * CC);
+      }
     }
   }
   c->max_lin = 1;
@@ -730,6 +764,28 @@ GemmProb gprob(int N, int d, int K1, int Cout, const float* X1, int ldx1, int ba
   return P;
 }
 
+// grouped products: on fp16 matrix cores with split operands under the float32 policy when
+// enabled and every weight matrix has its split copy, else on fp32 matrix cores
+void run_gemm(mace_ctx* c, hipStream_t st, GemmGroup& g) {
+  g.split = 0;
+  if (c->split_products && !c->dims.feature_half && !g.round_half) {
+    bool ok = true;
+    for (int q = 0; q < g.n && ok; ++q) {
+      GemmProb& P = g.p[q];
+      auto a = c->wsplit.find(P.WT1);
+      auto b = P.K2 > 0 ? c->wsplit.find(P.WT2) : a;
+      ok = a != c->wsplit.end() && b != c->wsplit.end() && P.Cout % 128 == 0 && P.K1 % 32 == 0 && P.K2 % 32 == 0;
+      if (!ok) break;
+      P.WX1 = a->second.x.p;
+      P.winv1 = a->second.winv;
+      P.WX2 = b->second.x.p;
+      P.winv2 = b->second.winv;
+    }
+    g.split = ok ? 1 : 0;
+  }
+  launch_gemm_group(st, g);
+}
+
 void slot_range(const Layer& L, int lo, int* first, int* cnt) {
   const int* l3 = tp_l3(L.lin);
   *first = -1;
@@ -843,7 +899,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
   const int64_t E = c->E;
   const int nb = c->dims.num_bessel;
   const int half = c->dims.feature_half != 0;
-  const bool split = !half && c->split_mlp;
+  const bool split = !half && c->split_products;
   FrontParams fp = front_params(c);
   {
     Site s(c, "edge_fwd");
@@ -884,7 +940,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
       g.round_half = half;
       for (int b = 0; b < L.lin; ++b)
         g.p[g.n++] = gprob(N, 2 * b + 1, NC, NC, h, L.din, NC * b * b, 0, L.upT[b].p, L.h_up.p, L.din, NC * b * b, 0);
-      launch_gemm_group(st, g);
+      run_gemm(c, st, g);
     }
     {
       Site s(c, lname("tp_fwd", l));
@@ -908,7 +964,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
                            NC * lo * lo, 0);
         if (c->dims.density_norm) g.p[g.n - 1].rowscale = L.rinv.p;
       }
-      launch_gemm_group(st, g);
+      run_gemm(c, st, g);
     }
     if (!L.resid) {  // non-residual block: species-dependent skip FCTP on the message
       Site s(c, lname("message_skip", l));
@@ -938,7 +994,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
         }
         g.p[g.n++] = P;
       }
-      launch_gemm_group(st, g);
+      run_gemm(c, st, g);
     }
     if (!one_el)
       for (int b = 0; b < L.nskip; ++b) {
@@ -965,7 +1021,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
   const int nb = c->dims.num_bessel;
   const int L = (int)c->layers.size();
   const int half = c->dims.feature_half != 0;
-  const bool split = !half && c->split_mlp;
+  const bool split = !half && c->split_products;
   // dE/dh_L from the nonlinear readout
   float* gh = c->gh0.p;
   float* gh_next = c->gh1.p;
@@ -983,7 +1039,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
       for (int b = 0; b < Ly.lhid; ++b)
         g.p[g.n++] =
             gprob(N, 2 * b + 1, NC, NC, gh, Ly.dhid, NC * b * b, 0, Ly.plin[b].p, c->gB.p, Ly.dhid, NC * b * b, 0);
-      launch_gemm_group(st, g);
+      run_gemm(c, st, g);
     }
     const float* scw[3] = {Ly.sc[0].p, Ly.sc[1].p, Ly.sc[2].p};
     {
@@ -1014,7 +1070,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
                            NC * ao[first], NC * d);
         if (c->dims.density_norm) g.p[g.n - 1].rowscale = Ly.rinv.p;
       }
-      launch_gemm_group(st, g);
+      run_gemm(c, st, g);
     }
     const int first_edge_grad = (l == L - 1) ? 0 : 1;  // gY / gef: write on the first layer visited
     {
@@ -1065,7 +1121,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
           if (b == 0) P.bias = c->layers[l - 1].ro.p;
           g.p[g.n++] = P;
         }
-        launch_gemm_group(st, g);
+        run_gemm(c, st, g);
       }
       if (!one_el)
         for (int b = 0; b < Ly.nskip; ++b) {
@@ -1364,11 +1420,11 @@ int mace_set_graphs(mace_ctx* c, int32_t enable) {
   });
 }
 
-int mace_set_mlp_split(mace_ctx* c, int32_t enable) {
+int mace_set_split_products(mace_ctx* c, int32_t enable) {
   if (!c) return MACE_ERR_INVALID;
   return guard(c, [&] {
     set_device(c);
-    c->split_mlp = enable != 0;
+    c->split_products = enable != 0;
     invalidate_graphs(c);
   });
 }

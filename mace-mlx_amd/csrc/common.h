@@ -151,12 +151,17 @@ struct GemmProb {
   const float* rowscale;  // optional per-node factor on the product (before bias / accumulate)
   int accumulate;
   int tiles_n, tile_begin;
+  // split products (GemmGroup::split): [hi | lo] fp16 planes of WT1 / WT2 scaled by 1 / winv
+  const _Float16* WX1;
+  const _Float16* WX2;
+  float winv1, winv2;
 };
 struct GemmGroup {
   GemmProb p[GEMM_MAX];
   int n;
   int total_tiles;
   int round_half;  // outputs rounded to fp16 values (float16 feature policy)
+  int split;       // float32 policy on fp16 matrix cores (split operands, WX1 / WX2 set)
 };
 void launch_gemm_group(hipStream_t st, GemmGroup& g);
 

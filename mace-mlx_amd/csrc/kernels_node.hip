@@ -206,6 +206,160 @@ __global__ void __launch_bounds__(256) k_gemm_group(GemmGroup G) {
   }
 }
 
+// Float32 policy on fp16 matrix cores: the grouped products of k_gemm_group with
+// both operands split into fp16 pairs (a = a_hi + a_lo, three products per pair,
+// fp32 accumulation; about 2^-22 relative per product).  Roles are swapped: A =
+// weight rows (output columns), B = X^T with a tile's 16 rows as columns, so lane
+// (g, r) owns row r's eight k values of a 32-wide chunk and the accumulators of
+// that row: it scales the values by the power of two that maps their chunk's
+// largest magnitude (reduced over the row's four lanes) into [2^14, 2^15), splits
+// them and folds the inverse scale (times the weights' own, winv) into the
+// accumulators after the chunk.  Weights come as [hi | lo] planes WX [Cout][K]
+// scaled by 1 / winv.  Block = 32 rows x 128 output columns (wave = 16 rows x 64
+// columns); the block stages each chunk of its 128 weight rows in LDS,
+// double-buffered, and the X chunks are loaded two ahead.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f4v mfma16h(h8 a, h8 b, f4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+struct GemmXSrc {
+  const float* xr[2];     // row n, component m of operands 1 and 2
+  const _Float16* w[2];   // hi plane row of the staging thread's column
+  int K1, stride[2], K[2];
+  float winv[2];
+};
+
+// this lane's eight X values of chunk ci (k = 32 ci + 8 g ...)
+__device__ __forceinline__ void gx_load_x(const GemmXSrc& S, int ci, int g, float4& x0, float4& x1) {
+  int k = 32 * ci;
+  const int o = k < S.K1 ? 0 : 1;
+  if (o) k -= S.K1;
+  const float* p = S.xr[o] + (k / NC) * S.stride[o] + (k % NC) + 8 * g;
+  x0 = *reinterpret_cast<const float4*>(p);
+  x1 = *reinterpret_cast<const float4*>(p + 4);
+}
+
+__global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
+  __shared__ __align__(16) _Float16 sW[2][2][128][32];  // [buffer][hi, lo][column][k of the chunk]
+  int q = 0;
+  while (q + 1 < G.n && (int)blockIdx.x >= G.p[q + 1].tile_begin) ++q;
+  const GemmProb& P = G.p[q];
+  const int t = blockIdx.x - P.tile_begin;
+  const int tm = t / P.tiles_n, tn = t % P.tiles_n;
+  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const int rt = tm * 2 + (wv >> 1), chalf = wv & 1;
+  const int row = rt * 16 + r;
+  const bool live = row < P.rows;
+  const int n = live ? row / P.d : 0, m = live ? row - n * P.d : 0;  // dead rows read row 0, store nothing
+  GemmXSrc S;
+  S.K1 = P.K1;
+  S.K[0] = P.K1;
+  S.K[1] = P.K2;
+  S.stride[0] = P.in_stride1;
+  S.stride[1] = P.in_stride2;
+  S.xr[0] = P.X1 + (int64_t)n * P.ldx1 + P.in_base1 + m * NC;
+  S.xr[1] = P.K2 > 0 ? P.X2 + (int64_t)n * P.ldx2 + P.in_base2 + m * NC : S.xr[0];
+  S.winv[0] = P.winv1;
+  S.winv[1] = P.winv2;
+  // staging: thread -> column tn * 128 + (tid >> 1), k quarter 16 (tid & 1)
+  const int scol = threadIdx.x >> 1, kq = 16 * (threadIdx.x & 1);
+  S.w[0] = P.WX1 + (int64_t)(tn * 128 + scol) * P.K1;
+  S.w[1] = P.K2 > 0 ? P.WX2 + (int64_t)(tn * 128 + scol) * P.K2 : S.w[0];
+  const int64_t plane[2] = {(int64_t)P.Cout * P.K1, (int64_t)P.Cout * P.K2};
+  const int nch = (P.K1 + P.K2) / 32;
+  float4 ring[2][2];
+  gx_load_x(S, 0, g, ring[0][0], ring[0][1]);
+  gx_load_x(S, min(1, nch - 1), g, ring[1][0], ring[1][1]);
+  auto load_w = [&](int ci, h8* w) {  // both planes: w[0..1] hi, w[2..3] lo
+    int k = 32 * ci;
+    const int o = k < S.K1 ? 0 : 1;
+    if (o) k -= S.K1;
+    const _Float16* p = S.w[o] + k + kq;
+    w[0] = *reinterpret_cast<const h8*>(p);
+    w[1] = *reinterpret_cast<const h8*>(p + 8);
+    w[2] = *reinterpret_cast<const h8*>(p + plane[o]);
+    w[3] = *reinterpret_cast<const h8*>(p + plane[o] + 8);
+  };
+  h8 ws[4];
+  load_w(0, ws);
+  *reinterpret_cast<h8*>(&sW[0][0][scol][kq]) = ws[0];
+  *reinterpret_cast<h8*>(&sW[0][0][scol][kq + 8]) = ws[1];
+  *reinterpret_cast<h8*>(&sW[0][1][scol][kq]) = ws[2];
+  *reinterpret_cast<h8*>(&sW[0][1][scol][kq + 8]) = ws[3];
+  __syncthreads();
+  f4v acc[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) acc[u] = f4v{0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < nch; c0 += 2) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int cc = c0 + p;
+      if (cc < nch) {  // uniform over the block
+        const int buf = cc & 1;
+        if (cc + 1 < nch) load_w(cc + 1, ws);
+        const float4 c0v = ring[p][0], c1v = ring[p][1];
+        gx_load_x(S, min(cc + 2, nch - 1), g, ring[p][0], ring[p][1]);
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the arithmetic
+        const float v[8] = {c0v.x, c0v.y, c0v.z, c0v.w, c1v.x, c1v.y, c1v.z, c1v.w};
+        float mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // floor(log2 mx) from the exponent field; zero / subnormal chunks take -100 (finite scales)
+        const int ex = max((int)((__float_as_uint(mx) >> 23) & 0xff) - 127, -100);
+        const float sc = __uint_as_float((unsigned)(127 + 14 - ex) << 23);
+        const float inv = __uint_as_float((unsigned)(127 - 14 + ex) << 23) * S.winv[32 * cc < S.K1 ? 0 : 1];
+        h8 xh, xl;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float x = v[j] * sc;
+          const _Float16 hi = (_Float16)x;
+          xh[j] = hi;
+          xl[j] = (_Float16)(x - (float)hi);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int col = 64 * chalf + 16 * u + r;
+          const h8 wh = *reinterpret_cast<const h8*>(&sW[buf][0][col][8 * g]);
+          const h8 wl = *reinterpret_cast<const h8*>(&sW[buf][1][col][8 * g]);
+          f4v d = mfma16h(wl, xh, f4v{0.f, 0.f, 0.f, 0.f});
+          d = mfma16h(wh, xl, d);
+          d = mfma16h(wh, xh, d);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[u][i] = fmaf(d[i], inv, acc[u][i]);
+        }
+        if (cc + 1 < nch) {
+          *reinterpret_cast<h8*>(&sW[buf ^ 1][0][scol][kq]) = ws[0];
+          *reinterpret_cast<h8*>(&sW[buf ^ 1][0][scol][kq + 8]) = ws[1];
+          *reinterpret_cast<h8*>(&sW[buf ^ 1][1][scol][kq]) = ws[2];
+          *reinterpret_cast<h8*>(&sW[buf ^ 1][1][scol][kq + 8]) = ws[3];
+        }
+        __syncthreads();
+      }
+    }
+  }
+  if (!live) return;
+  const float rs = P.rowscale ? P.rowscale[n] : 1.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int col = tn * 128 + 64 * chalf + 16 * u + 4 * g;  // four consecutive output columns
+    float* y = P.Y + (int64_t)n * P.ldy + P.out_base + (col / NC) * P.out_stride + m * NC + (col % NC);
+    float4 v = float4{acc[u][0] * rs, acc[u][1] * rs, acc[u][2] * rs, acc[u][3] * rs};
+    if (P.bias) {
+      const float4 b = *reinterpret_cast<const float4*>(P.bias + col);
+      v.x += b.x, v.y += b.y, v.z += b.z, v.w += b.w;
+    }
+    if (P.accumulate) {
+      const float4 o = *reinterpret_cast<const float4*>(y);
+      v.x += o.x, v.y += o.y, v.z += o.z, v.w += o.w;
+    }
+    *reinterpret_cast<float4*>(y) = v;
+  }
+}
+
 __global__ void k_embed(int N, const int* __restrict__ species, const float* __restrict__ emb, int ld,
                         float* __restrict__ h, int half) {
   const int n = blockIdx.x, u = threadIdx.x;
@@ -576,6 +730,18 @@ void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s
 }
 
 void launch_gemm_group(hipStream_t st, GemmGroup& g) {
+  if (g.split) {  // 32 rows x 128 columns per block
+    int tiles = 0;
+    for (int q = 0; q < g.n; ++q) {
+      GemmProb& P = g.p[q];
+      P.tiles_n = P.Cout / 128;
+      P.tile_begin = tiles;
+      tiles += (int)cdiv(P.rows, 32) * P.tiles_n;
+    }
+    g.total_tiles = tiles;
+    if (tiles > 0) hipLaunchKernelGGL(k_gemm_group_x, dim3(tiles), dim3(256), 0, st, g);
+    return;
+  }
   int row_tiles = 0;
   for (int q = 0; q < g.n; ++q) row_tiles += (int)cdiv(g.p[q].rows, 16) * (g.p[q].Cout / 64);
   const bool wide = row_tiles >= 1024;  // enough blocks even with four column tiles per wave

@@ -33,7 +33,7 @@ EXPORTED_SYMBOLS = (
     "mace_model_end", "mace_set_system", "mace_step", "mace_set_edges", "mace_get_edges",
     "mace_get_timings", "mace_step_device", "mace_sync", "mace_set_profiling", "mace_get_kernel_times",
     "mace_set_graphs",
-    "mace_set_mlp_split",
+    "mace_set_split_products",
 )
 
 
@@ -87,7 +87,7 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
         "mace_sync": (ctypes.c_int, [P]),
         "mace_set_profiling": (ctypes.c_int, [P, I32]),
         "mace_set_graphs": (ctypes.c_int, [P, I32]),
-        "mace_set_mlp_split": (ctypes.c_int, [P, I32]),
+        "mace_set_split_products": (ctypes.c_int, [P, I32]),
         "mace_get_kernel_times": (ctypes.c_int, [P, ctypes.c_char_p, I64, P, P, I32, ctypes.POINTER(I32)]),
     }
     for name, (res, args) in sig.items():
@@ -214,10 +214,10 @@ class Engine:
         """Replay steps through captured HIP graphs (default) or launch them eagerly."""
         self._check(self._lib.mace_set_graphs(self._h, int(bool(enable))))
 
-    def set_mlp_split(self, enable: bool) -> None:
-        """Float32 policy: radial-MLP output products on fp16 matrix cores with split operands
-        (default) or on fp32 matrix cores."""
-        self._check(self._lib.mace_set_mlp_split(self._h, int(bool(enable))))
+    def set_split_products(self, enable: bool) -> None:
+        """Float32 policy: matrix products (radial-MLP output layer, node linears) on fp16 matrix
+        cores with split operands (default) or on fp32 matrix cores."""
+        self._check(self._lib.mace_set_split_products(self._h, int(bool(enable))))
 
     def kernel_times(self) -> dict:
         """{site: (total_ms, launches)} accumulated since the last call."""

@@ -374,22 +374,23 @@ def test_graph_replay_matches_eager(medium_zbl):
 
 
 @pytest.mark.parametrize("arch", ["medium_zbl", "large"])
-def test_split_mlp_products_match_fp32(arch, request):
-    """Float32 policy: the radial-MLP output products on fp16 matrix cores with split
-    operands (default) and on fp32 matrix cores both meet the float32 tolerances against
-    the float64 oracle, and the split path's force error is of the same order as the fp32
-    path's (per-product error about 2^-21 relative against 2^-24)."""
+def test_split_products_match_fp32(arch, request):
+    """Float32 policy: the matrix products (radial-MLP output layer, node linears) on fp16
+    matrix cores with split operands (default) and on fp32 matrix cores both meet the
+    float32 tolerances against the float64 oracle, and the split path's force error is of
+    the same order as the fp32 path's (per-product error about 2^-21 relative against
+    2^-24)."""
     case = request.getfixturevalue(arch)
     s = rattle(diamond_si((2, 2, 2)), 0.05, 11)
     errs = {}
     try:
         for split in (False, True):
-            case.eng.set_mlp_split(split)
+            case.eng.set_split_products(split)
             got = case.run(s, stress=True)
             ref = case.reference(s, got["sp"], case.edges(), stress=True)
             errs[split] = assert_parity(got, ref, len(s), stress=True, vol=abs(np.linalg.det(s.cell)))
     finally:
-        case.eng.set_mlp_split(True)
+        case.eng.set_split_products(True)
     print(f"{arch}: fp32 products dE={errs[False][0]:.3g} dF={errs[False][1]:.3g}; "
           f"split dE={errs[True][0]:.3g} dF={errs[True][1]:.3g}")
     assert errs[True][1] <= max(8 * errs[False][1], 5e-6), errs
