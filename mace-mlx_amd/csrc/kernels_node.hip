@@ -215,9 +215,9 @@ __global__ void __launch_bounds__(256) k_gemm_group(GemmGroup G) {
 // largest magnitude (reduced over the row's four lanes) into [2^14, 2^15), splits
 // them and folds the inverse scale (times the weights' own, winv) into the
 // accumulators after the chunk.  Weights come as [hi | lo] planes WX [Cout][K]
-// scaled by 1 / winv.  Block = 32 rows x 128 output columns (wave = 16 rows x 64
-// columns); the block stages each chunk of its 128 weight rows in LDS,
-// double-buffered, and the X chunks are loaded two ahead.
+// scaled by 1 / winv.  Block = 64 rows x 64 output columns (wave = one 16-row
+// tile x the 64 columns); the block stages each chunk of its 64 weight rows in
+// LDS, double-buffered, and the X chunks are loaded two ahead.
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ f4v mfma16h(h8 a, h8 b, f4v c) {
@@ -242,14 +242,14 @@ __device__ __forceinline__ void gx_load_x(const GemmXSrc& S, int ci, int g, floa
 }
 
 __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
-  __shared__ __align__(16) _Float16 sW[2][2][128][32];  // [buffer][hi, lo][column][k of the chunk]
+  __shared__ __align__(16) _Float16 sW[2][2][64][32];  // [buffer][hi, lo][column][k of the chunk]
   int q = 0;
   while (q + 1 < G.n && (int)blockIdx.x >= G.p[q + 1].tile_begin) ++q;
   const GemmProb& P = G.p[q];
   const int t = blockIdx.x - P.tile_begin;
   const int tm = t / P.tiles_n, tn = t % P.tiles_n;
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
-  const int rt = tm * 2 + (wv >> 1), chalf = wv & 1;
+  const int rt = tm * 4 + wv;
   const int row = rt * 16 + r;
   const bool live = row < P.rows;
   const int n = live ? row / P.d : 0, m = live ? row - n * P.d : 0;  // dead rows read row 0, store nothing
@@ -263,31 +263,26 @@ __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
   S.xr[1] = P.K2 > 0 ? P.X2 + (int64_t)n * P.ldx2 + P.in_base2 + m * NC : S.xr[0];
   S.winv[0] = P.winv1;
   S.winv[1] = P.winv2;
-  // staging: thread -> column tn * 128 + (tid >> 1), k quarter 16 (tid & 1)
-  const int scol = threadIdx.x >> 1, kq = 16 * (threadIdx.x & 1);
-  S.w[0] = P.WX1 + (int64_t)(tn * 128 + scol) * P.K1;
-  S.w[1] = P.K2 > 0 ? P.WX2 + (int64_t)(tn * 128 + scol) * P.K2 : S.w[0];
+  // staging: thread -> column tn * 64 + tid / 4, eight k at 8 (tid & 3), both planes
+  const int scol = threadIdx.x >> 2, kq = 8 * (threadIdx.x & 3);
+  S.w[0] = P.WX1 + (int64_t)(tn * 64 + scol) * P.K1;
+  S.w[1] = P.K2 > 0 ? P.WX2 + (int64_t)(tn * 64 + scol) * P.K2 : S.w[0];
   const int64_t plane[2] = {(int64_t)P.Cout * P.K1, (int64_t)P.Cout * P.K2};
   const int nch = (P.K1 + P.K2) / 32;
   float4 ring[2][2];
   gx_load_x(S, 0, g, ring[0][0], ring[0][1]);
   gx_load_x(S, min(1, nch - 1), g, ring[1][0], ring[1][1]);
-  auto load_w = [&](int ci, h8* w) {  // both planes: w[0..1] hi, w[2..3] lo
+  auto load_w = [&](int ci, h8* w) {  // this thread's eight values of chunk ci, hi and lo
     int k = 32 * ci;
     const int o = k < S.K1 ? 0 : 1;
     if (o) k -= S.K1;
-    const _Float16* p = S.w[o] + k + kq;
-    w[0] = *reinterpret_cast<const h8*>(p);
-    w[1] = *reinterpret_cast<const h8*>(p + 8);
-    w[2] = *reinterpret_cast<const h8*>(p + plane[o]);
-    w[3] = *reinterpret_cast<const h8*>(p + plane[o] + 8);
+    w[0] = *reinterpret_cast<const h8*>(S.w[o] + k + kq);
+    w[1] = *reinterpret_cast<const h8*>(S.w[o] + plane[o] + k + kq);
   };
-  h8 ws[4];
+  h8 ws[2];
   load_w(0, ws);
   *reinterpret_cast<h8*>(&sW[0][0][scol][kq]) = ws[0];
-  *reinterpret_cast<h8*>(&sW[0][0][scol][kq + 8]) = ws[1];
-  *reinterpret_cast<h8*>(&sW[0][1][scol][kq]) = ws[2];
-  *reinterpret_cast<h8*>(&sW[0][1][scol][kq + 8]) = ws[3];
+  *reinterpret_cast<h8*>(&sW[0][1][scol][kq]) = ws[1];
   __syncthreads();
   f4v acc[4];
 #pragma unroll
@@ -322,7 +317,7 @@ __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          const int col = 64 * chalf + 16 * u + r;
+          const int col = 16 * u + r;
           const h8 wh = *reinterpret_cast<const h8*>(&sW[buf][0][col][8 * g]);
           const h8 wl = *reinterpret_cast<const h8*>(&sW[buf][1][col][8 * g]);
           f4v d = mfma16h(wl, xh, f4v{0.f, 0.f, 0.f, 0.f});
@@ -333,9 +328,7 @@ __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
         }
         if (cc + 1 < nch) {
           *reinterpret_cast<h8*>(&sW[buf ^ 1][0][scol][kq]) = ws[0];
-          *reinterpret_cast<h8*>(&sW[buf ^ 1][0][scol][kq + 8]) = ws[1];
-          *reinterpret_cast<h8*>(&sW[buf ^ 1][1][scol][kq]) = ws[2];
-          *reinterpret_cast<h8*>(&sW[buf ^ 1][1][scol][kq + 8]) = ws[3];
+          *reinterpret_cast<h8*>(&sW[buf ^ 1][1][scol][kq]) = ws[1];
         }
         __syncthreads();
       }
@@ -345,7 +338,7 @@ __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
   const float rs = P.rowscale ? P.rowscale[n] : 1.f;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    const int col = tn * 128 + 64 * chalf + 16 * u + 4 * g;  // four consecutive output columns
+    const int col = tn * 64 + 16 * u + 4 * g;  // four consecutive output columns
     float* y = P.Y + (int64_t)n * P.ldy + P.out_base + (col / NC) * P.out_stride + m * NC + (col % NC);
     float4 v = float4{acc[u][0] * rs, acc[u][1] * rs, acc[u][2] * rs, acc[u][3] * rs};
     if (P.bias) {
@@ -730,13 +723,13 @@ void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s
 }
 
 void launch_gemm_group(hipStream_t st, GemmGroup& g) {
-  if (g.split) {  // 32 rows x 128 columns per block
+  if (g.split) {  // 64 rows x 64 columns per block
     int tiles = 0;
     for (int q = 0; q < g.n; ++q) {
       GemmProb& P = g.p[q];
-      P.tiles_n = P.Cout / 128;
+      P.tiles_n = P.Cout / 64;
       P.tile_begin = tiles;
-      tiles += (int)cdiv(P.rows, 32) * P.tiles_n;
+      tiles += (int)cdiv(P.rows, 64) * P.tiles_n;
     }
     g.total_tiles = tiles;
     if (tiles > 0) hipLaunchKernelGGL(k_gemm_group_x, dim3(tiles), dim3(256), 0, st, g);
