@@ -107,6 +107,7 @@ struct mace_ctx {
   int max_lin = 1;
   int mts = 0;  // row stride of the per-edge TP tables Mt (0: no layer has l1 >= 1 inputs)
   DBuf<float> e0, bessel_w, zbl_z, zbl_cov, ag_cov, embed;
+  DBuf<float> up0_tab;  // first linear_up per species [n_el][C]
   DBuf<float> gA2, grho;  // backward scratch of the message skip / density normalisation
   // system
   int N = 0;
@@ -325,6 +326,20 @@ void build_model(mace_ctx* c) {
   upload(c, c->e0, tensor(c, "e0", nel));
   upload(c, c->bessel_w, tensor(c, "bessel_w", nb));
   upload(c, c->embed, tensor(c, "embed", (size_t)nel * C));
+  {  // first linear_up as a per-species table: up0[z] = h0[z] W (fp64 sums; fp16-rounded values under
+     // the float16 feature policy, as the product would give)
+    const auto& emb = tensor(c, "embed", (size_t)nel * C);
+    const auto& w = tensor(c, "L0.up.0", (size_t)C * C);
+    auto rnd = [&](float x) { return d.feature_half ? (float)(_Float16)x : x; };
+    std::vector<float> tab((size_t)nel * C);
+    for (int z = 0; z < nel; ++z)
+      for (int col = 0; col < C; ++col) {
+        double a = 0.0;
+        for (int k = 0; k < C; ++k) a += (double)rnd(emb[(size_t)z * C + k]) * w[(size_t)k * C + col];
+        tab[(size_t)z * C + col] = rnd((float)a);
+      }
+    upload(c, c->up0_tab, tab);
+  }
   if (d.has_zbl) {
     upload(c, c->zbl_z, tensor(c, "zbl_z", nel));
     upload(c, c->zbl_cov, tensor(c, "zbl_cov", nel));
@@ -468,6 +483,7 @@ void ensure_node_buffers(mace_ctx* c) {
   c->ypre.ensure((size_t)N * 16);
   c->node_e.ensure(N);
   c->e_part.ensure((N + 3) / 4 + 1);
+
   c->out.ensure(10 + 3 * (size_t)N);
   c->pos.ensure(3 * (size_t)N);
   if (c->out_pinned_n < (size_t)N) {
@@ -514,6 +530,7 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   c->gscale.ensure(e * 2);
   c->h3inv.ensure(e);
   c->vir_part.ensure(9 * ((e + 255) / 256));
+
 }
 
 void ensure_edge_index(mace_ctx* c, int64_t E) {
@@ -912,7 +929,8 @@ void forward(mace_ctx* c, const double* pos, double* out) {
   }
   {
     Site s(c, "embed");
-    launch_embed(st, N, c->species.p, c->embed.p, c->layers[0].din, c->h[0].p, half);
+    launch_embed(st, N, c->species.p, c->embed.p, c->layers[0].din, c->h[0].p, half, c->up0_tab.p,
+                 c->layers[0].h_up.p);
   }
   for (size_t l = 0; l < c->layers.size(); ++l) {
     Layer& L = c->layers[l];
@@ -934,7 +952,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
       else
         launch_mlp_out(st, E, L.wn, c->h3.p, L.mlpT[3].p, L.w.p, 0);
     }
-    {
+    if (l > 0) {  // the first layer's comes from the species table (launch_embed)
       Site s(c, lname("linear_up", l));
       GemmGroup g{};
       g.round_half = half;
@@ -1132,19 +1150,21 @@ void backward(mace_ctx* c, bool stress, double* out) {
     }
   }
   FrontParams fp = front_params(c);
-  const int nblk = (int)((E + 255) / 256);
   {
     Site s(c, "edge_bwd");
     launch_edge_bwd(st, E, c->sender.p, c->receiver.p, c->species.p, c->bessel_w.p, c->zbl_z.p, c->zbl_cov.p,
                     c->ag_cov.p, fp,
-                    c->geom.p, c->gY.p, c->gef.p, c->gv.p, stress ? c->vir_part.p : nullptr, nblk);
+                    c->geom.p, c->gY.p, c->gef.p, c->gv.p, stress ? c->vir_part.p : nullptr);
   }
   {
     Site s(c, "forces");
-    launch_forces(st, N, c->rowptr.p, c->rowptr_s.p, c->perm_s.p, c->gv.p, out + 10);
+    launch_forces(st, N, c->rowptr.p, c->rowptr_s.p, c->perm_s.p, c->gv.p, out + 10,
+                  (stress && E > 0) ? nullptr : out + 1);
   }
-  Site s(c, "virial");
-  launch_virial_reduce(st, c->vir_part.p, (stress && E > 0) ? nblk : 0, out + 1);
+  if (stress && E > 0) {
+    Site s(c, "virial");
+    launch_virial_reduce(st, c->vir_part.p, (int)((E + 255) / 256), out + 1);
+  }
 }
 
 }  // namespace
@@ -1183,7 +1203,7 @@ static void free_all(mace_ctx* c) {
   c->h3h.release();
   c->gwh.release();
   c->gscale.release();
-  for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->ag_cov, &c->gA2, &c->grho, &c->embed, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
+  for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->ag_cov, &c->gA2, &c->grho, &c->embed, &c->up0_tab, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
                   &c->gv, &c->gw, &c->gxe, &c->h3, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup, &c->ypre,
                   &c->node_e})
     b->release();

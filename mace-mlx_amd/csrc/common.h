@@ -14,6 +14,20 @@ constexpr int NC = 128;
 constexpr int NBESSEL_MAX = 16;
 constexpr int RADIAL_H = 64;   // radial-MLP hidden width compiled in
 
+// fixed-order tree sum over a 256-thread block (result in every thread)
+__device__ inline double block_sum_fixed(double a) {
+  __shared__ double red[256];
+  red[threadIdx.x] = a;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+    __syncthreads();
+  }
+  const double t = red[0];
+  __syncthreads();
+  return t;
+}
+
 // Node feature layout (all internal node tensors): blocks in irreps order,
 // inside a block the element (channel u, component m) sits at m * NC + u.
 __host__ __device__ constexpr int block_off(int l) { return NC * l * l; }  // blocks 0..l-1 dense
@@ -52,11 +66,12 @@ void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* se
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov,
                      const float* ag_cov, const FrontParams& p, EdgeGeom* geom, float* Y, float* ef,
                      float* zbl_e);
-void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver,
-                     const int* species, const float* bessel_w, const float* zbl_z,
-                     const float* zbl_cov, const float* ag_cov, const FrontParams& p,
-                     const EdgeGeom* geom, const float* gY, const float* gef, float* gv,
-                     double* vir_part, int nblk_vir);
+void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,
+                     const float* bessel_w, const float* zbl_z, const float* zbl_cov, const float* ag_cov,
+                     const FrontParams& p, const EdgeGeom* geom, const float* gY, const float* gef, float* gv,
+                     double* vir_part);
+// symmetrised virial from the per-block partials of launch_edge_bwd
+void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir);
 // density normalisation (blocks.py:372-380): rinv[n] = 1 / (1 + sum_{e -> n} tanh((ef_e . wd)^2))
 void launch_density_fwd(hipStream_t st, int N, const int* rowptr, const float* ef, int nb,
                         const float* wd, float* rinv);
@@ -165,7 +180,10 @@ struct GemmGroup {
 };
 void launch_gemm_group(hipStream_t st, GemmGroup& g);
 
-void launch_embed(hipStream_t st, int N, const int* species, const float* emb, int ld, float* h, int half);
+// h0 = embedding per species; with up_tab, also h_up = up_tab[species] (first linear_up, which
+// depends on the species only)
+void launch_embed(hipStream_t st, int N, const int* species, const float* emb, int ld, float* h, int half,
+                  const float* up_tab, float* h_up);
 
 // symmetric contraction (all output blocks of one product layer)
 void launch_sc_fwd(hipStream_t st, int N, int nout, int corr, const float* A, int ldA,
@@ -184,12 +202,13 @@ void launch_readout_mlp_bwd(hipStream_t st, int N, const float* ypre, const floa
 void launch_readout_linear_bwd(hipStream_t st, int N, const float* w, float* gh, int ldh,
                                int accumulate);
 
-void launch_node_energy(hipStream_t st, int N, const int* species, const float* e0,
-                        const int* rowptr, const float* zbl_e, const float* const* ro,
-                        int nro, float* node_e, double* part, double* energy);
-void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s,
-                   const int* perm_s, const float* gv, double* forces);
-void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir);
+// node energies and their total (block partials, then a fixed-order sum)
+void launch_node_energy(hipStream_t st, int N, const int* species, const float* e0, const int* rowptr,
+                        const float* zbl_e, const float* const* ro, int nro, float* node_e, double* part,
+                        double* energy);
+// vir_zero (may be null) receives nine zeros
+void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s, const int* perm_s,
+                   const float* gv, double* forces, double* vir_zero);
 
 // neighbour list
 struct NLParams {

@@ -416,9 +416,8 @@ void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* se
 void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov, const float* ag_cov,
                      const FrontParams& p, const EdgeGeom* geom, const float* gY, const float* gef, float* gv,
-                     double* vir_part, int nblk_vir) {
+                     double* vir_part) {
   if (E <= 0) return;
-  (void)nblk_vir;
   hipLaunchKernelGGL(k_edge_bwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, sender, receiver, species,
                      bessel_w, zbl_z, zbl_cov, ag_cov, p, geom, gY, gef, gv, vir_part);
 }

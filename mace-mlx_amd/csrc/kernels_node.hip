@@ -353,10 +353,13 @@ __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
   }
 }
 
+// first-layer node features h0[n] = embedding of the species and, with a table, the first
+// linear_up output up0[z] (a function of the species only, built once per model)
 __global__ void k_embed(int N, const int* __restrict__ species, const float* __restrict__ emb, int ld,
-                        float* __restrict__ h, int half) {
-  const int n = blockIdx.x, u = threadIdx.x;
-  h[(int64_t)n * ld + u] = qh(emb[species[n] * NC + u], half);
+                        float* __restrict__ h, int half, const float* __restrict__ up_tab, float* __restrict__ h_up) {
+  const int n = blockIdx.x, u = threadIdx.x, z = species[n];
+  h[(int64_t)n * ld + u] = qh(emb[z * NC + u], half);
+  if (up_tab) h_up[(int64_t)n * ld + u] = up_tab[z * NC + u];
 }
 
 // ---------------------------------------------------------------------------
@@ -552,20 +555,15 @@ __global__ void __launch_bounds__(256) k_node_energy(int N, const int* __restric
   if (threadIdx.x == 0) part[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// fixed-order sum of block partials (deterministic)
+// fixed-order sum of block partials (deterministic); one block
 __global__ void __launch_bounds__(256) k_sum_partials(const double* __restrict__ part, int nblk,
                                                       double* __restrict__ out) {
-  __shared__ double red[256];
   double a = 0.0;
   for (int b = threadIdx.x; b < nblk; b += 256) a += part[b];
-  red[threadIdx.x] = a;
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) *out = red[0];
+  const double t = block_sum_fixed(a);
+  if (threadIdx.x == 0) *out = t;
 }
+
 
 __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
@@ -574,9 +572,11 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 }
 
 // one wavefront per atom: F_a = -(sum over edges received by a - sum over edges sent by a) of dE/dv
+// vir_zero (may be null): receives nine zeros (no virial requested, or no edges)
 __global__ void __launch_bounds__(256) k_forces(int N, const int* __restrict__ rowptr, const int* __restrict__ rowptr_s,
                                                 const int* __restrict__ perm_s, const float* __restrict__ gv,
-                                                double* __restrict__ F) {
+                                                double* __restrict__ F, double* __restrict__ vir_zero) {
+  if (vir_zero && blockIdx.x == 0 && threadIdx.x < 9) vir_zero[threadIdx.x] = 0.0;
   const int a = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
   if (a >= N) return;  // whole wavefront exits together
   double fx = 0.0, fy = 0.0, fz = 0.0;
@@ -601,34 +601,26 @@ __global__ void __launch_bounds__(256) k_forces(int N, const int* __restrict__ r
   }
 }
 
-// G[a][b] = sum_e v_e[a] g_e[b] summed over blocks in order; writes the
+// writes zeros to vir[0..8] (no atoms)
+__global__ void __launch_bounds__(64) k_zeros(double* __restrict__ vir) {
+  if (threadIdx.x < 9) vir[threadIdx.x] = 0.0;
+}
+
+// G[a][b] = sum_e v_e[a] g_e[b]: the per-block partials of k_edge_bwd summed in block order
+// (thread t adds partials t, t + 256, ..., then a fixed-order tree: deterministic); writes the
 // symmetrised virial dE/d(eps_sym) = (G + G^T) / 2 (calculators.py:536-561).
-// nblk == 0 writes zeros.
-// Sum of the per-block virial partials (one 256-thread block): thread t adds
-// partials t, t + 256, ... in order, then a fixed-order tree over the threads
-// (deterministic); the result is symmetrised.
 __global__ void __launch_bounds__(256) k_virial_reduce(const double* __restrict__ part, int nblk,
                                                        double* __restrict__ vir) {
-  __shared__ double red[9][256];
-  const int t = threadIdx.x;
-  double a[9];
+  double G[9];
 #pragma unroll
-  for (int k = 0; k < 9; ++k) a[k] = 0.0;
-  for (int b = t; b < nblk; b += 256)
-#pragma unroll
-    for (int k = 0; k < 9; ++k) a[k] += part[9 * b + k];
-#pragma unroll
-  for (int k = 0; k < 9; ++k) red[k][t] = a[k];
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if (t < off)
-#pragma unroll
-      for (int k = 0; k < 9; ++k) red[k][t] += red[k][t + off];
-    __syncthreads();
+  for (int k = 0; k < 9; ++k) {
+    double a = 0.0;
+    for (int b = threadIdx.x; b < nblk; b += 256) a += part[9 * b + k];
+    G[k] = block_sum_fixed(a);
   }
-  if (t < 9) {
-    const int r = t / 3, c = t % 3;
-    vir[t] = 0.5 * (red[3 * r + c][0] + red[3 * c + r][0]);
+  if (threadIdx.x < 9) {
+    const int r = threadIdx.x / 3, c = threadIdx.x % 3;
+    vir[threadIdx.x] = 0.5 * (G[3 * r + c] + G[3 * c + r]);
   }
 }
 
@@ -649,9 +641,10 @@ void launch_linear_species(hipStream_t st, int N, const LinearDesc& d, const flo
   hipLaunchKernelGGL(k_linear_species, dim3(rows, d.Cout / NC), dim3(NC), 0, st, rows, d, X, W, species, Y);
 }
 
-void launch_embed(hipStream_t st, int N, const int* species, const float* emb, int ld, float* h, int half) {
+void launch_embed(hipStream_t st, int N, const int* species, const float* emb, int ld, float* h, int half,
+                  const float* up_tab, float* h_up) {
   if (N <= 0) return;
-  hipLaunchKernelGGL(k_embed, dim3(N), dim3(NC), 0, st, N, species, emb, ld, h, half);
+  hipLaunchKernelGGL(k_embed, dim3(N), dim3(NC), 0, st, N, species, emb, ld, h, half, up_tab, h_up);
 }
 
 void launch_sc_fwd(hipStream_t st, int N, int nout, int corr, const float* A, int ldA, const int* species,
@@ -716,10 +709,18 @@ void launch_node_energy(hipStream_t st, int N, const int* species, const float* 
   hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(256), 0, st, part, nblk, energy);
 }
 
+void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir) {
+  hipLaunchKernelGGL(k_virial_reduce, dim3(1), dim3(256), 0, st, part, nblk, vir);
+}
+
 void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s, const int* perm_s,
-                   const float* gv, double* forces) {
-  if (N <= 0) return;
-  hipLaunchKernelGGL(k_forces, dim3(cdiv(N, 4)), dim3(256), 0, st, N, rowptr, rowptr_s, perm_s, gv, forces);
+                   const float* gv, double* forces, double* vir_zero) {
+  if (N <= 0) {
+    if (vir_zero) hipLaunchKernelGGL(k_zeros, dim3(1), dim3(64), 0, st, vir_zero);
+    return;
+  }
+  hipLaunchKernelGGL(k_forces, dim3(cdiv(N, 4)), dim3(256), 0, st, N, rowptr, rowptr_s, perm_s, gv, forces,
+                     vir_zero);
 }
 
 void launch_gemm_group(hipStream_t st, GemmGroup& g) {
@@ -754,8 +755,5 @@ void launch_gemm_group(hipStream_t st, GemmGroup& g) {
     hipLaunchKernelGGL((k_gemm_group<1, 8, true>), dim3(tiles), dim3(256), 0, st, g);
 }
 
-void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir) {
-  hipLaunchKernelGGL(k_virial_reduce, dim3(1), dim3(256), 0, st, part, nblk, vir);
-}
 
 }  // namespace mace
