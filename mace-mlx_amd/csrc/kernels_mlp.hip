@@ -659,91 +659,117 @@ __global__ void __launch_bounds__(256) k_mlp_gh3_h(int64_t E, int W, const _Floa
 }
 
 // Float32 policy on fp16 matrix cores: gh3 = gw @ W3^T from the fp32 gradient gw
-// [E][W].  Each wave runs the whole K loop for 16 edges in 32-wide chunks; the
-// block stages each chunk of W3x = [hi | lo] planes of W3 [64][W] (scaled by
-// 1 / cscale) in LDS, double-buffered.  Operand roles are swapped (A = W3 rows
-// j, B = gw^T with the edges as columns), so lane (g, r) owns edge r's eight k
-// values of the chunk and the output column of that edge: it scales them by the
-// power of two that maps the chunk's largest |gw| of the edge (reduced over the
-// four lanes of the edge) into [2^14, 2^15), splits them into fp16 hi + lo and
-// folds the inverse scale into its accumulators after the chunk's three products
+// [E][W].  Each wave runs the whole K loop for 16 edges in 64-wide stages; the
+// block stages each stage of W3x = [hi | lo] planes of W3 [64][W] (scaled by
+// 1 / cscale) in LDS, double-buffered (rows padded to 72 halves: conflict-free
+// 16-byte reads).  Operand roles are swapped (A = W3 rows j, B = gw^T with the
+// edges as columns), so lane (g, r) owns edge r's sixteen k values of the stage
+// (two 32-wide MFMA chunks) and the output column of that edge: it scales them by
+// the power of two that maps the stage's largest |gw| of the edge (reduced over
+// the four lanes of the edge) into [2^14, 2^15), splits them into fp16 hi + lo and
+// folds the inverse scale into its accumulators after the stage's products
 //   W3_hi x gw_lo + W3_lo x gw_hi + W3_hi x gw_hi
-// (about 2^-22 relative per product).  gw loaded GX_PF chunks ahead.
-constexpr int GX_PF = 2;
+// (about 2^-22 relative per product).  gw loaded two stages ahead.
+constexpr int GX_KS = 64;       // k per stage (one scale, one barrier)
+constexpr int GX_RS = GX_KS + 8;
 
 __global__ void __launch_bounds__(256) k_mlp_gh3_x(int64_t E, int W, const float* __restrict__ gw,
                                                    const _Float16* __restrict__ W3x, float cscale,
                                                    float* __restrict__ gh3) {
-  __shared__ __align__(16) _Float16 sB[2][2][H][32];  // [buffer][hi, lo][j][k of the chunk]
+  __shared__ __align__(16) _Float16 sB[2][2][H][GX_RS];  // [buffer][hi, lo][j][k of the stage]
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + wv) * 16, lo_b = (int64_t)H * W;
-  const int nch = W / 32;
+  const int nst = W / GX_KS;
   const float* ar = gw + min(row0 + r, E - 1) * (int64_t)W + 8 * g;  // rows past the end: computed, not stored
-  const int bj = threadIdx.x >> 2, bk = 8 * (threadIdx.x & 3);      // staging: one 8-wide k piece of row bj
+  const int bj = threadIdx.x >> 2, bk = 8 * (threadIdx.x & 3);      // staging: row bj, k bk and bk + 32
   const _Float16* bsrc = W3x + (int64_t)bj * W + bk;
-  float4 ring[GX_PF][2];
+  float4 ring[2][2][2];  // [stage slot][32-wide chunk][two float4]
+  auto load_x = [&](int st, float4 (*dst)[2]) {
 #pragma unroll
-  for (int p = 0; p < GX_PF; ++p) {
-    const float* q = ar + 32 * min(p, nch - 1);
-    ring[p][0] = ld4(q);
-    ring[p][1] = ld4(q + 4);
-  }
-  h8 st0 = *reinterpret_cast<const h8*>(bsrc), st1 = *reinterpret_cast<const h8*>(bsrc + lo_b);
-  *reinterpret_cast<h8*>(&sB[0][0][bj][bk]) = st0;
-  *reinterpret_cast<h8*>(&sB[0][1][bj][bk]) = st1;
+    for (int q = 0; q < 2; ++q) {
+      const float* p = ar + GX_KS * st + 32 * q;
+      dst[q][0] = ld4(p);
+      dst[q][1] = ld4(p + 4);
+    }
+  };
+  h8 stw[2][2];  // [chunk][hi, lo]
+  auto load_w = [&](int st) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const _Float16* p = bsrc + GX_KS * st + 32 * q;
+      stw[q][0] = *reinterpret_cast<const h8*>(p);
+      stw[q][1] = *reinterpret_cast<const h8*>(p + lo_b);
+    }
+  };
+  auto store_w = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      *reinterpret_cast<h8*>(&sB[buf][0][bj][32 * q + bk]) = stw[q][0];
+      *reinterpret_cast<h8*>(&sB[buf][1][bj][32 * q + bk]) = stw[q][1];
+    }
+  };
+  load_x(0, ring[0]);
+  load_x(min(1, nst - 1), ring[1]);
+  load_w(0);
+  store_w(0);
   __syncthreads();
   f4v acc[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) acc[u] = f4v{0.f, 0.f, 0.f, 0.f};
-  for (int ch = 0; ch < nch; ch += GX_PF) {
+  for (int s0 = 0; s0 < nst; s0 += 2) {
 #pragma unroll
-    for (int p = 0; p < GX_PF; ++p) {
-      const int cc = ch + p;
-      if (cc < nch) {  // uniform over the block
-        const int buf = cc & 1;
-        if (cc + 1 < nch) {
-          st0 = *reinterpret_cast<const h8*>(bsrc + 32 * (cc + 1));
-          st1 = *reinterpret_cast<const h8*>(bsrc + lo_b + 32 * (cc + 1));
-        }
-        const float4 c0 = ring[p][0], c1 = ring[p][1];
-        {
-          const float* q = ar + 32 * min(cc + GX_PF, nch - 1);
-          ring[p][0] = ld4(q);
-          ring[p][1] = ld4(q + 4);
-        }
+    for (int p = 0; p < 2; ++p) {
+      const int st = s0 + p;
+      if (st < nst) {  // uniform over the block
+        const int buf = st & 1;
+        if (st + 1 < nst) load_w(st + 1);
+        float4 cur[2][2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) cur[q][0] = ring[p][q][0], cur[q][1] = ring[p][q][1];
+        load_x(min(st + 2, nst - 1), ring[p]);
         __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the arithmetic
-        const float v[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
         float m = 0.f;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(v[q]));
-        m = fmaxf(m, __shfl_xor(m, 16));
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(cur[q][h].x), fabsf(cur[q][h].y)),
+                               fmaxf(fabsf(cur[q][h].z), fabsf(cur[q][h].w))));
+        m = fmaxf(m, __shfl_xor(m, 16));  // the four lanes of edge r
         m = fmaxf(m, __shfl_xor(m, 32));
-        // floor(log2 m) from the exponent field; zero / subnormal chunks take -100 (finite scales)
+        // floor(log2 m) from the exponent field; zero / subnormal stages take -100 (finite scales)
         const int ex = max((int)((__float_as_uint(m) >> 23) & 0xff) - 127, -100);
         const float sc = __uint_as_float((unsigned)(127 + 14 - ex) << 23);
         const float inv = __uint_as_float((unsigned)(127 - 14 + ex) << 23);
-        h8 xh, xl;
+        f4v d[4];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const float x = v[q] * sc;
-          const _Float16 hi = (_Float16)x;
-          xh[q] = hi;
-          xl[q] = (_Float16)(x - (float)hi);
+        for (int u = 0; u < 4; ++u) d[u] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const float v[8] = {cur[q][0].x, cur[q][0].y, cur[q][0].z, cur[q][0].w,
+                              cur[q][1].x, cur[q][1].y, cur[q][1].z, cur[q][1].w};
+          h8 xh, xl;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float x = v[j] * sc;
+            const _Float16 hi = (_Float16)x;
+            xh[j] = hi;
+            xl[j] = (_Float16)(x - (float)hi);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const h8 wh = *reinterpret_cast<const h8*>(&sB[buf][0][16 * u + r][32 * q + 8 * g]);
+            const h8 wl = *reinterpret_cast<const h8*>(&sB[buf][1][16 * u + r][32 * q + 8 * g]);
+            d[u] = mfma16h(wl, xh, d[u]);
+            d[u] = mfma16h(wh, xl, d[u]);
+            d[u] = mfma16h(wh, xh, d[u]);
+          }
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const h8 wh = *reinterpret_cast<const h8*>(&sB[buf][0][16 * u + r][8 * g]);
-          const h8 wl = *reinterpret_cast<const h8*>(&sB[buf][1][16 * u + r][8 * g]);
-          f4v d = mfma16h(wl, xh, f4v{0.f, 0.f, 0.f, 0.f});
-          d = mfma16h(wh, xl, d);
-          d = mfma16h(wh, xh, d);
+        for (int u = 0; u < 4; ++u)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[u][i] = fmaf(d[i], inv, acc[u][i]);
-        }
-        if (cc + 1 < nch) {
-          *reinterpret_cast<h8*>(&sB[buf ^ 1][0][bj][bk]) = st0;
-          *reinterpret_cast<h8*>(&sB[buf ^ 1][1][bj][bk]) = st1;
-        }
+          for (int i = 0; i < 4; ++i) acc[u][i] = fmaf(d[u][i], inv, acc[u][i]);
+        if (st + 1 < nst) store_w(buf ^ 1);
         __syncthreads();
       }
     }

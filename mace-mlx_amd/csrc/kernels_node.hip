@@ -242,7 +242,7 @@ __device__ __forceinline__ void gx_load_x(const GemmXSrc& S, int ci, int g, floa
 }
 
 __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
-  __shared__ __align__(16) _Float16 sW[2][2][64][32];  // [buffer][hi, lo][column][k of the chunk]
+  __shared__ __align__(16) _Float16 sW[2][2][64][40];  // [buffer][hi, lo][column][k of the chunk + pad]
   int q = 0;
   while (q + 1 < G.n && (int)blockIdx.x >= G.p[q + 1].tile_begin) ++q;
   const GemmProb& P = G.p[q];
