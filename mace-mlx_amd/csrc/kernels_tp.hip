@@ -212,7 +212,7 @@ __global__ void __launch_bounds__(NC* NG) k_tp_fwd(int N, const int* __restrict_
   if (gb < ge) {
     EdgeIn<LIN> cur, nxt;
     M2Stage stg;
-    load_w<LIN, false, WT>(w + (int64_t)gb * WN + u, cur.w);
+    load_w<LIN, true, WT>(w + (int64_t)gb * WN + u, cur.w);
     load_x<LIN>(up + (int64_t)sender[gb] * DIN + u, cur.x0, cur.x1, cur.x2);
     if constexpr (STAGE) {
       stg.load(Mt + (int64_t)gb * mts + MT_M2, lane);
@@ -223,7 +223,7 @@ __global__ void __launch_bounds__(NC* NG) k_tp_fwd(int N, const int* __restrict_
 #pragma unroll 1
     for (int e = gb; e < ge; ++e) {
       if (e + 1 < ge) {
-        load_w<LIN, false, WT>(w + (int64_t)(e + 1) * WN + u, nxt.w);
+        load_w<LIN, true, WT>(w + (int64_t)(e + 1) * WN + u, nxt.w);
         load_x<LIN>(up + (int64_t)sender[e + 1] * DIN + u, nxt.x0, nxt.x1, nxt.x2);
         if constexpr (STAGE) stg.load(Mt + (int64_t)(e + 1) * mts + MT_M2, lane);
       }
@@ -299,7 +299,7 @@ __device__ __forceinline__ void store_gw(const float* gws, GWT* __restrict__ gwe
                                          int64_t e, int u) {
   if constexpr (sizeof(GWT) == 4) {
 #pragma unroll
-    for (int s = 0; s < NSLOT; ++s) gwe[s * NC] = gws[s];
+    for (int s = 0; s < NSLOT; ++s) __builtin_nontemporal_store(gws[s], gwe + s * NC);
   } else {
     float m = 0.f;
 #pragma unroll
