@@ -80,7 +80,9 @@ struct Layer {
   DBuf<float> ro, ro1, ro2;
   DBuf<_Float16> mlpT3h, mlp3h;  // fp16 copies of W3^T and W3 (float16 feature policy)
   DBuf<_Float16> mlpT3x, mlp3x;  // [hi | lo] fp16 planes of W3^T and W3 scaled by 1 / w3inv (float32 policy)
-  DBuf<unsigned char> mlp_tiles;  // permuted W0..W2 tile images of the hidden-layer kernels
+  DBuf<unsigned char> mlp_tiles;    // permuted W0..W2 tile images of the hidden-layer kernels
+  DBuf<unsigned char> mlp_tiles_x;  // the same, split into fp16 pairs (float32 policy)
+  float mlp_winv[3] = {1.f, 1.f, 1.f};
   float w3inv = 1.f;
   bool resid = true;       // residual block (skip from the input); else the skip acts on the message
   DBuf<float> mskip[4], mskipT[4], dens;
@@ -302,7 +304,8 @@ void free_layers(mace_ctx* c) {
     for (int i = 0; i < 4; ++i) L.mlp[i].release(), L.mlpT[i].release(), L.lin_[i].release(), L.linT[i].release();
     L.ro.release(), L.ro1.release(), L.ro2.release(), L.h_up.release(), L.A.release(), L.w.release(),
         L.ro_e.release(), L.wh.release(), L.mlpT3h.release(), L.mlp3h.release(), L.A2.release(), L.rinv.release(),
-        L.dens.release(), L.mlpT3x.release(), L.mlp3x.release(), L.mlp_tiles.release(), L.ds.release();
+        L.dens.release(), L.mlpT3x.release(), L.mlp3x.release(), L.mlp_tiles.release(), L.ds.release(),
+        L.mlp_tiles_x.release();
     for (int i = 0; i < 4; ++i) L.mskip[i].release(), L.mskipT[i].release();
   }
   c->layers.clear();
@@ -404,6 +407,18 @@ void build_model(mace_ctx* c) {
       }
       L.mlp_tiles.ensure(mlp_tile_bytes());
       launch_mlp_permute(c->stream, nb, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, L.mlp_tiles.p);
+      if (!d.feature_half) {  // split images, one power-of-two scale per matrix
+        float sc[3];
+        for (int k = 0; k < 3; ++k) {
+          float m = 0.f;
+          for (float x : tensor(c, p + "mlp." + std::to_string(k), (size_t)rows[k] * cols[k])) m = std::max(m, std::fabs(x));
+          const int ex = m > 0.f ? std::ilogb(m) : 0;
+          sc[k] = std::ldexp(1.f, 14 - ex);
+          L.mlp_winv[k] = std::ldexp(1.f, ex - 14);
+        }
+        L.mlp_tiles_x.ensure(mlp_tile_x_bytes());
+        launch_mlp_permute_x(c->stream, nb, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, sc, L.mlp_tiles_x.p);
+      }
       HIPCHK(hipGetLastError());
       HIPCHK(hipStreamSynchronize(c->stream));
     }
@@ -939,9 +954,12 @@ void forward(mace_ctx* c, const double* pos, double* out) {
     {
       Site s(c, lname("mlp_hidden", l));
       // split: h3 holds E x 2 x 64 fp16 (the same bytes as E x 64 floats)
-      launch_mlp_hidden(st, E, nb, c->ef.p, L.mlp_tiles.p,
-                        half ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), c->h3inv.p, L.ds.p,
-                        half ? 1 : split ? 2 : 0);
+      if (split)
+        launch_mlp_hidden_x(st, E, nb, c->ef.p, L.mlp_tiles_x.p, L.mlp_winv, c->h3.p, c->h3inv.p, L.ds.p);
+      else
+        launch_mlp_hidden(st, E, nb, c->ef.p, L.mlp_tiles.p,
+                          half ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), c->h3inv.p, L.ds.p,
+                          half ? 1 : 0);
     }
     {
       Site s(c, lname("mlp_out", l));
@@ -1113,7 +1131,11 @@ void backward(mace_ctx* c, bool stress, double* out) {
     }
     {
       Site s(c, lname("mlp_hidden_bwd", l));
-      launch_mlp_hidden_bwd(st, E, nb, Ly.mlp_tiles.p, Ly.ds.p, c->h3.p, c->gef.p, first_edge_grad);
+      if (split)
+        launch_mlp_hidden_bwd_x(st, E, nb, Ly.mlp_tiles_x.p, Ly.mlp_winv, Ly.ds.p, c->h3.p, c->gef.p,
+                                first_edge_grad);
+      else
+        launch_mlp_hidden_bwd(st, E, nb, Ly.mlp_tiles.p, Ly.ds.p, c->h3.p, c->gef.p, first_edge_grad);
     }
     if (c->dims.density_norm) {  // edge densities' share of dL/def (after gef has been written)
       Site s(c, lname("density_edge_bwd", l));

@@ -92,6 +92,15 @@ size_t mlp_tile_bytes();
 void launch_mlp_permute(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2, void* tiles);
 void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const void* tiles, void* h3,
                        float* h3inv, float* ds, int mode);
+// float32 policy on fp16 matrix cores (split operands): tile images of W0..W2 split with the
+// power-of-two scales scale3 (inverse winv3), h3 written as in mode 2
+size_t mlp_tile_x_bytes();
+void launch_mlp_permute_x(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2,
+                          const float* scale3, void* tiles);
+void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, const void* tiles,
+                         const float* winv3, void* h3x, float* h3inv, float* ds);
+void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tiles, const float* winv3,
+                             const float* ds, const float* gh3, float* gef, int accumulate);
 // half: h3, W3T and w fp16 arrays (fp32 accumulation); else fp32
 void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w,
                     int half);

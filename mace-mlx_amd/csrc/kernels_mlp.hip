@@ -841,6 +841,276 @@ __global__ void __launch_bounds__(256) k_mlp_hidden_bwd(int64_t E, int nb, const
   }
 }
 
+// ---------------------------------------------------------------------------
+// Hidden layers on fp16 matrix cores with split operands (float32 policy).
+//
+// Same register layout as the fp32 kernels (lane (g, r) holds edge r's features
+// n = 16t + 4g + i as v[4t + i]); v_mfma_f32_16x16x32_f16 takes eight k per lane,
+// so a 64-wide layer is two chunks c, lane group g supplying in chunk c the eight
+// values of tiles t = 2c, 2c + 1:
+//   slot (c, g, j) <-> k = kperm2(c, g, j) = 16 (2c + j/4) + 4g + j%4.
+// Activations are scaled per edge and layer (largest magnitude of the edge's 64
+// values into [2^14, 2^15), reduced over its four lanes) and split into fp16
+// hi + lo; weights are split once per model with one power-of-two scale per
+// matrix; three products per pair, fp32 accumulation (about 2^-22 relative per
+// product).  The first layer contracts over the Bessel features, slot (g, j) <->
+// k = 8g + j (zero past nb).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int kperm2(int c, int g, int j) { return 16 * (2 * c + (j >> 2)) + 4 * g + (j & 3); }
+
+// split tile images, [.. ][hi, lo][lane] (lane = 16 g + r)
+struct MlpFwdX {
+  h8 w0[4][2][64];     // [t'] A[n = 16t' + r][8g + j] = W0[8g + j][n]
+  h8 w1[2][4][2][64];  // [c][t'] A[n = 16t' + r][slot] = W1[kperm2(c, g, j)][n]
+  h8 w2[2][4][2][64];
+};
+struct MlpBwdX {
+  h8 w2T[2][4][2][64];  // [c][t'] A[k = 16t' + r][slot] = W2[k][kperm2(c, g, j)]
+  h8 w1T[2][4][2][64];
+  h8 w0T[2][2][64];     // [c] A[k = r][slot] = W0[r][kperm2(c, g, j)] (zero for r >= nb)
+};
+
+__device__ __forceinline__ void split_pair(float x, _Float16& hi, _Float16& lo) {
+  hi = (_Float16)x;
+  lo = (_Float16)(x - (float)hi);
+}
+// element j of the pair of vectors (hi, lo)
+__device__ __forceinline__ void split_into(float x, h8& hi, h8& lo, int j) {
+  const _Float16 a = (_Float16)x;
+  hi[j] = a;
+  lo[j] = (_Float16)(x - (float)a);
+}
+
+__global__ void __launch_bounds__(256) k_mlp_permute_x(int nb, const float* __restrict__ W0,
+                                                       const float* __restrict__ W1, const float* __restrict__ W2,
+                                                       float s0, float s1, float s2, MlpFwdX* __restrict__ fw,
+                                                       MlpBwdX* __restrict__ bw) {
+  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4, q = threadIdx.x >> 6;  // q: one of 4 tiles
+  for (int c = 0; c < 2; ++c) {
+    h8 a[2][2], b[2][2];  // [forward W1, W2 | backward W2T, W1T][hi, lo]
+    for (int j = 0; j < 8; ++j) {
+      const int k = kperm2(c, g, j), n = 16 * q + r;
+      split_into(W1[k * H + n] * s1, a[0][0], a[0][1], j);
+      split_into(W2[k * H + n] * s2, a[1][0], a[1][1], j);
+      split_into(W2[n * H + k] * s2, b[0][0], b[0][1], j);
+      split_into(W1[n * H + k] * s1, b[1][0], b[1][1], j);
+    }
+    for (int pl = 0; pl < 2; ++pl) {
+      fw->w1[c][q][pl][l] = a[0][pl];
+      fw->w2[c][q][pl][l] = a[1][pl];
+      bw->w2T[c][q][pl][l] = b[0][pl];
+      bw->w1T[c][q][pl][l] = b[1][pl];
+    }
+    if (q == 0) {
+      h8 t[2];
+      for (int j = 0; j < 8; ++j) split_into(r < nb ? W0[r * H + kperm2(c, g, j)] * s0 : 0.f, t[0], t[1], j);
+      bw->w0T[c][0][l] = t[0];
+      bw->w0T[c][1][l] = t[1];
+    }
+  }
+  h8 t[2];
+  for (int j = 0; j < 8; ++j) {
+    const int k = 8 * g + j;
+    split_into(k < nb ? W0[k * H + 16 * q + r] * s0 : 0.f, t[0], t[1], j);
+  }
+  fw->w0[q][0][l] = t[0];
+  fw->w0[q][1][l] = t[1];
+}
+
+// per-edge scale of a lane's values: returns the scale, sets *inv = its inverse
+template <int NV>
+__device__ __forceinline__ float edge_scale(const float* v, float* inv) {
+  float m = 0.f;
+#pragma unroll
+  for (int q = 0; q < NV; ++q) m = fmaxf(m, fabsf(v[q]));
+  m = fmaxf(m, __shfl_xor(m, 16));
+  m = fmaxf(m, __shfl_xor(m, 32));
+  // floor(log2 m) from the exponent field; zero / subnormal edges take -100 (finite scales)
+  const int ex = max((int)((__float_as_uint(m) >> 23) & 0xff) - 127, -100);
+  *inv = __uint_as_float((unsigned)(127 - 14 + ex) << 23);
+  return __uint_as_float((unsigned)(127 + 14 - ex) << 23);
+}
+
+// one 64-wide layer from the lane's 16 values v (all four output tiles t'):
+// acc[t'] = (A_t' x v) with A = tile image w[c][t'][hi, lo][lane], times winv
+__device__ __forceinline__ void layer64x(const h8 (*w)[4][2][64], const float* v, float winv, f4v* acc) {
+  const int l = threadIdx.x & 63;
+  float inv;
+  const float sc = edge_scale<16>(v, &inv);
+  inv *= winv;
+  f4v d[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) d[t] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    h8 xh, xl;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      _Float16 hi, lo;
+      split_pair(v[4 * (2 * c + (j >> 2)) + (j & 3)] * sc, hi, lo);
+      xh[j] = hi;
+      xl[j] = lo;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const h8 wh = w[c][t][0][l], wl = w[c][t][1][l];
+      d[t] = mfma16h(wl, xh, d[t]);
+      d[t] = mfma16h(wh, xl, d[t]);
+      d[t] = mfma16h(wh, xh, d[t]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = d[t] * inv;
+}
+
+// forward of the split kernels: first layer over the Bessel features, then two 64-wide
+// layers; dsp as in hidden_fwd; leaves a3
+__device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* winv, int64_t E, int64_t e0, int nb,
+                                             const float* __restrict__ ef, f4v* a3, float* dsp) {
+  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const int64_t e = e0 + r;
+  float x[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int k = 8 * g + j;
+    x[j] = (e < E && k < nb) ? ef[e * nb + k] : 0.f;
+  }
+  f4v a1[4], a2[4];
+  {
+    float inv;
+    const float sc = edge_scale<8>(x, &inv);
+    inv *= winv[0];
+    h8 xh, xl;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      _Float16 hi, lo;
+      split_pair(x[j] * sc, hi, lo);
+      xh[j] = hi;
+      xl[j] = lo;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const h8 wh = sw.w0[t][0][l], wl = sw.w0[t][1][l];
+      f4v d = mfma16h(wl, xh, f4v{0.f, 0.f, 0.f, 0.f});
+      d = mfma16h(wh, xl, d);
+      d = mfma16h(wh, xh, d);
+      a1[t] = d * inv;
+    }
+  }
+  float v[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) v[q] = silu(a1[q >> 2][q & 3]);
+  if (dsp) store_ds(dsp, a1);
+  layer64x(sw.w1, v, winv[1], a2);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) v[q] = silu(a2[q >> 2][q & 3]);
+  if (dsp) store_ds(dsp + H, a2);
+  layer64x(sw.w2, v, winv[2], a3);
+  if (dsp) store_ds(dsp + 2 * H, a3);
+}
+
+struct MlpWinv {
+  float w[3];
+};
+
+// h3 as split pairs [E][2][64] + h3inv (H3_SPLIT layout) and silu' saved in ds
+__global__ void __launch_bounds__(256) k_mlp_hidden_x(int64_t E, int nb, const float* __restrict__ ef,
+                                                      const MlpFwdX* __restrict__ tiles, MlpWinv wi,
+                                                      _Float16* __restrict__ h3x, float* __restrict__ h3inv,
+                                                      float* __restrict__ ds) {
+  __shared__ MlpFwdX sw;
+  stage_copy(sw, tiles);
+  __syncthreads();
+  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const int64_t ngroups = (E + 15) / 16;
+  for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
+    const int64_t e0 = gi * 16, e = e0 + r;
+    f4v a3[4];
+    hidden_fwd_x(sw, wi.w, E, e0, nb, ef, a3, (ds && e < E) ? ds + e * 3 * H + 4 * g : nullptr);
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v[q] = silu(a3[q >> 2][q & 3]);
+    float inv;
+    const float sc = edge_scale<16>(v, &inv);
+    if (e < E) {
+      _Float16* dst = h3x + e * 2 * H;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        h4 hi, lo;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          _Float16 a, b;
+          split_pair(v[4 * t + i] * sc, a, b);
+          hi[i] = a;
+          lo[i] = b;
+        }
+        *reinterpret_cast<h4*>(dst + 16 * t + 4 * g) = hi;
+        *reinterpret_cast<h4*>(dst + H + 16 * t + 4 * g) = lo;
+      }
+      if (g == 0) h3inv[e] = inv;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) k_mlp_hidden_bwd_x(int64_t E, int nb, const MlpBwdX* __restrict__ tiles,
+                                                          MlpWinv wi, const float* __restrict__ ds,
+                                                          const float* __restrict__ gh3, float* __restrict__ gef,
+                                                          int accumulate) {
+  __shared__ MlpBwdX sw;
+  stage_copy(sw, tiles);
+  __syncthreads();
+  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const int64_t ngroups = (E + 15) / 16;
+  for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
+    const int64_t e0 = gi * 16, e = e0 + r, ec = e < E ? e : E - 1;  // rows past the end: computed, not stored
+    const float* d = ds + ec * 3 * H;
+    float v[16], dv[16];
+    f4v acc[4];
+    ld_row16(gh3 + ec * H, g, v);
+    ld_row16(d + 2 * H, g, dv);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v[q] *= dv[q];
+    ld_row16(d + H, g, dv);
+    layer64x(sw.w2T, v, wi.w[2], acc);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v[q] = acc[q >> 2][q & 3] * dv[q];
+    ld_row16(d, g, dv);
+    layer64x(sw.w1T, v, wi.w[1], acc);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v[q] = acc[q >> 2][q & 3] * dv[q];
+    // g_ef = g_a1 W0^T: one output tile (rows k < nb)
+    float inv;
+    const float sc = edge_scale<16>(v, &inv);
+    inv *= wi.w[0];
+    f4v o = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      h8 xh, xl;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        _Float16 hi, lo;
+        split_pair(v[4 * (2 * c + (j >> 2)) + (j & 3)] * sc, hi, lo);
+        xh[j] = hi;
+        xl[j] = lo;
+      }
+      const h8 wh = sw.w0T[c][0][l], wl = sw.w0T[c][1][l];
+      o = mfma16h(wl, xh, o);
+      o = mfma16h(wh, xl, o);
+      o = mfma16h(wh, xh, o);
+    }
+    if (e < E) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int k = 4 * g + i;
+        if (k < nb) {
+          float* dst = gef + e * nb + k;
+          *dst = accumulate ? *dst + o[i] * inv : o[i] * inv;
+        }
+      }
+    }
+  }
+}
+
 inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
 
 }  // namespace
@@ -850,6 +1120,32 @@ inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
 inline unsigned hidden_grid(int64_t E) { return (unsigned)std::min<int64_t>((E + 63) / 64, 512); }
 
 size_t mlp_tile_bytes() { return sizeof(MlpFwdW) + sizeof(MlpBwdW); }
+size_t mlp_tile_x_bytes() { return sizeof(MlpFwdX) + sizeof(MlpBwdX); }
+
+void launch_mlp_permute_x(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2,
+                          const float* scale3, void* tiles) {
+  MlpFwdX* fw = static_cast<MlpFwdX*>(tiles);
+  MlpBwdX* bw = reinterpret_cast<MlpBwdX*>(static_cast<char*>(tiles) + sizeof(MlpFwdX));
+  hipLaunchKernelGGL(k_mlp_permute_x, dim3(1), dim3(256), 0, st, nb, W0, W1, W2, scale3[0], scale3[1], scale3[2],
+                     fw, bw);
+}
+
+void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, const void* tiles,
+                         const float* winv3, void* h3x, float* h3inv, float* ds) {
+  if (E <= 0) return;
+  MlpWinv wi{{winv3[0], winv3[1], winv3[2]}};
+  hipLaunchKernelGGL(k_mlp_hidden_x, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef,
+                     static_cast<const MlpFwdX*>(tiles), wi, static_cast<_Float16*>(h3x), h3inv, ds);
+}
+
+void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tiles, const float* winv3,
+                             const float* ds, const float* gh3, float* gef, int accumulate) {
+  if (E <= 0) return;
+  MlpWinv wi{{winv3[0], winv3[1], winv3[2]}};
+  const MlpBwdX* bw = reinterpret_cast<const MlpBwdX*>(static_cast<const char*>(tiles) + sizeof(MlpFwdX));
+  hipLaunchKernelGGL(k_mlp_hidden_bwd_x, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, bw, wi, ds, gh3, gef,
+                     accumulate);
+}
 
 void launch_mlp_permute(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2, void* tiles) {
   MlpFwdW* fw = static_cast<MlpFwdW*>(tiles);
