@@ -414,7 +414,8 @@ __global__ void __launch_bounds__(256) k_mlp_out_h(int64_t E, int W, const _Floa
 // on v_mfma_f32_16x16x32_f16 with fp32 accumulation (the dropped a_lo b_lo and
 // the split residuals are about 2^-22 of |a b|).  W3Tx = [hi | lo] planes of W3^T
 // [W][64].  Tiling, prefetch and the LDS-staged 128-byte row stores as in
-// k_mlp_out; the row scales are applied when the tile is staged.
+// k_mlp_out (stores nontemporal: the TP kernel streams w back with nontemporal loads);
+// the row scales are applied when the tile is staged.
 __global__ void __launch_bounds__(256) k_mlp_out_x(int64_t E, int W, const _Float16* __restrict__ h3x,
                                                    const float* __restrict__ h3inv,
                                                    const _Float16* __restrict__ W3Tx, float cscale,
@@ -487,7 +488,8 @@ __global__ void __launch_bounds__(256) k_mlp_out_x(int64_t E, int W, const _Floa
       const int rr = (l >> 3) + 8 * q;
       const int64_t row = row0 + rr;
       if (row < E && c0 + 4 * (l & 7) < ce)
-        *reinterpret_cast<float4*>(&w[row * W + c0 + 4 * (l & 7)]) = ld4(&O[rr][4 * (l & 7)]);
+        __builtin_nontemporal_store(*reinterpret_cast<const f4v*>(&O[rr][4 * (l & 7)]),
+                                    reinterpret_cast<f4v*>(&w[row * W + c0 + 4 * (l & 7)]));
     }
     wave_sync();
 #pragma unroll
