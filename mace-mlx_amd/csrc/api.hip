@@ -88,7 +88,7 @@ struct Layer {
   DBuf<float> mskip[4], mskipT[4], dens;
   int nskip = 0;
   // per-step activations (TP weights: w, or wh under the float16 feature policy)
-  DBuf<float> h_up, A, w, ro_e;
+  DBuf<float> h_up, A, w;
   DBuf<float> A2, rinv;  // message after its skip FCTP (non-residual block); 1 / (1 + density)
   DBuf<float> ds;        // silu' of the radial MLP's pre-activations, [E][3][64]
   DBuf<_Float16> wh;
@@ -140,7 +140,7 @@ struct mace_ctx {
   DBuf<double> vir_part;
   // node buffers
   std::vector<DBuf<float>> h;  // h[0..L]
-  DBuf<float> M, B, gB, gA, gM, gh0, gh1, gup, ypre, node_e;
+  DBuf<float> M, B, gB, gA, gM, gh0, gh1, gup, node_e;
   DBuf<double> out;  // [energy, vir9, forces 3N]
   DBuf<double> e_part;  // per-block energy partials
   double* out_pinned = nullptr;
@@ -303,7 +303,7 @@ void free_layers(mace_ctx* c) {
       for (int i = 0; i < 3; ++i) arr[i].release();
     for (int i = 0; i < 4; ++i) L.mlp[i].release(), L.mlpT[i].release(), L.lin_[i].release(), L.linT[i].release();
     L.ro.release(), L.ro1.release(), L.ro2.release(), L.h_up.release(), L.A.release(), L.w.release(),
-        L.ro_e.release(), L.wh.release(), L.mlpT3h.release(), L.mlp3h.release(), L.A2.release(), L.rinv.release(),
+        L.wh.release(), L.mlpT3h.release(), L.mlp3h.release(), L.A2.release(), L.rinv.release(),
         L.dens.release(), L.mlpT3x.release(), L.mlp3x.release(), L.mlp_tiles.release(), L.ds.release(),
         L.mlp_tiles_x.release();
     for (int i = 0; i < 4; ++i) L.mskip[i].release(), L.mskipT[i].release();
@@ -479,7 +479,6 @@ void ensure_node_buffers(mace_ctx* c) {
     c->h[l].ensure((size_t)N * ly.din);
     ly.h_up.ensure((size_t)N * ly.din);
     ly.A.ensure((size_t)N * ly.dint);
-    ly.ro_e.ensure(N);
     if (!ly.resid) ly.A2.ensure((size_t)N * ly.dint);
     if (c->dims.density_norm) ly.rinv.ensure(N);
     maxd = std::max({maxd, ly.dmid, ly.din, ly.dhid});
@@ -495,7 +494,6 @@ void ensure_node_buffers(mace_ctx* c) {
   c->gup.ensure((size_t)N * maxd);
   c->gA2.ensure((size_t)N * maxd);
   c->grho.ensure(N);
-  c->ypre.ensure((size_t)N * 16);
   c->node_e.ensure(N);
   c->e_part.ensure((N + 3) / 4 + 1);
 
@@ -1037,17 +1035,21 @@ void forward(mace_ctx* c, const double* pos, double* out) {
         Site s(c, lname("skip", l));
         run_skip(c, L, b, h, hn, L.dhid, 1, half);
       }
-    Site s(c, lname("readout", l));
-    if (l + 1 < c->layers.size())
-      launch_readout_linear(st, N, hn, L.dhid, L.ro.p, L.ro_e.p, half);
-    else
-      launch_readout_mlp(st, N, hn, L.dhid, L.ro1.p, L.ro2.p, L.ro_e.p, c->ypre.p, half);
   }
-  const float* ro[4];
-  for (size_t l = 0; l < c->layers.size(); ++l) ro[l] = c->layers[l].ro_e.p;
-  Site s(c, "node_energy");
-  launch_node_energy(st, N, c->species.p, c->e0.p, c->rowptr.p, c->dims.has_zbl ? c->zbl_e.p : nullptr, ro,
-                     (int)c->layers.size(), c->node_e.p, c->e_part.p, out);
+  // readouts, node energies and dE/dh_L (the backward's starting gradient) in one pass
+  const int L = (int)c->layers.size();
+  const float* hs[4] = {nullptr, nullptr, nullptr, nullptr};
+  const float* ros[4] = {nullptr, nullptr, nullptr, nullptr};
+  int lds[4] = {0, 0, 0, 0};
+  for (int l = 0; l < L; ++l) {
+    hs[l] = c->h[l + 1].p;
+    lds[l] = c->layers[l].dhid;
+    ros[l] = c->layers[l].ro.p;
+  }
+  Site s(c, "energy_readout");
+  launch_energy_readout(st, N, c->species.p, c->e0.p, c->rowptr.p, c->dims.has_zbl ? c->zbl_e.p : nullptr, L, hs,
+                        lds, ros, c->layers[L - 1].ro1.p, c->layers[L - 1].ro2.p, c->gh0.p, c->layers[L - 1].dhid,
+                        c->node_e.p, c->e_part.p, out, half);
 }
 
 void backward(mace_ctx* c, bool stress, double* out) {
@@ -1058,14 +1060,9 @@ void backward(mace_ctx* c, bool stress, double* out) {
   const int L = (int)c->layers.size();
   const int half = c->dims.feature_half != 0;
   const bool split = !half && c->split_products;
-  // dE/dh_L from the nonlinear readout
+  // dE/dh_L from the nonlinear readout: written by the forward's energy_readout pass
   float* gh = c->gh0.p;
   float* gh_next = c->gh1.p;
-  {
-    Site s(c, "readout_bwd");
-    launch_readout_mlp_bwd(st, N, c->ypre.p, c->layers[L - 1].ro1.p, c->layers[L - 1].ro2.p, gh,
-                           c->layers[L - 1].dhid);
-  }
   for (int l = L - 1; l >= 0; --l) {
     Layer& Ly = c->layers[l];
     const bool one_el = c->dims.num_elements == 1;
@@ -1226,7 +1223,7 @@ static void free_all(mace_ctx* c) {
   c->gwh.release();
   c->gscale.release();
   for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->ag_cov, &c->gA2, &c->grho, &c->embed, &c->up0_tab, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
-                  &c->gv, &c->gw, &c->gxe, &c->h3, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup, &c->ypre,
+                  &c->gv, &c->gw, &c->gxe, &c->h3, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup,
                   &c->node_e})
     b->release();
   for (auto* b : {&c->species, &c->sender, &c->receiver, &c->shifts, &c->rowptr, &c->rowptr_s, &c->perm_s, &c->pos_s,

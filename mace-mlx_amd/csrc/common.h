@@ -201,20 +201,13 @@ void launch_sc_bwd(hipStream_t st, int N, int nout, int corr, const float* A, in
                    const int* species, const float* const* Wsc, const float* gB, int ldB,
                    float* gA);
 
-// readouts.  linear: e[n] = h[n, 0:NC] . w ; nonlinear: 16-wide SiLU MLP
-void launch_readout_linear(hipStream_t st, int N, const float* h, int ldh, const float* w,
-                           float* e, int half);
-void launch_readout_mlp(hipStream_t st, int N, const float* h, int ldh, const float* W1,
-                        const float* W2, float* e, float* ypre, int half);
-void launch_readout_mlp_bwd(hipStream_t st, int N, const float* ypre, const float* W1,
-                            const float* W2, float* gh, int ldh);
-void launch_readout_linear_bwd(hipStream_t st, int N, const float* w, float* gh, int ldh,
-                               int accumulate);
 
-// node energies and their total (block partials, then a fixed-order sum)
-void launch_node_energy(hipStream_t st, int N, const int* species, const float* e0, const int* rowptr,
-                        const float* zbl_e, const float* const* ro, int nro, float* node_e, double* part,
-                        double* energy);
+// readouts of every layer (linear for l < L-1 on h[l], MLP W1 [128][16], W2 [16] for the last),
+// node energies, their total and dE/dh_L (gh, row stride ldgh) in one pass
+void launch_energy_readout(hipStream_t st, int N, const int* species, const float* e0, const int* rowptr,
+                           const float* zbl_e, int L, const float* const* h, const int* ldh, const float* const* ro,
+                           const float* W1, const float* W2, float* gh, int ldgh, float* node_e, double* part,
+                           double* energy, int half);
 // vir_zero (may be null) receives nine zeros
 void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s, const int* perm_s,
                    const float* gv, double* forces, double* vir_zero);

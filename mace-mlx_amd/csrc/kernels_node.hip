@@ -455,7 +455,7 @@ __global__ void __launch_bounds__(NC) k_sc_bwd(int N, int nout, const float* __r
 }
 
 // ---------------------------------------------------------------------------
-// readouts (one 64-lane wavefront per node)
+// wave reductions
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -463,79 +463,33 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-__global__ void __launch_bounds__(64) k_readout_linear(int N, const float* __restrict__ h, int ldh,
-                                                       const float* __restrict__ w, float* __restrict__ e, int half) {
-  const int n = blockIdx.x, l = threadIdx.x;
-  const float* hn = h + (int64_t)n * ldh;
-  float a = 0.f;
-  for (int u = l; u < NC; u += 64) a = fmaf(hn[u], w[u], a);
-  a = wave_sum(a);
-  if (l == 0) e[n] = qh(a, half);
-}
-
-__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
-
-__global__ void __launch_bounds__(64) k_readout_mlp(int N, const float* __restrict__ h, int ldh,
-                                                    const float* __restrict__ W1, const float* __restrict__ W2,
-                                                    float* __restrict__ e, float* __restrict__ ypre, int half) {
-  const int n = blockIdx.x, l = threadIdx.x;
-  const float* hn = h + (int64_t)n * ldh;
-  float y[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) y[j] = 0.f;
-  for (int u = l; u < NC; u += 64) {
-    const float x = hn[u];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) y[j] = fmaf(x, W1[u * 16 + j], y[j]);
-  }
-#pragma unroll
-  for (int j = 0; j < 16; ++j) y[j] = wave_sum(y[j]);
-  if (l == 0) {
-    float a = 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float yj = qh(y[j], half);
-      ypre[(int64_t)n * 16 + j] = yj;
-      a = fmaf(qh(silu_f(yj), half), W2[j], a);
-    }
-    e[n] = qh(a, half);
-  }
-}
-
-__global__ void __launch_bounds__(NC) k_readout_mlp_bwd(int N, const float* __restrict__ ypre,
-                                                        const float* __restrict__ W1, const float* __restrict__ W2,
-                                                        float* __restrict__ gh, int ldh) {
-  const int n = blockIdx.x, u = threadIdx.x;
-  float a = 0.f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const float y = ypre[(int64_t)n * 16 + j];
-    const float s = 1.f / (1.f + expf(-y));
-    a = fmaf(W1[u * 16 + j], W2[j] * s * (1.f + y * (1.f - s)), a);
-  }
-  gh[(int64_t)n * ldh + u] = a;
-}
-
-__global__ void __launch_bounds__(NC) k_readout_linear_bwd(int N, const float* __restrict__ w,
-                                                           float* __restrict__ gh, int ldh, int accumulate) {
-  const int n = blockIdx.x, u = threadIdx.x;
-  float* p = gh + (int64_t)n * ldh + u;
-  *p = accumulate ? *p + w[u] : w[u];
-}
-
 // ---------------------------------------------------------------------------
 // energy assembly and reductions (fixed order: deterministic)
 // ---------------------------------------------------------------------------
-struct RoPtrs {
-  const float* p[4];
+// Readouts, node energies and the first backward gradient in one pass, one
+// wavefront per atom (layers 0 .. L-2: linear readouts of h_{l+1}; layer L-1: the
+// MLP readout 128 -> 16 -> silu -> 1, `blocks.py:540-608`):
+//   node_e[n] = E0[z] + sum of the atom's pair-repulsion edge energies + readouts,
+//   gh[n][u] = dE/dh_L[n][u] = sum_j W1[u][j] W2[j] silu'(y_j)
+// (dE/dnode_e = 1, so the readout's VJP needs nothing from later kernels).  Lane l
+// computes hidden unit j = l / 4 over the channel quarter 32 (l % 4) .. + 31.
+struct ReadoutArgs {
+  const float* h[4];   // h_{l+1}, 0e block at the row start
+  const float* ro[4];  // linear readout weights (layers < L-1)
+  int ldh[4];
+  int L;
+  const float* W1;     // last layer: [128][16]
+  const float* W2;     // [16]
+  float* gh;           // dE/dh_L, row stride ldgh
+  int ldgh;
 };
 
-// one wavefront per atom: the pair-repulsion energies of the atom's received edges are read
-// coalesced and summed by a fixed shuffle tree; block partial = sum of its four atoms
-__global__ void __launch_bounds__(256) k_node_energy(int N, const int* __restrict__ species,
-                                                     const float* __restrict__ e0, const int* __restrict__ rowptr,
-                                                     const float* __restrict__ zbl_e, RoPtrs ro, int nro,
-                                                     float* __restrict__ node_e, double* __restrict__ part) {
+__global__ void __launch_bounds__(256) k_energy_readout(int N, const int* __restrict__ species,
+                                                        const float* __restrict__ e0,
+                                                        const int* __restrict__ rowptr,
+                                                        const float* __restrict__ zbl_e, ReadoutArgs A,
+                                                        float* __restrict__ node_e, double* __restrict__ part,
+                                                        int half) {
   __shared__ double red[4];
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + w;
@@ -544,9 +498,38 @@ __global__ void __launch_bounds__(256) k_node_energy(int N, const int* __restric
     float z = 0.f;
     if (zbl_e)
       for (int e = rowptr[n] + l; e < rowptr[n + 1]; e += 64) z += zbl_e[e];
-    z = wave_sum(z);
-    float v = e0[species[n]] + z;
-    for (int k = 0; k < nro; ++k) v += ro.p[k][n];
+    float v = e0[species[n]] + wave_sum(z);
+    for (int k = 0; k + 1 < A.L; ++k) {  // linear readouts
+      const float* hn = A.h[k] + (int64_t)n * A.ldh[k];
+      const float a = wave_sum(fmaf(hn[l], A.ro[k][l], hn[l + 64] * A.ro[k][l + 64]));
+      v += qh(a, half);
+    }
+    {  // MLP readout of the last layer and its gradient
+      const float* hn = A.h[A.L - 1] + (int64_t)n * A.ldh[A.L - 1];
+      const int j = l >> 2, q = l & 3;
+      float y = 0.f;
+#pragma unroll 8
+      for (int u = 32 * q; u < 32 * q + 32; ++u) y = fmaf(hn[u], A.W1[u * 16 + j], y);
+      y += __shfl_xor(y, 1);
+      y += __shfl_xor(y, 2);
+      y = qh(y, half);
+      const float sg = 1.f / (1.f + expf(-y));
+      float a = (q == 0) ? qh(y * sg, half) * A.W2[j] : 0.f;
+#pragma unroll
+      for (int off = 4; off < 64; off <<= 1) a += __shfl_xor(a, off);
+      v += qh(a, half);
+      const float cj = A.W2[j] * sg * (1.f + y * (1.f - sg));  // on the four lanes of unit j
+      float g0 = 0.f, g1 = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const float c = __shfl(cj, 4 * jj);
+        g0 = fmaf(A.W1[l * 16 + jj], c, g0);
+        g1 = fmaf(A.W1[(l + 64) * 16 + jj], c, g1);
+      }
+      float* gn = A.gh + (int64_t)n * A.ldgh;
+      gn[l] = g0;
+      gn[l + 64] = g1;
+    }
     if (l == 0) node_e[n] = v;
     acc = (double)v;
   }
@@ -675,42 +658,30 @@ void launch_sc_bwd(hipStream_t st, int N, int nout, int corr, const float* A, in
   }
 }
 
-void launch_readout_linear(hipStream_t st, int N, const float* h, int ldh, const float* w, float* e, int half) {
-  if (N <= 0) return;
-  hipLaunchKernelGGL(k_readout_linear, dim3(N), dim3(64), 0, st, N, h, ldh, w, e, half);
-}
-
-void launch_readout_mlp(hipStream_t st, int N, const float* h, int ldh, const float* W1, const float* W2,
-                        float* e, float* ypre, int half) {
-  if (N <= 0) return;
-  hipLaunchKernelGGL(k_readout_mlp, dim3(N), dim3(64), 0, st, N, h, ldh, W1, W2, e, ypre, half);
-}
-
-void launch_readout_mlp_bwd(hipStream_t st, int N, const float* ypre, const float* W1, const float* W2,
-                            float* gh, int ldh) {
-  if (N <= 0) return;
-  hipLaunchKernelGGL(k_readout_mlp_bwd, dim3(N), dim3(NC), 0, st, N, ypre, W1, W2, gh, ldh);
-}
-
-void launch_readout_linear_bwd(hipStream_t st, int N, const float* w, float* gh, int ldh, int accumulate) {
-  if (N <= 0) return;
-  hipLaunchKernelGGL(k_readout_linear_bwd, dim3(N), dim3(NC), 0, st, N, w, gh, ldh, accumulate);
-}
-
-void launch_node_energy(hipStream_t st, int N, const int* species, const float* e0, const int* rowptr,
-                        const float* zbl_e, const float* const* ro, int nro, float* node_e, double* part,
-                        double* energy) {
-  RoPtrs r{{nullptr, nullptr, nullptr, nullptr}};
-  for (int l = 0; l < nro && l < 4; ++l) r.p[l] = ro[l];
-  const int nblk = (int)cdiv(N, 4);
-  if (nblk > 0)
-    hipLaunchKernelGGL(k_node_energy, dim3(nblk), dim3(256), 0, st, N, species, e0, rowptr, zbl_e, r, nro, node_e,
-                       part);
-  hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(256), 0, st, part, nblk, energy);
-}
-
 void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir) {
   hipLaunchKernelGGL(k_virial_reduce, dim3(1), dim3(256), 0, st, part, nblk, vir);
+}
+
+void launch_energy_readout(hipStream_t st, int N, const int* species, const float* e0, const int* rowptr,
+                           const float* zbl_e, int L, const float* const* h, const int* ldh, const float* const* ro,
+                           const float* W1, const float* W2, float* gh, int ldgh, float* node_e, double* part,
+                           double* energy, int half) {
+  ReadoutArgs A{};
+  A.L = L;
+  for (int k = 0; k < L && k < 4; ++k) {
+    A.h[k] = h[k];
+    A.ldh[k] = ldh[k];
+    A.ro[k] = ro[k];
+  }
+  A.W1 = W1;
+  A.W2 = W2;
+  A.gh = gh;
+  A.ldgh = ldgh;
+  const int nblk = (int)cdiv(N, 4);
+  if (nblk > 0)
+    hipLaunchKernelGGL(k_energy_readout, dim3(nblk), dim3(256), 0, st, N, species, e0, rowptr, zbl_e, A, node_e,
+                       part, half);
+  hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(256), 0, st, part, nblk, energy);
 }
 
 void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s, const int* perm_s,
