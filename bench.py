@@ -180,6 +180,8 @@ def measure_config(idx, steps, warmup):
     dm = build_device_model(bc.model, weights, dtype=bc.dtype)
     eng = Engine(0)
     eng.load_model(dm)
+    if args.separate_mlp_out:
+        eng.set_fused_tp(False)
     s = bc.system
     zmap = {int(z): k for k, z in enumerate(dm.z_table)}
     species = np.array([zmap[int(z)] for z in s.numbers], np.int32)
@@ -233,6 +235,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=1, help="benchmark configuration index 0..4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--separate-mlp-out", action="store_true",
+                    help="float32 policy: radial-MLP output layer as its own pass (not fused into the TP)")
     ap.add_argument("--kernel-table", action="store_true", help="print per-kernel times to stderr")
     ap.add_argument("--sweep", action="store_true",
                     help="also measure every benchmark configuration (table on stderr, 'sweep' in the JSON)")

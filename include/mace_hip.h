@@ -159,6 +159,15 @@ int mace_set_graphs(mace_ctx* ctx, int32_t enable);
  * dtype, model.py:592-661). */
 int mace_set_split_products(mace_ctx* ctx, int32_t enable);
 
+/* With split products on (float32 feature policy): build the radial MLP's
+ * per-edge tensor-product weights inside the tensor-product kernels, tile by
+ * tile, instead of materialising them in a separate pass first (enable != 0,
+ * the default).  The arithmetic is the same split product; only the order of
+ * the work changes.  Off selects the separate passes (kept for comparison).
+ * No counterpart in the reference (the same evaluation as
+ * blocks.py:253-274). */
+int mace_set_fused_tp(mace_ctx* ctx, int32_t enable);
+
 /* Timing of the last mace_step (device milliseconds, HIP events on the
  * context's stream): [0] whole step, [1] neighbour list (0 if cached),
  * [2] forward, [3] backward.  Returns the number of values written. */

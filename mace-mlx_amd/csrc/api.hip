@@ -110,6 +110,7 @@ struct mace_ctx {
   int mts = 0;  // row stride of the per-edge TP tables Mt (0: no layer has l1 >= 1 inputs)
   DBuf<float> e0, bessel_w, zbl_z, zbl_cov, ag_cov, embed;
   DBuf<float> up0_tab;  // first linear_up per species [n_el][C]
+  DBuf<float> sink;     // fused TP: target of the weight stores of padding edges (max slots x C floats)
   DBuf<float> gA2, grho;  // backward scratch of the message skip / density normalisation
   // system
   int N = 0;
@@ -158,6 +159,7 @@ struct mace_ctx {
   };
   bool use_graphs = true;
   bool split_products = true;  // float32 policy: matrix products on fp16 matrix cores (split operands)
+  bool fused_tp = true;        // with split products: radial-MLP output layer fused into the TP kernels
   struct SplitW {
     DBuf<_Float16> x;  // [hi | lo] planes of the weights scaled by 1 / winv
     float winv = 1.f;
@@ -461,6 +463,9 @@ void build_model(mace_ctx* c) {
   c->max_lin = 1;
   for (const Layer& L : c->layers) c->max_lin = std::max(c->max_lin, L.lin);
   c->mts = (tp_table_entries(c->max_lin) + 15) / 16 * 16;
+  int wmax = 0;
+  for (const Layer& L : c->layers) wmax = std::max(wmax, L.wn);
+  c->sink.ensure((size_t)wmax);
   c->host_tensors.clear();
   c->model_ready = true;
 }
@@ -930,6 +935,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
   const int nb = c->dims.num_bessel;
   const int half = c->dims.feature_half != 0;
   const bool split = !half && c->split_products;
+  const bool fused = split && c->fused_tp && c->max_lin <= 2;
   FrontParams fp = front_params(c);
   {
     Site s(c, "edge_fwd");
@@ -959,7 +965,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
                           half ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), c->h3inv.p, L.ds.p,
                           half ? 1 : 0);
     }
-    {
+    if (!fused) {
       Site s(c, lname("mlp_out", l));
       if (half)
         launch_mlp_out(st, E, L.wn, c->h3h.p, L.mlpT3h.p, L.wh.p, 1);
@@ -978,8 +984,12 @@ void forward(mace_ctx* c, const double* pos, double* out) {
     }
     {
       Site s(c, lname("tp_fwd", l));
-      launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.wptr(half), L.h_up.p, c->M.p,
-                    half);
+      if (fused)
+        launch_tpx_fwd(st, L.lin, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, c->h3.p, c->h3inv.p,
+                       L.mlpT3x.p, L.wn, L.w3inv, L.h_up.p, c->M.p, L.w.p, c->sink.p);
+      else
+        launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.wptr(half), L.h_up.p,
+                      c->M.p, half);
     }
     const int* ao = tp_accoff(L.lin);
     if (c->dims.density_norm) {
@@ -1222,7 +1232,7 @@ static void free_all(mace_ctx* c) {
   c->h3h.release();
   c->gwh.release();
   c->gscale.release();
-  for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->ag_cov, &c->gA2, &c->grho, &c->embed, &c->up0_tab, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
+  for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->ag_cov, &c->gA2, &c->grho, &c->embed, &c->up0_tab, &c->sink, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
                   &c->gv, &c->gw, &c->gxe, &c->h3, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup,
                   &c->node_e})
     b->release();
@@ -1464,6 +1474,15 @@ int mace_set_split_products(mace_ctx* c, int32_t enable) {
   return guard(c, [&] {
     set_device(c);
     c->split_products = enable != 0;
+    invalidate_graphs(c);
+  });
+}
+
+int mace_set_fused_tp(mace_ctx* c, int32_t enable) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    set_device(c);
+    c->fused_tp = enable != 0;
     invalidate_graphs(c);
   });
 }

@@ -138,6 +138,14 @@ void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const
                         const float* gM, void* gw, float* gscale, float* gY, int accumulate_gY,
                         const int* pos_s, float* gxe, int half);
 // gup[a] = sum of the sender-ordered gxe rows of node a
+// Radial-MLP output layer fused into the TP forward (float32 policy with split
+// products, lin <= 2): w is built per 16-edge tile from the split h3 planes
+// (h3x, h3inv) and the split W3^T planes (W3Tx, scale wscale), M is written as
+// by launch_tp_fwd and w ([E][W]) for the VJP; sink: W scratch floats that
+// absorb the stores of padding edges.
+void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
+                    const float* Mt, int mts, const void* h3x, const float* h3inv, const void* W3Tx, int W,
+                    float wscale, const float* up, float* M, float* w, float* sink);
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe,
                          float* gup);
 

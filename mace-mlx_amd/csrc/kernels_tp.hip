@@ -27,6 +27,8 @@
 // adds the two halves.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace mace {
@@ -95,13 +97,15 @@ __device__ __forceinline__ void load_w(const WT* __restrict__ we, float* wv) {
     wv[s] = (float)(NT ? __builtin_nontemporal_load(we + s * NC) : we[s * NC]);
 }
 
-// Forward contribution of one edge to this channel's accumulators.
-template <int LIN>
+// Forward contribution of one edge to this channel's accumulators.  GRP >= 0
+// restricts the sum to the slots whose input block is l1 = GRP.
+template <int LIN, int GRP = -1>
 __device__ __forceinline__ void tp_edge_fwd(float* acc, const EdgeIn<LIN>& in, const float* __restrict__ Ye,
                                             const float* __restrict__ Me, const float* M2) {
   using T = TPT<LIN>;
 #pragma unroll
   for (int s = 0; s < T::NSLOT; ++s) {
+    if (GRP >= 0 && T::l1(s) != GRP) continue;
     const float ww = in.w[s];
     const int a0 = T::acc(s), d = 2 * T::l3(s) + 1;
     if (T::l1(s) == 0) {
@@ -526,6 +530,285 @@ __global__ void __launch_bounds__(64) k_tp_tables(int64_t E, const float* __rest
   }
 }
 
+// ---------------------------------------------------------------------------
+// Radial-MLP output layer fused into the TP forward (float32 policy).
+//
+// The per-edge weights w[e, slot, u] = wscale * h3inv[e] * sum_q h3[e, q] W3[q, slot NC + u]
+// are made per 16-edge tile on the fp16 matrix cores with split operands
+// (h3 as hi / lo planes scaled per edge, W3 as hi / lo planes scaled per matrix:
+// lo.hi + hi.lo + hi.hi, the terms and order of k_mlp_out_x) straight into LDS,
+// consumed there by the TP, and written out once for the VJP.
+//
+// Block = XW waves; wave k owns receiver XW * blockIdx.x + k and walks its
+// edges two per step, lane = channel c0 + u of the block's 64-channel slice
+// (blockIdx.y).  blockIdx.z selects the slots handled: those whose input block
+// is one l1 (highest l1 first), so the groups read and write disjoint data.
+// Tile column r = 2k + b holds edge b of wave k's current pair.  The W3 rows of
+// the block's (slots, slice) stay in registers as MFMA A fragments (roles
+// swapped: D[column 4g + i][edge r], so each lane writes four consecutive
+// columns of one edge); wave k holds column tiles k, k + XW, ...  The tile is
+// double-buffered, one barrier per step.
+// ---------------------------------------------------------------------------
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f4v mfma16h(h8 a, h8 b, f4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+constexpr int XW = 8;          // waves per fused block (receivers in flight)
+constexpr int XH = RADIAL_H;   // radial hidden width (the contraction of the output layer)
+static_assert(XH == 64, "two 32-wide k steps");
+
+// the slots of one input block l1
+template <int LIN, int L1>
+struct GrpT {
+  using T = TPT<LIN>;
+  __host__ __device__ static constexpr int count() {
+    int n = 0;
+    for (int s = 0; s < T::NSLOT; ++s) n += T::l1(s) == L1 ? 1 : 0;
+    return n;
+  }
+  static constexpr int G = count();
+  // position of slot s among the group's slots
+  __host__ __device__ static constexpr int local(int s) {
+    int k = 0;
+    for (int q = 0; q < s; ++q) k += T::l1(q) == L1 ? 1 : 0;
+    return k;
+  }
+  // slot of group position si (run-time si: a select chain over the slots)
+  __device__ static int slot(int si) {
+    int res = 0;
+#pragma unroll
+    for (int s = 0; s < T::NSLOT; ++s)
+      if (T::l1(s) == L1 && local(s) == si) res = s;
+    return res;
+  }
+};
+
+// largest group (LDS size of the fused kernels)
+template <int LIN>
+constexpr int gmax() {
+  return LIN == 1 ? GrpT<1, 0>::G : std::max(GrpT<2, 0>::G, GrpT<2, 1>::G);
+}
+
+// scalar parameters of the fused forward (pointers are passed separately, as
+// __restrict__ kernel arguments: uniform loads through them then use the
+// scalar cache)
+struct TpxDims {
+  int N, W, mts;
+  int64_t E;
+  float wscale;
+};
+
+#define MACE_TPX_FWD_PTRS                                                                                   \
+  const int *__restrict__ rowptr, const int *__restrict__ sender, const float *__restrict__ Y,              \
+      const float *__restrict__ Mt, const _Float16 *__restrict__ h3x, const float *__restrict__ h3inv,     \
+      const _Float16 *__restrict__ W3Tx, const float *__restrict__ up, float *__restrict__ M,               \
+      float *__restrict__ w, float *__restrict__ sink
+#define MACE_TPX_FWD_ARGS rowptr, sender, Y, Mt, h3x, h3inv, W3Tx, up, M, w, sink
+// h3x: [E][hi 64 | lo 64]; h3inv: [E]; W3Tx: [W][64] hi plane, then lo plane;
+// w: [E][W] for the VJP; sink: W floats, target of the stores of padding edges
+
+template <int LIN, int L1>
+__device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, float* sw, float* stab) {
+  using T = TPT<LIN>;
+  using GR = GrpT<LIN, L1>;
+  constexpr int G = GR::G, CT = 4 * G, NCTW = (CT + XW - 1) / XW, RS = 64 * G + 4;
+  constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, NX = 2 * L1 + 1;
+  // wave index through readfirstlane: receiver, edge indices and senders are then
+  // wave-uniform scalars (scalar loads, no vector-memory waits on the prefetches)
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4, u = l;
+  const int c0 = 64 * blockIdx.y, nb0 = XW * blockIdx.x;
+  const int n = nb0 + wv;
+  const int beg = rowptr[min(n, a.N)], end = n < a.N ? rowptr[n + 1] : beg;
+  const int nr = nb0 + (r >> 1);  // receiver of tile column r
+  const int cb = rowptr[min(nr, a.N)], ce = nr < a.N ? rowptr[nr + 1] : cb;
+  int ns = (ce - cb + 1) >> 1;
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) ns = max(ns, __shfl_xor(ns, off));
+  const int nsteps = __builtin_amdgcn_readfirstlane(ns);
+
+  h8 wa[NCTW][2][2];  // [tile][k step][hi, lo]
+#pragma unroll
+  for (int m = 0; m < NCTW; ++m) {
+    const int ct = wv + XW * m;
+    if (CT % XW == 0 || ct < CT) {
+      const int gc = 16 * ct + r;
+      const int64_t col = (int64_t)GR::slot(gc >> 6) * NC + c0 + (gc & 63);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        wa[m][c][0] = *reinterpret_cast<const h8*>(W3Tx + col * XH + 32 * c + 8 * g);
+        wa[m][c][1] = *reinterpret_cast<const h8*>(W3Tx + ((int64_t)a.W + col) * XH + 32 * c + 8 * g);
+      }
+    }
+  }
+  // Every vector-memory operation below is unconditional (indices clamped,
+  // stores of past-the-end edges sent to sink), so the number in flight is
+  // the same on every path and the compiler's wait counts stay exact: a step
+  // waits only for what it consumes, never for the prefetches behind it.
+  const int64_t elast = a.E - 1;  // E >= 1 whenever a step runs
+  // h3 of tile column r, two steps ahead: [k step][hi, lo] per ring slot
+  h8 bx0[2][2], bx1[2][2];
+  float hinv0 = 0.f, hinv1 = 0.f;
+  auto load_b = [&](int j, h8 (&bx)[2][2], float& hinv) {
+    const int64_t row = min<int64_t>(cb + 2 * j + (r & 1), elast);  // columns past a receiver's end: not stored
+    const _Float16* p = h3x + row * 2 * XH + 8 * g;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      bx[c][0] = *reinterpret_cast<const h8*>(p + 32 * c);
+      bx[c][1] = *reinterpret_cast<const h8*>(p + XH + 32 * c);
+    }
+    hinv = h3inv[row];
+  };
+  // sender rows of the next step's edges; their indices (scalar loads) are
+  // fetched a step earlier still
+  float xv[2][NX], xn[2][NX];
+  int snd[2];
+  auto load_snd = [&](int j) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) snd[b] = sender[min<int64_t>(beg + 2 * j + b, elast)];
+  };
+  auto load_x = [&](float (*dst)[NX]) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const float* xs = up + (int64_t)snd[b] * DIN + NC * L1 * L1 + c0 + u;
+#pragma unroll
+      for (int i = 0; i < NX; ++i) dst[b][i] = xs[NC * i];
+    }
+  };
+  // this wave's two edges' table rows (Y for l1 = 0 slots, M1 for l1 = 1
+  // slots): loaded a step ahead, stored to a wave-private LDS row at the start
+  // of their step and read back as broadcast loads
+  constexpr int TY = L1 == 0 ? 16 : 0, TS = TY + (L1 == 1 ? TP3_M1_NE : 0), TSP = (TS + 3) & ~3;
+  constexpr int TH = (TS + 63) / 64;
+  static_assert(TS <= 128 && L1 <= 1, "table rows of up to 128 entries");
+  float* tb = stab + wv * 2 * TSP;  // [edge b][TSP]
+  float tr[2][TH];
+  auto load_t = [&](int j) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int64_t e = min<int64_t>(beg + 2 * j + b, elast);
+#pragma unroll
+      for (int h = 0; h < TH; ++h) {
+        const int i = min(l + 64 * h, TS - 1);
+        tr[b][h] = i < TY ? Y[e * 16 + i] : Mt[e * a.mts + i - TY];
+      }
+    }
+  };
+  auto store_t = [&]() {
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int h = 0; h < TH; ++h)
+        if (l + 64 * h < TS) tb[b * TSP + l + 64 * h] = tr[b][h];
+  };
+  float acc[T::NACC];
+#pragma unroll
+  for (int q = 0; q < T::NACC; ++q) acc[q] = 0.f;
+  auto step = [&](int j, h8 (&bx)[2][2], float& hinv) {
+    float* tile = sw + (j & 1) * 16 * RS;
+    f4v d[NCTW];
+#pragma unroll
+    for (int m = 0; m < NCTW; ++m) d[m] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int m = 0; m < NCTW; ++m)
+          if (CT % XW == 0 || wv + XW * m < CT)  // every wave's tiles exist when XW divides CT
+            d[m] = mfma16h(wa[m][c][p == 2 ? 0 : p ^ 1], bx[c][p == 1 ? 1 : 0], d[m]);  // lo.hi, hi.lo, hi.hi
+    const float bsc = hinv * a.wscale;
+#pragma unroll
+    for (int m = 0; m < NCTW; ++m) {
+      const int ct = wv + XW * m;
+      if (CT % XW == 0 || ct < CT)
+        *reinterpret_cast<float4*>(tile + r * RS + 16 * ct + 4 * g) =
+            float4{d[m][0] * bsc, d[m][1] * bsc, d[m][2] * bsc, d[m][3] * bsc};
+    }
+    load_b(j + 2, bx, hinv);
+    __syncthreads();
+    store_t();
+    wave_sync();
+    load_x(xn);
+    load_snd(j + 2);
+    load_t(j + 1);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int e = beg + 2 * j + b;
+      const bool valid = e < end;
+      float wv_s[T::NSLOT];
+      const float* trow = tile + (2 * wv + b) * RS + u;
+#pragma unroll
+      for (int s = 0; s < T::NSLOT; ++s)
+        if (T::l1(s) == L1) wv_s[s] = trow[64 * GR::local(s)];
+      if (valid) {
+        EdgeIn<LIN> in;
+        in.x0 = 0.f;
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+          if constexpr (L1 == 0) in.x0 = xv[b][i];
+          if constexpr (L1 == 1) in.x1[i] = xv[b][i];
+          if constexpr (L1 == 2) in.x2[i] = xv[b][i];
+        }
+#pragma unroll
+        for (int s = 0; s < T::NSLOT; ++s)
+          if (T::l1(s) == L1) in.w[s] = wv_s[s];
+        const float* trow_t = tb + b * TSP;  // Y (l1 = 0) or M1 (l1 = 1)
+        tp_edge_fwd<LIN, L1>(acc, in, trow_t, trow_t, trow_t);
+      }
+      float* we = (valid ? w + (int64_t)e * a.W : sink) + c0 + u;
+#pragma unroll
+      for (int s = 0; s < T::NSLOT; ++s)
+        if (T::l1(s) == L1) __builtin_nontemporal_store(wv_s[s], we + s * NC);
+    }
+    wave_sync();  // table row reads done before the next step's store
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < NX; ++i) xv[b][i] = xn[b][i];
+  };
+  const int nsteps2 = (nsteps + 1) & ~1;  // even: both ring slots every trip
+  if (nsteps2 > 0) {
+    load_b(0, bx0, hinv0);
+    load_b(1, bx1, hinv1);
+    load_snd(0);
+    load_x(xv);
+    load_snd(1);
+    load_t(0);
+  }
+#pragma unroll 1
+  for (int j = 0; j < nsteps2; j += 2) {
+    step(j, bx0, hinv0);
+    step(j + 1, bx1, hinv1);
+  }
+  if (n < a.N) {
+    float* Mn = M + (int64_t)n * DMID + c0 + u;
+#pragma unroll
+    for (int s = 0; s < T::NSLOT; ++s)
+      if (T::l1(s) == L1)
+#pragma unroll
+        for (int m = 0; m < 2 * T::l3(s) + 1; ++m) Mn[NC * (T::acc(s) + m)] = acc[T::acc(s) + m];
+  }
+}
+
+template <int LIN>
+__global__ void __launch_bounds__(64 * XW, LIN == 1 ? 4 : 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_PTRS) {
+  static_assert(LIN <= 2, "three input blocks are not fused");
+  __shared__ __align__(16) float sw[2 * 16 * (64 * gmax<LIN>() + 4)];
+  __shared__ __align__(16) float stab[XW * 2 * (LIN == 1 ? 16 : TP3_M1_NE)];
+  if constexpr (LIN == 1) {
+    tpx_fwd<1, 0>(a, MACE_TPX_FWD_ARGS, sw, stab);
+  } else {
+    if (blockIdx.z == 0)
+      tpx_fwd<2, 1>(a, MACE_TPX_FWD_ARGS, sw, stab);
+    else
+      tpx_fwd<2, 0>(a, MACE_TPX_FWD_ARGS, sw, stab);
+  }
+}
+
 // groups per node for each number of input blocks
 constexpr int ng_for(int lin) { return lin == 1 ? 2 : 2; }
 
@@ -591,6 +874,22 @@ void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const
     case 3: gx ? MACE_RECV(3, true) : MACE_RECV(3, false); break;
   }
 #undef MACE_RECV
+}
+
+void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
+                    const float* Mt, int mts, const void* h3x, const float* h3inv, const void* W3Tx, int W,
+                    float wscale, const float* up, float* M, float* w, float* sink) {
+  if (N <= 0) return;
+  const TpxDims a{N, W, mts, E, wscale};
+  const dim3 grid((unsigned)((N + XW - 1) / XW), 2, lin == 1 ? 1 : 2);
+  const _Float16* hx = static_cast<const _Float16*>(h3x);
+  const _Float16* wt = static_cast<const _Float16*>(W3Tx);
+  if (lin == 1)
+    hipLaunchKernelGGL(k_tpx_fwd<1>, grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w,
+                       sink);
+  else
+    hipLaunchKernelGGL(k_tpx_fwd<2>, grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w,
+                       sink);
 }
 
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe, float* gup) {

@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "mace_get_timings", "mace_step_device", "mace_sync", "mace_set_profiling", "mace_get_kernel_times",
     "mace_set_graphs",
     "mace_set_split_products",
+    "mace_set_fused_tp",
 )
 
 
@@ -88,6 +89,7 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
         "mace_set_profiling": (ctypes.c_int, [P, I32]),
         "mace_set_graphs": (ctypes.c_int, [P, I32]),
         "mace_set_split_products": (ctypes.c_int, [P, I32]),
+        "mace_set_fused_tp": (ctypes.c_int, [P, I32]),
         "mace_get_kernel_times": (ctypes.c_int, [P, ctypes.c_char_p, I64, P, P, I32, ctypes.POINTER(I32)]),
     }
     for name, (res, args) in sig.items():
@@ -218,6 +220,11 @@ class Engine:
         """Float32 policy: matrix products (radial-MLP output layer, node linears) on fp16 matrix
         cores with split operands (default) or on fp32 matrix cores."""
         self._check(self._lib.mace_set_split_products(self._h, int(bool(enable))))
+
+    def set_fused_tp(self, enable: bool) -> None:
+        """With split products: radial-MLP output layer built inside the tensor-product kernels
+        (default) or in a separate pass."""
+        self._check(self._lib.mace_set_fused_tp(self._h, int(bool(enable))))
 
     def kernel_times(self) -> dict:
         """{site: (total_ms, launches)} accumulated since the last call."""

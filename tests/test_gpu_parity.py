@@ -394,3 +394,30 @@ def test_split_products_match_fp32(arch, request):
     print(f"{arch}: fp32 products dE={errs[False][0]:.3g} dF={errs[False][1]:.3g}; "
           f"split dE={errs[True][0]:.3g} dF={errs[True][1]:.3g}")
     assert errs[True][1] <= max(8 * errs[False][1], 5e-6), errs
+
+
+@pytest.mark.parametrize("arch", ["small", "medium_zbl"])
+def test_fused_tp_matches_separate_passes(arch, request):
+    """Float32 policy with split products: building the radial MLP's per-edge TP weights inside
+    the TP kernels (default) and in a separate pass give the same energy, forces and virial to
+    float32 rounding (the same split products in the same order; only where the work runs
+    differs), and the fused path meets the tolerances against the float64 oracle."""
+    case = request.getfixturevalue(arch)
+    s = rattle(diamond_si((2, 2, 2)), 0.05, 11)
+    got = {}
+    try:
+        for fused in (False, True):
+            case.eng.set_fused_tp(fused)
+            got[fused] = case.run(s, stress=True)
+    finally:
+        case.eng.set_fused_tp(True)
+    ref = case.reference(s, got[True]["sp"], case.edges(), stress=True)
+    assert_parity(got[True], ref, len(s), stress=True, vol=abs(np.linalg.det(s.cell)))
+    a, b = got[False], got[True]
+    dE = abs(a["E"] - b["E"])
+    dF = float(np.abs(a["F"] - b["F"]).max())
+    dv = float(np.abs(a["vir"] - b["vir"]).max())
+    print(f"{arch}: fused vs separate dE={dE:.3g} dF={dF:.3g} dvir={dv:.3g}")
+    assert dE <= 1e-6 * max(abs(a["E"]), float(len(s))), dE
+    assert dF <= 1e-5, dF
+    assert dv <= 1e-5 * max(1.0, float(np.abs(a["vir"]).max())), dv
