@@ -43,6 +43,11 @@ struct DBuf {
 };
 
 std::string g_fail_msg;
+
+// partials of dL/dY and dL/dh3 per edge: the receiver VJP writes one per
+// channel half; the fused TP VJP one per (input degree, 64-channel slice)
+constexpr int kGyMax = 4;
+inline int tpx_parts(int lin) { return lin == 1 ? 2 : 4; }
 [[noreturn]] void fail(int code, const char* fmt, ...) {
   char buf[1024];
   va_list ap;
@@ -135,6 +140,7 @@ struct mace_ctx {
   // per-step edge buffers
   DBuf<EdgeGeom> geom;
   DBuf<float> Y, Mt, ef, zbl_e, gY, gef, gv, gw, gxe, h3;
+  DBuf<float> gh3p;  // fused TP VJP: dL/dh3 partials [P][E][64]
   DBuf<_Float16> h3h, gwh;  // radial-MLP hidden output, dL/dw under the float16 feature policy
   DBuf<float> gscale;       // per-(edge, channel half) scale of gwh
   DBuf<float> h3inv;        // per-edge inverse scale of h3 as split fp16 pairs
@@ -536,7 +542,8 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   c->Y.ensure(e * 16);
   c->ef.ensure(e * c->dims.num_bessel);
   c->zbl_e.ensure(e);
-  c->gY.ensure(e * 32);
+  c->gY.ensure(e * 16 * kGyMax);
+  c->gh3p.ensure(e * RADIAL_H * kGyMax);
   if (c->mts > 0) c->Mt.ensure(e * c->mts);
   c->gef.ensure(e * c->dims.num_bessel);
   c->h3.ensure(e * RADIAL_H);
@@ -1070,6 +1077,10 @@ void backward(mace_ctx* c, bool stress, double* out) {
   const int L = (int)c->layers.size();
   const int half = c->dims.feature_half != 0;
   const bool split = !half && c->split_products;
+  const bool fused = split && c->fused_tp && c->max_lin <= 2;
+  int gyp = 2;  // dL/dY partials per edge
+  if (fused)
+    for (const Layer& Ly : c->layers) gyp = std::max(gyp, tpx_parts(Ly.lin));
   // dE/dh_L from the nonlinear readout: written by the forward's energy_readout pass
   float* gh = c->gh0.p;
   float* gh_next = c->gh1.p;
@@ -1116,7 +1127,18 @@ void backward(mace_ctx* c, bool stress, double* out) {
       run_gemm(c, st, g);
     }
     const int first_edge_grad = (l == L - 1) ? 0 : 1;  // gY / gef: write on the first layer visited
-    {
+    if (fused) {
+      // dL/dw stays on chip: the radial-MLP output layer's VJP (dL/dh3 partials) is fused in
+      Site s(c, lname("tp_bwd", l));
+      int acc_gy = first_edge_grad;
+      if (!acc_gy && tpx_parts(Ly.lin) < gyp) {  // partials this layer does not write start at zero
+        launch_fill_zero(st, c->gY.p, E * 16 * gyp);
+        acc_gy = 1;
+      }
+      launch_tpx_bwd(st, Ly.lin, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p, Ly.mlp3x.p, Ly.wn,
+                     Ly.w3inv, Ly.h_up.p, c->gM.p, c->pos_s.p, l > 0 ? c->gxe.p : nullptr, c->gY.p, gyp, acc_gy,
+                     c->gh3p.p, c->sink.p);
+    } else {
       // layers after the first also need dL/dx: per-edge rows in sender order, then a segmented sum
       Site s(c, lname("tp_bwd", l));
       launch_tp_bwd_recv(st, Ly.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.wptr(half),
@@ -1127,7 +1149,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
       Site s(c, lname("tp_gather", l));
       launch_tp_gather_gx(st, Ly.lin, N, c->rowptr_s.p, c->gxe.p, c->gup.p);
     }
-    {
+    if (!fused) {
       Site s(c, lname("mlp_gh3", l));
       if (half)
         launch_mlp_gh3_h(st, E, Ly.wn, c->gwh.p, c->gscale.p, Ly.mlp3h.p, c->h3.p);
@@ -1139,8 +1161,8 @@ void backward(mace_ctx* c, bool stress, double* out) {
     {
       Site s(c, lname("mlp_hidden_bwd", l));
       if (split)
-        launch_mlp_hidden_bwd_x(st, E, nb, Ly.mlp_tiles_x.p, Ly.mlp_winv, Ly.ds.p, c->h3.p, c->gef.p,
-                                first_edge_grad);
+        launch_mlp_hidden_bwd_x(st, E, nb, Ly.mlp_tiles_x.p, Ly.mlp_winv, Ly.ds.p, fused ? c->gh3p.p : c->h3.p,
+                                fused ? tpx_parts(Ly.lin) : 1, c->gef.p, first_edge_grad);
       else
         launch_mlp_hidden_bwd(st, E, nb, Ly.mlp_tiles.p, Ly.ds.p, c->h3.p, c->gef.p, first_edge_grad);
     }
@@ -1183,7 +1205,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
     Site s(c, "edge_bwd");
     launch_edge_bwd(st, E, c->sender.p, c->receiver.p, c->species.p, c->bessel_w.p, c->zbl_z.p, c->zbl_cov.p,
                     c->ag_cov.p, fp,
-                    c->geom.p, c->gY.p, c->gef.p, c->gv.p, stress ? c->vir_part.p : nullptr);
+                    c->geom.p, c->gY.p, gyp, c->gef.p, c->gv.p, stress ? c->vir_part.p : nullptr);
   }
   {
     Site s(c, "forces");
@@ -1233,7 +1255,7 @@ static void free_all(mace_ctx* c) {
   c->gwh.release();
   c->gscale.release();
   for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->ag_cov, &c->gA2, &c->grho, &c->embed, &c->up0_tab, &c->sink, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
-                  &c->gv, &c->gw, &c->gxe, &c->h3, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup,
+                  &c->gv, &c->gw, &c->gxe, &c->h3, &c->gh3p, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup,
                   &c->node_e})
     b->release();
   for (auto* b : {&c->species, &c->sender, &c->receiver, &c->shifts, &c->rowptr, &c->rowptr_s, &c->perm_s, &c->pos_s,

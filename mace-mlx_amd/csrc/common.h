@@ -68,7 +68,7 @@ void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* se
                      float* zbl_e);
 void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov, const float* ag_cov,
-                     const FrontParams& p, const EdgeGeom* geom, const float* gY, const float* gef, float* gv,
+                     const FrontParams& p, const EdgeGeom* geom, const float* gY, int gyp, const float* gef, float* gv,
                      double* vir_part);
 // symmetrised virial from the per-block partials of launch_edge_bwd
 void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir);
@@ -99,8 +99,9 @@ void launch_mlp_permute_x(hipStream_t st, int nb, const float* W0, const float* 
                           const float* scale3, void* tiles);
 void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, const void* tiles,
                          const float* winv3, void* h3x, float* h3inv, float* ds);
+// gh3: np partials of dL/dh3 ([np][E][64]), added in order
 void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tiles, const float* winv3,
-                             const float* ds, const float* gh3, float* gef, int accumulate);
+                             const float* ds, const float* gh3, int np, float* gef, int accumulate);
 // half: h3, W3T and w fp16 arrays (fp32 accumulation); else fp32
 void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w,
                     int half);
@@ -146,6 +147,18 @@ void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const
 void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const void* h3x, const float* h3inv, const void* W3Tx, int W,
                     float wscale, const float* up, float* M, float* w, float* sink);
+// TP VJP with the radial-MLP output layer's backward product fused in (float32
+// policy, split products, lin <= 2): reads w ([E][W], written by
+// launch_tpx_fwd), writes the dL/dh3 partials gh3p ([P][E][64], P = 2 x input
+// degrees of the layer), dL/dY partials into gY[e][p][16] (gyp partials per
+// edge; written, or added when accumulate_gY) and, with gxe, the per-edge dL/dx
+// rows as launch_tp_bwd_recv does.  sink: scratch floats (>= W) for padding.
+void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
+                    const float* Mt, int mts, const float* w, const void* W3x, int W, float wscale, const float* up,
+                    const float* gM, const int* pos_s, float* gxe, float* gY, int gyp, int accumulate_gY,
+                    float* gh3p, float* sink);
+// p[0 .. n) = 0 (a kernel, not a memset: safe inside captured graphs)
+void launch_fill_zero(hipStream_t st, float* p, int64_t n);
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe,
                          float* gup);
 

@@ -118,8 +118,8 @@ __global__ void __launch_bounds__(256) k_edge_bwd(
     int64_t E, const int* __restrict__ sender, const int* __restrict__ receiver,
     const int* __restrict__ species, const float* __restrict__ bessel_w,
     const float* __restrict__ zbl_z, const float* __restrict__ zbl_cov, const float* __restrict__ ag_cov,
-    FrontParams p, const EdgeGeom* __restrict__ geom, const float* __restrict__ gY, const float* __restrict__ gef,
-    float* __restrict__ gv, double* __restrict__ vir_part) {
+    FrontParams p, const EdgeGeom* __restrict__ geom, const float* __restrict__ gY, int gyp,
+    const float* __restrict__ gef, float* __restrict__ gv, double* __restrict__ vir_part) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   double vir[9];
 #pragma unroll
@@ -133,7 +133,10 @@ __global__ void __launch_bounds__(256) k_edge_bwd(
     sh16(ux, uy, uz, Yl);
     float G[16];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) G[k] = gY[32 * e + k] + gY[32 * e + 16 + k];  // two channel halves
+    for (int k = 0; k < 16; ++k) G[k] = gY[16 * gyp * e + k];
+    for (int q = 1; q < gyp; ++q)  // the TP VJP's partials (channel slices / slot groups), in order
+#pragma unroll
+      for (int k = 0; k < 16; ++k) G[k] += gY[16 * (gyp * e + q) + k];
     // reverse through the recursion (l = 3, then l = 2)
 #pragma unroll
     for (int t = 0; t < SH3_NT; ++t) {
@@ -415,11 +418,11 @@ void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* se
 
 void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov, const float* ag_cov,
-                     const FrontParams& p, const EdgeGeom* geom, const float* gY, const float* gef, float* gv,
-                     double* vir_part) {
+                     const FrontParams& p, const EdgeGeom* geom, const float* gY, int gyp, const float* gef,
+                     float* gv, double* vir_part) {
   if (E <= 0) return;
   hipLaunchKernelGGL(k_edge_bwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, sender, receiver, species,
-                     bessel_w, zbl_z, zbl_cov, ag_cov, p, geom, gY, gef, gv, vir_part);
+                     bessel_w, zbl_z, zbl_cov, ag_cov, p, geom, gY, gyp, gef, gv, vir_part);
 }
 
 void launch_density_fwd(hipStream_t st, int N, const int* rowptr, const float* ef, int nb, const float* wd,

@@ -1054,10 +1054,11 @@ __global__ void __launch_bounds__(256) k_mlp_hidden_x(int64_t E, int nb, const f
   }
 }
 
+// gh3: np partials [np][E][64] (stride pstride floats), added in order
 __global__ void __launch_bounds__(256) k_mlp_hidden_bwd_x(int64_t E, int nb, const MlpBwdX* __restrict__ tiles,
                                                           MlpWinv wi, const float* __restrict__ ds,
-                                                          const float* __restrict__ gh3, float* __restrict__ gef,
-                                                          int accumulate) {
+                                                          const float* __restrict__ gh3, int np, int64_t pstride,
+                                                          float* __restrict__ gef, int accumulate) {
   __shared__ MlpBwdX sw;
   stage_copy(sw, tiles);
   __syncthreads();
@@ -1069,6 +1070,11 @@ __global__ void __launch_bounds__(256) k_mlp_hidden_bwd_x(int64_t E, int nb, con
     float v[16], dv[16];
     f4v acc[4];
     ld_row16(gh3 + ec * H, g, v);
+    for (int pp = 1; pp < np; ++pp) {
+      ld_row16(gh3 + pp * pstride + ec * H, g, dv);
+#pragma unroll
+      for (int q = 0; q < 16; ++q) v[q] += dv[q];
+    }
     ld_row16(d + 2 * H, g, dv);
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] *= dv[q];
@@ -1141,12 +1147,12 @@ void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, con
 }
 
 void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tiles, const float* winv3,
-                             const float* ds, const float* gh3, float* gef, int accumulate) {
+                             const float* ds, const float* gh3, int np, float* gef, int accumulate) {
   if (E <= 0) return;
   MlpWinv wi{{winv3[0], winv3[1], winv3[2]}};
   const MlpBwdX* bw = reinterpret_cast<const MlpBwdX*>(static_cast<const char*>(tiles) + sizeof(MlpFwdX));
-  hipLaunchKernelGGL(k_mlp_hidden_bwd_x, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, bw, wi, ds, gh3, gef,
-                     accumulate);
+  hipLaunchKernelGGL(k_mlp_hidden_bwd_x, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, bw, wi, ds, gh3, np,
+                     E * H, gef, accumulate);
 }
 
 void launch_mlp_permute(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2, void* tiles) {

@@ -330,13 +330,14 @@ __device__ __forceinline__ void store_gY(const float* gYu, int64_t e, int u, flo
 
 // Per-edge VJP of one channel: given g = dL/dM[recv] (this channel), writes
 // dL/dw, accumulates the input gradient (if GX) and this channel's dL/dY.
-template <int LIN, bool GX>
+template <int LIN, bool GX, int GRP = -1>
 __device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& in, float* gw_out,
                                             const float* __restrict__ Ye, const float* __restrict__ Me,
                                             const float* M2, float& gx0, float* gx1, float* gx2, float* gYu) {
   using T = TPT<LIN>;
 #pragma unroll
   for (int s = 0; s < T::NSLOT; ++s) {
+    if (GRP >= 0 && T::l1(s) != GRP) continue;  // only the slots of input block l1 = GRP
     const float ww = in.w[s];
     const int a0 = T::acc(s), d = 2 * T::l3(s) + 1, l2 = T::l2(s);
     float gws = 0.f;
@@ -809,6 +810,296 @@ __global__ void __launch_bounds__(64 * XW, LIN == 1 ? 4 : 2) k_tpx_fwd(TpxDims a
   }
 }
 
+// ---------------------------------------------------------------------------
+// TP VJP with the radial-MLP output layer's backward product fused in.
+//
+// Same decomposition as the fused forward (wave = receiver, 64-channel slice,
+// one input degree l1 per block).  A step runs the per-edge VJP of the wave's
+// two edges (dL/dw, dL/dx, dL/dY), stores dL/dw into the block's 16-edge LDS
+// tile, and after the barrier multiplies the tile by the block's W3 rows on
+// the fp16 matrix cores:
+//   gh3p[p][e][q] = wscale * sum_{slot in group, u in slice} dL/dw[e, slot, u] W3[q, slot NC + u]
+// with split operands (W3 as hi / lo planes scaled per matrix; dL/dw split
+// once, by the wave that made it, after scaling the edge's largest magnitude
+// over the block's columns into [2^14, 2^15): its hi / lo planes and inverse
+// scale go to LDS; lo.hi + hi.lo + hi.hi).  p = 2 blockIdx.z + blockIdx.y indexes
+// the (group, slice) partials; the hidden-layer VJP adds them in order.
+// Roles are swapped (D[q][edge]); wave k takes q tile k & 3 and half k >> 2 of
+// the group's k steps, holding those W3 fragments in registers; the two halves
+// of a q tile meet through LDS one step later (no second barrier).
+// dL/dY partials go to gY[e][p][16] and dL/dx rows to gxe[pos_s[e]] (this
+// group's components, this slice's channels).  As in the forward, every
+// vector-memory operation is unconditional (padding goes to the sink).
+// ---------------------------------------------------------------------------
+// Largest value of a nonnegative x over the wave (DPP row scan, then the two
+// row broadcasts; lane 63 ends with the total), as a wave-uniform value.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float wave_max_nonneg(float x) {
+  float m = x;
+  m = fmaxf(m, dpp_f<0x111>(m));  // row_shr:1
+  m = fmaxf(m, dpp_f<0x112>(m));  // row_shr:2
+  m = fmaxf(m, dpp_f<0x114>(m));  // row_shr:4
+  m = fmaxf(m, dpp_f<0x118>(m));  // row_shr:8
+  m = fmaxf(m, dpp_f<0x142>(m));  // row_bcast:15
+  m = fmaxf(m, dpp_f<0x143>(m));  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 63));
+}
+
+struct TpxBwdDims {
+  int N, W, mts;
+  int64_t E;
+  float wscale;
+  int accumulate_gY;
+  int gyp;  // partials per edge in gY
+};
+
+#define MACE_TPX_BWD_PTRS                                                                                   \
+  const int *__restrict__ rowptr, const int *__restrict__ sender, const float *__restrict__ Y,              \
+      const float *__restrict__ Mt, const float *__restrict__ w, const _Float16 *__restrict__ W3x,           \
+      const float *__restrict__ up, const float *__restrict__ gM, const int *__restrict__ pos_s,            \
+      float *__restrict__ gxe, float *__restrict__ gY, float *__restrict__ gh3p, float *__restrict__ sink
+#define MACE_TPX_BWD_ARGS rowptr, sender, Y, Mt, w, W3x, up, gM, pos_s, gxe, gY, gh3p, sink
+// W3x: [64][W] hi plane, then lo plane; gh3p: [P][E][64]
+
+template <int LIN, int L1, bool GX>
+__device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, _Float16* sg, float* sinv,
+                                        float* stab, float* sp) {
+  using T = TPT<LIN>;
+  using GR = GrpT<LIN, L1>;
+  constexpr int G = GR::G, RS = 64 * G + 8;  // fp16 row stride: 16-byte reads of 8 lanes hit distinct banks
+  constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, NX = 2 * L1 + 1;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4, u = l;
+  const int c0 = 64 * blockIdx.y, nb0 = XW * blockIdx.x, p = 2 * blockIdx.z + blockIdx.y;
+  const int n = nb0 + wv;
+  const int beg = rowptr[min(n, a.N)], end = n < a.N ? rowptr[n + 1] : beg;
+  const int nr = nb0 + (r >> 1);  // receiver of tile column r
+  const int cb = rowptr[min(nr, a.N)], ce = nr < a.N ? rowptr[nr + 1] : cb;
+  int ns = (ce - cb + 1) >> 1;
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) ns = max(ns, __shfl_xor(ns, off));
+  const int nsteps = __builtin_amdgcn_readfirstlane(ns);
+  const int64_t elast = a.E - 1;
+
+  // W3 rows q = 16 qt + r, group k steps kh G .. kh G + G - 1 (32 columns each)
+  const int qt = wv & 3, kh = wv >> 2;
+  h8 wa[G][2];
+#pragma unroll
+  for (int ks = 0; ks < G; ++ks) {
+    const int kk = kh * G + ks;
+    const int64_t o = (int64_t)(16 * qt + r) * a.W + GR::slot(kk >> 1) * NC + c0 + 32 * (kk & 1) + 8 * g;
+    wa[ks][0] = *reinterpret_cast<const h8*>(W3x + o);
+    wa[ks][1] = *reinterpret_cast<const h8*>(W3x + (int64_t)XH * a.W + o);
+  }
+  // dL/dM of this wave's receiver (group slots, slice channels)
+  float gm[T::NACC];
+  {
+    const float* gMn = gM + (int64_t)min(n, a.N - 1) * DMID + c0 + u;
+#pragma unroll
+    for (int s = 0; s < T::NSLOT; ++s)
+      if (T::l1(s) == L1)
+#pragma unroll
+        for (int m = 0; m < 2 * T::l3(s) + 1; ++m) gm[T::acc(s) + m] = gMn[NC * (T::acc(s) + m)];
+  }
+  // next step's inputs: weights and sender rows of the two edges (indices and
+  // pos_s a step earlier still), table rows staged through LDS as in the forward
+  float wn[2][T::NSLOT], xv[2][NX], xn[2][NX], wc[2][T::NSLOT];
+  int snd[2], psn[2], pnx[2], pss[2];  // indices of step j + 2 / pos_s of step j + 1 / of this step
+  float gyn[2], gyc[2];                 // dL/dY partials already held (accumulate_gY), a step ahead
+  // gY[e][p][16] entry of lane l (lanes 4k hold component k after the wave sum); padding -> sink
+  auto gy_addr = [&](int e, bool valid) {
+    return valid && (l & 3) == 0 ? gY + ((int64_t)e * a.gyp + p) * 16 + (l >> 2) : sink + l;
+  };
+  auto load_idx = [&](int j) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int64_t e = min<int64_t>(beg + 2 * j + b, elast);
+      snd[b] = sender[e];
+      if (GX) psn[b] = pos_s[e];
+    }
+  };
+  auto load_in = [&](int j) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int64_t e = min<int64_t>(beg + 2 * j + b, elast);
+      const float* we = w + e * a.W + c0 + u;
+#pragma unroll
+      for (int s = 0; s < T::NSLOT; ++s)
+        if (T::l1(s) == L1) wn[b][s] = __builtin_nontemporal_load(we + s * NC);
+      const float* xs = up + (int64_t)snd[b] * DIN + NC * L1 * L1 + c0 + u;
+#pragma unroll
+      for (int i = 0; i < NX; ++i) xn[b][i] = xs[NC * i];
+      if (GX) pnx[b] = psn[b];
+      const int ej = beg + 2 * j + b;
+      gyn[b] = *gy_addr(ej, ej < end);
+    }
+  };
+  constexpr int TY = L1 == 0 ? 16 : 0, TS = TY + (L1 == 1 ? TP3_M1_NE : 0), TSP = (TS + 3) & ~3;
+  constexpr int TH = (TS + 63) / 64;
+  static_assert(TS <= 128 && L1 <= 1, "table rows of up to 128 entries");
+  float* tb = stab + wv * 2 * TSP;  // [edge b][TSP]
+  float tr[2][TH];
+  auto load_t = [&](int j) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int64_t e = min<int64_t>(beg + 2 * j + b, elast);
+#pragma unroll
+      for (int h = 0; h < TH; ++h) {
+        const int i = min(l + 64 * h, TS - 1);
+        tr[b][h] = i < TY ? Y[e * 16 + i] : Mt[e * a.mts + i - TY];
+      }
+    }
+  };
+  auto store_t = [&]() {
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int h = 0; h < TH; ++h)
+        if (l + 64 * h < TS) tb[b * TSP + l + 64 * h] = tr[b][h];
+  };
+  f4v prev = f4v{0.f, 0.f, 0.f, 0.f};  // this wave's share of the previous tile's dL/dh3
+  // dL/dh3 of the tile before step j: add the partner half (k steps of the other
+  // half, written to LDS last step) and store; the upper half only feeds LDS
+  auto flush = [&](int j) {
+    const f4v o = *reinterpret_cast<const f4v*>(sp + (((j - 1) & 1) * 4 + qt) * 256 + 4 * l);
+    const int e = cb + 2 * (j - 1) + (r & 1);
+    const bool valid = kh == 0 && j > 0 && e < ce;
+    float* dst = valid ? gh3p + ((int64_t)p * a.E + e) * XH + 16 * qt + 4 * g : sink + 4 * l;
+    *reinterpret_cast<float4*>(dst) = float4{(prev[0] + o[0]) * a.wscale, (prev[1] + o[1]) * a.wscale,
+                                             (prev[2] + o[2]) * a.wscale, (prev[3] + o[3]) * a.wscale};
+  };
+  auto step = [&](int j) {
+    _Float16* tile = sg + (j & 1) * 2 * 16 * RS;  // [hi, lo][edge column][RS]
+    float* tinv = sinv + (j & 1) * 16;
+    store_t();
+    wave_sync();
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      xv[b][0] = xn[b][0];
+#pragma unroll
+      for (int i = 1; i < NX; ++i) xv[b][i] = xn[b][i];
+#pragma unroll
+      for (int s = 0; s < T::NSLOT; ++s)
+        if (T::l1(s) == L1) wc[b][s] = wn[b][s];
+      if (GX) pss[b] = pnx[b];
+      gyc[b] = gyn[b];
+    }
+    load_in(j + 1);
+    load_idx(j + 2);
+    load_t(j + 1);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int e = beg + 2 * j + b;
+      const bool valid = e < end;
+      float gYu[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) gYu[q] = 0.f;
+      float gx0 = 0.f, gx1[3] = {0.f, 0.f, 0.f}, gx2[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+      float gws[T::NSLOT];
+#pragma unroll
+      for (int s = 0; s < T::NSLOT; ++s) gws[s] = 0.f;
+      if (valid) {
+        EdgeIn<LIN> in;
+        in.x0 = 0.f;
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+          if constexpr (L1 == 0) in.x0 = xv[b][i];
+          if constexpr (L1 == 1) in.x1[i] = xv[b][i];
+          if constexpr (L1 == 2) in.x2[i] = xv[b][i];
+        }
+#pragma unroll
+        for (int s = 0; s < T::NSLOT; ++s)
+          if (T::l1(s) == L1) in.w[s] = wc[b][s];
+        const float* trow_t = tb + b * TSP;
+        tp_edge_vjp<LIN, GX, L1>(gm, in, gws, trow_t, trow_t, trow_t, gx0, gx1, gx2, gYu);
+      }
+      {  // split dL/dw for the matrix cores: one scale per edge (over the block's columns)
+        float m = 0.f;
+#pragma unroll
+        for (int s = 0; s < T::NSLOT; ++s)
+          if (T::l1(s) == L1) m = fmaxf(m, fabsf(gws[s]));
+        m = wave_max_nonneg(m);
+        // floor(log2 m) from the exponent field; zero / subnormal edges take -100 (finite scales)
+        const int ex = max((int)((__float_as_uint(m) >> 23) & 0xff) - 127, -100);
+        const float sc = __uint_as_float((unsigned)(127 + 14 - ex) << 23);
+        _Float16* trow = tile + (2 * wv + b) * RS + u;
+#pragma unroll
+        for (int s = 0; s < T::NSLOT; ++s)
+          if (T::l1(s) == L1) {
+            const float x = gws[s] * sc;
+            const _Float16 hi = (_Float16)x;
+            trow[64 * GR::local(s)] = hi;
+            trow[16 * RS + 64 * GR::local(s)] = (_Float16)(x - (float)hi);
+          }
+        if (l == 0) tinv[2 * wv + b] = __uint_as_float((unsigned)(127 - 14 + ex) << 23);
+      }
+      if constexpr (GX) {
+        float* dst = (valid ? gxe + (int64_t)pss[b] * DIN + NC * L1 * L1 : sink) + c0 + u;
+#pragma unroll
+        for (int i = 0; i < NX; ++i) dst[NC * i] = L1 == 0 ? gx0 : L1 == 1 ? gx1[i] : gx2[i];
+      }
+      const float sy = wave_sum16(gYu);
+      *gy_addr(e, valid) = a.accumulate_gY ? gyc[b] + sy : sy;
+    }
+    __syncthreads();
+    // dL/dh3 of this tile (half kh of the k steps), then the previous tile's flush
+    f4v acc = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < G; ++ks) {
+      const _Float16* src = tile + r * RS + 32 * (kh * G + ks) + 8 * g;
+      const h8 xh = *reinterpret_cast<const h8*>(src), xl = *reinterpret_cast<const h8*>(src + 16 * RS);
+      acc = mfma16h(wa[ks][1], xh, acc);
+      acc = mfma16h(wa[ks][0], xl, acc);
+      acc = mfma16h(wa[ks][0], xh, acc);
+    }
+    {
+      const float inv = tinv[r];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] *= inv;
+    }
+    flush(j);
+    // the upper half's share, read by the lower half next step (the lower half
+    // writes a slot nobody reads: no branch)
+    *reinterpret_cast<f4v*>(sp + ((kh ? (j & 1) : 2) * 4 + qt) * 256 + 4 * l) = acc;
+    prev = acc;
+  };
+  const int nsteps2 = (nsteps + 1) & ~1;
+  if (nsteps2 > 0) {  // some receiver of the block has edges, so E >= 1 and the clamped indices are valid
+    load_idx(0);
+    load_in(0);
+    load_idx(1);
+    load_t(0);
+  }
+#pragma unroll 1
+  for (int j = 0; j < nsteps2; ++j) step(j);
+  __syncthreads();
+  flush(nsteps2);
+}
+
+template <int LIN, bool GX>
+__global__ void __launch_bounds__(64 * XW, 2) k_tpx_bwd(TpxBwdDims a, MACE_TPX_BWD_PTRS) {
+  static_assert(LIN <= 2, "three input blocks are not fused");
+  __shared__ __align__(16) _Float16 sg[2 * 2 * 16 * (64 * gmax<LIN>() + 8)];  // [step][hi, lo][edge][RS]
+  __shared__ float sinv[2 * 16];
+  __shared__ __align__(16) float stab[XW * 2 * (LIN == 1 ? 16 : TP3_M1_NE)];
+  __shared__ __align__(16) float sp[3 * 4 * 256];  // [two steps + the lower half's slot][q tile][lane][4]
+  if constexpr (LIN == 1) {
+    tpx_bwd<1, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, stab, sp);
+  } else {
+    if (blockIdx.z == 0)
+      tpx_bwd<2, 1, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, stab, sp);
+    else
+      tpx_bwd<2, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, stab, sp);
+  }
+}
+
+__global__ void __launch_bounds__(256) k_fill_zero(float* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0.f;
+}
+
 // groups per node for each number of input blocks
 constexpr int ng_for(int lin) { return lin == 1 ? 2 : 2; }
 
@@ -890,6 +1181,31 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
   else
     hipLaunchKernelGGL(k_tpx_fwd<2>, grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w,
                        sink);
+}
+
+void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
+                    const float* Mt, int mts, const float* w, const void* W3x, int W, float wscale, const float* up,
+                    const float* gM, const int* pos_s, float* gxe, float* gY, int gyp, int accumulate_gY,
+                    float* gh3p, float* sink) {
+  if (N <= 0 || E <= 0) return;  // no edges: no dL/dw, dL/dY, dL/dx rows to write
+  const TpxBwdDims a{N, W, mts, E, wscale, accumulate_gY, gyp};
+  const dim3 grid((unsigned)((N + XW - 1) / XW), 2, lin == 1 ? 1 : 2);
+  const _Float16* wx = static_cast<const _Float16*>(W3x);
+#define MACE_TPXB(L, GXV)                                                                                        \
+  hipLaunchKernelGGL((k_tpx_bwd<L, GXV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \
+                     pos_s, gxe, gY, gh3p, sink)
+  const bool gx = gxe != nullptr;
+  if (lin == 1) {
+    if (gx) MACE_TPXB(1, true); else MACE_TPXB(1, false);
+  } else {
+    if (gx) MACE_TPXB(2, true); else MACE_TPXB(2, false);
+  }
+#undef MACE_TPXB
+}
+
+void launch_fill_zero(hipStream_t st, float* p, int64_t n) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 1024)), dim3(256), 0, st, p, n);
 }
 
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe, float* gup) {
