@@ -255,41 +255,45 @@ __global__ void __launch_bounds__(NC* NG) k_tp_fwd(int N, const int* __restrict_
   }
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+
 // Sum over the 64 lanes of a wave of v[16]: lane l returns the total of
-// component (l >> 2) & 15.  Recursive halving: each exchange step halves the
-// components a lane keeps, then two plain butterflies finish the sum.
+// component (l >> 2) & 15.  Recursive halving, all in VALU: each exchange step
+// halves the components a lane keeps (the 32- and 16-lane exchanges with the
+// permlane swaps of gfx950, the 8- and 4-lane ones with DPP), then two
+// butterflies inside each quad finish the sum.
 __device__ __forceinline__ float wave_sum16(const float* v) {
   const int lane = __lane_id();
   float a[8], b[4], c[2];
-  {
-    const bool hi = lane & 32;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float send = hi ? v[k] : v[k + 8], keep = hi ? v[k + 8] : v[k];
-      a[k] = keep + __shfl_xor(send, 32);
-    }
+  for (int k = 0; k < 8; ++k) {  // lanes 0-31 keep component k, lanes 32-63 component k + 8
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 8]), false, false);
+    a[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {  // rows 0 and 2 keep a[k], rows 1 and 3 a[k + 4]
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[k]), __float_as_uint(a[k + 4]), false, false);
+    b[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
   {
-    const bool hi = lane & 16;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float send = hi ? a[k] : a[k + 4], keep = hi ? a[k + 4] : a[k];
-      b[k] = keep + __shfl_xor(send, 16);
-    }
-  }
-  {
-    const bool hi = lane & 8;
+    const bool hi = lane & 8;  // partner lane ^ 8: rotation of the 16-lane row by 8
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const float send = hi ? b[k] : b[k + 2], keep = hi ? b[k + 2] : b[k];
-      c[k] = keep + __shfl_xor(send, 8);
+      c[k] = keep + dpp_f<0x128>(send);  // row_ror:8
     }
   }
-  const bool hi = lane & 4;
+  const bool hi = lane & 4;  // partner lane ^ 4: lane - 4 for the upper four of each eight, lane + 4 below
   const float send = hi ? c[0] : c[1], keep = hi ? c[1] : c[0];
-  float d = keep + __shfl_xor(send, 4);
-  d += __shfl_xor(d, 2);
-  d += __shfl_xor(d, 1);
+  // both shifts run on the whole wave (a DPP read from a lane outside a divergent
+  // branch would see 0), then each lane picks its partner's
+  const float from_below = dpp_f<0x114>(send), from_above = dpp_f<0x104>(send);  // row_shr:4 / row_shl:4
+  float d = keep + (hi ? from_below : from_above);
+  d += dpp_f<0x4e>(d);  // quad_perm [2, 3, 0, 1]: lane ^ 2
+  d += dpp_f<0xb1>(d);  // quad_perm [1, 0, 3, 2]: lane ^ 1
   return d;
 }
 
@@ -833,10 +837,6 @@ __global__ void __launch_bounds__(64 * XW, LIN == 1 ? 4 : 2) k_tpx_fwd(TpxDims a
 // ---------------------------------------------------------------------------
 // Largest value of a nonnegative x over the wave (DPP row scan, then the two
 // row broadcasts; lane 63 ends with the total), as a wave-uniform value.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
-}
 __device__ __forceinline__ float wave_max_nonneg(float x) {
   float m = x;
   m = fmaxf(m, dpp_f<0x111>(m));  // row_shr:1
