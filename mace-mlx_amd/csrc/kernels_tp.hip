@@ -616,7 +616,8 @@ struct TpxDims {
 // w: [E][W] for the VJP; sink: W floats, target of the stores of padding edges
 
 template <int LIN, int L1>
-__device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, float* sw, float* stab) {
+__device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, float* sw, float* stab, _Float16* hbuf,
+                                        float* hiv) {
   using T = TPT<LIN>;
   using GR = GrpT<LIN, L1>;
   constexpr int G = GR::G, CT = 4 * G, NCTW = (CT + XW - 1) / XW, RS = 64 * G + 4;
@@ -650,70 +651,78 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
     }
   }
   // Every vector-memory operation below is unconditional (indices clamped,
-  // stores of past-the-end edges sent to sink), so the number in flight is
-  // the same on every path and the compiler's wait counts stay exact: a step
-  // waits only for what it consumes, never for the prefetches behind it.
+  // stores of past-the-end edges sent to sink), so the number in flight is the
+  // same on every path and the compiler's wait counts stay exact: a step waits
+  // only for what it consumes, never for the prefetches behind it.
+  //
+  // Two ring slots (the step loop is unrolled by two, so a slot is a set of
+  // registers): slot j & 1 holds step j's inputs, and step j refills it for step
+  // j + 2 once its edges are done; sender indices (scalar loads) are fetched a
+  // step before the rows they address.
   const int64_t elast = a.E - 1;  // E >= 1 whenever a step runs
-  // h3 of tile column r, two steps ahead: [k step][hi, lo] per ring slot
-  h8 bx0[2][2], bx1[2][2];
-  float hinv0 = 0.f, hinv1 = 0.f;
-  auto load_b = [&](int j, h8 (&bx)[2][2], float& hinv) {
-    const int64_t row = min<int64_t>(cb + 2 * j + (r & 1), elast);  // columns past a receiver's end: not stored
-    const _Float16* p = h3x + row * 2 * XH + 8 * g;
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      bx[c][0] = *reinterpret_cast<const h8*>(p + 32 * c);
-      bx[c][1] = *reinterpret_cast<const h8*>(p + XH + 32 * c);
-    }
-    hinv = h3inv[row];
-  };
-  // sender rows of the next step's edges; their indices (scalar loads) are
-  // fetched a step earlier still
-  float xv[2][NX], xn[2][NX];
-  int snd[2];
-  auto load_snd = [&](int j) {
-#pragma unroll
-    for (int b = 0; b < 2; ++b) snd[b] = sender[min<int64_t>(beg + 2 * j + b, elast)];
-  };
-  auto load_x = [&](float (*dst)[NX]) {
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const float* xs = up + (int64_t)snd[b] * DIN + NC * L1 * L1 + c0 + u;
-#pragma unroll
-      for (int i = 0; i < NX; ++i) dst[b][i] = xs[NC * i];
-    }
-  };
-  // this wave's two edges' table rows (Y for l1 = 0 slots, M1 for l1 = 1
-  // slots): loaded a step ahead, stored to a wave-private LDS row at the start
-  // of their step and read back as broadcast loads
   constexpr int TY = L1 == 0 ? 16 : 0, TS = TY + (L1 == 1 ? TP3_M1_NE : 0), TSP = (TS + 3) & ~3;
   constexpr int TH = (TS + 63) / 64;
   static_assert(TS <= 128 && L1 <= 1, "table rows of up to 128 entries");
-  float* tb = stab + wv * 2 * TSP;  // [edge b][TSP]
-  float tr[2][TH];
-  auto load_t = [&](int j) {
+  float* tb = stab + wv * 2 * TSP;  // this wave's two table rows (Y for l1 = 0 slots, M1 for l1 = 1)
+  // The 16 h3 rows of a step's tile (hi and lo planes, 4 KB) are fetched once
+  // per block, 8 bytes per thread, and staged in LDS (double-buffered, written
+  // before the barrier of the step before their use); each wave then reads its
+  // B fragments from there.  Thread t fetches column hr = t / 32, plane hp,
+  // fp16 entries 4 hq .. 4 hq + 3.
+  static_assert(XW == 8, "the h3 tile is fetched by 512 threads");
+  const int hr = threadIdx.x >> 5, hpl = (threadIdx.x >> 4) & 1, hq = threadIdx.x & 15;
+  const int hn = nb0 + (hr >> 1);
+  const int hb0 = rowptr[min(hn, a.N)];
+  struct Slot {
+    uint2 h;        // this thread's 8 bytes of the step's h3 tile
+    float hinv;     // inverse scale of its row
+    float x[2][NX]; // sender rows of the wave's two edges
+    float t[2][TH]; // their table rows (this lane's entries)
+    int snd[2];     // sender indices
+  };
+  Slot s0, s1;
+  auto load_snd = [&](int j, Slot& S) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) S.snd[b] = sender[min<int64_t>(beg + 2 * j + b, elast)];
+  };
+  auto load_h = [&](int j, Slot& S) {
+    const int64_t row = min<int64_t>(hb0 + 2 * j + (hr & 1), elast);  // columns past a receiver's end: not stored
+    S.h = *reinterpret_cast<const uint2*>(h3x + row * 2 * XH + hpl * XH + 4 * hq);
+    S.hinv = h3inv[row];
+  };
+  auto store_h = [&](int j, const Slot& S) {  // S holds step j's tile share
+    *reinterpret_cast<uint2*>(hbuf + (((j & 1) * 2 + hpl) * 16 + hr) * 72 + 4 * hq) = S.h;
+    if (hpl == 0 && hq == 0) hiv[(j & 1) * 16 + hr] = S.hinv;
+  };
+  auto load_slot = [&](int j, Slot& S) {  // S.snd already holds step j's indices
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
+      const float* xs = up + (int64_t)S.snd[b] * DIN + NC * L1 * L1 + c0 + u;
+#pragma unroll
+      for (int i = 0; i < NX; ++i) S.x[b][i] = xs[NC * i];
       const int64_t e = min<int64_t>(beg + 2 * j + b, elast);
 #pragma unroll
       for (int h = 0; h < TH; ++h) {
         const int i = min(l + 64 * h, TS - 1);
-        tr[b][h] = i < TY ? Y[e * 16 + i] : Mt[e * a.mts + i - TY];
+        S.t[b][h] = i < TY ? Y[e * 16 + i] : Mt[e * a.mts + i - TY];
       }
     }
-  };
-  auto store_t = [&]() {
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int h = 0; h < TH; ++h)
-        if (l + 64 * h < TS) tb[b * TSP + l + 64 * h] = tr[b][h];
   };
   float acc[T::NACC];
 #pragma unroll
   for (int q = 0; q < T::NACC; ++q) acc[q] = 0.f;
-  auto step = [&](int j, h8 (&bx)[2][2], float& hinv) {
+  auto step = [&](int j, Slot& S, Slot& Snext) {
     float* tile = sw + (j & 1) * 16 * RS;
+    load_h(j + 2, S);  // S's share of step j was staged during step j - 1
+    h8 bx[2][2];       // B fragments of tile column r: [k step][hi, lo]
+    {
+      const _Float16* hrow = hbuf + ((j & 1) * 2 * 16 + r) * 72 + 8 * g;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        bx[c][0] = *reinterpret_cast<const h8*>(hrow + 32 * c);
+        bx[c][1] = *reinterpret_cast<const h8*>(hrow + 16 * 72 + 32 * c);
+      }
+    }
     f4v d[NCTW];
 #pragma unroll
     for (int m = 0; m < NCTW; ++m) d[m] = f4v{0.f, 0.f, 0.f, 0.f};
@@ -725,7 +734,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
         for (int m = 0; m < NCTW; ++m)
           if (CT % XW == 0 || wv + XW * m < CT)  // every wave's tiles exist when XW divides CT
             d[m] = mfma16h(wa[m][c][p == 2 ? 0 : p ^ 1], bx[c][p == 1 ? 1 : 0], d[m]);  // lo.hi, hi.lo, hi.hi
-    const float bsc = hinv * a.wscale;
+    const float bsc = hiv[(j & 1) * 16 + r] * a.wscale;
 #pragma unroll
     for (int m = 0; m < NCTW; ++m) {
       const int ct = wv + XW * m;
@@ -733,13 +742,15 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
         *reinterpret_cast<float4*>(tile + r * RS + 16 * ct + 4 * g) =
             float4{d[m][0] * bsc, d[m][1] * bsc, d[m][2] * bsc, d[m][3] * bsc};
     }
-    load_b(j + 2, bx, hinv);
+    store_h(j + 1, Snext);  // its last readers (step j - 1) are past the previous barrier
     __syncthreads();
-    store_t();
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int h = 0; h < TH; ++h)
+        if (l + 64 * h < TS) tb[b * TSP + l + 64 * h] = S.t[b][h];
     wave_sync();
-    load_x(xn);
-    load_snd(j + 2);
-    load_t(j + 1);
+    load_snd(j + 3, Snext);  // Snext's step j + 1 rows are already in flight
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int e = beg + 2 * j + b;
@@ -754,9 +765,9 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
         in.x0 = 0.f;
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
-          if constexpr (L1 == 0) in.x0 = xv[b][i];
-          if constexpr (L1 == 1) in.x1[i] = xv[b][i];
-          if constexpr (L1 == 2) in.x2[i] = xv[b][i];
+          if constexpr (L1 == 0) in.x0 = S.x[b][i];
+          if constexpr (L1 == 1) in.x1[i] = S.x[b][i];
+          if constexpr (L1 == 2) in.x2[i] = S.x[b][i];
         }
 #pragma unroll
         for (int s = 0; s < T::NSLOT; ++s)
@@ -770,24 +781,24 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
         if (T::l1(s) == L1) __builtin_nontemporal_store(wv_s[s], we + s * NC);
     }
     wave_sync();  // table row reads done before the next step's store
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int i = 0; i < NX; ++i) xv[b][i] = xn[b][i];
+    load_slot(j + 2, S);  // S.snd was refilled with step j + 2's indices during step j - 1
   };
   const int nsteps2 = (nsteps + 1) & ~1;  // even: both ring slots every trip
   if (nsteps2 > 0) {
-    load_b(0, bx0, hinv0);
-    load_b(1, bx1, hinv1);
-    load_snd(0);
-    load_x(xv);
-    load_snd(1);
-    load_t(0);
+    load_snd(0, s0);
+    load_snd(1, s1);
+    load_h(0, s0);
+    load_h(1, s1);
+    load_slot(0, s0);
+    load_slot(1, s1);
+    load_snd(2, s0);
+    store_h(0, s0);
+    __syncthreads();  // nsteps2 is uniform over the block
   }
 #pragma unroll 1
   for (int j = 0; j < nsteps2; j += 2) {
-    step(j, bx0, hinv0);
-    step(j + 1, bx1, hinv1);
+    step(j, s0, s1);
+    step(j + 1, s1, s0);
   }
   if (n < a.N) {
     float* Mn = M + (int64_t)n * DMID + c0 + u;
@@ -804,13 +815,15 @@ __global__ void __launch_bounds__(64 * XW, LIN == 1 ? 4 : 2) k_tpx_fwd(TpxDims a
   static_assert(LIN <= 2, "three input blocks are not fused");
   __shared__ __align__(16) float sw[2 * 16 * (64 * gmax<LIN>() + 4)];
   __shared__ __align__(16) float stab[XW * 2 * (LIN == 1 ? 16 : TP3_M1_NE)];
+  __shared__ __align__(16) _Float16 hbuf[2 * 2 * 16 * 72];  // [step][hi, lo][tile column][64 + pad]
+  __shared__ float hiv[2 * 16];
   if constexpr (LIN == 1) {
-    tpx_fwd<1, 0>(a, MACE_TPX_FWD_ARGS, sw, stab);
+    tpx_fwd<1, 0>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
   } else {
     if (blockIdx.z == 0)
-      tpx_fwd<2, 1>(a, MACE_TPX_FWD_ARGS, sw, stab);
+      tpx_fwd<2, 1>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
     else
-      tpx_fwd<2, 0>(a, MACE_TPX_FWD_ARGS, sw, stab);
+      tpx_fwd<2, 0>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
   }
 }
 
