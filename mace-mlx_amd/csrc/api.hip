@@ -966,7 +966,8 @@ void forward(mace_ctx* c, const double* pos, double* out) {
       Site s(c, lname("mlp_hidden", l));
       // split: h3 holds E x 2 x 64 fp16 (the same bytes as E x 64 floats)
       if (split)
-        launch_mlp_hidden_x(st, E, nb, c->ef.p, L.mlp_tiles_x.p, L.mlp_winv, c->h3.p, c->h3inv.p, L.ds.p);
+        // no silu' saved: the VJP recomputes the hidden layers from ef
+        launch_mlp_hidden_x(st, E, nb, c->ef.p, L.mlp_tiles_x.p, L.mlp_winv, c->h3.p, c->h3inv.p, nullptr);
       else
         launch_mlp_hidden(st, E, nb, c->ef.p, L.mlp_tiles.p,
                           half ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), c->h3inv.p, L.ds.p,
@@ -1161,7 +1162,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
     {
       Site s(c, lname("mlp_hidden_bwd", l));
       if (split)
-        launch_mlp_hidden_bwd_x(st, E, nb, Ly.mlp_tiles_x.p, Ly.mlp_winv, Ly.ds.p, fused ? c->gh3p.p : c->h3.p,
+        launch_mlp_hidden_bwd_x(st, E, nb, Ly.mlp_tiles_x.p, Ly.mlp_winv, c->ef.p, nullptr, fused ? c->gh3p.p : c->h3.p,
                                 fused ? tpx_parts(Ly.lin) : 1, c->gef.p, first_edge_grad);
       else
         launch_mlp_hidden_bwd(st, E, nb, Ly.mlp_tiles.p, Ly.ds.p, c->h3.p, c->gef.p, first_edge_grad);

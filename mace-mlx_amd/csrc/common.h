@@ -60,6 +60,18 @@ struct FrontParams {
 // x rounded to the nearest fp16 value when `half` (the stored activations of a
 // model run under the float16 feature policy), else x
 __device__ __forceinline__ float qh(float x, bool half) { return half ? (float)(_Float16)x : x; }
+
+// max over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the lanes holding one
+// edge's k values in the 16x16 fragments), with the gfx950 permlane swaps: after
+// swapping x's upper half with its own lower half, the two results hold each
+// lane's value and its partner's (likewise for odd / even 16-lane rows)
+__device__ __forceinline__ float max4_rows(float m) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  m = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // ag_cov: covalent radius per species for the Agnesi transform (unused without it)
 void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* sender,
                      const int* receiver, const int* shifts, const int* species,
@@ -99,9 +111,11 @@ void launch_mlp_permute_x(hipStream_t st, int nb, const float* W0, const float* 
                           const float* scale3, void* tiles);
 void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, const void* tiles,
                          const float* winv3, void* h3x, float* h3inv, float* ds);
-// gh3: np partials of dL/dh3 ([np][E][64]), added in order
+// gh3: np partials of dL/dh3 ([np][E][64]), added in order; ds null: silu' of the
+// hidden pre-activations recomputed from ef (the forward then need not save them)
 void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tiles, const float* winv3,
-                             const float* ds, const float* gh3, int np, float* gef, int accumulate);
+                             const float* ef, const float* ds, const float* gh3, int np, float* gef,
+                             int accumulate);
 // half: h3, W3T and w fp16 arrays (fp32 accumulation); else fp32
 void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w,
                     int half);

@@ -222,8 +222,7 @@ __global__ void __launch_bounds__(256) k_mlp_hidden(int64_t E, int nb, const flo
       float m = 0.f;
 #pragma unroll
       for (int q = 0; q < 16; ++q) m = fmaxf(m, fabsf(v[q]));
-      m = fmaxf(m, __shfl_xor(m, 16));  // the four lanes of edge r
-      m = fmaxf(m, __shfl_xor(m, 32));
+      m = max4_rows(m);  // the four lanes of edge r
       // floor(log2 m) from the exponent field; zero / subnormal rows take -100 (finite scales)
       const int ex = max((int)((__float_as_uint(m) >> 23) & 0xff) - 127, -100);
       const float sc = __uint_as_float((unsigned)(127 + 14 - ex) << 23);
@@ -737,8 +736,7 @@ __global__ void __launch_bounds__(256) k_mlp_gh3_x(int64_t E, int W, const float
           for (int h = 0; h < 2; ++h)
             m = fmaxf(m, fmaxf(fmaxf(fabsf(cur[q][h].x), fabsf(cur[q][h].y)),
                                fmaxf(fabsf(cur[q][h].z), fabsf(cur[q][h].w))));
-        m = fmaxf(m, __shfl_xor(m, 16));  // the four lanes of edge r
-        m = fmaxf(m, __shfl_xor(m, 32));
+        m = max4_rows(m);  // the four lanes of edge r
         // floor(log2 m) from the exponent field; zero / subnormal stages take -100 (finite scales)
         const int ex = max((int)((__float_as_uint(m) >> 23) & 0xff) - 127, -100);
         const float sc = __uint_as_float((unsigned)(127 + 14 - ex) << 23);
@@ -925,8 +923,7 @@ __device__ __forceinline__ float edge_scale(const float* v, float* inv) {
   float m = 0.f;
 #pragma unroll
   for (int q = 0; q < NV; ++q) m = fmaxf(m, fabsf(v[q]));
-  m = fmaxf(m, __shfl_xor(m, 16));
-  m = fmaxf(m, __shfl_xor(m, 32));
+  m = max4_rows(m);  // the four lanes of edge r
   // floor(log2 m) from the exponent field; zero / subnormal edges take -100 (finite scales)
   const int ex = max((int)((__float_as_uint(m) >> 23) & 0xff) - 127, -100);
   *inv = __uint_as_float((unsigned)(127 - 14 + ex) << 23);
@@ -966,9 +963,10 @@ __device__ __forceinline__ void layer64x(const h8 (*w)[4][2][64], const float* v
 }
 
 // forward of the split kernels: first layer over the Bessel features, then two 64-wide
-// layers; dsp as in hidden_fwd; leaves a3
+// layers; dsp as in hidden_fwd; leaves a1, a2, a3 (the VJP recomputes them this
+// way, with the same instructions, instead of reading saved derivatives)
 __device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* winv, int64_t E, int64_t e0, int nb,
-                                             const float* __restrict__ ef, f4v* a3, float* dsp) {
+                                             const float* __restrict__ ef, f4v* a1, f4v* a2, f4v* a3, float* dsp) {
   const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t e = e0 + r;
   float x[8];
@@ -977,7 +975,6 @@ __device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* win
     const int k = 8 * g + j;
     x[j] = (e < E && k < nb) ? ef[e * nb + k] : 0.f;
   }
-  f4v a1[4], a2[4];
   {
     float inv;
     const float sc = edge_scale<8>(x, &inv);
@@ -1027,8 +1024,8 @@ __global__ void __launch_bounds__(256) k_mlp_hidden_x(int64_t E, int nb, const f
   const int64_t ngroups = (E + 15) / 16;
   for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
     const int64_t e0 = gi * 16, e = e0 + r;
-    f4v a3[4];
-    hidden_fwd_x(sw, wi.w, E, e0, nb, ef, a3, (ds && e < E) ? ds + e * 3 * H + 4 * g : nullptr);
+    f4v a1[4], a2[4], a3[4];
+    hidden_fwd_x(sw, wi.w, E, e0, nb, ef, a1, a2, a3, (ds && e < E) ? ds + e * 3 * H + 4 * g : nullptr);
     float v[16];
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = silu(a3[q >> 2][q & 3]);
@@ -1054,35 +1051,53 @@ __global__ void __launch_bounds__(256) k_mlp_hidden_x(int64_t E, int nb, const f
   }
 }
 
-// gh3: np partials [np][E][64] (stride pstride floats), added in order
-__global__ void __launch_bounds__(256) k_mlp_hidden_bwd_x(int64_t E, int nb, const MlpBwdX* __restrict__ tiles,
-                                                          MlpWinv wi, const float* __restrict__ ds,
+// gh3: np partials [np][E][64] (stride pstride floats), added in order.  RECOMP:
+// silu'(a1..a3) from the forward layers recomputed from ef (tiles ftiles) instead
+// of read from ds.
+template <bool RECOMP>
+__global__ void __launch_bounds__(256) k_mlp_hidden_bwd_x(int64_t E, int nb, const MlpFwdX* __restrict__ ftiles,
+                                                          const MlpBwdX* __restrict__ tiles, MlpWinv wi,
+                                                          const float* __restrict__ ef, const float* __restrict__ ds,
                                                           const float* __restrict__ gh3, int np, int64_t pstride,
                                                           float* __restrict__ gef, int accumulate) {
   __shared__ MlpBwdX sw;
+  __shared__ __align__(16) char swf_raw[RECOMP ? sizeof(MlpFwdX) : 16];
+  MlpFwdX& swf = *reinterpret_cast<MlpFwdX*>(swf_raw);
   stage_copy(sw, tiles);
+  if constexpr (RECOMP) stage_copy(swf, ftiles);
   __syncthreads();
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t ngroups = (E + 15) / 16;
   for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
     const int64_t e0 = gi * 16, e = e0 + r, ec = e < E ? e : E - 1;  // rows past the end: computed, not stored
-    const float* d = ds + ec * 3 * H;
     float v[16], dv[16];
     f4v acc[4];
+    f4v a1[4], a2[4], a3[4];  // RECOMP: the pre-activations, rebuilt
+    if constexpr (RECOMP) hidden_fwd_x(swf, wi.w, E, e0, nb, ef, a1, a2, a3, nullptr);
+    // silu' of layer k's pre-activations in the lane's layout (feature 16t + 4g + i -> [4t + i])
+    auto dsl = [&](int k, float* out) {
+      if constexpr (RECOMP) {
+        const f4v* a = k == 0 ? a1 : k == 1 ? a2 : a3;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) out[q] = dsilu(a[q >> 2][q & 3]);
+      } else {
+        ld_row16(ds + ec * 3 * H + k * H, g, out);
+      }
+    };
     ld_row16(gh3 + ec * H, g, v);
     for (int pp = 1; pp < np; ++pp) {
       ld_row16(gh3 + pp * pstride + ec * H, g, dv);
 #pragma unroll
       for (int q = 0; q < 16; ++q) v[q] += dv[q];
     }
-    ld_row16(d + 2 * H, g, dv);
+    dsl(2, dv);
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] *= dv[q];
-    ld_row16(d + H, g, dv);
+    dsl(1, dv);
     layer64x(sw.w2T, v, wi.w[2], acc);
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = acc[q >> 2][q & 3] * dv[q];
-    ld_row16(d, g, dv);
+    dsl(0, dv);
     layer64x(sw.w1T, v, wi.w[1], acc);
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = acc[q >> 2][q & 3] * dv[q];
@@ -1147,12 +1162,17 @@ void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, con
 }
 
 void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tiles, const float* winv3,
-                             const float* ds, const float* gh3, int np, float* gef, int accumulate) {
+                             const float* ef, const float* ds, const float* gh3, int np, float* gef, int accumulate) {
   if (E <= 0) return;
   MlpWinv wi{{winv3[0], winv3[1], winv3[2]}};
+  const MlpFwdX* fw = static_cast<const MlpFwdX*>(tiles);
   const MlpBwdX* bw = reinterpret_cast<const MlpBwdX*>(static_cast<const char*>(tiles) + sizeof(MlpFwdX));
-  hipLaunchKernelGGL(k_mlp_hidden_bwd_x, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, bw, wi, ds, gh3, np,
-                     E * H, gef, accumulate);
+  if (ds)
+    hipLaunchKernelGGL(k_mlp_hidden_bwd_x<false>, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, fw, bw, wi, ef, ds,
+                       gh3, np, E * H, gef, accumulate);
+  else
+    hipLaunchKernelGGL(k_mlp_hidden_bwd_x<true>, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, fw, bw, wi, ef, ds,
+                       gh3, np, E * H, gef, accumulate);
 }
 
 void launch_mlp_permute(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2, void* tiles) {

@@ -301,8 +301,7 @@ __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
         float mx = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = max4_rows(mx);  // the four lanes of row r
         // floor(log2 mx) from the exponent field; zero / subnormal chunks take -100 (finite scales)
         const int ex = max((int)((__float_as_uint(mx) >> 23) & 0xff) - 127, -100);
         const float sc = __uint_as_float((unsigned)(127 + 14 - ex) << 23);
