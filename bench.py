@@ -48,10 +48,21 @@ def algorithmic_work(site: str, ctx: dict):
     N, E, C, nb, H = ctx["N"], ctx["E"], 128, ctx["nb"], 64
     name, _, lyr = site.partition(".L")
     lay = ctx["layers"][int(lyr)] if lyr else None
+    fused = ctx.get("fused")
+    tabw = 72 if lay and lay["lin"] >= 2 else 0  # M1 table entries per edge (l1 = 1 slots)
     if name == "tp_fwd":
+        if fused:  # radial-MLP output layer inside: reads h3 (split planes + scale), writes w for the VJP
+            b = 4 * (N * lay["din"] + E * (16 + tabw) + E * lay["wn"] + N * lay["dmid"]) + E * (4 * H + 4)
+            return "hbm", b + 4 * (E + N + 1), "GB/s"
         b = 4 * (N * lay["din"] + E * 16 + E * lay["wn"] + N * lay["dmid"]) + 4 * (E + N + 1)
         return "hbm", b, "GB/s"
     if name == "tp_bwd":
+        if fused:  # reads w, writes dL/dx rows (after the first layer), dL/dY and dL/dh3 partials
+            parts = 2 if lay["lin"] == 1 else 4
+            gx = E * lay["din"] if int(lyr) > 0 else 0
+            b = 4 * (N * lay["dmid"] + N * lay["din"] + E * (16 + tabw) + E * lay["wn"] + gx
+                     + E * 16 * parts + E * H * parts)
+            return "hbm", b + 8 * (E + N + 1), "GB/s"
         b = 4 * (N * lay["dmid"] + N * lay["din"] + 2 * E * 16 + 2 * E * lay["wn"]) + 8 * (E + N + 1)
         return "hbm", b, "GB/s"
     if name == "tp_gather":  # segmented sum of the per-edge input-gradient rows
@@ -67,8 +78,10 @@ def algorithmic_work(site: str, ctx: dict):
         if ctx.get("split"):
             return "hbm", 4 * E * lay["wn"] + 4 * E * H + 4 * E, "GB/s"
         return "mfma", 2 * E * H * lay["wn"], "TFLOP/s"
-    if name == "mlp_hidden_bwd":  # the three transposed products (silu' saved by the forward)
-        return "mfma", 2 * E * (nb * H + 2 * H * H), "TFLOP/s"
+    if name == "mlp_hidden_bwd":
+        # the three transposed products; with split products the forward layers are recomputed
+        # (no saved derivatives), doubling the work
+        return "mfma", 2 * E * (nb * H + 2 * H * H) * (2 if ctx.get("split") else 1), "TFLOP/s"
     if name.startswith("linear") or name.startswith("skip"):
         return "mfma", ctx["linear_flops"].get(site, 0), "TFLOP/s"
     if name in ("sc_fwd", "sc_bwd"):
@@ -168,7 +181,7 @@ def tp_scatter_frac(per_step, ctx):
     return (b / (t * 1e-3) / 1e9) / HBM_PEAK_GBS if t > 0 else 0.0
 
 
-def measure_config(idx, steps, warmup):
+def measure_config(idx, steps, warmup, separate=False):
     """Steady-state and rebuild step times plus per-site roofline for configuration idx."""
     import torch
     from mace_mlx_amd._ffi import Engine
@@ -180,7 +193,7 @@ def measure_config(idx, steps, warmup):
     dm = build_device_model(bc.model, weights, dtype=bc.dtype)
     eng = Engine(0)
     eng.load_model(dm)
-    if args.separate_mlp_out:
+    if separate:
         eng.set_fused_tp(False)
     s = bc.system
     zmap = {int(z): k for k, z in enumerate(dm.z_table)}
@@ -212,7 +225,8 @@ def measure_config(idx, steps, warmup):
     eng.set_profiling(False)
     layers = layer_shapes(dm)
     ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_flops=linear_flops(layers, N),
-               half=bc.dtype == "float16", split=bc.dtype != "float16")
+               half=bc.dtype == "float16", split=bc.dtype != "float16",
+               fused=not separate and bc.dtype != "float16" and max(x["lin"] for x in layers) <= 2)
     per_step = {k: (v[0] / steps, v[1] // steps) for k, v in kt.items()}
     dom = max(per_step, key=lambda k: per_step[k][0])
     b, a, u = algorithmic_work(dom, ctx)
@@ -269,6 +283,8 @@ def main():
     dm = build_device_model(bc.model, weights, dtype=bc.dtype)
     eng = Engine(0)
     eng.load_model(dm)
+    if args.separate_mlp_out:
+        eng.set_fused_tp(False)
     s = bc.system
     zmap = {int(z): k for k, z in enumerate(dm.z_table)}
     species = np.array([zmap[int(z)] for z in s.numbers], np.int32)
@@ -309,7 +325,9 @@ def main():
     eng.set_profiling(False)
     layers = layer_shapes(dm)
     ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_flops=linear_flops(layers, N),
-               half=bc.dtype == "float16", split=bc.dtype != "float16")
+               half=bc.dtype == "float16", split=bc.dtype != "float16",
+               fused=not args.separate_mlp_out and bc.dtype != "float16"
+               and max(x["lin"] for x in layers) <= 2)
     per_step = {k: (v[0] / args.steps, v[1] // args.steps) for k, v in kt.items()}
     dom = max(per_step, key=lambda k: per_step[k][0])
     bound, amount, unit = algorithmic_work(dom, ctx)
@@ -347,7 +365,7 @@ def main():
     sweep = None
     if args.sweep:
         del eng
-        sweep = [measure_config(i, max(5, args.steps // 2), args.warmup) for i in range(5)]
+        sweep = [measure_config(i, max(5, args.steps // 2), args.warmup, args.separate_mlp_out) for i in range(5)]
         print(f"{'config':16s} {'N':>6s} {'E':>9s} {'ms/step':>9s} {'+NL ms':>8s} {'atom-steps/s':>13s}  "
               f"dominant site (frac of its roofline)   TP+scatter HBM frac", file=sys.stderr)
         for r in sweep:
