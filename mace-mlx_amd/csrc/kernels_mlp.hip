@@ -1141,6 +1141,9 @@ inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
 // grid of the hidden-layer kernels: enough blocks to fill the device, each
 // staging the weights once and walking several 64-edge groups
 inline unsigned hidden_grid(int64_t E) { return (unsigned)std::min<int64_t>((E + 63) / 64, 512); }
+// the VJP stages both tile images (76 KB) and holds three layers' pre-activations: one
+// block per CU, several 16-edge groups per wave (measured 10% faster than the forward's grid)
+inline unsigned hidden_bwd_grid(int64_t E) { return (unsigned)std::min<int64_t>((E + 63) / 64, 256); }
 
 size_t mlp_tile_bytes() { return sizeof(MlpFwdW) + sizeof(MlpBwdW); }
 size_t mlp_tile_x_bytes() { return sizeof(MlpFwdX) + sizeof(MlpBwdX); }
@@ -1171,8 +1174,8 @@ void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tile
     hipLaunchKernelGGL(k_mlp_hidden_bwd_x<false>, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, fw, bw, wi, ef, ds,
                        gh3, np, E * H, gef, accumulate);
   else
-    hipLaunchKernelGGL(k_mlp_hidden_bwd_x<true>, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, fw, bw, wi, ef, ds,
-                       gh3, np, E * H, gef, accumulate);
+    hipLaunchKernelGGL(k_mlp_hidden_bwd_x<true>, dim3(hidden_bwd_grid(E)), dim3(256), 0, st, E, nb, fw, bw, wi, ef,
+                       ds, gh3, np, E * H, gef, accumulate);
 }
 
 void launch_mlp_permute(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2, void* tiles) {

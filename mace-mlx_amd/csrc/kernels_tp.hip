@@ -334,11 +334,29 @@ __device__ __forceinline__ void store_gY(const float* gYu, int64_t e, int u, flo
 
 // Per-edge VJP of one channel: given g = dL/dM[recv] (this channel), writes
 // dL/dw, accumulates the input gradient (if GX) and this channel's dL/dY.
+// bit j of CG1_MASK[i]: the l1 = 1 table row i (entries i*K1 .. i*K1 + 23) has a CG term in
+// Y component j (a compile-time table, so the tests below fold away)
+constexpr unsigned cg1_mask_row(int i) {
+  unsigned m = 0;
+  for (int q = i * TP3_K1; q < (i + 1) * TP3_K1; ++q)
+    for (int x = TP3_M1_START[q]; x < TP3_M1_START[q + 1]; ++x) m |= 1u << TP3_M1_J[x];
+  return m;
+}
+constexpr unsigned CG1_MASK[3] = {cg1_mask_row(0), cg1_mask_row(1), cg1_mask_row(2)};
+
 template <int LIN, bool GX, int GRP = -1>
 __device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& in, float* gw_out,
                                             const float* __restrict__ Ye, const float* __restrict__ Me,
                                             const float* M2, float& gx0, float* gx1, float* gx2, float* gYu) {
   using T = TPT<LIN>;
+  // l1 = 1 slots: dL/dY_j = sum_i x1[i] u1[i][j] with u1[i][j] = sum_(s,k) w g C1[i, j, col(s) + k]
+  // (the x1 factor taken out of the CG sums: one product per (i, j) pair, not one per term)
+  constexpr bool L1SLOTS = LIN >= 2 && (GRP == -1 || GRP == 1);
+  float u1[3][16];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) u1[i][j] = 0.f;
 #pragma unroll
   for (int s = 0; s < T::NSLOT; ++s) {
     if (GRP >= 0 && T::l1(s) != GRP) continue;  // only the slots of input block l1 = GRP
@@ -367,9 +385,8 @@ __device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& i
           const float mq = Me[q];
           mk = fmaf(in.x1[i], mq, mk);
           if (GX) gx1[i] = fmaf(wg, mq, gx1[i]);
-          const float cq = wg * in.x1[i];
 #pragma unroll
-          for (int x = m1s(q); x < m1s(q + 1); ++x) gYu[m1j(x)] = fmaf(cq, m1v(x), gYu[m1j(x)]);
+          for (int x = m1s(q); x < m1s(q + 1); ++x) u1[i][m1j(x)] = fmaf(wg, m1v(x), u1[i][m1j(x)]);
         }
         gws = fmaf(g[a0 + k], mk, gws);
       }
@@ -394,6 +411,13 @@ __device__ __forceinline__ void tp_edge_vjp(const float* g, const EdgeIn<LIN>& i
     }
     gw_out[s] = gws;
     if constexpr (LIN == 3) __builtin_amdgcn_sched_barrier(0);  // as in tp_edge_fwd
+  }
+  if constexpr (L1SLOTS) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if ((CG1_MASK[i] >> j) & 1u) gYu[j] = fmaf(in.x1[i], u1[i][j], gYu[j]);
   }
 }
 
