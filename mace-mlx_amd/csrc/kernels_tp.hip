@@ -586,6 +586,10 @@ __device__ __forceinline__ f4v mfma16h(h8 a, h8 b, f4v c) {
 }
 
 constexpr int XW = 8;          // waves per fused block (receivers in flight)
+// edges per wave and step in the fused forward (a step's tile: XW * EPW edges).  4 halves the
+// steps and made the forward 2-4% faster, but the VJP that later reads the weights it wrote
+// ran 5% slower (same code; only the order in which w reached memory differed): net loss
+constexpr int EPW = 2;
 constexpr int XH = RADIAL_H;   // radial hidden width (the contraction of the output layer)
 static_assert(XH == 64, "two 32-wide k steps");
 
@@ -646,6 +650,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   using GR = GrpT<LIN, L1>;
   constexpr int G = GR::G, CT = 4 * G, NCTW = (CT + XW - 1) / XW, RS = 64 * G + 4;
   constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, NX = 2 * L1 + 1;
+  constexpr int TC = XW * EPW, NTC = TC / 16;  // tile columns (edges) per step; 16-column MFMA tiles
   // wave index through readfirstlane: receiver, edge indices and senders are then
   // wave-uniform scalars (scalar loads, no vector-memory waits on the prefetches)
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -653,11 +658,14 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   const int c0 = 64 * blockIdx.y, nb0 = XW * blockIdx.x;
   const int n = nb0 + wv;
   const int beg = rowptr[min(n, a.N)], end = n < a.N ? rowptr[n + 1] : beg;
-  const int nr = nb0 + (r >> 1);  // receiver of tile column r
-  const int cb = rowptr[min(nr, a.N)], ce = nr < a.N ? rowptr[nr + 1] : cb;
-  int ns = (ce - cb + 1) >> 1;
+  int ns;
+  {
+    const int nq = nb0 + (l & (XW - 1));  // lanes 0..7: the block's receivers
+    const int qb = rowptr[min(nq, a.N)], qe = nq < a.N ? rowptr[nq + 1] : qb;
+    ns = (qe - qb + EPW - 1) / EPW;
+  }
 #pragma unroll
-  for (int off = 8; off > 0; off >>= 1) ns = max(ns, __shfl_xor(ns, off));
+  for (int off = 1; off < XW; off <<= 1) ns = max(ns, __shfl_xor(ns, off));
   const int nsteps = __builtin_amdgcn_readfirstlane(ns);
 
   h8 wa[NCTW][2][2];  // [tile][k step][hi, lo]
@@ -687,44 +695,46 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   constexpr int TY = L1 == 0 ? 16 : 0, TS = TY + (L1 == 1 ? TP3_M1_NE : 0), TSP = (TS + 3) & ~3;
   constexpr int TH = (TS + 63) / 64;
   static_assert(TS <= 128 && L1 <= 1, "table rows of up to 128 entries");
-  float* tb = stab + wv * 2 * TSP;  // this wave's two table rows (Y for l1 = 0 slots, M1 for l1 = 1)
-  // The 16 h3 rows of a step's tile (hi and lo planes, 4 KB) are fetched once
-  // per block, 8 bytes per thread, and staged in LDS (double-buffered, written
-  // before the barrier of the step before their use); each wave then reads its
-  // B fragments from there.  Thread t fetches column hr = t / 32, plane hp,
-  // fp16 entries 4 hq .. 4 hq + 3.
-  static_assert(XW == 8, "the h3 tile is fetched by 512 threads");
-  const int hr = threadIdx.x >> 5, hpl = (threadIdx.x >> 4) & 1, hq = threadIdx.x & 15;
-  const int hn = nb0 + (hr >> 1);
+  float* tb = stab + wv * EPW * TSP;  // this wave's table rows (Y for l1 = 0 slots, M1 for l1 = 1)
+  // The TC h3 rows of a step's tile (hi and lo planes) are fetched once per block,
+  // TC / 2 bytes per thread, and staged in LDS (double-buffered, written before the
+  // barrier of the step before their use); each wave then reads its B fragments
+  // from there.  Thread t fetches tile column hr, plane hpl, fp16 entries
+  // HQ hq .. HQ hq + HQ - 1.
+  static_assert(XW == 8 && (TC == 16 || TC == 32), "the h3 tile is fetched by 512 threads");
+  constexpr int TPR = 512 / TC, HQ = 128 / TPR;  // threads per tile row; fp16 entries per thread
+  typedef unsigned hv __attribute__((ext_vector_type(HQ / 2)));
+  const int hr = threadIdx.x / TPR, hpl = (threadIdx.x % TPR) / (TPR / 2), hq = threadIdx.x % (TPR / 2);
+  const int hn = nb0 + hr / EPW;
   const int hb0 = rowptr[min(hn, a.N)];
   struct Slot {
-    uint2 h;        // this thread's 8 bytes of the step's h3 tile
-    float hinv;     // inverse scale of its row
-    float x[2][NX]; // sender rows of the wave's two edges
-    float t[2][TH]; // their table rows (this lane's entries)
-    int snd[2];     // sender indices
+    hv h;               // this thread's share of the step's h3 tile
+    float hinv;         // inverse scale of its row
+    float x[EPW][NX];   // sender rows of the wave's edges
+    float t[EPW][TH];   // their table rows (this lane's entries)
+    int snd[EPW];       // sender indices
   };
   Slot s0, s1;
   auto load_snd = [&](int j, Slot& S) {
 #pragma unroll
-    for (int b = 0; b < 2; ++b) S.snd[b] = sender[min<int64_t>(beg + 2 * j + b, elast)];
+    for (int b = 0; b < EPW; ++b) S.snd[b] = sender[min<int64_t>(beg + EPW * j + b, elast)];
   };
   auto load_h = [&](int j, Slot& S) {
-    const int64_t row = min<int64_t>(hb0 + 2 * j + (hr & 1), elast);  // columns past a receiver's end: not stored
-    S.h = *reinterpret_cast<const uint2*>(h3x + row * 2 * XH + hpl * XH + 4 * hq);
+    const int64_t row = min<int64_t>(hb0 + EPW * j + hr % EPW, elast);  // columns past a receiver's end: not stored
+    S.h = *reinterpret_cast<const hv*>(h3x + row * 2 * XH + hpl * XH + HQ * hq);
     S.hinv = h3inv[row];
   };
   auto store_h = [&](int j, const Slot& S) {  // S holds step j's tile share
-    *reinterpret_cast<uint2*>(hbuf + (((j & 1) * 2 + hpl) * 16 + hr) * 72 + 4 * hq) = S.h;
-    if (hpl == 0 && hq == 0) hiv[(j & 1) * 16 + hr] = S.hinv;
+    *reinterpret_cast<hv*>(hbuf + (((j & 1) * 2 + hpl) * TC + hr) * 72 + HQ * hq) = S.h;
+    if (hpl == 0 && hq == 0) hiv[(j & 1) * TC + hr] = S.hinv;
   };
   auto load_slot = [&](int j, Slot& S) {  // S.snd already holds step j's indices
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < EPW; ++b) {
       const float* xs = up + (int64_t)S.snd[b] * DIN + NC * L1 * L1 + c0 + u;
 #pragma unroll
       for (int i = 0; i < NX; ++i) S.x[b][i] = xs[NC * i];
-      const int64_t e = min<int64_t>(beg + 2 * j + b, elast);
+      const int64_t e = min<int64_t>(beg + EPW * j + b, elast);
 #pragma unroll
       for (int h = 0; h < TH; ++h) {
         const int i = min(l + 64 * h, TS - 1);
@@ -736,51 +746,53 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 #pragma unroll
   for (int q = 0; q < T::NACC; ++q) acc[q] = 0.f;
   auto step = [&](int j, Slot& S, Slot& Snext) {
-    float* tile = sw + (j & 1) * 16 * RS;
+    float* tile = sw + (j & 1) * TC * RS;
     load_h(j + 2, S);  // S's share of step j was staged during step j - 1
-    h8 bx[2][2];       // B fragments of tile column r: [k step][hi, lo]
-    {
-      const _Float16* hrow = hbuf + ((j & 1) * 2 * 16 + r) * 72 + 8 * g;
+#pragma unroll
+    for (int t2 = 0; t2 < NTC; ++t2) {
+      h8 bx[2][2];  // B fragments of tile column 16 t2 + r: [k step][hi, lo]
+      const int col = 16 * t2 + r;
+      const _Float16* hrow = hbuf + ((j & 1) * 2 * TC + col) * 72 + 8 * g;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         bx[c][0] = *reinterpret_cast<const h8*>(hrow + 32 * c);
-        bx[c][1] = *reinterpret_cast<const h8*>(hrow + 16 * 72 + 32 * c);
+        bx[c][1] = *reinterpret_cast<const h8*>(hrow + TC * 72 + 32 * c);
       }
-    }
-    f4v d[NCTW];
+      f4v d[NCTW];
 #pragma unroll
-    for (int m = 0; m < NCTW; ++m) d[m] = f4v{0.f, 0.f, 0.f, 0.f};
+      for (int m = 0; m < NCTW; ++m) d[m] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int p = 0; p < 3; ++p)
+        for (int p = 0; p < 3; ++p)
 #pragma unroll
-        for (int m = 0; m < NCTW; ++m)
-          if (CT % XW == 0 || wv + XW * m < CT)  // every wave's tiles exist when XW divides CT
-            d[m] = mfma16h(wa[m][c][p == 2 ? 0 : p ^ 1], bx[c][p == 1 ? 1 : 0], d[m]);  // lo.hi, hi.lo, hi.hi
-    const float bsc = hiv[(j & 1) * 16 + r] * a.wscale;
+          for (int m = 0; m < NCTW; ++m)
+            if (CT % XW == 0 || wv + XW * m < CT)  // every wave's tiles exist when XW divides CT
+              d[m] = mfma16h(wa[m][c][p == 2 ? 0 : p ^ 1], bx[c][p == 1 ? 1 : 0], d[m]);  // lo.hi, hi.lo, hi.hi
+      const float bsc = hiv[(j & 1) * TC + col] * a.wscale;
 #pragma unroll
-    for (int m = 0; m < NCTW; ++m) {
-      const int ct = wv + XW * m;
-      if (CT % XW == 0 || ct < CT)
-        *reinterpret_cast<float4*>(tile + r * RS + 16 * ct + 4 * g) =
-            float4{d[m][0] * bsc, d[m][1] * bsc, d[m][2] * bsc, d[m][3] * bsc};
+      for (int m = 0; m < NCTW; ++m) {
+        const int ct = wv + XW * m;
+        if (CT % XW == 0 || ct < CT)
+          *reinterpret_cast<float4*>(tile + col * RS + 16 * ct + 4 * g) =
+              float4{d[m][0] * bsc, d[m][1] * bsc, d[m][2] * bsc, d[m][3] * bsc};
+      }
     }
     store_h(j + 1, Snext);  // its last readers (step j - 1) are past the previous barrier
     __syncthreads();
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < EPW; ++b)
 #pragma unroll
       for (int h = 0; h < TH; ++h)
         if (l + 64 * h < TS) tb[b * TSP + l + 64 * h] = S.t[b][h];
     wave_sync();
     load_snd(j + 3, Snext);  // Snext's step j + 1 rows are already in flight
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int e = beg + 2 * j + b;
+    for (int b = 0; b < EPW; ++b) {
+      const int e = beg + EPW * j + b;
       const bool valid = e < end;
       float wv_s[T::NSLOT];
-      const float* trow = tile + (2 * wv + b) * RS + u;
+      const float* trow = tile + (EPW * wv + b) * RS + u;
 #pragma unroll
       for (int s = 0; s < T::NSLOT; ++s)
         if (T::l1(s) == L1) wv_s[s] = trow[64 * GR::local(s)];
@@ -835,12 +847,13 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 }
 
 template <int LIN>
-__global__ void __launch_bounds__(64 * XW, LIN == 1 ? 4 : 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_PTRS) {
+__global__ void __launch_bounds__(64 * XW, 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_PTRS) {
   static_assert(LIN <= 2, "three input blocks are not fused");
-  __shared__ __align__(16) float sw[2 * 16 * (64 * gmax<LIN>() + 4)];
-  __shared__ __align__(16) float stab[XW * 2 * (LIN == 1 ? 16 : TP3_M1_NE)];
-  __shared__ __align__(16) _Float16 hbuf[2 * 2 * 16 * 72];  // [step][hi, lo][tile column][64 + pad]
-  __shared__ float hiv[2 * 16];
+  constexpr int TC = XW * EPW;
+  __shared__ __align__(16) float sw[2 * TC * (64 * gmax<LIN>() + 4)];
+  __shared__ __align__(16) float stab[XW * EPW * (LIN == 1 ? 16 : TP3_M1_NE)];
+  __shared__ __align__(16) _Float16 hbuf[2 * 2 * TC * 72];  // [step][hi, lo][tile column][64 + pad]
+  __shared__ float hiv[2 * TC];
   if constexpr (LIN == 1) {
     tpx_fwd<1, 0>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
   } else {
