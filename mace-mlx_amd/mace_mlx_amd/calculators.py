@@ -14,6 +14,8 @@ Behaviour kept from the reference:
   (atol 1e-10) or an atom moved more than ``skin / 2`` (266-283) -- evaluated
   inside the engine, on the device;
 * unknown atomic numbers raise ValueError with the supported list (345-354);
+* multi-head models evaluate the ``head`` named at construction, else the first;
+  an unknown name raises ValueError (128-137);
 * stress = dE/d(eps_sym) / |det cell| in Voigt order xx, yy, zz, yz, xz, xy
   (515-523), computed in the same backward pass; once requested for a 3-D
   periodic cell it stays on for later steps (385-388).
@@ -35,7 +37,7 @@ import numpy as np
 
 from ._ffi import Engine
 from .device_model import build_device_model
-from .model_io import load_config, load_weights
+from .model_io import head_index, load_config, load_weights
 
 try:  # ASE is optional: the engine works with any object exposing the Atoms API
     from ase.calculators.calculator import Calculator as _AseCalculator, all_changes  # type: ignore
@@ -134,13 +136,13 @@ class MACEHIPCalculator(_AseCalculator):
         super().__init__(**kwargs)
         model_dir = self._resolve_model(str(model_path))
         self.config = load_config(model_dir)
-        if self.config.heads is not None and len(self.config.heads) > 1:
-            raise NotImplementedError("multi-head models are not supported yet")
-        if head is not None and self.config.heads is not None and head not in self.config.heads:
-            raise ValueError(f"Head '{head}' not found in model heads: {self.config.heads}")
-        self._head = head
+        # multi-head: the named head, else the first; ValueError for an unknown name
+        # (calculators.py:128-137); the engine holds that head's readouts only
+        self._head = None
+        if self.config.num_heads > 1:
+            self._head = self.config.heads[head_index(self.config, head)]
         weights = load_weights(model_dir)
-        self._dm = build_device_model(self.config, weights, dtype=default_dtype)
+        self._dm = build_device_model(self.config, weights, dtype=default_dtype, head=self._head)
         self.default_dtype = default_dtype
         self.r_max = float(self.config.r_max)
         self.z_table = list(self._dm.z_table)

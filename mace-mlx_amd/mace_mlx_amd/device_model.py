@@ -30,13 +30,13 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass
-from typing import Dict, List
+from typing import Dict, List, Optional
 
 import numpy as np
 
 from .cg import u_matrix, wigner_3j
 from .irreps import Irrep, Irreps
-from .model_io import COVALENT_RADII, ModelConfig, conv_tp_instructions, linear_instructions
+from .model_io import COVALENT_RADII, ModelConfig, conv_tp_instructions, linear_instructions, select_head
 
 
 class UnsupportedModel(NotImplementedError):
@@ -75,14 +75,17 @@ def round_weights_fp16(w: Dict[str, np.ndarray]) -> Dict[str, np.ndarray]:
             for k, v in w.items()}
 
 
-def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = "float32") -> DeviceModel:
+def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = "float32",
+                       head: Optional[str] = None) -> DeviceModel:
     """Fold a model (config + reference-layout weights) into the engine's tensors.  dtype
-    "float16" selects the reference's half-precision feature policy."""
+    "float16" selects the reference's half-precision feature policy; ``head`` the readout
+    head of a multi-head model (default: the first, as `calculators.py:128-137`)."""
     if dtype not in ("float32", "float16"):
         raise UnsupportedModel(f"dtype={dtype!r} (float32 and float16 are implemented)")
     if dtype == "float16":
         w = round_weights_fp16(w)
     cfg.check_supported()
+    cfg, w = select_head(cfg, w, head)
     if cfg.model_type not in ("MACE", "ScaleShiftMACE"):
         raise UnsupportedModel(f"model_type={cfg.model_type}")
     C = cfg.num_features
@@ -93,9 +96,6 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = 
         raise UnsupportedModel(f"radial_MLP={cfg.radial_MLP}")
     scale = float(cfg.scale) if cfg.model_type == "ScaleShiftMACE" else 1.0
     shift = float(cfg.shift) if cfg.model_type == "ScaleShiftMACE" else 0.0
-    for v, nm in ((scale, "scale"), (shift, "shift")):
-        if isinstance(v, (list, tuple)):
-            raise UnsupportedModel(f"per-head {nm}")
     z_table = list(cfg.z_table) if cfg.z_table else list(range(nel))
     T: Dict[str, np.ndarray] = {}
     f64 = lambda k: np.asarray(w[k], dtype=np.float64)

@@ -26,7 +26,7 @@ from __future__ import annotations
 
 import json
 import math
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 from pathlib import Path
 from typing import Dict, List, Optional
 
@@ -127,6 +127,11 @@ class ModelConfig:
         return Irreps(self.hidden_irreps)
 
     @property
+    def num_heads(self) -> int:
+        """Readout heads (`model.py:89-91`): one per entry of ``heads``, else one."""
+        return len(self.heads) if self.heads else 1
+
+    @property
     def num_features(self) -> int:
         return self.hidden[0].mul
 
@@ -160,8 +165,6 @@ class ModelConfig:
                 raise NotImplementedError(f"distance_transform keys {sorted(unknown)}")
         if not self.apply_cutoff:
             raise NotImplementedError("apply_cutoff=False")
-        if self.heads is not None and len(self.heads) > 1:
-            raise NotImplementedError("multi-head models")
         if self.gate != "silu":
             raise NotImplementedError(f"gate={self.gate}")
         if any(b.ir.l == 0 and b.ir.p != 1 for b in self.hidden):
@@ -259,7 +262,9 @@ def weight_shapes(cfg: ModelConfig) -> Dict[str, tuple]:
     nel = cfg.num_elements
     C = cfg.num_features
     attrs = Irreps(f"{nel}x0e")
-    shapes["atomic_energies_fn.atomic_energies"] = (nel,)
+    H = cfg.num_heads
+    # (num_elements,) single-head, (num_heads, num_elements) multi-head (converter.py:175-185)
+    shapes["atomic_energies_fn.atomic_energies"] = (H, nel) if H > 1 else (nel,)
     scal = Irreps([b for b in cfg.hidden if b.ir.l == 0])
     for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(attrs, scal)):
         shapes[f"node_embedding.linear.weights.{n}"] = (mi, mo)
@@ -294,14 +299,17 @@ def weight_shapes(cfg: ModelConfig) -> Dict[str, tuple]:
         for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(hid, hid)):
             shapes[f"{q}.linear.weights.{n}"] = (mi, mo)
         r = f"readouts.{li}"
+        # readouts give num_heads x 0e; the last one's MLP has 16 x num_heads scalars
+        # (model.py:135-139)
+        out = Irreps(f"{H}x0e")
         if li < cfg.num_interactions - 1:
-            for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(hid, Irreps("0e"))):
+            for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(hid, out)):
                 shapes[f"{r}.linear.weights.{n}"] = (mi, mo)
         else:
-            mlp = Irreps("16x0e")
+            mlp = Irreps(f"{16 * H}x0e")
             for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(hid, mlp)):
                 shapes[f"{r}.linear_1.weights.{n}"] = (mi, mo)
-            for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(mlp, Irreps("0e"))):
+            for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(mlp, out)):
                 shapes[f"{r}.linear_2.weights.{n}"] = (mi, mo)
     return shapes
 
@@ -332,3 +340,58 @@ def random_init(cfg: ModelConfig, seed: int = 0) -> Dict[str, np.ndarray]:
         else:
             w[key] = rng.standard_normal(shp)
     return {k: v.astype(np.float32) for k, v in w.items()}
+
+
+def head_index(cfg: ModelConfig, head: Optional[str] = None) -> int:
+    """Index of the active head: the named one, else the first (`calculators.py:128-137`);
+    single-head models ignore ``head``."""
+    if cfg.num_heads == 1:
+        return 0
+    name = cfg.heads[0] if head is None else head
+    if name not in cfg.heads:
+        raise ValueError(f"Head '{name}' not found in model heads: {cfg.heads}")
+    return cfg.heads.index(name)
+
+
+def select_head(cfg: ModelConfig, w: Dict[str, np.ndarray],
+                head: Optional[str] = None) -> tuple:
+    """The single-head model whose energy equals head ``head`` of ``cfg``.
+
+    The reference evaluates every head and then picks one column: E0 and the readouts
+    give (N, num_heads) and `_e0_select_head` / `_readout_select_head` take the active
+    column (`model.py:302-326`); the non-linear readout multiplies its 16 x num_heads
+    gated features by a mask that keeps the active head's 16 (`blocks.py:583-608`)
+    before `linear_2`, whose path weight is 1/sqrt(16 x num_heads) (`linear.py:46-74`);
+    ScaleShiftMACE takes the active entry of per-head scale / shift lists, falling back
+    to entry 0 (`model.py:530-548`).  Keeping only the active head's weights gives the
+    same numbers: `linear_2`'s rows are rescaled by 1/sqrt(num_heads) so that the
+    single-head path weight 1/sqrt(16) reproduces 1/sqrt(16 x num_heads)."""
+    h = head_index(cfg, head)
+    H = cfg.num_heads
+
+    def pick(v):
+        if isinstance(v, (list, tuple)):
+            return float(v[h] if h < len(v) else v[0])
+        return float(v)
+
+    ae = cfg.atomic_energies
+    if ae is not None and H > 1:
+        ae = [float(x) for x in np.asarray(ae, dtype=np.float64).reshape(H, -1)[h]]
+    out_cfg = replace(cfg, heads=None, scale=pick(cfg.scale), shift=pick(cfg.shift), atomic_energies=ae)
+    if H == 1:
+        return out_cfg, dict(w)
+    last = f"readouts.{cfg.num_interactions - 1}."
+    out: Dict[str, np.ndarray] = {}
+    for k, v in w.items():
+        v = np.asarray(v)
+        if k == "atomic_energies_fn.atomic_energies":
+            v = v.reshape(H, -1)[h]
+        elif k.startswith(last + "linear_1.weights."):
+            v = v[:, 16 * h:16 * (h + 1)]
+        elif k.startswith(last + "linear_2.weights."):
+            # kept in float64: the reference applies the path weight at run time
+            v = v[16 * h:16 * (h + 1), h:h + 1].astype(np.float64) / math.sqrt(H)
+        elif k.startswith("readouts.") and ".linear.weights." in k:
+            v = v[:, h:h + 1]
+        out[k] = np.ascontiguousarray(v)
+    return out_cfg, out

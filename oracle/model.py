@@ -17,7 +17,10 @@ Semantics follow the reference's generic code paths:
                                variants: Agnesi distance transform `radial.py:207-262`,
                                density normalisation `blocks.py:282-490`, non-residual
                                first interaction `blocks.py:68-176`, `model.py:213-247`
-* energy assembly              `model.py:403-438`
+* energy assembly              `model.py:403-438`; ScaleShiftMACE `model.py:508-589`;
+                               multi-head readouts: every head evaluated, the non-linear
+                               readout's features masked to the active head, the active
+                               column taken (`model.py:302-326,392-400`, `blocks.py:553-608`)
 * forces / stress              `calculators.py:440-563` (autograd; symmetric displacement)
 
 Constants (3j, U) come from ``mace_mlx_amd.cg``, which is pinned against golden
@@ -325,11 +328,19 @@ class OracleMACE:
 
     def __init__(self, model_dir=None, cfg: Optional[ModelConfig] = None,
                  weights: Optional[Dict[str, np.ndarray]] = None,
-                 dtype=torch.float64, edge_chunk: int = 8192):
+                 dtype=torch.float64, edge_chunk: int = 8192, head: Optional[str] = None):
         if model_dir is not None:
             cfg = load_config(model_dir)
             weights = load_weights(model_dir)
         cfg.check_supported()
+        # active head (`calculators.py:128-137`): named, else the first
+        self.H = len(cfg.heads) if cfg.heads else 1
+        self.h = 0
+        if self.H > 1:
+            name = cfg.heads[0] if head is None else head
+            if name not in cfg.heads:
+                raise ValueError(f"Head '{name}' not found in model heads: {cfg.heads}")
+            self.h = cfg.heads.index(name)
         self.cfg, self.dtype, self.edge_chunk = cfg, dtype, edge_chunk
         W = {k: _t(v, dtype) for k, v in weights.items()}
         self.W = W
@@ -381,16 +392,27 @@ class OracleMACE:
             L["sc"] = SymmetricContraction(inter, hid, cfg.correlation[li], wfn, dtype)
             L["plin"] = Linear(hid, hid, wl(f"products.{li}.linear.weights"))
             r = f"readouts.{li}"
+            ro_out = Irreps(f"{self.H}x0e")   # model.py:135-139
             if li < cfg.num_interactions - 1:
-                L["ro"] = ("linear", Linear(hid, Irreps("0e"), wl(f"{r}.linear.weights")))
+                L["ro"] = ("linear", Linear(hid, ro_out, wl(f"{r}.linear.weights")))
             else:
-                mlp = Irreps("16x0e")
+                mlp = Irreps(f"{16 * self.H}x0e")
                 L["ro"] = ("nonlinear", Linear(hid, mlp, wl(f"{r}.linear_1.weights")),
-                           Linear(mlp, Irreps("0e"), wl(f"{r}.linear_2.weights")))
+                           Linear(mlp, ro_out, wl(f"{r}.linear_2.weights")))
             self.layers.append(L)
             irr_in = hid
         self.sh_lmax = cfg.max_ell
-        self.e0 = W["atomic_energies_fn.atomic_energies"].reshape(-1)
+        # (num_heads, num_elements) for multi-head models; x @ ae.T, then the active column
+        # (blocks.py:45-65, model.py:316-326)
+        self.e0 = W["atomic_energies_fn.atomic_energies"].reshape(self.H, -1)[self.h]
+        ss = cfg.model_type == "ScaleShiftMACE"
+
+        def per_head(v):   # ScaleShiftMACE.scale_val / shift_val, model.py:530-548
+            if isinstance(v, (list, tuple)):
+                return float(v[self.h] if self.h < len(v) else v[0])
+            return float(v)
+        self.scale = per_head(cfg.scale) if ss else None
+        self.shift = per_head(cfg.shift) if ss else 0.0
         self.bw = W["radial_embedding.bessel_fn.bessel_weights"]
         self.agnesi = cfg.agnesi()
         self.radii = _t(cfg.agnesi_radii(), dtype)
@@ -433,9 +455,18 @@ class OracleMACE:
                 h = h + sc
             ro = L["ro"]
             if ro[0] == "linear":
-                terms.append(ro[1](h)[:, 0])
+                terms.append(ro[1](h)[:, self.h])
             else:
-                terms.append(ro[2](_silu(ro[1](h)))[:, 0])
+                g = _silu(ro[1](h))
+                if self.H > 1:   # keep the active head's 16 features (blocks.py:583-608)
+                    mask = torch.zeros(g.shape[1], dtype=g.dtype)
+                    mask[16 * self.h:16 * (self.h + 1)] = 1.0
+                    g = g * mask
+                terms.append(ro[2](g)[:, self.h])
+        if self.scale is not None:
+            # ScaleShiftMACE (model.py:550-589): pair + readouts scaled, shift per atom
+            inter = torch.stack(terms[1:], 0).sum(0)
+            terms = [terms[0], self.scale * inter + self.shift]
         node_energy = torch.stack(terms, 0).sum(0)
         return node_energy.sum(), node_energy
 

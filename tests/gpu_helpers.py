@@ -24,11 +24,11 @@ class Case:
     oracle evaluates the same half-precision model (weights rounded to fp16 except the
     pinned ones) in float64, i.e. without the feature-path roundings."""
 
-    def __init__(self, cfg, seed=0, dtype="float32"):
-        self.cfg = cfg
+    def __init__(self, cfg, seed=0, dtype="float32", head=None):
+        self.cfg, self.head = cfg, head
         self.w = random_init(cfg, seed)
         self.w_model = round_weights_fp16(self.w) if dtype == "float16" else self.w
-        self.dm = build_device_model(cfg, self.w, dtype=dtype)
+        self.dm = build_device_model(cfg, self.w, dtype=dtype, head=head)
         self.eng = Engine(0)
         self.eng.load_model(self.dm)
         self._oracle = None
@@ -36,7 +36,8 @@ class Case:
     @property
     def oracle(self):
         if self._oracle is None:
-            self._oracle = OracleMACE(cfg=self.cfg, weights=self.w_model, dtype=torch.float64)
+            self._oracle = OracleMACE(cfg=self.cfg, weights=self.w_model, dtype=torch.float64,
+                                      head=self.head)
         return self._oracle
 
     def run(self, s, stress=False, skin=0.5, force_nl=False):

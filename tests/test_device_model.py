@@ -114,3 +114,100 @@ def test_float16_policy_rounds_all_but_pinned_weights():
         np.testing.assert_array_equal(dm16.tensors[k], dm_r.tensors[k])
     with pytest.raises(UnsupportedModel):
         build_device_model(cfg, w, dtype="bfloat16")
+
+
+def _multihead_cfg(heads, **kw):
+    cfg = arch_config("medium", num_elements=2, z_table=[8, 14], zbl=True, **kw)
+    cfg.heads = list(heads)
+    return cfg
+
+
+def test_multi_head_oracle_pinned_by_embedding():
+    """The oracle's multi-head readouts (every head evaluated, the non-linear readout's
+    features masked to the active head, the active column taken; `model.py:302-326`,
+    `blocks.py:553-608`) pinned by embedding a single-head model as head "b" of a two-head
+    model: the single-head weights become head b's columns, `linear_2`'s rows scaled by
+    sqrt(2) because its path weight drops from 1/sqrt(16) to 1/sqrt(32) (`linear.py:46-74`).
+    Head b must then reproduce the single-head energies exactly, and head a must not."""
+    s, i, j, S = _two_species_system()
+    one = arch_config("medium", num_elements=2, z_table=[8, 14], zbl=True, atomic_energies=[-2.0, -1.0])
+    w1 = random_init(one, 7)
+    two = _multihead_cfg(["a", "b"], atomic_energies=[[0.5, 0.25], [-2.0, -1.0]])
+    w2 = {k: v.astype(np.float64) for k, v in random_init(two, 8).items()}
+    last = f"readouts.{one.num_interactions - 1}"
+    w2["atomic_energies_fn.atomic_energies"] = np.array([[0.5, 0.25], [-2.0, -1.0]], np.float32)
+    for k, v in w1.items():
+        if k.startswith("readouts.") and ".linear.weights." in k:
+            w2[k][:, 1:2] = v
+        elif k.startswith(f"{last}.linear_1."):
+            w2[k][:, 16:32] = v
+        elif k.startswith(f"{last}.linear_2."):
+            w2[k][16:32, 1:2] = v * np.sqrt(2.0)
+        elif k != "atomic_energies_fn.atomic_energies":
+            w2[k] = v
+    sp = np.array([0 if z == 8 else 1 for z in s.numbers])
+    ei = np.stack([i, j])
+    E1, ne1 = OracleMACE(cfg=one, weights=w1).energy(s.positions, sp, ei, S, s.cell)
+    Eb, neb = OracleMACE(cfg=two, weights=w2, head="b").energy(s.positions, sp, ei, S, s.cell)
+    Ea, nea = OracleMACE(cfg=two, weights=w2, head="a").energy(s.positions, sp, ei, S, s.cell)
+    np.testing.assert_allclose(neb, ne1, rtol=0, atol=1e-10)
+    assert abs(Ea - E1) > 1e-3
+    with pytest.raises(ValueError):
+        OracleMACE(cfg=two, weights=w2, head="nope")
+
+
+def _two_species_system():
+    s = rattle(diamond_si((2, 2, 2)), 0.05, 11)
+    s.numbers = np.where(np.arange(len(s)) % 4 == 0, 8, 14)
+    i, j, S = neighbor_list(s.positions, s.cell, s.pbc, 6.5)
+    return s, i, j, S
+
+
+@pytest.mark.parametrize("head", ["pbe", "r2scan", "third"])
+def test_multi_head_selection_matches_oracle(head):
+    """build_device_model(head=...) keeps one head's readouts, E0 row and ScaleShift
+    entry (`model_io.select_head`); the folded tensors, re-evaluated in float64, equal the
+    oracle's evaluation of the full three-head ScaleShiftMACE.  The shift list is shorter
+    than the head list, so head "third" takes entry 0 (`model.py:530-548`)."""
+    s, i, j, S = _two_species_system()
+    cfg = _multihead_cfg(["pbe", "r2scan", "third"],
+                         atomic_energies=[[-3.0, -1.5], [0.5, 0.25], [1.0, -0.75]])
+    cfg.model_type = "ScaleShiftMACE"
+    cfg.scale, cfg.shift = [1.7, 0.8, 1.1], [-0.3, 0.2]
+    w = random_init(cfg, 9)
+    sp = np.array([0 if z == 8 else 1 for z in s.numbers])
+    Eo, neo = OracleMACE(cfg=cfg, weights=w, head=head).energy(s.positions, sp, np.stack([i, j]), S, s.cell)
+    dm = build_device_model(cfg, w, head=head)
+    Ek, nek = kernel_model.energy(dm, s.positions, sp, i, j, S.astype(float), s.cell)
+    np.testing.assert_allclose(nek, neo, atol=5e-6)
+    assert abs(Ek - Eo) < 1e-6 * max(1.0, abs(Eo)) * len(s)
+
+
+def test_scaleshift_oracle_matches_definition():
+    """The oracle's ScaleShiftMACE (`model.py:550-589`: e0 + scale x (pair + readouts) +
+    shift per atom) against the plain-MACE terms of the same weights."""
+    s, i, j, S = _two_species_system()
+    cfg = arch_config("medium", num_elements=2, z_table=[8, 14], zbl=True, atomic_energies=[-3.0, 0.5])
+    w = random_init(cfg, 4)
+    sp = np.array([0 if z == 8 else 1 for z in s.numbers])
+    ei = np.stack([i, j])
+    _, ne_plain = OracleMACE(cfg=cfg, weights=w).energy(s.positions, sp, ei, S, s.cell)
+    cfg.model_type = "ScaleShiftMACE"
+    cfg.scale, cfg.shift = 1.3, -0.4
+    _, ne_ss = OracleMACE(cfg=cfg, weights=w).energy(s.positions, sp, ei, S, s.cell)
+    e0 = np.array([-3.0, 0.5])[sp]
+    np.testing.assert_allclose(ne_ss, e0 + 1.3 * (ne_plain - e0) - 0.4, atol=1e-10)
+
+
+def test_head_selection_errors_and_single_head():
+    cfg = _multihead_cfg(["a", "b"])
+    w = random_init(cfg, 0)
+    with pytest.raises(ValueError):
+        build_device_model(cfg, w, head="c")
+    one = arch_config("medium")
+    one.heads = ["Default"]
+    w1 = random_init(one, 0)
+    dm_a = build_device_model(one, w1, head="anything")   # single-head models ignore head
+    dm_b = build_device_model(arch_config("medium"), w1)
+    for k in dm_b.tensors:
+        np.testing.assert_array_equal(dm_a.tensors[k], dm_b.tensors[k])

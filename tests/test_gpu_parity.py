@@ -110,6 +110,24 @@ def test_trained_topology_parity(arch):
     assert_parity(got, case.reference(s, got["sp"], edges, stress=True), len(s), stress=True)
 
 
+@pytest.mark.parametrize("head", ["pbe", "r2scan"])
+def test_multi_head_parity(head):
+    """A two-head ScaleShiftMACE (per-head E0 rows, readout columns, masked non-linear
+    readout, scale / shift lists; `model.py:302-326,508-589`, `blocks.py:553-608`): the
+    engine loaded with one head against the oracle evaluating all heads and selecting."""
+    cfg = arch_config("medium", num_elements=2, z_table=[8, 14], zbl=True,
+                      atomic_energies=[[-3.0, -1.5], [0.5, 0.25]])
+    cfg.heads = ["pbe", "r2scan"]
+    cfg.model_type = "ScaleShiftMACE"
+    cfg.scale, cfg.shift = [1.2, 0.9], [-0.1, 0.3]
+    case = Case(cfg, seed=5, head=head)
+    s = rattle(diamond_si((3, 3, 3)), 0.05, 13)
+    s.numbers = np.where(np.arange(len(s)) % 5 == 0, 8, 14)
+    got = case.run(s, stress=True)
+    edges = case.edges()
+    assert_parity(got, case.reference(s, got["sp"], edges, stress=True), len(s), stress=True)
+
+
 def _fp16_errors(got, ref, n):
     dF = got["F"] - ref["F"]
     rms = float(np.sqrt((ref["F"] ** 2).mean()))
