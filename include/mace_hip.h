@@ -108,6 +108,22 @@ int mace_set_system(mace_ctx* ctx, int32_t n_atoms, const int32_t* species,
 int mace_step(mace_ctx* ctx, const double* positions, uint32_t flags, double* energy,
               double* node_energy, double* forces, double* virial9);
 
+/* A batch of independent structures evaluated in one step: the reference model's
+ * batched call (`model.py:440-484`: positions of all structures, `batch` = structure
+ * index per atom, energies summed per structure by `graph_sum`, `utils.py:35-44`).
+ * Structure g has n_atoms[g] atoms (consecutive in species / positions / forces),
+ * its own cell (cells9 + 9 g) and pbc (pbc3 + 3 g); no edge joins two structures.
+ * mace_set_system is the one-structure case.  mace_step_batch returns
+ *   energies   : n_structures energies (eV)
+ *   virials9   : n_structures x 9, per-structure dE/d(eps_sym) with MACE_STEP_STRESS
+ *                (zeros without), may be NULL
+ * and node_energy / forces over all atoms as mace_step; the total energy and virial
+ * of the batch are what mace_step / mace_step_device report for it. */
+int mace_set_batch(mace_ctx* ctx, int32_t n_structures, const int32_t* n_atoms,
+                   const int32_t* species, const double* cells9, const uint8_t* pbc3, double skin);
+int mace_step_batch(mace_ctx* ctx, const double* positions, uint32_t flags, double* energies,
+                    double* node_energy, double* forces, double* virials9);
+
 /* Test hooks.  mace_set_edges installs an explicit edge list (bypassing the
  * neighbour list until the next mace_set_system); mace_get_edges copies the
  * current list (receiver-sorted) out.  *n_edges returns the count; arrays may be

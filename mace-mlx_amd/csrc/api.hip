@@ -124,6 +124,14 @@ struct mace_ctx {
   uint8_t pbc[3] = {0, 0, 0};
   double skin = 0.5;
   bool system_ready = false;
+  // a batch of G structures (G = 1 for mace_set_system): atoms [gptr[g], gptr[g+1]), each with
+  // its own cell and pbc; cell / pbc above hold structure 0
+  int G = 1;
+  std::vector<int> gptr_h{0, 0};
+  std::vector<double> gcell_h = std::vector<double>(9, 0.0);
+  std::vector<uint8_t> gpbc_h = std::vector<uint8_t>(3, 0);
+  DBuf<int> gptr, gid;
+  DBuf<double> gcell, eg, gvir;  // per-structure cells, energies, virials
   DBuf<int> species;
   DBuf<double> pos;
   double* pos_pinned = nullptr;
@@ -651,19 +659,18 @@ bool invert3(const double* m, double* inv) {
 // Effective cell for the binning: periodic rows are the cell rows; each
 // non-periodic row is replaced by a vector orthogonal to the periodic rows that
 // spans the atoms' extent plus a margin (positions along it are never wrapped).
-NLParams nl_params(mace_ctx* c, const double* pos, double cutoff) {
+NLParams nl_params(const double* cell_in, const uint8_t* pbc, const double* pos, int N, double cutoff) {
   NLParams p{};
   double cell[9];
-  std::memcpy(cell, c->cell, sizeof cell);
-  const int N = c->N;
+  std::memcpy(cell, cell_in, sizeof cell);
   int nper = 0;
-  for (int k = 0; k < 3; ++k) nper += c->pbc[k] ? 1 : 0;
+  for (int k = 0; k < 3; ++k) nper += pbc[k] ? 1 : 0;
   double origin[3] = {0, 0, 0};
   if (nper < 3) {
     // orthonormal directions for the non-periodic axes
     double dirs[3][3];
     std::vector<int> per, non;
-    for (int k = 0; k < 3; ++k) (c->pbc[k] ? per : non).push_back(k);
+    for (int k = 0; k < 3; ++k) (pbc[k] ? per : non).push_back(k);
     if (per.size() == 2) {
       const double* a = cell + 3 * per[0];
       const double* b = cell + 3 * per[1];
@@ -706,7 +713,7 @@ NLParams nl_params(mace_ctx* c, const double* pos, double cutoff) {
   if (!invert3(cell, p.inv)) fail(MACE_ERR_INVALID, "cell is singular for a periodic direction");
   for (int k = 0; k < 3; ++k) {
     p.origin[k] = origin[k];
-    p.periodic[k] = c->pbc[k] ? 1 : 0;
+    p.periodic[k] = pbc[k] ? 1 : 0;
     const double d = plane_spacing(cell, k);
     int nbin = (int)std::floor(d / cutoff);
     nbin = std::max(1, std::min(nbin, 256));
@@ -718,12 +725,23 @@ NLParams nl_params(mace_ctx* c, const double* pos, double cutoff) {
   return p;
 }
 
+// One cell list per structure of the batch (each in its own cell, atoms [gptr[g], gptr[g+1])),
+// bins numbered consecutively across structures so that one sort and one scan serve all.
 void build_nl(mace_ctx* c, const double* pos_host) {
   invalidate_graphs(c);
   const int N = c->N;
+  const int G = c->G;
   const double cutoff = c->dims.r_max + std::max(c->skin, 0.0);
-  NLParams p = nl_params(c, pos_host, cutoff);
-  const int nbins = p.nbin[0] * p.nbin[1] * p.nbin[2];
+  std::vector<NLParams> ps(G);
+  std::vector<int> bin_off(G + 1, 0);
+  for (int g = 0; g < G; ++g) {
+    const int i0 = c->gptr_h[g], n = c->gptr_h[g + 1] - i0;
+    ps[g] = nl_params(c->gcell_h.data() + 9 * g, c->gpbc_h.data() + 3 * g, pos_host + 3 * (size_t)i0, n, cutoff);
+    const int64_t nb = (int64_t)ps[g].nbin[0] * ps[g].nbin[1] * ps[g].nbin[2];
+    if (bin_off[g] + nb > INT32_MAX / 2) fail(MACE_ERR_INVALID, "too many neighbour-list bins");
+    bin_off[g + 1] = bin_off[g] + (int)nb;
+  }
+  const int nbins = bin_off[G];
   c->nl_wpos.ensure(3 * (size_t)N);
   c->nl_img.ensure(3 * (size_t)N);
   c->nl_bin.ensure(N);
@@ -732,13 +750,17 @@ void build_nl(mace_ctx* c, const double* pos_host) {
   c->nl_iota.ensure((size_t)N + 1);
   c->nl_bin_start.ensure((size_t)nbins + 1);
   c->rowptr.ensure((size_t)N + 1);
-  launch_nl_bin(c->stream, N, c->pos.p, p, c->nl_wpos.p, c->nl_img.p, c->nl_bin.p);
+  for (int g = 0; g < G; ++g)
+    launch_nl_bin(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], c->pos.p, ps[g], bin_off[g],
+                  c->nl_wpos.p, c->nl_img.p, c->nl_bin.p);
   launch_fill_iota(c->stream, N, c->nl_iota.p);
   cub_sort_pairs(c, c->nl_bin.p, c->nl_bin_sorted.p, c->nl_iota.p, c->nl_atoms.p, N, nbins);
   build_rowptr(c, c->nl_bin.p, N, nbins, c->nl_bin_start.p);
   c->nl_counts.ensure((size_t)N + 1);
   HIPCHK(hipMemsetAsync(c->nl_counts.p, 0, ((size_t)N + 1) * sizeof(int), c->stream));
-  launch_nl_count(c->stream, N, p, c->nl_wpos.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, c->nl_counts.p);
+  for (int g = 0; g < G; ++g)
+    launch_nl_count(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], ps[g], bin_off[g], c->nl_wpos.p,
+                    c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, c->nl_counts.p);
   // reuse nl_iota as scan output scratch? rowptr directly:
   cub_exclusive_sum(c, c->nl_counts.p, c->rowptr.p, (int64_t)N + 1);
   int Eh = 0;
@@ -746,8 +768,10 @@ void build_nl(mace_ctx* c, const double* pos_host) {
   HIPCHK(hipStreamSynchronize(c->stream));
   c->E = Eh;
   ensure_edge_index(c, c->E);
-  launch_nl_fill(c->stream, N, p, c->nl_wpos.p, c->nl_img.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p,
-                 c->rowptr.p, c->sender.p, c->receiver.p, c->shifts.p);
+  for (int g = 0; g < G; ++g)
+    launch_nl_fill(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], ps[g], bin_off[g], c->nl_wpos.p,
+                   c->nl_img.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, c->rowptr.p, c->sender.p,
+                   c->receiver.p, c->shifts.p);
   build_sender_csr(c);
   ensure_edge_buffers(c, c->E);
   c->nl_pos.assign(pos_host, pos_host + 3 * (size_t)N);
@@ -947,7 +971,8 @@ void forward(mace_ctx* c, const double* pos, double* out) {
   {
     Site s(c, "edge_fwd");
     launch_edge_fwd(st, E, pos, c->sender.p, c->receiver.p, c->shifts.p, c->species.p, c->bessel_w.p, c->zbl_z.p,
-                    c->zbl_cov.p, c->ag_cov.p, fp, c->geom.p, c->Y.p, c->ef.p, c->zbl_e.p);
+                    c->zbl_cov.p, c->ag_cov.p, fp, c->G > 1 ? c->gcell.p : nullptr, c->gid.p, c->geom.p, c->Y.p,
+                    c->ef.p, c->zbl_e.p);
   }
   if (c->mts > 0) {
     Site s(c, "tp_tables");
@@ -1068,6 +1093,10 @@ void forward(mace_ctx* c, const double* pos, double* out) {
   launch_energy_readout(st, N, c->species.p, c->e0.p, c->rowptr.p, c->dims.has_zbl ? c->zbl_e.p : nullptr, L, hs,
                         lds, ros, c->layers[L - 1].ro1.p, c->layers[L - 1].ro2.p, c->gh0.p, c->layers[L - 1].dhid,
                         c->node_e.p, c->e_part.p, out, half);
+  if (c->G > 1) {
+    Site s2(c, "graph_energy");
+    launch_graph_energy(st, c->G, c->gptr.p, c->node_e.p, c->eg.p);
+  }
 }
 
 void backward(mace_ctx* c, bool stress, double* out) {
@@ -1217,6 +1246,10 @@ void backward(mace_ctx* c, bool stress, double* out) {
     Site s(c, "virial");
     launch_virial_reduce(st, c->vir_part.p, (int)((E + 255) / 256), out + 1);
   }
+  if (stress && c->G > 1) {
+    Site s(c, "graph_virial");
+    launch_graph_virial(st, c->G, c->gptr.p, c->rowptr.p, c->geom.p, c->gv.p, c->gvir.p);
+  }
 }
 
 }  // namespace
@@ -1319,25 +1352,58 @@ int mace_model_end(mace_ctx* c) {
   });
 }
 
-int mace_set_system(mace_ctx* c, int32_t n, const int32_t* species, const double* cell9, const uint8_t* pbc3,
-                    double skin) {
-  if (!c) return MACE_ERR_INVALID;
-  return guard(c, [&] {
-    if (!c->model_ready) fail(MACE_ERR_STATE, "model not loaded");
-    if (n < 0 || (n > 0 && !species) || !cell9 || !pbc3) fail(MACE_ERR_INVALID, "bad system arguments");
-    set_device(c);
-    for (int i = 0; i < n; ++i)
-      if (species[i] < 0 || species[i] >= c->dims.num_elements)
-        fail(MACE_ERR_SPECIES, "atom %d: species index %d outside [0, %d)", i, species[i], c->dims.num_elements);
-    bool topo_changed = (n != c->N) || !c->system_ready;
-    for (int k = 0; k < 3; ++k) topo_changed |= ((pbc3[k] != 0) != (c->pbc[k] != 0));
-    for (int k = 0; k < 9; ++k) topo_changed |= std::fabs(cell9[k] - c->cell[k]) > 1e-10;
-    topo_changed |= (skin != c->skin);
-    c->N = n;
-    c->skin = skin;
-    std::memcpy(c->cell, cell9, sizeof c->cell);
-    for (int k = 0; k < 3; ++k) c->pbc[k] = pbc3[k] ? 1 : 0;
-    ensure_node_buffers(c);
+namespace {
+
+// G structures, n_atoms[g] atoms each, concatenated; cells9 [G][9], pbc3 [G][3].
+void set_batch(mace_ctx* c, int32_t G, const int32_t* n_atoms, const int32_t* species, const double* cells9,
+               const uint8_t* pbc3, double skin) {
+  if (!c->model_ready) fail(MACE_ERR_STATE, "model not loaded");
+  if (G < 1 || !n_atoms || !cells9 || !pbc3) fail(MACE_ERR_INVALID, "bad system arguments");
+  std::vector<int> gp(G + 1, 0);
+  for (int g = 0; g < G; ++g) {
+    if (n_atoms[g] < 0) fail(MACE_ERR_INVALID, "structure %d: negative atom count", g);
+    if ((int64_t)gp[g] + n_atoms[g] > INT32_MAX / 4) fail(MACE_ERR_INVALID, "too many atoms");
+    gp[g + 1] = gp[g] + n_atoms[g];
+  }
+  const int n = gp[G];
+  if (n > 0 && !species) fail(MACE_ERR_INVALID, "species is NULL");
+  set_device(c);
+  for (int i = 0; i < n; ++i)
+    if (species[i] < 0 || species[i] >= c->dims.num_elements)
+      fail(MACE_ERR_SPECIES, "atom %d: species index %d outside [0, %d)", i, species[i], c->dims.num_elements);
+  bool topo_changed = (n != c->N) || !c->system_ready || G != c->G || gp != c->gptr_h;
+  if (!topo_changed) {
+    for (int k = 0; k < 3 * G; ++k) topo_changed |= ((pbc3[k] != 0) != (c->gpbc_h[k] != 0));
+    for (int k = 0; k < 9 * G; ++k) topo_changed |= std::fabs(cells9[k] - c->gcell_h[k]) > 1e-10;
+  }
+  topo_changed |= (skin != c->skin);
+  c->N = n;
+  c->skin = skin;
+  c->G = G;
+  c->gptr_h = gp;
+  c->gcell_h.assign(cells9, cells9 + 9 * (size_t)G);
+  c->gpbc_h.resize(3 * (size_t)G);
+  for (int k = 0; k < 3 * G; ++k) c->gpbc_h[k] = pbc3[k] ? 1 : 0;
+  std::memcpy(c->cell, cells9, sizeof c->cell);
+  for (int k = 0; k < 3; ++k) c->pbc[k] = c->gpbc_h[k];
+  // per-structure device arrays (read only when G > 1)
+  std::vector<int> gid(std::max(n, 1), 0);
+  for (int g = 0; g < G; ++g)
+    for (int i = gp[g]; i < gp[g + 1]; ++i) gid[i] = g;
+  const void* before[5] = {c->gptr.p, c->gid.p, c->gcell.p, c->eg.p, c->gvir.p};
+  c->gptr.ensure(G + 1);
+  c->gid.ensure(std::max(n, 1));
+  c->gcell.ensure(9 * (size_t)G);
+  c->eg.ensure(G);
+  c->gvir.ensure(9 * (size_t)G);
+  const void* after[5] = {c->gptr.p, c->gid.p, c->gcell.p, c->eg.p, c->gvir.p};
+  if (std::memcmp(before, after, sizeof before) != 0) invalidate_graphs(c);  // captured steps hold pointers
+  HIPCHK(hipMemcpy(c->gptr.p, gp.data(), (G + 1) * sizeof(int), hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->gid.p, gid.data(), gid.size() * sizeof(int), hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->gcell.p, cells9, 9 * (size_t)G * sizeof(double), hipMemcpyHostToDevice));
+  HIPCHK(hipMemset(c->gvir.p, 0, 9 * (size_t)G * sizeof(double)));
+  ensure_node_buffers(c);
+  {
     c->species.ensure(std::max(n, 1));
     if (n > 0) HIPCHK(hipMemcpy(c->species.p, species, (size_t)n * sizeof(int), hipMemcpyHostToDevice));
     c->species_h.assign(species, species + n);
@@ -1346,7 +1412,24 @@ int mace_set_system(mace_ctx* c, int32_t n, const int32_t* species, const double
       c->edges_manual = false;
     }
     c->system_ready = true;
+  }
+}
+
+}  // namespace
+
+int mace_set_system(mace_ctx* c, int32_t n, const int32_t* species, const double* cell9, const uint8_t* pbc3,
+                    double skin) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    if (n < 0 || (n > 0 && !species) || !cell9 || !pbc3) fail(MACE_ERR_INVALID, "bad system arguments");
+    set_batch(c, 1, &n, species, cell9, pbc3, skin);
   });
+}
+
+int mace_set_batch(mace_ctx* c, int32_t n_structures, const int32_t* n_atoms, const int32_t* species,
+                   const double* cells9, const uint8_t* pbc3, double skin) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] { set_batch(c, n_structures, n_atoms, species, cells9, pbc3, skin); });
 }
 
 int mace_set_edges(mace_ctx* c, int64_t E, const int32_t* sender, const int32_t* receiver, const int32_t* shifts3) {
@@ -1456,6 +1539,33 @@ int mace_step(mace_ctx* c, const double* positions, uint32_t flags, double* ener
     for (int k = 0; k < 4; ++k) c->timings[k] = ms[k];
     if (!c->last_nl) c->timings[1] = 0.0;
     prof_harvest(c);
+  });
+}
+
+int mace_step_batch(mace_ctx* c, const double* positions, uint32_t flags, double* energies, double* node_energy,
+                    double* forces, double* virials9) {
+  if (!c) return MACE_ERR_INVALID;
+  if (!energies) {
+    c->err = "energies is NULL";
+    return MACE_ERR_INVALID;
+  }
+  const bool stress = (flags & MACE_STEP_STRESS) != 0;
+  double e = 0.0, vir[9] = {0};
+  const int rc = mace_step(c, positions, flags, &e, node_energy, forces, stress ? vir : nullptr);
+  if (rc != MACE_OK) return rc;
+  return guard(c, [&] {
+    const int G = c->G;
+    if (G == 1) {
+      energies[0] = e;
+      if (virials9) std::memcpy(virials9, vir, sizeof vir);
+      return;
+    }
+    set_device(c);
+    HIPCHK(hipMemcpy(energies, c->eg.p, G * sizeof(double), hipMemcpyDeviceToHost));
+    if (virials9) {
+      if (stress) HIPCHK(hipMemcpy(virials9, c->gvir.p, 9 * (size_t)G * sizeof(double), hipMemcpyDeviceToHost));
+      else std::fill(virials9, virials9 + 9 * (size_t)G, 0.0);
+    }
   });
 }
 

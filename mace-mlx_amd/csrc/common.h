@@ -76,14 +76,18 @@ __device__ __forceinline__ float max4_rows(float m) {
 void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* sender,
                      const int* receiver, const int* shifts, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov,
-                     const float* ag_cov, const FrontParams& p, EdgeGeom* geom, float* Y, float* ef,
-                     float* zbl_e);
+                     const float* ag_cov, const FrontParams& p, const double* gcell, const int* gid,
+                     EdgeGeom* geom, float* Y, float* ef, float* zbl_e);
 void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov, const float* ag_cov,
                      const FrontParams& p, const EdgeGeom* geom, const float* gY, int gyp, const float* gef, float* gv,
                      double* vir_part);
 // symmetrised virial from the per-block partials of launch_edge_bwd
 void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir);
+// a batch of G structures with atoms [gptr[g], gptr[g+1]): per-structure energies and virials
+void launch_graph_energy(hipStream_t st, int G, const int* gptr, const float* node_e, double* eg);
+void launch_graph_virial(hipStream_t st, int G, const int* gptr, const int* rowptr, const EdgeGeom* geom,
+                         const float* gv, double* vir);
 // density normalisation (blocks.py:372-380): rinv[n] = 1 / (1 + sum_{e -> n} tanh((ef_e . wd)^2))
 void launch_density_fwd(hipStream_t st, int N, const int* rowptr, const float* ef, int nb,
                         const float* wd, float* rinv);
@@ -257,11 +261,12 @@ struct NLParams {
   int range[3];
   double cutoff2;
 };
-void launch_nl_bin(hipStream_t st, int N, const double* pos, const NLParams& p, double* wpos,
-                   int* img, int* bin);
-void launch_nl_count(hipStream_t st, int N, const NLParams& p, const double* wpos,
+// atoms [i0, i0 + n): one structure, its bins numbered from bin_off
+void launch_nl_bin(hipStream_t st, int i0, int n, const double* pos, const NLParams& p, int bin_off,
+                   double* wpos, int* img, int* bin);
+void launch_nl_count(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
                      const int* bin, const int* bin_start, const int* bin_atoms, int* counts);
-void launch_nl_fill(hipStream_t st, int N, const NLParams& p, const double* wpos,
+void launch_nl_fill(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
                     const int* img, const int* bin, const int* bin_start, const int* bin_atoms,
                     const int* rowptr, int* sender, int* receiver, int* shifts);
 void launch_fill_iota(hipStream_t st, int n, int* out);

@@ -72,13 +72,15 @@ __global__ void __launch_bounds__(256) k_edge_fwd(
     int64_t E, const double* __restrict__ pos, const int* __restrict__ sender,
     const int* __restrict__ receiver, const int* __restrict__ shifts, const int* __restrict__ species,
     const float* __restrict__ bessel_w, const float* __restrict__ zbl_z,
-    const float* __restrict__ zbl_cov, const float* __restrict__ ag_cov, FrontParams p, EdgeGeom* __restrict__ geom,
+    const float* __restrict__ zbl_cov, const float* __restrict__ ag_cov, FrontParams p,
+    const double* __restrict__ gcell, const int* __restrict__ gid, EdgeGeom* __restrict__ geom,
     float* __restrict__ Y, float* __restrict__ ef, float* __restrict__ zbl_e) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= E) return;
   const int s = sender[e], r = receiver[e];
   float x, y, z;
-  edge_vec(pos, shifts, p.cell, s, r, e, x, y, z);
+  // a batch of structures: the receiver's structure's cell (gcell [G][9], gid per atom)
+  edge_vec(pos, shifts, gcell ? gcell + 9 * gid[r] : p.cell, s, r, e, x, y, z);
   const float rr = sqrtf(fmaxf(x * x + y * y + z * z, 1e-24f));
   geom[e] = EdgeGeom{x, y, z, rr};
   const float inv = 1.f / rr;
@@ -276,10 +278,12 @@ __device__ __forceinline__ int floordiv(int a, int b) {
   return q;
 }
 
-__global__ void k_nl_bin(int N, const double* __restrict__ pos, NLParams p, double* __restrict__ wpos,
-                         int* __restrict__ img, int* __restrict__ bin) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= N) return;
+// Atoms [i0, i0 + n) form one structure (a batch is a union of structures, each in its own
+// cell); its bins are numbered from bin_off so that all structures share one sorted bin array.
+__global__ void k_nl_bin(int i0, int n, const double* __restrict__ pos, NLParams p, int bin_off,
+                         double* __restrict__ wpos, int* __restrict__ img, int* __restrict__ bin) {
+  if ((int)(blockIdx.x * blockDim.x + threadIdx.x) >= n) return;
+  const int i = i0 + blockIdx.x * blockDim.x + threadIdx.x;
   const double d0 = pos[3 * i] - p.origin[0], d1 = pos[3 * i + 1] - p.origin[1],
                d2 = pos[3 * i + 2] - p.origin[2];
   double f[3], w[3];
@@ -304,7 +308,7 @@ __global__ void k_nl_bin(int N, const double* __restrict__ pos, NLParams p, doub
   }
   for (int k = 0; k < 3; ++k)
     wpos[3 * i + k] = w[0] * p.cell[0 * 3 + k] + w[1] * p.cell[1 * 3 + k] + w[2] * p.cell[2 * 3 + k];
-  bin[i] = (b[0] * p.nbin[1] + b[1]) * p.nbin[2] + b[2];
+  bin[i] = bin_off + (b[0] * p.nbin[1] + b[1]) * p.nbin[2] + b[2];
 }
 
 // One wave per receiver atom j: the wave walks j's neighbour cells in a fixed
@@ -313,14 +317,14 @@ __global__ void k_nl_bin(int N, const double* __restrict__ pos, NLParams p, doub
 // count plus its rank among the hit lanes, so the edge order (cell order, then
 // position in the cell) is deterministic and identical in both passes.
 template <bool FILL>
-__device__ __forceinline__ int nl_visit(int j, const NLParams& p, const double* __restrict__ wpos,
+__device__ __forceinline__ int nl_visit(int j, const NLParams& p, int bin_off, const double* __restrict__ wpos,
                                         const int* __restrict__ img, const int* __restrict__ bin,
                                         const int* __restrict__ bin_start,
                                         const int* __restrict__ bin_atoms, int out0,
                                         int* __restrict__ sender, int* __restrict__ receiver,
                                         int* __restrict__ shifts) {
   const int lane = __lane_id();
-  const int bj = bin[j];
+  const int bj = bin[j] - bin_off;
   const int b2 = bj % p.nbin[2], b1 = (bj / p.nbin[2]) % p.nbin[1], b0 = bj / (p.nbin[2] * p.nbin[1]);
   const double xj = wpos[3 * j], yj = wpos[3 * j + 1], zj = wpos[3 * j + 2];
   int cnt = 0;
@@ -339,7 +343,7 @@ __device__ __forceinline__ int nl_visit(int j, const NLParams& p, const double* 
         const double tx = T0 * p.cell[0] + T1 * p.cell[3] + T2 * p.cell[6];
         const double ty = T0 * p.cell[1] + T1 * p.cell[4] + T2 * p.cell[7];
         const double tz = T0 * p.cell[2] + T1 * p.cell[5] + T2 * p.cell[8];
-        const int cb = (c0 * p.nbin[1] + c1) * p.nbin[2] + c2;
+        const int cb = bin_off + (c0 * p.nbin[1] + c1) * p.nbin[2] + c2;
         const int qe = bin_start[cb + 1];
         for (int q0 = bin_start[cb]; q0 < qe; q0 += 64) {
           const int q = q0 + lane;
@@ -373,24 +377,27 @@ __device__ __forceinline__ int nl_visit(int j, const NLParams& p, const double* 
 }
 
 // four receiver atoms per 256-thread block, one wave each
-__global__ void __launch_bounds__(256) k_nl_count(int N, NLParams p, const double* __restrict__ wpos,
+__global__ void __launch_bounds__(256) k_nl_count(int i0, int n, NLParams p, int bin_off,
+                                                  const double* __restrict__ wpos,
                                                   const int* __restrict__ bin, const int* __restrict__ bin_start,
                                                   const int* __restrict__ bin_atoms, int* __restrict__ counts) {
-  const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (j >= N) return;
-  const int c = nl_visit<false>(j, p, wpos, nullptr, bin, bin_start, bin_atoms, 0, nullptr, nullptr, nullptr);
+  if ((int)(blockIdx.x * 4 + (threadIdx.x >> 6)) >= n) return;
+  const int j = i0 + blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int c = nl_visit<false>(j, p, bin_off, wpos, nullptr, bin, bin_start, bin_atoms, 0, nullptr, nullptr,
+                                nullptr);
   if (__lane_id() == 0) counts[j] = c;
 }
 
-__global__ void __launch_bounds__(256) k_nl_fill(int N, NLParams p, const double* __restrict__ wpos,
+__global__ void __launch_bounds__(256) k_nl_fill(int i0, int n, NLParams p, int bin_off,
+                                                 const double* __restrict__ wpos,
                                                  const int* __restrict__ img, const int* __restrict__ bin,
                                                  const int* __restrict__ bin_start,
                                                  const int* __restrict__ bin_atoms, const int* __restrict__ rowptr,
                                                  int* __restrict__ sender, int* __restrict__ receiver,
                                                  int* __restrict__ shifts) {
-  const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (j >= N) return;
-  nl_visit<true>(j, p, wpos, img, bin, bin_start, bin_atoms, rowptr[j], sender, receiver, shifts);
+  if ((int)(blockIdx.x * 4 + (threadIdx.x >> 6)) >= n) return;
+  const int j = i0 + blockIdx.x * 4 + (threadIdx.x >> 6);
+  nl_visit<true>(j, p, bin_off, wpos, img, bin, bin_start, bin_atoms, rowptr[j], sender, receiver, shifts);
 }
 
 __global__ void k_iota(int n, int* out) {
@@ -409,11 +416,11 @@ static inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / 
 
 void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* sender, const int* receiver,
                      const int* shifts, const int* species, const float* bessel_w, const float* zbl_z,
-                     const float* zbl_cov, const float* ag_cov, const FrontParams& p, EdgeGeom* geom, float* Y,
-                     float* ef, float* zbl_e) {
+                     const float* zbl_cov, const float* ag_cov, const FrontParams& p, const double* gcell,
+                     const int* gid, EdgeGeom* geom, float* Y, float* ef, float* zbl_e) {
   if (E <= 0) return;
   hipLaunchKernelGGL(k_edge_fwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, pos, sender, receiver, shifts,
-                     species, bessel_w, zbl_z, zbl_cov, ag_cov, p, geom, Y, ef, zbl_e);
+                     species, bessel_w, zbl_z, zbl_cov, ag_cov, p, gcell, gid, geom, Y, ef, zbl_e);
 }
 
 void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,
@@ -443,24 +450,24 @@ void launch_density_edge_bwd(hipStream_t st, int64_t E, const int* receiver, con
   hipLaunchKernelGGL(k_density_edge_bwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, receiver, ef, nb, wd, grho, gef);
 }
 
-void launch_nl_bin(hipStream_t st, int N, const double* pos, const NLParams& p, double* wpos, int* img,
-                   int* bin) {
-  if (N <= 0) return;
-  hipLaunchKernelGGL(k_nl_bin, dim3(nblk(N, 256)), dim3(256), 0, st, N, pos, p, wpos, img, bin);
+void launch_nl_bin(hipStream_t st, int i0, int n, const double* pos, const NLParams& p, int bin_off, double* wpos,
+                   int* img, int* bin) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_nl_bin, dim3(nblk(n, 256)), dim3(256), 0, st, i0, n, pos, p, bin_off, wpos, img, bin);
 }
 
-void launch_nl_count(hipStream_t st, int N, const NLParams& p, const double* wpos, const int* bin,
-                     const int* bin_start, const int* bin_atoms, int* counts) {
-  if (N <= 0) return;
-  hipLaunchKernelGGL(k_nl_count, dim3(nblk(N, 4)), dim3(256), 0, st, N, p, wpos, bin, bin_start, bin_atoms,
-                     counts);
+void launch_nl_count(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
+                     const int* bin, const int* bin_start, const int* bin_atoms, int* counts) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_nl_count, dim3(nblk(n, 4)), dim3(256), 0, st, i0, n, p, bin_off, wpos, bin, bin_start,
+                     bin_atoms, counts);
 }
 
-void launch_nl_fill(hipStream_t st, int N, const NLParams& p, const double* wpos, const int* img,
-                    const int* bin, const int* bin_start, const int* bin_atoms, const int* rowptr,
+void launch_nl_fill(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
+                    const int* img, const int* bin, const int* bin_start, const int* bin_atoms, const int* rowptr,
                     int* sender, int* receiver, int* shifts) {
-  if (N <= 0) return;
-  hipLaunchKernelGGL(k_nl_fill, dim3(nblk(N, 4)), dim3(256), 0, st, N, p, wpos, img, bin, bin_start,
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_nl_fill, dim3(nblk(n, 4)), dim3(256), 0, st, i0, n, p, bin_off, wpos, img, bin, bin_start,
                      bin_atoms, rowptr, sender, receiver, shifts);
 }
 

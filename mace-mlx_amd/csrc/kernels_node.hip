@@ -606,9 +606,59 @@ __global__ void __launch_bounds__(256) k_virial_reduce(const double* __restrict_
   }
 }
 
+// A batch of structures (graph_sum, utils.py:35-44): block g sums the node energies of
+// structure g's atoms [gptr[g], gptr[g+1]) in a fixed order -- the same float node energies
+// the total is summed from.
+__global__ void __launch_bounds__(256) k_graph_energy(const int* __restrict__ gptr, const float* __restrict__ node_e,
+                                                      double* __restrict__ eg) {
+  const int g = blockIdx.x;
+  double a = 0.0;
+  for (int i = gptr[g] + threadIdx.x; i < gptr[g + 1]; i += 256) a += (double)node_e[i];
+  const double t = block_sum_fixed(a);
+  if (threadIdx.x == 0) eg[g] = t;
+}
+
+// Per-structure virial: structure g's edges are the receiver-CSR range of its atoms; the same
+// products v_e[a] g_e[b] as k_edge_bwd's partials, summed in a fixed order and symmetrised.
+__global__ void __launch_bounds__(256) k_graph_virial(const int* __restrict__ gptr, const int* __restrict__ rowptr,
+                                                      const EdgeGeom* __restrict__ geom, const float* __restrict__ gv,
+                                                      double* __restrict__ vir) {
+  const int g = blockIdx.x;
+  const int e0 = rowptr[gptr[g]], e1 = rowptr[gptr[g + 1]];
+  double G[9];
+#pragma unroll
+  for (int k = 0; k < 9; ++k) G[k] = 0.0;
+  for (int e = e0 + threadIdx.x; e < e1; e += 256) {
+    const EdgeGeom q = geom[e];
+    const double v[3] = {q.x, q.y, q.z};
+    const double d[3] = {gv[3 * e], gv[3 * e + 1], gv[3 * e + 2]};
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int b = 0; b < 3; ++b) G[3 * a + b] += v[a] * d[b];
+  }
+#pragma unroll
+  for (int k = 0; k < 9; ++k) G[k] = block_sum_fixed(G[k]);
+  if (threadIdx.x < 9) {
+    const int r = threadIdx.x / 3, c = threadIdx.x % 3;
+    vir[9 * g + threadIdx.x] = 0.5 * (G[3 * r + c] + G[3 * c + r]);
+  }
+}
+
 }  // namespace
 
 static inline unsigned cdiv(int64_t a, int b) { return (unsigned)((a + b - 1) / b); }
+
+void launch_graph_energy(hipStream_t st, int G, const int* gptr, const float* node_e, double* eg) {
+  if (G <= 0) return;
+  hipLaunchKernelGGL(k_graph_energy, dim3(G), dim3(256), 0, st, gptr, node_e, eg);
+}
+
+void launch_graph_virial(hipStream_t st, int G, const int* gptr, const int* rowptr, const EdgeGeom* geom,
+                         const float* gv, double* vir) {
+  if (G <= 0) return;
+  hipLaunchKernelGGL(k_graph_virial, dim3(G), dim3(256), 0, st, gptr, rowptr, geom, gv, vir);
+}
 
 void launch_linear(hipStream_t st, int N, const LinearDesc& d, const float* X, const float* W, float* Y) {
   const int rows = N * d.d;

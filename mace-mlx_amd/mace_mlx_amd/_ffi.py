@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "mace_set_graphs",
     "mace_set_split_products",
     "mace_set_fused_tp",
+    "mace_set_batch", "mace_step_batch",
 )
 
 
@@ -90,6 +91,8 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
         "mace_set_graphs": (ctypes.c_int, [P, I32]),
         "mace_set_split_products": (ctypes.c_int, [P, I32]),
         "mace_set_fused_tp": (ctypes.c_int, [P, I32]),
+        "mace_set_batch": (ctypes.c_int, [P, I32, P, P, P, P, D]),
+        "mace_step_batch": (ctypes.c_int, [P, P, U32, P, P, P, P]),
         "mace_get_kernel_times": (ctypes.c_int, [P, ctypes.c_char_p, I64, P, P, I32, ctypes.POINTER(I32)]),
     }
     for name, (res, args) in sig.items():
@@ -167,6 +170,7 @@ class Engine:
         pb = np.ascontiguousarray(np.asarray(pbc, dtype=bool).reshape(3).astype(np.uint8))
         self._check(self._lib.mace_set_system(self._h, len(sp), _ptr(sp), _ptr(cl), _ptr(pb), float(skin)))
         self.n_atoms = len(sp)
+        self.batch_sizes = np.array([len(sp)], dtype=np.int32)
 
     def step(self, positions: np.ndarray, stress: bool = False, force_nl: bool = False,
              node_energy: bool = True) -> Tuple[float, Optional[np.ndarray], np.ndarray, Optional[np.ndarray]]:
@@ -180,6 +184,36 @@ class Engine:
         flags = STEP_FORCES | (STEP_STRESS if stress else 0) | (STEP_FORCE_NL if force_nl else 0)
         self._check(self._lib.mace_step(self._h, _ptr(pos), flags, ctypes.byref(e), _ptr(ne), _ptr(f), _ptr(v)))
         return e.value, ne, f, v
+
+    # -- batches of structures (model.py:440-484 with `batch`, utils.py:35-44) ---
+    def set_batch(self, species_list, cells, pbcs, skin: float) -> None:
+        """Structures g = 0..G-1 (species arrays, 3x3 cells, pbc triples) evaluated together."""
+        sizes = np.array([len(sp) for sp in species_list], dtype=np.int32)
+        if len(sizes) == 0:
+            raise ValueError("empty batch")
+        sp = np.ascontiguousarray(np.concatenate([np.asarray(x, dtype=np.int32).reshape(-1) for x in species_list]),
+                                  dtype=np.int32)
+        cl = np.ascontiguousarray(np.asarray(cells, dtype=np.float64).reshape(len(sizes), 9))
+        pb = np.ascontiguousarray(np.asarray(pbcs, dtype=bool).reshape(len(sizes), 3).astype(np.uint8))
+        self._check(self._lib.mace_set_batch(self._h, len(sizes), _ptr(sizes), _ptr(sp), _ptr(cl), _ptr(pb),
+                                             float(skin)))
+        self.n_atoms = int(sizes.sum())
+        self.batch_sizes = sizes
+
+    def step_batch(self, positions, stress: bool = False, force_nl: bool = False):
+        """(energies [G], node_energy [N], forces [N, 3], virials [G, 3, 3] or None) of the batch;
+        ``positions`` are the structures' positions concatenated in batch order."""
+        pos = np.ascontiguousarray(positions, dtype=np.float64).reshape(-1, 3)
+        if len(pos) != self.n_atoms:
+            raise ValueError(f"positions has {len(pos)} atoms, batch has {self.n_atoms}")
+        G = len(self.batch_sizes)
+        eg = np.empty(G, dtype=np.float64)
+        ne = np.empty(self.n_atoms, dtype=np.float64)
+        f = np.empty((self.n_atoms, 3), dtype=np.float64)
+        v = np.empty((G, 3, 3), dtype=np.float64) if stress else None
+        flags = STEP_FORCES | (STEP_STRESS if stress else 0) | (STEP_FORCE_NL if force_nl else 0)
+        self._check(self._lib.mace_step_batch(self._h, _ptr(pos), flags, _ptr(eg), _ptr(ne), _ptr(f), _ptr(v)))
+        return eg, ne, f, v
 
     # -- test hooks -----------------------------------------------------------
     def set_edges(self, sender, receiver, shifts) -> None:

@@ -209,6 +209,35 @@ class MACEHIPCalculator(_AseCalculator):
             st = vir / vol
             self.results["stress"] = st[[0, 1, 2, 1, 0, 0], [0, 1, 2, 2, 2, 1]]
 
+    def calculate_batch(self, atoms_list, properties=("energy", "forces")):
+        """Several structures in one engine step: the reference model's batched call
+        (`model.py:440-484` with `batch` / `num_graphs`; energies per structure by
+        `graph_sum`, `utils.py:35-44`), each structure in its own cell.  Returns one dict per
+        structure with the keys `calculate` fills (stress only for 3-D periodic cells when
+        requested); the calculator's own `results` are left alone."""
+        atoms_list = list(atoms_list)
+        if not atoms_list:
+            return []
+        species = [self._species(a) for a in atoms_list]
+        cells = np.stack([np.asarray(a.get_cell(), dtype=np.float64).reshape(3, 3) for a in atoms_list])
+        pbcs = np.stack([_pbc(a) for a in atoms_list])
+        self._engine.set_batch(species, cells, pbcs, self._skin)
+        self._sys_key = None   # the engine now holds the batch; calculate() re-uploads its system
+        stress = "stress" in properties
+        pos = np.concatenate([np.asarray(a.get_positions(), dtype=np.float64).reshape(-1, 3) for a in atoms_list])
+        eg, ne, f, vir = self._engine.step_batch(pos, stress=stress)
+        out, i0 = [], 0
+        for g, a in enumerate(atoms_list):
+            n = len(species[g])
+            r = {"energy": float(eg[g]), "free_energy": float(eg[g]), "forces": f[i0:i0 + n],
+                 "node_energy": ne[i0:i0 + n], "energies": ne[i0:i0 + n]}
+            if stress and _cell_rank(a) == 3:
+                st = vir[g] / abs(np.linalg.det(cells[g]))
+                r["stress"] = st[[0, 1, 2, 1, 0, 0], [0, 1, 2, 2, 2, 1]]
+            out.append(r)
+            i0 += n
+        return out
+
     # timing of the last step on the device (ms): total, neighbour list, forward, backward
     def last_timings(self) -> np.ndarray:
         return self._engine.timings()

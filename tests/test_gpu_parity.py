@@ -292,6 +292,40 @@ def test_skin_cache(medium_zbl):
     assert edge_set(*medium_zbl.edges()) == bruteforce_edges(far)
 
 
+def test_batch_of_structures(medium_zbl):
+    """Several structures in one step (the reference model's batched call, `model.py:440-484`,
+    energies per structure by `graph_sum`, `utils.py:35-44`), each in its own cell: a
+    triclinic cell, a molecule, a slab and a rattled Si64.  Per-structure energies, virials,
+    forces and edge lists equal those of separate steps of the same engine, no edge joins two
+    structures, and every structure meets the oracle tolerances."""
+    case = medium_zbl
+    structs = [_triclinic(), _molecule(), _slab(), rattle(diamond_si((2, 2, 2)), 0.03, 21)]
+    sps = [species_of(case.dm, s.numbers) for s in structs]
+    case.eng.set_batch(sps, [s.cell for s in structs], [s.pbc for s in structs], 0.5)
+    eg, ne, F, vir = case.eng.step_batch(np.concatenate([s.positions for s in structs]), stress=True)
+    bs, br, bS = case.edges()
+    offs = np.cumsum([0] + [len(s) for s in structs])
+    assert np.array_equal(np.searchsorted(offs, bs, side="right"), np.searchsorted(offs, br, side="right"))
+    for g, s in enumerate(structs):
+        a, b = offs[g], offs[g + 1]
+        m = (br >= a) & (br < b)
+        edges_g = (bs[m] - a, br[m] - a, bS[m])
+        got = case.run(s, stress=True)
+        assert edge_set(*edges_g) == edge_set(*case.edges())
+        n = len(s)
+        dE = abs(eg[g] - got["E"])
+        dF = float(np.abs(F[a:b] - got["F"]).max())
+        dV = float(np.abs(vir[g] - got["vir"]).max())
+        print(f"structure {g}: batch vs single dE={dE:.2e} dF={dF:.2e} dvir={dV:.2e}")
+        assert dE <= 1e-10 * max(abs(got["E"]), n)
+        assert dF <= 1e-7
+        assert dV <= 1e-9 * max(1.0, float(np.abs(got["vir"]).max()))
+        np.testing.assert_allclose(ne[a:b], got["ne"], rtol=0, atol=1e-7)
+        per = bool(s.pbc.all())
+        ref = case.reference(s, sps[g], edges_g, stress=per)
+        assert_parity(dict(E=eg[g], F=F[a:b], ne=ne[a:b], vir=vir[g]), ref, n, stress=per)
+
+
 def test_isolated_atoms_and_no_edges(small):
     one = System(np.zeros((1, 3)), np.array([14]), np.eye(3) * 30.0, np.array([True, True, True]))
     a = small.run(one, stress=True)
@@ -345,6 +379,14 @@ def test_calculator_end_to_end(tmp_path):
     bad.numbers[0] = 8
     with pytest.raises(ValueError):
         calc.calculate(bad, ["energy"])
+    # several structures in one step, then a single one again
+    small = rattle(diamond_si((2, 2, 2)), 0.03, 5)
+    res = calc.calculate_batch([s, small], ["energy", "forces", "stress"])
+    assert abs(res[0]["energy"] - r["energy"]) <= 1e-9 * abs(r["energy"])
+    np.testing.assert_allclose(res[0]["forces"], r["forces"], rtol=0, atol=1e-7)
+    calc.calculate(small, ["energy", "forces", "stress"])
+    assert abs(res[1]["energy"] - calc.results["energy"]) <= 1e-9 * abs(calc.results["energy"])
+    np.testing.assert_allclose(res[1]["stress"], calc.results["stress"], rtol=0, atol=1e-9)
 
 
 def test_graph_replay_matches_eager(medium_zbl):
