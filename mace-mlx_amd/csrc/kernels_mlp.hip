@@ -930,10 +930,22 @@ __device__ __forceinline__ float edge_scale(const float* v, float* inv) {
   return __uint_as_float((unsigned)(127 + 14 - ex) << 23);
 }
 
+// The lane index, with OPQ through an empty asm statement: weight-fragment reads indexed by it
+// stay inside the edge-group loops.  Hoisted out of the loop, the six layers' fragments of the
+// recomputing VJP hold ~300 VGPRs and leave one wave per SIMD (measured: 29 -> 26 us per
+// launch un-hoisted); the forward's three layers are faster hoisted (97 -> 240 VGPRs).
+template <bool OPQ>
+__device__ __forceinline__ int lane_opaque() {
+  int l = threadIdx.x & 63;
+  if constexpr (OPQ) asm volatile("" : "+v"(l));
+  return l;
+}
+
 // one 64-wide layer from the lane's 16 values v (all four output tiles t'):
 // acc[t'] = (A_t' x v) with A = tile image w[c][t'][hi, lo][lane], times winv
+template <bool OPQ>
 __device__ __forceinline__ void layer64x(const h8 (*w)[4][2][64], const float* v, float winv, f4v* acc) {
-  const int l = threadIdx.x & 63;
+  const int l = lane_opaque<OPQ>();
   float inv;
   const float sc = edge_scale<16>(v, &inv);
   inv *= winv;
@@ -965,6 +977,7 @@ __device__ __forceinline__ void layer64x(const h8 (*w)[4][2][64], const float* v
 // forward of the split kernels: first layer over the Bessel features, then two 64-wide
 // layers; dsp as in hidden_fwd; leaves a1, a2, a3 (the VJP recomputes them this
 // way, with the same instructions, instead of reading saved derivatives)
+template <bool OPQ>
 __device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* winv, int64_t E, int64_t e0, int nb,
                                              const float* __restrict__ ef, f4v* a1, f4v* a2, f4v* a3, float* dsp) {
   const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
@@ -987,9 +1000,10 @@ __device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* win
       xh[j] = hi;
       xl[j] = lo;
     }
+    const int lo = lane_opaque<OPQ>();
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const h8 wh = sw.w0[t][0][l], wl = sw.w0[t][1][l];
+      const h8 wh = sw.w0[t][0][lo], wl = sw.w0[t][1][lo];
       f4v d = mfma16h(wl, xh, f4v{0.f, 0.f, 0.f, 0.f});
       d = mfma16h(wh, xl, d);
       d = mfma16h(wh, xh, d);
@@ -1000,11 +1014,11 @@ __device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* win
 #pragma unroll
   for (int q = 0; q < 16; ++q) v[q] = silu(a1[q >> 2][q & 3]);
   if (dsp) store_ds(dsp, a1);
-  layer64x(sw.w1, v, winv[1], a2);
+  layer64x<OPQ>(sw.w1, v, winv[1], a2);
 #pragma unroll
   for (int q = 0; q < 16; ++q) v[q] = silu(a2[q >> 2][q & 3]);
   if (dsp) store_ds(dsp + H, a2);
-  layer64x(sw.w2, v, winv[2], a3);
+  layer64x<OPQ>(sw.w2, v, winv[2], a3);
   if (dsp) store_ds(dsp + 2 * H, a3);
 }
 
@@ -1012,8 +1026,13 @@ struct MlpWinv {
   float w[3];
 };
 
+// waves per block of the split hidden-layer kernels (forward; recomputing VJP; measured: six-wave
+// VJP blocks, three waves per SIMD, are slower than four-wave ones, 27.6 vs 25.9 us)
+constexpr int kHidFwdWaves = 4;
+constexpr int kHidBwdWaves = 4;
+
 // h3 as split pairs [E][2][64] + h3inv (H3_SPLIT layout) and silu' saved in ds
-__global__ void __launch_bounds__(256) k_mlp_hidden_x(int64_t E, int nb, const float* __restrict__ ef,
+__global__ void __launch_bounds__(64 * kHidFwdWaves) k_mlp_hidden_x(int64_t E, int nb, const float* __restrict__ ef,
                                                       const MlpFwdX* __restrict__ tiles, MlpWinv wi,
                                                       _Float16* __restrict__ h3x, float* __restrict__ h3inv,
                                                       float* __restrict__ ds) {
@@ -1022,10 +1041,10 @@ __global__ void __launch_bounds__(256) k_mlp_hidden_x(int64_t E, int nb, const f
   __syncthreads();
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t ngroups = (E + 15) / 16;
-  for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
+  for (int64_t gi = (int64_t)blockIdx.x * kHidFwdWaves + wv; gi < ngroups; gi += (int64_t)gridDim.x * kHidFwdWaves) {
     const int64_t e0 = gi * 16, e = e0 + r;
     f4v a1[4], a2[4], a3[4];
-    hidden_fwd_x(sw, wi.w, E, e0, nb, ef, a1, a2, a3, (ds && e < E) ? ds + e * 3 * H + 4 * g : nullptr);
+    hidden_fwd_x<false>(sw, wi.w, E, e0, nb, ef, a1, a2, a3, (ds && e < E) ? ds + e * 3 * H + 4 * g : nullptr);
     float v[16];
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = silu(a3[q >> 2][q & 3]);
@@ -1054,8 +1073,8 @@ __global__ void __launch_bounds__(256) k_mlp_hidden_x(int64_t E, int nb, const f
 // gh3: np partials [np][E][64] (stride pstride floats), added in order.  RECOMP:
 // silu'(a1..a3) from the forward layers recomputed from ef (tiles ftiles) instead
 // of read from ds.
-template <bool RECOMP>
-__global__ void __launch_bounds__(256) k_mlp_hidden_bwd_x(int64_t E, int nb, const MlpFwdX* __restrict__ ftiles,
+template <bool RECOMP, int NW>
+__global__ void __launch_bounds__(64 * NW) k_mlp_hidden_bwd_x(int64_t E, int nb, const MlpFwdX* __restrict__ ftiles,
                                                           const MlpBwdX* __restrict__ tiles, MlpWinv wi,
                                                           const float* __restrict__ ef, const float* __restrict__ ds,
                                                           const float* __restrict__ gh3, int np, int64_t pstride,
@@ -1068,12 +1087,12 @@ __global__ void __launch_bounds__(256) k_mlp_hidden_bwd_x(int64_t E, int nb, con
   __syncthreads();
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t ngroups = (E + 15) / 16;
-  for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
+  for (int64_t gi = (int64_t)blockIdx.x * NW + wv; gi < ngroups; gi += (int64_t)gridDim.x * NW) {
     const int64_t e0 = gi * 16, e = e0 + r, ec = e < E ? e : E - 1;  // rows past the end: computed, not stored
     float v[16], dv[16];
     f4v acc[4];
     f4v a1[4], a2[4], a3[4];  // RECOMP: the pre-activations, rebuilt
-    if constexpr (RECOMP) hidden_fwd_x(swf, wi.w, E, e0, nb, ef, a1, a2, a3, nullptr);
+    if constexpr (RECOMP) hidden_fwd_x<true>(swf, wi.w, E, e0, nb, ef, a1, a2, a3, nullptr);
     // silu' of layer k's pre-activations in the lane's layout (feature 16t + 4g + i -> [4t + i])
     auto dsl = [&](int k, float* out) {
       if constexpr (RECOMP) {
@@ -1094,11 +1113,11 @@ __global__ void __launch_bounds__(256) k_mlp_hidden_bwd_x(int64_t E, int nb, con
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] *= dv[q];
     dsl(1, dv);
-    layer64x(sw.w2T, v, wi.w[2], acc);
+    layer64x<RECOMP>(sw.w2T, v, wi.w[2], acc);
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = acc[q >> 2][q & 3] * dv[q];
     dsl(0, dv);
-    layer64x(sw.w1T, v, wi.w[1], acc);
+    layer64x<RECOMP>(sw.w1T, v, wi.w[1], acc);
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = acc[q >> 2][q & 3] * dv[q];
     // g_ef = g_a1 W0^T: one output tile (rows k < nb)
@@ -1116,7 +1135,8 @@ __global__ void __launch_bounds__(256) k_mlp_hidden_bwd_x(int64_t E, int nb, con
         xh[j] = hi;
         xl[j] = lo;
       }
-      const h8 wh = sw.w0T[c][0][l], wl = sw.w0T[c][1][l];
+      const int lo = lane_opaque<RECOMP>();
+      const h8 wh = sw.w0T[c][0][lo], wl = sw.w0T[c][1][lo];
       o = mfma16h(wl, xh, o);
       o = mfma16h(wh, xl, o);
       o = mfma16h(wh, xh, o);
@@ -1140,10 +1160,14 @@ inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
 
 // grid of the hidden-layer kernels: enough blocks to fill the device, each
 // staging the weights once and walking several 64-edge groups
-inline unsigned hidden_grid(int64_t E) { return (unsigned)std::min<int64_t>((E + 63) / 64, 512); }
-// the VJP stages both tile images (76 KB) and holds three layers' pre-activations: one
-// block per CU, several 16-edge groups per wave (measured 10% faster than the forward's grid)
-inline unsigned hidden_bwd_grid(int64_t E) { return (unsigned)std::min<int64_t>((E + 63) / 64, 256); }
+inline unsigned hidden_grid(int64_t E) {
+  return (unsigned)std::min<int64_t>((E + 16 * kHidFwdWaves - 1) / (16 * kHidFwdWaves), 512);
+}
+// the recomputing VJP stages both tile images (76 KB): two blocks per CU, one 16-edge group or a
+// few per wave
+inline unsigned hidden_bwd_grid(int64_t E) {
+  return (unsigned)std::min<int64_t>((E + 16 * kHidBwdWaves - 1) / (16 * kHidBwdWaves), 512);
+}
 
 size_t mlp_tile_bytes() { return sizeof(MlpFwdW) + sizeof(MlpBwdW); }
 size_t mlp_tile_x_bytes() { return sizeof(MlpFwdX) + sizeof(MlpBwdX); }
@@ -1160,7 +1184,7 @@ void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, con
                          const float* winv3, void* h3x, float* h3inv, float* ds) {
   if (E <= 0) return;
   MlpWinv wi{{winv3[0], winv3[1], winv3[2]}};
-  hipLaunchKernelGGL(k_mlp_hidden_x, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef,
+  hipLaunchKernelGGL(k_mlp_hidden_x, dim3(hidden_grid(E)), dim3(64 * kHidFwdWaves), 0, st, E, nb, ef,
                      static_cast<const MlpFwdX*>(tiles), wi, static_cast<_Float16*>(h3x), h3inv, ds);
 }
 
@@ -1171,10 +1195,11 @@ void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tile
   const MlpFwdX* fw = static_cast<const MlpFwdX*>(tiles);
   const MlpBwdX* bw = reinterpret_cast<const MlpBwdX*>(static_cast<const char*>(tiles) + sizeof(MlpFwdX));
   if (ds)
-    hipLaunchKernelGGL(k_mlp_hidden_bwd_x<false>, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, fw, bw, wi, ef, ds,
+    hipLaunchKernelGGL((k_mlp_hidden_bwd_x<false, 4>), dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, fw, bw, wi, ef, ds,
                        gh3, np, E * H, gef, accumulate);
   else
-    hipLaunchKernelGGL(k_mlp_hidden_bwd_x<true>, dim3(hidden_bwd_grid(E)), dim3(256), 0, st, E, nb, fw, bw, wi, ef,
+    hipLaunchKernelGGL((k_mlp_hidden_bwd_x<true, kHidBwdWaves>), dim3(hidden_bwd_grid(E)), dim3(64 * kHidBwdWaves), 0,
+                       st, E, nb, fw, bw, wi, ef,
                        ds, gh3, np, E * H, gef, accumulate);
 }
 
