@@ -164,6 +164,7 @@ struct mace_ctx {
   hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
   double timings[4] = {0, 0, 0, 0};
   bool last_nl = false;
+  bool embed_valid = false;  // h0 / first h_up written for the current species and buffers
   // captured step graphs (forward, backward) and what they were captured for
   struct StepGraph {
     hipGraphExec_t exec = nullptr;
@@ -922,6 +923,18 @@ void invalidate_graphs(mace_ctx* c) {
     if (g->exec) (void)hipGraphExecDestroy(g->exec);
     *g = mace_ctx::StepGraph{};
   }
+  c->embed_valid = false;  // every model / system / buffer change comes through here
+}
+
+// First-layer node features h0 and the first linear_up output: functions of the species
+// only (the embedding is stop_gradient'ed, model.py:382), so they are written once per
+// system / model / buffer set, before the step, not by every step.
+void ensure_embed(mace_ctx* c) {
+  if (c->embed_valid) return;
+  Site s(c, "embed");
+  launch_embed(c->stream, c->N, c->species.p, c->embed.p, c->layers[0].din, c->h[0].p, c->dims.feature_half != 0,
+               c->up0_tab.p, c->layers[0].h_up.p);
+  c->embed_valid = true;
 }
 
 // Run body() (a sequence of launches on c->stream) through a graph captured
@@ -977,11 +990,6 @@ void forward(mace_ctx* c, const double* pos, double* out) {
   if (c->mts > 0) {
     Site s(c, "tp_tables");
     launch_tp_tables(st, E, c->max_lin, c->Y.p, c->Mt.p, c->mts);
-  }
-  {
-    Site s(c, "embed");
-    launch_embed(st, N, c->species.p, c->embed.p, c->layers[0].din, c->h[0].p, half, c->up0_tab.p,
-                 c->layers[0].h_up.p);
   }
   for (size_t l = 0; l < c->layers.size(); ++l) {
     Layer& L = c->layers[l];
@@ -1092,7 +1100,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
   Site s(c, "energy_readout");
   launch_energy_readout(st, N, c->species.p, c->e0.p, c->rowptr.p, c->dims.has_zbl ? c->zbl_e.p : nullptr, L, hs,
                         lds, ros, c->layers[L - 1].ro1.p, c->layers[L - 1].ro2.p, c->gh0.p, c->layers[L - 1].dhid,
-                        c->node_e.p, c->e_part.p, out, half);
+                        c->node_e.p, c->e_part.p, half);
   if (c->G > 1) {
     Site s2(c, "graph_energy");
     launch_graph_energy(st, c->G, c->gptr.p, c->node_e.p, c->eg.p);
@@ -1240,7 +1248,7 @@ void backward(mace_ctx* c, bool stress, double* out) {
   {
     Site s(c, "forces");
     launch_forces(st, N, c->rowptr.p, c->rowptr_s.p, c->perm_s.p, c->gv.p, out + 10,
-                  (stress && E > 0) ? nullptr : out + 1);
+                  (stress && E > 0) ? nullptr : out + 1, c->e_part.p, out);
   }
   if (stress && E > 0) {
     Site s(c, "virial");
@@ -1516,6 +1524,7 @@ int mace_step(mace_ctx* c, const double* positions, uint32_t flags, double* ener
     c->last_nl = rebuild && !c->edges_manual;
     if (c->last_nl) build_nl(c, positions);
     HIPCHK(hipEventRecord(c->ev[1], st));
+    ensure_embed(c);
     run_captured(c, c->g_fwd, c->pos.p, c->out.p, 0, [&] { forward(c, c->pos.p, c->out.p); });
     HIPCHK(hipEventRecord(c->ev[2], st));
     run_captured(c, c->g_bwd, c->out.p, nullptr, stress, [&] { backward(c, stress, c->out.p); });
@@ -1588,6 +1597,7 @@ int mace_step_device(mace_ctx* c, const double* d_positions, uint32_t flags, dou
       build_nl(c, host.data());
     }
     const bool stress = (flags & MACE_STEP_STRESS) != 0;
+    ensure_embed(c);
     run_captured(c, c->g_fwd, d_positions, d_out, 0, [&] { forward(c, d_positions, d_out); });
     run_captured(c, c->g_bwd, d_out, nullptr, stress, [&] { backward(c, stress, d_out); });
   });

@@ -246,10 +246,11 @@ void launch_sc_bwd(hipStream_t st, int N, int nout, int corr, const float* A, in
 void launch_energy_readout(hipStream_t st, int N, const int* species, const float* e0, const int* rowptr,
                            const float* zbl_e, int L, const float* const* h, const int* ldh, const float* const* ro,
                            const float* W1, const float* W2, float* gh, int ldgh, float* node_e, double* part,
-                           double* energy, int half);
+                           int half);
 // vir_zero (may be null) receives nine zeros
+// also writes the total energy from the readout's block partials (fixed order)
 void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s, const int* perm_s,
-                   const float* gv, double* forces, double* vir_zero);
+                   const float* gv, double* forces, double* vir_zero, const double* e_part, double* energy);
 
 // neighbour list
 struct NLParams {

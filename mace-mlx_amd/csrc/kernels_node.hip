@@ -557,8 +557,18 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 // vir_zero (may be null): receives nine zeros (no virial requested, or no edges)
 __global__ void __launch_bounds__(256) k_forces(int N, const int* __restrict__ rowptr, const int* __restrict__ rowptr_s,
                                                 const int* __restrict__ perm_s, const float* __restrict__ gv,
-                                                double* __restrict__ F, double* __restrict__ vir_zero) {
-  if (vir_zero && blockIdx.x == 0 && threadIdx.x < 9) vir_zero[threadIdx.x] = 0.0;
+                                                double* __restrict__ F, double* __restrict__ vir_zero,
+                                                const double* __restrict__ e_part, int e_nblk,
+                                                double* __restrict__ energy) {
+  if (blockIdx.x == 0) {
+    // the total energy: k_energy_readout's block partials in k_sum_partials' fixed order (a
+    // launch of its own on the step's critical path otherwise; nothing before needs the sum)
+    double s = 0.0;
+    for (int b = threadIdx.x; b < e_nblk; b += 256) s += e_part[b];
+    s = block_sum_fixed(s);
+    if (threadIdx.x == 0) *energy = s;
+    if (vir_zero && threadIdx.x < 9) vir_zero[threadIdx.x] = 0.0;
+  }
   const int a = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
   if (a >= N) return;  // whole wavefront exits together
   double fx = 0.0, fy = 0.0, fz = 0.0;
@@ -714,7 +724,7 @@ void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* 
 void launch_energy_readout(hipStream_t st, int N, const int* species, const float* e0, const int* rowptr,
                            const float* zbl_e, int L, const float* const* h, const int* ldh, const float* const* ro,
                            const float* W1, const float* W2, float* gh, int ldgh, float* node_e, double* part,
-                           double* energy, int half) {
+                           int half) {
   ReadoutArgs A{};
   A.L = L;
   for (int k = 0; k < L && k < 4; ++k) {
@@ -730,17 +740,18 @@ void launch_energy_readout(hipStream_t st, int N, const int* species, const floa
   if (nblk > 0)
     hipLaunchKernelGGL(k_energy_readout, dim3(nblk), dim3(256), 0, st, N, species, e0, rowptr, zbl_e, A, node_e,
                        part, half);
-  hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(256), 0, st, part, nblk, energy);
 }
 
 void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s, const int* perm_s,
-                   const float* gv, double* forces, double* vir_zero) {
+                   const float* gv, double* forces, double* vir_zero, const double* e_part, double* energy) {
+  const int e_nblk = (int)cdiv(N, 4);  // k_energy_readout's grid
   if (N <= 0) {
+    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(256), 0, st, e_part, 0, energy);
     if (vir_zero) hipLaunchKernelGGL(k_zeros, dim3(1), dim3(64), 0, st, vir_zero);
     return;
   }
   hipLaunchKernelGGL(k_forces, dim3(cdiv(N, 4)), dim3(256), 0, st, N, rowptr, rowptr_s, perm_s, gv, forces,
-                     vir_zero);
+                     vir_zero, e_part, e_nblk, energy);
 }
 
 void launch_gemm_group(hipStream_t st, GemmGroup& g) {

@@ -326,6 +326,20 @@ def test_batch_of_structures(medium_zbl):
         assert_parity(dict(E=eg[g], F=F[a:b], ne=ne[a:b], vir=vir[g]), ref, n, stress=per)
 
 
+def test_species_change_at_same_size():
+    """The first layer's species features are written once per system: a new species
+    assignment with the same atom count (and cell) must give what a fresh engine gives."""
+    cfg = arch_config("medium", num_elements=2, z_table=[8, 14], zbl=True)
+    a, b = Case(cfg, seed=6), Case(cfg, seed=6)
+    s = rattle(diamond_si((2, 2, 2)), 0.03, 7)
+    a.run(s)
+    t = s.copy()
+    t.numbers = np.where(np.arange(len(s)) % 3 == 0, 8, 14)
+    got, want = a.run(t), b.run(t)
+    assert got["E"] == want["E"]
+    assert np.array_equal(got["F"], want["F"])
+
+
 def test_isolated_atoms_and_no_edges(small):
     one = System(np.zeros((1, 3)), np.array([14]), np.eye(3) * 30.0, np.array([True, True, True]))
     a = small.run(one, stress=True)
