@@ -1296,6 +1296,9 @@ static void free_all(mace_ctx* c) {
   c->h3h.release();
   c->gwh.release();
   c->gscale.release();
+  c->h3inv.release();
+  for (auto* b : {&c->gptr, &c->gid}) b->release();
+  for (auto* b : {&c->gcell, &c->eg, &c->gvir}) b->release();
   for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->ag_cov, &c->gA2, &c->grho, &c->embed, &c->up0_tab, &c->sink, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
                   &c->gv, &c->gw, &c->gxe, &c->h3, &c->gh3p, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup,
                   &c->node_e})
