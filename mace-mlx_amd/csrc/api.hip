@@ -985,11 +985,7 @@ void forward(mace_ctx* c, const double* pos, double* out) {
     Site s(c, "edge_fwd");
     launch_edge_fwd(st, E, pos, c->sender.p, c->receiver.p, c->shifts.p, c->species.p, c->bessel_w.p, c->zbl_z.p,
                     c->zbl_cov.p, c->ag_cov.p, fp, c->G > 1 ? c->gcell.p : nullptr, c->gid.p, c->geom.p, c->Y.p,
-                    c->ef.p, c->zbl_e.p);
-  }
-  if (c->mts > 0) {
-    Site s(c, "tp_tables");
-    launch_tp_tables(st, E, c->max_lin, c->Y.p, c->Mt.p, c->mts);
+                    c->ef.p, c->zbl_e.p, c->Mt.p, c->mts, c->mts > 0 ? tp_table_entries(c->max_lin) : 0);
   }
   for (size_t l = 0; l < c->layers.size(); ++l) {
     Layer& L = c->layers[l];

@@ -32,6 +32,15 @@ __device__ inline double block_sum_fixed(double a) {
 // inside a block the element (channel u, component m) sits at m * NC + u.
 __host__ __device__ constexpr int block_off(int l) { return NC * l * l; }  // blocks 0..l-1 dense
 
+// Per-edge TP table entry q (row-major i*K + c) of the shared (3-block) layout: the sum over
+// x in [m1s(q), m1s(q+1)) of Y[m1j(x)] * m1v(x) (M1, l1 = 1), likewise m2* for M2 (l1 = 2)
+__device__ constexpr int m1s(int q) { return TP3_M1_START[q]; }
+__device__ constexpr int m1j(int x) { return TP3_M1_J[x]; }
+__device__ constexpr float m1v(int x) { return TP3_M1_V[x]; }
+__device__ constexpr int m2s(int q) { return TP3_M2_START[q]; }
+__device__ constexpr int m2j(int x) { return TP3_M2_J[x]; }
+__device__ constexpr float m2v(int x) { return TP3_M2_V[x]; }
+
 struct EdgeGeom {        // per-edge record written by the front end
   float x, y, z, r;
 };
@@ -77,7 +86,7 @@ void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* se
                      const int* receiver, const int* shifts, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov,
                      const float* ag_cov, const FrontParams& p, const double* gcell, const int* gid,
-                     EdgeGeom* geom, float* Y, float* ef, float* zbl_e);
+                     EdgeGeom* geom, float* Y, float* ef, float* zbl_e, float* Mt, int mts, int nent);
 void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov, const float* ag_cov,
                      const FrontParams& p, const EdgeGeom* geom, const float* gY, int gyp, const float* gef, float* gv,
@@ -141,7 +150,6 @@ void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const void* tiles,
 
 // per-edge x2-first tables Mt[e] (row stride mts) for the l1 >= 1 TP paths
 int tp_table_entries(int max_lin);
-void launch_tp_tables(hipStream_t st, int64_t E, int max_lin, const float* Y, float* Mt, int mts);
 // conv TP fused with the receiver-CSR scatter; w is float, or _Float16 when half (float16
 // feature policy: M rounded to fp16 values)
 void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,

@@ -68,13 +68,16 @@ __device__ __forceinline__ float agnesi_t(float r, float r0, const FrontParams& 
   return t;
 }
 
+// Also writes the per-edge TP tables Mt[e] = [M1 (3 x K1) | M2 (5 x K2)] (NENT = 72 or 227
+// entries, row stride mts, a multiple of 16) from the edge's stored Y, four entries per store.
+template <int NENT>
 __global__ void __launch_bounds__(256) k_edge_fwd(
     int64_t E, const double* __restrict__ pos, const int* __restrict__ sender,
     const int* __restrict__ receiver, const int* __restrict__ shifts, const int* __restrict__ species,
     const float* __restrict__ bessel_w, const float* __restrict__ zbl_z,
     const float* __restrict__ zbl_cov, const float* __restrict__ ag_cov, FrontParams p,
     const double* __restrict__ gcell, const int* __restrict__ gid, EdgeGeom* __restrict__ geom,
-    float* __restrict__ Y, float* __restrict__ ef, float* __restrict__ zbl_e) {
+    float* __restrict__ Y, float* __restrict__ ef, float* __restrict__ zbl_e, float* __restrict__ Mt, int mts) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= E) return;
   const int s = sender[e], r = receiver[e];
@@ -88,9 +91,25 @@ __global__ void __launch_bounds__(256) k_edge_fwd(
   sh16(x * inv, y * inv, z * inv, Yl);
   float4* Y4 = reinterpret_cast<float4*>(Y + 16 * e);
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
-    Y4[q] = make_float4(qh(Yl[4 * q], p.feature_half), qh(Yl[4 * q + 1], p.feature_half),
-                        qh(Yl[4 * q + 2], p.feature_half), qh(Yl[4 * q + 3], p.feature_half));
+  for (int j = 0; j < 16; ++j) Yl[j] = qh(Yl[j], p.feature_half);  // the stored values
+#pragma unroll
+  for (int q = 0; q < 4; ++q) Y4[q] = make_float4(Yl[4 * q], Yl[4 * q + 1], Yl[4 * q + 2], Yl[4 * q + 3]);
+  if constexpr (NENT > 0) {
+    float4* T4 = reinterpret_cast<float4*>(Mt + e * mts);
+    auto entry = [&](int q) {
+      float a = 0.f;
+      if (q < TP3_M1_NE) {
+#pragma unroll
+        for (int x = m1s(q); x < m1s(q + 1); ++x) a = fmaf(Yl[m1j(x)], m1v(x), a);
+      } else if (q < NENT) {
+#pragma unroll
+        for (int x = m2s(q - TP3_M1_NE); x < m2s(q - TP3_M1_NE + 1); ++x) a = fmaf(Yl[m2j(x)], m2v(x), a);
+      }
+      return a;
+    };
+#pragma unroll
+    for (int q = 0; q < NENT; q += 4) T4[q / 4] = make_float4(entry(q), entry(q + 1), entry(q + 2), entry(q + 3));
+  }
   float denv;
   const float env = poly_env(rr / p.r_max, p.pcut, &denv);
   float rb = rr;  // argument of the Bessel basis
@@ -417,10 +436,16 @@ static inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / 
 void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* sender, const int* receiver,
                      const int* shifts, const int* species, const float* bessel_w, const float* zbl_z,
                      const float* zbl_cov, const float* ag_cov, const FrontParams& p, const double* gcell,
-                     const int* gid, EdgeGeom* geom, float* Y, float* ef, float* zbl_e) {
+                     const int* gid, EdgeGeom* geom, float* Y, float* ef, float* zbl_e, float* Mt, int mts,
+                     int nent) {
   if (E <= 0) return;
-  hipLaunchKernelGGL(k_edge_fwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, pos, sender, receiver, shifts,
-                     species, bessel_w, zbl_z, zbl_cov, ag_cov, p, gcell, gid, geom, Y, ef, zbl_e);
+#define MACE_EDGE_FWD(NE)                                                                                      \
+  hipLaunchKernelGGL(k_edge_fwd<NE>, dim3(nblk(E, 256)), dim3(256), 0, st, E, pos, sender, receiver, shifts, \
+                     species, bessel_w, zbl_z, zbl_cov, ag_cov, p, gcell, gid, geom, Y, ef, zbl_e, Mt, mts)
+  if (nent == 0) MACE_EDGE_FWD(0);
+  else if (nent == TP3_M1_NE) MACE_EDGE_FWD(TP3_M1_NE);
+  else MACE_EDGE_FWD(TP3_M1_NE + TP3_M2_NE);
+#undef MACE_EDGE_FWD
 }
 
 void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,

@@ -11,7 +11,7 @@
 //
 // Per-edge x2-first tables Mt[e] = [M1(3 x K1) | M2(5 x K2)] with
 // M_l1[i][col] = sum_j Y_j C[i, j, k] pw are built once per step by
-// k_tp_tables (they depend only on Y) and shared by every layer.
+// the edge front end, k_edge_fwd (they depend only on Y), and shared by every layer.
 //
 // TP kernels: one workgroup per node, NG groups of NC threads (thread = channel
 // u, so a node's 128 channels are two wave64s per group).  Group g takes a
@@ -53,13 +53,6 @@ MACE_TP_TRAITS(2)
 MACE_TP_TRAITS(3)
 #undef MACE_TP_TRAITS
 
-// M-table entry q (row-major i*K + c) terms, in the shared (3-block) layout
-__device__ constexpr int m1s(int q) { return TP3_M1_START[q]; }
-__device__ constexpr int m1j(int x) { return TP3_M1_J[x]; }
-__device__ constexpr float m1v(int x) { return TP3_M1_V[x]; }
-__device__ constexpr int m2s(int q) { return TP3_M2_START[q]; }
-__device__ constexpr int m2j(int x) { return TP3_M2_J[x]; }
-__device__ constexpr float m2v(int x) { return TP3_M2_V[x]; }
 constexpr int MT_M2 = TP3_M1_NE;  // offset of the l1 = 2 table inside an Mt row
 
 static_assert(TP2_K1 == TP3_K1, "shared M1 layout");
@@ -518,45 +511,6 @@ __global__ void __launch_bounds__(NC) k_tp_gather_gx(int N, int din, const int* 
   }
   for (; k < end; ++k) s0 += src[(int64_t)k * din];
   gup[(int64_t)a * din + row * NC + u] = (s0 + s1) + (s2 + s3);
-}
-
-// Mt[e] = [M1 (3 x K1) | M2 (5 x K2)] from Y[e].  Block of 64 edges: thread e
-// evaluates its edge's entries with compile-time CG terms into an LDS row, then
-// the block writes the 64 rows out coalesced.  NENT = 72 (M1) or 227 (M1 + M2).
-template <int NENT>
-__global__ void __launch_bounds__(64) k_tp_tables(int64_t E, const float* __restrict__ Y, float* __restrict__ Mt,
-                                                  int mts) {
-  constexpr int RS = NENT + 1;  // odd LDS row stride: conflict-free column writes
-  __shared__ float sT[64 * RS];
-  const int t = threadIdx.x;
-  const int64_t e0 = (int64_t)blockIdx.x * 64, e = e0 + t;
-  float y[16];
-  const float* ye = Y + min(e, E - 1) * 16;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) y[j] = ye[j];
-  float* row = sT + t * RS;
-#pragma unroll
-  for (int q = 0; q < TP3_M1_NE; ++q) {
-    float a = 0.f;
-#pragma unroll
-    for (int x = m1s(q); x < m1s(q + 1); ++x) a = fmaf(y[m1j(x)], m1v(x), a);
-    row[q] = a;
-  }
-  if constexpr (NENT > TP3_M1_NE) {
-#pragma unroll
-    for (int q = 0; q < TP3_M2_NE; ++q) {
-      float a = 0.f;
-#pragma unroll
-      for (int x = m2s(q); x < m2s(q + 1); ++x) a = fmaf(y[m2j(x)], m2v(x), a);
-      row[TP3_M1_NE + q] = a;
-    }
-  }
-  __syncthreads();
-  const int nrow = (int)min<int64_t>(64, E - e0);
-  for (int i = t; i < nrow * NENT; i += 64) {
-    const int rr = i / NENT, q = i - rr * NENT;
-    Mt[(e0 + rr) * mts + q] = sT[rr * RS + q];
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1175,15 +1129,6 @@ void launch_recv(hipStream_t st, int N, const int* rowptr, const int* sender, co
 
 int tp_table_entries(int max_lin) { return max_lin >= 3 ? TP3_M1_NE + TP3_M2_NE : max_lin == 2 ? TP3_M1_NE : 0; }
 
-void launch_tp_tables(hipStream_t st, int64_t E, int max_lin, const float* Y, float* Mt, int mts) {
-  const int nent = tp_table_entries(max_lin);
-  if (E <= 0 || nent == 0) return;
-  const unsigned nb = (unsigned)((E + 63) / 64);
-  if (nent == TP3_M1_NE)
-    hipLaunchKernelGGL(k_tp_tables<TP3_M1_NE>, dim3(nb), dim3(64), 0, st, E, Y, Mt, mts);
-  else
-    hipLaunchKernelGGL(k_tp_tables<TP3_M1_NE + TP3_M2_NE>, dim3(nb), dim3(64), 0, st, E, Y, Mt, mts);
-}
 
 void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int* sender, const float* Y,
                    const float* Mt, int mts, const void* w, const float* up, float* M, int half) {
