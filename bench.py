@@ -181,7 +181,7 @@ def tp_scatter_frac(per_step, ctx):
     return (b / (t * 1e-3) / 1e9) / HBM_PEAK_GBS if t > 0 else 0.0
 
 
-def measure_config(idx, steps, warmup, separate=False):
+def measure_config(idx, steps, warmup, separate=False, graphs=None):
     """Steady-state and rebuild step times plus per-site roofline for configuration idx."""
     import torch
     from mace_mlx_amd._ffi import Engine
@@ -195,6 +195,8 @@ def measure_config(idx, steps, warmup, separate=False):
     eng.load_model(dm)
     if separate:
         eng.set_fused_tp(False)
+    if graphs is not None:
+        eng.set_graphs(graphs)
     s = bc.system
     zmap = {int(z): k for k, z in enumerate(dm.z_table)}
     species = np.array([zmap[int(z)] for z in s.numbers], np.int32)
@@ -252,6 +254,9 @@ def main():
     ap.add_argument("--separate-mlp-out", action="store_true",
                     help="float32 policy: radial-MLP output layer as its own pass (not fused into the TP)")
     ap.add_argument("--kernel-table", action="store_true", help="print per-kernel times to stderr")
+    ap.add_argument("--graphs", choices=("on", "off"), default=None,
+                    help="replay the step through captured HIP graphs (on) or launch it eagerly (off); "
+                         "default: the engine's default")
     ap.add_argument("--sweep", action="store_true",
                     help="also measure every benchmark configuration (table on stderr, 'sweep' in the JSON)")
     ap.add_argument("--copy-calib-mb", type=float, default=0.0,
@@ -285,6 +290,9 @@ def main():
     eng.load_model(dm)
     if args.separate_mlp_out:
         eng.set_fused_tp(False)
+    graphs = None if args.graphs is None else args.graphs == "on"
+    if graphs is not None:
+        eng.set_graphs(graphs)
     s = bc.system
     zmap = {int(z): k for k, z in enumerate(dm.z_table)}
     species = np.array([zmap[int(z)] for z in s.numbers], np.int32)
@@ -365,7 +373,8 @@ def main():
     sweep = None
     if args.sweep:
         del eng
-        sweep = [measure_config(i, max(5, args.steps // 2), args.warmup, args.separate_mlp_out) for i in range(5)]
+        sweep = [measure_config(i, max(5, args.steps // 2), args.warmup, args.separate_mlp_out, graphs)
+                 for i in range(5)]
         print(f"{'config':16s} {'N':>6s} {'E':>9s} {'ms/step':>9s} {'+NL ms':>8s} {'atom-steps/s':>13s}  "
               f"dominant site (frac of its roofline)   TP+scatter HBM frac", file=sys.stderr)
         for r in sweep:
