@@ -326,6 +326,31 @@ def test_batch_of_structures(medium_zbl):
         assert_parity(dict(E=eg[g], F=F[a:b], ne=ne[a:b], vir=vir[g]), ref, n, stress=per)
 
 
+def test_batch_edge_cases(small):
+    """Batches with an empty structure, a single isolated atom and a one-structure batch:
+    zero energy / virial for the empty one, E0 only for the lone atom, and the one-structure
+    batch equals mace_step (`graph_sum` over one graph, `utils.py:35-44`)."""
+    case = small
+    si = rattle(diamond_si((2, 2, 2)), 0.02, 31)
+    lone = System(np.zeros((1, 3)), np.array([14]), np.eye(3) * 20.0, np.array([True, True, True]))
+    empty = System(np.zeros((0, 3)), np.zeros(0, dtype=int), np.eye(3) * 10.0, np.array([True, True, True]))
+    structs = [si, empty, lone]
+    sps = [species_of(case.dm, s.numbers) for s in structs]
+    case.eng.set_batch(sps, [s.cell for s in structs], [s.pbc for s in structs], 0.5)
+    eg, ne, F, vir = case.eng.step_batch(np.concatenate([s.positions for s in structs]), stress=True)
+    assert eg[1] == 0.0 and np.abs(vir[1]).max() == 0.0
+    assert np.abs(F[len(si):]).max() == 0.0 and np.abs(vir[2]).max() == 0.0
+    one = case.run(si, stress=True)
+    e_lone = case.run(lone)["E"]
+    assert abs(eg[2] - e_lone) <= 1e-12 * max(1.0, abs(e_lone))
+    assert abs(eg[0] - one["E"]) <= 1e-10 * max(abs(one["E"]), len(si))
+    np.testing.assert_allclose(F[:len(si)], one["F"], rtol=0, atol=1e-7)
+    case.eng.set_batch([sps[0]], [si.cell], [si.pbc], 0.5)
+    eg1, _, F1, vir1 = case.eng.step_batch(si.positions, stress=True)
+    assert eg1[0] == one["E"] and np.array_equal(F1, one["F"])
+    np.testing.assert_allclose(vir1[0], one["vir"], rtol=0, atol=1e-12)
+
+
 def test_species_change_at_same_size():
     """The first layer's species features are written once per system: a new species
     assignment with the same atom count (and cell) must give what a fresh engine gives."""
