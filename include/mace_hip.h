@@ -16,6 +16,13 @@
  *   - The caller owns every host array; the context owns all device memory and
  *     one HIP stream.  A context is not re-entrant (one thread at a time);
  *     several contexts may share a device.
+ *   - Ordering: the context's stream is a blocking stream, so its work is ordered
+ *     with the null stream (PyTorch's default stream): device arrays written there
+ *     before mace_step_device are read after the writes land, and null-stream work
+ *     queued after mace_step_device waits for the step.  Work on any other stream
+ *     must be synchronised by the caller first.  mace_model_begin / _end,
+ *     mace_set_system / _batch and mace_set_edges wait for the context's queued
+ *     steps before they replace what those steps read.
  *   - Edges follow the reference: edge_index = [sender i; receiver j], shift S,
  *     edge vector D = x_j - x_i + S @ cell (`utils.py:47-84`).
  */
@@ -154,6 +161,13 @@ int mace_sync(mace_ctx* ctx);
 int mace_set_profiling(mace_ctx* ctx, int32_t enable);
 int mace_get_kernel_times(mace_ctx* ctx, char* names, int64_t names_len, double* total_ms,
                           int64_t* counts, int32_t capacity, int32_t* n_sites);
+
+/* The launch site of every kernel dispatch of the last step run with profiling
+ * enabled, in dispatch order ('\n'-separated; a site that dispatches k kernels is
+ * listed k times).  *n_dispatches receives the count; names may be NULL to query
+ * it only.  Used to map a profiler's per-dispatch records (rocprofv3 kernel trace,
+ * counters) to launch sites.  No counterpart in the reference. */
+int mace_get_launch_order(mace_ctx* ctx, char* names, int64_t names_len, int32_t* n_dispatches);
 
 /* Step replay through HIP graphs (default on).  The forward and the backward
  * launches of a step are captured once per (positions, output, stress) binding

@@ -18,6 +18,8 @@
 
 using namespace mace;
 
+thread_local int64_t mace::g_dispatches = 0;
+
 namespace {
 
 struct Err {
@@ -191,6 +193,7 @@ struct mace_ctx {
   };
   std::vector<Pending> pending;
   std::map<std::string, std::pair<double, int64_t>> prof_acc;
+  std::vector<std::string> launch_log;  // site of every dispatch of the last profiled step
 };
 
 namespace {
@@ -225,16 +228,19 @@ struct Site {
   mace_ctx* c;
   std::string name;
   size_t e0 = 0;
+  int64_t d0 = 0;
   Site(mace_ctx* ctx, std::string nm) : c(ctx), name(std::move(nm)) {
     if (!c->profiling) return;
     e0 = prof_event(c);
     HIPCHK(hipEventRecord(c->ev_pool[e0], c->stream));
+    d0 = g_dispatches;
   }
   ~Site() noexcept(false) {
     if (!c->profiling) return;
     const size_t e1 = prof_event(c);
     HIPCHK(hipEventRecord(c->ev_pool[e1], c->stream));
     c->pending.push_back({name, e0, e1});
+    for (int64_t k = d0; k < g_dispatches; ++k) c->launch_log.push_back(name);
   }
 };
 
@@ -625,7 +631,7 @@ void build_sender_csr(mace_ctx* c) {
   if (E > 0) {
     launch_fill_iota(c->stream, (int)E, c->nl_iota.p);
     cub_sort_pairs(c, c->sender.p, c->e_keys.p, c->nl_iota.p, c->perm_s.p, E, c->N);
-    hipLaunchKernelGGL(k_invert_perm, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, c->stream, E, c->perm_s.p,
+    MACE_LAUNCH(k_invert_perm, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, c->stream, E, c->perm_s.p,
                        c->pos_s.p);
   }
   build_rowptr(c, c->sender.p, E, c->N, c->rowptr_s.p);
@@ -973,6 +979,7 @@ void run_captured(mace_ctx* c, mace_ctx::StepGraph& g, const void* a, const void
 }
 
 void forward(mace_ctx* c, const double* pos, double* out) {
+  if (c->profiling) c->launch_log.clear();  // a step starts here
   hipStream_t st = c->stream;
   const int N = c->N;
   const int64_t E = c->E;
@@ -1273,7 +1280,10 @@ int mace_create(int32_t device, mace_ctx** out) {
     HIPCHK(hipGetDeviceCount(&n));
     if (device < 0 || device >= n) fail(MACE_ERR_INVALID, "device %d out of range (%d devices)", device, n);
     set_device(c);
-    HIPCHK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    // A blocking stream: its work is ordered with the null stream's (PyTorch's default
+    // stream, and the synchronous copies of this library), so positions written there
+    // before mace_step_device are seen by the step without an explicit wait.
+    HIPCHK(hipStreamCreateWithFlags(&c->stream, hipStreamDefault));
     for (auto& e : c->ev) HIPCHK(hipEventCreate(&e));
   });
   if (rc != MACE_OK) {
@@ -1336,6 +1346,8 @@ const char* mace_last_error(const mace_ctx* c) { return c ? c->err.c_str() : g_f
 int mace_model_begin(mace_ctx* c, const mace_model_dims* dims) {
   if (!c || !dims) return MACE_ERR_INVALID;
   return guard(c, [&] {
+    set_device(c);
+    HIPCHK(hipStreamSynchronize(c->stream));  // queued steps still read the old model
     c->dims = *dims;
     c->host_tensors.clear();
     c->model_ready = false;
@@ -1351,7 +1363,10 @@ int mace_model_end(mace_ctx* c) {
   if (!c) return MACE_ERR_INVALID;
   return guard(c, [&] {
     set_device(c);
+    HIPCHK(hipStreamSynchronize(c->stream));
     build_model(c);
+    // the cached edges were built for the previous model's r_max + skin
+    if (!c->edges_manual) c->nl_valid = false;
     if (c->system_ready) {
       ensure_node_buffers(c);
       ensure_edge_buffers(c, c->E);  // per-layer edge buffers of the new model
@@ -1375,6 +1390,8 @@ void set_batch(mace_ctx* c, int32_t G, const int32_t* n_atoms, const int32_t* sp
   const int n = gp[G];
   if (n > 0 && !species) fail(MACE_ERR_INVALID, "species is NULL");
   set_device(c);
+  // steps queued by mace_step_device may still read the arrays rewritten below
+  HIPCHK(hipStreamSynchronize(c->stream));
   for (int i = 0; i < n; ++i)
     if (species[i] < 0 || species[i] >= c->dims.num_elements)
       fail(MACE_ERR_SPECIES, "atom %d: species index %d outside [0, %d)", i, species[i], c->dims.num_elements);
@@ -1449,6 +1466,7 @@ int mace_set_edges(mace_ctx* c, int64_t E, const int32_t* sender, const int32_t*
       if (sender[e] < 0 || sender[e] >= c->N || receiver[e] < 0 || receiver[e] >= c->N)
         fail(MACE_ERR_INVALID, "edge %lld references atom outside [0, %d)", (long long)e, c->N);
     set_device(c);
+    HIPCHK(hipStreamSynchronize(c->stream));
     c->E = E;
     ensure_edge_index(c, E);
     if (E > 0) {
@@ -1457,7 +1475,7 @@ int mace_set_edges(mace_ctx* c, int64_t E, const int32_t* sender, const int32_t*
       HIPCHK(hipMemcpy(c->e_tmp_s.p, shifts3, 3 * E * sizeof(int), hipMemcpyHostToDevice));
       launch_fill_iota(c->stream, (int)E, c->nl_iota.p);
       cub_sort_pairs(c, c->e_tmp_j.p, c->e_keys.p, c->nl_iota.p, c->e_perm.p, E, c->N);
-      hipLaunchKernelGGL(k_gather_edges, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, c->stream, E, c->e_perm.p,
+      MACE_LAUNCH(k_gather_edges, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, c->stream, E, c->e_perm.p,
                          c->e_tmp_i.p, c->e_tmp_j.p, c->e_tmp_s.p, c->sender.p, c->receiver.p, c->shifts.p);
     }
     c->rowptr.ensure((size_t)c->N + 1);
@@ -1668,6 +1686,18 @@ int mace_get_kernel_times(mace_ctx* c, char* names, int64_t names_len, double* t
     if ((int64_t)all.size() + 1 > names_len) fail(MACE_ERR_INVALID, "names buffer too small (%zu)", all.size() + 1);
     std::memcpy(names, all.c_str(), all.size() + 1);
     c->prof_acc.clear();
+  });
+}
+
+int mace_get_launch_order(mace_ctx* c, char* names, int64_t names_len, int32_t* n_dispatches) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    if (n_dispatches) *n_dispatches = (int32_t)c->launch_log.size();
+    if (!names) return;
+    std::string all;
+    for (auto& s : c->launch_log) all += s + "\n";
+    if ((int64_t)all.size() + 1 > names_len) fail(MACE_ERR_INVALID, "names buffer too small (%zu)", all.size() + 1);
+    std::memcpy(names, all.c_str(), all.size() + 1);
   });
 }
 

@@ -14,6 +14,15 @@ constexpr int NC = 128;
 constexpr int NBESSEL_MAX = 16;
 constexpr int RADIAL_H = 64;   // radial-MLP hidden width compiled in
 
+// Host-side count of the kernel dispatches this library has issued on the calling
+// thread; the per-site profiler uses it to name every dispatch of a step.
+extern thread_local int64_t g_dispatches;
+#define MACE_LAUNCH(...)                \
+  do {                                  \
+    ++::mace::g_dispatches;             \
+    hipLaunchKernelGGL(__VA_ARGS__);    \
+  } while (0)
+
 // fixed-order tree sum over a 256-thread block (result in every thread)
 __device__ inline double block_sum_fixed(double a) {
   __shared__ double red[256];

@@ -52,6 +52,13 @@ def tp_layout(lin: int):
     return [created[k] for k in order]
 
 
+def tp_path_weight(slot) -> float:
+    """Path weight of one uvu instruction, `utils.py:143-154`: sqrt(dim_out / alpha)
+    with alpha the summed multiplicity of the SH block, which is 1 for every slot
+    here (each instruction owns its output slot)."""
+    return math.sqrt(2 * slot[2] + 1)
+
+
 def emit_sh(out):
     out.append("// SH recursion Y_l[k] += Y_{l-1}[i] * Y_1[j] * v  (e3nn basis)")
     for l in (2, 3):
@@ -100,7 +107,7 @@ def emit_tp(out, lin: int):
                 for sidx, (a, l2, l3) in enumerate(slots):
                     if a == l1 and col[sidx] <= c < col[sidx] + 2 * l3 + 1:
                         k = c - col[sidx]
-                        pw = math.sqrt(2 * l3 + 1)
+                        pw = tp_path_weight(slots[sidx])
                         C = wigner_3j(l1, l2, l3)
                         for j in range(2 * l2 + 1):
                             v = C[i, j, k] * pw

@@ -440,7 +440,7 @@ void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* se
                      int nent) {
   if (E <= 0) return;
 #define MACE_EDGE_FWD(NE)                                                                                      \
-  hipLaunchKernelGGL(k_edge_fwd<NE>, dim3(nblk(E, 256)), dim3(256), 0, st, E, pos, sender, receiver, shifts, \
+  MACE_LAUNCH(k_edge_fwd<NE>, dim3(nblk(E, 256)), dim3(256), 0, st, E, pos, sender, receiver, shifts, \
                      species, bessel_w, zbl_z, zbl_cov, ag_cov, p, gcell, gid, geom, Y, ef, zbl_e, Mt, mts)
   if (nent == 0) MACE_EDGE_FWD(0);
   else if (nent == TP3_M1_NE) MACE_EDGE_FWD(TP3_M1_NE);
@@ -453,38 +453,38 @@ void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* re
                      const FrontParams& p, const EdgeGeom* geom, const float* gY, int gyp, const float* gef,
                      float* gv, double* vir_part) {
   if (E <= 0) return;
-  hipLaunchKernelGGL(k_edge_bwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, sender, receiver, species,
+  MACE_LAUNCH(k_edge_bwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, sender, receiver, species,
                      bessel_w, zbl_z, zbl_cov, ag_cov, p, geom, gY, gyp, gef, gv, vir_part);
 }
 
 void launch_density_fwd(hipStream_t st, int N, const int* rowptr, const float* ef, int nb, const float* wd,
                         float* rinv) {
   if (N <= 0) return;
-  hipLaunchKernelGGL(k_density_fwd, dim3(nblk(N, 4)), dim3(256), 0, st, N, rowptr, ef, nb, wd, rinv);
+  MACE_LAUNCH(k_density_fwd, dim3(nblk(N, 4)), dim3(256), 0, st, N, rowptr, ef, nb, wd, rinv);
 }
 
 void launch_density_node_bwd(hipStream_t st, int N, int dint, const float* gA, const float* A, const float* rinv,
                              float* grho) {
   if (N <= 0) return;
-  hipLaunchKernelGGL(k_density_node_bwd, dim3(nblk(N, 4)), dim3(256), 0, st, N, dint, gA, A, rinv, grho);
+  MACE_LAUNCH(k_density_node_bwd, dim3(nblk(N, 4)), dim3(256), 0, st, N, dint, gA, A, rinv, grho);
 }
 
 void launch_density_edge_bwd(hipStream_t st, int64_t E, const int* receiver, const float* ef, int nb,
                              const float* wd, const float* grho, float* gef) {
   if (E <= 0) return;
-  hipLaunchKernelGGL(k_density_edge_bwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, receiver, ef, nb, wd, grho, gef);
+  MACE_LAUNCH(k_density_edge_bwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, receiver, ef, nb, wd, grho, gef);
 }
 
 void launch_nl_bin(hipStream_t st, int i0, int n, const double* pos, const NLParams& p, int bin_off, double* wpos,
                    int* img, int* bin) {
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_nl_bin, dim3(nblk(n, 256)), dim3(256), 0, st, i0, n, pos, p, bin_off, wpos, img, bin);
+  MACE_LAUNCH(k_nl_bin, dim3(nblk(n, 256)), dim3(256), 0, st, i0, n, pos, p, bin_off, wpos, img, bin);
 }
 
 void launch_nl_count(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
                      const int* bin, const int* bin_start, const int* bin_atoms, int* counts) {
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_nl_count, dim3(nblk(n, 4)), dim3(256), 0, st, i0, n, p, bin_off, wpos, bin, bin_start,
+  MACE_LAUNCH(k_nl_count, dim3(nblk(n, 4)), dim3(256), 0, st, i0, n, p, bin_off, wpos, bin, bin_start,
                      bin_atoms, counts);
 }
 
@@ -492,18 +492,18 @@ void launch_nl_fill(hipStream_t st, int i0, int n, const NLParams& p, int bin_of
                     const int* img, const int* bin, const int* bin_start, const int* bin_atoms, const int* rowptr,
                     int* sender, int* receiver, int* shifts) {
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_nl_fill, dim3(nblk(n, 4)), dim3(256), 0, st, i0, n, p, bin_off, wpos, img, bin, bin_start,
+  MACE_LAUNCH(k_nl_fill, dim3(nblk(n, 4)), dim3(256), 0, st, i0, n, p, bin_off, wpos, img, bin, bin_start,
                      bin_atoms, rowptr, sender, receiver, shifts);
 }
 
 void launch_fill_iota(hipStream_t st, int n, int* out) {
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_iota, dim3(nblk(n, 256)), dim3(256), 0, st, n, out);
+  MACE_LAUNCH(k_iota, dim3(nblk(n, 256)), dim3(256), 0, st, n, out);
 }
 
 void launch_count_keys(hipStream_t st, int64_t E, const int* keys, int* counts) {
   if (E <= 0) return;
-  hipLaunchKernelGGL(k_count_keys, dim3(nblk(E, 256)), dim3(256), 0, st, E, keys, counts);
+  MACE_LAUNCH(k_count_keys, dim3(nblk(E, 256)), dim3(256), 0, st, E, keys, counts);
 }
 
 }  // namespace mace

@@ -1176,7 +1176,7 @@ void launch_mlp_permute_x(hipStream_t st, int nb, const float* W0, const float* 
                           const float* scale3, void* tiles) {
   MlpFwdX* fw = static_cast<MlpFwdX*>(tiles);
   MlpBwdX* bw = reinterpret_cast<MlpBwdX*>(static_cast<char*>(tiles) + sizeof(MlpFwdX));
-  hipLaunchKernelGGL(k_mlp_permute_x, dim3(1), dim3(256), 0, st, nb, W0, W1, W2, scale3[0], scale3[1], scale3[2],
+  MACE_LAUNCH(k_mlp_permute_x, dim3(1), dim3(256), 0, st, nb, W0, W1, W2, scale3[0], scale3[1], scale3[2],
                      fw, bw);
 }
 
@@ -1184,7 +1184,7 @@ void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, con
                          const float* winv3, void* h3x, float* h3inv, float* ds) {
   if (E <= 0) return;
   MlpWinv wi{{winv3[0], winv3[1], winv3[2]}};
-  hipLaunchKernelGGL(k_mlp_hidden_x, dim3(hidden_grid(E)), dim3(64 * kHidFwdWaves), 0, st, E, nb, ef,
+  MACE_LAUNCH(k_mlp_hidden_x, dim3(hidden_grid(E)), dim3(64 * kHidFwdWaves), 0, st, E, nb, ef,
                      static_cast<const MlpFwdX*>(tiles), wi, static_cast<_Float16*>(h3x), h3inv, ds);
 }
 
@@ -1195,10 +1195,10 @@ void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tile
   const MlpFwdX* fw = static_cast<const MlpFwdX*>(tiles);
   const MlpBwdX* bw = reinterpret_cast<const MlpBwdX*>(static_cast<const char*>(tiles) + sizeof(MlpFwdX));
   if (ds)
-    hipLaunchKernelGGL((k_mlp_hidden_bwd_x<false, 4>), dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, fw, bw, wi, ef, ds,
+    MACE_LAUNCH((k_mlp_hidden_bwd_x<false, 4>), dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, fw, bw, wi, ef, ds,
                        gh3, np, E * H, gef, accumulate);
   else
-    hipLaunchKernelGGL((k_mlp_hidden_bwd_x<true, kHidBwdWaves>), dim3(hidden_bwd_grid(E)), dim3(64 * kHidBwdWaves), 0,
+    MACE_LAUNCH((k_mlp_hidden_bwd_x<true, kHidBwdWaves>), dim3(hidden_bwd_grid(E)), dim3(64 * kHidBwdWaves), 0,
                        st, E, nb, fw, bw, wi, ef,
                        ds, gh3, np, E * H, gef, accumulate);
 }
@@ -1206,7 +1206,7 @@ void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tile
 void launch_mlp_permute(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2, void* tiles) {
   MlpFwdW* fw = static_cast<MlpFwdW*>(tiles);
   MlpBwdW* bw = reinterpret_cast<MlpBwdW*>(static_cast<char*>(tiles) + sizeof(MlpFwdW));
-  hipLaunchKernelGGL(k_mlp_permute, dim3(1), dim3(256), 0, st, nb, W0, W1, W2, fw, bw);
+  MACE_LAUNCH(k_mlp_permute, dim3(1), dim3(256), 0, st, nb, W0, W1, W2, fw, bw);
 }
 
 void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const void* tiles, void* h3,
@@ -1215,46 +1215,46 @@ void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const
   const dim3 grid(hidden_grid(E)), blk(256);
   const MlpFwdW* fw = static_cast<const MlpFwdW*>(tiles);
   if (mode == H3_SPLIT)
-    hipLaunchKernelGGL(k_mlp_hidden<H3_SPLIT>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
+    MACE_LAUNCH(k_mlp_hidden<H3_SPLIT>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
   else if (mode == H3_F16)
-    hipLaunchKernelGGL(k_mlp_hidden<H3_F16>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
+    MACE_LAUNCH(k_mlp_hidden<H3_F16>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
   else
-    hipLaunchKernelGGL(k_mlp_hidden<H3_F32>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
+    MACE_LAUNCH(k_mlp_hidden<H3_F32>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
 }
 
 void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w, int half) {
   if (E <= 0) return;
   if (half)
-    hipLaunchKernelGGL(k_mlp_out_h, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const _Float16*>(h3),
+    MACE_LAUNCH(k_mlp_out_h, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const _Float16*>(h3),
                        static_cast<const _Float16*>(W3T), static_cast<_Float16*>(w));
   else
-    hipLaunchKernelGGL(k_mlp_out, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const float*>(h3),
+    MACE_LAUNCH(k_mlp_out, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const float*>(h3),
                        static_cast<const float*>(W3T), static_cast<float*>(w));
 }
 
 void launch_mlp_out_x(hipStream_t st, int64_t E, int W, const void* h3x, const float* h3inv, const void* W3Tx,
                       float cscale, float* w) {
   if (E <= 0) return;
-  hipLaunchKernelGGL(k_mlp_out_x, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const _Float16*>(h3x),
+  MACE_LAUNCH(k_mlp_out_x, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const _Float16*>(h3x),
                      h3inv, static_cast<const _Float16*>(W3Tx), cscale, w);
 }
 
 void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3) {
   if (E <= 0) return;
-  hipLaunchKernelGGL(k_mlp_gh3, dim3(nblk(E, 32)), dim3(256), 0, st, E, W, gw, W3, gh3);
+  MACE_LAUNCH(k_mlp_gh3, dim3(nblk(E, 32)), dim3(256), 0, st, E, W, gw, W3, gh3);
 }
 
 void launch_mlp_gh3_x(hipStream_t st, int64_t E, int W, const float* gw, const void* W3x, float cscale,
                       float* gh3) {
   if (E <= 0) return;
-  hipLaunchKernelGGL(k_mlp_gh3_x, dim3(nblk(E, 64)), dim3(256), 0, st, E, W, gw,
+  MACE_LAUNCH(k_mlp_gh3_x, dim3(nblk(E, 64)), dim3(256), 0, st, E, W, gw,
                      static_cast<const _Float16*>(W3x), cscale, gh3);
 }
 
 void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const float* gscale, const void* W3h,
                       float* gh3) {
   if (E <= 0) return;
-  hipLaunchKernelGGL(k_mlp_gh3_h, dim3(nblk(E, 32)), dim3(256), 0, st, E, W, static_cast<const _Float16*>(gw),
+  MACE_LAUNCH(k_mlp_gh3_h, dim3(nblk(E, 32)), dim3(256), 0, st, E, W, static_cast<const _Float16*>(gw),
                      gscale, static_cast<const _Float16*>(W3h), gh3);
 }
 
@@ -1262,7 +1262,7 @@ void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const void* tiles,
                            float* gef, int accumulate) {
   if (E <= 0) return;
   const MlpBwdW* bw = reinterpret_cast<const MlpBwdW*>(static_cast<const char*>(tiles) + sizeof(MlpFwdW));
-  hipLaunchKernelGGL(k_mlp_hidden_bwd, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, bw, ds, gh3, gef, accumulate);
+  MACE_LAUNCH(k_mlp_hidden_bwd, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, bw, ds, gh3, gef, accumulate);
 }
 
 }  // namespace mace

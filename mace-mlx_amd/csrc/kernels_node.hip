@@ -661,32 +661,32 @@ static inline unsigned cdiv(int64_t a, int b) { return (unsigned)((a + b - 1) / 
 
 void launch_graph_energy(hipStream_t st, int G, const int* gptr, const float* node_e, double* eg) {
   if (G <= 0) return;
-  hipLaunchKernelGGL(k_graph_energy, dim3(G), dim3(256), 0, st, gptr, node_e, eg);
+  MACE_LAUNCH(k_graph_energy, dim3(G), dim3(256), 0, st, gptr, node_e, eg);
 }
 
 void launch_graph_virial(hipStream_t st, int G, const int* gptr, const int* rowptr, const EdgeGeom* geom,
                          const float* gv, double* vir) {
   if (G <= 0) return;
-  hipLaunchKernelGGL(k_graph_virial, dim3(G), dim3(256), 0, st, gptr, rowptr, geom, gv, vir);
+  MACE_LAUNCH(k_graph_virial, dim3(G), dim3(256), 0, st, gptr, rowptr, geom, gv, vir);
 }
 
 void launch_linear(hipStream_t st, int N, const LinearDesc& d, const float* X, const float* W, float* Y) {
   const int rows = N * d.d;
   if (rows <= 0) return;
-  hipLaunchKernelGGL(k_linear, dim3(cdiv(rows, LT), d.Cout / LT), dim3(256), 0, st, rows, d, X, W, Y);
+  MACE_LAUNCH(k_linear, dim3(cdiv(rows, LT), d.Cout / LT), dim3(256), 0, st, rows, d, X, W, Y);
 }
 
 void launch_linear_species(hipStream_t st, int N, const LinearDesc& d, const float* X, const float* W,
                            const int* species, float* Y) {
   const int rows = N * d.d;
   if (rows <= 0) return;
-  hipLaunchKernelGGL(k_linear_species, dim3(rows, d.Cout / NC), dim3(NC), 0, st, rows, d, X, W, species, Y);
+  MACE_LAUNCH(k_linear_species, dim3(rows, d.Cout / NC), dim3(NC), 0, st, rows, d, X, W, species, Y);
 }
 
 void launch_embed(hipStream_t st, int N, const int* species, const float* emb, int ld, float* h, int half,
                   const float* up_tab, float* h_up) {
   if (N <= 0) return;
-  hipLaunchKernelGGL(k_embed, dim3(N), dim3(NC), 0, st, N, species, emb, ld, h, half, up_tab, h_up);
+  MACE_LAUNCH(k_embed, dim3(N), dim3(NC), 0, st, N, species, emb, ld, h, half, up_tab, h_up);
 }
 
 void launch_sc_fwd(hipStream_t st, int N, int nout, int corr, const float* A, int ldA, const int* species,
@@ -694,9 +694,9 @@ void launch_sc_fwd(hipStream_t st, int N, int nout, int corr, const float* A, in
   if (N <= 0) return;
   ScW w{{Wsc[0], nout > 1 ? Wsc[1] : nullptr, nout > 2 ? Wsc[2] : nullptr}};
   switch (corr) {
-    case 1: hipLaunchKernelGGL(k_sc_fwd<1>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB, half); break;
-    case 2: hipLaunchKernelGGL(k_sc_fwd<2>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB, half); break;
-    case 3: hipLaunchKernelGGL(k_sc_fwd<3>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB, half); break;
+    case 1: MACE_LAUNCH(k_sc_fwd<1>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB, half); break;
+    case 2: MACE_LAUNCH(k_sc_fwd<2>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB, half); break;
+    case 3: MACE_LAUNCH(k_sc_fwd<3>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB, half); break;
   }
 }
 
@@ -706,19 +706,19 @@ void launch_sc_bwd(hipStream_t st, int N, int nout, int corr, const float* A, in
   ScW w{{Wsc[0], nout > 1 ? Wsc[1] : nullptr, nout > 2 ? Wsc[2] : nullptr}};
   switch (corr) {
     case 1:
-      hipLaunchKernelGGL(k_sc_bwd<1>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, gB, ldB, gA);
+      MACE_LAUNCH(k_sc_bwd<1>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, gB, ldB, gA);
       break;
     case 2:
-      hipLaunchKernelGGL(k_sc_bwd<2>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, gB, ldB, gA);
+      MACE_LAUNCH(k_sc_bwd<2>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, gB, ldB, gA);
       break;
     case 3:
-      hipLaunchKernelGGL(k_sc_bwd<3>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, gB, ldB, gA);
+      MACE_LAUNCH(k_sc_bwd<3>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, gB, ldB, gA);
       break;
   }
 }
 
 void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir) {
-  hipLaunchKernelGGL(k_virial_reduce, dim3(1), dim3(256), 0, st, part, nblk, vir);
+  MACE_LAUNCH(k_virial_reduce, dim3(1), dim3(256), 0, st, part, nblk, vir);
 }
 
 void launch_energy_readout(hipStream_t st, int N, const int* species, const float* e0, const int* rowptr,
@@ -738,7 +738,7 @@ void launch_energy_readout(hipStream_t st, int N, const int* species, const floa
   A.ldgh = ldgh;
   const int nblk = (int)cdiv(N, 4);
   if (nblk > 0)
-    hipLaunchKernelGGL(k_energy_readout, dim3(nblk), dim3(256), 0, st, N, species, e0, rowptr, zbl_e, A, node_e,
+    MACE_LAUNCH(k_energy_readout, dim3(nblk), dim3(256), 0, st, N, species, e0, rowptr, zbl_e, A, node_e,
                        part, half);
 }
 
@@ -746,11 +746,11 @@ void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s
                    const float* gv, double* forces, double* vir_zero, const double* e_part, double* energy) {
   const int e_nblk = (int)cdiv(N, 4);  // k_energy_readout's grid
   if (N <= 0) {
-    hipLaunchKernelGGL(k_sum_partials, dim3(1), dim3(256), 0, st, e_part, 0, energy);
-    if (vir_zero) hipLaunchKernelGGL(k_zeros, dim3(1), dim3(64), 0, st, vir_zero);
+    MACE_LAUNCH(k_sum_partials, dim3(1), dim3(256), 0, st, e_part, 0, energy);
+    if (vir_zero) MACE_LAUNCH(k_zeros, dim3(1), dim3(64), 0, st, vir_zero);
     return;
   }
-  hipLaunchKernelGGL(k_forces, dim3(cdiv(N, 4)), dim3(256), 0, st, N, rowptr, rowptr_s, perm_s, gv, forces,
+  MACE_LAUNCH(k_forces, dim3(cdiv(N, 4)), dim3(256), 0, st, N, rowptr, rowptr_s, perm_s, gv, forces,
                      vir_zero, e_part, e_nblk, energy);
 }
 
@@ -764,7 +764,7 @@ void launch_gemm_group(hipStream_t st, GemmGroup& g) {
       tiles += (int)cdiv(P.rows, 64) * P.tiles_n;
     }
     g.total_tiles = tiles;
-    if (tiles > 0) hipLaunchKernelGGL(k_gemm_group_x, dim3(tiles), dim3(256), 0, st, g);
+    if (tiles > 0) MACE_LAUNCH(k_gemm_group_x, dim3(tiles), dim3(256), 0, st, g);
     return;
   }
   int row_tiles = 0;
@@ -781,9 +781,9 @@ void launch_gemm_group(hipStream_t st, GemmGroup& g) {
   g.total_tiles = tiles;
   if (tiles <= 0) return;
   if (wide)
-    hipLaunchKernelGGL((k_gemm_group<4, 2, false>), dim3(tiles), dim3(256), 0, st, g);
+    MACE_LAUNCH((k_gemm_group<4, 2, false>), dim3(tiles), dim3(256), 0, st, g);
   else
-    hipLaunchKernelGGL((k_gemm_group<1, 8, true>), dim3(tiles), dim3(256), 0, st, g);
+    MACE_LAUNCH((k_gemm_group<1, 8, true>), dim3(tiles), dim3(256), 0, st, g);
 }
 
 

@@ -1111,7 +1111,7 @@ template <int LIN, typename WT>
 void launch_fwd(hipStream_t st, int N, const int* rowptr, const int* sender, const float* Y, const float* Mt, int mts,
                 const void* w, const float* up, float* M, int half) {
   constexpr int NG = ng_for(LIN);
-  hipLaunchKernelGGL((k_tp_fwd<LIN, NG, WT>), dim3(N), dim3(NC * NG), 0, st, N, rowptr, sender, Y, Mt, mts,
+  MACE_LAUNCH((k_tp_fwd<LIN, NG, WT>), dim3(N), dim3(NC * NG), 0, st, N, rowptr, sender, Y, Mt, mts,
                      static_cast<const WT*>(w), up, M, half);
 }
 
@@ -1120,7 +1120,7 @@ void launch_recv(hipStream_t st, int N, const int* rowptr, const int* sender, co
                  int mts, const void* w, const float* up, const float* gM, void* gw, float* gscale, float* gY,
                  int accumulate_gY, const int* pos_s, float* gxe) {
   constexpr int NG = ng_for(LIN);
-  hipLaunchKernelGGL((k_tp_bwd_recv<LIN, NG, GX, WT>), dim3(N), dim3(NC * NG), 0, st, N, rowptr, sender, Y, Mt,
+  MACE_LAUNCH((k_tp_bwd_recv<LIN, NG, GX, WT>), dim3(N), dim3(NC * NG), 0, st, N, rowptr, sender, Y, Mt,
                      mts, static_cast<const WT*>(w), up, gM, static_cast<WT*>(gw), gscale, gY, accumulate_gY,
                      pos_s, gxe);
 }
@@ -1171,10 +1171,10 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
   const _Float16* hx = static_cast<const _Float16*>(h3x);
   const _Float16* wt = static_cast<const _Float16*>(W3Tx);
   if (lin == 1)
-    hipLaunchKernelGGL(k_tpx_fwd<1>, grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w,
+    MACE_LAUNCH(k_tpx_fwd<1>, grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w,
                        sink);
   else
-    hipLaunchKernelGGL(k_tpx_fwd<2>, grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w,
+    MACE_LAUNCH(k_tpx_fwd<2>, grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w,
                        sink);
 }
 
@@ -1187,7 +1187,7 @@ void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
   const dim3 grid((unsigned)((N + XW - 1) / XW), 2, lin == 1 ? 1 : 2);
   const _Float16* wx = static_cast<const _Float16*>(W3x);
 #define MACE_TPXB(L, GXV)                                                                                        \
-  hipLaunchKernelGGL((k_tpx_bwd<L, GXV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \
+  MACE_LAUNCH((k_tpx_bwd<L, GXV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \
                      pos_s, gxe, gY, gh3p, sink)
   const bool gx = gxe != nullptr;
   if (lin == 1) {
@@ -1200,12 +1200,12 @@ void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
 
 void launch_fill_zero(hipStream_t st, float* p, int64_t n) {
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 1024)), dim3(256), 0, st, p, n);
+  MACE_LAUNCH(k_fill_zero, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 1024)), dim3(256), 0, st, p, n);
 }
 
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe, float* gup) {
   if (N <= 0) return;
-  hipLaunchKernelGGL(k_tp_gather_gx, dim3(N, lin * lin), dim3(NC), 0, st, N, NC * lin * lin, rowptr_s, gxe, gup);
+  MACE_LAUNCH(k_tp_gather_gx, dim3(N, lin * lin), dim3(NC), 0, st, N, NC * lin * lin, rowptr_s, gxe, gup);
 }
 
 }  // namespace mace

@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "mace_set_split_products",
     "mace_set_fused_tp",
     "mace_set_batch", "mace_step_batch",
+    "mace_get_launch_order",
 )
 
 
@@ -94,6 +95,7 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
         "mace_set_batch": (ctypes.c_int, [P, I32, P, P, P, P, D]),
         "mace_step_batch": (ctypes.c_int, [P, P, U32, P, P, P, P]),
         "mace_get_kernel_times": (ctypes.c_int, [P, ctypes.c_char_p, I64, P, P, I32, ctypes.POINTER(I32)]),
+        "mace_get_launch_order": (ctypes.c_int, [P, ctypes.c_char_p, I64, ctypes.POINTER(I32)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -272,6 +274,14 @@ class Engine:
                                                     ctypes.byref(n)))
         names = buf.value.decode().split("\n")[:cap]
         return {nm: (float(tot[i]), int(cnt[i])) for i, nm in enumerate(names)}
+
+    def launch_order(self) -> list:
+        """Launch site of every kernel dispatch of the last profiled step, in order."""
+        n = ctypes.c_int32()
+        self._check(self._lib.mace_get_launch_order(self._h, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(64 * max(n.value, 1) + 1)
+        self._check(self._lib.mace_get_launch_order(self._h, buf, len(buf), ctypes.byref(n)))
+        return buf.value.decode().split("\n")[:n.value]
 
     def timings(self) -> np.ndarray:
         out = np.zeros(4, dtype=np.float64)

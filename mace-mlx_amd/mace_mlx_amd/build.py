@@ -13,12 +13,13 @@ from pathlib import Path
 CSRC = Path(__file__).resolve().parents[1] / "csrc"
 
 
-def build(jobs: int = 4, verbose: bool = False) -> Path:
+def build(jobs: int = 5, verbose: bool = False) -> Path:
     env = dict(os.environ)
     env.setdefault("PYTHON", sys.executable)
     subprocess.run([sys.executable, str(CSRC / "gen_tables.py"), str(CSRC / "gen")], check=True,
                    stdout=None if verbose else subprocess.DEVNULL)
-    proc = subprocess.run(["make", "-C", str(CSRC), f"-j{jobs}"], env=env, capture_output=not verbose, text=True)
+    # -B: compile every source each time (the build is also the "does it build" check)
+    proc = subprocess.run(["make", "-B", "-C", str(CSRC), f"-j{jobs}"], env=env, capture_output=not verbose, text=True)
     if proc.returncode != 0:
         sys.stderr.write((proc.stdout or "") + (proc.stderr or ""))
         raise RuntimeError("HIP engine build failed")

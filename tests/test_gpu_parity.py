@@ -1,7 +1,9 @@
 """GPU parity: the HIP engine against the CPU oracle on the same seeded inputs.
 
-Tolerances (written here, from the benchmark definition): energy relative 1e-6
-on the scale max(|E|, N x 1 eV) (see gpu_helpers.assert_parity), forces max-abs 1e-4 eV/A, stress/virial relative 1e-5; neighbour lists equal as
+Tolerances (written here, from the benchmark definition): energy |dE|/|E| <= 1e-6, or
+|dE|/N <= 1e-6 eV/atom for the cases named energy="per_atom" (random-init large
+architecture, whose per-atom energies cancel; see gpu_helpers.assert_parity), forces
+max-abs 1e-4 eV/A, stress/virial relative 1e-5; neighbour lists equal as
 sets of (i, j, S) to the float64 brute force.  Full-size configurations that the
 oracle cannot evaluate in seconds are checked through size-independent
 properties (periodic replication, translation / rotation covariance, sum of
@@ -76,7 +78,8 @@ def test_config4_large_l2_paths_reduced(large):
     s = rattle(diamond_si((3, 3, 3)), 0.05, 3)
     got = large.run(s, stress=True)
     edges = large.edges()
-    assert_parity(got, large.reference(s, got["sp"], edges, stress=True), len(s), stress=True)
+    assert_parity(got, large.reference(s, got["sp"], edges, stress=True), len(s), stress=True,
+                  energy="per_atom")
 
 
 def test_hea_89_elements_reduced():
@@ -107,7 +110,8 @@ def test_trained_topology_parity(arch):
     got = case.run(s, stress=True)
     edges = case.edges()
     assert edge_set(*edges) == bruteforce_edges(s)
-    assert_parity(got, case.reference(s, got["sp"], edges, stress=True), len(s), stress=True)
+    assert_parity(got, case.reference(s, got["sp"], edges, stress=True), len(s), stress=True,
+                  energy="per_atom" if arch == "large" else "relative")
 
 
 @pytest.mark.parametrize("head", ["pbe", "r2scan"])
@@ -165,7 +169,8 @@ def test_float16_feature_policy(arch):
     # the same rounded weights on the float32 path reproduce the float64 model to float32 tolerance
     from mace_mlx_amd.device_model import build_device_model
     case.eng.load_model(build_device_model(cfg, case.w_model, dtype="float32"))
-    assert_parity(case.run(s, stress=True), ref, len(s), stress=True)
+    assert_parity(case.run(s, stress=True), ref, len(s), stress=True,
+                  energy="per_atom" if arch == "large" else "relative")
 
 
 # ---------------------------------------------------------------------------
@@ -428,6 +433,35 @@ def test_calculator_end_to_end(tmp_path):
     np.testing.assert_allclose(res[1]["stress"], calc.results["stress"], rtol=0, atol=1e-9)
 
 
+def test_calculator_matches_oracle(tmp_path):
+    """MACECalculator.calculate against the float64 oracle's energy / forces / stress
+    (`calculators.py:385-418,515-523`: stress = dE/d(eps_sym) / |det cell| in Voigt order
+    xx, yy, zz, yz, xz, xy) on a strained triclinic cell with ZBL on: energy |dE|/|E| <=
+    1e-6, forces max-abs 1e-4 eV/A, every Voigt component within 1e-5 of the largest."""
+    from mace_mlx_amd import MACECalculator
+    from mace_mlx_amd.systems import write_model_dir
+    from oracle.model import OracleMACE
+    from oracle.neighbors import neighbor_list
+    cfg = arch_config("medium", zbl=True)
+    d = write_model_dir(cfg, tmp_path / "si-medium-zbl", seed=7)
+    s = _triclinic()
+    strain = np.eye(3) + np.array([[0.02, 0.01, -0.015], [0.01, -0.01, 0.005], [-0.015, 0.005, 0.03]])
+    s.positions, s.cell = s.positions @ strain, s.cell @ strain
+    calc = MACECalculator(model_path=str(d), device="cuda")
+    calc.calculate(s, ["energy", "forces", "stress"])
+    r = calc.results
+    i, j, S = neighbor_list(s.positions, s.cell, s.pbc, cfg.r_max + 0.5)
+    ref = OracleMACE(model_dir=str(d))
+    E, F, voigt, ne, _ = ref.energy_forces_stress(s.positions, np.zeros(len(s), np.int64),
+                                                  np.stack([i, j]), S, s.cell)
+    dE = abs(r["energy"] - E) / abs(E)
+    dF = float(np.abs(r["forces"] - F).max())
+    dS = float(np.abs(r["stress"] - voigt).max() / np.abs(voigt).max())
+    print(f"calculator vs oracle: |dE|/|E|={dE:.2e} max|dF|={dF:.2e} stress rel={dS:.2e}")
+    assert dE <= 1e-6 and dF <= 1e-4 and dS <= 1e-5, (dE, dF, dS, r["stress"], voigt)
+    np.testing.assert_allclose(r["energies"], ne, rtol=0, atol=1e-5 * max(1.0, np.abs(ne).max()))
+
+
 def test_graph_replay_matches_eager(medium_zbl):
     """Captured step graphs: every replay, with eager steps and host synchronisations in
     between, equals the eager step bit for bit (the kernels are deterministic); new
@@ -463,7 +497,7 @@ def test_graph_replay_matches_eager(medium_zbl):
         out_d = torch.zeros(10 + 3 * N, dtype=torch.float64, device="cuda")
         eng.set_graphs(True)
         for _ in range(3):
-            out_d.zero_()
+            out_d.zero_()   # on torch's default (null) stream: the engine's blocking stream orders after it
             eng.step_device(pos_d.data_ptr(), out_d.data_ptr())
             eng.sync()
             out = out_d.cpu().numpy()
@@ -487,7 +521,8 @@ def test_split_products_match_fp32(arch, request):
             case.eng.set_split_products(split)
             got = case.run(s, stress=True)
             ref = case.reference(s, got["sp"], case.edges(), stress=True)
-            errs[split] = assert_parity(got, ref, len(s), stress=True, vol=abs(np.linalg.det(s.cell)))
+            errs[split] = assert_parity(got, ref, len(s), stress=True, vol=abs(np.linalg.det(s.cell)),
+                                        energy="per_atom" if arch == "large" else "relative")
     finally:
         case.eng.set_split_products(True)
     print(f"{arch}: fp32 products dE={errs[False][0]:.3g} dF={errs[False][1]:.3g}; "
@@ -517,6 +552,6 @@ def test_fused_tp_matches_separate_passes(arch, request):
     dF = float(np.abs(a["F"] - b["F"]).max())
     dv = float(np.abs(a["vir"] - b["vir"]).max())
     print(f"{arch}: fused vs separate dE={dE:.3g} dF={dF:.3g} dvir={dv:.3g}")
-    assert dE <= 1e-6 * max(abs(a["E"]), float(len(s))), dE
+    assert dE <= 1e-6 * abs(a["E"]), dE
     assert dF <= 1e-5, dF
     assert dv <= 1e-5 * max(1.0, float(np.abs(a["vir"]).max())), dv
