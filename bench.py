@@ -33,70 +33,87 @@ sys.path.insert(0, str(ROOT / "mace-mlx_amd"))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_MFMA_PEAK_TFS = 157.3     # MI355X dense fp32 matrix
+FP16_MFMA_PEAK_TFS = 2500.0    # MI355X dense fp16 / bf16 matrix
+RADIAL_H = 64                  # radial-MLP hidden width (last hidden layer -> TP weights)
 
 
-def peak_of(site: str, bound: str, ctx: dict) -> float:
-    """Roofline peak for a site: HBM bandwidth, or the matrix-core rate of its data type."""
-    return HBM_PEAK_GBS if bound == "hbm" else FP32_MFMA_PEAK_TFS
+def tp_bytes(name, lay, N, E, s, fused):
+    """Algorithmic HBM bytes of one edge-TP + scatter layer-pass (the benchmark's definition):
+
+        B_fwd = s (N D_in + E 16 + E W + N D_mid) + 4 (E + N + 1)
+        B_bwd = s (N D_mid + 2 N D_in + 2 E 16 + 2 E W) + 8 (E + N + 1)
+
+    with s = 4 bytes (2 for fp16 features) and W the TP weights per edge.  With the radial
+    MLP's output layer fused into the TP kernel (`fused`), the per-edge weights never reach
+    HBM: E W is replaced by E 64 (the last hidden activation) and the layer's flops are
+    counted separately (tp_flops)."""
+    W = RADIAL_H if fused else lay["wn"]
+    if name == "tp_fwd":
+        return s * (N * lay["din"] + E * 16 + E * W + N * lay["dmid"]) + 4 * (E + N + 1)
+    return s * (N * lay["dmid"] + 2 * N * lay["din"] + 2 * E * 16 + 2 * E * W) + 8 * (E + N + 1)
 
 
-def algorithmic_work(site: str, ctx: dict):
-    """(bound, amount per launch, unit) for a kernel site of the step.
+def tp_flops(lay, E, fused):
+    """Flops of the radial MLP's output layer inside a fused TP pass: w = h3 W3 (forward) or
+    dL/dh3 = dL/dw W3^T (VJP), 2 E 64 W each; 0 when the layer runs as its own pass."""
+    return 2 * E * RADIAL_H * lay["wn"] if fused else 0
 
-    Bytes count compulsory unique traffic (node arrays once, fp32, int32
-    indices); flops count multiply-adds as 2."""
-    N, E, C, nb, H = ctx["N"], ctx["E"], 128, ctx["nb"], 64
+
+def site_work(site: str, ctx: dict):
+    """(algorithmic bytes, algorithmic flops, flop peak TF/s) per launch of a launch site.
+
+    Bytes count compulsory unique traffic (node arrays once, int32 indices); flops count
+    multiply-adds as 2 and are priced on the matrix-core peak of the arithmetic type the
+    product computes in (fp32 for the float32 policy: the split-fp16 products emulate it)."""
+    N, E, C, nb, H = ctx["N"], ctx["E"], 128, ctx["nb"], RADIAL_H
+    half = ctx.get("half")
+    s = 2 if half else 4
+    fpk = FP16_MFMA_PEAK_TFS if half else FP32_MFMA_PEAK_TFS
     name, _, lyr = site.partition(".L")
     lay = ctx["layers"][int(lyr)] if lyr else None
     fused = ctx.get("fused")
-    tabw = 72 if lay and lay["lin"] >= 2 else 0  # M1 table entries per edge (l1 = 1 slots)
-    if name == "tp_fwd":
-        if fused:  # radial-MLP output layer inside: reads h3 (split planes + scale), writes w for the VJP
-            b = 4 * (N * lay["din"] + E * (16 + tabw) + E * lay["wn"] + N * lay["dmid"]) + E * (4 * H + 4)
-            return "hbm", b + 4 * (E + N + 1), "GB/s"
-        b = 4 * (N * lay["din"] + E * 16 + E * lay["wn"] + N * lay["dmid"]) + 4 * (E + N + 1)
-        return "hbm", b, "GB/s"
-    if name == "tp_bwd":
-        if fused:  # reads w, writes dL/dx rows (after the first layer), dL/dY and dL/dh3 partials
-            parts = 2 if lay["lin"] == 1 else 4
-            gx = E * lay["din"] if int(lyr) > 0 else 0
-            b = 4 * (N * lay["dmid"] + N * lay["din"] + E * (16 + tabw) + E * lay["wn"] + gx
-                     + E * 16 * parts + E * H * parts)
-            return "hbm", b + 8 * (E + N + 1), "GB/s"
-        b = 4 * (N * lay["dmid"] + N * lay["din"] + 2 * E * 16 + 2 * E * lay["wn"]) + 8 * (E + N + 1)
-        return "hbm", b, "GB/s"
-    if name == "tp_gather":  # segmented sum of the per-edge input-gradient rows
-        return "hbm", 4 * (E * lay["din"] + N * lay["din"]) + 4 * (N + 1), "GB/s"
-    if name == "mlp_hidden":  # three small layers
-        return "mfma", 2 * E * (nb * H + 2 * H * H), "TFLOP/s"
-    if name in ("mlp_out", "mlp_gh3"):
-        # w = h3 @ W3 and dL/dh3 = gw @ W3^T.  On fp16 matrix cores (split fp32 operands, or the
-        # float16 policy) the product needs at most a quarter of the time of the E x W stream it
-        # writes / reads, so the bound is HBM: that stream plus the E x 64 side
-        if ctx.get("half"):
-            return "hbm", 2 * E * lay["wn"] + 2 * E * H + (8 * E if name == "mlp_gh3" else 0), "GB/s"
-        if ctx.get("split"):
-            return "hbm", 4 * E * lay["wn"] + 4 * E * H + 4 * E, "GB/s"
-        return "mfma", 2 * E * H * lay["wn"], "TFLOP/s"
-    if name == "mlp_hidden_bwd":
-        # the three transposed products; with split products the forward layers are recomputed
-        # (no saved derivatives), doubling the work
-        return "mfma", 2 * E * (nb * H + 2 * H * H) * (2 if ctx.get("split") else 1), "TFLOP/s"
-    if name.startswith("linear") or name.startswith("skip"):
-        return "mfma", ctx["linear_flops"].get(site, 0), "TFLOP/s"
+    if name in ("tp_fwd", "tp_bwd"):
+        return tp_bytes(name, lay, N, E, s, fused), tp_flops(lay, E, fused), fpk
+    if name == "tp_gather":  # segmented sum of the per-edge input-gradient rows (implementation traffic)
+        return 4 * (E * lay["din"] + N * lay["din"]) + 4 * (N + 1), 0, fpk
+    if name == "mlp_hidden":  # three small layers: ef in, last hidden activation out
+        return E * (4 * nb + s * H), 2 * E * (nb * H + 2 * H * H), fpk
+    if name == "mlp_hidden_bwd":  # the three transposed products: dL/dh3 in, dL/def out (+ ef)
+        return E * (8 * nb + 4 * H), 2 * E * (nb * H + 2 * H * H), fpk
+    if name in ("mlp_out", "mlp_gh3"):  # w = h3 W3, dL/dh3 = dL/dw W3^T over the E x W stream
+        return s * E * (lay["wn"] + H), 2 * E * H * lay["wn"], fpk
+    if name.startswith("linear") or name.startswith("skip") or name.startswith("message_skip"):
+        f, b = ctx["linear_work"].get(site, (0, 0))
+        return b, f, fpk
     if name in ("sc_fwd", "sc_bwd"):
-        return "hbm", 4 * N * (16 * C + lay["dhid"]) * (2 if name == "sc_bwd" else 1), "GB/s"
+        return 4 * N * (16 * C + lay["dhid"]) * (2 if name == "sc_bwd" else 1), 0, fpk
     if name == "edge_fwd":
-        return "hbm", E * (8 + 12 + 16 + 16 * 4 + nb * 4 + 4) + N * 24, "GB/s"
+        return E * (8 + 12 + 16 + 16 * 4 + nb * 4 + 4) + N * 24, 0, fpk
     if name == "edge_bwd":
-        return "hbm", E * (16 + 16 * 4 + nb * 4 + 12 + 8), "GB/s"
+        return E * (16 + 16 * 4 + nb * 4 + 12 + 8), 0, fpk
     if name == "forces":
-        return "hbm", E * (12 * 2 + 8) + N * 24 + 8 * (N + 1), "GB/s"
-    return "hbm", 0, "GB/s"
+        return E * (12 * 2 + 8) + N * 24 + 8 * (N + 1), 0, fpk
+    return 0, 0, fpk
 
 
-def linear_flops(cfg_layers, N):
-    """2 * rows * K * Cout summed per linear site (all blocks of a layer)."""
+def roofline_of(site: str, ctx: dict, avg_ms: float):
+    """Roofline record of one launch: the binding bound is the larger of bytes / HBM peak
+    and flops / matrix peak; frac = that time / the measured launch time."""
+    b, f, fpk = site_work(site, ctx)
+    t = avg_ms * 1e-3
+    tb, tf = b / (HBM_PEAK_GBS * 1e9), f / (fpk * 1e12)
+    if tb >= tf:
+        rec = {"bound": "hbm", "achieved": b / t / 1e9 if t > 0 else 0.0, "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+    else:
+        rec = {"bound": "mfma", "achieved": f / t / 1e12 if t > 0 else 0.0, "peak": fpk, "unit": "TFLOP/s"}
+    rec.update(frac=max(tb, tf) / t if t > 0 else 0.0, algorithmic_bytes=int(b), algorithmic_flops=int(f),
+               hbm_frac=tb / t if t > 0 else 0.0, mfma_frac=tf / t if t > 0 else 0.0)
+    return rec
+
+
+def linear_work(cfg_layers, N):
+    """(flops, bytes) per linear site: 2 rows K Cout summed over the blocks of a layer; bytes =
+    the input and output node rows (fp32) plus the weights."""
     out = {}
     C = 128
     for l, lay in enumerate(cfg_layers):
@@ -105,10 +122,42 @@ def linear_flops(cfg_layers, N):
         msg = sum(2 * N * (2 * lo + 1) * nslot_by_l[lo] * C * C for lo in range(4))
         prod = sum(2 * N * (2 * b + 1) * C * C for b in range(lhid))
         skip = sum(2 * N * (2 * b + 1) * C * C for b in range(min(lin, lhid)))
-        out.update({f"linear_up.L{l}": up, f"linear_msg.L{l}": msg, f"linear_prod.L{l}": prod,
-                    f"skip.L{l}": skip, f"linear_up_bwd.L{l}": up, f"linear_msg_bwd.L{l}": msg,
-                    f"linear_prod_bwd.L{l}": prod, f"skip_bwd.L{l}": skip})
+        dint = 16 * C
+        by = {"up": 4 * N * 2 * lay["din"] + 4 * lin * C * C,
+              "msg": 4 * N * (lay["dmid"] + dint) + 4 * sum(nslot_by_l) * C * C,
+              "prod": 4 * N * (dint + 2 * lay["dhid"]) + 4 * 2 * lhid * C * C,
+              "skip": 4 * N * (lay["din"] + lay["dhid"]) + 4 * min(lin, lhid) * C * C}
+        for nm, f in (("linear_up", up), ("linear_msg", msg), ("linear_prod", prod), ("skip", skip)):
+            k = nm.split("_")[-1]
+            out[f"{nm}.L{l}"] = (f, by[k])
+            out[f"{nm}_bwd.L{l}"] = (f, by[k])
     return out
+
+
+def tp_scatter_summary(per_step, ctx):
+    """The edge TP + scatter kernels of a step (forward, VJP and the gather of the VJP's
+    per-edge rows, both layers) against (a) the benchmark's unfused compulsory bytes at HBM
+    peak (`hbm_frac_unfused_bytes`: the TP weights counted as an E x W stream, the
+    definition of the <= 60 % target) and (b) their own roofline with the radial MLP's
+    output layer fused in (`roofline_frac`: sum over sites of max(bytes / HBM peak,
+    flops / matrix peak) over the measured time)."""
+    sites = [k for k in per_step if k.split(".")[0] in ("tp_fwd", "tp_bwd", "tp_gather")]
+    t = sum(per_step[k][0] for k in sites) * 1e-3
+    if t <= 0:
+        return {"ms": 0.0, "hbm_frac_unfused_bytes": 0.0, "roofline_frac": 0.0}
+    s = 2 if ctx.get("half") else 4
+    unf = tmin = 0.0
+    for k in sites:
+        name, _, lyr = k.partition(".L")
+        if name == "tp_gather":
+            continue
+        lay = ctx["layers"][int(lyr)]
+        unf += tp_bytes(name, lay, ctx["N"], ctx["E"], s, False)
+        b, f, fpk = site_work(k, ctx)
+        tmin += max(b / (HBM_PEAK_GBS * 1e9), f / (fpk * 1e12))
+    return {"ms": round(t * 1e3, 4), "unfused_bytes": int(unf),
+            "hbm_frac_unfused_bytes": round(unf / t / (HBM_PEAK_GBS * 1e9), 4),
+            "roofline_frac": round(tmin / t, 4)}
 
 
 def load_traffic(site: str, workload: str):
@@ -172,18 +221,7 @@ def layer_shapes(dm):
     return layers
 
 
-def tp_scatter_frac(per_step, ctx):
-    """Edge TP + scatter kernels (forward, VJP, gather) against the compulsory bytes of both
-    passes of every layer: achieved GB/s / HBM peak."""
-    sites = [k for k in per_step if k.split(".")[0] in ("tp_fwd", "tp_bwd", "tp_gather")]
-    t = sum(per_step[k][0] for k in sites)
-    b = sum(algorithmic_work(k, ctx)[1] for k in sites if not k.startswith("tp_gather"))
-    return (b / (t * 1e-3) / 1e9) / HBM_PEAK_GBS if t > 0 else 0.0
-
-
-def measure_config(idx, steps, warmup, separate=False, graphs=None):
-    """Steady-state and rebuild step times plus per-site roofline for configuration idx."""
-    import torch
+def _setup(idx, separate=False, graphs=None):
     from mace_mlx_amd._ffi import Engine
     from mace_mlx_amd.device_model import build_device_model
     from mace_mlx_amd.model_io import random_init
@@ -197,51 +235,102 @@ def measure_config(idx, steps, warmup, separate=False, graphs=None):
         eng.set_fused_tp(False)
     if graphs is not None:
         eng.set_graphs(graphs)
-    s = bc.system
     zmap = {int(z): k for k, z in enumerate(dm.z_table)}
-    species = np.array([zmap[int(z)] for z in s.numbers], np.int32)
-    eng.set_system(species, s.cell, s.pbc, 0.5)
-    stress = "stress" in bc.properties
-    eng.step(s.positions, stress=stress)
-    N, E = len(s), len(eng.get_edges()[0])
-    pos_d = torch.from_numpy(np.ascontiguousarray(s.positions, dtype=np.float64)).cuda()
-    out_d = torch.zeros(10 + 3 * N, dtype=torch.float64, device="cuda")
-    for _ in range(warmup):
-        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress)
+    species = np.array([zmap[int(z)] for z in bc.system.numbers], np.int32)
+    eng.set_system(species, bc.system.cell, bc.system.pbc, 0.5)
+    return bc, weights, dm, eng, species
+
+
+def _timed(eng, pos_d, out_d, stress, steps, force_nl=False):
+    """Wall time per step of `steps` device-resident steps, bracketed by device synchronisation."""
+    import torch
     eng.sync()
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress)
+        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress, force_nl=force_nl)
     eng.sync()
-    ms = (time.perf_counter() - t0) / steps * 1e3
-    t0 = time.perf_counter()
-    for _ in range(3):
-        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress, force_nl=True)
-    eng.sync()
-    ms_nl = (time.perf_counter() - t0) / 3 * 1e3
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+def run_workload(idx, steps, warmup, separate=False, graphs=None, extras=False, launch_order=None):
+    """Measure one benchmark configuration: steady-state device-resident steps (neighbour
+    list cached), steps that rebuild the neighbour list, and a per-launch-site pass with HIP
+    events; with `extras` also the host-array path, the true-fp32 matrix-core variant and
+    the CPU-baseline inputs."""
+    import torch
+    bc, weights, dm, eng, species = _setup(idx, separate, graphs)
+    s = bc.system
+    stress = "stress" in bc.properties
+    E_host, _, F_host, _ = eng.step(s.positions, stress=stress)          # builds the neighbour list
+    edges = eng.get_edges()
+    N, E = len(s), len(edges[0])
+    pos_d = torch.from_numpy(np.ascontiguousarray(s.positions, dtype=np.float64)).cuda()
+    out_d = torch.zeros(10 + 3 * N, dtype=torch.float64, device="cuda")
+    torch.cuda.synchronize()
+    _timed(eng, pos_d, out_d, stress, warmup)
+    wall = _timed(eng, pos_d, out_d, stress, steps)
+    ms = wall / steps * 1e3
+    out = out_d.cpu().numpy()
+    assert abs(out[0] - E_host) <= 1e-9 * abs(E_host) and np.abs(out[10:].reshape(N, 3) - F_host).max() < 1e-9
+    res = {"workload": bc.name, "n_atoms": N, "n_edges": E,
+           "properties": "energy+forces+stress" if stress else "energy+forces", "feature_dtype": bc.dtype,
+           "ms_per_step": round(ms, 4), "atom_steps_per_s": round(N / ms * 1e3, 1), "_wall": wall}
+    if extras:
+        th = time.perf_counter()
+        for _ in range(steps):
+            eng.step(s.positions, stress=stress)
+        res["ms_per_step_host_arrays"] = round((time.perf_counter() - th) / steps * 1e3, 4)
+        if bc.dtype == "float32":   # the same step with every product on fp32 matrix cores
+            eng.set_split_products(False)
+            _timed(eng, pos_d, out_d, stress, 2)
+            res["ms_per_step_fp32_mfma"] = round(_timed(eng, pos_d, out_d, stress, steps) / steps * 1e3, 4)
+            eng.set_split_products(True)
     eng.set_profiling(True)
     for _ in range(steps):
         eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress)
-    eng.sync()
     kt = eng.kernel_times()
+    order = eng.launch_order()
     eng.set_profiling(False)
+    if launch_order:
+        Path(launch_order).parent.mkdir(parents=True, exist_ok=True)
+        Path(launch_order).write_text("\n".join(order) + "\n")
     layers = layer_shapes(dm)
-    ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_flops=linear_flops(layers, N),
-               half=bc.dtype == "float16", split=bc.dtype != "float16",
+    ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_work=linear_work(layers, N),
+               half=bc.dtype == "float16",
                fused=not separate and bc.dtype != "float16" and max(x["lin"] for x in layers) <= 2)
     per_step = {k: (v[0] / steps, v[1] // steps) for k, v in kt.items()}
     dom = max(per_step, key=lambda k: per_step[k][0])
-    b, a, u = algorithmic_work(dom, ctx)
-    t, n = per_step[dom]
-    ach = (a / max(n, 1)) / (t / max(n, 1) * 1e-3) / (1e9 if b == "hbm" else 1e12)
-    frac = ach / peak_of(dom, b, ctx)
-    res = {"workload": bc.name, "n_atoms": N, "n_edges": E, "properties": "+".join(bc.properties),
-           "feature_dtype": bc.dtype, "ms_per_step": round(ms, 4), "ms_per_step_nl_rebuild": round(ms_nl, 4),
-           "atom_steps_per_s": round(N / ms * 1e3, 1), "dominant": dom, "dominant_frac": round(frac, 4),
-           "tp_scatter_hbm_frac": round(tp_scatter_frac(per_step, ctx), 4)}
+    launches = max(per_step[dom][1], 1)
+    avg_ms = per_step[dom][0] / launches
+    rl = roofline_of(dom, ctx, avg_ms)
+    traffic = load_traffic(dom, bc.name)
+    roof = {"bound": rl["bound"], "achieved": round(rl["achieved"], 3), "peak": rl["peak"], "unit": rl["unit"],
+            "frac": round(rl["frac"], 4), "traffic": traffic, "kernel": dom, "avg_launch_ms": round(avg_ms, 5),
+            "algorithmic_bytes": rl["algorithmic_bytes"], "algorithmic_flops": rl["algorithmic_flops"],
+            "hbm_frac": round(rl["hbm_frac"], 4), "mfma_frac": round(rl["mfma_frac"], 4),
+            "traffic_over_algorithmic_bytes": round(traffic / rl["algorithmic_bytes"], 2) if traffic else None,
+            "boundary": ("radial-MLP output layer fused into the TP kernels: E*W -> E*64 in the TP bytes, "
+                         "2*E*64*W flops added" if ctx["fused"] else "separate radial-MLP output pass")}
+    res.update(dominant=dom, dominant_frac=roof["frac"], roofline=roof,
+               tp_scatter=tp_scatter_summary(per_step, ctx), per_step=per_step, ctx=ctx)
+    # steps that rebuild the neighbour list (the reference's benchmark.py:168-style number)
+    nrb = max(3, steps // 4)
+    res["ms_per_step_nl_rebuild"] = round(_timed(eng, pos_d, out_d, stress, nrb, force_nl=True) / nrb * 1e3, 4)
+    res["_edges"], res["_species"], res["_bc"], res["_weights"] = edges, species, bc, weights
     del eng, pos_d, out_d
     torch.cuda.empty_cache()
     return res
+
+
+def kernel_table(per_step, ctx):
+    tot = sum(v[0] for v in per_step.values())
+    print(f"{'site':24s} {'ms/step':>9s} {'share':>6s} {'launch':>6s}  roofline (binding bound)", file=sys.stderr)
+    for k, (t, n) in sorted(per_step.items(), key=lambda kv: -kv[1][0]):
+        rl = roofline_of(k, ctx, t / max(n, 1))
+        print(f"{k:24s} {t:9.4f} {t / tot * 100:5.1f}% {n:6d}  {rl['achieved']:9.2f} {rl['unit']} "
+              f"({rl['frac'] * 100:.1f}% of {rl['bound']})", file=sys.stderr)
 
 
 def main():
@@ -257,21 +346,32 @@ def main():
     ap.add_argument("--graphs", choices=("on", "off"), default=None,
                     help="replay the step through captured HIP graphs (on) or launch it eagerly (off); "
                          "default: the engine's default")
-    ap.add_argument("--sweep", action="store_true",
-                    help="also measure every benchmark configuration (table on stderr, 'sweep' in the JSON)")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the bounded measurement of every benchmark configuration ('sweep' in the JSON)")
     ap.add_argument("--copy-calib-mb", type=float, default=0.0,
                     help="run a plain device copy of this size first (rocprof counter calibration)")
+    ap.add_argument("--launch-order", default=None,
+                    help="write the launch site of every dispatch of one profiled step to this file")
+    ap.add_argument("--json-out", default=None, help="also write the JSON line to this file")
+    ap.add_argument("--summarize", default=None, metavar="DIR",
+                    help="no GPU: summarise a measurement directory (launch_order.txt, bench.json, rocprofv3 "
+                         "trace/ and pmc_fetch/ pmc_write/ csv) into profiles/")
     args = ap.parse_args()
+    if args.summarize:
+        from mace_mlx_amd.rocprof_sites import summarize
+        cmd = {}
+        cf = Path(args.summarize) / "commands.json"
+        if cf.exists():
+            cmd = json.loads(cf.read_text())
+        r = summarize(args.summarize, str(ROOT / "profiles"), args.copy_calib_mb or 256.0, cmd)
+        print(json.dumps({"sites": len(r["sites"]), "steps": r["steps"], "traffic": "traffic" in r}))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
               "multi-GPU sharding is design-only", file=sys.stderr)
         sys.exit(2)
 
     import torch
-    from mace_mlx_amd._ffi import Engine
-    from mace_mlx_amd.device_model import build_device_model
-    from mace_mlx_amd.model_io import random_init
-    from mace_mlx_amd.systems import make_config
     if args.copy_calib_mb > 0:
         # counter calibration: one elementwise kernel that reads and writes exactly
         # copy_calib_mb MiB each (b = 2 a); its FETCH_SIZE / WRITE_SIZE give the scale
@@ -283,130 +383,62 @@ def main():
         torch.cuda.synchronize()
         del a, b
 
-    bc = make_config(args.config)
-    weights = random_init(bc.model, 0)
-    dm = build_device_model(bc.model, weights, dtype=bc.dtype)
-    eng = Engine(0)
-    eng.load_model(dm)
-    if args.separate_mlp_out:
-        eng.set_fused_tp(False)
     graphs = None if args.graphs is None else args.graphs == "on"
-    if graphs is not None:
-        eng.set_graphs(graphs)
-    s = bc.system
-    zmap = {int(z): k for k, z in enumerate(dm.z_table)}
-    species = np.array([zmap[int(z)] for z in s.numbers], np.int32)
-    eng.set_system(species, s.cell, s.pbc, 0.5)
-    stress = "stress" in bc.properties
-    E_host, _, F_host, _ = eng.step(s.positions, stress=stress)          # builds the neighbour list
-    edges = eng.get_edges()
-    N, E = len(s), len(edges[0])
-
-    pos_d = torch.from_numpy(np.ascontiguousarray(s.positions, dtype=np.float64)).cuda()
-    out_d = torch.zeros(10 + 3 * N, dtype=torch.float64, device="cuda")
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress)
-    eng.sync()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress)
-    eng.sync()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms = (t1 - t0) / args.steps * 1e3
-    out = out_d.cpu().numpy()
-    assert abs(out[0] - E_host) <= 1e-9 * abs(E_host) and np.abs(out[10:].reshape(N, 3) - F_host).max() < 1e-9
-
-    # host-array path (PCIe-inclusive, as the ASE calculator uses it)
-    th = time.perf_counter()
-    for _ in range(args.steps):
-        eng.step(s.positions, stress=stress)
-    ms_host = (time.perf_counter() - th) / args.steps * 1e3
-
-    # per-kernel pass
-    eng.set_profiling(True)
-    for _ in range(args.steps):
-        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress)
-    kt = eng.kernel_times()
-    eng.set_profiling(False)
-    layers = layer_shapes(dm)
-    ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_flops=linear_flops(layers, N),
-               half=bc.dtype == "float16", split=bc.dtype != "float16",
-               fused=not args.separate_mlp_out and bc.dtype != "float16"
-               and max(x["lin"] for x in layers) <= 2)
-    per_step = {k: (v[0] / args.steps, v[1] // args.steps) for k, v in kt.items()}
-    dom = max(per_step, key=lambda k: per_step[k][0])
-    bound, amount, unit = algorithmic_work(dom, ctx)
-    launches = max(per_step[dom][1], 1)
-    avg_ms = per_step[dom][0] / launches
-    if bound == "hbm":
-        achieved = amount / launches / (avg_ms * 1e-3) / 1e9 if launches > 1 else amount / (avg_ms * 1e-3) / 1e9
-    else:
-        achieved = amount / launches / (avg_ms * 1e-3) / 1e12
-    peak = peak_of(dom, bound, ctx)
-    roofline = {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-                "frac": round(achieved / peak, 4), "traffic": load_traffic(dom, bc.name), "kernel": dom,
-                "avg_launch_ms": round(avg_ms, 5), "tp_scatter_hbm_frac": round(tp_scatter_frac(per_step, ctx), 4)}
+    head = run_workload(args.config, args.steps, args.warmup, args.separate_mlp_out, graphs, extras=True,
+                        launch_order=args.launch_order)
     if args.kernel_table:
-        tot = sum(v[0] for v in per_step.values())
-        print(f"{'site':24s} {'ms/step':>9s} {'share':>6s} {'launch':>6s}  roofline", file=sys.stderr)
-        for k, (t, n) in sorted(per_step.items(), key=lambda kv: -kv[1][0]):
-            b, a, u = algorithmic_work(k, ctx)
-            per = t / max(n, 1) * 1e-3
-            ach = (a / max(n, 1)) / per / (1e9 if b == "hbm" else 1e12) if a else 0.0
-            pk = peak_of(k, b, ctx)
-            print(f"{k:24s} {t:9.4f} {t / tot * 100:5.1f}% {n:6d}  {ach:9.2f} {u} ({ach / pk * 100:.1f}% of {b})",
-                  file=sys.stderr)
-
-    # neighbour-list rebuild included (the reference's benchmark.py:168-style number)
-    eng.sync()
-    tr = time.perf_counter()
-    nrb = max(3, args.steps // 4)
-    for _ in range(nrb):
-        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), stress=stress, force_nl=True)
-    eng.sync()
-    ms_rebuild = (time.perf_counter() - tr) / nrb * 1e3
-    del pos_d, out_d
-
+        kernel_table(head["per_step"], head["ctx"])
     sweep = None
-    if args.sweep:
-        del eng
-        sweep = [measure_config(i, max(5, args.steps // 2), args.warmup, args.separate_mlp_out, graphs)
-                 for i in range(5)]
-        print(f"{'config':16s} {'N':>6s} {'E':>9s} {'ms/step':>9s} {'+NL ms':>8s} {'atom-steps/s':>13s}  "
-              f"dominant site (frac of its roofline)   TP+scatter HBM frac", file=sys.stderr)
+    if not args.no_sweep:
+        sweep = []
+        for i in range(5):
+            r = head if i == args.config else run_workload(i, max(5, args.steps // 2), args.warmup,
+                                                           args.separate_mlp_out, graphs)
+            sweep.append({k: r[k] for k in ("workload", "n_atoms", "n_edges", "properties", "feature_dtype",
+                                             "ms_per_step", "ms_per_step_nl_rebuild", "atom_steps_per_s",
+                                             "dominant", "dominant_frac")}
+                         | {"tp_scatter_hbm_frac_unfused_bytes": r["tp_scatter"]["hbm_frac_unfused_bytes"],
+                            "tp_scatter_roofline_frac": r["tp_scatter"]["roofline_frac"]})
+        print(f"{'config':24s} {'N':>6s} {'E':>9s} {'ms/step':>9s} {'+NL ms':>8s} {'atom-steps/s':>13s}  "
+              f"dominant site (frac of its roofline)   TP+scatter HBM frac (unfused bytes)", file=sys.stderr)
         for r in sweep:
-            print(f"{r['workload']:16s} {r['n_atoms']:6d} {r['n_edges']:9d} {r['ms_per_step']:9.3f} "
+            print(f"{r['workload']:24s} {r['n_atoms']:6d} {r['n_edges']:9d} {r['ms_per_step']:9.3f} "
                   f"{r['ms_per_step_nl_rebuild']:8.3f} {r['atom_steps_per_s']:13.0f}  "
-                  f"{r['dominant']:18s} ({r['dominant_frac']:.3f})   {r['tp_scatter_hbm_frac']:.3f}", file=sys.stderr)
+                  f"{r['dominant']:18s} ({r['dominant_frac']:.3f})   "
+                  f"{r['tp_scatter_hbm_frac_unfused_bytes']:.3f}", file=sys.stderr)
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(bc, weights, edges, species)
+    bc = head["_bc"]
+    cpu = None if args.no_cpu_baseline else cpu_baseline(bc, head["_weights"], head["_edges"], head["_species"])
+    N, E = head["n_atoms"], head["n_edges"]
     line = {
         "metric": "ms per energy+forces step (Si1000, medium arch, fp32); atom-steps/sec",
-        "value": round(N * args.steps / (t1 - t0), 1),
+        "value": round(N * args.steps / head["_wall"], 1),
         "unit": "atom-steps/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
-        "ms_per_step_host_arrays": round(ms_host, 4),
-        "ms_per_step_nl_rebuild": round(ms_rebuild, 4),
+        "ms_per_step": head["ms_per_step"],
+        "ms_per_step_host_arrays": head["ms_per_step_host_arrays"],
+        "ms_per_step_nl_rebuild": head["ms_per_step_nl_rebuild"],
+        "ms_per_step_fp32_mfma": head.get("ms_per_step_fp32_mfma"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32" if bc.dtype == "float32" else "fp16 features / fp32 accumulation",
         "data": "synthetic (seeded lattice + rattle, random-init weights)",
-        "config": {"workload": bc.name, "n_atoms": N, "n_edges": E,
-                   "properties": "energy+forces+stress" if stress else "energy+forces",
+        "config": {"workload": bc.name, "n_atoms": N, "n_edges": E, "properties": head["properties"],
                    "neighbour_list": "cached (skin 0.5)"},
-        "roofline": roofline,
+        "roofline": head["roofline"],
+        "tp_scatter": head["tp_scatter"],
         "cpu_baseline": cpu,
     }
     if sweep is not None:
         line["sweep"] = sweep
-    print(json.dumps(line))
+    text = json.dumps(line)
+    if args.json_out:
+        Path(args.json_out).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.json_out).write_text(text + "\n")
+    print(text)
 
 
 if __name__ == "__main__":
