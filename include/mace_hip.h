@@ -153,6 +153,24 @@ int mace_get_edges(mace_ctx* ctx, int64_t capacity, int32_t* sender, int32_t* re
 int mace_step_device(mace_ctx* ctx, const double* d_positions, uint32_t flags, double* d_out);
 int mace_sync(mace_ctx* ctx);
 
+/* mace_step_device for callers that cannot allocate device memory: code that captures
+ * the step into its own HIP graph, tight serving / MD loops, harnesses that forbid
+ * allocation.  No counterpart in the reference.  Same arguments and results as
+ * mace_step_device; the call allocates and frees nothing (no hipMalloc / hipFree, no
+ * event creation, no graph capture of its own: the step's kernels are launched one by one
+ * on the context's stream, so a caller may capture them).  The per-block energy and
+ * virial partials come from a fixed per-device array of 2 MiB inside the library
+ * ((ceil(n_atoms / 4) + 1) + 9 ceil(n_edges / 256) doubles must fit 262144: about 7
+ * million edges), which every call on that device shares and which keeps the last
+ * call's contents; calls that overlap on one device (several contexts, several streams)
+ * race on it.  Everything else uses the context's buffers, sized by mace_set_system /
+ * mace_set_batch and the last neighbour-list build, so the neighbour list must exist
+ * (built by mace_step or mace_step_device) and is never rebuilt here: the caller keeps
+ * every atom within skin/2 of where it was built.  Errors: MACE_ERR_STATE without a
+ * neighbour list or with profiling on; MACE_ERR_INVALID for MACE_STEP_FORCE_NL or a
+ * system beyond the array's size. */
+int mace_step_device_noalloc(mace_ctx* ctx, const double* d_positions, uint32_t flags, double* d_out);
+
 /* Per-launch-site device timing (HIP events around every kernel launch of the
  * step, on the context's stream).  Enabling adds two event records per launch.
  * mace_get_kernel_times synchronises, then reports for each site its name

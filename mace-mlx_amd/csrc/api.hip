@@ -10,6 +10,7 @@
 #include <cstring>
 #include <functional>
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -19,6 +20,14 @@
 using namespace mace;
 
 thread_local int64_t mace::g_dispatches = 0;
+
+// Scratch of mace_step_device_noalloc: the per-block energy partials of the readout
+// (ceil(N / 4) + 1 doubles) followed by the per-block virial partials of the edge VJP
+// (9 ceil(E / 256) doubles).  One copy per device, held until the process ends.  Host
+// code never uses the name: its device address, looked up once per device with
+// hipGetSymbolAddress, is kept in g_scratch_ptr.
+constexpr size_t kScratchDoubles = size_t(1) << 18;  // 2 MiB
+static __device__ __align__(256) double scratch[kScratchDoubles];
 
 namespace {
 
@@ -45,6 +54,9 @@ struct DBuf {
 };
 
 std::string g_fail_msg;
+
+std::mutex g_scratch_mu;
+std::vector<double*> g_scratch_ptr;  // per device ordinal: address of `scratch` there
 
 // partials of dL/dY and dL/dh3 per edge: the receiver VJP writes one per
 // channel half; the fused TP VJP one per (input degree, 64-channel slice)
@@ -194,6 +206,7 @@ struct mace_ctx {
   std::vector<Pending> pending;
   std::map<std::string, std::pair<double, int64_t>> prof_acc;
   std::vector<std::string> launch_log;  // site of every dispatch of the last profiled step
+  double* scratch = nullptr;            // this device's `scratch` (mace_step_device_noalloc)
 };
 
 namespace {
@@ -212,6 +225,19 @@ int guard(mace_ctx* ctx, const std::function<void()>& fn) {
 }
 
 void set_device(mace_ctx* c) { HIPCHK(hipSetDevice(c->device)); }
+
+// Device address of `scratch` on `device` (current), looked up on the first call per device.
+double* scratch_on(int device) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if ((int)g_scratch_ptr.size() <= device) g_scratch_ptr.resize(device + 1, nullptr);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    HIPCHK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) fail(MACE_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[device] = static_cast<double*>(p);
+  }
+  return g_scratch_ptr[device];
+}
 
 size_t prof_event(mace_ctx* c) {
   if (c->ev_used == c->ev_pool.size()) {
@@ -978,7 +1004,7 @@ void run_captured(mace_ctx* c, mace_ctx::StepGraph& g, const void* a, const void
   HIPCHK(hipGraphLaunch(g.exec, c->stream));
 }
 
-void forward(mace_ctx* c, const double* pos, double* out) {
+void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
   if (c->profiling) c->launch_log.clear();  // a step starts here
   hipStream_t st = c->stream;
   const int N = c->N;
@@ -1103,14 +1129,14 @@ void forward(mace_ctx* c, const double* pos, double* out) {
   Site s(c, "energy_readout");
   launch_energy_readout(st, N, c->species.p, c->e0.p, c->rowptr.p, c->dims.has_zbl ? c->zbl_e.p : nullptr, L, hs,
                         lds, ros, c->layers[L - 1].ro1.p, c->layers[L - 1].ro2.p, c->gh0.p, c->layers[L - 1].dhid,
-                        c->node_e.p, c->e_part.p, half);
+                        c->node_e.p, e_part, half);
   if (c->G > 1) {
     Site s2(c, "graph_energy");
     launch_graph_energy(st, c->G, c->gptr.p, c->node_e.p, c->eg.p);
   }
 }
 
-void backward(mace_ctx* c, bool stress, double* out) {
+void backward(mace_ctx* c, bool stress, double* out, const double* e_part, double* vir_part) {
   hipStream_t st = c->stream;
   const int N = c->N;
   const int64_t E = c->E;
@@ -1246,16 +1272,16 @@ void backward(mace_ctx* c, bool stress, double* out) {
     Site s(c, "edge_bwd");
     launch_edge_bwd(st, E, c->sender.p, c->receiver.p, c->species.p, c->bessel_w.p, c->zbl_z.p, c->zbl_cov.p,
                     c->ag_cov.p, fp,
-                    c->geom.p, c->gY.p, gyp, c->gef.p, c->gv.p, stress ? c->vir_part.p : nullptr);
+                    c->geom.p, c->gY.p, gyp, c->gef.p, c->gv.p, stress ? vir_part : nullptr);
   }
   {
     Site s(c, "forces");
     launch_forces(st, N, c->rowptr.p, c->rowptr_s.p, c->perm_s.p, c->gv.p, out + 10,
-                  (stress && E > 0) ? nullptr : out + 1, c->e_part.p, out);
+                  (stress && E > 0) ? nullptr : out + 1, e_part, out);
   }
   if (stress && E > 0) {
     Site s(c, "virial");
-    launch_virial_reduce(st, c->vir_part.p, (int)((E + 255) / 256), out + 1);
+    launch_virial_reduce(st, vir_part, (int)((E + 255) / 256), out + 1);
   }
   if (stress && c->G > 1) {
     Site s(c, "graph_virial");
@@ -1280,6 +1306,7 @@ int mace_create(int32_t device, mace_ctx** out) {
     HIPCHK(hipGetDeviceCount(&n));
     if (device < 0 || device >= n) fail(MACE_ERR_INVALID, "device %d out of range (%d devices)", device, n);
     set_device(c);
+    c->scratch = scratch_on(device);
     // A blocking stream: its work is ordered with the null stream's (PyTorch's default
     // stream, and the synchronous copies of this library), so positions written there
     // before mace_step_device are seen by the step without an explicit wait.
@@ -1542,9 +1569,10 @@ int mace_step(mace_ctx* c, const double* positions, uint32_t flags, double* ener
     if (c->last_nl) build_nl(c, positions);
     HIPCHK(hipEventRecord(c->ev[1], st));
     ensure_embed(c);
-    run_captured(c, c->g_fwd, c->pos.p, c->out.p, 0, [&] { forward(c, c->pos.p, c->out.p); });
+    run_captured(c, c->g_fwd, c->pos.p, c->out.p, 0, [&] { forward(c, c->pos.p, c->out.p, c->e_part.p); });
     HIPCHK(hipEventRecord(c->ev[2], st));
-    run_captured(c, c->g_bwd, c->out.p, nullptr, stress, [&] { backward(c, stress, c->out.p); });
+    run_captured(c, c->g_bwd, c->out.p, nullptr, stress,
+                 [&] { backward(c, stress, c->out.p, c->e_part.p, c->vir_part.p); });
     HIPCHK(hipEventRecord(c->ev[3], st));
     HIPCHK(hipMemcpyAsync(c->out_pinned, c->out.p, (10 + 3 * (size_t)N) * sizeof(double), hipMemcpyDeviceToHost, st));
     if (node_energy && N > 0)
@@ -1615,8 +1643,38 @@ int mace_step_device(mace_ctx* c, const double* d_positions, uint32_t flags, dou
     }
     const bool stress = (flags & MACE_STEP_STRESS) != 0;
     ensure_embed(c);
-    run_captured(c, c->g_fwd, d_positions, d_out, 0, [&] { forward(c, d_positions, d_out); });
-    run_captured(c, c->g_bwd, d_out, nullptr, stress, [&] { backward(c, stress, d_out); });
+    run_captured(c, c->g_fwd, d_positions, d_out, 0, [&] { forward(c, d_positions, d_out, c->e_part.p); });
+    run_captured(c, c->g_bwd, d_out, nullptr, stress,
+                 [&] { backward(c, stress, d_out, c->e_part.p, c->vir_part.p); });
+  });
+}
+
+int mace_step_device_noalloc(mace_ctx* c, const double* d_positions, uint32_t flags, double* d_out) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    if (!c->system_ready) fail(MACE_ERR_STATE, "system not set");
+    if ((c->N > 0 && !d_positions) || !d_out) fail(MACE_ERR_INVALID, "NULL device pointer");
+    if (flags & MACE_STEP_FORCE_NL)
+      fail(MACE_ERR_INVALID, "mace_step_device_noalloc never rebuilds the neighbour list (MACE_STEP_FORCE_NL)");
+    if (!c->nl_valid)
+      fail(MACE_ERR_STATE, "no neighbour list: build it with mace_step or mace_step_device first");
+    if (c->profiling) fail(MACE_ERR_STATE, "per-launch profiling is on (it creates events): switch it off");
+    if (!c->scratch) fail(MACE_ERR_STATE, "scratch address not set up for this context's device");
+    const int64_t E = c->E;
+    const size_t e_n = (size_t)((c->N + 3) / 4) + 1;
+    const size_t v_n = 9 * (size_t)((E + 255) / 256);
+    if (e_n + v_n > kScratchDoubles)
+      fail(MACE_ERR_INVALID,
+           "system too large for mace_step_device_noalloc: %d atoms and %lld edges need %zu scratch doubles, "
+           "the maximum is %zu (use mace_step_device)",
+           c->N, (long long)E, e_n + v_n, kScratchDoubles);
+    set_device(c);
+    const bool stress = (flags & MACE_STEP_STRESS) != 0;
+    double* e_part = c->scratch;      // every block writes its own slot: nothing to clear
+    double* vir_part = c->scratch + e_n;
+    ensure_embed(c);
+    forward(c, d_positions, d_out, e_part);
+    backward(c, stress, d_out, e_part, vir_part);
   });
 }
 

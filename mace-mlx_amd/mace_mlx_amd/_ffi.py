@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "mace_set_fused_tp",
     "mace_set_batch", "mace_step_batch",
     "mace_get_launch_order",
+    "mace_step_device_noalloc",
 )
 
 
@@ -87,6 +88,7 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
         "mace_get_edges": (ctypes.c_int, [P, I64, P, P, P, ctypes.POINTER(I64)]),
         "mace_get_timings": (ctypes.c_int, [P, P, I32]),
         "mace_step_device": (ctypes.c_int, [P, P, U32, P]),
+        "mace_step_device_noalloc": (ctypes.c_int, [P, P, U32, P]),
         "mace_sync": (ctypes.c_int, [P]),
         "mace_set_profiling": (ctypes.c_int, [P, I32]),
         "mace_set_graphs": (ctypes.c_int, [P, I32]),
@@ -241,6 +243,13 @@ class Engine:
         flags = STEP_FORCES | (STEP_STRESS if stress else 0) | (STEP_FORCE_NL if force_nl else 0)
         self._check(self._lib.mace_step_device(self._h, ctypes.c_void_p(d_positions), flags,
                                                ctypes.c_void_p(d_out)))
+
+    def step_device_noalloc(self, d_positions: int, d_out: int, stress: bool = False) -> None:
+        """mace_step_device without any device allocation (see mace_step_device_noalloc):
+        needs a neighbour list built by a previous step; launches eagerly."""
+        flags = STEP_FORCES | (STEP_STRESS if stress else 0)
+        self._check(self._lib.mace_step_device_noalloc(self._h, ctypes.c_void_p(d_positions), flags,
+                                                       ctypes.c_void_p(d_out)))
 
     def sync(self) -> None:
         self._check(self._lib.mace_sync(self._h))
