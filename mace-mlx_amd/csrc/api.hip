@@ -1018,7 +1018,9 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
     Site s(c, "edge_fwd");
     launch_edge_fwd(st, E, pos, c->sender.p, c->receiver.p, c->shifts.p, c->species.p, c->bessel_w.p, c->zbl_z.p,
                     c->zbl_cov.p, c->ag_cov.p, fp, c->G > 1 ? c->gcell.p : nullptr, c->gid.p, c->geom.p, c->Y.p,
-                    c->ef.p, c->zbl_e.p, c->Mt.p, c->mts, c->mts > 0 ? tp_table_entries(c->max_lin) : 0);
+                    c->ef.p, c->zbl_e.p, c->Mt.p, c->mts,
+                    // the fused TP kernels build their tables on chip from Y
+                    (c->mts > 0 && !fused) ? tp_table_entries(c->max_lin) : 0);
   }
   for (size_t l = 0; l < c->layers.size(); ++l) {
     Layer& L = c->layers[l];

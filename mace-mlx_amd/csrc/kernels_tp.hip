@@ -55,6 +55,29 @@ MACE_TP_TRAITS(3)
 
 constexpr int MT_M2 = TP3_M1_NE;  // offset of the l1 = 2 table inside an Mt row
 
+// The CG terms of each M1 entry q (M1[q] = sum over terms of Y[j] v), padded to two
+// with (j, v) = (0, 0): a table a lane indexes with its own entry number.
+struct M1Terms {
+  int j[TP3_M1_NE][2];
+  float v[TP3_M1_NE][2];
+};
+constexpr int m1_max_terms() {
+  int m = 0;
+  for (int q = 0; q < TP3_M1_NE; ++q) m = TP3_M1_START[q + 1] - TP3_M1_START[q] > m ? TP3_M1_START[q + 1] - TP3_M1_START[q] : m;
+  return m;
+}
+static_assert(m1_max_terms() <= 2, "M1 entries with more than two CG terms");
+constexpr M1Terms make_m1_terms() {
+  M1Terms t{};
+  for (int q = 0; q < TP3_M1_NE; ++q)
+    for (int x = TP3_M1_START[q]; x < TP3_M1_START[q + 1]; ++x) {
+      t.j[q][x - TP3_M1_START[q]] = TP3_M1_J[x];
+      t.v[q][x - TP3_M1_START[q]] = TP3_M1_V[x];
+    }
+  return t;
+}
+__constant__ const M1Terms kM1Terms = make_m1_terms();
+
 static_assert(TP2_K1 == TP3_K1, "shared M1 layout");
 
 // Inputs of one edge for one channel, loaded ahead of use.
@@ -648,8 +671,24 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   const int64_t elast = a.E - 1;  // E >= 1 whenever a step runs
   constexpr int TY = L1 == 0 ? 16 : 0, TS = TY + (L1 == 1 ? TP3_M1_NE : 0), TSP = (TS + 3) & ~3;
   constexpr int TH = (TS + 63) / 64;
+  // entries of a table row a lane loads: l1 = 0, the Y row itself; l1 = 1, Y component l & 15,
+  // from which the M1 row is built in LDS (m1_row_entry)
+  constexpr int TL = L1 == 1 ? 1 : TH;
   static_assert(TS <= 128 && L1 <= 1, "table rows of up to 128 entries");
   float* tb = stab + wv * EPW * TSP;  // this wave's table rows (Y for l1 = 0 slots, M1 for l1 = 1)
+  float* yb = stab + XW * EPW * TSP + wv * EPW * 16;  // l1 = 1: this wave's Y rows
+  // l1 = 1: the CG terms (at most two) of the M1 entries q = l + 64 h this lane builds
+  int mj[TH][2];
+  float mv[TH][2];
+#pragma unroll
+  for (int h = 0; h < TH; ++h) {
+    const int q = min(l + 64 * h, TP3_M1_NE - 1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      mj[h][t] = L1 == 1 ? kM1Terms.j[q][t] : 0;
+      mv[h][t] = L1 == 1 ? kM1Terms.v[q][t] : 0.f;
+    }
+  }
   // The TC h3 rows of a step's tile (hi and lo planes) are fetched once per block,
   // TC / 2 bytes per thread, and staged in LDS (double-buffered, written before the
   // barrier of the step before their use); each wave then reads its B fragments
@@ -665,7 +704,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
     hv h;               // this thread's share of the step's h3 tile
     float hinv;         // inverse scale of its row
     float x[EPW][NX];   // sender rows of the wave's edges
-    float t[EPW][TH];   // their table rows (this lane's entries)
+    float t[EPW][TL];   // their table rows (this lane's entries; l1 = 1: Y components)
     int snd[EPW];       // sender indices
   };
   Slot s0, s1;
@@ -689,10 +728,11 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 #pragma unroll
       for (int i = 0; i < NX; ++i) S.x[b][i] = xs[NC * i];
       const int64_t e = min<int64_t>(beg + EPW * j + b, elast);
+      if constexpr (L1 == 1) {
+        S.t[b][0] = Y[e * 16 + (l & 15)];
+      } else {
 #pragma unroll
-      for (int h = 0; h < TH; ++h) {
-        const int i = min(l + 64 * h, TS - 1);
-        S.t[b][h] = i < TY ? Y[e * 16 + i] : Mt[e * a.mts + i - TY];
+        for (int h = 0; h < TH; ++h) S.t[b][h] = Y[e * 16 + min(l + 64 * h, TS - 1)];
       }
     }
   };
@@ -734,11 +774,25 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
     }
     store_h(j + 1, Snext);  // its last readers (step j - 1) are past the previous barrier
     __syncthreads();
+    if constexpr (L1 == 1) {  // M1 rows from the Y rows: the terms and order of k_edge_fwd
 #pragma unroll
-    for (int b = 0; b < EPW; ++b)
+      for (int b = 0; b < EPW; ++b)
+        if (l < 16) yb[16 * b + l] = S.t[b][0];
+      wave_sync();
 #pragma unroll
-      for (int h = 0; h < TH; ++h)
-        if (l + 64 * h < TS) tb[b * TSP + l + 64 * h] = S.t[b][h];
+      for (int b = 0; b < EPW; ++b)
+#pragma unroll
+        for (int h = 0; h < TH; ++h)
+          if (l + 64 * h < TS)
+            tb[b * TSP + l + 64 * h] =
+                fmaf(yb[16 * b + mj[h][1]], mv[h][1], fmaf(yb[16 * b + mj[h][0]], mv[h][0], 0.f));
+    } else {
+#pragma unroll
+      for (int b = 0; b < EPW; ++b)
+#pragma unroll
+        for (int h = 0; h < TH; ++h)
+          if (l + 64 * h < TS) tb[b * TSP + l + 64 * h] = S.t[b][h];
+    }
     wave_sync();
     load_snd(j + 3, Snext);  // Snext's step j + 1 rows are already in flight
 #pragma unroll
@@ -805,7 +859,7 @@ __global__ void __launch_bounds__(64 * XW, 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_
   static_assert(LIN <= 2, "three input blocks are not fused");
   constexpr int TC = XW * EPW;
   __shared__ __align__(16) float sw[2 * TC * (64 * gmax<LIN>() + 4)];
-  __shared__ __align__(16) float stab[XW * EPW * (LIN == 1 ? 16 : TP3_M1_NE)];
+  __shared__ __align__(16) float stab[XW * EPW * (LIN == 1 ? 16 : TP3_M1_NE + 16)];  // table rows + Y rows
   __shared__ __align__(16) _Float16 hbuf[2 * 2 * TC * 72];  // [step][hi, lo][tile column][64 + pad]
   __shared__ float hiv[2 * TC];
   if constexpr (LIN == 1) {
@@ -839,6 +893,79 @@ __global__ void __launch_bounds__(64 * XW, 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_
 // group's components, this slice's channels).  As in the forward, every
 // vector-memory operation is unconditional (padding goes to the sink).
 // ---------------------------------------------------------------------------
+// l1 = 1 slots of a receiver-centric VJP, refactored around what stays fixed while a
+// wave walks one receiver's edges: g = dL/dM[recv] (per channel) and the CG tables B
+// (CG x path weight, Me[i][col] = sum_j Y_j B[j, i, col]).  With the per-receiver table
+//   R[s][i][j] = sum_(k in s) g[col_s + k] B[j, i, col_s + k]        (vjp_l1_table)
+// the per-edge VJP is one bilinear form in (x1 w, Y):
+//   h[i][s]   = sum_(k in s) g[col_s + k] Me[i][col_s + k] = sum_j Y_j R[s][i][j]
+//   dL/dw[s]  = sum_i x1[i] h[i][s],  dL/dx1[i] += sum_s w[s] h[i][s]
+//   dL/dY_j  += sum_(s, i) x1[i] w[s] R[s][i][j]
+// two products per nonzero (s, i, j) instead of the per-edge CG sums over (i, k, terms)
+// of tp_edge_vjp, and no per-edge M1 table.  R is held in registers (its zero pattern is
+// compile-time).
+// bit j: row i of the M1 table has a CG term in Y component j in one of the columns
+// [col, col + d) (one slot); folded to a constant where the arguments are
+__device__ constexpr unsigned rmask(int col, int d, int i) {
+  unsigned m = 0;
+  for (int k = 0; k < d; ++k) {
+    const int q = i * TP3_K1 + col + k;
+    for (int x = m1s(q); x < m1s(q + 1); ++x) m |= 1u << m1j(x);
+  }
+  return m;
+}
+
+template <int LIN>
+__device__ __forceinline__ void vjp_l1_table(const float* g, float (*R)[3][16]) {
+  using T = TPT<LIN>;
+  using GR = GrpT<LIN, 1>;
+#pragma unroll
+  for (int s = 0; s < T::NSLOT; ++s) {
+    if (T::l1(s) != 1) continue;
+    const int ls = GR::local(s), a0 = T::acc(s), d = 2 * T::l3(s) + 1, c0 = T::col(s);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) R[ls][i][j] = 0.f;
+#pragma unroll
+      for (int k = 0; k < d; ++k) {
+        const int q = i * T::K1 + c0 + k;
+#pragma unroll
+        for (int x = m1s(q); x < m1s(q + 1); ++x) R[ls][i][m1j(x)] = fmaf(g[a0 + k], m1v(x), R[ls][i][m1j(x)]);
+      }
+    }
+  }
+}
+
+template <int LIN, bool GX>
+__device__ __forceinline__ void tp_edge_vjp_l1(const float (*R)[3][16], const EdgeIn<LIN>& in, float* gw_out,
+                                               const float* Ye, float* gx1, float* gYu) {
+  using T = TPT<LIN>;
+  using GR = GrpT<LIN, 1>;
+#pragma unroll
+  for (int s = 0; s < T::NSLOT; ++s) {
+    if (T::l1(s) != 1) continue;
+    const int ls = GR::local(s), d = 2 * T::l3(s) + 1, c0 = T::col(s);
+    const float ww = in.w[s];
+    float gws = 0.f;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const unsigned mask = rmask(c0, d, i);
+      float h = 0.f;  // sum_k g[col_s + k] Me[i][col_s + k] = sum_j Y_j R[s][i][j]
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if ((mask >> j) & 1u) h = fmaf(Ye[j], R[ls][i][j], h);
+      gws = fmaf(in.x1[i], h, gws);
+      if (GX) gx1[i] = fmaf(ww, h, gx1[i]);
+      const float z = in.x1[i] * ww;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if ((mask >> j) & 1u) gYu[j] = fmaf(z, R[ls][i][j], gYu[j]);
+    }
+    gw_out[s] = gws;
+  }
+}
+
 // Largest value of a nonnegative x over the wave (DPP row scan, then the two
 // row broadcasts; lane 63 ends with the total), as a wave-uniform value.
 __device__ __forceinline__ float wave_max_nonneg(float x) {
@@ -870,11 +997,12 @@ struct TpxBwdDims {
 
 template <int LIN, int L1, bool GX>
 __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, _Float16* sg, float* sinv,
-                                        float* stab, float* sp) {
+                                        float* sy, float* sp) {
   using T = TPT<LIN>;
   using GR = GrpT<LIN, L1>;
   constexpr int G = GR::G, RS = 64 * G + 8;  // fp16 row stride: 16-byte reads of 8 lanes hit distinct banks
   constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, NX = 2 * L1 + 1;
+  static_assert(L1 <= 1, "input blocks l1 = 0, 1");
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, r = l & 15, g = l >> 4, u = l;
   const int c0 = 64 * blockIdx.y, nb0 = XW * blockIdx.x, p = 2 * blockIdx.z + blockIdx.y;
@@ -898,7 +1026,8 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
     wa[ks][0] = *reinterpret_cast<const h8*>(W3x + o);
     wa[ks][1] = *reinterpret_cast<const h8*>(W3x + (int64_t)XH * a.W + o);
   }
-  // dL/dM of this wave's receiver (group slots, slice channels)
+  // dL/dM of this wave's receiver (group slots, slice channels); for l1 = 1 only through
+  // its CG contraction R (tp_edge_vjp_l1)
   float gm[T::NACC];
   {
     const float* gMn = gM + (int64_t)min(n, a.N - 1) * DMID + c0 + u;
@@ -908,9 +1037,11 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
 #pragma unroll
         for (int m = 0; m < 2 * T::l3(s) + 1; ++m) gm[T::acc(s) + m] = gMn[NC * (T::acc(s) + m)];
   }
-  // next step's inputs: weights and sender rows of the two edges (indices and
-  // pos_s a step earlier still), table rows staged through LDS as in the forward
-  float wn[2][T::NSLOT], xv[2][NX], xn[2][NX], wc[2][T::NSLOT];
+  float R1[L1 == 1 ? G : 1][3][16];
+  if constexpr (L1 == 1) vjp_l1_table<LIN>(gm, R1);
+  // next step's inputs: weights, sender rows and Y rows of the two edges (indices and
+  // pos_s a step earlier still); the Y rows are wave-uniform (scalar loads)
+  float wn[2][T::NSLOT], xv[2][NX], xn[2][NX], wc[2][T::NSLOT], yn[2];
   int snd[2], psn[2], pnx[2], pss[2];  // indices of step j + 2 / pos_s of step j + 1 / of this step
   float gyn[2], gyc[2];                 // dL/dY partials already held (accumulate_gY), a step ahead
   // gY[e][p][16] entry of lane l (lanes 4k hold component k after the wave sum); padding -> sink
@@ -936,33 +1067,11 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
       const float* xs = up + (int64_t)snd[b] * DIN + NC * L1 * L1 + c0 + u;
 #pragma unroll
       for (int i = 0; i < NX; ++i) xn[b][i] = xs[NC * i];
+      yn[b] = Y[e * 16 + (l & 15)];  // lane l holds component l & 15 (stored to LDS a step later)
       if (GX) pnx[b] = psn[b];
       const int ej = beg + 2 * j + b;
       gyn[b] = *gy_addr(ej, ej < end);
     }
-  };
-  constexpr int TY = L1 == 0 ? 16 : 0, TS = TY + (L1 == 1 ? TP3_M1_NE : 0), TSP = (TS + 3) & ~3;
-  constexpr int TH = (TS + 63) / 64;
-  static_assert(TS <= 128 && L1 <= 1, "table rows of up to 128 entries");
-  float* tb = stab + wv * 2 * TSP;  // [edge b][TSP]
-  float tr[2][TH];
-  auto load_t = [&](int j) {
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int64_t e = min<int64_t>(beg + 2 * j + b, elast);
-#pragma unroll
-      for (int h = 0; h < TH; ++h) {
-        const int i = min(l + 64 * h, TS - 1);
-        tr[b][h] = i < TY ? Y[e * 16 + i] : Mt[e * a.mts + i - TY];
-      }
-    }
-  };
-  auto store_t = [&]() {
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int h = 0; h < TH; ++h)
-        if (l + 64 * h < TS) tb[b * TSP + l + 64 * h] = tr[b][h];
   };
   f4v prev = f4v{0.f, 0.f, 0.f, 0.f};  // this wave's share of the previous tile's dL/dh3
   // dL/dh3 of the tile before step j: add the partner half (k steps of the other
@@ -975,16 +1084,16 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
     *reinterpret_cast<float4*>(dst) = float4{(prev[0] + o[0]) * a.wscale, (prev[1] + o[1]) * a.wscale,
                                              (prev[2] + o[2]) * a.wscale, (prev[3] + o[3]) * a.wscale};
   };
+  float* ys = sy + wv * 32;  // this wave's two Y rows (LDS; read back as broadcasts)
   auto step = [&](int j) {
     _Float16* tile = sg + (j & 1) * 2 * 16 * RS;  // [hi, lo][edge column][RS]
     float* tinv = sinv + (j & 1) * 16;
-    store_t();
+    if (l < 32) ys[l] = yn[l >> 4];
     wave_sync();
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      xv[b][0] = xn[b][0];
 #pragma unroll
-      for (int i = 1; i < NX; ++i) xv[b][i] = xn[b][i];
+      for (int i = 0; i < NX; ++i) xv[b][i] = xn[b][i];
 #pragma unroll
       for (int s = 0; s < T::NSLOT; ++s)
         if (T::l1(s) == L1) wc[b][s] = wn[b][s];
@@ -993,7 +1102,6 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
     }
     load_in(j + 1);
     load_idx(j + 2);
-    load_t(j + 1);
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int e = beg + 2 * j + b;
@@ -1012,13 +1120,15 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
         for (int i = 0; i < NX; ++i) {
           if constexpr (L1 == 0) in.x0 = xv[b][i];
           if constexpr (L1 == 1) in.x1[i] = xv[b][i];
-          if constexpr (L1 == 2) in.x2[i] = xv[b][i];
         }
 #pragma unroll
         for (int s = 0; s < T::NSLOT; ++s)
           if (T::l1(s) == L1) in.w[s] = wc[b][s];
-        const float* trow_t = tb + b * TSP;
-        tp_edge_vjp<LIN, GX, L1>(gm, in, gws, trow_t, trow_t, trow_t, gx0, gx1, gx2, gYu);
+        const float* yrow = ys + 16 * b;
+        if constexpr (L1 == 1)
+          tp_edge_vjp_l1<LIN, GX>(R1, in, gws, yrow, gx1, gYu);
+        else
+          tp_edge_vjp<LIN, GX, L1>(gm, in, gws, yrow, yrow, yrow, gx0, gx1, gx2, gYu);
       }
       {  // split dL/dw for the matrix cores: one scale per edge (over the block's columns)
         float m = 0.f;
@@ -1043,12 +1153,12 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
       if constexpr (GX) {
         float* dst = (valid ? gxe + (int64_t)pss[b] * DIN + NC * L1 * L1 : sink) + c0 + u;
 #pragma unroll
-        for (int i = 0; i < NX; ++i) dst[NC * i] = L1 == 0 ? gx0 : L1 == 1 ? gx1[i] : gx2[i];
+        for (int i = 0; i < NX; ++i) dst[NC * i] = L1 == 0 ? gx0 : gx1[i];
       }
-      const float sy = wave_sum16(gYu);
-      *gy_addr(e, valid) = a.accumulate_gY ? gyc[b] + sy : sy;
+      const float ysum = wave_sum16(gYu);
+      *gy_addr(e, valid) = a.accumulate_gY ? gyc[b] + ysum : ysum;
     }
-    __syncthreads();
+    __syncthreads();  // also: this step's Y-row reads are done before the next step's store
     // dL/dh3 of this tile (half kh of the k steps), then the previous tile's flush
     f4v acc = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1075,7 +1185,6 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
     load_idx(0);
     load_in(0);
     load_idx(1);
-    load_t(0);
   }
 #pragma unroll 1
   for (int j = 0; j < nsteps2; ++j) step(j);
@@ -1088,15 +1197,15 @@ __global__ void __launch_bounds__(64 * XW, 2) k_tpx_bwd(TpxBwdDims a, MACE_TPX_B
   static_assert(LIN <= 2, "three input blocks are not fused");
   __shared__ __align__(16) _Float16 sg[2 * 2 * 16 * (64 * gmax<LIN>() + 8)];  // [step][hi, lo][edge][RS]
   __shared__ float sinv[2 * 16];
-  __shared__ __align__(16) float stab[XW * 2 * (LIN == 1 ? 16 : TP3_M1_NE)];
+  __shared__ __align__(16) float sy[XW * 32];      // [wave][edge][16]: the step's Y rows
   __shared__ __align__(16) float sp[3 * 4 * 256];  // [two steps + the lower half's slot][q tile][lane][4]
   if constexpr (LIN == 1) {
-    tpx_bwd<1, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, stab, sp);
+    tpx_bwd<1, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp);
   } else {
     if (blockIdx.z == 0)
-      tpx_bwd<2, 1, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, stab, sp);
+      tpx_bwd<2, 1, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp);
     else
-      tpx_bwd<2, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, stab, sp);
+      tpx_bwd<2, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp);
   }
 }
 
