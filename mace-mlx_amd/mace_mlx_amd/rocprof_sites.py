@@ -163,6 +163,22 @@ def summarize(d: str, out_dir: str, calib_mib: float = 256.0, commands: Dict[str
         for r in st[:16]:
             w(f"| {short_name(r['Name'])} | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.3f} | "
               f"{float(r['AverageNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
+    spath = os.path.join(d, "pmc_sq")
+    if os.path.isdir(spath):  # instruction counts (rocprofv3 --pmc SQ_INSTS_VALU SQ_INSTS_LDS SQ_INSTS_SALU)
+        srows = _csv(os.path.join(spath, "**", "*counter_collection.csv"))
+        names = [c for c in ("SQ_INSTS_VALU", "SQ_INSTS_LDS", "SQ_INSTS_SALU")
+                 if any(r.get("Counter_Name") == c for r in srows)]
+        per = {c: site_counters(srows, order, c)[0] for c in names}
+        w("\n## Instructions per launch (millions of wave-instructions)\n")
+        w("    " + commands.get("sq", "rocprofv3 --pmc " + " ".join(names) + " ... -- python3 bench.py ..."))
+        w("\nVALU issue time = VALU wave-instructions x 4 cycles / (1024 SIMDs x 2.4 GHz).\n")
+        w("| site | " + " | ".join(names) + " | VALU issue us | avg us |\n|---|" + "---:|" * (len(names) + 2))
+        top = sorted(per[names[0]].items(), key=lambda kv: -kv[1])[:10] if names else []
+        for k, _ in top:
+            vals = " | ".join(f"{per[c].get(k, 0.0) / 1e6:.2f}" for c in names)
+            issue = per["SQ_INSTS_VALU"].get(k, 0.0) * 4 / (1024 * 2.4e3) if "SQ_INSTS_VALU" in per else 0.0
+            avg = sum(acc[k]) / len(acc[k]) / 1e3 if k in acc else float("nan")
+            w(f"| {k} | {vals} | {issue:.1f} | {avg:.1f} |")
     os.makedirs(out_dir, exist_ok=True)
     with open(os.path.join(out_dir, f"kernel_trace_{tag}.md"), "w") as f:
         f.write("\n".join(L) + "\n")
