@@ -148,6 +148,17 @@ class Irreps:
             inv[i] = k
         return Irreps([self.blocks[i] for i in order]), tuple(order), tuple(inv)
 
+    def simplify(self) -> "Irreps":
+        """Adjacent blocks of the same irrep merged (e3nn ``Irreps.simplify``); the flat
+        feature layout is unchanged, since each block is mul-major."""
+        out: List[MulIrrep] = []
+        for b in self.blocks:
+            if out and out[-1].ir == b.ir:
+                out[-1] = MulIrrep(out[-1].mul + b.mul, b.ir)
+            elif b.mul > 0:
+                out.append(b)
+        return Irreps(out)
+
     def __iter__(self):
         return iter(self.blocks)
 
