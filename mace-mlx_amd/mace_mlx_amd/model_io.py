@@ -36,6 +36,9 @@ from .irreps import Irrep, Irreps
 
 # 1 / sqrt(E[silu(x)^2]) for x ~ N(0, 1) (`utils.py:17`)
 SILU_NORM_FACTOR = 1.6791768074035645
+# the same for the sigmoid gate of the non-linear interaction block (`blocks.py:708-717`)
+SIGMOID_NORM_FACTOR = 1.8467055569904827
+NONLINEAR_BLOCK = "RealAgnosticResidualNonLinearInteractionBlock"
 
 # Published covalent radii (Cordero et al., Dalton Trans. 2008, 2832), in
 # Angstrom, indexed by atomic number (index 0 is a placeholder).  The reference
@@ -121,6 +124,34 @@ class ModelConfig:
         """Interaction `layer` adds the skip FCTP of its input (`model.py:213-247`)."""
         return not (layer == 0 and self.first_interaction_nonresidual)
 
+    @property
+    def nonlinear(self) -> bool:
+        """mh-1 family: every interaction is the non-linear block (`model.py:175-211`,
+        `blocks.py:611-807`)."""
+        return self.interaction_cls == NONLINEAR_BLOCK
+
+    def edge_irreps_per_layer(self) -> List[Irreps]:
+        """Output irreps of linear_up in the non-linear block: ``edge_irreps`` (its scalar part
+        in the first layer), else the layer's input irreps (`model.py:192-211`,
+        `blocks.py:646-657`)."""
+        out = []
+        for i, irr_in in enumerate(self.layer_inputs()):
+            if self.edge_irreps is None:
+                out.append(irr_in)
+            elif i == 0:
+                out.append(Irreps([b for b in Irreps(self.edge_irreps) if b.ir.l == 0]))
+            else:
+                out.append(Irreps(self.edge_irreps))
+        return out
+
+    def nonlin_irreps(self) -> Irreps:
+        """Input irreps of the non-linear block's gate: activated scalars, one gate scalar
+        block per gated block, then the gated blocks (`blocks.py:700-733`, `gate.py:57-60`)."""
+        inter = self.interaction_irreps
+        scal = [b for b in inter if b.ir.l == 0]
+        gated = [b for b in inter if b.ir.l > 0]
+        return Irreps(scal + [(b.mul, Irrep(0, 1)) for b in gated] + gated)
+
     # --- derived architecture (model.py:96-145) -----------------------------
     @property
     def hidden(self) -> Irreps:
@@ -155,16 +186,16 @@ class ModelConfig:
 
     def check_supported(self) -> None:
         """Raise NotImplementedError for topology options outside this engine."""
-        if self.interaction_cls != "RealAgnosticResidualInteractionBlock":
+        if self.interaction_cls not in ("RealAgnosticResidualInteractionBlock", NONLINEAR_BLOCK):
             raise NotImplementedError(f"interaction_cls={self.interaction_cls}")
-        if self.use_agnostic_product:
-            raise NotImplementedError("use_agnostic_product")
+        if self.nonlinear and (self.first_interaction_nonresidual or self.use_density_normalization):
+            raise NotImplementedError("non-linear interaction blocks with the density / non-residual layout")
         if self.distance_transform is not None:
             unknown = set(self.distance_transform) - {"q", "p", "a", "covalent_radii"}
             if unknown:
                 raise NotImplementedError(f"distance_transform keys {sorted(unknown)}")
-        if not self.apply_cutoff:
-            raise NotImplementedError("apply_cutoff=False")
+        if not self.apply_cutoff and not self.nonlinear:
+            raise NotImplementedError("apply_cutoff=False outside the non-linear interaction block")
         if self.gate != "silu":
             raise NotImplementedError(f"gate={self.gate}")
         if any(b.ir.l == 0 and b.ir.p != 1 for b in self.hidden):
@@ -270,8 +301,13 @@ def weight_shapes(cfg: ModelConfig) -> Dict[str, tuple]:
         shapes[f"node_embedding.linear.weights.{n}"] = (mi, mo)
     shapes["radial_embedding.bessel_fn.bessel_weights"] = (cfg.num_bessel,)
     inter = cfg.interaction_irreps
+    if cfg.nonlinear:
+        _nonlinear_shapes(cfg, shapes)
     for li, (irr_in, hid) in enumerate(zip(cfg.layer_inputs(), cfg.hidden_per_layer())):
         p = f"interactions.{li}"
+        if cfg.nonlinear:
+            _product_readout_shapes(cfg, li, hid, shapes)
+            continue
         # residual blocks skip from the layer input to the hidden irreps; the non-residual
         # first block (blocks.py:68-176) applies its skip FCTP to the message
         s_in, s_out = (irr_in, hid) if cfg.residual(li) else (inter, inter)
@@ -288,30 +324,80 @@ def weight_shapes(cfg: ModelConfig) -> Dict[str, tuple]:
             shapes[f"{p}.conv_tp_weights.layers.{2 * n}.weight"] = (dims[n + 1], dims[n])
         for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(mid, inter)):
             shapes[f"{p}.linear.weights.{n}"] = (mi, mo)
-        q = f"products.{li}"
-        coupling = Irreps([(1, b.ir) for b in inter])
-        for ci, b in enumerate(hid):
-            cp = f"{q}.symmetric_contractions.contractions.{ci}"
-            corr = cfg.correlation[li]
-            shapes[f"{cp}.weights_max"] = (nel, u_matrix(coupling, b.ir, corr).shape[-1], C)
-            for wi, nu in enumerate(range(corr - 1, 0, -1)):
-                shapes[f"{cp}.weights.{wi}"] = (nel, u_matrix(coupling, b.ir, nu).shape[-1], C)
-        for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(hid, hid)):
-            shapes[f"{q}.linear.weights.{n}"] = (mi, mo)
-        r = f"readouts.{li}"
-        # readouts give num_heads x 0e; the last one's MLP has 16 x num_heads scalars
-        # (model.py:135-139)
-        out = Irreps(f"{H}x0e")
-        if li < cfg.num_interactions - 1:
-            for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(hid, out)):
-                shapes[f"{r}.linear.weights.{n}"] = (mi, mo)
-        else:
-            mlp = Irreps(f"{16 * H}x0e")
-            for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(hid, mlp)):
-                shapes[f"{r}.linear_1.weights.{n}"] = (mi, mo)
-            for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(mlp, out)):
-                shapes[f"{r}.linear_2.weights.{n}"] = (mi, mo)
+        _product_readout_shapes(cfg, li, hid, shapes)
     return shapes
+
+
+def _product_readout_shapes(cfg: ModelConfig, li: int, hid: Irreps, shapes: Dict[str, tuple]) -> None:
+    from .cg import u_matrix
+
+    C, H, inter = cfg.num_features, cfg.num_heads, cfg.interaction_irreps
+    # the element-agnostic product has one set of weights (`model.py:250-258`)
+    nel = 1 if cfg.use_agnostic_product else cfg.num_elements
+    q = f"products.{li}"
+    coupling = Irreps([(1, b.ir) for b in inter])
+    for ci, b in enumerate(hid):
+        cp = f"{q}.symmetric_contractions.contractions.{ci}"
+        corr = cfg.correlation[li]
+        shapes[f"{cp}.weights_max"] = (nel, u_matrix(coupling, b.ir, corr).shape[-1], C)
+        for wi, nu in enumerate(range(corr - 1, 0, -1)):
+            shapes[f"{cp}.weights.{wi}"] = (nel, u_matrix(coupling, b.ir, nu).shape[-1], C)
+    for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(hid, hid)):
+        shapes[f"{q}.linear.weights.{n}"] = (mi, mo)
+    r = f"readouts.{li}"
+    # readouts give num_heads x 0e; the last one's MLP has 16 x num_heads scalars
+    # (model.py:135-139)
+    out = Irreps(f"{H}x0e")
+    if li < cfg.num_interactions - 1:
+        for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(hid, out)):
+            shapes[f"{r}.linear.weights.{n}"] = (mi, mo)
+    else:
+        mlp = Irreps(f"{16 * H}x0e")
+        for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(hid, mlp)):
+            shapes[f"{r}.linear_1.weights.{n}"] = (mi, mo)
+        for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(mlp, out)):
+            shapes[f"{r}.linear_2.weights.{n}"] = (mi, mo)
+
+
+def _nonlinear_shapes(cfg: ModelConfig, shapes: Dict[str, tuple]) -> None:
+    """Arrays of the non-linear interaction block (`blocks.py:611-733`): source / target
+    species embeddings, plain-linear skip, linear_up, LayerNorm radial MLP and density MLP
+    (``layers.{k}``: Linear at 0, 3, 6, ..., LayerNorm at 1, 4, 7, ...; `radial.py:344-357`),
+    alpha / beta, linear_res, linear_1, linear_2."""
+    nel = cfg.num_elements
+    attrs = Irreps(f"{nel}x0e")
+    inter = cfg.interaction_irreps
+    nonlin = cfg.nonlin_irreps()
+    for li, (irr_in, hid, edge) in enumerate(zip(cfg.layer_inputs(), cfg.hidden_per_layer(),
+                                                 cfg.edge_irreps_per_layer())):
+        p = f"interactions.{li}"
+        nsc = irr_in.count("0e")
+        for name in ("source_embedding", "target_embedding"):
+            for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(attrs, Irreps(f"{nsc}x0e"))):
+                shapes[f"{p}.{name}.weights.{n}"] = (mi, mo)
+        for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(irr_in, hid)):
+            shapes[f"{p}.skip_tp.weights.{n}"] = (mi, mo)
+        for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(irr_in, edge)):
+            shapes[f"{p}.linear_up.weights.{n}"] = (mi, mo)
+        mid, tpi = conv_tp_instructions(edge, cfg.sh_irreps, inter)
+        wnum = sum(edge[i].mul * cfg.sh_irreps[j].mul for (i, j, _, _) in tpi)
+        aug = cfg.num_bessel + 2 * nsc
+        for name, dims in (("conv_tp_weights", [aug] + list(cfg.radial_MLP) + [wnum]),
+                           ("density_fn", [aug, 64, 1])):
+            for k in range(len(dims) - 1):
+                shapes[f"{p}.{name}.layers.{3 * k}.weight"] = (dims[k + 1], dims[k])
+                shapes[f"{p}.{name}.layers.{3 * k}.bias"] = (dims[k + 1],)
+                if k < len(dims) - 2:
+                    shapes[f"{p}.{name}.layers.{3 * k + 1}.weight"] = (dims[k + 1],)
+                    shapes[f"{p}.{name}.layers.{3 * k + 1}.bias"] = (dims[k + 1],)
+        shapes[f"{p}.alpha"] = ()
+        shapes[f"{p}.beta"] = ()
+        for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(edge, nonlin)):
+            shapes[f"{p}.linear_res.weights.{n}"] = (mi, mo)
+        for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(mid, nonlin)):
+            shapes[f"{p}.linear_1.weights.{n}"] = (mi, mo)
+        for n, (ji, jo, mi, mo, _) in enumerate(linear_instructions(inter, inter)):
+            shapes[f"{p}.linear_2.weights.{n}"] = (mi, mo)
 
 
 def random_init(cfg: ModelConfig, seed: int = 0) -> Dict[str, np.ndarray]:
@@ -329,6 +415,21 @@ def random_init(cfg: ModelConfig, seed: int = 0) -> Dict[str, np.ndarray]:
             w[key] = np.zeros(shp) if ae is None else np.asarray(ae, dtype=np.float64).reshape(shp)
         elif key == "radial_embedding.bessel_fn.bessel_weights":
             w[key] = np.arange(1, shp[0] + 1, dtype=np.float64) * math.pi / cfg.r_max
+        elif cfg.nonlinear and (".conv_tp_weights." in key or ".density_fn." in key):
+            # nn.Linear's U(+-1/sqrt(fan_in)) for weights and biases (MLX default); LayerNorm
+            # scale / shift drawn around MLX's 1 / 0 so that a test exercises them
+            k = int(key.split(".layers.")[1].split(".")[0])
+            if k % 3 == 1:
+                w[key] = (1.0 if key.endswith(".weight") else 0.0) + 0.1 * rng.standard_normal(shp)
+            else:
+                fan_in = shapes[key.rsplit(".", 1)[0] + ".weight"][1]
+                w[key] = rng.uniform(-1.0, 1.0, shp) / math.sqrt(fan_in)
+        elif key.endswith(".alpha") or key.endswith(".beta"):
+            # the block starts from alpha = 20, beta = 0 (blocks.py:697-698): the density off and
+            # every message damped 20x, which leaves a random model with forces ~0.01 eV/A;
+            # a random model takes alpha in [1, ~3] and beta in [0.1, ~0.4] instead
+            a0, sc = (1.0, 1.0) if key.endswith(".alpha") else (0.1, 0.1)
+            w[key] = np.asarray(a0 + sc * abs(rng.standard_normal()))
         elif ".conv_tp_weights." in key:
             layer = int(key.split(".layers.")[1].split(".")[0])
             scale = 1.0 / math.sqrt(shp[1]) * (SILU_NORM_FACTOR if layer > 0 else 1.0)

@@ -17,6 +17,13 @@ Semantics follow the reference's generic code paths:
                                variants: Agnesi distance transform `radial.py:207-262`,
                                density normalisation `blocks.py:282-490`, non-residual
                                first interaction `blocks.py:68-176`, `model.py:213-247`
+* mh-1 family                  non-linear interaction block `blocks.py:611-807` (species
+                               source / target embeddings, LayerNorm radial and density
+                               MLPs `radial.py:344-357`, gate `gate.py:19-164` with the
+                               normalize2mom constants `blocks.py:708-717`, linear_res,
+                               linear_1 / (beta rho + alpha), linear_2), separate cutoff
+                               (`radial.py:265-321` apply_cutoff=False), element-agnostic
+                               product (`blocks.py:493-537`)
 * energy assembly              `model.py:403-438`; ScaleShiftMACE `model.py:508-589`;
                                multi-head readouts: every head evaluated, the non-linear
                                readout's features masked to the active head, the active
@@ -46,8 +53,8 @@ if str(_PKG) not in sys.path:
 
 from mace_mlx_amd.cg import so3_cg, u_matrix, wigner_3j  # noqa: E402
 from mace_mlx_amd.irreps import Irrep, Irreps  # noqa: E402
-from mace_mlx_amd.model_io import (COVALENT_RADII, ModelConfig, load_config,  # noqa: E402
-                                   load_weights)
+from mace_mlx_amd.model_io import (COVALENT_RADII, SIGMOID_NORM_FACTOR,  # noqa: E402
+                                   SILU_NORM_FACTOR, ModelConfig, load_config, load_weights)
 
 
 def _t(x, dtype):
@@ -318,6 +325,60 @@ class RadialMLP:
         return x
 
 
+def layer_norm(x, w, b, eps=1e-5):
+    """MLX nn.LayerNorm over the last axis: (x - mean) / sqrt(var + eps) * w + b with the
+    population variance."""
+    mu = x.mean(-1, keepdim=True)
+    var = ((x - mu) ** 2).mean(-1, keepdim=True)
+    return (x - mu) / torch.sqrt(var + eps) * w + b
+
+
+class RadialMLPLN:
+    """`make_radial_mlp_with_layernorm` (`radial.py:344-357`): Linear(bias) -> LayerNorm ->
+    SiLU -> ... -> Linear(bias); ``layers.{k}`` with Linear at k = 0, 3, 6, ... and
+    LayerNorm at k = 1, 4, 7, ..."""
+
+    def __init__(self, W, prefix):
+        self.lin, self.ln = [], []
+        k = 0
+        while f"{prefix}.layers.{3 * k}.weight" in W:
+            self.lin.append((W[f"{prefix}.layers.{3 * k}.weight"], W[f"{prefix}.layers.{3 * k}.bias"]))
+            if f"{prefix}.layers.{3 * k + 1}.weight" in W:
+                self.ln.append((W[f"{prefix}.layers.{3 * k + 1}.weight"], W[f"{prefix}.layers.{3 * k + 1}.bias"]))
+            k += 1
+        assert len(self.ln) == len(self.lin) - 1
+
+    def __call__(self, x):
+        for n, (Wl, bl) in enumerate(self.lin):
+            x = x @ Wl.T + bl
+            if n < len(self.lin) - 1:
+                x = _silu(layer_norm(x, *self.ln[n]))
+        return x
+
+
+class Gate:
+    """`gate.py:19-164` as the non-linear block builds it (`blocks.py:700-733`): input
+    [scalars | gate scalars | gated blocks]; output [c_silu silu(scalars) | c_sig
+    sigmoid(gate_k) x gated block k]."""
+
+    def __init__(self, irreps_out: Irreps):
+        self.scal = Irreps([b for b in irreps_out if b.ir.l == 0])
+        self.gated = Irreps([b for b in irreps_out if b.ir.l > 0])
+        self.ngate = sum(b.mul for b in self.gated)
+
+    def __call__(self, x):
+        ds = self.scal.dim
+        out = [SILU_NORM_FACTOR * _silu(x[:, :ds])]
+        gates = SIGMOID_NORM_FACTOR * torch.sigmoid(x[:, ds:ds + self.ngate])
+        off, go = ds + self.ngate, 0
+        for b in self.gated:
+            blk = x[:, off:off + b.dim].reshape(-1, b.mul, b.ir.dim)
+            out.append((gates[:, go:go + b.mul, None] * blk).reshape(x.shape[0], -1))
+            off += b.dim
+            go += b.mul
+        return torch.cat(out, dim=-1)
+
+
 # ---------------------------------------------------------------------------
 # Whole model
 # ---------------------------------------------------------------------------
@@ -365,9 +426,14 @@ class OracleMACE:
         self.embed = Linear(Irreps(f"{nel}x0e"), scal, wl("node_embedding.linear.weights"))
         self.layers = []
         irr_in = scal
+        edges = cfg.edge_irreps_per_layer()
         for li in range(cfg.num_interactions):
             p = f"interactions.{li}"
             hid = hid_layers[li]
+            if cfg.nonlinear:
+                self.layers.append(self._nonlinear_layer(li, irr_in, hid, edges[li], inter, sh, wl))
+                irr_in = hid
+                continue
             L = {"resid": cfg.residual(li)}
             if L["resid"]:
                 L["skip"] = SkipFCTP(irr_in, nel, hid, wl(f"{p}.skip_tp.tp.weights"))
@@ -417,6 +483,78 @@ class OracleMACE:
         self.agnesi = cfg.agnesi()
         self.radii = _t(cfg.agnesi_radii(), dtype)
 
+    def _product_readout(self, L, li, hid, inter, wl):
+        cfg, W = self.cfg, self.W
+        q = f"products.{li}.symmetric_contractions.contractions"
+
+        def wfn(ci, q=q):
+            return W[f"{q}.{ci}.weights_max"], wl(f"{q}.{ci}.weights")
+
+        L["sc"] = SymmetricContraction(inter, hid, cfg.correlation[li], wfn, self.dtype)
+        L["plin"] = Linear(hid, hid, wl(f"products.{li}.linear.weights"))
+        r = f"readouts.{li}"
+        ro_out = Irreps(f"{self.H}x0e")   # model.py:135-139
+        if li < cfg.num_interactions - 1:
+            L["ro"] = ("linear", Linear(hid, ro_out, wl(f"{r}.linear.weights")))
+        else:
+            mlp = Irreps(f"{16 * self.H}x0e")
+            L["ro"] = ("nonlinear", Linear(hid, mlp, wl(f"{r}.linear_1.weights")),
+                       Linear(mlp, ro_out, wl(f"{r}.linear_2.weights")))
+
+    def _nonlinear_layer(self, li, irr_in, hid, edge, inter, sh, wl):
+        """`blocks.py:611-733` with the element-agnostic product option (`blocks.py:493-537`)."""
+        cfg, W = self.cfg, self.W
+        p = f"interactions.{li}"
+        attrs = Irreps(f"{self.nel}x0e")
+        nsc = Irreps(f"{irr_in.count('0e')}x0e")
+        nonlin = cfg.nonlin_irreps()
+        L = {"nonlin": True, "resid": True}
+        L["src"] = Linear(attrs, nsc, wl(f"{p}.source_embedding.weights"))
+        L["tgt"] = Linear(attrs, nsc, wl(f"{p}.target_embedding.weights"))
+        L["skip"] = Linear(irr_in, hid, wl(f"{p}.skip_tp.weights"))
+        L["up"] = Linear(irr_in, edge, wl(f"{p}.linear_up.weights"))
+        L["tp"] = ConvTP(edge, sh, inter)
+        L["mlp"] = RadialMLPLN(W, f"{p}.conv_tp_weights")
+        assert L["mlp"].lin[-1][0].shape[0] == L["tp"].weight_numel
+        L["dens"] = RadialMLPLN(W, f"{p}.density_fn")
+        L["alpha"], L["beta"] = W[f"{p}.alpha"].reshape(()), W[f"{p}.beta"].reshape(())
+        L["res"] = Linear(edge, nonlin, wl(f"{p}.linear_res.weights"))
+        L["lin1"] = Linear(L["tp"].mid, nonlin, wl(f"{p}.linear_1.weights"))
+        L["gate"] = Gate(inter)
+        L["lin2"] = Linear(inter, inter, wl(f"{p}.linear_2.weights"))
+        self._product_readout(L, li, hid, inter, wl)
+        return L
+
+    def _nonlinear_message(self, L, h, onehot, Y, ef, cut, sender, receiver, N):
+        """message of the non-linear block (`blocks.py:735-807`)."""
+        dtype = self.dtype
+        up = L["up"](h)
+        res = L["res"](up)
+        src, tgt = L["src"](onehot), L["tgt"](onehot)
+        D = L["tp"].mid.dim
+        E = Y.shape[0]
+        M = torch.zeros(N, D, dtype=dtype)
+        rho = torch.zeros(N, dtype=dtype)
+        if E == 0:
+            M = M + 0.0 * up.sum()
+
+        def chunk_fn(up_, Y_, ef_, cut_, s_, r_, accM, accR):
+            aug = torch.cat([ef_, src[s_], tgt[r_]], dim=-1)
+            w = L["mlp"](aug)
+            d = torch.tanh(L["dens"](aug) ** 2)
+            if cut_ is not None:
+                w = w * cut_
+                d = d * cut_
+            m = L["tp"](up_[s_], Y_, w)
+            return accM.index_add(0, r_, m), accR.index_add(0, r_, d[:, 0])
+
+        for a in range(0, E, self.edge_chunk):
+            b = min(E, a + self.edge_chunk)
+            M, rho = checkpoint(chunk_fn, up, Y[a:b], ef[a:b], None if cut is None else cut[a:b],
+                                sender[a:b], receiver[a:b], M, rho, use_reentrant=False)
+        msg = L["lin1"](M) / (rho * L["beta"] + L["alpha"])[:, None] + res
+        return L["lin2"](L["gate"](msg))
+
     # -- forward from edge vectors ------------------------------------------
     def energy_from_vectors(self, vec, species, sender, receiver):
         cfg, dtype = self.cfg, self.dtype
@@ -431,13 +569,24 @@ class OracleMACE:
             rb = agnesi(r, z[sender], z[receiver], self.agnesi, self.radii)
         else:
             rb = r
-        ef = bessel(rb, self.bw, cfg.r_max) * poly_envelope(r / cfg.r_max, cfg.num_polynomial_cutoff)[:, None]
+        env = poly_envelope(r / cfg.r_max, cfg.num_polynomial_cutoff)[:, None]
+        if cfg.apply_cutoff:
+            ef, cut = bessel(rb, self.bw, cfg.r_max) * env, None
+        else:  # radial.py:316-318: basis and cutoff returned separately
+            ef, cut = bessel(rb, self.bw, cfg.r_max), env
         terms = [node_e0]
         if cfg.pair_repulsion:
             z = self.z_table[species]
             terms.append(zbl_node_energy(r, z[sender], z[receiver], receiver, N, cfg.pair_repulsion))
         h = self.embed(onehot).detach()
         for L in self.layers:
+            if L.get("nonlin"):
+                sc = L["skip"](h)
+                msg = self._nonlinear_message(L, h, onehot, Y, ef, cut, sender, receiver, N)
+                sp = torch.zeros_like(species) if cfg.use_agnostic_product else species
+                h = L["plin"](L["sc"](msg, sp)) + sc
+                terms.append(self._readout(L, h))
+                continue
             sc = L["skip"](h, onehot) if L["resid"] else None
             up = L["up"](h)
             msg = self._message(L, up, Y, ef, sender, receiver, N)
@@ -453,22 +602,24 @@ class OracleMACE:
             h = L["plin"](L["sc"](msg, species))
             if sc is not None:
                 h = h + sc
-            ro = L["ro"]
-            if ro[0] == "linear":
-                terms.append(ro[1](h)[:, self.h])
-            else:
-                g = _silu(ro[1](h))
-                if self.H > 1:   # keep the active head's 16 features (blocks.py:583-608)
-                    mask = torch.zeros(g.shape[1], dtype=g.dtype)
-                    mask[16 * self.h:16 * (self.h + 1)] = 1.0
-                    g = g * mask
-                terms.append(ro[2](g)[:, self.h])
+            terms.append(self._readout(L, h))
         if self.scale is not None:
             # ScaleShiftMACE (model.py:550-589): pair + readouts scaled, shift per atom
             inter = torch.stack(terms[1:], 0).sum(0)
             terms = [terms[0], self.scale * inter + self.shift]
         node_energy = torch.stack(terms, 0).sum(0)
         return node_energy.sum(), node_energy
+
+    def _readout(self, L, h):
+        ro = L["ro"]
+        if ro[0] == "linear":
+            return ro[1](h)[:, self.h]
+        g = _silu(ro[1](h))
+        if self.H > 1:   # keep the active head's 16 features (blocks.py:583-608)
+            mask = torch.zeros(g.shape[1], dtype=g.dtype)
+            mask[16 * self.h:16 * (self.h + 1)] = 1.0
+            g = g * mask
+        return ro[2](g)[:, self.h]
 
     def _message(self, L, up, Y, ef, sender, receiver, N):
         E = Y.shape[0]
