@@ -85,6 +85,8 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = 
     if dtype == "float16":
         w = round_weights_fp16(w)
     cfg.check_supported()
+    if cfg.nonlinear or cfg.use_agnostic_product or not cfg.apply_cutoff:
+        raise UnsupportedModel("non-linear interaction blocks / agnostic product / separate cutoff")
     cfg, w = select_head(cfg, w, head)
     if cfg.model_type not in ("MACE", "ScaleShiftMACE"):
         raise UnsupportedModel(f"model_type={cfg.model_type}")
