@@ -83,6 +83,18 @@ typedef struct mace_model_dims {
   double agnesi_q;
   double agnesi_p;
   double agnesi_a;
+  int32_t nonlinear;         /* 1: mh-1 non-linear interaction blocks (blocks.py:611-807):
+                                LayerNorm radial / density MLPs over [ef | source | target
+                                species embedding], message linear_1 / (beta rho + alpha) +
+                                linear_res, gate, linear_2; plain-linear skip (tensors
+                                L<l>.rmlp.*, L<l>.dmlp.*, L<l>.ab, L<l>.res.<l>, L<l>.lin2.<l>) */
+  int32_t separate_cutoff;   /* 1: apply_cutoff = False (radial.py:316-318): the polynomial
+                                envelope multiplies the TP weights and the edge densities
+                                instead of the radial basis; only with nonlinear = 1          */
+  int32_t agnostic_product;  /* 1: one set of symmetric-contraction weights for every element
+                                (blocks.py:510-533): tensors L<l>.sc.<b> hold one element        */
+  int32_t layer_edge_blocks[4]; /* nonlinear: blocks 0e,1o,2e[:n] of linear_up's output (edge
+                                irreps, model.py:192-211); 0 otherwise                          */
 } mace_model_dims;
 
 /* Context lifetime.  device = HIP device ordinal. */

@@ -112,6 +112,22 @@ struct Layer {
   DBuf<float> ds;        // silu' of the radial MLP's pre-activations, [E][3][64]
   DBuf<_Float16> wh;
   const void* wptr(bool half) const { return half ? static_cast<const void*>(wh.p) : static_cast<const void*>(w.p); }
+  // mh-1 non-linear interaction block (blocks.py:611-807).  The conv TP acts on linear_up's
+  // output (ledge blocks, dedge floats per node); lin / din stay the layer input's.
+  bool nonlin = false;
+  int ledge = 0, dedge = 0;
+  int nres = 0;                  // columns of linear_res's output (a prefix of the gate input)
+  float alpha = 1.f, beta = 0.f;
+  DBuf<float> b3;                // radial-MLP output bias [W]
+  DBuf<float> rmlp_ts, rmlp_tt, rmlp_ln, rmlp_bias, dmlp_ts, dmlp_tt, dmlp_ln, dmlp_w1;
+  DBuf<unsigned char> dmlp_tiles;  // tile images of the density MLP's first layer (ef part)
+  DBuf<float> res_[4], resT[4], lin2[4], lin2T[4];
+  DBuf<float> Q, R, Gt;          // per step: linear_1 / (beta rho + alpha), linear_res, gate output
+  LnMlpParams lnp() const {
+    return LnMlpParams{rmlp_ts.p, rmlp_tt.p, rmlp_ln.p, rmlp_bias.p, dmlp_ts.p, dmlp_tt.p, dmlp_ln.p, dmlp_w1.p};
+  }
+  int tl() const { return nonlin ? ledge : lin; }  // input blocks of the conv TP
+  int dtp() const { return nonlin ? dedge : din; }
 };
 
 }  // namespace
@@ -131,6 +147,10 @@ struct mace_ctx {
   DBuf<float> up0_tab;  // first linear_up per species [n_el][C]
   DBuf<float> sink;     // fused TP: target of the weight stores of padding edges (max slots x C floats)
   DBuf<float> gA2, grho;  // backward scratch of the message skip / density normalisation
+  // mh-1: per-edge envelope and its gradient (apply_cutoff = 0), edge densities, gw . b3,
+  // dL/d(gate input), all-zero species (element-agnostic product)
+  DBuf<float> cutv, gcut, mh_dens, gwb, gP;
+  DBuf<int> zero_species;
   // system
   int N = 0;
   std::vector<int> species_h;
@@ -354,12 +374,116 @@ void free_layers(mace_ctx* c) {
     L.ro.release(), L.ro1.release(), L.ro2.release(), L.h_up.release(), L.A.release(), L.w.release(),
         L.wh.release(), L.mlpT3h.release(), L.mlp3h.release(), L.A2.release(), L.rinv.release(),
         L.dens.release(), L.mlpT3x.release(), L.mlp3x.release(), L.mlp_tiles.release(), L.ds.release(),
-        L.mlp_tiles_x.release();
+        L.mlp_tiles_x.release(), L.b3.release(), L.rmlp_ts.release(), L.rmlp_tt.release(), L.rmlp_ln.release(),
+        L.rmlp_bias.release(), L.dmlp_ts.release(), L.dmlp_tt.release(), L.dmlp_ln.release(), L.dmlp_w1.release(),
+        L.dmlp_tiles.release(), L.Q.release(), L.R.release(), L.Gt.release();
     for (int i = 0; i < 4; ++i) L.mskip[i].release(), L.mskipT[i].release();
+    for (int i = 0; i < 4; ++i) L.res_[i].release(), L.resT[i].release(), L.lin2[i].release(), L.lin2T[i].release();
   }
   c->layers.clear();
   for (auto& kv : c->wsplit) kv.second.x.release();
   c->wsplit.clear();
+}
+
+// symmetric contraction, product linear and readout of layer l (both interaction kinds)
+void build_product_readout(mace_ctx* c, Layer& L, int l) {
+  const auto& d = c->dims;
+  const int C = NC;
+  const int nel = d.agnostic_product ? 1 : d.num_elements;  // blocks.py:510-533
+  const std::string p = "L" + std::to_string(l) + ".";
+  for (int b = 0; b < L.lhid; ++b) {
+    upload(c, L.sc[b], tensor(c, p + "sc." + std::to_string(b), (size_t)nel * sc_kt(b, L.corr) * C));
+    const auto& w = tensor(c, p + "plin." + std::to_string(b), (size_t)C * C);
+    upload(c, L.plin[b], w);
+    upload(c, L.plinT[b], transpose(w, C, C));
+  }
+  if (l < d.num_layers - 1) {
+    upload(c, L.ro, tensor(c, p + "ro", C));
+  } else {
+    if (L.lhid != 1) fail(MACE_ERR_UNSUPPORTED, "last layer must be scalar");
+    upload(c, L.ro1, tensor(c, p + "ro1", (size_t)C * 16));
+    upload(c, L.ro2, tensor(c, p + "ro2", 16));
+  }
+}
+
+// mh-1 non-linear interaction block (blocks.py:611-733): tensors L<l>.up.<b> (input block b ->
+// edge block b), skip.<b> (plain linear, [C][C]), rmlp.{w0 [nb][64], w1, w2 [64][64] ([in][out]),
+// ts, tt [n_el][64], ln [3][2][64], bias [2][64], b3 [W]}, mlp.3 [64][W], dmlp.{w0 [nb][64],
+// ts, tt [n_el][64], ln [2][64], w1 [65]}, ab [2] (alpha, beta), res.<lo> [C][C or 4C],
+// lin.<lo> [slots x C][C or 4C], lin2.<lo> [C][C]
+void build_layer_nonlin(mace_ctx* c, Layer& L, int l) {
+  const auto& d = c->dims;
+  const int C = NC, nel = d.num_elements, nb = d.num_bessel;
+  const std::string p = "L" + std::to_string(l) + ".";
+  L.nonlin = true;
+  L.ledge = d.layer_edge_blocks[l];
+  if (L.ledge < 1 || L.ledge > 3) fail(MACE_ERR_UNSUPPORTED, "layer %d edge irreps blocks %d", l, L.ledge);
+  if (l == 0 && L.ledge != 1) fail(MACE_ERR_UNSUPPORTED, "first layer edge irreps must be scalar");
+  L.dedge = C * L.ledge * L.ledge;
+  L.dmid = C * n_tp_acc(L.ledge);
+  L.wn = C * n_tp_slots(L.ledge);
+  L.nres = 4 * C + C * (L.ledge * L.ledge - 1);
+  L.resid = true;
+  for (int b = 0; b < std::min(L.lin, L.ledge); ++b) {
+    const auto& w = tensor(c, p + "up." + std::to_string(b), (size_t)C * C);
+    upload(c, L.up[b], w);
+    upload(c, L.upT[b], transpose(w, C, C));
+  }
+  L.nskip = std::min(L.lin, L.lhid);
+  for (int b = 0; b < L.nskip; ++b) {
+    const auto& w = tensor(c, p + "skip." + std::to_string(b), (size_t)C * C);
+    upload(c, L.skip[b], w);
+    upload(c, L.skipT[b], transpose(w, C, C));
+  }
+  {  // LayerNorm radial MLP and density MLP
+    const auto& w0 = tensor(c, p + "rmlp.w0", (size_t)nb * RADIAL_H);
+    const auto& w1 = tensor(c, p + "rmlp.w1", (size_t)RADIAL_H * RADIAL_H);
+    const auto& w2 = tensor(c, p + "rmlp.w2", (size_t)RADIAL_H * RADIAL_H);
+    DBuf<float> t0, t1, t2;
+    upload(c, t0, w0), upload(c, t1, w1), upload(c, t2, w2);
+    L.mlp_tiles.ensure(mlp_tile_bytes());
+    launch_mlp_permute(c->stream, nb, t0.p, t1.p, t2.p, L.mlp_tiles.p);
+    DBuf<float> d0;
+    upload(c, d0, tensor(c, p + "dmlp.w0", (size_t)nb * RADIAL_H));
+    L.dmlp_tiles.ensure(mlp_tile_bytes());
+    launch_mlp_permute(c->stream, nb, d0.p, t1.p, t2.p, L.dmlp_tiles.p);  // only the first matrix is used
+    HIPCHK(hipGetLastError());
+    HIPCHK(hipStreamSynchronize(c->stream));
+    t0.release(), t1.release(), t2.release(), d0.release();
+    upload(c, L.rmlp_ts, tensor(c, p + "rmlp.ts", (size_t)nel * RADIAL_H));
+    upload(c, L.rmlp_tt, tensor(c, p + "rmlp.tt", (size_t)nel * RADIAL_H));
+    upload(c, L.rmlp_ln, tensor(c, p + "rmlp.ln", (size_t)6 * RADIAL_H));
+    upload(c, L.rmlp_bias, tensor(c, p + "rmlp.bias", (size_t)2 * RADIAL_H));
+    upload(c, L.b3, tensor(c, p + "rmlp.b3", (size_t)L.wn));
+    const auto& w3 = tensor(c, p + "mlp.3", (size_t)RADIAL_H * L.wn);
+    upload(c, L.mlp[3], w3);
+    upload(c, L.mlpT[3], transpose(w3, RADIAL_H, L.wn));
+    upload(c, L.dmlp_ts, tensor(c, p + "dmlp.ts", (size_t)nel * RADIAL_H));
+    upload(c, L.dmlp_tt, tensor(c, p + "dmlp.tt", (size_t)nel * RADIAL_H));
+    upload(c, L.dmlp_ln, tensor(c, p + "dmlp.ln", (size_t)2 * RADIAL_H));
+    upload(c, L.dmlp_w1, tensor(c, p + "dmlp.w1", (size_t)RADIAL_H + 1));
+    const auto& ab = tensor(c, p + "ab", 2);
+    L.alpha = ab[0];
+    L.beta = ab[1];
+  }
+  const int* l3 = tp_l3(L.ledge);
+  for (int lo = 0; lo < 4; ++lo) {
+    const int cout = lo == 0 ? 4 * C : C;
+    int ns = 0;
+    for (int s = 0; s < n_tp_slots(L.ledge); ++s) ns += (l3[s] == lo);
+    const auto& w = tensor(c, p + "lin." + std::to_string(lo), (size_t)ns * C * cout);
+    upload(c, L.lin_[lo], w);
+    upload(c, L.linT[lo], transpose(w, ns * C, cout));
+    if (lo < L.ledge) {
+      const auto& r = tensor(c, p + "res." + std::to_string(lo), (size_t)C * cout);
+      upload(c, L.res_[lo], r);
+      upload(c, L.resT[lo], transpose(r, C, cout));
+    }
+    const auto& w2 = tensor(c, p + "lin2." + std::to_string(lo), (size_t)C * C);
+    upload(c, L.lin2[lo], w2);
+    upload(c, L.lin2T[lo], transpose(w2, C, C));
+  }
+  build_product_readout(c, L, l);
 }
 
 void build_model(mace_ctx* c) {
@@ -414,6 +538,12 @@ void build_model(mace_ctx* c) {
     L.dint = C * 16;
     L.dmid = C * n_tp_acc(L.lin);
     L.wn = C * n_tp_slots(L.lin);
+    if (d.nonlinear) {
+      if (d.feature_half) fail(MACE_ERR_UNSUPPORTED, "non-linear interaction blocks under the float16 policy");
+      build_layer_nonlin(c, L, l);
+      continue;
+    }
+    if (d.separate_cutoff) fail(MACE_ERR_UNSUPPORTED, "a separate cutoff outside the non-linear interaction block");
     const std::string p = "L" + std::to_string(l) + ".";
     for (int b = 0; b < L.lin; ++b) {
       const auto& w = tensor(c, p + "up." + std::to_string(b), (size_t)C * C);
@@ -479,19 +609,7 @@ void build_model(mace_ctx* c) {
       upload(c, L.lin_[lo], w);
       upload(c, L.linT[lo], transpose(w, ns * C, C));
     }
-    for (int b = 0; b < L.lhid; ++b) {
-      upload(c, L.sc[b], tensor(c, p + "sc." + std::to_string(b), (size_t)nel * sc_kt(b, L.corr) * C));
-      const auto& w = tensor(c, p + "plin." + std::to_string(b), (size_t)C * C);
-      upload(c, L.plin[b], w);
-      upload(c, L.plinT[b], transpose(w, C, C));
-    }
-    if (l < d.num_layers - 1) {
-      upload(c, L.ro, tensor(c, p + "ro", C));
-    } else {
-      if (L.lhid != 1) fail(MACE_ERR_UNSUPPORTED, "last layer must be scalar");
-      upload(c, L.ro1, tensor(c, p + "ro1", (size_t)C * 16));
-      upload(c, L.ro2, tensor(c, p + "ro2", 16));
-    }
+    build_product_readout(c, L, l);
   }
   if (!d.feature_half) {  // split copies of every weight matrix the grouped products use
     const size_t CC = (size_t)C * C;
@@ -499,16 +617,21 @@ void build_model(mace_ctx* c) {
       for (int b = 0; b < L.lin; ++b) make_split(c, L.up[b].p, CC), make_split(c, L.upT[b].p, CC);
       for (int b = 0; b < L.lhid; ++b) make_split(c, L.plin[b].p, CC), make_split(c, L.plinT[b].p, CC);
       for (int b = 0; b < L.nskip; ++b) make_split(c, L.skip[b].p, CC), make_split(c, L.skipT[b].p, CC);
-      const int* l3 = tp_l3(L.lin);
+      const int* l3 = tp_l3(L.tl());
       for (int lo = 0; lo < 4; ++lo) {
         size_t ns = 0;
-        for (int q = 0; q < n_tp_slots(L.lin); ++q) ns += (l3[q] == lo);
-        make_split(c, L.lin_[lo].p, ns * CC), make_split(c, L.linT[lo].p, ns * CC);
+        for (int q = 0; q < n_tp_slots(L.tl()); ++q) ns += (l3[q] == lo);
+        const size_t cw = (L.nonlin && lo == 0) ? 4 : 1;  // the mh-1 scalar outputs: 4 C columns
+        make_split(c, L.lin_[lo].p, ns * CC * cw), make_split(c, L.linT[lo].p, ns * CC * cw);
+        if (L.nonlin) {
+          if (lo < L.ledge) make_split(c, L.res_[lo].p, CC * cw), make_split(c, L.resT[lo].p, CC * cw);
+          make_split(c, L.lin2[lo].p, CC), make_split(c, L.lin2T[lo].p, CC);
+        }
       }
     }
   }
   c->max_lin = 1;
-  for (const Layer& L : c->layers) c->max_lin = std::max(c->max_lin, L.lin);
+  for (const Layer& L : c->layers) c->max_lin = std::max(c->max_lin, L.tl());
   c->mts = (tp_table_entries(c->max_lin) + 15) / 16 * 16;
   int wmax = 0;
   for (const Layer& L : c->layers) wmax = std::max(wmax, L.wn);
@@ -529,11 +652,21 @@ void ensure_node_buffers(mace_ctx* c) {
   for (int l = 0; l < L; ++l) {
     Layer& ly = c->layers[l];
     c->h[l].ensure((size_t)N * ly.din);
-    ly.h_up.ensure((size_t)N * ly.din);
+    ly.h_up.ensure((size_t)N * ly.dtp());
     ly.A.ensure((size_t)N * ly.dint);
     if (!ly.resid) ly.A2.ensure((size_t)N * ly.dint);
-    if (c->dims.density_norm) ly.rinv.ensure(N);
-    maxd = std::max({maxd, ly.dmid, ly.din, ly.dhid});
+    if (c->dims.density_norm || ly.nonlin) ly.rinv.ensure(N);
+    if (ly.nonlin) {
+      ly.Q.ensure((size_t)N * kGateInDim);
+      ly.R.ensure((size_t)N * ly.nres);
+      ly.Gt.ensure((size_t)N * ly.dint);
+      c->gP.ensure((size_t)N * kGateInDim);
+    }
+    maxd = std::max({maxd, ly.dmid, ly.din, ly.dhid, ly.dtp()});
+  }
+  if (c->dims.agnostic_product && c->zero_species.n < (size_t)N) {
+    c->zero_species.ensure(N);
+    HIPCHK(hipMemset(c->zero_species.p, 0, (size_t)N * sizeof(int)));
   }
   c->h[L].ensure((size_t)N * c->layers[L - 1].dhid);
   c->M.ensure((size_t)N * maxd);
@@ -577,7 +710,12 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   }
   if (half) c->h3h.ensure(e * RADIAL_H);
   size_t maxdin = 0;  // per-edge input gradients of the layers after the first
-  for (size_t l = 1; l < c->layers.size(); ++l) maxdin = std::max(maxdin, (size_t)c->layers[l].din);
+  for (size_t l = 1; l < c->layers.size(); ++l) maxdin = std::max(maxdin, (size_t)c->layers[l].dtp());
+  if (!c->layers.empty() && c->layers[0].nonlin) {
+    c->mh_dens.ensure(e);
+    c->gwb.ensure(e);
+    if (c->dims.separate_cutoff) c->cutv.ensure(e), c->gcut.ensure(e);
+  }
   if (maxdin > 0) c->gxe.ensure(e * maxdin);
   c->geom.ensure(e);
   c->Y.ensure(e * 16);
@@ -886,10 +1024,10 @@ void run_gemm(mace_ctx* c, hipStream_t st, GemmGroup& g) {
 }
 
 void slot_range(const Layer& L, int lo, int* first, int* cnt) {
-  const int* l3 = tp_l3(L.lin);
+  const int* l3 = tp_l3(L.tl());
   *first = -1;
   *cnt = 0;
-  for (int q = 0; q < n_tp_slots(L.lin); ++q)
+  for (int q = 0; q < n_tp_slots(L.tl()); ++q)
     if (l3[q] == lo) {
       if (*first < 0) *first = q;
       ++*cnt;
@@ -913,6 +1051,7 @@ FrontParams front_params(mace_ctx* c) {
   p.ag_q = (float)c->dims.agnesi_q;
   p.ag_p = (float)c->dims.agnesi_p;
   p.ag_a = (float)c->dims.agnesi_a;
+  p.apply_cutoff = !c->dims.separate_cutoff;
   return p;
 }
 
@@ -1004,6 +1143,218 @@ void run_captured(mace_ctx* c, mace_ctx::StepGraph& g, const void* a, const void
   HIPCHK(hipGraphLaunch(g.exec, c->stream));
 }
 
+// the species index array the symmetric contraction reads: all zeros for the element-agnostic
+// product (blocks.py:510-533)
+const int* sc_species(mace_ctx* c) { return c->dims.agnostic_product ? c->zero_species.p : c->species.p; }
+
+// column offset of output degree lo in the gate-input layout [scalars | 3 gate blocks | 1o | 2e | 3o]
+inline int gate_in_base(int lo) { return lo == 0 ? 0 : 4 * NC + NC * (lo * lo - 1); }
+
+// mh-1 non-linear interaction block and its product, h -> hn (blocks.py:735-807, 493-537)
+void forward_nonlin(mace_ctx* c, int l, const float* h, float* hn) {
+  hipStream_t st = c->stream;
+  Layer& L = c->layers[l];
+  const int N = c->N;
+  const int64_t E = c->E;
+  const int nb = c->dims.num_bessel;
+  const float* cut = c->dims.separate_cutoff ? c->cutv.p : nullptr;
+  {  // LayerNorm radial MLP (last hidden activation) and the edge densities
+    Site s(c, lname("mlp_ln", l));
+    launch_rmlp_ln_fwd(st, E, nb, c->ef.p, cut, c->sender.p, c->receiver.p, c->species.p, L.mlp_tiles.p,
+                       L.dmlp_tiles.p, L.lnp(), c->h3.p, c->mh_dens.p);
+  }
+  {  // w = (h3 W3 + b3) cut
+    Site s(c, lname("mlp_out", l));
+    launch_mlp_out(st, E, L.wn, c->h3.p, L.mlpT[3].p, L.w.p, 0, L.b3.p, cut);
+  }
+  if (l > 0) {  // the first layer's comes from the species table (launch_embed)
+    Site s(c, lname("linear_up", l));
+    if (L.ledge > L.lin) launch_fill_zero(st, L.h_up.p, (int64_t)N * L.dedge);  // edge blocks without input
+    GemmGroup g{};
+    for (int b = 0; b < std::min(L.lin, L.ledge); ++b)
+      g.p[g.n++] = gprob(N, 2 * b + 1, NC, NC, h, L.din, NC * b * b, 0, L.upT[b].p, L.h_up.p, L.dedge, NC * b * b, 0);
+    run_gemm(c, st, g);
+  }
+  {
+    Site s(c, lname("tp_fwd", l));
+    launch_tp_fwd(st, L.ledge, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.w.p, L.h_up.p, c->M.p, 0);
+  }
+  {  // rinv = 1 / (beta rho + alpha)
+    Site s(c, lname("density", l));
+    launch_mh1_rho(st, N, c->rowptr.p, c->mh_dens.p, L.alpha, L.beta, L.rinv.p);
+  }
+  {
+    Site s(c, lname("linear_res", l));
+    GemmGroup g{};
+    for (int lo = 0; lo < L.ledge; ++lo) {
+      const int d = 2 * lo + 1;
+      g.p[g.n++] = gprob(N, d, NC, lo == 0 ? 4 * NC : NC, L.h_up.p, L.dedge, NC * lo * lo, 0, L.resT[lo].p, L.R.p,
+                         L.nres, gate_in_base(lo), NC * d);
+    }
+    run_gemm(c, st, g);
+  }
+  {  // Q = linear_1(M) / (beta rho + alpha)
+    Site s(c, lname("linear_msg", l));
+    const int* ao = tp_accoff(L.ledge);
+    GemmGroup g{};
+    for (int lo = 0; lo < 4; ++lo) {
+      int first, cnt;
+      slot_range(L, lo, &first, &cnt);
+      const int d = 2 * lo + 1;
+      g.p[g.n++] = gprob(N, d, cnt * NC, lo == 0 ? 4 * NC : NC, c->M.p, L.dmid, NC * ao[first], NC * d,
+                         L.linT[lo].p, L.Q.p, kGateInDim, gate_in_base(lo), NC * d);
+      g.p[g.n - 1].rowscale = L.rinv.p;
+    }
+    run_gemm(c, st, g);
+  }
+  {
+    Site s(c, lname("gate", l));
+    launch_mh1_gate(st, N, L.Q.p, L.R.p, L.nres, L.Gt.p);
+  }
+  {
+    Site s(c, lname("linear_2", l));
+    GemmGroup g{};
+    for (int lo = 0; lo < 4; ++lo)
+      g.p[g.n++] = gprob(N, 2 * lo + 1, NC, NC, L.Gt.p, L.dint, NC * lo * lo, 0, L.lin2T[lo].p, L.A.p, L.dint,
+                         NC * lo * lo, 0);
+    run_gemm(c, st, g);
+  }
+  const float* scw[3] = {L.sc[0].p, L.sc[1].p, L.sc[2].p};
+  {
+    Site s(c, lname("sc_fwd", l));
+    launch_sc_fwd(st, N, L.lhid, L.corr, L.A.p, L.dint, sc_species(c), scw, c->B.p, L.dhid, 0);
+  }
+  {  // h' = PLin(B) + Skip(h) (plain linear skip)
+    Site s(c, lname("linear_prod", l));
+    GemmGroup g{};
+    for (int b = 0; b < L.lhid; ++b) {
+      GemmProb P = gprob(N, 2 * b + 1, NC, NC, c->B.p, L.dhid, NC * b * b, 0, L.plinT[b].p, hn, L.dhid, NC * b * b, 0);
+      if (b < L.nskip) {
+        P.K2 = NC;
+        P.X2 = h;
+        P.ldx2 = L.din;
+        P.in_base2 = NC * b * b;
+        P.in_stride2 = 0;
+        P.WT2 = L.skipT[b].p;
+      }
+      g.p[g.n++] = P;
+    }
+    run_gemm(c, st, g);
+  }
+}
+
+// VJP of forward_nonlin: from gh = dE/dh_{l+1}; for l > 0 writes gh_next = dE/dh_l (with the
+// previous layer's linear readout as the 0e bias)
+void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int first_edge_grad) {
+  hipStream_t st = c->stream;
+  Layer& Ly = c->layers[l];
+  const int N = c->N;
+  const int64_t E = c->E;
+  const int nb = c->dims.num_bessel;
+  const float* cut = c->dims.separate_cutoff ? c->cutv.p : nullptr;
+  {  // gB = PLin^T gh
+    Site s(c, lname("linear_prod_bwd", l));
+    GemmGroup g{};
+    for (int b = 0; b < Ly.lhid; ++b)
+      g.p[g.n++] = gprob(N, 2 * b + 1, NC, NC, gh, Ly.dhid, NC * b * b, 0, Ly.plin[b].p, c->gB.p, Ly.dhid, NC * b * b, 0);
+    run_gemm(c, st, g);
+  }
+  const float* scw[3] = {Ly.sc[0].p, Ly.sc[1].p, Ly.sc[2].p};
+  {
+    Site s(c, lname("sc_bwd", l));
+    launch_sc_bwd(st, N, Ly.lhid, Ly.corr, Ly.A.p, Ly.dint, sc_species(c), scw, c->gB.p, Ly.dhid, c->gA.p);
+  }
+  {  // dL/dgate-output = Lin2^T gA
+    Site s(c, lname("linear_2_bwd", l));
+    GemmGroup g{};
+    for (int lo = 0; lo < 4; ++lo)
+      g.p[g.n++] = gprob(N, 2 * lo + 1, NC, NC, c->gA.p, Ly.dint, NC * lo * lo, 0, Ly.lin2[lo].p, c->gA2.p, Ly.dint,
+                         NC * lo * lo, 0);
+    run_gemm(c, st, g);
+  }
+  {
+    Site s(c, lname("gate_bwd", l));
+    launch_mh1_gate_bwd(st, N, Ly.Q.p, Ly.R.p, Ly.nres, c->gA2.p, c->gP.p);
+  }
+  {
+    Site s(c, lname("density_bwd", l));
+    launch_mh1_drho(st, N, c->gP.p, Ly.Q.p, Ly.rinv.p, Ly.beta, c->grho.p);
+  }
+  {  // gM = Lin1^T gP / (beta rho + alpha)
+    Site s(c, lname("linear_msg_bwd", l));
+    const int* ao = tp_accoff(Ly.ledge);
+    GemmGroup g{};
+    for (int lo = 0; lo < 4; ++lo) {
+      int first, cnt;
+      slot_range(Ly, lo, &first, &cnt);
+      const int d = 2 * lo + 1;
+      g.p[g.n++] = gprob(N, d, lo == 0 ? 4 * NC : NC, cnt * NC, c->gP.p, kGateInDim, gate_in_base(lo), NC * d,
+                         Ly.lin_[lo].p, c->gM.p, Ly.dmid, NC * ao[first], NC * d);
+      g.p[g.n - 1].rowscale = Ly.rinv.p;
+    }
+    run_gemm(c, st, g);
+  }
+  {
+    Site s(c, lname("tp_bwd", l));
+    launch_tp_bwd_recv(st, Ly.ledge, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p, Ly.h_up.p,
+                       c->gM.p, c->gw.p, c->gscale.p, c->gY.p, first_edge_grad, c->pos_s.p,
+                       l > 0 ? c->gxe.p : nullptr, 0);
+  }
+  if (l > 0) {
+    Site s(c, lname("tp_gather", l));
+    launch_tp_gather_gx(st, Ly.ledge, N, c->rowptr_s.p, c->gxe.p, c->gup.p);
+  }
+  {  // G = gw W3^T (into h3), gwb = gw . b3
+    Site s(c, lname("mlp_gh3", l));
+    launch_mlp_gh3(st, E, Ly.wn, c->gw.p, Ly.mlp[3].p, c->h3.p, Ly.b3.p, c->gwb.p);
+  }
+  {
+    Site s(c, lname("mlp_ln_bwd", l));
+    const size_t fb = mlp_tile_fwd_bytes();
+    launch_rmlp_ln_bwd(st, E, nb, c->ef.p, cut, c->sender.p, c->receiver.p, c->species.p, Ly.mlp_tiles.p,
+                       Ly.mlp_tiles.p + fb, Ly.dmlp_tiles.p, Ly.dmlp_tiles.p + fb, Ly.lnp(), c->h3.p, c->gwb.p,
+                       c->grho.p, c->gef.p, cut ? c->gcut.p : nullptr, first_edge_grad);
+  }
+  if (l == 0) return;
+  {  // gup += Res^T gP
+    Site s(c, lname("linear_res_bwd", l));
+    GemmGroup g{};
+    for (int lo = 0; lo < Ly.ledge; ++lo) {
+      const int d = 2 * lo + 1;
+      g.p[g.n++] = gprob(N, d, lo == 0 ? 4 * NC : NC, NC, c->gP.p, kGateInDim, gate_in_base(lo), NC * d,
+                         Ly.res_[lo].p, c->gup.p, Ly.dedge, NC * lo * lo, 0);
+      g.p[g.n - 1].accumulate = 1;
+    }
+    run_gemm(c, st, g);
+  }
+  {  // dE/dh_l = Up^T gup + Skip^T gh + readout_{l-1}' (bias on the 0e block)
+    Site s(c, lname("linear_up_bwd", l));
+    if (Ly.lin > std::max(Ly.ledge, Ly.nskip)) launch_fill_zero(st, gh_next, (int64_t)N * Ly.din);
+    GemmGroup g{};
+    for (int b = 0; b < Ly.lin; ++b) {
+      GemmProb P{};
+      if (b < Ly.ledge) {
+        P = gprob(N, 2 * b + 1, NC, NC, c->gup.p, Ly.dedge, NC * b * b, 0, Ly.up[b].p, gh_next, Ly.din, NC * b * b, 0);
+        if (b < Ly.nskip) {
+          P.K2 = NC;
+          P.X2 = gh;
+          P.ldx2 = Ly.dhid;
+          P.in_base2 = NC * b * b;
+          P.in_stride2 = 0;
+          P.WT2 = Ly.skip[b].p;
+        }
+      } else if (b < Ly.nskip) {
+        P = gprob(N, 2 * b + 1, NC, NC, gh, Ly.dhid, NC * b * b, 0, Ly.skip[b].p, gh_next, Ly.din, NC * b * b, 0);
+      } else {
+        continue;
+      }
+      if (b == 0) P.bias = c->layers[l - 1].ro.p;
+      g.p[g.n++] = P;
+    }
+    run_gemm(c, st, g);
+  }
+}
+
 void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
   if (c->profiling) c->launch_log.clear();  // a step starts here
   hipStream_t st = c->stream;
@@ -1012,7 +1363,7 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
   const int nb = c->dims.num_bessel;
   const int half = c->dims.feature_half != 0;
   const bool split = !half && c->split_products;
-  const bool fused = split && c->fused_tp && c->max_lin <= 2;
+  const bool fused = split && c->fused_tp && c->max_lin <= 2 && !c->dims.nonlinear;
   FrontParams fp = front_params(c);
   {
     Site s(c, "edge_fwd");
@@ -1020,12 +1371,16 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
                     c->zbl_cov.p, c->ag_cov.p, fp, c->G > 1 ? c->gcell.p : nullptr, c->gid.p, c->geom.p, c->Y.p,
                     c->ef.p, c->zbl_e.p, c->Mt.p, c->mts,
                     // the fused TP kernels build their tables on chip from Y
-                    (c->mts > 0 && !fused) ? tp_table_entries(c->max_lin) : 0);
+                    (c->mts > 0 && !fused) ? tp_table_entries(c->max_lin) : 0, c->cutv.p);
   }
   for (size_t l = 0; l < c->layers.size(); ++l) {
     Layer& L = c->layers[l];
     const float* h = c->h[l].p;
     float* hn = c->h[l + 1].p;
+    if (L.nonlin) {
+      forward_nonlin(c, (int)l, h, hn);
+      continue;
+    }
     {
       Site s(c, lname("mlp_hidden", l));
       // split: h3 holds E x 2 x 64 fp16 (the same bytes as E x 64 floats)
@@ -1040,11 +1395,11 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
     if (!fused) {
       Site s(c, lname("mlp_out", l));
       if (half)
-        launch_mlp_out(st, E, L.wn, c->h3h.p, L.mlpT3h.p, L.wh.p, 1);
+        launch_mlp_out(st, E, L.wn, c->h3h.p, L.mlpT3h.p, L.wh.p, 1, nullptr, nullptr);
       else if (split)
         launch_mlp_out_x(st, E, L.wn, c->h3.p, c->h3inv.p, L.mlpT3x.p, L.w3inv, L.w.p);
       else
-        launch_mlp_out(st, E, L.wn, c->h3.p, L.mlpT[3].p, L.w.p, 0);
+        launch_mlp_out(st, E, L.wn, c->h3.p, L.mlpT[3].p, L.w.p, 0, nullptr, nullptr);
     }
     if (l > 0) {  // the first layer's comes from the species table (launch_embed)
       Site s(c, lname("linear_up", l));
@@ -1090,7 +1445,7 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
     const float* scw[3] = {L.sc[0].p, L.sc[1].p, L.sc[2].p};
     {
       Site s(c, lname("sc_fwd", l));
-      launch_sc_fwd(st, N, L.lhid, L.corr, sc_in, L.dint, c->species.p, scw, c->B.p, L.dhid, half);
+      launch_sc_fwd(st, N, L.lhid, L.corr, sc_in, L.dint, sc_species(c), scw, c->B.p, L.dhid, half);
     }
     const bool one_el = c->dims.num_elements == 1;
     {
@@ -1146,7 +1501,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
   const int L = (int)c->layers.size();
   const int half = c->dims.feature_half != 0;
   const bool split = !half && c->split_products;
-  const bool fused = split && c->fused_tp && c->max_lin <= 2;
+  const bool fused = split && c->fused_tp && c->max_lin <= 2 && !c->dims.nonlinear;
   int gyp = 2;  // dL/dY partials per edge
   if (fused)
     for (const Layer& Ly : c->layers) gyp = std::max(gyp, tpx_parts(Ly.lin));
@@ -1155,6 +1510,11 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
   float* gh_next = c->gh1.p;
   for (int l = L - 1; l >= 0; --l) {
     Layer& Ly = c->layers[l];
+    if (Ly.nonlin) {
+      backward_nonlin(c, l, gh, gh_next, (l == L - 1) ? 0 : 1);
+      if (l > 0) std::swap(gh, gh_next);
+      continue;
+    }
     const bool one_el = c->dims.num_elements == 1;
     {  // gB = PLin^T gh
       Site s(c, lname("linear_prod_bwd", l));
@@ -1167,7 +1527,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
     const float* scw[3] = {Ly.sc[0].p, Ly.sc[1].p, Ly.sc[2].p};
     {
       Site s(c, lname("sc_bwd", l));
-      launch_sc_bwd(st, N, Ly.lhid, Ly.corr, Ly.resid ? Ly.A.p : Ly.A2.p, Ly.dint, c->species.p, scw, c->gB.p,
+      launch_sc_bwd(st, N, Ly.lhid, Ly.corr, Ly.resid ? Ly.A.p : Ly.A2.p, Ly.dint, sc_species(c), scw, c->gB.p,
                     Ly.dhid, c->gA.p);
     }
     // gradient of the (normalised) message linear's output
@@ -1225,7 +1585,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
       else if (split)
         launch_mlp_gh3_x(st, E, Ly.wn, c->gw.p, Ly.mlp3x.p, Ly.w3inv, c->h3.p);
       else
-        launch_mlp_gh3(st, E, Ly.wn, c->gw.p, Ly.mlp[3].p, c->h3.p);
+        launch_mlp_gh3(st, E, Ly.wn, c->gw.p, Ly.mlp[3].p, c->h3.p, nullptr, nullptr);
     }
     {
       Site s(c, lname("mlp_hidden_bwd", l));
@@ -1274,7 +1634,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
     Site s(c, "edge_bwd");
     launch_edge_bwd(st, E, c->sender.p, c->receiver.p, c->species.p, c->bessel_w.p, c->zbl_z.p, c->zbl_cov.p,
                     c->ag_cov.p, fp,
-                    c->geom.p, c->gY.p, gyp, c->gef.p, c->gv.p, stress ? vir_part : nullptr);
+                    c->geom.p, c->gY.p, gyp, c->gef.p, c->gv.p, stress ? vir_part : nullptr, c->gcut.p);
   }
   {
     Site s(c, "forces");
@@ -1336,8 +1696,9 @@ static void free_all(mace_ctx* c) {
   for (auto* b : {&c->gcell, &c->eg, &c->gvir}) b->release();
   for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->ag_cov, &c->gA2, &c->grho, &c->embed, &c->up0_tab, &c->sink, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
                   &c->gv, &c->gw, &c->gxe, &c->h3, &c->gh3p, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup,
-                  &c->node_e})
+                  &c->node_e, &c->cutv, &c->gcut, &c->mh_dens, &c->gwb, &c->gP})
     b->release();
+  c->zero_species.release();
   for (auto* b : {&c->species, &c->sender, &c->receiver, &c->shifts, &c->rowptr, &c->rowptr_s, &c->perm_s, &c->pos_s,
                   &c->nl_img, &c->nl_bin, &c->nl_bin_sorted, &c->nl_atoms, &c->nl_iota, &c->nl_counts,
                   &c->nl_bin_count, &c->nl_bin_start, &c->e_tmp_i, &c->e_tmp_j, &c->e_tmp_s, &c->e_perm,

@@ -73,6 +73,7 @@ struct FrontParams {
   int feature_half;      // float16 feature policy: SH and radial features rounded to fp16
   int agnesi;            // Agnesi distance transform of r before the Bessel basis
   float ag_q, ag_p, ag_a;
+  int apply_cutoff;      // 0: the envelope is not applied to ef; it goes to cut[e] (mh-1)
 };
 
 // x rounded to the nearest fp16 value when `half` (the stored activations of a
@@ -90,16 +91,28 @@ __device__ __forceinline__ float max4_rows(float m) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// sum of x over the four lanes {l, l ^ 16, l ^ 32, l ^ 48} (the same value, in the same
+// order of additions, on all four)
+__device__ __forceinline__ float sum4_rows(float m) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  m = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ag_cov: covalent radius per species for the Agnesi transform (unused without it)
+// cut (used when p.apply_cutoff == 0): the envelope of every edge, cut[e]
 void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* sender,
                      const int* receiver, const int* shifts, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov,
                      const float* ag_cov, const FrontParams& p, const double* gcell, const int* gid,
-                     EdgeGeom* geom, float* Y, float* ef, float* zbl_e, float* Mt, int mts, int nent);
+                     EdgeGeom* geom, float* Y, float* ef, float* zbl_e, float* Mt, int mts, int nent,
+                     float* cut);
+// gcut (used when p.apply_cutoff == 0): dL/dcut[e]
 void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov, const float* ag_cov,
                      const FrontParams& p, const EdgeGeom* geom, const float* gY, int gyp, const float* gef, float* gv,
-                     double* vir_part);
+                     double* vir_part, const float* gcut);
 // symmetrised virial from the per-block partials of launch_edge_bwd
 void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir);
 // a batch of G structures with atoms [gptr[g], gptr[g+1]): per-structure energies and virials
@@ -138,15 +151,59 @@ void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, con
 void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tiles, const float* winv3,
                              const float* ef, const float* ds, const float* gh3, int np, float* gef,
                              int accumulate);
-// half: h3, W3T and w fp16 arrays (fp32 accumulation); else fp32
+// half: h3, W3T and w fp16 arrays (fp32 accumulation); else fp32, and then with bias ([W], may be
+// null) and rs ([E], may be null): w = (h3 W3 + bias) rs[e]
 void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w,
-                    int half);
+                    int half, const float* bias, const float* rs);
 // float32 policy on fp16 matrix cores: w (fp32) from the split h3 of mode 2 and W3Tx = [hi | lo]
 // fp16 planes of W3^T [W][64] scaled by 1 / cscale
 void launch_mlp_out_x(hipStream_t st, int64_t E, int W, const void* h3x, const float* h3inv,
                       const void* W3Tx, float cscale, float* w);
-// VJP: gh3 = gw W3^T, then gef (+)= dL/def through the hidden layers (saved silu' values)
-void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3);
+// VJP: gh3 = gw W3^T, then gef (+)= dL/def through the hidden layers (saved silu' values);
+// with b3 ([W]) also gwb[e] = gw[e] . b3
+void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3,
+                    const float* b3, float* gwb);
+
+// mh-1 non-linear interaction block (blocks.py:611-807).  LayerNorm radial MLP (radial.py:344-357)
+// over [ef | source species embedding | target species embedding]: the species parts of the
+// first Linear are per-species tables ts / tt ([n_el][64], tt with the bias); tiles: the
+// launch_mlp_permute image of (ef part of layer 1 [nb][64], layer 2 [64][64], layer 3 [64][64]);
+// dtiles: the same for the density MLP's first layer (only its first matrix is used).
+struct LnMlpParams {
+  const float* ts;    // [n_el][64]
+  const float* tt;    // [n_el][64]
+  const float* ln;    // [3][2][64]: LayerNorm scale, shift after layers 1..3
+  const float* bias;  // [2][64]: biases of layers 2, 3
+  const float* dts;   // [n_el][64] density MLP
+  const float* dtt;   // [n_el][64] (+ bias)
+  const float* dln;   // [2][64]
+  const float* dw1;   // [65]: output weights, then the output bias
+};
+// h3 [E][64] = silu(LN(...)) of the third layer; dens[e] = tanh(x^2) cut[e] (cut may be null: 1)
+void launch_rmlp_ln_fwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut,
+                        const int* sender, const int* receiver, const int* species, const void* tiles,
+                        const void* dtiles, const LnMlpParams& P, float* h3, float* dens);
+// VJP from G = gw W3^T ([E][64]), gwb = gw . b3 ([E]) and drho ([N], dL/d(sum of the receiver's
+// edge densities)): gef (+)= dL/def ([E][nb]) and, with cut, gcut (+)= dL/dcut ([E]);
+// btiles / dbtiles: the transposed images (launch_mlp_permute's second half)
+void launch_rmlp_ln_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut,
+                        const int* sender, const int* receiver, const int* species, const void* tiles,
+                        const void* btiles, const void* dtiles, const void* dbtiles, const LnMlpParams& P,
+                        const float* G, const float* gwb, const float* drho, float* gef, float* gcut,
+                        int accumulate);
+size_t mlp_tile_fwd_bytes();  // offset of the transposed image inside an mlp_tile_bytes() block
+// node side of the mh-1 block.  Q [N][kGateInDim] = linear_1(M) / (beta rho + alpha), R [N][nres]
+// = linear_res(linear_up(h)) over the leading nres columns of the gate input layout
+// [scalars C | gates C x 3 | 1o 3C | 2e 5C | 3o 7C]; gout [N][16 C] = gate(Q + R)
+constexpr int kGateInDim = 19 * NC;
+void launch_mh1_rho(hipStream_t st, int N, const int* rowptr, const float* dens, float alpha, float beta,
+                    float* rinv);
+void launch_mh1_gate(hipStream_t st, int N, const float* Q, const float* R, int nres, float* gout);
+void launch_mh1_gate_bwd(hipStream_t st, int N, const float* Q, const float* R, int nres, const float* gG,
+                         float* gP);
+void launch_mh1_drho(hipStream_t st, int N, const float* gP, const float* Q, const float* rinv, float beta,
+                     float* drho);
+
 // float16 feature policy: gw fp16 with per-(edge, channel half) scales, W3 fp16 [64][W]
 void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const float* gscale, const void* W3h,
                       float* gh3);

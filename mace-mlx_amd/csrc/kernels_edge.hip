@@ -77,7 +77,8 @@ __global__ void __launch_bounds__(256) k_edge_fwd(
     const float* __restrict__ bessel_w, const float* __restrict__ zbl_z,
     const float* __restrict__ zbl_cov, const float* __restrict__ ag_cov, FrontParams p,
     const double* __restrict__ gcell, const int* __restrict__ gid, EdgeGeom* __restrict__ geom,
-    float* __restrict__ Y, float* __restrict__ ef, float* __restrict__ zbl_e, float* __restrict__ Mt, int mts) {
+    float* __restrict__ Y, float* __restrict__ ef, float* __restrict__ zbl_e, float* __restrict__ Mt, int mts,
+    float* __restrict__ cut) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= E) return;
   const int s = sender[e], r = receiver[e];
@@ -117,10 +118,13 @@ __global__ void __launch_bounds__(256) k_edge_fwd(
     float dtdr;
     rb = agnesi_t(rr, 0.5f * (ag_cov[species[s]] + ag_cov[species[r]]), p, &dtdr);
   }
+  // apply_cutoff = 0 (radial.py:316-318): the basis alone; the envelope goes to cut
+  const float envb = p.apply_cutoff ? env : 1.f;
+  if (!p.apply_cutoff) cut[e] = env;
   for (int n = 0; n < p.nbessel; ++n) {
     const float w = bessel_w[n];
     const float b = (rb == 0.f) ? p.bessel_pref * w : p.bessel_pref * sinf(w * rb) / rb;
-    ef[(int64_t)p.nbessel * e + n] = qh(b * env, p.feature_half);
+    ef[(int64_t)p.nbessel * e + n] = qh(b * envb, p.feature_half);
   }
   if (p.has_zbl) {
     const int zs = species[s], zr = species[r];
@@ -140,7 +144,8 @@ __global__ void __launch_bounds__(256) k_edge_bwd(
     const int* __restrict__ species, const float* __restrict__ bessel_w,
     const float* __restrict__ zbl_z, const float* __restrict__ zbl_cov, const float* __restrict__ ag_cov,
     FrontParams p, const EdgeGeom* __restrict__ geom, const float* __restrict__ gY, int gyp,
-    const float* __restrict__ gef, float* __restrict__ gv, double* __restrict__ vir_part) {
+    const float* __restrict__ gef, float* __restrict__ gv, double* __restrict__ vir_part,
+    const float* __restrict__ gcut) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   double vir[9];
 #pragma unroll
@@ -179,7 +184,9 @@ __global__ void __launch_bounds__(256) k_edge_bwd(
     const float env = poly_env(rr / p.r_max, p.pcut, &denv);
     float rb = rr, drb = 1.f;  // Bessel argument and its derivative in r
     if (p.agnesi) rb = agnesi_t(rr, 0.5f * (ag_cov[species[sender[e]]] + ag_cov[species[receiver[e]]]), p, &drb);
-    float gr = 0.f;
+    // with a separate cutoff the features are the basis alone and dL/dcut enters here
+    float gr = p.apply_cutoff ? 0.f : gcut[e] * denv / p.r_max;
+    const float envb = p.apply_cutoff ? env : 1.f, denvb = p.apply_cutoff ? denv : 0.f;
     for (int n = 0; n < p.nbessel; ++n) {
       const float w = bessel_w[n];
       float b, db;
@@ -192,7 +199,7 @@ __global__ void __launch_bounds__(256) k_edge_bwd(
         b = p.bessel_pref * sn / rb;
         db = p.bessel_pref * (w * cs * rb - sn) / (rb * rb);
       }
-      gr += gef[(int64_t)p.nbessel * e + n] * (db * drb * env + b * denv / p.r_max);
+      gr += gef[(int64_t)p.nbessel * e + n] * (db * drb * envb + b * denvb / p.r_max);
     }
     if (p.has_zbl) {
       const int zs = species[sender[e]], zr = species[receiver[e]];
@@ -437,11 +444,11 @@ void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* se
                      const int* shifts, const int* species, const float* bessel_w, const float* zbl_z,
                      const float* zbl_cov, const float* ag_cov, const FrontParams& p, const double* gcell,
                      const int* gid, EdgeGeom* geom, float* Y, float* ef, float* zbl_e, float* Mt, int mts,
-                     int nent) {
+                     int nent, float* cut) {
   if (E <= 0) return;
 #define MACE_EDGE_FWD(NE)                                                                                      \
   MACE_LAUNCH(k_edge_fwd<NE>, dim3(nblk(E, 256)), dim3(256), 0, st, E, pos, sender, receiver, shifts, \
-                     species, bessel_w, zbl_z, zbl_cov, ag_cov, p, gcell, gid, geom, Y, ef, zbl_e, Mt, mts)
+                     species, bessel_w, zbl_z, zbl_cov, ag_cov, p, gcell, gid, geom, Y, ef, zbl_e, Mt, mts, cut)
   if (nent == 0) MACE_EDGE_FWD(0);
   else if (nent == TP3_M1_NE) MACE_EDGE_FWD(TP3_M1_NE);
   else MACE_EDGE_FWD(TP3_M1_NE + TP3_M2_NE);
@@ -451,10 +458,10 @@ void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* se
 void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov, const float* ag_cov,
                      const FrontParams& p, const EdgeGeom* geom, const float* gY, int gyp, const float* gef,
-                     float* gv, double* vir_part) {
+                     float* gv, double* vir_part, const float* gcut) {
   if (E <= 0) return;
   MACE_LAUNCH(k_edge_bwd, dim3(nblk(E, 256)), dim3(256), 0, st, E, sender, receiver, species,
-                     bessel_w, zbl_z, zbl_cov, ag_cov, p, geom, gY, gyp, gef, gv, vir_part);
+                     bessel_w, zbl_z, zbl_cov, ag_cov, p, geom, gY, gyp, gef, gv, vir_part, gcut);
 }
 
 void launch_density_fwd(hipStream_t st, int N, const int* rowptr, const float* ef, int nb, const float* wd,

@@ -265,8 +265,11 @@ __global__ void __launch_bounds__(256) k_mlp_hidden(int64_t E, int nb, const flo
 // result goes through a wave-private LDS tile so that it is written as whole
 // 128-byte row segments.  (Plain stores: the TP kernel that reads w next finds
 // it in the last-level cache.)
+// bias (optional, [W]) and rs (optional, [E]): w = (h3 W3 + bias) rs[row] (the mh-1 block's output
+// layer with its bias and, under apply_cutoff = false, the edge's envelope)
 __global__ void __launch_bounds__(256) k_mlp_out(int64_t E, int W, const float* __restrict__ h3,
-                                                 const float* __restrict__ W3T, float* __restrict__ w) {
+                                                 const float* __restrict__ W3T, float* __restrict__ w,
+                                                 const float* __restrict__ bias, const float* __restrict__ rs) {
   __shared__ __align__(16) float sO[4][64][36];
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t row0 = (int64_t)blockIdx.x * 64;
@@ -319,7 +322,16 @@ __global__ void __launch_bounds__(256) k_mlp_out(int64_t E, int W, const float* 
       const int rr = (l >> 3) + 8 * q;
       const int64_t row = row0 + rr;
       if (row < E && c0 + 4 * (l & 7) < ce) {
-        *reinterpret_cast<float4*>(&w[row * W + c0 + 4 * (l & 7)]) = ld4(&O[rr][4 * (l & 7)]);
+        float4 o = ld4(&O[rr][4 * (l & 7)]);
+        if (bias) {
+          const float4 bb = ld4(bias + c0 + 4 * (l & 7));
+          o = float4{o.x + bb.x, o.y + bb.y, o.z + bb.z, o.w + bb.w};
+        }
+        if (rs) {
+          const float f = rs[row];
+          o = float4{o.x * f, o.y * f, o.z * f, o.w * f};
+        }
+        *reinterpret_cast<float4*>(&w[row * W + c0 + 4 * (l & 7)]) = o;
       }
     }
     wave_sync();
@@ -508,9 +520,13 @@ __global__ void __launch_bounds__(256) k_mlp_out_x(int64_t E, int W, const _Floa
 // LDS in a fixed order.
 constexpr int GH_PF = 4;
 
+// b3 (optional, [W]): also gwb[row] = sum_c gw[row][c] b3[c] (the mh-1 output layer's bias), summed
+// per lane, over the lane's four k groups and over the four waves in a fixed order
 __global__ void __launch_bounds__(256) k_mlp_gh3(int64_t E, int W, const float* __restrict__ gw,
-                                                 const float* __restrict__ W3, float* __restrict__ gh3) {
+                                                 const float* __restrict__ W3, float* __restrict__ gh3,
+                                                 const float* __restrict__ b3, float* __restrict__ gwb) {
   __shared__ f4v sP[4][8][64];
+  __shared__ float sB[4][2][16];
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t row0 = (int64_t)blockIdx.x * 32;
   const int kq = W / 4, kb = wv * kq, nch = kq / 16;
@@ -533,6 +549,7 @@ __global__ void __launch_bounds__(256) k_mlp_gh3(int64_t E, int W, const float* 
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc[t][u] = f4v{0.f, 0.f, 0.f, 0.f};
+  float pb[2] = {0.f, 0.f};  // this lane's share of gw . b3 for its two rows
   for (int ch = 0; ch < nch; ch += GH_PF) {
 #pragma unroll
     for (int p = 0; p < GH_PF; ++p) {
@@ -542,6 +559,12 @@ __global__ void __launch_bounds__(256) k_mlp_gh3(int64_t E, int W, const float* 
 #pragma unroll
         for (int u = 0; u < 4; ++u) bn[u] = ld4(br + (int64_t)16 * u * W + 16 * nbk);
         const float4 cur[2] = {ring[p][0], ring[p][1]};
+        if (b3) {
+          const float4 bb = ld4(b3 + kb + 16 * cc + 4 * g);
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+            pb[t] = fmaf(cur[t].w, bb.w, fmaf(cur[t].z, bb.z, fmaf(cur[t].y, bb.y, fmaf(cur[t].x, bb.x, pb[t]))));
+        }
 #pragma unroll
         for (int t = 0; t < 2; ++t) ring[p][t] = ld4(ar[t] + 16 * na);
         __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the multiplies
@@ -558,7 +581,19 @@ __global__ void __launch_bounds__(256) k_mlp_gh3(int64_t E, int W, const float* 
   }
 #pragma unroll
   for (int t = 0; t < 8; ++t) sP[wv][t][l] = acc[t >> 2][t & 3];
+  if (b3) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const float q = sum4_rows(pb[t]);  // the four k groups of row 16 t + r
+      if (g == 0) sB[wv][t][r] = q;
+    }
+  }
   __syncthreads();
+  if (b3 && wv == 0 && l < 32) {
+    const int t = l >> 4;
+    const int64_t row = row0 + 16 * t + r;
+    if (row < E) gwb[row] = ((sB[0][t][r] + sB[1][t][r]) + sB[2][t][r]) + sB[3][t][r];
+  }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int t = 2 * wv + h, rt = t >> 2, ct = t & 3;
@@ -1156,6 +1191,266 @@ __global__ void __launch_bounds__(64 * NW) k_mlp_hidden_bwd_x(int64_t E, int nb,
 
 inline unsigned nblk(int64_t n, int b) { return (unsigned)((n + b - 1) / b); }
 
+
+// ---------------------------------------------------------------------------
+// mh-1 non-linear interaction block: LayerNorm radial MLP and density MLP
+// (blocks.py:735-807, radial.py:344-357) on fp32 matrix cores, 16 edges per
+// wave in the register layout of the hidden-layer kernels above (lane (g, r)
+// holds edge r's features n = 16t + 4g + i as v[4t + i]).
+//   z1 = W0e^T ef + ts[species(sender)] + tt[species(receiver)]   (tt holds b1)
+//   a_k = silu(LN(z_k) s_k + c_k),  z_{k+1} = W_k^T a_k + bias_k,  h3 = a_3
+// A LayerNorm's statistics over an edge's 64 features: 16 values in each of its
+// four lanes, summed locally, then over the lanes (sum4_rows); two passes (mean,
+// then the centred second moment), eps 1e-5 (MLX's default).
+// Density: zd = Wd0e^T ef + dts + dtt, ad = silu(LN(zd) sd + cd), x = wd1 . ad + bd1,
+// dens = tanh(x^2) cut.
+// ---------------------------------------------------------------------------
+struct LnSmall {  // the small per-layer vectors, staged in LDS
+  float ln[3][2][64];
+  float bias[2][64];
+  float dln[2][64];
+  float dw1[68];
+};
+
+__device__ __forceinline__ void stage_small(LnSmall& S, const LnMlpParams& P) {
+  for (int i = threadIdx.x; i < 384; i += blockDim.x) (&S.ln[0][0][0])[i] = P.ln[i];
+  for (int i = threadIdx.x; i < 128; i += blockDim.x) {
+    (&S.bias[0][0])[i] = P.bias[i];
+    (&S.dln[0][0])[i] = P.dln[i];
+  }
+  for (int i = threadIdx.x; i < 65; i += blockDim.x) S.dw1[i] = P.dw1[i];
+}
+
+// the lane's 16 features of a per-species table row
+__device__ __forceinline__ void add_row16(const float* __restrict__ row, int g, float* z) {
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const float4 x = ld4(row + 16 * t + 4 * g);
+    z[4 * t] += x.x, z[4 * t + 1] += x.y, z[4 * t + 2] += x.z, z[4 * t + 3] += x.w;
+  }
+}
+
+// LayerNorm of an edge's features z (the lane's 16): xh = (z - mean) * rstd
+__device__ __forceinline__ float ln_stats(const float* z, float* xh) {
+  float s = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) s += z[q];
+  const float mu = sum4_rows(s) * (1.f / 64.f);
+  float v = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const float d = z[q] - mu;
+    v = fmaf(d, d, v);
+  }
+  const float rstd = 1.f / sqrtf(sum4_rows(v) * (1.f / 64.f) + 1e-5f);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) xh[q] = (z[q] - mu) * rstd;
+  return rstd;
+}
+
+__device__ __forceinline__ int fidx(int q, int g) { return 16 * (q >> 2) + 4 * g + (q & 3); }
+
+// the first layer's ef part: acc[t'] = W0^T ef for the lane's edge (w0 tile image)
+__device__ __forceinline__ void first_layer(const float4 (*w0)[4][16], const float* __restrict__ ef, int64_t ec,
+                                            int nb, f4v* acc) {
+  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
+  const int nst = (nb + 3) >> 2;
+  for (int st = 0; st < nst; ++st) {
+    const int k = 4 * st + g;
+    const float x = k < nb ? ef[ec * nb + k] : 0.f;
+    const float4 wv = w0[st][g][r];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = mfma16(comp(wv, t), x, acc[t]);
+  }
+}
+
+// forward of one edge group, keeping what the VJP needs: xh[k] (normalised z of layer k),
+// rstd[k], h3 = a_3; density: xhd, rstdd, x
+struct LnFwdState {
+  float xh[3][16];
+  float rstd[3];
+  float h3[16];
+  float xhd[16];
+  float rstdd, x;
+};
+
+__device__ __forceinline__ void ln_mlp_fwd(const MlpFwdW& sw, const float4 (*dw0)[4][16], const LnSmall& S,
+                                           const LnMlpParams& P, const float* __restrict__ ef, int64_t ec, int nb,
+                                           int zs, int zr, LnFwdState& F) {
+  const int l = threadIdx.x & 63, g = l >> 4;
+  f4v acc[4];
+  float z[16], v[16];
+  first_layer(sw.w0, ef, ec, nb, acc);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) z[q] = acc[q >> 2][q & 3];
+  add_row16(P.ts + (int64_t)zs * H, g, z);
+  add_row16(P.tt + (int64_t)zr * H, g, z);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    F.rstd[k] = ln_stats(z, F.xh[k]);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int n = fidx(q, g);
+      v[q] = silu(fmaf(F.xh[k][q], S.ln[k][0][n], S.ln[k][1][n]));
+    }
+    if (k < 2) {
+      layer64(k == 0 ? sw.w1 : sw.w2, v, acc);
+#pragma unroll
+      for (int q = 0; q < 16; ++q) z[q] = acc[q >> 2][q & 3] + S.bias[k][fidx(q, g)];
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 16; ++q) F.h3[q] = v[q];
+  // density MLP
+  first_layer(dw0, ef, ec, nb, acc);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) z[q] = acc[q >> 2][q & 3];
+  add_row16(P.dts + (int64_t)zs * H, g, z);
+  add_row16(P.dtt + (int64_t)zr * H, g, z);
+  F.rstdd = ln_stats(z, F.xhd);
+  float xs = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int n = fidx(q, g);
+    xs = fmaf(silu(fmaf(F.xhd[q], S.dln[0][n], S.dln[1][n])), S.dw1[n], xs);
+  }
+  F.x = sum4_rows(xs) + S.dw1[64];
+}
+
+__global__ void __launch_bounds__(256) k_rmlp_ln_fwd(int64_t E, int nb, const float* __restrict__ ef,
+                                                     const float* __restrict__ cut, const int* __restrict__ sender,
+                                                     const int* __restrict__ receiver,
+                                                     const int* __restrict__ species, const MlpFwdW* __restrict__ tiles,
+                                                     const MlpFwdW* __restrict__ dtiles, LnMlpParams P,
+                                                     float* __restrict__ h3, float* __restrict__ dens) {
+  __shared__ MlpFwdW sw;
+  __shared__ float4 sdw0[NB4][4][16];
+  __shared__ LnSmall S;
+  stage_copy(sw, tiles);
+  for (int i = threadIdx.x; i < NB4 * 4 * 16; i += blockDim.x) (&sdw0[0][0][0])[i] = (&dtiles->w0[0][0][0])[i];
+  stage_small(S, P);
+  __syncthreads();
+  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const int64_t ngroups = (E + 15) / 16;
+  for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
+    const int64_t e = gi * 16 + r, ec = e < E ? e : E - 1;  // rows past the end: computed, not stored
+    const int zs = species[sender[ec]], zr = species[receiver[ec]];
+    LnFwdState F;
+    ln_mlp_fwd(sw, sdw0, S, P, ef, ec, nb, zs, zr, F);
+    if (e < E) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        *reinterpret_cast<float4*>(h3 + e * H + 16 * t + 4 * g) =
+            float4{F.h3[4 * t], F.h3[4 * t + 1], F.h3[4 * t + 2], F.h3[4 * t + 3]};
+      if (g == 0) dens[e] = tanhf(F.x * F.x) * (cut ? cut[e] : 1.f);
+    }
+  }
+}
+
+// LayerNorm + SiLU VJP of one layer: dz from dL/da (g), in place
+__device__ __forceinline__ void ln_silu_bwd(float* gv, const float* xh, float rstd, const float* sc, const float* sh,
+                                            int g) {
+  float dxh[16], s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int n = fidx(q, g);
+    const float y = fmaf(xh[q], sc[n], sh[n]);
+    dxh[q] = gv[q] * dsilu(y) * sc[n];
+    s1 += dxh[q];
+    s2 = fmaf(dxh[q], xh[q], s2);
+  }
+  s1 = sum4_rows(s1) * (1.f / 64.f);
+  s2 = sum4_rows(s2) * (1.f / 64.f);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) gv[q] = rstd * (dxh[q] - s1 - xh[q] * s2);
+}
+
+// gef contributions of a first layer: o[i] = sum_n W0[k = 4g + i][n] dz[n] (w0T tile image)
+__device__ __forceinline__ void first_layer_T(const float4 (*w0T)[4][16], const float* dz, f4v& o) {
+  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const float4 wq = w0T[t][g][r];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o = mfma16(comp(wq, i), dz[4 * t + i], o);
+  }
+}
+
+__global__ void __launch_bounds__(256) k_rmlp_ln_bwd(int64_t E, int nb, const float* __restrict__ ef,
+                                                     const float* __restrict__ cut, const int* __restrict__ sender,
+                                                     const int* __restrict__ receiver,
+                                                     const int* __restrict__ species, const MlpFwdW* __restrict__ tiles,
+                                                     const MlpBwdW* __restrict__ btiles,
+                                                     const MlpFwdW* __restrict__ dtiles,
+                                                     const MlpBwdW* __restrict__ dbtiles, LnMlpParams P,
+                                                     const float* __restrict__ G, const float* __restrict__ gwb,
+                                                     const float* __restrict__ drho, float* __restrict__ gef,
+                                                     float* __restrict__ gcut, int accumulate) {
+  __shared__ MlpFwdW sw;
+  __shared__ MlpBwdW sb;
+  __shared__ float4 sdw0[NB4][4][16];
+  __shared__ float4 sdw0T[4][4][16];
+  __shared__ LnSmall S;
+  stage_copy(sw, tiles);
+  stage_copy(sb, btiles);
+  for (int i = threadIdx.x; i < NB4 * 4 * 16; i += blockDim.x) (&sdw0[0][0][0])[i] = (&dtiles->w0[0][0][0])[i];
+  for (int i = threadIdx.x; i < 4 * 4 * 16; i += blockDim.x) (&sdw0T[0][0][0])[i] = (&dbtiles->w0T[0][0][0])[i];
+  stage_small(S, P);
+  __syncthreads();
+  const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const int64_t ngroups = (E + 15) / 16;
+  for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
+    const int64_t e = gi * 16 + r, ec = e < E ? e : E - 1;
+    const int rcv = receiver[ec];
+    const int zs = species[sender[ec]], zr = species[rcv];
+    LnFwdState F;
+    ln_mlp_fwd(sw, sdw0, S, P, ef, ec, nb, zs, zr, F);
+    const float ce = cut ? cut[ec] : 1.f;
+    float gv[16];
+    ld_row16(G + ec * H, g, gv);
+    // w = cut (h3 W3 + b3): dL/dcut = h3 . G + gw . b3, dL/dh3 = cut G
+    float hg = 0.f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) hg = fmaf(F.h3[q], gv[q], hg);
+    float gc = sum4_rows(hg) + gwb[ec];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) gv[q] *= ce;
+    f4v acc[4];
+#pragma unroll
+    for (int k = 2; k >= 0; --k) {
+      ln_silu_bwd(gv, F.xh[k], F.rstd[k], S.ln[k][0], S.ln[k][1], g);
+      if (k > 0) {
+        layer64(k == 2 ? sb.w2T : sb.w1T, gv, acc);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) gv[q] = acc[q >> 2][q & 3];
+      }
+    }
+    f4v o = f4v{0.f, 0.f, 0.f, 0.f};
+    first_layer_T(sb.w0T, gv, o);
+    // density: dens = tanh(x^2) cut, rho[receiver] = sum of dens
+    const float th = tanhf(F.x * F.x);
+    const float gd = drho[rcv];
+    gc = fmaf(gd, th, gc);
+    const float gx = gd * ce * (1.f - th * th) * 2.f * F.x;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) gv[q] = gx * S.dw1[fidx(q, g)];
+    ln_silu_bwd(gv, F.xhd, F.rstdd, S.dln[0], S.dln[1], g);
+    first_layer_T(sdw0T, gv, o);
+    if (e < E) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int k = 4 * g + i;
+        if (k < nb) {
+          float* dst = gef + e * nb + k;
+          *dst = accumulate ? *dst + o[i] : o[i];
+        }
+      }
+      if (gcut && g == 0) gcut[e] = accumulate ? gcut[e] + gc : gc;
+    }
+  }
+}
 }  // namespace
 
 // grid of the hidden-layer kernels: enough blocks to fill the device, each
@@ -1222,14 +1517,15 @@ void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const
     MACE_LAUNCH(k_mlp_hidden<H3_F32>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
 }
 
-void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w, int half) {
+void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w, int half,
+                    const float* bias, const float* rs) {
   if (E <= 0) return;
   if (half)
     MACE_LAUNCH(k_mlp_out_h, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const _Float16*>(h3),
                        static_cast<const _Float16*>(W3T), static_cast<_Float16*>(w));
   else
     MACE_LAUNCH(k_mlp_out, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const float*>(h3),
-                       static_cast<const float*>(W3T), static_cast<float*>(w));
+                       static_cast<const float*>(W3T), static_cast<float*>(w), bias, rs);
 }
 
 void launch_mlp_out_x(hipStream_t st, int64_t E, int W, const void* h3x, const float* h3inv, const void* W3Tx,
@@ -1239,9 +1535,10 @@ void launch_mlp_out_x(hipStream_t st, int64_t E, int W, const void* h3x, const f
                      h3inv, static_cast<const _Float16*>(W3Tx), cscale, w);
 }
 
-void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3) {
+void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3,
+                    const float* b3, float* gwb) {
   if (E <= 0) return;
-  MACE_LAUNCH(k_mlp_gh3, dim3(nblk(E, 32)), dim3(256), 0, st, E, W, gw, W3, gh3);
+  MACE_LAUNCH(k_mlp_gh3, dim3(nblk(E, 32)), dim3(256), 0, st, E, W, gw, W3, gh3, b3, gwb);
 }
 
 void launch_mlp_gh3_x(hipStream_t st, int64_t E, int W, const float* gw, const void* W3x, float cscale,
@@ -1263,6 +1560,27 @@ void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const void* tiles,
   if (E <= 0) return;
   const MlpBwdW* bw = reinterpret_cast<const MlpBwdW*>(static_cast<const char*>(tiles) + sizeof(MlpFwdW));
   MACE_LAUNCH(k_mlp_hidden_bwd, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, bw, ds, gh3, gef, accumulate);
+}
+
+size_t mlp_tile_fwd_bytes() { return sizeof(MlpFwdW); }
+
+void launch_rmlp_ln_fwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut, const int* sender,
+                        const int* receiver, const int* species, const void* tiles, const void* dtiles,
+                        const LnMlpParams& P, float* h3, float* dens) {
+  if (E <= 0) return;
+  MACE_LAUNCH(k_rmlp_ln_fwd, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, cut, sender, receiver, species,
+              static_cast<const MlpFwdW*>(tiles), static_cast<const MlpFwdW*>(dtiles), P, h3, dens);
+}
+
+void launch_rmlp_ln_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut, const int* sender,
+                        const int* receiver, const int* species, const void* tiles, const void* btiles,
+                        const void* dtiles, const void* dbtiles, const LnMlpParams& P, const float* G,
+                        const float* gwb, const float* drho, float* gef, float* gcut, int accumulate) {
+  if (E <= 0) return;
+  MACE_LAUNCH(k_rmlp_ln_bwd, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, cut, sender, receiver, species,
+              static_cast<const MlpFwdW*>(tiles), static_cast<const MlpBwdW*>(btiles),
+              static_cast<const MlpFwdW*>(dtiles), static_cast<const MlpBwdW*>(dbtiles), P, G, gwb, drho, gef,
+              gcut, accumulate);
 }
 
 }  // namespace mace

@@ -655,6 +655,88 @@ __global__ void __launch_bounds__(256) k_graph_virial(const int* __restrict__ gp
   }
 }
 
+// ---------------------------------------------------------------------------
+// mh-1 non-linear interaction block, node side (blocks.py:735-807).  Q = linear_1(M) / (beta
+// rho + alpha) and R = linear_res(up) in the gate-input layout [scalars C | gates of the
+// l = 1, 2, 3 blocks, C each | 1o 3C | 2e 5C | 3o 7C] (component-major blocks; R covers the
+// prefix of nres columns its input blocks reach); the gate (gate.py:19-164) writes the
+// interaction irreps [0e C | 1o 3C | 2e 5C | 3o 7C].
+// ---------------------------------------------------------------------------
+constexpr float kSiluNorm = 1.6791768074035645f;     // normalize2mom(silu)
+constexpr float kSigmoidNorm = 1.8467055569904827f;  // normalize2mom(sigmoid)
+
+__device__ __forceinline__ float sigm(float x) { return 1.f / (1.f + expf(-x)); }
+
+// rinv[n] = 1 / (beta rho_n + alpha), rho_n = sum of the receiver's edge densities (fixed order)
+__global__ void __launch_bounds__(256) k_mh1_rho(int N, const int* __restrict__ rowptr, const float* __restrict__ dens,
+                                                 float alpha, float beta, float* __restrict__ rinv) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+  if (n >= N) return;
+  float acc = 0.f;
+  for (int e = rowptr[n] + l; e < rowptr[n + 1]; e += 64) acc += dens[e];
+  acc = wave_sum(acc);
+  if (l == 0) rinv[n] = 1.f / fmaf(beta, acc, alpha);
+}
+
+__device__ __forceinline__ float gate_in(const float* __restrict__ q, const float* __restrict__ rr, int nres, int j) {
+  return j < nres ? q[j] + rr[j] : q[j];
+}
+
+// one thread per (node, channel): gout = gate(Q + R)
+__global__ void __launch_bounds__(NC) k_mh1_gate(int N, const float* __restrict__ Q, const float* __restrict__ R,
+                                                 int nres, float* __restrict__ gout) {
+  const int n = blockIdx.x, u = threadIdx.x;
+  const float* q = Q + (int64_t)n * kGateInDim;
+  const float* rr = R + (int64_t)n * nres;
+  float* o = gout + (int64_t)n * 16 * NC;
+  const float s = gate_in(q, rr, nres, u);
+  o[u] = kSiluNorm * s * sigm(s);
+#pragma unroll
+  for (int l = 1; l <= 3; ++l) {
+    const float gt = kSigmoidNorm * sigm(gate_in(q, rr, nres, l * NC + u));
+    const int qb = 4 * NC + NC * (l * l - 1), ob = NC * l * l;
+    for (int m = 0; m < 2 * l + 1; ++m) o[ob + m * NC + u] = gt * gate_in(q, rr, nres, qb + m * NC + u);
+  }
+}
+
+// VJP: gP = dL/d(Q + R) from gG = dL/dgout
+__global__ void __launch_bounds__(NC) k_mh1_gate_bwd(int N, const float* __restrict__ Q, const float* __restrict__ R,
+                                                     int nres, const float* __restrict__ gG, float* __restrict__ gP) {
+  const int n = blockIdx.x, u = threadIdx.x;
+  const float* q = Q + (int64_t)n * kGateInDim;
+  const float* rr = R + (int64_t)n * nres;
+  const float* go = gG + (int64_t)n * 16 * NC;
+  float* gp = gP + (int64_t)n * kGateInDim;
+  const float s = gate_in(q, rr, nres, u);
+  const float sg = sigm(s);
+  gp[u] = go[u] * kSiluNorm * sg * (1.f + s * (1.f - sg));
+#pragma unroll
+  for (int l = 1; l <= 3; ++l) {
+    const float gs = sigm(gate_in(q, rr, nres, l * NC + u));
+    const int qb = 4 * NC + NC * (l * l - 1), ob = NC * l * l;
+    float dgt = 0.f;
+    for (int m = 0; m < 2 * l + 1; ++m) {
+      const float gm = go[ob + m * NC + u];
+      dgt = fmaf(gm, gate_in(q, rr, nres, qb + m * NC + u), dgt);
+      gp[qb + m * NC + u] = kSigmoidNorm * gs * gm;
+    }
+    gp[l * NC + u] = dgt * kSigmoidNorm * gs * (1.f - gs);
+  }
+}
+
+// dL/drho[n] = -beta rinv[n] sum_j gP[n][j] Q[n][j]   (Q = linear_1(M) rinv)
+__global__ void __launch_bounds__(256) k_mh1_drho(int N, const float* __restrict__ gP, const float* __restrict__ Q,
+                                                  const float* __restrict__ rinv, float beta, float* __restrict__ drho) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
+  if (n >= N) return;
+  const float* g = gP + (int64_t)n * kGateInDim;
+  const float* q = Q + (int64_t)n * kGateInDim;
+  float acc = 0.f;
+  for (int j = l; j < kGateInDim; j += 64) acc = fmaf(g[j], q[j], acc);
+  acc = wave_sum(acc);
+  if (l == 0) drho[n] = -beta * rinv[n] * acc;
+}
+
 }  // namespace
 
 static inline unsigned cdiv(int64_t a, int b) { return (unsigned)((a + b - 1) / b); }
@@ -786,5 +868,28 @@ void launch_gemm_group(hipStream_t st, GemmGroup& g) {
     MACE_LAUNCH((k_gemm_group<1, 8, true>), dim3(tiles), dim3(256), 0, st, g);
 }
 
+
+void launch_mh1_rho(hipStream_t st, int N, const int* rowptr, const float* dens, float alpha, float beta,
+                    float* rinv) {
+  if (N <= 0) return;
+  MACE_LAUNCH(k_mh1_rho, dim3((N + 3) / 4), dim3(256), 0, st, N, rowptr, dens, alpha, beta, rinv);
+}
+
+void launch_mh1_gate(hipStream_t st, int N, const float* Q, const float* R, int nres, float* gout) {
+  if (N <= 0) return;
+  MACE_LAUNCH(k_mh1_gate, dim3(N), dim3(NC), 0, st, N, Q, R, nres, gout);
+}
+
+void launch_mh1_gate_bwd(hipStream_t st, int N, const float* Q, const float* R, int nres, const float* gG,
+                         float* gP) {
+  if (N <= 0) return;
+  MACE_LAUNCH(k_mh1_gate_bwd, dim3(N), dim3(NC), 0, st, N, Q, R, nres, gG, gP);
+}
+
+void launch_mh1_drho(hipStream_t st, int N, const float* gP, const float* Q, const float* rinv, float beta,
+                     float* drho) {
+  if (N <= 0) return;
+  MACE_LAUNCH(k_mh1_drho, dim3((N + 3) / 4), dim3(256), 0, st, N, gP, Q, rinv, beta, drho);
+}
 
 }  // namespace mace

@@ -58,6 +58,8 @@ class ModelDims(ctypes.Structure):
         ("feature_half", ctypes.c_int32), ("density_norm", ctypes.c_int32),
         ("first_nonresidual", ctypes.c_int32), ("agnesi", ctypes.c_int32),
         ("agnesi_q", ctypes.c_double), ("agnesi_p", ctypes.c_double), ("agnesi_a", ctypes.c_double),
+        ("nonlinear", ctypes.c_int32), ("separate_cutoff", ctypes.c_int32),
+        ("agnostic_product", ctypes.c_int32), ("layer_edge_blocks", ctypes.c_int32 * 4),
     ]
 
 

@@ -85,8 +85,8 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = 
     if dtype == "float16":
         w = round_weights_fp16(w)
     cfg.check_supported()
-    if cfg.nonlinear or cfg.use_agnostic_product or not cfg.apply_cutoff:
-        raise UnsupportedModel("non-linear interaction blocks / agnostic product / separate cutoff")
+    if cfg.nonlinear and dtype == "float16":
+        raise UnsupportedModel("non-linear interaction blocks under the float16 feature policy")
     cfg, w = select_head(cfg, w, head)
     if cfg.model_type not in ("MACE", "ScaleShiftMACE"):
         raise UnsupportedModel(f"model_type={cfg.model_type}")
@@ -121,7 +121,9 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = 
                 feature_half=int(dtype == "float16"),
                 density_norm=int(bool(cfg.use_density_normalization)),
                 first_nonresidual=int(bool(cfg.first_interaction_nonresidual)),
-                agnesi=int(cfg.agnesi() is not None), agnesi_q=0.0, agnesi_p=0.0, agnesi_a=0.0)
+                agnesi=int(cfg.agnesi() is not None), agnesi_q=0.0, agnesi_p=0.0, agnesi_a=0.0,
+                nonlinear=int(cfg.nonlinear), separate_cutoff=int(not cfg.apply_cutoff),
+                agnostic_product=int(bool(cfg.use_agnostic_product)), layer_edge_blocks=[0] * 4)
     ag = cfg.agnesi()
     if ag is not None:
         dims.update(agnesi_q=ag["q"], agnesi_p=ag["p"], agnesi_a=ag["a"])
@@ -132,6 +134,7 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = 
         dims["zbl_a_prefactor"] = float(cfg.pair_repulsion.get("a_prefactor", 0.4543))
     inter = cfg.interaction_irreps
     coupling = Irreps([(1, b.ir) for b in inter])
+    edges = cfg.edge_irreps_per_layer()
     for l in range(n_layers):
         p = f"L{l}."
         q = f"interactions.{l}"
@@ -140,6 +143,11 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = 
         dims["layer_in_blocks"][l] = lin
         dims["layer_hid_blocks"][l] = lhid
         dims["correlation"][l] = int(cfg.correlation[l])
+        if cfg.nonlinear:
+            dims["layer_edge_blocks"][l] = _blocks(edges[l], C)
+            _fold_nonlinear(cfg, w, l, irr_in, hid, edges[l], T)
+            _fold_product_readout(cfg, w, l, hid, T, scale, coupling)
+            continue
         # linear_up
         for n, (ji, jo, mi, mo, pw) in enumerate(linear_instructions(irr_in, irr_in)):
             assert ji == jo
@@ -171,28 +179,97 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = 
             per_out.setdefault(jo, []).append(f64(f"{q}.linear.weights.{n}") * pw * norm)
         for jo in range(len(inter)):
             T[f"{p}lin.{jo}"] = np.concatenate(per_out[jo], axis=0)
-        # symmetric contraction
-        r = f"products.{l}.symmetric_contractions.contractions"
-        corr = int(cfg.correlation[l])
-        for b, blk in enumerate(hid):
-            parts = []
-            keys = [f"{r}.{b}.weights_max"] + [f"{r}.{b}.weights.{i}" for i in range(corr - 1)]
-            for key, nu in zip(keys, range(corr, 0, -1)):
-                Wn = f64(key)
-                if not np.any(np.abs(u_matrix(coupling, blk.ir, nu)) > 1e-15):
-                    Wn = np.zeros_like(Wn)   # symmetric_contraction.py:255-262
-                parts.append(Wn)
-            T[f"{p}sc.{b}"] = np.concatenate(parts, axis=1)   # (n_el, KT, C)
-        for n, (ji, jo, mi, mo, pw) in enumerate(linear_instructions(hid, hid)):
-            T[f"{p}plin.{jo}"] = f64(f"products.{l}.linear.weights.{n}") * pw
-        ro = f"readouts.{l}"
-        if l < n_layers - 1:
-            (ji, jo, mi, mo, pw), = linear_instructions(hid, Irreps("0e"))
-            T[f"{p}ro"] = f64(f"{ro}.linear.weights.0").reshape(-1) * pw * scale
-        else:
-            (i1,) = linear_instructions(hid, Irreps("16x0e"))
-            (i2,) = linear_instructions(Irreps("16x0e"), Irreps("0e"))
-            T[f"{p}ro1"] = f64(f"{ro}.linear_1.weights.0") * i1[4]
-            T[f"{p}ro2"] = f64(f"{ro}.linear_2.weights.0").reshape(-1) * i2[4] * scale
+        _fold_product_readout(cfg, w, l, hid, T, scale, coupling)
     return DeviceModel(dims=dims, tensors={k: np.ascontiguousarray(v, dtype=np.float32) for k, v in T.items()},
                        z_table=z_table, r_max=float(cfg.r_max))
+
+
+def _fold_product_readout(cfg: ModelConfig, w, l: int, hid: Irreps, T: Dict[str, np.ndarray], scale: float,
+                          coupling: Irreps) -> None:
+    """Symmetric contraction (one weight set when the product is element-agnostic), product
+    linear and readout of layer l."""
+    p = f"L{l}."
+    f64 = lambda k: np.asarray(w[k], dtype=np.float64)
+    r = f"products.{l}.symmetric_contractions.contractions"
+    corr = int(cfg.correlation[l])
+    for b, blk in enumerate(hid):
+        parts = []
+        keys = [f"{r}.{b}.weights_max"] + [f"{r}.{b}.weights.{i}" for i in range(corr - 1)]
+        for key, nu in zip(keys, range(corr, 0, -1)):
+            Wn = f64(key)
+            if not np.any(np.abs(u_matrix(coupling, blk.ir, nu)) > 1e-15):
+                Wn = np.zeros_like(Wn)   # symmetric_contraction.py:255-262
+            parts.append(Wn)
+        T[f"{p}sc.{b}"] = np.concatenate(parts, axis=1)   # (n_el or 1, KT, C)
+    for n, (ji, jo, mi, mo, pw) in enumerate(linear_instructions(hid, hid)):
+        T[f"{p}plin.{jo}"] = f64(f"products.{l}.linear.weights.{n}") * pw
+    ro = f"readouts.{l}"
+    if l < cfg.num_interactions - 1:
+        (ji, jo, mi, mo, pw), = linear_instructions(hid, Irreps("0e"))
+        T[f"{p}ro"] = f64(f"{ro}.linear.weights.0").reshape(-1) * pw * scale
+    else:
+        (i1,) = linear_instructions(hid, Irreps("16x0e"))
+        (i2,) = linear_instructions(Irreps("16x0e"), Irreps("0e"))
+        T[f"{p}ro1"] = f64(f"{ro}.linear_1.weights.0") * i1[4]
+        T[f"{p}ro2"] = f64(f"{ro}.linear_2.weights.0").reshape(-1) * i2[4] * scale
+
+
+def _fold_nonlinear(cfg: ModelConfig, w, l: int, irr_in: Irreps, hid: Irreps, edge: Irreps,
+                    T: Dict[str, np.ndarray]) -> None:
+    """The non-linear interaction block's tensors (`blocks.py:611-807`): path weights folded in,
+    the species parts of both MLPs' first Linear turned into per-species tables (the one-hot
+    embedding is a row lookup), linear_1 / linear_res output columns laid out as the gate input
+    [scalars | gates of 1o, 2e, 3o | 1o | 2e | 3o] with the four 0e blocks side by side."""
+    p, q = f"L{l}.", f"interactions.{l}"
+    f64 = lambda k: np.asarray(w[k], dtype=np.float64)
+    nel, nb = cfg.num_elements, cfg.num_bessel
+    attrs = Irreps(f"{nel}x0e")
+    nsc = irr_in.count("0e")
+    inter, nonlin = cfg.interaction_irreps, cfg.nonlin_irreps()
+    for n, (ji, jo, mi, mo, pw) in enumerate(linear_instructions(irr_in, edge)):
+        assert ji == jo
+        T[f"{p}up.{ji}"] = f64(f"{q}.linear_up.weights.{n}") * pw
+    for n, (ji, jo, mi, mo, pw) in enumerate(linear_instructions(irr_in, hid)):
+        assert ji == jo
+        T[f"{p}skip.{ji}"] = f64(f"{q}.skip_tp.weights.{n}") * pw
+    (es,) = linear_instructions(attrs, Irreps(f"{nsc}x0e"))
+    src = f64(f"{q}.source_embedding.weights.0") * es[4]   # (n_el, nsc)
+    tgt = f64(f"{q}.target_embedding.weights.0") * es[4]
+    mp = f"{q}.conv_tp_weights.layers"
+    W0 = f64(f"{mp}.0.weight")                            # (64, nb + 2 nsc)
+    T[f"{p}rmlp.w0"] = W0[:, :nb].T
+    T[f"{p}rmlp.ts"] = src @ W0[:, nb:nb + nsc].T
+    T[f"{p}rmlp.tt"] = tgt @ W0[:, nb + nsc:].T + f64(f"{mp}.0.bias")
+    T[f"{p}rmlp.w1"] = f64(f"{mp}.3.weight").T
+    T[f"{p}rmlp.w2"] = f64(f"{mp}.6.weight").T
+    T[f"{p}rmlp.ln"] = np.stack([np.stack([f64(f"{mp}.{k}.weight"), f64(f"{mp}.{k}.bias")]) for k in (1, 4, 7)])
+    T[f"{p}rmlp.bias"] = np.stack([f64(f"{mp}.3.bias"), f64(f"{mp}.6.bias")])
+    T[f"{p}mlp.3"] = f64(f"{mp}.9.weight").T
+    T[f"{p}rmlp.b3"] = f64(f"{mp}.9.bias")
+    dp = f"{q}.density_fn.layers"
+    D0 = f64(f"{dp}.0.weight")
+    T[f"{p}dmlp.w0"] = D0[:, :nb].T
+    T[f"{p}dmlp.ts"] = src @ D0[:, nb:nb + nsc].T
+    T[f"{p}dmlp.tt"] = tgt @ D0[:, nb + nsc:].T + f64(f"{dp}.0.bias")
+    T[f"{p}dmlp.ln"] = np.stack([f64(f"{dp}.1.weight"), f64(f"{dp}.1.bias")])
+    T[f"{p}dmlp.w1"] = np.concatenate([f64(f"{dp}.3.weight").reshape(-1), f64(f"{dp}.3.bias").reshape(-1)])
+    T[f"{p}ab"] = np.array([float(f64(f"{q}.alpha")), float(f64(f"{q}.beta"))])
+
+    def by_degree(instrs, prefix):
+        """{output degree: [C * rows][columns]} with the 0e outputs side by side"""
+        cols = {}
+        for n, (ji, jo, mi, mo, pw) in enumerate(instrs):
+            cols.setdefault(jo, []).append(f64(f"{prefix}.{n}") * pw)
+        out = {}
+        for jo, mats in cols.items():
+            lo = nonlin[jo].ir.l
+            out.setdefault(lo, []).append((jo, np.concatenate(mats, axis=0)))
+        return {lo: np.concatenate([m for _, m in sorted(v)], axis=1) for lo, v in out.items()}
+
+    mid, _ = conv_tp_instructions(edge, cfg.sh_irreps, inter)
+    for lo, m in by_degree(linear_instructions(mid, nonlin), f"{q}.linear_1.weights").items():
+        T[f"{p}lin.{lo}"] = m
+    for lo, m in by_degree(linear_instructions(edge, nonlin), f"{q}.linear_res.weights").items():
+        T[f"{p}res.{lo}"] = m
+    for n, (ji, jo, mi, mo, pw) in enumerate(linear_instructions(inter, inter)):
+        T[f"{p}lin2.{jo}"] = f64(f"{q}.linear_2.weights.{n}") * pw

@@ -84,9 +84,12 @@ def test_unsupported_topologies_raise():
     bad = ModelConfig.from_dict({**cfg.to_dict(), "hidden_irreps": "128x0e+64x1o"})
     with pytest.raises((UnsupportedModel, NotImplementedError, KeyError)):
         build_device_model(bad, w)
-    for key, val in (("use_agnostic_product", True), ("apply_cutoff", False),
-                     ("interaction_cls", "RealAgnosticResidualNonLinearInteractionBlock")):
-        bad2 = ModelConfig.from_dict({**cfg.to_dict(), key: val})
+    # a separate cutoff exists only in the non-linear (mh-1) block here; the non-linear block
+    # with the density / non-residual layout of the 0b2 family is not a reference topology
+    for upd in ({"apply_cutoff": False},
+                {"interaction_cls": "RealAgnosticResidualNonLinearInteractionBlock",
+                 "first_interaction_nonresidual": True}):
+        bad2 = ModelConfig.from_dict({**cfg.to_dict(), **upd})
         with pytest.raises(NotImplementedError):
             build_device_model(bad2, w)
 
@@ -211,3 +214,20 @@ def test_head_selection_errors_and_single_head():
     dm_b = build_device_model(arch_config("medium"), w1)
     for k in dm_b.tensors:
         np.testing.assert_array_equal(dm_a.tensors[k], dm_b.tensors[k])
+
+
+@pytest.mark.parametrize("apply_cutoff,agnostic,edge", [(False, True, "128x0e+128x1o"), (True, False, "128x0e+128x1o"),
+                                                        (False, True, "128x0e+128x1o+128x2e")])
+def test_mh1_kernel_formulation_matches_oracle(apply_cutoff, agnostic, edge):
+    """mh-1 family: the engine's folded tensors (per-species first-layer tables, gate-input
+    column layout, path weights) re-evaluated on the CPU equal the oracle's energy."""
+    from test_oracle_mh1 import _system, mh1_config
+    cfg = mh1_config(apply_cutoff, agnostic, edge)
+    w = random_init(cfg, seed=9)
+    s, sp = _system(6)
+    i, j, S = neighbor_list(s.positions, s.cell, s.pbc, cfg.r_max)
+    E, ne = OracleMACE(cfg=cfg, weights=w).energy(s.positions, sp, np.stack([i, j]), S, s.cell)
+    Ek, nek = kernel_model.energy(build_device_model(cfg, w), s.positions, sp, i, j, S.astype(float), s.cell)
+    # the engine's tensors are float32 (folded in float64, then rounded): ~1e-8 relative
+    assert abs(Ek - E) < 1e-6 * max(1.0, abs(E)), (Ek, E)
+    np.testing.assert_allclose(nek, ne, rtol=0, atol=1e-6 * max(1.0, np.abs(ne).max()))
