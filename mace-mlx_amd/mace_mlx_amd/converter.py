@@ -184,8 +184,28 @@ def convert_state_dict(sd: Mapping[str, np.ndarray], cfg: ModelConfig) -> Dict[s
     res["atomic_energies_fn.atomic_energies"] = np.asarray(sd["atomic_energies_fn.atomic_energies"])
     lin("node_embedding.linear.weight", "node_embedding.linear", attrs, scal)
     res["radial_embedding.bessel_fn.bessel_weights"] = np.asarray(sd["radial_embedding.bessel_fn.bessel_weights"])
+    edges = cfg.edge_irreps_per_layer()
     for li, (irr_in, hid) in enumerate(zip(cfg.layer_inputs(), cfg.hidden_per_layer())):
         p = f"interactions.{li}"
+        if cfg.nonlinear:  # converter.py:679-762
+            nsc = Irreps(f"{irr_in.count('0e')}x0e")
+            edge, nonlin = edges[li], cfg.nonlin_irreps()
+            mid, _ = conv_tp_instructions(edge, cfg.sh_irreps, inter)
+            lin(f"{p}.source_embedding.weight", f"{p}.source_embedding", attrs, nsc)
+            lin(f"{p}.target_embedding.weight", f"{p}.target_embedding", attrs, nsc)
+            lin(f"{p}.skip_tp.weight", f"{p}.skip_tp", irr_in, hid)
+            lin(f"{p}.linear_up.weight", f"{p}.linear_up", irr_in, edge)
+            res.update(radial_mlp_layernorm(sd, f"{p}.conv_tp_weights", f"{p}.conv_tp_weights"))
+            res.update(radial_mlp_layernorm(sd, f"{p}.density_fn", f"{p}.density_fn"))
+            res[f"{p}.alpha"] = np.asarray(sd[f"{p}.alpha"])
+            res[f"{p}.beta"] = np.asarray(sd[f"{p}.beta"])
+            # e3nn's Gate concatenates its input irreps (scalars + gates + gated) unsimplified, as
+            # the reference does; the message enters linear_1 simplified, as in the other blocks
+            lin(f"{p}.linear_res.weight", f"{p}.linear_res", edge, nonlin)
+            lin(f"{p}.linear_1.weight", f"{p}.linear_1", mid.simplify(), nonlin, mid, nonlin)
+            lin(f"{p}.linear_2.weight", f"{p}.linear_2", inter, inter)
+            _convert_product_readout(sd, cfg, li, hid, res, lin)
+            continue
         lin(f"{p}.linear_up.weight", f"{p}.linear_up", irr_in, irr_in)
         k, ws = 0, []
         while f"{p}.conv_tp_weights.layer{k}.weight" in sd:
@@ -200,21 +220,28 @@ def convert_state_dict(sd: Mapping[str, np.ndarray], cfg: ModelConfig) -> Dict[s
             res[f"{p}.skip_tp.tp.weights.{n}"] = w
         if cfg.use_density_normalization:
             res[f"{p}.density_fn.weight"] = density_fn_weight(sd[f"{p}.density_fn.layer0.weight"])
-        q = f"products.{li}"
-        for key, v in sd.items():
-            if key.startswith(f"{q}.symmetric_contractions."):
-                res[key] = np.asarray(v)
-        lin(f"{q}.linear.weight", f"{q}.linear", hid, hid)
-        r = f"readouts.{li}"
-        out = Irreps(f"{H}x0e")
-        if li < cfg.num_interactions - 1:
-            lin(f"{r}.linear.weight", f"{r}.linear", hid, out)
-        else:
-            mlp = Irreps(f"{16 * H}x0e")
-            lin(f"{r}.linear_1.weight", f"{r}.linear_1", hid, mlp)
-            for n, w in enumerate(readout_linear_2(split_e3nn_linear(sd[f"{r}.linear_2.weight"], mlp, out))):
-                res[f"{r}.linear_2.weights.{n}"] = w
+        _convert_product_readout(sd, cfg, li, hid, res, lin)
     return {k: np.asarray(v, dtype=np.float32) for k, v in res.items()}
+
+
+def _convert_product_readout(sd, cfg: ModelConfig, li: int, hid: Irreps, res: dict, lin) -> None:
+    """Symmetric-contraction weights (same layout), product linear, readouts with the SiLU
+    constant folded into the non-linear readout's linear_2 (`converter.py:836-929`)."""
+    H = cfg.num_heads
+    q = f"products.{li}"
+    for key, v in sd.items():
+        if key.startswith(f"{q}.symmetric_contractions."):
+            res[key] = np.asarray(v)
+    lin(f"{q}.linear.weight", f"{q}.linear", hid, hid)
+    r = f"readouts.{li}"
+    out = Irreps(f"{H}x0e")
+    if li < cfg.num_interactions - 1:
+        lin(f"{r}.linear.weight", f"{r}.linear", hid, out)
+    else:
+        mlp = Irreps(f"{16 * H}x0e")
+        lin(f"{r}.linear_1.weight", f"{r}.linear_1", hid, mlp)
+        for n, w in enumerate(readout_linear_2(split_e3nn_linear(sd[f"{r}.linear_2.weight"], mlp, out))):
+            res[f"{r}.linear_2.weights.{n}"] = w
 
 
 def convert_npz(state_npz: str, config: dict | ModelConfig, out_dir: str):

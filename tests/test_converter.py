@@ -180,8 +180,42 @@ def _to_mace_torch(cfg: ModelConfig, w: dict) -> dict:
     sd["atomic_energies_fn.atomic_energies"] = w["atomic_energies_fn.atomic_energies"]
     sd["radial_embedding.bessel_fn.bessel_weights"] = w["radial_embedding.bessel_fn.bessel_weights"]
     sd["node_embedding.linear.weight"] = flat("node_embedding.linear", cnt("node_embedding.linear"))
+
+    def merged_linear(prefix, r_in, r_out, t_in):
+        """e3nn flat weight over the simplified input irreps t_in from the reference's
+        per-instruction weights over the unsimplified r_in"""
+        paths = {}
+        for (ji, jo, mi, mo, _), k in zip(linear_instructions(r_in, r_out), range(10 ** 6)):
+            paths.setdefault((r_in[ji].ir, jo), []).append(np.asarray(w[f"{prefix}.weights.{k}"], np.float64))
+        return np.concatenate([np.concatenate(paths[(t_in[i].ir, o)], axis=0).reshape(-1)
+                               for i, o, _, _ in cv.e3nn_linear_instructions(t_in, r_out)])
+
     for li, (irr_in, hid) in enumerate(zip(cfg.layer_inputs(), cfg.hidden_per_layer())):
         p = f"interactions.{li}"
+        if cfg.nonlinear:
+            for name in ("source_embedding", "target_embedding", "skip_tp", "linear_up", "linear_res", "linear_2"):
+                sd[f"{p}.{name}.weight"] = flat(f"{p}.{name}", cnt(f"{p}.{name}"))
+            for name in ("conv_tp_weights", "density_fn"):
+                for k, v in w.items():
+                    if k.startswith(f"{p}.{name}.layers."):
+                        sd[k.replace(".layers.", ".net.")] = v
+            sd[f"{p}.alpha"], sd[f"{p}.beta"] = w[f"{p}.alpha"], w[f"{p}.beta"]
+            edge = cfg.edge_irreps_per_layer()[li]
+            mid, _ = conv_tp_instructions(edge, cfg.sh_irreps, cfg.interaction_irreps)
+            sd[f"{p}.linear_1.weight"] = merged_linear(f"{p}.linear_1", mid, cfg.nonlin_irreps(), mid.simplify())
+        if cfg.nonlinear:
+            q = f"products.{li}"
+            for k, v in w.items():
+                if k.startswith(f"{q}.symmetric_contractions."):
+                    sd[k] = v
+            sd[f"{q}.linear.weight"] = flat(f"{q}.linear", cnt(f"{q}.linear"))
+            r = f"readouts.{li}"
+            if li < cfg.num_interactions - 1:
+                sd[f"{r}.linear.weight"] = flat(f"{r}.linear", cnt(f"{r}.linear"))
+            else:
+                sd[f"{r}.linear_1.weight"] = flat(f"{r}.linear_1", cnt(f"{r}.linear_1"))
+                sd[f"{r}.linear_2.weight"] = flat(f"{r}.linear_2", cnt(f"{r}.linear_2")) / SILU_NORM_FACTOR
+            continue
         sd[f"{p}.linear_up.weight"] = flat(f"{p}.linear_up", cnt(f"{p}.linear_up"))
         ks = sorted(int(k.split(".layers.")[1].split(".")[0]) for k in w if k.startswith(f"{p}.conv_tp_weights."))
         n = len(ks)
@@ -216,13 +250,16 @@ def _to_mace_torch(cfg: ModelConfig, w: dict) -> dict:
     return sd
 
 
-@pytest.mark.parametrize("kind", ["medium", "mpa0_like"])
+@pytest.mark.parametrize("kind", ["medium", "mpa0_like", "mh1"])
 def test_convert_state_dict_roundtrip(kind):
     from mace_mlx_amd.systems import arch_config
     cfg = arch_config("medium", zbl=True)
     if kind == "mpa0_like":
         cfg.first_interaction_nonresidual = True
         cfg.use_density_normalization = True
+    if kind == "mh1":
+        from test_oracle_mh1 import mh1_config
+        cfg = mh1_config()
     w = random_init(cfg, seed=11)
     got = cv.convert_state_dict(_to_mace_torch(cfg, w), cfg)
     assert set(got) == set(w)
