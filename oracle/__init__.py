@@ -26,9 +26,19 @@ Pinning (what checks each part against something other than itself):
   permutation invariance, sum of forces = 0, stress symmetry, the stress-path
   forces equal the energy-path forces, single-atom and far-pair cases;
 * symmetric contraction -- the row-compressed main step equals the dense einsum
-  definition (`symmetric_contraction.py:95-121`) on random tensors.
+  definition (`symmetric_contraction.py:95-121`) on random tensors;
+* architecture bookkeeping -- the layer-1 conv-TP instruction table the reference
+  records (`docs/prototypes/teamA_convtp_batch.md:18-29`), the EquivariantLinear
+  known answer of the reference's own test (`tests/test_linear.py:194-226`), and
+  the unit second moment every Linear / FCTP / conv-TP output must have;
+* mh-1 block -- LayerNorm and the LayerNorm MLP against torch's own modules, the
+  gate against its closed form and equivariance, e3nn's normalize2mom constants
+  recomputed the way e3nn computes them, FD forces / stress, and the reductions
+  beta = 0 (density off) and agnostic product = copied per-element weights.
 
 Parity unpinned: the MLX-executed values of the reference itself (MLX is not
 installable here), MLX's RNG / initialisers (weights are exchanged as files),
-and ASE's covalent-radius table (a published table is vendored instead).
+ASE's covalent-radius table (a published table is vendored instead), and the
+ZBL screening coefficients (restated from `radial.py:142-199`; only the
+short-range Coulomb limit and the cutoff are checked).
 """
