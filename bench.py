@@ -177,8 +177,12 @@ def load_traffic(site: str, workload: str):
         return None
 
 
-def cpu_baseline(bc, weights, edges, species, budget_s=25.0):
-    """float32 oracle on the host cores (bounded sample: 1 warm-up + up to 3 steps)."""
+def cpu_baseline(bc, weights, edges, species, budget_s=40.0):
+    """float32 CPU restatement on the host cores with the reference's CPU-path forms (the conv TP
+    as x2-first batched products, `tensor_product.py:545-575`; the row-compressed symmetric
+    contraction, `symmetric_contraction.py:530-540`; activations kept, no recomputation), timed as
+    the reference's benchmark protocol: 3 warm-ups, then the median of 10 E+F steps
+    (`docs/prototypes/xbench.py:89-101`), fewer if the budget runs out (the count is reported)."""
     import torch
     sys.path.insert(0, str(ROOT))
     from oracle.model import OracleMACE
@@ -190,21 +194,26 @@ def cpu_baseline(bc, weights, edges, species, budget_s=25.0):
             model = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
     except (OSError, StopIteration):
         pass
-    m = OracleMACE(cfg=bc.model, weights=weights, dtype=torch.float32)
+    m = OracleMACE(cfg=bc.model, weights=weights, dtype=torch.float32, gemm_tp=True, recompute=False,
+                   edge_chunk=4096)
     s = bc.system
     ei = np.stack([edges[0], edges[1]]).astype(np.int64)
     t0 = time.perf_counter()
-    m.energy_forces(s.positions, species, ei, edges[2], s.cell)
+    nwarm = 0
+    while nwarm < 3 and (nwarm == 0 or time.perf_counter() - t0 < budget_s / 4):
+        m.energy_forces(s.positions, species, ei, edges[2], s.cell)
+        nwarm += 1
     warm = time.perf_counter() - t0
     times = []
-    while len(times) < 3 and sum(times) + warm < budget_s:
+    while len(times) < 10 and (not times or sum(times) + warm < budget_s):
         t = time.perf_counter()
         m.energy_forces(s.positions, species, ei, edges[2], s.cell)
         times.append(time.perf_counter() - t)
-    med = float(np.median(times)) if times else warm
+    med = float(np.median(times))
     return {"value": len(s) / med, "unit": "atom-steps/s", "cores": threads, "kind": "port",
-            "sample": f"{bc.name} E+F, float32 CPU oracle (torch, {threads} threads on {model}), median of "
-                      f"{max(len(times), 1)} step(s) after 1 warm-up; {med * 1e3:.0f} ms/step"}
+            "sample": f"{bc.name} E+F, float32 CPU restatement in the reference's CPU-path forms (torch, "
+                      f"{threads} threads on {model}), median of {len(times)} step(s) after {nwarm} warm-up(s); "
+                      f"{med * 1e3:.0f} ms/step"}
 
 
 def layer_shapes(dm):

@@ -210,6 +210,48 @@ class ConvTP:
         return torch.cat(parts, dim=-1)
 
 
+class ConvTPGemm(ConvTP):
+    """The same tensor product in the x2-first GEMM form of the reference's CPU path
+    (`tensor_product.py:497-513,545-575`): for each input block, the edge's CG table
+    M[e, i, col] = sum_j Y[e, j] C_s[i, j, k] pw_s over that block's output slots, then one batched
+    product x1[e] (mul x d1) @ M[e] (d1 x K), times the slot's per-channel weight.  Used to time the
+    CPU baseline; equal to the loop form (tests/test_oracle.py)."""
+
+    def __init__(self, irreps1, irreps2, target):
+        super().__init__(irreps1, irreps2, target)
+        self.groups = {}
+        woff = 0
+        for (i, j, k, pw) in self.inst:
+            b1, b2, bo = self.i1[i], self.i2[j], self.mid[k]
+            cg = np.asarray(wigner_3j(b1.ir.l, b2.ir.l, bo.ir.l)) * pw
+            self.groups.setdefault(i, []).append((j, k, cg, woff))
+            woff += b1.mul * b2.mul
+
+    def __call__(self, x1, x2, w):
+        E = x1.shape[0]
+        o1, o2 = self.i1.offsets, self.i2.offsets
+        parts = [None] * len(self.mid)
+        for i, slots in self.groups.items():
+            b1 = self.i1[i]
+            d1 = b1.ir.dim
+            cols, widths = [], []
+            for (j, k, cg, woff) in slots:
+                b2 = self.i2[j]
+                yj = x2[:, o2[j]:o2[j] + b2.dim]                                   # (E, d2)
+                cols.append(torch.einsum("ej,ijk->eik", yj, torch.as_tensor(cg, dtype=x1.dtype)))
+                widths.append(cg.shape[2])
+            M = torch.cat(cols, dim=2)                                           # (E, d1, K)
+            xa = x1[:, o1[i]:o1[i] + b1.dim].reshape(E, b1.mul, d1)
+            T = torch.bmm(xa, M)                                                 # (E, mul, K)
+            c0 = 0
+            for (j, k, cg, woff), wd in zip(slots, widths):
+                ww = w[:, woff:woff + b1.mul]                                    # uvu, mul2 = 1
+                out = (T[:, :, c0:c0 + wd] * ww[:, :, None]).reshape(E, -1)
+                parts[k] = out if parts[k] is None else parts[k] + out
+                c0 += wd
+        return torch.cat(parts, dim=-1)
+
+
 class SkipFCTP:
     """FullyConnectedTensorProduct (uvw, internal weights) with the one-hot
     attributes as second input, `tensor_product.py:1046-1098` + `_compute_mode`."""
@@ -389,7 +431,8 @@ class OracleMACE:
 
     def __init__(self, model_dir=None, cfg: Optional[ModelConfig] = None,
                  weights: Optional[Dict[str, np.ndarray]] = None,
-                 dtype=torch.float64, edge_chunk: int = 8192, head: Optional[str] = None):
+                 dtype=torch.float64, edge_chunk: int = 8192, head: Optional[str] = None,
+                 gemm_tp: bool = False, recompute: bool = True):
         if model_dir is not None:
             cfg = load_config(model_dir)
             weights = load_weights(model_dir)
@@ -403,6 +446,10 @@ class OracleMACE:
                 raise ValueError(f"Head '{name}' not found in model heads: {cfg.heads}")
             self.h = cfg.heads.index(name)
         self.cfg, self.dtype, self.edge_chunk = cfg, dtype, edge_chunk
+        self.gemm_tp = gemm_tp
+        # recompute: edge chunks re-run in the backward (bounded memory, for parity runs);
+        # off for the CPU baseline, which keeps every activation as the reference's CPU path does
+        self.recompute = recompute
         W = {k: _t(v, dtype) for k, v in weights.items()}
         self.W = W
         nel = cfg.num_elements
@@ -442,7 +489,7 @@ class OracleMACE:
             if cfg.use_density_normalization:
                 L["dens"] = W[f"{p}.density_fn.weight"]
             L["up"] = Linear(irr_in, irr_in, wl(f"{p}.linear_up.weights"))
-            L["tp"] = ConvTP(irr_in, sh, inter)
+            L["tp"] = (ConvTPGemm if gemm_tp else ConvTP)(irr_in, sh, inter)
             mats, n = [], 0
             while f"{p}.conv_tp_weights.layers.{2 * n}.weight" in W:
                 mats.append(W[f"{p}.conv_tp_weights.layers.{2 * n}.weight"])
@@ -513,7 +560,7 @@ class OracleMACE:
         L["tgt"] = Linear(attrs, nsc, wl(f"{p}.target_embedding.weights"))
         L["skip"] = Linear(irr_in, hid, wl(f"{p}.skip_tp.weights"))
         L["up"] = Linear(irr_in, edge, wl(f"{p}.linear_up.weights"))
-        L["tp"] = ConvTP(edge, sh, inter)
+        L["tp"] = (ConvTPGemm if self.gemm_tp else ConvTP)(edge, sh, inter)
         L["mlp"] = RadialMLPLN(W, f"{p}.conv_tp_weights")
         assert L["mlp"].lin[-1][0].shape[0] == L["tp"].weight_numel
         L["dens"] = RadialMLPLN(W, f"{p}.density_fn")
@@ -550,8 +597,8 @@ class OracleMACE:
 
         for a in range(0, E, self.edge_chunk):
             b = min(E, a + self.edge_chunk)
-            M, rho = checkpoint(chunk_fn, up, Y[a:b], ef[a:b], None if cut is None else cut[a:b],
-                                sender[a:b], receiver[a:b], M, rho, use_reentrant=False)
+            args = (up, Y[a:b], ef[a:b], None if cut is None else cut[a:b], sender[a:b], receiver[a:b], M, rho)
+            M, rho = checkpoint(chunk_fn, *args, use_reentrant=False) if self.recompute else chunk_fn(*args)
         msg = L["lin1"](M) / (rho * L["beta"] + L["alpha"])[:, None] + res
         return L["lin2"](L["gate"](msg))
 
@@ -635,8 +682,8 @@ class OracleMACE:
 
         for a in range(0, E, self.edge_chunk):
             b = min(E, a + self.edge_chunk)
-            out = checkpoint(chunk_fn, up, Y[a:b], ef[a:b], sender[a:b], receiver[a:b], out,
-                             use_reentrant=False)
+            args = (up, Y[a:b], ef[a:b], sender[a:b], receiver[a:b], out)
+            out = checkpoint(chunk_fn, *args, use_reentrant=False) if self.recompute else chunk_fn(*args)
         return out
 
     # -- public entry points -------------------------------------------------

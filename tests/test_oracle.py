@@ -315,3 +315,22 @@ def test_nonresidual_first_block_with_identity_skip():
     Ea = om.OracleMACE(cfg=cfg, weights=w_id).energy(s.positions, sp, ei, S, s.cell)[0]
     Eb = om.OracleMACE(cfg=cfg_res, weights=w_res).energy(s.positions, sp, ei, S, s.cell)[0]
     assert abs(Ea - Eb) < 1e-9 * max(1.0, abs(Eb))
+
+
+@pytest.mark.parametrize("lin_irreps", ["8x0e", "8x0e+8x1o", "8x0e+8x1o+8x2e"])
+def test_gemm_form_tp_equals_loop_form(lin_irreps):
+    """The x2-first GEMM form of the conv TP (the reference's CPU path, `tensor_product.py:545-575`,
+    used to time the CPU baseline) equals the per-instruction loop form."""
+    import torch
+    from mace_mlx_amd.irreps import Irreps
+    from oracle.model import ConvTP, ConvTPGemm, spherical_harmonics
+    irr = Irreps(lin_irreps)
+    sh = Irreps.spherical_harmonics(3)
+    target = Irreps([(8, b.ir) for b in sh])
+    g = torch.Generator().manual_seed(1)
+    loop, gemm = ConvTP(irr, sh, target), ConvTPGemm(irr, sh, target)
+    E = 11
+    x1 = torch.randn(E, irr.dim, dtype=torch.float64, generator=g)
+    Y = spherical_harmonics(torch.randn(E, 3, dtype=torch.float64, generator=g), 3)
+    w = torch.randn(E, loop.weight_numel, dtype=torch.float64, generator=g)
+    assert torch.allclose(gemm(x1, Y, w), loop(x1, Y, w), rtol=1e-12, atol=1e-12)
