@@ -218,8 +218,11 @@ def test_periodic_replication_is_exact(medium_zbl):
 
 
 def test_hea_full_size_runs_and_pairs():
+    """Configuration 5 at full size (32,000 atoms, 2.75 M edges) in its own dtype (float16
+    feature policy): pairing of the neighbour list, sum of forces, translation invariance."""
     bc = make_config(4)
-    case = Case(bc.model)
+    assert bc.dtype == "float16"
+    case = Case(bc.model, dtype=bc.dtype)
     got = case.run(bc.system)
     snd, rcv, sh = case.edges()
     s = bc.system
@@ -231,7 +234,14 @@ def test_hea_full_size_runs_and_pairs():
     assert np.array_equal(keys(snd, rcv, sh), keys(rcv, snd, -sh))
     assert 84 * len(s) < len(snd) < 90 * len(s)   # FCC a=3.6: 86 neighbours within 6.5 A
     assert np.isfinite(got["E"]) and np.isfinite(got["F"]).all()
-    assert np.abs(got["F"].sum(0)).max() < 1e-4 * np.sqrt(len(s))
+    Fmax = float(np.abs(got["F"]).max())
+    print(f"HEA32000 fp16: E={got['E']:.6f} max|F|={Fmax:.3f} |sum F|={np.abs(got['F'].sum(0)).max():.2e}", flush=True)
+    assert np.abs(got["F"].sum(0)).max() < 1e-5 * max(1.0, Fmax) * np.sqrt(len(s))
+    t = s.copy()
+    t.positions = t.positions + np.array([0.37, -1.21, 0.58])
+    b = case.run(t)
+    assert abs(b["E"] - got["E"]) <= 1e-6 * abs(got["E"])
+    assert np.abs(b["F"] - got["F"]).max() <= 1e-3 * max(1.0, Fmax)
 
 
 # ---------------------------------------------------------------------------
