@@ -151,6 +151,8 @@ struct mace_ctx {
   // dL/d(gate input), all-zero species (element-agnostic product)
   DBuf<float> cutv, gcut, mh_dens, gwb, gP;
   DBuf<int> zero_species;
+  DBuf<int> nl_missing;       // edges of the last list build without a reverse edge (device count)
+  int* nl_missing_h = nullptr;  // pinned host copy, read after the next synchronisation
   // system
   int N = 0;
   std::vector<int> species_h;
@@ -943,10 +945,34 @@ void build_nl(mace_ctx* c, const double* pos_host) {
     launch_nl_fill(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], ps[g], bin_off[g], c->nl_wpos.p,
                    c->nl_img.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, c->rowptr.p, c->sender.p,
                    c->receiver.p, c->shifts.p);
-  build_sender_csr(c);
+  // sender-side CSR of the (symmetric) list without a sort: rowptr_s = rowptr, perm_s = pos_s = rev
+  c->rowptr_s.ensure((size_t)N + 1);
+  HIPCHK(hipMemcpyAsync(c->rowptr_s.p, c->rowptr.p, ((size_t)N + 1) * sizeof(int), hipMemcpyDeviceToDevice,
+                        c->stream));
+  if (!c->nl_missing_h) HIPCHK(hipHostMalloc((void**)&c->nl_missing_h, sizeof(int), hipHostMallocDefault));
+  c->nl_missing.ensure(1);
+  HIPCHK(hipMemsetAsync(c->nl_missing.p, 0, sizeof(int), c->stream));
+  launch_nl_rev(c->stream, c->E, c->rowptr.p, c->sender.p, c->receiver.p, c->shifts.p, c->perm_s.p, c->pos_s.p,
+                c->nl_missing.p);
+  HIPCHK(hipMemcpyAsync(c->nl_missing_h, c->nl_missing.p, sizeof(int), hipMemcpyDeviceToHost, c->stream));
   ensure_edge_buffers(c, c->E);
-  c->nl_pos.assign(pos_host, pos_host + 3 * (size_t)N);
+  // positions at this build, for the host-side skin check of mace_step (unknown when the build
+  // took device positions of a fully periodic system: the next mace_step then rebuilds)
+  if (pos_host)
+    c->nl_pos.assign(pos_host, pos_host + 3 * (size_t)N);
+  else
+    c->nl_pos.clear();
   c->nl_valid = true;
+}
+
+// after a synchronisation: a list build whose edges lacked reverses is an internal error
+void check_nl_missing(mace_ctx* c) {
+  if (c->nl_missing_h && *c->nl_missing_h > 0) {
+    const int m = *c->nl_missing_h;
+    *c->nl_missing_h = 0;
+    c->nl_valid = false;
+    fail(MACE_ERR_STATE, "neighbour list not symmetric: %d edges without a reverse", m);
+  }
 }
 
 __global__ void k_gather_edges(int64_t E, const int* perm, const int* si, const int* ri, const int* ss, int* so,
@@ -1714,9 +1740,12 @@ static void free_all(mace_ctx* c) {
   if (c->out_pinned) (void)hipHostFree(c->out_pinned);
   if (c->ne_pinned) (void)hipHostFree(c->ne_pinned);
   if (c->pos_pinned) (void)hipHostFree(c->pos_pinned);
+  if (c->nl_missing_h) (void)hipHostFree(c->nl_missing_h);
   c->out_pinned = nullptr;
   c->ne_pinned = nullptr;
   c->pos_pinned = nullptr;
+  c->nl_missing_h = nullptr;
+  c->nl_missing.release();
 }
 
 void mace_destroy(mace_ctx* c) {
@@ -1912,7 +1941,7 @@ int mace_step(mace_ctx* c, const double* positions, uint32_t flags, double* ener
     // neighbour-list cache check (calculators.py:266-283)
     bool rebuild = !c->nl_valid || (flags & MACE_STEP_FORCE_NL);
     if (!rebuild && !c->edges_manual) {
-      if (c->skin <= 0) {
+      if (c->skin <= 0 || c->nl_pos.size() != 3 * (size_t)N) {
         rebuild = true;
       } else {
         double maxd2 = 0;
@@ -1943,6 +1972,7 @@ int mace_step(mace_ctx* c, const double* positions, uint32_t flags, double* ener
     HIPCHK(hipEventRecord(c->ev[4], st));
     HIPCHK(hipStreamSynchronize(st));
     HIPCHK(hipGetLastError());
+    check_nl_missing(c);
     *energy = c->out_pinned[0];
     if (virial9 && stress) std::memcpy(virial9, c->out_pinned + 1, 9 * sizeof(double));
     if (forces) std::memcpy(forces, c->out_pinned + 10, 3 * (size_t)N * sizeof(double));
@@ -1995,14 +2025,20 @@ int mace_step_device(mace_ctx* c, const double* d_positions, uint32_t flags, dou
     const int N = c->N;
     hipStream_t st = c->stream;
     if ((flags & MACE_STEP_FORCE_NL) || !c->nl_valid) {
-      // rebuild needs host positions for the non-periodic extents: synchronous
       if (N > 0)
         HIPCHK(hipMemcpyAsync(c->pos.p, d_positions, 3 * (size_t)N * sizeof(double), hipMemcpyDeviceToDevice, st));
-      std::vector<double> host(3 * (size_t)N);
-      if (N > 0) HIPCHK(hipMemcpyAsync(host.data(), d_positions, host.size() * sizeof(double), hipMemcpyDeviceToHost, st));
-      HIPCHK(hipStreamSynchronize(st));
+      // host positions only for the extents of non-periodic directions
+      bool periodic = true;
+      for (uint8_t f : c->gpbc_h) periodic = periodic && f;
+      std::vector<double> host;
+      if (!periodic) {
+        host.resize(3 * (size_t)N);
+        if (N > 0)
+          HIPCHK(hipMemcpyAsync(host.data(), d_positions, host.size() * sizeof(double), hipMemcpyDeviceToHost, st));
+        HIPCHK(hipStreamSynchronize(st));
+      }
       c->edges_manual = false;
-      build_nl(c, host.data());
+      build_nl(c, periodic ? nullptr : host.data());
     }
     const bool stress = (flags & MACE_STEP_STRESS) != 0;
     ensure_embed(c);
@@ -2074,6 +2110,7 @@ int mace_sync(mace_ctx* c) {
     set_device(c);
     HIPCHK(hipStreamSynchronize(c->stream));
     HIPCHK(hipGetLastError());
+    check_nl_missing(c);
     prof_harvest(c);
   });
 }

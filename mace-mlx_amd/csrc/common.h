@@ -108,6 +108,10 @@ void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* se
                      const float* ag_cov, const FrontParams& p, const double* gcell, const int* gid,
                      EdgeGeom* geom, float* Y, float* ef, float* zbl_e, float* Mt, int mts, int nent,
                      float* cut);
+// sender-side CSR of a symmetric neighbour list without a sort: perm_s = pos_s = the reverse of
+// every edge (edges without one map to themselves and are counted in *missing)
+void launch_nl_rev(hipStream_t st, int64_t E, const int* rowptr, const int* sender, const int* receiver,
+                   const int* shifts, int* perm_s, int* pos_s, int* missing);
 // gcut (used when p.apply_cutoff == 0): dL/dcut[e]
 void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov, const float* ag_cov,

@@ -337,67 +337,109 @@ __global__ void k_nl_bin(int i0, int n, const double* __restrict__ pos, NLParams
   bin[i] = bin_off + (b[0] * p.nbin[1] + b[1]) * p.nbin[2] + b[2];
 }
 
-// One wave per receiver atom j: the wave walks j's neighbour cells in a fixed
-// order and its lanes test the cell's atoms 64 at a time; hits are counted
-// with a ballot, and in the fill pass each hit lane writes at the running
-// count plus its rank among the hit lanes, so the edge order (cell order, then
-// position in the cell) is deterministic and identical in both passes.
+// One wave per receiver atom j.  Its neighbour cells, in a fixed order (o0 outer, o2 inner),
+// are taken 64 at a time: lane k looks up cell k's image shift T and atom range, a wave
+// prefix sum lays the cells' atoms out as one candidate range, and the lanes test those
+// candidates 64 at a time (a lane finds its candidate's cell by a binary search over the
+// prefix sums in LDS).  Hits are counted with a ballot, and in the fill pass each hit lane
+// writes at the running count plus its rank among the hit lanes, so the edge order (cell
+// order, then position in the cell) is deterministic and identical in both passes.
+struct NLWaveScratch {
+  int end[64];    // inclusive prefix sums of the chunk's cell sizes
+  int start[64];  // first entry of each cell in bin_atoms
+  int T[64][3];   // image shift of each cell
+};
+
 template <bool FILL>
 __device__ __forceinline__ int nl_visit(int j, const NLParams& p, int bin_off, const double* __restrict__ wpos,
                                         const int* __restrict__ img, const int* __restrict__ bin,
                                         const int* __restrict__ bin_start,
                                         const int* __restrict__ bin_atoms, int out0,
                                         int* __restrict__ sender, int* __restrict__ receiver,
-                                        int* __restrict__ shifts) {
+                                        int* __restrict__ shifts, NLWaveScratch& sc) {
   const int lane = __lane_id();
   const int bj = bin[j] - bin_off;
   const int b2 = bj % p.nbin[2], b1 = (bj / p.nbin[2]) % p.nbin[1], b0 = bj / (p.nbin[2] * p.nbin[1]);
   const double xj = wpos[3 * j], yj = wpos[3 * j + 1], zj = wpos[3 * j + 2];
+  const int n1 = 2 * p.range[1] + 1, n2 = 2 * p.range[2] + 1;
+  const int ncell = (2 * p.range[0] + 1) * n1 * n2;
   int cnt = 0;
-  for (int o0 = -p.range[0]; o0 <= p.range[0]; ++o0) {
-    int c0 = b0 + o0, T0 = 0;
-    if (p.periodic[0]) { T0 = floordiv(c0, p.nbin[0]); c0 -= T0 * p.nbin[0]; }
-    else if (c0 < 0 || c0 >= p.nbin[0]) continue;
-    for (int o1 = -p.range[1]; o1 <= p.range[1]; ++o1) {
-      int c1 = b1 + o1, T1 = 0;
-      if (p.periodic[1]) { T1 = floordiv(c1, p.nbin[1]); c1 -= T1 * p.nbin[1]; }
-      else if (c1 < 0 || c1 >= p.nbin[1]) continue;
-      for (int o2 = -p.range[2]; o2 <= p.range[2]; ++o2) {
-        int c2 = b2 + o2, T2 = 0;
-        if (p.periodic[2]) { T2 = floordiv(c2, p.nbin[2]); c2 -= T2 * p.nbin[2]; }
-        else if (c2 < 0 || c2 >= p.nbin[2]) continue;
-        const double tx = T0 * p.cell[0] + T1 * p.cell[3] + T2 * p.cell[6];
-        const double ty = T0 * p.cell[1] + T1 * p.cell[4] + T2 * p.cell[7];
-        const double tz = T0 * p.cell[2] + T1 * p.cell[5] + T2 * p.cell[8];
-        const int cb = bin_off + (c0 * p.nbin[1] + c1) * p.nbin[2] + c2;
-        const int qe = bin_start[cb + 1];
-        for (int q0 = bin_start[cb]; q0 < qe; q0 += 64) {
-          const int q = q0 + lane;
-          bool hit = false;
-          int i = 0;
-          if (q < qe) {
-            i = bin_atoms[q];
-            if (!(i == j && T0 == 0 && T1 == 0 && T2 == 0)) {
-              // image of atom i at wpos_i + T.cell; D = x_j - x_i(image)
-              const double dx = xj - (wpos[3 * i] + tx), dy = yj - (wpos[3 * i + 1] + ty),
-                           dz = zj - (wpos[3 * i + 2] + tz);
-              hit = dx * dx + dy * dy + dz * dz < p.cutoff2;
-            }
-          }
-          const unsigned long long m = __ballot(hit);
-          if (FILL && hit) {
-            const int o = out0 + cnt + __popcll(m & ((1ull << lane) - 1ull));
-            sender[o] = i;
-            receiver[o] = j;
-            // D = x_j - x_i + S.cell with x = wpos + img.cell  =>  S = -T - img_j + img_i
-            shifts[3 * o + 0] = -T0 - img[3 * j + 0] + img[3 * i + 0];
-            shifts[3 * o + 1] = -T1 - img[3 * j + 1] + img[3 * i + 1];
-            shifts[3 * o + 2] = -T2 - img[3 * j + 2] + img[3 * i + 2];
-          }
-          cnt += __popcll(m);
+  for (int k0 = 0; k0 < ncell; k0 += 64) {
+    // lane k: cell k0 + k (size 0 when past the end or outside a non-periodic direction)
+    int size = 0, first = 0, T[3] = {0, 0, 0};
+    const int k = k0 + lane;
+    if (k < ncell) {
+      const int o[3] = {k / (n1 * n2) - p.range[0], (k / n2) % n1 - p.range[1], k % n2 - p.range[2]};
+      const int bb[3] = {b0, b1, b2};
+      int c[3];
+      bool ok = true;
+      for (int d = 0; d < 3; ++d) {
+        c[d] = bb[d] + o[d];
+        if (p.periodic[d]) {
+          T[d] = floordiv(c[d], p.nbin[d]);
+          c[d] -= T[d] * p.nbin[d];
+        } else if (c[d] < 0 || c[d] >= p.nbin[d]) {
+          ok = false;
         }
       }
+      if (ok) {
+        const int cb = bin_off + (c[0] * p.nbin[1] + c[1]) * p.nbin[2] + c[2];
+        first = bin_start[cb];
+        size = bin_start[cb + 1] - first;
+      }
     }
+    int incl = size;  // inclusive prefix sum over the lanes
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int v = __shfl_up(incl, off);
+      if (lane >= off) incl += v;
+    }
+    sc.end[lane] = incl;
+    sc.start[lane] = first;
+    sc.T[lane][0] = T[0], sc.T[lane][1] = T[1], sc.T[lane][2] = T[2];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const int total = __shfl(incl, 63);
+    for (int t0 = 0; t0 < total; t0 += 64) {
+      const int t = t0 + lane;
+      bool hit = false;
+      int i = 0, Tc[3] = {0, 0, 0};
+      if (t < total) {
+        int lo = 0, hi = 63;  // first cell whose inclusive end exceeds t
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (sc.end[mid] > t) hi = mid;
+          else lo = mid + 1;
+        }
+        const int before = lo > 0 ? sc.end[lo - 1] : 0;
+        i = bin_atoms[sc.start[lo] + (t - before)];
+        Tc[0] = sc.T[lo][0], Tc[1] = sc.T[lo][1], Tc[2] = sc.T[lo][2];
+        if (!(i == j && Tc[0] == 0 && Tc[1] == 0 && Tc[2] == 0)) {
+          const double tx = Tc[0] * p.cell[0] + Tc[1] * p.cell[3] + Tc[2] * p.cell[6];
+          const double ty = Tc[0] * p.cell[1] + Tc[1] * p.cell[4] + Tc[2] * p.cell[7];
+          const double tz = Tc[0] * p.cell[2] + Tc[1] * p.cell[5] + Tc[2] * p.cell[8];
+          // image of atom i at wpos_i + T.cell; D = (x_j - x_i) - T.cell, rounded so that the
+          // reverse pair (i, j, -T) gets exactly -D: the list is symmetric bit for bit
+          const double dx = (xj - wpos[3 * i]) - tx, dy = (yj - wpos[3 * i + 1]) - ty,
+                       dz = (zj - wpos[3 * i + 2]) - tz;
+          hit = dx * dx + dy * dy + dz * dz < p.cutoff2;
+        }
+      }
+      const unsigned long long m = __ballot(hit);
+      if (FILL && hit) {
+        const int o = out0 + cnt + __popcll(m & ((1ull << lane) - 1ull));
+        sender[o] = i;
+        receiver[o] = j;
+        // D = x_j - x_i + S.cell with x = wpos + img.cell  =>  S = -T - img_j + img_i
+        shifts[3 * o + 0] = -Tc[0] - img[3 * j + 0] + img[3 * i + 0];
+        shifts[3 * o + 1] = -Tc[1] - img[3 * j + 1] + img[3 * i + 1];
+        shifts[3 * o + 2] = -Tc[2] - img[3 * j + 2] + img[3 * i + 2];
+      }
+      cnt += __popcll(m);
+    }
+    // the scratch is rewritten by the next chunk only after every lane is done with it
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
   }
   return cnt;
 }
@@ -407,10 +449,11 @@ __global__ void __launch_bounds__(256) k_nl_count(int i0, int n, NLParams p, int
                                                   const double* __restrict__ wpos,
                                                   const int* __restrict__ bin, const int* __restrict__ bin_start,
                                                   const int* __restrict__ bin_atoms, int* __restrict__ counts) {
+  __shared__ NLWaveScratch sc[4];
   if ((int)(blockIdx.x * 4 + (threadIdx.x >> 6)) >= n) return;
   const int j = i0 + blockIdx.x * 4 + (threadIdx.x >> 6);
   const int c = nl_visit<false>(j, p, bin_off, wpos, nullptr, bin, bin_start, bin_atoms, 0, nullptr, nullptr,
-                                nullptr);
+                                nullptr, sc[threadIdx.x >> 6]);
   if (__lane_id() == 0) counts[j] = c;
 }
 
@@ -421,9 +464,38 @@ __global__ void __launch_bounds__(256) k_nl_fill(int i0, int n, NLParams p, int 
                                                  const int* __restrict__ bin_atoms, const int* __restrict__ rowptr,
                                                  int* __restrict__ sender, int* __restrict__ receiver,
                                                  int* __restrict__ shifts) {
+  __shared__ NLWaveScratch sc[4];
   if ((int)(blockIdx.x * 4 + (threadIdx.x >> 6)) >= n) return;
   const int j = i0 + blockIdx.x * 4 + (threadIdx.x >> 6);
-  nl_visit<true>(j, p, bin_off, wpos, img, bin, bin_start, bin_atoms, rowptr[j], sender, receiver, shifts);
+  nl_visit<true>(j, p, bin_off, wpos, img, bin, bin_start, bin_atoms, rowptr[j], sender, receiver, shifts,
+                 sc[threadIdx.x >> 6]);
+}
+
+// The reverse of every edge of a symmetric list: for e = (i -> j, S) in receiver j's row, the
+// edge (j -> i, -S) in receiver i's row (a search of that row).  rev is an involution, so it is
+// both the sender-side permutation (edges sent by a = reverses of the edges a receives, in the
+// order of a's row) and its inverse.  An edge without a reverse (a list that is not symmetric)
+// maps to itself and is counted in *missing.
+__global__ void __launch_bounds__(256) k_nl_rev(int64_t E, const int* __restrict__ rowptr,
+                                                const int* __restrict__ sender, const int* __restrict__ receiver,
+                                                const int* __restrict__ shifts, int* __restrict__ perm_s,
+                                                int* __restrict__ pos_s, int* __restrict__ missing) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const int i = sender[e], j = receiver[e];
+  const int s0 = -shifts[3 * e], s1 = -shifts[3 * e + 1], s2 = -shifts[3 * e + 2];
+  int found = -1;
+  for (int f = rowptr[i]; f < rowptr[i + 1]; ++f)
+    if (sender[f] == j && shifts[3 * f] == s0 && shifts[3 * f + 1] == s1 && shifts[3 * f + 2] == s2) {
+      found = f;
+      break;
+    }
+  if (found < 0) {
+    atomicAdd(missing, 1);
+    found = (int)e;
+  }
+  perm_s[e] = found;
+  pos_s[e] = found;
 }
 
 __global__ void k_iota(int n, int* out) {
@@ -511,6 +583,13 @@ void launch_fill_iota(hipStream_t st, int n, int* out) {
 void launch_count_keys(hipStream_t st, int64_t E, const int* keys, int* counts) {
   if (E <= 0) return;
   MACE_LAUNCH(k_count_keys, dim3(nblk(E, 256)), dim3(256), 0, st, E, keys, counts);
+}
+
+void launch_nl_rev(hipStream_t st, int64_t E, const int* rowptr, const int* sender, const int* receiver,
+                   const int* shifts, int* perm_s, int* pos_s, int* missing) {
+  if (E <= 0) return;
+  MACE_LAUNCH(k_nl_rev, dim3(nblk(E, 256)), dim3(256), 0, st, E, rowptr, sender, receiver, shifts, perm_s, pos_s,
+              missing);
 }
 
 }  // namespace mace
