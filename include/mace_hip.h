@@ -73,7 +73,9 @@ typedef struct mace_model_dims {
                                 rounded to fp16 on the host except E0 / Bessel frequencies,
                                 SH and radial features and every stored activation of the
                                 feature path rounded to fp16, TP weights held in fp16,
-                                accumulation in fp32; 0: float32 throughout               */
+                                accumulation in fp32; 2: bfloat16 policy (model.py:592-596,
+                                705-711): the same rounding points with bf16 values (round
+                                to nearest even), held in fp32 arrays; 0: float32 throughout */
   int32_t density_norm;      /* 1: density-normalised interactions (blocks.py:282-490):
                                 tensor L<l>.dens, message linear / (1 + sum tanh((ef.w)^2)) */
   int32_t first_nonresidual; /* 1: first interaction without residual skip; its skip FCTP

@@ -500,15 +500,19 @@ void build_model(mace_ctx* c) {
   if (d.num_bessel < 1 || d.num_bessel > NBESSEL_MAX) fail(MACE_ERR_UNSUPPORTED, "num_bessel=%d", d.num_bessel);
   if (d.num_layers < 1 || d.num_layers > 4) fail(MACE_ERR_UNSUPPORTED, "num_layers=%d", d.num_layers);
   if (d.num_elements < 1) fail(MACE_ERR_INVALID, "num_elements=%d", d.num_elements);
+  if (d.feature_half < RND_NONE || d.feature_half > RND_BF16)
+    fail(MACE_ERR_INVALID, "feature_half=%d (0 float32, 1 float16, 2 bfloat16)", d.feature_half);
   const int nel = d.num_elements, nb = d.num_bessel;
   upload(c, c->e0, tensor(c, "e0", nel));
   upload(c, c->bessel_w, tensor(c, "bessel_w", nb));
   upload(c, c->embed, tensor(c, "embed", (size_t)nel * C));
-  {  // first linear_up as a per-species table: up0[z] = h0[z] W (fp64 sums; fp16-rounded values under
-     // the float16 feature policy, as the product would give)
+  {  // first linear_up as a per-species table: up0[z] = h0[z] W (fp64 sums; rounded values under
+     // the half-precision feature policies, as the product would give)
     const auto& emb = tensor(c, "embed", (size_t)nel * C);
     const auto& w = tensor(c, "L0.up.0", (size_t)C * C);
-    auto rnd = [&](float x) { return d.feature_half ? (float)(_Float16)x : x; };
+    auto rnd = [&](float x) {
+      return d.feature_half == RND_F16 ? (float)(_Float16)x : d.feature_half == RND_BF16 ? round_bf16(x) : x;
+    };
     std::vector<float> tab((size_t)nel * C);
     for (int z = 0; z < nel; ++z)
       for (int col = 0; col < C; ++col) {
@@ -541,7 +545,8 @@ void build_model(mace_ctx* c) {
     L.dmid = C * n_tp_acc(L.lin);
     L.wn = C * n_tp_slots(L.lin);
     if (d.nonlinear) {
-      if (d.feature_half) fail(MACE_ERR_UNSUPPORTED, "non-linear interaction blocks under the float16 policy");
+      if (d.feature_half)
+        fail(MACE_ERR_UNSUPPORTED, "non-linear interaction blocks under a half-precision feature policy");
       build_layer_nonlin(c, L, l);
       continue;
     }
@@ -573,7 +578,7 @@ void build_model(mace_ctx* c) {
         const auto& w = tensor(c, p + "mlp." + std::to_string(k), (size_t)rows[k] * cols[k]);
         upload(c, L.mlp[k], w);
         upload(c, L.mlpT[k], transpose(w, rows[k], cols[k]));
-        if (k == 3 && d.feature_half) {
+        if (k == 3 && d.feature_half == RND_F16) {
           upload_half(c, L.mlpT3h, transpose(w, rows[k], cols[k]));
           upload_half(c, L.mlp3h, w);
         }
@@ -701,7 +706,7 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   invalidate_graphs(c);
   const size_t e = (size_t)std::max<int64_t>(E, 1);
   int maxw = 0;
-  const bool half = c->dims.feature_half != 0;
+  const bool half = c->dims.feature_half == RND_F16;  // fp16 w / h3 / gw storage
   for (auto& ly : c->layers) {
     if (half)
       ly.wh.ensure(e * ly.wn);
@@ -1072,7 +1077,7 @@ FrontParams front_params(mace_ctx* c) {
   p.zbl_a_exp = (float)c->dims.zbl_a_exp;
   p.zbl_a_pref = (float)c->dims.zbl_a_prefactor;
   p.zbl_scale = (float)c->dims.zbl_scale;
-  p.feature_half = c->dims.feature_half != 0;
+  p.feature_half = c->dims.feature_half;
   p.agnesi = c->dims.agnesi != 0;
   p.ag_q = (float)c->dims.agnesi_q;
   p.ag_p = (float)c->dims.agnesi_p;
@@ -1129,7 +1134,7 @@ void invalidate_graphs(mace_ctx* c) {
 void ensure_embed(mace_ctx* c) {
   if (c->embed_valid) return;
   Site s(c, "embed");
-  launch_embed(c->stream, c->N, c->species.p, c->embed.p, c->layers[0].din, c->h[0].p, c->dims.feature_half != 0,
+  launch_embed(c->stream, c->N, c->species.p, c->embed.p, c->layers[0].din, c->h[0].p, c->dims.feature_half,
                c->up0_tab.p, c->layers[0].h_up.p);
   c->embed_valid = true;
 }
@@ -1387,7 +1392,8 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
   const int N = c->N;
   const int64_t E = c->E;
   const int nb = c->dims.num_bessel;
-  const int half = c->dims.feature_half != 0;
+  const int half = c->dims.feature_half;  // rounding mode of the stored activations (RND_*)
+  const bool h16 = half == RND_F16;       // fp16 storage of h3 / w
   const bool split = !half && c->split_products;
   const bool fused = split && c->fused_tp && c->max_lin <= 2 && !c->dims.nonlinear;
   FrontParams fp = front_params(c);
@@ -1415,17 +1421,17 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
         launch_mlp_hidden_x(st, E, nb, c->ef.p, L.mlp_tiles_x.p, L.mlp_winv, c->h3.p, c->h3inv.p, nullptr);
       else
         launch_mlp_hidden(st, E, nb, c->ef.p, L.mlp_tiles.p,
-                          half ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), c->h3inv.p, L.ds.p,
-                          half ? 1 : 0);
+                          h16 ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), c->h3inv.p, L.ds.p,
+                          h16 ? H3_F16 : half == RND_BF16 ? H3_BF16 : H3_F32);
     }
     if (!fused) {
       Site s(c, lname("mlp_out", l));
-      if (half)
-        launch_mlp_out(st, E, L.wn, c->h3h.p, L.mlpT3h.p, L.wh.p, 1, nullptr, nullptr);
+      if (h16)
+        launch_mlp_out(st, E, L.wn, c->h3h.p, L.mlpT3h.p, L.wh.p, RND_F16, nullptr, nullptr);
       else if (split)
         launch_mlp_out_x(st, E, L.wn, c->h3.p, c->h3inv.p, L.mlpT3x.p, L.w3inv, L.w.p);
       else
-        launch_mlp_out(st, E, L.wn, c->h3.p, L.mlpT[3].p, L.w.p, 0, nullptr, nullptr);
+        launch_mlp_out(st, E, L.wn, c->h3.p, L.mlpT[3].p, L.w.p, half, nullptr, nullptr);
     }
     if (l > 0) {  // the first layer's comes from the species table (launch_embed)
       Site s(c, lname("linear_up", l));
@@ -1441,7 +1447,7 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
         launch_tpx_fwd(st, L.lin, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, c->h3.p, c->h3inv.p,
                        L.mlpT3x.p, L.wn, L.w3inv, L.h_up.p, c->M.p, L.w.p, c->sink.p);
       else
-        launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.wptr(half), L.h_up.p,
+        launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.wptr(h16), L.h_up.p,
                       c->M.p, half);
     }
     const int* ao = tp_accoff(L.lin);
@@ -1525,7 +1531,8 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
   const int64_t E = c->E;
   const int nb = c->dims.num_bessel;
   const int L = (int)c->layers.size();
-  const int half = c->dims.feature_half != 0;
+  const int half = c->dims.feature_half;
+  const bool h16 = half == RND_F16;
   const bool split = !half && c->split_products;
   const bool fused = split && c->fused_tp && c->max_lin <= 2 && !c->dims.nonlinear;
   int gyp = 2;  // dL/dY partials per edge
@@ -1596,8 +1603,8 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
     } else {
       // layers after the first also need dL/dx: per-edge rows in sender order, then a segmented sum
       Site s(c, lname("tp_bwd", l));
-      launch_tp_bwd_recv(st, Ly.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.wptr(half),
-                         Ly.h_up.p, c->gM.p, half ? static_cast<void*>(c->gwh.p) : static_cast<void*>(c->gw.p),
+      launch_tp_bwd_recv(st, Ly.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.wptr(h16),
+                         Ly.h_up.p, c->gM.p, h16 ? static_cast<void*>(c->gwh.p) : static_cast<void*>(c->gw.p),
                          c->gscale.p, c->gY.p, first_edge_grad, c->pos_s.p, l > 0 ? c->gxe.p : nullptr, half);
     }
     if (l > 0) {
@@ -1606,7 +1613,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
     }
     if (!fused) {
       Site s(c, lname("mlp_gh3", l));
-      if (half)
+      if (h16)
         launch_mlp_gh3_h(st, E, Ly.wn, c->gwh.p, c->gscale.p, Ly.mlp3h.p, c->h3.p);
       else if (split)
         launch_mlp_gh3_x(st, E, Ly.wn, c->gw.p, Ly.mlp3x.p, Ly.w3inv, c->h3.p);

@@ -70,15 +70,25 @@ struct FrontParams {
   float zbl_a_exp;
   float zbl_a_pref;
   float zbl_scale;
-  int feature_half;      // float16 feature policy: SH and radial features rounded to fp16
+  int feature_half;      // rounding mode of the stored SH and radial features (RND_*)
   int agnesi;            // Agnesi distance transform of r before the Bessel basis
   float ag_q, ag_p, ag_a;
   int apply_cutoff;      // 0: the envelope is not applied to ef; it goes to cut[e] (mh-1)
 };
 
-// x rounded to the nearest fp16 value when `half` (the stored activations of a
-// model run under the float16 feature policy), else x
-__device__ __forceinline__ float qh(float x, bool half) { return half ? (float)(_Float16)x : x; }
+// Rounding of the stored activations of the feature path: RND_F16 (float16 feature
+// policy) to the nearest fp16 value, RND_BF16 (bfloat16 policy) to the nearest bf16
+// value (ties to even: the upper 16 bits of the fp32 pattern after adding 0x7fff plus
+// the lowest kept bit; infinities and NaNs keep their class), RND_NONE leaves x
+constexpr int RND_NONE = 0, RND_F16 = 1, RND_BF16 = 2;
+__host__ __device__ __forceinline__ float round_bf16(float x) {
+  unsigned u = __builtin_bit_cast(unsigned, x);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return __builtin_bit_cast(float, u & 0xffff0000u);
+}
+__device__ __forceinline__ float qh(float x, int mode) {
+  return mode == RND_F16 ? (float)(_Float16)x : mode == RND_BF16 ? round_bf16(x) : x;
+}
 
 // max over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the lanes holding one
 // edge's k values in the 16x16 fragments), with the gfx950 permlane swaps: after
@@ -137,8 +147,10 @@ void launch_density_edge_bwd(hipStream_t st, int64_t E, const int* receiver, con
 // h3 [E][64] = silu(silu(silu(ef W0) W1) W2); w = h3 W3.  W0..W2 enter as tile images built once
 // per model by launch_mlp_permute (mlp_tile_bytes() bytes).  mode 0: fp32 h3; 1 (float16 feature
 // policy): hidden activations rounded to fp16, h3 fp16; 2: h3 as scaled fp16 hi/lo pairs [E][2][64]
-// with inverse row scales h3inv[E] (operand of launch_mlp_out_x).  ds (may be null): silu' of the
+// with inverse row scales h3inv[E] (operand of launch_mlp_out_x); 3 (bfloat16 policy): hidden
+// activations and the fp32 h3 rounded to bf16 values.  ds (may be null): silu' of the
 // three pre-activations, ds[E][3][64], for launch_mlp_hidden_bwd.
+constexpr int H3_F32 = 0, H3_F16 = 1, H3_SPLIT = 2, H3_BF16 = 3;  // launch_mlp_hidden modes
 size_t mlp_tile_bytes();
 void launch_mlp_permute(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2, void* tiles);
 void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const void* tiles, void* h3,
@@ -155,10 +167,10 @@ void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, con
 void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tiles, const float* winv3,
                              const float* ef, const float* ds, const float* gh3, int np, float* gef,
                              int accumulate);
-// half: h3, W3T and w fp16 arrays (fp32 accumulation); else fp32, and then with bias ([W], may be
-// null) and rs ([E], may be null): w = (h3 W3 + bias) rs[e]
+// rnd RND_F16: h3, W3T and w fp16 arrays (fp32 accumulation); else fp32, with bias ([W], may be
+// null) and rs ([E], may be null): w = (h3 W3 + bias) rs[e], rounded by rnd (RND_NONE / RND_BF16)
 void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w,
-                    int half, const float* bias, const float* rs);
+                    int rnd, const float* bias, const float* rs);
 // float32 policy on fp16 matrix cores: w (fp32) from the split h3 of mode 2 and W3Tx = [hi | lo]
 // fp16 planes of W3^T [W][64] scaled by 1 / cscale
 void launch_mlp_out_x(hipStream_t st, int64_t E, int W, const void* h3x, const float* h3inv,
@@ -220,16 +232,15 @@ void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const void* tiles,
 
 // per-edge x2-first tables Mt[e] (row stride mts) for the l1 >= 1 TP paths
 int tp_table_entries(int max_lin);
-// conv TP fused with the receiver-CSR scatter; w is float, or _Float16 when half (float16
-// feature policy: M rounded to fp16 values)
+// conv TP fused with the receiver-CSR scatter; half is the rounding mode of M (RND_*); w is
+// _Float16 under RND_F16 (float16 feature policy), else float
 void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
                    const float* Y, const float* Mt, int mts, const void* w, const float* up, float* M,
                    int half);
 // TP VJP, receiver-centric; gY is [E][2][16] (per channel half).  With gxe != null the
 // per-edge input gradient is also stored, row pos_s[e] of gxe ([E][LIN^2 * NC], sender order).
-// half: w and gw are fp16, gw scaled per (edge, channel half) by 1 / gscale[e][half]
-// gw: float [E][W], or under the float16 policy (half) fp16 [E][W] scaled per (edge, channel
-// half) by gscale
+// half == RND_F16 (float16 policy): w and gw are fp16, gw [E][W] scaled per (edge, channel half)
+// by 1 / gscale[e][half]; else w and gw are float [E][W]
 void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const int* sender,
                         const float* Y, const float* Mt, int mts, const void* w, const float* up,
                         const float* gM, void* gw, float* gscale, float* gY, int accumulate_gY,
@@ -266,7 +277,7 @@ struct LinearDesc {
   int ldx, in_base, in_stride;
   int ldy, out_base, out_stride;
   int accumulate;   // 0: overwrite, 1: add into Y
-  int round_half;   // stored value rounded to fp16 (float16 feature policy)
+  int round_half;   // rounding mode of the stored value (RND_*)
 };
 void launch_linear(hipStream_t st, int N, const LinearDesc& d, const float* X, const float* W,
                    float* Y);
@@ -301,7 +312,7 @@ struct GemmGroup {
   GemmProb p[GEMM_MAX];
   int n;
   int total_tiles;
-  int round_half;  // outputs rounded to fp16 values (float16 feature policy)
+  int round_half;  // rounding mode of the outputs (RND_*)
   int split;       // float32 policy on fp16 matrix cores (split operands, WX1 / WX2 set)
 };
 void launch_gemm_group(hipStream_t st, GemmGroup& g);

@@ -162,10 +162,10 @@ __device__ __forceinline__ void store_ds(float* d, const f4v* a) {
 
 // The three hidden layers for edges e0 .. e0+15 (lane's edge e0 + r): leaves the
 // pre-activations a3 (a[t][i] = feature 16t + 4g + i); activations between
-// layers rounded to fp16 values under the float16 feature policy.  dsp (null or
+// layers rounded by mode rnd (RND_*, the feature policy).  dsp (null or
 // the lane's position in row ds[e][0][.]) receives silu' of a1..a3.
 __device__ __forceinline__ void hidden_fwd(const MlpFwdW& sw, int64_t E, int64_t e0, int nb,
-                                           const float* __restrict__ ef, f4v* a3, bool half, float* dsp) {
+                                           const float* __restrict__ ef, f4v* a3, int rnd, float* dsp) {
   f4v a1[4], a2[4];
   const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t e = e0 + r;
@@ -181,11 +181,11 @@ __device__ __forceinline__ void hidden_fwd(const MlpFwdW& sw, int64_t E, int64_t
   }
   float v[16];
 #pragma unroll
-  for (int q = 0; q < 16; ++q) v[q] = qh(silu(a1[q >> 2][q & 3]), half);
+  for (int q = 0; q < 16; ++q) v[q] = qh(silu(a1[q >> 2][q & 3]), rnd);
   if (dsp) store_ds(dsp, a1);
   layer64(sw.w1, v, a2);
 #pragma unroll
-  for (int q = 0; q < 16; ++q) v[q] = qh(silu(a2[q >> 2][q & 3]), half);
+  for (int q = 0; q < 16; ++q) v[q] = qh(silu(a2[q >> 2][q & 3]), rnd);
   if (dsp) store_ds(dsp + H, a2);
   layer64(sw.w2, v, a3);
   if (dsp) store_ds(dsp + 2 * H, a3);
@@ -193,11 +193,10 @@ __device__ __forceinline__ void hidden_fwd(const MlpFwdW& sw, int64_t E, int64_t
 
 // 16-edge groups per wave (grid-stride) after the block has staged the weights.
 // Output h3 by MODE: H3_F32 float [E][64]; H3_F16 (float16 feature policy)
-// _Float16 [E][64]; H3_SPLIT (operand of the split-fp16 product) _Float16
+// _Float16 [E][64]; H3_BF16 (bfloat16 policy) float [E][64] holding bf16 values; H3_SPLIT (operand of the split-fp16 product) _Float16
 // [E][2][64]: row e scaled by a power of two that maps its largest magnitude into
 // [2^14, 2^15), then hi = fp16(v) in [e][0] and lo = fp16(v - hi) in [e][1];
 // h3inv[e] = the inverse scale.
-constexpr int H3_F32 = 0, H3_F16 = 1, H3_SPLIT = 2;
 
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
@@ -214,10 +213,14 @@ __global__ void __launch_bounds__(256) k_mlp_hidden(int64_t E, int nb, const flo
   for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
     const int64_t e0 = gi * 16, e = e0 + r;
     f4v a3[4];
-    hidden_fwd(sw, E, e0, nb, ef, a3, MODE == H3_F16, (ds && e < E) ? ds + e * 3 * H + 4 * g : nullptr);
+    constexpr int rnd = MODE == H3_F16 ? RND_F16 : MODE == H3_BF16 ? RND_BF16 : RND_NONE;
+    hidden_fwd(sw, E, e0, nb, ef, a3, rnd, (ds && e < E) ? ds + e * 3 * H + 4 * g : nullptr);
     float v[16];
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = silu(a3[q >> 2][q & 3]);
+    if constexpr (MODE == H3_BF16)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) v[q] = round_bf16(v[q]);
     if constexpr (MODE == H3_SPLIT) {
       float m = 0.f;
 #pragma unroll
@@ -269,7 +272,8 @@ __global__ void __launch_bounds__(256) k_mlp_hidden(int64_t E, int nb, const flo
 // layer with its bias and, under apply_cutoff = false, the edge's envelope)
 __global__ void __launch_bounds__(256) k_mlp_out(int64_t E, int W, const float* __restrict__ h3,
                                                  const float* __restrict__ W3T, float* __restrict__ w,
-                                                 const float* __restrict__ bias, const float* __restrict__ rs) {
+                                                 const float* __restrict__ bias, const float* __restrict__ rs,
+                                                 int rnd) {
   __shared__ __align__(16) float sO[4][64][36];
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t row0 = (int64_t)blockIdx.x * 64;
@@ -331,6 +335,7 @@ __global__ void __launch_bounds__(256) k_mlp_out(int64_t E, int W, const float* 
           const float f = rs[row];
           o = float4{o.x * f, o.y * f, o.z * f, o.w * f};
         }
+        if (rnd) o = float4{qh(o.x, rnd), qh(o.y, rnd), qh(o.z, rnd), qh(o.w, rnd)};
         *reinterpret_cast<float4*>(&w[row * W + c0 + 4 * (l & 7)]) = o;
       }
     }
@@ -1513,19 +1518,21 @@ void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const
     MACE_LAUNCH(k_mlp_hidden<H3_SPLIT>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
   else if (mode == H3_F16)
     MACE_LAUNCH(k_mlp_hidden<H3_F16>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
+  else if (mode == H3_BF16)
+    MACE_LAUNCH(k_mlp_hidden<H3_BF16>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
   else
     MACE_LAUNCH(k_mlp_hidden<H3_F32>, grid, blk, 0, st, E, nb, ef, fw, h3, h3inv, ds);
 }
 
-void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w, int half,
+void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w, int rnd,
                     const float* bias, const float* rs) {
   if (E <= 0) return;
-  if (half)
+  if (rnd == RND_F16)
     MACE_LAUNCH(k_mlp_out_h, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const _Float16*>(h3),
                        static_cast<const _Float16*>(W3T), static_cast<_Float16*>(w));
   else
     MACE_LAUNCH(k_mlp_out, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const float*>(h3),
-                       static_cast<const float*>(W3T), static_cast<float*>(w), bias, rs);
+                       static_cast<const float*>(W3T), static_cast<float*>(w), bias, rs, rnd);
 }
 
 void launch_mlp_out_x(hipStream_t st, int64_t E, int W, const void* h3x, const float* h3inv, const void* W3Tx,

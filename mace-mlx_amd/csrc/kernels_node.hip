@@ -386,7 +386,7 @@ MACE_SC(2, 1) MACE_SC(2, 2) MACE_SC(2, 3)
 
 template <int LOUT, int CORR>
 __device__ __forceinline__ void sc_block_fwd(const float* f, const float* __restrict__ Wl, int z, int c,
-                                             float* __restrict__ Bn, bool half) {
+                                             float* __restrict__ Bn, int half) {
   using P = ScPoly<LOUT, CORR>;
   float w[P::KT];
   const float* wz = Wl + (int64_t)z * P::KT * NC + c;

@@ -1243,8 +1243,8 @@ void launch_tp_fwd(hipStream_t st, int lin, int N, const int* rowptr, const int*
                    const float* Mt, int mts, const void* w, const float* up, float* M, int half) {
   if (N <= 0) return;
 #define MACE_FWD(L)                                                        \
-  half ? launch_fwd<L, _Float16>(st, N, rowptr, sender, Y, Mt, mts, w, up, M, half) \
-       : launch_fwd<L, float>(st, N, rowptr, sender, Y, Mt, mts, w, up, M, half)
+  half == RND_F16 ? launch_fwd<L, _Float16>(st, N, rowptr, sender, Y, Mt, mts, w, up, M, half) \
+                  : launch_fwd<L, float>(st, N, rowptr, sender, Y, Mt, mts, w, up, M, half)
   switch (lin) {
     case 1: MACE_FWD(1); break;
     case 2: MACE_FWD(2); break;
@@ -1258,7 +1258,7 @@ void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const
                         float* gscale, float* gY, int accumulate_gY, const int* pos_s, float* gxe, int half) {
   if (N <= 0) return;
 #define MACE_RECV(L, G)                                                                                          \
-  half ? launch_recv<L, G, _Float16>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gscale, gY, accumulate_gY, \
+  half == RND_F16 ? launch_recv<L, G, _Float16>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gscale, gY, accumulate_gY, \
                                      pos_s, gxe)                                                                 \
        : launch_recv<L, G, float>(st, N, rowptr, sender, Y, Mt, mts, w, up, gM, gw, gscale, gY, accumulate_gY,   \
                                   pos_s, gxe)

@@ -127,8 +127,9 @@ class MACEHIPCalculator(_AseCalculator):
             warnings.warn("the HIP engine computes in float32; falling back from float64 "
                           "(results differ from float64 at the float32 precision level)")
             default_dtype = "float32"
-        if default_dtype not in ("float32", "float16"):
-            raise NotImplementedError(f"default_dtype={default_dtype!r} (float32 and float16 are implemented)")
+        if default_dtype not in ("float32", "float16", "bfloat16"):
+            raise NotImplementedError(
+                f"default_dtype={default_dtype!r} (float32, float16 and bfloat16 are implemented)")
         dev = _DEVICE_MAP.get(str(device).split(":")[0], device)
         if dev != "gpu":
             raise NotImplementedError(f"device={device!r}: this engine runs on AMD GPUs only")

@@ -61,8 +61,8 @@ class DeviceModel:
     r_max: float
 
 
-# Arrays the reference keeps in float32 when the model runs in float16
-# (`model.py:627-647` _pin_float32): baseline energies and Bessel frequencies
+# Arrays the reference keeps in float32 when the model runs in float16 or bfloat16
+# (`model.py:642-661` _pin_float32): baseline energies and Bessel frequencies
 # (covalent radii are tables, never model weights).
 FP32_PINNED = ("atomic_energies_fn.atomic_energies", "radial_embedding.bessel_fn.bessel_weights")
 
@@ -75,18 +75,41 @@ def round_weights_fp16(w: Dict[str, np.ndarray]) -> Dict[str, np.ndarray]:
             for k, v in w.items()}
 
 
+def to_bf16(x) -> np.ndarray:
+    """float32 values rounded to the nearest bfloat16 value (ties to even), returned as float64:
+    the upper 16 bits of the float32 pattern after adding 0x7fff plus the lowest kept bit."""
+    u = np.ascontiguousarray(np.asarray(x, dtype=np.float32)).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def round_weights_bf16(w: Dict[str, np.ndarray]) -> Dict[str, np.ndarray]:
+    """The weights of a bfloat16 model (`model.py:705-711`): every floating array rounded to
+    bf16 except FP32_PINNED."""
+    return {k: (np.asarray(v) if k in FP32_PINNED else to_bf16(v)) for k, v in w.items()}
+
+
+def round_weights(w: Dict[str, np.ndarray], dtype: str) -> Dict[str, np.ndarray]:
+    """The weights a model of dtype ("float32", "float16", "bfloat16") computes with."""
+    return {"float16": round_weights_fp16, "bfloat16": round_weights_bf16}.get(dtype, dict)(w)
+
+
+# mace_model_dims.feature_half per dtype (the rounding mode of the stored activations)
+FEATURE_POLICY = {"float32": 0, "float16": 1, "bfloat16": 2}
+
+
 def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = "float32",
                        head: Optional[str] = None) -> DeviceModel:
     """Fold a model (config + reference-layout weights) into the engine's tensors.  dtype
-    "float16" selects the reference's half-precision feature policy; ``head`` the readout
-    head of a multi-head model (default: the first, as `calculators.py:128-137`)."""
-    if dtype not in ("float32", "float16"):
-        raise UnsupportedModel(f"dtype={dtype!r} (float32 and float16 are implemented)")
-    if dtype == "float16":
-        w = round_weights_fp16(w)
+    "float16" / "bfloat16" select the reference's half-precision feature policies (`model.py:1-15,
+    592-596, 705-711`); ``head`` the readout head of a multi-head model (default: the first, as
+    `calculators.py:128-137`)."""
+    if dtype not in FEATURE_POLICY:
+        raise UnsupportedModel(f"dtype={dtype!r} (float32, float16 and bfloat16 are implemented)")
+    w = round_weights(w, dtype)
     cfg.check_supported()
-    if cfg.nonlinear and dtype == "float16":
-        raise UnsupportedModel("non-linear interaction blocks under the float16 feature policy")
+    if cfg.nonlinear and dtype != "float32":
+        raise UnsupportedModel(f"non-linear interaction blocks under the {dtype} feature policy")
     cfg, w = select_head(cfg, w, head)
     if cfg.model_type not in ("MACE", "ScaleShiftMACE"):
         raise UnsupportedModel(f"model_type={cfg.model_type}")
@@ -118,7 +141,7 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = 
                 radial_depth=3, layer_in_blocks=[0] * 4, layer_hid_blocks=[0] * 4, correlation=[0] * 4,
                 has_zbl=int(bool(cfg.pair_repulsion)), zbl_p=6, r_max=float(cfg.r_max),
                 zbl_a_exp=0.3, zbl_a_prefactor=0.4543, zbl_scale=scale,
-                feature_half=int(dtype == "float16"),
+                feature_half=FEATURE_POLICY[dtype],
                 density_norm=int(bool(cfg.use_density_normalization)),
                 first_nonresidual=int(bool(cfg.first_interaction_nonresidual)),
                 agnesi=int(cfg.agnesi() is not None), agnesi_q=0.0, agnesi_p=0.0, agnesi_a=0.0,

@@ -6,7 +6,7 @@ import numpy as np
 import torch
 
 from mace_mlx_amd._ffi import Engine
-from mace_mlx_amd.device_model import build_device_model, round_weights_fp16
+from mace_mlx_amd.device_model import build_device_model, round_weights
 from mace_mlx_amd.model_io import random_init
 from oracle.model import OracleMACE
 from oracle.neighbors import neighbor_list
@@ -20,14 +20,14 @@ def species_of(dm, numbers):
 
 
 class Case:
-    """Engine + oracle for one (model config, seed, feature dtype).  For "float16" the
-    oracle evaluates the same half-precision model (weights rounded to fp16 except the
-    pinned ones) in float64, i.e. without the feature-path roundings."""
+    """Engine + oracle for one (model config, seed, feature dtype).  For "float16" and
+    "bfloat16" the oracle evaluates the same half-precision model (weights rounded to fp16 /
+    bf16 except the pinned ones) in float64, i.e. without the feature-path roundings."""
 
     def __init__(self, cfg, seed=0, dtype="float32", head=None):
         self.cfg, self.head = cfg, head
         self.w = random_init(cfg, seed)
-        self.w_model = round_weights_fp16(self.w) if dtype == "float16" else self.w
+        self.w_model = round_weights(self.w, dtype)
         self.dm = build_device_model(cfg, self.w, dtype=dtype, head=head)
         self.eng = Engine(0)
         self.eng.load_model(self.dm)

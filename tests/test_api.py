@@ -34,7 +34,7 @@ def test_argument_errors():
     with pytest.raises(NotImplementedError):
         calc.MACEHIPCalculator(model_path="x", device="cpu")
     with pytest.raises(NotImplementedError):
-        calc.MACEHIPCalculator(model_path="x", default_dtype="bfloat16")
+        calc.MACEHIPCalculator(model_path="x", default_dtype="float8")
     with pytest.raises(NotImplementedError):
         calc.mace_anicc()
     with pytest.raises(NotImplementedError):

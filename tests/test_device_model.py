@@ -116,7 +116,52 @@ def test_float16_policy_rounds_all_but_pinned_weights():
     for k in dm16.tensors:   # the half model is the float32 fold of the rounded weights
         np.testing.assert_array_equal(dm16.tensors[k], dm_r.tensors[k])
     with pytest.raises(UnsupportedModel):
-        build_device_model(cfg, w, dtype="bfloat16")
+        build_device_model(cfg, w, dtype="float64")
+
+
+def test_bf16_rounding_matches_torch():
+    """to_bf16 against torch's own float32 -> bfloat16 conversion (round to nearest, ties to
+    even): random magnitudes across the exponent range, exact ties, values next to ties,
+    subnormals, signed zeros, infinities and the largest finite bf16 neighbourhood."""
+    import torch
+    from mace_mlx_amd.device_model import to_bf16
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal(20000) * np.exp2(rng.integers(-140, 120, 20000))).astype(np.float32)
+    base = rng.integers(0, 1 << 16, 4000, dtype=np.uint64) << 16
+    ties = np.concatenate([base | 0x8000, base | 0x7FFF, base | 0x8001]).astype(np.uint32).view(np.float32)
+    special = np.array([0.0, -0.0, 1e-45, -1e-40, np.inf, -np.inf, 3.3895314e38, 3.38e38, 1.0, -1.00390625],
+                       np.float32)
+    x = np.concatenate([x, ties[np.isfinite(ties)], special])
+    want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float64).numpy()
+    np.testing.assert_array_equal(to_bf16(x), want)
+    assert np.array_equal(np.signbit(to_bf16(x)), np.signbit(want))
+
+
+def test_bfloat16_policy_rounds_all_but_pinned_weights():
+    """bfloat16 models (`model.py:592-596,705-711`): every weight array becomes bf16 except the
+    pinned ones; the device model is the float32 fold of those rounded weights with feature
+    policy 2, and the non-linear block stays float32-only."""
+    from mace_mlx_amd.device_model import FP32_PINNED, round_weights_bf16, to_bf16
+    cfg = arch_config("medium")
+    w = random_init(cfg, 0)
+    wb = round_weights_bf16(w)
+    for k, v in wb.items():
+        v = np.asarray(v, dtype=np.float64)
+        if k in FP32_PINNED:
+            np.testing.assert_array_equal(v, np.asarray(w[k], dtype=np.float64))
+        else:
+            np.testing.assert_array_equal(v, to_bf16(v))
+    up = "interactions.0.linear_up.weights.0"
+    assert not np.array_equal(wb[up], np.asarray(w[up], np.float64))
+    dmb = build_device_model(cfg, w, dtype="bfloat16")
+    dm_r = build_device_model(cfg, wb, dtype="float32")
+    assert dmb.dims["feature_half"] == 2
+    for k in dmb.tensors:
+        np.testing.assert_array_equal(dmb.tensors[k], dm_r.tensors[k])
+    from test_oracle_mh1 import mh1_config
+    c1 = mh1_config()
+    with pytest.raises(UnsupportedModel):
+        build_device_model(c1, random_init(c1, 0), dtype="bfloat16")
 
 
 def _multihead_cfg(heads, **kw):

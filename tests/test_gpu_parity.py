@@ -173,6 +173,42 @@ def test_float16_feature_policy(arch):
                   energy="per_atom" if arch == "large" else "relative")
 
 
+@pytest.mark.parametrize("arch", ["hea", "medium", "large"])
+def test_bfloat16_feature_policy(arch):
+    """bfloat16 models (`model.py:592-596,705-711`: set_dtype(bfloat16), E0 and Bessel
+    frequencies re-pinned to float32) against the float64 oracle evaluating the same
+    bf16-rounded weights.  The reference's bf16 path lands 3.6 meV/atom from float32 on a
+    trained model (docs/OPTIMIZATION_REVIEW.md:36); bf16 keeps 8 significand bits against
+    fp16's 11, so the float16 test's force bounds scale by 2^3: |dE|/N <= 3.6 meV/atom,
+    relative force RMS <= 8%, max |dF| <= 0.16 eV/A."""
+    if arch == "hea":
+        bc = make_config(4)
+        cfg = bc.model
+        rng = np.random.default_rng(4)
+        base = lattice(_FCC, 3.6, (3, 3, 3), 26)
+        base.numbers = np.array([26, 28, 27, 24, 25])[rng.integers(0, 5, len(base))]
+        s = rattle(base, 0.05, 4, rng=rng)
+    else:
+        cfg = arch_config(arch)
+        s = rattle(diamond_si((3, 3, 3)), 0.05, 3)
+    case = Case(cfg, dtype="bfloat16")
+    got = case.run(s, stress=True)
+    edges = case.edges()
+    assert edge_set(*edges) == bruteforce_edges(s)
+    ref = case.reference(s, got["sp"], edges, stress=True)
+    de, rel, mx = _fp16_errors(got, ref, len(s))
+    print(f"bf16 {arch}: |dE|/N={de:.2e} relF={rel:.2e} max|dF|={mx:.2e}", flush=True)
+    assert de <= 3.6e-3 and rel <= 8e-2 and mx <= 0.16, (de, rel, mx)
+    dv = np.abs(got["vir"] - ref["vir"]).max()
+    assert dv <= 8e-2 * max(1.0, np.abs(ref["vir"]).max()), (got["vir"], ref["vir"])
+    # the bf16 rounding is what separates the two: the float16 policy on the same weights
+    # lands closer to the float64 model
+    from mace_mlx_amd.device_model import build_device_model
+    case.eng.load_model(build_device_model(cfg, case.w_model, dtype="float16"))
+    de16, rel16, _ = _fp16_errors(case.run(s), ref, len(s))
+    assert 2 * rel16 < rel, (rel16, rel)
+
+
 # ---------------------------------------------------------------------------
 # full-size configurations: size-independent properties
 # ---------------------------------------------------------------------------
