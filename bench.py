@@ -307,8 +307,8 @@ def run_workload(idx, steps, warmup, separate=False, graphs=None, extras=False, 
         Path(launch_order).write_text("\n".join(order) + "\n")
     layers = layer_shapes(dm)
     ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_work=linear_work(layers, N),
-               half=bc.dtype == "float16",
-               fused=not separate and bc.dtype != "float16" and max(x["lin"] for x in layers) <= 2)
+               half=bc.dtype in ("float16", "bfloat16"),
+               fused=not separate and max(x["lin"] for x in layers) <= 2)
     per_step = {k: (v[0] / steps, v[1] // steps) for k, v in kt.items()}
     dom = max(per_step, key=lambda k: per_step[k][0])
     launches = max(per_step[dom][1], 1)
@@ -433,7 +433,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32" if bc.dtype == "float32" else "fp16 features / fp32 accumulation",
+        "dtype": {"float32": "fp32", "float16": "fp16 features / fp32 accumulation",
+                  "bfloat16": "bf16 features / fp32 accumulation"}[bc.dtype],
         "data": "synthetic (seeded lattice + rattle, random-init weights)",
         "config": {"workload": bc.name, "n_atoms": N, "n_edges": E, "properties": head["properties"],
                    "neighbour_list": "cached (skin 0.5)"},

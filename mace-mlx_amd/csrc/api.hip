@@ -582,7 +582,7 @@ void build_model(mace_ctx* c) {
           upload_half(c, L.mlpT3h, transpose(w, rows[k], cols[k]));
           upload_half(c, L.mlp3h, w);
         }
-        if (k == 3 && !d.feature_half) {  // split operands: largest magnitude scaled into [2^14, 2^15)
+        if (k == 3) {  // split operands: largest magnitude scaled into [2^14, 2^15)
           float m = 0.f;
           for (float x : w) m = std::max(m, std::fabs(x));
           const int ex = m > 0.f ? std::ilogb(m) : 0;
@@ -593,7 +593,7 @@ void build_model(mace_ctx* c) {
       }
       L.mlp_tiles.ensure(mlp_tile_bytes());
       launch_mlp_permute(c->stream, nb, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, L.mlp_tiles.p);
-      if (!d.feature_half) {  // split images, one power-of-two scale per matrix
+      {  // split images, one power-of-two scale per matrix (lo planes 0 for rounded weights)
         float sc[3];
         for (int k = 0; k < 3; ++k) {
           float m = 0.f;
@@ -618,7 +618,7 @@ void build_model(mace_ctx* c) {
     }
     build_product_readout(c, L, l);
   }
-  if (!d.feature_half) {  // split copies of every weight matrix the grouped products use
+  {  // split copies of every weight matrix the grouped products use
     const size_t CC = (size_t)C * C;
     for (Layer& L : c->layers) {
       for (int b = 0; b < L.lin; ++b) make_split(c, L.up[b].p, CC), make_split(c, L.upT[b].p, CC);
@@ -702,18 +702,36 @@ void ensure_node_buffers(mace_ctx* c) {
   }
 }
 
+// Which kernels a step runs (from the model and the two switches).  fused: the radial-MLP
+// output layer inside the TP kernels (split products, at most two input blocks, standard
+// interaction blocks), under every feature policy (the rounding modes are template
+// parameters of the fused forward); split: the radial MLP's hidden layers on split-fp16
+// products (fused path, or the float32 policy); h16: the float16 policy's separate path with
+// fp16 h3 / w / dL/dw arrays.  Neither split nor h16: fp32 products, silu' saved (ds).
+struct StepPath {
+  bool fused, split, h16;
+};
+StepPath step_path(const mace_ctx* c) {
+  StepPath p;
+  p.fused = c->split_products && c->fused_tp && c->max_lin <= 2 && !c->dims.nonlinear;
+  p.split = p.fused || (c->dims.feature_half == RND_NONE && c->split_products);
+  p.h16 = !p.split && c->dims.feature_half == RND_F16;
+  return p;
+}
+
 void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   invalidate_graphs(c);
   const size_t e = (size_t)std::max<int64_t>(E, 1);
   int maxw = 0;
-  const bool half = c->dims.feature_half == RND_F16;  // fp16 w / h3 / gw storage
+  const StepPath path = step_path(c);
+  const bool half = path.h16;  // fp16 w / h3 / gw storage
   for (auto& ly : c->layers) {
     if (half)
       ly.wh.ensure(e * ly.wn);
     else
       ly.w.ensure(e * ly.wn);
     maxw = std::max(maxw, ly.wn);
-    ly.ds.ensure(e * 3 * RADIAL_H);
+    if (!path.split) ly.ds.ensure(e * 3 * RADIAL_H);
   }
   if (half) c->h3h.ensure(e * RADIAL_H);
   size_t maxdin = 0;  // per-edge input gradients of the layers after the first
@@ -1032,11 +1050,11 @@ GemmProb gprob(int N, int d, int K1, int Cout, const float* X1, int ldx1, int ba
   return P;
 }
 
-// grouped products: on fp16 matrix cores with split operands under the float32 policy when
-// enabled and every weight matrix has its split copy, else on fp32 matrix cores
+// grouped products: on fp16 matrix cores with split operands when enabled and every weight
+// matrix has its split copy, else on fp32 matrix cores (either way rounded by g.round_half)
 void run_gemm(mace_ctx* c, hipStream_t st, GemmGroup& g) {
   g.split = 0;
-  if (c->split_products && !c->dims.feature_half && !g.round_half) {
+  if (c->split_products) {
     bool ok = true;
     for (int q = 0; q < g.n && ok; ++q) {
       GemmProb& P = g.p[q];
@@ -1393,9 +1411,8 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
   const int64_t E = c->E;
   const int nb = c->dims.num_bessel;
   const int half = c->dims.feature_half;  // rounding mode of the stored activations (RND_*)
-  const bool h16 = half == RND_F16;       // fp16 storage of h3 / w
-  const bool split = !half && c->split_products;
-  const bool fused = split && c->fused_tp && c->max_lin <= 2 && !c->dims.nonlinear;
+  const StepPath path = step_path(c);
+  const bool h16 = path.h16, split = path.split, fused = path.fused;
   FrontParams fp = front_params(c);
   {
     Site s(c, "edge_fwd");
@@ -1418,7 +1435,7 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
       // split: h3 holds E x 2 x 64 fp16 (the same bytes as E x 64 floats)
       if (split)
         // no silu' saved: the VJP recomputes the hidden layers from ef
-        launch_mlp_hidden_x(st, E, nb, c->ef.p, L.mlp_tiles_x.p, L.mlp_winv, c->h3.p, c->h3inv.p, nullptr);
+        launch_mlp_hidden_x(st, E, nb, c->ef.p, L.mlp_tiles_x.p, L.mlp_winv, c->h3.p, c->h3inv.p, nullptr, half);
       else
         launch_mlp_hidden(st, E, nb, c->ef.p, L.mlp_tiles.p,
                           h16 ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), c->h3inv.p, L.ds.p,
@@ -1445,7 +1462,7 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
       Site s(c, lname("tp_fwd", l));
       if (fused)
         launch_tpx_fwd(st, L.lin, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, c->h3.p, c->h3inv.p,
-                       L.mlpT3x.p, L.wn, L.w3inv, L.h_up.p, c->M.p, L.w.p, c->sink.p);
+                       L.mlpT3x.p, L.wn, L.w3inv, L.h_up.p, c->M.p, L.w.p, c->sink.p, half);
       else
         launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.wptr(h16), L.h_up.p,
                       c->M.p, half);
@@ -1532,9 +1549,8 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
   const int nb = c->dims.num_bessel;
   const int L = (int)c->layers.size();
   const int half = c->dims.feature_half;
-  const bool h16 = half == RND_F16;
-  const bool split = !half && c->split_products;
-  const bool fused = split && c->fused_tp && c->max_lin <= 2 && !c->dims.nonlinear;
+  const StepPath path = step_path(c);
+  const bool h16 = path.h16, split = path.split, fused = path.fused;
   int gyp = 2;  // dL/dY partials per edge
   if (fused)
     for (const Layer& Ly : c->layers) gyp = std::max(gyp, tpx_parts(Ly.lin));
@@ -1624,7 +1640,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
       Site s(c, lname("mlp_hidden_bwd", l));
       if (split)
         launch_mlp_hidden_bwd_x(st, E, nb, Ly.mlp_tiles_x.p, Ly.mlp_winv, c->ef.p, nullptr, fused ? c->gh3p.p : c->h3.p,
-                                fused ? tpx_parts(Ly.lin) : 1, c->gef.p, first_edge_grad);
+                                fused ? tpx_parts(Ly.lin) : 1, c->gef.p, first_edge_grad, half);
       else
         launch_mlp_hidden_bwd(st, E, nb, Ly.mlp_tiles.p, Ly.ds.p, c->h3.p, c->gef.p, first_edge_grad);
     }
@@ -2099,6 +2115,7 @@ int mace_set_split_products(mace_ctx* c, int32_t enable) {
     set_device(c);
     c->split_products = enable != 0;
     invalidate_graphs(c);
+    if (c->model_ready && c->E > 0) ensure_edge_buffers(c, c->E);  // the arrays of the path now taken
   });
 }
 
@@ -2108,6 +2125,7 @@ int mace_set_fused_tp(mace_ctx* c, int32_t enable) {
     set_device(c);
     c->fused_tp = enable != 0;
     invalidate_graphs(c);
+    if (c->model_ready && c->E > 0) ensure_edge_buffers(c, c->E);
   });
 }
 

@@ -160,13 +160,15 @@ void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const
 size_t mlp_tile_x_bytes();
 void launch_mlp_permute_x(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2,
                           const float* scale3, void* tiles);
+// rnd: rounding mode of the activations (RND_*; the split of a rounded h3 has a zero lo plane)
 void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, const void* tiles,
-                         const float* winv3, void* h3x, float* h3inv, float* ds);
+                         const float* winv3, void* h3x, float* h3inv, float* ds, int rnd);
 // gh3: np partials of dL/dh3 ([np][E][64]), added in order; ds null: silu' of the
-// hidden pre-activations recomputed from ef (the forward then need not save them)
+// hidden pre-activations recomputed from ef with the forward's rounding mode rnd (the forward
+// then need not save them)
 void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tiles, const float* winv3,
                              const float* ef, const float* ds, const float* gh3, int np, float* gef,
-                             int accumulate);
+                             int accumulate, int rnd);
 // rnd RND_F16: h3, W3T and w fp16 arrays (fp32 accumulation); else fp32, with bias ([W], may be
 // null) and rs ([E], may be null): w = (h3 W3 + bias) rs[e], rounded by rnd (RND_NONE / RND_BF16)
 void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w,
@@ -246,16 +248,16 @@ void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const
                         const float* gM, void* gw, float* gscale, float* gY, int accumulate_gY,
                         const int* pos_s, float* gxe, int half);
 // gup[a] = sum of the sender-ordered gxe rows of node a
-// Radial-MLP output layer fused into the TP forward (float32 policy with split
-// products, lin <= 2): w is built per 16-edge tile from the split h3 planes
-// (h3x, h3inv) and the split W3^T planes (W3Tx, scale wscale), M is written as
-// by launch_tp_fwd and w ([E][W]) for the VJP; sink: W scratch floats that
-// absorb the stores of padding edges.
+// Radial-MLP output layer fused into the TP forward (split products, lin <= 2): w is
+// built per 16-edge tile from the split h3 planes (h3x, h3inv) and the split W3^T planes
+// (W3Tx, scale wscale), M is written as by launch_tp_fwd and w ([E][W]) for the VJP; w and
+// M rounded by rnd (RND_*, the feature policy); sink: W scratch floats that absorb the
+// stores of padding edges.
 void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const void* h3x, const float* h3inv, const void* W3Tx, int W,
-                    float wscale, const float* up, float* M, float* w, float* sink);
-// TP VJP with the radial-MLP output layer's backward product fused in (float32
-// policy, split products, lin <= 2): reads w ([E][W], written by
+                    float wscale, const float* up, float* M, float* w, float* sink, int rnd);
+// TP VJP with the radial-MLP output layer's backward product fused in (split products,
+// lin <= 2): reads w ([E][W], written by
 // launch_tpx_fwd), writes the dL/dh3 partials gh3p ([P][E][64], P = 2 x input
 // degrees of the layer), dL/dY partials into gY[e][p][16] (gyp partials per
 // edge; written, or added when accumulate_gY) and, with gxe, the per-edge dL/dx

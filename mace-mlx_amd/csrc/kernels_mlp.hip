@@ -1015,9 +1015,10 @@ __device__ __forceinline__ void layer64x(const h8 (*w)[4][2][64], const float* v
 }
 
 // forward of the split kernels: first layer over the Bessel features, then two 64-wide
-// layers; dsp as in hidden_fwd; leaves a1, a2, a3 (the VJP recomputes them this
-// way, with the same instructions, instead of reading saved derivatives)
-template <bool OPQ>
+// layers, the activations between them rounded by mode RND (the feature policy); dsp as in
+// hidden_fwd; leaves a1, a2, a3 (the VJP recomputes them this way, with the same
+// instructions, instead of reading saved derivatives)
+template <bool OPQ, int RND>
 __device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* winv, int64_t E, int64_t e0, int nb,
                                              const float* __restrict__ ef, f4v* a1, f4v* a2, f4v* a3, float* dsp) {
   const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
@@ -1052,11 +1053,11 @@ __device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* win
   }
   float v[16];
 #pragma unroll
-  for (int q = 0; q < 16; ++q) v[q] = silu(a1[q >> 2][q & 3]);
+  for (int q = 0; q < 16; ++q) v[q] = qh(silu(a1[q >> 2][q & 3]), RND);
   if (dsp) store_ds(dsp, a1);
   layer64x<OPQ>(sw.w1, v, winv[1], a2);
 #pragma unroll
-  for (int q = 0; q < 16; ++q) v[q] = silu(a2[q >> 2][q & 3]);
+  for (int q = 0; q < 16; ++q) v[q] = qh(silu(a2[q >> 2][q & 3]), RND);
   if (dsp) store_ds(dsp + H, a2);
   layer64x<OPQ>(sw.w2, v, winv[2], a3);
   if (dsp) store_ds(dsp + 2 * H, a3);
@@ -1071,7 +1072,9 @@ struct MlpWinv {
 constexpr int kHidFwdWaves = 4;
 constexpr int kHidBwdWaves = 4;
 
-// h3 as split pairs [E][2][64] + h3inv (H3_SPLIT layout) and silu' saved in ds
+// h3 as split pairs [E][2][64] + h3inv (H3_SPLIT layout) and silu' saved in ds; under a
+// half-precision feature policy (RND) the activations are rounded first (h3's lo plane is then 0)
+template <int RND>
 __global__ void __launch_bounds__(64 * kHidFwdWaves) k_mlp_hidden_x(int64_t E, int nb, const float* __restrict__ ef,
                                                       const MlpFwdX* __restrict__ tiles, MlpWinv wi,
                                                       _Float16* __restrict__ h3x, float* __restrict__ h3inv,
@@ -1084,10 +1087,10 @@ __global__ void __launch_bounds__(64 * kHidFwdWaves) k_mlp_hidden_x(int64_t E, i
   for (int64_t gi = (int64_t)blockIdx.x * kHidFwdWaves + wv; gi < ngroups; gi += (int64_t)gridDim.x * kHidFwdWaves) {
     const int64_t e0 = gi * 16, e = e0 + r;
     f4v a1[4], a2[4], a3[4];
-    hidden_fwd_x<false>(sw, wi.w, E, e0, nb, ef, a1, a2, a3, (ds && e < E) ? ds + e * 3 * H + 4 * g : nullptr);
+    hidden_fwd_x<false, RND>(sw, wi.w, E, e0, nb, ef, a1, a2, a3, (ds && e < E) ? ds + e * 3 * H + 4 * g : nullptr);
     float v[16];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) v[q] = silu(a3[q >> 2][q & 3]);
+    for (int q = 0; q < 16; ++q) v[q] = qh(silu(a3[q >> 2][q & 3]), RND);
     float inv;
     const float sc = edge_scale<16>(v, &inv);
     if (e < E) {
@@ -1111,9 +1114,9 @@ __global__ void __launch_bounds__(64 * kHidFwdWaves) k_mlp_hidden_x(int64_t E, i
 }
 
 // gh3: np partials [np][E][64] (stride pstride floats), added in order.  RECOMP:
-// silu'(a1..a3) from the forward layers recomputed from ef (tiles ftiles) instead
-// of read from ds.
-template <bool RECOMP, int NW>
+// silu'(a1..a3) from the forward layers recomputed from ef (tiles ftiles, rounding mode
+// RND as the forward) instead of read from ds.
+template <bool RECOMP, int NW, int RND>
 __global__ void __launch_bounds__(64 * NW) k_mlp_hidden_bwd_x(int64_t E, int nb, const MlpFwdX* __restrict__ ftiles,
                                                           const MlpBwdX* __restrict__ tiles, MlpWinv wi,
                                                           const float* __restrict__ ef, const float* __restrict__ ds,
@@ -1132,7 +1135,7 @@ __global__ void __launch_bounds__(64 * NW) k_mlp_hidden_bwd_x(int64_t E, int nb,
     float v[16], dv[16];
     f4v acc[4];
     f4v a1[4], a2[4], a3[4];  // RECOMP: the pre-activations, rebuilt
-    if constexpr (RECOMP) hidden_fwd_x<true>(swf, wi.w, E, e0, nb, ef, a1, a2, a3, nullptr);
+    if constexpr (RECOMP) hidden_fwd_x<true, RND>(swf, wi.w, E, e0, nb, ef, a1, a2, a3, nullptr);
     // silu' of layer k's pre-activations in the lane's layout (feature 16t + 4g + i -> [4t + i])
     auto dsl = [&](int k, float* out) {
       if constexpr (RECOMP) {
@@ -1481,26 +1484,43 @@ void launch_mlp_permute_x(hipStream_t st, int nb, const float* W0, const float* 
 }
 
 void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, const void* tiles,
-                         const float* winv3, void* h3x, float* h3inv, float* ds) {
+                         const float* winv3, void* h3x, float* h3inv, float* ds, int rnd) {
   if (E <= 0) return;
   MlpWinv wi{{winv3[0], winv3[1], winv3[2]}};
-  MACE_LAUNCH(k_mlp_hidden_x, dim3(hidden_grid(E)), dim3(64 * kHidFwdWaves), 0, st, E, nb, ef,
-                     static_cast<const MlpFwdX*>(tiles), wi, static_cast<_Float16*>(h3x), h3inv, ds);
+#define MACE_HX(R)                                                                                 \
+  MACE_LAUNCH(k_mlp_hidden_x<R>, dim3(hidden_grid(E)), dim3(64 * kHidFwdWaves), 0, st, E, nb, ef, \
+              static_cast<const MlpFwdX*>(tiles), wi, static_cast<_Float16*>(h3x), h3inv, ds)
+  if (rnd == RND_F16)
+    MACE_HX(RND_F16);
+  else if (rnd == RND_BF16)
+    MACE_HX(RND_BF16);
+  else
+    MACE_HX(RND_NONE);
+#undef MACE_HX
 }
 
 void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tiles, const float* winv3,
-                             const float* ef, const float* ds, const float* gh3, int np, float* gef, int accumulate) {
+                             const float* ef, const float* ds, const float* gh3, int np, float* gef, int accumulate,
+                             int rnd) {
   if (E <= 0) return;
   MlpWinv wi{{winv3[0], winv3[1], winv3[2]}};
   const MlpFwdX* fw = static_cast<const MlpFwdX*>(tiles);
   const MlpBwdX* bw = reinterpret_cast<const MlpBwdX*>(static_cast<const char*>(tiles) + sizeof(MlpFwdX));
-  if (ds)
-    MACE_LAUNCH((k_mlp_hidden_bwd_x<false, 4>), dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, fw, bw, wi, ef, ds,
-                       gh3, np, E * H, gef, accumulate);
+  if (ds) {
+    MACE_LAUNCH((k_mlp_hidden_bwd_x<false, 4, RND_NONE>), dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, fw, bw, wi,
+                ef, ds, gh3, np, E * H, gef, accumulate);
+    return;
+  }
+#define MACE_HBX(R)                                                                                              \
+  MACE_LAUNCH((k_mlp_hidden_bwd_x<true, kHidBwdWaves, R>), dim3(hidden_bwd_grid(E)), dim3(64 * kHidBwdWaves), 0, \
+              st, E, nb, fw, bw, wi, ef, ds, gh3, np, E * H, gef, accumulate)
+  if (rnd == RND_F16)
+    MACE_HBX(RND_F16);
+  else if (rnd == RND_BF16)
+    MACE_HBX(RND_BF16);
   else
-    MACE_LAUNCH((k_mlp_hidden_bwd_x<true, kHidBwdWaves>), dim3(hidden_bwd_grid(E)), dim3(64 * kHidBwdWaves), 0,
-                       st, E, nb, fw, bw, wi, ef,
-                       ds, gh3, np, E * H, gef, accumulate);
+    MACE_HBX(RND_NONE);
+#undef MACE_HBX
 }
 
 void launch_mlp_permute(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2, void* tiles) {

@@ -348,6 +348,7 @@ __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
       const float4 o = *reinterpret_cast<const float4*>(y);
       v.x += o.x, v.y += o.y, v.z += o.z, v.w += o.w;
     }
+    if (G.round_half) v = float4{qh(v.x, G.round_half), qh(v.y, G.round_half), qh(v.z, G.round_half), qh(v.w, G.round_half)};
     *reinterpret_cast<float4*>(y) = v;
   }
 }

@@ -620,7 +620,7 @@ struct TpxDims {
 // h3x: [E][hi 64 | lo 64]; h3inv: [E]; W3Tx: [W][64] hi plane, then lo plane;
 // w: [E][W] for the VJP; sink: W floats, target of the stores of padding edges
 
-template <int LIN, int L1>
+template <int LIN, int L1, int RND>
 __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, float* sw, float* stab, _Float16* hbuf,
                                         float* hiv) {
   using T = TPT<LIN>;
@@ -769,7 +769,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
         const int ct = wv + XW * m;
         if (CT % XW == 0 || ct < CT)
           *reinterpret_cast<float4*>(tile + col * RS + 16 * ct + 4 * g) =
-              float4{d[m][0] * bsc, d[m][1] * bsc, d[m][2] * bsc, d[m][3] * bsc};
+              float4{qh(d[m][0] * bsc, RND), qh(d[m][1] * bsc, RND), qh(d[m][2] * bsc, RND), qh(d[m][3] * bsc, RND)};
       }
     }
     store_h(j + 1, Snext);  // its last readers (step j - 1) are past the previous barrier
@@ -850,11 +850,13 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
     for (int s = 0; s < T::NSLOT; ++s)
       if (T::l1(s) == L1)
 #pragma unroll
-        for (int m = 0; m < 2 * T::l3(s) + 1; ++m) Mn[NC * (T::acc(s) + m)] = acc[T::acc(s) + m];
+        for (int m = 0; m < 2 * T::l3(s) + 1; ++m) Mn[NC * (T::acc(s) + m)] = qh(acc[T::acc(s) + m], RND);
   }
 }
 
-template <int LIN>
+// RND: rounding mode of w and M under a half-precision feature policy (the split operands
+// of rounded h3 and weights have zero lo planes, so w is the float32 product, then rounded)
+template <int LIN, int RND>
 __global__ void __launch_bounds__(64 * XW, 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_PTRS) {
   static_assert(LIN <= 2, "three input blocks are not fused");
   constexpr int TC = XW * EPW;
@@ -863,12 +865,12 @@ __global__ void __launch_bounds__(64 * XW, 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_
   __shared__ __align__(16) _Float16 hbuf[2 * 2 * TC * 72];  // [step][hi, lo][tile column][64 + pad]
   __shared__ float hiv[2 * TC];
   if constexpr (LIN == 1) {
-    tpx_fwd<1, 0>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
+    tpx_fwd<1, 0, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
   } else {
     if (blockIdx.z == 0)
-      tpx_fwd<2, 1>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
+      tpx_fwd<2, 1, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
     else
-      tpx_fwd<2, 0>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
+      tpx_fwd<2, 0, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
   }
 }
 
@@ -1273,18 +1275,28 @@ void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const
 
 void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const void* h3x, const float* h3inv, const void* W3Tx, int W,
-                    float wscale, const float* up, float* M, float* w, float* sink) {
+                    float wscale, const float* up, float* M, float* w, float* sink, int rnd) {
   if (N <= 0) return;
   const TpxDims a{N, W, mts, E, wscale};
   const dim3 grid((unsigned)((N + XW - 1) / XW), 2, lin == 1 ? 1 : 2);
   const _Float16* hx = static_cast<const _Float16*>(h3x);
   const _Float16* wt = static_cast<const _Float16*>(W3Tx);
-  if (lin == 1)
-    MACE_LAUNCH(k_tpx_fwd<1>, grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w,
-                       sink);
-  else
-    MACE_LAUNCH(k_tpx_fwd<2>, grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w,
-                       sink);
+#define MACE_TPXF(L, R) \
+  MACE_LAUNCH((k_tpx_fwd<L, R>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w, sink)
+#define MACE_TPXF_R(L)         \
+  if (rnd == RND_F16)          \
+    MACE_TPXF(L, RND_F16);     \
+  else if (rnd == RND_BF16)    \
+    MACE_TPXF(L, RND_BF16);    \
+  else                         \
+    MACE_TPXF(L, RND_NONE);
+  if (lin == 1) {
+    MACE_TPXF_R(1)
+  } else {
+    MACE_TPXF_R(2)
+  }
+#undef MACE_TPXF_R
+#undef MACE_TPXF
 }
 
 void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
