@@ -60,8 +60,8 @@ std::vector<double*> g_scratch_ptr;  // per device ordinal: address of `scratch`
 
 // partials of dL/dY and dL/dh3 per edge: the receiver VJP writes one per
 // channel half; the fused TP VJP one per (input degree, 64-channel slice)
-constexpr int kGyMax = 4;
-inline int tpx_parts(int lin) { return lin == 1 ? 2 : 4; }
+constexpr int kGyMax = 6;
+inline int tpx_parts(int lin) { return 2 * lin; }
 [[noreturn]] void fail(int code, const char* fmt, ...) {
   char buf[1024];
   va_list ap;
@@ -703,8 +703,8 @@ void ensure_node_buffers(mace_ctx* c) {
 }
 
 // Which kernels a step runs (from the model and the two switches).  fused: the radial-MLP
-// output layer inside the TP kernels (split products, at most two input blocks, standard
-// interaction blocks), under every feature policy (the rounding modes are template
+// output layer inside the TP kernels (split products, standard interaction blocks), under
+// every feature policy (the rounding modes are template
 // parameters of the fused forward); split: the radial MLP's hidden layers on split-fp16
 // products (fused path, or the float32 policy); h16: the float16 policy's separate path with
 // fp16 h3 / w / dL/dw arrays.  Neither split nor h16: fp32 products, silu' saved (ds).
@@ -713,7 +713,7 @@ struct StepPath {
 };
 StepPath step_path(const mace_ctx* c) {
   StepPath p;
-  p.fused = c->split_products && c->fused_tp && c->max_lin <= 2 && !c->dims.nonlinear;
+  p.fused = c->split_products && c->fused_tp && !c->dims.nonlinear;
   p.split = p.fused || (c->dims.feature_half == RND_NONE && c->split_products);
   p.h16 = !p.split && c->dims.feature_half == RND_F16;
   return p;

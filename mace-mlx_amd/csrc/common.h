@@ -248,7 +248,7 @@ void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const
                         const float* gM, void* gw, float* gscale, float* gY, int accumulate_gY,
                         const int* pos_s, float* gxe, int half);
 // gup[a] = sum of the sender-ordered gxe rows of node a
-// Radial-MLP output layer fused into the TP forward (split products, lin <= 2): w is
+// Radial-MLP output layer fused into the TP forward (split products, lin = 1..3): w is
 // built per 16-edge tile from the split h3 planes (h3x, h3inv) and the split W3^T planes
 // (W3Tx, scale wscale), M is written as by launch_tp_fwd and w ([E][W]) for the VJP; w and
 // M rounded by rnd (RND_*, the feature policy); sink: W scratch floats that absorb the
@@ -257,7 +257,7 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
                     const float* Mt, int mts, const void* h3x, const float* h3inv, const void* W3Tx, int W,
                     float wscale, const float* up, float* M, float* w, float* sink, int rnd);
 // TP VJP with the radial-MLP output layer's backward product fused in (split products,
-// lin <= 2): reads w ([E][W], written by
+// lin = 1..3): reads w ([E][W], written by
 // launch_tpx_fwd), writes the dL/dh3 partials gh3p ([P][E][64], P = 2 x input
 // degrees of the layer), dL/dY partials into gY[e][p][16] (gyp partials per
 // edge; written, or added when accumulate_gY) and, with gxe, the per-edge dL/dx

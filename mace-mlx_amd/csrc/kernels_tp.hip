@@ -28,6 +28,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <utility>
 
 #include "common.h"
 
@@ -55,28 +56,33 @@ MACE_TP_TRAITS(3)
 
 constexpr int MT_M2 = TP3_M1_NE;  // offset of the l1 = 2 table inside an Mt row
 
-// The CG terms of each M1 entry q (M1[q] = sum over terms of Y[j] v), padded to two
-// with (j, v) = (0, 0): a table a lane indexes with its own entry number.
-struct M1Terms {
-  int j[TP3_M1_NE][2];
-  float v[TP3_M1_NE][2];
+// The CG terms of each M1 (l1 = 1) / M2 (l1 = 2) table entry q (M[q] = sum over terms of
+// Y[j] v), padded to two with (j, v) = (0, 0): tables a lane indexes with its own entry number.
+template <int NE>
+struct MTerms {
+  int j[NE][2];
+  float v[NE][2];
 };
-constexpr int m1_max_terms() {
+template <int NE>
+constexpr int max_terms(const int (&start)[NE + 1]) {
   int m = 0;
-  for (int q = 0; q < TP3_M1_NE; ++q) m = TP3_M1_START[q + 1] - TP3_M1_START[q] > m ? TP3_M1_START[q + 1] - TP3_M1_START[q] : m;
+  for (int q = 0; q < NE; ++q) m = start[q + 1] - start[q] > m ? start[q + 1] - start[q] : m;
   return m;
 }
-static_assert(m1_max_terms() <= 2, "M1 entries with more than two CG terms");
-constexpr M1Terms make_m1_terms() {
-  M1Terms t{};
-  for (int q = 0; q < TP3_M1_NE; ++q)
-    for (int x = TP3_M1_START[q]; x < TP3_M1_START[q + 1]; ++x) {
-      t.j[q][x - TP3_M1_START[q]] = TP3_M1_J[x];
-      t.v[q][x - TP3_M1_START[q]] = TP3_M1_V[x];
+static_assert(max_terms<TP3_M1_NE>(TP3_M1_START) <= 2, "M1 entries with more than two CG terms");
+static_assert(max_terms<TP3_M2_NE>(TP3_M2_START) <= 2, "M2 entries with more than two CG terms");
+template <int NE, int NT>
+constexpr MTerms<NE> make_terms(const int (&start)[NE + 1], const int (&js)[NT], const float (&vs)[NT]) {
+  MTerms<NE> t{};
+  for (int q = 0; q < NE; ++q)
+    for (int x = start[q]; x < start[q + 1]; ++x) {
+      t.j[q][x - start[q]] = js[x];
+      t.v[q][x - start[q]] = vs[x];
     }
   return t;
 }
-__constant__ const M1Terms kM1Terms = make_m1_terms();
+__constant__ const MTerms<TP3_M1_NE> kM1Terms = make_terms<TP3_M1_NE>(TP3_M1_START, TP3_M1_J, TP3_M1_V);
+__constant__ const MTerms<TP3_M2_NE> kM2Terms = make_terms<TP3_M2_NE>(TP3_M2_START, TP3_M2_J, TP3_M2_V);
 
 static_assert(TP2_K1 == TP3_K1, "shared M1 layout");
 
@@ -586,6 +592,12 @@ struct GrpT {
     for (int q = 0; q < s; ++q) k += T::l1(q) == L1 ? 1 : 0;
     return k;
   }
+  // slot of group position si (compile-time si)
+  __host__ __device__ static constexpr int slot_of(int si) {
+    for (int s = 0; s < T::NSLOT; ++s)
+      if (T::l1(s) == L1 && local(s) == si) return s;
+    return 0;
+  }
   // slot of group position si (run-time si: a select chain over the slots)
   __device__ static int slot(int si) {
     int res = 0;
@@ -599,8 +611,14 @@ struct GrpT {
 // largest group (LDS size of the fused kernels)
 template <int LIN>
 constexpr int gmax() {
-  return LIN == 1 ? GrpT<1, 0>::G : std::max(GrpT<2, 0>::G, GrpT<2, 1>::G);
+  return LIN == 1   ? GrpT<1, 0>::G
+         : LIN == 2 ? std::max(GrpT<2, 0>::G, GrpT<2, 1>::G)
+                    : std::max({GrpT<3, 0>::G, GrpT<3, 1>::G, GrpT<3, 2>::G});
 }
+// entries of the per-edge table row an l1 group reads (Y itself for l1 = 0, M1 / M2 else),
+// and that count rounded up to four (the row stride in LDS)
+constexpr int tpx_tab(int l1) { return l1 == 0 ? 16 : l1 == 1 ? TP3_M1_NE : TP3_M2_NE; }
+constexpr int tpx_tab_pad(int l1) { return (tpx_tab(l1) + 3) & ~3; }
 
 // scalar parameters of the fused forward (pointers are passed separately, as
 // __restrict__ kernel arguments: uniform loads through them then use the
@@ -669,24 +687,24 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   // j + 2 once its edges are done; sender indices (scalar loads) are fetched a
   // step before the rows they address.
   const int64_t elast = a.E - 1;  // E >= 1 whenever a step runs
-  constexpr int TY = L1 == 0 ? 16 : 0, TS = TY + (L1 == 1 ? TP3_M1_NE : 0), TSP = (TS + 3) & ~3;
-  constexpr int TH = (TS + 63) / 64;
-  // entries of a table row a lane loads: l1 = 0, the Y row itself; l1 = 1, Y component l & 15,
-  // from which the M1 row is built in LDS (m1_row_entry)
-  constexpr int TL = L1 == 1 ? 1 : TH;
-  static_assert(TS <= 128 && L1 <= 1, "table rows of up to 128 entries");
-  float* tb = stab + wv * EPW * TSP;  // this wave's table rows (Y for l1 = 0 slots, M1 for l1 = 1)
-  float* yb = stab + XW * EPW * TSP + wv * EPW * 16;  // l1 = 1: this wave's Y rows
-  // l1 = 1: the CG terms (at most two) of the M1 entries q = l + 64 h this lane builds
+  constexpr int TS = tpx_tab(L1), TSP = tpx_tab_pad(L1), TH = (TS + 63) / 64;
+  // entries of a table row a lane loads: l1 = 0, the Y row itself; l1 = 1, 2, Y component
+  // l & 15, from which the M1 / M2 row is built in LDS
+  constexpr int TL = L1 >= 1 ? 1 : TH;
+  static_assert(TS <= 192 && L1 <= 2, "table rows of up to 192 entries");
+  // this wave's table rows (Y for l1 = 0 slots, M1 for l1 = 1, M2 for l1 = 2), then its Y rows
+  float* tb = stab + wv * EPW * TSP;
+  float* yb = stab + XW * EPW * TSP + wv * EPW * 16;
+  // l1 >= 1: the CG terms (at most two) of the table entries q = l + 64 h this lane builds
   int mj[TH][2];
   float mv[TH][2];
 #pragma unroll
   for (int h = 0; h < TH; ++h) {
-    const int q = min(l + 64 * h, TP3_M1_NE - 1);
+    const int q = min(l + 64 * h, TS - 1);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      mj[h][t] = L1 == 1 ? kM1Terms.j[q][t] : 0;
-      mv[h][t] = L1 == 1 ? kM1Terms.v[q][t] : 0.f;
+      mj[h][t] = L1 == 1 ? kM1Terms.j[q][t] : L1 == 2 ? kM2Terms.j[q][t] : 0;
+      mv[h][t] = L1 == 1 ? kM1Terms.v[q][t] : L1 == 2 ? kM2Terms.v[q][t] : 0.f;
     }
   }
   // The TC h3 rows of a step's tile (hi and lo planes) are fetched once per block,
@@ -728,7 +746,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 #pragma unroll
       for (int i = 0; i < NX; ++i) S.x[b][i] = xs[NC * i];
       const int64_t e = min<int64_t>(beg + EPW * j + b, elast);
-      if constexpr (L1 == 1) {
+      if constexpr (L1 >= 1) {
         S.t[b][0] = Y[e * 16 + (l & 15)];
       } else {
 #pragma unroll
@@ -774,7 +792,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
     }
     store_h(j + 1, Snext);  // its last readers (step j - 1) are past the previous barrier
     __syncthreads();
-    if constexpr (L1 == 1) {  // M1 rows from the Y rows: the terms and order of k_edge_fwd
+    if constexpr (L1 >= 1) {  // M1 / M2 rows from the Y rows: the terms and order of k_edge_fwd
 #pragma unroll
       for (int b = 0; b < EPW; ++b)
         if (l < 16) yb[16 * b + l] = S.t[b][0];
@@ -816,7 +834,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 #pragma unroll
         for (int s = 0; s < T::NSLOT; ++s)
           if (T::l1(s) == L1) in.w[s] = wv_s[s];
-        const float* trow_t = tb + b * TSP;  // Y (l1 = 0) or M1 (l1 = 1)
+        const float* trow_t = tb + b * TSP;  // Y (l1 = 0), M1 (l1 = 1) or M2 (l1 = 2)
         tp_edge_fwd<LIN, L1>(acc, in, trow_t, trow_t, trow_t);
       }
       float* we = (valid ? w + (int64_t)e * a.W : sink) + c0 + u;
@@ -858,19 +876,25 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 // of rounded h3 and weights have zero lo planes, so w is the float32 product, then rounded)
 template <int LIN, int RND>
 __global__ void __launch_bounds__(64 * XW, 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_PTRS) {
-  static_assert(LIN <= 2, "three input blocks are not fused");
   constexpr int TC = XW * EPW;
   __shared__ __align__(16) float sw[2 * TC * (64 * gmax<LIN>() + 4)];
-  __shared__ __align__(16) float stab[XW * EPW * (LIN == 1 ? 16 : TP3_M1_NE + 16)];  // table rows + Y rows
+  __shared__ __align__(16) float stab[XW * EPW * (tpx_tab_pad(LIN - 1) + 16)];  // table rows + Y rows
   __shared__ __align__(16) _Float16 hbuf[2 * 2 * TC * 72];  // [step][hi, lo][tile column][64 + pad]
   __shared__ float hiv[2 * TC];
   if constexpr (LIN == 1) {
     tpx_fwd<1, 0, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
-  } else {
+  } else if constexpr (LIN == 2) {
     if (blockIdx.z == 0)
       tpx_fwd<2, 1, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
     else
       tpx_fwd<2, 0, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
+  } else {
+    if (blockIdx.z == 0)
+      tpx_fwd<3, 2, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
+    else if (blockIdx.z == 1)
+      tpx_fwd<3, 1, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
+    else
+      tpx_fwd<3, 0, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
   }
 }
 
@@ -917,14 +941,25 @@ __device__ constexpr unsigned rmask(int col, int d, int i) {
   return m;
 }
 
+// f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>): loop indices that are
+// constants by construction (a register array indexed by them never needs memory, whatever
+// the unroller decides for a long loop)
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_seq(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
 template <int LIN>
 __device__ __forceinline__ void vjp_l1_table(const float* g, float (*R)[3][16]) {
   using T = TPT<LIN>;
   using GR = GrpT<LIN, 1>;
-#pragma unroll
-  for (int s = 0; s < T::NSLOT; ++s) {
-    if (T::l1(s) != 1) continue;
-    const int ls = GR::local(s), a0 = T::acc(s), d = 2 * T::l3(s) + 1, c0 = T::col(s);
+  static_for<GR::G>([&](auto lsc) {
+    constexpr int ls = decltype(lsc)::value, s = GR::slot_of(ls);
+    constexpr int a0 = T::acc(s), d = 2 * T::l3(s) + 1, c0 = T::col(s);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
 #pragma unroll
@@ -936,7 +971,7 @@ __device__ __forceinline__ void vjp_l1_table(const float* g, float (*R)[3][16]) 
         for (int x = m1s(q); x < m1s(q + 1); ++x) R[ls][i][m1j(x)] = fmaf(g[a0 + k], m1v(x), R[ls][i][m1j(x)]);
       }
     }
-  }
+  });
 }
 
 template <int LIN, bool GX>
@@ -944,10 +979,9 @@ __device__ __forceinline__ void tp_edge_vjp_l1(const float (*R)[3][16], const Ed
                                                const float* Ye, float* gx1, float* gYu) {
   using T = TPT<LIN>;
   using GR = GrpT<LIN, 1>;
-#pragma unroll
-  for (int s = 0; s < T::NSLOT; ++s) {
-    if (T::l1(s) != 1) continue;
-    const int ls = GR::local(s), d = 2 * T::l3(s) + 1, c0 = T::col(s);
+  static_for<GR::G>([&](auto lsc) {
+    constexpr int ls = decltype(lsc)::value, s = GR::slot_of(ls);
+    constexpr int d = 2 * T::l3(s) + 1, c0 = T::col(s);
     const float ww = in.w[s];
     float gws = 0.f;
 #pragma unroll
@@ -965,7 +999,7 @@ __device__ __forceinline__ void tp_edge_vjp_l1(const float (*R)[3][16], const Ed
         if ((mask >> j) & 1u) gYu[j] = fmaf(z, R[ls][i][j], gYu[j]);
     }
     gw_out[s] = gws;
-  }
+  });
 }
 
 // Largest value of a nonnegative x over the wave (DPP row scan, then the two
@@ -999,12 +1033,26 @@ struct TpxBwdDims {
 
 template <int LIN, int L1, bool GX>
 __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, _Float16* sg, float* sinv,
-                                        float* sy, float* sp) {
+                                        float* sy, float* sp, float* sm2) {
   using T = TPT<LIN>;
   using GR = GrpT<LIN, L1>;
   constexpr int G = GR::G, RS = 64 * G + 8;  // fp16 row stride: 16-byte reads of 8 lanes hit distinct banks
   constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, NX = 2 * L1 + 1;
-  static_assert(L1 <= 1, "input blocks l1 = 0, 1");
+  static_assert(L1 <= 2, "input blocks l1 = 0, 1, 2");
+  // l1 = 2: the CG terms (at most two) of the M2 entries q = l + 64 h this lane builds from the
+  // step's Y rows (into sm2: this wave's two rows)
+  constexpr int M2H = L1 == 2 ? (TP3_M2_NE + 63) / 64 : 1, M2S = tpx_tab_pad(2);
+  int m2j_[M2H][2];
+  float m2v_[M2H][2];
+#pragma unroll
+  for (int h = 0; h < M2H; ++h) {
+    const int q = min((int)(threadIdx.x & 63) + 64 * h, TP3_M2_NE - 1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      m2j_[h][t] = L1 == 2 ? kM2Terms.j[q][t] : 0;
+      m2v_[h][t] = L1 == 2 ? kM2Terms.v[q][t] : 0.f;
+    }
+  }
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, r = l & 15, g = l >> 4, u = l;
   const int c0 = 64 * blockIdx.y, nb0 = XW * blockIdx.x, p = 2 * blockIdx.z + blockIdx.y;
@@ -1092,6 +1140,17 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
     float* tinv = sinv + (j & 1) * 16;
     if (l < 32) ys[l] = yn[l >> 4];
     wave_sync();
+    float* m2w = sm2 + wv * 2 * M2S;  // l1 = 2: this wave's two M2 rows
+    if constexpr (L1 == 2) {  // the terms and order of k_edge_fwd
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int h = 0; h < M2H; ++h)
+          if (l + 64 * h < TP3_M2_NE)
+            m2w[b * M2S + l + 64 * h] =
+                fmaf(ys[16 * b + m2j_[h][1]], m2v_[h][1], fmaf(ys[16 * b + m2j_[h][0]], m2v_[h][0], 0.f));
+      wave_sync();
+    }
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
 #pragma unroll
@@ -1122,6 +1181,7 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
         for (int i = 0; i < NX; ++i) {
           if constexpr (L1 == 0) in.x0 = xv[b][i];
           if constexpr (L1 == 1) in.x1[i] = xv[b][i];
+          if constexpr (L1 == 2) in.x2[i] = xv[b][i];
         }
 #pragma unroll
         for (int s = 0; s < T::NSLOT; ++s)
@@ -1130,7 +1190,7 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
         if constexpr (L1 == 1)
           tp_edge_vjp_l1<LIN, GX>(R1, in, gws, yrow, gx1, gYu);
         else
-          tp_edge_vjp<LIN, GX, L1>(gm, in, gws, yrow, yrow, yrow, gx0, gx1, gx2, gYu);
+          tp_edge_vjp<LIN, GX, L1>(gm, in, gws, yrow, yrow, m2w + b * M2S, gx0, gx1, gx2, gYu);
       }
       {  // split dL/dw for the matrix cores: one scale per edge (over the block's columns)
         float m = 0.f;
@@ -1155,12 +1215,12 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
       if constexpr (GX) {
         float* dst = (valid ? gxe + (int64_t)pss[b] * DIN + NC * L1 * L1 : sink) + c0 + u;
 #pragma unroll
-        for (int i = 0; i < NX; ++i) dst[NC * i] = L1 == 0 ? gx0 : gx1[i];
+        for (int i = 0; i < NX; ++i) dst[NC * i] = L1 == 0 ? gx0 : L1 == 1 ? gx1[i] : gx2[i];
       }
       const float ysum = wave_sum16(gYu);
       *gy_addr(e, valid) = a.accumulate_gY ? gyc[b] + ysum : ysum;
     }
-    __syncthreads();  // also: this step's Y-row reads are done before the next step's store
+    __syncthreads();  // also: this step's Y- and M2-row reads are done before the next step's stores
     // dL/dh3 of this tile (half kh of the k steps), then the previous tile's flush
     f4v acc = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1196,18 +1256,25 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
 
 template <int LIN, bool GX>
 __global__ void __launch_bounds__(64 * XW, 2) k_tpx_bwd(TpxBwdDims a, MACE_TPX_BWD_PTRS) {
-  static_assert(LIN <= 2, "three input blocks are not fused");
   __shared__ __align__(16) _Float16 sg[2 * 2 * 16 * (64 * gmax<LIN>() + 8)];  // [step][hi, lo][edge][RS]
   __shared__ float sinv[2 * 16];
   __shared__ __align__(16) float sy[XW * 32];      // [wave][edge][16]: the step's Y rows
   __shared__ __align__(16) float sp[3 * 4 * 256];  // [two steps + the lower half's slot][q tile][lane][4]
+  __shared__ __align__(16) float sm2[LIN == 3 ? XW * 2 * tpx_tab_pad(2) : 4];  // [wave][edge][M2 row]
   if constexpr (LIN == 1) {
-    tpx_bwd<1, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp);
+    tpx_bwd<1, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+  } else if constexpr (LIN == 2) {
+    if (blockIdx.z == 0)
+      tpx_bwd<2, 1, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+    else
+      tpx_bwd<2, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
   } else {
     if (blockIdx.z == 0)
-      tpx_bwd<2, 1, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp);
+      tpx_bwd<3, 2, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+    else if (blockIdx.z == 1)
+      tpx_bwd<3, 1, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
     else
-      tpx_bwd<2, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp);
+      tpx_bwd<3, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
   }
 }
 
@@ -1278,7 +1345,7 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
                     float wscale, const float* up, float* M, float* w, float* sink, int rnd) {
   if (N <= 0) return;
   const TpxDims a{N, W, mts, E, wscale};
-  const dim3 grid((unsigned)((N + XW - 1) / XW), 2, lin == 1 ? 1 : 2);
+  const dim3 grid((unsigned)((N + XW - 1) / XW), 2, (unsigned)lin);  // z: one input block l1 each
   const _Float16* hx = static_cast<const _Float16*>(h3x);
   const _Float16* wt = static_cast<const _Float16*>(W3Tx);
 #define MACE_TPXF(L, R) \
@@ -1292,8 +1359,10 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
     MACE_TPXF(L, RND_NONE);
   if (lin == 1) {
     MACE_TPXF_R(1)
-  } else {
+  } else if (lin == 2) {
     MACE_TPXF_R(2)
+  } else {
+    MACE_TPXF_R(3)
   }
 #undef MACE_TPXF_R
 #undef MACE_TPXF
@@ -1305,7 +1374,7 @@ void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
                     float* gh3p, float* sink) {
   if (N <= 0 || E <= 0) return;  // no edges: no dL/dw, dL/dY, dL/dx rows to write
   const TpxBwdDims a{N, W, mts, E, wscale, accumulate_gY, gyp};
-  const dim3 grid((unsigned)((N + XW - 1) / XW), 2, lin == 1 ? 1 : 2);
+  const dim3 grid((unsigned)((N + XW - 1) / XW), 2, (unsigned)lin);
   const _Float16* wx = static_cast<const _Float16*>(W3x);
 #define MACE_TPXB(L, GXV)                                                                                        \
   MACE_LAUNCH((k_tpx_bwd<L, GXV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \
@@ -1313,8 +1382,10 @@ void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
   const bool gx = gxe != nullptr;
   if (lin == 1) {
     if (gx) MACE_TPXB(1, true); else MACE_TPXB(1, false);
-  } else {
+  } else if (lin == 2) {
     if (gx) MACE_TPXB(2, true); else MACE_TPXB(2, false);
+  } else {
+    if (gx) MACE_TPXB(3, true); else MACE_TPXB(3, false);
   }
 #undef MACE_TPXB
 }
