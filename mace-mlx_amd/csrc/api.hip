@@ -948,16 +948,20 @@ void build_nl(mace_ctx* c, const double* pos_host) {
   c->rowptr.ensure((size_t)N + 1);
   for (int g = 0; g < G; ++g)
     launch_nl_bin(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], c->pos.p, ps[g], bin_off[g],
-                  c->nl_wpos.p, c->nl_img.p, c->nl_bin.p);
-  launch_fill_iota(c->stream, N, c->nl_iota.p);
+                  c->nl_wpos.p, c->nl_img.p, c->nl_bin.p, c->nl_iota.p);
+  // atoms sorted by bin (stable: within a bin by index), then each bin's first position
   cub_sort_pairs(c, c->nl_bin.p, c->nl_bin_sorted.p, c->nl_iota.p, c->nl_atoms.p, N, nbins);
-  build_rowptr(c, c->nl_bin.p, N, nbins, c->nl_bin_start.p);
+  launch_key_starts(c->stream, N, c->nl_bin_sorted.p, nbins, c->nl_bin_start.p);
   c->nl_counts.ensure((size_t)N + 1);
-  HIPCHK(hipMemsetAsync(c->nl_counts.p, 0, ((size_t)N + 1) * sizeof(int), c->stream));
+  c->nl_missing.ensure(1);
+  if (N == 0) {  // no count pass to clear the scan's last slot and the reverse-edge counter
+    HIPCHK(hipMemsetAsync(c->nl_counts.p, 0, sizeof(int), c->stream));
+    HIPCHK(hipMemsetAsync(c->nl_missing.p, 0, sizeof(int), c->stream));
+  }
   for (int g = 0; g < G; ++g)
     launch_nl_count(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], ps[g], bin_off[g], c->nl_wpos.p,
-                    c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, c->nl_counts.p);
-  // reuse nl_iota as scan output scratch? rowptr directly:
+                    c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, c->nl_counts.p, c->nl_counts.p + N,
+                    c->nl_missing.p);
   cub_exclusive_sum(c, c->nl_counts.p, c->rowptr.p, (int64_t)N + 1);
   int Eh = 0;
   HIPCHK(hipMemcpyAsync(&Eh, c->rowptr.p + N, sizeof(int), hipMemcpyDeviceToHost, c->stream));
@@ -973,8 +977,6 @@ void build_nl(mace_ctx* c, const double* pos_host) {
   HIPCHK(hipMemcpyAsync(c->rowptr_s.p, c->rowptr.p, ((size_t)N + 1) * sizeof(int), hipMemcpyDeviceToDevice,
                         c->stream));
   if (!c->nl_missing_h) HIPCHK(hipHostMalloc((void**)&c->nl_missing_h, sizeof(int), hipHostMallocDefault));
-  c->nl_missing.ensure(1);
-  HIPCHK(hipMemsetAsync(c->nl_missing.p, 0, sizeof(int), c->stream));
   launch_nl_rev(c->stream, c->E, c->rowptr.p, c->sender.p, c->receiver.p, c->shifts.p, c->perm_s.p, c->pos_s.p,
                 c->nl_missing.p);
   HIPCHK(hipMemcpyAsync(c->nl_missing_h, c->nl_missing.p, sizeof(int), hipMemcpyDeviceToHost, c->stream));

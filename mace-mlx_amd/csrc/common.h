@@ -353,11 +353,15 @@ struct NLParams {
   int range[3];
   double cutoff2;
 };
-// atoms [i0, i0 + n): one structure, its bins numbered from bin_off
+// atoms [i0, i0 + n): one structure, its bins numbered from bin_off; iota[i] = i for the sort
 void launch_nl_bin(hipStream_t st, int i0, int n, const double* pos, const NLParams& p, int bin_off,
-                   double* wpos, int* img, int* bin);
+                   double* wpos, int* img, int* bin, int* iota);
+// start[b] (b = 0 .. nbins) = first position of key b in the sorted keys[0 .. n)
+void launch_key_starts(hipStream_t st, int n, const int* keys, int nbins, int* start);
+// counts[j] for the structure's atoms; also sets *tail = 0 and *missing = 0
 void launch_nl_count(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
-                     const int* bin, const int* bin_start, const int* bin_atoms, int* counts);
+                     const int* bin, const int* bin_start, const int* bin_atoms, int* counts, int* tail,
+                     int* missing);
 void launch_nl_fill(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
                     const int* img, const int* bin, const int* bin_start, const int* bin_atoms,
                     const int* rowptr, int* sender, int* receiver, int* shifts);

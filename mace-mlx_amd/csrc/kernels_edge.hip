@@ -2,6 +2,8 @@
 // ZBL), its VJP, the radial MLP forward/backward, and the device neighbour list.
 #include <hip/hip_runtime.h>
 
+#include <climits>
+
 #include "common.h"
 
 namespace mace {
@@ -306,10 +308,13 @@ __device__ __forceinline__ int floordiv(int a, int b) {
 
 // Atoms [i0, i0 + n) form one structure (a batch is a union of structures, each in its own
 // cell); its bins are numbered from bin_off so that all structures share one sorted bin array.
+// iota[i] = i: the values of the sort by bin.
 __global__ void k_nl_bin(int i0, int n, const double* __restrict__ pos, NLParams p, int bin_off,
-                         double* __restrict__ wpos, int* __restrict__ img, int* __restrict__ bin) {
+                         double* __restrict__ wpos, int* __restrict__ img, int* __restrict__ bin,
+                         int* __restrict__ iota) {
   if ((int)(blockIdx.x * blockDim.x + threadIdx.x) >= n) return;
   const int i = i0 + blockIdx.x * blockDim.x + threadIdx.x;
+  iota[i] = i;
   const double d0 = pos[3 * i] - p.origin[0], d1 = pos[3 * i + 1] - p.origin[1],
                d2 = pos[3 * i + 2] - p.origin[2];
   double f[3], w[3];
@@ -445,11 +450,15 @@ __device__ __forceinline__ int nl_visit(int j, const NLParams& p, int bin_off, c
 }
 
 // four receiver atoms per 256-thread block, one wave each
+// also clears *tail (the count slot past the last atom, so that the exclusive scan ends on the
+// total) and *missing (the reverse-edge check's counter)
 __global__ void __launch_bounds__(256) k_nl_count(int i0, int n, NLParams p, int bin_off,
                                                   const double* __restrict__ wpos,
                                                   const int* __restrict__ bin, const int* __restrict__ bin_start,
-                                                  const int* __restrict__ bin_atoms, int* __restrict__ counts) {
+                                                  const int* __restrict__ bin_atoms, int* __restrict__ counts,
+                                                  int* __restrict__ tail, int* __restrict__ missing) {
   __shared__ NLWaveScratch sc[4];
+  if (blockIdx.x == 0 && threadIdx.x == 0) *tail = 0, *missing = 0;
   if ((int)(blockIdx.x * 4 + (threadIdx.x >> 6)) >= n) return;
   const int j = i0 + blockIdx.x * 4 + (threadIdx.x >> 6);
   const int c = nl_visit<false>(j, p, bin_off, wpos, nullptr, bin, bin_start, bin_atoms, 0, nullptr, nullptr,
@@ -476,26 +485,50 @@ __global__ void __launch_bounds__(256) k_nl_fill(int i0, int n, NLParams p, int 
 // both the sender-side permutation (edges sent by a = reverses of the edges a receives, in the
 // order of a's row) and its inverse.  An edge without a reverse (a list that is not symmetric)
 // maps to itself and is counted in *missing.
+// Sixteen lanes per edge: lane k of the group compares entries k, k + 16, ... of the row (all
+// loads independent, a few per lane), and the group takes the smallest matching position.
+constexpr int kRevLanes = 16;
 __global__ void __launch_bounds__(256) k_nl_rev(int64_t E, const int* __restrict__ rowptr,
                                                 const int* __restrict__ sender, const int* __restrict__ receiver,
                                                 const int* __restrict__ shifts, int* __restrict__ perm_s,
                                                 int* __restrict__ pos_s, int* __restrict__ missing) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= E) return;
-  const int i = sender[e], j = receiver[e];
-  const int s0 = -shifts[3 * e], s1 = -shifts[3 * e + 1], s2 = -shifts[3 * e + 2];
-  int found = -1;
-  for (int f = rowptr[i]; f < rowptr[i + 1]; ++f)
-    if (sender[f] == j && shifts[3 * f] == s0 && shifts[3 * f + 1] == s1 && shifts[3 * f + 2] == s2) {
-      found = f;
-      break;
-    }
-  if (found < 0) {
-    atomicAdd(missing, 1);
-    found = (int)e;
+  const int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kRevLanes;
+  const int k = threadIdx.x % kRevLanes;
+  const bool live = e < E;  // a group's lanes share e (256 is a multiple of the group size)
+  int j = 0, s0 = 0, s1 = 0, s2 = 0, beg = 0, end = 0;
+  if (live) {
+    const int i = sender[e];
+    j = receiver[e];
+    s0 = -shifts[3 * e], s1 = -shifts[3 * e + 1], s2 = -shifts[3 * e + 2];
+    beg = rowptr[i], end = rowptr[i + 1];
   }
-  perm_s[e] = found;
-  pos_s[e] = found;
+  int found = INT_MAX;
+  for (int f = beg + k; f < end; f += kRevLanes)
+    if (sender[f] == j && shifts[3 * f] == s0 && shifts[3 * f + 1] == s1 && shifts[3 * f + 2] == s2)
+      found = min(found, f);
+#pragma unroll
+  for (int off = kRevLanes / 2; off > 0; off >>= 1) found = min(found, __shfl_xor(found, off, kRevLanes));
+  if (live && k == 0) {
+    if (found == INT_MAX) {
+      atomicAdd(missing, 1);
+      found = (int)e;
+    }
+    perm_s[e] = found;
+    pos_s[e] = found;
+  }
+}
+
+// start[b] = first position of key b in the sorted keys[0 .. n) (b = 0 .. nbins): the CSR of a
+// sorted key array by binary search, with no counts to clear or scan
+__global__ void k_key_starts(int n, const int* __restrict__ keys, int nbins, int* __restrict__ start) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b > nbins) return;
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (keys[mid] < b) lo = mid + 1; else hi = mid;
+  }
+  start[b] = lo;
 }
 
 __global__ void k_iota(int n, int* out) {
@@ -555,16 +588,21 @@ void launch_density_edge_bwd(hipStream_t st, int64_t E, const int* receiver, con
 }
 
 void launch_nl_bin(hipStream_t st, int i0, int n, const double* pos, const NLParams& p, int bin_off, double* wpos,
-                   int* img, int* bin) {
+                   int* img, int* bin, int* iota) {
   if (n <= 0) return;
-  MACE_LAUNCH(k_nl_bin, dim3(nblk(n, 256)), dim3(256), 0, st, i0, n, pos, p, bin_off, wpos, img, bin);
+  MACE_LAUNCH(k_nl_bin, dim3(nblk(n, 256)), dim3(256), 0, st, i0, n, pos, p, bin_off, wpos, img, bin, iota);
+}
+
+void launch_key_starts(hipStream_t st, int n, const int* keys, int nbins, int* start) {
+  MACE_LAUNCH(k_key_starts, dim3(nblk((int64_t)nbins + 1, 256)), dim3(256), 0, st, n, keys, nbins, start);
 }
 
 void launch_nl_count(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
-                     const int* bin, const int* bin_start, const int* bin_atoms, int* counts) {
+                     const int* bin, const int* bin_start, const int* bin_atoms, int* counts, int* tail,
+                     int* missing) {
   if (n <= 0) return;
   MACE_LAUNCH(k_nl_count, dim3(nblk(n, 4)), dim3(256), 0, st, i0, n, p, bin_off, wpos, bin, bin_start,
-                     bin_atoms, counts);
+                     bin_atoms, counts, tail, missing);
 }
 
 void launch_nl_fill(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
@@ -588,8 +626,8 @@ void launch_count_keys(hipStream_t st, int64_t E, const int* keys, int* counts) 
 void launch_nl_rev(hipStream_t st, int64_t E, const int* rowptr, const int* sender, const int* receiver,
                    const int* shifts, int* perm_s, int* pos_s, int* missing) {
   if (E <= 0) return;
-  MACE_LAUNCH(k_nl_rev, dim3(nblk(E, 256)), dim3(256), 0, st, E, rowptr, sender, receiver, shifts, perm_s, pos_s,
-              missing);
+  MACE_LAUNCH(k_nl_rev, dim3(nblk(E * kRevLanes, 256)), dim3(256), 0, st, E, rowptr, sender, receiver, shifts,
+              perm_s, pos_s, missing);
 }
 
 }  // namespace mace
