@@ -153,6 +153,9 @@ struct mace_ctx {
   DBuf<int> zero_species;
   DBuf<int> nl_missing;       // edges of the last list build without a reverse edge (device count)
   int* nl_missing_h = nullptr;  // pinned host copy, read after the next synchronisation
+  int* e_pinned = nullptr;      // the list build's edge count, read back through pinned memory
+  bool nl_check_pending = false;  // a list build whose reverse-edge count is not yet read
+  bool srow_shared = false;       // sender CSR row pointers = rowptr (symmetric device-built list)
   // system
   int N = 0;
   std::vector<int> species_h;
@@ -217,6 +220,7 @@ struct mace_ctx {
   };
   std::map<const float*, SplitW> wsplit;  // split copies of the grouped-GEMM weights, by device pointer
   StepGraph g_fwd, g_bwd;
+  hipStream_t cap_stream = nullptr;  // step graphs are captured here (nothing runs on it)
   // per-launch-site profiling
   bool profiling = false;
   std::vector<hipEvent_t> ev_pool;
@@ -367,6 +371,7 @@ std::vector<float> transpose(const std::vector<float>& a, int rows, int cols, in
 }
 
 void invalidate_graphs(mace_ctx* c);
+void invalidate_node_state(mace_ctx* c);
 
 void free_layers(mace_ctx* c) {
   for (auto& L : c->layers) {
@@ -489,7 +494,7 @@ void build_layer_nonlin(mace_ctx* c, Layer& L, int l) {
 }
 
 void build_model(mace_ctx* c) {
-  invalidate_graphs(c);
+  invalidate_node_state(c);
   const auto& d = c->dims;
   const int C = NC;
   if (d.num_channels != NC) fail(MACE_ERR_UNSUPPORTED, "num_channels=%d (compiled for %d)", d.num_channels, NC);
@@ -651,7 +656,7 @@ void build_model(mace_ctx* c) {
 // buffers
 // ---------------------------------------------------------------------------
 void ensure_node_buffers(mace_ctx* c) {
-  invalidate_graphs(c);
+  invalidate_node_state(c);
   const int N = std::max(c->N, 1);
   const int L = (int)c->layers.size();
   c->h.resize(L + 1);
@@ -824,6 +829,7 @@ void build_sender_csr(mace_ctx* c) {
                        c->pos_s.p);
   }
   build_rowptr(c, c->sender.p, E, c->N, c->rowptr_s.p);
+  c->srow_shared = false;
 }
 
 double plane_spacing(const double* cell, int k) {
@@ -963,23 +969,24 @@ void build_nl(mace_ctx* c, const double* pos_host) {
                     c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, c->nl_counts.p, c->nl_counts.p + N,
                     c->nl_missing.p);
   cub_exclusive_sum(c, c->nl_counts.p, c->rowptr.p, (int64_t)N + 1);
-  int Eh = 0;
-  HIPCHK(hipMemcpyAsync(&Eh, c->rowptr.p + N, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+  // the edge count sizes the per-edge arrays and the launches: read back (pinned memory: a copy
+  // into pageable memory costs more than this whole wait)
+  if (!c->e_pinned) HIPCHK(hipHostMalloc((void**)&c->e_pinned, sizeof(int), hipHostMallocDefault));
+  HIPCHK(hipMemcpyAsync(c->e_pinned, c->rowptr.p + N, sizeof(int), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(hipStreamSynchronize(c->stream));
-  c->E = Eh;
+  c->E = *c->e_pinned;
   ensure_edge_index(c, c->E);
   for (int g = 0; g < G; ++g)
     launch_nl_fill(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], ps[g], bin_off[g], c->nl_wpos.p,
                    c->nl_img.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, c->rowptr.p, c->sender.p,
                    c->receiver.p, c->shifts.p);
-  // sender-side CSR of the (symmetric) list without a sort: rowptr_s = rowptr, perm_s = pos_s = rev
-  c->rowptr_s.ensure((size_t)N + 1);
-  HIPCHK(hipMemcpyAsync(c->rowptr_s.p, c->rowptr.p, ((size_t)N + 1) * sizeof(int), hipMemcpyDeviceToDevice,
-                        c->stream));
-  if (!c->nl_missing_h) HIPCHK(hipHostMalloc((void**)&c->nl_missing_h, sizeof(int), hipHostMallocDefault));
+  // sender-side CSR of the (symmetric) list without a sort: its row pointers are rowptr's
+  // (srow), perm_s = pos_s = the reverse of each edge; the reverse-edge count is read at the
+  // next synchronisation (check_nl_missing)
+  c->srow_shared = true;
+  c->nl_check_pending = true;
   launch_nl_rev(c->stream, c->E, c->rowptr.p, c->sender.p, c->receiver.p, c->shifts.p, c->perm_s.p, c->pos_s.p,
                 c->nl_missing.p);
-  HIPCHK(hipMemcpyAsync(c->nl_missing_h, c->nl_missing.p, sizeof(int), hipMemcpyDeviceToHost, c->stream));
   ensure_edge_buffers(c, c->E);
   // positions at this build, for the host-side skin check of mace_step (unknown when the build
   // took device positions of a fully periodic system: the next mace_step then rebuilds)
@@ -990,15 +997,27 @@ void build_nl(mace_ctx* c, const double* pos_host) {
   c->nl_valid = true;
 }
 
-// after a synchronisation: a list build whose edges lacked reverses is an internal error
+// Reverse-edge count of the last list build into pinned memory (queued before a
+// synchronisation, when a build has not been checked yet)
+void queue_nl_missing(mace_ctx* c) {
+  if (!c->nl_check_pending) return;
+  if (!c->nl_missing_h) HIPCHK(hipHostMalloc((void**)&c->nl_missing_h, sizeof(int), hipHostMallocDefault));
+  HIPCHK(hipMemcpyAsync(c->nl_missing_h, c->nl_missing.p, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+}
+
+// after that synchronisation: a list build whose edges lacked reverses is an internal error
 void check_nl_missing(mace_ctx* c) {
-  if (c->nl_missing_h && *c->nl_missing_h > 0) {
+  if (!c->nl_check_pending) return;
+  c->nl_check_pending = false;
+  if (*c->nl_missing_h > 0) {
     const int m = *c->nl_missing_h;
-    *c->nl_missing_h = 0;
     c->nl_valid = false;
     fail(MACE_ERR_STATE, "neighbour list not symmetric: %d edges without a reverse", m);
   }
 }
+
+// row pointers of the sender-side CSR
+const int* srow(const mace_ctx* c) { return c->srow_shared ? c->rowptr.p : c->rowptr_s.p; }
 
 __global__ void k_gather_edges(int64_t E, const int* perm, const int* si, const int* ri, const int* ss, int* so,
                                int* ro, int* sso) {
@@ -1145,7 +1164,13 @@ void invalidate_graphs(mace_ctx* c) {
     if (g->exec) (void)hipGraphExecDestroy(g->exec);
     *g = mace_ctx::StepGraph{};
   }
-  c->embed_valid = false;  // every model / system / buffer change comes through here
+}
+
+// ... and the species features (model, species or node buffers changed; an edge-list
+// change leaves them valid)
+void invalidate_node_state(mace_ctx* c) {
+  invalidate_graphs(c);
+  c->embed_valid = false;
 }
 
 // First-layer node features h0 and the first linear_up output: functions of the species
@@ -1159,38 +1184,51 @@ void ensure_embed(mace_ctx* c) {
   c->embed_valid = true;
 }
 
-// Run body() (a sequence of launches on c->stream) through a graph captured
-// for the binding (a, b, flag), capturing it first if needed; eager when
-// graphs are off or per-launch profiling is on.
+bool graphs_active(const mace_ctx* c) { return c->use_graphs && !c->profiling; }
+
+// Capture body() (a sequence of launches on c->stream) into g for the binding (a, b, flag),
+// without running it: c->stream is the capture stream meanwhile, so this can happen while the
+// engine stream still executes earlier work.
+template <class F>
+void capture_graph(mace_ctx* c, mace_ctx::StepGraph& g, const void* a, const void* b, int flag, F&& body) {
+  if (g.exec) (void)hipGraphExecDestroy(g.exec);
+  g = mace_ctx::StepGraph{};
+  struct Swap {  // the engine stream is back in place on every exit
+    mace_ctx* c;
+    hipStream_t run;
+    ~Swap() { c->stream = run; }
+  } swap{c, c->stream};
+  c->stream = c->cap_stream;
+  hipGraph_t graph = nullptr;
+  HIPCHK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+  try {
+    body();
+  } catch (...) {
+    (void)hipStreamEndCapture(c->stream, &graph);
+    if (graph) (void)hipGraphDestroy(graph);
+    throw;
+  }
+  HIPCHK(hipStreamEndCapture(c->stream, &graph));
+  const hipError_t e = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (e != hipSuccess) {
+    g.exec = nullptr;
+    fail(MACE_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+  }
+  g.a = a;
+  g.b = b;
+  g.flag = flag;
+}
+
+// Run body() through the graph captured for the binding (a, b, flag), capturing it first if
+// needed; eager when graphs are off or per-launch profiling is on.
 template <class F>
 void run_captured(mace_ctx* c, mace_ctx::StepGraph& g, const void* a, const void* b, int flag, F&& body) {
-  if (!c->use_graphs || c->profiling) {
+  if (!graphs_active(c)) {
     body();
     return;
   }
-  if (!g.exec || g.a != a || g.b != b || g.flag != flag) {
-    if (g.exec) (void)hipGraphExecDestroy(g.exec);
-    g = mace_ctx::StepGraph{};
-    hipGraph_t graph = nullptr;
-    HIPCHK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    try {
-      body();
-    } catch (...) {
-      (void)hipStreamEndCapture(c->stream, &graph);
-      if (graph) (void)hipGraphDestroy(graph);
-      throw;
-    }
-    HIPCHK(hipStreamEndCapture(c->stream, &graph));
-    const hipError_t e = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(graph);
-    if (e != hipSuccess) {
-      g.exec = nullptr;
-      fail(MACE_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
-    }
-    g.a = a;
-    g.b = b;
-    g.flag = flag;
-  }
+  if (!g.exec || g.a != a || g.b != b || g.flag != flag) capture_graph(c, g, a, b, flag, body);
   HIPCHK(hipGraphLaunch(g.exec, c->stream));
 }
 
@@ -1353,7 +1391,7 @@ void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int fi
   }
   if (l > 0) {
     Site s(c, lname("tp_gather", l));
-    launch_tp_gather_gx(st, Ly.ledge, N, c->rowptr_s.p, c->gxe.p, c->gup.p);
+    launch_tp_gather_gx(st, Ly.ledge, N, srow(c), c->gxe.p, c->gup.p);
   }
   {  // G = gw W3^T (into h3), gwb = gw . b3
     Site s(c, lname("mlp_gh3", l));
@@ -1627,7 +1665,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
     }
     if (l > 0) {
       Site s(c, lname("tp_gather", l));
-      launch_tp_gather_gx(st, Ly.lin, N, c->rowptr_s.p, c->gxe.p, c->gup.p);
+      launch_tp_gather_gx(st, Ly.lin, N, srow(c), c->gxe.p, c->gup.p);
     }
     if (!fused) {
       Site s(c, lname("mlp_gh3", l));
@@ -1689,7 +1727,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
   }
   {
     Site s(c, "forces");
-    launch_forces(st, N, c->rowptr.p, c->rowptr_s.p, c->perm_s.p, c->gv.p, out + 10,
+    launch_forces(st, N, c->rowptr.p, srow(c), c->perm_s.p, c->gv.p, out + 10,
                   (stress && E > 0) ? nullptr : out + 1, e_part, out);
   }
   if (stress && E > 0) {
@@ -1724,6 +1762,7 @@ int mace_create(int32_t device, mace_ctx** out) {
     // stream, and the synchronous copies of this library), so positions written there
     // before mace_step_device are seen by the step without an explicit wait.
     HIPCHK(hipStreamCreateWithFlags(&c->stream, hipStreamDefault));
+    HIPCHK(hipStreamCreateWithFlags(&c->cap_stream, hipStreamNonBlocking));
     for (auto& e : c->ev) HIPCHK(hipEventCreate(&e));
   });
   if (rc != MACE_OK) {
@@ -1736,7 +1775,7 @@ int mace_create(int32_t device, mace_ctx** out) {
 }
 
 static void free_all(mace_ctx* c) {
-  invalidate_graphs(c);
+  invalidate_node_state(c);
   free_layers(c);
   for (auto& b : c->h) b.release();
   c->h3h.release();
@@ -1766,11 +1805,14 @@ static void free_all(mace_ctx* c) {
   if (c->ne_pinned) (void)hipHostFree(c->ne_pinned);
   if (c->pos_pinned) (void)hipHostFree(c->pos_pinned);
   if (c->nl_missing_h) (void)hipHostFree(c->nl_missing_h);
+  if (c->e_pinned) (void)hipHostFree(c->e_pinned);
+  c->e_pinned = nullptr;
   c->out_pinned = nullptr;
   c->ne_pinned = nullptr;
   c->pos_pinned = nullptr;
   c->nl_missing_h = nullptr;
   c->nl_missing.release();
+  c->nl_check_pending = false;
 }
 
 void mace_destroy(mace_ctx* c) {
@@ -1782,6 +1824,7 @@ void mace_destroy(mace_ctx* c) {
     if (e) (void)hipEventDestroy(e);
   for (auto& e : c->ev_pool) (void)hipEventDestroy(e);
   if (c->stream) (void)hipStreamDestroy(c->stream);
+  if (c->cap_stream) (void)hipStreamDestroy(c->cap_stream);
   delete c;
 }
 
@@ -1986,15 +2029,24 @@ int mace_step(mace_ctx* c, const double* positions, uint32_t flags, double* ener
     if (c->last_nl) build_nl(c, positions);
     HIPCHK(hipEventRecord(c->ev[1], st));
     ensure_embed(c);
-    run_captured(c, c->g_fwd, c->pos.p, c->out.p, 0, [&] { forward(c, c->pos.p, c->out.p, c->e_part.p); });
+    // a step on a freshly built list runs eagerly; the graphs for the next steps are captured
+    // below, while the GPU executes it
+    const bool ahead = c->last_nl && graphs_active(c);
+    auto fwd = [&] { forward(c, c->pos.p, c->out.p, c->e_part.p); };
+    auto bwd = [&] { backward(c, stress, c->out.p, c->e_part.p, c->vir_part.p); };
+    if (ahead) fwd(); else run_captured(c, c->g_fwd, c->pos.p, c->out.p, 0, fwd);
     HIPCHK(hipEventRecord(c->ev[2], st));
-    run_captured(c, c->g_bwd, c->out.p, nullptr, stress,
-                 [&] { backward(c, stress, c->out.p, c->e_part.p, c->vir_part.p); });
+    if (ahead) bwd(); else run_captured(c, c->g_bwd, c->out.p, nullptr, stress, bwd);
     HIPCHK(hipEventRecord(c->ev[3], st));
     HIPCHK(hipMemcpyAsync(c->out_pinned, c->out.p, (10 + 3 * (size_t)N) * sizeof(double), hipMemcpyDeviceToHost, st));
     if (node_energy && N > 0)
       HIPCHK(hipMemcpyAsync(c->ne_pinned, c->node_e.p, (size_t)N * sizeof(float), hipMemcpyDeviceToHost, st));
     HIPCHK(hipEventRecord(c->ev[4], st));
+    queue_nl_missing(c);
+    if (ahead) {
+      capture_graph(c, c->g_fwd, c->pos.p, c->out.p, 0, fwd);
+      capture_graph(c, c->g_bwd, c->out.p, nullptr, stress, bwd);
+    }
     HIPCHK(hipStreamSynchronize(st));
     HIPCHK(hipGetLastError());
     check_nl_missing(c);
@@ -2049,6 +2101,7 @@ int mace_step_device(mace_ctx* c, const double* d_positions, uint32_t flags, dou
     set_device(c);
     const int N = c->N;
     hipStream_t st = c->stream;
+    bool rebuilt = false;
     if ((flags & MACE_STEP_FORCE_NL) || !c->nl_valid) {
       if (N > 0)
         HIPCHK(hipMemcpyAsync(c->pos.p, d_positions, 3 * (size_t)N * sizeof(double), hipMemcpyDeviceToDevice, st));
@@ -2064,12 +2117,22 @@ int mace_step_device(mace_ctx* c, const double* d_positions, uint32_t flags, dou
       }
       c->edges_manual = false;
       build_nl(c, periodic ? nullptr : host.data());
+      rebuilt = true;
     }
     const bool stress = (flags & MACE_STEP_STRESS) != 0;
     ensure_embed(c);
-    run_captured(c, c->g_fwd, d_positions, d_out, 0, [&] { forward(c, d_positions, d_out, c->e_part.p); });
-    run_captured(c, c->g_bwd, d_out, nullptr, stress,
-                 [&] { backward(c, stress, d_out, c->e_part.p, c->vir_part.p); });
+    auto fwd = [&] { forward(c, d_positions, d_out, c->e_part.p); };
+    auto bwd = [&] { backward(c, stress, d_out, c->e_part.p, c->vir_part.p); };
+    if (rebuilt && graphs_active(c)) {
+      // eagerly on the fresh list; the next steps' graphs are captured while the GPU runs it
+      fwd();
+      bwd();
+      capture_graph(c, c->g_fwd, d_positions, d_out, 0, fwd);
+      capture_graph(c, c->g_bwd, d_out, nullptr, stress, bwd);
+    } else {
+      run_captured(c, c->g_fwd, d_positions, d_out, 0, fwd);
+      run_captured(c, c->g_bwd, d_out, nullptr, stress, bwd);
+    }
   });
 }
 
@@ -2135,6 +2198,7 @@ int mace_sync(mace_ctx* c) {
   if (!c) return MACE_ERR_INVALID;
   return guard(c, [&] {
     set_device(c);
+    queue_nl_missing(c);
     HIPCHK(hipStreamSynchronize(c->stream));
     HIPCHK(hipGetLastError());
     check_nl_missing(c);

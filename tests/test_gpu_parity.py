@@ -548,6 +548,17 @@ def test_graph_replay_matches_eager(medium_zbl):
             eng.sync()
             out = out_d.cpu().numpy()
             assert out[0] == f_ref[0] and np.array_equal(out[10:].reshape(N, 3), f_ref[1])
+        # a step that rebuilds the list runs eagerly and captures the next steps' graphs while
+        # the GPU runs it; those graphs, replayed, give the same numbers, as do further rebuilds
+        for k in range(4):
+            out_d.zero_()
+            eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), force_nl=(k % 2 == 0))
+            eng.sync()
+            out = out_d.cpu().numpy()
+            assert out[0] == f_ref[0] and np.array_equal(out[10:].reshape(N, 3), f_ref[1]), k
+        for k in range(3):
+            h = step(far, True) if k != 1 else eng.step(far, force_nl=True)[::2]
+            assert h[0] == f_ref[0] and np.array_equal(h[1], f_ref[1]), k
     finally:
         eng.set_graphs(True)
 
