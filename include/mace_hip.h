@@ -46,6 +46,8 @@ extern "C" {
 #define MACE_STEP_FORCES 1u        /* compute forces (always on in practice)               */
 #define MACE_STEP_STRESS 2u        /* also compute the virial dE/d(eps) (calculators.py:526) */
 #define MACE_STEP_FORCE_NL 4u      /* rebuild the neighbour list regardless of the skin     */
+#define MACE_STEP_SKIN_CHECK 8u    /* mace_step_device: apply the skin criterion on the
+                                      device (calculators.py:266-283)                     */
 
 typedef struct mace_ctx mace_ctx;
 
@@ -161,7 +163,10 @@ int mace_get_edges(mace_ctx* ctx, int64_t capacity, int32_t* sender, int32_t* re
  * forces (n_atoms x 3)].  Work is queued on the context's stream and the call
  * returns without synchronising (mace_sync waits).  The neighbour list is used
  * as cached: the caller guarantees no atom moved more than skin/2 since the last
- * rebuild, or passes MACE_STEP_FORCE_NL (which rebuilds, synchronously).
+ * rebuild, or passes MACE_STEP_FORCE_NL (which rebuilds, synchronously), or passes
+ * MACE_STEP_SKIN_CHECK: the largest displacement since the last rebuild is then reduced
+ * on the device and read back (one synchronisation per step), and the list is rebuilt
+ * when it exceeds skin/2 (skin <= 0: every step), the criterion of mace_step.
  * No host-side counterpart in the reference (its step always round-trips
  * through host arrays, calculators.py:455-476). */
 int mace_step_device(mace_ctx* ctx, const double* d_positions, uint32_t flags, double* d_out);

@@ -154,6 +154,9 @@ struct mace_ctx {
   DBuf<int> nl_missing;       // edges of the last list build without a reverse edge (device count)
   int* nl_missing_h = nullptr;  // pinned host copy, read after the next synchronisation
   int* e_pinned = nullptr;      // the list build's edge count, read back through pinned memory
+  DBuf<double> nl_pos_d;        // positions at the last list build (device skin criterion)
+  DBuf<int> skin_flag;
+  int* skin_pinned = nullptr;
   bool nl_check_pending = false;  // a list build whose reverse-edge count is not yet read
   bool srow_shared = false;       // sender CSR row pointers = rowptr (symmetric device-built list)
   // system
@@ -945,6 +948,7 @@ void build_nl(mace_ctx* c, const double* pos_host) {
   }
   const int nbins = bin_off[G];
   c->nl_wpos.ensure(3 * (size_t)N);
+  c->nl_pos_d.ensure(3 * (size_t)N);
   c->nl_img.ensure(3 * (size_t)N);
   c->nl_bin.ensure(N);
   c->nl_bin_sorted.ensure(N);
@@ -954,7 +958,7 @@ void build_nl(mace_ctx* c, const double* pos_host) {
   c->rowptr.ensure((size_t)N + 1);
   for (int g = 0; g < G; ++g)
     launch_nl_bin(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], c->pos.p, ps[g], bin_off[g],
-                  c->nl_wpos.p, c->nl_img.p, c->nl_bin.p, c->nl_iota.p);
+                  c->nl_wpos.p, c->nl_img.p, c->nl_bin.p, c->nl_iota.p, c->nl_pos_d.p);
   // atoms sorted by bin (stable: within a bin by index), then each bin's first position
   cub_sort_pairs(c, c->nl_bin.p, c->nl_bin_sorted.p, c->nl_iota.p, c->nl_atoms.p, N, nbins);
   launch_key_starts(c->stream, N, c->nl_bin_sorted.p, nbins, c->nl_bin_start.p);
@@ -1014,6 +1018,21 @@ void check_nl_missing(mace_ctx* c) {
     c->nl_valid = false;
     fail(MACE_ERR_STATE, "neighbour list not symmetric: %d edges without a reverse", m);
   }
+}
+
+// The skin criterion of mace_step (calculators.py:266-283) for device-resident positions: the
+// largest displacement since the last list build, reduced on the device and read back.
+bool skin_exceeded_on_device(mace_ctx* c, const double* d_positions) {
+  const int N = c->N;
+  if (c->skin <= 0 || c->nl_pos_d.n < 3 * (size_t)N) return true;
+  if (N == 0) return false;
+  c->skin_flag.ensure(1);
+  if (!c->skin_pinned) HIPCHK(hipHostMalloc((void**)&c->skin_pinned, sizeof(int), hipHostMallocDefault));
+  HIPCHK(hipMemsetAsync(c->skin_flag.p, 0, sizeof(int), c->stream));
+  launch_max_disp(c->stream, N, d_positions, c->nl_pos_d.p, 0.25 * c->skin * c->skin, c->skin_flag.p);
+  HIPCHK(hipMemcpyAsync(c->skin_pinned, c->skin_flag.p, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(hipStreamSynchronize(c->stream));
+  return *c->skin_pinned != 0;
 }
 
 // row pointers of the sender-side CSR
@@ -1806,7 +1825,11 @@ static void free_all(mace_ctx* c) {
   if (c->pos_pinned) (void)hipHostFree(c->pos_pinned);
   if (c->nl_missing_h) (void)hipHostFree(c->nl_missing_h);
   if (c->e_pinned) (void)hipHostFree(c->e_pinned);
+  if (c->skin_pinned) (void)hipHostFree(c->skin_pinned);
   c->e_pinned = nullptr;
+  c->skin_pinned = nullptr;
+  c->nl_pos_d.release();
+  c->skin_flag.release();
   c->out_pinned = nullptr;
   c->ne_pinned = nullptr;
   c->pos_pinned = nullptr;
@@ -2102,7 +2125,9 @@ int mace_step_device(mace_ctx* c, const double* d_positions, uint32_t flags, dou
     const int N = c->N;
     hipStream_t st = c->stream;
     bool rebuilt = false;
-    if ((flags & MACE_STEP_FORCE_NL) || !c->nl_valid) {
+    bool rebuild = (flags & MACE_STEP_FORCE_NL) || !c->nl_valid;
+    if (!rebuild && (flags & MACE_STEP_SKIN_CHECK) && !c->edges_manual) rebuild = skin_exceeded_on_device(c, d_positions);
+    if (rebuild) {
       if (N > 0)
         HIPCHK(hipMemcpyAsync(c->pos.p, d_positions, 3 * (size_t)N * sizeof(double), hipMemcpyDeviceToDevice, st));
       // host positions only for the extents of non-periodic directions

@@ -353,9 +353,12 @@ struct NLParams {
   int range[3];
   double cutoff2;
 };
-// atoms [i0, i0 + n): one structure, its bins numbered from bin_off; iota[i] = i for the sort
+// atoms [i0, i0 + n): one structure, its bins numbered from bin_off; iota[i] = i for the sort;
+// pos_build: a copy of the positions (the reference of the skin criterion)
 void launch_nl_bin(hipStream_t st, int i0, int n, const double* pos, const NLParams& p, int bin_off,
-                   double* wpos, int* img, int* bin, int* iota);
+                   double* wpos, int* img, int* bin, int* iota, double* pos_build);
+// *flag = 1 if some atom's squared displacement from pos_build exceeds thr2 (flag not cleared)
+void launch_max_disp(hipStream_t st, int n, const double* pos, const double* pos_build, double thr2, int* flag);
 // start[b] (b = 0 .. nbins) = first position of key b in the sorted keys[0 .. n)
 void launch_key_starts(hipStream_t st, int n, const int* keys, int nbins, int* start);
 // counts[j] for the structure's atoms; also sets *tail = 0 and *missing = 0

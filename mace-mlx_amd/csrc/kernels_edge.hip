@@ -308,13 +308,15 @@ __device__ __forceinline__ int floordiv(int a, int b) {
 
 // Atoms [i0, i0 + n) form one structure (a batch is a union of structures, each in its own
 // cell); its bins are numbered from bin_off so that all structures share one sorted bin array.
-// iota[i] = i: the values of the sort by bin.
+// iota[i] = i: the values of the sort by bin; pos_build: the positions of this build (the
+// reference of the skin criterion).
 __global__ void k_nl_bin(int i0, int n, const double* __restrict__ pos, NLParams p, int bin_off,
                          double* __restrict__ wpos, int* __restrict__ img, int* __restrict__ bin,
-                         int* __restrict__ iota) {
+                         int* __restrict__ iota, double* __restrict__ pos_build) {
   if ((int)(blockIdx.x * blockDim.x + threadIdx.x) >= n) return;
   const int i = i0 + blockIdx.x * blockDim.x + threadIdx.x;
   iota[i] = i;
+  for (int k = 0; k < 3; ++k) pos_build[3 * i + k] = pos[3 * i + k];
   const double d0 = pos[3 * i] - p.origin[0], d1 = pos[3 * i + 1] - p.origin[1],
                d2 = pos[3 * i + 2] - p.origin[2];
   double f[3], w[3];
@@ -518,6 +520,20 @@ __global__ void __launch_bounds__(256) k_nl_rev(int64_t E, const int* __restrict
   }
 }
 
+// *flag = 1 when some atom moved by more than sqrt(thr2) since pos_build (every writer stores
+// the same value, so the order does not matter)
+__global__ void k_max_disp(int n, const double* __restrict__ pos, const double* __restrict__ pos_build,
+                           double thr2, int* __restrict__ flag) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  double d2 = 0.0;
+  for (int k = 0; k < 3; ++k) {
+    const double d = pos[3 * i + k] - pos_build[3 * i + k];
+    d2 += d * d;
+  }
+  if (d2 > thr2) *flag = 1;
+}
+
 // start[b] = first position of key b in the sorted keys[0 .. n) (b = 0 .. nbins): the CSR of a
 // sorted key array by binary search, with no counts to clear or scan
 __global__ void k_key_starts(int n, const int* __restrict__ keys, int nbins, int* __restrict__ start) {
@@ -588,9 +604,15 @@ void launch_density_edge_bwd(hipStream_t st, int64_t E, const int* receiver, con
 }
 
 void launch_nl_bin(hipStream_t st, int i0, int n, const double* pos, const NLParams& p, int bin_off, double* wpos,
-                   int* img, int* bin, int* iota) {
+                   int* img, int* bin, int* iota, double* pos_build) {
   if (n <= 0) return;
-  MACE_LAUNCH(k_nl_bin, dim3(nblk(n, 256)), dim3(256), 0, st, i0, n, pos, p, bin_off, wpos, img, bin, iota);
+  MACE_LAUNCH(k_nl_bin, dim3(nblk(n, 256)), dim3(256), 0, st, i0, n, pos, p, bin_off, wpos, img, bin, iota,
+              pos_build);
+}
+
+void launch_max_disp(hipStream_t st, int n, const double* pos, const double* pos_build, double thr2, int* flag) {
+  if (n <= 0) return;
+  MACE_LAUNCH(k_max_disp, dim3(nblk(n, 256)), dim3(256), 0, st, n, pos, pos_build, thr2, flag);
 }
 
 void launch_key_starts(hipStream_t st, int n, const int* keys, int nbins, int* start) {

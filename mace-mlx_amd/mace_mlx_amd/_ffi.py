@@ -27,6 +27,7 @@ MACE_ERR_SPECIES = -5
 STEP_FORCES = 1
 STEP_STRESS = 2
 STEP_FORCE_NL = 4
+STEP_SKIN_CHECK = 8
 
 EXPORTED_SYMBOLS = (
     "mace_create", "mace_destroy", "mace_last_error", "mace_model_begin", "mace_model_set_tensor",
@@ -240,9 +241,12 @@ class Engine:
         self._check(self._lib.mace_get_edges(self._h, E, _ptr(s), _ptr(r), _ptr(S), ctypes.byref(n)))
         return s, r, S
 
-    def step_device(self, d_positions: int, d_out: int, stress: bool = False, force_nl: bool = False) -> None:
-        """Queue one step on device buffers (raw device addresses); see mace_step_device."""
-        flags = STEP_FORCES | (STEP_STRESS if stress else 0) | (STEP_FORCE_NL if force_nl else 0)
+    def step_device(self, d_positions: int, d_out: int, stress: bool = False, force_nl: bool = False,
+                    skin_check: bool = False) -> None:
+        """Queue one step on device buffers (raw device addresses); see mace_step_device.
+        ``skin_check``: the engine applies the skin criterion itself (one synchronisation)."""
+        flags = (STEP_FORCES | (STEP_STRESS if stress else 0) | (STEP_FORCE_NL if force_nl else 0)
+                 | (STEP_SKIN_CHECK if skin_check else 0))
         self._check(self._lib.mace_step_device(self._h, ctypes.c_void_p(d_positions), flags,
                                                ctypes.c_void_p(d_out)))
 

@@ -563,6 +563,54 @@ def test_graph_replay_matches_eager(medium_zbl):
         eng.set_graphs(True)
 
 
+def test_device_skin_check(medium_zbl):
+    """MACE_STEP_SKIN_CHECK: mace_step_device applies the skin criterion itself
+    (`calculators.py:266-283`, rebuild when some atom moved more than skin/2 since the last
+    build): moves below skin/2 keep the list (and still give the energy and forces of a fresh
+    list, to float32 summation order), a move beyond it rebuilds, and the rebuilt list gives
+    the numbers of a host-array step on a list built at the same positions, bit for bit."""
+    import torch
+    from mace_mlx_amd.systems import diamond_si
+    eng = medium_zbl.eng
+    s = rattle(diamond_si((3, 3, 3)), 0.03, 11)
+    sp = species_of(medium_zbl.dm, s.numbers)
+    eng.set_system(sp, s.cell, s.pbc, 0.5)
+    N = len(s)
+    out_d = torch.zeros(10 + 3 * N, dtype=torch.float64, device="cuda")
+
+    def dev(pos):
+        pos_d = torch.from_numpy(np.ascontiguousarray(pos)).cuda()
+        torch.cuda.synchronize()
+        eng.step_device(pos_d.data_ptr(), out_d.data_ptr(), skin_check=True)
+        eng.sync()
+        o = out_d.cpu().numpy()
+        return o[0], o[10:].reshape(N, 3).copy()
+
+    def same_edges(a, b):
+        return all(np.array_equal(x, y) for x, y in zip(a, b))
+
+    dev(s.positions)
+    edges0 = eng.get_edges()
+    rng = np.random.default_rng(5)
+    u = rng.normal(size=s.positions.shape)
+    u /= np.linalg.norm(u, axis=1, keepdims=True)
+    near = s.positions + 0.24 * u  # every atom moved 0.24 A < skin/2
+    E1, F1 = dev(near)
+    assert same_edges(eng.get_edges(), edges0)  # kept
+    far = near.copy()
+    far[7] += 0.3 * u[7]  # atom 7 now 0.54 A from its build position
+    E2, F2 = dev(far)
+    edges2 = eng.get_edges()
+    assert not same_edges(edges2, edges0)  # rebuilt (pairs of the 5.43 A shell crossed r_max + skin)
+    Eh, _, Fh, _ = eng.step(far, force_nl=True)  # the same list, built on the host path
+    assert same_edges(eng.get_edges(), edges2)
+    assert E2 == Eh and np.array_equal(F2, Fh)
+    E3, F3 = dev(far)  # no move since that build: list kept, same numbers
+    assert E3 == Eh and np.array_equal(F3, Fh)
+    En, _, Fn, _ = eng.step(near, force_nl=True)  # a fresh list at the near positions
+    assert abs(E1 - En) <= 1e-6 * abs(En) and np.abs(F1 - Fn).max() <= 1e-5, (E1 - En, np.abs(F1 - Fn).max())
+
+
 @pytest.mark.parametrize("arch", ["medium_zbl", "large"])
 def test_split_products_match_fp32(arch, request):
     """Float32 policy: the matrix products (radial-MLP output layer, node linears) on fp16
