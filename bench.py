@@ -162,9 +162,8 @@ def tp_scatter_summary(per_step, ctx):
 
 def load_traffic(site: str, workload: str):
     """HBM bytes per launch of `site` measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
-    (profiles/traffic.json, written from the committed pmc summaries) for this workload,
-    or None."""
-    p = ROOT / "profiles" / "traffic.json"
+    (profiles/traffic_<workload>.json, written from the committed pmc summaries), or None."""
+    p = ROOT / "profiles" / f"traffic_{workload.lower().replace('-', '_')}.json"
     if not p.exists():
         return None
     try:

@@ -119,7 +119,7 @@ def calibration(counter_rows: List[dict], mib: float) -> float:
 
 
 def summarize(d: str, out_dir: str, calib_mib: float = 256.0, commands: Dict[str, str] = None) -> dict:
-    """Write <out_dir>/kernel_trace_<workload>.md, hbm_traffic_<workload>.md and traffic.json
+    """Write <out_dir>/kernel_trace_<workload>.md, hbm_traffic_<workload>.md and traffic_<workload>.json
     from a measurement directory holding launch_order.txt, bench.json (the bench line of the
     traced run), trace/ (rocprofv3 --kernel-trace --stats csv) and, optionally, pmc_fetch/ and
     pmc_write/ (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE csv)."""
@@ -196,7 +196,7 @@ def summarize(d: str, out_dir: str, calib_mib: float = 256.0, commands: Dict[str
     for k in sorted(fk):
         tj[k] = {"fetch_kib": round(fk[k], 1), "write_kib": round(wk.get(k, 0.0), 1),
                  "bytes_per_launch": round((fk[k] * fs_ + wk.get(k, 0.0) * ws_) * 1024.0)}
-    with open(os.path.join(out_dir, "traffic.json"), "w") as f:
+    with open(os.path.join(out_dir, f"traffic_{tag}.json"), "w") as f:
         json.dump(tj, f, indent=1, sort_keys=True)
     T = []
     t = T.append
@@ -209,7 +209,7 @@ def summarize(d: str, out_dir: str, calib_mib: float = 256.0, commands: Dict[str
       f"{calib_mib:g} MiB (reads and writes {calib_mib * 1024:.0f} KiB).  FETCH_SIZE is scaled by {fs_:.4f} and "
       f"WRITE_SIZE by {ws_:.4f} so that the calibration kernel reads its true bytes; HBM bytes per launch = "
       f"(FETCH_SIZE x {fs_:.3f} + WRITE_SIZE x {ws_:.3f}) KiB x 1024, averaged over {nf} steady-state steps "
-      "(dispatches mapped to sites as in the kernel-trace summary).  `traffic.json` holds the same numbers for "
+      f"(dispatches mapped to sites as in the kernel-trace summary).  `traffic_{tag}.json` holds the same numbers for "
       "bench.py.  FETCH_SIZE counts L2 misses, which may still hit the last-level (Infinity) cache.\n")
     t("| site | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM MB per launch (scaled) |\n|---|---:|---:|---:|")
     for k in sorted(fk, key=lambda k: -tj[k]["bytes_per_launch"]):
