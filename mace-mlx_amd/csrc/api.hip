@@ -1674,7 +1674,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
       }
       launch_tpx_bwd(st, Ly.lin, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p, Ly.mlp3x.p, Ly.wn,
                      Ly.w3inv, Ly.h_up.p, c->gM.p, c->pos_s.p, l > 0 ? c->gxe.p : nullptr, c->gY.p, gyp, acc_gy,
-                     c->gh3p.p, c->sink.p);
+                     c->gh3p.p, c->sink.p, half);
     } else {
       // layers after the first also need dL/dx: per-edge rows in sender order, then a segmented sum
       Site s(c, lname("tp_bwd", l));

@@ -568,6 +568,29 @@ __device__ __forceinline__ f4v mfma16h(h8 a, h8 b, f4v c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// The per-edge weights w the fused forward keeps for its VJP: float, or under a half-precision
+// feature policy the 16-bit pattern of the value it already holds (fp16, or the upper half of
+// the fp32 pattern for bf16), exact either way: half the bytes of the largest per-edge stream.
+template <int RND>
+__device__ __forceinline__ void store_w(float* w, int64_t o, float x) {
+  if constexpr (RND == RND_NONE) {
+    __builtin_nontemporal_store(x, w + o);
+  } else {
+    const unsigned short h = RND == RND_F16 ? __builtin_bit_cast(unsigned short, (_Float16)x)
+                                            : (unsigned short)(__float_as_uint(x) >> 16);
+    __builtin_nontemporal_store(h, reinterpret_cast<unsigned short*>(w) + o);
+  }
+}
+template <int RND>
+__device__ __forceinline__ float load_w_nt(const float* w, int64_t o) {
+  if constexpr (RND == RND_NONE) {
+    return __builtin_nontemporal_load(w + o);
+  } else {
+    const unsigned short h = __builtin_nontemporal_load(reinterpret_cast<const unsigned short*>(w) + o);
+    return RND == RND_F16 ? (float)__builtin_bit_cast(_Float16, h) : __uint_as_float((unsigned)h << 16);
+  }
+}
+
 constexpr int XW = 8;          // waves per fused block (receivers in flight)
 // edges per wave and step in the fused forward (a step's tile: XW * EPW edges).  4 halves the
 // steps and made the forward 2-4% faster, but the VJP that later reads the weights it wrote
@@ -837,10 +860,11 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
         const float* trow_t = tb + b * TSP;  // Y (l1 = 0), M1 (l1 = 1) or M2 (l1 = 2)
         tp_edge_fwd<LIN, L1>(acc, in, trow_t, trow_t, trow_t);
       }
-      float* we = (valid ? w + (int64_t)e * a.W : sink) + c0 + u;
+      float* wb = valid ? w : sink;
+      const int64_t wo = (valid ? (int64_t)e * a.W : 0) + c0 + u;
 #pragma unroll
       for (int s = 0; s < T::NSLOT; ++s)
-        if (T::l1(s) == L1) __builtin_nontemporal_store(wv_s[s], we + s * NC);
+        if (T::l1(s) == L1) store_w<RND>(wb, wo + s * NC, wv_s[s]);
     }
     wave_sync();  // table row reads done before the next step's store
     load_slot(j + 2, S);  // S.snd was refilled with step j + 2's indices during step j - 1
@@ -1031,7 +1055,7 @@ struct TpxBwdDims {
 #define MACE_TPX_BWD_ARGS rowptr, sender, Y, Mt, w, W3x, up, gM, pos_s, gxe, gY, gh3p, sink
 // W3x: [64][W] hi plane, then lo plane; gh3p: [P][E][64]
 
-template <int LIN, int L1, bool GX>
+template <int LIN, int L1, bool GX, int WF>
 __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, _Float16* sg, float* sinv,
                                         float* sy, float* sp, float* sm2) {
   using T = TPT<LIN>;
@@ -1110,10 +1134,10 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int64_t e = min<int64_t>(beg + 2 * j + b, elast);
-      const float* we = w + e * a.W + c0 + u;
+      const int64_t wo = e * a.W + c0 + u;
 #pragma unroll
       for (int s = 0; s < T::NSLOT; ++s)
-        if (T::l1(s) == L1) wn[b][s] = __builtin_nontemporal_load(we + s * NC);
+        if (T::l1(s) == L1) wn[b][s] = load_w_nt<WF>(w, wo + s * NC);
       const float* xs = up + (int64_t)snd[b] * DIN + NC * L1 * L1 + c0 + u;
 #pragma unroll
       for (int i = 0; i < NX; ++i) xn[b][i] = xs[NC * i];
@@ -1254,7 +1278,8 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   flush(nsteps2);
 }
 
-template <int LIN, bool GX>
+// WF: storage format of w (RND_*, as the forward that wrote it)
+template <int LIN, bool GX, int WF>
 __global__ void __launch_bounds__(64 * XW, 2) k_tpx_bwd(TpxBwdDims a, MACE_TPX_BWD_PTRS) {
   __shared__ __align__(16) _Float16 sg[2 * 2 * 16 * (64 * gmax<LIN>() + 8)];  // [step][hi, lo][edge][RS]
   __shared__ float sinv[2 * 16];
@@ -1262,19 +1287,19 @@ __global__ void __launch_bounds__(64 * XW, 2) k_tpx_bwd(TpxBwdDims a, MACE_TPX_B
   __shared__ __align__(16) float sp[3 * 4 * 256];  // [two steps + the lower half's slot][q tile][lane][4]
   __shared__ __align__(16) float sm2[LIN == 3 ? XW * 2 * tpx_tab_pad(2) : 4];  // [wave][edge][M2 row]
   if constexpr (LIN == 1) {
-    tpx_bwd<1, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+    tpx_bwd<1, 0, GX, WF>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
   } else if constexpr (LIN == 2) {
     if (blockIdx.z == 0)
-      tpx_bwd<2, 1, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<2, 1, GX, WF>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
     else
-      tpx_bwd<2, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<2, 0, GX, WF>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
   } else {
     if (blockIdx.z == 0)
-      tpx_bwd<3, 2, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<3, 2, GX, WF>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
     else if (blockIdx.z == 1)
-      tpx_bwd<3, 1, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<3, 1, GX, WF>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
     else
-      tpx_bwd<3, 0, GX>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<3, 0, GX, WF>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
   }
 }
 
@@ -1371,22 +1396,30 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
 void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const float* w, const void* W3x, int W, float wscale, const float* up,
                     const float* gM, const int* pos_s, float* gxe, float* gY, int gyp, int accumulate_gY,
-                    float* gh3p, float* sink) {
+                    float* gh3p, float* sink, int wfmt) {
   if (N <= 0 || E <= 0) return;  // no edges: no dL/dw, dL/dY, dL/dx rows to write
   const TpxBwdDims a{N, W, mts, E, wscale, accumulate_gY, gyp};
   const dim3 grid((unsigned)((N + XW - 1) / XW), 2, (unsigned)lin);
   const _Float16* wx = static_cast<const _Float16*>(W3x);
-#define MACE_TPXB(L, GXV)                                                                                        \
-  MACE_LAUNCH((k_tpx_bwd<L, GXV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \
-                     pos_s, gxe, gY, gh3p, sink)
+#define MACE_TPXB(L, GXV, WF)                                                                         \
+  MACE_LAUNCH((k_tpx_bwd<L, GXV, WF>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \
+              pos_s, gxe, gY, gh3p, sink)
+#define MACE_TPXB_WF(L, GXV)       \
+  if (wfmt == RND_F16)             \
+    MACE_TPXB(L, GXV, RND_F16);    \
+  else if (wfmt == RND_BF16)       \
+    MACE_TPXB(L, GXV, RND_BF16);   \
+  else                             \
+    MACE_TPXB(L, GXV, RND_NONE);
   const bool gx = gxe != nullptr;
   if (lin == 1) {
-    if (gx) MACE_TPXB(1, true); else MACE_TPXB(1, false);
+    if (gx) { MACE_TPXB_WF(1, true) } else { MACE_TPXB_WF(1, false) }
   } else if (lin == 2) {
-    if (gx) MACE_TPXB(2, true); else MACE_TPXB(2, false);
+    if (gx) { MACE_TPXB_WF(2, true) } else { MACE_TPXB_WF(2, false) }
   } else {
-    if (gx) MACE_TPXB(3, true); else MACE_TPXB(3, false);
+    if (gx) { MACE_TPXB_WF(3, true) } else { MACE_TPXB_WF(3, false) }
   }
+#undef MACE_TPXB_WF
 #undef MACE_TPXB
 }
 
