@@ -1113,11 +1113,16 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   }
   float R1[L1 == 1 ? G : 1][3][16];
   if constexpr (L1 == 1) vjp_l1_table<LIN>(gm, R1);
-  // next step's inputs: weights, sender rows and Y rows of the two edges (indices and
-  // pos_s a step earlier still); the Y rows are wave-uniform (scalar loads)
-  float wn[2][T::NSLOT], xv[2][NX], xn[2][NX], wc[2][T::NSLOT], yn[2];
-  int snd[2], psn[2], pnx[2], pss[2];  // indices of step j + 2 / pos_s of step j + 1 / of this step
-  float gyn[2], gyc[2];                 // dL/dY partials already held (accumulate_gY), a step ahead
+  // A step's inputs: weights, sender rows, Y components, pos_s and the dL/dY partials already
+  // held (accumulate_gY) of its two edges, loaded a step ahead (indices and pos_s a step earlier
+  // still).  Two sets: the step loop is unrolled by two, so a step reads one set and fills the
+  // other, with no copies between them.
+  struct StepIn {
+    float w[2][T::NSLOT], x[2][NX], y[2], gy[2];
+    int ps[2];
+  };
+  StepIn in0, in1;
+  int snd[2], psn[2];  // indices / pos_s of step j + 2
   // gY[e][p][16] entry of lane l (lanes 4k hold component k after the wave sum); padding -> sink
   auto gy_addr = [&](int e, bool valid) {
     return valid && (l & 3) == 0 ? gY + ((int64_t)e * a.gyp + p) * 16 + (l >> 2) : sink + l;
@@ -1130,21 +1135,21 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
       if (GX) psn[b] = pos_s[e];
     }
   };
-  auto load_in = [&](int j) {
+  auto load_in = [&](int j, StepIn& S) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int64_t e = min<int64_t>(beg + 2 * j + b, elast);
       const int64_t wo = e * a.W + c0 + u;
 #pragma unroll
       for (int s = 0; s < T::NSLOT; ++s)
-        if (T::l1(s) == L1) wn[b][s] = load_w_nt<WF>(w, wo + s * NC);
+        if (T::l1(s) == L1) S.w[b][s] = load_w_nt<WF>(w, wo + s * NC);
       const float* xs = up + (int64_t)snd[b] * DIN + NC * L1 * L1 + c0 + u;
 #pragma unroll
-      for (int i = 0; i < NX; ++i) xn[b][i] = xs[NC * i];
-      yn[b] = Y[e * 16 + (l & 15)];  // lane l holds component l & 15 (stored to LDS a step later)
-      if (GX) pnx[b] = psn[b];
+      for (int i = 0; i < NX; ++i) S.x[b][i] = xs[NC * i];
+      S.y[b] = Y[e * 16 + (l & 15)];  // lane l holds component l & 15 (stored to LDS at the step)
+      if (GX) S.ps[b] = psn[b];
       const int ej = beg + 2 * j + b;
-      gyn[b] = *gy_addr(ej, ej < end);
+      S.gy[b] = *gy_addr(ej, ej < end);
     }
   };
   f4v prev = f4v{0.f, 0.f, 0.f, 0.f};  // this wave's share of the previous tile's dL/dh3
@@ -1159,10 +1164,10 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
                                              (prev[2] + o[2]) * a.wscale, (prev[3] + o[3]) * a.wscale};
   };
   float* ys = sy + wv * 32;  // this wave's two Y rows (LDS; read back as broadcasts)
-  auto step = [&](int j) {
+  auto step = [&](int j, const StepIn& S, StepIn& Snext) {
     _Float16* tile = sg + (j & 1) * 2 * 16 * RS;  // [hi, lo][edge column][RS]
     float* tinv = sinv + (j & 1) * 16;
-    if (l < 32) ys[l] = yn[l >> 4];
+    if (l < 32) ys[l] = l < 16 ? S.y[0] : S.y[1];  // constant indices: S stays in registers
     wave_sync();
     float* m2w = sm2 + wv * 2 * M2S;  // l1 = 2: this wave's two M2 rows
     if constexpr (L1 == 2) {  // the terms and order of k_edge_fwd
@@ -1175,17 +1180,7 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
                 fmaf(ys[16 * b + m2j_[h][1]], m2v_[h][1], fmaf(ys[16 * b + m2j_[h][0]], m2v_[h][0], 0.f));
       wave_sync();
     }
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-#pragma unroll
-      for (int i = 0; i < NX; ++i) xv[b][i] = xn[b][i];
-#pragma unroll
-      for (int s = 0; s < T::NSLOT; ++s)
-        if (T::l1(s) == L1) wc[b][s] = wn[b][s];
-      if (GX) pss[b] = pnx[b];
-      gyc[b] = gyn[b];
-    }
-    load_in(j + 1);
+    load_in(j + 1, Snext);
     load_idx(j + 2);
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
@@ -1203,13 +1198,13 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
         in.x0 = 0.f;
 #pragma unroll
         for (int i = 0; i < NX; ++i) {
-          if constexpr (L1 == 0) in.x0 = xv[b][i];
-          if constexpr (L1 == 1) in.x1[i] = xv[b][i];
-          if constexpr (L1 == 2) in.x2[i] = xv[b][i];
+          if constexpr (L1 == 0) in.x0 = S.x[b][i];
+          if constexpr (L1 == 1) in.x1[i] = S.x[b][i];
+          if constexpr (L1 == 2) in.x2[i] = S.x[b][i];
         }
 #pragma unroll
         for (int s = 0; s < T::NSLOT; ++s)
-          if (T::l1(s) == L1) in.w[s] = wc[b][s];
+          if (T::l1(s) == L1) in.w[s] = S.w[b][s];
         const float* yrow = ys + 16 * b;
         if constexpr (L1 == 1)
           tp_edge_vjp_l1<LIN, GX>(R1, in, gws, yrow, gx1, gYu);
@@ -1237,12 +1232,12 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
         if (l == 0) tinv[2 * wv + b] = __uint_as_float((unsigned)(127 - 14 + ex) << 23);
       }
       if constexpr (GX) {
-        float* dst = (valid ? gxe + (int64_t)pss[b] * DIN + NC * L1 * L1 : sink) + c0 + u;
+        float* dst = (valid ? gxe + (int64_t)S.ps[b] * DIN + NC * L1 * L1 : sink) + c0 + u;
 #pragma unroll
         for (int i = 0; i < NX; ++i) dst[NC * i] = L1 == 0 ? gx0 : L1 == 1 ? gx1[i] : gx2[i];
       }
       const float ysum = wave_sum16(gYu);
-      *gy_addr(e, valid) = a.accumulate_gY ? gyc[b] + ysum : ysum;
+      *gy_addr(e, valid) = a.accumulate_gY ? S.gy[b] + ysum : ysum;
     }
     __syncthreads();  // also: this step's Y- and M2-row reads are done before the next step's stores
     // dL/dh3 of this tile (half kh of the k steps), then the previous tile's flush
@@ -1269,11 +1264,14 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   const int nsteps2 = (nsteps + 1) & ~1;
   if (nsteps2 > 0) {  // some receiver of the block has edges, so E >= 1 and the clamped indices are valid
     load_idx(0);
-    load_in(0);
+    load_in(0, in0);
     load_idx(1);
   }
 #pragma unroll 1
-  for (int j = 0; j < nsteps2; ++j) step(j);
+  for (int j = 0; j < nsteps2; j += 2) {  // nsteps2 is even
+    step(j, in0, in1);
+    step(j + 1, in1, in0);
+  }
   __syncthreads();
   flush(nsteps2);
 }
