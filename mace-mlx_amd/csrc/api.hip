@@ -145,7 +145,6 @@ struct mace_ctx {
   int mts = 0;  // row stride of the per-edge TP tables Mt (0: no layer has l1 >= 1 inputs)
   DBuf<float> e0, bessel_w, zbl_z, zbl_cov, ag_cov, embed;
   DBuf<float> up0_tab;  // first linear_up per species [n_el][C]
-  DBuf<float> sink;     // fused TP: target of the weight stores of padding edges (max slots x C floats)
   DBuf<float> gA2, grho;  // backward scratch of the message skip / density normalisation
   // mh-1: per-edge envelope and its gradient (apply_cutoff = 0), edge densities, gw . b3,
   // dL/d(gate input), all-zero species (element-agnostic product)
@@ -648,9 +647,6 @@ void build_model(mace_ctx* c) {
   c->max_lin = 1;
   for (const Layer& L : c->layers) c->max_lin = std::max(c->max_lin, L.tl());
   c->mts = (tp_table_entries(c->max_lin) + 15) / 16 * 16;
-  int wmax = 0;
-  for (const Layer& L : c->layers) wmax = std::max(wmax, L.wn);
-  c->sink.ensure((size_t)wmax);
   c->host_tensors.clear();
   c->model_ready = true;
 }
@@ -1521,7 +1517,7 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
       Site s(c, lname("tp_fwd", l));
       if (fused)
         launch_tpx_fwd(st, L.lin, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, c->h3.p, c->h3inv.p,
-                       L.mlpT3x.p, L.wn, L.w3inv, L.h_up.p, c->M.p, L.w.p, c->sink.p, half);
+                       L.mlpT3x.p, L.wn, L.w3inv, L.h_up.p, c->M.p, L.w.p, half);
       else
         launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.wptr(h16), L.h_up.p,
                       c->M.p, half);
@@ -1674,7 +1670,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
       }
       launch_tpx_bwd(st, Ly.lin, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p, Ly.mlp3x.p, Ly.wn,
                      Ly.w3inv, Ly.h_up.p, c->gM.p, c->pos_s.p, l > 0 ? c->gxe.p : nullptr, c->gY.p, gyp, acc_gy,
-                     c->gh3p.p, c->sink.p, half);
+                     c->gh3p.p, half);
     } else {
       // layers after the first also need dL/dx: per-edge rows in sender order, then a segmented sum
       Site s(c, lname("tp_bwd", l));
@@ -1803,7 +1799,7 @@ static void free_all(mace_ctx* c) {
   c->h3inv.release();
   for (auto* b : {&c->gptr, &c->gid}) b->release();
   for (auto* b : {&c->gcell, &c->eg, &c->gvir}) b->release();
-  for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->ag_cov, &c->gA2, &c->grho, &c->embed, &c->up0_tab, &c->sink, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
+  for (auto* b : {&c->e0, &c->bessel_w, &c->zbl_z, &c->zbl_cov, &c->ag_cov, &c->gA2, &c->grho, &c->embed, &c->up0_tab, &c->Y, &c->Mt, &c->ef, &c->zbl_e, &c->gY, &c->gef,
                   &c->gv, &c->gw, &c->gxe, &c->h3, &c->gh3p, &c->M, &c->B, &c->gB, &c->gA, &c->gM, &c->gh0, &c->gh1, &c->gup,
                   &c->node_e, &c->cutv, &c->gcut, &c->mh_dens, &c->gwb, &c->gP})
     b->release();

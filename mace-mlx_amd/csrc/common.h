@@ -252,22 +252,20 @@ void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const
 // built per 16-edge tile from the split h3 planes (h3x, h3inv) and the split W3^T planes
 // (W3Tx, scale wscale), M is written as by launch_tp_fwd and w ([E][W]) for the VJP; w and
 // M rounded by rnd (RND_*, the feature policy), w stored as 16-bit fp16 / bf16 patterns under
-// RND_F16 / RND_BF16 (exact: the values are already rounded); sink: W scratch floats that
-// absorb the stores of padding edges.
+// RND_F16 / RND_BF16 (exact: the values are already rounded).
 void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const void* h3x, const float* h3inv, const void* W3Tx, int W,
-                    float wscale, const float* up, float* M, float* w, float* sink, int rnd);
+                    float wscale, const float* up, float* M, float* w, int rnd);
 // TP VJP with the radial-MLP output layer's backward product fused in (split products,
 // lin = 1..3): reads w ([E][W], written by
 // launch_tpx_fwd), writes the dL/dh3 partials gh3p ([P][E][64], P = 2 x input
 // degrees of the layer), dL/dY partials into gY[e][p][16] (gyp partials per
 // edge; written, or added when accumulate_gY) and, with gxe, the per-edge dL/dx
-// rows as launch_tp_bwd_recv does.  sink: scratch floats (>= W) for padding.  wfmt: the
-// storage format of w (the forward's rnd).
+// rows as launch_tp_bwd_recv does.  wfmt: the storage format of w (the forward's rnd).
 void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const float* w, const void* W3x, int W, float wscale, const float* up,
                     const float* gM, const int* pos_s, float* gxe, float* gY, int gyp, int accumulate_gY,
-                    float* gh3p, float* sink, int wfmt);
+                    float* gh3p, int wfmt);
 // p[0 .. n) = 0 (a kernel, not a memset: safe inside captured graphs)
 void launch_fill_zero(hipStream_t st, float* p, int64_t n);
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe,

@@ -28,6 +28,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <utility>
 
 #include "common.h"
@@ -591,6 +592,37 @@ __device__ __forceinline__ float load_w_nt(const float* w, int64_t o) {
   }
 }
 
+// Raw buffer views (stride 0): the hardware range check drops a store, and returns zero for a
+// load, whose byte offset is at or past the view's size.  Padding lanes and past-the-end edges
+// take an offset past every view (or a view of size 0), so the fused kernels' stores need no
+// branch and no dummy target: every path issues the same memory operations (the compiler's
+// wait counts stay exact) and no wave writes memory that another wave writes.
+constexpr unsigned BUF_OOB = 0x80000000u;  // views are smaller than 2 GiB
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_view(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void buf_store(float v, __amdgpu_buffer_rsrc_t r, unsigned off) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)off, 0, 0);
+}
+__device__ __forceinline__ void buf_store4(float4 v, __amdgpu_buffer_rsrc_t r, unsigned off) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), r,
+                                         (int)off, 0, 0);
+}
+__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+// store_w through a view of one edge's row (element index o; aux 2 = nontemporal)
+template <int RND>
+__device__ __forceinline__ void store_w_buf(__amdgpu_buffer_rsrc_t r, unsigned o, float x) {
+  if constexpr (RND == RND_NONE) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, (int)(4 * o), 0, 2);
+  } else {
+    const unsigned short h = RND == RND_F16 ? __builtin_bit_cast(unsigned short, (_Float16)x)
+                                            : (unsigned short)(__float_as_uint(x) >> 16);
+    __builtin_amdgcn_raw_buffer_store_b16(h, r, (int)(2 * o), 0, 2);
+  }
+}
+
 constexpr int XW = 8;          // waves per fused block (receivers in flight)
 // edges per wave and step in the fused forward (a step's tile: XW * EPW edges).  4 halves the
 // steps and made the forward 2-4% faster, but the VJP that later reads the weights it wrote
@@ -656,10 +688,10 @@ struct TpxDims {
   const int *__restrict__ rowptr, const int *__restrict__ sender, const float *__restrict__ Y,              \
       const float *__restrict__ Mt, const _Float16 *__restrict__ h3x, const float *__restrict__ h3inv,     \
       const _Float16 *__restrict__ W3Tx, const float *__restrict__ up, float *__restrict__ M,               \
-      float *__restrict__ w, float *__restrict__ sink
-#define MACE_TPX_FWD_ARGS rowptr, sender, Y, Mt, h3x, h3inv, W3Tx, up, M, w, sink
+      float *__restrict__ w
+#define MACE_TPX_FWD_ARGS rowptr, sender, Y, Mt, h3x, h3inv, W3Tx, up, M, w
 // h3x: [E][hi 64 | lo 64]; h3inv: [E]; W3Tx: [W][64] hi plane, then lo plane;
-// w: [E][W] for the VJP; sink: W floats, target of the stores of padding edges
+// w: [E][W] for the VJP
 
 template <int LIN, int L1, int RND>
 __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, float* sw, float* stab, _Float16* hbuf,
@@ -700,10 +732,10 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
       }
     }
   }
-  // Every vector-memory operation below is unconditional (indices clamped,
-  // stores of past-the-end edges sent to sink), so the number in flight is the
-  // same on every path and the compiler's wait counts stay exact: a step waits
-  // only for what it consumes, never for the prefetches behind it.
+  // Every vector-memory operation below is unconditional (indices clamped, stores
+  // of past-the-end edges dropped by a buffer view of size 0), so the number in
+  // flight is the same on every path and the compiler's wait counts stay exact: a
+  // step waits only for what it consumes, never for the prefetches behind it.
   //
   // Two ring slots (the step loop is unrolled by two, so a slot is a set of
   // registers): slot j & 1 holds step j's inputs, and step j refills it for step
@@ -860,11 +892,14 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
         const float* trow_t = tb + b * TSP;  // Y (l1 = 0), M1 (l1 = 1) or M2 (l1 = 2)
         tp_edge_fwd<LIN, L1>(acc, in, trow_t, trow_t, trow_t);
       }
-      float* wb = valid ? w : sink;
-      const int64_t wo = (valid ? (int64_t)e * a.W : 0) + c0 + u;
+      {
+        constexpr unsigned WB = RND == RND_NONE ? 4 : 2;  // bytes per stored weight
+        const auto wr = buf_view(reinterpret_cast<char*>(w) + (int64_t)min<int64_t>(e, elast) * a.W * WB,
+                                 valid ? (unsigned)a.W * WB : 0u);
 #pragma unroll
-      for (int s = 0; s < T::NSLOT; ++s)
-        if (T::l1(s) == L1) store_w<RND>(wb, wo + s * NC, wv_s[s]);
+        for (int s = 0; s < T::NSLOT; ++s)
+          if (T::l1(s) == L1) store_w_buf<RND>(wr, (unsigned)(c0 + u + s * NC), wv_s[s]);
+      }
     }
     wave_sync();  // table row reads done before the next step's store
     load_slot(j + 2, S);  // S.snd was refilled with step j + 2's indices during step j - 1
@@ -940,8 +975,8 @@ __global__ void __launch_bounds__(64 * XW, 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_
 // the group's k steps, holding those W3 fragments in registers; the two halves
 // of a q tile meet through LDS one step later (no second barrier).
 // dL/dY partials go to gY[e][p][16] and dL/dx rows to gxe[pos_s[e]] (this
-// group's components, this slice's channels).  As in the forward, every
-// vector-memory operation is unconditional (padding goes to the sink).
+// group's components, this slice's channels).  As in the forward, every load
+// is unconditional (clamped indices); stores of padding edges are skipped.
 // ---------------------------------------------------------------------------
 // l1 = 1 slots of a receiver-centric VJP, refactored around what stays fixed while a
 // wave walks one receiver's edges: g = dL/dM[recv] (per channel) and the CG tables B
@@ -1051,8 +1086,8 @@ struct TpxBwdDims {
   const int *__restrict__ rowptr, const int *__restrict__ sender, const float *__restrict__ Y,              \
       const float *__restrict__ Mt, const float *__restrict__ w, const _Float16 *__restrict__ W3x,           \
       const float *__restrict__ up, const float *__restrict__ gM, const int *__restrict__ pos_s,            \
-      float *__restrict__ gxe, float *__restrict__ gY, float *__restrict__ gh3p, float *__restrict__ sink
-#define MACE_TPX_BWD_ARGS rowptr, sender, Y, Mt, w, W3x, up, gM, pos_s, gxe, gY, gh3p, sink
+      float *__restrict__ gxe, float *__restrict__ gY, float *__restrict__ gh3p
+#define MACE_TPX_BWD_ARGS rowptr, sender, Y, Mt, w, W3x, up, gM, pos_s, gxe, gY, gh3p
 // W3x: [64][W] hi plane, then lo plane; gh3p: [P][E][64]
 
 template <int LIN, int L1, bool GX, int WF>
@@ -1089,6 +1124,9 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   for (int off = 8; off > 0; off >>= 1) ns = max(ns, __shfl_xor(ns, off));
   const int nsteps = __builtin_amdgcn_readfirstlane(ns);
   const int64_t elast = a.E - 1;
+  // the block's edges [eb0, eb1) (its receivers' rows): a view of their dL/dh3 partial rows p
+  const int eb0 = rowptr[min(nb0, a.N)], eb1 = rowptr[min(nb0 + XW, a.N)];
+  const auto gh3v = buf_view(gh3p + ((int64_t)p * a.E + eb0) * XH, 4u * XH * (unsigned)(eb1 - eb0));
 
   // W3 rows q = 16 qt + r, group k steps kh G .. kh G + G - 1 (32 columns each)
   const int qt = wv & 3, kh = wv >> 2;
@@ -1123,9 +1161,11 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   };
   StepIn in0, in1;
   int snd[2], psn[2];  // indices / pos_s of step j + 2
-  // gY[e][p][16] entry of lane l (lanes 4k hold component k after the wave sum); padding -> sink
-  auto gy_addr = [&](int e, bool valid) {
-    return valid && (l & 3) == 0 ? gY + ((int64_t)e * a.gyp + p) * 16 + (l >> 2) : sink + l;
+  // gY[e][p][16] entry of lane l (lanes 4k hold component k after the wave sum): a view of
+  // edge e's partials that only those lanes of an edge that exists address
+  const unsigned gyo = (l & 3) == 0 ? 4u * (16 * p + (l >> 2)) : BUF_OOB;
+  auto gy_view = [&](int e, bool on) {
+    return buf_view(gY + min<int64_t>(e, elast) * a.gyp * 16, on ? 64u * a.gyp : 0u);
   };
   auto load_idx = [&](int j) {
 #pragma unroll
@@ -1149,24 +1189,33 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
       S.y[b] = Y[e * 16 + (l & 15)];  // lane l holds component l & 15 (stored to LDS at the step)
       if (GX) S.ps[b] = psn[b];
       const int ej = beg + 2 * j + b;
-      S.gy[b] = *gy_addr(ej, ej < end);
+      S.gy[b] = buf_load(gy_view(ej, a.accumulate_gY && ej < end), gyo);
     }
   };
-  f4v prev = f4v{0.f, 0.f, 0.f, 0.f};  // this wave's share of the previous tile's dL/dh3
-  // dL/dh3 of the tile before step j: add the partner half (k steps of the other
-  // half, written to LDS last step) and store; the upper half only feeds LDS
-  auto flush = [&](int j) {
-    const f4v o = *reinterpret_cast<const f4v*>(sp + (((j - 1) & 1) * 4 + qt) * 256 + 4 * l);
-    const int e = cb + 2 * (j - 1) + (r & 1);
-    const bool valid = kh == 0 && j > 0 && e < ce;
-    float* dst = valid ? gh3p + ((int64_t)p * a.E + e) * XH + 16 * qt + 4 * g : sink + 4 * l;
-    *reinterpret_cast<float4*>(dst) = float4{(prev[0] + o[0]) * a.wscale, (prev[1] + o[1]) * a.wscale,
-                                             (prev[2] + o[2]) * a.wscale, (prev[3] + o[3]) * a.wscale};
+  // The dL/dw tile of a pair of steps t (steps 2t, 2t + 1: sub-tile h = step & 1, 16 edge
+  // columns each) is multiplied by W3 during the next pair's first step, after the barrier
+  // that ends pair t: one barrier per two steps, and the two waves that share a SIMD (wave k
+  // and k + 4: halves kh = 0, 1 of the k steps) run their products at opposite ends of that
+  // step, so one wave's matrix-core work overlaps the other's VALU work.
+  f4v prev[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};  // lower half: its share of pair t - 1
+  // dL/dh3 of the pair before t: add the upper half's share (written to LDS during the
+  // previous pair) and store (lower half only)
+  auto flush = [&](int t, bool lower) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const f4v o = *reinterpret_cast<const f4v*>(sp + ((((t - 1) & 1) * 2 + h) * 4 + qt) * 256 + 4 * l);
+      const int e = cb + 2 * (2 * (t - 1) + h) + (r & 1);
+      const bool valid = lower && t > 0 && e < ce;
+      buf_store4(float4{(prev[h][0] + o[0]) * a.wscale, (prev[h][1] + o[1]) * a.wscale,
+                        (prev[h][2] + o[2]) * a.wscale, (prev[h][3] + o[3]) * a.wscale},
+                 gh3v, valid ? 4u * (XH * (unsigned)(e - eb0) + 16 * qt + 4 * g) : BUF_OOB);
+    }
   };
   float* ys = sy + wv * 32;  // this wave's two Y rows (LDS; read back as broadcasts)
-  auto step = [&](int j, const StepIn& S, StepIn& Snext) {
-    _Float16* tile = sg + (j & 1) * 2 * 16 * RS;  // [hi, lo][edge column][RS]
-    float* tinv = sinv + (j & 1) * 16;
+  auto edges = [&](int j, const StepIn& S, StepIn& Snext) {
+    // [pair buffer][hi, lo][32 edge columns][RS]; this step's sub-tile
+    _Float16* tile = sg + ((j >> 1) & 1) * 2 * 32 * RS + (j & 1) * 16 * RS;
+    float* tinv = sinv + ((j >> 1) & 1) * 32 + (j & 1) * 16;
     if (l < 32) ys[l] = l < 16 ? S.y[0] : S.y[1];  // constant indices: S stays in registers
     wave_sync();
     float* m2w = sm2 + wv * 2 * M2S;  // l1 = 2: this wave's two M2 rows
@@ -1227,62 +1276,107 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
             const float x = gws[s] * sc;
             const _Float16 hi = (_Float16)x;
             trow[64 * GR::local(s)] = hi;
-            trow[16 * RS + 64 * GR::local(s)] = (_Float16)(x - (float)hi);
+            trow[32 * RS + 64 * GR::local(s)] = (_Float16)(x - (float)hi);
           }
         if (l == 0) tinv[2 * wv + b] = __uint_as_float((unsigned)(127 - 14 + ex) << 23);
       }
       if constexpr (GX) {
-        float* dst = (valid ? gxe + (int64_t)S.ps[b] * DIN + NC * L1 * L1 : sink) + c0 + u;
+        const auto gxv = buf_view(gxe + (int64_t)S.ps[b] * DIN, valid ? 4u * DIN : 0u);
 #pragma unroll
-        for (int i = 0; i < NX; ++i) dst[NC * i] = L1 == 0 ? gx0 : L1 == 1 ? gx1[i] : gx2[i];
+        for (int i = 0; i < NX; ++i)
+          buf_store(L1 == 0 ? gx0 : L1 == 1 ? gx1[i] : gx2[i], gxv, 4u * (NC * (L1 * L1 + i) + c0 + u));
       }
       const float ysum = wave_sum16(gYu);
-      *gy_addr(e, valid) = a.accumulate_gY ? S.gy[b] + ysum : ysum;
+      buf_store(a.accumulate_gY ? S.gy[b] + ysum : ysum, gy_view(e, valid), gyo);
     }
-    __syncthreads();  // also: this step's Y- and M2-row reads are done before the next step's stores
-    // dL/dh3 of this tile (half kh of the k steps), then the previous tile's flush
-    f4v acc = f4v{0.f, 0.f, 0.f, 0.f};
+  };
+  // dL/dh3 of pair t (half kh of the k steps; the two sub-tiles' products interleaved); the
+  // lower half then flushes pair t - 1, the upper half leaves its share in LDS.  HALF: 0 lower,
+  // 1 upper, 2 either (kh at run time: the lower half's LDS writes go to slots nobody reads)
+  auto products = [&](int t, auto half) {
+    constexpr int HALF = decltype(half)::value;
+    const _Float16* pt = sg + (t & 1) * 2 * 32 * RS;
+    f4v acc[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int ks = 0; ks < G; ++ks) {
-      const _Float16* src = tile + r * RS + 32 * (kh * G + ks) + 8 * g;
-      const h8 xh = *reinterpret_cast<const h8*>(src), xl = *reinterpret_cast<const h8*>(src + 16 * RS);
-      acc = mfma16h(wa[ks][1], xh, acc);
-      acc = mfma16h(wa[ks][0], xl, acc);
-      acc = mfma16h(wa[ks][0], xh, acc);
-    }
-    {
-      const float inv = tinv[r];
+    for (int ks = 0; ks < G; ++ks)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] *= inv;
+      for (int h = 0; h < 2; ++h) {
+        const _Float16* src = pt + (16 * h + r) * RS + 32 * (kh * G + ks) + 8 * g;
+        const h8 xh = *reinterpret_cast<const h8*>(src), xl = *reinterpret_cast<const h8*>(src + 32 * RS);
+        acc[h] = mfma16h(wa[ks][1], xh, acc[h]);
+        acc[h] = mfma16h(wa[ks][0], xl, acc[h]);
+        acc[h] = mfma16h(wa[ks][0], xh, acc[h]);
+      }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float inv = sinv[(t & 1) * 32 + 16 * h + r];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[h][i] *= inv;
     }
-    flush(j);
-    // the upper half's share, read by the lower half next step (the lower half
-    // writes a slot nobody reads: no branch)
-    *reinterpret_cast<f4v*>(sp + ((kh ? (j & 1) : 2) * 4 + qt) * 256 + 4 * l) = acc;
-    prev = acc;
+    if constexpr (HALF != 1) flush(t, HALF == 0 || kh == 0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if constexpr (HALF != 0)
+        *reinterpret_cast<f4v*>(sp + ((HALF == 1 || kh ? (t & 1) * 2 + h : 4 + h) * 4 + qt) * 256 + 4 * l) = acc[h];
+      if constexpr (HALF != 1) prev[h] = acc[h];
+    }
   };
   const int nsteps2 = (nsteps + 1) & ~1;
-  if (nsteps2 > 0) {  // some receiver of the block has edges, so E >= 1 and the clamped indices are valid
-    load_idx(0);
-    load_in(0, in0);
-    load_idx(1);
-  }
+  // the step loop of one half (kh uniform per wave: the barriers of both loops pair up)
+  auto run = [&](auto half) {
+    constexpr int HALF = decltype(half)::value;
+    edges(0, in0, in1);
+    wave_sync();  // this step's Y- and M2-row reads are done before the next step's stores
+    edges(1, in1, in0);
+    __syncthreads();
 #pragma unroll 1
-  for (int j = 0; j < nsteps2; j += 2) {  // nsteps2 is even
-    step(j, in0, in1);
-    step(j + 1, in1, in0);
-  }
-  __syncthreads();
-  flush(nsteps2);
+    for (int j = 2; j < nsteps2; j += 2) {  // nsteps2 is even
+      if constexpr (HALF == 0) products((j >> 1) - 1, half);
+      edges(j, in0, in1);
+      if constexpr (HALF == 1) products((j >> 1) - 1, half);
+      wave_sync();
+      edges(j + 1, in1, in0);
+      __syncthreads();  // also: the Y- and M2-row reads are done before the next step's stores
+    }
+    products((nsteps2 >> 1) - 1, half);
+    __syncthreads();
+    if constexpr (HALF == 0) flush(nsteps2 >> 1, true);
+  };
+  // three input blocks: both halves run their products right after the barrier that ends each
+  // pair (the staggered order's longer live ranges spill registers there)
+  auto run_unstaggered = [&]() {
+#pragma unroll 1
+    for (int j = 0; j < nsteps2; j += 2) {
+      edges(j, in0, in1);
+      wave_sync();
+      edges(j + 1, in1, in0);
+      __syncthreads();
+      products(j >> 1, std::integral_constant<int, 2>{});
+    }
+    __syncthreads();
+    flush(nsteps2 >> 1, kh == 0);
+  };
+  if (nsteps2 == 0) return;  // uniform over the block: no receiver of it has edges
+  // some receiver of the block has edges, so E >= 1 and the clamped indices are valid
+  load_idx(0);
+  load_in(0, in0);
+  load_idx(1);
+  if constexpr (LIN == 3)
+    run_unstaggered();
+  else if (kh == 0)
+    run(std::integral_constant<int, 0>{});
+  else
+    run(std::integral_constant<int, 1>{});
 }
 
 // WF: storage format of w (RND_*, as the forward that wrote it)
 template <int LIN, bool GX, int WF>
 __global__ void __launch_bounds__(64 * XW, 2) k_tpx_bwd(TpxBwdDims a, MACE_TPX_BWD_PTRS) {
-  __shared__ __align__(16) _Float16 sg[2 * 2 * 16 * (64 * gmax<LIN>() + 8)];  // [step][hi, lo][edge][RS]
-  __shared__ float sinv[2 * 16];
+  __shared__ __align__(16) _Float16 sg[2 * 2 * 32 * (64 * gmax<LIN>() + 8)];  // [pair][hi, lo][edge][RS]
+  __shared__ float sinv[2 * 32];
   __shared__ __align__(16) float sy[XW * 32];      // [wave][edge][16]: the step's Y rows
-  __shared__ __align__(16) float sp[3 * 4 * 256];  // [two steps + the lower half's slot][q tile][lane][4]
+  // [two pairs + the lower half's slots][sub-tile][q tile][lane][4]
+  __shared__ __align__(16) float sp[6 * 4 * 256];
   __shared__ __align__(16) float sm2[LIN == 3 ? XW * 2 * tpx_tab_pad(2) : 4];  // [wave][edge][M2 row]
   if constexpr (LIN == 1) {
     tpx_bwd<1, 0, GX, WF>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
@@ -1365,14 +1459,14 @@ void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const
 
 void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const void* h3x, const float* h3inv, const void* W3Tx, int W,
-                    float wscale, const float* up, float* M, float* w, float* sink, int rnd) {
+                    float wscale, const float* up, float* M, float* w, int rnd) {
   if (N <= 0) return;
   const TpxDims a{N, W, mts, E, wscale};
   const dim3 grid((unsigned)((N + XW - 1) / XW), 2, (unsigned)lin);  // z: one input block l1 each
   const _Float16* hx = static_cast<const _Float16*>(h3x);
   const _Float16* wt = static_cast<const _Float16*>(W3Tx);
 #define MACE_TPXF(L, R) \
-  MACE_LAUNCH((k_tpx_fwd<L, R>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w, sink)
+  MACE_LAUNCH((k_tpx_fwd<L, R>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w)
 #define MACE_TPXF_R(L)         \
   if (rnd == RND_F16)          \
     MACE_TPXF(L, RND_F16);     \
@@ -1394,14 +1488,14 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
 void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const float* w, const void* W3x, int W, float wscale, const float* up,
                     const float* gM, const int* pos_s, float* gxe, float* gY, int gyp, int accumulate_gY,
-                    float* gh3p, float* sink, int wfmt) {
+                    float* gh3p, int wfmt) {
   if (N <= 0 || E <= 0) return;  // no edges: no dL/dw, dL/dY, dL/dx rows to write
   const TpxBwdDims a{N, W, mts, E, wscale, accumulate_gY, gyp};
   const dim3 grid((unsigned)((N + XW - 1) / XW), 2, (unsigned)lin);
   const _Float16* wx = static_cast<const _Float16*>(W3x);
 #define MACE_TPXB(L, GXV, WF)                                                                         \
   MACE_LAUNCH((k_tpx_bwd<L, GXV, WF>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \
-              pos_s, gxe, gY, gh3p, sink)
+              pos_s, gxe, gY, gh3p)
 #define MACE_TPXB_WF(L, GXV)       \
   if (wfmt == RND_F16)             \
     MACE_TPXB(L, GXV, RND_F16);    \
