@@ -1062,16 +1062,23 @@ __device__ __forceinline__ void tp_edge_vjp_l1(const float (*R)[3][16], const Ed
 }
 
 // Largest value of a nonnegative x over the wave (DPP row scan, then the two
-// row broadcasts; lane 63 ends with the total), as a wave-uniform value.
+// row broadcasts; lane 63 ends with the total), as a wave-uniform value.  The
+// scan runs on the bit patterns, whose unsigned order is that of nonnegative
+// floats: unsigned max needs no NaN canonicalisation and fuses with the DPP
+// move (lanes without a source read 0, the identity).
+template <int CTRL>
+__device__ __forceinline__ unsigned dpp_u(unsigned v) {
+  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, true);
+}
 __device__ __forceinline__ float wave_max_nonneg(float x) {
-  float m = x;
-  m = fmaxf(m, dpp_f<0x111>(m));  // row_shr:1
-  m = fmaxf(m, dpp_f<0x112>(m));  // row_shr:2
-  m = fmaxf(m, dpp_f<0x114>(m));  // row_shr:4
-  m = fmaxf(m, dpp_f<0x118>(m));  // row_shr:8
-  m = fmaxf(m, dpp_f<0x142>(m));  // row_bcast:15
-  m = fmaxf(m, dpp_f<0x143>(m));  // row_bcast:31
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 63));
+  unsigned m = __float_as_uint(x);
+  m = max(m, dpp_u<0x111>(m));  // row_shr:1
+  m = max(m, dpp_u<0x112>(m));  // row_shr:2
+  m = max(m, dpp_u<0x114>(m));  // row_shr:4
+  m = max(m, dpp_u<0x118>(m));  // row_shr:8
+  m = max(m, dpp_u<0x142>(m));  // row_bcast:15
+  m = max(m, dpp_u<0x143>(m));  // row_bcast:31
+  return __uint_as_float((unsigned)__builtin_amdgcn_readlane((int)m, 63));
 }
 
 struct TpxBwdDims {
@@ -1242,7 +1249,9 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
       float gws[T::NSLOT];
 #pragma unroll
       for (int s = 0; s < T::NSLOT; ++s) gws[s] = 0.f;
-      if (valid) {
+      // a past-the-end edge computes on the clamped edge's inputs and its results are dropped
+      // (no branch); three input blocks keep the branch, whose shorter live ranges fit in registers
+      if (LIN < 3 || valid) {
         EdgeIn<LIN> in;
         in.x0 = 0.f;
 #pragma unroll
