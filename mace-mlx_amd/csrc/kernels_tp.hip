@@ -674,6 +674,9 @@ constexpr int gmax() {
 // and that count rounded up to four (the row stride in LDS)
 constexpr int tpx_tab(int l1) { return l1 == 0 ? 16 : l1 == 1 ? TP3_M1_NE : TP3_M2_NE; }
 constexpr int tpx_tab_pad(int l1) { return (tpx_tab(l1) + 3) & ~3; }
+// steps per w tile of the fused forward: two (one barrier per two steps) where the doubled LDS
+// tile still leaves the block's occupancy unchanged (one input block runs two blocks per CU)
+constexpr int tpx_fwd_steps(int lin) { return lin == 1 ? 1 : 2; }
 
 // scalar parameters of the fused forward (pointers are passed separately, as
 // __restrict__ kernel arguments: uniform loads through them then use the
@@ -700,7 +703,8 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   using GR = GrpT<LIN, L1>;
   constexpr int G = GR::G, CT = 4 * G, NCTW = (CT + XW - 1) / XW, RS = 64 * G + 4;
   constexpr int DIN = NC * LIN * LIN, DMID = NC * T::NACC, NX = 2 * L1 + 1;
-  constexpr int TC = XW * EPW, NTC = TC / 16;  // tile columns (edges) per step; 16-column MFMA tiles
+  // steps per w tile (one barrier each), tile columns (edges) per tile, 16-column MFMA tiles
+  constexpr int TPS = tpx_fwd_steps(LIN), TC = XW * EPW * TPS, NTC = TC / 16;
   // wave index through readfirstlane: receiver, edge indices and senders are then
   // wave-uniform scalars (scalar loads, no vector-memory waits on the prefetches)
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -771,11 +775,15 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   constexpr int TPR = 512 / TC, HQ = 128 / TPR;  // threads per tile row; fp16 entries per thread
   typedef unsigned hv __attribute__((ext_vector_type(HQ / 2)));
   const int hr = threadIdx.x / TPR, hpl = (threadIdx.x % TPR) / (TPR / 2), hq = threadIdx.x % (TPR / 2);
-  const int hn = nb0 + hr / EPW;
+  // tile column hr: step TPS t + hr / 16 of the tile, edge hr % EPW of receiver nb0 + (hr % 16) / EPW
+  const int hn = nb0 + (hr % 16) / EPW, hs = hr / 16;
   const int hb0 = rowptr[min(hn, a.N)];
+  struct HSlot {
+    hv h;        // this thread's share of a tile's h3 rows
+    float hinv;  // inverse scale of its row
+  };
+  HSlot H;
   struct Slot {
-    hv h;               // this thread's share of the step's h3 tile
-    float hinv;         // inverse scale of its row
     float x[EPW][NX];   // sender rows of the wave's edges
     float t[EPW][TL];   // their table rows (this lane's entries; l1 = 1: Y components)
     int snd[EPW];       // sender indices
@@ -785,14 +793,15 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 #pragma unroll
     for (int b = 0; b < EPW; ++b) S.snd[b] = sender[min<int64_t>(beg + EPW * j + b, elast)];
   };
-  auto load_h = [&](int j, Slot& S) {
-    const int64_t row = min<int64_t>(hb0 + EPW * j + hr % EPW, elast);  // columns past a receiver's end: not stored
-    S.h = *reinterpret_cast<const hv*>(h3x + row * 2 * XH + hpl * XH + HQ * hq);
-    S.hinv = h3inv[row];
+  auto load_h = [&](int t) {  // tile t's share
+    // columns past a receiver's end: not stored
+    const int64_t row = min<int64_t>(hb0 + EPW * (TPS * t + hs) + hr % EPW, elast);
+    H.h = *reinterpret_cast<const hv*>(h3x + row * 2 * XH + hpl * XH + HQ * hq);
+    H.hinv = h3inv[row];
   };
-  auto store_h = [&](int j, const Slot& S) {  // S holds step j's tile share
-    *reinterpret_cast<hv*>(hbuf + (((j & 1) * 2 + hpl) * TC + hr) * 72 + HQ * hq) = S.h;
-    if (hpl == 0 && hq == 0) hiv[(j & 1) * TC + hr] = S.hinv;
+  auto store_h = [&](int t) {  // H holds tile t's share
+    *reinterpret_cast<hv*>(hbuf + (((t & 1) * 2 + hpl) * TC + hr) * 72 + HQ * hq) = H.h;
+    if (hpl == 0 && hq == 0) hiv[(t & 1) * TC + hr] = H.hinv;
   };
   auto load_slot = [&](int j, Slot& S) {  // S.snd already holds step j's indices
 #pragma unroll
@@ -812,14 +821,15 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   float acc[T::NACC];
 #pragma unroll
   for (int q = 0; q < T::NACC; ++q) acc[q] = 0.f;
-  auto step = [&](int j, Slot& S, Slot& Snext) {
-    float* tile = sw + (j & 1) * TC * RS;
-    load_h(j + 2, S);  // S's share of step j was staged during step j - 1
+  // w tile t (the columns of steps TPS t .. TPS t + TPS - 1): this wave's column tiles of
+  // W3^T h3, from the h3 rows staged in hbuf t & 1, into LDS buffer t & 1
+  auto products = [&](int t) {
+    float* tile = sw + (t & 1) * TC * RS;
 #pragma unroll
     for (int t2 = 0; t2 < NTC; ++t2) {
       h8 bx[2][2];  // B fragments of tile column 16 t2 + r: [k step][hi, lo]
       const int col = 16 * t2 + r;
-      const _Float16* hrow = hbuf + ((j & 1) * 2 * TC + col) * 72 + 8 * g;
+      const _Float16* hrow = hbuf + ((t & 1) * 2 * TC + col) * 72 + 8 * g;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         bx[c][0] = *reinterpret_cast<const h8*>(hrow + 32 * c);
@@ -836,7 +846,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
           for (int m = 0; m < NCTW; ++m)
             if (CT % XW == 0 || wv + XW * m < CT)  // every wave's tiles exist when XW divides CT
               d[m] = mfma16h(wa[m][c][p == 2 ? 0 : p ^ 1], bx[c][p == 1 ? 1 : 0], d[m]);  // lo.hi, hi.lo, hi.hi
-      const float bsc = hiv[(j & 1) * TC + col] * a.wscale;
+      const float bsc = hiv[(t & 1) * TC + col] * a.wscale;
 #pragma unroll
       for (int m = 0; m < NCTW; ++m) {
         const int ct = wv + XW * m;
@@ -845,8 +855,18 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
               float4{qh(d[m][0] * bsc, RND), qh(d[m][1] * bsc, RND), qh(d[m][2] * bsc, RND), qh(d[m][3] * bsc, RND)};
       }
     }
-    store_h(j + 1, Snext);  // its last readers (step j - 1) are past the previous barrier
+  };
+  // tile t: its products, the next tile's h3 rows staged (their last readers, products(t - 1),
+  // are past the previous barrier) and the one after fetched, then the barrier that publishes it
+  auto tile_begin = [&](int t) {
+    products(t);
+    store_h(t + 1);
+    load_h(t + 2);
     __syncthreads();
+  };
+  // the channel-wise TP of the wave's edges of step j (w tile j / TPS) and the w stores
+  auto edges = [&](int j, Slot& S, Slot& Snext) {
+    const float* tile = sw + ((j / TPS) & 1) * TC * RS;
     if constexpr (L1 >= 1) {  // M1 / M2 rows from the Y rows: the terms and order of k_edge_fwd
 #pragma unroll
       for (int b = 0; b < EPW; ++b)
@@ -873,7 +893,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
       const int e = beg + EPW * j + b;
       const bool valid = e < end;
       float wv_s[T::NSLOT];
-      const float* trow = tile + (EPW * wv + b) * RS + u;
+      const float* trow = tile + (16 * (j % TPS) + EPW * wv + b) * RS + u;
 #pragma unroll
       for (int s = 0; s < T::NSLOT; ++s)
         if (T::l1(s) == L1) wv_s[s] = trow[64 * GR::local(s)];
@@ -904,22 +924,24 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
     wave_sync();  // table row reads done before the next step's store
     load_slot(j + 2, S);  // S.snd was refilled with step j + 2's indices during step j - 1
   };
-  const int nsteps2 = (nsteps + 1) & ~1;  // even: both ring slots every trip
+  const int nsteps2 = (nsteps + 1) & ~1;  // even: both ring slots every trip (TPS divides it)
   if (nsteps2 > 0) {
     load_snd(0, s0);
     load_snd(1, s1);
-    load_h(0, s0);
-    load_h(1, s1);
+    load_h(0);
     load_slot(0, s0);
     load_slot(1, s1);
     load_snd(2, s0);
-    store_h(0, s0);
+    store_h(0);
+    load_h(1);
     __syncthreads();  // nsteps2 is uniform over the block
   }
 #pragma unroll 1
   for (int j = 0; j < nsteps2; j += 2) {
-    step(j, s0, s1);
-    step(j + 1, s1, s0);
+    tile_begin(j / TPS);
+    edges(j, s0, s1);
+    if constexpr (TPS == 1) tile_begin(j + 1);
+    edges(j + 1, s1, s0);
   }
   if (n < a.N) {
     float* Mn = M + (int64_t)n * DMID + c0 + u;
@@ -935,10 +957,10 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 // of rounded h3 and weights have zero lo planes, so w is the float32 product, then rounded)
 template <int LIN, int RND>
 __global__ void __launch_bounds__(64 * XW, 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_PTRS) {
-  constexpr int TC = XW * EPW;
+  constexpr int TC = XW * EPW * tpx_fwd_steps(LIN);
   __shared__ __align__(16) float sw[2 * TC * (64 * gmax<LIN>() + 4)];
   __shared__ __align__(16) float stab[XW * EPW * (tpx_tab_pad(LIN - 1) + 16)];  // table rows + Y rows
-  __shared__ __align__(16) _Float16 hbuf[2 * 2 * TC * 72];  // [step][hi, lo][tile column][64 + pad]
+  __shared__ __align__(16) _Float16 hbuf[2 * 2 * TC * 72];  // [tile][hi, lo][tile column][64 + pad]
   __shared__ float hiv[2 * TC];
   if constexpr (LIN == 1) {
     tpx_fwd<1, 0, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
