@@ -429,6 +429,26 @@ def test_isolated_atoms_and_no_edges(small):
     assert abs(a["E"] - ref["E"]) < 1e-5
 
 
+@pytest.mark.parametrize("arch", ["medium", "large"])
+def test_ragged_degrees_fused_tp(arch, request):
+    """The fused TP kernels' block-level step structure on ragged rows: a block of eight
+    receivers with no edges at all (the VJP's early exit), blocks whose receivers have 0 to a few
+    edges (one or two steps, padding lanes and padding edges in every tile), next to a dense
+    cluster (tens of edges per receiver) - E, F and virial against the oracle."""
+    case = request.getfixturevalue(arch)
+    lone = np.array([[4.0 + 9.0 * (i % 4), 4.0 + 9.0 * (i // 4), 40.0] for i in range(8)])  # atoms 0-7: isolated
+    chain = np.array([[3.0 + 2.3 * i, 20.0, 20.0 + 0.3 * (i % 2)] for i in range(9)])  # 2-4 neighbours
+    cluster = 30.0 + rattle(diamond_si((2, 2, 2)), 0.05, 5).positions  # 64 atoms: tens of neighbours
+    pos = np.concatenate([lone, chain, cluster])
+    s = System(pos, np.full(len(pos), 14), np.eye(3) * 60.0, np.array([True, True, True]))
+    got = case.run(s, stress=True)
+    edges = case.edges()
+    deg = np.bincount(edges[1], minlength=len(s))
+    assert (deg[:8] == 0).all() and deg[8:17].max() <= 6 and deg[17:].min() >= 8
+    assert_parity(got, case.reference(s, got["sp"], edges, stress=True), len(s), stress=True,
+                  energy="per_atom" if arch == "large" else "relative")
+
+
 def test_deterministic_and_edge_order_independent(medium_zbl):
     s = make_config(1).system
     a = medium_zbl.run(s, force_nl=True)
