@@ -372,6 +372,16 @@ std::vector<float> transpose(const std::vector<float>& a, int rows, int cols, in
   return t;
 }
 
+// split operands of the radial output matrix w3 [64][W]: largest magnitude scaled into [2^14, 2^15)
+void upload_w3_split(mace_ctx* c, Layer& L, const std::vector<float>& w3) {
+  float m = 0.f;
+  for (float x : w3) m = std::max(m, std::fabs(x));
+  const int ex = m > 0.f ? std::ilogb(m) : 0;
+  L.w3inv = std::ldexp(1.f, ex - 14);
+  upload_split(c, L.mlpT3x, transpose(w3, RADIAL_H, L.wn), std::ldexp(1.f, 14 - ex));
+  upload_split(c, L.mlp3x, w3, std::ldexp(1.f, 14 - ex));
+}
+
 void invalidate_graphs(mace_ctx* c);
 void invalidate_node_state(mace_ctx* c);
 
@@ -467,6 +477,7 @@ void build_layer_nonlin(mace_ctx* c, Layer& L, int l) {
     const auto& w3 = tensor(c, p + "mlp.3", (size_t)RADIAL_H * L.wn);
     upload(c, L.mlp[3], w3);
     upload(c, L.mlpT[3], transpose(w3, RADIAL_H, L.wn));
+    upload_w3_split(c, L, w3);
     upload(c, L.dmlp_ts, tensor(c, p + "dmlp.ts", (size_t)nel * RADIAL_H));
     upload(c, L.dmlp_tt, tensor(c, p + "dmlp.tt", (size_t)nel * RADIAL_H));
     upload(c, L.dmlp_ln, tensor(c, p + "dmlp.ln", (size_t)2 * RADIAL_H));
@@ -589,14 +600,7 @@ void build_model(mace_ctx* c) {
           upload_half(c, L.mlpT3h, transpose(w, rows[k], cols[k]));
           upload_half(c, L.mlp3h, w);
         }
-        if (k == 3) {  // split operands: largest magnitude scaled into [2^14, 2^15)
-          float m = 0.f;
-          for (float x : w) m = std::max(m, std::fabs(x));
-          const int ex = m > 0.f ? std::ilogb(m) : 0;
-          L.w3inv = std::ldexp(1.f, ex - 14);
-          upload_split(c, L.mlpT3x, transpose(w, rows[k], cols[k]), std::ldexp(1.f, 14 - ex));
-          upload_split(c, L.mlp3x, w, std::ldexp(1.f, 14 - ex));
-        }
+        if (k == 3) upload_w3_split(c, L, w);
       }
       L.mlp_tiles.ensure(mlp_tile_bytes());
       launch_mlp_permute(c->stream, nb, L.mlp[0].p, L.mlp[1].p, L.mlp[2].p, L.mlp_tiles.p);
@@ -1262,14 +1266,18 @@ void forward_nonlin(mace_ctx* c, int l, const float* h, float* hn) {
   const int64_t E = c->E;
   const int nb = c->dims.num_bessel;
   const float* cut = c->dims.separate_cutoff ? c->cutv.p : nullptr;
+  const bool split = c->split_products;  // h3 W3 on fp16 matrix cores (split operands)
   {  // LayerNorm radial MLP (last hidden activation) and the edge densities
     Site s(c, lname("mlp_ln", l));
     launch_rmlp_ln_fwd(st, E, nb, c->ef.p, cut, c->sender.p, c->receiver.p, c->species.p, L.mlp_tiles.p,
-                       L.dmlp_tiles.p, L.lnp(), c->h3.p, c->mh_dens.p);
+                       L.dmlp_tiles.p, L.lnp(), c->h3.p, split ? c->h3inv.p : nullptr, c->mh_dens.p);
   }
   {  // w = (h3 W3 + b3) cut
     Site s(c, lname("mlp_out", l));
-    launch_mlp_out(st, E, L.wn, c->h3.p, L.mlpT[3].p, L.w.p, 0, L.b3.p, cut);
+    if (split)
+      launch_mlp_out_x(st, E, L.wn, c->h3.p, c->h3inv.p, L.mlpT3x.p, L.w3inv, L.w.p, L.b3.p, cut);
+    else
+      launch_mlp_out(st, E, L.wn, c->h3.p, L.mlpT[3].p, L.w.p, 0, L.b3.p, cut);
   }
   if (l > 0) {  // the first layer's comes from the species table (launch_embed)
     Site s(c, lname("linear_up", l));
@@ -1410,7 +1418,10 @@ void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int fi
   }
   {  // G = gw W3^T (into h3), gwb = gw . b3
     Site s(c, lname("mlp_gh3", l));
-    launch_mlp_gh3(st, E, Ly.wn, c->gw.p, Ly.mlp[3].p, c->h3.p, Ly.b3.p, c->gwb.p);
+    if (c->split_products)
+      launch_mlp_gh3_x(st, E, Ly.wn, c->gw.p, Ly.mlp3x.p, Ly.w3inv, c->h3.p, Ly.b3.p, c->gwb.p);
+    else
+      launch_mlp_gh3(st, E, Ly.wn, c->gw.p, Ly.mlp[3].p, c->h3.p, Ly.b3.p, c->gwb.p);
   }
   {
     Site s(c, lname("mlp_ln_bwd", l));
@@ -1501,7 +1512,7 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
       if (h16)
         launch_mlp_out(st, E, L.wn, c->h3h.p, L.mlpT3h.p, L.wh.p, RND_F16, nullptr, nullptr);
       else if (split)
-        launch_mlp_out_x(st, E, L.wn, c->h3.p, c->h3inv.p, L.mlpT3x.p, L.w3inv, L.w.p);
+        launch_mlp_out_x(st, E, L.wn, c->h3.p, c->h3inv.p, L.mlpT3x.p, L.w3inv, L.w.p, nullptr, nullptr);
       else
         launch_mlp_out(st, E, L.wn, c->h3.p, L.mlpT[3].p, L.w.p, half, nullptr, nullptr);
     }
@@ -1687,7 +1698,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
       if (h16)
         launch_mlp_gh3_h(st, E, Ly.wn, c->gwh.p, c->gscale.p, Ly.mlp3h.p, c->h3.p);
       else if (split)
-        launch_mlp_gh3_x(st, E, Ly.wn, c->gw.p, Ly.mlp3x.p, Ly.w3inv, c->h3.p);
+        launch_mlp_gh3_x(st, E, Ly.wn, c->gw.p, Ly.mlp3x.p, Ly.w3inv, c->h3.p, nullptr, nullptr);
       else
         launch_mlp_gh3(st, E, Ly.wn, c->gw.p, Ly.mlp[3].p, c->h3.p, nullptr, nullptr);
     }

@@ -174,9 +174,9 @@ void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tile
 void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void* W3T, void* w,
                     int rnd, const float* bias, const float* rs);
 // float32 policy on fp16 matrix cores: w (fp32) from the split h3 of mode 2 and W3Tx = [hi | lo]
-// fp16 planes of W3^T [W][64] scaled by 1 / cscale
+// fp16 planes of W3^T [W][64] scaled by 1 / cscale; bias ([W]) and rs ([E]) as launch_mlp_out
 void launch_mlp_out_x(hipStream_t st, int64_t E, int W, const void* h3x, const float* h3inv,
-                      const void* W3Tx, float cscale, float* w);
+                      const void* W3Tx, float cscale, float* w, const float* bias, const float* rs);
 // VJP: gh3 = gw W3^T, then gef (+)= dL/def through the hidden layers (saved silu' values);
 // with b3 ([W]) also gwb[e] = gw[e] . b3
 void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3,
@@ -197,10 +197,12 @@ struct LnMlpParams {
   const float* dln;   // [2][64]
   const float* dw1;   // [65]: output weights, then the output bias
 };
-// h3 [E][64] = silu(LN(...)) of the third layer; dens[e] = tanh(x^2) cut[e] (cut may be null: 1)
+// h3 = silu(LN(...)) of the third layer, fp32 [E][64] with h3inv null, else split pairs
+// [E][2][64] with inverse row scales h3inv[E] (as launch_mlp_hidden mode 2);
+// dens[e] = tanh(x^2) cut[e] (cut may be null: 1)
 void launch_rmlp_ln_fwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut,
                         const int* sender, const int* receiver, const int* species, const void* tiles,
-                        const void* dtiles, const LnMlpParams& P, float* h3, float* dens);
+                        const void* dtiles, const LnMlpParams& P, void* h3, float* h3inv, float* dens);
 // VJP from G = gw W3^T ([E][64]), gwb = gw . b3 ([E]) and drho ([N], dL/d(sum of the receiver's
 // edge densities)): gef (+)= dL/def ([E][nb]) and, with cut, gcut (+)= dL/dcut ([E]);
 // btiles / dbtiles: the transposed images (launch_mlp_permute's second half)
@@ -226,9 +228,10 @@ void launch_mh1_drho(hipStream_t st, int N, const float* gP, const float* Q, con
 void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const float* gscale, const void* W3h,
                       float* gh3);
 // float32 policy on fp16 matrix cores: gw fp32 [E][W] (split per edge and 32-wide k chunk in the
-// kernel), W3x = [hi | lo] fp16 planes of W3 [64][W] scaled by 1 / cscale
+// kernel), W3x = [hi | lo] fp16 planes of W3 [64][W] scaled by 1 / cscale; b3 and gwb as
+// launch_mlp_gh3
 void launch_mlp_gh3_x(hipStream_t st, int64_t E, int W, const float* gw, const void* W3x, float cscale,
-                      float* gh3);
+                      float* gh3, const float* b3, float* gwb);
 void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const void* tiles, const float* ds,
                            const float* gh3, float* gef, int accumulate);
 

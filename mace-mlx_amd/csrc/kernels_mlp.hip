@@ -431,11 +431,13 @@ __global__ void __launch_bounds__(256) k_mlp_out_h(int64_t E, int W, const _Floa
 // the split residuals are about 2^-22 of |a b|).  W3Tx = [hi | lo] planes of W3^T
 // [W][64].  Tiling, prefetch and the LDS-staged 128-byte row stores as in
 // k_mlp_out (stores nontemporal: the TP kernel streams w back with nontemporal loads);
-// the row scales are applied when the tile is staged.
+// the row scales are applied when the tile is staged.  bias ([W]) and cut ([E]), each
+// optional, make it w = (h3 W3 + bias) cut[e] (the mh-1 output layer).
 __global__ void __launch_bounds__(256) k_mlp_out_x(int64_t E, int W, const _Float16* __restrict__ h3x,
                                                    const float* __restrict__ h3inv,
                                                    const _Float16* __restrict__ W3Tx, float cscale,
-                                                   float* __restrict__ w) {
+                                                   float* __restrict__ w, const float* __restrict__ bias,
+                                                   const float* __restrict__ cut) {
   __shared__ __align__(16) float sO[4][64][36];
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t row0 = (int64_t)blockIdx.x * 64;
@@ -503,9 +505,12 @@ __global__ void __launch_bounds__(256) k_mlp_out_x(int64_t E, int W, const _Floa
     for (int q = 0; q < 8; ++q) {  // lane l: row l/8 + 8q, columns 4 (l%8) .. + 3
       const int rr = (l >> 3) + 8 * q;
       const int64_t row = row0 + rr;
-      if (row < E && c0 + 4 * (l & 7) < ce)
-        __builtin_nontemporal_store(*reinterpret_cast<const f4v*>(&O[rr][4 * (l & 7)]),
-                                    reinterpret_cast<f4v*>(&w[row * W + c0 + 4 * (l & 7)]));
+      if (row < E && c0 + 4 * (l & 7) < ce) {
+        f4v o = *reinterpret_cast<const f4v*>(&O[rr][4 * (l & 7)]);
+        if (bias) o += *reinterpret_cast<const f4v*>(bias + c0 + 4 * (l & 7));
+        if (cut) o *= cut[row];
+        __builtin_nontemporal_store(o, reinterpret_cast<f4v*>(&w[row * W + c0 + 4 * (l & 7)]));
+      }
     }
     wave_sync();
 #pragma unroll
@@ -710,13 +715,15 @@ __global__ void __launch_bounds__(256) k_mlp_gh3_h(int64_t E, int W, const _Floa
 // the four lanes of the edge) into [2^14, 2^15), splits them into fp16 hi + lo and
 // folds the inverse scale into its accumulators after the stage's products
 //   W3_hi x gw_lo + W3_lo x gw_hi + W3_hi x gw_hi
-// (about 2^-22 relative per product).  gw loaded two stages ahead.
+// (about 2^-22 relative per product).  gw loaded two stages ahead.  b3 (optional,
+// [W]): also gwb[e] = gw[e] . b3 in fp32, per lane, then over the edge's four lanes.
 constexpr int GX_KS = 64;       // k per stage (one scale, one barrier)
 constexpr int GX_RS = GX_KS + 8;
 
 __global__ void __launch_bounds__(256) k_mlp_gh3_x(int64_t E, int W, const float* __restrict__ gw,
                                                    const _Float16* __restrict__ W3x, float cscale,
-                                                   float* __restrict__ gh3) {
+                                                   float* __restrict__ gh3, const float* __restrict__ b3,
+                                                   float* __restrict__ gwb) {
   __shared__ __align__(16) _Float16 sB[2][2][H][GX_RS];  // [buffer][hi, lo][j][k of the stage]
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t row0 = ((int64_t)blockIdx.x * 4 + wv) * 16, lo_b = (int64_t)H * W;
@@ -757,6 +764,7 @@ __global__ void __launch_bounds__(256) k_mlp_gh3_x(int64_t E, int W, const float
   f4v acc[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) acc[u] = f4v{0.f, 0.f, 0.f, 0.f};
+  float pb = 0.f;  // this lane's share of gw . b3
   for (int s0 = 0; s0 < nst; s0 += 2) {
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
@@ -769,6 +777,15 @@ __global__ void __launch_bounds__(256) k_mlp_gh3_x(int64_t E, int W, const float
         for (int q = 0; q < 2; ++q) cur[q][0] = ring[p][q][0], cur[q][1] = ring[p][q][1];
         load_x(min(st + 2, nst - 1), ring[p]);
         __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the arithmetic
+        if (b3) {
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const float4 bb = ld4(b3 + GX_KS * st + 32 * q + 8 * g + 4 * h), x = cur[q][h];
+              pb = fmaf(x.w, bb.w, fmaf(x.z, bb.z, fmaf(x.y, bb.y, fmaf(x.x, bb.x, pb))));
+            }
+        }
         float m = 0.f;
 #pragma unroll
         for (int q = 0; q < 2; ++q)
@@ -815,6 +832,10 @@ __global__ void __launch_bounds__(256) k_mlp_gh3_x(int64_t E, int W, const float
     }
   }
   const int64_t row = row0 + r;  // lane (g, r) holds gh3[row][16u + 4g + i]
+  if (b3) {
+    pb = sum4_rows(pb);
+    if (g == 0 && row < E) gwb[row] = pb;
+  }
   if (row < E)
 #pragma unroll
     for (int u = 0; u < 4; ++u)
@@ -1332,7 +1353,8 @@ __global__ void __launch_bounds__(256) k_rmlp_ln_fwd(int64_t E, int nb, const fl
                                                      const int* __restrict__ receiver,
                                                      const int* __restrict__ species, const MlpFwdW* __restrict__ tiles,
                                                      const MlpFwdW* __restrict__ dtiles, LnMlpParams P,
-                                                     float* __restrict__ h3, float* __restrict__ dens) {
+                                                     void* __restrict__ h3, float* __restrict__ h3inv,
+                                                     float* __restrict__ dens) {
   __shared__ MlpFwdW sw;
   __shared__ float4 sdw0[NB4][4][16];
   __shared__ LnSmall S;
@@ -1347,13 +1369,33 @@ __global__ void __launch_bounds__(256) k_rmlp_ln_fwd(int64_t E, int nb, const fl
     const int zs = species[sender[ec]], zr = species[receiver[ec]];
     LnFwdState F;
     ln_mlp_fwd(sw, sdw0, S, P, ef, ec, nb, zs, zr, F);
-    if (e < E) {
+    if (h3inv) {  // split pairs [E][2][64] with the row scale's inverse, as k_mlp_hidden_x writes them
+      float inv;
+      const float sc = edge_scale<16>(F.h3, &inv);
+      if (e < E) {
+        _Float16* dst = static_cast<_Float16*>(h3) + e * 2 * H;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          h4 hi, lo;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            _Float16 a, b;
+            split_pair(F.h3[4 * t + i] * sc, a, b);
+            hi[i] = a;
+            lo[i] = b;
+          }
+          *reinterpret_cast<h4*>(dst + 16 * t + 4 * g) = hi;
+          *reinterpret_cast<h4*>(dst + H + 16 * t + 4 * g) = lo;
+        }
+        if (g == 0) h3inv[e] = inv;
+      }
+    } else if (e < E) {
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        *reinterpret_cast<float4*>(h3 + e * H + 16 * t + 4 * g) =
+        *reinterpret_cast<float4*>(static_cast<float*>(h3) + e * H + 16 * t + 4 * g) =
             float4{F.h3[4 * t], F.h3[4 * t + 1], F.h3[4 * t + 2], F.h3[4 * t + 3]};
-      if (g == 0) dens[e] = tanhf(F.x * F.x) * (cut ? cut[e] : 1.f);
     }
+    if (e < E && g == 0) dens[e] = tanhf(F.x * F.x) * (cut ? cut[e] : 1.f);
   }
 }
 
@@ -1556,10 +1598,10 @@ void launch_mlp_out(hipStream_t st, int64_t E, int W, const void* h3, const void
 }
 
 void launch_mlp_out_x(hipStream_t st, int64_t E, int W, const void* h3x, const float* h3inv, const void* W3Tx,
-                      float cscale, float* w) {
+                      float cscale, float* w, const float* bias, const float* rs) {
   if (E <= 0) return;
   MACE_LAUNCH(k_mlp_out_x, dim3(nblk(E, 64), 2), dim3(256), 0, st, E, W, static_cast<const _Float16*>(h3x),
-                     h3inv, static_cast<const _Float16*>(W3Tx), cscale, w);
+                     h3inv, static_cast<const _Float16*>(W3Tx), cscale, w, bias, rs);
 }
 
 void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const float* W3, float* gh3,
@@ -1569,10 +1611,10 @@ void launch_mlp_gh3(hipStream_t st, int64_t E, int W, const float* gw, const flo
 }
 
 void launch_mlp_gh3_x(hipStream_t st, int64_t E, int W, const float* gw, const void* W3x, float cscale,
-                      float* gh3) {
+                      float* gh3, const float* b3, float* gwb) {
   if (E <= 0) return;
   MACE_LAUNCH(k_mlp_gh3_x, dim3(nblk(E, 64)), dim3(256), 0, st, E, W, gw,
-                     static_cast<const _Float16*>(W3x), cscale, gh3);
+                     static_cast<const _Float16*>(W3x), cscale, gh3, b3, gwb);
 }
 
 void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const float* gscale, const void* W3h,
@@ -1593,10 +1635,10 @@ size_t mlp_tile_fwd_bytes() { return sizeof(MlpFwdW); }
 
 void launch_rmlp_ln_fwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut, const int* sender,
                         const int* receiver, const int* species, const void* tiles, const void* dtiles,
-                        const LnMlpParams& P, float* h3, float* dens) {
+                        const LnMlpParams& P, void* h3, float* h3inv, float* dens) {
   if (E <= 0) return;
   MACE_LAUNCH(k_rmlp_ln_fwd, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, cut, sender, receiver, species,
-              static_cast<const MlpFwdW*>(tiles), static_cast<const MlpFwdW*>(dtiles), P, h3, dens);
+              static_cast<const MlpFwdW*>(tiles), static_cast<const MlpFwdW*>(dtiles), P, h3, h3inv, dens);
 }
 
 void launch_rmlp_ln_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut, const int* sender,
