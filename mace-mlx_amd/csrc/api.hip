@@ -711,9 +711,9 @@ void ensure_node_buffers(mace_ctx* c) {
 }
 
 // Which kernels a step runs (from the model and the two switches).  fused: the radial-MLP
-// output layer inside the TP kernels (split products, standard interaction blocks), under
-// every feature policy (the rounding modes are template
-// parameters of the fused forward); split: the radial MLP's hidden layers on split-fp16
+// output layer inside the TP kernels (split products), under every feature policy (the
+// rounding modes are template parameters of the fused forward; the non-linear interaction
+// block exists under the float32 policy only); split: the radial MLP's hidden layers on split-fp16
 // products (fused path, or the float32 policy); h16: the float16 policy's separate path with
 // fp16 h3 / w / dL/dw arrays.  Neither split nor h16: fp32 products, silu' saved (ds).
 struct StepPath {
@@ -721,7 +721,7 @@ struct StepPath {
 };
 StepPath step_path(const mace_ctx* c) {
   StepPath p;
-  p.fused = c->split_products && c->fused_tp && !c->dims.nonlinear;
+  p.fused = c->split_products && c->fused_tp;
   p.split = p.fused || (c->dims.feature_half == RND_NONE && c->split_products);
   p.h16 = !p.split && c->dims.feature_half == RND_F16;
   return p;
@@ -746,7 +746,7 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   for (size_t l = 1; l < c->layers.size(); ++l) maxdin = std::max(maxdin, (size_t)c->layers[l].dtp());
   if (!c->layers.empty() && c->layers[0].nonlin) {
     c->mh_dens.ensure(e);
-    c->gwb.ensure(e);
+    c->gwb.ensure(e * kGyMax);  // gw . b3, one partial per fused-VJP block column
     if (c->dims.separate_cutoff) c->cutv.ensure(e), c->gcut.ensure(e);
   }
   if (maxdin > 0) c->gxe.ensure(e * maxdin);
@@ -1267,12 +1267,13 @@ void forward_nonlin(mace_ctx* c, int l, const float* h, float* hn) {
   const int nb = c->dims.num_bessel;
   const float* cut = c->dims.separate_cutoff ? c->cutv.p : nullptr;
   const bool split = c->split_products;  // h3 W3 on fp16 matrix cores (split operands)
+  const bool fused = step_path(c).fused;   // ... inside the TP kernels
   {  // LayerNorm radial MLP (last hidden activation) and the edge densities
     Site s(c, lname("mlp_ln", l));
     launch_rmlp_ln_fwd(st, E, nb, c->ef.p, cut, c->sender.p, c->receiver.p, c->species.p, L.mlp_tiles.p,
                        L.dmlp_tiles.p, L.lnp(), c->h3.p, split ? c->h3inv.p : nullptr, c->mh_dens.p);
   }
-  {  // w = (h3 W3 + b3) cut
+  if (!fused) {  // w = (h3 W3 + b3) cut
     Site s(c, lname("mlp_out", l));
     if (split)
       launch_mlp_out_x(st, E, L.wn, c->h3.p, c->h3inv.p, L.mlpT3x.p, L.w3inv, L.w.p, L.b3.p, cut);
@@ -1289,7 +1290,11 @@ void forward_nonlin(mace_ctx* c, int l, const float* h, float* hn) {
   }
   {
     Site s(c, lname("tp_fwd", l));
-    launch_tp_fwd(st, L.ledge, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.w.p, L.h_up.p, c->M.p, 0);
+    if (fused)  // w = (h3 W3 + b3) cut formed per edge tile, and stored for the VJP
+      launch_tpx_fwd(st, L.ledge, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, c->h3.p, c->h3inv.p,
+                     L.mlpT3x.p, L.wn, L.w3inv, L.h_up.p, c->M.p, L.w.p, RND_NONE, L.b3.p, cut);
+    else
+      launch_tp_fwd(st, L.ledge, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.w.p, L.h_up.p, c->M.p, 0);
   }
   {  // rinv = 1 / (beta rho + alpha)
     Site s(c, lname("density", l));
@@ -1357,7 +1362,7 @@ void forward_nonlin(mace_ctx* c, int l, const float* h, float* hn) {
 
 // VJP of forward_nonlin: from gh = dE/dh_{l+1}; for l > 0 writes gh_next = dE/dh_l (with the
 // previous layer's linear readout as the 0e bias)
-void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int first_edge_grad) {
+void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int first_edge_grad, int gyp) {
   hipStream_t st = c->stream;
   Layer& Ly = c->layers[l];
   const int N = c->N;
@@ -1406,7 +1411,18 @@ void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int fi
     }
     run_gemm(c, st, g);
   }
-  {
+  const bool fused = step_path(c).fused;
+  if (fused) {  // dL/dw stays on chip: G = gw W3^T and gw . b3 as per-block-column partials
+    Site s(c, lname("tp_bwd", l));
+    int acc_gy = first_edge_grad;
+    if (!acc_gy && tpx_parts(Ly.ledge) < gyp) {  // partials this layer does not write start at zero
+      launch_fill_zero(st, c->gY.p, E * 16 * gyp);
+      acc_gy = 1;
+    }
+    launch_tpx_bwd(st, Ly.ledge, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p, Ly.mlp3x.p, Ly.wn,
+                   Ly.w3inv, Ly.h_up.p, c->gM.p, c->pos_s.p, l > 0 ? c->gxe.p : nullptr, c->gY.p, gyp, acc_gy,
+                   c->gh3p.p, RND_NONE, Ly.b3.p, c->gwb.p);
+  } else {
     Site s(c, lname("tp_bwd", l));
     launch_tp_bwd_recv(st, Ly.ledge, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p, Ly.h_up.p,
                        c->gM.p, c->gw.p, c->gscale.p, c->gY.p, first_edge_grad, c->pos_s.p,
@@ -1416,7 +1432,7 @@ void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int fi
     Site s(c, lname("tp_gather", l));
     launch_tp_gather_gx(st, Ly.ledge, N, srow(c), c->gxe.p, c->gup.p);
   }
-  {  // G = gw W3^T (into h3), gwb = gw . b3
+  if (!fused) {  // G = gw W3^T (into h3), gwb = gw . b3
     Site s(c, lname("mlp_gh3", l));
     if (c->split_products)
       launch_mlp_gh3_x(st, E, Ly.wn, c->gw.p, Ly.mlp3x.p, Ly.w3inv, c->h3.p, Ly.b3.p, c->gwb.p);
@@ -1427,8 +1443,9 @@ void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int fi
     Site s(c, lname("mlp_ln_bwd", l));
     const size_t fb = mlp_tile_fwd_bytes();
     launch_rmlp_ln_bwd(st, E, nb, c->ef.p, cut, c->sender.p, c->receiver.p, c->species.p, Ly.mlp_tiles.p,
-                       Ly.mlp_tiles.p + fb, Ly.dmlp_tiles.p, Ly.dmlp_tiles.p + fb, Ly.lnp(), c->h3.p, c->gwb.p,
-                       c->grho.p, c->gef.p, cut ? c->gcut.p : nullptr, first_edge_grad);
+                       Ly.mlp_tiles.p + fb, Ly.dmlp_tiles.p, Ly.dmlp_tiles.p + fb, Ly.lnp(),
+                       fused ? c->gh3p.p : c->h3.p, c->gwb.p, fused ? tpx_parts(Ly.ledge) : 1, c->grho.p, c->gef.p,
+                       cut ? c->gcut.p : nullptr, first_edge_grad);
   }
   if (l == 0) return;
   {  // gup += Res^T gP
@@ -1528,7 +1545,7 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
       Site s(c, lname("tp_fwd", l));
       if (fused)
         launch_tpx_fwd(st, L.lin, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, c->h3.p, c->h3inv.p,
-                       L.mlpT3x.p, L.wn, L.w3inv, L.h_up.p, c->M.p, L.w.p, half);
+                       L.mlpT3x.p, L.wn, L.w3inv, L.h_up.p, c->M.p, L.w.p, half, nullptr, nullptr);
       else
         launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.wptr(h16), L.h_up.p,
                       c->M.p, half);
@@ -1619,14 +1636,14 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
   const bool h16 = path.h16, split = path.split, fused = path.fused;
   int gyp = 2;  // dL/dY partials per edge
   if (fused)
-    for (const Layer& Ly : c->layers) gyp = std::max(gyp, tpx_parts(Ly.lin));
+    for (const Layer& Ly : c->layers) gyp = std::max(gyp, tpx_parts(Ly.tl()));
   // dE/dh_L from the nonlinear readout: written by the forward's energy_readout pass
   float* gh = c->gh0.p;
   float* gh_next = c->gh1.p;
   for (int l = L - 1; l >= 0; --l) {
     Layer& Ly = c->layers[l];
     if (Ly.nonlin) {
-      backward_nonlin(c, l, gh, gh_next, (l == L - 1) ? 0 : 1);
+      backward_nonlin(c, l, gh, gh_next, (l == L - 1) ? 0 : 1, gyp);
       if (l > 0) std::swap(gh, gh_next);
       continue;
     }
@@ -1681,7 +1698,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
       }
       launch_tpx_bwd(st, Ly.lin, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p, Ly.mlp3x.p, Ly.wn,
                      Ly.w3inv, Ly.h_up.p, c->gM.p, c->pos_s.p, l > 0 ? c->gxe.p : nullptr, c->gY.p, gyp, acc_gy,
-                     c->gh3p.p, half);
+                     c->gh3p.p, half, nullptr, nullptr);
     } else {
       // layers after the first also need dL/dx: per-edge rows in sender order, then a segmented sum
       Site s(c, lname("tp_bwd", l));

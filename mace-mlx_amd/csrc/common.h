@@ -203,13 +203,14 @@ struct LnMlpParams {
 void launch_rmlp_ln_fwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut,
                         const int* sender, const int* receiver, const int* species, const void* tiles,
                         const void* dtiles, const LnMlpParams& P, void* h3, float* h3inv, float* dens);
-// VJP from G = gw W3^T ([E][64]), gwb = gw . b3 ([E]) and drho ([N], dL/d(sum of the receiver's
-// edge densities)): gef (+)= dL/def ([E][nb]) and, with cut, gcut (+)= dL/dcut ([E]);
-// btiles / dbtiles: the transposed images (launch_mlp_permute's second half)
+// VJP from G = gw W3^T (np partials [np][E][64], added in order), gwb = gw . b3 (np partials
+// [np][E]) and drho ([N], dL/d(sum of the receiver's edge densities)): gef (+)= dL/def ([E][nb])
+// and, with cut, gcut (+)= dL/dcut ([E]); btiles / dbtiles: the transposed images
+// (launch_mlp_permute's second half)
 void launch_rmlp_ln_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut,
                         const int* sender, const int* receiver, const int* species, const void* tiles,
                         const void* btiles, const void* dtiles, const void* dbtiles, const LnMlpParams& P,
-                        const float* G, const float* gwb, const float* drho, float* gef, float* gcut,
+                        const float* G, const float* gwb, int np, const float* drho, float* gef, float* gcut,
                         int accumulate);
 size_t mlp_tile_fwd_bytes();  // offset of the transposed image inside an mlp_tile_bytes() block
 // node side of the mh-1 block.  Q [N][kGateInDim] = linear_1(M) / (beta rho + alpha), R [N][nres]
@@ -256,19 +257,23 @@ void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const
 // (W3Tx, scale wscale), M is written as by launch_tp_fwd and w ([E][W]) for the VJP; w and
 // M rounded by rnd (RND_*, the feature policy), w stored as 16-bit fp16 / bf16 patterns under
 // RND_F16 / RND_BF16 (exact: the values are already rounded).
+// b3 (non-linear interaction block, float32 policy; null otherwise): w = (W3^T h3 + b3) cut
+// (cut [E], may be null: 1)
 void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const void* h3x, const float* h3inv, const void* W3Tx, int W,
-                    float wscale, const float* up, float* M, float* w, int rnd);
+                    float wscale, const float* up, float* M, float* w, int rnd, const float* b3, const float* cut);
 // TP VJP with the radial-MLP output layer's backward product fused in (split products,
 // lin = 1..3): reads w ([E][W], written by
 // launch_tpx_fwd), writes the dL/dh3 partials gh3p ([P][E][64], P = 2 x input
 // degrees of the layer), dL/dY partials into gY[e][p][16] (gyp partials per
 // edge; written, or added when accumulate_gY) and, with gxe, the per-edge dL/dx
-// rows as launch_tp_bwd_recv does.  wfmt: the storage format of w (the forward's rnd).
+// rows as launch_tp_bwd_recv does.  wfmt: the storage format of w (the forward's rnd).  b3
+// (non-linear interaction block, float32 policy; null otherwise): also the partials
+// gwbp[p][e] = sum over partial p's columns k of dL/dw[e][k] b3[k] ([P][E]).
 void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const float* w, const void* W3x, int W, float wscale, const float* up,
                     const float* gM, const int* pos_s, float* gxe, float* gY, int gyp, int accumulate_gY,
-                    float* gh3p, int wfmt);
+                    float* gh3p, int wfmt, const float* b3, float* gwbp);
 // p[0 .. n) = 0 (a kernel, not a memset: safe inside captured graphs)
 void launch_fill_zero(hipStream_t st, float* p, int64_t n);
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe,

@@ -1436,8 +1436,9 @@ __global__ void __launch_bounds__(256) k_rmlp_ln_bwd(int64_t E, int nb, const fl
                                                      const MlpFwdW* __restrict__ dtiles,
                                                      const MlpBwdW* __restrict__ dbtiles, LnMlpParams P,
                                                      const float* __restrict__ G, const float* __restrict__ gwb,
-                                                     const float* __restrict__ drho, float* __restrict__ gef,
-                                                     float* __restrict__ gcut, int accumulate) {
+                                                     int np, const float* __restrict__ drho,
+                                                     float* __restrict__ gef, float* __restrict__ gcut,
+                                                     int accumulate) {
   __shared__ MlpFwdW sw;
   __shared__ MlpBwdW sb;
   __shared__ float4 sdw0[NB4][4][16];
@@ -1458,13 +1459,20 @@ __global__ void __launch_bounds__(256) k_rmlp_ln_bwd(int64_t E, int nb, const fl
     LnFwdState F;
     ln_mlp_fwd(sw, sdw0, S, P, ef, ec, nb, zs, zr, F);
     const float ce = cut ? cut[ec] : 1.f;
-    float gv[16];
+    float gv[16], gb = gwb[ec];
     ld_row16(G + ec * H, g, gv);
+    for (int k = 1; k < np; ++k) {  // partials added in order
+      float t[16];
+      ld_row16(G + (k * E + ec) * H, g, t);
+#pragma unroll
+      for (int q = 0; q < 16; ++q) gv[q] += t[q];
+      gb += gwb[k * E + ec];
+    }
     // w = cut (h3 W3 + b3): dL/dcut = h3 . G + gw . b3, dL/dh3 = cut G
     float hg = 0.f;
 #pragma unroll
     for (int q = 0; q < 16; ++q) hg = fmaf(F.h3[q], gv[q], hg);
-    float gc = sum4_rows(hg) + gwb[ec];
+    float gc = sum4_rows(hg) + gb;
 #pragma unroll
     for (int q = 0; q < 16; ++q) gv[q] *= ce;
     f4v acc[4];
@@ -1644,11 +1652,11 @@ void launch_rmlp_ln_fwd(hipStream_t st, int64_t E, int nb, const float* ef, cons
 void launch_rmlp_ln_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut, const int* sender,
                         const int* receiver, const int* species, const void* tiles, const void* btiles,
                         const void* dtiles, const void* dbtiles, const LnMlpParams& P, const float* G,
-                        const float* gwb, const float* drho, float* gef, float* gcut, int accumulate) {
+                        const float* gwb, int np, const float* drho, float* gef, float* gcut, int accumulate) {
   if (E <= 0) return;
   MACE_LAUNCH(k_rmlp_ln_bwd, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, cut, sender, receiver, species,
               static_cast<const MlpFwdW*>(tiles), static_cast<const MlpBwdW*>(btiles),
-              static_cast<const MlpFwdW*>(dtiles), static_cast<const MlpBwdW*>(dbtiles), P, G, gwb, drho, gef,
+              static_cast<const MlpFwdW*>(dtiles), static_cast<const MlpBwdW*>(dbtiles), P, G, gwb, np, drho, gef,
               gcut, accumulate);
 }
 

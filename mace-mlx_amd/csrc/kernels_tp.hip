@@ -685,6 +685,9 @@ struct TpxDims {
   int N, W, mts;
   int64_t E;
   float wscale;
+  // non-linear interaction block (NL): w = (W3^T h3 + b3) cut, b3 [W], cut [E] (null: 1)
+  const float* b3;
+  const float* cut;
 };
 
 #define MACE_TPX_FWD_PTRS                                                                                   \
@@ -696,9 +699,9 @@ struct TpxDims {
 // h3x: [E][hi 64 | lo 64]; h3inv: [E]; W3Tx: [W][64] hi plane, then lo plane;
 // w: [E][W] for the VJP
 
-template <int LIN, int L1, int RND>
+template <int LIN, int L1, int RND, bool NL>
 __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, float* sw, float* stab, _Float16* hbuf,
-                                        float* hiv) {
+                                        float* hiv, float* hcv) {
   using T = TPT<LIN>;
   using GR = GrpT<LIN, L1>;
   constexpr int G = GR::G, CT = 4 * G, NCTW = (CT + XW - 1) / XW, RS = 64 * G + 4;
@@ -736,6 +739,20 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
       }
     }
   }
+  // NL: b3 of this lane's result rows (channels 16 ct + 4 g + i of the group's columns)
+  float bw[NL ? NCTW : 1][4];
+  if constexpr (NL) {
+#pragma unroll
+    for (int m = 0; m < NCTW; ++m) {
+      const int ct = wv + XW * m;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int gc = min(16 * ct + 4 * g + i, 64 * G - 1);  // rows of absent tiles: not used
+        bw[m][i] = a.b3[GR::slot(gc >> 6) * NC + c0 + (gc & 63)];
+      }
+    }
+  }
+  const auto cutv = buf_view(a.cut, a.cut ? 4u * (unsigned)a.E : 0u);
   // Every vector-memory operation below is unconditional (indices clamped, stores
   // of past-the-end edges dropped by a buffer view of size 0), so the number in
   // flight is the same on every path and the compiler's wait counts stay exact: a
@@ -781,6 +798,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   struct HSlot {
     hv h;        // this thread's share of a tile's h3 rows
     float hinv;  // inverse scale of its row
+    float cut;   // NL: its cutoff factor
   };
   HSlot H;
   struct Slot {
@@ -798,10 +816,14 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
     const int64_t row = min<int64_t>(hb0 + EPW * (TPS * t + hs) + hr % EPW, elast);
     H.h = *reinterpret_cast<const hv*>(h3x + row * 2 * XH + hpl * XH + HQ * hq);
     H.hinv = h3inv[row];
+    if constexpr (NL) H.cut = buf_load(cutv, 4u * (unsigned)row);  // 0 without a cut array
   };
   auto store_h = [&](int t) {  // H holds tile t's share
     *reinterpret_cast<hv*>(hbuf + (((t & 1) * 2 + hpl) * TC + hr) * 72 + HQ * hq) = H.h;
-    if (hpl == 0 && hq == 0) hiv[(t & 1) * TC + hr] = H.hinv;
+    if (hpl == 0 && hq == 0) {
+      hiv[(t & 1) * TC + hr] = H.hinv;
+      if constexpr (NL) hcv[(t & 1) * TC + hr] = a.cut ? H.cut : 1.f;
+    }
   };
   auto load_slot = [&](int j, Slot& S) {  // S.snd already holds step j's indices
 #pragma unroll
@@ -847,12 +869,22 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
             if (CT % XW == 0 || wv + XW * m < CT)  // every wave's tiles exist when XW divides CT
               d[m] = mfma16h(wa[m][c][p == 2 ? 0 : p ^ 1], bx[c][p == 1 ? 1 : 0], d[m]);  // lo.hi, hi.lo, hi.hi
       const float bsc = hiv[(t & 1) * TC + col] * a.wscale;
+      if constexpr (NL) {
+        const float cc = hcv[(t & 1) * TC + col];
+#pragma unroll
+        for (int m = 0; m < NCTW; ++m)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) d[m][i] = fmaf(d[m][i], bsc, bw[m][i]) * cc;
+      } else {
+#pragma unroll
+        for (int m = 0; m < NCTW; ++m) d[m] *= bsc;
+      }
 #pragma unroll
       for (int m = 0; m < NCTW; ++m) {
         const int ct = wv + XW * m;
         if (CT % XW == 0 || ct < CT)
           *reinterpret_cast<float4*>(tile + col * RS + 16 * ct + 4 * g) =
-              float4{qh(d[m][0] * bsc, RND), qh(d[m][1] * bsc, RND), qh(d[m][2] * bsc, RND), qh(d[m][3] * bsc, RND)};
+              float4{qh(d[m][0], RND), qh(d[m][1], RND), qh(d[m][2], RND), qh(d[m][3], RND)};
       }
     }
   };
@@ -955,27 +987,28 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 
 // RND: rounding mode of w and M under a half-precision feature policy (the split operands
 // of rounded h3 and weights have zero lo planes, so w is the float32 product, then rounded)
-template <int LIN, int RND>
+template <int LIN, int RND, bool NL>
 __global__ void __launch_bounds__(64 * XW, 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_PTRS) {
   constexpr int TC = XW * EPW * tpx_fwd_steps(LIN);
   __shared__ __align__(16) float sw[2 * TC * (64 * gmax<LIN>() + 4)];
   __shared__ __align__(16) float stab[XW * EPW * (tpx_tab_pad(LIN - 1) + 16)];  // table rows + Y rows
   __shared__ __align__(16) _Float16 hbuf[2 * 2 * TC * 72];  // [tile][hi, lo][tile column][64 + pad]
   __shared__ float hiv[2 * TC];
+  __shared__ float hcv[NL ? 2 * TC : 1];  // NL: the tile columns' cutoff factors
   if constexpr (LIN == 1) {
-    tpx_fwd<1, 0, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
+    tpx_fwd<1, 0, RND, NL>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv, hcv);
   } else if constexpr (LIN == 2) {
     if (blockIdx.z == 0)
-      tpx_fwd<2, 1, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
+      tpx_fwd<2, 1, RND, NL>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv, hcv);
     else
-      tpx_fwd<2, 0, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
+      tpx_fwd<2, 0, RND, NL>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv, hcv);
   } else {
     if (blockIdx.z == 0)
-      tpx_fwd<3, 2, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
+      tpx_fwd<3, 2, RND, NL>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv, hcv);
     else if (blockIdx.z == 1)
-      tpx_fwd<3, 1, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
+      tpx_fwd<3, 1, RND, NL>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv, hcv);
     else
-      tpx_fwd<3, 0, RND>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv);
+      tpx_fwd<3, 0, RND, NL>(a, MACE_TPX_FWD_ARGS, sw, stab, hbuf, hiv, hcv);
   }
 }
 
@@ -1102,6 +1135,17 @@ __device__ __forceinline__ float wave_max_nonneg(float x) {
   m = max(m, dpp_u<0x143>(m));  // row_bcast:31
   return __uint_as_float((unsigned)__builtin_amdgcn_readlane((int)m, 63));
 }
+// Sum of x over the wave, in lane 63 (the same DPP scan: row prefix sums, then the two row
+// broadcasts; lanes without a source add 0).  Fixed order, so the result is deterministic.
+__device__ __forceinline__ float wave_sum_lane63(float x) {
+  x += dpp_f<0x111>(x);  // row_shr:1
+  x += dpp_f<0x112>(x);  // row_shr:2
+  x += dpp_f<0x114>(x);  // row_shr:4
+  x += dpp_f<0x118>(x);  // row_shr:8
+  x += dpp_f<0x142>(x);  // row_bcast:15
+  x += dpp_f<0x143>(x);  // row_bcast:31
+  return x;
+}
 
 struct TpxBwdDims {
   int N, W, mts;
@@ -1109,6 +1153,10 @@ struct TpxBwdDims {
   float wscale;
   int accumulate_gY;
   int gyp;  // partials per edge in gY
+  // non-linear interaction block (NL): gwbp[p][e] = sum over partial p's columns k of
+  // dL/dw[e][k] b3[k] (b3 [W], gwbp [P][E])
+  const float* b3;
+  float* gwbp;
 };
 
 #define MACE_TPX_BWD_PTRS                                                                                   \
@@ -1119,7 +1167,7 @@ struct TpxBwdDims {
 #define MACE_TPX_BWD_ARGS rowptr, sender, Y, Mt, w, W3x, up, gM, pos_s, gxe, gY, gh3p
 // W3x: [64][W] hi plane, then lo plane; gh3p: [P][E][64]
 
-template <int LIN, int L1, bool GX, int WF>
+template <int LIN, int L1, bool GX, int WF, bool NL>
 __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, _Float16* sg, float* sinv,
                                         float* sy, float* sp, float* sm2) {
   using T = TPT<LIN>;
@@ -1156,6 +1204,14 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   // the block's edges [eb0, eb1) (its receivers' rows): a view of their dL/dh3 partial rows p
   const int eb0 = rowptr[min(nb0, a.N)], eb1 = rowptr[min(nb0 + XW, a.N)];
   const auto gh3v = buf_view(gh3p + ((int64_t)p * a.E + eb0) * XH, 4u * XH * (unsigned)(eb1 - eb0));
+  // NL: the block's entries of gw . b3 partial p, and b3 of this lane's channel in the group slots
+  const auto gwbv = buf_view(NL ? a.gwbp + (int64_t)p * a.E + eb0 : nullptr, NL ? 4u * (unsigned)(eb1 - eb0) : 0u);
+  float b3c[NL ? T::NSLOT : 1];
+  if constexpr (NL) {
+#pragma unroll
+    for (int s = 0; s < T::NSLOT; ++s)
+      if (T::l1(s) == L1) b3c[s] = a.b3[s * NC + c0 + u];
+  }
 
   // W3 rows q = 16 qt + r, group k steps kh G .. kh G + G - 1 (32 columns each)
   const int qt = wv & 3, kh = wv >> 2;
@@ -1311,6 +1367,14 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
           }
         if (l == 0) tinv[2 * wv + b] = __uint_as_float((unsigned)(127 - 14 + ex) << 23);
       }
+      if constexpr (NL) {  // gw . b3 over this block's columns, stored by lane 63
+        float pb = 0.f;
+#pragma unroll
+        for (int s = 0; s < T::NSLOT; ++s)
+          if (T::l1(s) == L1) pb = fmaf(gws[s], b3c[s], pb);
+        pb = wave_sum_lane63(pb);
+        buf_store(pb, gwbv, l == 63 && valid ? 4u * (unsigned)(e - eb0) : BUF_OOB);
+      }
       if constexpr (GX) {
         const auto gxv = buf_view(gxe + (int64_t)S.ps[b] * DIN, valid ? 4u * DIN : 0u);
 #pragma unroll
@@ -1401,7 +1465,7 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
 }
 
 // WF: storage format of w (RND_*, as the forward that wrote it)
-template <int LIN, bool GX, int WF>
+template <int LIN, bool GX, int WF, bool NL>
 __global__ void __launch_bounds__(64 * XW, 2) k_tpx_bwd(TpxBwdDims a, MACE_TPX_BWD_PTRS) {
   __shared__ __align__(16) _Float16 sg[2 * 2 * 32 * (64 * gmax<LIN>() + 8)];  // [pair][hi, lo][edge][RS]
   __shared__ float sinv[2 * 32];
@@ -1410,19 +1474,19 @@ __global__ void __launch_bounds__(64 * XW, 2) k_tpx_bwd(TpxBwdDims a, MACE_TPX_B
   __shared__ __align__(16) float sp[6 * 4 * 256];
   __shared__ __align__(16) float sm2[LIN == 3 ? XW * 2 * tpx_tab_pad(2) : 4];  // [wave][edge][M2 row]
   if constexpr (LIN == 1) {
-    tpx_bwd<1, 0, GX, WF>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+    tpx_bwd<1, 0, GX, WF, NL>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
   } else if constexpr (LIN == 2) {
     if (blockIdx.z == 0)
-      tpx_bwd<2, 1, GX, WF>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<2, 1, GX, WF, NL>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
     else
-      tpx_bwd<2, 0, GX, WF>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<2, 0, GX, WF, NL>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
   } else {
     if (blockIdx.z == 0)
-      tpx_bwd<3, 2, GX, WF>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<3, 2, GX, WF, NL>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
     else if (blockIdx.z == 1)
-      tpx_bwd<3, 1, GX, WF>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<3, 1, GX, WF, NL>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
     else
-      tpx_bwd<3, 0, GX, WF>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<3, 0, GX, WF, NL>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
   }
 }
 
@@ -1490,21 +1554,24 @@ void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const
 
 void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const void* h3x, const float* h3inv, const void* W3Tx, int W,
-                    float wscale, const float* up, float* M, float* w, int rnd) {
+                    float wscale, const float* up, float* M, float* w, int rnd, const float* b3, const float* cut) {
   if (N <= 0) return;
-  const TpxDims a{N, W, mts, E, wscale};
+  const TpxDims a{N, W, mts, E, wscale, b3, cut};
   const dim3 grid((unsigned)((N + XW - 1) / XW), 2, (unsigned)lin);  // z: one input block l1 each
   const _Float16* hx = static_cast<const _Float16*>(h3x);
   const _Float16* wt = static_cast<const _Float16*>(W3Tx);
-#define MACE_TPXF(L, R) \
-  MACE_LAUNCH((k_tpx_fwd<L, R>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w)
+#define MACE_TPXF(L, R, NLV) \
+  MACE_LAUNCH((k_tpx_fwd<L, R, NLV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w)
+  // the non-linear block (b3 given) runs under the float32 policy only
 #define MACE_TPXF_R(L)         \
-  if (rnd == RND_F16)          \
-    MACE_TPXF(L, RND_F16);     \
+  if (b3)                      \
+    MACE_TPXF(L, RND_NONE, true); \
+  else if (rnd == RND_F16)     \
+    MACE_TPXF(L, RND_F16, false); \
   else if (rnd == RND_BF16)    \
-    MACE_TPXF(L, RND_BF16);    \
+    MACE_TPXF(L, RND_BF16, false); \
   else                         \
-    MACE_TPXF(L, RND_NONE);
+    MACE_TPXF(L, RND_NONE, false);
   if (lin == 1) {
     MACE_TPXF_R(1)
   } else if (lin == 2) {
@@ -1519,21 +1586,24 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
 void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const float* w, const void* W3x, int W, float wscale, const float* up,
                     const float* gM, const int* pos_s, float* gxe, float* gY, int gyp, int accumulate_gY,
-                    float* gh3p, int wfmt) {
+                    float* gh3p, int wfmt, const float* b3, float* gwbp) {
   if (N <= 0 || E <= 0) return;  // no edges: no dL/dw, dL/dY, dL/dx rows to write
-  const TpxBwdDims a{N, W, mts, E, wscale, accumulate_gY, gyp};
+  const TpxBwdDims a{N, W, mts, E, wscale, accumulate_gY, gyp, b3, gwbp};
   const dim3 grid((unsigned)((N + XW - 1) / XW), 2, (unsigned)lin);
   const _Float16* wx = static_cast<const _Float16*>(W3x);
-#define MACE_TPXB(L, GXV, WF)                                                                         \
-  MACE_LAUNCH((k_tpx_bwd<L, GXV, WF>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \
+#define MACE_TPXB(L, GXV, WF, NLV)                                                                         \
+  MACE_LAUNCH((k_tpx_bwd<L, GXV, WF, NLV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \
               pos_s, gxe, gY, gh3p)
+  // the non-linear block (b3 given) runs under the float32 policy only
 #define MACE_TPXB_WF(L, GXV)       \
-  if (wfmt == RND_F16)             \
-    MACE_TPXB(L, GXV, RND_F16);    \
+  if (b3)                          \
+    MACE_TPXB(L, GXV, RND_NONE, true); \
+  else if (wfmt == RND_F16)        \
+    MACE_TPXB(L, GXV, RND_F16, false); \
   else if (wfmt == RND_BF16)       \
-    MACE_TPXB(L, GXV, RND_BF16);   \
+    MACE_TPXB(L, GXV, RND_BF16, false); \
   else                             \
-    MACE_TPXB(L, GXV, RND_NONE);
+    MACE_TPXB(L, GXV, RND_NONE, false);
   const bool gx = gxe != nullptr;
   if (lin == 1) {
     if (gx) { MACE_TPXB_WF(1, true) } else { MACE_TPXB_WF(1, false) }

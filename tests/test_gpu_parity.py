@@ -708,4 +708,16 @@ def test_mh1_nonlinear_block_parity(apply_cutoff, agnostic, edge):
     # With 2e edge irreps this random model's forces reach 89 eV/A; a float32 CPU restatement of
     # the reference misses float64 there by 3.5e-4 eV/A (3.9e-6 of max|F|), so the force bar is
     # relative to the force scale for that case.
-    assert_parity(got, ref, len(s), stress=True, force_rel=5e-6 if "2e" in edge else None)
+    frel = 5e-6 if "2e" in edge else None
+    assert_parity(got, ref, len(s), stress=True, force_rel=frel)
+    # the same step on the other kernel paths: radial output layer in separate split-fp16 kernels
+    # (w and dL/dw through memory), and everything on fp32 matrix cores
+    try:
+        for split, fused in ((True, False), (False, False)):
+            case.eng.set_split_products(split)
+            case.eng.set_fused_tp(fused)
+            print(f"  path split={split} fused={fused}", flush=True)
+            assert_parity(case.run(s, stress=True), ref, len(s), stress=True, force_rel=frel)
+    finally:
+        case.eng.set_split_products(True)
+        case.eng.set_fused_tp(True)
