@@ -140,9 +140,11 @@ __device__ __forceinline__ void stage_copy(T& dst, const T* __restrict__ src) {
   for (int i = threadIdx.x; i < N4; i += blockDim.x) d[i] = q[i];
 }
 
-// one 64-wide layer: acc[t'] = sum over the 16 k steps of W-tile (t') x v[s]
-__device__ __forceinline__ void layer64(const float4 (*w)[4][16], const float* v, f4v* acc) {
-  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+// one 64-wide layer: acc[t'] = sum over the 16 k steps of W-tile (t') x v[s]; lane: the
+// lane index (the LayerNorm kernels pass one the compiler cannot see as loop-invariant)
+__device__ __forceinline__ void layer64(const float4 (*w)[4][16], const float* v, f4v* acc,
+                                        int lane = threadIdx.x & 63) {
+  const int r = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1281,8 +1283,8 @@ __device__ __forceinline__ int fidx(int q, int g) { return 16 * (q >> 2) + 4 * g
 
 // the first layer's ef part: acc[t'] = W0^T ef for the lane's edge (w0 tile image)
 __device__ __forceinline__ void first_layer(const float4 (*w0)[4][16], const float* __restrict__ ef, int64_t ec,
-                                            int nb, f4v* acc) {
-  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+                                            int nb, f4v* acc, int lane) {
+  const int r = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
   const int nst = (nb + 3) >> 2;
@@ -1307,11 +1309,11 @@ struct LnFwdState {
 
 __device__ __forceinline__ void ln_mlp_fwd(const MlpFwdW& sw, const float4 (*dw0)[4][16], const LnSmall& S,
                                            const LnMlpParams& P, const float* __restrict__ ef, int64_t ec, int nb,
-                                           int zs, int zr, LnFwdState& F) {
-  const int l = threadIdx.x & 63, g = l >> 4;
+                                           int zs, int zr, LnFwdState& F, int lane) {
+  const int g = lane >> 4;
   f4v acc[4];
   float z[16], v[16];
-  first_layer(sw.w0, ef, ec, nb, acc);
+  first_layer(sw.w0, ef, ec, nb, acc, lane);
 #pragma unroll
   for (int q = 0; q < 16; ++q) z[q] = acc[q >> 2][q & 3];
   add_row16(P.ts + (int64_t)zs * H, g, z);
@@ -1325,7 +1327,7 @@ __device__ __forceinline__ void ln_mlp_fwd(const MlpFwdW& sw, const float4 (*dw0
       v[q] = silu(fmaf(F.xh[k][q], S.ln[k][0][n], S.ln[k][1][n]));
     }
     if (k < 2) {
-      layer64(k == 0 ? sw.w1 : sw.w2, v, acc);
+      layer64(k == 0 ? sw.w1 : sw.w2, v, acc, lane);
 #pragma unroll
       for (int q = 0; q < 16; ++q) z[q] = acc[q >> 2][q & 3] + S.bias[k][fidx(q, g)];
     }
@@ -1333,7 +1335,7 @@ __device__ __forceinline__ void ln_mlp_fwd(const MlpFwdW& sw, const float4 (*dw0
 #pragma unroll
   for (int q = 0; q < 16; ++q) F.h3[q] = v[q];
   // density MLP
-  first_layer(dw0, ef, ec, nb, acc);
+  first_layer(dw0, ef, ec, nb, acc, lane);
 #pragma unroll
   for (int q = 0; q < 16; ++q) z[q] = acc[q >> 2][q & 3];
   add_row16(P.dts + (int64_t)zs * H, g, z);
@@ -1367,8 +1369,11 @@ __global__ void __launch_bounds__(256) k_rmlp_ln_fwd(int64_t E, int nb, const fl
   for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
     const int64_t e = gi * 16 + r, ec = e < E ? e : E - 1;  // rows past the end: computed, not stored
     const int zs = species[sender[ec]], zr = species[receiver[ec]];
+    // the lane index as a value the compiler cannot hoist: the LDS reads of weights and
+    // LayerNorm vectors indexed by it stay inside the loop (hoisted, they hold ~400 registers)
+    const int lo = lane_opaque<true>();
     LnFwdState F;
-    ln_mlp_fwd(sw, sdw0, S, P, ef, ec, nb, zs, zr, F);
+    ln_mlp_fwd(sw, sdw0, S, P, ef, ec, nb, zs, zr, F, lo);
     if (h3inv) {  // split pairs [E][2][64] with the row scale's inverse, as k_mlp_hidden_x writes them
       float inv;
       const float sc = edge_scale<16>(F.h3, &inv);
@@ -1418,8 +1423,8 @@ __device__ __forceinline__ void ln_silu_bwd(float* gv, const float* xh, float rs
 }
 
 // gef contributions of a first layer: o[i] = sum_n W0[k = 4g + i][n] dz[n] (w0T tile image)
-__device__ __forceinline__ void first_layer_T(const float4 (*w0T)[4][16], const float* dz, f4v& o) {
-  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+__device__ __forceinline__ void first_layer_T(const float4 (*w0T)[4][16], const float* dz, f4v& o, int lane) {
+  const int r = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const float4 wq = w0T[t][g][r];
@@ -1428,7 +1433,11 @@ __device__ __forceinline__ void first_layer_T(const float4 (*w0T)[4][16], const 
   }
 }
 
-__global__ void __launch_bounds__(256) k_rmlp_ln_bwd(int64_t E, int nb, const float* __restrict__ ef,
+// waves per block of the LayerNorm VJP: its staged weights (85 KB) fit once per CU, so two
+// waves per SIMD come from one eight-wave block
+constexpr int kLnBwdWaves = 8;
+
+__global__ void __launch_bounds__(64 * kLnBwdWaves) k_rmlp_ln_bwd(int64_t E, int nb, const float* __restrict__ ef,
                                                      const float* __restrict__ cut, const int* __restrict__ sender,
                                                      const int* __restrict__ receiver,
                                                      const int* __restrict__ species, const MlpFwdW* __restrict__ tiles,
@@ -1452,12 +1461,13 @@ __global__ void __launch_bounds__(256) k_rmlp_ln_bwd(int64_t E, int nb, const fl
   __syncthreads();
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t ngroups = (E + 15) / 16;
-  for (int64_t gi = (int64_t)blockIdx.x * 4 + wv; gi < ngroups; gi += (int64_t)gridDim.x * 4) {
+  for (int64_t gi = (int64_t)blockIdx.x * kLnBwdWaves + wv; gi < ngroups; gi += (int64_t)gridDim.x * kLnBwdWaves) {
     const int64_t e = gi * 16 + r, ec = e < E ? e : E - 1;
     const int rcv = receiver[ec];
     const int zs = species[sender[ec]], zr = species[rcv];
+    const int lo = lane_opaque<true>(), go = lo >> 4;  // as in k_rmlp_ln_fwd
     LnFwdState F;
-    ln_mlp_fwd(sw, sdw0, S, P, ef, ec, nb, zs, zr, F);
+    ln_mlp_fwd(sw, sdw0, S, P, ef, ec, nb, zs, zr, F, lo);
     const float ce = cut ? cut[ec] : 1.f;
     float gv[16], gb = gwb[ec];
     ld_row16(G + ec * H, g, gv);
@@ -1478,24 +1488,24 @@ __global__ void __launch_bounds__(256) k_rmlp_ln_bwd(int64_t E, int nb, const fl
     f4v acc[4];
 #pragma unroll
     for (int k = 2; k >= 0; --k) {
-      ln_silu_bwd(gv, F.xh[k], F.rstd[k], S.ln[k][0], S.ln[k][1], g);
+      ln_silu_bwd(gv, F.xh[k], F.rstd[k], S.ln[k][0], S.ln[k][1], go);
       if (k > 0) {
-        layer64(k == 2 ? sb.w2T : sb.w1T, gv, acc);
+        layer64(k == 2 ? sb.w2T : sb.w1T, gv, acc, lo);
 #pragma unroll
         for (int q = 0; q < 16; ++q) gv[q] = acc[q >> 2][q & 3];
       }
     }
     f4v o = f4v{0.f, 0.f, 0.f, 0.f};
-    first_layer_T(sb.w0T, gv, o);
+    first_layer_T(sb.w0T, gv, o, lo);
     // density: dens = tanh(x^2) cut, rho[receiver] = sum of dens
     const float th = tanhf(F.x * F.x);
     const float gd = drho[rcv];
     gc = fmaf(gd, th, gc);
     const float gx = gd * ce * (1.f - th * th) * 2.f * F.x;
 #pragma unroll
-    for (int q = 0; q < 16; ++q) gv[q] = gx * S.dw1[fidx(q, g)];
-    ln_silu_bwd(gv, F.xhd, F.rstdd, S.dln[0], S.dln[1], g);
-    first_layer_T(sdw0T, gv, o);
+    for (int q = 0; q < 16; ++q) gv[q] = gx * S.dw1[fidx(q, go)];
+    ln_silu_bwd(gv, F.xhd, F.rstdd, S.dln[0], S.dln[1], go);
+    first_layer_T(sdw0T, gv, o, lo);
     if (e < E) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -1645,7 +1655,9 @@ void launch_rmlp_ln_fwd(hipStream_t st, int64_t E, int nb, const float* ef, cons
                         const int* receiver, const int* species, const void* tiles, const void* dtiles,
                         const LnMlpParams& P, void* h3, float* h3inv, float* dens) {
   if (E <= 0) return;
-  MACE_LAUNCH(k_rmlp_ln_fwd, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, cut, sender, receiver, species,
+  // one 16-edge group per wave up to three blocks per CU (44 KB of LDS each)
+  const unsigned grid = (unsigned)std::min<int64_t>((E + 63) / 64, 768);
+  MACE_LAUNCH(k_rmlp_ln_fwd, dim3(grid), dim3(256), 0, st, E, nb, ef, cut, sender, receiver, species,
               static_cast<const MlpFwdW*>(tiles), static_cast<const MlpFwdW*>(dtiles), P, h3, h3inv, dens);
 }
 
@@ -1654,7 +1666,8 @@ void launch_rmlp_ln_bwd(hipStream_t st, int64_t E, int nb, const float* ef, cons
                         const void* dtiles, const void* dbtiles, const LnMlpParams& P, const float* G,
                         const float* gwb, int np, const float* drho, float* gef, float* gcut, int accumulate) {
   if (E <= 0) return;
-  MACE_LAUNCH(k_rmlp_ln_bwd, dim3(hidden_grid(E)), dim3(256), 0, st, E, nb, ef, cut, sender, receiver, species,
+  const unsigned grid = (unsigned)std::min<int64_t>((E + 16 * kLnBwdWaves - 1) / (16 * kLnBwdWaves), 256);
+  MACE_LAUNCH(k_rmlp_ln_bwd, dim3(grid), dim3(64 * kLnBwdWaves), 0, st, E, nb, ef, cut, sender, receiver, species,
               static_cast<const MlpFwdW*>(tiles), static_cast<const MlpBwdW*>(btiles),
               static_cast<const MlpFwdW*>(dtiles), static_cast<const MlpBwdW*>(dbtiles), P, G, gwb, np, drho, gef,
               gcut, accumulate);
