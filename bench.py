@@ -221,7 +221,9 @@ def layer_shapes(dm):
     import gen_tables
     layers = []
     for l in range(dm.dims["num_layers"]):
-        lin, lhid = dm.dims["layer_in_blocks"][l], dm.dims["layer_hid_blocks"][l]
+        lhid = dm.dims["layer_hid_blocks"][l]
+        # input blocks of the conv TP: linear_up's output in a non-linear (mh-1) layer
+        lin = dm.dims["layer_edge_blocks"][l] if dm.dims.get("nonlinear") else dm.dims["layer_in_blocks"][l]
         slots = gen_tables.tp_layout(lin)
         layers.append(dict(lin=lin, lhid=lhid, din=128 * lin * lin, dhid=128 * lhid * lhid,
                            dmid=128 * sum(2 * x[2] + 1 for x in slots), wn=128 * len(slots),
@@ -350,7 +352,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=1, help="benchmark configuration index 0..4")
+    ap.add_argument("--config", type=int, default=1, help="benchmark configuration index 0..4 (5: an mh-1 model on the Si1000 system)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--separate-mlp-out", action="store_true",
                     help="float32 policy: radial-MLP output layer as its own pass (not fused into the TP)")
@@ -403,7 +405,7 @@ def main():
     sweep = None
     if not args.no_sweep:
         sweep = []
-        for i in range(5):
+        for i in range(6):  # the five benchmark configurations, then an mh-1 model on Si1000
             r = head if i == args.config else run_workload(i, max(5, args.steps // 2), args.warmup,
                                                            args.separate_mlp_out, graphs)
             sweep.append({k: r[k] for k in ("workload", "n_atoms", "n_edges", "properties", "feature_dtype",

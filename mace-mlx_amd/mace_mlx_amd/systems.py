@@ -16,7 +16,7 @@ from typing import List, Optional
 
 import numpy as np
 
-from .model_io import ModelConfig, random_init, save_model
+from .model_io import NONLINEAR_BLOCK, ModelConfig, random_init, save_model
 
 # conventional cells in fractional coordinates
 _DIAMOND = np.array([
@@ -115,7 +115,10 @@ class BenchConfig:
 
 
 def make_config(index: int) -> BenchConfig:
-    """Configurations 1..5 of the benchmark definition (0-based index 0..4)."""
+    """Configurations 1..5 of the benchmark definition (0-based index 0..4); index 5, outside
+    that definition, is the Si1000 system under an mh-1 model (non-linear interaction blocks,
+    `blocks.py:611-807`, with the mh-1 foundation models' element-agnostic product, separate
+    cutoff, 1o edge irreps and 89 elements)."""
     if index == 0:
         s = rattle(diamond_si((2, 2, 2)), 0.01, 0)
         m = arch_config("small")
@@ -147,6 +150,14 @@ def make_config(index: int) -> BenchConfig:
                         atomic_energies=e0)
         return BenchConfig(4, "HEA32000-medium-fp16", s, m, ["energy", "forces"],
                            dtype="float16")
+    if index == 5:
+        s = rattle(diamond_si((5, 5, 5)), 0.03, 1)
+        m = arch_config("medium", num_elements=89, z_table=range(1, 90))
+        m.interaction_cls = NONLINEAR_BLOCK
+        m.edge_irreps = "128x0e+128x1o"
+        m.apply_cutoff = False
+        m.use_agnostic_product = True
+        return BenchConfig(5, "Si1000-mh1", s, m, ["energy", "forces"])
     raise ValueError(index)
 
 
