@@ -416,24 +416,42 @@ __device__ __forceinline__ void sc_block_vjp(const float* f, const float* __rest
   for (int i = 0; i < 16; ++i) g[i] += gl[i];
 }
 
-template <int CORR>
-__global__ void __launch_bounds__(NC) k_sc_fwd(int N, int nout, const float* __restrict__ A, int ldA,
+// Block (n, b) evaluates output block b (0e, 1o, 2e) of node n; NOUT, the layer's number of
+// output blocks, is a template parameter so an instantiation holds only the polynomials it can
+// run.  Correlation 3: 0e alone takes 59 VGPRs (eight waves per SIMD), 0e / 1o 255 (two),
+// 0e / 1o / 2e 381 (one), against 456 for one thread running every block in turn.
+template <int CORR, int NOUT>
+__global__ void __launch_bounds__(NC) __attribute__((amdgpu_waves_per_eu(NOUT < 3 ? 2 : 1))) k_sc_fwd(int N, const float* __restrict__ A, int ldA,
                                                const int* __restrict__ species, ScW W, float* __restrict__ B,
                                                int ldB, int half) {
-  const int n = blockIdx.x, c = threadIdx.x;
+  const int n = blockIdx.x, c = threadIdx.x, b = blockIdx.y;
   float f[16];
   const float* An = A + (int64_t)n * ldA + c;
 #pragma unroll
   for (int i = 0; i < 16; ++i) f[i] = An[i * NC];
   const int z = species[n];
   float* Bn = B + (int64_t)n * ldB;
-  sc_block_fwd<0, CORR>(f, W.w[0], z, c, Bn, half);
-  if (nout > 1) sc_block_fwd<1, CORR>(f, W.w[1], z, c, Bn, half);
-  if (nout > 2) sc_block_fwd<2, CORR>(f, W.w[2], z, c, Bn, half);
+  if constexpr (NOUT == 1) {
+    sc_block_fwd<0, CORR>(f, W.w[0], z, c, Bn, half);
+  } else if constexpr (NOUT == 2) {
+    if (b == 0)
+      sc_block_fwd<0, CORR>(f, W.w[0], z, c, Bn, half);
+    else
+      sc_block_fwd<1, CORR>(f, W.w[1], z, c, Bn, half);
+  } else {
+    if (b == 0)
+      sc_block_fwd<0, CORR>(f, W.w[0], z, c, Bn, half);
+    else if (b == 1)
+      sc_block_fwd<1, CORR>(f, W.w[1], z, c, Bn, half);
+    else
+      sc_block_fwd<2, CORR>(f, W.w[2], z, c, Bn, half);
+  }
 }
 
-template <int CORR>
-__global__ void __launch_bounds__(NC) k_sc_bwd(int N, int nout, const float* __restrict__ A, int ldA,
+// NOUT: output blocks of the layer (a template parameter: a layer with the 0e block only runs
+// an instantiation without the larger polynomials' registers)
+template <int CORR, int NOUT>
+__global__ void __launch_bounds__(NC) k_sc_bwd(int N, const float* __restrict__ A, int ldA,
                                                const int* __restrict__ species, ScW W, const float* __restrict__ gB,
                                                int ldB, float* __restrict__ gA) {
   const int n = blockIdx.x, c = threadIdx.x;
@@ -447,8 +465,8 @@ __global__ void __launch_bounds__(NC) k_sc_bwd(int N, int nout, const float* __r
   const int z = species[n];
   const float* gBn = gB + (int64_t)n * ldB;
   sc_block_vjp<0, CORR>(f, W.w[0], z, c, gBn, g);
-  if (nout > 1) sc_block_vjp<1, CORR>(f, W.w[1], z, c, gBn, g);
-  if (nout > 2) sc_block_vjp<2, CORR>(f, W.w[2], z, c, gBn, g);
+  if constexpr (NOUT > 1) sc_block_vjp<1, CORR>(f, W.w[1], z, c, gBn, g);
+  if constexpr (NOUT > 2) sc_block_vjp<2, CORR>(f, W.w[2], z, c, gBn, g);
   float* gAn = gA + (int64_t)n * ldA + c;
 #pragma unroll
   for (int i = 0; i < 16; ++i) gAn[i * NC] = g[i];
@@ -776,28 +794,39 @@ void launch_sc_fwd(hipStream_t st, int N, int nout, int corr, const float* A, in
                    const float* const* Wsc, float* B, int ldB, int half) {
   if (N <= 0) return;
   ScW w{{Wsc[0], nout > 1 ? Wsc[1] : nullptr, nout > 2 ? Wsc[2] : nullptr}};
+  const dim3 grid((unsigned)N, (unsigned)nout);
+#define MACE_SCF(C)                                                                                   \
+  if (nout == 1)                                                                                      \
+    MACE_LAUNCH((k_sc_fwd<C, 1>), grid, dim3(NC), 0, st, N, A, ldA, species, w, B, ldB, half);        \
+  else if (nout == 2)                                                                                 \
+    MACE_LAUNCH((k_sc_fwd<C, 2>), grid, dim3(NC), 0, st, N, A, ldA, species, w, B, ldB, half);        \
+  else                                                                                                \
+    MACE_LAUNCH((k_sc_fwd<C, 3>), grid, dim3(NC), 0, st, N, A, ldA, species, w, B, ldB, half);
   switch (corr) {
-    case 1: MACE_LAUNCH(k_sc_fwd<1>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB, half); break;
-    case 2: MACE_LAUNCH(k_sc_fwd<2>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB, half); break;
-    case 3: MACE_LAUNCH(k_sc_fwd<3>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, B, ldB, half); break;
+    case 1: MACE_SCF(1) break;
+    case 2: MACE_SCF(2) break;
+    case 3: MACE_SCF(3) break;
   }
+#undef MACE_SCF
 }
 
 void launch_sc_bwd(hipStream_t st, int N, int nout, int corr, const float* A, int ldA, const int* species,
                    const float* const* Wsc, const float* gB, int ldB, float* gA) {
   if (N <= 0) return;
   ScW w{{Wsc[0], nout > 1 ? Wsc[1] : nullptr, nout > 2 ? Wsc[2] : nullptr}};
-  switch (corr) {
-    case 1:
-      MACE_LAUNCH(k_sc_bwd<1>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, gB, ldB, gA);
-      break;
-    case 2:
-      MACE_LAUNCH(k_sc_bwd<2>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, gB, ldB, gA);
-      break;
-    case 3:
-      MACE_LAUNCH(k_sc_bwd<3>, dim3(N), dim3(NC), 0, st, N, nout, A, ldA, species, w, gB, ldB, gA);
-      break;
+#define MACE_SCB(C)                                                                                   \
+  if (nout == 1)                                                                                      \
+    MACE_LAUNCH((k_sc_bwd<C, 1>), dim3(N), dim3(NC), 0, st, N, A, ldA, species, w, gB, ldB, gA);      \
+  else if (nout == 2)                                                                                 \
+    MACE_LAUNCH((k_sc_bwd<C, 2>), dim3(N), dim3(NC), 0, st, N, A, ldA, species, w, gB, ldB, gA);      \
+  else                                                                                                \
+    MACE_LAUNCH((k_sc_bwd<C, 3>), dim3(N), dim3(NC), 0, st, N, A, ldA, species, w, gB, ldB, gA);
+  switch (corr) {  // nout is 1..3: checked at model load
+    case 1: MACE_SCB(1) break;
+    case 2: MACE_SCB(2) break;
+    case 3: MACE_SCB(3) break;
   }
+#undef MACE_SCB
 }
 
 void launch_virial_reduce(hipStream_t st, const double* part, int nblk, double* vir) {
