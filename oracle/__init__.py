@@ -18,7 +18,15 @@ Pinning (what checks each part against something other than itself):
   own `clebsch_gordan.py` (tests/golden/cg_fixtures.npz) plus 3j invariants;
 * spherical harmonics -- closed forms for l <= 2, component norm 2l+1,
   equivariance under the reference's Wigner-D;
-* Bessel / cutoff / ZBL -- closed-form values and boundary behaviour;
+* Bessel / cutoff -- closed-form values and boundary behaviour;
+* ZBL -- at the universal screening parameters, an isolated pair's energy equals
+  the published ZBL universal potential (Ziegler, Biersack & Littmark 1985,
+  five-digit coefficients, CODATA constants) within the reference's four-digit
+  rounding, and planted coefficient / exponent swaps fail by more than 1 %;
+* radial MLP -- the model file's layers load strictly into a torch
+  ``nn.Sequential(Linear(bias=False), SiLU, ...)`` with the same output;
+* density normalisation -- on a lattice where every edge has the same features,
+  the block equals the plain block with avg_num_neighbors = 1 + k tanh(c^2);
 * neighbour list -- edge counts recorded by the reference (2944 for Si64,
   46000 for Si1000, `docs/prototypes/profile_results.json`), shell counts, and
   the (i, j, S) <-> (j, i, -S) pairing;
@@ -36,9 +44,8 @@ Pinning (what checks each part against something other than itself):
   recomputed the way e3nn computes them, FD forces / stress, and the reductions
   beta = 0 (density off) and agnostic product = copied per-element weights.
 
-Parity unpinned: the MLX-executed values of the reference itself (MLX is not
-installable here), MLX's RNG / initialisers (weights are exchanged as files),
-ASE's covalent-radius table (a published table is vendored instead), and the
-ZBL screening coefficients (restated from `radial.py:142-199`; only the
-short-range Coulomb limit and the cutoff are checked).
+Every function of ``model`` and ``neighbors`` has a check above.  Parity
+unpinned outside them: the MLX-executed values of the reference itself (MLX is
+not installable here), MLX's RNG / initialisers (weights are exchanged as
+files), and ASE's covalent-radius table (a published table is vendored instead).
 """

@@ -110,19 +110,29 @@ def agnesi(r, zs, zr, params, radii):
     return 1.0 / (1.0 + a * x ** q / (1.0 + x ** (q - p)))
 
 
+# Universal screening function phi(x) = sum_k c_k exp(-d_k x) of Ziegler, Biersack and
+# Littmark, at the 4-digit rounding the reference uses (`radial.py:149,184-189`), with its
+# Bohr radius (Angstrom) and e^2 / (4 pi eps0) (eV Angstrom, `radial.py:179-181,191-192`).
+ZBL_C = (0.1818, 0.5099, 0.2802, 0.02817)
+ZBL_D = (3.2, 0.9423, 0.4028, 0.2016)
+ZBL_BOHR = 0.529
+ZBL_COULOMB = 14.3996
+
+
 def zbl_node_energy(r, zs, zr, receiver, n_nodes, params):
-    """Per-node ZBL repulsion, `radial.py:156-201`."""
+    """Per-node ZBL repulsion, `radial.py:156-201`: half of each edge's pair energy
+    V(r) = ke Z_u Z_v / r phi(r / a), a = a_prefactor a0 / (Z_u^a_exp + Z_v^a_exp), times the
+    polynomial envelope at r / (r_cov(Z_u) + r_cov(Z_v)), summed onto the receiver."""
     dtype = r.dtype
     p = int(params.get("p", 6))
     a_exp = float(params.get("a_exp", 0.3))
     a_pref = float(params.get("a_prefactor", 0.4543))
     zu = zs.to(dtype)
     zv = zr.to(dtype)
-    a = a_pref * 0.529 / (zu ** a_exp + zv ** a_exp)
+    a = a_pref * ZBL_BOHR / (zu ** a_exp + zv ** a_exp)
     x = r / a
-    phi = (0.1818 * torch.exp(-3.2 * x) + 0.5099 * torch.exp(-0.9423 * x)
-           + 0.2802 * torch.exp(-0.4028 * x) + 0.02817 * torch.exp(-0.2016 * x))
-    v = 14.3996 * zu * zv / r * phi
+    phi = sum(c * torch.exp(-d * x) for c, d in zip(ZBL_C, ZBL_D))
+    v = ZBL_COULOMB * zu * zv / r * phi
     cov = torch.as_tensor(COVALENT_RADII, dtype=dtype)
     rmax = cov[zs] + cov[zr]
     v = 0.5 * v * poly_envelope(r / rmax, p)
