@@ -427,8 +427,10 @@ def random_init(cfg: ModelConfig, seed: int = 0) -> Dict[str, np.ndarray]:
         elif key.endswith(".alpha") or key.endswith(".beta"):
             # the block starts from alpha = 20, beta = 0 (blocks.py:697-698): the density off and
             # every message damped 20x, which leaves a random model with forces ~0.01 eV/A;
-            # a random model takes alpha in [1, ~3] and beta in [0.1, ~0.4] instead
-            a0, sc = (1.0, 1.0) if key.endswith(".alpha") else (0.1, 0.1)
+            # a random model takes alpha in [1.5, ~4.5] and beta in [0.1, ~0.4] instead, which
+            # keeps its forces at O(1-10) eV/A on bulk, ragged and three-species systems (the
+            # correlation-3 product makes them scale roughly with alpha^-3)
+            a0, sc = (1.5, 1.5) if key.endswith(".alpha") else (0.1, 0.1)
             w[key] = np.asarray(a0 + sc * abs(rng.standard_normal()))
         elif ".conv_tp_weights." in key:
             layer = int(key.split(".layers.")[1].split(".")[0])

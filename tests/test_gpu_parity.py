@@ -458,17 +458,15 @@ def _check_ragged(case, energy):
 def test_ragged_degrees_mh1_fused():
     """The same ragged rows through the mh-1 block (`blocks.py:611-807`) on the fused path: the
     forward's bias / envelope epilogue of the w tiles and the VJP's gw . b3 partials beside blocks
-    and receivers without edges.  This random mh-1 model reaches |F| = 319 eV/A on these rows,
-    where the split-fp16 products' error (about 2^-22 per product) sums to 1.2e-6 of E on the fused
-    path and 1.3e-6 on the separate split passes (fp32 matrix cores: 2.9e-7).  So the oracle
-    check runs on fp32 matrix cores, and the fused kernels are checked against the separate
-    split passes, which compute the same products through other kernels (no block-level steps)."""
+    and receivers without edges.  Every product path (the default split-fp16 fused kernels, the
+    separate split passes, fp32 matrix cores) meets the oracle tolerances, and the fused kernels
+    match the separate split passes, which compute the same products through other kernels."""
     from test_oracle_mh1 import mh1_config
     case = Case(mh1_config(False, True, "128x0e+128x1o"), seed=11)
     s = _ragged_system()
     got = {}
     try:
-        for split, fused in ((False, False), (True, False), (True, True)):
+        for split, fused in ((True, True), (True, False), (False, False)):
             case.eng.set_split_products(split)
             case.eng.set_fused_tp(fused)
             got[(split, fused)] = case.run(s, stress=True)
@@ -477,14 +475,16 @@ def test_ragged_degrees_mh1_fused():
         case.eng.set_fused_tp(True)
     edges = case.edges()
     assert (np.bincount(edges[1], minlength=len(s))[:8] == 0).all()
-    ref = case.reference(s, got[(False, False)]["sp"], edges, stress=True)
-    assert_parity(got[(False, False)], ref, len(s), stress=True, force_rel=5e-6)
-    a, b = got[(True, False)], got[(True, True)]
+    ref = case.reference(s, got[(True, True)]["sp"], edges, stress=True)
     fmax = float(np.abs(ref["F"]).max())
-    print(f"mh-1 ragged: fused vs separate split dE={abs(a['E'] - b['E']):.3g} "
-          f"dF={np.abs(a['F'] - b['F']).max():.3g} (max|F| {fmax:.3g})")
+    assert 0.5 < fmax < 50.0, fmax
+    for key, g in got.items():
+        print(f"mh-1 ragged split={key[0]} fused={key[1]}: |dE|/|E| {abs(g['E'] - ref['E']) / abs(ref['E']):.3g} "
+              f"max|dF| {np.abs(g['F'] - ref['F']).max():.3g} (max|F| {fmax:.3g})", flush=True)
+        assert_parity(g, ref, len(s), stress=True)
+    a, b = got[(True, False)], got[(True, True)]
     assert abs(a["E"] - b["E"]) <= 1e-6 * abs(a["E"])
-    assert np.abs(a["F"] - b["F"]).max() <= 5e-6 * fmax
+    assert np.abs(a["F"] - b["F"]).max() <= 1e-4
     assert np.abs(a["vir"] - b["vir"]).max() <= 1e-5 * max(1.0, float(np.abs(a["vir"]).max()))
 
 
@@ -721,10 +721,14 @@ def test_fused_tp_matches_separate_passes(arch, request):
     assert dv <= 1e-5 * max(1.0, float(np.abs(a["vir"]).max())), dv
 
 
-@pytest.mark.parametrize("apply_cutoff,agnostic,edge", [(False, True, "128x0e+128x1o"),
-                                                        (False, False, "128x0e+128x1o"),
-                                                        (False, True, "128x0e+128x1o+128x2e")])
-def test_mh1_nonlinear_block_parity(apply_cutoff, agnostic, edge):
+@pytest.mark.parametrize("apply_cutoff,agnostic,edge,energy", [
+    # this model's per-atom energies cancel to |E| / N = 0.19 eV: a float32 CPU restatement of
+    # the reference itself misses float64 by 2.8e-6 of E there (5.3e-7 eV/atom), so its energy
+    # bar is the per-atom one
+    (False, True, "128x0e+128x1o", "per_atom"),
+    (False, False, "128x0e+128x1o", "relative"),
+    (False, True, "128x0e+128x1o+128x2e", "relative")])
+def test_mh1_nonlinear_block_parity(apply_cutoff, agnostic, edge, energy):
     """mh-1 family (`blocks.py:611-807`): LayerNorm radial / density MLPs over species-augmented
     edge features, separate cutoff (`radial.py:316-318`), gate, linear_res / linear_1 /
     linear_2, element-agnostic product (`blocks.py:510-533`); three species, E + F + S against
@@ -743,12 +747,9 @@ def test_mh1_nonlinear_block_parity(apply_cutoff, agnostic, edge):
     edges = case.edges()
     assert edge_set(*edges) == bruteforce_edges(s)
     ref = case.reference(s, got["sp"], edges, stress=True)
-    assert np.abs(ref["F"]).max() > 0.05
-    # With 2e edge irreps this random model's forces reach 89 eV/A; a float32 CPU restatement of
-    # the reference misses float64 there by 3.5e-4 eV/A (3.9e-6 of max|F|), so the force bar is
-    # relative to the force scale for that case.
-    frel = 5e-6 if "2e" in edge else None
-    assert_parity(got, ref, len(s), stress=True, force_rel=frel)
+    fmax = float(np.abs(ref["F"]).max())
+    assert 0.5 < fmax < 50.0, fmax
+    assert_parity(got, ref, len(s), stress=True, energy=energy)
     # the same step on the other kernel paths: radial output layer in separate split-fp16 kernels
     # (w and dL/dw through memory), and everything on fp32 matrix cores
     try:
@@ -756,7 +757,7 @@ def test_mh1_nonlinear_block_parity(apply_cutoff, agnostic, edge):
             case.eng.set_split_products(split)
             case.eng.set_fused_tp(fused)
             print(f"  path split={split} fused={fused}", flush=True)
-            assert_parity(case.run(s, stress=True), ref, len(s), stress=True, force_rel=frel)
+            assert_parity(case.run(s, stress=True), ref, len(s), stress=True, energy=energy)
     finally:
         case.eng.set_split_products(True)
         case.eng.set_fused_tp(True)
