@@ -60,3 +60,18 @@ def test_float64_warns_then_requires_model():
         with pytest.raises(FileNotFoundError):
             calc.MACEHIPCalculator(model_path="/nonexistent/dir", default_dtype="float64")
     assert any("float32" in str(r.message) for r in rec)
+
+
+def test_load_model_surface(tmp_path):
+    """`model.py:664-720`: load_model(model_dir, dtype) returns a MACE or ScaleShiftMACE object
+    (ScaleShiftMACE when config.json names no model_type); a bad dtype raises before any GPU
+    work, and the call signature follows `MACE.__call__` (`model.py:440-449`)."""
+    from mace_mlx_amd import model as mm
+    assert mace_mlx_amd.load_model is mm.load_model
+    assert issubclass(mm.ScaleShiftMACE, mm.MACE)
+    sig = inspect.signature(mm.MACE.__call__)
+    assert list(sig.parameters)[1:] == ["positions", "node_attrs", "edge_index", "shifts", "cell", "batch",
+                                         "num_graphs"]
+    assert sig.parameters["num_graphs"].default == 1
+    with pytest.raises(ValueError):
+        mace_mlx_amd.load_model(str(tmp_path), dtype="float8")
