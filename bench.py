@@ -264,6 +264,29 @@ def _timed(eng, pos_d, out_d, stress, steps, force_nl=False):
     return time.perf_counter() - t0
 
 
+def calculator_ms(bc, weights, warmup=3, reps=10):
+    """The reference's end-to-end timing protocol (`docs/prototypes/xbench.py:89-101`): through
+    the ASE calculator, `warmup` calls of get_potential_energy() + get_forces() with the results
+    cleared before each, then the median over `reps` such calls (ms).  Also (min, max)."""
+    import tempfile
+    from mace_mlx_amd.calculators import MACECalculator
+    from mace_mlx_amd.model_io import save_model
+    with tempfile.TemporaryDirectory() as d:
+        save_model(d, bc.model, weights)
+        calc = MACECalculator(model_path=d, default_dtype=bc.dtype)
+    atoms = bc.system.copy()
+    ts = []
+    for k in range(warmup + reps):
+        calc.results = {}
+        t0 = time.perf_counter()
+        calc.get_potential_energy(atoms)
+        calc.get_forces(atoms)
+        if k >= warmup:
+            ts.append(time.perf_counter() - t0)
+    del calc
+    return float(np.median(ts)) * 1e3, float(np.min(ts)) * 1e3, float(np.max(ts)) * 1e3
+
+
 def run_workload(idx, steps, warmup, separate=False, graphs=None, extras=False, launch_order=None):
     """Measure one benchmark configuration: steady-state device-resident steps (neighbour
     list cached), steps that rebuild the neighbour list, and a per-launch-site pass with HIP
@@ -292,10 +315,18 @@ def run_workload(idx, steps, warmup, separate=False, graphs=None, extras=False, 
         # on the device only, so the first host-array step rebuilds the list: warm up first
         for _ in range(max(warmup, 2)):
             eng.step(s.positions, stress=stress)
-        th = time.perf_counter()
+        # per-step wall times of back-to-back host-array steps: the median (the reference's
+        # protocol) and the mean
+        ts = []
         for _ in range(steps):
+            th = time.perf_counter()
             eng.step(s.positions, stress=stress)
-        res["ms_per_step_host_arrays"] = round((time.perf_counter() - th) / steps * 1e3, 4)
+            ts.append(time.perf_counter() - th)
+        res["ms_per_step_host_arrays"] = round(float(np.median(ts)) * 1e3, 4)
+        res["ms_per_step_host_arrays_mean"] = round(float(np.mean(ts)) * 1e3, 4)
+        med, lo, hi = calculator_ms(bc, weights)
+        res["ms_per_step_calculator"] = round(med, 4)
+        res["ms_per_step_calculator_range"] = [round(lo, 4), round(hi, 4)]
         if bc.dtype == "float32":   # the same step with every product on fp32 matrix cores
             eng.set_split_products(False)
             _timed(eng, pos_d, out_d, stress, 2)
@@ -433,6 +464,9 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": head["ms_per_step"],
         "ms_per_step_host_arrays": head["ms_per_step_host_arrays"],
+        "ms_per_step_host_arrays_mean": head["ms_per_step_host_arrays_mean"],
+        "ms_per_step_calculator": head["ms_per_step_calculator"],
+        "ms_per_step_calculator_range": head["ms_per_step_calculator_range"],
         "ms_per_step_nl_rebuild": head["ms_per_step_nl_rebuild"],
         "ms_per_step_fp32_mfma": head.get("ms_per_step_fp32_mfma"),
         "higher_is_better": True,

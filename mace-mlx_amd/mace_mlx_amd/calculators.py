@@ -173,14 +173,28 @@ class MACEHIPCalculator(_AseCalculator):
 
     # -- ASE -----------------------------------------------------------------
     def _species(self, atoms) -> np.ndarray:
+        """Element indices of the atoms, cached while the atomic numbers stay the same (the
+        reference's one-hot cache, `calculators.py:330-364`); ValueError names the first
+        unsupported atomic number (345-354)."""
         numbers = np.asarray(atoms.get_atomic_numbers())
-        out = np.empty(len(numbers), dtype=np.int32)
-        for i, z in enumerate(numbers):
-            idx = self._z_to_idx.get(int(z))
-            if idx is None:
-                raise ValueError(f"Atomic number {int(z)} is not supported by this model. "
-                                 f"Supported: {sorted(self._z_to_idx)}")
-            out[i] = idx
+        key = numbers.tobytes()
+        cache = getattr(self, "_species_cache", None)
+        if cache is not None and cache[0] == key:
+            return cache[1]
+        lut = getattr(self, "_z_lut", None)
+        if lut is None:
+            lut = np.full(max(self._z_to_idx, default=0) + 1, -1, dtype=np.int64)
+            for z, i in self._z_to_idx.items():
+                lut[z] = i
+            self._z_lut = lut
+        z = numbers.astype(np.int64).reshape(-1)
+        idx = np.where((z >= 0) & (z < len(lut)), lut[np.clip(z, 0, len(lut) - 1)], -1)
+        if (idx < 0).any():
+            bad = int(z[np.argmax(idx < 0)])
+            raise ValueError(f"Atomic number {bad} is not supported by this model. "
+                             f"Supported: {sorted(self._z_to_idx)}")
+        out = idx.astype(np.int32)
+        self._species_cache = (key, out)
         return out
 
     def calculate(self, atoms=None, properties=None, system_changes=all_changes):
