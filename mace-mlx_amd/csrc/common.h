@@ -79,10 +79,13 @@ struct FrontParams {
 // Rounding of the stored activations of the feature path: RND_F16 (float16 feature
 // policy) to the nearest fp16 value, RND_BF16 (bfloat16 policy) to the nearest bf16
 // value (ties to even: the upper 16 bits of the fp32 pattern after adding 0x7fff plus
-// the lowest kept bit; infinities and NaNs keep their class), RND_NONE leaves x
+// the lowest kept bit; infinities stay infinite; a NaN, which the addition could carry
+// into the sign or exponent, becomes the quiet NaN of its upper bits instead), RND_NONE
+// leaves x
 constexpr int RND_NONE = 0, RND_F16 = 1, RND_BF16 = 2;
 __host__ __device__ __forceinline__ float round_bf16(float x) {
   unsigned u = __builtin_bit_cast(unsigned, x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return __builtin_bit_cast(float, (u | 0x00400000u) & 0xffff0000u);
   u += 0x7fffu + ((u >> 16) & 1u);
   return __builtin_bit_cast(float, u & 0xffff0000u);
 }

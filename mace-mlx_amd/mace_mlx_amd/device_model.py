@@ -77,9 +77,12 @@ def round_weights_fp16(w: Dict[str, np.ndarray]) -> Dict[str, np.ndarray]:
 
 def to_bf16(x) -> np.ndarray:
     """float32 values rounded to the nearest bfloat16 value (ties to even), returned as float64:
-    the upper 16 bits of the float32 pattern after adding 0x7fff plus the lowest kept bit."""
+    the upper 16 bits of the float32 pattern after adding 0x7fff plus the lowest kept bit; a NaN
+    becomes the quiet NaN of its upper bits (the addition could carry it into the sign or the
+    exponent).  The device's round_bf16 is the same bit operation."""
     u = np.ascontiguousarray(np.asarray(x, dtype=np.float32)).view(np.uint32).astype(np.uint64)
-    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    u = np.where(nan, (u | 0x00400000) & 0xFFFF0000, (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000)
     return u.astype(np.uint32).view(np.float32).astype(np.float64)
 
 

@@ -135,6 +135,14 @@ def test_bf16_rounding_matches_torch():
     want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float64).numpy()
     np.testing.assert_array_equal(to_bf16(x), want)
     assert np.array_equal(np.signbit(to_bf16(x)), np.signbit(want))
+    # NaNs stay NaN with their sign, including the patterns the 0x7fff carry would turn into
+    # -0.0 (0x7fffffff), +0.0 (0xffffffff) or an infinity (0x7f800001)
+    nans = np.array([0x7FFFFFFF, 0xFFFFFFFF, 0x7F800001, 0xFF800001, 0x7FC00000, 0x7FBFFFFF, 0xFFC12345],
+                    np.uint32).view(np.float32)
+    got = to_bf16(nans)
+    assert np.isnan(got).all()
+    assert np.array_equal(np.signbit(got), np.signbit(nans))
+    assert np.isnan(torch.from_numpy(nans).to(torch.bfloat16).to(torch.float64).numpy()).all()
 
 
 def test_bfloat16_policy_rounds_all_but_pinned_weights():
