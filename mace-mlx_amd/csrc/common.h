@@ -9,8 +9,13 @@
 namespace mace {
 
 // Channel multiplicity of every irrep block.  The launchers check it at model
-// load time; all kernels are compiled for this width.
-constexpr int NC = 128;
+// load time; all kernels are compiled for this width (MACE_NC: 128, or 256 for the
+// wide library; a multiple of 64, the channel slice of the tensor-product kernels).
+#ifndef MACE_NC
+#define MACE_NC 128
+#endif
+constexpr int NC = MACE_NC;
+static_assert(NC % 64 == 0, "channel count must be a multiple of 64");
 constexpr int NBESSEL_MAX = 16;
 constexpr int RADIAL_H = 64;   // radial-MLP hidden width compiled in
 

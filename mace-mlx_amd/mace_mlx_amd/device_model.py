@@ -36,7 +36,12 @@ import numpy as np
 
 from .cg import u_matrix, wigner_3j
 from .irreps import Irrep, Irreps
-from .model_io import COVALENT_RADII, ModelConfig, conv_tp_instructions, linear_instructions, select_head
+from .model_io import (COVALENT_RADII, ModelConfig, conv_tp_instructions, linear_instructions, pad_channels,
+                       select_head)
+
+# channel multiplicity the HIP engine is compiled for (csrc/common.h NC); models with fewer
+# channels are zero-padded to it
+ENGINE_CHANNELS = 128
 
 
 class UnsupportedModel(NotImplementedError):
@@ -116,6 +121,16 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = 
     cfg, w = select_head(cfg, w, head)
     if cfg.model_type not in ("MACE", "ScaleShiftMACE"):
         raise UnsupportedModel(f"model_type={cfg.model_type}")
+    if cfg.num_features != ENGINE_CHANNELS:
+        # fewer channels than the engine is compiled for (e.g. MACE-OFF small, 96): the same model
+        # with zero channels appended and the path weights compensated (model_io.pad_channels)
+        if cfg.num_features > ENGINE_CHANNELS:
+            raise UnsupportedModel(f"{cfg.num_features} channels (the engine is compiled for at most "
+                                   f"{ENGINE_CHANNELS})")
+        try:
+            cfg, w = pad_channels(cfg, w, ENGINE_CHANNELS)
+        except NotImplementedError as exc:
+            raise UnsupportedModel(str(exc)) from exc
     C = cfg.num_features
     nel = cfg.num_elements
     if cfg.max_ell != 3:

@@ -498,3 +498,61 @@ def select_head(cfg: ModelConfig, w: Dict[str, np.ndarray],
             v = v[:, h:h + 1]
         out[k] = np.ascontiguousarray(v)
     return out_cfg, out
+
+
+# ---------------------------------------------------------------------------
+# Channel padding: a model of C channels as an equivalent model of C' > C channels
+# ---------------------------------------------------------------------------
+
+def pad_channels(cfg: ModelConfig, w: Dict[str, np.ndarray], target: int):
+    """(cfg', w') with every irrep multiplicity C raised to ``target`` such that the padded
+    model computes the same energies as the original: the extra channels carry zeros
+    everywhere.  Rules, checked against the weight inventories of both configs:
+
+    * per-channel weights -- conv-TP weights of the radial MLP's last layer (rows slot-major,
+      channel-minor, `tensor_product.py:728-735`), symmetric-contraction weights
+      [n_el][k][C], the node embedding's outputs, output columns of every linear -- are
+      zero-padded;
+    * weights summed over an input channel axis (EquivariantLinear `linear.py:46-74` and the
+      skip FCTP `tensor_product.py:1080-1098`, whose path weights are 1/sqrt(fan-in) with the
+      fan-in proportional to C) are zero-padded and multiplied by sqrt(target / C), so that the
+      padded model's path weight 1/sqrt(n target) reproduces 1/sqrt(n C).
+
+    A zero channel stays zero through the channel-wise conv TP, the symmetric contraction (no
+    constant term) and the gate-free readouts, so no padded value reaches a real one."""
+    C = cfg.num_features
+    if any(b.mul != C for b in cfg.hidden):
+        raise NotImplementedError(f"hidden irreps {cfg.hidden_irreps} with unequal multiplicities")
+    if target < C:
+        raise ValueError(f"cannot pad {C} channels down to {target}")
+    if target == C:
+        return cfg, dict(w)
+    if cfg.nonlinear:
+        raise NotImplementedError("channel padding of the non-linear interaction block")
+    hid = Irreps([(target, b.ir) for b in cfg.hidden])
+    cfg2 = replace(cfg, hidden_irreps=str(hid))
+    s1, s2 = weight_shapes(cfg), weight_shapes(cfg2)
+    assert set(s1) == set(s2)
+    f = math.sqrt(target / C)
+    out: Dict[str, np.ndarray] = {}
+    for k, v in w.items():
+        a, b = s1.get(k), s2.get(k)
+        v = np.asarray(v)
+        if a is None or tuple(a) == tuple(b):
+            out[k] = v
+            continue
+        if ".conv_tp_weights." in k:
+            n = a[0] // C
+            assert a[0] == n * C and b[0] == n * target and a[1:] == b[1:], (k, a, b)
+            p = np.zeros((n, target) + tuple(a[1:]), dtype=v.dtype)
+            p[:, :C] = v.reshape((n, C) + tuple(a[1:]))
+            out[k] = p.reshape(b)
+            continue
+        assert len(a) == len(b), (k, a, b)
+        axes = [i for i in range(len(a)) if a[i] != b[i]]
+        assert all(a[i] == C and b[i] == target for i in axes), (k, a, b)
+        p = np.zeros(b, dtype=np.float64)      # the compensation factor applied in float64
+        p[tuple(slice(0, s) for s in a)] = v
+        summed = (".symmetric_contractions." not in k and not k.startswith("node_embedding.") and 0 in axes)
+        out[k] = p * f if summed else p
+    return cfg2, out

@@ -104,6 +104,36 @@ def arch_config(arch: str, num_elements: int = 1, z_table=None, zbl: bool = Fals
     )
 
 
+# MACE-OFF23 elements (H, C, N, O, F, P, S, Cl, Br, I) and widths by model size
+OFF_ELEMENTS = [1, 6, 7, 8, 9, 15, 16, 17, 35, 53]
+OFF_HIDDEN = {"small": "96x0e", "medium": "128x0e+128x1o", "large": "192x0e+192x1o+192x2e"}
+
+
+def off_config(size: str = "small") -> ModelConfig:
+    """The layout of the MACE-OFF23 organic force fields that ``mace_off`` loads (`README.md:75`,
+    `calculators.py:601-617`): ScaleShiftMACE over ten elements, r_max 5 A, non-residual first
+    interaction, 96 / 128 / 192 channels.  E0, scale / shift and avg_num_neighbors are chosen so
+    that a random model's interaction energy is not hidden under E0 and its forces are O(1) eV/A."""
+    rng = np.random.default_rng(40)
+    return ModelConfig(
+        r_max=5.0, num_bessel=8, num_polynomial_cutoff=5, max_ell=3, num_interactions=2,
+        hidden_irreps=OFF_HIDDEN[size], correlation=[3, 3], num_elements=len(OFF_ELEMENTS),
+        atomic_energies=[float(x) for x in -rng.uniform(0.5, 2.0, len(OFF_ELEMENTS))],
+        avg_num_neighbors=3.0, radial_MLP=[64, 64, 64], model_type="ScaleShiftMACE", scale=8.0,
+        shift=0.05, z_table=list(OFF_ELEMENTS), first_interaction_nonresidual=True)
+
+
+def organic_cluster(n: int = 48, seed: int = 41) -> System:
+    """A non-periodic cluster of H / C / N / O atoms on a rattled 1.5 A grid (a stand-in for
+    the organic molecules MACE-OFF is used on)."""
+    rng = np.random.default_rng(seed)
+    k = int(np.ceil(n ** (1 / 3)))
+    g = np.stack(np.meshgrid(*[np.arange(k)] * 3, indexing="ij"), -1).reshape(-1, 3)[:n]
+    pos = 10.0 + 1.5 * g + rng.normal(scale=0.1, size=(n, 3))
+    z = np.array([1, 6, 7, 8])[rng.integers(0, 4, n)]
+    return System(pos, z.astype(np.int64), np.eye(3) * 40.0, np.array([False, False, False]))
+
+
 @dataclass
 class BenchConfig:
     index: int

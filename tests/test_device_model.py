@@ -284,3 +284,25 @@ def test_mh1_kernel_formulation_matches_oracle(apply_cutoff, agnostic, edge):
     # the engine's tensors are float32 (folded in float64, then rounded): ~1e-8 relative
     assert abs(Ek - E) < 1e-6 * max(1.0, abs(E)), (Ek, E)
     np.testing.assert_allclose(nek, ne, rtol=0, atol=1e-6 * max(1.0, np.abs(ne).max()))
+
+
+@pytest.mark.parametrize("arch,C", [("small", 96), ("medium", 96), ("large", 64)])
+def test_narrow_model_padded_in_the_fold(si64, arch, C):
+    """A model with fewer channels than the engine (MACE-OFF small: 96x0e) is folded as its
+    zero-padded 128-channel equivalent; the kernel formulation of the folded tensors matches the
+    oracle evaluating the original model."""
+    s, i, j, S = si64
+    cfg = arch_config(arch, zbl=True)
+    cfg.hidden_irreps = "+".join(f"{C}x{b.ir}" for b in cfg.hidden)
+    w = random_init(cfg, 4)
+    dm = build_device_model(cfg, w)
+    assert dm.dims["num_channels"] == 128
+    sp = np.zeros(len(s), int)
+    Eo, neo = OracleMACE(cfg=cfg, weights=w).energy(s.positions, sp, np.stack([i, j]), S, s.cell)
+    Ek, nek = kernel_model.energy(dm, s.positions, sp, i, j, S.astype(float), s.cell)
+    np.testing.assert_allclose(nek, neo, atol=5e-6)
+    assert abs(Ek - Eo) < 1e-6 * max(1.0, abs(Eo)) * len(s)
+    wide = arch_config(arch)
+    wide.hidden_irreps = "+".join(f"192x{b.ir}" for b in wide.hidden)
+    with pytest.raises(UnsupportedModel):
+        build_device_model(wide, random_init(wide, 0))

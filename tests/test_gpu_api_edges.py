@@ -117,3 +117,45 @@ def test_skin_zero_rebuilds_every_step():
     case.eng.step(s.positions)
     case.eng.step(s.positions)
     assert case.eng.timings()[1] == 0
+
+
+def test_mace_off_small_width_96():
+    """A MACE-OFF-small-shaped model (96x0e, ten elements, r_max 5 A, non-residual first block,
+    ScaleShiftMACE) runs as its zero-padded 128-channel equivalent; E, F and stress against the
+    float64 oracle evaluating the original 96-channel model."""
+    from mace_mlx_amd.systems import off_config, organic_cluster
+    cfg = off_config("small")
+    case = Case(cfg, seed=42)
+    assert case.dm.dims["num_channels"] == 128
+    s = organic_cluster()
+    got = case.run(s)
+    edges = case.edges()
+    assert edge_set(*edges) == bruteforce_edges(s, cutoff=5.5)
+    assert_parity(got, case.reference(s, got["sp"], edges), len(s))
+    per = rattle(diamond_si((2, 2, 2)), 0.05, 43)
+    per.positions *= 0.7                       # C-C distances of ~1.6 A
+    per.cell *= 0.7
+    per.numbers = np.full(len(per), 6)
+    got = case.run(per, stress=True)
+    edges = case.edges()
+    assert_parity(got, case.reference(per, got["sp"], edges, stress=True), len(per), stress=True)
+
+
+def test_mace_off_calculator_from_cache(tmp_path, monkeypatch):
+    """``mace_off("small")`` resolves the converted model from the reference's cache layout
+    (`<cache>/off-small/v2`) and evaluates it through the ASE calculator API."""
+    from mace_mlx_amd import mace_off
+    from mace_mlx_amd.systems import off_config, organic_cluster
+    cfg = off_config("small")
+    w = random_init(cfg, 44)
+    save_model(tmp_path / "off-small" / "v2", cfg, w)
+    monkeypatch.setenv("MACE_MLX_CACHE_DIR", str(tmp_path))
+    calc = mace_off("small", device="cuda")
+    s = organic_cluster(30, 45)
+    calc.calculate(s, ["energy", "forces"])
+    z = {int(v): k for k, v in enumerate(cfg.z_table)}
+    sp = np.array([z[int(a)] for a in s.numbers])
+    i, j, S = neighbor_list(s.positions, s.cell, s.pbc, cfg.r_max + 0.5)
+    E, F, ne = OracleMACE(cfg=cfg, weights=w).energy_forces(s.positions, sp, np.stack([i, j]), S, s.cell)
+    assert_parity({"E": calc.results["energy"], "F": calc.results["forces"], "ne": calc.results["node_energy"]},
+                  {"E": E, "F": F, "ne": ne}, len(s))
