@@ -1005,8 +1005,11 @@ __device__ __forceinline__ int lane_opaque() {
 }
 
 // one 64-wide layer from the lane's 16 values v (all four output tiles t'):
-// acc[t'] = (A_t' x v) with A = tile image w[c][t'][hi, lo][lane], times winv
-template <bool OPQ>
+// acc[t'] = (A_t' x v) with A = tile image w[c][t'][hi, lo][lane], times winv.  ALO / XLO: the
+// weights' / the inputs' lo planes may be nonzero; under a half-precision feature policy the
+// rounded weights and activations have zero lo planes (an fp16 value, or a bf16 value, times a
+// power of two is one fp16 value), so those products add exact zeros and are skipped
+template <bool OPQ, bool ALO = true, bool XLO = true>
 __device__ __forceinline__ void layer64x(const h8 (*w)[4][2][64], const float* v, float winv, f4v* acc) {
   const int l = lane_opaque<OPQ>();
   float inv;
@@ -1027,9 +1030,9 @@ __device__ __forceinline__ void layer64x(const h8 (*w)[4][2][64], const float* v
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const h8 wh = w[c][t][0][l], wl = w[c][t][1][l];
-      d[t] = mfma16h(wl, xh, d[t]);
-      d[t] = mfma16h(wh, xl, d[t]);
+      const h8 wh = w[c][t][0][l];
+      if constexpr (ALO) d[t] = mfma16h(w[c][t][1][l], xh, d[t]);
+      if constexpr (XLO) d[t] = mfma16h(wh, xl, d[t]);
       d[t] = mfma16h(wh, xh, d[t]);
     }
   }
@@ -1044,6 +1047,9 @@ __device__ __forceinline__ void layer64x(const h8 (*w)[4][2][64], const float* v
 template <bool OPQ, int RND>
 __device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* winv, int64_t E, int64_t e0, int nb,
                                              const float* __restrict__ ef, f4v* a1, f4v* a2, f4v* a3, float* dsp) {
+  // half-precision policies: weights, features and activations are rounded values (zero lo
+  // planes), so one product per operand pair
+  constexpr bool FULL = RND == RND_NONE;
   const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t e = e0 + r;
   float x[8];
@@ -1067,9 +1073,12 @@ __device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* win
     const int lo = lane_opaque<OPQ>();
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const h8 wh = sw.w0[t][0][lo], wl = sw.w0[t][1][lo];
-      f4v d = mfma16h(wl, xh, f4v{0.f, 0.f, 0.f, 0.f});
-      d = mfma16h(wh, xl, d);
+      const h8 wh = sw.w0[t][0][lo];
+      f4v d = f4v{0.f, 0.f, 0.f, 0.f};
+      if constexpr (FULL) {
+        d = mfma16h(sw.w0[t][1][lo], xh, d);
+        d = mfma16h(wh, xl, d);
+      }
       d = mfma16h(wh, xh, d);
       a1[t] = d * inv;
     }
@@ -1078,11 +1087,11 @@ __device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* win
 #pragma unroll
   for (int q = 0; q < 16; ++q) v[q] = qh(silu(a1[q >> 2][q & 3]), RND);
   if (dsp) store_ds(dsp, a1);
-  layer64x<OPQ>(sw.w1, v, winv[1], a2);
+  layer64x<OPQ, FULL, FULL>(sw.w1, v, winv[1], a2);
 #pragma unroll
   for (int q = 0; q < 16; ++q) v[q] = qh(silu(a2[q >> 2][q & 3]), RND);
   if (dsp) store_ds(dsp + H, a2);
-  layer64x<OPQ>(sw.w2, v, winv[2], a3);
+  layer64x<OPQ, FULL, FULL>(sw.w2, v, winv[2], a3);
   if (dsp) store_ds(dsp + 2 * H, a3);
 }
 
@@ -1179,11 +1188,14 @@ __global__ void __launch_bounds__(64 * NW) k_mlp_hidden_bwd_x(int64_t E, int nb,
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] *= dv[q];
     dsl(1, dv);
-    layer64x<RECOMP>(sw.w2T, v, wi.w[2], acc);
+    // the gradients are float32 (lo planes nonzero); the weights' lo planes are zero under a
+    // half-precision policy
+    constexpr bool WLO = RND == RND_NONE;
+    layer64x<RECOMP, WLO, true>(sw.w2T, v, wi.w[2], acc);
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = acc[q >> 2][q & 3] * dv[q];
     dsl(0, dv);
-    layer64x<RECOMP>(sw.w1T, v, wi.w[1], acc);
+    layer64x<RECOMP, WLO, true>(sw.w1T, v, wi.w[1], acc);
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = acc[q >> 2][q & 3] * dv[q];
     // g_ef = g_a1 W0^T: one output tile (rows k < nb)
@@ -1202,8 +1214,8 @@ __global__ void __launch_bounds__(64 * NW) k_mlp_hidden_bwd_x(int64_t E, int nb,
         xl[j] = lo;
       }
       const int lo = lane_opaque<RECOMP>();
-      const h8 wh = sw.w0T[c][0][lo], wl = sw.w0T[c][1][lo];
-      o = mfma16h(wl, xh, o);
+      const h8 wh = sw.w0T[c][0][lo];
+      if constexpr (WLO) o = mfma16h(sw.w0T[c][1][lo], xh, o);
       o = mfma16h(wh, xl, o);
       o = mfma16h(wh, xh, o);
     }

@@ -725,7 +725,10 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   for (int off = 1; off < XW; off <<= 1) ns = max(ns, __shfl_xor(ns, off));
   const int nsteps = __builtin_amdgcn_readfirstlane(ns);
 
-  h8 wa[NCTW][2][2];  // [tile][k step][hi, lo]
+  // Under a half-precision policy (RND) W3 and h3 hold rounded values: their lo planes are zero,
+  // so a w tile is the one product hi.hi (the same sums: the skipped products add exact zeros)
+  constexpr bool FULL = RND == RND_NONE;
+  h8 wa[NCTW][2][FULL ? 2 : 1];  // [tile][k step][hi, lo]
 #pragma unroll
   for (int m = 0; m < NCTW; ++m) {
     const int ct = wv + XW * m;
@@ -735,7 +738,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         wa[m][c][0] = *reinterpret_cast<const h8*>(W3Tx + col * XH + 32 * c + 8 * g);
-        wa[m][c][1] = *reinterpret_cast<const h8*>(W3Tx + ((int64_t)a.W + col) * XH + 32 * c + 8 * g);
+        if constexpr (FULL) wa[m][c][FULL ? 1 : 0] = *reinterpret_cast<const h8*>(W3Tx + ((int64_t)a.W + col) * XH + 32 * c + 8 * g);
       }
     }
   }
@@ -814,7 +817,8 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   auto load_h = [&](int t) {  // tile t's share
     // columns past a receiver's end: not stored
     const int64_t row = min<int64_t>(hb0 + EPW * (TPS * t + hs) + hr % EPW, elast);
-    H.h = *reinterpret_cast<const hv*>(h3x + row * 2 * XH + hpl * XH + HQ * hq);
+    // (half policies: the lo-plane threads fetch the hi row beside them, same cache lines)
+    H.h = *reinterpret_cast<const hv*>(h3x + row * 2 * XH + (FULL ? hpl : 0) * XH + HQ * hq);
     H.hinv = h3inv[row];
     if constexpr (NL) H.cut = buf_load(cutv, 4u * (unsigned)row);  // 0 without a cut array
   };
@@ -855,7 +859,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         bx[c][0] = *reinterpret_cast<const h8*>(hrow + 32 * c);
-        bx[c][1] = *reinterpret_cast<const h8*>(hrow + TC * 72 + 32 * c);
+        if constexpr (FULL) bx[c][1] = *reinterpret_cast<const h8*>(hrow + TC * 72 + 32 * c);
       }
       f4v d[NCTW];
 #pragma unroll
@@ -863,11 +867,12 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int p = 0; p < 3; ++p)
+        for (int p = FULL ? 0 : 2; p < 3; ++p)
 #pragma unroll
           for (int m = 0; m < NCTW; ++m)
             if (CT % XW == 0 || wv + XW * m < CT)  // every wave's tiles exist when XW divides CT
-              d[m] = mfma16h(wa[m][c][p == 2 ? 0 : p ^ 1], bx[c][p == 1 ? 1 : 0], d[m]);  // lo.hi, hi.lo, hi.hi
+              d[m] = mfma16h(wa[m][c][p == 2 ? 0 : (p ^ 1) & (FULL ? 1 : 0)],
+                             bx[c][p == 1 ? 1 : 0], d[m]);  // lo.hi, hi.lo, hi.hi
       const float bsc = hiv[(t & 1) * TC + col] * a.wscale;
       if constexpr (NL) {
         const float cc = hcv[(t & 1) * TC + col];
@@ -1213,15 +1218,18 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
       if (T::l1(s) == L1) b3c[s] = a.b3[s * NC + c0 + u];
   }
 
-  // W3 rows q = 16 qt + r, group k steps kh G .. kh G + G - 1 (32 columns each)
+  // W3 rows q = 16 qt + r, group k steps kh G .. kh G + G - 1 (32 columns each).  Under a
+  // half-precision policy (WF) W3 holds rounded values: its lo plane is zero and the product
+  // lo.hi is skipped (it adds exact zeros); dL/dw stays float32, so hi.lo and hi.hi remain
+  constexpr bool WLO = WF == RND_NONE;
   const int qt = wv & 3, kh = wv >> 2;
-  h8 wa[G][2];
+  h8 wa[G][WLO ? 2 : 1];
 #pragma unroll
   for (int ks = 0; ks < G; ++ks) {
     const int kk = kh * G + ks;
     const int64_t o = (int64_t)(16 * qt + r) * a.W + GR::slot(kk >> 1) * NC + c0 + 32 * (kk & 1) + 8 * g;
     wa[ks][0] = *reinterpret_cast<const h8*>(W3x + o);
-    wa[ks][1] = *reinterpret_cast<const h8*>(W3x + (int64_t)XH * a.W + o);
+    if constexpr (WLO) wa[ks][WLO ? 1 : 0] = *reinterpret_cast<const h8*>(W3x + (int64_t)XH * a.W + o);
   }
   // dL/dM of this wave's receiver (group slots, slice channels); for l1 = 1 only through
   // its CG contraction R (tp_edge_vjp_l1)
@@ -1398,7 +1406,7 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
       for (int h = 0; h < 2; ++h) {
         const _Float16* src = pt + (16 * h + r) * RS + 32 * (kh * G + ks) + 8 * g;
         const h8 xh = *reinterpret_cast<const h8*>(src), xl = *reinterpret_cast<const h8*>(src + 32 * RS);
-        acc[h] = mfma16h(wa[ks][1], xh, acc[h]);
+        if constexpr (WLO) acc[h] = mfma16h(wa[ks][WLO ? 1 : 0], xh, acc[h]);
         acc[h] = mfma16h(wa[ks][0], xl, acc[h]);
         acc[h] = mfma16h(wa[ks][0], xh, acc[h]);
       }
