@@ -563,8 +563,6 @@ void build_model(mace_ctx* c) {
     L.dmid = C * n_tp_acc(L.lin);
     L.wn = C * n_tp_slots(L.lin);
     if (d.nonlinear) {
-      if (d.feature_half)
-        fail(MACE_ERR_UNSUPPORTED, "non-linear interaction blocks under a half-precision feature policy");
       build_layer_nonlin(c, L, l);
       continue;
     }
@@ -712,8 +710,9 @@ void ensure_node_buffers(mace_ctx* c) {
 
 // Which kernels a step runs (from the model and the two switches).  fused: the radial-MLP
 // output layer inside the TP kernels (split products), under every feature policy (the
-// rounding modes are template parameters of the fused forward; the non-linear interaction
-// block exists under the float32 policy only); split: the radial MLP's hidden layers on split-fp16
+// rounding modes are template parameters of the fused forward; under a half-precision policy the
+// non-linear interaction block runs on this path only, check_step_path); split: the radial MLP's
+// hidden layers on split-fp16
 // products (fused path, or the float32 policy); h16: the float16 policy's separate path with
 // fp16 h3 / w / dL/dw arrays.  Neither split nor h16: fp32 products, silu' saved (ds).
 struct StepPath {
@@ -1195,6 +1194,15 @@ void invalidate_node_state(mace_ctx* c) {
 // First-layer node features h0 and the first linear_up output: functions of the species
 // only (the embedding is stop_gradient'ed, model.py:382), so they are written once per
 // system / model / buffer set, before the step, not by every step.
+// Product paths a step can take for the loaded model, checked before anything is launched or
+// captured: non-linear interaction blocks under a half-precision policy run on the fused
+// split-product path only (the comparison paths keep float32 buffers)
+void check_step_path(const mace_ctx* c) {
+  if (c->dims.nonlinear && c->dims.feature_half && !step_path(c).fused)
+    fail(MACE_ERR_UNSUPPORTED, "non-linear interaction blocks under a half-precision policy run on the fused "
+                               "split-product path only (split products and the fused TP on)");
+}
+
 void ensure_embed(mace_ctx* c) {
   if (c->embed_valid) return;
   Site s(c, "embed");
@@ -1268,10 +1276,14 @@ void forward_nonlin(mace_ctx* c, int l, const float* h, float* hn) {
   const float* cut = c->dims.separate_cutoff ? c->cutv.p : nullptr;
   const bool split = c->split_products;  // h3 W3 on fp16 matrix cores (split operands)
   const bool fused = step_path(c).fused;   // ... inside the TP kernels
+  // rounding mode of the stored activations (float16 / bfloat16 feature policies): the default
+  // fused path carries it; the comparison paths (separate radial output pass, fp32 matrix cores)
+  // keep their float32 buffers and run under the float32 policy only
+  const int half = c->dims.feature_half;  // check_step_path: half implies split && fused here
   {  // LayerNorm radial MLP (last hidden activation) and the edge densities
     Site s(c, lname("mlp_ln", l));
     launch_rmlp_ln_fwd(st, E, nb, c->ef.p, cut, c->sender.p, c->receiver.p, c->species.p, L.mlp_tiles.p,
-                       L.dmlp_tiles.p, L.lnp(), c->h3.p, split ? c->h3inv.p : nullptr, c->mh_dens.p);
+                       L.dmlp_tiles.p, L.lnp(), c->h3.p, split ? c->h3inv.p : nullptr, c->mh_dens.p, half);
   }
   if (!fused) {  // w = (h3 W3 + b3) cut
     Site s(c, lname("mlp_out", l));
@@ -1286,13 +1298,14 @@ void forward_nonlin(mace_ctx* c, int l, const float* h, float* hn) {
     GemmGroup g{};
     for (int b = 0; b < std::min(L.lin, L.ledge); ++b)
       g.p[g.n++] = gprob(N, 2 * b + 1, NC, NC, h, L.din, NC * b * b, 0, L.upT[b].p, L.h_up.p, L.dedge, NC * b * b, 0);
+    g.round_half = half;
     run_gemm(c, st, g);
   }
   {
     Site s(c, lname("tp_fwd", l));
     if (fused)  // w = (h3 W3 + b3) cut formed per edge tile, and stored for the VJP
       launch_tpx_fwd(st, L.ledge, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, c->h3.p, c->h3inv.p,
-                     L.mlpT3x.p, L.wn, L.w3inv, L.h_up.p, c->M.p, L.w.p, RND_NONE, L.b3.p, cut);
+                     L.mlpT3x.p, L.wn, L.w3inv, L.h_up.p, c->M.p, L.w.p, half, L.b3.p, cut);
     else
       launch_tp_fwd(st, L.ledge, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.w.p, L.h_up.p, c->M.p, 0);
   }
@@ -1308,6 +1321,7 @@ void forward_nonlin(mace_ctx* c, int l, const float* h, float* hn) {
       g.p[g.n++] = gprob(N, d, NC, lo == 0 ? 4 * NC : NC, L.h_up.p, L.dedge, NC * lo * lo, 0, L.resT[lo].p, L.R.p,
                          L.nres, gate_in_base(lo), NC * d);
     }
+    g.round_half = half;
     run_gemm(c, st, g);
   }
   {  // Q = linear_1(M) / (beta rho + alpha)
@@ -1322,11 +1336,12 @@ void forward_nonlin(mace_ctx* c, int l, const float* h, float* hn) {
                          L.linT[lo].p, L.Q.p, kGateInDim, gate_in_base(lo), NC * d);
       g.p[g.n - 1].rowscale = L.rinv.p;
     }
+    g.round_half = half;
     run_gemm(c, st, g);
   }
   {
     Site s(c, lname("gate", l));
-    launch_mh1_gate(st, N, L.Q.p, L.R.p, L.nres, L.Gt.p);
+    launch_mh1_gate(st, N, L.Q.p, L.R.p, L.nres, L.Gt.p, half);
   }
   {
     Site s(c, lname("linear_2", l));
@@ -1334,12 +1349,13 @@ void forward_nonlin(mace_ctx* c, int l, const float* h, float* hn) {
     for (int lo = 0; lo < 4; ++lo)
       g.p[g.n++] = gprob(N, 2 * lo + 1, NC, NC, L.Gt.p, L.dint, NC * lo * lo, 0, L.lin2T[lo].p, L.A.p, L.dint,
                          NC * lo * lo, 0);
+    g.round_half = half;
     run_gemm(c, st, g);
   }
   const float* scw[3] = {L.sc[0].p, L.sc[1].p, L.sc[2].p};
   {
     Site s(c, lname("sc_fwd", l));
-    launch_sc_fwd(st, N, L.lhid, L.corr, L.A.p, L.dint, sc_species(c), scw, c->B.p, L.dhid, 0);
+    launch_sc_fwd(st, N, L.lhid, L.corr, L.A.p, L.dint, sc_species(c), scw, c->B.p, L.dhid, half);
   }
   {  // h' = PLin(B) + Skip(h) (plain linear skip)
     Site s(c, lname("linear_prod", l));
@@ -1356,6 +1372,7 @@ void forward_nonlin(mace_ctx* c, int l, const float* h, float* hn) {
       }
       g.p[g.n++] = P;
     }
+    g.round_half = half;
     run_gemm(c, st, g);
   }
 }
@@ -1421,7 +1438,7 @@ void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int fi
     }
     launch_tpx_bwd(st, Ly.ledge, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p, Ly.mlp3x.p, Ly.wn,
                    Ly.w3inv, Ly.h_up.p, c->gM.p, c->pos_s.p, l > 0 ? c->gxe.p : nullptr, c->gY.p, gyp, acc_gy,
-                   c->gh3p.p, RND_NONE, Ly.b3.p, c->gwb.p);
+                   c->gh3p.p, c->dims.feature_half, Ly.b3.p, c->gwb.p);  // w as the forward stored it
   } else {
     Site s(c, lname("tp_bwd", l));
     launch_tp_bwd_recv(st, Ly.ledge, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p, Ly.h_up.p,
@@ -2047,6 +2064,7 @@ int mace_step(mace_ctx* c, const double* positions, uint32_t flags, double* ener
     if (c->N > 0 && !positions) fail(MACE_ERR_INVALID, "positions is NULL");
     if (!energy) fail(MACE_ERR_INVALID, "energy is NULL");
     set_device(c);
+    check_step_path(c);
     const int N = c->N;
     const bool stress = (flags & MACE_STEP_STRESS) != 0;
     hipStream_t st = c->stream;
@@ -2146,6 +2164,7 @@ int mace_step_device(mace_ctx* c, const double* d_positions, uint32_t flags, dou
     if (!c->system_ready) fail(MACE_ERR_STATE, "system not set");
     if ((c->N > 0 && !d_positions) || !d_out) fail(MACE_ERR_INVALID, "NULL device pointer");
     set_device(c);
+    check_step_path(c);
     const int N = c->N;
     hipStream_t st = c->stream;
     bool rebuilt = false;
@@ -2205,6 +2224,7 @@ int mace_step_device_noalloc(mace_ctx* c, const double* d_positions, uint32_t fl
            "the maximum is %zu (use mace_step_device)",
            c->N, (long long)E, e_n + v_n, kScratchDoubles);
     set_device(c);
+    check_step_path(c);
     const bool stress = (flags & MACE_STEP_STRESS) != 0;
     double* e_part = c->scratch;      // every block writes its own slot: nothing to clear
     double* vir_part = c->scratch + e_n;

@@ -207,10 +207,11 @@ struct LnMlpParams {
 };
 // h3 = silu(LN(...)) of the third layer, fp32 [E][64] with h3inv null, else split pairs
 // [E][2][64] with inverse row scales h3inv[E] (as launch_mlp_hidden mode 2);
-// dens[e] = tanh(x^2) cut[e] (cut may be null: 1)
+// dens[e] = tanh(x^2) cut[e] (cut may be null: 1); both rounded by mode half (RND_*, the feature
+// policy) before they are stored
 void launch_rmlp_ln_fwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut,
                         const int* sender, const int* receiver, const int* species, const void* tiles,
-                        const void* dtiles, const LnMlpParams& P, void* h3, float* h3inv, float* dens);
+                        const void* dtiles, const LnMlpParams& P, void* h3, float* h3inv, float* dens, int half);
 // VJP from G = gw W3^T (np partials [np][E][64], added in order), gwb = gw . b3 (np partials
 // [np][E]) and drho ([N], dL/d(sum of the receiver's edge densities)): gef (+)= dL/def ([E][nb])
 // and, with cut, gcut (+)= dL/dcut ([E]); btiles / dbtiles: the transposed images
@@ -227,7 +228,7 @@ size_t mlp_tile_fwd_bytes();  // offset of the transposed image inside an mlp_ti
 constexpr int kGateInDim = 19 * NC;
 void launch_mh1_rho(hipStream_t st, int N, const int* rowptr, const float* dens, float alpha, float beta,
                     float* rinv);
-void launch_mh1_gate(hipStream_t st, int N, const float* Q, const float* R, int nres, float* gout);
+void launch_mh1_gate(hipStream_t st, int N, const float* Q, const float* R, int nres, float* gout, int half);
 void launch_mh1_gate_bwd(hipStream_t st, int N, const float* Q, const float* R, int nres, const float* gG,
                          float* gP);
 void launch_mh1_drho(hipStream_t st, int N, const float* gP, const float* Q, const float* rinv, float beta,

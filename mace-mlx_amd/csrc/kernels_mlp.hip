@@ -1368,7 +1368,7 @@ __global__ void __launch_bounds__(256) k_rmlp_ln_fwd(int64_t E, int nb, const fl
                                                      const int* __restrict__ species, const MlpFwdW* __restrict__ tiles,
                                                      const MlpFwdW* __restrict__ dtiles, LnMlpParams P,
                                                      void* __restrict__ h3, float* __restrict__ h3inv,
-                                                     float* __restrict__ dens) {
+                                                     float* __restrict__ dens, int half) {
   __shared__ MlpFwdW sw;
   __shared__ float4 sdw0[NB4][4][16];
   __shared__ LnSmall S;
@@ -1386,6 +1386,9 @@ __global__ void __launch_bounds__(256) k_rmlp_ln_fwd(int64_t E, int nb, const fl
     const int lo = lane_opaque<true>();
     LnFwdState F;
     ln_mlp_fwd(sw, sdw0, S, P, ef, ec, nb, zs, zr, F, lo);
+    // the stored activation under a half-precision policy (its split lo plane is then zero)
+#pragma unroll
+    for (int q = 0; q < 16; ++q) F.h3[q] = qh(F.h3[q], half);
     if (h3inv) {  // split pairs [E][2][64] with the row scale's inverse, as k_mlp_hidden_x writes them
       float inv;
       const float sc = edge_scale<16>(F.h3, &inv);
@@ -1412,7 +1415,7 @@ __global__ void __launch_bounds__(256) k_rmlp_ln_fwd(int64_t E, int nb, const fl
         *reinterpret_cast<float4*>(static_cast<float*>(h3) + e * H + 16 * t + 4 * g) =
             float4{F.h3[4 * t], F.h3[4 * t + 1], F.h3[4 * t + 2], F.h3[4 * t + 3]};
     }
-    if (e < E && g == 0) dens[e] = tanhf(F.x * F.x) * (cut ? cut[e] : 1.f);
+    if (e < E && g == 0) dens[e] = qh(tanhf(F.x * F.x) * (cut ? cut[e] : 1.f), half);
   }
 }
 
@@ -1665,12 +1668,12 @@ size_t mlp_tile_fwd_bytes() { return sizeof(MlpFwdW); }
 
 void launch_rmlp_ln_fwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut, const int* sender,
                         const int* receiver, const int* species, const void* tiles, const void* dtiles,
-                        const LnMlpParams& P, void* h3, float* h3inv, float* dens) {
+                        const LnMlpParams& P, void* h3, float* h3inv, float* dens, int half) {
   if (E <= 0) return;
   // one 16-edge group per wave up to three blocks per CU (44 KB of LDS each)
   const unsigned grid = (unsigned)std::min<int64_t>((E + 63) / 64, 768);
   MACE_LAUNCH(k_rmlp_ln_fwd, dim3(grid), dim3(256), 0, st, E, nb, ef, cut, sender, receiver, species,
-              static_cast<const MlpFwdW*>(tiles), static_cast<const MlpFwdW*>(dtiles), P, h3, h3inv, dens);
+              static_cast<const MlpFwdW*>(tiles), static_cast<const MlpFwdW*>(dtiles), P, h3, h3inv, dens, half);
 }
 
 void launch_rmlp_ln_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut, const int* sender,

@@ -359,7 +359,7 @@ __global__ void k_embed(int N, const int* __restrict__ species, const float* __r
                         float* __restrict__ h, int half, const float* __restrict__ up_tab, float* __restrict__ h_up) {
   const int n = blockIdx.x, u = threadIdx.x, z = species[n];
   h[(int64_t)n * ld + u] = qh(emb[z * NC + u], half);
-  if (up_tab) h_up[(int64_t)n * ld + u] = up_tab[z * NC + u];
+  if (up_tab) h_up[(int64_t)n * ld + u] = qh(up_tab[z * NC + u], half);
 }
 
 // ---------------------------------------------------------------------------
@@ -703,18 +703,18 @@ __device__ __forceinline__ float gate_in(const float* __restrict__ q, const floa
 
 // one thread per (node, channel): gout = gate(Q + R)
 __global__ void __launch_bounds__(NC) k_mh1_gate(int N, const float* __restrict__ Q, const float* __restrict__ R,
-                                                 int nres, float* __restrict__ gout) {
+                                                 int nres, float* __restrict__ gout, int half) {
   const int n = blockIdx.x, u = threadIdx.x;
   const float* q = Q + (int64_t)n * kGateInDim;
   const float* rr = R + (int64_t)n * nres;
   float* o = gout + (int64_t)n * 16 * NC;
   const float s = gate_in(q, rr, nres, u);
-  o[u] = kSiluNorm * s * sigm(s);
+  o[u] = qh(kSiluNorm * s * sigm(s), half);
 #pragma unroll
   for (int l = 1; l <= 3; ++l) {
     const float gt = kSigmoidNorm * sigm(gate_in(q, rr, nres, l * NC + u));
     const int qb = 4 * NC + NC * (l * l - 1), ob = NC * l * l;
-    for (int m = 0; m < 2 * l + 1; ++m) o[ob + m * NC + u] = gt * gate_in(q, rr, nres, qb + m * NC + u);
+    for (int m = 0; m < 2 * l + 1; ++m) o[ob + m * NC + u] = qh(gt * gate_in(q, rr, nres, qb + m * NC + u), half);
   }
 }
 
@@ -905,9 +905,9 @@ void launch_mh1_rho(hipStream_t st, int N, const int* rowptr, const float* dens,
   MACE_LAUNCH(k_mh1_rho, dim3((N + 3) / 4), dim3(256), 0, st, N, rowptr, dens, alpha, beta, rinv);
 }
 
-void launch_mh1_gate(hipStream_t st, int N, const float* Q, const float* R, int nres, float* gout) {
+void launch_mh1_gate(hipStream_t st, int N, const float* Q, const float* R, int nres, float* gout, int half) {
   if (N <= 0) return;
-  MACE_LAUNCH(k_mh1_gate, dim3(N), dim3(NC), 0, st, N, Q, R, nres, gout);
+  MACE_LAUNCH(k_mh1_gate, dim3(N), dim3(NC), 0, st, N, Q, R, nres, gout, half);
 }
 
 void launch_mh1_gate_bwd(hipStream_t st, int N, const float* Q, const float* R, int nres, const float* gG,

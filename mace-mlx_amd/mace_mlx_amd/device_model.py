@@ -85,10 +85,11 @@ def to_bf16(x) -> np.ndarray:
     the upper 16 bits of the float32 pattern after adding 0x7fff plus the lowest kept bit; a NaN
     becomes the quiet NaN of its upper bits (the addition could carry it into the sign or the
     exponent).  The device's round_bf16 is the same bit operation."""
+    shape = np.shape(x)
     u = np.ascontiguousarray(np.asarray(x, dtype=np.float32)).view(np.uint32).astype(np.uint64)
     nan = (u & 0x7FFFFFFF) > 0x7F800000
     u = np.where(nan, (u | 0x00400000) & 0xFFFF0000, (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000)
-    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+    return u.astype(np.uint32).view(np.float32).astype(np.float64).reshape(shape)
 
 
 def round_weights_bf16(w: Dict[str, np.ndarray]) -> Dict[str, np.ndarray]:
@@ -116,8 +117,6 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = 
         raise UnsupportedModel(f"dtype={dtype!r} (float32, float16 and bfloat16 are implemented)")
     w = round_weights(w, dtype)
     cfg.check_supported()
-    if cfg.nonlinear and dtype != "float32":
-        raise UnsupportedModel(f"non-linear interaction blocks under the {dtype} feature policy")
     cfg, w = select_head(cfg, w, head)
     if cfg.model_type not in ("MACE", "ScaleShiftMACE"):
         raise UnsupportedModel(f"model_type={cfg.model_type}")

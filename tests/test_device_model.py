@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import kernel_model
-from mace_mlx_amd.device_model import UnsupportedModel, build_device_model
+from mace_mlx_amd.device_model import UnsupportedModel, build_device_model, round_weights_bf16
 from mace_mlx_amd.model_io import ModelConfig, random_init, weight_shapes
 from mace_mlx_amd.systems import arch_config, diamond_si, lattice, rattle, _FCC
 from oracle.model import OracleMACE
@@ -166,10 +166,14 @@ def test_bfloat16_policy_rounds_all_but_pinned_weights():
     assert dmb.dims["feature_half"] == 2
     for k in dmb.tensors:
         np.testing.assert_array_equal(dmb.tensors[k], dm_r.tensors[k])
+    # mh-1 models take the bf16 policy too: their fold is the float32 fold of the rounded weights
     from test_oracle_mh1 import mh1_config
     c1 = mh1_config()
-    with pytest.raises(UnsupportedModel):
-        build_device_model(c1, random_init(c1, 0), dtype="bfloat16")
+    w1 = random_init(c1, 0)
+    d1, d1r = build_device_model(c1, w1, dtype="bfloat16"), build_device_model(c1, round_weights_bf16(w1))
+    assert d1.dims["feature_half"] == 2
+    for k in d1.tensors:
+        np.testing.assert_array_equal(d1.tensors[k], d1r.tensors[k])
 
 
 def _multihead_cfg(heads, **kw):

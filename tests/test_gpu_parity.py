@@ -209,6 +209,45 @@ def test_bfloat16_feature_policy(arch):
     assert 2 * rel16 < rel, (rel16, rel)
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_mh1_half_precision_policies(dtype):
+    """mh-1 models (`blocks.py:611-807`) under the half-precision policies (`model.py:592-661`: the
+    reference applies set_dtype to every interaction class) against the float64 oracle on the same
+    rounded weights, with the bars of test_float16_feature_policy / test_bfloat16_feature_policy;
+    the same rounded weights on the float32 path meet the float32 tolerances, and the fp16 policy
+    lands closer to the float64 model than bf16.  The comparison paths (split products off or the
+    radial output layer in its own pass) run mh-1 under the float32 policy only and raise."""
+    from test_oracle_mh1 import mh1_config
+    cfg = mh1_config(False, True, "128x0e+128x1o")
+    case = Case(cfg, seed=11, dtype=dtype)
+    rng = np.random.default_rng(12)
+    base = diamond_si((3, 3, 3))
+    base.numbers = np.array([1, 6, 14])[rng.integers(0, 3, len(base))]
+    s = rattle(base, 0.05, 13, rng=rng)
+    got = case.run(s, stress=True)
+    edges = case.edges()
+    ref = case.reference(s, got["sp"], edges, stress=True)
+    de, rel, mx = _fp16_errors(got, ref, len(s))
+    print(f"mh-1 {dtype}: |dE|/N={de:.2e} relF={rel:.2e} max|dF|={mx:.2e}", flush=True)
+    bars = (1e-3, 1e-2, 2e-2) if dtype == "float16" else (3.6e-3, 8e-2, 0.16)
+    assert de <= bars[0] and rel <= bars[1] and mx <= bars[2], (de, rel, mx)
+    assert rel > 1e-6   # the rounding is applied
+    for split, fused in ((True, False), (False, False)):
+        case.eng.set_split_products(split)
+        case.eng.set_fused_tp(fused)
+        with pytest.raises(NotImplementedError):
+            case.run(s)
+    case.eng.set_split_products(True)
+    case.eng.set_fused_tp(True)
+    from mace_mlx_amd.device_model import build_device_model
+    case.eng.load_model(build_device_model(cfg, case.w_model, dtype="float32"))
+    assert_parity(case.run(s, stress=True), ref, len(s), stress=True, energy="per_atom")
+    if dtype == "bfloat16":
+        case.eng.load_model(build_device_model(cfg, case.w_model, dtype="float16"))
+        _, rel16, _ = _fp16_errors(case.run(s), ref, len(s))
+        assert 2 * rel16 < rel, (rel16, rel)
+
+
 # ---------------------------------------------------------------------------
 # full-size configurations: size-independent properties
 # ---------------------------------------------------------------------------
