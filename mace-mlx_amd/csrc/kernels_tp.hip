@@ -1570,16 +1570,20 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
   const _Float16* wt = static_cast<const _Float16*>(W3Tx);
 #define MACE_TPXF(L, R, NLV) \
   MACE_LAUNCH((k_tpx_fwd<L, R, NLV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, hx, h3inv, wt, up, M, w)
-  // the non-linear block (b3 given) runs under the float32 policy only
-#define MACE_TPXF_R(L)         \
-  if (b3)                      \
-    MACE_TPXF(L, RND_NONE, true); \
-  else if (rnd == RND_F16)     \
-    MACE_TPXF(L, RND_F16, false); \
-  else if (rnd == RND_BF16)    \
-    MACE_TPXF(L, RND_BF16, false); \
-  else                         \
-    MACE_TPXF(L, RND_NONE, false);
+  // NL: the non-linear block's bias / envelope epilogue (b3 given)
+#define MACE_TPXF_RN(L, NLV)     \
+  if (rnd == RND_F16)            \
+    MACE_TPXF(L, RND_F16, NLV);  \
+  else if (rnd == RND_BF16)      \
+    MACE_TPXF(L, RND_BF16, NLV); \
+  else                           \
+    MACE_TPXF(L, RND_NONE, NLV);
+#define MACE_TPXF_R(L)          \
+  if (b3) {                     \
+    MACE_TPXF_RN(L, true)       \
+  } else {                      \
+    MACE_TPXF_RN(L, false)      \
+  }
   if (lin == 1) {
     MACE_TPXF_R(1)
   } else if (lin == 2) {
@@ -1588,6 +1592,7 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
     MACE_TPXF_R(3)
   }
 #undef MACE_TPXF_R
+#undef MACE_TPXF_RN
 #undef MACE_TPXF
 }
 
@@ -1602,16 +1607,20 @@ void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
 #define MACE_TPXB(L, GXV, WF, NLV)                                                                         \
   MACE_LAUNCH((k_tpx_bwd<L, GXV, WF, NLV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \
               pos_s, gxe, gY, gh3p)
-  // the non-linear block (b3 given) runs under the float32 policy only
-#define MACE_TPXB_WF(L, GXV)       \
-  if (b3)                          \
-    MACE_TPXB(L, GXV, RND_NONE, true); \
-  else if (wfmt == RND_F16)        \
-    MACE_TPXB(L, GXV, RND_F16, false); \
-  else if (wfmt == RND_BF16)       \
-    MACE_TPXB(L, GXV, RND_BF16, false); \
-  else                             \
-    MACE_TPXB(L, GXV, RND_NONE, false);
+  // NL: the non-linear block's gw . b3 partials (b3 given)
+#define MACE_TPXB_WN(L, GXV, NLV)       \
+  if (wfmt == RND_F16)                  \
+    MACE_TPXB(L, GXV, RND_F16, NLV);    \
+  else if (wfmt == RND_BF16)            \
+    MACE_TPXB(L, GXV, RND_BF16, NLV);   \
+  else                                  \
+    MACE_TPXB(L, GXV, RND_NONE, NLV);
+#define MACE_TPXB_WF(L, GXV)         \
+  if (b3) {                          \
+    MACE_TPXB_WN(L, GXV, true)       \
+  } else {                           \
+    MACE_TPXB_WN(L, GXV, false)      \
+  }
   const bool gx = gxe != nullptr;
   if (lin == 1) {
     if (gx) { MACE_TPXB_WF(1, true) } else { MACE_TPXB_WF(1, false) }
@@ -1621,6 +1630,7 @@ void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
     if (gx) { MACE_TPXB_WF(3, true) } else { MACE_TPXB_WF(3, false) }
   }
 #undef MACE_TPXB_WF
+#undef MACE_TPXB_WN
 #undef MACE_TPXB
 }
 
