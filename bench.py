@@ -239,7 +239,7 @@ def _setup(idx, separate=False, graphs=None):
     bc = make_config(idx)
     weights = random_init(bc.model, 0)
     dm = build_device_model(bc.model, weights, dtype=bc.dtype)
-    eng = Engine(0)
+    eng = Engine(0, channels=dm.dims["num_channels"])
     eng.load_model(dm)
     if separate:
         eng.set_fused_tp(False)

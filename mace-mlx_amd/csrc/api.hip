@@ -60,8 +60,8 @@ std::vector<double*> g_scratch_ptr;  // per device ordinal: address of `scratch`
 
 // partials of dL/dY and dL/dh3 per edge: the receiver VJP writes one per
 // channel half; the fused TP VJP one per (input degree, 64-channel slice)
-constexpr int kGyMax = 6;
-inline int tpx_parts(int lin) { return 2 * lin; }
+constexpr int kGyMax = 3 * NSLICE;  // dL/dY / dL/dh3 partials per edge, at most
+inline int tpx_parts(int lin) { return NSLICE * lin; }  // (channel slice, input block) partials
 [[noreturn]] void fail(int code, const char* fmt, ...) {
   char buf[1024];
   va_list ap;
@@ -763,7 +763,7 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
     c->gwh.ensure(e * maxw);
   else
     c->gw.ensure(e * maxw);
-  c->gscale.ensure(e * 2);
+  c->gscale.ensure(e * NSLICE);
   c->h3inv.ensure(e);
   c->vir_part.ensure(9 * ((e + 255) / 256));
 
@@ -1201,6 +1201,9 @@ void check_step_path(const mace_ctx* c) {
   if (c->dims.nonlinear && c->dims.feature_half && !step_path(c).fused)
     fail(MACE_ERR_UNSUPPORTED, "non-linear interaction blocks under a half-precision policy run on the fused "
                                "split-product path only (split products and the fused TP on)");
+  // the comparison paths' separate radial output kernels are laid out for two channel slices
+  if (NC != 128 && !step_path(c).fused)
+    fail(MACE_ERR_UNSUPPORTED, "the %d-channel engine runs the fused split-product path only", NC);
 }
 
 void ensure_embed(mace_ctx* c) {
@@ -1651,7 +1654,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
   const int half = c->dims.feature_half;
   const StepPath path = step_path(c);
   const bool h16 = path.h16, split = path.split, fused = path.fused;
-  int gyp = 2;  // dL/dY partials per edge
+  int gyp = NSLICE;  // dL/dY partials per edge
   if (fused)
     for (const Layer& Ly : c->layers) gyp = std::max(gyp, tpx_parts(Ly.tl()));
   // dE/dh_L from the nonlinear readout: written by the forward's energy_readout pass

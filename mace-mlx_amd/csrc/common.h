@@ -16,6 +16,7 @@ namespace mace {
 #endif
 constexpr int NC = MACE_NC;
 static_assert(NC % 64 == 0, "channel count must be a multiple of 64");
+constexpr int NSLICE = NC / 64;  // 64-channel slices (one wave's lanes) of a channel block
 constexpr int NBESSEL_MAX = 16;
 constexpr int RADIAL_H = 64;   // radial-MLP hidden width compiled in
 

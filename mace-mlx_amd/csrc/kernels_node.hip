@@ -490,13 +490,15 @@ __device__ __forceinline__ float wave_sum(float v) {
 //   node_e[n] = E0[z] + sum of the atom's pair-repulsion edge energies + readouts,
 //   gh[n][u] = dE/dh_L[n][u] = sum_j W1[u][j] W2[j] silu'(y_j)
 // (dE/dnode_e = 1, so the readout's VJP needs nothing from later kernels).  Lane l
-// computes hidden unit j = l / 4 over the channel quarter 32 (l % 4) .. + 31.
+// computes hidden unit j = l / 4 over the channel quarter (NC / 4) (l % 4) .. + NC / 4 - 1;
+// a channel sum of the linear readouts and of the gradient takes lane l's channels
+// l, l + 64, ... (NSLICE of them), the highest first.
 struct ReadoutArgs {
   const float* h[4];   // h_{l+1}, 0e block at the row start
   const float* ro[4];  // linear readout weights (layers < L-1)
   int ldh[4];
   int L;
-  const float* W1;     // last layer: [128][16]
+  const float* W1;     // last layer: [NC][16]
   const float* W2;     // [16]
   float* gh;           // dE/dh_L, row stride ldgh
   int ldgh;
@@ -519,7 +521,10 @@ __global__ void __launch_bounds__(256) k_energy_readout(int N, const int* __rest
     float v = e0[species[n]] + wave_sum(z);
     for (int k = 0; k + 1 < A.L; ++k) {  // linear readouts
       const float* hn = A.h[k] + (int64_t)n * A.ldh[k];
-      const float a = wave_sum(fmaf(hn[l], A.ro[k][l], hn[l + 64] * A.ro[k][l + 64]));
+      float t = hn[l + 64 * (NSLICE - 1)] * A.ro[k][l + 64 * (NSLICE - 1)];
+#pragma unroll
+      for (int q = NSLICE - 2; q >= 0; --q) t = fmaf(hn[l + 64 * q], A.ro[k][l + 64 * q], t);
+      const float a = wave_sum(t);
       v += qh(a, half);
     }
     {  // MLP readout of the last layer and its gradient
@@ -527,7 +532,7 @@ __global__ void __launch_bounds__(256) k_energy_readout(int N, const int* __rest
       const int j = l >> 2, q = l & 3;
       float y = 0.f;
 #pragma unroll 8
-      for (int u = 32 * q; u < 32 * q + 32; ++u) y = fmaf(hn[u], A.W1[u * 16 + j], y);
+      for (int u = (NC / 4) * q; u < (NC / 4) * (q + 1); ++u) y = fmaf(hn[u], A.W1[u * 16 + j], y);
       y += __shfl_xor(y, 1);
       y += __shfl_xor(y, 2);
       y = qh(y, half);
@@ -537,16 +542,18 @@ __global__ void __launch_bounds__(256) k_energy_readout(int N, const int* __rest
       for (int off = 4; off < 64; off <<= 1) a += __shfl_xor(a, off);
       v += qh(a, half);
       const float cj = A.W2[j] * sg * (1.f + y * (1.f - sg));  // on the four lanes of unit j
-      float g0 = 0.f, g1 = 0.f;
+      float gq[NSLICE];
+#pragma unroll
+      for (int q2 = 0; q2 < NSLICE; ++q2) gq[q2] = 0.f;
 #pragma unroll
       for (int jj = 0; jj < 16; ++jj) {
         const float c = __shfl(cj, 4 * jj);
-        g0 = fmaf(A.W1[l * 16 + jj], c, g0);
-        g1 = fmaf(A.W1[(l + 64) * 16 + jj], c, g1);
+#pragma unroll
+        for (int q2 = 0; q2 < NSLICE; ++q2) gq[q2] = fmaf(A.W1[(l + 64 * q2) * 16 + jj], c, gq[q2]);
       }
       float* gn = A.gh + (int64_t)n * A.ldgh;
-      gn[l] = g0;
-      gn[l + 64] = g1;
+#pragma unroll
+      for (int q2 = 0; q2 < NSLICE; ++q2) gn[l + 64 * q2] = gq[q2];
     }
     if (l == 0) node_e[n] = v;
     acc = (double)v;

@@ -23,7 +23,7 @@
 //
 // dL/dY of an edge is a sum over the 128 channels: each wave reduces its 64
 // lanes' 16 partials with a recursive-halving shuffle (17 exchanges) and
-// stores them in gY[e][half][16] (half = which 64 channels); the edge backward
+// stores them in gY[e][slice][16] (slice = which 64 channels); the edge backward
 // adds the two halves.
 #include <hip/hip_runtime.h>
 
@@ -231,7 +231,7 @@ __global__ void __launch_bounds__(NC* NG) k_tp_fwd(int N, const int* __restrict_
 #pragma unroll
   for (int a = 0; a < T::NACC; ++a) acc[a] = 0.f;
   constexpr bool STAGE = LIN == 3;
-  __shared__ float sM2[STAGE ? 2 * NG * 2 * M2PAD : 1];  // [wave][buffer][M2PAD]
+  __shared__ float sM2[STAGE ? NSLICE * NG * 2 * M2PAD : 1];  // [wave][buffer][M2PAD]
   const int lane = threadIdx.x & 63;
   float* m2buf = sM2 + (STAGE ? (threadIdx.x >> 6) * 2 * M2PAD : 0);
   int gb, ge;
@@ -324,7 +324,7 @@ __device__ __forceinline__ float wave_sum16(const float* v) {
 // float, or _Float16 under the float16 feature policy: each wave then scales
 // its 64 channels x slots by a power of two that maps their largest magnitude
 // into [2^14, 2^15) (so small gradients keep fp16 precision) and stores the
-// inverse in gscale[e][half].
+// inverse in gscale[e][slice].
 template <int NSLOT, typename GWT>
 __device__ __forceinline__ void store_gw(const float* gws, GWT* __restrict__ gwe, float* __restrict__ gscale,
                                          int64_t e, int u) {
@@ -341,16 +341,16 @@ __device__ __forceinline__ void store_gw(const float* gws, GWT* __restrict__ gwe
     const float sc = ldexpf(1.f, 14 - ex);
 #pragma unroll
     for (int s = 0; s < NSLOT; ++s) gwe[s * NC] = (GWT)(gws[s] * sc);
-    if ((u & 63) == 0) gscale[e * 2 + (u >> 6)] = ldexpf(1.f, ex - 14);
+    if ((u & 63) == 0) gscale[e * NSLICE + (u >> 6)] = ldexpf(1.f, ex - 14);
   }
 }
 
-// Store this wave's reduced dL/dY of edge e into gY[e][half][16].
+// Store this wave's reduced dL/dY of edge e into gY[e][slice][16].
 __device__ __forceinline__ void store_gY(const float* gYu, int64_t e, int u, float* __restrict__ gY, int accumulate) {
   const float s = wave_sum16(gYu);
   const int lane = __lane_id();
   if ((lane & 3) == 0) {
-    float* dst = gY + e * 32 + (u >> 6) * 16 + (lane >> 2);
+    float* dst = gY + e * 16 * NSLICE + (u >> 6) * 16 + (lane >> 2);
     *dst = accumulate ? *dst + s : s;
   }
 }
@@ -470,7 +470,7 @@ __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __rest
 #pragma unroll
   for (int a = 0; a < T::NACC; ++a) gm[a] = gMn[a * NC];
   constexpr bool STAGE = LIN == 3;
-  __shared__ float sM2[STAGE ? 2 * NG * 2 * M2PAD : 1];  // [wave][buffer][M2PAD]
+  __shared__ float sM2[STAGE ? NSLICE * NG * 2 * M2PAD : 1];  // [wave][buffer][M2PAD]
   const int lane = threadIdx.x & 63;
   float* m2buf = sM2 + (STAGE ? (threadIdx.x >> 6) * 2 * M2PAD : 0);
   EdgeIn<LIN> cur, nxt;
@@ -1029,7 +1029,7 @@ __global__ void __launch_bounds__(64 * XW, 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_
 // with split operands (W3 as hi / lo planes scaled per matrix; dL/dw split
 // once, by the wave that made it, after scaling the edge's largest magnitude
 // over the block's columns into [2^14, 2^15): its hi / lo planes and inverse
-// scale go to LDS; lo.hi + hi.lo + hi.hi).  p = 2 blockIdx.z + blockIdx.y indexes
+// scale go to LDS; lo.hi + hi.lo + hi.hi).  p = NSLICE blockIdx.z + blockIdx.y indexes
 // the (group, slice) partials; the hidden-layer VJP adds them in order.
 // Roles are swapped (D[q][edge]); wave k takes q tile k & 3 and half k >> 2 of
 // the group's k steps, holding those W3 fragments in registers; the two halves
@@ -1196,7 +1196,7 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   }
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, r = l & 15, g = l >> 4, u = l;
-  const int c0 = 64 * blockIdx.y, nb0 = XW * blockIdx.x, p = 2 * blockIdx.z + blockIdx.y;
+  const int c0 = 64 * blockIdx.y, nb0 = XW * blockIdx.x, p = NSLICE * blockIdx.z + blockIdx.y;
   const int n = nb0 + wv;
   const int beg = rowptr[min(n, a.N)], end = n < a.N ? rowptr[n + 1] : beg;
   const int nr = nb0 + (r >> 1);  // receiver of tile column r
@@ -1565,7 +1565,7 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
                     float wscale, const float* up, float* M, float* w, int rnd, const float* b3, const float* cut) {
   if (N <= 0) return;
   const TpxDims a{N, W, mts, E, wscale, b3, cut};
-  const dim3 grid((unsigned)((N + XW - 1) / XW), 2, (unsigned)lin);  // z: one input block l1 each
+  const dim3 grid((unsigned)((N + XW - 1) / XW), NSLICE, (unsigned)lin);  // y: channel slice; z: input block l1
   const _Float16* hx = static_cast<const _Float16*>(h3x);
   const _Float16* wt = static_cast<const _Float16*>(W3Tx);
 #define MACE_TPXF(L, R, NLV) \
@@ -1602,7 +1602,7 @@ void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
                     float* gh3p, int wfmt, const float* b3, float* gwbp) {
   if (N <= 0 || E <= 0) return;  // no edges: no dL/dw, dL/dY, dL/dx rows to write
   const TpxBwdDims a{N, W, mts, E, wscale, accumulate_gY, gyp, b3, gwbp};
-  const dim3 grid((unsigned)((N + XW - 1) / XW), 2, (unsigned)lin);
+  const dim3 grid((unsigned)((N + XW - 1) / XW), NSLICE, (unsigned)lin);
   const _Float16* wx = static_cast<const _Float16*>(W3x);
 #define MACE_TPXB(L, GXV, WF, NLV)                                                                         \
   MACE_LAUNCH((k_tpx_bwd<L, GXV, WF, NLV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \

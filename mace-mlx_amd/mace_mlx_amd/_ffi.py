@@ -16,6 +16,10 @@ from typing import Optional, Tuple
 import numpy as np
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmace_hip.so"
+# the same engine compiled for each channel count (csrc/common.h MACE_NC); a model with C
+# channels runs on the smallest width >= C (device_model pads the rest with zeros)
+ENGINE_WIDTHS = (128, 256)
+LIB_PATHS = {128: LIB_PATH, 256: LIB_PATH.with_name("libmace_hip_c256.so")}
 
 MACE_OK = 0
 MACE_ERR_INVALID = -1
@@ -64,15 +68,18 @@ class ModelDims(ctypes.Structure):
     ]
 
 
-_lib = None
+_libs: dict = {}
 
 
-def load_library(path: Optional[str] = None) -> ctypes.CDLL:
-    """Load (once) and type the engine library; raises if it is not built."""
-    global _lib
-    if _lib is not None and path is None:
-        return _lib
-    p = Path(path) if path else Path(os.environ.get("MACE_HIP_LIB", LIB_PATH))
+def load_library(path: Optional[str] = None, channels: int = 128) -> ctypes.CDLL:
+    """Load (once per channel width) and type the engine library; raises if it is not built.
+    ``MACE_HIP_LIB`` overrides the 128-channel library's path."""
+    if path is None and channels in _libs:
+        return _libs[channels]
+    if channels not in LIB_PATHS:
+        raise ValueError(f"no engine compiled for {channels} channels (widths {ENGINE_WIDTHS})")
+    default = os.environ.get("MACE_HIP_LIB", LIB_PATHS[128]) if channels == 128 else LIB_PATHS[channels]
+    p = Path(path) if path else Path(default)
     if not p.exists():
         raise ImportError(f"HIP engine library not found at {p}; build it with "
                           "`python -c 'import __graft_entry__ as g; g.build()'` (hipcc, gfx950)")
@@ -107,7 +114,7 @@ def load_library(path: Optional[str] = None) -> ctypes.CDLL:
         fn.restype = res
         fn.argtypes = args
     if path is None:
-        _lib = lib
+        _libs[channels] = lib
     return lib
 
 
@@ -119,8 +126,11 @@ class Engine:
     """One engine context on one HIP device (not thread-safe, like the reference's
     calculator which is driven from one Python thread)."""
 
-    def __init__(self, device: int = 0):
-        self._lib = load_library()
+    def __init__(self, device: int = 0, channels: int = 128):
+        """``channels``: the width of the models this context will load (a device model's
+        ``dims["num_channels"]``), which selects the library compiled for it."""
+        self._lib = load_library(channels=channels)
+        self.channels = channels
         h = ctypes.c_void_p()
         rc = self._lib.mace_create(int(device), ctypes.byref(h))
         if rc != MACE_OK:
@@ -156,6 +166,10 @@ class Engine:
 
     # -- model --------------------------------------------------------------
     def load_model(self, dm) -> None:
+        if int(dm.dims["num_channels"]) != self.channels:
+            raise ValueError(f"a {dm.dims['num_channels']}-channel device model needs "
+                             f"Engine(device, channels={dm.dims['num_channels']}); this context runs "
+                             f"the {self.channels}-channel engine")
         d = ModelDims()
         for k, v in dm.dims.items():
             if isinstance(v, list):

@@ -13,7 +13,7 @@ from pathlib import Path
 CSRC = Path(__file__).resolve().parents[1] / "csrc"
 
 
-def build(jobs: int = 5, verbose: bool = False) -> Path:
+def build(jobs: int = 8, verbose: bool = False) -> Path:
     env = dict(os.environ)
     env.setdefault("PYTHON", sys.executable)
     subprocess.run([sys.executable, str(CSRC / "gen_tables.py"), str(CSRC / "gen")], check=True,
@@ -23,14 +23,15 @@ def build(jobs: int = 5, verbose: bool = False) -> Path:
     if proc.returncode != 0:
         sys.stderr.write((proc.stdout or "") + (proc.stderr or ""))
         raise RuntimeError("HIP engine build failed")
-    from ._ffi import LIB_PATH
-    # every kernel the host registers must exist in the gfx950 code object (the HIP runtime
-    # aborts at the first launch of one that does not)
-    chk = subprocess.run([sys.executable, str(CSRC / "check_kernel_symbols.py"), str(LIB_PATH)],
-                         capture_output=True, text=True)
-    if chk.returncode != 0:
-        sys.stderr.write(chk.stdout + chk.stderr)
-        raise RuntimeError("HIP engine build: host / device kernel names differ")
+    from ._ffi import LIB_PATH, LIB_PATHS
+    # every kernel the host registers must exist in the gfx950 code objects of each library (the
+    # HIP runtime aborts at the first launch of one that does not)
+    for path in LIB_PATHS.values():
+        chk = subprocess.run([sys.executable, str(CSRC / "check_kernel_symbols.py"), str(path)],
+                             capture_output=True, text=True)
+        if chk.returncode != 0:
+            sys.stderr.write(chk.stdout + chk.stderr)
+            raise RuntimeError(f"HIP engine build ({path.name}): host / device kernel names differ")
     return LIB_PATH
 
 

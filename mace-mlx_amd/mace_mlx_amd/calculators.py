@@ -150,7 +150,7 @@ class MACEHIPCalculator(_AseCalculator):
         self._z_to_idx = {int(z): i for i, z in enumerate(self.z_table)}
         self._skin = float(skin)
         self._use_compile = use_compile
-        self._engine = Engine(dev_index)
+        self._engine = Engine(dev_index, channels=self._dm.dims["num_channels"])
         self._engine.load_model(self._dm)
         self._sys_key = None
         self._stress_always = False

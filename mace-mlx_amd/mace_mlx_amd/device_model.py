@@ -39,9 +39,9 @@ from .irreps import Irrep, Irreps
 from .model_io import (COVALENT_RADII, ModelConfig, conv_tp_instructions, linear_instructions, pad_channels,
                        select_head)
 
-# channel multiplicity the HIP engine is compiled for (csrc/common.h NC); models with fewer
-# channels are zero-padded to it
-ENGINE_CHANNELS = 128
+# channel multiplicities the HIP engine is compiled for (csrc/common.h NC, one library each);
+# a model runs on the smallest one that holds its channels, zero-padded up to it
+from ._ffi import ENGINE_WIDTHS  # noqa: E402
 
 
 class UnsupportedModel(NotImplementedError):
@@ -120,14 +120,15 @@ def build_device_model(cfg: ModelConfig, w: Dict[str, np.ndarray], dtype: str = 
     cfg, w = select_head(cfg, w, head)
     if cfg.model_type not in ("MACE", "ScaleShiftMACE"):
         raise UnsupportedModel(f"model_type={cfg.model_type}")
-    if cfg.num_features != ENGINE_CHANNELS:
-        # fewer channels than the engine is compiled for (e.g. MACE-OFF small, 96): the same model
-        # with zero channels appended and the path weights compensated (model_io.pad_channels)
-        if cfg.num_features > ENGINE_CHANNELS:
-            raise UnsupportedModel(f"{cfg.num_features} channels (the engine is compiled for at most "
-                                   f"{ENGINE_CHANNELS})")
+    width = min((c for c in ENGINE_WIDTHS if c >= cfg.num_features), default=None)
+    if width is None:
+        raise UnsupportedModel(f"{cfg.num_features} channels (the engine is compiled for at most "
+                               f"{max(ENGINE_WIDTHS)})")
+    if cfg.num_features != width:
+        # a width between the compiled ones (MACE-OFF small 96, large 192): the same model with
+        # zero channels appended and the path weights compensated (model_io.pad_channels)
         try:
-            cfg, w = pad_channels(cfg, w, ENGINE_CHANNELS)
+            cfg, w = pad_channels(cfg, w, width)
         except NotImplementedError as exc:
             raise UnsupportedModel(str(exc)) from exc
     C = cfg.num_features

@@ -46,7 +46,7 @@ class MACE:
         self._dm = build_device_model(config, weights, dtype=dtype, head=head)
         sel_cfg, sel_w = select_head(config, round_weights(weights, dtype), head)
         self._e0 = np.asarray(sel_w["atomic_energies_fn.atomic_energies"], dtype=np.float64).reshape(-1)
-        self._engine = Engine(device)
+        self._engine = Engine(device, channels=self._dm.dims["num_channels"])
         self._engine.load_model(self._dm)
         self._sys_key = None
         self._edge_key = None

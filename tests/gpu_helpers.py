@@ -29,7 +29,7 @@ class Case:
         self.w = random_init(cfg, seed)
         self.w_model = round_weights(self.w, dtype)
         self.dm = build_device_model(cfg, self.w, dtype=dtype, head=head)
-        self.eng = Engine(0)
+        self.eng = Engine(0, channels=self.dm.dims["num_channels"])
         self.eng.load_model(self.dm)
         self._oracle = None
 

@@ -18,8 +18,10 @@ def _declared():
     return sorted(set(re.findall(r"\b(mace_[a-z_]+)\s*\(", text)))
 
 
-def test_library_loads_and_exports_every_declared_symbol():
-    lib = _ffi.load_library()
+@pytest.mark.parametrize("channels", _ffi.ENGINE_WIDTHS)
+def test_library_loads_and_exports_every_declared_symbol(channels):
+    """Each channel width's library (libmace_hip.so, libmace_hip_c256.so)."""
+    lib = _ffi.load_library(channels=channels)
     declared = _declared()
     assert set(declared) == set(_ffi.EXPORTED_SYMBOLS)
     for name in declared:

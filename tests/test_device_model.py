@@ -290,23 +290,28 @@ def test_mh1_kernel_formulation_matches_oracle(apply_cutoff, agnostic, edge):
     np.testing.assert_allclose(nek, ne, rtol=0, atol=1e-6 * max(1.0, np.abs(ne).max()))
 
 
-@pytest.mark.parametrize("arch,C", [("small", 96), ("medium", 96), ("large", 64)])
-def test_narrow_model_padded_in_the_fold(si64, arch, C):
-    """A model with fewer channels than the engine (MACE-OFF small: 96x0e) is folded as its
-    zero-padded 128-channel equivalent; the kernel formulation of the folded tensors matches the
-    oracle evaluating the original model."""
+@pytest.mark.parametrize("arch,C,width", [("small", 96, 128), ("medium", 96, 128), ("large", 64, 128),
+                                          ("small", 192, 256), ("large", 192, 256), ("medium", 256, 256)])
+def test_model_padded_to_engine_width_in_the_fold(si64, arch, C, width):
+    """A model runs on the narrowest compiled engine width that holds its channels (128 or 256):
+    MACE-OFF small (96x0e) as its zero-padded 128-channel equivalent, MACE-OFF large (192x0e +
+    192x1o + 192x2e) as a 256-channel one.  The kernel formulation of the folded tensors
+    matches the oracle evaluating the original model."""
     s, i, j, S = si64
     cfg = arch_config(arch, zbl=True)
     cfg.hidden_irreps = "+".join(f"{C}x{b.ir}" for b in cfg.hidden)
     w = random_init(cfg, 4)
     dm = build_device_model(cfg, w)
-    assert dm.dims["num_channels"] == 128
+    assert dm.dims["num_channels"] == width
     sp = np.zeros(len(s), int)
     Eo, neo = OracleMACE(cfg=cfg, weights=w).energy(s.positions, sp, np.stack([i, j]), S, s.cell)
     Ek, nek = kernel_model.energy(dm, s.positions, sp, i, j, S.astype(float), s.cell)
     np.testing.assert_allclose(nek, neo, atol=5e-6)
     assert abs(Ek - Eo) < 1e-6 * max(1.0, abs(Eo)) * len(s)
-    wide = arch_config(arch)
-    wide.hidden_irreps = "+".join(f"192x{b.ir}" for b in wide.hidden)
+
+
+def test_wider_than_every_engine_raises():
+    wide = arch_config("small")
+    wide.hidden_irreps = "320x0e"
     with pytest.raises(UnsupportedModel):
         build_device_model(wide, random_init(wide, 0))

@@ -159,3 +159,35 @@ def test_mace_off_calculator_from_cache(tmp_path, monkeypatch):
     E, F, ne = OracleMACE(cfg=cfg, weights=w).energy_forces(s.positions, sp, np.stack([i, j]), S, s.cell)
     assert_parity({"E": calc.results["energy"], "F": calc.results["forces"], "ne": calc.results["node_energy"]},
                   {"E": E, "F": F, "ne": ne}, len(s))
+
+
+def test_mace_off_large_width_192():
+    """A MACE-OFF-large-shaped model (192x0e + 192x1o + 192x2e: three input blocks, the l1 = 2
+    CG paths) runs on the 256-channel engine (libmace_hip_c256.so) as its zero-padded
+    equivalent; E, F and stress against the float64 oracle evaluating the 192-channel model.
+    That engine runs the default path only: the comparison paths raise before any launch."""
+    from mace_mlx_amd.systems import off_config, organic_cluster
+    cfg = off_config("large")
+    case = Case(cfg, seed=46)
+    assert case.dm.dims["num_channels"] == 256 and case.eng.channels == 256
+    s = organic_cluster(40, 47)
+    print("192-channel model on the 256-channel engine: organic cluster", flush=True)
+    got = case.run(s)
+    edges = case.edges()
+    assert edge_set(*edges) == bruteforce_edges(s, cutoff=5.5)
+    assert_parity(got, case.reference(s, got["sp"], edges), len(s))
+    per = rattle(diamond_si((2, 2, 2)), 0.05, 48)
+    per.positions *= 0.7
+    per.cell *= 0.7
+    per.numbers = np.full(len(per), 6)
+    print("192-channel model on the 256-channel engine: periodic carbon with stress", flush=True)
+    got = case.run(per, stress=True)
+    assert_parity(got, case.reference(per, got["sp"], case.edges(), stress=True), len(per), stress=True)
+    case.eng.set_split_products(False)
+    with pytest.raises(NotImplementedError):
+        case.run(per)
+    case.eng.set_split_products(True)
+    case.eng.set_fused_tp(False)
+    with pytest.raises(NotImplementedError):
+        case.run(per)
+    case.eng.set_fused_tp(True)
