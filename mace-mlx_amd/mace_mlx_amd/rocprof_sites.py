@@ -25,6 +25,10 @@ import re
 from typing import Dict, List, Tuple
 
 FIRST_KERNEL = "k_edge_fwd"
+# one rocprofv3 --pmc pass (6 SQ counters and 1 GRBM counter fit the block limits together)
+N_XCD = 8  # MI355X: GRBM_GUI_ACTIVE of a dispatch is summed over its eight XCDs
+MFMA_COUNTERS = ("SQ_INSTS_MFMA", "SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_INSTS_VALU_MFMA_MOPS_F32",
+                 "SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
 
 
 def short_name(n: str) -> str:
@@ -179,10 +183,45 @@ def summarize(d: str, out_dir: str, calib_mib: float = 256.0, commands: Dict[str
             issue = per["SQ_INSTS_VALU"].get(k, 0.0) * 4 / (1024 * 2.4e3) if "SQ_INSTS_VALU" in per else 0.0
             avg = sum(acc[k]) / len(acc[k]) / 1e3 if k in acc else float("nan")
             w(f"| {k} | {vals} | {issue:.1f} | {avg:.1f} |")
+    mpath = os.path.join(d, "pmc_mfma")
+    if os.path.isdir(mpath):  # matrix-core counters (rocprofv3 --pmc SQ_INSTS_MFMA ... GRBM_GUI_ACTIVE)
+        mrows = _csv(os.path.join(mpath, "**", "*counter_collection.csv"))
+        have = {r.get("Counter_Name") for r in mrows}
+        mc = {c: site_counters(mrows, order, c)[0] for c in MFMA_COUNTERS if c in have}
+        w("\n## Matrix cores per launch\n")
+        w("    " + commands.get("mfma", "rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) + " ... -- python3 bench.py ..."))
+        w("\nMFMA instructions (`SQ_INSTS_MFMA`); matrix flops executed = (`SQ_INSTS_VALU_MFMA_MOPS_F16` + "
+          "`_F32`) x 512, i.e. the hardware's count, which includes the three fp16 products of each split-operand "
+          "product; achieved = those flops / the launch's trace duration; MFMA busy = "
+          "`SQ_VALU_MFMA_BUSY_CYCLES` / (`GRBM_GUI_ACTIVE` / 8 x 1024 SIMDs), the share of SIMD cycles the matrix "
+          "unit was busy while the kernel ran (rocprofv3's MfmaUtil; `GRBM_GUI_ACTIVE` per dispatch is the sum over "
+          "the eight XCDs: 8 x 2.35 GHz x the duration).  A 16x16x32 fp16 MFMA keeps the unit busy 16 cycles, the "
+          "dense-peak rate (2.5 PF/s over 1024 SIMDs), so MFMA busy is also the achieved share of the fp16 matrix "
+          "peak.\n")
+        w("| site | MFMA instr (M) | fp16 matrix GFLOP | fp32 matrix GFLOP | achieved TF/s | MFMA busy | avg us |\n"
+          "|---|---:|---:|---:|---:|---:|---:|")
+        key = "SQ_INSTS_MFMA"
+        top = sorted(mc.get(key, {}).items(), key=lambda kv: -kv[1])
+        for k, v in top:
+            if v <= 0:
+                continue
+            f16 = mc.get("SQ_INSTS_VALU_MFMA_MOPS_F16", {}).get(k, 0.0) * 512
+            f32 = mc.get("SQ_INSTS_VALU_MFMA_MOPS_F32", {}).get(k, 0.0) * 512
+            busy = mc.get("SQ_VALU_MFMA_BUSY_CYCLES", {}).get(k, 0.0)
+            gui = mc.get("GRBM_GUI_ACTIVE", {}).get(k, 0.0)
+            avg = sum(acc[k]) / len(acc[k]) / 1e3 if k in acc else float("nan")
+            tfs = (f16 + f32) / (avg * 1e-6) / 1e12 if avg == avg and avg > 0 else float("nan")
+            util = busy / (gui / N_XCD * 1024) if gui > 0 else float("nan")
+            w(f"| {k} | {v / 1e6:.3f} | {f16 / 1e9:.2f} | {f32 / 1e9:.2f} | {tfs:.1f} | {util * 100:.1f}% | {avg:.1f} |")
+        result_mfma = {k: {c: mc[c].get(k, 0.0) for c in mc} for k in mc.get(key, {})}
+    else:
+        result_mfma = None
     os.makedirs(out_dir, exist_ok=True)
     with open(os.path.join(out_dir, f"kernel_trace_{tag}.md"), "w") as f:
         f.write("\n".join(L) + "\n")
     result = {"sites": {k: sum(v) / len(v) / 1e3 for k, v in acc.items()}, "steps": nsteps}
+    if result_mfma is not None:
+        result["mfma"] = result_mfma
     fpath, wpath = os.path.join(d, "pmc_fetch"), os.path.join(d, "pmc_write")
     if not (os.path.isdir(fpath) and os.path.isdir(wpath)):
         return result
