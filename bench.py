@@ -80,6 +80,10 @@ def site_work(site: str, ctx: dict):
         return E * (4 * nb + s * H), 2 * E * (nb * H + 2 * H * H), fpk
     if name == "mlp_hidden_bwd":  # the three transposed products: dL/dh3 in, dL/def out (+ ef)
         return E * (8 * nb + 4 * H), 2 * E * (nb * H + 2 * H * H), fpk
+    if name == "mlp_ln":  # mh-1 LayerNorm radial MLP (three layers) and density MLP: ef in, h3 + density out
+        return E * (4 * nb + s * H + 4), 2 * E * (2 * nb * H + 2 * H * H + H), fpk
+    if name == "mlp_ln_bwd":  # both MLPs recomputed, then their transposed products: dL/dh3 in, dL/def out
+        return E * (8 * nb + 4 * H + 8), 4 * E * (2 * nb * H + 2 * H * H + H), fpk
     if name in ("mlp_out", "mlp_gh3"):  # w = h3 W3, dL/dh3 = dL/dw W3^T over the E x W stream
         return s * E * (lay["wn"] + H), 2 * E * H * lay["wn"], fpk
     if name.startswith("linear") or name.startswith("skip") or name.startswith("message_skip"):

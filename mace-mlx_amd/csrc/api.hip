@@ -124,7 +124,8 @@ struct Layer {
   DBuf<float> res_[4], resT[4], lin2[4], lin2T[4];
   DBuf<float> Q, R, Gt;          // per step: linear_1 / (beta rho + alpha), linear_res, gate output
   LnMlpParams lnp() const {
-    return LnMlpParams{rmlp_ts.p, rmlp_tt.p, rmlp_ln.p, rmlp_bias.p, dmlp_ts.p, dmlp_tt.p, dmlp_ln.p, dmlp_w1.p};
+    return LnMlpParams{rmlp_ts.p, rmlp_tt.p, rmlp_ln.p, rmlp_bias.p, dmlp_ts.p, dmlp_tt.p, dmlp_ln.p, dmlp_w1.p,
+                       {mlp_winv[0], mlp_winv[1], mlp_winv[2]}};
   }
   int tl() const { return nonlin ? ledge : lin; }  // input blocks of the conv TP
   int dtp() const { return nonlin ? dedge : din; }
@@ -462,6 +463,19 @@ void build_layer_nonlin(mace_ctx* c, Layer& L, int l) {
     upload(c, t0, w0), upload(c, t1, w1), upload(c, t2, w2);
     L.mlp_tiles.ensure(mlp_tile_bytes());
     launch_mlp_permute(c->stream, nb, t0.p, t1.p, t2.p, L.mlp_tiles.p);
+    {  // split images for the hidden layers on fp16 matrix cores, one power-of-two scale per matrix
+      float sc[3];
+      const std::vector<float>* ws[3] = {&w0, &w1, &w2};
+      for (int k = 0; k < 3; ++k) {
+        float m = 0.f;
+        for (float x : *ws[k]) m = std::max(m, std::fabs(x));
+        const int ex = m > 0.f ? std::ilogb(m) : 0;
+        sc[k] = std::ldexp(1.f, 14 - ex);
+        L.mlp_winv[k] = std::ldexp(1.f, ex - 14);
+      }
+      L.mlp_tiles_x.ensure(mlp_tile_x_bytes());
+      launch_mlp_permute_x(c->stream, nb, t0.p, t1.p, t2.p, sc, L.mlp_tiles_x.p);
+    }
     DBuf<float> d0;
     upload(c, d0, tensor(c, p + "dmlp.w0", (size_t)nb * RADIAL_H));
     L.dmlp_tiles.ensure(mlp_tile_bytes());
@@ -1286,7 +1300,8 @@ void forward_nonlin(mace_ctx* c, int l, const float* h, float* hn) {
   {  // LayerNorm radial MLP (last hidden activation) and the edge densities
     Site s(c, lname("mlp_ln", l));
     launch_rmlp_ln_fwd(st, E, nb, c->ef.p, cut, c->sender.p, c->receiver.p, c->species.p, L.mlp_tiles.p,
-                       L.dmlp_tiles.p, L.lnp(), c->h3.p, split ? c->h3inv.p : nullptr, c->mh_dens.p, half);
+                       split ? L.mlp_tiles_x.p : nullptr, L.dmlp_tiles.p, L.lnp(), c->h3.p,
+                       split ? c->h3inv.p : nullptr, c->mh_dens.p, half);
   }
   if (!fused) {  // w = (h3 W3 + b3) cut
     Site s(c, lname("mlp_out", l));
@@ -1461,9 +1476,11 @@ void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int fi
   }
   {
     Site s(c, lname("mlp_ln_bwd", l));
-    const size_t fb = mlp_tile_fwd_bytes();
+    const size_t fb = mlp_tile_fwd_bytes(), fbx = mlp_tile_x_fwd_bytes();
+    const bool sx = c->split_products;  // the hidden layers on split-fp16 products, as the forward
     launch_rmlp_ln_bwd(st, E, nb, c->ef.p, cut, c->sender.p, c->receiver.p, c->species.p, Ly.mlp_tiles.p,
-                       Ly.mlp_tiles.p + fb, Ly.dmlp_tiles.p, Ly.dmlp_tiles.p + fb, Ly.lnp(),
+                       Ly.mlp_tiles.p + fb, sx ? Ly.mlp_tiles_x.p : nullptr, sx ? Ly.mlp_tiles_x.p + fbx : nullptr,
+                       Ly.dmlp_tiles.p, Ly.dmlp_tiles.p + fb, Ly.lnp(),
                        fused ? c->gh3p.p : c->h3.p, c->gwb.p, fused ? tpx_parts(Ly.ledge) : 1, c->grho.p, c->gef.p,
                        cut ? c->gcut.p : nullptr, first_edge_grad);
   }

@@ -205,24 +205,29 @@ struct LnMlpParams {
   const float* dtt;   // [n_el][64] (+ bias)
   const float* dln;   // [2][64]
   const float* dw1;   // [65]: output weights, then the output bias
+  float winv[3];      // inverse power-of-two scales of the split images of W0, W1, W2
 };
 // h3 = silu(LN(...)) of the third layer, fp32 [E][64] with h3inv null, else split pairs
 // [E][2][64] with inverse row scales h3inv[E] (as launch_mlp_hidden mode 2);
 // dens[e] = tanh(x^2) cut[e] (cut may be null: 1); both rounded by mode half (RND_*, the feature
 // policy) before they are stored
+// tiles_x (null: the hidden layers on fp32 matrix cores): the split images of W0..W2 as
+// launch_mlp_permute_x writes them, for the hidden layers on fp16 matrix cores (split operands)
 void launch_rmlp_ln_fwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut,
                         const int* sender, const int* receiver, const int* species, const void* tiles,
-                        const void* dtiles, const LnMlpParams& P, void* h3, float* h3inv, float* dens, int half);
+                        const void* tiles_x, const void* dtiles, const LnMlpParams& P, void* h3, float* h3inv,
+                        float* dens, int half);
 // VJP from G = gw W3^T (np partials [np][E][64], added in order), gwb = gw . b3 (np partials
 // [np][E]) and drho ([N], dL/d(sum of the receiver's edge densities)): gef (+)= dL/def ([E][nb])
 // and, with cut, gcut (+)= dL/dcut ([E]); btiles / dbtiles: the transposed images
 // (launch_mlp_permute's second half)
 void launch_rmlp_ln_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut,
                         const int* sender, const int* receiver, const int* species, const void* tiles,
-                        const void* btiles, const void* dtiles, const void* dbtiles, const LnMlpParams& P,
-                        const float* G, const float* gwb, int np, const float* drho, float* gef, float* gcut,
-                        int accumulate);
+                        const void* btiles, const void* tiles_x, const void* btiles_x, const void* dtiles,
+                        const void* dbtiles, const LnMlpParams& P, const float* G, const float* gwb, int np,
+                        const float* drho, float* gef, float* gcut, int accumulate);
 size_t mlp_tile_fwd_bytes();  // offset of the transposed image inside an mlp_tile_bytes() block
+size_t mlp_tile_x_fwd_bytes();  // ... inside an mlp_tile_x_bytes() block
 // node side of the mh-1 block.  Q [N][kGateInDim] = linear_1(M) / (beta rho + alpha), R [N][nres]
 // = linear_res(linear_up(h)) over the leading nres columns of the gate input layout
 // [scalars C | gates C x 3 | 1o 3C | 2e 5C | 3o 7C]; gout [N][16 C] = gate(Q + R)

@@ -1319,13 +1319,23 @@ struct LnFwdState {
   float rstdd, x;
 };
 
-__device__ __forceinline__ void ln_mlp_fwd(const MlpFwdW& sw, const float4 (*dw0)[4][16], const LnSmall& S,
+// the two 64-wide hidden layers as split-fp16 tile images (the layout of MlpFwdX.w1 / w2, and of
+// MlpBwdX.w2T / w1T for the VJP), one power-of-two scale per matrix (LnMlpParams.winv)
+struct LnHidX {
+  h8 a[2][2][4][2][64];  // [layer 1, 2 | VJP: layer 2^T, 1^T][c][t'][hi, lo][lane]
+};
+
+// SPLIT: the hidden layers on fp16 matrix cores with split operands (hx), else fp32 matrix cores
+// (sw.w1 / w2); the first layer (K = num_bessel) stays on fp32 matrix cores either way
+template <bool SPLIT>
+__device__ __forceinline__ void ln_mlp_fwd(const float4 (*w0)[4][16], const MlpFwdW& sw, const LnHidX& hx,
+                                           const float4 (*dw0)[4][16], const LnSmall& S,
                                            const LnMlpParams& P, const float* __restrict__ ef, int64_t ec, int nb,
                                            int zs, int zr, LnFwdState& F, int lane) {
   const int g = lane >> 4;
   f4v acc[4];
   float z[16], v[16];
-  first_layer(sw.w0, ef, ec, nb, acc, lane);
+  first_layer(w0, ef, ec, nb, acc, lane);
 #pragma unroll
   for (int q = 0; q < 16; ++q) z[q] = acc[q >> 2][q & 3];
   add_row16(P.ts + (int64_t)zs * H, g, z);
@@ -1339,7 +1349,10 @@ __device__ __forceinline__ void ln_mlp_fwd(const MlpFwdW& sw, const float4 (*dw0
       v[q] = silu(fmaf(F.xh[k][q], S.ln[k][0][n], S.ln[k][1][n]));
     }
     if (k < 2) {
-      layer64(k == 0 ? sw.w1 : sw.w2, v, acc, lane);
+      if constexpr (SPLIT)
+        layer64x<true>(hx.a[k], v, P.winv[k + 1], acc);  // layer k + 1's weights W_{k+1}
+      else
+        layer64(k == 0 ? sw.w1 : sw.w2, v, acc, lane);
 #pragma unroll
       for (int q = 0; q < 16; ++q) z[q] = acc[q >> 2][q & 3] + S.bias[k][fidx(q, g)];
     }
@@ -1362,17 +1375,40 @@ __device__ __forceinline__ void ln_mlp_fwd(const MlpFwdW& sw, const float4 (*dw0
   F.x = sum4_rows(xs) + S.dw1[64];
 }
 
+// hidden layers of the split path: layers 1, 2 of an MlpFwdX image (tx, forward) or layers 2^T,
+// 1^T of an MlpBwdX image (VJP) into LDS
+__device__ __forceinline__ void stage_hid(h8 (*dst)[2][4][2][64], const h8 (*l0)[4][2][64], const h8 (*l1)[4][2][64]) {
+  constexpr int N = 2 * 4 * 2 * 64;
+  for (int i = threadIdx.x; i < N; i += blockDim.x) {
+    (&dst[0][0][0][0][0])[i] = (&l0[0][0][0][0])[i];
+    (&dst[1][0][0][0][0])[i] = (&l1[0][0][0][0])[i];
+  }
+}
+
+template <bool SPLIT>
 __global__ void __launch_bounds__(256) k_rmlp_ln_fwd(int64_t E, int nb, const float* __restrict__ ef,
                                                      const float* __restrict__ cut, const int* __restrict__ sender,
                                                      const int* __restrict__ receiver,
                                                      const int* __restrict__ species, const MlpFwdW* __restrict__ tiles,
+                                                     const MlpFwdX* __restrict__ tiles_x,
                                                      const MlpFwdW* __restrict__ dtiles, LnMlpParams P,
                                                      void* __restrict__ h3, float* __restrict__ h3inv,
                                                      float* __restrict__ dens, int half) {
-  __shared__ MlpFwdW sw;
+  // SPLIT stages the first layer (fp32) and the split hidden images; else the fp32 tile image
+  __shared__ __align__(16) char sw_raw[SPLIT ? 16 : sizeof(MlpFwdW)];
+  __shared__ __align__(16) char hx_raw[SPLIT ? sizeof(LnHidX) : 16];
+  __shared__ float4 sw0[SPLIT ? NB4 : 1][4][16];
   __shared__ float4 sdw0[NB4][4][16];
   __shared__ LnSmall S;
-  stage_copy(sw, tiles);
+  MlpFwdW& sw = *reinterpret_cast<MlpFwdW*>(sw_raw);
+  LnHidX& hx = *reinterpret_cast<LnHidX*>(hx_raw);
+  if constexpr (SPLIT) {
+    for (int i = threadIdx.x; i < NB4 * 4 * 16; i += blockDim.x) (&sw0[0][0][0])[i] = (&tiles->w0[0][0][0])[i];
+    stage_hid(hx.a, tiles_x->w1, tiles_x->w2);
+  } else {
+    stage_copy(sw, tiles);
+  }
+  const float4 (*w0)[4][16] = SPLIT ? sw0 : sw.w0;
   for (int i = threadIdx.x; i < NB4 * 4 * 16; i += blockDim.x) (&sdw0[0][0][0])[i] = (&dtiles->w0[0][0][0])[i];
   stage_small(S, P);
   __syncthreads();
@@ -1385,7 +1421,7 @@ __global__ void __launch_bounds__(256) k_rmlp_ln_fwd(int64_t E, int nb, const fl
     // LayerNorm vectors indexed by it stay inside the loop (hoisted, they hold ~400 registers)
     const int lo = lane_opaque<true>();
     LnFwdState F;
-    ln_mlp_fwd(sw, sdw0, S, P, ef, ec, nb, zs, zr, F, lo);
+    ln_mlp_fwd<SPLIT>(w0, sw, hx, sdw0, S, P, ef, ec, nb, zs, zr, F, lo);
     // the stored activation under a half-precision policy (its split lo plane is then zero)
 #pragma unroll
     for (int q = 0; q < 16; ++q) F.h3[q] = qh(F.h3[q], half);
@@ -1452,24 +1488,46 @@ __device__ __forceinline__ void first_layer_T(const float4 (*w0T)[4][16], const 
 // waves per SIMD come from one eight-wave block
 constexpr int kLnBwdWaves = 8;
 
+template <bool SPLIT>
 __global__ void __launch_bounds__(64 * kLnBwdWaves) k_rmlp_ln_bwd(int64_t E, int nb, const float* __restrict__ ef,
                                                      const float* __restrict__ cut, const int* __restrict__ sender,
                                                      const int* __restrict__ receiver,
                                                      const int* __restrict__ species, const MlpFwdW* __restrict__ tiles,
                                                      const MlpBwdW* __restrict__ btiles,
+                                                     const MlpFwdX* __restrict__ tiles_x,
+                                                     const MlpBwdX* __restrict__ btiles_x,
                                                      const MlpFwdW* __restrict__ dtiles,
                                                      const MlpBwdW* __restrict__ dbtiles, LnMlpParams P,
                                                      const float* __restrict__ G, const float* __restrict__ gwb,
                                                      int np, const float* __restrict__ drho,
                                                      float* __restrict__ gef, float* __restrict__ gcut,
                                                      int accumulate) {
-  __shared__ MlpFwdW sw;
-  __shared__ MlpBwdW sb;
+  // SPLIT: the first layers (fp32) and the split images of the hidden layers (forward and
+  // transposed); else the fp32 tile images
+  __shared__ __align__(16) char sw_raw[SPLIT ? 16 : sizeof(MlpFwdW)];
+  __shared__ __align__(16) char sb_raw[SPLIT ? 16 : sizeof(MlpBwdW)];
+  __shared__ __align__(16) char hx_raw[SPLIT ? sizeof(LnHidX) : 16];
+  __shared__ __align__(16) char hb_raw[SPLIT ? sizeof(LnHidX) : 16];
+  __shared__ float4 sw0[SPLIT ? NB4 : 1][4][16];
+  __shared__ float4 sw0T[SPLIT ? 4 : 1][4][16];
   __shared__ float4 sdw0[NB4][4][16];
   __shared__ float4 sdw0T[4][4][16];
   __shared__ LnSmall S;
-  stage_copy(sw, tiles);
-  stage_copy(sb, btiles);
+  MlpFwdW& sw = *reinterpret_cast<MlpFwdW*>(sw_raw);
+  MlpBwdW& sb = *reinterpret_cast<MlpBwdW*>(sb_raw);
+  LnHidX& hx = *reinterpret_cast<LnHidX*>(hx_raw);
+  LnHidX& hb = *reinterpret_cast<LnHidX*>(hb_raw);
+  if constexpr (SPLIT) {
+    for (int i = threadIdx.x; i < NB4 * 4 * 16; i += blockDim.x) (&sw0[0][0][0])[i] = (&tiles->w0[0][0][0])[i];
+    for (int i = threadIdx.x; i < 4 * 4 * 16; i += blockDim.x) (&sw0T[0][0][0])[i] = (&btiles->w0T[0][0][0])[i];
+    stage_hid(hx.a, tiles_x->w1, tiles_x->w2);
+    stage_hid(hb.a, btiles_x->w2T, btiles_x->w1T);
+  } else {
+    stage_copy(sw, tiles);
+    stage_copy(sb, btiles);
+  }
+  const float4 (*w0)[4][16] = SPLIT ? sw0 : sw.w0;
+  const float4 (*w0T)[4][16] = SPLIT ? sw0T : sb.w0T;
   for (int i = threadIdx.x; i < NB4 * 4 * 16; i += blockDim.x) (&sdw0[0][0][0])[i] = (&dtiles->w0[0][0][0])[i];
   for (int i = threadIdx.x; i < 4 * 4 * 16; i += blockDim.x) (&sdw0T[0][0][0])[i] = (&dbtiles->w0T[0][0][0])[i];
   stage_small(S, P);
@@ -1482,7 +1540,7 @@ __global__ void __launch_bounds__(64 * kLnBwdWaves) k_rmlp_ln_bwd(int64_t E, int
     const int zs = species[sender[ec]], zr = species[rcv];
     const int lo = lane_opaque<true>(), go = lo >> 4;  // as in k_rmlp_ln_fwd
     LnFwdState F;
-    ln_mlp_fwd(sw, sdw0, S, P, ef, ec, nb, zs, zr, F, lo);
+    ln_mlp_fwd<SPLIT>(w0, sw, hx, sdw0, S, P, ef, ec, nb, zs, zr, F, lo);
     const float ce = cut ? cut[ec] : 1.f;
     float gv[16], gb = gwb[ec];
     ld_row16(G + ec * H, g, gv);
@@ -1505,13 +1563,16 @@ __global__ void __launch_bounds__(64 * kLnBwdWaves) k_rmlp_ln_bwd(int64_t E, int
     for (int k = 2; k >= 0; --k) {
       ln_silu_bwd(gv, F.xh[k], F.rstd[k], S.ln[k][0], S.ln[k][1], go);
       if (k > 0) {
-        layer64(k == 2 ? sb.w2T : sb.w1T, gv, acc, lo);
+        if constexpr (SPLIT)
+          layer64x<true>(hb.a[2 - k], gv, P.winv[k], acc);  // layer k's transpose: image 2 - k
+        else
+          layer64(k == 2 ? sb.w2T : sb.w1T, gv, acc, lo);
 #pragma unroll
         for (int q = 0; q < 16; ++q) gv[q] = acc[q >> 2][q & 3];
       }
     }
     f4v o = f4v{0.f, 0.f, 0.f, 0.f};
-    first_layer_T(sb.w0T, gv, o, lo);
+    first_layer_T(w0T, gv, o, lo);
     // density: dens = tanh(x^2) cut, rho[receiver] = sum of dens
     const float th = tanhf(F.x * F.x);
     const float gd = drho[rcv];
@@ -1665,27 +1726,44 @@ void launch_mlp_hidden_bwd(hipStream_t st, int64_t E, int nb, const void* tiles,
 }
 
 size_t mlp_tile_fwd_bytes() { return sizeof(MlpFwdW); }
+size_t mlp_tile_x_fwd_bytes() { return sizeof(MlpFwdX); }
 
 void launch_rmlp_ln_fwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut, const int* sender,
-                        const int* receiver, const int* species, const void* tiles, const void* dtiles,
-                        const LnMlpParams& P, void* h3, float* h3inv, float* dens, int half) {
+                        const int* receiver, const int* species, const void* tiles, const void* tiles_x,
+                        const void* dtiles, const LnMlpParams& P, void* h3, float* h3inv, float* dens, int half) {
   if (E <= 0) return;
-  // one 16-edge group per wave up to three blocks per CU (44 KB of LDS each)
+  // one 16-edge group per wave up to three blocks per CU (44 / 46 KB of LDS each)
   const unsigned grid = (unsigned)std::min<int64_t>((E + 63) / 64, 768);
-  MACE_LAUNCH(k_rmlp_ln_fwd, dim3(grid), dim3(256), 0, st, E, nb, ef, cut, sender, receiver, species,
-              static_cast<const MlpFwdW*>(tiles), static_cast<const MlpFwdW*>(dtiles), P, h3, h3inv, dens, half);
+  const MlpFwdX* tx = static_cast<const MlpFwdX*>(tiles_x);
+#define MACE_LNF(SP)                                                                                            \
+  MACE_LAUNCH(k_rmlp_ln_fwd<SP>, dim3(grid), dim3(256), 0, st, E, nb, ef, cut, sender, receiver, species,        \
+              static_cast<const MlpFwdW*>(tiles), tx, static_cast<const MlpFwdW*>(dtiles), P, h3, h3inv, dens, half)
+  if (tx)
+    MACE_LNF(true);
+  else
+    MACE_LNF(false);
+#undef MACE_LNF
 }
 
 void launch_rmlp_ln_bwd(hipStream_t st, int64_t E, int nb, const float* ef, const float* cut, const int* sender,
                         const int* receiver, const int* species, const void* tiles, const void* btiles,
-                        const void* dtiles, const void* dbtiles, const LnMlpParams& P, const float* G,
-                        const float* gwb, int np, const float* drho, float* gef, float* gcut, int accumulate) {
+                        const void* tiles_x, const void* btiles_x, const void* dtiles, const void* dbtiles,
+                        const LnMlpParams& P, const float* G, const float* gwb, int np, const float* drho, float* gef,
+                        float* gcut, int accumulate) {
   if (E <= 0) return;
   const unsigned grid = (unsigned)std::min<int64_t>((E + 16 * kLnBwdWaves - 1) / (16 * kLnBwdWaves), 256);
-  MACE_LAUNCH(k_rmlp_ln_bwd, dim3(grid), dim3(64 * kLnBwdWaves), 0, st, E, nb, ef, cut, sender, receiver, species,
-              static_cast<const MlpFwdW*>(tiles), static_cast<const MlpBwdW*>(btiles),
-              static_cast<const MlpFwdW*>(dtiles), static_cast<const MlpBwdW*>(dbtiles), P, G, gwb, np, drho, gef,
-              gcut, accumulate);
+  const MlpFwdX* tx = static_cast<const MlpFwdX*>(tiles_x);
+  const MlpBwdX* bx = static_cast<const MlpBwdX*>(btiles_x);
+#define MACE_LNB(SP)                                                                                             \
+  MACE_LAUNCH(k_rmlp_ln_bwd<SP>, dim3(grid), dim3(64 * kLnBwdWaves), 0, st, E, nb, ef, cut, sender, receiver,   \
+              species, static_cast<const MlpFwdW*>(tiles), static_cast<const MlpBwdW*>(btiles), tx, bx,          \
+              static_cast<const MlpFwdW*>(dtiles), static_cast<const MlpBwdW*>(dbtiles), P, G, gwb, np, drho, gef, \
+              gcut, accumulate)
+  if (tx)
+    MACE_LNB(true);
+  else
+    MACE_LNB(false);
+#undef MACE_LNB
 }
 
 }  // namespace mace
