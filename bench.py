@@ -65,7 +65,7 @@ def site_work(site: str, ctx: dict):
     Bytes count compulsory unique traffic (node arrays once, int32 indices); flops count
     multiply-adds as 2 and are priced on the matrix-core peak of the arithmetic type the
     product computes in (fp32 for the float32 policy: the split-fp16 products emulate it)."""
-    N, E, C, nb, H = ctx["N"], ctx["E"], 128, ctx["nb"], RADIAL_H
+    N, E, C, nb, H = ctx["N"], ctx["E"], ctx.get("C", 128), ctx["nb"], RADIAL_H
     half = ctx.get("half")
     s = 2 if half else 4
     fpk = FP16_MFMA_PEAK_TFS if half else FP32_MFMA_PEAK_TFS
@@ -119,8 +119,8 @@ def linear_work(cfg_layers, N):
     """(flops, bytes) per linear site: 2 rows K Cout summed over the blocks of a layer; bytes =
     the input and output node rows (fp32) plus the weights."""
     out = {}
-    C = 128
     for l, lay in enumerate(cfg_layers):
+        C = lay["C"]
         lin, lhid, nslot_by_l = lay["lin"], lay["lhid"], lay["nslot_by_l"]
         up = sum(2 * N * (2 * b + 1) * C * C for b in range(lin))
         msg = sum(2 * N * (2 * lo + 1) * nslot_by_l[lo] * C * C for lo in range(4))
@@ -220,7 +220,8 @@ def cpu_baseline(bc, weights, edges, species, budget_s=40.0):
 
 
 def layer_shapes(dm):
-    """Per-layer widths (din, dhid, dmid, wn, slots per output degree) of a device model."""
+    """Per-layer widths (din, dhid, dmid, wn, slots per output degree) of a device model, at the
+    engine's channel count (a narrower model runs zero-padded to it: this is the work executed)."""
     sys.path.insert(0, str(ROOT / "mace-mlx_amd" / "csrc"))
     import gen_tables
     layers = []
@@ -229,8 +230,9 @@ def layer_shapes(dm):
         # input blocks of the conv TP: linear_up's output in a non-linear (mh-1) layer
         lin = dm.dims["layer_edge_blocks"][l] if dm.dims.get("nonlinear") else dm.dims["layer_in_blocks"][l]
         slots = gen_tables.tp_layout(lin)
-        layers.append(dict(lin=lin, lhid=lhid, din=128 * lin * lin, dhid=128 * lhid * lhid,
-                           dmid=128 * sum(2 * x[2] + 1 for x in slots), wn=128 * len(slots),
+        C = dm.dims["num_channels"]
+        layers.append(dict(lin=lin, lhid=lhid, C=C, din=C * lin * lin, dhid=C * lhid * lhid,
+                           dmid=C * sum(2 * x[2] + 1 for x in slots), wn=C * len(slots),
                            nslot_by_l=[sum(1 for x in slots if x[2] == lo) for lo in range(4)]))
     return layers
 
@@ -313,6 +315,7 @@ def run_workload(idx, steps, warmup, separate=False, graphs=None, extras=False, 
     assert abs(out[0] - E_host) <= 1e-9 * abs(E_host) and np.abs(out[10:].reshape(N, 3) - F_host).max() < 1e-9
     res = {"workload": bc.name, "n_atoms": N, "n_edges": E,
            "properties": "energy+forces+stress" if stress else "energy+forces", "feature_dtype": bc.dtype,
+           "channels": bc.model.num_features, "engine_channels": dm.dims["num_channels"],
            "ms_per_step": round(ms, 4), "atom_steps_per_s": round(N / ms * 1e3, 1), "_wall": wall}
     if extras:
         # device-resident steps of a periodic system leave the positions of the last list build
@@ -346,7 +349,8 @@ def run_workload(idx, steps, warmup, separate=False, graphs=None, extras=False, 
         Path(launch_order).parent.mkdir(parents=True, exist_ok=True)
         Path(launch_order).write_text("\n".join(order) + "\n")
     layers = layer_shapes(dm)
-    ctx = dict(N=N, E=E, nb=dm.dims["num_bessel"], layers=layers, linear_work=linear_work(layers, N),
+    ctx = dict(N=N, E=E, C=dm.dims["num_channels"], nb=dm.dims["num_bessel"], layers=layers,
+               linear_work=linear_work(layers, N),
                half=bc.dtype in ("float16", "bfloat16"),
                fused=not separate)
     per_step = {k: (v[0] / steps, v[1] // steps) for k, v in kt.items()}
@@ -387,7 +391,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=1, help="benchmark configuration index 0..4 (5: an mh-1 model on the Si1000 system)")
+    ap.add_argument("--config", type=int, default=1, help="benchmark configuration index 0..4 (5: an mh-1 model on the "
+                    "Si1000 system; 6, 7: MACE-OFF-shaped models of 96 and 192 channels on an organic liquid)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--separate-mlp-out", action="store_true",
                     help="float32 policy: radial-MLP output layer as its own pass (not fused into the TP)")
@@ -440,12 +445,13 @@ def main():
     sweep = None
     if not args.no_sweep:
         sweep = []
-        for i in range(6):  # the five benchmark configurations, then an mh-1 model on Si1000
+        for i in range(8):  # the five benchmark configurations, an mh-1 model on Si1000, MACE-OFF widths
             r = head if i == args.config else run_workload(i, max(5, args.steps // 2), args.warmup,
                                                            args.separate_mlp_out, graphs)
             sweep.append({k: r[k] for k in ("workload", "n_atoms", "n_edges", "properties", "feature_dtype",
-                                             "ms_per_step", "ms_per_step_nl_rebuild", "atom_steps_per_s",
-                                             "dominant", "dominant_frac")}
+                                             "channels", "engine_channels", "ms_per_step",
+                                             "ms_per_step_nl_rebuild", "atom_steps_per_s", "dominant",
+                                             "dominant_frac")}
                          | {"tp_scatter_hbm_frac_unfused_bytes": r["tp_scatter"]["hbm_frac_unfused_bytes"],
                             "tp_scatter_roofline_frac": r["tp_scatter"]["roofline_frac"]})
         print(f"{'config':24s} {'N':>6s} {'E':>9s} {'ms/step':>9s} {'+NL ms':>8s} {'atom-steps/s':>13s}  "

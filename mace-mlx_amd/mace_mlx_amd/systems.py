@@ -148,7 +148,9 @@ def make_config(index: int) -> BenchConfig:
     """Configurations 1..5 of the benchmark definition (0-based index 0..4); index 5, outside
     that definition, is the Si1000 system under an mh-1 model (non-linear interaction blocks,
     `blocks.py:611-807`, with the mh-1 foundation models' element-agnostic product, separate
-    cutoff, 1o edge irreps and 89 elements)."""
+    cutoff, 1o edge irreps and 89 elements); indices 6 and 7, also outside it, are MACE-OFF-shaped
+    models (96 and 192 channels, run zero-padded on the 128- and 256-channel engines) on a periodic
+    1000-atom organic liquid stand-in."""
     if index == 0:
         s = rattle(diamond_si((2, 2, 2)), 0.01, 0)
         m = arch_config("small")
@@ -188,7 +190,23 @@ def make_config(index: int) -> BenchConfig:
         m.apply_cutoff = False
         m.use_agnostic_product = True
         return BenchConfig(5, "Si1000-mh1", s, m, ["energy", "forces"])
+    if index in (6, 7):
+        size = "small" if index == 6 else "large"
+        return BenchConfig(index, f"Organic1000-off-{size}", organic_liquid(), off_config(size),
+                           ["energy", "forces"])
     raise ValueError(index)
+
+
+def organic_liquid(n_side: int = 10, density: float = 0.1, seed: int = 49) -> System:
+    """A periodic H / C / N / O liquid stand-in at a molecular liquid's atom density (0.1 per
+    cubic Angstrom, ~50 neighbours within 5.5 A): n_side^3 atoms on a cubic grid jittered by
+    0.25 A, elements drawn 5 : 3 : 1 : 1."""
+    rng = np.random.default_rng(seed)
+    a = density ** (-1.0 / 3.0)
+    g = np.stack(np.meshgrid(*[np.arange(n_side)] * 3, indexing="ij"), -1).reshape(-1, 3)
+    pos = a * g + rng.normal(scale=0.25, size=g.shape)
+    z = rng.choice(np.array([1, 6, 7, 8]), size=len(g), p=[0.5, 0.3, 0.1, 0.1])
+    return System(pos, z.astype(np.int64), np.eye(3) * a * n_side, np.array([True, True, True]))
 
 
 def write_model_dir(cfg: ModelConfig, path, seed: int = 0) -> Path:

@@ -13,8 +13,8 @@ import pytest
 import bench
 from mace_mlx_amd import rocprof_sites
 
-LAYERS = [dict(lin=1, lhid=2, din=128, dhid=512, dmid=2048, wn=512, nslot_by_l=[1, 1, 1, 1]),
-          dict(lin=2, lhid=1, din=512, dhid=128, dmid=5120, wn=1280, nslot_by_l=[2, 3, 3, 2])]
+LAYERS = [dict(lin=1, lhid=2, C=128, din=128, dhid=512, dmid=2048, wn=512, nslot_by_l=[1, 1, 1, 1]),
+          dict(lin=2, lhid=1, C=128, din=512, dhid=128, dmid=5120, wn=1280, nslot_by_l=[2, 3, 3, 2])]
 
 
 def _ctx(E=46000, fused=True):
