@@ -86,7 +86,7 @@ def site_work(site: str, ctx: dict):
         return E * (8 * nb + 4 * H + 8), 4 * E * (2 * nb * H + 2 * H * H + H), fpk
     if name in ("mlp_out", "mlp_gh3"):  # w = h3 W3, dL/dh3 = dL/dw W3^T over the E x W stream
         return s * E * (lay["wn"] + H), 2 * E * H * lay["wn"], fpk
-    if name.startswith("linear") or name.startswith("skip") or name.startswith("message_skip"):
+    if name.startswith("linear") or name.startswith("message_skip"):
         f, b = ctx["linear_work"].get(site, (0, 0))
         return b, f, fpk
     if name in ("sc_fwd", "sc_bwd"):
@@ -116,25 +116,28 @@ def roofline_of(site: str, ctx: dict, avg_ms: float):
 
 
 def linear_work(cfg_layers, N):
-    """(flops, bytes) per linear site: 2 rows K Cout summed over the blocks of a layer; bytes =
-    the input and output node rows (fp32) plus the weights."""
+    """(flops, bytes) per grouped-product site: 2 rows K Cout summed over the problems of a
+    layer; bytes = the input and output node rows (fp32) plus the weights.  The skip
+    connection's product is the second operand of linear_prod (forward) and linear_up_bwd
+    (VJP); the message skip of a non-residual block is a site of its own."""
     out = {}
     for l, lay in enumerate(cfg_layers):
         C = lay["C"]
-        lin, lhid, nslot_by_l = lay["lin"], lay["lhid"], lay["nslot_by_l"]
-        up = sum(2 * N * (2 * b + 1) * C * C for b in range(lin))
-        msg = sum(2 * N * (2 * lo + 1) * nslot_by_l[lo] * C * C for lo in range(4))
-        prod = sum(2 * N * (2 * b + 1) * C * C for b in range(lhid))
-        skip = sum(2 * N * (2 * b + 1) * C * C for b in range(min(lin, lhid)))
+        lin, lhid, nslot_by_l, nskip = lay["lin"], lay["lhid"], lay["nslot_by_l"], lay["nskip"]
+        blk = lambda nb: sum(2 * N * (2 * b + 1) * C * C for b in range(nb))
         dint = 16 * C
-        by = {"up": 4 * N * 2 * lay["din"] + 4 * lin * C * C,
-              "msg": 4 * N * (lay["dmid"] + dint) + 4 * sum(nslot_by_l) * C * C,
-              "prod": 4 * N * (dint + 2 * lay["dhid"]) + 4 * 2 * lhid * C * C,
-              "skip": 4 * N * (lay["din"] + lay["dhid"]) + 4 * min(lin, lhid) * C * C}
-        for nm, f in (("linear_up", up), ("linear_msg", msg), ("linear_prod", prod), ("skip", skip)):
-            k = nm.split("_")[-1]
-            out[f"{nm}.L{l}"] = (f, by[k])
-            out[f"{nm}_bwd.L{l}"] = (f, by[k])
+        skip_in = 4 * N * C * sum((2 * b + 1) for b in range(nskip))
+        msg = sum(2 * N * (2 * lo + 1) * nslot_by_l[lo] * C * C for lo in range(4))
+        by_msg = 4 * N * (lay["dmid"] + dint) + 4 * sum(nslot_by_l) * C * C
+        out[f"linear_up.L{l}"] = (blk(lin), 4 * N * 2 * lay["din"] + 4 * lin * C * C)
+        out[f"linear_up_bwd.L{l}"] = (blk(lin) + blk(nskip),
+                                      4 * N * 2 * lay["din"] + skip_in + 4 * (lin + nskip) * C * C)
+        out[f"linear_msg.L{l}"] = out[f"linear_msg_bwd.L{l}"] = (msg, by_msg)
+        out[f"linear_prod.L{l}"] = (blk(lhid) + blk(nskip),
+                                    4 * N * (dint + lay["dhid"]) + skip_in + 4 * (lhid + nskip) * C * C)
+        out[f"linear_prod_bwd.L{l}"] = (blk(lhid), 4 * N * (dint + lay["dhid"]) + 4 * lhid * C * C)
+        if not lay["resid"]:
+            out[f"message_skip.L{l}"] = out[f"message_skip_bwd.L{l}"] = (blk(4), 4 * N * 2 * dint + 4 * 4 * C * C)
     return out
 
 
@@ -231,7 +234,8 @@ def layer_shapes(dm):
         lin = dm.dims["layer_edge_blocks"][l] if dm.dims.get("nonlinear") else dm.dims["layer_in_blocks"][l]
         slots = gen_tables.tp_layout(lin)
         C = dm.dims["num_channels"]
-        layers.append(dict(lin=lin, lhid=lhid, C=C, din=C * lin * lin, dhid=C * lhid * lhid,
+        resid = not (l == 0 and dm.dims.get("first_nonresidual")) or bool(dm.dims.get("nonlinear"))
+        layers.append(dict(lin=lin, lhid=lhid, C=C, resid=resid, nskip=min(lin, lhid) if resid else 0, din=C * lin * lin, dhid=C * lhid * lhid,
                            dmid=C * sum(2 * x[2] + 1 for x in slots), wn=C * len(slots),
                            nslot_by_l=[sum(1 for x in slots if x[2] == lo) for lo in range(4)]))
     return layers
@@ -334,7 +338,9 @@ def run_workload(idx, steps, warmup, separate=False, graphs=None, extras=False, 
         med, lo, hi = calculator_ms(bc, weights)
         res["ms_per_step_calculator"] = round(med, 4)
         res["ms_per_step_calculator_range"] = [round(lo, 4), round(hi, 4)]
-        if bc.dtype == "float32":   # the same step with every product on fp32 matrix cores
+        if bc.dtype == "float32" and dm.dims["num_channels"] == 128:
+            # the same step with every product on fp32 matrix cores (the 256-channel engine runs
+            # the split-product path only)
             eng.set_split_products(False)
             _timed(eng, pos_d, out_d, stress, 2)
             res["ms_per_step_fp32_mfma"] = round(_timed(eng, pos_d, out_d, stress, steps) / steps * 1e3, 4)

@@ -175,6 +175,10 @@ struct mace_ctx {
   DBuf<int> gptr, gid;
   DBuf<double> gcell, eg, gvir;  // per-structure cells, energies, virials
   DBuf<int> species;
+  // atoms sorted by species (stable): sp_perm[sp_off[z] .. sp_off[z] + sp_cnt[z]) = the atoms of
+  // species z, the row maps of the per-species products
+  DBuf<int> sp_perm;
+  std::vector<int> sp_cnt, sp_off;
   DBuf<double> pos;
   double* pos_pinned = nullptr;
   size_t pos_pinned_n = 0;
@@ -646,7 +650,13 @@ void build_model(mace_ctx* c) {
     for (Layer& L : c->layers) {
       for (int b = 0; b < L.lin; ++b) make_split(c, L.up[b].p, CC), make_split(c, L.upT[b].p, CC);
       for (int b = 0; b < L.lhid; ++b) make_split(c, L.plin[b].p, CC), make_split(c, L.plinT[b].p, CC);
-      for (int b = 0; b < L.nskip; ++b) make_split(c, L.skip[b].p, CC), make_split(c, L.skipT[b].p, CC);
+      // per-species weights (skip connection, message skip): one split copy per element's slice
+      const int nsl = L.nonlin ? 1 : c->dims.num_elements;
+      for (int z = 0; z < nsl; ++z) {
+        for (int b = 0; b < L.nskip; ++b) make_split(c, L.skip[b].p + z * CC, CC), make_split(c, L.skipT[b].p + z * CC, CC);
+        if (!L.resid)
+          for (int lo = 0; lo < 4; ++lo) make_split(c, L.mskip[lo].p + z * CC, CC), make_split(c, L.mskipT[lo].p + z * CC, CC);
+      }
       const int* l3 = tp_l3(L.tl());
       for (int lo = 0; lo < 4; ++lo) {
         size_t ns = 0;
@@ -1066,23 +1076,6 @@ __global__ void k_gather_edges(int64_t E, const int* perm, const int* si, const 
 // ---------------------------------------------------------------------------
 // the step
 // ---------------------------------------------------------------------------
-LinearDesc lin_desc(int d, int K, int Cout, int ldx, int in_base, int in_stride, int ldy, int out_base,
-                    int out_stride, int acc) {
-  LinearDesc D;
-  D.d = d;
-  D.K = K;
-  D.Cout = Cout;
-  D.ldx = ldx;
-  D.in_base = in_base;
-  D.in_stride = in_stride;
-  D.ldy = ldy;
-  D.out_base = out_base;
-  D.out_stride = out_stride;
-  D.accumulate = acc;
-  D.round_half = 0;
-  return D;
-}
-
 GemmProb gprob(int N, int d, int K1, int Cout, const float* X1, int ldx1, int base1, int stride1, const float* WT1,
                 float* Y, int ldy, int obase, int ostride) {
   GemmProb P{};
@@ -1157,37 +1150,57 @@ FrontParams front_params(mace_ctx* c) {
   return p;
 }
 
-// skip connection for hidden block b (rows 2b+1, input block b of h)
-void run_skip(mace_ctx* c, Layer& L, int b, const float* h, float* out, int ldo, int acc, int half) {
-  const int d = 2 * b + 1;
-  LinearDesc D = lin_desc(d, NC, NC, L.din, NC * b * b, 0, ldo, NC * b * b, 0, acc);
-  D.round_half = half;
-  if (c->dims.num_elements == 1)
-    launch_linear(c->stream, c->N, D, h, L.skip[b].p, out);
-  else
-    launch_linear_species(c->stream, c->N, D, h, L.skip[b].p, c->species.p, out);
-}
-
-// Message skip FCTP of a non-residual block (blocks.py:171-176): per interaction block lo,
-// out[n][lo] = in[n][lo] W_lo[species(n)] (W given per element, pw and CG folded).
-void run_msg_skip(mace_ctx* c, Layer& L, const float* in, float* out, const DBuf<float>* W, int half) {
-  for (int lo = 0; lo < 4; ++lo) {
-    LinearDesc D = lin_desc(2 * lo + 1, NC, NC, L.dint, NC * lo * lo, 0, L.dint, NC * lo * lo, 0, 0);
-    D.round_half = half;
-    if (c->dims.num_elements == 1)
-      launch_linear(c->stream, c->N, D, in, W[lo].p, out);
-    else
-      launch_linear_species(c->stream, c->N, D, in, W[lo].p, c->species.p, out);
+// A list of grouped products in launches of at most GEMM_MAX problems each.
+void run_gemm_list(mace_ctx* c, hipStream_t st, const std::vector<GemmProb>& probs, int round_half) {
+  for (size_t q0 = 0; q0 < probs.size(); q0 += GEMM_MAX) {
+    GemmGroup g{};
+    g.round_half = round_half;
+    for (size_t q = q0; q < probs.size() && q < q0 + GEMM_MAX; ++q) g.p[g.n++] = probs[q];
+    run_gemm(c, st, g);
   }
 }
 
-void run_skip_T(mace_ctx* c, Layer& L, int b, const float* gout, int ldg, float* gh) {
-  const int d = 2 * b + 1;
-  LinearDesc D = lin_desc(d, NC, NC, ldg, NC * b * b, 0, L.din, NC * b * b, 0, 1);
-  if (c->dims.num_elements == 1)
-    launch_linear(c->stream, c->N, D, gout, L.skipT[b].p, gh);
-  else
-    launch_linear_species(c->stream, c->N, D, gout, L.skipT[b].p, c->species.p, gh);
+// Products with per-species weights (one-hot node attributes: the skip connection's and the
+// message skip's FCTPs, blocks.py:171-176, 225-230): P once per species present, over that
+// species' atoms (row map into the species-sorted atom order), operand `which` (1 or 2) taking
+// element z's [C][C] slice of W.  One element: P with W itself, over every atom.
+void add_species_probs(mace_ctx* c, const GemmProb& P, int which, const float* W, std::vector<GemmProb>& out) {
+  if (c->dims.num_elements == 1) {
+    GemmProb Q = P;
+    (which == 1 ? Q.WT1 : Q.WT2) = W;
+    out.push_back(Q);
+    return;
+  }
+  const size_t CC = (size_t)NC * NC;
+  for (int z = 0; z < c->dims.num_elements; ++z) {
+    if (c->sp_cnt[z] == 0) continue;
+    GemmProb Q = P;
+    Q.rows = c->sp_cnt[z] * P.d;
+    Q.rowmap = c->sp_perm.p + c->sp_off[z];
+    (which == 1 ? Q.WT1 : Q.WT2) = W + z * CC;
+    out.push_back(Q);
+  }
+}
+
+// operand 2 of P = the skip connection's input block b (x W_skip[species])
+void set_skip_operand(GemmProb& P, const float* X, int ldx, int b) {
+  P.K2 = NC;
+  P.X2 = X;
+  P.ldx2 = ldx;
+  P.in_base2 = NC * b * b;
+  P.in_stride2 = 0;
+}
+
+// Message skip FCTP of a non-residual block (blocks.py:171-176): per interaction block lo,
+// out[n][lo] = in[n][lo] W_lo[species(n)]; WT = the transposed per-element weights [n_el][C][C]
+// (pw and CG folded): mskipT for the forward, mskip for its VJP.
+void run_msg_skip(mace_ctx* c, Layer& L, const float* in, float* out, const DBuf<float>* WT, int half) {
+  std::vector<GemmProb> probs;
+  for (int lo = 0; lo < 4; ++lo)
+    add_species_probs(c, gprob(c->N, 2 * lo + 1, NC, NC, in, L.dint, NC * lo * lo, 0, nullptr, out, L.dint,
+                               NC * lo * lo, 0),
+                      1, WT[lo].p, probs);
+  run_gemm_list(c, c->stream, probs, half);
 }
 
 // Discard captured step graphs (launch arguments or buffers changed).
@@ -1608,7 +1621,7 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
     }
     if (!L.resid) {  // non-residual block: species-dependent skip FCTP on the message
       Site s(c, lname("message_skip", l));
-      run_msg_skip(c, L, L.A.p, L.A2.p, L.mskip, half);
+      run_msg_skip(c, L, L.A.p, L.A2.p, L.mskipT, half);
     }
     const float* sc_in = L.resid ? L.A.p : L.A2.p;
     const float* scw[3] = {L.sc[0].p, L.sc[1].p, L.sc[2].p};
@@ -1616,31 +1629,21 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
       Site s(c, lname("sc_fwd", l));
       launch_sc_fwd(st, N, L.lhid, L.corr, sc_in, L.dint, sc_species(c), scw, c->B.p, L.dhid, half);
     }
-    const bool one_el = c->dims.num_elements == 1;
     {
-      // h' = PLin(B) + Skip(h): one two-operand GEMM per hidden block (one element)
+      // h' = PLin(B) + Skip(h): one two-operand GEMM per hidden block (and species present)
       Site s(c, lname("linear_prod", l));
-      GemmGroup g{};
-      g.round_half = half;
+      std::vector<GemmProb> probs;
       for (int b = 0; b < L.lhid; ++b) {
         GemmProb P = gprob(N, 2 * b + 1, NC, NC, c->B.p, L.dhid, NC * b * b, 0, L.plinT[b].p, hn, L.dhid, NC * b * b, 0);
-        if (one_el && b < L.nskip) {
-          P.K2 = NC;
-          P.X2 = h;
-          P.ldx2 = L.din;
-          P.in_base2 = NC * b * b;
-          P.in_stride2 = 0;
-          P.WT2 = L.skipT[b].p;
+        if (b < L.nskip) {
+          set_skip_operand(P, h, L.din, b);
+          add_species_probs(c, P, 2, L.skipT[b].p, probs);
+        } else {
+          probs.push_back(P);
         }
-        g.p[g.n++] = P;
       }
-      run_gemm(c, st, g);
+      run_gemm_list(c, st, probs, half);
     }
-    if (!one_el)
-      for (int b = 0; b < L.nskip; ++b) {
-        Site s(c, lname("skip", l));
-        run_skip(c, L, b, h, hn, L.dhid, 1, half);
-      }
   }
   // readouts, node energies and dE/dh_L (the backward's starting gradient) in one pass
   const int L = (int)c->layers.size();
@@ -1684,7 +1687,6 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
       if (l > 0) std::swap(gh, gh_next);
       continue;
     }
-    const bool one_el = c->dims.num_elements == 1;
     {  // gB = PLin^T gh
       Site s(c, lname("linear_prod_bwd", l));
       GemmGroup g{};
@@ -1703,7 +1705,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
     const float* gmsg = c->gA.p;
     if (!Ly.resid) {
       Site s(c, lname("message_skip_bwd", l));
-      run_msg_skip(c, Ly, c->gA.p, c->gA2.p, Ly.mskipT, 0);
+      run_msg_skip(c, Ly, c->gA.p, c->gA2.p, Ly.mskip, 0);
       gmsg = c->gA2.p;
     }
     if (c->dims.density_norm) {
@@ -1771,30 +1773,22 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
     if (l > 0) {
       // dE/dh_l = Up^T gup + Skip^T gh + readout_{l-1}'
       {
-        // dE/dh_l = Up^T gup + Skip^T gh (one element) + readout_{l-1}' (bias on the 0e block)
+        // dE/dh_l = Up^T gup + Skip^T gh (per species present) + readout_{l-1}' (bias on the 0e block)
         Site s(c, lname("linear_up_bwd", l));
-        GemmGroup g{};
+        std::vector<GemmProb> probs;
         for (int b = 0; b < Ly.lin; ++b) {
           GemmProb P =
               gprob(N, 2 * b + 1, NC, NC, c->gup.p, Ly.din, NC * b * b, 0, Ly.up[b].p, gh_next, Ly.din, NC * b * b, 0);
-          if (one_el && b < Ly.nskip) {
-            P.K2 = NC;
-            P.X2 = gh;
-            P.ldx2 = Ly.dhid;
-            P.in_base2 = NC * b * b;
-            P.in_stride2 = 0;
-            P.WT2 = Ly.skip[b].p;
-          }
           if (b == 0) P.bias = c->layers[l - 1].ro.p;
-          g.p[g.n++] = P;
+          if (b < Ly.nskip) {
+            set_skip_operand(P, gh, Ly.dhid, b);
+            add_species_probs(c, P, 2, Ly.skip[b].p, probs);
+          } else {
+            probs.push_back(P);
+          }
         }
-        run_gemm(c, st, g);
+        run_gemm_list(c, st, probs, 0);
       }
-      if (!one_el)
-        for (int b = 0; b < Ly.nskip; ++b) {
-          Site s(c, lname("skip_bwd", l));
-          run_skip_T(c, Ly, b, gh, Ly.dhid, gh_next);
-        }
       std::swap(gh, gh_next);
     }
   }
@@ -1869,7 +1863,7 @@ static void free_all(mace_ctx* c) {
                   &c->node_e, &c->cutv, &c->gcut, &c->mh_dens, &c->gwb, &c->gP})
     b->release();
   c->zero_species.release();
-  for (auto* b : {&c->species, &c->sender, &c->receiver, &c->shifts, &c->rowptr, &c->rowptr_s, &c->perm_s, &c->pos_s,
+  for (auto* b : {&c->species, &c->sp_perm, &c->sender, &c->receiver, &c->shifts, &c->rowptr, &c->rowptr_s, &c->perm_s, &c->pos_s,
                   &c->nl_img, &c->nl_bin, &c->nl_bin_sorted, &c->nl_atoms, &c->nl_iota, &c->nl_counts,
                   &c->nl_bin_count, &c->nl_bin_start, &c->e_tmp_i, &c->e_tmp_j, &c->e_tmp_s, &c->e_perm,
                   &c->e_keys})
@@ -2002,6 +1996,15 @@ void set_batch(mace_ctx* c, int32_t G, const int32_t* n_atoms, const int32_t* sp
     c->species.ensure(std::max(n, 1));
     if (n > 0) HIPCHK(hipMemcpy(c->species.p, species, (size_t)n * sizeof(int), hipMemcpyHostToDevice));
     c->species_h.assign(species, species + n);
+    const int nel = c->dims.num_elements;
+    c->sp_cnt.assign(nel, 0);
+    c->sp_off.assign(nel + 1, 0);
+    for (int i = 0; i < n; ++i) ++c->sp_cnt[species[i]];
+    for (int z = 0; z < nel; ++z) c->sp_off[z + 1] = c->sp_off[z] + c->sp_cnt[z];
+    std::vector<int> perm(std::max(n, 1), 0), fill(c->sp_off.begin(), c->sp_off.end() - 1);
+    for (int i = 0; i < n; ++i) perm[fill[species[i]]++] = i;
+    c->sp_perm.ensure(perm.size());
+    HIPCHK(hipMemcpy(c->sp_perm.p, perm.data(), perm.size() * sizeof(int), hipMemcpyHostToDevice));
     if (topo_changed || c->edges_manual) {  // a manual edge list lasts until the next set_system
       c->nl_valid = false;
       c->edges_manual = false;

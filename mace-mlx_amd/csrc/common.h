@@ -294,25 +294,11 @@ void launch_fill_zero(hipStream_t st, float* p, int64_t n);
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe,
                          float* gup);
 
-// node linear: Y[n, out_base + (c/NC)*out_stride + m*NC + c%NC] (+)=
-//   sum_k X[n, in_base + (k/NC)*in_stride + m*NC + k%NC] * W[k][c]
-struct LinearDesc {
-  int d;            // rows per node (2l+1)
-  int K, Cout;      // multiples of NC
-  int ldx, in_base, in_stride;
-  int ldy, out_base, out_stride;
-  int accumulate;   // 0: overwrite, 1: add into Y
-  int round_half;   // rounding mode of the stored value (RND_*)
-};
-void launch_linear(hipStream_t st, int N, const LinearDesc& d, const float* X, const float* W,
-                   float* Y);
-// per-species weights W[z][K][Cout] (skip connection with one-hot attributes)
-void launch_linear_species(hipStream_t st, int N, const LinearDesc& d, const float* X,
-                           const float* W, const int* species, float* Y);
-
 // Grouped fp32-MFMA GEMM over node rows: up to GEMM_MAX problems in one launch.
 // Each problem: Y[row, c] (+)= sum_k X1[row, k] WT1[c][k] + sum_k X2[row, k] WT2[c][k] + bias[c]
-// with rows (node n, component m), row-addressing as in LinearDesc.
+// with rows (node n, component m): X[n, in_base + (k/NC) in_stride + m NC + k%NC], Y likewise
+// with out_base / out_stride.  With rowmap, problem row i d + m addresses node rowmap[i] (the
+// atoms of one species, for per-species weights).
 constexpr int GEMM_MAX = 8;
 struct GemmProb {
   int d, rows, K1, K2, Cout;
@@ -326,6 +312,7 @@ struct GemmProb {
   int ldy, out_base, out_stride;
   const float* bias;
   const float* rowscale;  // optional per-node factor on the product (before bias / accumulate)
+  const int* rowmap;      // optional: node of each problem row block (rows = d x its length)
   int accumulate;
   int tiles_n, tile_begin;
   // split products (GemmGroup::split): [hi | lo] fp16 planes of WT1 / WT2 scaled by 1 / winv

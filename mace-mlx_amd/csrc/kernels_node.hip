@@ -1,93 +1,13 @@
-// Node-parallel kernels: irrep-wise linears, the species-gathered skip
-// connection, node embedding, symmetric contraction (+VJP), readouts, energy
-// assembly and the deterministic force / virial reductions.
+// Node-parallel kernels: grouped products on matrix cores (irrep-wise linears, the
+// per-species skip connections over species-sorted rows), node embedding, symmetric
+// contraction (+VJP), readouts, energy assembly and the deterministic force / virial
+// reductions.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
 
 namespace mace {
 namespace {
-
-// ---------------------------------------------------------------------------
-// linear: rows (n, m), 64 x 64 output tiles, K staged 32 at a time through LDS
-// ---------------------------------------------------------------------------
-constexpr int LT = 64, LK = 32;
-
-__device__ __forceinline__ int64_t lin_in_addr(const LinearDesc& D, int row, int k) {
-  const int n = row / D.d, m = row - n * D.d;
-  return (int64_t)n * D.ldx + D.in_base + (k / NC) * D.in_stride + m * NC + (k % NC);
-}
-__device__ __forceinline__ int64_t lin_out_addr(const LinearDesc& D, int row, int c) {
-  const int n = row / D.d, m = row - n * D.d;
-  return (int64_t)n * D.ldy + D.out_base + (c / NC) * D.out_stride + m * NC + (c % NC);
-}
-
-__global__ void __launch_bounds__(256) k_linear(int rows, LinearDesc D, const float* __restrict__ X,
-                                                const float* __restrict__ W, float* __restrict__ Yo) {
-  __shared__ __align__(16) float sA[LK][LT + 4];
-  __shared__ __align__(16) float sB[LK][LT + 4];
-  const int t = threadIdx.x;
-  const int row0 = blockIdx.x * LT, col0 = blockIdx.y * LT;
-  const int tr = t >> 4, tc = t & 15;
-  float acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
-  for (int k0 = 0; k0 < D.K; k0 += LK) {
-    __syncthreads();
-    // A tile: 64 rows x 32 k (coalesced along k)
-#pragma unroll
-    for (int q = 0; q < (LT * LK) / 256; ++q) {
-      const int idx = t + 256 * q;
-      const int k = idx & (LK - 1), r = idx / LK;
-      const int row = row0 + r;
-      sA[k][r] = (row < rows) ? X[lin_in_addr(D, row, k0 + k)] : 0.f;
-    }
-    // B tile: 32 k x 64 cols
-#pragma unroll
-    for (int q = 0; q < (LT * LK) / 256; ++q) {
-      const int idx = t + 256 * q;
-      const int c = idx & (LT - 1), k = idx / LT;
-      sB[k][c] = W[(int64_t)(k0 + k) * D.Cout + col0 + c];
-    }
-    __syncthreads();
-#pragma unroll 8
-    for (int k = 0; k < LK; ++k) {
-      const float4 a = *reinterpret_cast<const float4*>(&sA[k][tr * 4]);
-      const float4 b = *reinterpret_cast<const float4*>(&sB[k][tc * 4]);
-      const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = row0 + tr * 4 + i;
-    if (row >= rows) continue;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t o = lin_out_addr(D, row, col0 + tc * 4 + j);
-      Yo[o] = qh(D.accumulate ? Yo[o] + acc[i][j] : acc[i][j], D.round_half);
-    }
-  }
-}
-
-// per-species weights: one thread per (row, output column)
-__global__ void __launch_bounds__(NC) k_linear_species(int rows, LinearDesc D, const float* __restrict__ X,
-                                                       const float* __restrict__ W, const int* __restrict__ species,
-                                                       float* __restrict__ Yo) {
-  const int row = blockIdx.x;
-  const int c = blockIdx.y * NC + threadIdx.x;
-  const int n = row / D.d;
-  const float* Wz = W + (int64_t)species[n] * D.K * D.Cout;
-  float acc = 0.f;
-  for (int k = 0; k < D.K; ++k) acc = fmaf(X[lin_in_addr(D, row, k)], Wz[(int64_t)k * D.Cout + c], acc);
-  const int64_t o = lin_out_addr(D, row, c);
-  Yo[o] = qh(D.accumulate ? Yo[o] + acc : acc, D.round_half);
-}
 
 // ---------------------------------------------------------------------------
 // grouped GEMM on fp32 matrix cores (v_mfma_f32_16x16x4f32; lane l holds
@@ -138,7 +58,8 @@ __global__ void __launch_bounds__(256) k_gemm_group(GemmGroup G) {
   const int col0 = tn * (WCOLS * 16 * CT) + (wv % WCOLS) * 16 * CT;
   const int row = rt * 16 + r;
   const bool live = row < P.rows;
-  const int n = live ? row / P.d : 0, m = live ? row - n * P.d : 0;  // dead rows read row 0, store nothing
+  const int nl = live ? row / P.d : 0, m = live ? row - nl * P.d : 0;  // dead rows read row 0, store nothing
+  const int n = P.rowmap ? P.rowmap[nl] : nl;
   GemmChunkSrc S;
   S.xrow1 = P.X1 + (int64_t)n * P.ldx1 + P.in_base1 + m * NC;
   S.xrow2 = P.K2 > 0 ? P.X2 + (int64_t)n * P.ldx2 + P.in_base2 + m * NC : S.xrow1;
@@ -198,7 +119,8 @@ __global__ void __launch_bounds__(256) k_gemm_group(GemmGroup G) {
     for (int i = 0; i < 4; ++i) {
       const int ro = rt * 16 + 4 * g + i;
       if (ro >= P.rows) continue;
-      const int no = ro / P.d, mo = ro - no * P.d;
+      const int nlo = ro / P.d, mo = ro - nlo * P.d;
+      const int no = P.rowmap ? P.rowmap[nlo] : nlo;
       float* y = P.Y + (int64_t)no * P.ldy + P.out_base + (col / NC) * P.out_stride + mo * NC + (col % NC);
       const float v = acc[u][i] * (P.rowscale ? P.rowscale[no] : 1.f) + bias;
       *y = qh(P.accumulate ? *y + v : v, G.round_half);
@@ -252,7 +174,8 @@ __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
   const int rt = tm * 4 + wv;
   const int row = rt * 16 + r;
   const bool live = row < P.rows;
-  const int n = live ? row / P.d : 0, m = live ? row - n * P.d : 0;  // dead rows read row 0, store nothing
+  const int nl = live ? row / P.d : 0, m = live ? row - nl * P.d : 0;  // dead rows read row 0, store nothing
+  const int n = P.rowmap ? P.rowmap[nl] : nl;
   GemmXSrc S;
   S.K1 = P.K1;
   S.K[0] = P.K1;
@@ -776,19 +699,6 @@ void launch_graph_virial(hipStream_t st, int G, const int* gptr, const int* rowp
                          const float* gv, double* vir) {
   if (G <= 0) return;
   MACE_LAUNCH(k_graph_virial, dim3(G), dim3(256), 0, st, gptr, rowptr, geom, gv, vir);
-}
-
-void launch_linear(hipStream_t st, int N, const LinearDesc& d, const float* X, const float* W, float* Y) {
-  const int rows = N * d.d;
-  if (rows <= 0) return;
-  MACE_LAUNCH(k_linear, dim3(cdiv(rows, LT), d.Cout / LT), dim3(256), 0, st, rows, d, X, W, Y);
-}
-
-void launch_linear_species(hipStream_t st, int N, const LinearDesc& d, const float* X, const float* W,
-                           const int* species, float* Y) {
-  const int rows = N * d.d;
-  if (rows <= 0) return;
-  MACE_LAUNCH(k_linear_species, dim3(rows, d.Cout / NC), dim3(NC), 0, st, rows, d, X, W, species, Y);
 }
 
 void launch_embed(hipStream_t st, int N, const int* species, const float* emb, int ld, float* h, int half,

@@ -13,8 +13,10 @@ import pytest
 import bench
 from mace_mlx_amd import rocprof_sites
 
-LAYERS = [dict(lin=1, lhid=2, C=128, din=128, dhid=512, dmid=2048, wn=512, nslot_by_l=[1, 1, 1, 1]),
-          dict(lin=2, lhid=1, C=128, din=512, dhid=128, dmid=5120, wn=1280, nslot_by_l=[2, 3, 3, 2])]
+LAYERS = [dict(lin=1, lhid=2, C=128, resid=True, nskip=1, din=128, dhid=512, dmid=2048, wn=512,
+               nslot_by_l=[1, 1, 1, 1]),
+          dict(lin=2, lhid=1, C=128, resid=True, nskip=1, din=512, dhid=128, dmid=5120, wn=1280,
+               nslot_by_l=[2, 3, 3, 2])]
 
 
 def _ctx(E=46000, fused=True):
@@ -40,6 +42,22 @@ def test_fused_boundary():
     assert abs(b / 1e6 - 54.4) < 0.05 and abs(f / 1e9 - 7.537) < 0.01 and pk == bench.FP32_MFMA_PEAK_TFS
     r = bench.roofline_of("tp_bwd.L1", _ctx(E=46002), 0.1662)
     assert r["bound"] == "mfma" and abs(r["frac"] - 0.288) < 0.002 and abs(r["hbm_frac"] - 0.041) < 0.001
+
+
+def test_linear_work_counts_the_fused_skip():
+    """The skip connection's product is counted where it runs: operand 2 of linear_prod and
+    of linear_up_bwd; a non-residual first block has a message-skip site (four blocks) and no
+    skip operand."""
+    N, CC = 1000, 128 * 128
+    w = bench.linear_work(LAYERS, N)
+    assert w["linear_prod.L0"][0] == 2 * N * (1 + 3 + 1) * CC          # PLin blocks 0, 1 + skip block 0
+    assert w["linear_prod_bwd.L0"][0] == 2 * N * (1 + 3) * CC
+    assert w["linear_up_bwd.L1"][0] == 2 * N * (1 + 3 + 1) * CC        # Up blocks 0, 1 + skip block 0
+    assert "message_skip.L0" not in w
+    nonres = [dict(LAYERS[0], resid=False, nskip=0)]
+    w = bench.linear_work(nonres, N)
+    assert w["message_skip.L0"][0] == w["message_skip_bwd.L0"][0] == 2 * N * 16 * CC
+    assert w["linear_prod.L0"][0] == 2 * N * 4 * CC
 
 
 def _write_trace(path, names):
