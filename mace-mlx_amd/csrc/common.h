@@ -299,7 +299,7 @@ void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, co
 // with rows (node n, component m): X[n, in_base + (k/NC) in_stride + m NC + k%NC], Y likewise
 // with out_base / out_stride.  With rowmap, problem row i d + m addresses node rowmap[i] (the
 // atoms of one species, for per-species weights).
-constexpr int GEMM_MAX = 8;
+constexpr int GEMM_MAX = 16;
 struct GemmProb {
   int d, rows, K1, K2, Cout;
   const float* X1;
@@ -327,6 +327,8 @@ struct GemmGroup {
   int round_half;  // rounding mode of the outputs (RND_*)
   int split;       // float32 policy on fp16 matrix cores (split operands, WX1 / WX2 set)
 };
+// passed by value as a kernel argument: keep it within the 4 KiB kernel-argument budget
+static_assert(sizeof(GemmGroup) <= 4096, "GemmGroup exceeds 4 KiB of kernel arguments");
 void launch_gemm_group(hipStream_t st, GemmGroup& g);
 
 // h0 = embedding per species; with up_tab, also h_up = up_tab[species] (first linear_up, which
