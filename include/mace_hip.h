@@ -116,7 +116,9 @@ int mace_model_end(mace_ctx* ctx);
 /* System topology: atom count, species index per atom (0..num_elements-1),
  * cell (row-major 3x3, rows = lattice vectors) and pbc flags.  Changing the
  * cell or pbc beyond 1e-10 invalidates the neighbour list
- * (`calculators.py:266-283`).  skin <= 0 rebuilds every step. */
+ * (`calculators.py:266-283`).  skin <= 0 rebuilds every step.  The species
+ * array is also sorted here (per-species row maps of the element-dependent skip
+ * products), so a new assignment at the same atom count goes through this call. */
 int mace_set_system(mace_ctx* ctx, int32_t n_atoms, const int32_t* species,
                     const double* cell9, const uint8_t* pbc3, double skin);
 
