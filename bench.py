@@ -74,8 +74,9 @@ def site_work(site: str, ctx: dict):
     fused = ctx.get("fused")
     if name in ("tp_fwd", "tp_bwd"):
         return tp_bytes(name, lay, N, E, s, fused), tp_flops(lay, E, fused), fpk
-    if name == "tp_gather":  # segmented sum of the per-edge input-gradient rows (implementation traffic)
-        return 4 * (E * lay["din"] + N * lay["din"]) + 4 * (N + 1), 0, fpk
+    if name == "tp_gather":  # segmented sum of the per-edge input-gradient rows (implementation traffic;
+        # the fused VJP writes them as fp16 values under the float16 policy)
+        return ctx.get("gx_bytes", 4) * E * lay["din"] + 4 * N * lay["din"] + 4 * (N + 1), 0, fpk
     if name == "mlp_hidden":  # three small layers: ef in, last hidden activation out
         return E * (4 * nb + s * H), 2 * E * (nb * H + 2 * H * H), fpk
     if name == "mlp_hidden_bwd":  # the three transposed products: dL/dh3 in, dL/def out (+ ef)
@@ -358,6 +359,7 @@ def run_workload(idx, steps, warmup, separate=False, graphs=None, extras=False, 
     ctx = dict(N=N, E=E, C=dm.dims["num_channels"], nb=dm.dims["num_bessel"], layers=layers,
                linear_work=linear_work(layers, N),
                half=bc.dtype in ("float16", "bfloat16"),
+               gx_bytes=2 if (bc.dtype == "float16" and not separate) else 4,
                fused=not separate)
     per_step = {k: (v[0] / steps, v[1] // steps) for k, v in kt.items()}
     dom = max(per_step, key=lambda k: per_step[k][0])

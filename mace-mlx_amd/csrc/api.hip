@@ -1478,7 +1478,7 @@ void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int fi
   }
   if (l > 0) {
     Site s(c, lname("tp_gather", l));
-    launch_tp_gather_gx(st, Ly.ledge, N, srow(c), c->gxe.p, c->gup.p);
+    launch_tp_gather_gx(st, Ly.ledge, N, srow(c), c->gxe.p, c->gup.p, fused && c->dims.feature_half == RND_F16);
   }
   if (!fused) {  // G = gw W3^T (into h3), gwb = gw . b3
     Site s(c, lname("mlp_gh3", l));
@@ -1747,7 +1747,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
     }
     if (l > 0) {
       Site s(c, lname("tp_gather", l));
-      launch_tp_gather_gx(st, Ly.lin, N, srow(c), c->gxe.p, c->gup.p);
+      launch_tp_gather_gx(st, Ly.lin, N, srow(c), c->gxe.p, c->gup.p, fused && half == RND_F16);
     }
     if (!fused) {
       Site s(c, lname("mlp_gh3", l));

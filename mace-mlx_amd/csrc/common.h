@@ -282,7 +282,8 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
 // launch_tpx_fwd), writes the dL/dh3 partials gh3p ([P][E][64], P = 2 x input
 // degrees of the layer), dL/dY partials into gY[e][p][16] (gyp partials per
 // edge; written, or added when accumulate_gY) and, with gxe, the per-edge dL/dx
-// rows as launch_tp_bwd_recv does.  wfmt: the storage format of w (the forward's rnd).  b3
+// rows as launch_tp_bwd_recv does (as fp16 values when wfmt is RND_F16).  wfmt: the storage
+// format of w (the forward's rnd).  b3
 // (non-linear interaction block, float32 policy; null otherwise): also the partials
 // gwbp[p][e] = sum over partial p's columns k of dL/dw[e][k] b3[k] ([P][E]).
 void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
@@ -291,8 +292,9 @@ void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
                     float* gh3p, int wfmt, const float* b3, float* gwbp);
 // p[0 .. n) = 0 (a kernel, not a memset: safe inside captured graphs)
 void launch_fill_zero(hipStream_t st, float* p, int64_t n);
+// gx16: the rows hold fp16 values (launch_tpx_bwd under the float16 policy), else floats
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe,
-                         float* gup);
+                         float* gup, int gx16);
 
 // Grouped fp32-MFMA GEMM over node rows: up to GEMM_MAX problems in one launch.
 // Each problem: Y[row, c] (+)= sum_k X1[row, k] WT1[c][k] + sum_k X2[row, k] WT2[c][k] + bias[c]

@@ -525,21 +525,23 @@ __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __rest
 }
 
 // gup[a][row][u] = sum over the edges sent by a (a contiguous segment of the
-// sender-ordered gxe rows, summed in order); grid (N, LIN^2), NC threads.
+// sender-ordered gxe rows, summed in order, fp32); grid (N, LIN^2), NC threads.
+// GT: the rows' element type (fp16 under the float16 policy's fused VJP).
+template <typename GT>
 __global__ void __launch_bounds__(NC) k_tp_gather_gx(int N, int din, const int* __restrict__ rowptr_s,
-                                                     const float* __restrict__ gxe, float* __restrict__ gup) {
+                                                     const GT* __restrict__ gxe, float* __restrict__ gup) {
   const int a = blockIdx.x, row = blockIdx.y, u = threadIdx.x;
   const int beg = rowptr_s[a], end = rowptr_s[a + 1];
-  const float* src = gxe + (int64_t)row * NC + u;
+  const GT* src = gxe + (int64_t)row * NC + u;
   float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
   int k = beg;
   for (; k + 3 < end; k += 4) {
-    s0 += src[(int64_t)k * din];
-    s1 += src[(int64_t)(k + 1) * din];
-    s2 += src[(int64_t)(k + 2) * din];
-    s3 += src[(int64_t)(k + 3) * din];
+    s0 += (float)src[(int64_t)k * din];
+    s1 += (float)src[(int64_t)(k + 1) * din];
+    s2 += (float)src[(int64_t)(k + 2) * din];
+    s3 += (float)src[(int64_t)(k + 3) * din];
   }
-  for (; k < end; ++k) s0 += src[(int64_t)k * din];
+  for (; k < end; ++k) s0 += (float)src[(int64_t)k * din];
   gup[(int64_t)a * din + row * NC + u] = (s0 + s1) + (s2 + s3);
 }
 
@@ -1035,7 +1037,8 @@ __global__ void __launch_bounds__(64 * XW, 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_
 // the group's k steps, holding those W3 fragments in registers; the two halves
 // of a q tile meet through LDS one step later (no second barrier).
 // dL/dY partials go to gY[e][p][16] and dL/dx rows to gxe[pos_s[e]] (this
-// group's components, this slice's channels).  As in the forward, every load
+// group's components, this slice's channels; fp16 values under the float16
+// policy, which halves the largest per-edge stream the VJP writes).  As in the forward, every load
 // is unconditional (clamped indices); stores of padding edges are skipped.
 // ---------------------------------------------------------------------------
 // l1 = 1 slots of a receiver-centric VJP, refactored around what stays fixed while a
@@ -1383,7 +1386,15 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
         pb = wave_sum_lane63(pb);
         buf_store(pb, gwbv, l == 63 && valid ? 4u * (unsigned)(e - eb0) : BUF_OOB);
       }
-      if constexpr (GX) {
+      if constexpr (GX && WF == RND_F16) {  // float16 policy: the rows as fp16 values
+        const auto gxv = buf_view(reinterpret_cast<_Float16*>(gxe) + (int64_t)S.ps[b] * DIN, valid ? 2u * DIN : 0u);
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+          const float v = L1 == 0 ? gx0 : L1 == 1 ? gx1[i] : gx2[i];
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (_Float16)v), gxv,
+                                                (int)(2u * (NC * (L1 * L1 + i) + c0 + u)), 0, 0);
+        }
+      } else if constexpr (GX) {
         const auto gxv = buf_view(gxe + (int64_t)S.ps[b] * DIN, valid ? 4u * DIN : 0u);
 #pragma unroll
         for (int i = 0; i < NX; ++i)
@@ -1639,9 +1650,14 @@ void launch_fill_zero(hipStream_t st, float* p, int64_t n) {
   MACE_LAUNCH(k_fill_zero, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 1024)), dim3(256), 0, st, p, n);
 }
 
-void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe, float* gup) {
+void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe, float* gup,
+                         int gx16) {
   if (N <= 0) return;
-  MACE_LAUNCH(k_tp_gather_gx, dim3(N, lin * lin), dim3(NC), 0, st, N, NC * lin * lin, rowptr_s, gxe, gup);
+  if (gx16)
+    MACE_LAUNCH(k_tp_gather_gx<_Float16>, dim3(N, lin * lin), dim3(NC), 0, st, N, NC * lin * lin, rowptr_s,
+                reinterpret_cast<const _Float16*>(gxe), gup);
+  else
+    MACE_LAUNCH(k_tp_gather_gx<float>, dim3(N, lin * lin), dim3(NC), 0, st, N, NC * lin * lin, rowptr_s, gxe, gup);
 }
 
 }  // namespace mace

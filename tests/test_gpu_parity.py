@@ -163,6 +163,7 @@ def test_float16_feature_policy(arch):
     assert edge_set(*edges) == bruteforce_edges(s)
     ref = case.reference(s, got["sp"], edges, stress=True)
     de, rel, mx = _fp16_errors(got, ref, len(s))
+    print(f"float16 {arch}: |dE|/N {de:.2e} eV, force RMS rel {rel:.2e}, max|dF| {mx:.2e} eV/A", flush=True)
     assert de <= 1e-3 and rel <= 1e-2 and mx <= 2e-2, (de, rel, mx)
     dv = np.abs(got["vir"] - ref["vir"]).max()
     assert dv <= 1e-2 * max(1.0, np.abs(ref["vir"]).max()), (got["vir"], ref["vir"])
