@@ -779,15 +779,17 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   c->zbl_e.ensure(e);
   c->gY.ensure(e * 16 * kGyMax);
   c->gh3p.ensure(e * RADIAL_H * kGyMax);
-  if (c->mts > 0) c->Mt.ensure(e * c->mts);
   c->gef.ensure(e * c->dims.num_bessel);
   c->h3.ensure(e * RADIAL_H);
   c->gv.ensure(e * 3);
-  if (half)
-    c->gwh.ensure(e * maxw);
-  else
-    c->gw.ensure(e * maxw);
-  c->gscale.ensure(e * NSLICE);
+  if (!path.fused) {  // the separate passes' per-edge CG tables and dL/dw (the fused kernels keep both on chip)
+    if (c->mts > 0) c->Mt.ensure(e * c->mts);
+    if (half)
+      c->gwh.ensure(e * maxw);
+    else
+      c->gw.ensure(e * maxw);
+    c->gscale.ensure(e * NSLICE);
+  }
   c->h3inv.ensure(e);
   c->vir_part.ensure(9 * ((e + 255) / 256));
 

@@ -245,6 +245,12 @@ class Engine:
             raise ValueError("sender / receiver / shifts lengths differ")
         self._check(self._lib.mace_set_edges(self._h, len(s), _ptr(s), _ptr(r), _ptr(S)))
 
+    def num_edges(self) -> int:
+        """Edge count of the current list (mace_get_edges without arrays)."""
+        n = ctypes.c_int64()
+        self._check(self._lib.mace_get_edges(self._h, 0, None, None, None, ctypes.byref(n)))
+        return n.value
+
     def get_edges(self):
         n = ctypes.c_int64()
         self._check(self._lib.mace_get_edges(self._h, 0, None, None, None, ctypes.byref(n)))

@@ -293,6 +293,34 @@ def test_periodic_replication_is_exact(medium_zbl):
     np.testing.assert_allclose(b["vir"], 2 * a["vir"], rtol=1e-5, atol=1e-6)
 
 
+def test_replication_at_256k_atoms(medium_zbl):
+    """Far past the benchmark sizes: Si1000 repeated 8 x 8 x 4 (256,000 atoms, 11.8 M edges,
+    ~11.6 KB of per-edge arrays per edge, ~140 GB) gives 256 times its edges and energy, and
+    every image repeats its forces and node energies; a 32-bit byte offset or an overfull
+    buffer view would break this."""
+    import torch
+    s = make_config(1).system
+    a = medium_zbl.run(s)
+    E1 = medium_zbl.eng.num_edges()
+    reps = (8, 8, 4)
+    shifts = np.array([[i, j, k] for i in range(reps[0]) for j in range(reps[1]) for k in range(reps[2])],
+                      dtype=np.float64) @ s.cell
+    big = System((s.positions[None, :, :] + shifts[:, None, :]).reshape(-1, 3), np.tile(s.numbers, len(shifts)),
+                 s.cell * np.array(reps, dtype=np.float64)[:, None], s.pbc)
+    free0 = torch.cuda.mem_get_info()[0]
+    b = medium_zbl.run(big)
+    used = (free0 - torch.cuda.mem_get_info()[0]) / 2**30
+    n_img = len(shifts)
+    print(f"256k atoms: {medium_zbl.eng.num_edges()} edges, E {b['E']:.6f} vs {n_img} x {a['E']:.6f}, "
+          f"device memory +{used:.1f} GiB", flush=True)
+    assert medium_zbl.eng.num_edges() == n_img * E1
+    assert abs(b["E"] - n_img * a["E"]) <= 1e-6 * abs(b["E"])
+    F = b["F"].reshape(n_img, len(s), 3)
+    assert np.abs(F - a["F"][None]).max() <= 1e-4
+    ne = b["ne"].reshape(n_img, len(s))
+    assert np.abs(ne - a["ne"][None]).max() <= 1e-5 * max(1.0, np.abs(a["ne"]).max())
+
+
 def test_hea_full_size_runs_and_pairs():
     """Configuration 5 at full size (32,000 atoms, 2.75 M edges) in its own dtype (float16
     feature policy): pairing of the neighbour list, sum of forces, translation invariance."""
