@@ -685,7 +685,9 @@ void ensure_node_buffers(mace_ctx* c) {
   const int N = std::max(c->N, 1);
   const int L = (int)c->layers.size();
   c->h.resize(L + 1);
-  int maxd = NC * 16;
+  // work-array row widths: the widest use over the layers (M / dL/dM: dmid; B / dL/dB: dhid;
+  // dL/dA: dint; dL/dh: din and dhid; dL/d(up): the conv TP input)
+  int wmid = 0, whid = 0, wint = NC * 16, win = 0, wtp = 0;
   for (int l = 0; l < L; ++l) {
     Layer& ly = c->layers[l];
     c->h[l].ensure((size_t)N * ly.din);
@@ -699,22 +701,26 @@ void ensure_node_buffers(mace_ctx* c) {
       ly.Gt.ensure((size_t)N * ly.dint);
       c->gP.ensure((size_t)N * kGateInDim);
     }
-    maxd = std::max({maxd, ly.dmid, ly.din, ly.dhid, ly.dtp()});
+    wmid = std::max(wmid, ly.dmid);
+    whid = std::max(whid, ly.dhid);
+    wint = std::max(wint, ly.dint);
+    win = std::max(win, ly.din);
+    wtp = std::max(wtp, ly.dtp());
   }
   if (c->dims.agnostic_product && c->zero_species.n < (size_t)N) {
     c->zero_species.ensure(N);
     HIPCHK(hipMemset(c->zero_species.p, 0, (size_t)N * sizeof(int)));
   }
   c->h[L].ensure((size_t)N * c->layers[L - 1].dhid);
-  c->M.ensure((size_t)N * maxd);
-  c->B.ensure((size_t)N * maxd);
-  c->gB.ensure((size_t)N * maxd);
-  c->gA.ensure((size_t)N * maxd);
-  c->gM.ensure((size_t)N * maxd);
-  c->gh0.ensure((size_t)N * maxd);
-  c->gh1.ensure((size_t)N * maxd);
-  c->gup.ensure((size_t)N * maxd);
-  c->gA2.ensure((size_t)N * maxd);
+  c->M.ensure((size_t)N * wmid);
+  c->gM.ensure((size_t)N * wmid);
+  c->B.ensure((size_t)N * whid);
+  c->gB.ensure((size_t)N * whid);
+  c->gA.ensure((size_t)N * wint);
+  c->gA2.ensure((size_t)N * wint);
+  c->gh0.ensure((size_t)N * std::max(win, whid));
+  c->gh1.ensure((size_t)N * std::max(win, whid));
+  c->gup.ensure((size_t)N * std::max(win, wtp));
   c->grho.ensure(N);
   c->node_e.ensure(N);
   c->e_part.ensure((N + 3) / 4 + 1);
