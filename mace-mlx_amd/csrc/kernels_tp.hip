@@ -1165,6 +1165,10 @@ struct TpxBwdDims {
   // dL/dw[e][k] b3[k] (b3 [W], gwbp [P][E])
   const float* b3;
   float* gwbp;
+  // waves per receiver (1, 2, 4 or 8; XW / spr receivers per block): a receiver's edges split
+  // into spr contiguous chunks, one per wave, so that a small system's few receivers fill the
+  // chip (the VJP of an edge depends on its receiver's dL/dM only: nothing to combine)
+  int spr;
 };
 
 #define MACE_TPX_BWD_PTRS                                                                                   \
@@ -1199,18 +1203,28 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   }
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, r = l & 15, g = l >> 4, u = l;
-  const int c0 = 64 * blockIdx.y, nb0 = XW * blockIdx.x, p = NSLICE * blockIdx.z + blockIdx.y;
-  const int n = nb0 + wv;
-  const int beg = rowptr[min(n, a.N)], end = n < a.N ? rowptr[n + 1] : beg;
-  const int nr = nb0 + (r >> 1);  // receiver of tile column r
-  const int cb = rowptr[min(nr, a.N)], ce = nr < a.N ? rowptr[nr + 1] : cb;
+  const int rpb = XW / a.spr;  // receivers per block
+  const int c0 = 64 * blockIdx.y, nb0 = rpb * blockIdx.x, p = NSLICE * blockIdx.z + blockIdx.y;
+  // wave k: receiver nb0 + k / spr, chunk k % spr of its edges -> [wb, we)
+  auto wave_range = [&](int k, int& wn, int& wb, int& we) {
+    wn = nb0 + k / a.spr;
+    const int c = k % a.spr;
+    const int rb = rowptr[min(wn, a.N)], re = wn < a.N ? rowptr[wn + 1] : rb;
+    const int cnt = re - rb, csz = (cnt + a.spr - 1) / a.spr;
+    wb = rb + min(cnt, c * csz);
+    we = rb + min(cnt, (c + 1) * csz);
+  };
+  int n, beg, end;
+  wave_range(wv, n, beg, end);
+  int nr, cb, ce;
+  wave_range(r >> 1, nr, cb, ce);  // the wave whose edges are tile columns r
   int ns = (ce - cb + 1) >> 1;
 #pragma unroll
   for (int off = 8; off > 0; off >>= 1) ns = max(ns, __shfl_xor(ns, off));
   const int nsteps = __builtin_amdgcn_readfirstlane(ns);
   const int64_t elast = a.E - 1;
   // the block's edges [eb0, eb1) (its receivers' rows): a view of their dL/dh3 partial rows p
-  const int eb0 = rowptr[min(nb0, a.N)], eb1 = rowptr[min(nb0 + XW, a.N)];
+  const int eb0 = rowptr[min(nb0, a.N)], eb1 = rowptr[min(nb0 + rpb, a.N)];
   const auto gh3v = buf_view(gh3p + ((int64_t)p * a.E + eb0) * XH, 4u * XH * (unsigned)(eb1 - eb0));
   // NL: the block's entries of gw . b3 partial p, and b3 of this lane's channel in the group slots
   const auto gwbv = buf_view(NL ? a.gwbp + (int64_t)p * a.E + eb0 : nullptr, NL ? 4u * (unsigned)(eb1 - eb0) : 0u);
@@ -1607,13 +1621,20 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
 #undef MACE_TPXF
 }
 
+// the VJP splits receivers over several waves below this many blocks (256 CUs; Si1000's layer 0
+// has 250 blocks of one receiver per wave and stays so)
+constexpr int kTpxBwdMinBlocks = 240;
+
 void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const float* w, const void* W3x, int W, float wscale, const float* up,
                     const float* gM, const int* pos_s, float* gxe, float* gY, int gyp, int accumulate_gY,
                     float* gh3p, int wfmt, const float* b3, float* gwbp) {
   if (N <= 0 || E <= 0) return;  // no edges: no dL/dw, dL/dY, dL/dx rows to write
-  const TpxBwdDims a{N, W, mts, E, wscale, accumulate_gY, gyp, b3, gwbp};
-  const dim3 grid((unsigned)((N + XW - 1) / XW), NSLICE, (unsigned)lin);
+  // waves per receiver: enough blocks for the CUs (small systems), one otherwise
+  int spr = 1;
+  while (spr < XW && (int64_t)((N + XW / spr - 1) / (XW / spr)) * NSLICE * lin < kTpxBwdMinBlocks) spr *= 2;
+  const TpxBwdDims a{N, W, mts, E, wscale, accumulate_gY, gyp, b3, gwbp, spr};
+  const dim3 grid((unsigned)((N + XW / spr - 1) / (XW / spr)), NSLICE, (unsigned)lin);
   const _Float16* wx = static_cast<const _Float16*>(W3x);
 #define MACE_TPXB(L, GXV, WF, NLV)                                                                         \
   MACE_LAUNCH((k_tpx_bwd<L, GXV, WF, NLV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \
