@@ -555,7 +555,9 @@ __global__ void __launch_bounds__(NC) k_tp_gather_gx(int N, int din, const int* 
 // consumed there by the TP, and written out once for the VJP.
 //
 // Block = XW waves; wave k owns receiver XW * blockIdx.x + k and walks its
-// edges two per step, lane = channel c0 + u of the block's 64-channel slice
+// edges two per step (small systems: spr waves per receiver, each walking a
+// contiguous chunk of its edges; the chunks' sums are added in order at the
+// end), lane = channel c0 + u of the block's 64-channel slice
 // (blockIdx.y).  blockIdx.z selects the slots handled: those whose input block
 // is one l1 (highest l1 first), so the groups read and write disjoint data.
 // Tile column r = 2k + b holds edge b of wave k's current pair.  The W3 rows of
@@ -643,6 +645,12 @@ struct GrpT {
     return n;
   }
   static constexpr int G = count();
+  // accumulator components of the group's slots
+  __host__ __device__ static constexpr int acc_count() {
+    int n = 0;
+    for (int s = 0; s < T::NSLOT; ++s) n += T::l1(s) == L1 ? 2 * T::l3(s) + 1 : 0;
+    return n;
+  }
   // position of slot s among the group's slots
   __host__ __device__ static constexpr int local(int s) {
     int k = 0;
@@ -690,6 +698,10 @@ struct TpxDims {
   // non-linear interaction block (NL): w = (W3^T h3 + b3) cut, b3 [W], cut [E] (null: 1)
   const float* b3;
   const float* cut;
+  // log2 of the waves per receiver (spr = 1, 2, 4 or 8; XW / spr receivers per block): a
+  // receiver's edges split into spr contiguous chunks, one per wave, their message sums added
+  // in chunk order at the end
+  int sprl;
 };
 
 #define MACE_TPX_FWD_PTRS                                                                                   \
@@ -714,13 +726,22 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   // wave-uniform scalars (scalar loads, no vector-memory waits on the prefetches)
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, r = l & 15, g = l >> 4, u = l;
-  const int c0 = 64 * blockIdx.y, nb0 = XW * blockIdx.x;
-  const int n = nb0 + wv;
-  const int beg = rowptr[min(n, a.N)], end = n < a.N ? rowptr[n + 1] : beg;
+  const int c0 = 64 * blockIdx.y, nb0 = (XW >> a.sprl) * blockIdx.x;  // XW / spr receivers per block
+  // wave k: receiver nb0 + k / spr, chunk k % spr of its edges -> [wb, we)
+  auto wave_range = [&](int k, int& wn, int& wb, int& we) {
+    wn = nb0 + (k >> a.sprl);
+    const int c = k & ((1 << a.sprl) - 1);
+    const int rb = rowptr[min(wn, a.N)], re = wn < a.N ? rowptr[wn + 1] : rb;
+    const int cnt = re - rb, csz = (cnt + (1 << a.sprl) - 1) >> a.sprl;
+    wb = rb + min(cnt, c * csz);
+    we = rb + min(cnt, (c + 1) * csz);
+  };
+  int n, beg, end;
+  wave_range(wv, n, beg, end);
   int ns;
   {
-    const int nq = nb0 + (l & (XW - 1));  // lanes 0..7: the block's receivers
-    const int qb = rowptr[min(nq, a.N)], qe = nq < a.N ? rowptr[nq + 1] : qb;
+    int nq, qb, qe;
+    wave_range(l & (XW - 1), nq, qb, qe);  // lanes 0..7: the block's waves
     ns = (qe - qb + EPW - 1) / EPW;
   }
 #pragma unroll
@@ -797,9 +818,13 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   constexpr int TPR = 512 / TC, HQ = 128 / TPR;  // threads per tile row; fp16 entries per thread
   typedef unsigned hv __attribute__((ext_vector_type(HQ / 2)));
   const int hr = threadIdx.x / TPR, hpl = (threadIdx.x % TPR) / (TPR / 2), hq = threadIdx.x % (TPR / 2);
-  // tile column hr: step TPS t + hr / 16 of the tile, edge hr % EPW of receiver nb0 + (hr % 16) / EPW
-  const int hn = nb0 + (hr % 16) / EPW, hs = hr / 16;
-  const int hb0 = rowptr[min(hn, a.N)];
+  // tile column hr: step TPS t + hr / 16 of the tile, edge hr % EPW of wave (hr % 16) / EPW
+  const int hs = hr / 16;
+  int hb0;
+  {
+    int hn, hend;
+    wave_range((hr % 16) / EPW, hn, hb0, hend);
+  }
   struct HSlot {
     hv h;        // this thread's share of a tile's h3 rows
     float hinv;  // inverse scale of its row
@@ -982,7 +1007,33 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
     if constexpr (TPS == 1) tile_begin(j + 1);
     edges(j + 1, s1, s0);
   }
-  if (n < a.N) {
+  if (a.sprl > 0) {  // uniform: the chunks' sums through LDS (the w tile buffer), in chunk order
+    constexpr int GA = GR::acc_count();
+    static_assert((XW - 1) * GA * 64 <= 2 * TC * RS, "chunk partials fit the w tile buffer");
+    __syncthreads();  // every wave is done with the tiles
+    const int c = wv & ((1 << a.sprl) - 1);
+    if (c > 0) {
+      float* part = sw + ((wv - 1) * GA) * 64 + u;
+      int q = 0;
+#pragma unroll
+      for (int s = 0; s < T::NSLOT; ++s)
+        if (T::l1(s) == L1)
+#pragma unroll
+          for (int m = 0; m < 2 * T::l3(s) + 1; ++m) part[64 * q++] = acc[T::acc(s) + m];
+    }
+    __syncthreads();
+    if (c == 0)
+      for (int k = 1; k < (1 << a.sprl); ++k) {
+        const float* part = sw + ((wv + k - 1) * GA) * 64 + u;
+        int q = 0;
+#pragma unroll
+        for (int s = 0; s < T::NSLOT; ++s)
+          if (T::l1(s) == L1)
+#pragma unroll
+            for (int m = 0; m < 2 * T::l3(s) + 1; ++m) acc[T::acc(s) + m] += part[64 * q++];
+      }
+  }
+  if (n < a.N && (wv & ((1 << a.sprl) - 1)) == 0) {
     float* Mn = M + (int64_t)n * DMID + c0 + u;
 #pragma unroll
     for (int s = 0; s < T::NSLOT; ++s)
@@ -1165,10 +1216,11 @@ struct TpxBwdDims {
   // dL/dw[e][k] b3[k] (b3 [W], gwbp [P][E])
   const float* b3;
   float* gwbp;
-  // waves per receiver (1, 2, 4 or 8; XW / spr receivers per block): a receiver's edges split
-  // into spr contiguous chunks, one per wave, so that a small system's few receivers fill the
-  // chip (the VJP of an edge depends on its receiver's dL/dM only: nothing to combine)
-  int spr;
+  // log2 of the waves per receiver (spr = 1, 2, 4 or 8; XW / spr receivers per block): a
+  // receiver's edges split into spr contiguous chunks, one per wave, so that a small system's
+  // few receivers fill the chip (the VJP of an edge depends on its receiver's dL/dM only:
+  // nothing to combine)
+  int sprl;
 };
 
 #define MACE_TPX_BWD_PTRS                                                                                   \
@@ -1203,14 +1255,14 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   }
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, r = l & 15, g = l >> 4, u = l;
-  const int rpb = XW / a.spr;  // receivers per block
+  const int rpb = XW >> a.sprl;  // receivers per block
   const int c0 = 64 * blockIdx.y, nb0 = rpb * blockIdx.x, p = NSLICE * blockIdx.z + blockIdx.y;
   // wave k: receiver nb0 + k / spr, chunk k % spr of its edges -> [wb, we)
   auto wave_range = [&](int k, int& wn, int& wb, int& we) {
-    wn = nb0 + k / a.spr;
-    const int c = k % a.spr;
+    wn = nb0 + (k >> a.sprl);
+    const int c = k & ((1 << a.sprl) - 1);
     const int rb = rowptr[min(wn, a.N)], re = wn < a.N ? rowptr[wn + 1] : rb;
-    const int cnt = re - rb, csz = (cnt + a.spr - 1) / a.spr;
+    const int cnt = re - rb, csz = (cnt + (1 << a.sprl) - 1) >> a.sprl;
     wb = rb + min(cnt, c * csz);
     we = rb + min(cnt, (c + 1) * csz);
   };
@@ -1585,12 +1637,26 @@ void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const
 #undef MACE_RECV
 }
 
+// the fused TP kernels split a receiver's edges over several waves below this many blocks per
+// layer (256 CUs; Si1000's layer 0 has 250 blocks of one receiver per wave and stays so)
+constexpr int kTpxMinBlocks = 240;
+// log2 of the waves per receiver of a fused TP launch over N receivers: the fewest (1 to XW) that
+// give kTpxMinBlocks blocks
+int tpx_split_log2(int N, int lin) {
+  int l = 0;
+  while ((1 << l) < XW && (int64_t)((N + (XW >> l) - 1) / (XW >> l)) * NSLICE * lin < kTpxMinBlocks) ++l;
+  return l;
+}
+
 void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const void* h3x, const float* h3inv, const void* W3Tx, int W,
                     float wscale, const float* up, float* M, float* w, int rnd, const float* b3, const float* cut) {
   if (N <= 0) return;
-  const TpxDims a{N, W, mts, E, wscale, b3, cut};
-  const dim3 grid((unsigned)((N + XW - 1) / XW), NSLICE, (unsigned)lin);  // y: channel slice; z: input block l1
+  // waves per receiver: enough blocks for the CUs (small systems), one otherwise
+  const int sprl = tpx_split_log2(N, lin);
+  const TpxDims a{N, W, mts, E, wscale, b3, cut, sprl};
+  // y: channel slice; z: input block l1
+  const dim3 grid((unsigned)((N + (XW >> sprl) - 1) / (XW >> sprl)), NSLICE, (unsigned)lin);
   const _Float16* hx = static_cast<const _Float16*>(h3x);
   const _Float16* wt = static_cast<const _Float16*>(W3Tx);
 #define MACE_TPXF(L, R, NLV) \
@@ -1621,9 +1687,6 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
 #undef MACE_TPXF
 }
 
-// the VJP splits receivers over several waves below this many blocks (256 CUs; Si1000's layer 0
-// has 250 blocks of one receiver per wave and stays so)
-constexpr int kTpxBwdMinBlocks = 240;
 
 void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const float* w, const void* W3x, int W, float wscale, const float* up,
@@ -1631,10 +1694,9 @@ void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
                     float* gh3p, int wfmt, const float* b3, float* gwbp) {
   if (N <= 0 || E <= 0) return;  // no edges: no dL/dw, dL/dY, dL/dx rows to write
   // waves per receiver: enough blocks for the CUs (small systems), one otherwise
-  int spr = 1;
-  while (spr < XW && (int64_t)((N + XW / spr - 1) / (XW / spr)) * NSLICE * lin < kTpxBwdMinBlocks) spr *= 2;
-  const TpxBwdDims a{N, W, mts, E, wscale, accumulate_gY, gyp, b3, gwbp, spr};
-  const dim3 grid((unsigned)((N + XW / spr - 1) / (XW / spr)), NSLICE, (unsigned)lin);
+  const int sprl = tpx_split_log2(N, lin);
+  const TpxBwdDims a{N, W, mts, E, wscale, accumulate_gY, gyp, b3, gwbp, sprl};
+  const dim3 grid((unsigned)((N + (XW >> sprl) - 1) / (XW >> sprl)), NSLICE, (unsigned)lin);
   const _Float16* wx = static_cast<const _Float16*>(W3x);
 #define MACE_TPXB(L, GXV, WF, NLV)                                                                         \
   MACE_LAUNCH((k_tpx_bwd<L, GXV, WF, NLV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \

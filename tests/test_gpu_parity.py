@@ -414,9 +414,11 @@ def test_skin_cache(medium_zbl):
 def test_batch_of_structures(medium_zbl):
     """Several structures in one step (the reference model's batched call, `model.py:440-484`,
     energies per structure by `graph_sum`, `utils.py:35-44`), each in its own cell: a
-    triclinic cell, a molecule, a slab and a rattled Si64.  Per-structure energies, virials,
-    forces and edge lists equal those of separate steps of the same engine, no edge joins two
-    structures, and every structure meets the oracle tolerances."""
+    triclinic cell, a molecule, a slab and a rattled Si64.  Per-structure edge lists equal those
+    of separate steps of the same engine and no edge joins two structures; energies, virials and
+    forces equal the separate steps' to float32 rounding (a launch over fewer receivers may split
+    each receiver's message sum over several waves, which changes only the order of its fp32
+    sums), and every structure meets the oracle tolerances."""
     case = medium_zbl
     structs = [_triclinic(), _molecule(), _slab(), rattle(diamond_si((2, 2, 2)), 0.03, 21)]
     sps = [species_of(case.dm, s.numbers) for s in structs]
@@ -436,10 +438,10 @@ def test_batch_of_structures(medium_zbl):
         dF = float(np.abs(F[a:b] - got["F"]).max())
         dV = float(np.abs(vir[g] - got["vir"]).max())
         print(f"structure {g}: batch vs single dE={dE:.2e} dF={dF:.2e} dvir={dV:.2e}")
-        assert dE <= 1e-10 * max(abs(got["E"]), n)
-        assert dF <= 1e-7
-        assert dV <= 1e-9 * max(1.0, float(np.abs(got["vir"]).max()))
-        np.testing.assert_allclose(ne[a:b], got["ne"], rtol=0, atol=1e-7)
+        assert dE <= 1e-7 * max(abs(got["E"]), n)
+        assert dF <= 1e-5
+        assert dV <= 1e-5 * max(1.0, float(np.abs(got["vir"]).max()))
+        np.testing.assert_allclose(ne[a:b], got["ne"], rtol=0, atol=1e-6)
         per = bool(s.pbc.all())
         ref = case.reference(s, sps[g], edges_g, stress=per)
         assert_parity(dict(E=eg[g], F=F[a:b], ne=ne[a:b], vir=vir[g]), ref, n, stress=per)
@@ -596,14 +598,15 @@ def test_calculator_end_to_end(tmp_path):
     bad.numbers[0] = 8
     with pytest.raises(ValueError):
         calc.calculate(bad, ["energy"])
-    # several structures in one step, then a single one again
+    # several structures in one step, then a single one again: equal to float32 rounding (the
+    # batch and the lone structure may split their message sums over waves differently)
     small = rattle(diamond_si((2, 2, 2)), 0.03, 5)
     res = calc.calculate_batch([s, small], ["energy", "forces", "stress"])
-    assert abs(res[0]["energy"] - r["energy"]) <= 1e-9 * abs(r["energy"])
-    np.testing.assert_allclose(res[0]["forces"], r["forces"], rtol=0, atol=1e-7)
+    assert abs(res[0]["energy"] - r["energy"]) <= 1e-7 * abs(r["energy"])
+    np.testing.assert_allclose(res[0]["forces"], r["forces"], rtol=0, atol=1e-5)
     calc.calculate(small, ["energy", "forces", "stress"])
-    assert abs(res[1]["energy"] - calc.results["energy"]) <= 1e-9 * abs(calc.results["energy"])
-    np.testing.assert_allclose(res[1]["stress"], calc.results["stress"], rtol=0, atol=1e-9)
+    assert abs(res[1]["energy"] - calc.results["energy"]) <= 1e-7 * abs(calc.results["energy"])
+    np.testing.assert_allclose(res[1]["stress"], calc.results["stress"], rtol=0, atol=1e-7)
 
 
 def test_calculator_matches_oracle(tmp_path):
