@@ -368,6 +368,20 @@ void make_split(mace_ctx* c, const float* p, size_t count) {
   upload_split(c, sw.x, h, std::ldexp(1.f, 14 - ex));
 }
 
+// The atoms sorted by species (stable) for the model's element count: row maps of the
+// per-species products (species_h holds valid indices)
+void set_species_order(mace_ctx* c) {
+  const int n = (int)c->species_h.size(), nel = c->dims.num_elements;
+  c->sp_cnt.assign(nel, 0);
+  c->sp_off.assign(nel + 1, 0);
+  for (int i = 0; i < n; ++i) ++c->sp_cnt[c->species_h[i]];
+  for (int z = 0; z < nel; ++z) c->sp_off[z + 1] = c->sp_off[z] + c->sp_cnt[z];
+  std::vector<int> perm(std::max(n, 1), 0), fill(c->sp_off.begin(), c->sp_off.end() - 1);
+  for (int i = 0; i < n; ++i) perm[fill[c->species_h[i]]++] = i;
+  c->sp_perm.ensure(perm.size());
+  HIPCHK(hipMemcpy(c->sp_perm.p, perm.data(), perm.size() * sizeof(int), hipMemcpyHostToDevice));
+}
+
 std::vector<float> transpose(const std::vector<float>& a, int rows, int cols, int batch = 1) {
   std::vector<float> t(a.size());
   for (int b = 0; b < batch; ++b)
@@ -1941,6 +1955,12 @@ int mace_model_end(mace_ctx* c) {
     // the cached edges were built for the previous model's r_max + skin
     if (!c->edges_manual) c->nl_valid = false;
     if (c->system_ready) {
+      // the system's species must be elements of the new model (else mace_set_system again)
+      for (int z : c->species_h)
+        if (z >= c->dims.num_elements) c->system_ready = false;
+    }
+    if (c->system_ready) {
+      set_species_order(c);
       ensure_node_buffers(c);
       ensure_edge_buffers(c, c->E);  // per-layer edge buffers of the new model
     }
@@ -2004,15 +2024,7 @@ void set_batch(mace_ctx* c, int32_t G, const int32_t* n_atoms, const int32_t* sp
     c->species.ensure(std::max(n, 1));
     if (n > 0) HIPCHK(hipMemcpy(c->species.p, species, (size_t)n * sizeof(int), hipMemcpyHostToDevice));
     c->species_h.assign(species, species + n);
-    const int nel = c->dims.num_elements;
-    c->sp_cnt.assign(nel, 0);
-    c->sp_off.assign(nel + 1, 0);
-    for (int i = 0; i < n; ++i) ++c->sp_cnt[species[i]];
-    for (int z = 0; z < nel; ++z) c->sp_off[z + 1] = c->sp_off[z] + c->sp_cnt[z];
-    std::vector<int> perm(std::max(n, 1), 0), fill(c->sp_off.begin(), c->sp_off.end() - 1);
-    for (int i = 0; i < n; ++i) perm[fill[species[i]]++] = i;
-    c->sp_perm.ensure(perm.size());
-    HIPCHK(hipMemcpy(c->sp_perm.p, perm.data(), perm.size() * sizeof(int), hipMemcpyHostToDevice));
+    set_species_order(c);
     if (topo_changed || c->edges_manual) {  // a manual edge list lasts until the next set_system
       c->nl_valid = false;
       c->edges_manual = false;

@@ -71,3 +71,32 @@ def test_species_change_at_same_size():
         results.append(got)
     assert results[3]["E"] == results[0]["E"]
     assert np.array_equal(results[3]["F"], results[0]["F"])
+
+
+def test_model_reload_keeps_or_drops_the_system():
+    """Loading another model keeps the system when its species are elements of the new model
+    (the species order is rebuilt for the new element count: the step equals a fresh engine's)
+    and drops it otherwise (the step raises until mace_set_system is called again)."""
+    cfg10 = arch_config("medium", num_elements=10, z_table=Z10, zbl=True, trained_topology=True)
+    a, b = Case(cfg10, seed=67), Case(cfg10, seed=68)
+    s = rattle(diamond_si((2, 2, 2)), 0.05, 69)
+    s.numbers = _ragged_numbers(len(s), 70)
+    a.run(s)
+    a.eng.load_model(b.dm)                       # same elements: the system stays
+    E, ne, F, _ = a.eng.step(s.positions)
+    want = b.run(s)
+    assert abs(E - want["E"]) <= 1e-7 * max(abs(want["E"]), len(s))
+    assert np.abs(F - want["F"]).max() <= 1e-5
+    cfg2 = arch_config("medium", num_elements=2, z_table=[6, 14], zbl=True)
+    c = Case(cfg2, seed=71)
+    a.eng.load_model(c.dm)                       # species 2..9 are not elements of this model
+    with pytest.raises(RuntimeError):
+        a.eng.step(s.positions)
+    s2 = s.copy()
+    s2.numbers = np.where(np.arange(len(s)) % 3 == 0, 6, 14)
+    sp = np.where(np.arange(len(s)) % 3 == 0, 0, 1).astype(np.int32)
+    a.eng.set_system(sp, s2.cell, s2.pbc, 0.5)
+    E2, _, F2, _ = a.eng.step(s2.positions)
+    want2 = c.run(s2)
+    assert abs(E2 - want2["E"]) <= 1e-7 * max(abs(want2["E"]), len(s))
+    assert np.abs(F2 - want2["F"]).max() <= 1e-5
