@@ -188,7 +188,8 @@ struct mace_ctx {
   int64_t E = 0;
   DBuf<int> sender, receiver, shifts, rowptr, rowptr_s, perm_s, pos_s;
   DBuf<int> nl_img, nl_bin, nl_bin_sorted, nl_atoms, nl_iota, nl_counts, nl_bin_count, nl_bin_start;
-  DBuf<double> nl_wpos;
+  DBuf<double> nl_wpos, nl_wpos_s;
+  DBuf<int> nl_img_s, nl_cpre;
   DBuf<int> e_tmp_i, e_tmp_j, e_tmp_s, e_perm, e_keys;
   DBuf<unsigned char> cub_tmp;
   // per-step edge buffers
@@ -964,13 +965,18 @@ NLParams nl_params(const double* cell_in, const uint8_t* pbc, const double* pos,
   for (int k = 0; k < 3; ++k) {
     p.origin[k] = origin[k];
     p.periodic[k] = pbc[k] ? 1 : 0;
+    // bins half a cutoff wide: a receiver's candidates are the atoms of (2r + 1)^3 = 125 bins
+    // (r = 2) instead of 27 cutoff-wide bins, i.e. about 0.58 of the volume
     const double d = plane_spacing(cell, k);
-    int nbin = (int)std::floor(d / cutoff);
+    int nbin = (int)std::floor(2.0 * d / cutoff);
     nbin = std::max(1, std::min(nbin, 256));
     p.nbin[k] = nbin;
     p.range[k] = (int)std::ceil(cutoff * nbin / d + 1e-9);
     if (!p.periodic[k]) p.range[k] = std::min(p.range[k], nbin);
   }
+  // the fill pass packs a cell index and the cell count into 16 bits each
+  if ((int64_t)(2 * p.range[0] + 1) * (2 * p.range[1] + 1) * (2 * p.range[2] + 1) >= 32768)
+    fail(MACE_ERR_INVALID, "cell too small for the cutoff (more than 32767 neighbour cells per atom)");
   p.cutoff2 = cutoff * cutoff;
   return p;
 }
@@ -992,6 +998,11 @@ void build_nl(mace_ctx* c, const double* pos_host) {
     bin_off[g + 1] = bin_off[g] + (int)nb;
   }
   const int nbins = bin_off[G];
+  // per receiver and neighbour cell, the edges of its row before that cell (count pass; the
+  // fill pass places each reverse edge with it): row stride = the largest cell count + 1
+  int cstride = 1;
+  for (int g = 0; g < G; ++g)
+    cstride = std::max(cstride, (2 * ps[g].range[0] + 1) * (2 * ps[g].range[1] + 1) * (2 * ps[g].range[2] + 1) + 1);
   c->nl_wpos.ensure(3 * (size_t)N);
   c->nl_pos_d.ensure(3 * (size_t)N);
   c->nl_img.ensure(3 * (size_t)N);
@@ -1006,17 +1017,21 @@ void build_nl(mace_ctx* c, const double* pos_host) {
                   c->nl_wpos.p, c->nl_img.p, c->nl_bin.p, c->nl_iota.p, c->nl_pos_d.p);
   // atoms sorted by bin (stable: within a bin by index), then each bin's first position
   cub_sort_pairs(c, c->nl_bin.p, c->nl_bin_sorted.p, c->nl_iota.p, c->nl_atoms.p, N, nbins);
-  launch_key_starts(c->stream, N, c->nl_bin_sorted.p, nbins, c->nl_bin_start.p);
+  c->nl_wpos_s.ensure(3 * (size_t)N);
+  c->nl_img_s.ensure(3 * (size_t)N);
+  launch_key_starts(c->stream, N, c->nl_bin_sorted.p, nbins, c->nl_bin_start.p, c->nl_atoms.p, c->nl_wpos.p,
+                    c->nl_img.p, c->nl_wpos_s.p, c->nl_img_s.p);
   c->nl_counts.ensure((size_t)N + 1);
   c->nl_missing.ensure(1);
+  c->nl_cpre.ensure(std::max<size_t>((size_t)N * cstride, 1));
   if (N == 0) {  // no count pass to clear the scan's last slot and the reverse-edge counter
     HIPCHK(hipMemsetAsync(c->nl_counts.p, 0, sizeof(int), c->stream));
     HIPCHK(hipMemsetAsync(c->nl_missing.p, 0, sizeof(int), c->stream));
   }
   for (int g = 0; g < G; ++g)
     launch_nl_count(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], ps[g], bin_off[g], c->nl_wpos.p,
-                    c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, c->nl_counts.p, c->nl_counts.p + N,
-                    c->nl_missing.p);
+                    c->nl_wpos_s.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, cstride, c->nl_cpre.p,
+                    c->nl_counts.p, c->nl_counts.p + N, c->nl_missing.p);
   cub_exclusive_sum(c, c->nl_counts.p, c->rowptr.p, (int64_t)N + 1);
   // the edge count sizes the per-edge arrays and the launches: read back (pinned memory: a copy
   // into pageable memory costs more than this whole wait)
@@ -1025,17 +1040,16 @@ void build_nl(mace_ctx* c, const double* pos_host) {
   HIPCHK(hipStreamSynchronize(c->stream));
   c->E = *c->e_pinned;
   ensure_edge_index(c, c->E);
+  // the fill pass also writes the sender-side CSR of the (symmetric) list without a sort: its
+  // row pointers are rowptr's (srow), perm_s = pos_s = the reverse of each edge; the count of
+  // edges without a reverse is read at the next synchronisation (check_nl_missing)
   for (int g = 0; g < G; ++g)
     launch_nl_fill(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], ps[g], bin_off[g], c->nl_wpos.p,
-                   c->nl_img.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, c->rowptr.p, c->sender.p,
-                   c->receiver.p, c->shifts.p);
-  // sender-side CSR of the (symmetric) list without a sort: its row pointers are rowptr's
-  // (srow), perm_s = pos_s = the reverse of each edge; the reverse-edge count is read at the
-  // next synchronisation (check_nl_missing)
+                   c->nl_wpos_s.p, c->nl_img.p, c->nl_img_s.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p,
+                   c->rowptr.p, cstride, c->nl_cpre.p, c->sender.p, c->receiver.p, c->shifts.p, c->perm_s.p,
+                   c->pos_s.p, c->nl_missing.p);
   c->srow_shared = true;
   c->nl_check_pending = true;
-  launch_nl_rev(c->stream, c->E, c->rowptr.p, c->sender.p, c->receiver.p, c->shifts.p, c->perm_s.p, c->pos_s.p,
-                c->nl_missing.p);
   ensure_edge_buffers(c, c->E);
   // positions at this build, for the host-side skin check of mace_step (unknown when the build
   // took device positions of a fully periodic system: the next mace_step then rebuilds)
@@ -1886,12 +1900,13 @@ static void free_all(mace_ctx* c) {
     b->release();
   c->zero_species.release();
   for (auto* b : {&c->species, &c->sp_perm, &c->sender, &c->receiver, &c->shifts, &c->rowptr, &c->rowptr_s, &c->perm_s, &c->pos_s,
-                  &c->nl_img, &c->nl_bin, &c->nl_bin_sorted, &c->nl_atoms, &c->nl_iota, &c->nl_counts,
+                  &c->nl_img, &c->nl_img_s, &c->nl_cpre, &c->nl_bin, &c->nl_bin_sorted, &c->nl_atoms, &c->nl_iota, &c->nl_counts,
                   &c->nl_bin_count, &c->nl_bin_start, &c->e_tmp_i, &c->e_tmp_j, &c->e_tmp_s, &c->e_perm,
                   &c->e_keys})
     b->release();
   c->pos.release();
   c->nl_wpos.release();
+  c->nl_wpos_s.release();
   c->vir_part.release();
   c->out.release();
   c->e_part.release();
@@ -2235,11 +2250,11 @@ int mace_step_device(mace_ctx* c, const double* d_positions, uint32_t flags, dou
     auto fwd = [&] { forward(c, d_positions, d_out, c->e_part.p); };
     auto bwd = [&] { backward(c, stress, d_out, c->e_part.p, c->vir_part.p); };
     if (rebuilt && graphs_active(c)) {
-      // eagerly on the fresh list; the next steps' graphs are captured while the GPU runs it
+      // eagerly on the fresh list (the build discarded the graphs).  The graphs are captured by
+      // the next step that replays them: this call returns without waiting, so that capture
+      // overlaps the GPU's work on this step, and a run of rebuilding steps captures none
       fwd();
       bwd();
-      capture_graph(c, c->g_fwd, d_positions, d_out, 0, fwd);
-      capture_graph(c, c->g_bwd, d_out, nullptr, stress, bwd);
     } else {
       run_captured(c, c->g_fwd, d_positions, d_out, 0, fwd);
       run_captured(c, c->g_bwd, d_out, nullptr, stress, bwd);

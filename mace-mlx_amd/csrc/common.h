@@ -127,10 +127,6 @@ void launch_edge_fwd(hipStream_t st, int64_t E, const double* pos, const int* se
                      const float* ag_cov, const FrontParams& p, const double* gcell, const int* gid,
                      EdgeGeom* geom, float* Y, float* ef, float* zbl_e, float* Mt, int mts, int nent,
                      float* cut);
-// sender-side CSR of a symmetric neighbour list without a sort: perm_s = pos_s = the reverse of
-// every edge (edges without one map to themselves and are counted in *missing)
-void launch_nl_rev(hipStream_t st, int64_t E, const int* rowptr, const int* sender, const int* receiver,
-                   const int* shifts, int* perm_s, int* pos_s, int* missing);
 // gcut (used when p.apply_cutoff == 0): dL/dcut[e]
 void launch_edge_bwd(hipStream_t st, int64_t E, const int* sender, const int* receiver, const int* species,
                      const float* bessel_w, const float* zbl_z, const float* zbl_cov, const float* ag_cov,
@@ -373,15 +369,23 @@ void launch_nl_bin(hipStream_t st, int i0, int n, const double* pos, const NLPar
                    double* wpos, int* img, int* bin, int* iota, double* pos_build);
 // *flag = 1 if some atom's squared displacement from pos_build exceeds thr2 (flag not cleared)
 void launch_max_disp(hipStream_t st, int n, const double* pos, const double* pos_build, double thr2, int* flag);
-// start[b] (b = 0 .. nbins) = first position of key b in the sorted keys[0 .. n)
-void launch_key_starts(hipStream_t st, int n, const int* keys, int nbins, int* start);
-// counts[j] for the structure's atoms; also sets *tail = 0 and *missing = 0
+// start[b] (b = 0 .. nbins) = first position of key b in the sorted keys[0 .. n); with wpos, also
+// wpos_s / img_s = the positions / images of atoms[0 .. n) (the atoms in key order)
+void launch_key_starts(hipStream_t st, int n, const int* keys, int nbins, int* start, const int* atoms = nullptr,
+                       const double* wpos = nullptr, const int* img = nullptr, double* wpos_s = nullptr,
+                       int* img_s = nullptr);
+// counts[j] for the structure's atoms and cpre[j][k] (row stride cstride) = the number of j's
+// edges before its k-th neighbour cell, k = 0 .. ncell; also sets *tail = 0 and *missing = 0
 void launch_nl_count(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
-                     const int* bin, const int* bin_start, const int* bin_atoms, int* counts, int* tail,
-                     int* missing);
+                     const double* wpos_s, const int* bin, const int* bin_start, const int* bin_atoms, int cstride,
+                     int* cpre, int* counts, int* tail, int* missing);
+// the edges of the structure's rows, and perm_s = pos_s = the reverse of every edge (the
+// sender-side CSR of the symmetric list; an edge without a reverse maps to itself and is counted
+// in *missing)
 void launch_nl_fill(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
-                    const int* img, const int* bin, const int* bin_start, const int* bin_atoms,
-                    const int* rowptr, int* sender, int* receiver, int* shifts);
+                    const double* wpos_s, const int* img, const int* img_s, const int* bin, const int* bin_start,
+                    const int* bin_atoms, const int* rowptr, int cstride, const int* cpre, int* sender,
+                    int* receiver, int* shifts, int* perm_s, int* pos_s, int* missing);
 void launch_fill_iota(hipStream_t st, int n, int* out);
 void launch_count_keys(hipStream_t st, int64_t E, const int* keys, int* counts);
 

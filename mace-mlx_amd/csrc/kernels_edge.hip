@@ -357,19 +357,43 @@ struct NLWaveScratch {
   int T[64][3];   // image shift of each cell
 };
 
+// wpos_s / img_s: the wrapped positions and images in bin order (entry s of bin_atoms), so that a
+// candidate's position is read at its slot, in parallel with its atom index.
+//
+// Reverse edges without a search.  A receiver's cells are visited in a fixed order k = 0 ..
+// ncell - 1 of their offsets o in [-r, r]^3, and negating the offset maps k to ncell - 1 - k.
+// If receiver j finds atom i through cell k (image T), then i finds j through cell
+// ncell - 1 - k (image -T, the bin of j), among the atoms of j's bin in slot order, and with the
+// same distance bit for bit.  The count pass therefore stores, per receiver and cell, the number
+// of edges of its row before that cell (cpre, row stride cstride >= ncell + 1), and the fill
+// pass places the reverse of each edge it writes at rowptr[i] + cpre[i][ncell - 1 - k] + the
+// number of atoms of j's bin before j that i also reaches through that cell (usually none or
+// one: bins are half a cutoff wide).  perm_s = pos_s = that position (the reverse map is an
+// involution).  A position outside that cell's range means the list is not symmetric: the edge
+// maps to itself and is counted in *missing.
 template <bool FILL>
 __device__ __forceinline__ int nl_visit(int j, const NLParams& p, int bin_off, const double* __restrict__ wpos,
-                                        const int* __restrict__ img, const int* __restrict__ bin,
-                                        const int* __restrict__ bin_start,
-                                        const int* __restrict__ bin_atoms, int out0,
+                                        const double* __restrict__ wpos_s, const int* __restrict__ img,
+                                        const int* __restrict__ img_s, const int* __restrict__ bin,
+                                        const int* __restrict__ bin_start, const int* __restrict__ bin_atoms,
+                                        const int* __restrict__ rowptr, int cstride, int* __restrict__ cpre,
                                         int* __restrict__ sender, int* __restrict__ receiver,
-                                        int* __restrict__ shifts, NLWaveScratch& sc) {
+                                        int* __restrict__ shifts, int* __restrict__ perm_s,
+                                        int* __restrict__ pos_s, int* __restrict__ missing, NLWaveScratch& sc) {
   const int lane = __lane_id();
   const int bj = bin[j] - bin_off;
   const int b2 = bj % p.nbin[2], b1 = (bj / p.nbin[2]) % p.nbin[1], b0 = bj / (p.nbin[2] * p.nbin[1]);
   const double xj = wpos[3 * j], yj = wpos[3 * j + 1], zj = wpos[3 * j + 2];
   const int n1 = 2 * p.range[1] + 1, n2 = 2 * p.range[2] + 1;
   const int ncell = (2 * p.range[0] + 1) * n1 * n2;
+  // fill pass: the slots of j's own bin before j (wave-uniform: every lane scans the same few)
+  int jb0 = 0, jslot = 0, out0 = 0;
+  if constexpr (FILL) {
+    out0 = rowptr[j];
+    jb0 = bin_start[bin[j]];
+    const int jb1 = bin_start[bin[j] + 1];
+    for (jslot = jb0; jslot < jb1 && bin_atoms[jslot] != j;) ++jslot;  // j is in its bin
+  }
   int cnt = 0;
   for (int k0 = 0; k0 < ncell; k0 += 64) {
     // lane k: cell k0 + k (size 0 when past the end or outside a non-periodic direction)
@@ -407,19 +431,24 @@ __device__ __forceinline__ int nl_visit(int j, const NLParams& p, int bin_off, c
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     const int total = __shfl(incl, 63);
+    const int cnt0 = cnt;
+    int ccnt = 0;  // count pass: hits in this lane's cell
     for (int t0 = 0; t0 < total; t0 += 64) {
       const int t = t0 + lane;
       bool hit = false;
-      int i = 0, Tc[3] = {0, 0, 0};
+      int i = 0, lo = 0, slot = 0, Tc[3] = {0, 0, 0};
+      double xi = 0.0, yi = 0.0, zi = 0.0;
       if (t < total) {
-        int lo = 0, hi = 63;  // first cell whose inclusive end exceeds t
+        int hi = 63;  // first cell whose inclusive end exceeds t
         while (lo < hi) {
           const int mid = (lo + hi) >> 1;
           if (sc.end[mid] > t) hi = mid;
           else lo = mid + 1;
         }
         const int before = lo > 0 ? sc.end[lo - 1] : 0;
-        i = bin_atoms[sc.start[lo] + (t - before)];
+        slot = sc.start[lo] + (t - before);
+        i = bin_atoms[slot];
+        xi = wpos_s[3 * slot], yi = wpos_s[3 * slot + 1], zi = wpos_s[3 * slot + 2];
         Tc[0] = sc.T[lo][0], Tc[1] = sc.T[lo][1], Tc[2] = sc.T[lo][2];
         if (!(i == j && Tc[0] == 0 && Tc[1] == 0 && Tc[2] == 0)) {
           const double tx = Tc[0] * p.cell[0] + Tc[1] * p.cell[3] + Tc[2] * p.cell[6];
@@ -427,27 +456,66 @@ __device__ __forceinline__ int nl_visit(int j, const NLParams& p, int bin_off, c
           const double tz = Tc[0] * p.cell[2] + Tc[1] * p.cell[5] + Tc[2] * p.cell[8];
           // image of atom i at wpos_i + T.cell; D = (x_j - x_i) - T.cell, rounded so that the
           // reverse pair (i, j, -T) gets exactly -D: the list is symmetric bit for bit
-          const double dx = (xj - wpos[3 * i]) - tx, dy = (yj - wpos[3 * i + 1]) - ty,
-                       dz = (zj - wpos[3 * i + 2]) - tz;
+          const double dx = (xj - xi) - tx, dy = (yj - yi) - ty, dz = (zj - zi) - tz;
           hit = dx * dx + dy * dy + dz * dz < p.cutoff2;
         }
       }
       const unsigned long long m = __ballot(hit);
+      if constexpr (!FILL) {  // this lane's cell covers candidates [incl - size, incl)
+        const int a = max(incl - size - t0, 0), b = min(incl - t0, 64);
+        if (b > a) {
+          const unsigned long long hm = b == 64 ? ~0ull : (1ull << b) - 1ull;
+          ccnt += __popcll(m & hm & ~((1ull << a) - 1ull));
+        }
+      }
       if (FILL && hit) {
         const int o = out0 + cnt + __popcll(m & ((1ull << lane) - 1ull));
         sender[o] = i;
         receiver[o] = j;
         // D = x_j - x_i + S.cell with x = wpos + img.cell  =>  S = -T - img_j + img_i
-        shifts[3 * o + 0] = -Tc[0] - img[3 * j + 0] + img[3 * i + 0];
-        shifts[3 * o + 1] = -Tc[1] - img[3 * j + 1] + img[3 * i + 1];
-        shifts[3 * o + 2] = -Tc[2] - img[3 * j + 2] + img[3 * i + 2];
+        shifts[3 * o + 0] = -Tc[0] - img[3 * j + 0] + img_s[3 * slot + 0];
+        shifts[3 * o + 1] = -Tc[1] - img[3 * j + 1] + img_s[3 * slot + 1];
+        shifts[3 * o + 2] = -Tc[2] - img[3 * j + 2] + img_s[3 * slot + 2];
+        // the reverse (j -> i, -S): row i, cell kr, after the atoms of j's bin before j that i
+        // reaches through it (i's visit: receiver i, candidate a, image -Tc, same expression)
+        const int kr = ncell - 1 - (k0 + lo);
+        const int R0 = -Tc[0], R1 = -Tc[1], R2 = -Tc[2];
+        const double rx = R0 * p.cell[0] + R1 * p.cell[3] + R2 * p.cell[6];
+        const double ry = R0 * p.cell[1] + R1 * p.cell[4] + R2 * p.cell[7];
+        const double rz = R0 * p.cell[2] + R1 * p.cell[5] + R2 * p.cell[8];
+        int rank = 0;
+        for (int s2 = jb0; s2 < jslot; ++s2) {
+          if (bin_atoms[s2] == i && R0 == 0 && R1 == 0 && R2 == 0) continue;
+          const double dx = (xi - wpos_s[3 * s2]) - rx, dy = (yi - wpos_s[3 * s2 + 1]) - ry,
+                       dz = (zi - wpos_s[3 * s2 + 2]) - rz;
+          rank += dx * dx + dy * dy + dz * dz < p.cutoff2 ? 1 : 0;
+        }
+        const int* ci = cpre + (int64_t)i * cstride + kr;
+        const int ri = rowptr[i];
+        int rv = ri + ci[0] + rank;
+        if (rv >= ri + ci[1]) {
+          atomicAdd(missing, 1);
+          rv = o;
+        }
+        perm_s[o] = rv;
+        pos_s[o] = rv;
       }
       cnt += __popcll(m);
+    }
+    if constexpr (!FILL) {  // cpre[j][k0 + lane] = edges of the row before this cell
+      int ex = ccnt;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(ex, off);
+        if (lane >= off) ex += v;
+      }
+      if (k < ncell) cpre[(int64_t)j * cstride + k] = cnt0 + ex - ccnt;
     }
     // the scratch is rewritten by the next chunk only after every lane is done with it
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     __builtin_amdgcn_wave_barrier();
   }
+  if (!FILL && lane == 0) cpre[(int64_t)j * cstride + ncell] = cnt;
   return cnt;
 }
 
@@ -455,69 +523,35 @@ __device__ __forceinline__ int nl_visit(int j, const NLParams& p, int bin_off, c
 // also clears *tail (the count slot past the last atom, so that the exclusive scan ends on the
 // total) and *missing (the reverse-edge check's counter)
 __global__ void __launch_bounds__(256) k_nl_count(int i0, int n, NLParams p, int bin_off,
-                                                  const double* __restrict__ wpos,
+                                                  const double* __restrict__ wpos, const double* __restrict__ wpos_s,
                                                   const int* __restrict__ bin, const int* __restrict__ bin_start,
-                                                  const int* __restrict__ bin_atoms, int* __restrict__ counts,
+                                                  const int* __restrict__ bin_atoms, int cstride,
+                                                  int* __restrict__ cpre, int* __restrict__ counts,
                                                   int* __restrict__ tail, int* __restrict__ missing) {
   __shared__ NLWaveScratch sc[4];
   if (blockIdx.x == 0 && threadIdx.x == 0) *tail = 0, *missing = 0;
   if ((int)(blockIdx.x * 4 + (threadIdx.x >> 6)) >= n) return;
   const int j = i0 + blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int c = nl_visit<false>(j, p, bin_off, wpos, nullptr, bin, bin_start, bin_atoms, 0, nullptr, nullptr,
-                                nullptr, sc[threadIdx.x >> 6]);
+  const int c = nl_visit<false>(j, p, bin_off, wpos, wpos_s, nullptr, nullptr, bin, bin_start, bin_atoms, nullptr,
+                                cstride, cpre, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                sc[threadIdx.x >> 6]);
   if (__lane_id() == 0) counts[j] = c;
 }
 
 __global__ void __launch_bounds__(256) k_nl_fill(int i0, int n, NLParams p, int bin_off,
-                                                 const double* __restrict__ wpos,
-                                                 const int* __restrict__ img, const int* __restrict__ bin,
-                                                 const int* __restrict__ bin_start,
+                                                 const double* __restrict__ wpos, const double* __restrict__ wpos_s,
+                                                 const int* __restrict__ img, const int* __restrict__ img_s,
+                                                 const int* __restrict__ bin, const int* __restrict__ bin_start,
                                                  const int* __restrict__ bin_atoms, const int* __restrict__ rowptr,
-                                                 int* __restrict__ sender, int* __restrict__ receiver,
-                                                 int* __restrict__ shifts) {
+                                                 int cstride, const int* __restrict__ cpre, int* __restrict__ sender,
+                                                 int* __restrict__ receiver, int* __restrict__ shifts,
+                                                 int* __restrict__ perm_s, int* __restrict__ pos_s,
+                                                 int* __restrict__ missing) {
   __shared__ NLWaveScratch sc[4];
   if ((int)(blockIdx.x * 4 + (threadIdx.x >> 6)) >= n) return;
   const int j = i0 + blockIdx.x * 4 + (threadIdx.x >> 6);
-  nl_visit<true>(j, p, bin_off, wpos, img, bin, bin_start, bin_atoms, rowptr[j], sender, receiver, shifts,
-                 sc[threadIdx.x >> 6]);
-}
-
-// The reverse of every edge of a symmetric list: for e = (i -> j, S) in receiver j's row, the
-// edge (j -> i, -S) in receiver i's row (a search of that row).  rev is an involution, so it is
-// both the sender-side permutation (edges sent by a = reverses of the edges a receives, in the
-// order of a's row) and its inverse.  An edge without a reverse (a list that is not symmetric)
-// maps to itself and is counted in *missing.
-// Sixteen lanes per edge: lane k of the group compares entries k, k + 16, ... of the row (all
-// loads independent, a few per lane), and the group takes the smallest matching position.
-constexpr int kRevLanes = 16;
-__global__ void __launch_bounds__(256) k_nl_rev(int64_t E, const int* __restrict__ rowptr,
-                                                const int* __restrict__ sender, const int* __restrict__ receiver,
-                                                const int* __restrict__ shifts, int* __restrict__ perm_s,
-                                                int* __restrict__ pos_s, int* __restrict__ missing) {
-  const int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kRevLanes;
-  const int k = threadIdx.x % kRevLanes;
-  const bool live = e < E;  // a group's lanes share e (256 is a multiple of the group size)
-  int j = 0, s0 = 0, s1 = 0, s2 = 0, beg = 0, end = 0;
-  if (live) {
-    const int i = sender[e];
-    j = receiver[e];
-    s0 = -shifts[3 * e], s1 = -shifts[3 * e + 1], s2 = -shifts[3 * e + 2];
-    beg = rowptr[i], end = rowptr[i + 1];
-  }
-  int found = INT_MAX;
-  for (int f = beg + k; f < end; f += kRevLanes)
-    if (sender[f] == j && shifts[3 * f] == s0 && shifts[3 * f + 1] == s1 && shifts[3 * f + 2] == s2)
-      found = min(found, f);
-#pragma unroll
-  for (int off = kRevLanes / 2; off > 0; off >>= 1) found = min(found, __shfl_xor(found, off, kRevLanes));
-  if (live && k == 0) {
-    if (found == INT_MAX) {
-      atomicAdd(missing, 1);
-      found = (int)e;
-    }
-    perm_s[e] = found;
-    pos_s[e] = found;
-  }
+  nl_visit<true>(j, p, bin_off, wpos, wpos_s, img, img_s, bin, bin_start, bin_atoms, rowptr, cstride,
+                 const_cast<int*>(cpre), sender, receiver, shifts, perm_s, pos_s, missing, sc[threadIdx.x >> 6]);
 }
 
 // *flag = 1 when some atom moved by more than sqrt(thr2) since pos_build (every writer stores
@@ -536,8 +570,16 @@ __global__ void k_max_disp(int n, const double* __restrict__ pos, const double* 
 
 // start[b] = first position of key b in the sorted keys[0 .. n) (b = 0 .. nbins): the CSR of a
 // sorted key array by binary search, with no counts to clear or scan
-__global__ void k_key_starts(int n, const int* __restrict__ keys, int nbins, int* __restrict__ start) {
+// The neighbour-list build also gathers the wrapped positions and images in bin order (slot r
+// of the sorted atoms), when wpos is given.
+__global__ void k_key_starts(int n, const int* __restrict__ keys, int nbins, int* __restrict__ start,
+                             const int* __restrict__ atoms, const double* __restrict__ wpos,
+                             const int* __restrict__ img, double* __restrict__ wpos_s, int* __restrict__ img_s) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (wpos && b < n) {
+    const int a = atoms[b];
+    for (int k = 0; k < 3; ++k) wpos_s[3 * b + k] = wpos[3 * a + k], img_s[3 * b + k] = img[3 * a + k];
+  }
   if (b > nbins) return;
   int lo = 0, hi = n;
   while (lo < hi) {
@@ -615,24 +657,28 @@ void launch_max_disp(hipStream_t st, int n, const double* pos, const double* pos
   MACE_LAUNCH(k_max_disp, dim3(nblk(n, 256)), dim3(256), 0, st, n, pos, pos_build, thr2, flag);
 }
 
-void launch_key_starts(hipStream_t st, int n, const int* keys, int nbins, int* start) {
-  MACE_LAUNCH(k_key_starts, dim3(nblk((int64_t)nbins + 1, 256)), dim3(256), 0, st, n, keys, nbins, start);
+void launch_key_starts(hipStream_t st, int n, const int* keys, int nbins, int* start, const int* atoms,
+                       const double* wpos, const int* img, double* wpos_s, int* img_s) {
+  const int64_t m = std::max<int64_t>((int64_t)nbins + 1, wpos ? n : 0);
+  MACE_LAUNCH(k_key_starts, dim3(nblk(m, 256)), dim3(256), 0, st, n, keys, nbins, start, atoms, wpos, img, wpos_s,
+              img_s);
 }
 
 void launch_nl_count(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
-                     const int* bin, const int* bin_start, const int* bin_atoms, int* counts, int* tail,
-                     int* missing) {
+                     const double* wpos_s, const int* bin, const int* bin_start, const int* bin_atoms, int cstride,
+                     int* cpre, int* counts, int* tail, int* missing) {
   if (n <= 0) return;
-  MACE_LAUNCH(k_nl_count, dim3(nblk(n, 4)), dim3(256), 0, st, i0, n, p, bin_off, wpos, bin, bin_start,
-                     bin_atoms, counts, tail, missing);
+  MACE_LAUNCH(k_nl_count, dim3(nblk(n, 4)), dim3(256), 0, st, i0, n, p, bin_off, wpos, wpos_s, bin, bin_start,
+                     bin_atoms, cstride, cpre, counts, tail, missing);
 }
 
 void launch_nl_fill(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
-                    const int* img, const int* bin, const int* bin_start, const int* bin_atoms, const int* rowptr,
-                    int* sender, int* receiver, int* shifts) {
+                    const double* wpos_s, const int* img, const int* img_s, const int* bin, const int* bin_start,
+                    const int* bin_atoms, const int* rowptr, int cstride, const int* cpre, int* sender,
+                    int* receiver, int* shifts, int* perm_s, int* pos_s, int* missing) {
   if (n <= 0) return;
-  MACE_LAUNCH(k_nl_fill, dim3(nblk(n, 4)), dim3(256), 0, st, i0, n, p, bin_off, wpos, img, bin, bin_start,
-                     bin_atoms, rowptr, sender, receiver, shifts);
+  MACE_LAUNCH(k_nl_fill, dim3(nblk(n, 4)), dim3(256), 0, st, i0, n, p, bin_off, wpos, wpos_s, img, img_s, bin,
+                     bin_start, bin_atoms, rowptr, cstride, cpre, sender, receiver, shifts, perm_s, pos_s, missing);
 }
 
 void launch_fill_iota(hipStream_t st, int n, int* out) {
@@ -645,11 +691,5 @@ void launch_count_keys(hipStream_t st, int64_t E, const int* keys, int* counts) 
   MACE_LAUNCH(k_count_keys, dim3(nblk(E, 256)), dim3(256), 0, st, E, keys, counts);
 }
 
-void launch_nl_rev(hipStream_t st, int64_t E, const int* rowptr, const int* sender, const int* receiver,
-                   const int* shifts, int* perm_s, int* pos_s, int* missing) {
-  if (E <= 0) return;
-  MACE_LAUNCH(k_nl_rev, dim3(nblk(E * kRevLanes, 256)), dim3(256), 0, st, E, rowptr, sender, receiver, shifts,
-              perm_s, pos_s, missing);
-}
 
 }  // namespace mace
