@@ -1473,13 +1473,9 @@ void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int fi
                          NC * lo * lo, 0);
     run_gemm(c, st, g);
   }
-  {
+  {  // gP = dL/d(Q + R) and dL/drho
     Site s(c, lname("gate_bwd", l));
-    launch_mh1_gate_bwd(st, N, Ly.Q.p, Ly.R.p, Ly.nres, c->gA2.p, c->gP.p);
-  }
-  {
-    Site s(c, lname("density_bwd", l));
-    launch_mh1_drho(st, N, c->gP.p, Ly.Q.p, Ly.rinv.p, Ly.beta, c->grho.p);
+    launch_mh1_gate_bwd(st, N, Ly.Q.p, Ly.R.p, Ly.nres, c->gA2.p, c->gP.p, Ly.rinv.p, Ly.beta, c->grho.p);
   }
   {  // gM = Lin1^T gP / (beta rho + alpha)
     Site s(c, lname("linear_msg_bwd", l));

@@ -231,10 +231,9 @@ constexpr int kGateInDim = 19 * NC;
 void launch_mh1_rho(hipStream_t st, int N, const int* rowptr, const float* dens, float alpha, float beta,
                     float* rinv);
 void launch_mh1_gate(hipStream_t st, int N, const float* Q, const float* R, int nres, float* gout, int half);
+// also drho[n] = dL/drho_n = -beta rinv[n] sum_j gP[n][j] Q[n][j]
 void launch_mh1_gate_bwd(hipStream_t st, int N, const float* Q, const float* R, int nres, const float* gG,
-                         float* gP);
-void launch_mh1_drho(hipStream_t st, int N, const float* gP, const float* Q, const float* rinv, float beta,
-                     float* drho);
+                         float* gP, const float* rinv, float beta, float* drho);
 
 // float16 feature policy: gw fp16 with per-(edge, channel half) scales, W3 fp16 [64][W]
 void launch_mlp_gh3_h(hipStream_t st, int64_t E, int W, const void* gw, const float* gscale, const void* W3h,

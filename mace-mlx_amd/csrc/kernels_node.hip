@@ -648,9 +648,14 @@ __global__ void __launch_bounds__(NC) k_mh1_gate(int N, const float* __restrict_
   }
 }
 
-// VJP: gP = dL/d(Q + R) from gG = dL/dgout
+// VJP: gP = dL/d(Q + R) from gG = dL/dgout, and dL/drho[n] = -beta rinv[n] sum_j gP[n][j] Q[n][j]
+// (Q = linear_1(M) rinv): thread u holds columns j = u + k C (k = 0 .. 18), the block sums its
+// waves' partial sums in wave order
 __global__ void __launch_bounds__(NC) k_mh1_gate_bwd(int N, const float* __restrict__ Q, const float* __restrict__ R,
-                                                     int nres, const float* __restrict__ gG, float* __restrict__ gP) {
+                                                     int nres, const float* __restrict__ gG, float* __restrict__ gP,
+                                                     const float* __restrict__ rinv, float beta,
+                                                     float* __restrict__ drho) {
+  __shared__ float part[NC / 64];
   const int n = blockIdx.x, u = threadIdx.x;
   const float* q = Q + (int64_t)n * kGateInDim;
   const float* rr = R + (int64_t)n * nres;
@@ -658,7 +663,9 @@ __global__ void __launch_bounds__(NC) k_mh1_gate_bwd(int N, const float* __restr
   float* gp = gP + (int64_t)n * kGateInDim;
   const float s = gate_in(q, rr, nres, u);
   const float sg = sigm(s);
-  gp[u] = go[u] * kSiluNorm * sg * (1.f + s * (1.f - sg));
+  const float g0 = go[u] * kSiluNorm * sg * (1.f + s * (1.f - sg));
+  gp[u] = g0;
+  float pd = g0 * q[u];
 #pragma unroll
   for (int l = 1; l <= 3; ++l) {
     const float gs = sigm(gate_in(q, rr, nres, l * NC + u));
@@ -667,23 +674,23 @@ __global__ void __launch_bounds__(NC) k_mh1_gate_bwd(int N, const float* __restr
     for (int m = 0; m < 2 * l + 1; ++m) {
       const float gm = go[ob + m * NC + u];
       dgt = fmaf(gm, gate_in(q, rr, nres, qb + m * NC + u), dgt);
-      gp[qb + m * NC + u] = kSigmoidNorm * gs * gm;
+      const float gv = kSigmoidNorm * gs * gm;
+      gp[qb + m * NC + u] = gv;
+      pd = fmaf(gv, q[qb + m * NC + u], pd);
     }
-    gp[l * NC + u] = dgt * kSigmoidNorm * gs * (1.f - gs);
+    const float gl = dgt * kSigmoidNorm * gs * (1.f - gs);
+    gp[l * NC + u] = gl;
+    pd = fmaf(gl, q[l * NC + u], pd);
   }
-}
-
-// dL/drho[n] = -beta rinv[n] sum_j gP[n][j] Q[n][j]   (Q = linear_1(M) rinv)
-__global__ void __launch_bounds__(256) k_mh1_drho(int N, const float* __restrict__ gP, const float* __restrict__ Q,
-                                                  const float* __restrict__ rinv, float beta, float* __restrict__ drho) {
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6), l = threadIdx.x & 63;
-  if (n >= N) return;
-  const float* g = gP + (int64_t)n * kGateInDim;
-  const float* q = Q + (int64_t)n * kGateInDim;
-  float acc = 0.f;
-  for (int j = l; j < kGateInDim; j += 64) acc = fmaf(g[j], q[j], acc);
-  acc = wave_sum(acc);
-  if (l == 0) drho[n] = -beta * rinv[n] * acc;
+  pd = wave_sum(pd);
+  if ((u & 63) == 0) part[u >> 6] = pd;
+  __syncthreads();
+  if (u == 0) {
+    float t = part[0];
+#pragma unroll
+    for (int w = 1; w < NC / 64; ++w) t += part[w];
+    drho[n] = -beta * rinv[n] * t;
+  }
 }
 
 }  // namespace
@@ -828,15 +835,9 @@ void launch_mh1_gate(hipStream_t st, int N, const float* Q, const float* R, int 
 }
 
 void launch_mh1_gate_bwd(hipStream_t st, int N, const float* Q, const float* R, int nres, const float* gG,
-                         float* gP) {
+                         float* gP, const float* rinv, float beta, float* drho) {
   if (N <= 0) return;
-  MACE_LAUNCH(k_mh1_gate_bwd, dim3(N), dim3(NC), 0, st, N, Q, R, nres, gG, gP);
-}
-
-void launch_mh1_drho(hipStream_t st, int N, const float* gP, const float* Q, const float* rinv, float beta,
-                     float* drho) {
-  if (N <= 0) return;
-  MACE_LAUNCH(k_mh1_drho, dim3((N + 3) / 4), dim3(256), 0, st, N, gP, Q, rinv, beta, drho);
+  MACE_LAUNCH(k_mh1_gate_bwd, dim3(N), dim3(NC), 0, st, N, Q, R, nres, gG, gP, rinv, beta, drho);
 }
 
 }  // namespace mace
