@@ -1380,21 +1380,15 @@ void forward_nonlin(mace_ctx* c, int l, const float* h, float* hn) {
     Site s(c, lname("density", l));
     launch_mh1_rho(st, N, c->rowptr.p, c->mh_dens.p, L.alpha, L.beta, L.rinv.p);
   }
-  {
-    Site s(c, lname("linear_res", l));
+  {  // Q = linear_1(M) / (beta rho + alpha), and in the same launch R = linear_res(up)
+    Site s(c, lname("linear_msg", l));
+    const int* ao = tp_accoff(L.ledge);
     GemmGroup g{};
     for (int lo = 0; lo < L.ledge; ++lo) {
       const int d = 2 * lo + 1;
       g.p[g.n++] = gprob(N, d, NC, lo == 0 ? 4 * NC : NC, L.h_up.p, L.dedge, NC * lo * lo, 0, L.resT[lo].p, L.R.p,
                          L.nres, gate_in_base(lo), NC * d);
     }
-    g.round_half = half;
-    run_gemm(c, st, g);
-  }
-  {  // Q = linear_1(M) / (beta rho + alpha)
-    Site s(c, lname("linear_msg", l));
-    const int* ao = tp_accoff(L.ledge);
-    GemmGroup g{};
     for (int lo = 0; lo < 4; ++lo) {
       int first, cnt;
       slot_range(L, lo, &first, &cnt);
@@ -1477,10 +1471,16 @@ void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int fi
     Site s(c, lname("gate_bwd", l));
     launch_mh1_gate_bwd(st, N, Ly.Q.p, Ly.R.p, Ly.nres, c->gA2.p, c->gP.p, Ly.rinv.p, Ly.beta, c->grho.p);
   }
-  {  // gM = Lin1^T gP / (beta rho + alpha)
+  {  // gM = Lin1^T gP / (beta rho + alpha), and for l > 0 in the same launch gup = Res^T gP (the
+     // gather of the TP's dL/dx rows adds to it)
     Site s(c, lname("linear_msg_bwd", l));
     const int* ao = tp_accoff(Ly.ledge);
     GemmGroup g{};
+    for (int lo = 0; l > 0 && lo < Ly.ledge; ++lo) {
+      const int d = 2 * lo + 1;
+      g.p[g.n++] = gprob(N, d, lo == 0 ? 4 * NC : NC, NC, c->gP.p, kGateInDim, gate_in_base(lo), NC * d,
+                         Ly.res_[lo].p, c->gup.p, Ly.dedge, NC * lo * lo, 0);
+    }
     for (int lo = 0; lo < 4; ++lo) {
       int first, cnt;
       slot_range(Ly, lo, &first, &cnt);
@@ -1510,7 +1510,8 @@ void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int fi
   }
   if (l > 0) {
     Site s(c, lname("tp_gather", l));
-    launch_tp_gather_gx(st, Ly.ledge, N, srow(c), c->gxe.p, c->gup.p, fused && c->dims.feature_half == RND_F16);
+    launch_tp_gather_gx(st, Ly.ledge, N, srow(c), c->gxe.p, c->gup.p, fused && c->dims.feature_half == RND_F16,
+                        1);
   }
   if (!fused) {  // G = gw W3^T (into h3), gwb = gw . b3
     Site s(c, lname("mlp_gh3", l));
@@ -1530,17 +1531,6 @@ void backward_nonlin(mace_ctx* c, int l, const float* gh, float* gh_next, int fi
                        cut ? c->gcut.p : nullptr, first_edge_grad);
   }
   if (l == 0) return;
-  {  // gup += Res^T gP
-    Site s(c, lname("linear_res_bwd", l));
-    GemmGroup g{};
-    for (int lo = 0; lo < Ly.ledge; ++lo) {
-      const int d = 2 * lo + 1;
-      g.p[g.n++] = gprob(N, d, lo == 0 ? 4 * NC : NC, NC, c->gP.p, kGateInDim, gate_in_base(lo), NC * d,
-                         Ly.res_[lo].p, c->gup.p, Ly.dedge, NC * lo * lo, 0);
-      g.p[g.n - 1].accumulate = 1;
-    }
-    run_gemm(c, st, g);
-  }
   {  // dE/dh_l = Up^T gup + Skip^T gh + readout_{l-1}' (bias on the 0e block)
     Site s(c, lname("linear_up_bwd", l));
     if (Ly.lin > std::max(Ly.ledge, Ly.nskip)) launch_fill_zero(st, gh_next, (int64_t)N * Ly.din);
@@ -1779,7 +1769,7 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
     }
     if (l > 0) {
       Site s(c, lname("tp_gather", l));
-      launch_tp_gather_gx(st, Ly.lin, N, srow(c), c->gxe.p, c->gup.p, fused && half == RND_F16);
+      launch_tp_gather_gx(st, Ly.lin, N, srow(c), c->gxe.p, c->gup.p, fused && half == RND_F16, 0);
     }
     if (!fused) {
       Site s(c, lname("mlp_gh3", l));

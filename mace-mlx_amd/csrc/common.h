@@ -287,9 +287,10 @@ void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
                     float* gh3p, int wfmt, const float* b3, float* gwbp);
 // p[0 .. n) = 0 (a kernel, not a memset: safe inside captured graphs)
 void launch_fill_zero(hipStream_t st, float* p, int64_t n);
-// gx16: the rows hold fp16 values (launch_tpx_bwd under the float16 policy), else floats
+// gx16: the rows hold fp16 values (launch_tpx_bwd under the float16 policy), else floats;
+// accumulate: gup += the sums (else gup = the sums)
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe,
-                         float* gup, int gx16);
+                         float* gup, int gx16, int accumulate);
 
 // Grouped fp32-MFMA GEMM over node rows: up to GEMM_MAX problems in one launch.
 // Each problem: Y[row, c] (+)= sum_k X1[row, k] WT1[c][k] + sum_k X2[row, k] WT2[c][k] + bias[c]

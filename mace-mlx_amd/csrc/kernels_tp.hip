@@ -524,12 +524,13 @@ __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __rest
   }
 }
 
-// gup[a][row][u] = sum over the edges sent by a (a contiguous segment of the
-// sender-ordered gxe rows, summed in order, fp32); grid (N, LIN^2), NC threads.
+// gup[a][row][u] (= or +=, accumulate) the sum over the edges sent by a (a contiguous segment of
+// the sender-ordered gxe rows, summed in order, fp32); grid (N, LIN^2), NC threads.
 // GT: the rows' element type (fp16 under the float16 policy's fused VJP).
 template <typename GT>
 __global__ void __launch_bounds__(NC) k_tp_gather_gx(int N, int din, const int* __restrict__ rowptr_s,
-                                                     const GT* __restrict__ gxe, float* __restrict__ gup) {
+                                                     const GT* __restrict__ gxe, float* __restrict__ gup,
+                                                     int accumulate) {
   const int a = blockIdx.x, row = blockIdx.y, u = threadIdx.x;
   const int beg = rowptr_s[a], end = rowptr_s[a + 1];
   const GT* src = gxe + (int64_t)row * NC + u;
@@ -542,7 +543,8 @@ __global__ void __launch_bounds__(NC) k_tp_gather_gx(int N, int din, const int* 
     s3 += (float)src[(int64_t)(k + 3) * din];
   }
   for (; k < end; ++k) s0 += (float)src[(int64_t)k * din];
-  gup[(int64_t)a * din + row * NC + u] = (s0 + s1) + (s2 + s3);
+  float* o = gup + (int64_t)a * din + row * NC + u;
+  *o = accumulate ? *o + ((s0 + s1) + (s2 + s3)) : (s0 + s1) + (s2 + s3);
 }
 
 // ---------------------------------------------------------------------------
@@ -1734,13 +1736,14 @@ void launch_fill_zero(hipStream_t st, float* p, int64_t n) {
 }
 
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe, float* gup,
-                         int gx16) {
+                         int gx16, int accumulate) {
   if (N <= 0) return;
   if (gx16)
     MACE_LAUNCH(k_tp_gather_gx<_Float16>, dim3(N, lin * lin), dim3(NC), 0, st, N, NC * lin * lin, rowptr_s,
-                reinterpret_cast<const _Float16*>(gxe), gup);
+                reinterpret_cast<const _Float16*>(gxe), gup, accumulate);
   else
-    MACE_LAUNCH(k_tp_gather_gx<float>, dim3(N, lin * lin), dim3(NC), 0, st, N, NC * lin * lin, rowptr_s, gxe, gup);
+    MACE_LAUNCH(k_tp_gather_gx<float>, dim3(N, lin * lin), dim3(NC), 0, st, N, NC * lin * lin, rowptr_s, gxe, gup,
+                accumulate);
 }
 
 }  // namespace mace
