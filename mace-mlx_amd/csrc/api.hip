@@ -189,7 +189,10 @@ struct mace_ctx {
   DBuf<int> sender, receiver, shifts, rowptr, rowptr_s, perm_s, pos_s;
   DBuf<int> nl_img, nl_bin, nl_bin_sorted, nl_atoms, nl_iota, nl_counts, nl_bin_count, nl_bin_start;
   DBuf<double> nl_wpos, nl_wpos_s;
-  DBuf<int> nl_img_s, nl_cpre;
+  DBuf<int> nl_img_s, nl_cpre, nl_hits;
+  // hits recorded per receiver by the count pass (rows up to this long are written from them):
+  // 1.5 x the last build's mean row, at least 128
+  int nl_hcap = 128;
   DBuf<int> e_tmp_i, e_tmp_j, e_tmp_s, e_perm, e_keys;
   DBuf<unsigned char> cub_tmp;
   // per-step edge buffers
@@ -1024,6 +1027,8 @@ void build_nl(mace_ctx* c, const double* pos_host) {
   c->nl_counts.ensure((size_t)N + 1);
   c->nl_missing.ensure(1);
   c->nl_cpre.ensure(std::max<size_t>((size_t)N * cstride, 1));
+  const int hcap = c->nl_hcap;
+  c->nl_hits.ensure(std::max<size_t>(2 * (size_t)N * hcap, 2));
   if (N == 0) {  // no count pass to clear the scan's last slot and the reverse-edge counter
     HIPCHK(hipMemsetAsync(c->nl_counts.p, 0, sizeof(int), c->stream));
     HIPCHK(hipMemsetAsync(c->nl_missing.p, 0, sizeof(int), c->stream));
@@ -1031,7 +1036,7 @@ void build_nl(mace_ctx* c, const double* pos_host) {
   for (int g = 0; g < G; ++g)
     launch_nl_count(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], ps[g], bin_off[g], c->nl_wpos.p,
                     c->nl_wpos_s.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, cstride, c->nl_cpre.p,
-                    c->nl_counts.p, c->nl_counts.p + N, c->nl_missing.p);
+                    c->nl_hits.p, hcap, c->nl_counts.p, c->nl_counts.p + N, c->nl_missing.p);
   cub_exclusive_sum(c, c->nl_counts.p, c->rowptr.p, (int64_t)N + 1);
   // the edge count sizes the per-edge arrays and the launches: read back (pinned memory: a copy
   // into pageable memory costs more than this whole wait)
@@ -1046,8 +1051,9 @@ void build_nl(mace_ctx* c, const double* pos_host) {
   for (int g = 0; g < G; ++g)
     launch_nl_fill(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], ps[g], bin_off[g], c->nl_wpos.p,
                    c->nl_wpos_s.p, c->nl_img.p, c->nl_img_s.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p,
-                   c->rowptr.p, cstride, c->nl_cpre.p, c->sender.p, c->receiver.p, c->shifts.p, c->perm_s.p,
-                   c->pos_s.p, c->nl_missing.p);
+                   c->rowptr.p, cstride, c->nl_cpre.p, c->nl_hits.p, hcap, c->sender.p, c->receiver.p,
+                   c->shifts.p, c->perm_s.p, c->pos_s.p, c->nl_missing.p);
+  if (N > 0) c->nl_hcap = std::max(128, (int)((3 * c->E / N) / 2 + 1));
   c->srow_shared = true;
   c->nl_check_pending = true;
   ensure_edge_buffers(c, c->E);
@@ -1886,7 +1892,7 @@ static void free_all(mace_ctx* c) {
     b->release();
   c->zero_species.release();
   for (auto* b : {&c->species, &c->sp_perm, &c->sender, &c->receiver, &c->shifts, &c->rowptr, &c->rowptr_s, &c->perm_s, &c->pos_s,
-                  &c->nl_img, &c->nl_img_s, &c->nl_cpre, &c->nl_bin, &c->nl_bin_sorted, &c->nl_atoms, &c->nl_iota, &c->nl_counts,
+                  &c->nl_img, &c->nl_img_s, &c->nl_cpre, &c->nl_hits, &c->nl_bin, &c->nl_bin_sorted, &c->nl_atoms, &c->nl_iota, &c->nl_counts,
                   &c->nl_bin_count, &c->nl_bin_start, &c->e_tmp_i, &c->e_tmp_j, &c->e_tmp_s, &c->e_perm,
                   &c->e_keys})
     b->release();

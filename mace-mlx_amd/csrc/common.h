@@ -375,17 +375,18 @@ void launch_key_starts(hipStream_t st, int n, const int* keys, int nbins, int* s
                        const double* wpos = nullptr, const int* img = nullptr, double* wpos_s = nullptr,
                        int* img_s = nullptr);
 // counts[j] for the structure's atoms and cpre[j][k] (row stride cstride) = the number of j's
-// edges before its k-th neighbour cell, k = 0 .. ncell; also sets *tail = 0 and *missing = 0
+// edges before its k-th neighbour cell, k = 0 .. ncell; hits[j] (hcap int pairs per atom): j's
+// first hcap edges as (candidate slot, cell index); also sets *tail = 0 and *missing = 0
 void launch_nl_count(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
                      const double* wpos_s, const int* bin, const int* bin_start, const int* bin_atoms, int cstride,
-                     int* cpre, int* counts, int* tail, int* missing);
+                     int* cpre, int* hits, int hcap, int* counts, int* tail, int* missing);
 // the edges of the structure's rows, and perm_s = pos_s = the reverse of every edge (the
 // sender-side CSR of the symmetric list; an edge without a reverse maps to itself and is counted
-// in *missing)
+// in *missing); rows of no more than hcap edges are written from the count pass's hits
 void launch_nl_fill(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
                     const double* wpos_s, const int* img, const int* img_s, const int* bin, const int* bin_start,
-                    const int* bin_atoms, const int* rowptr, int cstride, const int* cpre, int* sender,
-                    int* receiver, int* shifts, int* perm_s, int* pos_s, int* missing);
+                    const int* bin_atoms, const int* rowptr, int cstride, const int* cpre, const int* hits, int hcap,
+                    int* sender, int* receiver, int* shifts, int* perm_s, int* pos_s, int* missing);
 void launch_fill_iota(hipStream_t st, int n, int* out);
 void launch_count_keys(hipStream_t st, int64_t E, const int* keys, int* counts);
 

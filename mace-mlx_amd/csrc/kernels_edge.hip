@@ -371,28 +371,101 @@ struct NLWaveScratch {
 // one: bins are half a cutoff wide).  perm_s = pos_s = that position (the reverse map is an
 // involution).  A position outside that cell's range means the list is not symmetric: the edge
 // maps to itself and is counted in *missing.
+// What the fill pass writes for one edge e = (i -> j) of row j at position o: sender, receiver,
+// shift, and the position of its reverse (perm_s = pos_s).  slot: i's slot in bin order; k and
+// T: the cell of the receiver's visit that holds that image of i.
+struct NLFillCtx {
+  int j, jb0, jslot, ncell, cstride;
+  double xj, yj, zj;
+};
+__device__ __forceinline__ void nl_emit(const NLParams& p, const NLFillCtx& f, int o, int i, int slot, int k,
+                                        const int* Tc, const double* __restrict__ wpos_s,
+                                        const int* __restrict__ img, const int* __restrict__ img_s,
+                                        const int* __restrict__ bin_atoms, const int* __restrict__ rowptr,
+                                        const int* __restrict__ cpre, int* __restrict__ sender,
+                                        int* __restrict__ receiver, int* __restrict__ shifts,
+                                        int* __restrict__ perm_s, int* __restrict__ pos_s,
+                                        int* __restrict__ missing) {
+  const int j = f.j;
+  sender[o] = i;
+  receiver[o] = j;
+  // D = x_j - x_i + S.cell with x = wpos + img.cell  =>  S = -T - img_j + img_i
+  shifts[3 * o + 0] = -Tc[0] - img[3 * j + 0] + img_s[3 * slot + 0];
+  shifts[3 * o + 1] = -Tc[1] - img[3 * j + 1] + img_s[3 * slot + 1];
+  shifts[3 * o + 2] = -Tc[2] - img[3 * j + 2] + img_s[3 * slot + 2];
+  // the reverse (j -> i, -S): row i, cell kr, after the atoms of j's bin before j that i
+  // reaches through it (i's visit: receiver i, candidate a, image -Tc, same expression)
+  const int kr = f.ncell - 1 - k;
+  const int R0 = -Tc[0], R1 = -Tc[1], R2 = -Tc[2];
+  const double rx = R0 * p.cell[0] + R1 * p.cell[3] + R2 * p.cell[6];
+  const double ry = R0 * p.cell[1] + R1 * p.cell[4] + R2 * p.cell[7];
+  const double rz = R0 * p.cell[2] + R1 * p.cell[5] + R2 * p.cell[8];
+  const double xi = wpos_s[3 * slot], yi = wpos_s[3 * slot + 1], zi = wpos_s[3 * slot + 2];
+  int rank = 0;
+  for (int s2 = f.jb0; s2 < f.jslot; ++s2) {
+    if (bin_atoms[s2] == i && R0 == 0 && R1 == 0 && R2 == 0) continue;
+    const double dx = (xi - wpos_s[3 * s2]) - rx, dy = (yi - wpos_s[3 * s2 + 1]) - ry,
+                 dz = (zi - wpos_s[3 * s2 + 2]) - rz;
+    rank += dx * dx + dy * dy + dz * dz < p.cutoff2 ? 1 : 0;
+  }
+  const int* ci = cpre + (int64_t)i * f.cstride + kr;
+  const int ri = rowptr[i];
+  int rv = ri + ci[0] + rank;
+  if (rv >= ri + ci[1]) {
+    atomicAdd(missing, 1);
+    rv = o;
+  }
+  perm_s[o] = rv;
+  pos_s[o] = rv;
+}
+
+// The receiver j's bin coordinates (b0, b1, b2 within its structure's bins) and the image shift
+// of its candidate cell k (offset o in [-r, r]^3, k = o0 outer, o2 inner); false when the cell
+// lies outside a non-periodic direction
+__device__ __forceinline__ bool nl_cell(const NLParams& p, int b0, int b1, int b2, int k, int* T, int* c) {
+  const int n1 = 2 * p.range[1] + 1, n2 = 2 * p.range[2] + 1;
+  const int o[3] = {k / (n1 * n2) - p.range[0], (k / n2) % n1 - p.range[1], k % n2 - p.range[2]};
+  const int bb[3] = {b0, b1, b2};
+  bool ok = true;
+  for (int d = 0; d < 3; ++d) {
+    c[d] = bb[d] + o[d];
+    T[d] = 0;
+    if (p.periodic[d]) {
+      T[d] = floordiv(c[d], p.nbin[d]);
+      c[d] -= T[d] * p.nbin[d];
+    } else if (c[d] < 0 || c[d] >= p.nbin[d]) {
+      ok = false;
+    }
+  }
+  return ok;
+}
+
+// The count pass also records each hit of receiver j, in row order, as (slot, cell index) in
+// hits[j][0 .. hcap): the fill pass then writes the rows from those lists without testing any
+// distance again (a receiver with more than hcap hits is visited again in full).
 template <bool FILL>
 __device__ __forceinline__ int nl_visit(int j, const NLParams& p, int bin_off, const double* __restrict__ wpos,
                                         const double* __restrict__ wpos_s, const int* __restrict__ img,
                                         const int* __restrict__ img_s, const int* __restrict__ bin,
                                         const int* __restrict__ bin_start, const int* __restrict__ bin_atoms,
                                         const int* __restrict__ rowptr, int cstride, int* __restrict__ cpre,
-                                        int* __restrict__ sender, int* __restrict__ receiver,
-                                        int* __restrict__ shifts, int* __restrict__ perm_s,
-                                        int* __restrict__ pos_s, int* __restrict__ missing, NLWaveScratch& sc) {
+                                        int2* __restrict__ hits, int hcap, int* __restrict__ sender,
+                                        int* __restrict__ receiver, int* __restrict__ shifts,
+                                        int* __restrict__ perm_s, int* __restrict__ pos_s,
+                                        int* __restrict__ missing, NLWaveScratch& sc) {
   const int lane = __lane_id();
   const int bj = bin[j] - bin_off;
   const int b2 = bj % p.nbin[2], b1 = (bj / p.nbin[2]) % p.nbin[1], b0 = bj / (p.nbin[2] * p.nbin[1]);
   const double xj = wpos[3 * j], yj = wpos[3 * j + 1], zj = wpos[3 * j + 2];
-  const int n1 = 2 * p.range[1] + 1, n2 = 2 * p.range[2] + 1;
-  const int ncell = (2 * p.range[0] + 1) * n1 * n2;
+  const int ncell = (2 * p.range[0] + 1) * (2 * p.range[1] + 1) * (2 * p.range[2] + 1);
   // fill pass: the slots of j's own bin before j (wave-uniform: every lane scans the same few)
-  int jb0 = 0, jslot = 0, out0 = 0;
+  NLFillCtx f{j, 0, 0, ncell, cstride, xj, yj, zj};
+  int out0 = 0;
   if constexpr (FILL) {
     out0 = rowptr[j];
-    jb0 = bin_start[bin[j]];
+    f.jb0 = bin_start[bin[j]];
     const int jb1 = bin_start[bin[j] + 1];
-    for (jslot = jb0; jslot < jb1 && bin_atoms[jslot] != j;) ++jslot;  // j is in its bin
+    for (f.jslot = f.jb0; f.jslot < jb1 && bin_atoms[f.jslot] != j;) ++f.jslot;  // j is in its bin
   }
   int cnt = 0;
   for (int k0 = 0; k0 < ncell; k0 += 64) {
@@ -400,20 +473,8 @@ __device__ __forceinline__ int nl_visit(int j, const NLParams& p, int bin_off, c
     int size = 0, first = 0, T[3] = {0, 0, 0};
     const int k = k0 + lane;
     if (k < ncell) {
-      const int o[3] = {k / (n1 * n2) - p.range[0], (k / n2) % n1 - p.range[1], k % n2 - p.range[2]};
-      const int bb[3] = {b0, b1, b2};
       int c[3];
-      bool ok = true;
-      for (int d = 0; d < 3; ++d) {
-        c[d] = bb[d] + o[d];
-        if (p.periodic[d]) {
-          T[d] = floordiv(c[d], p.nbin[d]);
-          c[d] -= T[d] * p.nbin[d];
-        } else if (c[d] < 0 || c[d] >= p.nbin[d]) {
-          ok = false;
-        }
-      }
-      if (ok) {
+      if (nl_cell(p, b0, b1, b2, k, T, c)) {
         const int cb = bin_off + (c[0] * p.nbin[1] + c[1]) * p.nbin[2] + c[2];
         first = bin_start[cb];
         size = bin_start[cb + 1] - first;
@@ -437,7 +498,6 @@ __device__ __forceinline__ int nl_visit(int j, const NLParams& p, int bin_off, c
       const int t = t0 + lane;
       bool hit = false;
       int i = 0, lo = 0, slot = 0, Tc[3] = {0, 0, 0};
-      double xi = 0.0, yi = 0.0, zi = 0.0;
       if (t < total) {
         int hi = 63;  // first cell whose inclusive end exceeds t
         while (lo < hi) {
@@ -448,7 +508,7 @@ __device__ __forceinline__ int nl_visit(int j, const NLParams& p, int bin_off, c
         const int before = lo > 0 ? sc.end[lo - 1] : 0;
         slot = sc.start[lo] + (t - before);
         i = bin_atoms[slot];
-        xi = wpos_s[3 * slot], yi = wpos_s[3 * slot + 1], zi = wpos_s[3 * slot + 2];
+        const double xi = wpos_s[3 * slot], yi = wpos_s[3 * slot + 1], zi = wpos_s[3 * slot + 2];
         Tc[0] = sc.T[lo][0], Tc[1] = sc.T[lo][1], Tc[2] = sc.T[lo][2];
         if (!(i == j && Tc[0] == 0 && Tc[1] == 0 && Tc[2] == 0)) {
           const double tx = Tc[0] * p.cell[0] + Tc[1] * p.cell[3] + Tc[2] * p.cell[6];
@@ -461,45 +521,18 @@ __device__ __forceinline__ int nl_visit(int j, const NLParams& p, int bin_off, c
         }
       }
       const unsigned long long m = __ballot(hit);
+      const int rank = cnt + __popcll(m & ((1ull << lane) - 1ull));  // the hit's place in the row
       if constexpr (!FILL) {  // this lane's cell covers candidates [incl - size, incl)
         const int a = max(incl - size - t0, 0), b = min(incl - t0, 64);
         if (b > a) {
           const unsigned long long hm = b == 64 ? ~0ull : (1ull << b) - 1ull;
           ccnt += __popcll(m & hm & ~((1ull << a) - 1ull));
         }
+        if (hit && rank < hcap) hits[(int64_t)j * hcap + rank] = make_int2(slot, k0 + lo);
       }
-      if (FILL && hit) {
-        const int o = out0 + cnt + __popcll(m & ((1ull << lane) - 1ull));
-        sender[o] = i;
-        receiver[o] = j;
-        // D = x_j - x_i + S.cell with x = wpos + img.cell  =>  S = -T - img_j + img_i
-        shifts[3 * o + 0] = -Tc[0] - img[3 * j + 0] + img_s[3 * slot + 0];
-        shifts[3 * o + 1] = -Tc[1] - img[3 * j + 1] + img_s[3 * slot + 1];
-        shifts[3 * o + 2] = -Tc[2] - img[3 * j + 2] + img_s[3 * slot + 2];
-        // the reverse (j -> i, -S): row i, cell kr, after the atoms of j's bin before j that i
-        // reaches through it (i's visit: receiver i, candidate a, image -Tc, same expression)
-        const int kr = ncell - 1 - (k0 + lo);
-        const int R0 = -Tc[0], R1 = -Tc[1], R2 = -Tc[2];
-        const double rx = R0 * p.cell[0] + R1 * p.cell[3] + R2 * p.cell[6];
-        const double ry = R0 * p.cell[1] + R1 * p.cell[4] + R2 * p.cell[7];
-        const double rz = R0 * p.cell[2] + R1 * p.cell[5] + R2 * p.cell[8];
-        int rank = 0;
-        for (int s2 = jb0; s2 < jslot; ++s2) {
-          if (bin_atoms[s2] == i && R0 == 0 && R1 == 0 && R2 == 0) continue;
-          const double dx = (xi - wpos_s[3 * s2]) - rx, dy = (yi - wpos_s[3 * s2 + 1]) - ry,
-                       dz = (zi - wpos_s[3 * s2 + 2]) - rz;
-          rank += dx * dx + dy * dy + dz * dz < p.cutoff2 ? 1 : 0;
-        }
-        const int* ci = cpre + (int64_t)i * cstride + kr;
-        const int ri = rowptr[i];
-        int rv = ri + ci[0] + rank;
-        if (rv >= ri + ci[1]) {
-          atomicAdd(missing, 1);
-          rv = o;
-        }
-        perm_s[o] = rv;
-        pos_s[o] = rv;
-      }
+      if (FILL && hit)
+        nl_emit(p, f, out0 + rank, i, slot, k0 + lo, Tc, wpos_s, img, img_s, bin_atoms, rowptr, cpre, sender,
+                receiver, shifts, perm_s, pos_s, missing);
       cnt += __popcll(m);
     }
     if constexpr (!FILL) {  // cpre[j][k0 + lane] = edges of the row before this cell
@@ -526,32 +559,56 @@ __global__ void __launch_bounds__(256) k_nl_count(int i0, int n, NLParams p, int
                                                   const double* __restrict__ wpos, const double* __restrict__ wpos_s,
                                                   const int* __restrict__ bin, const int* __restrict__ bin_start,
                                                   const int* __restrict__ bin_atoms, int cstride,
-                                                  int* __restrict__ cpre, int* __restrict__ counts,
-                                                  int* __restrict__ tail, int* __restrict__ missing) {
+                                                  int* __restrict__ cpre, int2* __restrict__ hits, int hcap,
+                                                  int* __restrict__ counts, int* __restrict__ tail,
+                                                  int* __restrict__ missing) {
   __shared__ NLWaveScratch sc[4];
   if (blockIdx.x == 0 && threadIdx.x == 0) *tail = 0, *missing = 0;
   if ((int)(blockIdx.x * 4 + (threadIdx.x >> 6)) >= n) return;
   const int j = i0 + blockIdx.x * 4 + (threadIdx.x >> 6);
   const int c = nl_visit<false>(j, p, bin_off, wpos, wpos_s, nullptr, nullptr, bin, bin_start, bin_atoms, nullptr,
-                                cstride, cpre, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                cstride, cpre, hits, hcap, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                                 sc[threadIdx.x >> 6]);
   if (__lane_id() == 0) counts[j] = c;
 }
 
+// A receiver whose hits the count pass recorded (no more than hcap) writes its row from them:
+// lane t takes hits t, t + 64, ... (slot and cell index; the cell's image shift follows from the
+// index); others are visited again in full.
 __global__ void __launch_bounds__(256) k_nl_fill(int i0, int n, NLParams p, int bin_off,
                                                  const double* __restrict__ wpos, const double* __restrict__ wpos_s,
                                                  const int* __restrict__ img, const int* __restrict__ img_s,
                                                  const int* __restrict__ bin, const int* __restrict__ bin_start,
                                                  const int* __restrict__ bin_atoms, const int* __restrict__ rowptr,
-                                                 int cstride, const int* __restrict__ cpre, int* __restrict__ sender,
+                                                 int cstride, const int* __restrict__ cpre,
+                                                 const int2* __restrict__ hits, int hcap, int* __restrict__ sender,
                                                  int* __restrict__ receiver, int* __restrict__ shifts,
                                                  int* __restrict__ perm_s, int* __restrict__ pos_s,
                                                  int* __restrict__ missing) {
   __shared__ NLWaveScratch sc[4];
   if ((int)(blockIdx.x * 4 + (threadIdx.x >> 6)) >= n) return;
   const int j = i0 + blockIdx.x * 4 + (threadIdx.x >> 6);
-  nl_visit<true>(j, p, bin_off, wpos, wpos_s, img, img_s, bin, bin_start, bin_atoms, rowptr, cstride,
-                 const_cast<int*>(cpre), sender, receiver, shifts, perm_s, pos_s, missing, sc[threadIdx.x >> 6]);
+  const int out0 = rowptr[j], cnt = rowptr[j + 1] - out0;
+  if (cnt > hcap) {
+    nl_visit<true>(j, p, bin_off, wpos, wpos_s, img, img_s, bin, bin_start, bin_atoms, rowptr, cstride,
+                   const_cast<int*>(cpre), nullptr, 0, sender, receiver, shifts, perm_s, pos_s, missing,
+                   sc[threadIdx.x >> 6]);
+    return;
+  }
+  const int bj = bin[j] - bin_off;
+  const int b2 = bj % p.nbin[2], b1 = (bj / p.nbin[2]) % p.nbin[1], b0 = bj / (p.nbin[2] * p.nbin[1]);
+  NLFillCtx f{j, bin_start[bin[j]], 0, (2 * p.range[0] + 1) * (2 * p.range[1] + 1) * (2 * p.range[2] + 1),
+              cstride, wpos[3 * j], wpos[3 * j + 1], wpos[3 * j + 2]};
+  const int jb1 = bin_start[bin[j] + 1];
+  for (f.jslot = f.jb0; f.jslot < jb1 && bin_atoms[f.jslot] != j;) ++f.jslot;  // j is in its bin
+  const int2* hj = hits + (int64_t)j * hcap;
+  for (int t = __lane_id(); t < cnt; t += 64) {
+    const int2 h = hj[t];
+    int T[3], c[3];
+    nl_cell(p, b0, b1, b2, h.y, T, c);
+    nl_emit(p, f, out0 + t, bin_atoms[h.x], h.x, h.y, T, wpos_s, img, img_s, bin_atoms, rowptr, cpre, sender,
+            receiver, shifts, perm_s, pos_s, missing);
+  }
 }
 
 // *flag = 1 when some atom moved by more than sqrt(thr2) since pos_build (every writer stores
@@ -666,19 +723,20 @@ void launch_key_starts(hipStream_t st, int n, const int* keys, int nbins, int* s
 
 void launch_nl_count(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
                      const double* wpos_s, const int* bin, const int* bin_start, const int* bin_atoms, int cstride,
-                     int* cpre, int* counts, int* tail, int* missing) {
+                     int* cpre, int* hits, int hcap, int* counts, int* tail, int* missing) {
   if (n <= 0) return;
   MACE_LAUNCH(k_nl_count, dim3(nblk(n, 4)), dim3(256), 0, st, i0, n, p, bin_off, wpos, wpos_s, bin, bin_start,
-                     bin_atoms, cstride, cpre, counts, tail, missing);
+                     bin_atoms, cstride, cpre, reinterpret_cast<int2*>(hits), hcap, counts, tail, missing);
 }
 
 void launch_nl_fill(hipStream_t st, int i0, int n, const NLParams& p, int bin_off, const double* wpos,
                     const double* wpos_s, const int* img, const int* img_s, const int* bin, const int* bin_start,
-                    const int* bin_atoms, const int* rowptr, int cstride, const int* cpre, int* sender,
-                    int* receiver, int* shifts, int* perm_s, int* pos_s, int* missing) {
+                    const int* bin_atoms, const int* rowptr, int cstride, const int* cpre, const int* hits, int hcap,
+                    int* sender, int* receiver, int* shifts, int* perm_s, int* pos_s, int* missing) {
   if (n <= 0) return;
   MACE_LAUNCH(k_nl_fill, dim3(nblk(n, 4)), dim3(256), 0, st, i0, n, p, bin_off, wpos, wpos_s, img, img_s, bin,
-                     bin_start, bin_atoms, rowptr, cstride, cpre, sender, receiver, shifts, perm_s, pos_s, missing);
+                     bin_start, bin_atoms, rowptr, cstride, cpre, reinterpret_cast<const int2*>(hits), hcap, sender,
+                     receiver, shifts, perm_s, pos_s, missing);
 }
 
 void launch_fill_iota(hipStream_t st, int n, int* out) {

@@ -191,3 +191,21 @@ def test_mace_off_large_width_192():
     with pytest.raises(NotImplementedError):
         case.run(per)
     case.eng.set_fused_tp(True)
+
+
+def test_dense_rows_longer_than_recorded_hits():
+    """A compressed diamond lattice (a = 3.6 A, about 190 neighbours per atom within r_max +
+    skin): the count pass records at most 128 hits per receiver on the first build, so every row
+    is written by a second full visit; the next build records them all (its capacity follows the
+    first build's mean row) and writes the rows from the recorded hits.  Both builds give the
+    brute-force edge set and oracle parity (the sender-side CSR comes from the same pass)."""
+    case = Case(arch_config("small"), seed=27)
+    s = rattle(diamond_si((2, 2, 2), a=3.6), 0.02, 28)
+    for k in range(2):
+        got = case.run(s, force_nl=True)
+        edges = case.edges()
+        n_e = len(edges[0])
+        print(f"dense build {k}: {n_e} edges, {n_e / len(s):.1f} per atom", flush=True)
+        assert n_e / len(s) > 128
+        assert edge_set(*edges) == bruteforce_edges(s)
+        assert_parity(got, case.reference(s, got["sp"], edges), len(s))
