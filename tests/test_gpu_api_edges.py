@@ -99,12 +99,13 @@ def test_overlapping_atoms_zero_length_edge():
 
 def test_skin_zero_rebuilds_every_step():
     """skin = 0: every step rebuilds the list (`calculators.py:278-279`), also when no atom moved,
-    and each step matches the oracle on its freshly built list."""
+    and each step matches the oracle on its freshly built list (five builds on the same cell and
+    buffers, each against the brute-force list)."""
     case = Case(arch_config("small"), seed=25)
     s = rattle(diamond_si((2, 2, 2)), 0.03, 26)
     sp = np.zeros(len(s), dtype=np.int32)
     case.eng.set_system(sp, s.cell, s.pbc, 0.0)
-    for k in range(3):
+    for k in range(5):
         pos = s.positions + 0.004 * k
         E, ne, F, _ = case.eng.step(pos)
         assert case.eng.timings()[1] > 0, f"step {k} did not rebuild the neighbour list"
