@@ -4,6 +4,7 @@
 #include <hipcub/hipcub.hpp>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -191,7 +192,7 @@ struct mace_ctx {
   DBuf<double> nl_wpos, nl_wpos_s;
   DBuf<int> nl_img_s, nl_cpre, nl_hits;
   // hits recorded per receiver by the count pass (rows up to this long are written from them):
-  // 1.5 x the last build's mean row, at least 128
+  // 1.5 x the last build's mean row, at least 128 and at most 1024
   int nl_hcap = 128;
   DBuf<int> e_tmp_i, e_tmp_j, e_tmp_s, e_perm, e_keys;
   DBuf<unsigned char> cub_tmp;
@@ -1041,9 +1042,19 @@ void build_nl(mace_ctx* c, const double* pos_host) {
   // the edge count sizes the per-edge arrays and the launches: read back (pinned memory: a copy
   // into pageable memory costs more than this whole wait)
   if (!c->e_pinned) HIPCHK(hipHostMalloc((void**)&c->e_pinned, sizeof(int), hipHostMallocDefault));
+  // The copy lands after the scan (stream order): poll the pinned word, which returns sooner
+  // than a blocking synchronisation (the GPU idles until the fill is launched); synchronise
+  // instead if it has not landed within 0.2 s
+  volatile int* ep = c->e_pinned;
+  *ep = -1;
   HIPCHK(hipMemcpyAsync(c->e_pinned, c->rowptr.p + N, sizeof(int), hipMemcpyDeviceToHost, c->stream));
-  HIPCHK(hipStreamSynchronize(c->stream));
-  c->E = *c->e_pinned;
+  const auto t0 = std::chrono::steady_clock::now();
+  while (*ep < 0)
+    if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(200)) {
+      HIPCHK(hipStreamSynchronize(c->stream));
+      break;
+    }
+  c->E = *ep;
   ensure_edge_index(c, c->E);
   // the fill pass also writes the sender-side CSR of the (symmetric) list without a sort: its
   // row pointers are rowptr's (srow), perm_s = pos_s = the reverse of each edge; the count of
@@ -1053,7 +1064,7 @@ void build_nl(mace_ctx* c, const double* pos_host) {
                    c->nl_wpos_s.p, c->nl_img.p, c->nl_img_s.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p,
                    c->rowptr.p, cstride, c->nl_cpre.p, c->nl_hits.p, hcap, c->sender.p, c->receiver.p,
                    c->shifts.p, c->perm_s.p, c->pos_s.p, c->nl_missing.p);
-  if (N > 0) c->nl_hcap = std::max(128, (int)((3 * c->E / N) / 2 + 1));
+  if (N > 0) c->nl_hcap = (int)std::min<int64_t>(1024, std::max<int64_t>(128, (3 * c->E / N) / 2 + 1));
   c->srow_shared = true;
   c->nl_check_pending = true;
   ensure_edge_buffers(c, c->E);
