@@ -1159,7 +1159,7 @@ void run_gemm(mace_ctx* c, hipStream_t st, GemmGroup& g) {
       GemmProb& P = g.p[q];
       auto a = c->wsplit.find(P.WT1);
       auto b = P.K2 > 0 ? c->wsplit.find(P.WT2) : a;
-      ok = a != c->wsplit.end() && b != c->wsplit.end() && P.Cout % 128 == 0 && P.K1 % 32 == 0 && P.K2 % 32 == 0;
+      ok = a != c->wsplit.end() && b != c->wsplit.end() && P.Cout % 64 == 0 && P.K1 % 32 == 0 && P.K2 % 32 == 0;
       if (!ok) break;
       P.WX1 = a->second.x.p;
       P.winv1 = a->second.winv;

@@ -804,9 +804,13 @@ void launch_gemm_group(hipStream_t st, GemmGroup& g) {
     return;
   }
   int row_tiles = 0;
-  for (int q = 0; q < g.n; ++q) row_tiles += (int)cdiv(g.p[q].rows, 16) * (g.p[q].Cout / 64);
-  const bool wide = row_tiles >= 1024;  // enough blocks even with four column tiles per wave
-  const int rows_per_block = wide ? 32 : 16, cols_per_block = wide ? 128 : 64;  // Cout is a multiple of 128
+  bool c128 = true;  // every problem's output width a multiple of 128 (not so at 192 channels)
+  for (int q = 0; q < g.n; ++q) {
+    row_tiles += (int)cdiv(g.p[q].rows, 16) * (g.p[q].Cout / 64);
+    c128 = c128 && g.p[q].Cout % 128 == 0;
+  }
+  const bool wide = c128 && row_tiles >= 1024;  // enough blocks even with four column tiles per wave
+  const int rows_per_block = wide ? 32 : 16, cols_per_block = wide ? 128 : 64;  // Cout: a multiple of 64
   int tiles = 0;
   for (int q = 0; q < g.n; ++q) {
     GemmProb& P = g.p[q];

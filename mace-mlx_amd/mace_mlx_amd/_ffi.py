@@ -18,8 +18,9 @@ import numpy as np
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libmace_hip.so"
 # the same engine compiled for each channel count (csrc/common.h MACE_NC); a model with C
 # channels runs on the smallest width >= C (device_model pads the rest with zeros)
-ENGINE_WIDTHS = (128, 256)
-LIB_PATHS = {128: LIB_PATH, 256: LIB_PATH.with_name("libmace_hip_c256.so")}
+ENGINE_WIDTHS = (128, 192, 256)
+LIB_PATHS = {128: LIB_PATH, 192: LIB_PATH.with_name("libmace_hip_c192.so"),
+             256: LIB_PATH.with_name("libmace_hip_c256.so")}
 
 MACE_OK = 0
 MACE_ERR_INVALID = -1

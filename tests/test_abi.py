@@ -20,7 +20,7 @@ def _declared():
 
 @pytest.mark.parametrize("channels", _ffi.ENGINE_WIDTHS)
 def test_library_loads_and_exports_every_declared_symbol(channels):
-    """Each channel width's library (libmace_hip.so, libmace_hip_c256.so)."""
+    """Each channel width's library (libmace_hip.so, libmace_hip_c192.so, libmace_hip_c256.so)."""
     lib = _ffi.load_library(channels=channels)
     declared = _declared()
     assert set(declared) == set(_ffi.EXPORTED_SYMBOLS)

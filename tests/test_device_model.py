@@ -291,12 +291,14 @@ def test_mh1_kernel_formulation_matches_oracle(apply_cutoff, agnostic, edge):
 
 
 @pytest.mark.parametrize("arch,C,width", [("small", 96, 128), ("medium", 96, 128), ("large", 64, 128),
-                                          ("small", 192, 256), ("large", 192, 256), ("medium", 256, 256)])
+                                          ("small", 192, 192), ("large", 192, 192), ("medium", 160, 192),
+                                          ("small", 224, 256), ("medium", 256, 256)])
 def test_model_padded_to_engine_width_in_the_fold(si64, arch, C, width):
-    """A model runs on the narrowest compiled engine width that holds its channels (128 or 256):
-    MACE-OFF small (96x0e) as its zero-padded 128-channel equivalent, MACE-OFF large (192x0e +
-    192x1o + 192x2e) as a 256-channel one.  The kernel formulation of the folded tensors
-    matches the oracle evaluating the original model."""
+    """A model runs on the narrowest compiled engine width that holds its channels (128, 192 or
+    256): MACE-OFF small (96x0e) as its zero-padded 128-channel equivalent, MACE-OFF large
+    (192x0e + 192x1o + 192x2e) natively at 192, 160 and 224 channels padded to 192 and 256.
+    The kernel formulation of the folded tensors matches the oracle evaluating the original
+    model."""
     s, i, j, S = si64
     cfg = arch_config(arch, zbl=True)
     cfg.hidden_irreps = "+".join(f"{C}x{b.ir}" for b in cfg.hidden)

@@ -164,15 +164,16 @@ def test_mace_off_calculator_from_cache(tmp_path, monkeypatch):
 
 def test_mace_off_large_width_192():
     """A MACE-OFF-large-shaped model (192x0e + 192x1o + 192x2e: three input blocks, the l1 = 2
-    CG paths) runs on the 256-channel engine (libmace_hip_c256.so) as its zero-padded
-    equivalent; E, F and stress against the float64 oracle evaluating the 192-channel model.
-    That engine runs the default path only: the comparison paths raise before any launch."""
+    CG paths) runs natively on the 192-channel engine (libmace_hip_c192.so: three 64-channel
+    slices, grouped products whose output widths are not multiples of 128); E, F and stress
+    against the float64 oracle.  That engine runs the default path only: the comparison paths
+    raise before any launch."""
     from mace_mlx_amd.systems import off_config, organic_cluster
     cfg = off_config("large")
     case = Case(cfg, seed=46)
-    assert case.dm.dims["num_channels"] == 256 and case.eng.channels == 256
+    assert case.dm.dims["num_channels"] == 192 and case.eng.channels == 192
     s = organic_cluster(40, 47)
-    print("192-channel model on the 256-channel engine: organic cluster", flush=True)
+    print("192-channel model on the 192-channel engine: organic cluster", flush=True)
     got = case.run(s)
     edges = case.edges()
     assert edge_set(*edges) == bruteforce_edges(s, cutoff=5.5)
@@ -181,7 +182,7 @@ def test_mace_off_large_width_192():
     per.positions *= 0.7
     per.cell *= 0.7
     per.numbers = np.full(len(per), 6)
-    print("192-channel model on the 256-channel engine: periodic carbon with stress", flush=True)
+    print("192-channel model on the 192-channel engine: periodic carbon with stress", flush=True)
     got = case.run(per, stress=True)
     assert_parity(got, case.reference(per, got["sp"], case.edges(), stress=True), len(per), stress=True)
     case.eng.set_split_products(False)
@@ -192,6 +193,22 @@ def test_mace_off_large_width_192():
     with pytest.raises(NotImplementedError):
         case.run(per)
     case.eng.set_fused_tp(True)
+
+
+def test_width_224_on_the_256_engine():
+    """A medium-shaped model with 224 channels runs on the 256-channel engine as its zero-padded
+    equivalent (model_io.pad_channels); E, F and stress against the float64 oracle evaluating the
+    224-channel model."""
+    cfg = arch_config("medium", zbl=True)
+    cfg.hidden_irreps = "224x0e+224x1o"
+    case = Case(cfg, seed=49)
+    assert case.dm.dims["num_channels"] == 256 and case.eng.channels == 256
+    s = rattle(diamond_si((2, 2, 2)), 0.04, 50)
+    print("224-channel model on the 256-channel engine: Si64 with stress", flush=True)
+    got = case.run(s, stress=True)
+    edges = case.edges()
+    assert edge_set(*edges) == bruteforce_edges(s)
+    assert_parity(got, case.reference(s, got["sp"], edges, stress=True), len(s), stress=True)
 
 
 def test_dense_rows_longer_than_recorded_hits():
