@@ -1291,7 +1291,9 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
 
   // W3 rows q = 16 qt + r, group k steps kh G .. kh G + G - 1 (32 columns each).  Under a
   // half-precision policy (WF) W3 holds rounded values: its lo plane is zero and the product
-  // lo.hi is skipped (it adds exact zeros); dL/dw stays float32, so hi.lo and hi.hi remain
+  // lo.hi is skipped (it adds exact zeros); dL/dw is carried as one fp16 value (scaled per edge),
+  // as the reference's half-precision gradients are, so hi.hi is the only product.  The float32
+  // policy splits both operands: lo.hi + hi.lo + hi.hi
   constexpr bool WLO = WF == RND_NONE;
   const int qt = wv & 3, kh = wv >> 2;
   h8 wa[G][WLO ? 2 : 1];
@@ -1442,7 +1444,7 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
             const float x = gws[s] * sc;
             const _Float16 hi = (_Float16)x;
             trow[64 * GR::local(s)] = hi;
-            trow[32 * RS + 64 * GR::local(s)] = (_Float16)(x - (float)hi);
+            if constexpr (WLO) trow[32 * RS + 64 * GR::local(s)] = (_Float16)(x - (float)hi);
           }
         if (l == 0) tinv[2 * wv + b] = __uint_as_float((unsigned)(127 - 14 + ex) << 23);
       }
@@ -1484,9 +1486,12 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const _Float16* src = pt + (16 * h + r) * RS + 32 * (kh * G + ks) + 8 * g;
-        const h8 xh = *reinterpret_cast<const h8*>(src), xl = *reinterpret_cast<const h8*>(src + 32 * RS);
-        if constexpr (WLO) acc[h] = mfma16h(wa[ks][WLO ? 1 : 0], xh, acc[h]);
-        acc[h] = mfma16h(wa[ks][0], xl, acc[h]);
+        const h8 xh = *reinterpret_cast<const h8*>(src);
+        if constexpr (WLO) {
+          const h8 xl = *reinterpret_cast<const h8*>(src + 32 * RS);
+          acc[h] = mfma16h(wa[ks][WLO ? 1 : 0], xh, acc[h]);
+          acc[h] = mfma16h(wa[ks][0], xl, acc[h]);
+        }
         acc[h] = mfma16h(wa[ks][0], xh, acc[h]);
       }
 #pragma unroll
