@@ -242,7 +242,7 @@ def layer_shapes(dm):
     return layers
 
 
-def _setup(idx, separate=False, graphs=None):
+def _setup(idx, separate=False, graphs=None, store_w=False):
     from mace_mlx_amd._ffi import Engine
     from mace_mlx_amd.device_model import build_device_model
     from mace_mlx_amd.model_io import random_init
@@ -254,6 +254,8 @@ def _setup(idx, separate=False, graphs=None):
     eng.load_model(dm)
     if separate:
         eng.set_fused_tp(False)
+    if store_w:
+        eng.set_rebuild_w(False)
     if graphs is not None:
         eng.set_graphs(graphs)
     zmap = {int(z): k for k, z in enumerate(dm.z_table)}
@@ -298,13 +300,13 @@ def calculator_ms(bc, weights, warmup=3, reps=10):
     return float(np.median(ts)) * 1e3, float(np.min(ts)) * 1e3, float(np.max(ts)) * 1e3
 
 
-def run_workload(idx, steps, warmup, separate=False, graphs=None, extras=False, launch_order=None):
+def run_workload(idx, steps, warmup, separate=False, graphs=None, extras=False, launch_order=None, store_w=False):
     """Measure one benchmark configuration: steady-state device-resident steps (neighbour
     list cached), steps that rebuild the neighbour list, and a per-launch-site pass with HIP
     events; with `extras` also the host-array path, the true-fp32 matrix-core variant and
     the CPU-baseline inputs."""
     import torch
-    bc, weights, dm, eng, species = _setup(idx, separate, graphs)
+    bc, weights, dm, eng, species = _setup(idx, separate, graphs, store_w)
     s = bc.system
     stress = "stress" in bc.properties
     E_host, _, F_host, _ = eng.step(s.positions, stress=stress)          # builds the neighbour list
@@ -404,6 +406,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--separate-mlp-out", action="store_true",
                     help="float32 policy: radial-MLP output layer as its own pass (not fused into the TP)")
+    ap.add_argument("--store-w", action="store_true",
+                    help="half-precision policies: the forward stores the per-edge weights and the VJP reads "
+                         "them back (default: the VJP rebuilds them)")
     ap.add_argument("--kernel-table", action="store_true", help="print per-kernel times to stderr")
     ap.add_argument("--graphs", choices=("on", "off"), default=None,
                     help="replay the step through captured HIP graphs (on) or launch it eagerly (off); "
@@ -447,7 +452,7 @@ def main():
 
     graphs = None if args.graphs is None else args.graphs == "on"
     head = run_workload(args.config, args.steps, args.warmup, args.separate_mlp_out, graphs, extras=True,
-                        launch_order=args.launch_order)
+                        launch_order=args.launch_order, store_w=args.store_w)
     if args.kernel_table:
         kernel_table(head["per_step"], head["ctx"])
     sweep = None
@@ -455,7 +460,7 @@ def main():
         sweep = []
         for i in range(8):  # the five benchmark configurations, an mh-1 model on Si1000, MACE-OFF widths
             r = head if i == args.config else run_workload(i, max(5, args.steps // 2), args.warmup,
-                                                           args.separate_mlp_out, graphs)
+                                                           args.separate_mlp_out, graphs, store_w=args.store_w)
             sweep.append({k: r[k] for k in ("workload", "n_atoms", "n_edges", "properties", "feature_dtype",
                                              "channels", "engine_channels", "ms_per_step",
                                              "ms_per_step_nl_rebuild", "atom_steps_per_s", "dominant",

@@ -237,6 +237,15 @@ int mace_set_split_products(mace_ctx* ctx, int32_t enable);
  * blocks.py:253-274). */
 int mace_set_fused_tp(mace_ctx* ctx, int32_t enable);
 
+/* Float16 and bfloat16 feature policies, standard interaction blocks with one
+ * or two input-degree blocks: the tensor-product VJP rebuilds the per-edge
+ * weights w from the radial MLP's last hidden layer (kept by the forward) on
+ * matrix cores instead of reading w back from memory, and the forward then
+ * does not store w (enable != 0, the default).  The rebuilt values are the
+ * same 16-bit numbers the forward used, so results do not change.  No
+ * counterpart in the reference (the same evaluation as blocks.py:253-274). */
+int mace_set_rebuild_w(mace_ctx* ctx, int32_t enable);
+
 /* Timing of the last mace_step (device milliseconds, HIP events on the
  * context's stream): [0] whole step, [1] neighbour list (0 if cached),
  * [2] forward, [3] backward.  Returns the number of values written. */

@@ -112,6 +112,9 @@ struct Layer {
   DBuf<float> A2, rinv;  // message after its skip FCTP (non-residual block); 1 / (1 + density)
   DBuf<float> ds;        // silu' of the radial MLP's pre-activations, [E][3][64]
   DBuf<_Float16> wh;
+  // h3 and its inverse scales kept for this layer's VJP, which rebuilds w from them (a later
+  // layer overwrites the shared buffers)
+  DBuf<float> h3own, h3invown;
   const void* wptr(bool half) const { return half ? static_cast<const void*>(wh.p) : static_cast<const void*>(w.p); }
   // mh-1 non-linear interaction block (blocks.py:611-807).  The conv TP acts on linear_up's
   // output (ledge blocks, dedge floats per node); lin / din stay the layer input's.
@@ -226,6 +229,7 @@ struct mace_ctx {
   bool use_graphs = true;
   bool split_products = true;  // float32 policy: matrix products on fp16 matrix cores (split operands)
   bool fused_tp = true;        // with split products: radial-MLP output layer fused into the TP kernels
+  bool rebuild_w = true;       // half-precision policies: the fused VJP rebuilds w instead of reading it
   struct SplitW {
     DBuf<_Float16> x;  // [hi | lo] planes of the weights scaled by 1 / winv
     float winv = 1.f;
@@ -419,7 +423,8 @@ void free_layers(mace_ctx* c) {
         L.dens.release(), L.mlpT3x.release(), L.mlp3x.release(), L.mlp_tiles.release(), L.ds.release(),
         L.mlp_tiles_x.release(), L.b3.release(), L.rmlp_ts.release(), L.rmlp_tt.release(), L.rmlp_ln.release(),
         L.rmlp_bias.release(), L.dmlp_ts.release(), L.dmlp_tt.release(), L.dmlp_ln.release(), L.dmlp_w1.release(),
-        L.dmlp_tiles.release(), L.Q.release(), L.R.release(), L.Gt.release();
+        L.dmlp_tiles.release(), L.Q.release(), L.R.release(), L.Gt.release(), L.h3own.release(),
+        L.h3invown.release();
     for (int i = 0; i < 4; ++i) L.mskip[i].release(), L.mskipT[i].release();
     for (int i = 0; i < 4; ++i) L.res_[i].release(), L.resT[i].release(), L.lin2[i].release(), L.lin2T[i].release();
   }
@@ -775,6 +780,17 @@ StepPath step_path(const mace_ctx* c) {
   return p;
 }
 
+// The fused VJP of layer L rebuilds w from h3 (half-precision policies, one or two input blocks,
+// standard interaction block), so its forward does not store w
+bool layer_rw(const mace_ctx* c, const Layer& L) {
+  return c->rebuild_w && step_path(c).fused && !L.nonlin && tpx_rebuilds_w(L.lin, c->dims.feature_half, false);
+}
+// layer l's h3 / h3inv: its own buffers when its VJP reads them and a later layer would overwrite
+// the shared ones
+bool own_h3(const mace_ctx* c, size_t l) { return l + 1 < c->layers.size() && layer_rw(c, c->layers[l]); }
+float* h3_of(mace_ctx* c, size_t l) { return own_h3(c, l) ? c->layers[l].h3own.p : c->h3.p; }
+float* h3inv_of(mace_ctx* c, size_t l) { return own_h3(c, l) ? c->layers[l].h3invown.p : c->h3inv.p; }
+
 void ensure_edge_buffers(mace_ctx* c, int64_t E) {
   invalidate_graphs(c);
   const size_t e = (size_t)std::max<int64_t>(E, 1);
@@ -816,6 +832,8 @@ void ensure_edge_buffers(mace_ctx* c, int64_t E) {
     c->gscale.ensure(e * NSLICE);
   }
   c->h3inv.ensure(e);
+  for (size_t l = 0; l < c->layers.size(); ++l)
+    if (own_h3(c, l)) c->layers[l].h3own.ensure(e * RADIAL_H), c->layers[l].h3invown.ensure(e);
   c->vir_part.ensure(9 * ((e + 255) / 256));
 
 }
@@ -1607,7 +1625,8 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
       // split: h3 holds E x 2 x 64 fp16 (the same bytes as E x 64 floats)
       if (split)
         // no silu' saved: the VJP recomputes the hidden layers from ef
-        launch_mlp_hidden_x(st, E, nb, c->ef.p, L.mlp_tiles_x.p, L.mlp_winv, c->h3.p, c->h3inv.p, nullptr, half);
+        launch_mlp_hidden_x(st, E, nb, c->ef.p, L.mlp_tiles_x.p, L.mlp_winv, h3_of(c, l), h3inv_of(c, l), nullptr,
+                            half);
       else
         launch_mlp_hidden(st, E, nb, c->ef.p, L.mlp_tiles.p,
                           h16 ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), c->h3inv.p, L.ds.p,
@@ -1633,8 +1652,9 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
     {
       Site s(c, lname("tp_fwd", l));
       if (fused)
-        launch_tpx_fwd(st, L.lin, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, c->h3.p, c->h3inv.p,
-                       L.mlpT3x.p, L.wn, L.w3inv, L.h_up.p, c->M.p, L.w.p, half, nullptr, nullptr);
+        launch_tpx_fwd(st, L.lin, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, h3_of(c, l),
+                       h3inv_of(c, l), L.mlpT3x.p, L.wn, L.w3inv, L.h_up.p, c->M.p, L.w.p, half, nullptr, nullptr,
+                       !layer_rw(c, L));
       else
         launch_tp_fwd(st, L.lin, N, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, L.wptr(h16), L.h_up.p,
                       c->M.p, half);
@@ -1776,7 +1796,8 @@ void backward(mace_ctx* c, bool stress, double* out, const double* e_part, doubl
       }
       launch_tpx_bwd(st, Ly.lin, N, E, c->rowptr.p, c->sender.p, c->Y.p, c->Mt.p, c->mts, Ly.w.p, Ly.mlp3x.p, Ly.wn,
                      Ly.w3inv, Ly.h_up.p, c->gM.p, c->pos_s.p, l > 0 ? c->gxe.p : nullptr, c->gY.p, gyp, acc_gy,
-                     c->gh3p.p, half, nullptr, nullptr);
+                     c->gh3p.p, half, nullptr, nullptr, h3_of(c, l), h3inv_of(c, l), Ly.mlpT3x.p,
+                     layer_rw(c, Ly));
     } else {
       // layers after the first also need dL/dx: per-edge rows in sender order, then a segmented sum
       Site s(c, lname("tp_bwd", l));
@@ -2311,6 +2332,17 @@ int mace_set_split_products(mace_ctx* c, int32_t enable) {
     c->split_products = enable != 0;
     invalidate_graphs(c);
     if (c->model_ready && c->E > 0) ensure_edge_buffers(c, c->E);  // the arrays of the path now taken
+  });
+}
+
+int mace_set_rebuild_w(mace_ctx* c, int32_t enable) {
+  if (!c) return MACE_ERR_INVALID;
+  return guard(c, [&] {
+    set_device(c);
+    HIPCHK(hipStreamSynchronize(c->stream));  // queued steps still read the stored w
+    c->rebuild_w = enable != 0;
+    invalidate_graphs(c);
+    if (c->model_ready && c->E > 0) ensure_edge_buffers(c, c->E);
   });
 }
 

@@ -271,7 +271,8 @@ void launch_tp_bwd_recv(hipStream_t st, int lin, int N, const int* rowptr, const
 // (cut [E], may be null: 1)
 void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const void* h3x, const float* h3inv, const void* W3Tx, int W,
-                    float wscale, const float* up, float* M, float* w, int rnd, const float* b3, const float* cut);
+                    float wscale, const float* up, float* M, float* w, int rnd, const float* b3, const float* cut,
+                    int store_w = 1);
 // TP VJP with the radial-MLP output layer's backward product fused in (split products,
 // lin = 1..3): reads w ([E][W], written by
 // launch_tpx_fwd), writes the dL/dh3 partials gh3p ([P][E][64], P = 2 x input
@@ -284,7 +285,13 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
 void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const float* w, const void* W3x, int W, float wscale, const float* up,
                     const float* gM, const int* pos_s, float* gxe, float* gY, int gyp, int accumulate_gY,
-                    float* gh3p, int wfmt, const float* b3, float* gwbp);
+                    float* gh3p, int wfmt, const float* b3, float* gwbp, const void* h3x = nullptr,
+                    const float* h3inv = nullptr, const void* W3Tx = nullptr, int rebuild_w = 0);
+// rebuild_w: w is not read but made again from h3x / h3inv / W3Tx (the forward's operands), which
+// the forward then need not store (launch_tpx_fwd store_w = 0); allowed where
+// tpx_rebuilds_w(lin, wfmt, b3 != null): a half-precision policy (one product per tile), one or
+// two input blocks, the standard interaction block
+bool tpx_rebuilds_w(int lin, int wfmt, bool nonlinear);
 // p[0 .. n) = 0 (a kernel, not a memset: safe inside captured graphs)
 void launch_fill_zero(hipStream_t st, float* p, int64_t n);
 // gx16: the rows hold fp16 values (launch_tpx_bwd under the float16 policy), else floats;

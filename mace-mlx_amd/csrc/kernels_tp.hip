@@ -27,6 +27,8 @@
 // adds the two halves.
 #include <hip/hip_runtime.h>
 
+#include <stdexcept>
+
 #include <algorithm>
 #include <type_traits>
 #include <utility>
@@ -598,6 +600,16 @@ __device__ __forceinline__ float load_w_nt(const float* w, int64_t o) {
   }
 }
 
+// The 16-bit pattern of a weight already rounded under a half-precision policy, and back
+template <int RND>
+__device__ __forceinline__ unsigned short w16_bits(float x) {
+  return RND == RND_F16 ? __builtin_bit_cast(unsigned short, (_Float16)x) : (unsigned short)(__float_as_uint(x) >> 16);
+}
+template <int RND>
+__device__ __forceinline__ float w16_value(unsigned short h) {
+  return RND == RND_F16 ? (float)__builtin_bit_cast(_Float16, h) : __uint_as_float((unsigned)h << 16);
+}
+
 // Raw buffer views (stride 0): the hardware range check drops a store, and returns zero for a
 // load, whose byte offset is at or past the view's size.  Padding lanes and past-the-end edges
 // take an offset past every view (or a view of size 0), so the fused kernels' stores need no
@@ -704,6 +716,8 @@ struct TpxDims {
   // receiver's edges split into spr contiguous chunks, one per wave, their message sums added
   // in chunk order at the end
   int sprl;
+  // 0: w is not stored (the VJP rebuilds it from h3 and W3)
+  int store_w;
 };
 
 #define MACE_TPX_FWD_PTRS                                                                                   \
@@ -978,7 +992,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
         const float* trow_t = tb + b * TSP;  // Y (l1 = 0), M1 (l1 = 1) or M2 (l1 = 2)
         tp_edge_fwd<LIN, L1>(acc, in, trow_t, trow_t, trow_t);
       }
-      {
+      if (a.store_w) {
         constexpr unsigned WB = RND == RND_NONE ? 4 : 2;  // bytes per stored weight
         const auto wr = buf_view(reinterpret_cast<char*>(w) + (int64_t)min<int64_t>(e, elast) * a.W * WB,
                                  valid ? (unsigned)a.W * WB : 0u);
@@ -1229,13 +1243,15 @@ struct TpxBwdDims {
   const int *__restrict__ rowptr, const int *__restrict__ sender, const float *__restrict__ Y,              \
       const float *__restrict__ Mt, const float *__restrict__ w, const _Float16 *__restrict__ W3x,           \
       const float *__restrict__ up, const float *__restrict__ gM, const int *__restrict__ pos_s,            \
-      float *__restrict__ gxe, float *__restrict__ gY, float *__restrict__ gh3p
-#define MACE_TPX_BWD_ARGS rowptr, sender, Y, Mt, w, W3x, up, gM, pos_s, gxe, gY, gh3p
-// W3x: [64][W] hi plane, then lo plane; gh3p: [P][E][64]
+      float *__restrict__ gxe, float *__restrict__ gY, float *__restrict__ gh3p,                            \
+      const _Float16 *__restrict__ h3x, const float *__restrict__ h3inv, const _Float16 *__restrict__ W3Tx
+#define MACE_TPX_BWD_ARGS rowptr, sender, Y, Mt, w, W3x, up, gM, pos_s, gxe, gY, gh3p, h3x, h3inv, W3Tx
+// W3x: [64][W] hi plane, then lo plane; gh3p: [P][E][64]; with RW, h3x / h3inv / W3Tx as the
+// forward reads them (w is then not read)
 
-template <int LIN, int L1, bool GX, int WF, bool NL>
+template <int LIN, int L1, bool GX, int WF, bool NL, bool RW>
 __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, _Float16* sg, float* sinv,
-                                        float* sy, float* sp, float* sm2) {
+                                        float* sy, float* sp, float* sm2, _Float16* hbuf, float* hiv) {
   using T = TPT<LIN>;
   using GR = GrpT<LIN, L1>;
   constexpr int G = GR::G, RS = 64 * G + 8;  // fp16 row stride: 16-byte reads of 8 lanes hit distinct banks
@@ -1304,6 +1320,79 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
     wa[ks][0] = *reinterpret_cast<const h8*>(W3x + o);
     if constexpr (WLO) wa[ks][WLO ? 1 : 0] = *reinterpret_cast<const h8*>(W3x + (int64_t)XH * a.W + o);
   }
+  // RW (half-precision policies, one or two input blocks, standard interactions): w is not
+  // read back but rebuilt per pair of steps, 32 edges, from their h3 rows and W3^T with the
+  // forward's operands, products and epilogue (the values the forward used, bit for bit), into
+  // the lo-plane half of the pair's sg buffer (the dL/dw tile has one plane under these
+  // policies).  The tile of pair t + 1 is made during pair t (published by the barrier that ends
+  // it) from h3 rows staged in LDS during pair t - 1 and fetched during pair t - 2.
+  static_assert(!RW || (!WLO && LIN <= 2 && !NL), "w is rebuilt under the half policies only");
+  constexpr int CT = 4 * G, NCTW = (CT + XW - 1) / XW;  // 16-column tiles of the group, per wave
+  h8 wt[RW ? NCTW : 1][2];  // W3^T fragments: [column tile][k step]
+  // h3 staging: threads 0 .. 255 fetch eight fp16 each of tile column hr (pair-relative)
+  const int hr = (threadIdx.x >> 3) & 31, hq = threadIdx.x & 7;
+  int hb0 = 0;
+  h8 hreg;
+  float hinvr = 0.f;
+  if constexpr (RW) {
+#pragma unroll
+    for (int m = 0; m < NCTW; ++m) {
+      const int ct = wv + XW * m;
+      if (CT % XW == 0 || ct < CT) {
+        const int gc = 16 * ct + r;
+        const int64_t col = (int64_t)GR::slot(gc >> 6) * NC + c0 + (gc & 63);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) wt[m][c] = *reinterpret_cast<const h8*>(W3Tx + col * XH + 32 * c + 8 * g);
+      }
+    }
+    int hn, hend;
+    wave_range((hr % 16) >> 1, hn, hb0, hend);  // tile column hr: edge hr & 1 of wave (hr % 16) / 2
+  }
+  // pair t's h3 rows: tile column hr is step 2 t + hr / 16 of its wave
+  auto load_h = [&](int t) {
+    const int64_t row = min<int64_t>(hb0 + 2 * (2 * t + hr / 16) + (hr & 1), elast);
+    hreg = *reinterpret_cast<const h8*>(h3x + row * 2 * XH + 8 * hq);  // the hi plane
+    hinvr = h3inv[row];
+  };
+  auto store_h = [&](int t) {
+    if (threadIdx.x < 256) {
+      *reinterpret_cast<h8*>(hbuf + ((t & 1) * 32 + hr) * 72 + 8 * hq) = hreg;
+      if (hq == 0) hiv[(t & 1) * 32 + hr] = hinvr;
+    }
+  };
+  // w tile t: this wave's column tiles of W3^T h3 for the pair's two 16-edge halves (the
+  // forward's hi.hi products over two k steps, scale, rounding), as 16-bit patterns
+  auto wtile = [&](int t) {
+    _Float16* wb = sg + ((t & 1) * 2 + 1) * 32 * RS;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int col = 16 * h + r;
+      const _Float16* hrow = hbuf + ((t & 1) * 32 + col) * 72 + 8 * g;
+      h8 bx[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) bx[c] = *reinterpret_cast<const h8*>(hrow + 32 * c);
+      f4v d[NCTW];
+#pragma unroll
+      for (int m = 0; m < NCTW; ++m) d[m] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int m = 0; m < NCTW; ++m)
+          if (CT % XW == 0 || wv + XW * m < CT) d[m] = mfma16h(wt[m][c], bx[c], d[m]);
+      const float bsc = hiv[(t & 1) * 32 + col] * a.wscale;
+#pragma unroll
+      for (int m = 0; m < NCTW; ++m) {
+        const int ct = wv + XW * m;
+        if (CT % XW == 0 || ct < CT) {
+          d[m] *= bsc;
+          typedef unsigned short us4 __attribute__((ext_vector_type(4)));
+          const us4 v = {w16_bits<WF>(qh(d[m][0], WF)), w16_bits<WF>(qh(d[m][1], WF)),
+                         w16_bits<WF>(qh(d[m][2], WF)), w16_bits<WF>(qh(d[m][3], WF))};
+          *reinterpret_cast<us4*>(wb + col * RS + 16 * ct + 4 * g) = v;
+        }
+      }
+    }
+  };
   // dL/dM of this wave's receiver (group slots, slice channels); for l1 = 1 only through
   // its CG contraction R (tp_edge_vjp_l1)
   float gm[T::NACC];
@@ -1346,9 +1435,11 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
     for (int b = 0; b < 2; ++b) {
       const int64_t e = min<int64_t>(beg + 2 * j + b, elast);
       const int64_t wo = e * a.W + c0 + u;
+      if constexpr (!RW) {
 #pragma unroll
-      for (int s = 0; s < T::NSLOT; ++s)
-        if (T::l1(s) == L1) S.w[b][s] = load_w_nt<WF>(w, wo + s * NC);
+        for (int s = 0; s < T::NSLOT; ++s)
+          if (T::l1(s) == L1) S.w[b][s] = load_w_nt<WF>(w, wo + s * NC);
+      }
       const float* xs = up + (int64_t)snd[b] * DIN + NC * L1 * L1 + c0 + u;
 #pragma unroll
       for (int i = 0; i < NX; ++i) S.x[b][i] = xs[NC * i];
@@ -1419,9 +1510,17 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
           if constexpr (L1 == 1) in.x1[i] = S.x[b][i];
           if constexpr (L1 == 2) in.x2[i] = S.x[b][i];
         }
+        if constexpr (RW) {  // this edge's row of the rebuilt tile (column 16 (j & 1) + 2 wv + b)
+          const unsigned short* wrow = reinterpret_cast<const unsigned short*>(
+              sg + (((j >> 1) & 1) * 2 + 1) * 32 * RS + (16 * (j & 1) + 2 * wv + b) * RS + u);
 #pragma unroll
-        for (int s = 0; s < T::NSLOT; ++s)
-          if (T::l1(s) == L1) in.w[s] = S.w[b][s];
+          for (int s = 0; s < T::NSLOT; ++s)
+            if (T::l1(s) == L1) in.w[s] = w16_value<WF>(wrow[64 * GR::local(s)]);
+        } else {
+#pragma unroll
+          for (int s = 0; s < T::NSLOT; ++s)
+            if (T::l1(s) == L1) in.w[s] = S.w[b][s];
+        }
         const float* yrow = ys + 16 * b;
         if constexpr (L1 == 1)
           tp_edge_vjp_l1<LIN, GX>(R1, in, gws, yrow, gx1, gYu);
@@ -1512,12 +1611,22 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   // the step loop of one half (kh uniform per wave: the barriers of both loops pair up)
   auto run = [&](auto half) {
     constexpr int HALF = decltype(half)::value;
+    // RW: the next pair's w tile, the h3 rows of the one after staged, and the next fetched
+    auto rw_pair = [&](int t) {
+      if constexpr (RW) {
+        wtile(t + 1);
+        store_h(t + 2);
+        load_h(t + 3);
+      }
+    };
+    rw_pair(0);
     edges(0, in0, in1);
     wave_sync();  // this step's Y- and M2-row reads are done before the next step's stores
     edges(1, in1, in0);
     __syncthreads();
 #pragma unroll 1
     for (int j = 2; j < nsteps2; j += 2) {  // nsteps2 is even
+      rw_pair(j >> 1);
       if constexpr (HALF == 0) products((j >> 1) - 1, half);
       edges(j, in0, in1);
       if constexpr (HALF == 1) products((j >> 1) - 1, half);
@@ -1545,6 +1654,16 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   };
   if (nsteps2 == 0) return;  // uniform over the block: no receiver of it has edges
   // some receiver of the block has edges, so E >= 1 and the clamped indices are valid
+  if constexpr (RW) {  // the first w tile, and the h3 rows of the second staged
+    load_h(0);
+    store_h(0);
+    load_h(1);
+    store_h(1);
+    load_h(2);
+    __syncthreads();
+    wtile(0);
+    __syncthreads();
+  }
   load_idx(0);
   load_in(0, in0);
   load_idx(1);
@@ -1556,8 +1675,8 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
     run(std::integral_constant<int, 1>{});
 }
 
-// WF: storage format of w (RND_*, as the forward that wrote it)
-template <int LIN, bool GX, int WF, bool NL>
+// WF: storage format of w (RND_*, as the forward that wrote it); RW: w rebuilt instead of read
+template <int LIN, bool GX, int WF, bool NL, bool RW>
 __global__ void __launch_bounds__(64 * XW, 2) k_tpx_bwd(TpxBwdDims a, MACE_TPX_BWD_PTRS) {
   __shared__ __align__(16) _Float16 sg[2 * 2 * 32 * (64 * gmax<LIN>() + 8)];  // [pair][hi, lo][edge][RS]
   __shared__ float sinv[2 * 32];
@@ -1565,20 +1684,22 @@ __global__ void __launch_bounds__(64 * XW, 2) k_tpx_bwd(TpxBwdDims a, MACE_TPX_B
   // [two pairs + the lower half's slots][sub-tile][q tile][lane][4]
   __shared__ __align__(16) float sp[6 * 4 * 256];
   __shared__ __align__(16) float sm2[LIN == 3 ? XW * 2 * tpx_tab_pad(2) : 4];  // [wave][edge][M2 row]
+  __shared__ __align__(16) _Float16 hbuf[RW ? 2 * 32 * 72 : 8];  // RW: [pair buffer][edge][h3 row + pad]
+  __shared__ float hiv[RW ? 64 : 1];                              // RW: their inverse scales
   if constexpr (LIN == 1) {
-    tpx_bwd<1, 0, GX, WF, NL>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+    tpx_bwd<1, 0, GX, WF, NL, RW>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2, hbuf, hiv);
   } else if constexpr (LIN == 2) {
     if (blockIdx.z == 0)
-      tpx_bwd<2, 1, GX, WF, NL>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<2, 1, GX, WF, NL, RW>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2, hbuf, hiv);
     else
-      tpx_bwd<2, 0, GX, WF, NL>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<2, 0, GX, WF, NL, RW>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2, hbuf, hiv);
   } else {
     if (blockIdx.z == 0)
-      tpx_bwd<3, 2, GX, WF, NL>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<3, 2, GX, WF, NL, false>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2, hbuf, hiv);
     else if (blockIdx.z == 1)
-      tpx_bwd<3, 1, GX, WF, NL>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<3, 1, GX, WF, NL, false>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2, hbuf, hiv);
     else
-      tpx_bwd<3, 0, GX, WF, NL>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2);
+      tpx_bwd<3, 0, GX, WF, NL, false>(a, MACE_TPX_BWD_ARGS, sg, sinv, sy, sp, sm2, hbuf, hiv);
   }
 }
 
@@ -1657,11 +1778,12 @@ int tpx_split_log2(int N, int lin) {
 
 void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const void* h3x, const float* h3inv, const void* W3Tx, int W,
-                    float wscale, const float* up, float* M, float* w, int rnd, const float* b3, const float* cut) {
+                    float wscale, const float* up, float* M, float* w, int rnd, const float* b3, const float* cut,
+                    int store_w) {
   if (N <= 0) return;
   // waves per receiver: enough blocks for the CUs (small systems), one otherwise
   const int sprl = tpx_split_log2(N, lin);
-  const TpxDims a{N, W, mts, E, wscale, b3, cut, sprl};
+  const TpxDims a{N, W, mts, E, wscale, b3, cut, sprl, store_w};
   // y: channel slice; z: input block l1
   const dim3 grid((unsigned)((N + (XW >> sprl) - 1) / (XW >> sprl)), NSLICE, (unsigned)lin);
   const _Float16* hx = static_cast<const _Float16*>(h3x);
@@ -1698,16 +1820,34 @@ void launch_tpx_fwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
 void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr, const int* sender, const float* Y,
                     const float* Mt, int mts, const float* w, const void* W3x, int W, float wscale, const float* up,
                     const float* gM, const int* pos_s, float* gxe, float* gY, int gyp, int accumulate_gY,
-                    float* gh3p, int wfmt, const float* b3, float* gwbp) {
+                    float* gh3p, int wfmt, const float* b3, float* gwbp, const void* h3x, const float* h3inv,
+                    const void* W3Tx, int rebuild_w) {
   if (N <= 0 || E <= 0) return;  // no edges: no dL/dw, dL/dY, dL/dx rows to write
+  if (rebuild_w && !tpx_rebuilds_w(lin, wfmt, b3 != nullptr))
+    throw std::invalid_argument("launch_tpx_bwd: w is rebuilt only under a half-precision policy, one or two "
+                                "input blocks and the standard interaction block");
   // waves per receiver: enough blocks for the CUs (small systems), one otherwise
   const int sprl = tpx_split_log2(N, lin);
   const TpxBwdDims a{N, W, mts, E, wscale, accumulate_gY, gyp, b3, gwbp, sprl};
   const dim3 grid((unsigned)((N + (XW >> sprl) - 1) / (XW >> sprl)), NSLICE, (unsigned)lin);
   const _Float16* wx = static_cast<const _Float16*>(W3x);
-#define MACE_TPXB(L, GXV, WF, NLV)                                                                         \
-  MACE_LAUNCH((k_tpx_bwd<L, GXV, WF, NLV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, gM, \
-              pos_s, gxe, gY, gh3p)
+  const _Float16* hx = static_cast<const _Float16*>(h3x);
+  const _Float16* wtx = static_cast<const _Float16*>(W3Tx);
+#define MACE_TPXB_RW(L, GXV, WF, NLV, RWV)                                                                       \
+  MACE_LAUNCH((k_tpx_bwd<L, GXV, WF, NLV, RWV>), grid, dim3(64 * XW), 0, st, a, rowptr, sender, Y, Mt, w, wx, up, \
+              gM, pos_s, gxe, gY, gh3p, hx, h3inv, wtx)
+  // RW: only where tpx_rebuilds_w allows it (instantiated for those template arguments only)
+#define MACE_TPXB(L, GXV, WF, NLV)                                          \
+  do {                                                                      \
+    if constexpr (WF != RND_NONE && !NLV && L <= 2) {                       \
+      if (rebuild_w)                                                        \
+        MACE_TPXB_RW(L, GXV, WF, NLV, true);                                \
+      else                                                                  \
+        MACE_TPXB_RW(L, GXV, WF, NLV, false);                               \
+    } else {                                                                \
+      MACE_TPXB_RW(L, GXV, WF, NLV, false);                                 \
+    }                                                                       \
+  } while (0)
   // NL: the non-linear block's gw . b3 partials (b3 given)
 #define MACE_TPXB_WN(L, GXV, NLV)       \
   if (wfmt == RND_F16)                  \
@@ -1733,7 +1873,10 @@ void launch_tpx_bwd(hipStream_t st, int lin, int N, int64_t E, const int* rowptr
 #undef MACE_TPXB_WF
 #undef MACE_TPXB_WN
 #undef MACE_TPXB
+#undef MACE_TPXB_RW
 }
+
+bool tpx_rebuilds_w(int lin, int wfmt, bool nonlinear) { return wfmt != RND_NONE && lin <= 2 && !nonlinear; }
 
 void launch_fill_zero(hipStream_t st, float* p, int64_t n) {
   if (n <= 0) return;

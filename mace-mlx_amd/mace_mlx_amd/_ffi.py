@@ -41,6 +41,7 @@ EXPORTED_SYMBOLS = (
     "mace_set_graphs",
     "mace_set_split_products",
     "mace_set_fused_tp",
+    "mace_set_rebuild_w",
     "mace_set_batch", "mace_step_batch",
     "mace_get_launch_order",
     "mace_step_device_noalloc",
@@ -105,6 +106,7 @@ def load_library(path: Optional[str] = None, channels: int = 128) -> ctypes.CDLL
         "mace_set_graphs": (ctypes.c_int, [P, I32]),
         "mace_set_split_products": (ctypes.c_int, [P, I32]),
         "mace_set_fused_tp": (ctypes.c_int, [P, I32]),
+        "mace_set_rebuild_w": (ctypes.c_int, [P, I32]),
         "mace_set_batch": (ctypes.c_int, [P, I32, P, P, P, P, D]),
         "mace_step_batch": (ctypes.c_int, [P, P, U32, P, P, P, P]),
         "mace_get_kernel_times": (ctypes.c_int, [P, ctypes.c_char_p, I64, P, P, I32, ctypes.POINTER(I32)]),
@@ -297,6 +299,11 @@ class Engine:
         """With split products: radial-MLP output layer built inside the tensor-product kernels
         (default) or in a separate pass."""
         self._check(self._lib.mace_set_fused_tp(self._h, int(bool(enable))))
+
+    def set_rebuild_w(self, enable: bool) -> None:
+        """Half-precision feature policies: the tensor-product VJP rebuilds the per-edge weights
+        from the radial MLP's hidden layer (default) instead of reading them back."""
+        self._check(self._lib.mace_set_rebuild_w(self._h, int(bool(enable))))
 
     def kernel_times(self) -> dict:
         """{site: (total_ms, launches)} accumulated since the last call."""

@@ -211,6 +211,42 @@ def test_bfloat16_feature_policy(arch):
 
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("arch", ["hea", "medium", "large"])
+def test_half_policy_vjp_rebuilds_w_bit_for_bit(arch, dtype):
+    """Under the half-precision policies the tensor-product VJP rebuilds the per-edge weights w
+    (`blocks.py:253-274`: the radial MLP's output layer) from the saved hidden layer instead of
+    reading back what the forward stored (mace_set_rebuild_w).  The rebuilt values are the
+    forward's own 16-bit numbers, so energy, forces and virial are identical bit for bit to the
+    path that stores and reads w, on a system with ragged rows (receivers without edges) and on a
+    periodic cell; "large" (three input blocks) never rebuilds and must match as well."""
+    if arch == "hea":
+        cfg = make_config(4).model
+        rng = np.random.default_rng(7)
+        base = lattice(_FCC, 3.6, (3, 3, 3), 26)
+        base.numbers = np.array([26, 28, 27, 24, 25])[rng.integers(0, 5, len(base))]
+        systems = [rattle(base, 0.05, 8, rng=rng)]
+    else:
+        cfg = arch_config(arch)
+        systems = [rattle(diamond_si((2, 2, 2)), 0.05, 9), _ragged_system()]
+    case = Case(cfg, dtype=dtype)
+    try:
+        for k, s in enumerate(systems):
+            print(f"rebuild w {arch} {dtype}: system {k} ({len(s)} atoms)", flush=True)
+            on = case.run(s, stress=True)
+            case.eng.set_rebuild_w(False)
+            off = case.run(s, stress=True)
+            case.eng.set_rebuild_w(True)
+            again = case.run(s, stress=True)
+            for g in (off, again):
+                assert g["E"] == on["E"]
+                assert np.array_equal(g["F"], on["F"])
+                assert np.array_equal(g["vir"], on["vir"])
+            assert np.isfinite(on["F"]).all()
+    finally:
+        case.eng.set_rebuild_w(True)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
 def test_mh1_half_precision_policies(dtype):
     """mh-1 models (`blocks.py:611-807`) under the half-precision policies (`model.py:592-661`: the
     reference applies set_dtype to every interaction class) against the float64 oracle on the same
