@@ -1329,7 +1329,8 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   static_assert(!RW || (!WLO && LIN <= 2 && !NL), "w is rebuilt under the half policies only");
   constexpr int CT = 4 * G, NCTW = (CT + XW - 1) / XW;  // 16-column tiles of the group, per wave
   h8 wt[RW ? NCTW : 1][2];  // W3^T fragments: [column tile][k step]
-  // h3 staging: threads 0 .. 255 fetch eight fp16 each of tile column hr (pair-relative)
+  // h3 staging: threads 0 .. 255 (the lower half) fetch eight fp16 each of tile column hr
+  // (pair-relative)
   const int hr = (threadIdx.x >> 3) & 31, hq = threadIdx.x & 7;
   int hb0 = 0;
   h8 hreg;
@@ -1611,27 +1612,35 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   // the step loop of one half (kh uniform per wave: the barriers of both loops pair up)
   auto run = [&](auto half) {
     constexpr int HALF = decltype(half)::value;
-    // RW: the next pair's w tile, the h3 rows of the one after staged, and the next fetched
-    auto rw_pair = [&](int t) {
-      if constexpr (RW) {
-        wtile(t + 1);
+    // RW, during pair t: the lower half (waves 0 .. 3) stages the h3 rows of pair t + 2 and
+    // fetches those of pair t + 3 at its start and makes its share of pair t + 1's w tile at its
+    // end; the upper half makes its share at the start (the matrix work of the two waves on a
+    // SIMD at opposite ends of the pair, as their dL/dh3 products)
+    auto rw_begin = [&](int t) {
+      if constexpr (RW && HALF == 0) {
         store_h(t + 2);
         load_h(t + 3);
       }
+      if constexpr (RW && HALF == 1) wtile(t + 1);
     };
-    rw_pair(0);
+    auto rw_end = [&](int t) {
+      if constexpr (RW && HALF == 0) wtile(t + 1);
+    };
+    rw_begin(0);
     edges(0, in0, in1);
     wave_sync();  // this step's Y- and M2-row reads are done before the next step's stores
     edges(1, in1, in0);
+    rw_end(0);
     __syncthreads();
 #pragma unroll 1
     for (int j = 2; j < nsteps2; j += 2) {  // nsteps2 is even
-      rw_pair(j >> 1);
+      rw_begin(j >> 1);
       if constexpr (HALF == 0) products((j >> 1) - 1, half);
       edges(j, in0, in1);
       if constexpr (HALF == 1) products((j >> 1) - 1, half);
       wave_sync();
       edges(j + 1, in1, in0);
+      rw_end(j >> 1);
       __syncthreads();  // also: the Y- and M2-row reads are done before the next step's stores
     }
     products((nsteps2 >> 1) - 1, half);
@@ -1654,12 +1663,14 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   };
   if (nsteps2 == 0) return;  // uniform over the block: no receiver of it has edges
   // some receiver of the block has edges, so E >= 1 and the clamped indices are valid
-  if constexpr (RW) {  // the first w tile, and the h3 rows of the second staged
-    load_h(0);
-    store_h(0);
-    load_h(1);
-    store_h(1);
-    load_h(2);
+  if constexpr (RW) {  // the first w tile, and the h3 rows of the second staged (lower half)
+    if (kh == 0) {
+      load_h(0);
+      store_h(0);
+      load_h(1);
+      store_h(1);
+      load_h(2);
+    }
     __syncthreads();
     wtile(0);
     __syncthreads();
