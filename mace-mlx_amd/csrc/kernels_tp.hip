@@ -526,27 +526,62 @@ __global__ void __launch_bounds__(NC* NG) k_tp_bwd_recv(int N, const int* __rest
   }
 }
 
-// gup[a][row][u] (= or +=, accumulate) the sum over the edges sent by a (a contiguous segment of
-// the sender-ordered gxe rows, summed in order, fp32); grid (N, LIN^2), NC threads.
-// GT: the rows' element type (fp16 under the float16 policy's fused VJP).
+// gup[a][:] (= or +=, accumulate) the sum over the edges sent by a (a contiguous segment of the
+// sender-ordered gxe rows, din entries each, summed in order into four interleaved partial sums,
+// fp32).  GT: the rows' element type (fp16 under the float16 policy's fused VJP).  A wave per
+// (atom, chunk of 64 VEC columns): lane l sums columns VEC (64 chunk + l) .. + VEC - 1 of the
+// atom's rows with 16-byte loads (a whole 1 KB fp16 row per wave load), eight rows in flight.
 template <typename GT>
-__global__ void __launch_bounds__(NC) k_tp_gather_gx(int N, int din, const int* __restrict__ rowptr_s,
-                                                     const GT* __restrict__ gxe, float* __restrict__ gup,
-                                                     int accumulate) {
-  const int a = blockIdx.x, row = blockIdx.y, u = threadIdx.x;
+__global__ void __launch_bounds__(256) k_tp_gather_gx(int N, int din, int nchunk, const int* __restrict__ rowptr_s,
+                                                      const GT* __restrict__ gxe, float* __restrict__ gup,
+                                                      int accumulate) {
+  constexpr int VEC = 16 / sizeof(GT);
+  typedef GT gv __attribute__((ext_vector_type(VEC)));
+  const int unit = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int a = unit / nchunk, col = VEC * (64 * (unit % nchunk) + (threadIdx.x & 63));
+  if (a >= N || col >= din) return;  // din is a multiple of 64: a lane's VEC columns are all in or all out
   const int beg = rowptr_s[a], end = rowptr_s[a + 1];
-  const GT* src = gxe + (int64_t)row * NC + u;
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  const GT* src = gxe + col;
+  auto row = [&](int k) { return *reinterpret_cast<const gv*>(src + (int64_t)k * din); };
+  float s[4][VEC];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) s[q][v] = 0.f;
+  auto add = [&](int q, const gv& x) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) s[q][v] += (float)x[v];
+  };
   int k = beg;
-  for (; k + 3 < end; k += 4) {
-    s0 += (float)src[(int64_t)k * din];
-    s1 += (float)src[(int64_t)(k + 1) * din];
-    s2 += (float)src[(int64_t)(k + 2) * din];
-    s3 += (float)src[(int64_t)(k + 3) * din];
+  for (; k + 7 < end; k += 8) {
+    gv x[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) x[b] = row(k + b);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) add(b & 3, x[b]);
   }
-  for (; k < end; ++k) s0 += (float)src[(int64_t)k * din];
-  float* o = gup + (int64_t)a * din + row * NC + u;
-  *o = accumulate ? *o + ((s0 + s1) + (s2 + s3)) : (s0 + s1) + (s2 + s3);
+  for (; k + 3 < end; k += 4) {
+    gv x[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) x[b] = row(k + b);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) add(b, x[b]);
+  }
+  for (; k < end; ++k) add(0, row(k));
+  float4* o = reinterpret_cast<float4*>(gup + (int64_t)a * din + col);
+#pragma unroll
+  for (int h = 0; h < VEC / 4; ++h) {
+    float4 t;
+    t.x = (s[0][4 * h] + s[1][4 * h]) + (s[2][4 * h] + s[3][4 * h]);
+    t.y = (s[0][4 * h + 1] + s[1][4 * h + 1]) + (s[2][4 * h + 1] + s[3][4 * h + 1]);
+    t.z = (s[0][4 * h + 2] + s[1][4 * h + 2]) + (s[2][4 * h + 2] + s[3][4 * h + 2]);
+    t.w = (s[0][4 * h + 3] + s[1][4 * h + 3]) + (s[2][4 * h + 3] + s[3][4 * h + 3]);
+    if (accumulate) {
+      const float4 p = o[h];
+      t.x += p.x, t.y += p.y, t.z += p.z, t.w += p.w;
+    }
+    o[h] = t;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1897,12 +1932,18 @@ void launch_fill_zero(hipStream_t st, float* p, int64_t n) {
 void launch_tp_gather_gx(hipStream_t st, int lin, int N, const int* rowptr_s, const float* gxe, float* gup,
                          int gx16, int accumulate) {
   if (N <= 0) return;
+  const int din = NC * lin * lin;  // a multiple of 64
+  auto go = [&](auto tag, const auto* src) {
+    using GT = decltype(tag);
+    const int nchunk = (din + 64 * (16 / (int)sizeof(GT)) - 1) / (64 * (16 / (int)sizeof(GT)));
+    const int64_t units = (int64_t)N * nchunk;
+    MACE_LAUNCH(k_tp_gather_gx<GT>, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, st, N, din, nchunk, rowptr_s,
+                src, gup, accumulate);
+  };
   if (gx16)
-    MACE_LAUNCH(k_tp_gather_gx<_Float16>, dim3(N, lin * lin), dim3(NC), 0, st, N, NC * lin * lin, rowptr_s,
-                reinterpret_cast<const _Float16*>(gxe), gup, accumulate);
+    go(_Float16{}, reinterpret_cast<const _Float16*>(gxe));
   else
-    MACE_LAUNCH(k_tp_gather_gx<float>, dim3(N, lin * lin), dim3(NC), 0, st, N, NC * lin * lin, rowptr_s, gxe, gup,
-                accumulate);
+    go(float{}, gxe);
 }
 
 }  // namespace mace
