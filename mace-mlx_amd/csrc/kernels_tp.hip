@@ -1397,33 +1397,50 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
     }
   };
   // w tile t: this wave's column tiles of W3^T h3 for the pair's two 16-edge halves (the
-  // forward's hi.hi products over two k steps, scale, rounding), as 16-bit patterns
-  auto wtile = [&](int t) {
-    _Float16* wb = sg + ((t & 1) * 2 + 1) * 32 * RS;
+  // forward's hi.hi products over two k steps, scale, rounding), as 16-bit patterns, in three
+  // stages that the step loop spreads over a pair of steps (each stage's latency hidden behind
+  // an edge step): the B fragments and scales from LDS, the products, the epilogue and store
+  struct WtStage {
+    h8 bx[2][2];      // [half][k step]
+    f4v d[2][NCTW];   // [half][column tile]
+    float bsc[2];
+  };
+  WtStage wsg;
+  auto wt_read = [&](int t) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int col = 16 * h + r;
       const _Float16* hrow = hbuf + ((t & 1) * 32 + col) * 72 + 8 * g;
-      h8 bx[2];
 #pragma unroll
-      for (int c = 0; c < 2; ++c) bx[c] = *reinterpret_cast<const h8*>(hrow + 32 * c);
-      f4v d[NCTW];
+      for (int c = 0; c < 2; ++c) wsg.bx[h][c] = *reinterpret_cast<const h8*>(hrow + 32 * c);
+      wsg.bsc[h] = hiv[(t & 1) * 32 + col] * a.wscale;
+    }
+  };
+  auto wt_mma = [&]() {
 #pragma unroll
-      for (int m = 0; m < NCTW; ++m) d[m] = f4v{0.f, 0.f, 0.f, 0.f};
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int m = 0; m < NCTW; ++m) wsg.d[h][m] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int m = 0; m < NCTW; ++m)
-          if (CT % XW == 0 || wv + XW * m < CT) d[m] = mfma16h(wt[m][c], bx[c], d[m]);
-      const float bsc = hiv[(t & 1) * 32 + col] * a.wscale;
+          if (CT % XW == 0 || wv + XW * m < CT) wsg.d[h][m] = mfma16h(wt[m][c], wsg.bx[h][c], wsg.d[h][m]);
+    }
+  };
+  auto wt_store = [&](int t) {
+    _Float16* wb = sg + ((t & 1) * 2 + 1) * 32 * RS;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int col = 16 * h + r;
 #pragma unroll
       for (int m = 0; m < NCTW; ++m) {
         const int ct = wv + XW * m;
         if (CT % XW == 0 || ct < CT) {
-          d[m] *= bsc;
+          const f4v d = wsg.d[h][m] * wsg.bsc[h];
           typedef unsigned short us4 __attribute__((ext_vector_type(4)));
-          const us4 v = {w16_bits<WF>(qh(d[m][0], WF)), w16_bits<WF>(qh(d[m][1], WF)),
-                         w16_bits<WF>(qh(d[m][2], WF)), w16_bits<WF>(qh(d[m][3], WF))};
+          const us4 v = {w16_bits<WF>(qh(d[0], WF)), w16_bits<WF>(qh(d[1], WF)), w16_bits<WF>(qh(d[2], WF)),
+                         w16_bits<WF>(qh(d[3], WF))};
           *reinterpret_cast<us4*>(wb + col * RS + 16 * ct + 4 * g) = v;
         }
       }
@@ -1648,22 +1665,25 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
   auto run = [&](auto half) {
     constexpr int HALF = decltype(half)::value;
     // RW, during pair t: the lower half (waves 0 .. 3) stages the h3 rows of pair t + 2 and
-    // fetches those of pair t + 3 at its start and makes its share of pair t + 1's w tile at its
-    // end; the upper half makes its share at the start (the matrix work of the two waves on a
-    // SIMD at opposite ends of the pair, as their dL/dh3 products)
+    // fetches those of pair t + 3; every wave makes its share of pair t + 1's w tile (fragments
+    // read at the start, products between the two steps, stored at the end)
     auto rw_begin = [&](int t) {
       if constexpr (RW && HALF == 0) {
         store_h(t + 2);
         load_h(t + 3);
       }
-      if constexpr (RW && HALF == 1) wtile(t + 1);
+      if constexpr (RW) wt_read(t + 1);
+    };
+    auto rw_mid = [&]() {
+      if constexpr (RW) wt_mma();
     };
     auto rw_end = [&](int t) {
-      if constexpr (RW && HALF == 0) wtile(t + 1);
+      if constexpr (RW) wt_store(t + 1);
     };
     rw_begin(0);
     edges(0, in0, in1);
     wave_sync();  // this step's Y- and M2-row reads are done before the next step's stores
+    rw_mid();
     edges(1, in1, in0);
     rw_end(0);
     __syncthreads();
@@ -1674,6 +1694,7 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
       edges(j, in0, in1);
       if constexpr (HALF == 1) products((j >> 1) - 1, half);
       wave_sync();
+      rw_mid();
       edges(j + 1, in1, in0);
       rw_end(j >> 1);
       __syncthreads();  // also: the Y- and M2-row reads are done before the next step's stores
@@ -1707,7 +1728,9 @@ __device__ __forceinline__ void tpx_bwd(const TpxBwdDims& a, MACE_TPX_BWD_PTRS, 
       load_h(2);
     }
     __syncthreads();
-    wtile(0);
+    wt_read(0);
+    wt_mma();
+    wt_store(0);
     __syncthreads();
   }
   load_idx(0);
