@@ -163,8 +163,13 @@ __device__ __forceinline__ void gx_load_x(const GemmXSrc& S, int ci, int g, floa
   x1 = *reinterpret_cast<const float4*>(p + 4);
 }
 
+// CW: 16-column tiles per wave (4: blocks of 64 columns; 8: of 128, so that a row block's X is read
+// by half as many blocks when every problem's output width is a multiple of 128)
+template <int CW>
 __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
-  __shared__ __align__(16) _Float16 sW[2][2][64][40];  // [buffer][hi, lo][column][k of the chunk + pad]
+  constexpr int BC = 16 * CW;                          // output columns per block
+  constexpr int SPT = 256 / BC, SEG = 32 / SPT, NH = SEG / 8;  // staging: threads per column, k each, h8 each
+  __shared__ __align__(16) _Float16 sW[2][2][BC][40];  // [buffer][hi, lo][column][k of the chunk + pad]
   int q = 0;
   while (q + 1 < G.n && (int)blockIdx.x >= G.p[q + 1].tile_begin) ++q;
   const GemmProb& P = G.p[q];
@@ -186,30 +191,38 @@ __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
   S.xr[1] = P.K2 > 0 ? P.X2 + (int64_t)n * P.ldx2 + P.in_base2 + m * NC : S.xr[0];
   S.winv[0] = P.winv1;
   S.winv[1] = P.winv2;
-  // staging: thread -> column tn * 64 + tid / 4, eight k at 8 (tid & 3), both planes
-  const int scol = threadIdx.x >> 2, kq = 8 * (threadIdx.x & 3);
-  S.w[0] = P.WX1 + (int64_t)(tn * 64 + scol) * P.K1;
-  S.w[1] = P.K2 > 0 ? P.WX2 + (int64_t)(tn * 64 + scol) * P.K2 : S.w[0];
+  // staging: thread -> column tn * BC + tid / SPT, SEG k at SEG (tid % SPT), both planes
+  const int scol = threadIdx.x / SPT, kq = SEG * (threadIdx.x % SPT);
+  S.w[0] = P.WX1 + (int64_t)(tn * BC + scol) * P.K1;
+  S.w[1] = P.K2 > 0 ? P.WX2 + (int64_t)(tn * BC + scol) * P.K2 : S.w[0];
   const int64_t plane[2] = {(int64_t)P.Cout * P.K1, (int64_t)P.Cout * P.K2};
   const int nch = (P.K1 + P.K2) / 32;
   float4 ring[2][2];
   gx_load_x(S, 0, g, ring[0][0], ring[0][1]);
   gx_load_x(S, min(1, nch - 1), g, ring[1][0], ring[1][1]);
-  auto load_w = [&](int ci, h8* w) {  // this thread's eight values of chunk ci, hi and lo
+  auto load_w = [&](int ci, h8 (*w)[NH]) {  // this thread's SEG values of chunk ci, hi and lo
     int k = 32 * ci;
     const int o = k < S.K1 ? 0 : 1;
     if (o) k -= S.K1;
-    w[0] = *reinterpret_cast<const h8*>(S.w[o] + k + kq);
-    w[1] = *reinterpret_cast<const h8*>(S.w[o] + plane[o] + k + kq);
-  };
-  h8 ws[2];
-  load_w(0, ws);
-  *reinterpret_cast<h8*>(&sW[0][0][scol][kq]) = ws[0];
-  *reinterpret_cast<h8*>(&sW[0][1][scol][kq]) = ws[1];
-  __syncthreads();
-  f4v acc[4];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) acc[u] = f4v{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < NH; ++i) {
+      w[0][i] = *reinterpret_cast<const h8*>(S.w[o] + k + kq + 8 * i);
+      w[1][i] = *reinterpret_cast<const h8*>(S.w[o] + plane[o] + k + kq + 8 * i);
+    }
+  };
+  auto stage_w = [&](int buf, h8 (*w)[NH]) {
+#pragma unroll
+    for (int pl = 0; pl < 2; ++pl)
+#pragma unroll
+      for (int i = 0; i < NH; ++i) *reinterpret_cast<h8*>(&sW[buf][pl][scol][kq + 8 * i]) = w[pl][i];
+  };
+  h8 ws[2][NH];
+  load_w(0, ws);
+  stage_w(0, ws);
+  __syncthreads();
+  f4v acc[CW];
+#pragma unroll
+  for (int u = 0; u < CW; ++u) acc[u] = f4v{0.f, 0.f, 0.f, 0.f};
   for (int c0 = 0; c0 < nch; c0 += 2) {
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
@@ -238,7 +251,7 @@ __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
           xl[j] = (_Float16)(x - (float)hi);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < CW; ++u) {
           const int col = 16 * u + r;
           const h8 wh = *reinterpret_cast<const h8*>(&sW[buf][0][col][8 * g]);
           const h8 wl = *reinterpret_cast<const h8*>(&sW[buf][1][col][8 * g]);
@@ -248,10 +261,7 @@ __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[u][i] = fmaf(d[i], inv, acc[u][i]);
         }
-        if (cc + 1 < nch) {
-          *reinterpret_cast<h8*>(&sW[buf ^ 1][0][scol][kq]) = ws[0];
-          *reinterpret_cast<h8*>(&sW[buf ^ 1][1][scol][kq]) = ws[1];
-        }
+        if (cc + 1 < nch) stage_w(buf ^ 1, ws);
         __syncthreads();
       }
     }
@@ -259,8 +269,8 @@ __global__ void __launch_bounds__(256) k_gemm_group_x(GemmGroup G) {
   if (!live) return;
   const float rs = P.rowscale ? P.rowscale[n] : 1.f;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int col = tn * 64 + 16 * u + 4 * g;  // four consecutive output columns
+  for (int u = 0; u < CW; ++u) {
+    const int col = tn * BC + 16 * u + 4 * g;  // four consecutive output columns
     float* y = P.Y + (int64_t)n * P.ldy + P.out_base + (col / NC) * P.out_stride + m * NC + (col % NC);
     float4 v = float4{acc[u][0] * rs, acc[u][1] * rs, acc[u][2] * rs, acc[u][3] * rs};
     if (P.bias) {
@@ -791,16 +801,29 @@ void launch_forces(hipStream_t st, int N, const int* rowptr, const int* rowptr_s
 }
 
 void launch_gemm_group(hipStream_t st, GemmGroup& g) {
-  if (g.split) {  // 64 rows x 64 columns per block
+  if (g.split) {  // 64 rows x 64 (or 128) columns per block
+    // 128 columns when every output width allows it and the launch still has blocks for every CU
+    // several times over (each row block's X is then read by half as many blocks)
+    int64_t wide_tiles = 0;
+    bool c128 = true;
+    for (int q = 0; q < g.n; ++q) {
+      c128 = c128 && g.p[q].Cout % 128 == 0;
+      wide_tiles += cdiv(g.p[q].rows, 64) * (g.p[q].Cout / 128);
+    }
+    const int bc = c128 && wide_tiles >= 2048 ? 128 : 64;
     int tiles = 0;
     for (int q = 0; q < g.n; ++q) {
       GemmProb& P = g.p[q];
-      P.tiles_n = P.Cout / 64;
+      P.tiles_n = P.Cout / bc;
       P.tile_begin = tiles;
       tiles += (int)cdiv(P.rows, 64) * P.tiles_n;
     }
     g.total_tiles = tiles;
-    if (tiles > 0) MACE_LAUNCH(k_gemm_group_x, dim3(tiles), dim3(256), 0, st, g);
+    if (tiles <= 0) return;
+    if (bc == 128)
+      MACE_LAUNCH(k_gemm_group_x<8>, dim3(tiles), dim3(256), 0, st, g);
+    else
+      MACE_LAUNCH(k_gemm_group_x<4>, dim3(tiles), dim3(256), 0, st, g);
     return;
   }
   int row_tiles = 0;
