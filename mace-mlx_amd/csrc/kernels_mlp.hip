@@ -922,16 +922,40 @@ __global__ void __launch_bounds__(256) k_mlp_hidden_bwd(int64_t E, int nb, const
 __device__ __forceinline__ int kperm2(int c, int g, int j) { return 16 * (2 * c + (j >> 2)) + 4 * g + (j & 3); }
 
 // split tile images, [.. ][hi, lo][lane] (lane = 16 g + r)
-struct MlpFwdX {
-  h8 w0[4][2][64];     // [t'] A[n = 16t' + r][8g + j] = W0[8g + j][n]
-  h8 w1[2][4][2][64];  // [c][t'] A[n = 16t' + r][slot] = W1[kperm2(c, g, j)][n]
-  h8 w2[2][4][2][64];
+// NP planes: 2 (hi, lo) as built; 1 (hi) staged under a half-precision policy, whose rounded
+// weights have zero lo planes (half the LDS, so more blocks per CU)
+template <int NP>
+struct MlpFwdXT {
+  h8 w0[4][NP][64];     // [t'] A[n = 16t' + r][8g + j] = W0[8g + j][n]
+  h8 w1[2][4][NP][64];  // [c][t'] A[n = 16t' + r][slot] = W1[kperm2(c, g, j)][n]
+  h8 w2[2][4][NP][64];
 };
-struct MlpBwdX {
-  h8 w2T[2][4][2][64];  // [c][t'] A[k = 16t' + r][slot] = W2[k][kperm2(c, g, j)]
-  h8 w1T[2][4][2][64];
-  h8 w0T[2][2][64];     // [c] A[k = r][slot] = W0[r][kperm2(c, g, j)] (zero for r >= nb)
+template <int NP>
+struct MlpBwdXT {
+  h8 w2T[2][4][NP][64];  // [c][t'] A[k = 16t' + r][slot] = W2[k][kperm2(c, g, j)]
+  h8 w1T[2][4][NP][64];
+  h8 w0T[2][NP][64];     // [c] A[k = r][slot] = W0[r][kperm2(c, g, j)] (zero for r >= nb)
 };
+using MlpFwdX = MlpFwdXT<2>;
+using MlpBwdX = MlpBwdXT<2>;
+
+// stage the hi planes of a two-plane image (every member's innermost dimensions are [2][64])
+template <class D, class S>
+__device__ __forceinline__ void stage_hi(D& dst, const S* __restrict__ src) {
+  static_assert(2 * sizeof(D) == sizeof(S), "a one-plane image of a two-plane one");
+  constexpr int N = (int)(sizeof(D) / sizeof(h8));
+  const h8* q = reinterpret_cast<const h8*>(src);
+  h8* d = reinterpret_cast<h8*>(&dst);
+  for (int i = threadIdx.x; i < N; i += blockDim.x) d[i] = q[(i >> 6) * 128 + (i & 63)];
+}
+// the image as a kernel keeps it in LDS: both planes, or the hi planes (NP = 1)
+template <int NP, class D, class S>
+__device__ __forceinline__ void stage_planes(D& dst, const S* __restrict__ src) {
+  if constexpr (NP == 2)
+    stage_copy(dst, src);
+  else
+    stage_hi(dst, src);
+}
 
 __device__ __forceinline__ void split_pair(float x, _Float16& hi, _Float16& lo) {
   hi = (_Float16)x;
@@ -1009,8 +1033,9 @@ __device__ __forceinline__ int lane_opaque() {
 // weights' / the inputs' lo planes may be nonzero; under a half-precision feature policy the
 // rounded weights and activations have zero lo planes (an fp16 value, or a bf16 value, times a
 // power of two is one fp16 value), so those products add exact zeros and are skipped
-template <bool OPQ, bool ALO = true, bool XLO = true>
-__device__ __forceinline__ void layer64x(const h8 (*w)[4][2][64], const float* v, float winv, f4v* acc) {
+template <bool OPQ, bool ALO = true, bool XLO = true, int NP = 2>
+__device__ __forceinline__ void layer64x(const h8 (*w)[4][NP][64], const float* v, float winv, f4v* acc) {
+  static_assert(NP == 2 || !ALO, "the weights' lo planes are staged");
   const int l = lane_opaque<OPQ>();
   float inv;
   const float sc = edge_scale<16>(v, &inv);
@@ -1031,7 +1056,7 @@ __device__ __forceinline__ void layer64x(const h8 (*w)[4][2][64], const float* v
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const h8 wh = w[c][t][0][l];
-      if constexpr (ALO) d[t] = mfma16h(w[c][t][1][l], xh, d[t]);
+      if constexpr (ALO) d[t] = mfma16h(w[c][t][NP - 1][l], xh, d[t]);
       if constexpr (XLO) d[t] = mfma16h(wh, xl, d[t]);
       d[t] = mfma16h(wh, xh, d[t]);
     }
@@ -1044,8 +1069,8 @@ __device__ __forceinline__ void layer64x(const h8 (*w)[4][2][64], const float* v
 // layers, the activations between them rounded by mode RND (the feature policy); dsp as in
 // hidden_fwd; leaves a1, a2, a3 (the VJP recomputes them this way, with the same
 // instructions, instead of reading saved derivatives)
-template <bool OPQ, int RND>
-__device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* winv, int64_t E, int64_t e0, int nb,
+template <bool OPQ, int RND, int NP>
+__device__ __forceinline__ void hidden_fwd_x(const MlpFwdXT<NP>& sw, const float* winv, int64_t E, int64_t e0, int nb,
                                              const float* __restrict__ ef, f4v* a1, f4v* a2, f4v* a3, float* dsp) {
   // half-precision policies: weights, features and activations are rounded values (zero lo
   // planes), so one product per operand pair
@@ -1076,7 +1101,7 @@ __device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* win
       const h8 wh = sw.w0[t][0][lo];
       f4v d = f4v{0.f, 0.f, 0.f, 0.f};
       if constexpr (FULL) {
-        d = mfma16h(sw.w0[t][1][lo], xh, d);
+        d = mfma16h(sw.w0[t][NP - 1][lo], xh, d);
         d = mfma16h(wh, xl, d);
       }
       d = mfma16h(wh, xh, d);
@@ -1087,11 +1112,11 @@ __device__ __forceinline__ void hidden_fwd_x(const MlpFwdX& sw, const float* win
 #pragma unroll
   for (int q = 0; q < 16; ++q) v[q] = qh(silu(a1[q >> 2][q & 3]), RND);
   if (dsp) store_ds(dsp, a1);
-  layer64x<OPQ, FULL, FULL>(sw.w1, v, winv[1], a2);
+  layer64x<OPQ, FULL, FULL, NP>(sw.w1, v, winv[1], a2);
 #pragma unroll
   for (int q = 0; q < 16; ++q) v[q] = qh(silu(a2[q >> 2][q & 3]), RND);
   if (dsp) store_ds(dsp + H, a2);
-  layer64x<OPQ, FULL, FULL>(sw.w2, v, winv[2], a3);
+  layer64x<OPQ, FULL, FULL, NP>(sw.w2, v, winv[2], a3);
   if (dsp) store_ds(dsp + 2 * H, a3);
 }
 
@@ -1111,15 +1136,16 @@ __global__ void __launch_bounds__(64 * kHidFwdWaves) k_mlp_hidden_x(int64_t E, i
                                                       const MlpFwdX* __restrict__ tiles, MlpWinv wi,
                                                       _Float16* __restrict__ h3x, float* __restrict__ h3inv,
                                                       float* __restrict__ ds) {
-  __shared__ MlpFwdX sw;
-  stage_copy(sw, tiles);
+  constexpr int NP = RND == RND_NONE ? 2 : 1;
+  __shared__ MlpFwdXT<NP> sw;
+  stage_planes<NP>(sw, tiles);
   __syncthreads();
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t ngroups = (E + 15) / 16;
   for (int64_t gi = (int64_t)blockIdx.x * kHidFwdWaves + wv; gi < ngroups; gi += (int64_t)gridDim.x * kHidFwdWaves) {
     const int64_t e0 = gi * 16, e = e0 + r;
     f4v a1[4], a2[4], a3[4];
-    hidden_fwd_x<false, RND>(sw, wi.w, E, e0, nb, ef, a1, a2, a3, (ds && e < E) ? ds + e * 3 * H + 4 * g : nullptr);
+    hidden_fwd_x<false, RND, NP>(sw, wi.w, E, e0, nb, ef, a1, a2, a3, (ds && e < E) ? ds + e * 3 * H + 4 * g : nullptr);
     float v[16];
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = qh(silu(a3[q >> 2][q & 3]), RND);
@@ -1154,11 +1180,12 @@ __global__ void __launch_bounds__(64 * NW) k_mlp_hidden_bwd_x(int64_t E, int nb,
                                                           const float* __restrict__ ef, const float* __restrict__ ds,
                                                           const float* __restrict__ gh3, int np, int64_t pstride,
                                                           float* __restrict__ gef, int accumulate) {
-  __shared__ MlpBwdX sw;
-  __shared__ __align__(16) char swf_raw[RECOMP ? sizeof(MlpFwdX) : 16];
-  MlpFwdX& swf = *reinterpret_cast<MlpFwdX*>(swf_raw);
-  stage_copy(sw, tiles);
-  if constexpr (RECOMP) stage_copy(swf, ftiles);
+  constexpr int NP = RND == RND_NONE ? 2 : 1;
+  __shared__ MlpBwdXT<NP> sw;
+  __shared__ __align__(16) char swf_raw[RECOMP ? sizeof(MlpFwdXT<NP>) : 16];
+  MlpFwdXT<NP>& swf = *reinterpret_cast<MlpFwdXT<NP>*>(swf_raw);
+  stage_planes<NP>(sw, tiles);
+  if constexpr (RECOMP) stage_planes<NP>(swf, ftiles);
   __syncthreads();
   const int wv = threadIdx.x >> 6, l = threadIdx.x & 63, r = l & 15, g = l >> 4;
   const int64_t ngroups = (E + 15) / 16;
@@ -1167,7 +1194,7 @@ __global__ void __launch_bounds__(64 * NW) k_mlp_hidden_bwd_x(int64_t E, int nb,
     float v[16], dv[16];
     f4v acc[4];
     f4v a1[4], a2[4], a3[4];  // RECOMP: the pre-activations, rebuilt
-    if constexpr (RECOMP) hidden_fwd_x<true, RND>(swf, wi.w, E, e0, nb, ef, a1, a2, a3, nullptr);
+    if constexpr (RECOMP) hidden_fwd_x<true, RND, NP>(swf, wi.w, E, e0, nb, ef, a1, a2, a3, nullptr);
     // silu' of layer k's pre-activations in the lane's layout (feature 16t + 4g + i -> [4t + i])
     auto dsl = [&](int k, float* out) {
       if constexpr (RECOMP) {
@@ -1191,11 +1218,11 @@ __global__ void __launch_bounds__(64 * NW) k_mlp_hidden_bwd_x(int64_t E, int nb,
     // the gradients are float32 (lo planes nonzero); the weights' lo planes are zero under a
     // half-precision policy
     constexpr bool WLO = RND == RND_NONE;
-    layer64x<RECOMP, WLO, true>(sw.w2T, v, wi.w[2], acc);
+    layer64x<RECOMP, WLO, true, NP>(sw.w2T, v, wi.w[2], acc);
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = acc[q >> 2][q & 3] * dv[q];
     dsl(0, dv);
-    layer64x<RECOMP, WLO, true>(sw.w1T, v, wi.w[1], acc);
+    layer64x<RECOMP, WLO, true, NP>(sw.w1T, v, wi.w[1], acc);
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = acc[q >> 2][q & 3] * dv[q];
     // g_ef = g_a1 W0^T: one output tile (rows k < nb)
@@ -1215,7 +1242,7 @@ __global__ void __launch_bounds__(64 * NW) k_mlp_hidden_bwd_x(int64_t E, int nb,
       }
       const int lo = lane_opaque<RECOMP>();
       const h8 wh = sw.w0T[c][0][lo];
-      if constexpr (WLO) o = mfma16h(sw.w0T[c][1][lo], xh, o);
+      if constexpr (WLO) o = mfma16h(sw.w0T[c][NP - 1][lo], xh, o);
       o = mfma16h(wh, xl, o);
       o = mfma16h(wh, xh, o);
     }
@@ -1599,13 +1626,15 @@ __global__ void __launch_bounds__(64 * kLnBwdWaves) k_rmlp_ln_bwd(int64_t E, int
 
 // grid of the hidden-layer kernels: enough blocks to fill the device, each
 // staging the weights once and walking several 64-edge groups
+// persistent grids, each wave walking 16-edge groups: two blocks per CU for the forward (three
+// fit under the half policies; measured slower: 0.345 -> 0.352 ms per launch on HEA32000)
 inline unsigned hidden_grid(int64_t E) {
   return (unsigned)std::min<int64_t>((E + 16 * kHidFwdWaves - 1) / (16 * kHidFwdWaves), 512);
 }
-// the recomputing VJP stages both tile images (76 KB): two blocks per CU, one 16-edge group or a
-// few per wave
-inline unsigned hidden_bwd_grid(int64_t E) {
-  return (unsigned)std::min<int64_t>((E + 16 * kHidBwdWaves - 1) / (16 * kHidBwdWaves), 512);
+// the recomputing VJP stages both tile images (76 KB; 38 KB under the half policies, hi planes
+// only): as many blocks as fit at once, two per CU, or three under the half policies
+inline unsigned hidden_bwd_grid(int64_t E, int rnd) {
+  return (unsigned)std::min<int64_t>((E + 16 * kHidBwdWaves - 1) / (16 * kHidBwdWaves), rnd == RND_NONE ? 512 : 768);
 }
 
 size_t mlp_tile_bytes() { return sizeof(MlpFwdW) + sizeof(MlpBwdW); }
@@ -1648,7 +1677,7 @@ void launch_mlp_hidden_bwd_x(hipStream_t st, int64_t E, int nb, const void* tile
     return;
   }
 #define MACE_HBX(R)                                                                                              \
-  MACE_LAUNCH((k_mlp_hidden_bwd_x<true, kHidBwdWaves, R>), dim3(hidden_bwd_grid(E)), dim3(64 * kHidBwdWaves), 0, \
+  MACE_LAUNCH((k_mlp_hidden_bwd_x<true, kHidBwdWaves, R>), dim3(hidden_bwd_grid(E, R)), dim3(64 * kHidBwdWaves), 0, \
               st, E, nb, fw, bw, wi, ef, ds, gh3, np, E * H, gef, accumulate)
   if (rnd == RND_F16)
     MACE_HBX(RND_F16);
