@@ -1625,8 +1625,9 @@ void forward(mace_ctx* c, const double* pos, double* out, double* e_part) {
       // split: h3 holds E x 2 x 64 fp16 (the same bytes as E x 64 floats)
       if (split)
         // no silu' saved: the VJP recomputes the hidden layers from ef
+        // the fused kernels read h3's hi plane only (its lo plane is zero under a half policy)
         launch_mlp_hidden_x(st, E, nb, c->ef.p, L.mlp_tiles_x.p, L.mlp_winv, h3_of(c, l), h3inv_of(c, l), nullptr,
-                            half);
+                            half, !(fused && half != RND_NONE));
       else
         launch_mlp_hidden(st, E, nb, c->ef.p, L.mlp_tiles.p,
                           h16 ? static_cast<void*>(c->h3h.p) : static_cast<void*>(c->h3.p), c->h3inv.p, L.ds.p,

@@ -165,9 +165,10 @@ void launch_mlp_hidden(hipStream_t st, int64_t E, int nb, const float* ef, const
 size_t mlp_tile_x_bytes();
 void launch_mlp_permute_x(hipStream_t st, int nb, const float* W0, const float* W1, const float* W2,
                           const float* scale3, void* tiles);
-// rnd: rounding mode of the activations (RND_*; the split of a rounded h3 has a zero lo plane)
+// rnd: rounding mode of the activations (RND_*; the split of a rounded h3 has a zero lo plane,
+// which is not written when store_lo is 0: for readers of the hi plane only)
 void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, const void* tiles,
-                         const float* winv3, void* h3x, float* h3inv, float* ds, int rnd);
+                         const float* winv3, void* h3x, float* h3inv, float* ds, int rnd, int store_lo = 1);
 // gh3: np partials of dL/dh3 ([np][E][64]), added in order; ds null: silu' of the
 // hidden pre-activations recomputed from ef with the forward's rounding mode rnd (the forward
 // then need not save them)

@@ -1135,8 +1135,10 @@ template <int RND>
 __global__ void __launch_bounds__(64 * kHidFwdWaves) k_mlp_hidden_x(int64_t E, int nb, const float* __restrict__ ef,
                                                       const MlpFwdX* __restrict__ tiles, MlpWinv wi,
                                                       _Float16* __restrict__ h3x, float* __restrict__ h3inv,
-                                                      float* __restrict__ ds) {
+                                                      float* __restrict__ ds, int store_lo) {
   constexpr int NP = RND == RND_NONE ? 2 : 1;
+  // a rounded h3's lo plane is zero: written only for readers of both planes
+  const bool lo_out = RND == RND_NONE || store_lo;
   __shared__ MlpFwdXT<NP> sw;
   stage_planes<NP>(sw, tiles);
   __syncthreads();
@@ -1164,7 +1166,7 @@ __global__ void __launch_bounds__(64 * kHidFwdWaves) k_mlp_hidden_x(int64_t E, i
           lo[i] = b;
         }
         *reinterpret_cast<h4*>(dst + 16 * t + 4 * g) = hi;
-        *reinterpret_cast<h4*>(dst + H + 16 * t + 4 * g) = lo;
+        if (lo_out) *reinterpret_cast<h4*>(dst + H + 16 * t + 4 * g) = lo;
       }
       if (g == 0) h3inv[e] = inv;
     }
@@ -1649,12 +1651,12 @@ void launch_mlp_permute_x(hipStream_t st, int nb, const float* W0, const float* 
 }
 
 void launch_mlp_hidden_x(hipStream_t st, int64_t E, int nb, const float* ef, const void* tiles,
-                         const float* winv3, void* h3x, float* h3inv, float* ds, int rnd) {
+                         const float* winv3, void* h3x, float* h3inv, float* ds, int rnd, int store_lo) {
   if (E <= 0) return;
   MlpWinv wi{{winv3[0], winv3[1], winv3[2]}};
 #define MACE_HX(R)                                                                                 \
   MACE_LAUNCH(k_mlp_hidden_x<R>, dim3(hidden_grid(E)), dim3(64 * kHidFwdWaves), 0, st, E, nb, ef, \
-              static_cast<const MlpFwdX*>(tiles), wi, static_cast<_Float16*>(h3x), h3inv, ds)
+              static_cast<const MlpFwdX*>(tiles), wi, static_cast<_Float16*>(h3x), h3inv, ds, store_lo)
   if (rnd == RND_F16)
     MACE_HX(RND_F16);
   else if (rnd == RND_BF16)
