@@ -316,6 +316,27 @@ def test_full_size_invariants(idx, medium, large):
     np.testing.assert_allclose(c["vir"], R @ a["vir"] @ R.T, atol=1e-5 * np.abs(a["vir"]).max())
 
 
+def test_wide_linears_at_scale_match_the_fp32_path(medium):
+    """8192 Si atoms: every node linear of the default path runs in 64 x 128 blocks (the launch has
+    >= 2048 of them), the size below which the oracle-checked cases stay on 64 x 64 blocks.  The
+    fp32-matrix-core path (separate kernels for the linears, the radial MLP and the TP, each
+    checked against the oracle at small sizes) evaluates the same model: E, F and virial agree to
+    the float32 tolerances (`blocks.py:171-176,225-230`, `model.py:592-661` for the linears)."""
+    s = rattle(diamond_si((8, 8, 16)), 0.04, 61)
+    assert len(s) == 8192
+    print("8192-atom Si: default (split, fused, 128-column linears) vs fp32 matrix cores", flush=True)
+    a = medium.run(s, stress=True)
+    try:
+        medium.eng.set_split_products(False)
+        b = medium.run(s, stress=True)
+    finally:
+        medium.eng.set_split_products(True)
+    print(f"|dE|/|E| {abs(a['E'] - b['E']) / abs(b['E']):.2e} max|dF| {np.abs(a['F'] - b['F']).max():.2e}", flush=True)
+    assert abs(a["E"] - b["E"]) <= 1e-6 * max(abs(b["E"]), len(s))
+    assert np.abs(a["F"] - b["F"]).max() <= 1e-4
+    assert np.abs(a["vir"] - b["vir"]).max() <= 1e-5 * max(1.0, float(np.abs(b["vir"]).max()))
+
+
 def test_periodic_replication_is_exact(medium_zbl):
     """Doubling a periodic cell doubles E and repeats F (Si1000 -> Si2000)."""
     s = make_config(1).system
