@@ -378,8 +378,10 @@ def run_workload(idx, steps, warmup, separate=False, graphs=None, extras=False, 
                          "2*E*64*W flops added" if ctx["fused"] else "separate radial-MLP output pass")}
     res.update(dominant=dom, dominant_frac=roof["frac"], roofline=roof,
                tp_scatter=tp_scatter_summary(per_step, ctx), per_step=per_step, ctx=ctx)
-    # steps that rebuild the neighbour list (the reference's benchmark.py:168-style number)
-    nrb = max(3, steps // 4)
+    # steps that rebuild the neighbour list (the reference's benchmark.py:168-style number), after
+    # two untimed ones (as the steady steps have their warm-up)
+    nrb = max(8, steps // 2)
+    _timed(eng, pos_d, out_d, stress, 2, force_nl=True)
     res["ms_per_step_nl_rebuild"] = round(_timed(eng, pos_d, out_d, stress, nrb, force_nl=True) / nrb * 1e3, 4)
     res["_edges"], res["_species"], res["_bc"], res["_weights"] = edges, species, bc, weights
     del eng, pos_d, out_d
