@@ -1034,15 +1034,22 @@ void build_nl(mace_ctx* c, const double* pos_host) {
   c->nl_iota.ensure((size_t)N + 1);
   c->nl_bin_start.ensure((size_t)nbins + 1);
   c->rowptr.ensure((size_t)N + 1);
-  for (int g = 0; g < G; ++g)
-    launch_nl_bin(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], c->pos.p, ps[g], bin_off[g],
-                  c->nl_wpos.p, c->nl_img.p, c->nl_bin.p, c->nl_iota.p, c->nl_pos_d.p);
-  // atoms sorted by bin (stable: within a bin by index), then each bin's first position
-  cub_sort_pairs(c, c->nl_bin.p, c->nl_bin_sorted.p, c->nl_iota.p, c->nl_atoms.p, N, nbins);
   c->nl_wpos_s.ensure(3 * (size_t)N);
   c->nl_img_s.ensure(3 * (size_t)N);
-  launch_key_starts(c->stream, N, c->nl_bin_sorted.p, nbins, c->nl_bin_start.p, c->nl_atoms.p, c->nl_wpos.p,
-                    c->nl_img.p, c->nl_wpos_s.p, c->nl_img_s.p);
+  if (G == 1 && N > 0 && N <= kNlSmall) {
+    // one structure of up to kNlSmall atoms: binning, sort and bin starts in one block
+    launch_nl_prep_small(c->stream, N, c->pos.p, ps[0], nbins, bits_for(nbins), c->nl_wpos.p, c->nl_img.p,
+                         c->nl_bin.p, c->nl_pos_d.p, c->nl_bin_sorted.p, c->nl_atoms.p, c->nl_bin_start.p,
+                         c->nl_wpos_s.p, c->nl_img_s.p);
+  } else {
+    for (int g = 0; g < G; ++g)
+      launch_nl_bin(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], c->pos.p, ps[g], bin_off[g],
+                    c->nl_wpos.p, c->nl_img.p, c->nl_bin.p, c->nl_iota.p, c->nl_pos_d.p);
+    // atoms sorted by bin (stable: within a bin by index), then each bin's first position
+    cub_sort_pairs(c, c->nl_bin.p, c->nl_bin_sorted.p, c->nl_iota.p, c->nl_atoms.p, N, nbins);
+    launch_key_starts(c->stream, N, c->nl_bin_sorted.p, nbins, c->nl_bin_start.p, c->nl_atoms.p, c->nl_wpos.p,
+                      c->nl_img.p, c->nl_wpos_s.p, c->nl_img_s.p);
+  }
   c->nl_counts.ensure((size_t)N + 1);
   c->nl_missing.ensure(1);
   c->nl_cpre.ensure(std::max<size_t>((size_t)N * cstride, 1));
@@ -1056,7 +1063,10 @@ void build_nl(mace_ctx* c, const double* pos_host) {
     launch_nl_count(c->stream, c->gptr_h[g], c->gptr_h[g + 1] - c->gptr_h[g], ps[g], bin_off[g], c->nl_wpos.p,
                     c->nl_wpos_s.p, c->nl_bin.p, c->nl_bin_start.p, c->nl_atoms.p, cstride, c->nl_cpre.p,
                     c->nl_hits.p, hcap, c->nl_counts.p, c->nl_counts.p + N, c->nl_missing.p);
-  cub_exclusive_sum(c, c->nl_counts.p, c->rowptr.p, (int64_t)N + 1);
+  if (N + 1 <= 2 * kNlSmall)
+    launch_exclusive_sum_small(c->stream, N + 1, c->nl_counts.p, c->rowptr.p);
+  else
+    cub_exclusive_sum(c, c->nl_counts.p, c->rowptr.p, (int64_t)N + 1);
   // the edge count sizes the per-edge arrays and the launches: read back (pinned memory: a copy
   // into pageable memory costs more than this whole wait)
   if (!c->e_pinned) HIPCHK(hipHostMalloc((void**)&c->e_pinned, sizeof(int), hipHostMallocDefault));

@@ -379,6 +379,14 @@ void launch_nl_bin(hipStream_t st, int i0, int n, const double* pos, const NLPar
 void launch_max_disp(hipStream_t st, int n, const double* pos, const double* pos_build, double thr2, int* flag);
 // start[b] (b = 0 .. nbins) = first position of key b in the sorted keys[0 .. n); with wpos, also
 // wpos_s / img_s = the positions / images of atoms[0 .. n) (the atoms in key order)
+// One structure of at most kNlSmall atoms: binning, the stable sort by bin and the bins' first
+// positions in one block (the outputs of launch_nl_bin + a sort + launch_key_starts)
+constexpr int kNlSmall = 1024;
+void launch_nl_prep_small(hipStream_t st, int n, const double* pos, const NLParams& p, int nbins, int key_bits,
+                          double* wpos, int* img, int* bin, double* pos_build, int* bin_sorted, int* atoms,
+                          int* bin_start, double* wpos_s, int* img_s);
+// exclusive prefix sum of n <= 2 kNlSmall ints in one block
+void launch_exclusive_sum_small(hipStream_t st, int n, const int* in, int* out);
 void launch_key_starts(hipStream_t st, int n, const int* keys, int nbins, int* start, const int* atoms = nullptr,
                        const double* wpos = nullptr, const int* img = nullptr, double* wpos_s = nullptr,
                        int* img_s = nullptr);

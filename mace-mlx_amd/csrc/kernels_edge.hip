@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 
 #include <climits>
+#include <hipcub/hipcub.hpp>
+#include <stdexcept>
 
 #include "common.h"
 
@@ -310,12 +312,9 @@ __device__ __forceinline__ int floordiv(int a, int b) {
 // cell); its bins are numbered from bin_off so that all structures share one sorted bin array.
 // iota[i] = i: the values of the sort by bin; pos_build: the positions of this build (the
 // reference of the skin criterion).
-__global__ void k_nl_bin(int i0, int n, const double* __restrict__ pos, NLParams p, int bin_off,
-                         double* __restrict__ wpos, int* __restrict__ img, int* __restrict__ bin,
-                         int* __restrict__ iota, double* __restrict__ pos_build) {
-  if ((int)(blockIdx.x * blockDim.x + threadIdx.x) >= n) return;
-  const int i = i0 + blockIdx.x * blockDim.x + threadIdx.x;
-  iota[i] = i;
+// Atom i's wrapped position w (cell coordinates) and image, and its bin (returned)
+__device__ __forceinline__ int nl_bin_atom(int i, const double* __restrict__ pos, const NLParams& p, int bin_off,
+                                           double* __restrict__ pos_build, double* wpos_i, int* img_i) {
   for (int k = 0; k < 3; ++k) pos_build[3 * i + k] = pos[3 * i + k];
   const double d0 = pos[3 * i] - p.origin[0], d1 = pos[3 * i + 1] - p.origin[1],
                d2 = pos[3 * i + 2] - p.origin[2];
@@ -334,14 +333,92 @@ __global__ void k_nl_bin(int i0, int n, const double* __restrict__ pos, NLParams
     } else {
       w[k] = f[k];
     }
-    img[3 * i + k] = n;
+    img_i[k] = n;
     int bk = (int)floor(w[k] * p.nbin[k]);
     bk = bk < 0 ? 0 : (bk >= p.nbin[k] ? p.nbin[k] - 1 : bk);
     b[k] = bk;
   }
   for (int k = 0; k < 3; ++k)
-    wpos[3 * i + k] = w[0] * p.cell[0 * 3 + k] + w[1] * p.cell[1 * 3 + k] + w[2] * p.cell[2 * 3 + k];
-  bin[i] = bin_off + (b[0] * p.nbin[1] + b[1]) * p.nbin[2] + b[2];
+    wpos_i[k] = w[0] * p.cell[0 * 3 + k] + w[1] * p.cell[1 * 3 + k] + w[2] * p.cell[2 * 3 + k];
+  return bin_off + (b[0] * p.nbin[1] + b[1]) * p.nbin[2] + b[2];
+}
+
+__global__ void k_nl_bin(int i0, int n, const double* __restrict__ pos, NLParams p, int bin_off,
+                         double* __restrict__ wpos, int* __restrict__ img, int* __restrict__ bin,
+                         int* __restrict__ iota, double* __restrict__ pos_build) {
+  if ((int)(blockIdx.x * blockDim.x + threadIdx.x) >= n) return;
+  const int i = i0 + blockIdx.x * blockDim.x + threadIdx.x;
+  iota[i] = i;
+  double w[3];
+  int im[3];
+  bin[i] = nl_bin_atom(i, pos, p, bin_off, pos_build, w, im);
+  for (int k = 0; k < 3; ++k) wpos[3 * i + k] = w[k], img[3 * i + k] = im[k];
+}
+
+// One structure of at most kNlSmall atoms in one block, in place of k_nl_bin + the device-wide
+// sort by bin + k_key_starts (ten launches for a few microseconds of work each): thread t bins
+// atom t, a block radix sort (stable: the atoms of a bin stay in index order) orders the
+// atoms by bin, and each bin's first position is a binary search over the sorted bins.
+// Padding entries take the key nbins, past every bin.
+__global__ void __launch_bounds__(kNlSmall) k_nl_prep_small(int n, const double* __restrict__ pos, NLParams p,
+                                                            int nbins, int key_bits, double* __restrict__ wpos,
+                                                            int* __restrict__ img, int* __restrict__ bin,
+                                                            double* __restrict__ pos_build,
+                                                            int* __restrict__ bin_sorted, int* __restrict__ atoms,
+                                                            int* __restrict__ bin_start, double* __restrict__ wpos_s,
+                                                            int* __restrict__ img_s) {
+  using Sort = hipcub::BlockRadixSort<int, kNlSmall, 1, int>;
+  __shared__ typename Sort::TempStorage tmp;
+  __shared__ int sk[kNlSmall];
+  __shared__ double sw[kNlSmall][3];
+  __shared__ int si[kNlSmall][3];
+  const int t = threadIdx.x;
+  int key[1] = {nbins}, val[1] = {t};
+  if (t < n) {
+    double w[3];
+    int im[3];
+    key[0] = nl_bin_atom(t, pos, p, 0, pos_build, w, im);
+    bin[t] = key[0];
+    for (int k = 0; k < 3; ++k) {
+      wpos[3 * t + k] = w[k], img[3 * t + k] = im[k];
+      sw[t][k] = w[k], si[t][k] = im[k];
+    }
+  }
+  __syncthreads();  // sw / si complete before any thread reads them below
+  Sort(tmp).Sort(key, val, 0, key_bits);
+  sk[t] = key[0];
+  if (t < n) {
+    const int a = val[0];
+    bin_sorted[t] = key[0];
+    atoms[t] = a;
+    for (int k = 0; k < 3; ++k) wpos_s[3 * t + k] = sw[a][k], img_s[3 * t + k] = si[a][k];
+  }
+  __syncthreads();
+  for (int b = t; b <= nbins; b += kNlSmall) {
+    int lo = 0, hi = n;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (sk[mid] < b) lo = mid + 1; else hi = mid;
+    }
+    bin_start[b] = lo;
+  }
+}
+
+// out[i] = in[0] + .. + in[i - 1] for i < n <= 2 kNlSmall, in one block
+__global__ void __launch_bounds__(kNlSmall) k_exclusive_sum_small(int n, const int* __restrict__ in,
+                                                                  int* __restrict__ out) {
+  using Scan = hipcub::BlockScan<int, kNlSmall>;
+  __shared__ typename Scan::TempStorage tmp;
+  int v[2];
+  for (int q = 0; q < 2; ++q) {
+    const int i = 2 * threadIdx.x + q;
+    v[q] = i < n ? in[i] : 0;
+  }
+  Scan(tmp).ExclusiveSum(v, v);
+  for (int q = 0; q < 2; ++q) {
+    const int i = 2 * threadIdx.x + q;
+    if (i < n) out[i] = v[q];
+  }
 }
 
 // One wave per receiver atom j.  Its neighbour cells, in a fixed order (o0 outer, o2 inner),
@@ -707,6 +784,20 @@ void launch_nl_bin(hipStream_t st, int i0, int n, const double* pos, const NLPar
   if (n <= 0) return;
   MACE_LAUNCH(k_nl_bin, dim3(nblk(n, 256)), dim3(256), 0, st, i0, n, pos, p, bin_off, wpos, img, bin, iota,
               pos_build);
+}
+
+void launch_nl_prep_small(hipStream_t st, int n, const double* pos, const NLParams& p, int nbins, int key_bits,
+                          double* wpos, int* img, int* bin, double* pos_build, int* bin_sorted, int* atoms,
+                          int* bin_start, double* wpos_s, int* img_s) {
+  if (n <= 0 || n > kNlSmall) throw std::invalid_argument("launch_nl_prep_small: 1 .. kNlSmall atoms");
+  MACE_LAUNCH(k_nl_prep_small, dim3(1), dim3(kNlSmall), 0, st, n, pos, p, nbins, key_bits, wpos, img, bin, pos_build,
+              bin_sorted, atoms, bin_start, wpos_s, img_s);
+}
+
+void launch_exclusive_sum_small(hipStream_t st, int n, const int* in, int* out) {
+  if (n <= 0) return;
+  if (n > 2 * kNlSmall) throw std::invalid_argument("launch_exclusive_sum_small: at most 2 kNlSmall entries");
+  MACE_LAUNCH(k_exclusive_sum_small, dim3(1), dim3(kNlSmall), 0, st, n, in, out);
 }
 
 void launch_max_disp(hipStream_t st, int n, const double* pos, const double* pos_build, double thr2, int* flag) {
