@@ -211,14 +211,15 @@ def test_bfloat16_feature_policy(arch):
 
 
 @pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
-@pytest.mark.parametrize("arch", ["hea", "medium", "large"])
+@pytest.mark.parametrize("arch", ["hea", "medium", "large", "medium-192"])
 def test_half_policy_vjp_rebuilds_w_bit_for_bit(arch, dtype):
     """Under the half-precision policies the tensor-product VJP rebuilds the per-edge weights w
     (`blocks.py:253-274`: the radial MLP's output layer) from the saved hidden layer instead of
     reading back what the forward stored (mace_set_rebuild_w).  The rebuilt values are the
     forward's own 16-bit numbers, so energy, forces and virial are identical bit for bit to the
     path that stores and reads w, on a system with ragged rows (receivers without edges) and on a
-    periodic cell; "large" (three input blocks) never rebuilds and must match as well."""
+    periodic cell; "large" (three input blocks) never rebuilds and must match as well; a
+    192-channel model runs three channel slices."""
     if arch == "hea":
         cfg = make_config(4).model
         rng = np.random.default_rng(7)
@@ -226,9 +227,13 @@ def test_half_policy_vjp_rebuilds_w_bit_for_bit(arch, dtype):
         base.numbers = np.array([26, 28, 27, 24, 25])[rng.integers(0, 5, len(base))]
         systems = [rattle(base, 0.05, 8, rng=rng)]
     else:
-        cfg = arch_config(arch)
+        cfg = arch_config(arch.split("-")[0])
+        if arch == "medium-192":  # three 64-channel slices (the 192-channel library)
+            cfg.hidden_irreps = "192x0e+192x1o"
         systems = [rattle(diamond_si((2, 2, 2)), 0.05, 9), _ragged_system()]
     case = Case(cfg, dtype=dtype)
+    if arch == "medium-192":
+        assert case.eng.channels == 192
     try:
         for k, s in enumerate(systems):
             print(f"rebuild w {arch} {dtype}: system {k} ({len(s)} atoms)", flush=True)
