@@ -802,6 +802,9 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   // Under a half-precision policy (RND) W3 and h3 hold rounded values: their lo planes are zero,
   // so a w tile is the one product hi.hi (the same sums: the skipped products add exact zeros)
   constexpr bool FULL = RND == RND_NONE;
+  // half policies, two or three input blocks: the w tiles hold 16-bit patterns and only h3's hi
+  // planes are staged (half the LDS: two blocks per CU)
+  constexpr bool HT = !FULL && LIN >= 2;
   h8 wa[NCTW][2][FULL ? 2 : 1];  // [tile][k step][hi, lo]
 #pragma unroll
   for (int m = 0; m < NCTW; ++m) {
@@ -900,8 +903,9 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
     H.hinv = h3inv[row];
     if constexpr (NL) H.cut = buf_load(cutv, 4u * (unsigned)row);  // 0 without a cut array
   };
-  auto store_h = [&](int t) {  // H holds tile t's share
-    *reinterpret_cast<hv*>(hbuf + (((t & 1) * 2 + hpl) * TC + hr) * 72 + HQ * hq) = H.h;
+  auto store_h = [&](int t) {  // H holds tile t's share (half policies: hi planes only)
+    if (!HT || hpl == 0)
+      *reinterpret_cast<hv*>(hbuf + (((t & 1) * (HT ? 1 : 2) + hpl) * TC + hr) * 72 + HQ * hq) = H.h;
     if (hpl == 0 && hq == 0) {
       hiv[(t & 1) * TC + hr] = H.hinv;
       if constexpr (NL) hcv[(t & 1) * TC + hr] = a.cut ? H.cut : 1.f;
@@ -929,11 +933,12 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   // W3^T h3, from the h3 rows staged in hbuf t & 1, into LDS buffer t & 1
   auto products = [&](int t) {
     float* tile = sw + (t & 1) * TC * RS;
+    unsigned short* tile16 = reinterpret_cast<unsigned short*>(sw) + (t & 1) * TC * RS;
 #pragma unroll
     for (int t2 = 0; t2 < NTC; ++t2) {
       h8 bx[2][2];  // B fragments of tile column 16 t2 + r: [k step][hi, lo]
       const int col = 16 * t2 + r;
-      const _Float16* hrow = hbuf + ((t & 1) * 2 * TC + col) * 72 + 8 * g;
+      const _Float16* hrow = hbuf + ((t & 1) * (HT ? 1 : 2) * TC + col) * 72 + 8 * g;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         bx[c][0] = *reinterpret_cast<const h8*>(hrow + 32 * c);
@@ -965,9 +970,17 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 #pragma unroll
       for (int m = 0; m < NCTW; ++m) {
         const int ct = wv + XW * m;
-        if (CT % XW == 0 || ct < CT)
-          *reinterpret_cast<float4*>(tile + col * RS + 16 * ct + 4 * g) =
-              float4{qh(d[m][0], RND), qh(d[m][1], RND), qh(d[m][2], RND), qh(d[m][3], RND)};
+        if (CT % XW == 0 || ct < CT) {
+          if constexpr (!HT) {
+            *reinterpret_cast<float4*>(tile + col * RS + 16 * ct + 4 * g) =
+                float4{qh(d[m][0], RND), qh(d[m][1], RND), qh(d[m][2], RND), qh(d[m][3], RND)};
+          } else {  // the rounded values as 16-bit patterns
+            typedef unsigned short us4 __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<us4*>(tile16 + col * RS + 16 * ct + 4 * g) =
+                us4{w16_bits<RND>(qh(d[m][0], RND)), w16_bits<RND>(qh(d[m][1], RND)),
+                    w16_bits<RND>(qh(d[m][2], RND)), w16_bits<RND>(qh(d[m][3], RND))};
+          }
+        }
       }
     }
   };
@@ -981,7 +994,9 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   };
   // the channel-wise TP of the wave's edges of step j (w tile j / TPS) and the w stores
   auto edges = [&](int j, Slot& S, Slot& Snext) {
+    // half policies: 16-bit patterns, TC RS of them per tile
     const float* tile = sw + ((j / TPS) & 1) * TC * RS;
+    const unsigned short* tile16 = reinterpret_cast<const unsigned short*>(sw) + ((j / TPS) & 1) * TC * RS;
     if constexpr (L1 >= 1) {  // M1 / M2 rows from the Y rows: the terms and order of k_edge_fwd
 #pragma unroll
       for (int b = 0; b < EPW; ++b)
@@ -1008,10 +1023,12 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
       const int e = beg + EPW * j + b;
       const bool valid = e < end;
       float wv_s[T::NSLOT];
-      const float* trow = tile + (16 * (j % TPS) + EPW * wv + b) * RS + u;
+      const int ro = (16 * (j % TPS) + EPW * wv + b) * RS + u;
+      const float* trow = tile + ro;
+      const unsigned short* trow16 = tile16 + ro;
 #pragma unroll
       for (int s = 0; s < T::NSLOT; ++s)
-        if (T::l1(s) == L1) wv_s[s] = trow[64 * GR::local(s)];
+        if (T::l1(s) == L1) wv_s[s] = HT ? w16_value<RND>(trow16[64 * GR::local(s)]) : trow[64 * GR::local(s)];
       if (valid) {
         EdgeIn<LIN> in;
         in.x0 = 0.f;
@@ -1060,7 +1077,7 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
   }
   if (a.sprl > 0) {  // uniform: the chunks' sums through LDS (the w tile buffer), in chunk order
     constexpr int GA = GR::acc_count();
-    static_assert((XW - 1) * GA * 64 <= 2 * TC * RS, "chunk partials fit the w tile buffer");
+    static_assert((XW - 1) * GA * 64 <= (HT ? 1 : 2) * TC * RS, "chunk partials fit the w tile buffer");
     __syncthreads();  // every wave is done with the tiles
     const int c = wv & ((1 << a.sprl) - 1);
     if (c > 0) {
@@ -1097,11 +1114,14 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 // RND: rounding mode of w and M under a half-precision feature policy (the split operands
 // of rounded h3 and weights have zero lo planes, so w is the float32 product, then rounded)
 template <int LIN, int RND, bool NL>
-__global__ void __launch_bounds__(64 * XW, 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_PTRS) {
+// two input blocks under a half policy: 64 KB of LDS and at most 128 VGPRs (a few spilled), two
+// blocks per CU
+__global__ void __launch_bounds__(64 * XW, RND != RND_NONE && LIN == 2 ? 4 : 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_PTRS) {
   constexpr int TC = XW * EPW * tpx_fwd_steps(LIN);
-  __shared__ __align__(16) float sw[2 * TC * (64 * gmax<LIN>() + 4)];
+  constexpr int NPL = RND == RND_NONE || LIN == 1 ? 2 : 1;  // 1: 16-bit w tiles, h3 hi planes only
+  __shared__ __align__(16) float sw[NPL * TC * (64 * gmax<LIN>() + 4)];  // [tile][column][RS]
   __shared__ __align__(16) float stab[XW * EPW * (tpx_tab_pad(LIN - 1) + 16)];  // table rows + Y rows
-  __shared__ __align__(16) _Float16 hbuf[2 * 2 * TC * 72];  // [tile][hi, lo][tile column][64 + pad]
+  __shared__ __align__(16) _Float16 hbuf[2 * NPL * TC * 72];  // [tile][hi, lo][tile column][64 + pad]
   __shared__ float hiv[2 * TC];
   __shared__ float hcv[NL ? 2 * TC : 1];  // NL: the tile columns' cutoff factors
   if constexpr (LIN == 1) {
