@@ -1114,9 +1114,9 @@ __device__ __forceinline__ void tpx_fwd(const TpxDims& a, MACE_TPX_FWD_PTRS, flo
 // RND: rounding mode of w and M under a half-precision feature policy (the split operands
 // of rounded h3 and weights have zero lo planes, so w is the float32 product, then rounded)
 template <int LIN, int RND, bool NL>
-// two input blocks under a half policy: 64 KB of LDS and at most 128 VGPRs (a few spilled), two
-// blocks per CU
-__global__ void __launch_bounds__(64 * XW, RND != RND_NONE && LIN == 2 ? 4 : 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_PTRS) {
+// two input blocks under a half policy, standard interaction block: 64 KB of LDS and at most 128
+// VGPRs (a few spilled), two blocks per CU (the non-linear block's epilogue would spill more)
+__global__ void __launch_bounds__(64 * XW, RND != RND_NONE && LIN == 2 && !NL ? 4 : 2) k_tpx_fwd(TpxDims a, MACE_TPX_FWD_PTRS) {
   constexpr int TC = XW * EPW * tpx_fwd_steps(LIN);
   constexpr int NPL = RND == RND_NONE || LIN == 1 ? 2 : 1;  // 1: 16-bit w tiles, h3 hi planes only
   __shared__ __align__(16) float sw[NPL * TC * (64 * gmax<LIN>() + 4)];  // [tile][column][RS]
